@@ -1,0 +1,154 @@
+/*
+ * oi.h -- C ABI of the MI355X (gfx950) HIP library that replaces the
+ * arithmetic of odin-infer's token loop.
+ *
+ * The Odin host keeps the reference's Engine API (infer/engine.odin:7-60) and
+ * binds these entry points with `foreign import` (odin-infer_amd/odin/
+ * engine.odin).  Plain C types only: no torch, no HIP types in signatures.
+ * Streams are passed as `void*` (a hipStream_t, NULL = the library's stream).
+ *
+ * Errors: functions returning int return 0 on success and a negative code on
+ * failure; functions returning a pointer return NULL.  Either way the message
+ * is available from oi_last_error() (thread-local).
+ */
+#ifndef OI_H
+#define OI_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml tensor type ids (reference: ggml/gguf.odin:27-42). */
+enum {
+    OI_TYPE_F32 = 0, OI_TYPE_F16 = 1, OI_TYPE_Q4_0 = 2, OI_TYPE_Q4_1 = 3,
+    OI_TYPE_Q5_0 = 6, OI_TYPE_Q5_1 = 7, OI_TYPE_Q8_0 = 8, OI_TYPE_Q8_1 = 9,
+    OI_TYPE_Q2_K = 10, OI_TYPE_Q3_K = 11, OI_TYPE_Q4_K = 12, OI_TYPE_Q5_K = 13,
+    OI_TYPE_Q6_K = 14, OI_TYPE_Q8_K = 15
+};
+
+/* Error codes. */
+enum {
+    OI_OK = 0,
+    OI_E_ARG = -1,        /* bad argument (null pointer, bad size, bad type) */
+    OI_E_IO = -2,         /* file could not be opened or mapped */
+    OI_E_FORMAT = -3,     /* not a GGUF v2/v3 file, truncated or corrupt */
+    OI_E_MODEL = -4,      /* missing metadata key / tensor, wrong tensor type */
+    OI_E_UNSUPPORTED = -5,/* quant type not supported on this path */
+    OI_E_RANGE = -6,      /* token or pos out of range */
+    OI_E_DEVICE = -7,     /* no usable gfx950 device, or a HIP call failed */
+    OI_E_NOMEM = -8       /* device or pinned host allocation failed */
+};
+
+/* Engine_Opts (reference: infer/engine.odin:7-11).  `use_hip` replaces
+ * `use_metal`; there is no CPU fallback in this library. */
+typedef struct oi_opts {
+    int32_t max_ctx;     /* KV capacity cap; seq_len = min(context_length, max_ctx) */
+    int32_t use_hip;     /* must be 1 */
+    int32_t num_threads; /* accepted for source compatibility; unused on the GPU */
+    int32_t device;      /* HIP device ordinal */
+} oi_opts;
+
+/* Config (reference: infer/model.odin:12-24), same field order. */
+typedef struct oi_config {
+    int64_t dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size;
+    int64_t seq_len, max_seq, head_dim;
+    float rope_freq, rms_eps;
+} oi_config;
+
+typedef struct oi_engine oi_engine;
+typedef struct oi_weights oi_weights;
+
+/* ------------------------------------------------------------ engine API --- */
+
+/* engine_load (infer/engine.odin:18-34 -> infer/model.odin:216-242):
+ * parse the GGUF at `path`, check the tensors the dense Qwen3 loader requires
+ * (infer/model.odin:99-179), upload weights to HBM and allocate the f16 KV
+ * cache [layer][kv_head][seq_len][head_dim].  Returns 0 and *out on success. */
+int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out);
+
+/* engine_destroy (infer/engine.odin:36-43). NULL is allowed. */
+void oi_engine_destroy(oi_engine *e);
+
+/* engine_forward (infer/engine.odin:45-52 -> infer/forward.odin:17-146):
+ * consume `token` at `pos`, write K/V[pos], return vocab_size logits that
+ * predict pos+1.  The pointer is engine-owned pinned host memory, valid until
+ * the next call on this engine.  NULL on error (token/pos out of range:
+ * the reference prints and exits, forward.odin:22-29; the Odin binding does
+ * the same). */
+const float *oi_engine_forward(oi_engine *e, int32_t token, int32_t pos);
+
+/* engine_config (infer/engine.odin:54-56). */
+int oi_engine_config(const oi_engine *e, oi_config *out);
+
+/* Message of the last failure on this thread. */
+const char *oi_last_error(void);
+
+/* ------------------------------------------------- token loop (device side) --- */
+
+/* Greedy decode of `n_steps` tokens with the whole loop on the device: step i
+ * consumes the current token at pos+i and picks the next one by argmax with
+ * ties to the lowest id (sampler/sampler.odin:79-89), as the caller loop
+ * serve_harness/serve.odin:514-525 does with greedy sampling.  Writes the
+ * n_steps picked ids to out_tokens (host memory).  No logits cross PCIe. */
+int oi_engine_decode_greedy(oi_engine *e, int32_t token, int32_t pos, int32_t n_steps,
+                            int32_t *out_tokens);
+
+/* Overwrite positions [pos0, pos0+npos) of layers [layer0, layer0+nlayers) of
+ * the f16 KV cache with host data laid out [layer][kv_head][npos][head_dim]
+ * (binary16 bits).  Used to pre-fill long contexts for measurement. */
+int oi_engine_kv_fill(oi_engine *e, int32_t layer0, int32_t nlayers, int32_t pos0, int32_t npos,
+                      const uint16_t *k_f16, const uint16_t *v_f16);
+
+/* Device pointer to the engine's last logits (vocab_size floats). */
+const float *oi_engine_logits_device(oi_engine *e);
+
+/* Stream the engine enqueues on (a hipStream_t). */
+void *oi_engine_stream(oi_engine *e);
+
+/* Kernels of the token loop, for oi_engine_time_kernel. */
+enum {
+    OI_KERNEL_QKV = 0,     /* RMSNorm + fused Q/K/V GEMV */
+    OI_KERNEL_ATTN = 1,    /* q/k norm + RoPE + KV store + split-L attention */
+    OI_KERNEL_WO = 2,      /* attention output GEMV + residual */
+    OI_KERNEL_GATEUP = 3,  /* RMSNorm + gate/up GEMV + SwiGLU */
+    OI_KERNEL_DOWN = 4,    /* down GEMV + residual */
+    OI_KERNEL_OUTPUT = 5   /* final RMSNorm + vocab GEMV + greedy argmax */
+};
+
+/* Launch one kernel of the token loop `iters` times on the engine's stream,
+ * outside the graph, cycling through the layers' weights; report the mean
+ * duration per launch measured with HIP events on that stream (*avg_us) and
+ * the algorithmic HBM bytes of one launch (*bytes).  The attention kernel is
+ * timed at the position of the last forward/decode call.  Leaves the
+ * activations and the KV entry at that position modified. */
+int oi_engine_time_kernel(oi_engine *e, int32_t kernel, int32_t iters, double *avg_us, double *bytes);
+
+/* --------------------------------------------------- kernels (test, bench) --- */
+
+/* dequant_row (ggml/quant.odin:76-175) on the device for `n` elements of
+ * `type` stored in `blocks` (host memory, GGUF block layout).  The blocks go
+ * through the same device repack and unpack code as the GEMV, and the result
+ * is bit-exact with the reference.  Types: F32, F16, Q8_0, Q4_K, Q6_K. */
+int oi_dequant(int32_t type, const void *blocks, int64_t n, float *out);
+
+/* Upload a rows x cols matrix of `type` (GGUF layout, host memory) into HBM
+ * in the GEMV kernels' layout. */
+int oi_weights_upload(int32_t type, const void *host_blocks, int64_t rows, int64_t cols,
+                      oi_weights **out);
+void oi_weights_free(oi_weights *w);
+int64_t oi_weights_bytes(const oi_weights *w); /* GGUF bytes of the matrix */
+
+/* matmul_t (infer/matmul.odin:77-109): y[rows] = W[rows,cols] . x[cols] with
+ * x and y in device memory (f32), enqueued on `stream`. */
+int oi_gemv_launch(const oi_weights *w, const float *x_dev, float *y_dev, void *stream);
+
+/* Host-memory convenience form of oi_gemv_launch (synchronous). */
+int oi_gemv(int32_t type, const void *host_blocks, int64_t rows, int64_t cols, const float *x,
+            float *y);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* OI_H */

@@ -1,0 +1,738 @@
+// engine.cpp -- the C ABI (include/oi.h): engine load / forward / destroy on
+// one gfx950 GPU, plus the kernel test and bench hooks.
+//
+// One engine = one HIP stream, one device arena holding every weight matrix
+// (in the GEMV layout, oi_kernels.h), the f16 KV cache, activations and the
+// small device state [token, pos, step, capacity].  A token step is recorded
+// once into a hipGraph (5 kernels per layer + embedding + output) and
+// replayed; token and pos live in device memory so the same graph serves
+// every position and the device-side greedy loop.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <climits>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "gguf.h"
+#include "oi.h"
+#include "oi_kernels.h"
+
+using namespace oi;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string &msg) {
+    g_err = msg;
+    return code;
+}
+
+#define HIP_TRY(expr)                                                                     \
+    do {                                                                                  \
+        hipError_t e_ = (expr);                                                           \
+        if (e_ != hipSuccess)                                                             \
+            return fail(OI_E_DEVICE, std::string(#expr) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+bool device_type_ok(uint32_t t) {
+    return t == T_F32 || t == T_F16 || t == T_Q8_0 || t == T_Q4_K || t == T_Q6_K;
+}
+
+const char *type_name(uint32_t t) {
+    switch (t) {
+    case 0: return "F32";
+    case 1: return "F16";
+    case 2: return "Q4_0";
+    case 3: return "Q4_1";
+    case 6: return "Q5_0";
+    case 7: return "Q5_1";
+    case 8: return "Q8_0";
+    case 12: return "Q4_K";
+    case 14: return "Q6_K";
+    default: return "other";
+    }
+}
+
+int check_device(int dev) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return fail(OI_E_DEVICE, "no HIP device visible");
+    if (dev < 0 || dev >= n) return fail(OI_E_DEVICE, "device ordinal out of range");
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, dev) != hipSuccess) return fail(OI_E_DEVICE, "hipGetDeviceProperties failed");
+    if (std::strncmp(p.gcnArchName, "gfx950", 6) != 0)
+        return fail(OI_E_DEVICE, std::string("this library is built for gfx950; device is ") + p.gcnArchName);
+    if (hipSetDevice(dev) != hipSuccess) return fail(OI_E_DEVICE, "hipSetDevice failed");
+    return OI_OK;
+}
+
+// Bytes of a matrix in GGUF layout (= bytes in the device layout).
+bool matrix_bytes(uint32_t type, int64_t rows, int64_t cols, size_t &bytes) {
+    int e, b;
+    if (!block_info(type, e, b) || cols % e) return false;
+    bytes = (size_t)(rows * (cols / e) * b);
+    return true;
+}
+
+// Repack one GGUF matrix into the device layout (see DMat in oi_kernels.h).
+// Writes into `dst` (bytes from matrix_bytes) and returns the region offsets.
+struct Regions { size_t q = 0, s = 0, d = 0; };
+Regions repack(uint32_t type, const uint8_t *src, int64_t rows, int64_t cols, uint8_t *dst) {
+    Regions r;
+    const int64_t n = rows * cols;
+    if (type == T_Q6_K) {
+        const int64_t nsb = n / 256;
+        r.q = 0;
+        r.s = (size_t)nsb * 192;
+        r.d = r.s + (size_t)nsb * 16;
+        for (int64_t i = 0; i < nsb; i++) {
+            const uint8_t *b = src + i * 210;
+            std::memcpy(dst + r.q + i * 192, b, 192);  // ql[128], qh[64]
+            std::memcpy(dst + r.s + i * 16, b + 192, 16);
+            std::memcpy(dst + r.d + i * 2, b + 208, 2);
+        }
+    } else if (type == T_Q8_0) {
+        const int64_t nb = n / 32;
+        r.q = 0;
+        r.d = (size_t)nb * 32;
+        for (int64_t i = 0; i < nb; i++) {
+            const uint8_t *b = src + i * 34;
+            std::memcpy(dst + r.d + i * 2, b, 2);
+            std::memcpy(dst + r.q + i * 32, b + 2, 32);
+        }
+    } else {
+        size_t bytes = 0;
+        matrix_bytes(type, rows, cols, bytes);
+        std::memcpy(dst, src, bytes);
+    }
+    return r;
+}
+
+DMat make_dmat(uint32_t type, int64_t rows, int64_t cols, const uint8_t *dev, const Regions &r) {
+    DMat m{};
+    m.type = (int32_t)type;
+    m.rows = (int32_t)rows;
+    m.cols = (int32_t)cols;
+    m.q = dev + r.q;
+    m.s = dev + r.s;
+    m.d = (const uint16_t *)(dev + r.d);
+    return m;
+}
+
+// Host staging of a repacked matrix, then one copy into device memory.
+int upload_matrix(uint32_t type, const uint8_t *src, int64_t rows, int64_t cols, uint8_t *dev, hipStream_t st,
+                  std::vector<uint8_t> &stage, DMat &out) {
+    size_t bytes;
+    if (!matrix_bytes(type, rows, cols, bytes)) return fail(OI_E_ARG, "matrix size not a whole number of blocks");
+    stage.resize(bytes);
+    Regions r = repack(type, src, rows, cols, stage.data());
+    HIP_TRY(hipMemcpyAsync(dev, stage.data(), bytes, hipMemcpyHostToDevice, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    out = make_dmat(type, rows, cols, dev, r);
+    return OI_OK;
+}
+
+struct Arena {
+    uint8_t *base = nullptr;
+    size_t size = 0, used = 0;
+    uint8_t *take(size_t n) {
+        size_t at = (used + 255) & ~(size_t)255;
+        if (at + n > size) return nullptr;
+        used = at + n;
+        return base + at;
+    }
+};
+
+struct LayerDev {
+    DMat wq, wk, wv, wo, w1, w2, w3;
+    const float *attn_norm, *ffn_norm, *q_norm, *k_norm;
+    uint16_t *kc, *vc;
+};
+
+}  // namespace
+
+enum { K_QKV = 0, K_ATTN = 1, K_WO = 2, K_GATEUP = 3, K_DOWN = 4, K_OUTPUT = 5 };
+
+struct oi_engine {
+    oi_config cfg{};
+    int device = 0;
+    hipStream_t stream = nullptr;
+    Arena arena;
+    std::vector<LayerDev> layers;
+    DMat tok_embd{}, output{};
+    const float *output_norm = nullptr;
+    float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *hb = nullptr;
+    float *logits = nullptr, *part = nullptr, *am_val = nullptr;
+    int32_t *am_idx = nullptr, *am_counter = nullptr, *counters = nullptr, *state = nullptr, *tokens = nullptr;
+    float2 *rope_cs = nullptr;
+    float *logits_host = nullptr;
+    int32_t *state_host = nullptr;
+    int chunk = 64, max_splits = 0;
+    std::vector<GemvArgs> g_qkv, g_wo, g_gateup, g_down;
+    GemvArgs g_out{};
+    std::vector<AttnArgs> a_attn;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t gexec = nullptr;
+    int last_pos = 0;
+    size_t weight_bytes = 0;
+};
+
+namespace {
+
+int enqueue_token(oi_engine *e) {
+    const hipStream_t st = e->stream;
+    HIP_TRY(launch_embed(e->tok_embd, e->state, e->x, (int32_t)e->cfg.vocab_size, st));
+    for (size_t l = 0; l < e->layers.size(); l++) {
+        HIP_TRY(launch_gemv(e->g_qkv[l], st));
+        HIP_TRY(launch_attn(e->a_attn[l], (int)e->cfg.head_dim, st));
+        HIP_TRY(launch_gemv(e->g_wo[l], st));
+        HIP_TRY(launch_gemv(e->g_gateup[l], st));
+        HIP_TRY(launch_gemv(e->g_down[l], st));
+    }
+    HIP_TRY(launch_gemv(e->g_out, st));
+    return OI_OK;
+}
+
+int ensure_graph(oi_engine *e) {
+    if (e->gexec) return OI_OK;
+    HIP_TRY(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
+    int rc = enqueue_token(e);
+    hipGraph_t g = nullptr;
+    hipError_t ec = hipStreamEndCapture(e->stream, &g);
+    if (rc) return rc;
+    if (ec != hipSuccess) return fail(OI_E_DEVICE, std::string("hipStreamEndCapture: ") + hipGetErrorString(ec));
+    e->graph = g;
+    HIP_TRY(hipGraphInstantiate(&e->gexec, g, nullptr, nullptr, 0));
+    return OI_OK;
+}
+
+int set_state(oi_engine *e, int32_t token, int32_t pos, int32_t cap) {
+    e->state_host[0] = token;
+    e->state_host[1] = pos;
+    e->state_host[2] = 0;
+    e->state_host[3] = cap;
+    HIP_TRY(hipMemcpyAsync(e->state, e->state_host, 16, hipMemcpyHostToDevice, e->stream));
+    return OI_OK;
+}
+
+GemvArgs gemv_args(int mode, int K, const float *x, const float *norm_w, float eps) {
+    GemvArgs a{};
+    a.mode = mode;
+    a.K = K;
+    a.x = x;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    return a;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *oi_last_error(void) { return g_err.c_str(); }
+
+void oi_engine_destroy(oi_engine *e) {
+    if (!e) return;
+    hipSetDevice(e->device);
+    if (e->stream) hipStreamSynchronize(e->stream);
+    if (e->gexec) hipGraphExecDestroy(e->gexec);
+    if (e->graph) hipGraphDestroy(e->graph);
+    if (e->arena.base) hipFree(e->arena.base);
+    if (e->logits_host) hipHostFree(e->logits_host);
+    if (e->state_host) hipHostFree(e->state_host);
+    if (e->stream) hipStreamDestroy(e->stream);
+    delete e;
+}
+
+int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
+    if (!path || !opts || !out) return fail(OI_E_ARG, "null argument");
+    *out = nullptr;
+    if (!opts->use_hip) return fail(OI_E_ARG, "use_hip must be set: this library has no CPU path");
+    if (opts->max_ctx <= 0) return fail(OI_E_ARG, "max_ctx must be positive");
+    int rc = check_device(opts->device);
+    if (rc) return rc;
+
+    GgufFile g;
+    std::string err;
+    rc = g.open(path, err);
+    if (rc) return fail(rc, err);
+
+    // load_config (infer/model.odin:99-139)
+    auto *arch = g.meta("general.architecture");
+    if (!arch || arch->str != "qwen3")
+        std::fprintf(stderr, "warning: architecture is '%s', expected 'qwen3'\n", arch ? arch->str.c_str() : "");
+    const char *keys[7] = {"qwen3.embedding_length", "qwen3.feed_forward_length", "qwen3.block_count",
+                           "qwen3.attention.head_count", "qwen3.attention.head_count_kv", "qwen3.context_length",
+                           "qwen3.attention.key_length"};
+    int64_t kv[7];
+    for (int i = 0; i < 7; i++) {
+        auto *m = g.meta(keys[i]);
+        if (!m) return fail(OI_E_MODEL, std::string("missing metadata key: ") + keys[i]);
+        kv[i] = (int64_t)m->u;
+    }
+    std::unique_ptr<oi_engine> e(new oi_engine());
+    e->device = opts->device;
+    oi_config &c = e->cfg;
+    c.dim = kv[0];
+    c.hidden_dim = kv[1];
+    c.n_layers = kv[2];
+    c.n_heads = kv[3];
+    c.n_kv_heads = kv[4];
+    c.max_seq = kv[5];
+    c.head_dim = kv[6];
+    auto *rf = g.meta("qwen3.rope.freq_base");
+    c.rope_freq = rf ? (float)rf->f : 1000000.0f;
+    auto *re = g.meta("qwen3.attention.layer_norm_rms_epsilon");
+    c.rms_eps = re ? (float)re->f : 1e-6f;
+
+    auto require = [&](const std::string &name, const GgufTensor *&t) -> int {
+        t = g.tensor(name);
+        if (!t) return fail(OI_E_MODEL, "missing required tensor: " + name);
+        if (!device_type_ok(t->kind))
+            return fail(OI_E_UNSUPPORTED, "tensor " + name + " has quant type " + type_name(t->kind) +
+                                              " (supported on this path: F32, F16, Q8_0, Q4_K, Q6_K)");
+        return OI_OK;
+    };
+    const GgufTensor *emb;
+    if ((rc = require("token_embd.weight", emb))) return rc;
+    c.vocab_size = (int64_t)emb->dims.back();  // model.odin:137-138
+    c.seq_len = std::min<int64_t>(c.max_seq, opts->max_ctx);  // model.odin:220-223
+    if (c.seq_len <= 0) c.seq_len = opts->max_ctx;
+
+    if (c.dim <= 0 || c.dim % 256 || c.dim > 15360 || c.hidden_dim <= 0 || c.hidden_dim % 256 ||
+        c.hidden_dim > 15360 || c.n_layers <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads)
+        return fail(OI_E_MODEL, "model dimensions outside what this path supports");
+    const int G = (int)(c.n_heads / c.n_kv_heads);
+    if (!((c.head_dim == 128 && (G == 1 || G == 2 || G == 4 || G == 8)) || (c.head_dim == 256 && G <= 4 && (G & (G - 1)) == 0)))
+        return fail(OI_E_UNSUPPORTED, "head_dim / GQA group not supported (head_dim 128 with group 1-8, 256 with 1-4)");
+    if (c.n_heads * c.head_dim > 15360) return fail(OI_E_MODEL, "n_heads*head_dim too large");
+
+    // tensors (model.odin:141-179): shapes checked against the config
+    struct Want { std::string name; int64_t rows, cols; bool f32; const GgufTensor *t; };
+    std::vector<Want> want;
+    const int64_t D = c.dim, H = c.hidden_dim, QD = c.n_heads * c.head_dim, KVD = c.n_kv_heads * c.head_dim;
+    want.push_back({"token_embd.weight", c.vocab_size, D, false, nullptr});
+    want.push_back({"output_norm.weight", 1, D, true, nullptr});
+    const bool tied = g.tensor("output.weight") == nullptr;  // model.odin:149-158
+    if (!tied) want.push_back({"output.weight", c.vocab_size, D, false, nullptr});
+    for (int64_t l = 0; l < c.n_layers; l++) {
+        const std::string p = "blk." + std::to_string(l) + ".";
+        want.push_back({p + "attn_norm.weight", 1, D, true, nullptr});
+        want.push_back({p + "ffn_norm.weight", 1, D, true, nullptr});
+        want.push_back({p + "attn_q_norm.weight", 1, c.head_dim, true, nullptr});
+        want.push_back({p + "attn_k_norm.weight", 1, c.head_dim, true, nullptr});
+        want.push_back({p + "attn_q.weight", QD, D, false, nullptr});
+        want.push_back({p + "attn_k.weight", KVD, D, false, nullptr});
+        want.push_back({p + "attn_v.weight", KVD, D, false, nullptr});
+        want.push_back({p + "attn_output.weight", D, QD, false, nullptr});
+        want.push_back({p + "ffn_gate.weight", H, D, false, nullptr});
+        want.push_back({p + "ffn_down.weight", D, H, false, nullptr});
+        want.push_back({p + "ffn_up.weight", H, D, false, nullptr});
+    }
+    size_t wbytes = 0;
+    for (auto &w : want) {
+        if ((rc = require(w.name, w.t))) return rc;
+        if (w.f32 && w.t->kind != T_F32) return fail(OI_E_MODEL, "expected F32 tensor for " + w.name);
+        if (w.t->nelems() != (uint64_t)(w.rows * w.cols) || w.t->dims[0] != (uint64_t)w.cols)
+            return fail(OI_E_MODEL, "tensor " + w.name + " has an unexpected shape");
+        wbytes += ((size_t)w.t->nbytes + 255) & ~(size_t)255;
+    }
+    e->weight_bytes = wbytes;
+
+    // device memory plan
+    e->chunk = 64;
+    e->max_splits = (int)((c.seq_len + e->chunk - 1) / e->chunk);
+    const size_t kv_layer = (size_t)c.n_kv_heads * c.seq_len * c.head_dim * 2;
+    auto al = [](size_t n) { return (n + 255) & ~(size_t)255; };
+    const size_t out_rows = (size_t)c.vocab_size;
+    GemvArgs probe = gemv_args(GEMV_ARGMAX, (int)D, nullptr, nullptr, 0.f);
+    probe.nseg = 1;
+    probe.seg[0].m.rows = (int32_t)out_rows;
+    probe.seg[0].m.cols = (int32_t)D;
+    plan_gemv(probe);
+    size_t act = al(D * 4) + al(QD * 4) + 2 * al(KVD * 4) + al(QD * 4) + al(H * 4) + al(out_rows * 4) +
+                 al((size_t)c.n_heads * e->max_splits * (c.head_dim + 2) * 4) + 2 * al((size_t)probe.total_wgs * 4) +
+                 al(4) + al((size_t)c.n_layers * c.n_kv_heads * 4) + al(16) + al((size_t)(c.seq_len + 1) * 4) +
+                 al((size_t)c.seq_len * (c.head_dim / 2) * 8);
+    e->arena.size = wbytes + 2 * kv_layer * c.n_layers + act + 4096;
+    hipError_t he = hipMalloc(&e->arena.base, e->arena.size);
+    if (he != hipSuccess) return fail(OI_E_NOMEM, "hipMalloc of " + std::to_string(e->arena.size) + " bytes failed");
+    HIP_TRY(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking));
+    HIP_TRY(hipMemsetAsync(e->arena.base, 0, e->arena.size, e->stream));
+
+    // weights
+    std::vector<uint8_t> stage;
+    std::vector<DMat> mats(want.size());
+    std::vector<const float *> f32s(want.size(), nullptr);
+    for (size_t i = 0; i < want.size(); i++) {
+        const GgufTensor *t = want[i].t;
+        uint8_t *dev = e->arena.take((size_t)t->nbytes);
+        if (!dev) return fail(OI_E_NOMEM, "arena exhausted");
+        if ((rc = upload_matrix(t->kind, t->data, want[i].rows, want[i].cols, dev, e->stream, stage, mats[i])))
+            return rc;
+        f32s[i] = (const float *)dev;
+    }
+    size_t wi = 0;
+    e->tok_embd = mats[wi++];
+    e->output_norm = f32s[wi++];
+    e->output = tied ? e->tok_embd : mats[wi++];
+    e->layers.resize((size_t)c.n_layers);
+    for (auto &L : e->layers) {
+        L.attn_norm = f32s[wi++];
+        L.ffn_norm = f32s[wi++];
+        L.q_norm = f32s[wi++];
+        L.k_norm = f32s[wi++];
+        L.wq = mats[wi++];
+        L.wk = mats[wi++];
+        L.wv = mats[wi++];
+        L.wo = mats[wi++];
+        L.w1 = mats[wi++];
+        L.w2 = mats[wi++];
+        L.w3 = mats[wi++];
+    }
+    for (auto &L : e->layers) {
+        L.kc = (uint16_t *)e->arena.take(kv_layer);
+        L.vc = (uint16_t *)e->arena.take(kv_layer);
+    }
+    e->x = (float *)e->arena.take(D * 4);
+    e->q = (float *)e->arena.take(QD * 4);
+    e->k = (float *)e->arena.take(KVD * 4);
+    e->v = (float *)e->arena.take(KVD * 4);
+    e->att = (float *)e->arena.take(QD * 4);
+    e->hb = (float *)e->arena.take(H * 4);
+    e->logits = (float *)e->arena.take(out_rows * 4);
+    e->part = (float *)e->arena.take((size_t)c.n_heads * e->max_splits * (c.head_dim + 2) * 4);
+    e->am_val = (float *)e->arena.take((size_t)probe.total_wgs * 4);
+    e->am_idx = (int32_t *)e->arena.take((size_t)probe.total_wgs * 4);
+    e->am_counter = (int32_t *)e->arena.take(4);
+    e->counters = (int32_t *)e->arena.take((size_t)c.n_layers * c.n_kv_heads * 4);
+    e->state = (int32_t *)e->arena.take(16);
+    e->tokens = (int32_t *)e->arena.take((size_t)(c.seq_len + 1) * 4);
+    e->rope_cs = (float2 *)e->arena.take((size_t)c.seq_len * (c.head_dim / 2) * 8);
+    if (!e->rope_cs) return fail(OI_E_NOMEM, "arena exhausted (activations)");
+
+    // RoPE table, same f32 formula as infer/forward.odin:127-130
+    {
+        const int hd2 = (int)c.head_dim / 2;
+        std::vector<float> freq((size_t)hd2);
+        for (int i = 0; i < hd2; i++) freq[(size_t)i] = 1.0f / powf(c.rope_freq, (float)i / (float)hd2);
+        std::vector<float2> cs((size_t)c.seq_len * hd2);
+        for (int64_t p = 0; p < c.seq_len; p++)
+            for (int i = 0; i < hd2; i++) {
+                const float ang = (float)p * freq[(size_t)i];
+                cs[(size_t)p * hd2 + i] = make_float2(cosf(ang), sinf(ang));
+            }
+        HIP_TRY(hipMemcpyAsync(e->rope_cs, cs.data(), cs.size() * 8, hipMemcpyHostToDevice, e->stream));
+        HIP_TRY(hipStreamSynchronize(e->stream));
+    }
+    HIP_TRY(hipHostMalloc((void **)&e->logits_host, out_rows * 4, hipHostMallocDefault));
+    HIP_TRY(hipHostMalloc((void **)&e->state_host, 16, hipHostMallocDefault));
+
+    // launch plans
+    const float eps = c.rms_eps;
+    for (size_t l = 0; l < e->layers.size(); l++) {
+        LayerDev &L = e->layers[l];
+        GemvArgs a = gemv_args(GEMV_STORE, (int)D, e->x, L.attn_norm, eps);
+        a.nseg = 3;
+        a.seg[0].m = L.wq; a.seg[0].y = e->q;
+        a.seg[1].m = L.wk; a.seg[1].y = e->k;
+        a.seg[2].m = L.wv; a.seg[2].y = e->v;
+        plan_gemv(a);
+        e->g_qkv.push_back(a);
+
+        AttnArgs t{};
+        t.q = e->q; t.k = e->k; t.v = e->v;
+        t.q_norm = L.q_norm; t.k_norm = L.k_norm; t.eps = eps;
+        t.seq_len = (int32_t)c.seq_len;
+        t.rope_cs = e->rope_cs;
+        t.kc = L.kc; t.vc = L.vc;
+        t.state = e->state;
+        t.chunk = e->chunk;
+        t.max_splits = e->max_splits;
+        t.part = e->part;
+        t.counters = e->counters + l * c.n_kv_heads;
+        t.out = e->att;
+        t.n_heads = (int32_t)c.n_heads;
+        t.n_kv_heads = (int32_t)c.n_kv_heads;
+        e->a_attn.push_back(t);
+
+        a = gemv_args(GEMV_ADD, (int)QD, e->att, nullptr, eps);
+        a.nseg = 1;
+        a.seg[0].m = L.wo; a.seg[0].y = e->x;
+        plan_gemv(a);
+        e->g_wo.push_back(a);
+
+        a = gemv_args(GEMV_SWIGLU, (int)D, e->x, L.ffn_norm, eps);
+        a.nseg = 2;
+        a.seg[0].m = L.w1; a.seg[0].y = e->hb;
+        a.seg[1].m = L.w3; a.seg[1].y = e->hb;
+        plan_gemv(a);
+        e->g_gateup.push_back(a);
+
+        a = gemv_args(GEMV_ADD, (int)H, e->hb, nullptr, eps);
+        a.nseg = 1;
+        a.seg[0].m = L.w2; a.seg[0].y = e->x;
+        plan_gemv(a);
+        e->g_down.push_back(a);
+    }
+    GemvArgs a = gemv_args(GEMV_ARGMAX, (int)D, e->x, e->output_norm, eps);
+    a.nseg = 1;
+    a.seg[0].m = e->output; a.seg[0].y = e->logits;
+    plan_gemv(a);
+    a.am_val = e->am_val;
+    a.am_idx = e->am_idx;
+    a.am_counter = e->am_counter;
+    a.state = e->state;
+    a.tokens_out = e->tokens;
+    e->g_out = a;
+
+    std::printf("model: dim=%lld layers=%lld heads=%lld/%lld hidden=%lld vocab=%lld ctx=%lld/%lld  weights=%.0f MB  "
+                "KV cache (f16)=%.0f MB  [gfx950]\n",
+                (long long)c.dim, (long long)c.n_layers, (long long)c.n_heads, (long long)c.n_kv_heads,
+                (long long)c.hidden_dim, (long long)c.vocab_size, (long long)c.seq_len, (long long)c.max_seq,
+                wbytes / 1048576.0, 2.0 * kv_layer * c.n_layers / 1048576.0);
+    HIP_TRY(hipStreamSynchronize(e->stream));
+    *out = e.release();
+    return OI_OK;
+}
+
+int oi_engine_config(const oi_engine *e, oi_config *out) {
+    if (!e || !out) return fail(OI_E_ARG, "null argument");
+    *out = e->cfg;
+    return OI_OK;
+}
+
+const float *oi_engine_forward(oi_engine *e, int32_t token, int32_t pos) {
+    if (!e) {
+        fail(OI_E_ARG, "null engine");
+        return nullptr;
+    }
+    // forward.odin:82-89
+    if (pos < 0 || pos >= e->cfg.seq_len) {
+        fail(OI_E_RANGE, "forward: pos=" + std::to_string(pos) + " out of range (seq_len=" +
+                             std::to_string(e->cfg.seq_len) + ")");
+        return nullptr;
+    }
+    if (token < 0 || token >= e->cfg.vocab_size) {
+        fail(OI_E_RANGE, "forward: token=" + std::to_string(token) + " out of range (vocab=" +
+                             std::to_string(e->cfg.vocab_size) + ")");
+        return nullptr;
+    }
+    if (hipSetDevice(e->device) != hipSuccess || ensure_graph(e) || set_state(e, token, pos, 0)) return nullptr;
+    hipError_t r = hipGraphLaunch(e->gexec, e->stream);
+    if (r == hipSuccess)
+        r = hipMemcpyAsync(e->logits_host, e->logits, (size_t)e->cfg.vocab_size * 4, hipMemcpyDeviceToHost, e->stream);
+    if (r == hipSuccess) r = hipStreamSynchronize(e->stream);
+    if (r != hipSuccess) {
+        fail(OI_E_DEVICE, std::string("forward: ") + hipGetErrorString(r));
+        return nullptr;
+    }
+    e->last_pos = pos;
+    return e->logits_host;
+}
+
+int oi_engine_decode_greedy(oi_engine *e, int32_t token, int32_t pos, int32_t n_steps, int32_t *out_tokens) {
+    if (!e || !out_tokens || n_steps < 0) return fail(OI_E_ARG, "bad argument");
+    if (pos < 0 || (int64_t)pos + n_steps > e->cfg.seq_len)
+        return fail(OI_E_RANGE, "decode: positions [" + std::to_string(pos) + ", " + std::to_string(pos + n_steps) +
+                                    ") exceed seq_len=" + std::to_string(e->cfg.seq_len));
+    if (token < 0 || token >= e->cfg.vocab_size) return fail(OI_E_RANGE, "decode: token out of range");
+    if (n_steps == 0) return OI_OK;
+    HIP_TRY(hipSetDevice(e->device));
+    int rc = ensure_graph(e);
+    if (rc) return rc;
+    if ((rc = set_state(e, token, pos, n_steps))) return rc;
+    for (int i = 0; i < n_steps; i++) HIP_TRY(hipGraphLaunch(e->gexec, e->stream));
+    HIP_TRY(hipMemcpyAsync(out_tokens, e->tokens, (size_t)n_steps * 4, hipMemcpyDeviceToHost, e->stream));
+    HIP_TRY(hipStreamSynchronize(e->stream));
+    e->last_pos = pos + n_steps - 1;
+    return OI_OK;
+}
+
+int oi_engine_kv_fill(oi_engine *e, int32_t layer0, int32_t nlayers, int32_t pos0, int32_t npos, const uint16_t *k,
+                      const uint16_t *v) {
+    if (!e || !k || !v) return fail(OI_E_ARG, "null argument");
+    const oi_config &c = e->cfg;
+    if (layer0 < 0 || nlayers < 0 || layer0 + nlayers > c.n_layers || pos0 < 0 || npos < 0 ||
+        (int64_t)pos0 + npos > c.seq_len)
+        return fail(OI_E_RANGE, "kv_fill range out of bounds");
+    HIP_TRY(hipSetDevice(e->device));
+    const size_t hd = (size_t)c.head_dim;
+    for (int l = 0; l < nlayers; l++)
+        for (int h = 0; h < c.n_kv_heads; h++) {
+            const size_t src = (((size_t)l * c.n_kv_heads + h) * npos) * hd;
+            const size_t dst = ((size_t)h * c.seq_len + pos0) * hd;
+            HIP_TRY(hipMemcpyAsync(e->layers[(size_t)(layer0 + l)].kc + dst, k + src, (size_t)npos * hd * 2,
+                                   hipMemcpyHostToDevice, e->stream));
+            HIP_TRY(hipMemcpyAsync(e->layers[(size_t)(layer0 + l)].vc + dst, v + src, (size_t)npos * hd * 2,
+                                   hipMemcpyHostToDevice, e->stream));
+        }
+    HIP_TRY(hipStreamSynchronize(e->stream));
+    return OI_OK;
+}
+
+const float *oi_engine_logits_device(oi_engine *e) { return e ? e->logits : nullptr; }
+void *oi_engine_stream(oi_engine *e) { return e ? (void *)e->stream : nullptr; }
+
+int oi_engine_time_kernel(oi_engine *e, int32_t kernel, int32_t iters, double *avg_us, double *bytes) {
+    if (!e || !avg_us || !bytes || iters <= 0 || kernel < K_QKV || kernel > K_OUTPUT)
+        return fail(OI_E_ARG, "bad argument");
+    HIP_TRY(hipSetDevice(e->device));
+    const oi_config &c = e->cfg;
+    const size_t L = e->layers.size();
+    auto mat_bytes = [](const DMat &m) {
+        size_t b = 0;
+        matrix_bytes((uint32_t)m.type, m.rows, m.cols, b);
+        return (double)b;
+    };
+    double per = 0;
+    const double D = (double)c.dim, H = (double)c.hidden_dim, QD = (double)(c.n_heads * c.head_dim),
+                 KVD = (double)(c.n_kv_heads * c.head_dim);
+    const double pos = e->last_pos;
+    hipEvent_t e0, e1;
+    HIP_TRY(hipEventCreate(&e0));
+    HIP_TRY(hipEventCreate(&e1));
+    int rc = OI_OK;
+    auto run = [&](bool timed) -> int {
+        for (int it = 0; it < iters; it++) {
+            const size_t l = (size_t)it % L;
+            hipError_t r = hipSuccess;
+            switch (kernel) {
+            case K_QKV: r = launch_gemv(e->g_qkv[l], e->stream); break;
+            case K_ATTN: r = launch_attn(e->a_attn[l], (int)c.head_dim, e->stream); break;
+            case K_WO: r = launch_gemv(e->g_wo[l], e->stream); break;
+            case K_GATEUP: r = launch_gemv(e->g_gateup[l], e->stream); break;
+            case K_DOWN: r = launch_gemv(e->g_down[l], e->stream); break;
+            default: r = launch_gemv(e->g_out, e->stream); break;
+            }
+            if (r != hipSuccess) return fail(OI_E_DEVICE, std::string("launch: ") + hipGetErrorString(r));
+        }
+        (void)timed;
+        return OI_OK;
+    };
+    // the output kernel's argmax epilogue advances the device state: keep pos
+    if ((rc = set_state(e, 0, e->last_pos, 0))) return rc;
+    if ((rc = run(false))) return rc;
+    if ((rc = set_state(e, 0, e->last_pos, 0))) return rc;
+    HIP_TRY(hipEventRecord(e0, e->stream));
+    if ((rc = run(true))) return rc;
+    HIP_TRY(hipEventRecord(e1, e->stream));
+    HIP_TRY(hipEventSynchronize(e1));
+    float ms = 0;
+    HIP_TRY(hipEventElapsedTime(&ms, e0, e1));
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    *avg_us = ms * 1000.0 / iters;
+    const LayerDev &L0 = e->layers[0];
+    switch (kernel) {
+    case K_QKV: per = mat_bytes(L0.wq) + mat_bytes(L0.wk) + mat_bytes(L0.wv) + D * 8 + (QD + 2 * KVD) * 4; break;
+    case K_ATTN: per = 2.0 * KVD * 2 * (pos + 1) + (QD * 2 + 2 * KVD) * 4 + 2 * (c.head_dim + c.head_dim) * 4; break;
+    case K_WO: per = mat_bytes(L0.wo) + QD * 4 + D * 8; break;
+    case K_GATEUP: per = mat_bytes(L0.w1) + mat_bytes(L0.w3) + D * 8 + H * 4; break;
+    case K_DOWN: per = mat_bytes(L0.w2) + H * 4 + D * 8; break;
+    default: per = mat_bytes(e->output) + D * 8 + (double)c.vocab_size * 4; break;
+    }
+    *bytes = per;
+    return OI_OK;
+}
+
+// ------------------------------------------------------------ kernel hooks --
+
+struct oi_weights {
+    DMat m{};
+    uint8_t *dev = nullptr;
+    size_t bytes = 0;
+};
+
+int oi_weights_upload(int32_t type, const void *host_blocks, int64_t rows, int64_t cols, oi_weights **out) {
+    if (!host_blocks || !out || rows <= 0 || cols <= 0 || rows > INT32_MAX || cols > 15360)
+        return fail(OI_E_ARG, "bad argument");
+    if (!device_type_ok((uint32_t)type)) return fail(OI_E_UNSUPPORTED, "type not supported by the GEMV kernels");
+    if (cols % 64 || ((type == T_Q4_K || type == T_Q6_K) && cols % 256))
+        return fail(OI_E_ARG, "cols must be a multiple of 64 (256 for K-quants)");
+    int rc = check_device(0);
+    if (rc) return rc;
+    std::unique_ptr<oi_weights> w(new oi_weights());
+    if (!matrix_bytes((uint32_t)type, rows, cols, w->bytes)) return fail(OI_E_ARG, "bad size");
+    if (hipMalloc(&w->dev, w->bytes) != hipSuccess) return fail(OI_E_NOMEM, "hipMalloc failed");
+    std::vector<uint8_t> stage;
+    rc = upload_matrix((uint32_t)type, (const uint8_t *)host_blocks, rows, cols, w->dev, nullptr, stage, w->m);
+    if (rc) {
+        hipFree(w->dev);
+        return rc;
+    }
+    *out = w.release();
+    return OI_OK;
+}
+
+void oi_weights_free(oi_weights *w) {
+    if (!w) return;
+    if (w->dev) hipFree(w->dev);
+    delete w;
+}
+
+int64_t oi_weights_bytes(const oi_weights *w) { return w ? (int64_t)w->bytes : 0; }
+
+int oi_gemv_launch(const oi_weights *w, const float *x_dev, float *y_dev, void *stream) {
+    if (!w || !x_dev || !y_dev) return fail(OI_E_ARG, "null argument");
+    GemvArgs a = gemv_args(GEMV_STORE, w->m.cols, x_dev, nullptr, 0.f);
+    a.nseg = 1;
+    a.seg[0].m = w->m;
+    a.seg[0].y = y_dev;
+    if (!plan_gemv(a)) return fail(OI_E_ARG, "cols not a multiple of 64");
+    hipError_t r = launch_gemv(a, (hipStream_t)stream);
+    if (r != hipSuccess) return fail(OI_E_DEVICE, std::string("gemv launch: ") + hipGetErrorString(r));
+    return OI_OK;
+}
+
+int oi_gemv(int32_t type, const void *host_blocks, int64_t rows, int64_t cols, const float *x, float *y) {
+    if (!x || !y) return fail(OI_E_ARG, "null argument");
+    oi_weights *w = nullptr;
+    int rc = oi_weights_upload(type, host_blocks, rows, cols, &w);
+    if (rc) return rc;
+    float *dx = nullptr, *dy = nullptr;
+    hipError_t r = hipMalloc(&dx, (size_t)cols * 4);
+    if (r == hipSuccess) r = hipMalloc(&dy, (size_t)rows * 4);
+    if (r == hipSuccess) r = hipMemcpy(dx, x, (size_t)cols * 4, hipMemcpyHostToDevice);
+    if (r == hipSuccess) {
+        rc = oi_gemv_launch(w, dx, dy, nullptr);
+        if (!rc) r = hipMemcpy(y, dy, (size_t)rows * 4, hipMemcpyDeviceToHost);
+    }
+    if (dx) hipFree(dx);
+    if (dy) hipFree(dy);
+    oi_weights_free(w);
+    if (rc) return rc;
+    if (r != hipSuccess) return fail(OI_E_DEVICE, std::string("gemv: ") + hipGetErrorString(r));
+    return OI_OK;
+}
+
+int oi_dequant(int32_t type, const void *blocks, int64_t n, float *out) {
+    if (!blocks || !out || n <= 0) return fail(OI_E_ARG, "bad argument");
+    if (!device_type_ok((uint32_t)type)) return fail(OI_E_UNSUPPORTED, "type not supported on the device");
+    // one row of n elements; the kernels work in units of 64
+    if (n % 64 || ((type == T_Q4_K || type == T_Q6_K) && n % 256))
+        return fail(OI_E_ARG, "n must be a multiple of 64 (256 for K-quants)");
+    // long inputs are cut into rows of at most 15360 elements
+    int64_t cols = n;
+    while (cols > 15360 && cols % 2 == 0 && (cols / 2) % 256 == 0) cols /= 2;
+    const int64_t rows = n / cols;
+    oi_weights *w = nullptr;
+    int rc = oi_weights_upload(type, blocks, rows, cols, &w);
+    if (rc) return rc;
+    float *dy = nullptr;
+    hipError_t r = hipMalloc(&dy, (size_t)n * 4);
+    if (r == hipSuccess) r = launch_dequant(w->m, dy, nullptr);
+    if (r == hipSuccess) r = hipMemcpy(out, dy, (size_t)n * 4, hipMemcpyDeviceToHost);
+    if (dy) hipFree(dy);
+    oi_weights_free(w);
+    if (r != hipSuccess) return fail(OI_E_DEVICE, std::string("dequant: ") + hipGetErrorString(r));
+    return OI_OK;
+}
+
+}  // extern "C"

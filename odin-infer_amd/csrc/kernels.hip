@@ -1,0 +1,840 @@
+// kernels.hip -- gfx950 kernels of the decode token loop.
+//
+//   gemv_kernel    quantized GEMV (Q4_K, Q6_K, Q8_0, F16, F32) with a fused
+//                  RMSNorm prologue and store / residual-add / SwiGLU / greedy
+//                  argmax epilogues (reference: infer/matmul.odin:77-109,
+//                  ggml/quant.odin:76-282, infer/forward.odin:111-203)
+//   attn_kernel    split-L grouped-query decode attention over the f16 KV
+//                  cache, with the per-head q/k RMSNorm, RoPE and the K/V store
+//                  of the current position fused in (forward.odin:117-175;
+//                  the f16 store follows infer/metal.odin:443-454)
+//   embed_kernel   token embedding row (forward.odin:72-75)
+//   dequant_kernel bit-exact dequant of a matrix (test hook)
+//
+// Wave64 throughout; workgroups of 256 threads (4 waves).
+
+#include "oi_kernels.h"
+
+namespace oi {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int WAVE = 64;
+constexpr int WG = 256;
+
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+__device__ __forceinline__ uint16_t f2h(float f) {  // round to nearest even
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+template <class T>
+__device__ __forceinline__ T ldg_nt(const T *p) {
+    return __builtin_nontemporal_load(p);
+}
+
+// byte i (0..11) of the packed Q4_K scales held in three words
+__device__ __forceinline__ uint32_t sbyte(const uint32_t sw[3], int i) {
+    uint32_t w = i < 4 ? sw[0] : (i < 8 ? sw[1] : sw[2]);
+    return (w >> ((i & 3) * 8)) & 0xFFu;
+}
+
+// get_scale_min_k4 (ggml/quant.odin:64-73)
+__device__ __forceinline__ void scale_min_k4(int j, const uint32_t sw[3], uint32_t &sc, uint32_t &m) {
+    if (j < 4) {
+        sc = sbyte(sw, j) & 63u;
+        m = sbyte(sw, j + 4) & 63u;
+    } else {
+        sc = (sbyte(sw, j + 4) & 0xFu) | ((sbyte(sw, j - 4) >> 6) << 4);
+        m = (sbyte(sw, j + 4) >> 4) | ((sbyte(sw, j) >> 6) << 4);
+    }
+}
+
+// --------------------------------------------------------------------------
+// Bit-exact unit decoders (64 weights each).  Contraction is off so every
+// product and difference is rounded separately, as in the reference.
+// --------------------------------------------------------------------------
+
+// Q4_K unit u of a row: ggml/quant.odin:178-209
+__device__ void decode_unit_q4k(const uint8_t *row, int u, float *out) {
+#pragma clang fp contract(off)
+    const uint8_t *blk = row + (size_t)(u >> 2) * 144;
+    const int p = u & 3;
+    const u32x4 hdr = *(const u32x4 *)blk;
+    const u32x4 q0 = *(const u32x4 *)(blk + 16 + 32 * p);
+    const u32x4 q1 = *(const u32x4 *)(blk + 32 + 32 * p);
+    const float d = h2f(hdr.x & 0xFFFFu), dmin = h2f(hdr.x >> 16);
+    const uint32_t sw[3] = {hdr.y, hdr.z, hdr.w};
+    uint32_t sc0, m0, sc1, m1;
+    scale_min_k4(2 * p, sw, sc0, m0);
+    scale_min_k4(2 * p + 1, sw, sc1, m1);
+    const float d1 = d * (float)sc0, mm1 = dmin * (float)m0;
+    const float d2 = d * (float)sc1, mm2 = dmin * (float)m1;
+    const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+    for (int l = 0; l < 32; l++) {
+        const uint32_t b = (qw[l >> 2] >> ((l & 3) * 8)) & 0xFFu;
+        out[l] = d1 * (float)(b & 0xFu) - mm1;
+        out[32 + l] = d2 * (float)(b >> 4) - mm2;
+    }
+}
+
+// Q6_K unit u: ggml/quant.odin:212-247.  Writes the 64 values at their
+// positions in the 256-element super-block (out points at the super-block).
+__device__ void decode_unit_q6k(const DMat &m, int row, int u, float *sbout) {
+#pragma clang fp contract(off)
+    const int nsb = m.cols >> 8;
+    const int sb = u >> 2, h = (u >> 1) & 1, l0 = (u & 1) * 16;
+    const size_t sbi = (size_t)row * nsb + sb;
+    const uint8_t *qb = m.q + sbi * 192;
+    const int8_t *sc = (const int8_t *)(m.s + sbi * 16) + 8 * h;
+    const float d = h2f(m.d[sbi]);
+    const uint8_t *ql = qb + 64 * h, *qh = qb + 128 + 32 * h;
+    for (int i = 0; i < 16; i++) {
+        const int l = l0 + i, is = l / 16;
+        const int q1 = (int)((ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32;
+        const int q2 = (int)((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+        const int q3 = (int)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+        const int q4 = (int)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+        float *y = sbout + 128 * h;
+        y[l] = d * (float)sc[is + 0] * (float)q1;
+        y[l + 32] = d * (float)sc[is + 2] * (float)q2;
+        y[l + 64] = d * (float)sc[is + 4] * (float)q3;
+        y[l + 96] = d * (float)sc[is + 6] * (float)q4;
+    }
+}
+
+// Any type: decode unit u of `row` into out[64] (in element order).
+__device__ void decode_unit(const DMat &m, int row, int u, float *out) {
+#pragma clang fp contract(off)
+    switch (m.type) {
+    case T_Q4_K:
+        decode_unit_q4k(m.q + (size_t)row * (m.cols / 256) * 144, u, out);
+        break;
+    case T_Q6_K: {
+        // the unit's 64 values are spread over its super-block; decode into
+        // a local super-block image and copy the unit's elements out
+        float sbuf[256];
+        decode_unit_q6k(m, row, u, sbuf);
+        const int h = (u >> 1) & 1, l0 = (u & 1) * 16;
+        for (int k = 0; k < 4; k++)
+            for (int i = 0; i < 16; i++) out[16 * k + i] = sbuf[128 * h + 32 * k + l0 + i];
+        break;
+    }
+    case T_Q8_0: {  // ggml/quant.odin:87-96
+        const size_t blk0 = (size_t)row * (m.cols / 32) + 2 * u;
+        for (int b = 0; b < 2; b++) {
+            const float d = h2f(m.d[blk0 + b]);
+            const int8_t *qs = (const int8_t *)(m.q + (blk0 + b) * 32);
+            for (int j = 0; j < 32; j++) out[32 * b + j] = d * (float)qs[j];
+        }
+        break;
+    }
+    case T_F16: {
+        const uint16_t *p = (const uint16_t *)m.q + (size_t)row * m.cols + 64 * u;
+        for (int j = 0; j < 64; j++) out[j] = h2f(p[j]);
+        break;
+    }
+    default: {  // F32
+        const float *p = (const float *)m.q + (size_t)row * m.cols + 64 * u;
+        for (int j = 0; j < 64; j++) out[j] = p[j];
+        break;
+    }
+    }
+}
+
+// Element index (within the row) of the j-th value that decode_unit writes.
+__device__ __forceinline__ int unit_elem(int type, int u, int j) {
+    if (type == T_Q6_K) {
+        const int sb = u >> 2, h = (u >> 1) & 1, l0 = (u & 1) * 16;
+        return 256 * sb + 128 * h + 32 * (j >> 4) + l0 + (j & 15);
+    }
+    return 64 * u + j;
+}
+
+// --------------------------------------------------------------- dequant --
+__global__ __launch_bounds__(WG) void dequant_kernel(DMat m, float *out) {
+    const int units = m.cols / 64;
+    const long gid = (long)blockIdx.x * WG + threadIdx.x;
+    if (gid >= (long)m.rows * units) return;
+    const int row = (int)(gid / units), u = (int)(gid % units);
+    float v[64];
+    decode_unit(m, row, u, v);
+    float *o = out + (size_t)row * m.cols;
+    for (int j = 0; j < 64; j++) o[unit_elem(m.type, u, j)] = v[j];
+}
+
+// ------------------------------------------------------------- embedding --
+// x = dequant(token_embd[token]) (infer/forward.odin:72-75, 103)
+__global__ __launch_bounds__(WG) void embed_kernel(DMat emb, const int32_t *state, float *x, int32_t vocab) {
+    int tok = state[0];
+    if (tok < 0 || tok >= vocab) tok = 0;  // the host checks the range first
+    const int units = emb.cols / 64;
+    for (int u = threadIdx.x; u < units; u += WG) {
+        float v[64];
+        decode_unit(emb, tok, u, v);
+        for (int j = 0; j < 64; j++) x[unit_elem(emb.type, u, j)] = v[j];
+    }
+}
+
+// ------------------------------------------------------------------ GEMV --
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    return v;
+}
+
+// x in LDS: float4 chunk c (elements 4c..4c+3) lives at a swizzled slot so
+// that the 64 lanes of a wave, each reading chunk k of its own 64-element
+// unit, hit distinct banks.
+__device__ __forceinline__ int xswz(int c) { return (c & ~15) | ((c & 15) ^ ((c >> 4) & 15)); }
+
+struct XView {
+    const float4 *x4;  // LDS, swizzled
+    const float *s16;  // LDS, sums of 16 consecutive elements
+    __device__ __forceinline__ float4 chunk(int c) const { return x4[xswz(c)]; }
+};
+
+__device__ __forceinline__ float dot4_nib(uint32_t w, float4 x) {
+    // four bytes of w, each 0..255, times x
+    return (float)(w & 0xFFu) * x.x + (float)((w >> 8) & 0xFFu) * x.y + (float)((w >> 16) & 0xFFu) * x.z +
+           (float)(w >> 24) * x.w;
+}
+
+// Per-type unit GEMV pieces.  Each "load" fetches one unit's bytes for one
+// row into registers; each "dot" consumes them against x.
+
+struct Q4KRegs { u32x4 hdr, q0, q1; };
+__device__ __forceinline__ void load_q4k(const DMat &m, int row, int u, Q4KRegs &r) {
+    const uint8_t *blk = m.q + ((size_t)row * (m.cols >> 8) + (u >> 2)) * 144;
+    const int p = u & 3;
+    r.hdr = ldg_nt((const u32x4 *)blk);
+    r.q0 = ldg_nt((const u32x4 *)(blk + 16 + 32 * p));
+    r.q1 = ldg_nt((const u32x4 *)(blk + 32 + 32 * p));
+}
+// sum over the unit of dequant(w) * x, in the factored form
+// d*sc*sum(q*x) - dmin*m*sum(x) per group of 32
+__device__ __forceinline__ float dot_q4k(const Q4KRegs &r, int u, const XView &xv) {
+    const int p = u & 3;
+    const float d = h2f(r.hdr.x & 0xFFFFu), dmin = h2f(r.hdr.x >> 16);
+    const uint32_t sw[3] = {r.hdr.y, r.hdr.z, r.hdr.w};
+    uint32_t sc0, m0, sc1, m1;
+    scale_min_k4(2 * p, sw, sc0, m0);
+    scale_min_k4(2 * p + 1, sw, sc1, m1);
+    const uint32_t qw[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+    float alo = 0.f, ahi = 0.f;
+    const int cb = u * 16;
+#pragma unroll
+    for (int w = 0; w < 8; w++) {
+        alo += dot4_nib(qw[w] & 0x0F0F0F0Fu, xv.chunk(cb + w));
+        ahi += dot4_nib((qw[w] >> 4) & 0x0F0F0F0Fu, xv.chunk(cb + 8 + w));
+    }
+    const float slo = xv.s16[4 * u] + xv.s16[4 * u + 1];
+    const float shi = xv.s16[4 * u + 2] + xv.s16[4 * u + 3];
+    return d * (float)sc0 * alo - dmin * (float)m0 * slo + d * (float)sc1 * ahi - dmin * (float)m1 * shi;
+}
+
+struct Q6KRegs { u32x4 ql0, ql1, qh; u32x2 sc; uint32_t d; };
+__device__ __forceinline__ void load_q6k(const DMat &m, int row, int u, Q6KRegs &r) {
+    const size_t sbi = (size_t)row * (m.cols >> 8) + (u >> 2);
+    const int h = (u >> 1) & 1, l0 = (u & 1) * 16;
+    const uint8_t *qb = m.q + sbi * 192;
+    r.ql0 = ldg_nt((const u32x4 *)(qb + 64 * h + l0));
+    r.ql1 = ldg_nt((const u32x4 *)(qb + 64 * h + 32 + l0));
+    r.qh = ldg_nt((const u32x4 *)(qb + 128 + 32 * h + l0));
+    r.sc = ldg_nt((const u32x2 *)(m.s + sbi * 16 + 8 * h));
+    r.d = m.d[sbi];
+}
+__device__ __forceinline__ float dot_q6k(const Q6KRegs &r, int u, const XView &xv) {
+    const int sb = u >> 2, h = (u >> 1) & 1, l0 = (u & 1) * 16;
+    const uint32_t ql0[4] = {r.ql0.x, r.ql0.y, r.ql0.z, r.ql0.w};
+    const uint32_t ql1[4] = {r.ql1.x, r.ql1.y, r.ql1.z, r.ql1.w};
+    const uint32_t qh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+    float a[4] = {0.f, 0.f, 0.f, 0.f};
+    const int e0 = 256 * sb + 128 * h + l0;  // element of (k=0, i=0)
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        const uint32_t v0 = (ql0[w] & 0x0F0F0F0Fu) | ((qh[w] & 0x03030303u) << 4);
+        const uint32_t v1 = (ql1[w] & 0x0F0F0F0Fu) | (((qh[w] >> 2) & 0x03030303u) << 4);
+        const uint32_t v2 = ((ql0[w] >> 4) & 0x0F0F0F0Fu) | (((qh[w] >> 4) & 0x03030303u) << 4);
+        const uint32_t v3 = ((ql1[w] >> 4) & 0x0F0F0F0Fu) | (((qh[w] >> 6) & 0x03030303u) << 4);
+        a[0] += dot4_nib(v0, xv.chunk((e0 + 0) / 4 + w));
+        a[1] += dot4_nib(v1, xv.chunk((e0 + 32) / 4 + w));
+        a[2] += dot4_nib(v2, xv.chunk((e0 + 64) / 4 + w));
+        a[3] += dot4_nib(v3, xv.chunk((e0 + 96) / 4 + w));
+    }
+    // scales sc[8h + l0/16 + 2k] -> bytes (l0/16) + 2k of the 8-byte word
+    const int sh = l0 / 16;
+    const float d = h2f(r.d);
+    float acc = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int bi = sh + 2 * k;
+        const uint32_t word = bi < 4 ? r.sc.x : r.sc.y;
+        const int8_t s = (int8_t)((word >> ((bi & 3) * 8)) & 0xFFu);
+        // q = v - 32  ->  sum(q*x) = sum(v*x) - 32*sum(x)
+        const float sx = xv.s16[(e0 + 32 * k) / 16];
+        acc += d * (float)s * (a[k] - 32.f * sx);
+    }
+    return acc;
+}
+
+struct Q80Regs { u32x4 q[4]; uint32_t d01; };
+__device__ __forceinline__ void load_q80(const DMat &m, int row, int u, Q80Regs &r) {
+    const size_t b0 = (size_t)row * (m.cols >> 5) + 2 * u;
+    const u32x4 *p = (const u32x4 *)(m.q + b0 * 32);
+#pragma unroll
+    for (int i = 0; i < 4; i++) r.q[i] = ldg_nt(p + i);
+    r.d01 = *(const uint32_t *)(m.d + b0);
+}
+__device__ __forceinline__ float sdot4(uint32_t w, float4 x) {
+    return (float)(int8_t)(w & 0xFFu) * x.x + (float)(int8_t)((w >> 8) & 0xFFu) * x.y +
+           (float)(int8_t)((w >> 16) & 0xFFu) * x.z + (float)(int8_t)(w >> 24) * x.w;
+}
+__device__ __forceinline__ float dot_q80(const Q80Regs &r, int u, const XView &xv) {
+    float a0 = 0.f, a1 = 0.f;
+    const int cb = u * 16;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        a0 += sdot4(r.q[i].x, xv.chunk(cb + 4 * i + 0)) + sdot4(r.q[i].y, xv.chunk(cb + 4 * i + 1)) +
+              sdot4(r.q[i].z, xv.chunk(cb + 4 * i + 2)) + sdot4(r.q[i].w, xv.chunk(cb + 4 * i + 3));
+        a1 += sdot4(r.q[i + 2].x, xv.chunk(cb + 8 + 4 * i + 0)) + sdot4(r.q[i + 2].y, xv.chunk(cb + 8 + 4 * i + 1)) +
+              sdot4(r.q[i + 2].z, xv.chunk(cb + 8 + 4 * i + 2)) + sdot4(r.q[i + 2].w, xv.chunk(cb + 8 + 4 * i + 3));
+    }
+    return h2f(r.d01 & 0xFFFFu) * a0 + h2f(r.d01 >> 16) * a1;
+}
+
+__device__ __forceinline__ float dot_f16(const DMat &m, int row, int u, const XView &xv) {
+    const u32x4 *p = (const u32x4 *)((const uint16_t *)m.q + (size_t)row * m.cols + 64 * u);
+    float a = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const u32x4 w = ldg_nt(p + i);
+        const float4 x0 = xv.chunk(u * 16 + 2 * i), x1 = xv.chunk(u * 16 + 2 * i + 1);
+        a += h2f(w.x & 0xFFFFu) * x0.x + h2f(w.x >> 16) * x0.y + h2f(w.y & 0xFFFFu) * x0.z + h2f(w.y >> 16) * x0.w;
+        a += h2f(w.z & 0xFFFFu) * x1.x + h2f(w.z >> 16) * x1.y + h2f(w.w & 0xFFFFu) * x1.z + h2f(w.w >> 16) * x1.w;
+    }
+    return a;
+}
+__device__ __forceinline__ float dot_f32(const DMat &m, int row, int u, const XView &xv) {
+    const float4 *p = (const float4 *)((const float *)m.q + (size_t)row * m.cols + 64 * u);
+    float a = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const float4 w = p[i];
+        const float4 x = xv.chunk(u * 16 + i);
+        a += w.x * x.x + w.y * x.y + w.z * x.z + w.w * x.w;
+    }
+    return a;
+}
+
+// acc[r] += sum over lane units of row rows[r] (r < R); rows >= m.rows skipped
+template <int R>
+__device__ __forceinline__ void gemv_rows(const DMat &m, const int *rows, int j, int lpr, const XView &xv,
+                                          float *acc) {
+    const int U = m.cols >> 6;
+    switch (m.type) {
+    case T_Q4_K:
+        for (int u = j; u < U; u += lpr) {
+            Q4KRegs w[R];
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                if (rows[r] < m.rows) load_q4k(m, rows[r], u, w[r]);
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                if (rows[r] < m.rows) acc[r] += dot_q4k(w[r], u, xv);
+        }
+        break;
+    case T_Q6_K:
+        for (int u = j; u < U; u += lpr) {
+            Q6KRegs w[R];
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                if (rows[r] < m.rows) load_q6k(m, rows[r], u, w[r]);
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                if (rows[r] < m.rows) acc[r] += dot_q6k(w[r], u, xv);
+        }
+        break;
+    case T_Q8_0:
+        for (int u = j; u < U; u += lpr) {
+            Q80Regs w[R];
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                if (rows[r] < m.rows) load_q80(m, rows[r], u, w[r]);
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                if (rows[r] < m.rows) acc[r] += dot_q80(w[r], u, xv);
+        }
+        break;
+    case T_F16:
+        for (int u = j; u < U; u += lpr)
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                if (rows[r] < m.rows) acc[r] += dot_f16(m, rows[r], u, xv);
+        break;
+    default:
+        for (int u = j; u < U; u += lpr)
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                if (rows[r] < m.rows) acc[r] += dot_f32(m, rows[r], u, xv);
+        break;
+    }
+}
+
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+    return v > bv || (v == bv && i < bi);
+}
+
+// Workgroup tile: 4 waves; each wave holds 64/lpr lane groups; each group
+// owns R consecutive rows and lpr lanes that split the row's units.
+template <int R>
+__global__ __launch_bounds__(WG) void gemv_kernel(GemvArgs a) {
+    extern __shared__ float4 smem[];
+    __shared__ float red[WG / WAVE];
+    __shared__ int redi[WG / WAVE];
+    __shared__ int last_flag;
+    const int K = a.K, tid = threadIdx.x;
+    float4 *x4 = smem;
+    float *s16 = (float *)(smem + K / 4);
+
+    // ---- prologue: x (optionally RMS-normalised, ops.odin:7-19) into LDS
+    const float4 *gx = (const float4 *)a.x;
+    float s = 1.f;
+    if (a.norm_w) {
+        float ss = 0.f;
+        for (int c = tid; c < K / 4; c += WG) {
+            const float4 v = gx[c];
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+        ss = wave_sum(ss);
+        if ((tid & (WAVE - 1)) == 0) red[tid / WAVE] = ss;
+        __syncthreads();
+        ss = red[0] + red[1] + red[2] + red[3];
+        s = 1.0f / sqrtf(ss / (float)K + a.eps);
+    }
+    {
+#pragma clang fp contract(off)
+        const float4 *nw = (const float4 *)a.norm_w;
+        for (int c = tid; c < K / 4; c += WG) {
+            float4 v = gx[c];
+            if (nw) {
+                const float4 w = nw[c];
+                v.x = w.x * (s * v.x);
+                v.y = w.y * (s * v.y);
+                v.z = w.z * (s * v.z);
+                v.w = w.w * (s * v.w);
+            }
+            x4[xswz(c)] = v;
+        }
+    }
+    __syncthreads();
+    for (int g = tid; g < K / 16; g += WG) {
+        float t = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 v = x4[xswz(4 * g + i)];
+            t += (v.x + v.y) + (v.z + v.w);
+        }
+        s16[g] = t;
+    }
+    __syncthreads();
+    const XView xv{x4, s16};
+
+    // ---- segment and rows of this workgroup
+    const int wg = blockIdx.x;
+    int seg = 0;
+    if (a.nseg > 1 && a.mode != GEMV_SWIGLU && wg >= a.seg[1].wg_begin) seg = 1;
+    if (a.nseg > 2 && wg >= a.seg[2].wg_begin) seg = 2;
+    const GemvSeg &S = a.seg[seg];
+    const int lane = tid & (WAVE - 1), wave = tid / WAVE;
+    const int lpr = a.lpr, gpw = WAVE / lpr;
+    const int grp = lane / lpr, j = lane & (lpr - 1);
+    const int row0 = (wg - S.wg_begin) * a.rows_per_wg + (wave * gpw + grp) * R;
+    int rows[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) rows[r] = row0 + r;
+
+    float acc[R], acc2[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = acc2[r] = 0.f;
+    gemv_rows<R>(S.m, rows, j, lpr, xv, acc);
+    if (a.mode == GEMV_SWIGLU) gemv_rows<R>(a.seg[1].m, rows, j, lpr, xv, acc2);
+
+    // reduce over the lpr lanes of the group
+    for (int o = lpr >> 1; o > 0; o >>= 1) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            acc[r] += __shfl_xor(acc[r], o, WAVE);
+            if (a.mode == GEMV_SWIGLU) acc2[r] += __shfl_xor(acc2[r], o, WAVE);
+        }
+    }
+
+    float bv = -INFINITY;
+    int bi = 0x7FFFFFFF;
+    if (j == 0) {
+#pragma clang fp contract(off)
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int row = rows[r];
+            if (row >= S.m.rows) continue;
+            if (a.mode == GEMV_ADD) {
+                S.y[row] += acc[r];
+            } else if (a.mode == GEMV_SWIGLU) {  // infer/forward.odin:188-193
+                float val = acc[r];
+                val *= 1.0f / (1.0f + expf(-val));
+                val *= acc2[r];
+                S.y[row] = val;
+            } else {
+                S.y[row] = acc[r];
+                if (better(acc[r], row, bv, bi)) { bv = acc[r]; bi = row; }
+            }
+        }
+    }
+    if (a.mode != GEMV_ARGMAX) return;
+
+    // ---- greedy argmax (sampler/sampler.odin:79-89: first maximum wins)
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, WAVE);
+        const int oi = __shfl_xor(bi, o, WAVE);
+        if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    if (lane == 0) { red[wave] = bv; redi[wave] = bi; }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < WG / WAVE; w++)
+            if (better(red[w], redi[w], bv, bi)) { bv = red[w]; bi = redi[w]; }
+        a.am_val[wg] = bv;
+        a.am_idx[wg] = bi;
+        __threadfence();
+        const int prev = atomicAdd(a.am_counter, 1);
+        last_flag = (prev == a.total_wgs - 1);
+    }
+    __syncthreads();
+    if (!last_flag) return;
+    __threadfence();
+    bv = -INFINITY;
+    bi = 0x7FFFFFFF;
+    for (int i = tid; i < a.total_wgs; i += WG) {
+        const float v = __builtin_nontemporal_load(a.am_val + i);
+        const int ix = __builtin_nontemporal_load(a.am_idx + i);
+        if (better(v, ix, bv, bi)) { bv = v; bi = ix; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, WAVE);
+        const int oi = __shfl_xor(bi, o, WAVE);
+        if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    __syncthreads();
+    if (lane == 0) { red[wave] = bv; redi[wave] = bi; }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < WG / WAVE; w++)
+            if (better(red[w], redi[w], bv, bi)) { bv = red[w]; bi = redi[w]; }
+        if (bi == 0x7FFFFFFF) bi = 0;  // all NaN: keep index 0 as the reference does
+        int32_t *st = a.state;
+        const int step = st[2];
+        if (a.tokens_out && step >= 0 && step < st[3]) a.tokens_out[step] = bi;
+        st[0] = bi;
+        st[1] = st[1] + 1;
+        st[2] = step + 1;
+        *a.am_counter = 0;
+        __threadfence();
+    }
+}
+
+bool plan_gemv(GemvArgs &a) {
+    if (a.K <= 0 || a.K % 64) return false;
+    const int U = a.K / 64;
+    int lpr = 1;
+    while (lpr < 64 && U % (lpr * 2) == 0) lpr *= 2;
+    a.lpr = lpr;
+    const int gpw = 64 / lpr;
+    long rows = 0;
+    for (int i = 0; i < (a.mode == GEMV_SWIGLU ? 1 : a.nseg); i++) rows += a.seg[i].m.rows;
+    // rows per lane group: the largest R in {4,2,1} that still gives >= 512 workgroups
+    int R = 4;
+    while (R > 1 && rows / (4L * gpw * R) < 512) R >>= 1;
+    if (a.mode == GEMV_SWIGLU && R > 2) R = 2;
+    a.rows_per_wg = 4 * gpw * R;
+    int wg = 0;
+    for (int i = 0; i < a.nseg; i++) {
+        a.seg[i].wg_begin = wg;
+        if (a.mode == GEMV_SWIGLU && i == 1) {
+            a.seg[1].wg_begin = 0;
+            break;
+        }
+        wg += (a.seg[i].m.rows + a.rows_per_wg - 1) / a.rows_per_wg;
+    }
+    a.total_wgs = wg;
+    return true;
+}
+
+hipError_t launch_gemv(const GemvArgs &a, hipStream_t st) {
+    const size_t lds = (size_t)a.K * 4 + (size_t)(a.K / 16) * 4;
+    const int R = a.rows_per_wg / (4 * (64 / a.lpr));
+    dim3 grid(a.total_wgs), block(WG);
+    switch (R) {
+    case 4: hipLaunchKernelGGL(gemv_kernel<4>, grid, block, lds, st, a); break;
+    case 2: hipLaunchKernelGGL(gemv_kernel<2>, grid, block, lds, st, a); break;
+    default: hipLaunchKernelGGL(gemv_kernel<1>, grid, block, lds, st, a); break;
+    }
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------- attention --
+
+// RMSNorm + RoPE of one head held in LDS (raw -> out), forward.odin:117-145.
+template <int HD>
+__device__ void norm_rope_head(const float *raw, const float *w, float eps, const float2 *cs, float *out,
+                               float *red, int tid, int nthreads) {
+    // sum of squares over the head (first wave), reference ops.odin:7-19
+    if (tid < WAVE) {
+        float ss = 0.f;
+        for (int i = tid; i < HD; i += WAVE) ss += raw[i] * raw[i];
+        ss = wave_sum(ss);
+        if (tid == 0) red[0] = 1.0f / sqrtf(ss / (float)HD + eps);
+    }
+    __syncthreads();
+    const float s = red[0];
+    for (int i = tid; i < HD / 2; i += nthreads) {
+#pragma clang fp contract(off)
+        const float x = w[i] * (s * raw[i]);
+        const float y = w[i + HD / 2] * (s * raw[i + HD / 2]);
+        const float c = cs[i].x, sn = cs[i].y;
+        out[i] = x * c - y * sn;
+        out[i + HD / 2] = x * sn + y * c;
+    }
+    __syncthreads();
+}
+
+template <int HD, int G>
+__global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
+    constexpr int DPL = HD / 16;  // dims per lane (16 lanes per position)
+    constexpr int MAXC = 256;     // max positions per split
+    __shared__ float qr[G][HD];
+    __shared__ float raw[HD];
+    __shared__ float kp[HD], vp[HD];
+    __shared__ float sc[G][MAXC];
+    __shared__ float mx[G], sm[G];
+    __shared__ float ored[WG / WAVE][G][HD];
+    __shared__ float red[4];
+    __shared__ int last_flag;
+
+    const int split = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
+    const int lane = tid & (WAVE - 1), wave = tid / WAVE;
+    const int pos = a.state[1];
+    const int t0 = split * a.chunk;
+    if (t0 > pos) return;
+    const int t1 = min(t0 + a.chunk, pos + 1);
+    const int n = t1 - t0;
+    const int nsplit = pos / a.chunk + 1;
+    const float2 *cs = a.rope_cs + (size_t)pos * (HD / 2);
+
+    // q heads of this kv group: RMSNorm(q_norm) + RoPE
+    for (int g = 0; g < G; g++) {
+        const int h = kvh * G + g;
+        for (int i = tid; i < HD; i += WG) raw[i] = a.q[(size_t)h * HD + i];
+        __syncthreads();
+        norm_rope_head<HD>(raw, a.q_norm, a.eps, cs, qr[g], red, tid, WG);
+    }
+    // the current position: K/V formed here and stored to the cache as f16
+    const bool has_pos = pos >= t0 && pos < t1;
+    uint16_t *kc = a.kc + (size_t)kvh * a.seq_len * HD;
+    uint16_t *vc = a.vc + (size_t)kvh * a.seq_len * HD;
+    if (has_pos) {
+        for (int i = tid; i < HD; i += WG) raw[i] = a.k[(size_t)kvh * HD + i];
+        __syncthreads();
+        norm_rope_head<HD>(raw, a.k_norm, a.eps, cs, kp, red, tid, WG);
+        for (int i = tid; i < HD; i += WG) {
+            const uint16_t kb = f2h(kp[i]), vb = f2h(a.v[(size_t)kvh * HD + i]);
+            kc[(size_t)pos * HD + i] = kb;
+            vc[(size_t)pos * HD + i] = vb;
+            kp[i] = h2f(kb);
+            vp[i] = h2f(vb);
+        }
+        __syncthreads();
+    }
+
+    // scores: 16 lanes per position, DPL dims per lane
+    const int sub = lane & 15, pslot = lane >> 4;
+    const float inv_div = sqrtf((float)HD);
+    for (int tb = 0; tb < n; tb += 16) {
+        const int tl = tb + wave * 4 + pslot;
+        const int t = t0 + tl;
+        float kv[DPL];
+        if (tl < n) {
+            if (t == pos) {
+#pragma unroll
+                for (int i = 0; i < DPL; i++) kv[i] = kp[sub * DPL + i];
+            } else {
+                const u32x4 *p = (const u32x4 *)(kc + (size_t)t * HD + sub * DPL);
+#pragma unroll
+                for (int c = 0; c < DPL / 8; c++) {
+                    const u32x4 w = ldg_nt(p + c);
+                    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        kv[8 * c + 2 * e] = h2f(ws[e] & 0xFFFFu);
+                        kv[8 * c + 2 * e + 1] = h2f(ws[e] >> 16);
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < DPL; i++) kv[i] = 0.f;
+        }
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float d = 0.f;
+#pragma unroll
+            for (int i = 0; i < DPL; i++) d += qr[g][sub * DPL + i] * kv[i];
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1) d += __shfl_xor(d, o, 16);
+            if (sub == 0 && tl < n) sc[g][tl] = d / inv_div;  // forward.odin:158 divides
+        }
+    }
+    __syncthreads();
+
+    // per-head max and exp-sum over this split (one wave per head)
+    for (int g = wave; g < G; g += WG / WAVE) {
+        float m = -INFINITY;
+        for (int i = lane; i < n; i += WAVE) m = fmaxf(m, sc[g][i]);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, WAVE));
+        float l = 0.f;
+        for (int i = lane; i < n; i += WAVE) {
+            const float e = expf(sc[g][i] - m);
+            sc[g][i] = e;
+            l += e;
+        }
+        l = wave_sum(l);
+        if (lane == 0) { mx[g] = m; sm[g] = l; }
+    }
+    __syncthreads();
+
+    // o_g = sum_t p_g(t) v(t)
+    float acc[G][DPL];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int i = 0; i < DPL; i++) acc[g][i] = 0.f;
+    for (int tl = wave * 4 + pslot; tl < n; tl += 16) {
+        const int t = t0 + tl;
+        float vv[DPL];
+        if (t == pos) {
+#pragma unroll
+            for (int i = 0; i < DPL; i++) vv[i] = vp[sub * DPL + i];
+        } else {
+            const u32x4 *p = (const u32x4 *)(vc + (size_t)t * HD + sub * DPL);
+#pragma unroll
+            for (int c = 0; c < DPL / 8; c++) {
+                const u32x4 w = ldg_nt(p + c);
+                const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    vv[8 * c + 2 * e] = h2f(ws[e] & 0xFFFFu);
+                    vv[8 * c + 2 * e + 1] = h2f(ws[e] >> 16);
+                }
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const float pw = sc[g][tl];
+#pragma unroll
+            for (int i = 0; i < DPL; i++) acc[g][i] += pw * vv[i];
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int i = 0; i < DPL; i++) {
+            float v = acc[g][i];
+            v += __shfl_xor(v, 16, WAVE);
+            v += __shfl_xor(v, 32, WAVE);
+            acc[g][i] = v;
+        }
+    if (pslot == 0) {
+#pragma unroll
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int i = 0; i < DPL; i++) ored[wave][g][sub * DPL + i] = acc[g][i];
+    }
+    __syncthreads();
+    const int stride = HD + 2;
+    for (int idx = tid; idx < G * HD; idx += WG) {
+        const int g = idx / HD, i = idx % HD;
+        const float o = ored[0][g][i] + ored[1][g][i] + ored[2][g][i] + ored[3][g][i];
+        float *pp = a.part + ((size_t)(kvh * G + g) * a.max_splits + split) * stride;
+        pp[i] = o;
+        if (i == 0) { pp[HD] = mx[g]; pp[HD + 1] = sm[g]; }
+    }
+    __syncthreads();
+
+    // last split of this kv head combines all splits
+    if (tid == 0) {
+        __threadfence();
+        const int prev = atomicAdd(a.counters + kvh, 1);
+        last_flag = (prev == nsplit - 1);
+    }
+    __syncthreads();
+    if (!last_flag) return;
+    __threadfence();
+    for (int idx = tid; idx < G * HD; idx += WG) {
+        const int g = idx / HD, i = idx % HD;
+        const float *pb = a.part + (size_t)(kvh * G + g) * a.max_splits * stride;
+        float M = -INFINITY;
+        for (int s = 0; s < nsplit; s++) M = fmaxf(M, __builtin_nontemporal_load(pb + (size_t)s * stride + HD));
+        float L = 0.f, O = 0.f;
+        for (int s = 0; s < nsplit; s++) {
+            const float *ps = pb + (size_t)s * stride;
+            const float f = expf(__builtin_nontemporal_load(ps + HD) - M);
+            L += __builtin_nontemporal_load(ps + HD + 1) * f;
+            O += __builtin_nontemporal_load(ps + i) * f;
+        }
+        a.out[(size_t)(kvh * G + g) * HD + i] = O / L;
+    }
+    if (tid == 0) {
+        a.counters[kvh] = 0;
+        __threadfence();
+    }
+}
+
+template <int HD>
+static hipError_t launch_attn_hd(const AttnArgs &a, int G, hipStream_t st) {
+    dim3 grid(a.max_splits, a.n_kv_heads), block(WG);
+    switch (G) {
+    case 1: hipLaunchKernelGGL((attn_kernel<HD, 1>), grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((attn_kernel<HD, 2>), grid, block, 0, st, a); break;
+    case 4: hipLaunchKernelGGL((attn_kernel<HD, 4>), grid, block, 0, st, a); break;
+    case 8: hipLaunchKernelGGL((attn_kernel<HD, 8>), grid, block, 0, st, a); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_attn(const AttnArgs &a, int head_dim, hipStream_t st) {
+    const int G = a.n_heads / a.n_kv_heads;
+    if (a.chunk > 256 || a.chunk <= 0) return hipErrorInvalidValue;
+    if (head_dim == 128) return launch_attn_hd<128>(a, G, st);
+    if (head_dim == 256 && G <= 4) return launch_attn_hd<256>(a, G, st);
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_embed(const DMat &emb, const int32_t *state, float *x, int32_t vocab, hipStream_t st) {
+    hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(WG), 0, st, emb, state, x, vocab);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant(const DMat &m, float *out, hipStream_t st) {
+    const long units = (long)m.rows * (m.cols / 64);
+    hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)((units + WG - 1) / WG)), dim3(WG), 0, st, m, out);
+    return hipGetLastError();
+}
+
+}  // namespace oi

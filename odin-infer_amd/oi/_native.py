@@ -1,0 +1,97 @@
+"""Loading of the native libraries built in-tree (odin-infer_amd/build.py)."""
+import ctypes
+import os
+
+PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_HIP = os.path.join(PKG, "liboi_hip.so")
+LIB_SYNTH = os.path.join(PKG, "liboi_synth.so")
+
+_hip = None
+_synth = None
+
+c_i32, c_i64, c_vp, c_f, c_d = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p, ctypes.c_float, ctypes.c_double
+
+
+class OIError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__("oi error %d: %s" % (code, msg))
+        self.code = code
+
+
+class Opts(ctypes.Structure):
+    _fields_ = [("max_ctx", c_i32), ("use_hip", c_i32), ("num_threads", c_i32), ("device", c_i32)]
+
+
+class Config(ctypes.Structure):
+    _fields_ = [("dim", c_i64), ("hidden_dim", c_i64), ("n_layers", c_i64), ("n_heads", c_i64),
+                ("n_kv_heads", c_i64), ("vocab_size", c_i64), ("seq_len", c_i64), ("max_seq", c_i64),
+                ("head_dim", c_i64), ("rope_freq", c_f), ("rms_eps", c_f)]
+
+
+# every symbol include/oi.h declares, with (restype, argtypes)
+HIP_SYMBOLS = {
+    "oi_engine_load": (c_i32, [ctypes.c_char_p, ctypes.POINTER(Opts), ctypes.POINTER(c_vp)]),
+    "oi_engine_destroy": (None, [c_vp]),
+    "oi_engine_forward": (ctypes.POINTER(c_f), [c_vp, c_i32, c_i32]),
+    "oi_engine_config": (c_i32, [c_vp, ctypes.POINTER(Config)]),
+    "oi_last_error": (ctypes.c_char_p, []),
+    "oi_engine_decode_greedy": (c_i32, [c_vp, c_i32, c_i32, c_i32, c_vp]),
+    "oi_engine_kv_fill": (c_i32, [c_vp, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp]),
+    "oi_engine_logits_device": (c_vp, [c_vp]),
+    "oi_engine_stream": (c_vp, [c_vp]),
+    "oi_engine_time_kernel": (c_i32, [c_vp, c_i32, c_i32, ctypes.POINTER(c_d), ctypes.POINTER(c_d)]),
+    "oi_dequant": (c_i32, [c_i32, c_vp, c_i64, c_vp]),
+    "oi_weights_upload": (c_i32, [c_i32, c_vp, c_i64, c_i64, ctypes.POINTER(c_vp)]),
+    "oi_weights_free": (None, [c_vp]),
+    "oi_weights_bytes": (c_i64, [c_vp]),
+    "oi_gemv_launch": (c_i32, [c_vp, c_vp, c_vp, c_vp]),
+    "oi_gemv": (c_i32, [c_i32, c_vp, c_i64, c_i64, c_vp, c_vp]),
+}
+
+
+class SynthSpec(ctypes.Structure):
+    _fields_ = [("dim", c_i64), ("hidden_dim", c_i64), ("n_layers", c_i64), ("n_heads", c_i64),
+                ("n_kv_heads", c_i64), ("head_dim", c_i64), ("vocab_size", c_i64), ("context_length", c_i64),
+                ("rope_theta", c_f), ("rms_eps", c_f), ("type_default", c_i32), ("type_attn_v", c_i32),
+                ("type_ffn_down", c_i32), ("type_embd", c_i32), ("type_output", c_i32), ("sigma", c_f),
+                ("norm_sigma", c_f), ("seed", ctypes.c_uint64), ("n_threads", c_i32)]
+
+
+SYNTH_SYMBOLS = {
+    "oi_synth_write_gguf": (c_i32, [ctypes.c_char_p, ctypes.POINTER(SynthSpec)]),
+    "oi_quantize_rows": (c_i32, [c_i32, c_vp, c_i64, c_i64, c_vp]),
+    "oi_synth_normal_f32": (None, [ctypes.c_uint64, c_i64, c_f, c_vp, c_i32]),
+    "oi_synth_normal_f16": (None, [ctypes.c_uint64, c_i64, c_f, c_vp, c_i32]),
+    "oi_synth_tensor_f32": (None, [ctypes.c_uint64, ctypes.c_char_p, c_i64, c_i64, c_f, c_f, c_vp, c_i32]),
+}
+
+
+def _bind(path, symbols):
+    if not os.path.exists(path):
+        raise OIError(-7, "native library %s is not built (run odin-infer_amd/build.py)" % path)
+    L = ctypes.CDLL(path)
+    for name, (res, args) in symbols.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+    return L
+
+
+def hip():
+    global _hip
+    if _hip is None:
+        _hip = _bind(LIB_HIP, HIP_SYMBOLS)
+    return _hip
+
+
+def synth():
+    global _synth
+    if _synth is None:
+        _synth = _bind(LIB_SYNTH, SYNTH_SYMBOLS)
+    return _synth
+
+
+def check(rc):
+    if rc != 0:
+        raise OIError(rc, hip().oi_last_error().decode())
+    return rc

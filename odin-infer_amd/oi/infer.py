@@ -1,0 +1,134 @@
+"""Engine API, mirroring the reference's `infer` package (infer/engine.odin:7-60).
+
+    e, ok = engine_load(path, Engine_Opts(max_ctx=4096, use_hip=True))
+    logits = engine_forward(e, token, pos)   # numpy view of engine memory
+    engine_destroy(e)
+
+Same names, argument meaning and error behaviour as the reference: the
+returned logits alias engine-owned memory valid until the next call
+(forward.odin:145); an out-of-range token or pos is fatal in the reference
+(forward.odin:22-29) and raises OIError(OI_E_RANGE) here.  The reference's
+silent CPU fallback when the GPU is missing (engine.odin:23-31) is not
+reproduced: engine_load raises instead.
+"""
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _native
+from ._native import OIError, check
+
+OI_E_RANGE = -6
+KERNELS = {"qkv": 0, "attn": 1, "wo": 2, "gateup": 3, "down": 4, "output": 5}
+
+
+@dataclass
+class Engine_Opts:
+    max_ctx: int = 4096
+    use_hip: bool = True
+    num_threads: int = 1
+    device: int = 0
+
+
+@dataclass
+class Config:
+    """infer/model.odin:12-24, same fields and order."""
+    dim: int
+    hidden_dim: int
+    n_layers: int
+    n_heads: int
+    n_kv_heads: int
+    vocab_size: int
+    seq_len: int
+    max_seq: int
+    head_dim: int
+    rope_freq: float
+    rms_eps: float
+
+
+class Engine:
+    def __init__(self, handle, config):
+        self._h = handle
+        self.config = config
+        self.hip_ready = True
+
+    @property
+    def handle(self):
+        if not self._h:
+            raise OIError(-1, "engine destroyed")
+        return self._h
+
+
+def engine_load(path, opts=None):
+    """infer/engine.odin:18-34. Returns (Engine, True); raises OIError."""
+    opts = opts or Engine_Opts()
+    L = _native.hip()
+    o = _native.Opts(int(opts.max_ctx), int(bool(opts.use_hip)), int(opts.num_threads), int(opts.device))
+    h = ctypes.c_void_p()
+    check(L.oi_engine_load(str(path).encode(), ctypes.byref(o), ctypes.byref(h)))
+    c = _native.Config()
+    check(L.oi_engine_config(h, ctypes.byref(c)))
+    cfg = Config(c.dim, c.hidden_dim, c.n_layers, c.n_heads, c.n_kv_heads, c.vocab_size, c.seq_len, c.max_seq,
+                 c.head_dim, c.rope_freq, c.rms_eps)
+    return Engine(h.value, cfg), True
+
+
+def engine_destroy(e):
+    """infer/engine.odin:36-43."""
+    if e._h:
+        _native.hip().oi_engine_destroy(e._h)
+        e._h = None
+
+
+def engine_forward(e, token, pos):
+    """infer/engine.odin:45-52: logits for `token` at `pos` (predicting pos+1)."""
+    p = _native.hip().oi_engine_forward(e.handle, int(token), int(pos))
+    if not p:
+        L = _native.hip()
+        raise OIError(OI_E_RANGE if "out of range" in L.oi_last_error().decode() else -7,
+                      L.oi_last_error().decode())
+    return np.ctypeslib.as_array(p, shape=(e.config.vocab_size,))
+
+
+def engine_config(e):
+    """infer/engine.odin:54-56."""
+    return e.config
+
+
+def engine_hip_ready(e):
+    """counterpart of engine_metal_ready (infer/engine.odin:58-60)."""
+    return bool(e._h) and e.hip_ready
+
+
+def engine_decode_greedy(e, token, pos, n_steps):
+    """Device-side greedy token loop; returns the n_steps picked ids."""
+    out = np.empty(n_steps, np.int32)
+    check(_native.hip().oi_engine_decode_greedy(e.handle, int(token), int(pos), int(n_steps), out.ctypes.data))
+    return out
+
+
+def engine_kv_fill(e, layer0, pos0, k16, v16):
+    """k16, v16: uint16 [nlayers][n_kv_heads][npos][head_dim] binary16 bits."""
+    k16 = np.ascontiguousarray(k16, np.uint16)
+    v16 = np.ascontiguousarray(v16, np.uint16)
+    nl, _, npos, _ = k16.shape
+    check(_native.hip().oi_engine_kv_fill(e.handle, int(layer0), nl, int(pos0), npos, k16.ctypes.data,
+                                          v16.ctypes.data))
+
+
+def engine_time_kernel(e, kernel, iters):
+    """(mean us per launch from HIP events, algorithmic bytes per launch)."""
+    us = ctypes.c_double()
+    b = ctypes.c_double()
+    check(_native.hip().oi_engine_time_kernel(e.handle, KERNELS[kernel], int(iters), ctypes.byref(us),
+                                              ctypes.byref(b)))
+    return us.value, b.value
+
+
+def engine_stream(e):
+    return _native.hip().oi_engine_stream(e.handle)
+
+
+def engine_logits_device(e):
+    return _native.hip().oi_engine_logits_device(e.handle)

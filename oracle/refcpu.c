@@ -1,0 +1,994 @@
+/*
+ * refcpu.c -- CPU restatement of the odin-infer reference's CPU token loop.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the parity oracle and the timed CPU
+ * baseline.  Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg may load it, and only as the checker.  The product library
+ * (odin-infer_amd/csrc) never links, loads or calls it.
+ *
+ * Each function cites the reference file:line it restates (paths relative to
+ * the vajraimb/odin-infer tree).  The Odin toolchain is absent, so the
+ * reference binary cannot be run; this restatement keeps the reference's
+ * evaluation order:
+ *   - dequant: separately rounded mul / mul / sub, no FMA (ggml/quant.odin:76-247)
+ *   - dot_f32: two 8-lane FMA accumulators, ordered lane sum (ggml/quant.odin:250-269)
+ *   - matmul_t: atomic per-row work queue over a thread pool, the caller
+ *     participates, one dequant scratch per thread (infer/matmul.odin:28-109)
+ *   - forward: infer/forward.odin:17-146
+ * Built with -ffp-contract=off so the compiler adds no FMA of its own.
+ *
+ * Pinning (what checks each function; the tests live in tests/test_oracle.py):
+ *   ref_f16_to_f32        all 65536 patterns vs numpy float16
+ *   ref_get_scale_min_k4  exhaustive over all 8 j and 2^12-bit patterns vs an
+ *                         independent bit-field model
+ *   ref_dequant_row       independent element-wise forms (the reference's
+ *                         k4_dequant_elem / k6_dequant_elem, qwen3_5/metal.odin:
+ *                         476-486, 542-555) restated in numpy; closed-form KATs;
+ *                         committed golden fixtures
+ *   ref_dot_f32           float64 brute force; exact small-integer cases
+ *   ref_matmul_t          float64 brute force; thread-count invariance
+ *   ref_rmsnorm           KAT [3,4] -> x/sqrt(12.5) (qwen3_5/tests.odin:127-139)
+ *   ref_softmax           closed form, float64
+ *   ref_argmax            ties go to the lowest index (sampler/sampler.odin:79-89)
+ *   forward               float64 re-computation of one layer on a tiny model;
+ *                         position-0 attention identity; committed logits fixture
+ * Bit-level equality with the Odin binary (its simd/libm lowering) stays
+ * unpinned: parity is stated at tolerance level (1e-3) and greedy ids.
+ */
+#define _GNU_SOURCE
+#include <errno.h>
+#include <fcntl.h>
+#include <math.h>
+#include <pthread.h>
+#include <sched.h>
+#include <stdatomic.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#define EXPORT __attribute__((visibility("default")))
+
+/* ggml type ids, ggml/gguf.odin:27-42 */
+enum {
+    T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q4_1 = 3, T_Q5_0 = 6, T_Q5_1 = 7,
+    T_Q8_0 = 8, T_Q8_1 = 9, T_Q2_K = 10, T_Q3_K = 11, T_Q4_K = 12,
+    T_Q5_K = 13, T_Q6_K = 14, T_Q8_K = 15
+};
+#define QK_K 256
+
+static char g_err[512];
+EXPORT const char *ref_last_error(void) { return g_err; }
+
+/* ---------------------------------------------------------------- quant --- */
+
+/* ggml/quant.odin:10-42 */
+EXPORT void ref_block_info(int k, int *elems, int *bytes) {
+    int e = 1, b = 4;
+    switch (k) {
+    case T_F32: e = 1; b = 4; break;
+    case T_F16: e = 1; b = 2; break;
+    case T_Q4_0: e = 32; b = 18; break;
+    case T_Q4_1: e = 32; b = 20; break;
+    case T_Q5_0: e = 32; b = 22; break;
+    case T_Q5_1: e = 32; b = 24; break;
+    case T_Q8_0: e = 32; b = 34; break;
+    case T_Q8_1: e = 32; b = 36; break;
+    case T_Q2_K: e = 256; b = 84; break;
+    case T_Q3_K: e = 256; b = 110; break;
+    case T_Q4_K: e = 256; b = 144; break;
+    case T_Q5_K: e = 256; b = 176; break;
+    case T_Q6_K: e = 256; b = 210; break;
+    case T_Q8_K: e = 256; b = 292; break;
+    default: break;
+    }
+    *elems = e;
+    *bytes = b;
+}
+
+/* ggml/quant.odin:44-47 */
+EXPORT int64_t ref_row_byte_size(int k, int64_t n) {
+    int e, b;
+    ref_block_info(k, &e, &b);
+    return (n / e) * b;
+}
+
+/* ggml/quant.odin:49-55 */
+EXPORT int ref_is_supported_quant(int k) {
+    switch (k) {
+    case T_F32: case T_F16: case T_Q8_0: case T_Q4_0: case T_Q4_1:
+    case T_Q5_0: case T_Q5_1: case T_Q4_K: case T_Q6_K:
+        return 1;
+    default:
+        return 0;
+    }
+}
+
+/* IEEE binary16 -> binary32, exact widening (ggml/quant.odin:58-61).
+ * Written from the format definition: 1 sign, 5 exponent (bias 15), 10 mantissa. */
+EXPORT float ref_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1Fu;
+    uint32_t man = h & 0x3FFu;
+    uint32_t bits;
+    if (exp == 0) {
+        if (man == 0) {
+            bits = sign;
+        } else { /* subnormal: value = man * 2^-24, renormalise */
+            int e = -1;
+            do { man <<= 1; e++; } while ((man & 0x400u) == 0);
+            man &= 0x3FFu;
+            bits = sign | ((uint32_t)(127 - 15 - e) << 23) | (man << 13);
+        }
+    } else if (exp == 31) {
+        bits = sign | 0x7F800000u | (man << 13); /* inf / nan, payload kept */
+    } else {
+        bits = sign | ((exp + 127 - 15) << 23) | (man << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+static inline float f16_at(const uint8_t *b) {
+    return ref_f16_to_f32((uint16_t)(b[0] | (b[1] << 8)));
+}
+
+/* binary32 -> binary16, round to nearest even (the f16 KV store of the
+ * reference's GPU path rounds this way: infer/metal.odin:443-454). */
+EXPORT uint16_t ref_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t ax = x & 0x7FFFFFFFu;
+    if (ax >= 0x7F800000u) /* inf or nan */
+        return (uint16_t)(sign | 0x7C00u | (ax > 0x7F800000u ? (0x200u | ((ax >> 13) & 0x3FFu)) : 0));
+    if (ax >= 0x477FF000u) /* rounds to >= 65520 -> inf */
+        return (uint16_t)(sign | 0x7C00u);
+    if (ax < 0x38800000u) { /* below 2^-14: subnormal or zero */
+        if (ax < 0x33000000u) return (uint16_t)sign; /* < 2^-25 rounds to 0 */
+        uint32_t e = ax >> 23;
+        uint32_t m = (ax & 0x7FFFFFu) | 0x800000u;
+        uint32_t shift = 126 - e; /* value = m * 2^(e-150); f16 unit 2^-24 */
+        uint32_t q = m >> (shift - 0);
+        /* q currently in units of 2^(e-150+shift) = 2^-24 */
+        uint32_t rem = m & ((1u << shift) - 1);
+        uint32_t half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (q & 1))) q++;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t e = (ax >> 23) - 127 + 15;
+    uint32_t m = ax & 0x7FFFFFu;
+    uint32_t q = (e << 10) | (m >> 13);
+    uint32_t rem = m & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (q & 1))) q++;
+    return (uint16_t)(sign | q);
+}
+
+/* ggml/quant.odin:64-73 */
+EXPORT void ref_get_scale_min_k4(int j, const uint8_t *q, uint8_t *sc, uint8_t *m) {
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *sc = (uint8_t)((q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4));
+        *m = (uint8_t)((q[j + 4] >> 4) | ((q[j] >> 6) << 4));
+    }
+}
+
+/* ggml/quant.odin:178-209 */
+static void dequant_q4_k(const uint8_t *src, int64_t n, float *dst) {
+    int64_t nsb = n / QK_K;
+    for (int64_t sb = 0; sb < nsb; sb++) {
+        const uint8_t *base = src + sb * 144;
+        float d = f16_at(base);
+        float dmin = f16_at(base + 2);
+        const uint8_t *scales = base + 4;
+        const uint8_t *qs = base + 16;
+        float *y = dst + sb * QK_K;
+        int is = 0;
+        for (int j = 0; j < QK_K; j += 64) {
+            uint8_t sc0, m0, sc1, m1;
+            ref_get_scale_min_k4(is + 0, scales, &sc0, &m0);
+            ref_get_scale_min_k4(is + 1, scales, &sc1, &m1);
+            float d1 = d * (float)sc0;
+            float mm1 = dmin * (float)m0;
+            float d2 = d * (float)sc1;
+            float mm2 = dmin * (float)m1;
+            for (int l = 0; l < 32; l++) y[l] = d1 * (float)(qs[l] & 0xF) - mm1;
+            for (int l = 0; l < 32; l++) y[32 + l] = d2 * (float)(qs[l] >> 4) - mm2;
+            qs += 32;
+            is += 2;
+            y += 64;
+        }
+    }
+}
+
+/* ggml/quant.odin:212-247 */
+static void dequant_q6_k(const uint8_t *src, int64_t n, float *dst) {
+    int64_t nsb = n / QK_K;
+    for (int64_t sb = 0; sb < nsb; sb++) {
+        const uint8_t *base = src + sb * 210;
+        const uint8_t *ql = base;
+        const uint8_t *qh = base + 128;
+        const int8_t *sc = (const int8_t *)(base + 192);
+        float d = f16_at(base + 208);
+        float *y = dst + sb * QK_K;
+        for (int h = 0; h < 2; h++) {
+            for (int l = 0; l < 32; l++) {
+                int is = l / 16;
+                int q1 = (int)((ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32;
+                int q2 = (int)((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                int q3 = (int)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                int q4 = (int)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                /* d * f32(sc) * f32(q): left to right, two roundings */
+                y[l] = d * (float)sc[is + 0] * (float)q1;
+                y[l + 32] = d * (float)sc[is + 2] * (float)q2;
+                y[l + 64] = d * (float)sc[is + 4] * (float)q3;
+                y[l + 96] = d * (float)sc[is + 6] * (float)q4;
+            }
+            ql += 64;
+            qh += 32;
+            sc += 8;
+            y += 128;
+        }
+    }
+}
+
+/* ggml/quant.odin:76-175 */
+EXPORT void ref_dequant_row(int k, const uint8_t *src, int64_t n, float *dst) {
+    switch (k) {
+    case T_F32:
+        memcpy(dst, src, (size_t)n * 4);
+        break;
+    case T_F16:
+        for (int64_t i = 0; i < n; i++) dst[i] = f16_at(src + 2 * i);
+        break;
+    case T_Q8_0: {
+        int64_t nb = n / 32;
+        for (int64_t b = 0; b < nb; b++) {
+            const uint8_t *base = src + b * 34;
+            float d = f16_at(base);
+            for (int j = 0; j < 32; j++) dst[b * 32 + j] = d * (float)(int8_t)base[2 + j];
+        }
+        break;
+    }
+    case T_Q4_0: {
+        int64_t nb = n / 32;
+        for (int64_t b = 0; b < nb; b++) {
+            const uint8_t *base = src + b * 18;
+            float d = f16_at(base);
+            const uint8_t *qs = base + 2;
+            for (int j = 0; j < 16; j++) {
+                float x0 = (float)((int32_t)(qs[j] & 0xF) - 8);
+                float x1 = (float)((int32_t)(qs[j] >> 4) - 8);
+                dst[b * 32 + j] = x0 * d;
+                dst[b * 32 + j + 16] = x1 * d;
+            }
+        }
+        break;
+    }
+    case T_Q4_1: {
+        int64_t nb = n / 32;
+        for (int64_t b = 0; b < nb; b++) {
+            const uint8_t *base = src + b * 20;
+            float d = f16_at(base);
+            float m = f16_at(base + 2);
+            const uint8_t *qs = base + 4;
+            for (int j = 0; j < 16; j++) {
+                dst[b * 32 + j] = (float)(qs[j] & 0xF) * d + m;
+                dst[b * 32 + j + 16] = (float)(qs[j] >> 4) * d + m;
+            }
+        }
+        break;
+    }
+    case T_Q5_0: {
+        int64_t nb = n / 32;
+        for (int64_t b = 0; b < nb; b++) {
+            const uint8_t *base = src + b * 22;
+            float d = f16_at(base);
+            uint32_t qh = (uint32_t)base[2] | (uint32_t)base[3] << 8 |
+                          (uint32_t)base[4] << 16 | (uint32_t)base[5] << 24;
+            const uint8_t *qs = base + 6;
+            for (int j = 0; j < 16; j++) {
+                uint8_t xh0 = (uint8_t)((qh >> j) << 4) & 0x10;
+                uint8_t xh1 = (uint8_t)(qh >> (j + 12)) & 0x10;
+                int32_t x0 = (int32_t)((qs[j] & 0xF) | xh0) - 16;
+                int32_t x1 = (int32_t)((qs[j] >> 4) | xh1) - 16;
+                dst[b * 32 + j] = (float)x0 * d;
+                dst[b * 32 + j + 16] = (float)x1 * d;
+            }
+        }
+        break;
+    }
+    case T_Q5_1: {
+        int64_t nb = n / 32;
+        for (int64_t b = 0; b < nb; b++) {
+            const uint8_t *base = src + b * 24;
+            float d = f16_at(base);
+            float m = f16_at(base + 2);
+            uint32_t qh = (uint32_t)base[4] | (uint32_t)base[5] << 8 |
+                          (uint32_t)base[6] << 16 | (uint32_t)base[7] << 24;
+            const uint8_t *qs = base + 8;
+            for (int j = 0; j < 16; j++) {
+                uint8_t xh0 = (uint8_t)((qh >> j) << 4) & 0x10;
+                uint8_t xh1 = (uint8_t)(qh >> (j + 12)) & 0x10;
+                int32_t x0 = (int32_t)((qs[j] & 0xF) | xh0);
+                int32_t x1 = (int32_t)((qs[j] >> 4) | xh1);
+                dst[b * 32 + j] = (float)x0 * d + m;
+                dst[b * 32 + j + 16] = (float)x1 * d + m;
+            }
+        }
+        break;
+    }
+    case T_Q4_K:
+        dequant_q4_k(src, n, dst);
+        break;
+    case T_Q6_K:
+        dequant_q6_k(src, n, dst);
+        break;
+    default: /* Q8_1, Q2_K, Q3_K, Q5_K, Q8_K: zero-filled (quant.odin:170-173) */
+        memset(dst, 0, (size_t)n * 4);
+        break;
+    }
+}
+
+/* ggml/quant.odin:250-269: acc0/acc1 are 8-lane vectors updated with FMA over
+ * 16-element steps; the lanes of acc0+acc1 are summed in order; scalar tail. */
+EXPORT float ref_dot_f32(const float *a, const float *b, int64_t n) {
+    float acc0[8] = {0}, acc1[8] = {0};
+    int64_t i = 0;
+    for (; i + 16 <= n; i += 16) {
+        for (int k = 0; k < 8; k++) acc0[k] = fmaf(a[i + k], b[i + k], acc0[k]);
+        for (int k = 0; k < 8; k++) acc1[k] = fmaf(a[i + 8 + k], b[i + 8 + k], acc1[k]);
+    }
+    float s[8];
+    for (int k = 0; k < 8; k++) s[k] = acc0[k] + acc1[k];
+    float sum = s[0];
+    for (int k = 1; k < 8; k++) sum = sum + s[k];
+    for (; i < n; i++) sum += a[i] * b[i];
+    return sum;
+}
+
+/* ggml/quant.odin:273-282 */
+static float dot_row(int k, const uint8_t *src, const float *x, int64_t n, float *scratch) {
+    if (k == T_F32) return ref_dot_f32((const float *)src, x, n);
+    ref_dequant_row(k, src, n, scratch);
+    return ref_dot_f32(scratch, x, n);
+}
+
+/* --------------------------------------------------------------- matmul --- */
+/* infer/matmul.odin:10-109.  A persistent pool of (n-1) workers plus the
+ * calling thread pull rows through one atomic counter; every row is computed
+ * by exactly one thread, so results do not depend on the thread count. */
+
+#define MAX_MATMUL_N 262144 /* per-thread scratch (qwen3_5/matmul.odin:10 size) */
+
+typedef struct {
+    int kind;
+    const uint8_t *w;
+    const float *x;
+    float *xout;
+    int64_t n, d, row_bytes;
+    atomic_long next_row;
+} mm_ctx;
+
+typedef struct {
+    int nthreads;
+    pthread_t *th;
+    float **scratch;
+    pthread_mutex_t mu;
+    pthread_cond_t cv;
+    long generation;
+    mm_ctx *job;
+    atomic_int outstanding;
+    int stop;
+} mm_pool;
+
+static void run_rows(mm_ctx *c, float *scratch) { /* infer/matmul.odin:63-70 */
+    for (;;) {
+        long row = atomic_fetch_add(&c->next_row, 1);
+        if (row >= c->d) break;
+        c->xout[row] = dot_row(c->kind, c->w + row * c->row_bytes, c->x, c->n, scratch);
+    }
+}
+
+typedef struct { mm_pool *p; int idx; } worker_arg;
+
+static void *worker_main(void *arg) {
+    worker_arg *wa = (worker_arg *)arg;
+    mm_pool *p = wa->p;
+    int idx = wa->idx;
+    free(wa);
+    long seen = 0;
+    for (;;) {
+        pthread_mutex_lock(&p->mu);
+        while (p->generation == seen && !p->stop) pthread_cond_wait(&p->cv, &p->mu);
+        if (p->stop) { pthread_mutex_unlock(&p->mu); break; }
+        seen = p->generation;
+        mm_ctx *job = p->job;
+        pthread_mutex_unlock(&p->mu);
+        run_rows(job, p->scratch[idx]);
+        atomic_fetch_sub(&p->outstanding, 1);
+    }
+    return NULL;
+}
+
+static mm_pool *pool_create(int nthreads) { /* infer/matmul.odin:32-46 */
+    mm_pool *p = (mm_pool *)calloc(1, sizeof(mm_pool));
+    p->nthreads = nthreads < 1 ? 1 : nthreads;
+    p->scratch = (float **)calloc((size_t)p->nthreads, sizeof(float *));
+    for (int i = 0; i < p->nthreads; i++) p->scratch[i] = (float *)malloc(MAX_MATMUL_N * sizeof(float));
+    pthread_mutex_init(&p->mu, NULL);
+    pthread_cond_init(&p->cv, NULL);
+    if (p->nthreads > 1) {
+        p->th = (pthread_t *)calloc((size_t)p->nthreads - 1, sizeof(pthread_t));
+        for (int i = 0; i < p->nthreads - 1; i++) {
+            worker_arg *wa = (worker_arg *)malloc(sizeof(worker_arg));
+            wa->p = p;
+            wa->idx = i;
+            pthread_create(&p->th[i], NULL, worker_main, wa);
+        }
+    }
+    return p;
+}
+
+static void pool_destroy(mm_pool *p) { /* infer/matmul.odin:48-61 */
+    if (!p) return;
+    pthread_mutex_lock(&p->mu);
+    p->stop = 1;
+    pthread_cond_broadcast(&p->cv);
+    pthread_mutex_unlock(&p->mu);
+    for (int i = 0; i < p->nthreads - 1; i++) pthread_join(p->th[i], NULL);
+    for (int i = 0; i < p->nthreads; i++) free(p->scratch[i]);
+    free(p->scratch);
+    free(p->th);
+    free(p);
+}
+
+/* xout[d] = W[d,n] * x[n]  (infer/matmul.odin:77-109) */
+static void matmul_t(mm_pool *p, float *xout, const float *x, int kind, const uint8_t *w,
+                     int64_t n, int64_t d) {
+    mm_ctx c;
+    c.kind = kind;
+    c.w = w;
+    c.x = x;
+    c.xout = xout;
+    c.n = n;
+    c.d = d;
+    c.row_bytes = ref_row_byte_size(kind, n);
+    atomic_init(&c.next_row, 0);
+    if (p->nthreads <= 1) {
+        run_rows(&c, p->scratch[0]);
+        return;
+    }
+    atomic_store(&p->outstanding, p->nthreads - 1);
+    pthread_mutex_lock(&p->mu);
+    p->job = &c;
+    p->generation++;
+    pthread_cond_broadcast(&p->cv);
+    pthread_mutex_unlock(&p->mu);
+    run_rows(&c, p->scratch[p->nthreads - 1]); /* caller uses the last slot */
+    while (atomic_load(&p->outstanding) > 0) sched_yield();
+}
+
+static mm_pool *g_pool;
+static int g_pool_threads;
+
+/* Standalone GEMV entry for the tests and the CPU microbench. */
+EXPORT int ref_matmul_t(float *xout, const float *x, int kind, const uint8_t *w, int64_t n,
+                        int64_t d, int nthreads) {
+    if (n > MAX_MATMUL_N) {
+        snprintf(g_err, sizeof g_err, "n=%lld exceeds MAX_MATMUL_N", (long long)n);
+        return -1;
+    }
+    if (!g_pool || g_pool_threads != nthreads) {
+        pool_destroy(g_pool);
+        g_pool = pool_create(nthreads);
+        g_pool_threads = nthreads;
+    }
+    matmul_t(g_pool, xout, x, kind, w, n, d);
+    return 0;
+}
+
+EXPORT void ref_pool_shutdown(void) {
+    pool_destroy(g_pool);
+    g_pool = NULL;
+    g_pool_threads = 0;
+}
+
+/* ------------------------------------------------------------------ ops --- */
+
+/* infer/ops.odin:7-19 */
+EXPORT void ref_rmsnorm(float *o, const float *x, const float *weight, int64_t size, float eps) {
+    float ss = 0.0f;
+    for (int64_t j = 0; j < size; j++) ss += x[j] * x[j];
+    ss /= (float)size;
+    ss += eps;
+    ss = 1.0f / sqrtf(ss);
+    for (int64_t j = 0; j < size; j++) o[j] = weight[j] * (ss * x[j]);
+}
+
+/* infer/ops.odin:21-37 */
+EXPORT void ref_softmax(float *x, int64_t n) {
+    if (n == 0) return;
+    float max_val = x[0];
+    for (int64_t i = 1; i < n; i++)
+        if (x[i] > max_val) max_val = x[i];
+    float sum = 0.0f;
+    for (int64_t i = 0; i < n; i++) {
+        x[i] = expf(x[i] - max_val);
+        sum += x[i];
+    }
+    for (int64_t i = 0; i < n; i++) x[i] /= sum;
+}
+
+/* sampler/sampler.odin:79-89: strict '>' so the lowest index wins ties */
+EXPORT int64_t ref_argmax(const float *p, int64_t n) {
+    int64_t max_i = 0;
+    float max_p = p[0];
+    for (int64_t i = 1; i < n; i++) {
+        if (p[i] > max_p) {
+            max_i = i;
+            max_p = p[i];
+        }
+    }
+    return max_i;
+}
+
+/* ----------------------------------------------------------------- gguf --- */
+/* ggml/gguf.odin:9-229 */
+
+enum { G_U8 = 0, G_I8, G_U16, G_I16, G_U32, G_I32, G_F32, G_BOOL, G_STR, G_ARR, G_U64, G_I64, G_F64 };
+
+typedef struct {
+    char key[96];
+    int type;
+    uint64_t u;
+    double f;
+    const char *str;
+    uint64_t str_len;
+} gmeta;
+
+typedef struct {
+    char name[96];
+    int kind;
+    int n_dims;
+    uint64_t dims[4];
+    uint64_t offset;
+    const uint8_t *data;
+    uint64_t size;
+} gtensor;
+
+typedef struct {
+    uint8_t *map;
+    size_t map_len;
+    gmeta *meta;
+    int n_meta;
+    gtensor *tensors;
+    int n_tensors;
+} gfile;
+
+typedef struct { const uint8_t *d; size_t len, pos; int bad; } rdr;
+
+static int need(rdr *r, size_t n) {
+    if (r->bad || r->pos + n > r->len) { r->bad = 1; return 0; }
+    return 1;
+}
+static uint64_t rd_le(rdr *r, int n) {
+    if (!need(r, (size_t)n)) return 0;
+    uint64_t v = 0;
+    for (int i = 0; i < n; i++) v |= (uint64_t)r->d[r->pos + i] << (8 * i);
+    r->pos += (size_t)n;
+    return v;
+}
+static const char *rd_str(rdr *r, uint64_t *len) {
+    uint64_t l = rd_le(r, 8);
+    if (!need(r, l)) return NULL;
+    const char *s = (const char *)r->d + r->pos;
+    r->pos += l;
+    *len = l;
+    return s;
+}
+static void skip_val(rdr *r, int t, int depth) { /* gguf.odin:113-133 */
+    if (depth > 4) { r->bad = 1; return; }
+    uint64_t l;
+    switch (t) {
+    case G_U8: case G_I8: case G_BOOL: rd_le(r, 1); break;
+    case G_U16: case G_I16: rd_le(r, 2); break;
+    case G_U32: case G_I32: case G_F32: rd_le(r, 4); break;
+    case G_U64: case G_I64: case G_F64: rd_le(r, 8); break;
+    case G_STR: rd_str(r, &l); break;
+    case G_ARR: {
+        int et = (int)rd_le(r, 4);
+        uint64_t c = rd_le(r, 8);
+        for (uint64_t i = 0; i < c && !r->bad; i++) skip_val(r, et, depth + 1);
+        break;
+    }
+    default: r->bad = 1; break;
+    }
+}
+
+static void gfile_free(gfile *g) {
+    if (g->map) munmap(g->map, g->map_len);
+    free(g->meta);
+    free(g->tensors);
+    memset(g, 0, sizeof *g);
+}
+
+static int gfile_open(const char *path, gfile *g) { /* gguf.odin:167-229 */
+    memset(g, 0, sizeof *g);
+    int fd = open(path, O_RDONLY);
+    if (fd < 0) { snprintf(g_err, sizeof g_err, "mmap failed for %s: %s", path, strerror(errno)); return -1; }
+    struct stat st;
+    fstat(fd, &st);
+    g->map_len = (size_t)st.st_size;
+    g->map = (uint8_t *)mmap(NULL, g->map_len, PROT_READ, MAP_PRIVATE, fd, 0);
+    close(fd);
+    if (g->map == MAP_FAILED) { g->map = NULL; snprintf(g_err, sizeof g_err, "mmap failed for %s", path); return -1; }
+    rdr r = {g->map, g->map_len, 0, 0};
+    uint32_t magic = (uint32_t)rd_le(&r, 4);
+    if (magic != 0x46554747u) { snprintf(g_err, sizeof g_err, "not a GGUF file (magic=0x%x)", magic); return -2; }
+    uint32_t version = (uint32_t)rd_le(&r, 4);
+    if (version != 2 && version != 3) { snprintf(g_err, sizeof g_err, "unsupported GGUF version %u", version); return -3; }
+    uint64_t tc = rd_le(&r, 8), mc = rd_le(&r, 8);
+    if (tc > 1000000 || mc > 1000000) { snprintf(g_err, sizeof g_err, "corrupt GGUF header"); return -4; }
+    g->meta = (gmeta *)calloc(mc ? mc : 1, sizeof(gmeta));
+    for (uint64_t i = 0; i < mc && !r.bad; i++) {
+        gmeta *m = &g->meta[g->n_meta++];
+        uint64_t kl;
+        const char *k = rd_str(&r, &kl);
+        if (!k) break;
+        snprintf(m->key, sizeof m->key, "%.*s", (int)kl, k);
+        m->type = (int)rd_le(&r, 4);
+        switch (m->type) { /* gguf.odin:135-161 */
+        case G_U8: case G_I8: case G_BOOL: m->u = rd_le(&r, 1); break;
+        case G_U16: case G_I16: m->u = rd_le(&r, 2); break;
+        case G_U32: case G_I32: m->u = rd_le(&r, 4); break;
+        case G_U64: case G_I64: m->u = rd_le(&r, 8); break;
+        case G_F32: { uint32_t b = (uint32_t)rd_le(&r, 4); float f; memcpy(&f, &b, 4); m->f = f; break; }
+        case G_F64: { uint64_t b = rd_le(&r, 8); memcpy(&m->f, &b, 8); break; }
+        case G_STR: m->str = rd_str(&r, &m->str_len); break;
+        case G_ARR: {
+            int et = (int)rd_le(&r, 4);
+            uint64_t c = rd_le(&r, 8);
+            for (uint64_t j = 0; j < c && !r.bad; j++) skip_val(&r, et, 1);
+            break;
+        }
+        default: r.bad = 1; break;
+        }
+    }
+    g->tensors = (gtensor *)calloc(tc ? tc : 1, sizeof(gtensor));
+    for (uint64_t i = 0; i < tc && !r.bad; i++) {
+        gtensor *t = &g->tensors[g->n_tensors++];
+        uint64_t nl;
+        const char *nm = rd_str(&r, &nl);
+        if (!nm) break;
+        snprintf(t->name, sizeof t->name, "%.*s", (int)nl, nm);
+        t->n_dims = (int)rd_le(&r, 4);
+        if (t->n_dims < 1 || t->n_dims > 4) { r.bad = 1; break; }
+        for (int d = 0; d < t->n_dims; d++) t->dims[d] = rd_le(&r, 8);
+        t->kind = (int)rd_le(&r, 4);
+        t->offset = rd_le(&r, 8);
+    }
+    if (r.bad) { snprintf(g_err, sizeof g_err, "truncated or corrupt GGUF"); return -5; }
+    uint64_t alignment = 32;
+    for (int i = 0; i < g->n_meta; i++)
+        if (!strcmp(g->meta[i].key, "general.alignment")) alignment = g->meta[i].u;
+    if (alignment == 0 || (alignment & (alignment - 1))) { snprintf(g_err, sizeof g_err, "bad alignment"); return -6; }
+    uint64_t data_base = (r.pos + alignment - 1) & ~(alignment - 1);
+    for (int i = 0; i < g->n_tensors; i++) {
+        gtensor *t = &g->tensors[i];
+        uint64_t ne = 1;
+        for (int d = 0; d < t->n_dims; d++) ne *= t->dims[d];
+        t->size = (uint64_t)ref_row_byte_size(t->kind, (int64_t)ne);
+        uint64_t start = data_base + t->offset;
+        if (start + t->size > g->map_len) {
+            snprintf(g_err, sizeof g_err, "tensor %s extends past end of file", t->name);
+            return -7;
+        }
+        t->data = g->map + start;
+    }
+    return 0;
+}
+
+static gmeta *gmeta_get(gfile *g, const char *k) {
+    for (int i = 0; i < g->n_meta; i++)
+        if (!strcmp(g->meta[i].key, k)) return &g->meta[i];
+    return NULL;
+}
+static gtensor *gtensor_get(gfile *g, const char *k) {
+    for (int i = 0; i < g->n_tensors; i++)
+        if (!strcmp(g->tensors[i].name, k)) return &g->tensors[i];
+    return NULL;
+}
+
+/* ---------------------------------------------------------------- model --- */
+/* infer/model.odin:12-242 */
+
+typedef struct { int kind; const uint8_t *data; } tensor;
+
+typedef struct {
+    const float *attn_norm, *ffn_norm, *q_norm, *k_norm;
+    tensor wq, wk, wv, wo, w1, w2, w3;
+} layer_w;
+
+typedef struct {
+    /* Config, field order of infer/model.odin:12-24 */
+    int64_t dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, seq_len, max_seq, head_dim;
+    float rope_freq, rms_eps;
+    tensor token_embedding, output;
+    const float *output_norm;
+    layer_w *layers;
+    /* Run_State, infer/model.odin:53-65 */
+    float *x, *xb, *xb2, *xb3, *hb, *hb2, *q, *att, *logits, *key_cache, *value_cache;
+    float *ktmp, *vtmp;
+    int kv_f16;
+    gfile g;
+    mm_pool *pool;
+} ref_engine;
+
+static int require(ref_engine *e, const char *name, gtensor **out) { /* model.odin:82-97 */
+    gtensor *t = gtensor_get(&e->g, name);
+    if (!t) { snprintf(g_err, sizeof g_err, "missing required tensor: %s", name); return -10; }
+    if (!ref_is_supported_quant(t->kind)) {
+        snprintf(g_err, sizeof g_err, "tensor %s has unsupported quant type %d", name, t->kind);
+        return -11;
+    }
+    *out = t;
+    return 0;
+}
+
+static int as_f32(ref_engine *e, const char *name, const float **out) { /* model.odin:74-80 */
+    gtensor *t;
+    int rc = require(e, name, &t);
+    if (rc) return rc;
+    if (t->kind != T_F32) { snprintf(g_err, sizeof g_err, "expected F32 tensor for %s", name); return -12; }
+    *out = (const float *)t->data;
+    return 0;
+}
+
+EXPORT void ref_engine_destroy(void *h) {
+    ref_engine *e = (ref_engine *)h;
+    if (!e) return;
+    free(e->x); free(e->xb); free(e->xb2); free(e->xb3); free(e->hb); free(e->hb2);
+    free(e->q); free(e->att); free(e->logits); free(e->key_cache); free(e->value_cache);
+    free(e->ktmp); free(e->vtmp);
+    free(e->layers);
+    pool_destroy(e->pool);
+    gfile_free(&e->g);
+    free(e);
+}
+
+/* engine_load (infer/engine.odin:18-34) -> build_transformer (model.odin:216-242).
+ * kv_f16 != 0 selects the f16 KV mode: K and V at each position are rounded to
+ * binary16 (round-to-nearest-even) when stored, as the reference GPU path's
+ * store_kv does (infer/metal.odin:443-454), and attention reads them back. */
+EXPORT void *ref_engine_load(const char *path, int max_ctx, int num_threads, int kv_f16) {
+    ref_engine *e = (ref_engine *)calloc(1, sizeof(ref_engine));
+    int rc = gfile_open(path, &e->g);
+    if (rc) { ref_engine_destroy(e); return NULL; }
+    gfile *g = &e->g;
+    /* load_config, model.odin:99-139 */
+    const char *keys[7] = {"qwen3.embedding_length", "qwen3.feed_forward_length", "qwen3.block_count",
+                           "qwen3.attention.head_count", "qwen3.attention.head_count_kv",
+                           "qwen3.context_length", "qwen3.attention.key_length"};
+    int64_t vals[7];
+    for (int i = 0; i < 7; i++) {
+        gmeta *m = gmeta_get(g, keys[i]);
+        if (!m) { snprintf(g_err, sizeof g_err, "missing metadata key: %s", keys[i]); ref_engine_destroy(e); return NULL; }
+        vals[i] = (int64_t)m->u;
+    }
+    e->dim = vals[0]; e->hidden_dim = vals[1]; e->n_layers = vals[2]; e->n_heads = vals[3];
+    e->n_kv_heads = vals[4]; e->max_seq = vals[5]; e->head_dim = vals[6];
+    gmeta *m = gmeta_get(g, "qwen3.rope.freq_base");
+    e->rope_freq = m ? (float)m->f : 1000000.0f;
+    m = gmeta_get(g, "qwen3.attention.layer_norm_rms_epsilon");
+    e->rms_eps = m ? (float)m->f : 1e-6f;
+    gtensor *emb;
+    if (require(e, "token_embd.weight", &emb)) { ref_engine_destroy(e); return NULL; }
+    e->vocab_size = (int64_t)emb->dims[emb->n_dims - 1];
+    /* model.odin:220-223 */
+    e->seq_len = e->max_seq < max_ctx ? e->max_seq : max_ctx;
+    if (e->seq_len <= 0) e->seq_len = max_ctx;
+    /* memory_map_weights, model.odin:141-179 */
+    e->token_embedding = (tensor){emb->kind, emb->data};
+    if (as_f32(e, "output_norm.weight", &e->output_norm)) { ref_engine_destroy(e); return NULL; }
+    gtensor *out = gtensor_get(g, "output.weight");
+    if (out) {
+        if (!ref_is_supported_quant(out->kind)) {
+            snprintf(g_err, sizeof g_err, "output.weight has unsupported quant type %d", out->kind);
+            ref_engine_destroy(e);
+            return NULL;
+        }
+        e->output = (tensor){out->kind, out->data};
+    } else {
+        e->output = e->token_embedding; /* tied classifier */
+    }
+    e->layers = (layer_w *)calloc((size_t)e->n_layers, sizeof(layer_w));
+    char nm[96];
+    for (int64_t l = 0; l < e->n_layers; l++) {
+        layer_w *lw = &e->layers[l];
+        int bad = 0;
+#define F32W(field, suffix) snprintf(nm, sizeof nm, "blk.%lld." suffix, (long long)l); bad |= as_f32(e, nm, &lw->field);
+#define QW(field, suffix) { gtensor *t_; snprintf(nm, sizeof nm, "blk.%lld." suffix, (long long)l); \
+        if (require(e, nm, &t_)) bad = 1; else lw->field = (tensor){t_->kind, t_->data}; }
+        F32W(attn_norm, "attn_norm.weight")
+        F32W(ffn_norm, "ffn_norm.weight")
+        F32W(q_norm, "attn_q_norm.weight")
+        F32W(k_norm, "attn_k_norm.weight")
+        QW(wq, "attn_q.weight")
+        QW(wk, "attn_k.weight")
+        QW(wv, "attn_v.weight")
+        QW(wo, "attn_output.weight")
+        QW(w1, "ffn_gate.weight")
+        QW(w2, "ffn_down.weight")
+        QW(w3, "ffn_up.weight")
+#undef F32W
+#undef QW
+        if (bad) { ref_engine_destroy(e); return NULL; }
+    }
+    /* malloc_run_state, model.odin:185-200 */
+    int64_t att_head_dim = e->n_heads * e->head_dim, kv_dim = e->n_kv_heads * e->head_dim;
+    e->x = (float *)calloc((size_t)e->dim, 4);
+    e->xb = (float *)calloc((size_t)e->dim, 4);
+    e->xb2 = (float *)calloc((size_t)e->dim, 4);
+    e->xb3 = (float *)calloc((size_t)att_head_dim, 4);
+    e->hb = (float *)calloc((size_t)e->hidden_dim, 4);
+    e->hb2 = (float *)calloc((size_t)e->hidden_dim, 4);
+    e->q = (float *)calloc((size_t)att_head_dim, 4);
+    e->att = (float *)calloc((size_t)(e->n_heads * e->seq_len), 4);
+    e->logits = (float *)calloc((size_t)e->vocab_size, 4);
+    e->key_cache = (float *)calloc((size_t)(e->n_layers * e->seq_len * kv_dim), 4);
+    e->value_cache = (float *)calloc((size_t)(e->n_layers * e->seq_len * kv_dim), 4);
+    e->ktmp = (float *)calloc((size_t)kv_dim, 4);
+    e->vtmp = (float *)calloc((size_t)kv_dim, 4);
+    if (!e->key_cache || !e->value_cache) { snprintf(g_err, sizeof g_err, "KV cache allocation failed"); ref_engine_destroy(e); return NULL; }
+    e->kv_f16 = kv_f16;
+    e->pool = pool_create(num_threads < 1 ? 1 : num_threads); /* engine.odin:20 */
+    return e;
+}
+
+/* Config fields in infer/model.odin:12-24 order; floats returned as doubles. */
+EXPORT void ref_engine_config(void *h, int64_t *ints9, float *floats2) {
+    ref_engine *e = (ref_engine *)h;
+    int64_t v[9] = {e->dim, e->hidden_dim, e->n_layers, e->n_heads, e->n_kv_heads,
+                    e->vocab_size, e->seq_len, e->max_seq, e->head_dim};
+    memcpy(ints9, v, sizeof v);
+    floats2[0] = e->rope_freq;
+    floats2[1] = e->rms_eps;
+}
+
+/* Overwrite positions [pos0, pos0+npos) of one layer's K and V with given
+ * binary16 values laid out [kv_head][npos][head_dim]. */
+EXPORT int ref_engine_kv_fill(void *h, int layer, int pos0, int npos, const uint16_t *k16, const uint16_t *v16) {
+    ref_engine *e = (ref_engine *)h;
+    if (layer < 0 || layer >= e->n_layers || pos0 < 0 || npos < 0 || pos0 + npos > e->seq_len) {
+        snprintf(g_err, sizeof g_err, "kv_fill out of range");
+        return -1;
+    }
+    int64_t kv_dim = e->n_kv_heads * e->head_dim, hd = e->head_dim;
+    int64_t loff = (int64_t)layer * e->seq_len * kv_dim;
+    for (int64_t kh = 0; kh < e->n_kv_heads; kh++)
+        for (int64_t t = 0; t < npos; t++)
+            for (int64_t i = 0; i < hd; i++) {
+                int64_t src = (kh * npos + t) * hd + i;
+                int64_t dst = loff + (pos0 + t) * kv_dim + kh * hd + i;
+                e->key_cache[dst] = ref_f16_to_f32(k16[src]);
+                e->value_cache[dst] = ref_f16_to_f32(v16[src]);
+            }
+    return 0;
+}
+
+/* forward (infer/forward.odin:17-146).  Returns the engine-owned logits, or
+ * NULL (with ref_last_error) where the reference prints and exits. */
+EXPORT const float *ref_engine_forward(void *h, int token, int pos) {
+    ref_engine *e = (ref_engine *)h;
+    if (pos < 0 || pos >= e->seq_len) {
+        snprintf(g_err, sizeof g_err, "forward: pos=%d out of range (seq_len=%lld)", pos, (long long)e->seq_len);
+        return NULL;
+    }
+    if (token < 0 || token >= e->vocab_size) {
+        snprintf(g_err, sizeof g_err, "forward: token=%d out of range (vocab=%lld)", token, (long long)e->vocab_size);
+        return NULL;
+    }
+    int64_t dim = e->dim, hidden_dim = e->hidden_dim, head_dim = e->head_dim, n_heads = e->n_heads;
+    int64_t n_kv_heads = e->n_kv_heads, seq_len = e->seq_len, kv_dim = n_kv_heads * head_dim;
+    int64_t kv_mul = n_heads / n_kv_heads, att_head_dim = n_heads * head_dim;
+    float eps = e->rms_eps;
+    mm_pool *P = e->pool;
+
+    /* get_embedding_row, forward.odin:12-15 */
+    int64_t rb = ref_row_byte_size(e->token_embedding.kind, dim);
+    ref_dequant_row(e->token_embedding.kind, e->token_embedding.data + (int64_t)token * rb, dim, e->x);
+
+    for (int64_t l = 0; l < e->n_layers; l++) {
+        layer_w *lw = &e->layers[l];
+        int64_t loff = l * seq_len * kv_dim;
+        float *k_slice = e->key_cache + loff + (int64_t)pos * kv_dim;
+        float *v_slice = e->value_cache + loff + (int64_t)pos * kv_dim;
+        /* in f16 mode K/V are formed in f32 temporaries and rounded on store */
+        float *kk = e->kv_f16 ? e->ktmp : k_slice;
+        float *vv = e->kv_f16 ? e->vtmp : v_slice;
+
+        ref_rmsnorm(e->xb, e->x, lw->attn_norm, dim, eps);
+        matmul_t(P, e->q, e->xb, lw->wq.kind, lw->wq.data, dim, att_head_dim);
+        matmul_t(P, kk, e->xb, lw->wk.kind, lw->wk.data, dim, kv_dim);
+        matmul_t(P, vv, e->xb, lw->wv.kind, lw->wv.data, dim, kv_dim);
+
+        /* RoPE + per-head Q/K RMSNorm, forward.odin:57-85 */
+        for (int64_t h = 0; h < n_heads; h++) {
+            float *q = e->q + h * head_dim;
+            ref_rmsnorm(q, q, lw->q_norm, head_dim, eps);
+            if (h < n_kv_heads) {
+                float *k = kk + h * head_dim;
+                ref_rmsnorm(k, k, lw->k_norm, head_dim, eps);
+            }
+            for (int64_t i = 0; i < head_dim / 2; i++) {
+                float freq = 1.0f / powf(e->rope_freq, (float)i / (float)(head_dim / 2));
+                float fcr = cosf((float)pos * freq);
+                float fci = sinf((float)pos * freq);
+                float x_q = q[i], y_q = q[i + head_dim / 2];
+                q[i] = x_q * fcr - y_q * fci;
+                q[i + head_dim / 2] = x_q * fci + y_q * fcr;
+                if (h < n_kv_heads) {
+                    float *k = kk + h * head_dim;
+                    float x_k = k[i], y_k = k[i + head_dim / 2];
+                    k[i] = x_k * fcr - y_k * fci;
+                    k[i + head_dim / 2] = x_k * fci + y_k * fcr;
+                }
+            }
+        }
+        if (e->kv_f16) {
+            for (int64_t i = 0; i < kv_dim; i++) {
+                k_slice[i] = ref_f16_to_f32(ref_f32_to_f16(kk[i]));
+                v_slice[i] = ref_f16_to_f32(ref_f32_to_f16(vv[i]));
+            }
+        }
+
+        /* multihead attention, forward.odin:87-115 */
+        for (int64_t h = 0; h < n_heads; h++) {
+            float *q = e->q + h * head_dim;
+            float *att = e->att + h * seq_len;
+            for (int64_t t = 0; t <= pos; t++) {
+                const float *k = e->key_cache + loff + t * kv_dim + (h / kv_mul) * head_dim;
+                float score = 0.0f;
+                for (int64_t i = 0; i < head_dim; i++) score += q[i] * k[i];
+                att[t] = score / sqrtf((float)head_dim);
+            }
+            ref_softmax(att, (int64_t)pos + 1);
+            float *xb3 = e->xb3 + h * head_dim;
+            for (int64_t i = 0; i < head_dim; i++) xb3[i] = 0.0f;
+            for (int64_t t = 0; t <= pos; t++) {
+                const float *v = e->value_cache + loff + t * kv_dim + (h / kv_mul) * head_dim;
+                float a = att[t];
+                for (int64_t i = 0; i < head_dim; i++) xb3[i] += a * v[i];
+            }
+        }
+
+        matmul_t(P, e->xb2, e->xb3, lw->wo.kind, lw->wo.data, att_head_dim, dim);
+        for (int64_t i = 0; i < dim; i++) e->x[i] += e->xb2[i];
+
+        ref_rmsnorm(e->xb, e->x, lw->ffn_norm, dim, eps);
+        matmul_t(P, e->hb, e->xb, lw->w1.kind, lw->w1.data, dim, hidden_dim);
+        matmul_t(P, e->hb2, e->xb, lw->w3.kind, lw->w3.data, dim, hidden_dim);
+        for (int64_t i = 0; i < hidden_dim; i++) { /* forward.odin:128-133 */
+            float val = e->hb[i];
+            val *= 1.0f / (1.0f + expf(-val));
+            val *= e->hb2[i];
+            e->hb2[i] = val;
+        }
+        matmul_t(P, e->xb, e->hb2, lw->w2.kind, lw->w2.data, hidden_dim, dim);
+        for (int64_t i = 0; i < dim; i++) e->x[i] += e->xb[i];
+    }
+
+    ref_rmsnorm(e->x, e->x, e->output_norm, dim, eps);
+    matmul_t(P, e->logits, e->x, e->output.kind, e->output.data, dim, e->vocab_size);
+    return e->logits;
+}
+
+/* Hidden state after the final norm (test hook for layer-level checks). */
+EXPORT const float *ref_engine_hidden(void *h) { return ((ref_engine *)h)->x; }

@@ -1,0 +1,160 @@
+"""ctypes wrapper of the CPU oracle (oracle/refcpu.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, as the checker.  The product never imports it.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "librefcpu.so")
+
+_lib = None
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        c_i64, c_int, c_vp, c_f = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_float
+        L.ref_last_error.restype = ctypes.c_char_p
+        L.ref_row_byte_size.restype = c_i64
+        L.ref_row_byte_size.argtypes = [c_int, c_i64]
+        L.ref_block_info.argtypes = [c_int, c_vp, c_vp]
+        L.ref_is_supported_quant.argtypes = [c_int]
+        L.ref_f16_to_f32.restype = c_f
+        L.ref_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.ref_f32_to_f16.restype = ctypes.c_uint16
+        L.ref_f32_to_f16.argtypes = [c_f]
+        L.ref_get_scale_min_k4.argtypes = [c_int, c_vp, c_vp, c_vp]
+        L.ref_dequant_row.argtypes = [c_int, c_vp, c_i64, c_vp]
+        L.ref_dot_f32.restype = c_f
+        L.ref_dot_f32.argtypes = [c_vp, c_vp, c_i64]
+        L.ref_matmul_t.argtypes = [c_vp, c_vp, c_int, c_vp, c_i64, c_i64, c_int]
+        L.ref_rmsnorm.argtypes = [c_vp, c_vp, c_vp, c_i64, c_f]
+        L.ref_softmax.argtypes = [c_vp, c_i64]
+        L.ref_argmax.restype = c_i64
+        L.ref_argmax.argtypes = [c_vp, c_i64]
+        L.ref_engine_load.restype = c_vp
+        L.ref_engine_load.argtypes = [ctypes.c_char_p, c_int, c_int, c_int]
+        L.ref_engine_forward.restype = ctypes.POINTER(c_f)
+        L.ref_engine_forward.argtypes = [c_vp, c_int, c_int]
+        L.ref_engine_destroy.argtypes = [c_vp]
+        L.ref_engine_config.argtypes = [c_vp, c_vp, c_vp]
+        L.ref_engine_kv_fill.argtypes = [c_vp, c_int, c_int, c_int, c_vp, c_vp]
+        L.ref_engine_hidden.restype = ctypes.POINTER(c_f)
+        L.ref_engine_hidden.argtypes = [c_vp]
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data
+
+
+def row_byte_size(kind, n):
+    return lib().ref_row_byte_size(kind, n)
+
+
+def dequant_row(kind, blocks, n):
+    out = np.empty(n, np.float32)
+    src = np.ascontiguousarray(blocks, dtype=np.uint8)
+    lib().ref_dequant_row(kind, _p(src), n, _p(out))
+    return out
+
+
+def dot_f32(a, b):
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    return lib().ref_dot_f32(_p(a), _p(b), len(a))
+
+
+def matmul_t(w_blocks, kind, x, d, nthreads=1):
+    """xout[d] = W[d, n] . x[n] (infer/matmul.odin:77-109)."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w_blocks, np.uint8)
+    out = np.empty(d, np.float32)
+    rc = lib().ref_matmul_t(_p(out), _p(x), kind, _p(w), len(x), d, nthreads)
+    if rc:
+        raise RuntimeError(lib().ref_last_error().decode())
+    return out
+
+
+def rmsnorm(x, w, eps):
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    o = np.empty_like(x)
+    lib().ref_rmsnorm(_p(o), _p(x), _p(w), len(x), eps)
+    return o
+
+
+def softmax(x):
+    x = np.array(x, np.float32)
+    lib().ref_softmax(_p(x), len(x))
+    return x
+
+
+def argmax(p):
+    p = np.ascontiguousarray(p, np.float32)
+    return int(lib().ref_argmax(_p(p), len(p)))
+
+
+def get_scale_min_k4(j, q12):
+    q = np.ascontiguousarray(q12, np.uint8)
+    sc = ctypes.c_uint8()
+    m = ctypes.c_uint8()
+    lib().ref_get_scale_min_k4(j, _p(q), ctypes.byref(sc), ctypes.byref(m))
+    return sc.value, m.value
+
+
+class RefEngine:
+    """The reference CPU forward (infer/engine.odin + infer/forward.odin).
+
+    kv_f16=True rounds K/V to binary16 on store, as the reference GPU path's
+    f16 cache does (infer/metal.odin:443-454)."""
+
+    def __init__(self, path, max_ctx=4096, num_threads=1, kv_f16=False):
+        self.h = lib().ref_engine_load(path.encode(), max_ctx, num_threads, int(kv_f16))
+        if not self.h:
+            raise RuntimeError("oracle load failed: " + lib().ref_last_error().decode())
+        ints = (ctypes.c_int64 * 9)()
+        fl = (ctypes.c_float * 2)()
+        lib().ref_engine_config(self.h, ints, fl)
+        (self.dim, self.hidden_dim, self.n_layers, self.n_heads, self.n_kv_heads, self.vocab_size,
+         self.seq_len, self.max_seq, self.head_dim) = list(ints)
+        self.rope_freq, self.rms_eps = fl[0], fl[1]
+
+    def forward(self, token, pos):
+        p = lib().ref_engine_forward(self.h, token, pos)
+        if not p:
+            raise RuntimeError(lib().ref_last_error().decode())
+        return np.ctypeslib.as_array(p, shape=(self.vocab_size,)).copy()
+
+    def kv_fill(self, layer, pos0, k16, v16):
+        """k16, v16: uint16 [n_kv_heads][npos][head_dim] for one layer."""
+        k16 = np.ascontiguousarray(k16, np.uint16)
+        v16 = np.ascontiguousarray(v16, np.uint16)
+        npos = k16.shape[1]
+        rc = lib().ref_engine_kv_fill(self.h, layer, pos0, npos, _p(k16), _p(v16))
+        if rc:
+            raise RuntimeError(lib().ref_last_error().decode())
+
+    def close(self):
+        if self.h:
+            lib().ref_engine_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,46 @@
+"""Shared helpers for the tests."""
+import numpy as np
+
+
+def scaled_err(got, ref):
+    """max|got-ref| / max|ref| -- the error measure of the reference's GEMM
+    harness (gemm_harness/gemm_test.odin:885-888)."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float(np.max(np.abs(got - ref)) / max(np.max(np.abs(ref)), 1e-30))
+
+
+def random_blocks(kind, nblocks, rng):
+    """Random bytes for `nblocks` blocks of `kind`, with the f16 scale fields
+    set to finite values of assorted magnitude (any byte pattern is a valid
+    block for dequant; finite scales keep comparisons free of inf/nan)."""
+    e, b = {8: (32, 34), 12: (256, 144), 14: (256, 210), 1: (1, 2), 0: (1, 4)}[kind]
+    raw = rng.integers(0, 256, size=(nblocks, b), dtype=np.uint8)
+
+    def f16_field(n):
+        mag = rng.choice([1e-6, 1e-4, 1e-3, 0.01, 0.1, 1.0, 100.0], size=n)
+        v = (rng.standard_normal(n) * mag).astype(np.float16)
+        v[rng.random(n) < 0.05] = 0
+        return v.view(np.uint16)
+
+    if kind == 8:
+        raw[:, 0:2] = f16_field(nblocks).view(np.uint8).reshape(nblocks, 2)
+    elif kind == 12:
+        raw[:, 0:2] = f16_field(nblocks).view(np.uint8).reshape(nblocks, 2)
+        raw[:, 2:4] = f16_field(nblocks).view(np.uint8).reshape(nblocks, 2)
+    elif kind == 14:
+        raw[:, 208:210] = f16_field(nblocks).view(np.uint8).reshape(nblocks, 2)
+    elif kind == 1:
+        v = (rng.standard_normal(nblocks) * 3).astype(np.float16)
+        raw = v.view(np.uint8).reshape(nblocks, 2)
+    elif kind == 0:
+        v = rng.standard_normal(nblocks).astype(np.float32)
+        raw = v.view(np.uint8).reshape(nblocks, 4)
+    return raw.reshape(-1)
+
+
+def same_bits(a, b):
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    na, nb = np.isnan(a), np.isnan(b)
+    return bool(np.array_equal(na, nb) and np.array_equal(a[~na].view(np.uint32), b[~nb].view(np.uint32)))
