@@ -1,0 +1,191 @@
+#!/usr/bin/env python3
+"""Decode throughput of the token loop on one MI355X.
+
+Workload (the measured configuration): Qwen3-8B-shaped dense decoder,
+Q4_K_M-style weights (Q4_K, Q6_K for attn_v and output), f16 KV cache
+pre-filled with N(0,1) to context 4096, then greedy decode at batch 1 from
+position 4096.  A step is one token of the device-side greedy loop
+(oi_engine_decode_greedy): embedding, 36 layers, logits, argmax.
+
+Prints one JSON line.  `roofline` is for the dominant kernel (gate/up GEMV),
+timed with HIP events on the engine's stream; `token_loop` gives the whole
+step's algorithmic HBM bytes and rate.  `cpu_baseline` times the CPU oracle
+(oracle/refcpu.c, the restated reference CPU forward) on a bounded sample of
+the same workload and checks its greedy ids against the GPU's.
+
+usage: python bench.py [--gpus 1] [--steps 512] [--warmup 16]
+"""
+import argparse
+import json
+import os
+import shutil
+import sys
+import tempfile
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "odin-infer_amd"))
+
+PEAK_HBM_GBPS = 8000.0
+METRIC = "decode tok/s @bs1 Qwen3-8B-shape Q4_K; achieved HBM GB/s as % of peak"
+CONTEXT = 4096
+MODEL = "qwen3-8b-q4_k_m"
+
+
+def log(msg):
+    print("[bench] " + msg, file=sys.stderr, flush=True)
+
+
+def algorithmic_bytes_per_token(cfg, wbytes, pos):
+    """Weights read once per token + KV read over pos+1 positions + KV write
+    + logits write (f16 KV, f32 logits)."""
+    kvd = cfg.n_kv_heads * cfg.head_dim
+    return wbytes + cfg.n_layers * 2 * kvd * 2 * (pos + 1) + cfg.n_layers * 2 * kvd * 2 + cfg.vocab_size * 4
+
+
+def weight_bytes(spec):
+    from oi.ggml import row_byte_size
+    D, H, L, V = spec["dim"], spec["hidden_dim"], spec["n_layers"], spec["vocab_size"]
+    QD, KVD = spec["n_heads"] * spec["head_dim"], spec["n_kv_heads"] * spec["head_dim"]
+    td, tv, tdown = spec["type_default"], spec["type_attn_v"], spec["type_ffn_down"]
+    per_layer = (row_byte_size(td, D) * (QD + KVD + 2 * H) + row_byte_size(tv, D) * KVD +
+                 row_byte_size(td, QD) * D + row_byte_size(tdown, H) * D + 4 * (2 * D + 2 * spec["head_dim"]))
+    out = row_byte_size(spec["type_output"], D) * V if spec["type_output"] >= 0 else 0
+    # per token the embedding contributes one row
+    return L * per_layer + out + 4 * D + row_byte_size(spec["type_embd"], D)
+
+
+def cpu_baseline(path, k, v, cfg, gpu_tokens, budget_s):
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import refcpu  # the oracle, timed here as the CPU baseline
+    threads = min(16, os.cpu_count() or 1)
+    r = refcpu.RefEngine(path, max_ctx=cfg.seq_len, num_threads=threads, kv_f16=True)
+    try:
+        for layer in range(cfg.n_layers):
+            r.kv_fill(layer, 0, k[layer], v[layer])
+        tok, ids, t0 = 0, [], time.perf_counter()
+        while True:
+            logits = r.forward(tok, CONTEXT + len(ids))
+            tok = refcpu.argmax(logits)
+            ids.append(tok)
+            el = time.perf_counter() - t0
+            if el > budget_s or len(ids) >= len(gpu_tokens):
+                break
+        n = len(ids)
+        return {
+            "value": n / el, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": "%d greedy decode steps from pos %d of the same model and pre-filled f16 KV, "
+                      "oracle/refcpu.c (restated reference CPU forward, row work queue over %d threads)"
+                      % (n, CONTEXT, threads),
+            "ms_per_token": 1000 * el / n,
+            "greedy_ids_match_gpu": bool(list(gpu_tokens[:n]) == ids),
+            "compared_steps": n,
+        }
+    finally:
+        r.close()
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=512)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--model-path", default=None, help="reuse an existing synthetic GGUF")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: the token loop runs on a single MI355X "
+              "(multi-GPU sharding is a design note, not built); got --gpus %d" % args.gpus, file=sys.stderr)
+        sys.exit(2)
+    if CONTEXT + args.steps > 4608 + 8192:
+        sys.exit("too many steps")
+
+    from oi import infer, synth
+    import numpy as np
+
+    tmpdir = None
+    path = args.model_path
+    spec = dict(synth.CONFIGS[MODEL])
+    if path is None:
+        tmpdir = tempfile.mkdtemp(prefix="oi_bench_")
+        path = os.path.join(tmpdir, MODEL + ".gguf")
+        t = time.time()
+        synth.write_gguf(path, MODEL)
+        log("wrote synthetic %s (%.2f GB) in %.1fs" % (MODEL, os.path.getsize(path) / 1e9, time.time() - t))
+    try:
+        max_ctx = CONTEXT + max(args.steps, args.warmup) + 1
+        t = time.time()
+        e, _ = infer.engine_load(path, infer.Engine_Opts(max_ctx=max_ctx))
+        cfg = infer.engine_config(e)
+        log("engine loaded in %.1fs (seq_len %d)" % (time.time() - t, cfg.seq_len))
+        k, v = synth.kv_prefill(4242, cfg.n_layers, cfg.n_kv_heads, CONTEXT, cfg.head_dim)
+        infer.engine_kv_fill(e, 0, 0, k, v)
+        log("KV pre-filled to %d" % CONTEXT)
+
+        if args.warmup:
+            infer.engine_decode_greedy(e, 0, CONTEXT, args.warmup)
+        t0 = time.perf_counter()
+        toks = infer.engine_decode_greedy(e, 0, CONTEXT, args.steps)  # synchronizes
+        el = time.perf_counter() - t0
+        tok_s = args.steps / el
+        log("decode: %d steps in %.3fs -> %.1f tok/s" % (args.steps, el, tok_s))
+
+        # whole-step algorithmic bytes at the mean position of the timed steps
+        wb = weight_bytes(spec)
+        mean_pos = CONTEXT + (args.steps - 1) / 2.0
+        bpt = algorithmic_bytes_per_token(cfg, wb, mean_pos)
+        loop_gbps = bpt * tok_s / 1e9
+
+        # dominant kernel, timed alone with HIP events on the engine stream
+        infer.engine_forward(e, int(toks[-1]), CONTEXT + args.steps - 1)
+        kern = {}
+        for name in ("gateup", "qkv", "wo", "down", "attn", "output"):
+            iters = cfg.n_layers * 4 if name != "output" else 8
+            infer.engine_time_kernel(e, name, iters)  # warm
+            us, b = infer.engine_time_kernel(e, name, iters)
+            kern[name] = {"us": us, "bytes": b, "GBps": b / us / 1e3}
+        dom = "gateup"
+        roofline = {
+            "bound": "hbm", "kernel": "gemv_kernel gate/up Q4_K (RMSNorm prologue, SwiGLU epilogue)",
+            "achieved": round(kern[dom]["GBps"], 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+            "frac": round(kern[dom]["GBps"] / PEAK_HBM_GBPS, 4), "traffic": None,
+            "bytes_per_launch": kern[dom]["bytes"], "avg_launch_us": round(kern[dom]["us"], 3),
+        }
+        traffic_file = os.path.join(REPO, "profiles", "traffic_gateup.json")
+        if os.path.exists(traffic_file):
+            with open(traffic_file) as f:
+                roofline["traffic"] = json.load(f).get("traffic_bytes_per_launch")
+
+        cpu = None
+        if not args.no_cpu:
+            log("CPU baseline (oracle) for up to %.0fs ..." % args.cpu_budget)
+            cpu = cpu_baseline(path, k, v, cfg, list(toks), args.cpu_budget)
+            log("CPU baseline: %.3f tok/s, greedy ids match: %s" % (cpu["value"], cpu["greedy_ids_match_gpu"]))
+
+        out = {
+            "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(1000 * el / args.steps, 4), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+            "data": "synthetic (seeded N(0,0.02) weights quantized Q4_K/Q6_K; N(0,1) f16 KV prefill)",
+            "config": {"workload": "Qwen3-8B-shape dense decode, bs1, greedy, f16 KV pre-filled to 4096, "
+                                   "%d steps from pos 4096" % args.steps,
+                       "hidden": cfg.dim, "layers": cfg.n_layers, "heads": "%d/%d" % (cfg.n_heads, cfg.n_kv_heads),
+                       "ffn": cfg.hidden_dim, "vocab": cfg.vocab_size, "weights": "Q4_K + Q6_K(attn_v, output)",
+                       "kv_cache": "f16", "parallelism": "single GPU"},
+            "roofline": roofline,
+            "token_loop": {"bytes_per_token": int(bpt), "achieved_GBps": round(loop_gbps, 1),
+                           "frac_of_peak": round(loop_gbps / PEAK_HBM_GBPS, 4),
+                           "roofline_tok_s": round(PEAK_HBM_GBPS * 1e9 / bpt, 1)},
+            "kernels": {n: {"avg_us": round(d["us"], 3), "GBps": round(d["GBps"], 1)} for n, d in kern.items()},
+            "cpu_baseline": cpu,
+        }
+        print(json.dumps(out), flush=True)
+        infer.engine_destroy(e)
+    finally:
+        if tmpdir:
+            shutil.rmtree(tmpdir, ignore_errors=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -14,6 +14,7 @@
 #include <climits>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <string>
@@ -169,7 +170,9 @@ struct oi_engine {
     const float *output_norm = nullptr;
     float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *hb = nullptr;
     float *logits = nullptr, *part = nullptr, *am_val = nullptr;
-    int32_t *am_idx = nullptr, *am_counter = nullptr, *counters = nullptr, *state = nullptr, *tokens = nullptr;
+    int32_t *am_idx = nullptr, *state = nullptr, *tokens = nullptr;
+    int n_partials = 0;
+    bool use_graph = true;
     float2 *rope_cs = nullptr;
     float *logits_host = nullptr;
     int32_t *state_host = nullptr;
@@ -187,7 +190,8 @@ namespace {
 
 int enqueue_token(oi_engine *e) {
     const hipStream_t st = e->stream;
-    HIP_TRY(launch_embed(e->tok_embd, e->state, e->x, (int32_t)e->cfg.vocab_size, st));
+    HIP_TRY(launch_embed(e->tok_embd, e->state, e->x, (int32_t)e->cfg.vocab_size, e->am_val, e->am_idx, e->tokens,
+                         0, st));
     for (size_t l = 0; l < e->layers.size(); l++) {
         HIP_TRY(launch_gemv(e->g_qkv[l], st));
         HIP_TRY(launch_attn(e->a_attn[l], (int)e->cfg.head_dim, st));
@@ -200,7 +204,7 @@ int enqueue_token(oi_engine *e) {
 }
 
 int ensure_graph(oi_engine *e) {
-    if (e->gexec) return OI_OK;
+    if (e->gexec || !e->use_graph) return OI_OK;
     HIP_TRY(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
     int rc = enqueue_token(e);
     hipGraph_t g = nullptr;
@@ -213,12 +217,23 @@ int ensure_graph(oi_engine *e) {
 }
 
 int set_state(oi_engine *e, int32_t token, int32_t pos, int32_t cap) {
-    e->state_host[0] = token;
-    e->state_host[1] = pos;
-    e->state_host[2] = 0;
-    e->state_host[3] = cap;
-    HIP_TRY(hipMemcpyAsync(e->state, e->state_host, 16, hipMemcpyHostToDevice, e->stream));
+    for (int i = 0; i < ST_WORDS; i++) e->state_host[i] = 0;
+    e->state_host[ST_TOKEN] = token;
+    e->state_host[ST_POS] = pos;
+    e->state_host[ST_CAP] = cap;
+    e->state_host[ST_NPART] = e->n_partials;
+    HIP_TRY(hipMemcpyAsync(e->state, e->state_host, ST_WORDS * 4, hipMemcpyHostToDevice, e->stream));
     return OI_OK;
+}
+
+// One token step: the captured graph, or the same launches issued directly
+// (OI_NO_GRAPH=1, e.g. under tools that do not follow graph capture).
+int run_token(oi_engine *e) {
+    if (e->use_graph) {
+        HIP_TRY(hipGraphLaunch(e->gexec, e->stream));
+        return OI_OK;
+    }
+    return enqueue_token(e);
 }
 
 GemvArgs gemv_args(int mode, int K, const float *x, const float *norm_w, float eps) {
@@ -309,8 +324,8 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
         c.hidden_dim > 15360 || c.n_layers <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads)
         return fail(OI_E_MODEL, "model dimensions outside what this path supports");
     const int G = (int)(c.n_heads / c.n_kv_heads);
-    if (!((c.head_dim == 128 && (G == 1 || G == 2 || G == 4 || G == 8)) || (c.head_dim == 256 && G <= 4 && (G & (G - 1)) == 0)))
-        return fail(OI_E_UNSUPPORTED, "head_dim / GQA group not supported (head_dim 128 with group 1-8, 256 with 1-4)");
+    if (!((c.head_dim == 128 || c.head_dim == 256) && (G == 1 || G == 2 || G == 4 || G == 8)))
+        return fail(OI_E_UNSUPPORTED, "head_dim / GQA group not supported (head_dim 128 or 256, group 1, 2, 4 or 8)");
     if (c.n_heads * c.head_dim > 15360) return fail(OI_E_MODEL, "n_heads*head_dim too large");
 
     // tensors (model.odin:141-179): shapes checked against the config
@@ -346,19 +361,23 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     e->weight_bytes = wbytes;
 
     // device memory plan
-    e->chunk = 64;
+    e->chunk = attn_chunk((int)c.head_dim);
     e->max_splits = (int)((c.seq_len + e->chunk - 1) / e->chunk);
+    if (e->max_splits > attn_max_splits())
+        return fail(OI_E_UNSUPPORTED, "seq_len " + std::to_string(c.seq_len) + " exceeds the attention kernel's " +
+                                          std::to_string(attn_max_splits() * e->chunk) + " positions");
     const size_t kv_layer = (size_t)c.n_kv_heads * c.seq_len * c.head_dim * 2;
     auto al = [](size_t n) { return (n + 255) & ~(size_t)255; };
     const size_t out_rows = (size_t)c.vocab_size;
     GemvArgs probe = gemv_args(GEMV_ARGMAX, (int)D, nullptr, nullptr, 0.f);
     probe.nseg = 1;
+    probe.seg[0].m.type = (int32_t)(tied ? emb->kind : g.tensor("output.weight")->kind);
     probe.seg[0].m.rows = (int32_t)out_rows;
     probe.seg[0].m.cols = (int32_t)D;
     plan_gemv(probe);
     size_t act = al(D * 4) + al(QD * 4) + 2 * al(KVD * 4) + al(QD * 4) + al(H * 4) + al(out_rows * 4) +
                  al((size_t)c.n_heads * e->max_splits * (c.head_dim + 2) * 4) + 2 * al((size_t)probe.total_wgs * 4) +
-                 al(4) + al((size_t)c.n_layers * c.n_kv_heads * 4) + al(16) + al((size_t)(c.seq_len + 1) * 4) +
+                 al(ST_WORDS * 4) + al((size_t)(c.seq_len + 1) * 4) +
                  al((size_t)c.seq_len * (c.head_dim / 2) * 8);
     e->arena.size = wbytes + 2 * kv_layer * c.n_layers + act + 4096;
     hipError_t he = hipMalloc(&e->arena.base, e->arena.size);
@@ -410,9 +429,7 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     e->part = (float *)e->arena.take((size_t)c.n_heads * e->max_splits * (c.head_dim + 2) * 4);
     e->am_val = (float *)e->arena.take((size_t)probe.total_wgs * 4);
     e->am_idx = (int32_t *)e->arena.take((size_t)probe.total_wgs * 4);
-    e->am_counter = (int32_t *)e->arena.take(4);
-    e->counters = (int32_t *)e->arena.take((size_t)c.n_layers * c.n_kv_heads * 4);
-    e->state = (int32_t *)e->arena.take(16);
+    e->state = (int32_t *)e->arena.take(ST_WORDS * 4);
     e->tokens = (int32_t *)e->arena.take((size_t)(c.seq_len + 1) * 4);
     e->rope_cs = (float2 *)e->arena.take((size_t)c.seq_len * (c.head_dim / 2) * 8);
     if (!e->rope_cs) return fail(OI_E_NOMEM, "arena exhausted (activations)");
@@ -432,7 +449,7 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
         HIP_TRY(hipStreamSynchronize(e->stream));
     }
     HIP_TRY(hipHostMalloc((void **)&e->logits_host, out_rows * 4, hipHostMallocDefault));
-    HIP_TRY(hipHostMalloc((void **)&e->state_host, 16, hipHostMallocDefault));
+    HIP_TRY(hipHostMalloc((void **)&e->state_host, ST_WORDS * 4, hipHostMallocDefault));
 
     // launch plans
     const float eps = c.rms_eps;
@@ -456,7 +473,6 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
         t.chunk = e->chunk;
         t.max_splits = e->max_splits;
         t.part = e->part;
-        t.counters = e->counters + l * c.n_kv_heads;
         t.out = e->att;
         t.n_heads = (int32_t)c.n_heads;
         t.n_kv_heads = (int32_t)c.n_kv_heads;
@@ -487,10 +503,12 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     plan_gemv(a);
     a.am_val = e->am_val;
     a.am_idx = e->am_idx;
-    a.am_counter = e->am_counter;
     a.state = e->state;
-    a.tokens_out = e->tokens;
+    if (a.total_wgs != probe.total_wgs) return fail(OI_E_DEVICE, "internal: output plan mismatch");
+    e->n_partials = a.total_wgs;
     e->g_out = a;
+    const char *ng = std::getenv("OI_NO_GRAPH");
+    e->use_graph = !(ng && ng[0] == '1');
 
     std::printf("model: dim=%lld layers=%lld heads=%lld/%lld hidden=%lld vocab=%lld ctx=%lld/%lld  weights=%.0f MB  "
                 "KV cache (f16)=%.0f MB  [gfx950]\n",
@@ -524,8 +542,9 @@ const float *oi_engine_forward(oi_engine *e, int32_t token, int32_t pos) {
                              std::to_string(e->cfg.vocab_size) + ")");
         return nullptr;
     }
-    if (hipSetDevice(e->device) != hipSuccess || ensure_graph(e) || set_state(e, token, pos, 0)) return nullptr;
-    hipError_t r = hipGraphLaunch(e->gexec, e->stream);
+    if (hipSetDevice(e->device) != hipSuccess || ensure_graph(e) || set_state(e, token, pos, 0) || run_token(e))
+        return nullptr;
+    hipError_t r = hipSuccess;
     if (r == hipSuccess)
         r = hipMemcpyAsync(e->logits_host, e->logits, (size_t)e->cfg.vocab_size * 4, hipMemcpyDeviceToHost, e->stream);
     if (r == hipSuccess) r = hipStreamSynchronize(e->stream);
@@ -548,7 +567,11 @@ int oi_engine_decode_greedy(oi_engine *e, int32_t token, int32_t pos, int32_t n_
     int rc = ensure_graph(e);
     if (rc) return rc;
     if ((rc = set_state(e, token, pos, n_steps))) return rc;
-    for (int i = 0; i < n_steps; i++) HIP_TRY(hipGraphLaunch(e->gexec, e->stream));
+    for (int i = 0; i < n_steps; i++)
+        if ((rc = run_token(e))) return rc;
+    // the last step's argmax is still pending: reduce it
+    HIP_TRY(launch_embed(e->tok_embd, e->state, e->x, (int32_t)e->cfg.vocab_size, e->am_val, e->am_idx, e->tokens, 1,
+                         e->stream));
     HIP_TRY(hipMemcpyAsync(out_tokens, e->tokens, (size_t)n_steps * 4, hipMemcpyDeviceToHost, e->stream));
     HIP_TRY(hipStreamSynchronize(e->stream));
     e->last_pos = pos + n_steps - 1;
@@ -616,10 +639,8 @@ int oi_engine_time_kernel(oi_engine *e, int32_t kernel, int32_t iters, double *a
         (void)timed;
         return OI_OK;
     };
-    // the output kernel's argmax epilogue advances the device state: keep pos
     if ((rc = set_state(e, 0, e->last_pos, 0))) return rc;
     if ((rc = run(false))) return rc;
-    if ((rc = set_state(e, 0, e->last_pos, 0))) return rc;
     HIP_TRY(hipEventRecord(e0, e->stream));
     if ((rc = run(true))) return rc;
     HIP_TRY(hipEventRecord(e1, e->stream));

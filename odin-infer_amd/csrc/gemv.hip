@@ -1,0 +1,520 @@
+// gemv.hip -- quantized GEMV for Q4_K, Q6_K and Q8_0 weights on gfx950
+// (reference: infer/matmul.odin:77-109 over ggml/quant.odin:76-282), with the
+// token loop's fusions: RMSNorm prologue (infer/ops.odin:7-19), residual add,
+// SwiGLU (infer/forward.odin:185-193) and greedy-argmax partials
+// (sampler/sampler.odin:79-89).
+//
+// Layout of the work:
+//   * a row is cut into units of 64 weights; a lane owns units j, j+lpr, ...
+//     of its row (lpr lanes per row, a power of two <= 64);
+//   * a tile is R rows per lane group x (64/lpr) groups per wave x 4 waves;
+//   * every workgroup takes a contiguous range of tiles of ONE segment
+//     (so one weight type per workgroup), requests the weights of its first
+//     tile before the x prologue, and double-buffers the rest in registers.
+// Activations: x (after RMSNorm if asked) is quantized per 32 elements to a
+// 22-bit integer q = 2^14*hi + 2^7*mid + lo (hi int8, mid and lo 0..127) with
+// a float scale, so the products run on v_dot4_i32_i8 (three chains, one per
+// byte plane); the result is scaled back in float.  The per-group x sums
+// (exact float) serve the Q4_K min term and the Q6_K -32 offset.  The x
+// rounding error is <= 2^-22 of the group maximum, below f32 accumulation
+// noise, so greedy picks agree with an f32 reference down to ~1e-6 margins.
+
+#include "device_common.h"
+
+namespace oi {
+
+constexpr float XQ_MAX = 2097151.0f;  // 2^21 - 1
+
+static __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// x in LDS: bytes of hi and lo in 16-byte chunks (16 elements); chunk C is
+// stored at a slot that spreads the chunks read together over the banks.
+static __device__ __forceinline__ int cslot(int C) { return (C & ~3) | ((C & 3) ^ ((C >> 4) & 3)); }
+
+struct XQ {
+    const u32x4 *hi, *mid, *lo;  // [K/16] chunks each
+    const float *xs;       // [K/32] scale of the 15-bit integers
+    const float *s32;      // [K/32] sums of x
+    const float *s16;      // [K/16] sums of x
+};
+
+// ------------------------------------------------------------------ Q4_K --
+struct WQ4K {
+    u32x4 h, q0, q1;
+};
+static __device__ __forceinline__ void wload(const DMat &m, int row, int u, WQ4K &w) {
+    const uint8_t *blk = m.q + ((size_t)row * (m.cols >> 8) + (u >> 2)) * 144;
+    const int p = u & 3;
+    w.h = ldg_nt((const u32x4 *)blk);
+    w.q0 = ldg_nt((const u32x4 *)(blk + 16 + 32 * p));
+    w.q1 = ldg_nt((const u32x4 *)(blk + 32 + 32 * p));
+}
+struct XU4K {
+    u32x4 h[4], m[4], l[4];
+    float xs0, xs1, s0, s1;
+};
+static __device__ __forceinline__ void xload(const XQ &x, int u, XU4K &r) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        r.h[c] = x.hi[cslot(4 * u + c)];
+        r.m[c] = x.mid[cslot(4 * u + c)];
+        r.l[c] = x.lo[cslot(4 * u + c)];
+    }
+    r.xs0 = x.xs[2 * u];
+    r.xs1 = x.xs[2 * u + 1];
+    r.s0 = x.s32[2 * u];
+    r.s1 = x.s32[2 * u + 1];
+}
+// the three byte-plane dot products of one 32-element group, combined
+static __device__ __forceinline__ float plane_sum(int h, int m, int l) {
+    return (float)h * 16384.f + ((float)m * 128.f + (float)l);
+}
+
+static __device__ __forceinline__ float wdot(const WQ4K &w, int u, const XU4K &x) {
+    const uint32_t qw[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+    int ah0 = 0, am0 = 0, al0 = 0, ah1 = 0, am1 = 0, al1 = 0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const uint32_t lo = qw[k] & 0x0F0F0F0Fu, hi = (qw[k] >> 4) & 0x0F0F0F0Fu;
+        const int c0 = k >> 2, c1 = 2 + (k >> 2), e = k & 3;
+        ah0 = sdot4(lo, x.h[c0][e], ah0);
+        am0 = sdot4(lo, x.m[c0][e], am0);
+        al0 = sdot4(lo, x.l[c0][e], al0);
+        ah1 = sdot4(hi, x.h[c1][e], ah1);
+        am1 = sdot4(hi, x.m[c1][e], am1);
+        al1 = sdot4(hi, x.l[c1][e], al1);
+    }
+    const int p = u & 3;
+    const float d = h2f(w.h.x & 0xFFFFu), dmin = h2f(w.h.x >> 16);
+    const uint32_t sw[3] = {w.h.y, w.h.z, w.h.w};
+    uint32_t sc0, m0, sc1, m1;
+    scale_min_k4(2 * p, sw, sc0, m0);
+    scale_min_k4(2 * p + 1, sw, sc1, m1);
+    const float q0 = plane_sum(ah0, am0, al0) * x.xs0, q1 = plane_sum(ah1, am1, al1) * x.xs1;
+    return d * ((float)sc0 * q0 + (float)sc1 * q1) - dmin * ((float)m0 * x.s0 + (float)m1 * x.s1);
+}
+
+// ------------------------------------------------------------------ Q6_K --
+struct WQ6K {
+    u32x4 l0, l1, qh;
+    u32x2 sc;
+    uint32_t d;
+};
+static __device__ __forceinline__ void wload(const DMat &m, int row, int u, WQ6K &w) {
+    const size_t sbi = (size_t)row * (m.cols >> 8) + (u >> 2);
+    const int h = (u >> 1) & 1, l0 = (u & 1) * 16;
+    const uint8_t *qb = m.q + sbi * 192;
+    w.l0 = ldg_nt((const u32x4 *)(qb + 64 * h + l0));
+    w.l1 = ldg_nt((const u32x4 *)(qb + 64 * h + 32 + l0));
+    w.qh = ldg_nt((const u32x4 *)(qb + 128 + 32 * h + l0));
+    w.sc = ldg_nt((const u32x2 *)(m.s + sbi * 16 + 8 * h));
+    w.d = m.d[sbi];
+}
+// unit u covers elements e0 + 32k + [0,16), k = 0..3, e0 = 256 sb + 128 h + l0
+struct XU6K {
+    u32x4 h[4], m[4], l[4];
+    float xs[4], s[4];
+};
+static __device__ __forceinline__ void xload(const XQ &x, int u, XU6K &r) {
+    const int e0 = 256 * (u >> 2) + 128 * ((u >> 1) & 1) + 16 * (u & 1);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int C = (e0 + 32 * k) >> 4;
+        r.h[k] = x.hi[cslot(C)];
+        r.m[k] = x.mid[cslot(C)];
+        r.l[k] = x.lo[cslot(C)];
+        r.xs[k] = x.xs[C >> 1];
+        r.s[k] = x.s16[C];
+    }
+}
+static __device__ __forceinline__ float wdot(const WQ6K &w, int u, const XU6K &x) {
+    const uint32_t l0[4] = {w.l0.x, w.l0.y, w.l0.z, w.l0.w};
+    const uint32_t l1[4] = {w.l1.x, w.l1.y, w.l1.z, w.l1.w};
+    const uint32_t qh[4] = {w.qh.x, w.qh.y, w.qh.z, w.qh.w};
+    int ah[4] = {0, 0, 0, 0}, am[4] = {0, 0, 0, 0}, al[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        // 6-bit values v = q + 32 (0..63) of the four sub-blocks, 4 per word
+        const uint32_t v[4] = {(l0[i] & 0x0F0F0F0Fu) | ((qh[i] & 0x03030303u) << 4),
+                               (l1[i] & 0x0F0F0F0Fu) | (((qh[i] >> 2) & 0x03030303u) << 4),
+                               ((l0[i] >> 4) & 0x0F0F0F0Fu) | (((qh[i] >> 4) & 0x03030303u) << 4),
+                               ((l1[i] >> 4) & 0x0F0F0F0Fu) | (((qh[i] >> 6) & 0x03030303u) << 4)};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            ah[k] = sdot4(v[k], x.h[k][i], ah[k]);
+            am[k] = sdot4(v[k], x.m[k][i], am[k]);
+            al[k] = sdot4(v[k], x.l[k][i], al[k]);
+        }
+    }
+    const int bsh = (u & 1);  // scale byte (l0/16) + 2k of the 8 bytes of this half
+    const uint32_t scw[2] = {w.sc.x, w.sc.y};
+    float acc = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int bi = bsh + 2 * k;
+        const float s = (float)(int8_t)((scw[bi >> 2] >> ((bi & 3) * 8)) & 0xFFu);
+        acc += s * (plane_sum(ah[k], am[k], al[k]) * x.xs[k] - 32.f * x.s[k]);
+    }
+    return h2f(w.d) * acc;
+}
+
+// ------------------------------------------------------------------ Q8_0 --
+struct WQ80 {
+    u32x4 q[4];
+    uint32_t d;
+};
+static __device__ __forceinline__ void wload(const DMat &m, int row, int u, WQ80 &w) {
+    const size_t b0 = (size_t)row * (m.cols >> 5) + 2 * u;
+    const u32x4 *p = (const u32x4 *)(m.q + b0 * 32);
+#pragma unroll
+    for (int i = 0; i < 4; i++) w.q[i] = ldg_nt(p + i);
+    w.d = *(const uint32_t *)(m.d + b0);
+}
+static __device__ __forceinline__ float wdot(const WQ80 &w, int u, const XU4K &x) {
+    int ah[2] = {0, 0}, am[2] = {0, 0}, al[2] = {0, 0};
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const int b = c >> 1;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            ah[b] = sdot4(w.q[c][e], x.h[c][e], ah[b]);
+            am[b] = sdot4(w.q[c][e], x.m[c][e], am[b]);
+            al[b] = sdot4(w.q[c][e], x.l[c][e], al[b]);
+        }
+    }
+    return h2f(w.d & 0xFFFFu) * (plane_sum(ah[0], am[0], al[0]) * x.xs0) +
+           h2f(w.d >> 16) * (plane_sum(ah[1], am[1], al[1]) * x.xs1);
+}
+
+template <int T> struct Types;
+template <> struct Types<T_Q4_K> { using W = WQ4K; using X = XU4K; };
+template <> struct Types<T_Q6_K> { using W = WQ6K; using X = XU6K; };
+template <> struct Types<T_Q8_0> { using W = WQ80; using X = XU4K; };
+
+// Quantize 4 consecutive values (one float4 per thread, 8 threads per group
+// of 32) into the LDS layout.
+static __device__ __forceinline__ void quant4(float4 v, int c, uint32_t *hw, uint32_t *mw, uint32_t *lw, float *xs,
+                                              float *s32, float *s16) {
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    const float sum = (v.x + v.y) + (v.z + v.w);
+    float sum16 = sum + __shfl_xor(sum, 1, WAVE);
+    sum16 += __shfl_xor(sum16, 2, WAVE);
+    const float sum32 = sum16 + __shfl_xor(sum16, 4, WAVE);
+    amax = fmaxf(amax, __shfl_xor(amax, 1, WAVE));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, WAVE));
+    amax = fmaxf(amax, __shfl_xor(amax, 4, WAVE));
+    const float inv = amax > 0.f ? XQ_MAX / amax : 0.f;
+    const int q0 = (int)rintf(v.x * inv), q1 = (int)rintf(v.y * inv), q2 = (int)rintf(v.z * inv),
+              q3 = (int)rintf(v.w * inv);
+    const uint32_t hi = ((uint32_t)(q0 >> 14) & 0xFFu) | (((uint32_t)(q1 >> 14) & 0xFFu) << 8) |
+                        (((uint32_t)(q2 >> 14) & 0xFFu) << 16) | (((uint32_t)(q3 >> 14) & 0xFFu) << 24);
+    const uint32_t mid = ((uint32_t)(q0 >> 7) & 0x7Fu) | (((uint32_t)(q1 >> 7) & 0x7Fu) << 8) |
+                         (((uint32_t)(q2 >> 7) & 0x7Fu) << 16) | (((uint32_t)(q3 >> 7) & 0x7Fu) << 24);
+    const uint32_t lo = ((uint32_t)q0 & 0x7Fu) | (((uint32_t)q1 & 0x7Fu) << 8) | (((uint32_t)q2 & 0x7Fu) << 16) |
+                        (((uint32_t)q3 & 0x7Fu) << 24);
+    const int C = c >> 2, wi = c & 3;
+    hw[cslot(C) * 4 + wi] = hi;
+    mw[cslot(C) * 4 + wi] = mid;
+    lw[cslot(C) * 4 + wi] = lo;
+    if ((c & 7) == 0) {
+        xs[c >> 3] = amax / XQ_MAX;
+        s32[c >> 3] = sum32;
+    }
+    if ((c & 3) == 0) s16[c >> 2] = sum16;
+}
+
+// x -> (optional RMSNorm, ops.odin:7-19) -> 15-bit integers in LDS.  With a
+// norm and K <= 8192 the vector is read once into registers; K/4 is a
+// multiple of 8, so the 8-lane groups of quant4 are always whole.
+static __device__ void quantize_x(const GemvArgs &a, u32x4 *xhi, u32x4 *xmid, u32x4 *xlo, float *xs, float *s32,
+                                  float *s16, float *red) {
+    constexpr int NXR = 8;  // float4 per thread held in registers (K <= 8192)
+    const int K = a.K, tid = threadIdx.x;
+    const float4 *gx = (const float4 *)a.x;
+    const float4 *nw = (const float4 *)a.norm_w;
+    uint32_t *hw = (uint32_t *)xhi, *mw = (uint32_t *)xmid, *lw = (uint32_t *)xlo;
+    if (nw && K <= 4 * WG * NXR) {
+        float4 xv[NXR], wv[NXR];
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < NXR; i++) {
+            const int c = tid + i * WG;
+            if (c < K / 4) {
+                xv[i] = gx[c];
+                wv[i] = nw[c];
+                ss += xv[i].x * xv[i].x + xv[i].y * xv[i].y + xv[i].z * xv[i].z + xv[i].w * xv[i].w;
+            }
+        }
+        ss = wave_sum(ss);
+        if ((tid & (WAVE - 1)) == 0) red[tid / WAVE] = ss;
+        __syncthreads();
+        ss = (red[0] + red[1]) + (red[2] + red[3]);
+        const float s = 1.0f / sqrtf(ss / (float)K + a.eps);
+#pragma unroll
+        for (int i = 0; i < NXR; i++) {
+            const int c = tid + i * WG;
+            if (c < K / 4) {
+#pragma clang fp contract(off)
+                float4 v;
+                v.x = wv[i].x * (s * xv[i].x);
+                v.y = wv[i].y * (s * xv[i].y);
+                v.z = wv[i].z * (s * xv[i].z);
+                v.w = wv[i].w * (s * xv[i].w);
+                quant4(v, c, hw, mw, lw, xs, s32, s16);
+            }
+        }
+    } else {
+        float s = 1.f;
+        if (nw) {
+            float ss = 0.f;
+            for (int c = tid; c < K / 4; c += WG) {
+                const float4 v = gx[c];
+                ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            }
+            ss = wave_sum(ss);
+            if ((tid & (WAVE - 1)) == 0) red[tid / WAVE] = ss;
+            __syncthreads();
+            ss = (red[0] + red[1]) + (red[2] + red[3]);
+            s = 1.0f / sqrtf(ss / (float)K + a.eps);
+        }
+        for (int c = tid; c < K / 4; c += WG) {
+            float4 v = gx[c];
+            if (nw) {
+#pragma clang fp contract(off)
+                const float4 w = nw[c];
+                v.x = w.x * (s * v.x);
+                v.y = w.y * (s * v.y);
+                v.z = w.z * (s * v.z);
+                v.w = w.w * (s * v.w);
+            }
+            quant4(v, c, hw, mw, lw, xs, s32, s16);
+        }
+    }
+    __syncthreads();
+}
+
+// One workgroup: tiles [tb, te) of segment `seg`, all of weight type T.
+// A step is one unit per lane for the R rows (x NM matrices) of a tile; the
+// weights of step s+P-1 are requested before step s is computed (a ring of
+// P register stages), the first P-1 before the x prologue.
+template <int T, int R, int NM, int P>
+static __device__ void gemv_run(const GemvArgs &a, int seg, int tb, int te, int wg) {
+    using W = typename Types<T>::W;
+    using X = typename Types<T>::X;
+    extern __shared__ u32x4 smem[];
+    __shared__ float red[WG / WAVE];
+    __shared__ int redi[WG / WAVE];
+    const int K = a.K, tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid / WAVE;
+    const DMat &m0 = a.seg[seg].m;
+    const DMat &m1 = a.seg[NM == 2 ? 1 : seg].m;
+    const int lpr = a.lpr, gpw = WAVE / lpr, grp = lane / lpr, j = lane & (lpr - 1);
+    const int U = K >> 6, upl = U / lpr;
+    const int rows_m = m0.rows;
+    const int nsteps = (te - tb) * upl;
+    const int rbase = (wave * gpw + grp) * R;
+
+    W ring[P][NM][R];
+    auto issue = [&](int step, W (&w)[NM][R]) {
+        const int tile = tb + step / upl, u = j + (step % upl) * lpr;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int row = tile * a.rows_per_wg + rbase + r;
+            if (row < rows_m) {
+                wload(m0, row, u, w[0][r]);
+                if (NM == 2) wload(m1, row, u, w[NM - 1][r]);
+            }
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < P - 1; i++)
+        if (i < nsteps) issue(i, ring[i]);
+
+    u32x4 *xhi = smem, *xmid = smem + K / 16, *xlo = smem + 2 * (K / 16);
+    float *xs = (float *)(smem + 3 * (K / 16)), *s32 = xs + K / 32, *s16 = s32 + K / 32;
+    quantize_x(a, xhi, xmid, xlo, xs, s32, s16, red);
+    const XQ xq{xhi, xmid, xlo, xs, s32, s16};
+
+    float bv = -INFINITY;
+    int bi = 0x7FFFFFFF;
+    float acc[NM][R];
+#pragma unroll
+    for (int i = 0; i < NM; i++)
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[i][r] = 0.f;
+
+    for (int base = 0; base < nsteps; base += P) {
+#pragma unroll
+        for (int k = 0; k < P; k++) {
+            const int step = base + k;
+            if (step >= nsteps) break;
+            if (step + P - 1 < nsteps) issue(step + P - 1, ring[(k + P - 1) % P]);
+            const int tile = tb + step / upl, ui = step % upl, u = j + ui * lpr;
+            const int row0 = tile * a.rows_per_wg + rbase;
+            X xu;
+            xload(xq, u, xu);
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                if (row0 + r < rows_m) {
+                    acc[0][r] += wdot(ring[k][0][r], u, xu);
+                    if (NM == 2) acc[NM - 1][r] += wdot(ring[k][NM - 1][r], u, xu);
+                }
+            if (ui == upl - 1) {
+                // reduce over the lanes of the row, then the epilogue
+                for (int o = lpr >> 1; o > 0; o >>= 1)
+#pragma unroll
+                    for (int r = 0; r < R; r++) {
+                        acc[0][r] += __shfl_xor(acc[0][r], o, WAVE);
+                        if (NM == 2) acc[NM - 1][r] += __shfl_xor(acc[NM - 1][r], o, WAVE);
+                    }
+                if (j == 0) {
+#pragma unroll
+                    for (int r = 0; r < R; r++) {
+                        const int row = row0 + r;
+                        if (row >= rows_m) continue;
+                        float *y = a.seg[seg].y;
+                        if (NM == 2) {  // infer/forward.odin:188-193
+#pragma clang fp contract(off)
+                            float val = acc[0][r];
+                            val *= 1.0f / (1.0f + expf(-val));
+                            val *= acc[NM - 1][r];
+                            y[row] = val;
+                        } else if (a.mode == GEMV_ADD) {
+                            y[row] += acc[0][r];
+                        } else {
+                            y[row] = acc[0][r];
+                            if (a.mode == GEMV_ARGMAX && better(acc[0][r], row, bv, bi)) {
+                                bv = acc[0][r];
+                                bi = row;
+                            }
+                        }
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < NM; i++)
+#pragma unroll
+                    for (int r = 0; r < R; r++) acc[i][r] = 0.f;
+            }
+        }
+    }
+
+    if (a.mode == GEMV_ARGMAX) {  // this workgroup's best (value, lowest row)
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o, WAVE);
+            const int oi = __shfl_xor(bi, o, WAVE);
+            if (better(ov, oi, bv, bi)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if (lane == 0) {
+            red[wave] = bv;
+            redi[wave] = bi;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            for (int w = 1; w < WG / WAVE; w++)
+                if (better(red[w], redi[w], bv, bi)) {
+                    bv = red[w];
+                    bi = redi[w];
+                }
+            a.am_val[wg] = bv;
+            a.am_idx[wg] = bi;
+            if (wg == 0) a.state[ST_PENDING] = 1;  // argmax pending for the next embedding step
+        }
+    }
+}
+
+template <int R, int NM, int P>
+__global__ __launch_bounds__(WG) void gemv_q_kernel(GemvArgs a) {
+    const int wg = blockIdx.x;
+    int seg = 0;
+    if (NM == 1) {
+        if (a.nseg > 1 && wg >= a.seg[1].wg_begin) seg = 1;
+        if (a.nseg > 2 && wg >= a.seg[2].wg_begin) seg = 2;
+    }
+    const int seg_end = (NM == 1 && seg + 1 < a.nseg) ? a.seg[seg + 1].wg_begin : a.total_wgs;
+    const int nwg = seg_end - a.seg[seg].wg_begin, w = wg - a.seg[seg].wg_begin;
+    const int ntiles = a.seg[seg].ntiles;
+    const int tb = (int)((long)ntiles * w / nwg), te = (int)((long)ntiles * (w + 1) / nwg);
+    switch (a.seg[seg].m.type) {
+    case T_Q4_K: gemv_run<T_Q4_K, R, NM, P>(a, seg, tb, te, wg); break;
+    case T_Q6_K: gemv_run<T_Q6_K, R, NM, P>(a, seg, tb, te, wg); break;
+    default: gemv_run<T_Q8_0, R, NM, P>(a, seg, tb, te, wg); break;
+    }
+}
+
+// kernel configurations: (R, NM, P)
+#define GEMV_Q_MAIN gemv_q_kernel<2, 1, 3>
+#define GEMV_Q_SWIGLU gemv_q_kernel<1, 2, 3>
+constexpr int R_MAIN = 2, R_SWIGLU = 1;
+
+static int resident_wgs(const void *fn, size_t lds) {
+    static int cache[2] = {0, 0};
+    const int slot = fn == (const void *)GEMV_Q_SWIGLU ? 1 : 0;
+    if (!cache[slot]) {
+        int per_cu = 0, cus = 256, dev = 0;
+        hipGetDevice(&dev);
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, WG, lds) != hipSuccess || per_cu < 1) per_cu = 1;
+        cache[slot] = per_cu * cus;
+    }
+    return cache[slot];
+}
+
+static size_t gemv_q_lds(int K) { return (size_t)K / 16 * 48 + (size_t)K / 32 * 8 + (size_t)K / 16 * 4; }
+
+bool gemv_q_supported(const GemvArgs &a) {
+    const int n = a.mode == GEMV_SWIGLU ? 2 : a.nseg;
+    for (int i = 0; i < n; i++) {
+        const int t = a.seg[i].m.type;
+        if (t != T_Q4_K && t != T_Q6_K && t != T_Q8_0) return false;
+    }
+    if (a.mode == GEMV_SWIGLU && a.seg[0].m.type != a.seg[1].m.type) return false;
+    return a.K % 256 == 0 || (a.K % 64 == 0 && a.seg[0].m.type == T_Q8_0 && n == 1);
+}
+
+// Plan for gemv_q_kernel: workgroups spread over the segments in proportion
+// to their tiles, each with a whole number of tiles, no more workgroups than
+// can be resident at once.
+void plan_gemv_q(GemvArgs &a) {
+    const int U = a.K / 64;
+    int lpr = 1;
+    while (lpr < 64 && U % (lpr * 2) == 0) lpr *= 2;
+    a.lpr = lpr;
+    const bool sw = a.mode == GEMV_SWIGLU;
+    const int gpw = 64 / lpr, R = sw ? R_SWIGLU : R_MAIN;
+    a.rows_per_wg = 4 * gpw * R;
+    const int nseg = sw ? 1 : a.nseg;
+    long total_tiles = 0;
+    for (int i = 0; i < nseg; i++) {
+        a.seg[i].ntiles = (a.seg[i].m.rows + a.rows_per_wg - 1) / a.rows_per_wg;
+        total_tiles += a.seg[i].ntiles;
+    }
+    const long slots = resident_wgs(sw ? (const void *)GEMV_Q_SWIGLU : (const void *)GEMV_Q_MAIN, gemv_q_lds(a.K));
+    const long k = (total_tiles + slots - 1) / slots;  // tiles per workgroup
+    int wg = 0;
+    for (int i = 0; i < nseg; i++) {
+        a.seg[i].wg_begin = wg;
+        wg += (int)((a.seg[i].ntiles + k - 1) / k);
+    }
+    if (sw) {
+        a.seg[1].wg_begin = 0;
+        a.seg[1].ntiles = a.seg[0].ntiles;
+    }
+    a.total_wgs = wg;
+    a.kernel = 1;
+}
+
+hipError_t launch_gemv_q(const GemvArgs &a, hipStream_t st) {
+    dim3 grid(a.total_wgs), block(WG);
+    if (a.mode == GEMV_SWIGLU)
+        hipLaunchKernelGGL(GEMV_Q_SWIGLU, grid, block, gemv_q_lds(a.K), st, a);
+    else
+        hipLaunchKernelGGL(GEMV_Q_MAIN, grid, block, gemv_q_lds(a.K), st, a);
+    return hipGetLastError();
+}
+
+}  // namespace oi

@@ -1,56 +1,19 @@
 // kernels.hip -- gfx950 kernels of the decode token loop.
 //
-//   gemv_kernel    quantized GEMV (Q4_K, Q6_K, Q8_0, F16, F32) with a fused
-//                  RMSNorm prologue and store / residual-add / SwiGLU / greedy
-//                  argmax epilogues (reference: infer/matmul.odin:77-109,
-//                  ggml/quant.odin:76-282, infer/forward.odin:111-203)
-//   attn_kernel    split-L grouped-query decode attention over the f16 KV
-//                  cache, with the per-head q/k RMSNorm, RoPE and the K/V store
-//                  of the current position fused in (forward.odin:117-175;
-//                  the f16 store follows infer/metal.odin:443-454)
-//   embed_kernel   token embedding row (forward.odin:72-75)
+//   gemv_kernel    GEMV for any device type (F32, F16, Q8_0, Q4_K, Q6_K) in
+//                  float arithmetic, with the same fused prologue/epilogues as
+//                  gemv_q_kernel (gemv.hip), used where that one does not apply
+//                  (reference: infer/matmul.odin:77-109, ggml/quant.odin:76-282)
+//   embed_kernel   token embedding row (forward.odin:72-75), preceded by the
+//                  reduction of the previous step's argmax partials
+//                  (sampler/sampler.odin:79-89)
 //   dequant_kernel bit-exact dequant of a matrix (test hook)
 //
 // Wave64 throughout; workgroups of 256 threads (4 waves).
 
-#include "oi_kernels.h"
+#include "device_common.h"
 
 namespace oi {
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-
-constexpr int WAVE = 64;
-constexpr int WG = 256;
-
-__device__ __forceinline__ float h2f(uint32_t bits16) {
-    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
-}
-__device__ __forceinline__ uint16_t f2h(float f) {  // round to nearest even
-    return __builtin_bit_cast(uint16_t, (_Float16)f);
-}
-
-template <class T>
-__device__ __forceinline__ T ldg_nt(const T *p) {
-    return __builtin_nontemporal_load(p);
-}
-
-// byte i (0..11) of the packed Q4_K scales held in three words
-__device__ __forceinline__ uint32_t sbyte(const uint32_t sw[3], int i) {
-    uint32_t w = i < 4 ? sw[0] : (i < 8 ? sw[1] : sw[2]);
-    return (w >> ((i & 3) * 8)) & 0xFFu;
-}
-
-// get_scale_min_k4 (ggml/quant.odin:64-73)
-__device__ __forceinline__ void scale_min_k4(int j, const uint32_t sw[3], uint32_t &sc, uint32_t &m) {
-    if (j < 4) {
-        sc = sbyte(sw, j) & 63u;
-        m = sbyte(sw, j + 4) & 63u;
-    } else {
-        sc = (sbyte(sw, j + 4) & 0xFu) | ((sbyte(sw, j - 4) >> 6) << 4);
-        m = (sbyte(sw, j + 4) >> 4) | ((sbyte(sw, j) >> 6) << 4);
-    }
-}
 
 // --------------------------------------------------------------------------
 // Bit-exact unit decoders (64 weights each).  Contraction is off so every
@@ -167,12 +130,62 @@ __global__ __launch_bounds__(WG) void dequant_kernel(DMat m, float *out) {
 }
 
 // ------------------------------------------------------------- embedding --
-// x = dequant(token_embd[token]) (infer/forward.odin:72-75, 103)
-__global__ __launch_bounds__(WG) void embed_kernel(DMat emb, const int32_t *state, float *x, int32_t vocab) {
-    int tok = state[0];
+static // x = dequant(token_embd[token]) (infer/forward.odin:72-75, 103)
+__global__ __launch_bounds__(WG) void embed_kernel(DMat emb, int32_t *state, float *x, int32_t vocab,
+                                                   const float *am_val, const int32_t *am_idx, int32_t *tokens_out,
+                                                   int finalize_only) {
+    __shared__ float rv[WG / WAVE];
+    __shared__ int ri[WG / WAVE];
+    __shared__ int tok_s;
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid / WAVE;
+    const int pending = state[ST_PENDING];
+    if (pending) {  // first maximum of the previous logits wins
+        const int npart = state[ST_NPART];
+        float bv = -INFINITY;
+        int bi = 0x7FFFFFFF;
+        for (int i = tid; i < npart; i += WG)
+            if (better(am_val[i], am_idx[i], bv, bi)) {
+                bv = am_val[i];
+                bi = am_idx[i];
+            }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o, WAVE);
+            const int oi = __shfl_xor(bi, o, WAVE);
+            if (better(ov, oi, bv, bi)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if (lane == 0) {
+            rv[wave] = bv;
+            ri[wave] = bi;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            for (int w = 1; w < WG / WAVE; w++)
+                if (better(rv[w], ri[w], bv, bi)) {
+                    bv = rv[w];
+                    bi = ri[w];
+                }
+            if (bi == 0x7FFFFFFF) bi = 0;  // all NaN: index 0, as the reference's scan
+            const int step = state[ST_STEP];
+            if (tokens_out && step >= 0 && step < state[ST_CAP]) tokens_out[step] = bi;
+            state[ST_STEP] = step + 1;
+            state[ST_TOKEN] = bi;
+            state[ST_POS] = state[ST_POS] + 1;
+            state[ST_PENDING] = 0;
+            tok_s = bi;
+        }
+    } else if (tid == 0) {
+        tok_s = state[ST_TOKEN];
+    }
+    __syncthreads();
+    if (finalize_only) return;
+    int tok = tok_s;
     if (tok < 0 || tok >= vocab) tok = 0;  // the host checks the range first
     const int units = emb.cols / 64;
-    for (int u = threadIdx.x; u < units; u += WG) {
+    for (int u = tid; u < units; u += WG) {
         float v[64];
         decode_unit(emb, tok, u, v);
         for (int j = 0; j < 64; j++) x[unit_elem(emb.type, u, j)] = v[j];
@@ -181,11 +194,6 @@ __global__ __launch_bounds__(WG) void embed_kernel(DMat emb, const int32_t *stat
 
 // ------------------------------------------------------------------ GEMV --
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
-    return v;
-}
 
 // x in LDS: float4 chunk c (elements 4c..4c+3) lives at a swizzled slot so
 // that the 64 lanes of a wave, each reading chunk k of its own 64-element
@@ -385,9 +393,6 @@ __device__ __forceinline__ void gemv_rows(const DMat &m, const int *rows, int j,
     }
 }
 
-__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
-    return v > bv || (v == bv && i < bi);
-}
 
 // Workgroup tile: 4 waves; each wave holds 64/lpr lane groups; each group
 // owns R consecutive rows and lpr lanes that split the row's units.
@@ -396,7 +401,6 @@ __global__ __launch_bounds__(WG) void gemv_kernel(GemvArgs a) {
     extern __shared__ float4 smem[];
     __shared__ float red[WG / WAVE];
     __shared__ int redi[WG / WAVE];
-    __shared__ int last_flag;
     const int K = a.K, tid = threadIdx.x;
     float4 *x4 = smem;
     float *s16 = (float *)(smem + K / 4);
@@ -496,7 +500,7 @@ __global__ __launch_bounds__(WG) void gemv_kernel(GemvArgs a) {
     }
     if (a.mode != GEMV_ARGMAX) return;
 
-    // ---- greedy argmax (sampler/sampler.odin:79-89: first maximum wins)
+    // ---- greedy argmax partial of this workgroup (first maximum wins)
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         const float ov = __shfl_xor(bv, o, WAVE);
@@ -510,46 +514,17 @@ __global__ __launch_bounds__(WG) void gemv_kernel(GemvArgs a) {
             if (better(red[w], redi[w], bv, bi)) { bv = red[w]; bi = redi[w]; }
         a.am_val[wg] = bv;
         a.am_idx[wg] = bi;
-        __threadfence();
-        const int prev = atomicAdd(a.am_counter, 1);
-        last_flag = (prev == a.total_wgs - 1);
-    }
-    __syncthreads();
-    if (!last_flag) return;
-    __threadfence();
-    bv = -INFINITY;
-    bi = 0x7FFFFFFF;
-    for (int i = tid; i < a.total_wgs; i += WG) {
-        const float v = __builtin_nontemporal_load(a.am_val + i);
-        const int ix = __builtin_nontemporal_load(a.am_idx + i);
-        if (better(v, ix, bv, bi)) { bv = v; bi = ix; }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(bv, o, WAVE);
-        const int oi = __shfl_xor(bi, o, WAVE);
-        if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-    }
-    __syncthreads();
-    if (lane == 0) { red[wave] = bv; redi[wave] = bi; }
-    __syncthreads();
-    if (tid == 0) {
-        for (int w = 1; w < WG / WAVE; w++)
-            if (better(red[w], redi[w], bv, bi)) { bv = red[w]; bi = redi[w]; }
-        if (bi == 0x7FFFFFFF) bi = 0;  // all NaN: keep index 0 as the reference does
-        int32_t *st = a.state;
-        const int step = st[2];
-        if (a.tokens_out && step >= 0 && step < st[3]) a.tokens_out[step] = bi;
-        st[0] = bi;
-        st[1] = st[1] + 1;
-        st[2] = step + 1;
-        *a.am_counter = 0;
-        __threadfence();
+        if (wg == 0) a.state[ST_PENDING] = 1;
     }
 }
 
 bool plan_gemv(GemvArgs &a) {
     if (a.K <= 0 || a.K % 64) return false;
+    if (gemv_q_supported(a)) {
+        plan_gemv_q(a);
+        return true;
+    }
+    a.kernel = 0;
     const int U = a.K / 64;
     int lpr = 1;
     while (lpr < 64 && U % (lpr * 2) == 0) lpr *= 2;
@@ -576,6 +551,7 @@ bool plan_gemv(GemvArgs &a) {
 }
 
 hipError_t launch_gemv(const GemvArgs &a, hipStream_t st) {
+    if (a.kernel == 1) return launch_gemv_q(a, st);
     const size_t lds = (size_t)a.K * 4 + (size_t)(a.K / 16) * 4;
     const int R = a.rows_per_wg / (4 * (64 / a.lpr));
     dim3 grid(a.total_wgs), block(WG);
@@ -587,247 +563,10 @@ hipError_t launch_gemv(const GemvArgs &a, hipStream_t st) {
     return hipGetLastError();
 }
 
-// ------------------------------------------------------------- attention --
-
-// RMSNorm + RoPE of one head held in LDS (raw -> out), forward.odin:117-145.
-template <int HD>
-__device__ void norm_rope_head(const float *raw, const float *w, float eps, const float2 *cs, float *out,
-                               float *red, int tid, int nthreads) {
-    // sum of squares over the head (first wave), reference ops.odin:7-19
-    if (tid < WAVE) {
-        float ss = 0.f;
-        for (int i = tid; i < HD; i += WAVE) ss += raw[i] * raw[i];
-        ss = wave_sum(ss);
-        if (tid == 0) red[0] = 1.0f / sqrtf(ss / (float)HD + eps);
-    }
-    __syncthreads();
-    const float s = red[0];
-    for (int i = tid; i < HD / 2; i += nthreads) {
-#pragma clang fp contract(off)
-        const float x = w[i] * (s * raw[i]);
-        const float y = w[i + HD / 2] * (s * raw[i + HD / 2]);
-        const float c = cs[i].x, sn = cs[i].y;
-        out[i] = x * c - y * sn;
-        out[i + HD / 2] = x * sn + y * c;
-    }
-    __syncthreads();
-}
-
-template <int HD, int G>
-__global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
-    constexpr int DPL = HD / 16;  // dims per lane (16 lanes per position)
-    constexpr int MAXC = 256;     // max positions per split
-    __shared__ float qr[G][HD];
-    __shared__ float raw[HD];
-    __shared__ float kp[HD], vp[HD];
-    __shared__ float sc[G][MAXC];
-    __shared__ float mx[G], sm[G];
-    __shared__ float ored[WG / WAVE][G][HD];
-    __shared__ float red[4];
-    __shared__ int last_flag;
-
-    const int split = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
-    const int lane = tid & (WAVE - 1), wave = tid / WAVE;
-    const int pos = a.state[1];
-    const int t0 = split * a.chunk;
-    if (t0 > pos) return;
-    const int t1 = min(t0 + a.chunk, pos + 1);
-    const int n = t1 - t0;
-    const int nsplit = pos / a.chunk + 1;
-    const float2 *cs = a.rope_cs + (size_t)pos * (HD / 2);
-
-    // q heads of this kv group: RMSNorm(q_norm) + RoPE
-    for (int g = 0; g < G; g++) {
-        const int h = kvh * G + g;
-        for (int i = tid; i < HD; i += WG) raw[i] = a.q[(size_t)h * HD + i];
-        __syncthreads();
-        norm_rope_head<HD>(raw, a.q_norm, a.eps, cs, qr[g], red, tid, WG);
-    }
-    // the current position: K/V formed here and stored to the cache as f16
-    const bool has_pos = pos >= t0 && pos < t1;
-    uint16_t *kc = a.kc + (size_t)kvh * a.seq_len * HD;
-    uint16_t *vc = a.vc + (size_t)kvh * a.seq_len * HD;
-    if (has_pos) {
-        for (int i = tid; i < HD; i += WG) raw[i] = a.k[(size_t)kvh * HD + i];
-        __syncthreads();
-        norm_rope_head<HD>(raw, a.k_norm, a.eps, cs, kp, red, tid, WG);
-        for (int i = tid; i < HD; i += WG) {
-            const uint16_t kb = f2h(kp[i]), vb = f2h(a.v[(size_t)kvh * HD + i]);
-            kc[(size_t)pos * HD + i] = kb;
-            vc[(size_t)pos * HD + i] = vb;
-            kp[i] = h2f(kb);
-            vp[i] = h2f(vb);
-        }
-        __syncthreads();
-    }
-
-    // scores: 16 lanes per position, DPL dims per lane
-    const int sub = lane & 15, pslot = lane >> 4;
-    const float inv_div = sqrtf((float)HD);
-    for (int tb = 0; tb < n; tb += 16) {
-        const int tl = tb + wave * 4 + pslot;
-        const int t = t0 + tl;
-        float kv[DPL];
-        if (tl < n) {
-            if (t == pos) {
-#pragma unroll
-                for (int i = 0; i < DPL; i++) kv[i] = kp[sub * DPL + i];
-            } else {
-                const u32x4 *p = (const u32x4 *)(kc + (size_t)t * HD + sub * DPL);
-#pragma unroll
-                for (int c = 0; c < DPL / 8; c++) {
-                    const u32x4 w = ldg_nt(p + c);
-                    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        kv[8 * c + 2 * e] = h2f(ws[e] & 0xFFFFu);
-                        kv[8 * c + 2 * e + 1] = h2f(ws[e] >> 16);
-                    }
-                }
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < DPL; i++) kv[i] = 0.f;
-        }
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-            float d = 0.f;
-#pragma unroll
-            for (int i = 0; i < DPL; i++) d += qr[g][sub * DPL + i] * kv[i];
-#pragma unroll
-            for (int o = 8; o > 0; o >>= 1) d += __shfl_xor(d, o, 16);
-            if (sub == 0 && tl < n) sc[g][tl] = d / inv_div;  // forward.odin:158 divides
-        }
-    }
-    __syncthreads();
-
-    // per-head max and exp-sum over this split (one wave per head)
-    for (int g = wave; g < G; g += WG / WAVE) {
-        float m = -INFINITY;
-        for (int i = lane; i < n; i += WAVE) m = fmaxf(m, sc[g][i]);
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, WAVE));
-        float l = 0.f;
-        for (int i = lane; i < n; i += WAVE) {
-            const float e = expf(sc[g][i] - m);
-            sc[g][i] = e;
-            l += e;
-        }
-        l = wave_sum(l);
-        if (lane == 0) { mx[g] = m; sm[g] = l; }
-    }
-    __syncthreads();
-
-    // o_g = sum_t p_g(t) v(t)
-    float acc[G][DPL];
-#pragma unroll
-    for (int g = 0; g < G; g++)
-#pragma unroll
-        for (int i = 0; i < DPL; i++) acc[g][i] = 0.f;
-    for (int tl = wave * 4 + pslot; tl < n; tl += 16) {
-        const int t = t0 + tl;
-        float vv[DPL];
-        if (t == pos) {
-#pragma unroll
-            for (int i = 0; i < DPL; i++) vv[i] = vp[sub * DPL + i];
-        } else {
-            const u32x4 *p = (const u32x4 *)(vc + (size_t)t * HD + sub * DPL);
-#pragma unroll
-            for (int c = 0; c < DPL / 8; c++) {
-                const u32x4 w = ldg_nt(p + c);
-                const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    vv[8 * c + 2 * e] = h2f(ws[e] & 0xFFFFu);
-                    vv[8 * c + 2 * e + 1] = h2f(ws[e] >> 16);
-                }
-            }
-        }
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-            const float pw = sc[g][tl];
-#pragma unroll
-            for (int i = 0; i < DPL; i++) acc[g][i] += pw * vv[i];
-        }
-    }
-#pragma unroll
-    for (int g = 0; g < G; g++)
-#pragma unroll
-        for (int i = 0; i < DPL; i++) {
-            float v = acc[g][i];
-            v += __shfl_xor(v, 16, WAVE);
-            v += __shfl_xor(v, 32, WAVE);
-            acc[g][i] = v;
-        }
-    if (pslot == 0) {
-#pragma unroll
-        for (int g = 0; g < G; g++)
-#pragma unroll
-            for (int i = 0; i < DPL; i++) ored[wave][g][sub * DPL + i] = acc[g][i];
-    }
-    __syncthreads();
-    const int stride = HD + 2;
-    for (int idx = tid; idx < G * HD; idx += WG) {
-        const int g = idx / HD, i = idx % HD;
-        const float o = ored[0][g][i] + ored[1][g][i] + ored[2][g][i] + ored[3][g][i];
-        float *pp = a.part + ((size_t)(kvh * G + g) * a.max_splits + split) * stride;
-        pp[i] = o;
-        if (i == 0) { pp[HD] = mx[g]; pp[HD + 1] = sm[g]; }
-    }
-    __syncthreads();
-
-    // last split of this kv head combines all splits
-    if (tid == 0) {
-        __threadfence();
-        const int prev = atomicAdd(a.counters + kvh, 1);
-        last_flag = (prev == nsplit - 1);
-    }
-    __syncthreads();
-    if (!last_flag) return;
-    __threadfence();
-    for (int idx = tid; idx < G * HD; idx += WG) {
-        const int g = idx / HD, i = idx % HD;
-        const float *pb = a.part + (size_t)(kvh * G + g) * a.max_splits * stride;
-        float M = -INFINITY;
-        for (int s = 0; s < nsplit; s++) M = fmaxf(M, __builtin_nontemporal_load(pb + (size_t)s * stride + HD));
-        float L = 0.f, O = 0.f;
-        for (int s = 0; s < nsplit; s++) {
-            const float *ps = pb + (size_t)s * stride;
-            const float f = expf(__builtin_nontemporal_load(ps + HD) - M);
-            L += __builtin_nontemporal_load(ps + HD + 1) * f;
-            O += __builtin_nontemporal_load(ps + i) * f;
-        }
-        a.out[(size_t)(kvh * G + g) * HD + i] = O / L;
-    }
-    if (tid == 0) {
-        a.counters[kvh] = 0;
-        __threadfence();
-    }
-}
-
-template <int HD>
-static hipError_t launch_attn_hd(const AttnArgs &a, int G, hipStream_t st) {
-    dim3 grid(a.max_splits, a.n_kv_heads), block(WG);
-    switch (G) {
-    case 1: hipLaunchKernelGGL((attn_kernel<HD, 1>), grid, block, 0, st, a); break;
-    case 2: hipLaunchKernelGGL((attn_kernel<HD, 2>), grid, block, 0, st, a); break;
-    case 4: hipLaunchKernelGGL((attn_kernel<HD, 4>), grid, block, 0, st, a); break;
-    case 8: hipLaunchKernelGGL((attn_kernel<HD, 8>), grid, block, 0, st, a); break;
-    default: return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
-}
-
-hipError_t launch_attn(const AttnArgs &a, int head_dim, hipStream_t st) {
-    const int G = a.n_heads / a.n_kv_heads;
-    if (a.chunk > 256 || a.chunk <= 0) return hipErrorInvalidValue;
-    if (head_dim == 128) return launch_attn_hd<128>(a, G, st);
-    if (head_dim == 256 && G <= 4) return launch_attn_hd<256>(a, G, st);
-    return hipErrorInvalidValue;
-}
-
-hipError_t launch_embed(const DMat &emb, const int32_t *state, float *x, int32_t vocab, hipStream_t st) {
-    hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(WG), 0, st, emb, state, x, vocab);
+hipError_t launch_embed(const DMat &emb, int32_t *state, float *x, int32_t vocab, const float *am_val,
+                        const int32_t *am_idx, int32_t *tokens_out, int finalize_only, hipStream_t st) {
+    hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(WG), 0, st, emb, state, x, vocab, am_val, am_idx, tokens_out,
+                       finalize_only);
     return hipGetLastError();
 }
 

@@ -43,7 +43,7 @@ struct GemvSeg {
     DMat m;
     float *y;
     int32_t wg_begin;  // first workgroup of this segment
-    int32_t pad;
+    int32_t ntiles;    // row tiles of this segment (gemv_q_kernel)
 };
 
 struct GemvArgs {
@@ -57,14 +57,18 @@ struct GemvArgs {
     const float *x;        // input vector, K floats
     const float *norm_w;   // if set: x is replaced by rmsnorm(x) * norm_w
     float eps;
-    int32_t pad;
-    // GEMV_ARGMAX
+    int32_t kernel;        // 0: gemv_kernel (any type), 1: gemv_q_kernel (Q4_K/Q6_K/Q8_0)
+    // GEMV_ARGMAX: per-workgroup (max, lowest index); reduced by the next
+    // embedding step, which state[4] = 1 asks for
     float *am_val;         // [total_wgs]
     int32_t *am_idx;       // [total_wgs]
-    int32_t *am_counter;   // 1 int, zero between launches
-    int32_t *state;        // [token, pos, step, err]
-    int32_t *tokens_out;   // greedy ids by step
+    int32_t *state;
 };
+
+// Device state of the token loop (int32 x 8):
+//   [0] token  [1] pos  [2] step  [3] capacity of tokens_out
+//   [4] argmax pending  [5] number of argmax partials
+enum { ST_TOKEN = 0, ST_POS = 1, ST_STEP = 2, ST_CAP = 3, ST_PENDING = 4, ST_NPART = 5, ST_WORDS = 8 };
 
 struct AttnArgs {
     const float *q, *k, *v;    // this token's raw projections
@@ -77,7 +81,6 @@ struct AttnArgs {
     int32_t chunk;             // positions per split
     int32_t max_splits;
     float *part;               // [n_heads][max_splits][head_dim + 2]
-    int32_t *counters;         // [n_kv_heads], zero between launches
     float *out;                // [n_heads * head_dim]
     int32_t n_heads, n_kv_heads;
 };
@@ -85,11 +88,20 @@ struct AttnArgs {
 // Host launchers (kernels.hip).  All return hipSuccess or the launch error.
 hipError_t launch_gemv(const GemvArgs &a, hipStream_t st);
 hipError_t launch_attn(const AttnArgs &a, int head_dim, hipStream_t st);
-hipError_t launch_embed(const DMat &emb, const int32_t *state, float *x, int32_t vocab, hipStream_t st);
+// Embedding of state[token] into x.  If state[4] is set, first reduces the
+// pending argmax partials of the previous step: token = argmax, pos += 1,
+// tokens_out[step++] = token.  finalize_only: do the reduction and stop.
+hipError_t launch_embed(const DMat &emb, int32_t *state, float *x, int32_t vocab, const float *am_val,
+                        const int32_t *am_idx, int32_t *tokens_out, int finalize_only, hipStream_t st);
+int attn_chunk(int head_dim);
+int attn_max_splits();
 hipError_t launch_dequant(const DMat &m, float *out, hipStream_t st);
 
-// Plan a GEMV over segments sharing one K: fills lpr, rows_per_wg, wg_begin,
-// total_wgs.  Returns false if K is not a multiple of 64.
+// Plan a GEMV over segments sharing one K: picks the kernel and fills lpr,
+// rows_per_wg, wg_begin, ntiles, total_wgs.  False if K is not a multiple of 64.
 bool plan_gemv(GemvArgs &a);
+bool gemv_q_supported(const GemvArgs &a);
+void plan_gemv_q(GemvArgs &a);
+hipError_t launch_gemv_q(const GemvArgs &a, hipStream_t st);
 
 }  // namespace oi

@@ -197,19 +197,44 @@ def test_forward_range_errors(make_model):
         infer.engine_destroy(e)
 
 
+def greedy_tie_aware(e, r, token, pos, n, tie_rel=1e-4):
+    """Walk the oracle's greedy path (both engines teacher-forced on it).  At
+    every step the GPU's pick must equal the oracle's unless the oracle's own
+    logits put the two within tie_rel * max|logit| (a near-tie that any f32
+    reordering may flip).  Returns (steps, near-tie steps, max scaled error)."""
+    ties, worst = 0, 0.0
+    for i in range(n):
+        got = infer.engine_forward(e, token, pos + i).copy()
+        ref = r.forward(token, pos + i)
+        worst = max(worst, scaled_err(got, ref))
+        rt, gt = refcpu.argmax(ref), int(np.argmax(got))
+        if gt != rt:
+            margin = float(ref[rt] - ref[gt])
+            assert margin <= tie_rel * float(np.max(np.abs(ref))), \
+                "step %d: gpu %d vs oracle %d, oracle margin %.3g" % (i, gt, rt, margin)
+            ties += 1
+        token = rt
+    return n, ties, worst
+
+
 def test_qwen3_06b_q8_0_greedy(make_model):
     """BASELINE config 1 (Qwen3-0.6B shape, Q8_0, tied output): token 0 then
-    greedy steps, GPU vs the oracle with the same f16 KV precision."""
+    greedy steps.  This seed has a near-tie at step 1 (oracle margin 4.0e-5 of
+    max|logit| 2.9), so the greedy path is checked tie-aware; logits must stay
+    within the scaled error bound at every step."""
     path = make_model("qwen3-0.6b-q8_0")
     e, r = _engines(path, 4096)
     try:
-        steps = 24
-        got = infer.engine_decode_greedy(e, 0, 0, steps)
-        ref = _greedy_ref(r, 0, 0, steps)
-        assert np.array_equal(got, ref), (got, ref)
-        # per-step logits of the same trajectory
-        logits = infer.engine_forward(e, int(ref[-1]), steps).copy()
-        assert scaled_err(logits, r.forward(int(ref[-1]), steps)) <= TOL
+        n, ties, worst = greedy_tie_aware(e, r, 0, 0, 32)
+        assert worst <= TOL
+        assert ties <= 2, ties
+        # the device-side loop equals the GPU's own forward + argmax loop
+        dev = infer.engine_decode_greedy(e, 0, 0, 16)
+        tok, host = 0, []
+        for pos in range(16):
+            tok = int(np.argmax(infer.engine_forward(e, tok, pos)))
+            host.append(tok)
+        assert np.array_equal(dev, np.array(host, np.int32))
     finally:
         infer.engine_destroy(e)
         r.close()
