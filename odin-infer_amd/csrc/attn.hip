@@ -1,20 +1,22 @@
 // attn.hip -- split-L grouped-query decode attention over the f16 KV cache
 // (reference: infer/forward.odin:117-175; f16 cache as infer/metal.odin:443-474).
 //
-// Grid: (splits, n_kv_heads).  A workgroup takes CH consecutive positions of
-// one KV head and serves all G = n_heads / n_kv_heads query heads of that
-// group, so each K/V row is read from HBM once per token (the reference
-// re-reads it for every query head).  Per workgroup:
-//   1. issue every K and V load of its positions (16 B per lane) up front,
+// attn_kernel, grid (splits, n_kv_heads): a workgroup takes CH consecutive
+// positions of one KV head and serves all G = n_heads / n_kv_heads query
+// heads of the group, so each K/V row is read from HBM once per token (the
+// reference re-reads it for every query head).  Per workgroup:
+//   1. issue the loads of its K and V tiles (16 B per lane, coalesced),
 //   2. meanwhile RMSNorm + RoPE the G query heads (and, in the split that
 //      holds `pos`, the new key; K/V[pos] are rounded to f16 and stored),
-//   3. scores q.k / sqrt(hd), split max and exp-sum, o = sum p v,
-//   4. write (o, m, l) to a partial buffer.
-// attn_combine_kernel then merges the splits of every query head with
-// exp(m_s - M) weights (a separate launch: the kernel boundary orders the
-// partial writes before the reads, with no fences or atomics).
-// The current position is used from LDS, so no workgroup reads a cache entry
-// written in the same launch.
+//   3. stage K (rows padded against bank conflicts) and V in LDS,
+//   4. scores: lane t computes q_g . k_t over a quarter of the dimensions,
+//      one quarter per wave; divided by sqrt(hd) (forward.odin:158),
+//   5. split max / exp-sum per head, o = sum_t p v_t (2 dims per lane),
+//   6. write (o, m, l) to a partial buffer.
+// attn_combine_kernel merges the splits of each query head with
+// exp(m_s - M) weights; the kernel boundary orders the partial writes before
+// the reads, so no fences or atomics are needed.  The current position is
+// used from LDS, so no workgroup reads a cache entry written in this launch.
 
 #include "device_common.h"
 
@@ -22,12 +24,14 @@ namespace oi {
 
 template <int HD>
 struct AttnShape {
-    static constexpr int LPP = HD / 8;     // lanes per position (8 halves = 16 B each)
-    static constexpr int PPR = WG / LPP;   // positions per load round
-    static constexpr int CH = 16384 / HD;  // positions per workgroup
-    static constexpr int NR = CH / PPR;    // load rounds per thread
+    static constexpr int CH = 8192 / HD;              // positions per workgroup (64 at hd 128)
+    static constexpr int KPAD = HD + 8;               // LDS row stride of K, in halves
+    static constexpr int CPR = HD / 8;                // 16-byte chunks per row
+    static constexpr int NLD = CH * CPR / WG;         // loads per thread per tensor
+    static constexpr int DPW = HD / 4;                // score dimensions per wave
+    static constexpr int DPL = HD / WAVE;             // o dimensions per lane
 };
-constexpr int ATTN_MAX_SPLITS = 512;
+constexpr int ATTN_MAX_SPLITS = 1024;
 
 static __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -35,24 +39,16 @@ static __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
-static __device__ __forceinline__ void unpack8(const u32x4 &w, float *out) {
-    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        out[2 * e] = h2f(ws[e] & 0xFFFFu);
-        out[2 * e + 1] = h2f(ws[e] >> 16);
-    }
-}
-
 template <int HD, int G>
 __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
     using S = AttnShape<HD>;
-    constexpr int OSZ = 4 * G * HD;
-    __shared__ float qr[G][HD];
+    __shared__ __attribute__((aligned(16))) uint16_t ks[S::CH * S::KPAD];
+    __shared__ __attribute__((aligned(16))) uint16_t vs[S::CH * HD];
+    __shared__ __attribute__((aligned(16))) float qr[G][HD];
     __shared__ float kp[HD], vp[HD];
-    __shared__ float sc[G][S::CH];
+    __shared__ float sp[4][G][S::CH];  // per-wave partial scores, then p in sp[0]
+    __shared__ float ob[4][G][HD];
     __shared__ float mx[G], sm[G], nrm[G + 1];
-    __shared__ float obuf[OSZ];  // o reduction
 
     const int split = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
     const int lane = tid & (WAVE - 1), wave = tid / WAVE;
@@ -62,24 +58,23 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
     const int t1 = min(t0 + S::CH, pos + 1), n = t1 - t0;
     uint16_t *kc = a.kc + (size_t)kvh * a.seq_len * HD;
     uint16_t *vc = a.vc + (size_t)kvh * a.seq_len * HD;
-    const int sub = tid % S::LPP, pslot = tid / S::LPP;
 
-    // 1. all K and V loads of this split in flight
-    u32x4 kreg[S::NR], vreg[S::NR];
+    // 1. K and V tile loads
+    u32x4 kr[S::NLD], vr[S::NLD];
 #pragma unroll
-    for (int j = 0; j < S::NR; j++) {
-        const int tl = pslot + S::PPR * j, t = t0 + tl;
-        if (tl < n && t != pos) {
-            kreg[j] = ldg_nt((const u32x4 *)(kc + (size_t)t * HD) + sub);
-            vreg[j] = ldg_nt((const u32x4 *)(vc + (size_t)t * HD) + sub);
+    for (int j = 0; j < S::NLD; j++) {
+        const int c = tid + j * WG, tl = c / S::CPR, ch = c % S::CPR;
+        if (tl < n && t0 + tl != pos) {
+            kr[j] = ldg_nt((const u32x4 *)(kc + (size_t)(t0 + tl) * HD) + ch);
+            vr[j] = ldg_nt((const u32x4 *)(vc + (size_t)(t0 + tl) * HD) + ch);
         } else {
-            kreg[j] = u32x4{0u, 0u, 0u, 0u};
-            vreg[j] = u32x4{0u, 0u, 0u, 0u};
+            kr[j] = u32x4{0u, 0u, 0u, 0u};
+            vr[j] = u32x4{0u, 0u, 0u, 0u};
         }
     }
 
-    // 2. RMSNorm + RoPE of the G query heads (and of k at pos), ops.odin:7-19
-    //    and forward.odin:117-145; cos/sin come from the host-built table
+    // 2. RMSNorm + RoPE of the G query heads (and of k at pos): ops.odin:7-19,
+    //    forward.odin:117-145; cos/sin come from the host-built table
     const bool has_pos = pos >= t0 && pos < t1;
     const float2 *cs = a.rope_cs + (size_t)pos * (HD / 2);
     for (int i = tid; i < G * HD; i += WG) qr[i / HD][i % HD] = a.q[(size_t)kvh * G * HD + i];
@@ -110,54 +105,65 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
         v[i] = x * c - y * sn;
         v[i + HD / 2] = x * sn + y * c;
     }
+
+    // 3. stage the tiles in LDS (rows beyond n are zero; row pos-t0 is set below)
+#pragma unroll
+    for (int j = 0; j < S::NLD; j++) {
+        const int c = tid + j * WG, tl = c / S::CPR, ch = c % S::CPR;
+        *(u32x4 *)(ks + tl * S::KPAD + ch * 8) = kr[j];
+        *(u32x4 *)(vs + tl * HD + ch * 8) = vr[j];
+    }
     __syncthreads();
     if (has_pos) {
+        const int tl = pos - t0;
         for (int i = tid; i < HD; i += WG) {
             const uint16_t kb = f2h(kp[i]), vb = f2h(vp[i]);
             kc[(size_t)pos * HD + i] = kb;
             vc[(size_t)pos * HD + i] = vb;
-            kp[i] = h2f(kb);
-            vp[i] = h2f(vb);
+            ks[tl * S::KPAD + i] = kb;
+            vs[tl * HD + i] = vb;
         }
         __syncthreads();
     }
 
-    // 3. scores (forward.odin:152-159: the dot is divided by sqrt(head_dim))
-    const float div = sqrtf((float)HD);
+    // 4. partial scores: lane = position, wave = quarter of the dimensions
+    if (lane < S::CH) {
+        float acc[G];
 #pragma unroll
-    for (int j = 0; j < S::NR; j++) {
-        const int tl = pslot + S::PPR * j, t = t0 + tl;
-        float kv[8];
-        if (t == pos) {
+        for (int g = 0; g < G; g++) acc[g] = 0.f;
+        const uint16_t *krow = ks + lane * S::KPAD + wave * S::DPW;
 #pragma unroll
-            for (int e = 0; e < 8; e++) kv[e] = kp[8 * sub + e];
-        } else {
-            unpack8(kreg[j], kv);
+        for (int c = 0; c < S::DPW / 8; c++) {
+            const u32x4 w = *(const u32x4 *)(krow + 8 * c);
+            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+            float kv[8];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                kv[2 * e] = h2f(ws[e] & 0xFFFFu);
+                kv[2 * e + 1] = h2f(ws[e] >> 16);
+            }
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                const float4 q0 = *(const float4 *)&qr[g][wave * S::DPW + 8 * c];
+                const float4 q1 = *(const float4 *)&qr[g][wave * S::DPW + 8 * c + 4];
+                acc[g] += q0.x * kv[0] + q0.y * kv[1] + q0.z * kv[2] + q0.w * kv[3] + q1.x * kv[4] +
+                          q1.y * kv[5] + q1.z * kv[6] + q1.w * kv[7];
+            }
         }
 #pragma unroll
-        for (int g = 0; g < G; g++) {
-            float d = 0.f;
-#pragma unroll
-            for (int e = 0; e < 8; e++) d += qr[g][8 * sub + e] * kv[e];
-#pragma unroll
-            for (int o = S::LPP / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, S::LPP);
-            if (sub == 0 && tl < n) sc[g][tl] = d / div;
-        }
+        for (int g = 0; g < G; g++) sp[wave][g][lane] = acc[g];
     }
     __syncthreads();
 
-    // split-local softmax statistics (ops.odin:21-37 over this split)
+    // 5. scores, split-local max and exp-sum (ops.odin:21-37), one wave per head
+    const float div = sqrtf((float)HD);
     for (int g = wave; g < G; g += WG / WAVE) {
-        float m = -INFINITY;
-        for (int i = lane; i < n; i += WAVE) m = fmaxf(m, sc[g][i]);
-        m = wave_max(m);
-        float l = 0.f;
-        for (int i = lane; i < n; i += WAVE) {
-            const float e = expf(sc[g][i] - m);
-            sc[g][i] = e;
-            l += e;
-        }
-        l = wave_sum(l);
+        float sc = -INFINITY;
+        if (lane < n) sc = ((sp[0][g][lane] + sp[1][g][lane]) + (sp[2][g][lane] + sp[3][g][lane])) / div;
+        const float m = wave_max(sc);
+        const float e = lane < n ? expf(sc - m) : 0.f;
+        const float l = wave_sum(e);
+        if (lane < S::CH) sp[0][g][lane] = e;
         if (lane == 0) {
             mx[g] = m;
             sm[g] = l;
@@ -165,50 +171,42 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
     }
     __syncthreads();
 
-    // o_g = sum_t p_g(t) v(t) over this split
-    float acc[G][8];
+    // o_g = sum_t p_g(t) v(t): lane holds DPL dims, wave w takes t = w, w+4, ...
+    float acc[G][S::DPL];
 #pragma unroll
     for (int g = 0; g < G; g++)
 #pragma unroll
-        for (int e = 0; e < 8; e++) acc[g][e] = 0.f;
+        for (int e = 0; e < S::DPL; e++) acc[g][e] = 0.f;
+    for (int tl = wave; tl < n; tl += WG / WAVE) {
+        float vv[S::DPL];
+        if (S::DPL == 2) {
+            const uint32_t w = *(const uint32_t *)(vs + tl * HD + 2 * lane);
+            vv[0] = h2f(w & 0xFFFFu);
+            vv[S::DPL - 1] = h2f(w >> 16);
+        } else {
+            const u32x2 w = *(const u32x2 *)(vs + tl * HD + S::DPL * lane);
+            const uint32_t ws[2] = {w.x, w.y};
 #pragma unroll
-    for (int j = 0; j < S::NR; j++) {
-        const int tl = pslot + S::PPR * j, t = t0 + tl;
-        if (tl < n) {
-            float vv[8];
-            if (t == pos) {
+            for (int e = 0; e < S::DPL; e++) vv[e] = h2f((ws[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+        }
 #pragma unroll
-                for (int e = 0; e < 8; e++) vv[e] = vp[8 * sub + e];
-            } else {
-                unpack8(vreg[j], vv);
-            }
+        for (int g = 0; g < G; g++) {
+            const float p = sp[0][g][tl];
 #pragma unroll
-            for (int g = 0; g < G; g++) {
-                const float p = sc[g][tl];
-#pragma unroll
-                for (int e = 0; e < 8; e++) acc[g][e] += p * vv[e];
-            }
+            for (int e = 0; e < S::DPL; e++) acc[g][e] += p * vv[e];
         }
     }
 #pragma unroll
-    for (int o = S::LPP; o < WAVE; o <<= 1)
+    for (int g = 0; g < G; g++)
 #pragma unroll
-        for (int g = 0; g < G; g++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) acc[g][e] += __shfl_xor(acc[g][e], o, WAVE);
-    float(*ored)[G][HD] = (float(*)[G][HD])obuf;
-    if (lane < S::LPP)
-#pragma unroll
-        for (int g = 0; g < G; g++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) ored[wave][g][8 * sub + e] = acc[g][e];
+        for (int e = 0; e < S::DPL; e++) ob[wave][g][S::DPL * lane + e] = acc[g][e];
     __syncthreads();
 
-    // 4. partial (o, m, l) of this split
+    // 6. partial (o, m, l) of this split
     const int stride = HD + 2;
     for (int idx = tid; idx < G * HD; idx += WG) {
         const int g = idx / HD, i = idx % HD;
-        const float o = (ored[0][g][i] + ored[1][g][i]) + (ored[2][g][i] + ored[3][g][i]);
+        const float o = (ob[0][g][i] + ob[1][g][i]) + (ob[2][g][i] + ob[3][g][i]);
         float *pp = a.part + ((size_t)(kvh * G + g) * a.max_splits + split) * stride;
         pp[i] = o;
         if (i == 0) {

@@ -83,30 +83,52 @@ bool matrix_bytes(uint32_t type, int64_t rows, int64_t cols, size_t &bytes) {
 
 // Repack one GGUF matrix into the device layout (see DMat in oi_kernels.h).
 // Writes into `dst` (bytes from matrix_bytes) and returns the region offsets.
-struct Regions { size_t q = 0, s = 0, d = 0; };
+struct Regions { size_t q = 0, plane = 0, s = 0, d = 0; };
 Regions repack(uint32_t type, const uint8_t *src, int64_t rows, int64_t cols, uint8_t *dst) {
     Regions r;
-    const int64_t n = rows * cols;
-    if (type == T_Q6_K) {
-        const int64_t nsb = n / 256;
-        r.q = 0;
-        r.s = (size_t)nsb * 192;
-        r.d = r.s + (size_t)nsb * 16;
-        for (int64_t i = 0; i < nsb; i++) {
-            const uint8_t *b = src + i * 210;
-            std::memcpy(dst + r.q + i * 192, b, 192);  // ql[128], qh[64]
-            std::memcpy(dst + r.s + i * 16, b + 192, 16);
-            std::memcpy(dst + r.d + i * 2, b + 208, 2);
-        }
+    const int64_t U = cols / 64, NSB = cols / 256, NB = cols / 32;
+    if (type == T_Q4_K) {
+        r.plane = (size_t)(rows * U * 16);
+        r.s = 2 * r.plane;
+        for (int64_t row = 0; row < rows; row++)
+            for (int64_t sb = 0; sb < NSB; sb++) {
+                const uint8_t *b = src + (row * NSB + sb) * 144;
+                std::memcpy(dst + r.s + (row * NSB + sb) * 16, b, 16);
+                for (int p = 0; p < 4; p++) {
+                    const size_t u = (size_t)(row * U + 4 * sb + p);
+                    std::memcpy(dst + u * 16, b + 16 + 32 * p, 16);
+                    std::memcpy(dst + r.plane + u * 16, b + 32 + 32 * p, 16);
+                }
+            }
+    } else if (type == T_Q6_K) {
+        r.plane = (size_t)(rows * U * 16);
+        r.s = 3 * r.plane;
+        r.d = r.s + (size_t)(rows * NSB * 16);
+        for (int64_t row = 0; row < rows; row++)
+            for (int64_t sb = 0; sb < NSB; sb++) {
+                const uint8_t *b = src + (row * NSB + sb) * 210;  // ql[128] qh[64] sc[16] d
+                std::memcpy(dst + r.s + (row * NSB + sb) * 16, b + 192, 16);
+                std::memcpy(dst + r.d + (row * NSB + sb) * 2, b + 208, 2);
+                for (int h = 0; h < 2; h++)
+                    for (int half = 0; half < 2; half++) {
+                        const int l0 = 16 * half;
+                        const size_t u = (size_t)(row * U + 4 * sb + 2 * h + half);
+                        std::memcpy(dst + u * 16, b + 64 * h + l0, 16);
+                        std::memcpy(dst + r.plane + u * 16, b + 64 * h + 32 + l0, 16);
+                        std::memcpy(dst + 2 * r.plane + u * 16, b + 128 + 32 * h + l0, 16);
+                    }
+            }
     } else if (type == T_Q8_0) {
-        const int64_t nb = n / 32;
-        r.q = 0;
-        r.d = (size_t)nb * 32;
-        for (int64_t i = 0; i < nb; i++) {
-            const uint8_t *b = src + i * 34;
-            std::memcpy(dst + r.d + i * 2, b, 2);
-            std::memcpy(dst + r.q + i * 32, b + 2, 32);
-        }
+        r.plane = (size_t)(rows * U * 16);
+        r.d = 4 * r.plane;
+        for (int64_t row = 0; row < rows; row++)
+            for (int64_t blk = 0; blk < NB; blk++) {
+                const uint8_t *b = src + (row * NB + blk) * 34;
+                std::memcpy(dst + r.d + (row * NB + blk) * 2, b, 2);
+                const size_t u = (size_t)(row * U + blk / 2);
+                for (int h = 0; h < 2; h++)
+                    std::memcpy(dst + (size_t)(2 * (blk & 1) + h) * r.plane + u * 16, b + 2 + 16 * h, 16);
+            }
     } else {
         size_t bytes = 0;
         matrix_bytes(type, rows, cols, bytes);
@@ -121,6 +143,7 @@ DMat make_dmat(uint32_t type, int64_t rows, int64_t cols, const uint8_t *dev, co
     m.rows = (int32_t)rows;
     m.cols = (int32_t)cols;
     m.q = dev + r.q;
+    m.plane = (int64_t)r.plane;
     m.s = dev + r.s;
     m.d = (const uint16_t *)(dev + r.d);
     return m;

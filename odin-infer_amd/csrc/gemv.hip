@@ -45,11 +45,10 @@ struct WQ4K {
     u32x4 h, q0, q1;
 };
 static __device__ __forceinline__ void wload(const DMat &m, int row, int u, WQ4K &w) {
-    const uint8_t *blk = m.q + ((size_t)row * (m.cols >> 8) + (u >> 2)) * 144;
-    const int p = u & 3;
-    w.h = ldg_nt((const u32x4 *)blk);
-    w.q0 = ldg_nt((const u32x4 *)(blk + 16 + 32 * p));
-    w.q1 = ldg_nt((const u32x4 *)(blk + 32 + 32 * p));
+    const size_t ui = (size_t)row * (m.cols >> 6) + u;
+    w.h = ldg_nt((const u32x4 *)(m.s + ((size_t)row * (m.cols >> 8) + (u >> 2)) * 16));
+    w.q0 = ldg_nt((const u32x4 *)(m.q + ui * 16));
+    w.q1 = ldg_nt((const u32x4 *)(m.q + m.plane + ui * 16));
 }
 struct XU4K {
     u32x4 h[4], m[4], l[4];
@@ -104,11 +103,11 @@ struct WQ6K {
 };
 static __device__ __forceinline__ void wload(const DMat &m, int row, int u, WQ6K &w) {
     const size_t sbi = (size_t)row * (m.cols >> 8) + (u >> 2);
-    const int h = (u >> 1) & 1, l0 = (u & 1) * 16;
-    const uint8_t *qb = m.q + sbi * 192;
-    w.l0 = ldg_nt((const u32x4 *)(qb + 64 * h + l0));
-    w.l1 = ldg_nt((const u32x4 *)(qb + 64 * h + 32 + l0));
-    w.qh = ldg_nt((const u32x4 *)(qb + 128 + 32 * h + l0));
+    const size_t ui = (size_t)row * (m.cols >> 6) + u;
+    const int h = (u >> 1) & 1;
+    w.l0 = ldg_nt((const u32x4 *)(m.q + ui * 16));
+    w.l1 = ldg_nt((const u32x4 *)(m.q + m.plane + ui * 16));
+    w.qh = ldg_nt((const u32x4 *)(m.q + 2 * m.plane + ui * 16));
     w.sc = ldg_nt((const u32x2 *)(m.s + sbi * 16 + 8 * h));
     w.d = m.d[sbi];
 }
@@ -166,11 +165,10 @@ struct WQ80 {
     uint32_t d;
 };
 static __device__ __forceinline__ void wload(const DMat &m, int row, int u, WQ80 &w) {
-    const size_t b0 = (size_t)row * (m.cols >> 5) + 2 * u;
-    const u32x4 *p = (const u32x4 *)(m.q + b0 * 32);
+    const size_t ui = (size_t)row * (m.cols >> 6) + u;
 #pragma unroll
-    for (int i = 0; i < 4; i++) w.q[i] = ldg_nt(p + i);
-    w.d = *(const uint32_t *)(m.d + b0);
+    for (int c = 0; c < 4; c++) w.q[c] = ldg_nt((const u32x4 *)(m.q + c * m.plane + ui * 16));
+    w.d = *(const uint32_t *)(m.d + 2 * ui);
 }
 static __device__ __forceinline__ float wdot(const WQ80 &w, int u, const XU4K &x) {
     int ah[2] = {0, 0}, am[2] = {0, 0}, al[2] = {0, 0};

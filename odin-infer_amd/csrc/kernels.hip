@@ -21,13 +21,13 @@ namespace oi {
 // --------------------------------------------------------------------------
 
 // Q4_K unit u of a row: ggml/quant.odin:178-209
-__device__ void decode_unit_q4k(const uint8_t *row, int u, float *out) {
+__device__ void decode_unit_q4k(const DMat &m, int row, int u, float *out) {
 #pragma clang fp contract(off)
-    const uint8_t *blk = row + (size_t)(u >> 2) * 144;
-    const int p = u & 3;
-    const u32x4 hdr = *(const u32x4 *)blk;
-    const u32x4 q0 = *(const u32x4 *)(blk + 16 + 32 * p);
-    const u32x4 q1 = *(const u32x4 *)(blk + 32 + 32 * p);
+    const int U = m.cols >> 6, p = u & 3;
+    const size_t ui = (size_t)row * U + u;
+    const u32x4 hdr = *(const u32x4 *)(m.s + ((size_t)row * (m.cols >> 8) + (u >> 2)) * 16);
+    const u32x4 q0 = *(const u32x4 *)(m.q + ui * 16);
+    const u32x4 q1 = *(const u32x4 *)(m.q + m.plane + ui * 16);
     const float d = h2f(hdr.x & 0xFFFFu), dmin = h2f(hdr.x >> 16);
     const uint32_t sw[3] = {hdr.y, hdr.z, hdr.w};
     uint32_t sc0, m0, sc1, m1;
@@ -44,54 +44,44 @@ __device__ void decode_unit_q4k(const uint8_t *row, int u, float *out) {
     }
 }
 
-// Q6_K unit u: ggml/quant.odin:212-247.  Writes the 64 values at their
-// positions in the 256-element super-block (out points at the super-block).
-__device__ void decode_unit_q6k(const DMat &m, int row, int u, float *sbout) {
+// Q6_K unit u: ggml/quant.odin:212-247.  out[16k + i] is element
+// 128h + 32k + l0 + i of the super-block.
+__device__ void decode_unit_q6k(const DMat &m, int row, int u, float *out) {
 #pragma clang fp contract(off)
-    const int nsb = m.cols >> 8;
+    const int U = m.cols >> 6, nsb = m.cols >> 8;
     const int sb = u >> 2, h = (u >> 1) & 1, l0 = (u & 1) * 16;
-    const size_t sbi = (size_t)row * nsb + sb;
-    const uint8_t *qb = m.q + sbi * 192;
+    const size_t ui = (size_t)row * U + u, sbi = (size_t)row * nsb + sb;
+    const uint8_t *qlA = m.q + ui * 16;                // ql[64h + l0 + i]
+    const uint8_t *qlB = m.q + m.plane + ui * 16;      // ql[64h + 32 + l0 + i]
+    const uint8_t *qh = m.q + 2 * m.plane + ui * 16;   // qh[32h + l0 + i]
     const int8_t *sc = (const int8_t *)(m.s + sbi * 16) + 8 * h;
     const float d = h2f(m.d[sbi]);
-    const uint8_t *ql = qb + 64 * h, *qh = qb + 128 + 32 * h;
+    const int is = l0 / 16;
     for (int i = 0; i < 16; i++) {
-        const int l = l0 + i, is = l / 16;
-        const int q1 = (int)((ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32;
-        const int q2 = (int)((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
-        const int q3 = (int)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
-        const int q4 = (int)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
-        float *y = sbout + 128 * h;
-        y[l] = d * (float)sc[is + 0] * (float)q1;
-        y[l + 32] = d * (float)sc[is + 2] * (float)q2;
-        y[l + 64] = d * (float)sc[is + 4] * (float)q3;
-        y[l + 96] = d * (float)sc[is + 6] * (float)q4;
+        const int q1 = (int)((qlA[i] & 0xF) | (((qh[i] >> 0) & 3) << 4)) - 32;
+        const int q2 = (int)((qlB[i] & 0xF) | (((qh[i] >> 2) & 3) << 4)) - 32;
+        const int q3 = (int)((qlA[i] >> 4) | (((qh[i] >> 4) & 3) << 4)) - 32;
+        const int q4 = (int)((qlB[i] >> 4) | (((qh[i] >> 6) & 3) << 4)) - 32;
+        out[i] = d * (float)sc[is + 0] * (float)q1;
+        out[16 + i] = d * (float)sc[is + 2] * (float)q2;
+        out[32 + i] = d * (float)sc[is + 4] * (float)q3;
+        out[48 + i] = d * (float)sc[is + 6] * (float)q4;
     }
 }
 
-// Any type: decode unit u of `row` into out[64] (in element order).
+// Any type: decode unit u of `row` into out[64] (order: see unit_elem).
 __device__ void decode_unit(const DMat &m, int row, int u, float *out) {
 #pragma clang fp contract(off)
     switch (m.type) {
-    case T_Q4_K:
-        decode_unit_q4k(m.q + (size_t)row * (m.cols / 256) * 144, u, out);
-        break;
-    case T_Q6_K: {
-        // the unit's 64 values are spread over its super-block; decode into
-        // a local super-block image and copy the unit's elements out
-        float sbuf[256];
-        decode_unit_q6k(m, row, u, sbuf);
-        const int h = (u >> 1) & 1, l0 = (u & 1) * 16;
-        for (int k = 0; k < 4; k++)
-            for (int i = 0; i < 16; i++) out[16 * k + i] = sbuf[128 * h + 32 * k + l0 + i];
-        break;
-    }
+    case T_Q4_K: decode_unit_q4k(m, row, u, out); break;
+    case T_Q6_K: decode_unit_q6k(m, row, u, out); break;
     case T_Q8_0: {  // ggml/quant.odin:87-96
-        const size_t blk0 = (size_t)row * (m.cols / 32) + 2 * u;
-        for (int b = 0; b < 2; b++) {
-            const float d = h2f(m.d[blk0 + b]);
-            const int8_t *qs = (const int8_t *)(m.q + (blk0 + b) * 32);
-            for (int j = 0; j < 32; j++) out[32 * b + j] = d * (float)qs[j];
+        const size_t ui = (size_t)row * (m.cols >> 6) + u;
+        const size_t b0 = (size_t)row * (m.cols >> 5) + 2 * u;
+        for (int c = 0; c < 4; c++) {
+            const float d = h2f(m.d[b0 + (c >> 1)]);
+            const int8_t *qs = (const int8_t *)(m.q + c * m.plane + ui * 16);
+            for (int j = 0; j < 16; j++) out[16 * c + j] = d * (float)qs[j];
         }
         break;
     }
@@ -212,129 +202,25 @@ __device__ __forceinline__ float dot4_nib(uint32_t w, float4 x) {
            (float)(w >> 24) * x.w;
 }
 
-// Per-type unit GEMV pieces.  Each "load" fetches one unit's bytes for one
-// row into registers; each "dot" consumes them against x.
-
-struct Q4KRegs { u32x4 hdr, q0, q1; };
-__device__ __forceinline__ void load_q4k(const DMat &m, int row, int u, Q4KRegs &r) {
-    const uint8_t *blk = m.q + ((size_t)row * (m.cols >> 8) + (u >> 2)) * 144;
-    const int p = u & 3;
-    r.hdr = ldg_nt((const u32x4 *)blk);
-    r.q0 = ldg_nt((const u32x4 *)(blk + 16 + 32 * p));
-    r.q1 = ldg_nt((const u32x4 *)(blk + 32 + 32 * p));
-}
-// sum over the unit of dequant(w) * x, in the factored form
-// d*sc*sum(q*x) - dmin*m*sum(x) per group of 32
-__device__ __forceinline__ float dot_q4k(const Q4KRegs &r, int u, const XView &xv) {
-    const int p = u & 3;
-    const float d = h2f(r.hdr.x & 0xFFFFu), dmin = h2f(r.hdr.x >> 16);
-    const uint32_t sw[3] = {r.hdr.y, r.hdr.z, r.hdr.w};
-    uint32_t sc0, m0, sc1, m1;
-    scale_min_k4(2 * p, sw, sc0, m0);
-    scale_min_k4(2 * p + 1, sw, sc1, m1);
-    const uint32_t qw[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
-    float alo = 0.f, ahi = 0.f;
-    const int cb = u * 16;
+// dot of one unit of the row with x (from LDS), via the exact decode
+__device__ __forceinline__ float dot_unit(const DMat &m, int row, int u, const XView &xv) {
+    if (m.type == T_F32) {
+        const float4 *p = (const float4 *)((const float *)m.q + (size_t)row * m.cols + 64 * u);
+        float a = 0.f;
 #pragma unroll
-    for (int w = 0; w < 8; w++) {
-        alo += dot4_nib(qw[w] & 0x0F0F0F0Fu, xv.chunk(cb + w));
-        ahi += dot4_nib((qw[w] >> 4) & 0x0F0F0F0Fu, xv.chunk(cb + 8 + w));
+        for (int i = 0; i < 16; i++) {
+            const float4 w = p[i];
+            const float4 x = xv.chunk(u * 16 + i);
+            a += w.x * x.x + w.y * x.y + w.z * x.z + w.w * x.w;
+        }
+        return a;
     }
-    const float slo = xv.s16[4 * u] + xv.s16[4 * u + 1];
-    const float shi = xv.s16[4 * u + 2] + xv.s16[4 * u + 3];
-    return d * (float)sc0 * alo - dmin * (float)m0 * slo + d * (float)sc1 * ahi - dmin * (float)m1 * shi;
-}
-
-struct Q6KRegs { u32x4 ql0, ql1, qh; u32x2 sc; uint32_t d; };
-__device__ __forceinline__ void load_q6k(const DMat &m, int row, int u, Q6KRegs &r) {
-    const size_t sbi = (size_t)row * (m.cols >> 8) + (u >> 2);
-    const int h = (u >> 1) & 1, l0 = (u & 1) * 16;
-    const uint8_t *qb = m.q + sbi * 192;
-    r.ql0 = ldg_nt((const u32x4 *)(qb + 64 * h + l0));
-    r.ql1 = ldg_nt((const u32x4 *)(qb + 64 * h + 32 + l0));
-    r.qh = ldg_nt((const u32x4 *)(qb + 128 + 32 * h + l0));
-    r.sc = ldg_nt((const u32x2 *)(m.s + sbi * 16 + 8 * h));
-    r.d = m.d[sbi];
-}
-__device__ __forceinline__ float dot_q6k(const Q6KRegs &r, int u, const XView &xv) {
-    const int sb = u >> 2, h = (u >> 1) & 1, l0 = (u & 1) * 16;
-    const uint32_t ql0[4] = {r.ql0.x, r.ql0.y, r.ql0.z, r.ql0.w};
-    const uint32_t ql1[4] = {r.ql1.x, r.ql1.y, r.ql1.z, r.ql1.w};
-    const uint32_t qh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
-    float a[4] = {0.f, 0.f, 0.f, 0.f};
-    const int e0 = 256 * sb + 128 * h + l0;  // element of (k=0, i=0)
-#pragma unroll
-    for (int w = 0; w < 4; w++) {
-        const uint32_t v0 = (ql0[w] & 0x0F0F0F0Fu) | ((qh[w] & 0x03030303u) << 4);
-        const uint32_t v1 = (ql1[w] & 0x0F0F0F0Fu) | (((qh[w] >> 2) & 0x03030303u) << 4);
-        const uint32_t v2 = ((ql0[w] >> 4) & 0x0F0F0F0Fu) | (((qh[w] >> 4) & 0x03030303u) << 4);
-        const uint32_t v3 = ((ql1[w] >> 4) & 0x0F0F0F0Fu) | (((qh[w] >> 6) & 0x03030303u) << 4);
-        a[0] += dot4_nib(v0, xv.chunk((e0 + 0) / 4 + w));
-        a[1] += dot4_nib(v1, xv.chunk((e0 + 32) / 4 + w));
-        a[2] += dot4_nib(v2, xv.chunk((e0 + 64) / 4 + w));
-        a[3] += dot4_nib(v3, xv.chunk((e0 + 96) / 4 + w));
-    }
-    // scales sc[8h + l0/16 + 2k] -> bytes (l0/16) + 2k of the 8-byte word
-    const int sh = l0 / 16;
-    const float d = h2f(r.d);
-    float acc = 0.f;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int bi = sh + 2 * k;
-        const uint32_t word = bi < 4 ? r.sc.x : r.sc.y;
-        const int8_t s = (int8_t)((word >> ((bi & 3) * 8)) & 0xFFu);
-        // q = v - 32  ->  sum(q*x) = sum(v*x) - 32*sum(x)
-        const float sx = xv.s16[(e0 + 32 * k) / 16];
-        acc += d * (float)s * (a[k] - 32.f * sx);
-    }
-    return acc;
-}
-
-struct Q80Regs { u32x4 q[4]; uint32_t d01; };
-__device__ __forceinline__ void load_q80(const DMat &m, int row, int u, Q80Regs &r) {
-    const size_t b0 = (size_t)row * (m.cols >> 5) + 2 * u;
-    const u32x4 *p = (const u32x4 *)(m.q + b0 * 32);
-#pragma unroll
-    for (int i = 0; i < 4; i++) r.q[i] = ldg_nt(p + i);
-    r.d01 = *(const uint32_t *)(m.d + b0);
-}
-__device__ __forceinline__ float sdot4(uint32_t w, float4 x) {
-    return (float)(int8_t)(w & 0xFFu) * x.x + (float)(int8_t)((w >> 8) & 0xFFu) * x.y +
-           (float)(int8_t)((w >> 16) & 0xFFu) * x.z + (float)(int8_t)(w >> 24) * x.w;
-}
-__device__ __forceinline__ float dot_q80(const Q80Regs &r, int u, const XView &xv) {
-    float a0 = 0.f, a1 = 0.f;
-    const int cb = u * 16;
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        a0 += sdot4(r.q[i].x, xv.chunk(cb + 4 * i + 0)) + sdot4(r.q[i].y, xv.chunk(cb + 4 * i + 1)) +
-              sdot4(r.q[i].z, xv.chunk(cb + 4 * i + 2)) + sdot4(r.q[i].w, xv.chunk(cb + 4 * i + 3));
-        a1 += sdot4(r.q[i + 2].x, xv.chunk(cb + 8 + 4 * i + 0)) + sdot4(r.q[i + 2].y, xv.chunk(cb + 8 + 4 * i + 1)) +
-              sdot4(r.q[i + 2].z, xv.chunk(cb + 8 + 4 * i + 2)) + sdot4(r.q[i + 2].w, xv.chunk(cb + 8 + 4 * i + 3));
-    }
-    return h2f(r.d01 & 0xFFFFu) * a0 + h2f(r.d01 >> 16) * a1;
-}
-
-__device__ __forceinline__ float dot_f16(const DMat &m, int row, int u, const XView &xv) {
-    const u32x4 *p = (const u32x4 *)((const uint16_t *)m.q + (size_t)row * m.cols + 64 * u);
+    float w[64];
+    decode_unit(m, row, u, w);
     float a = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const u32x4 w = ldg_nt(p + i);
-        const float4 x0 = xv.chunk(u * 16 + 2 * i), x1 = xv.chunk(u * 16 + 2 * i + 1);
-        a += h2f(w.x & 0xFFFFu) * x0.x + h2f(w.x >> 16) * x0.y + h2f(w.y & 0xFFFFu) * x0.z + h2f(w.y >> 16) * x0.w;
-        a += h2f(w.z & 0xFFFFu) * x1.x + h2f(w.z >> 16) * x1.y + h2f(w.w & 0xFFFFu) * x1.z + h2f(w.w >> 16) * x1.w;
-    }
-    return a;
-}
-__device__ __forceinline__ float dot_f32(const DMat &m, int row, int u, const XView &xv) {
-    const float4 *p = (const float4 *)((const float *)m.q + (size_t)row * m.cols + 64 * u);
-    float a = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const float4 w = p[i];
-        const float4 x = xv.chunk(u * 16 + i);
-        a += w.x * x.x + w.y * x.y + w.z * x.z + w.w * x.w;
+    for (int j = 0; j < 64; j++) {
+        const int g = unit_elem(m.type, u, j);  // element of the row
+        a += w[j] * ((const float *)&xv.x4[xswz(g >> 2)])[g & 3];
     }
     return a;
 }
@@ -344,55 +230,11 @@ template <int R>
 __device__ __forceinline__ void gemv_rows(const DMat &m, const int *rows, int j, int lpr, const XView &xv,
                                           float *acc) {
     const int U = m.cols >> 6;
-    switch (m.type) {
-    case T_Q4_K:
-        for (int u = j; u < U; u += lpr) {
-            Q4KRegs w[R];
+    for (int u = j; u < U; u += lpr)
 #pragma unroll
-            for (int r = 0; r < R; r++)
-                if (rows[r] < m.rows) load_q4k(m, rows[r], u, w[r]);
-#pragma unroll
-            for (int r = 0; r < R; r++)
-                if (rows[r] < m.rows) acc[r] += dot_q4k(w[r], u, xv);
-        }
-        break;
-    case T_Q6_K:
-        for (int u = j; u < U; u += lpr) {
-            Q6KRegs w[R];
-#pragma unroll
-            for (int r = 0; r < R; r++)
-                if (rows[r] < m.rows) load_q6k(m, rows[r], u, w[r]);
-#pragma unroll
-            for (int r = 0; r < R; r++)
-                if (rows[r] < m.rows) acc[r] += dot_q6k(w[r], u, xv);
-        }
-        break;
-    case T_Q8_0:
-        for (int u = j; u < U; u += lpr) {
-            Q80Regs w[R];
-#pragma unroll
-            for (int r = 0; r < R; r++)
-                if (rows[r] < m.rows) load_q80(m, rows[r], u, w[r]);
-#pragma unroll
-            for (int r = 0; r < R; r++)
-                if (rows[r] < m.rows) acc[r] += dot_q80(w[r], u, xv);
-        }
-        break;
-    case T_F16:
-        for (int u = j; u < U; u += lpr)
-#pragma unroll
-            for (int r = 0; r < R; r++)
-                if (rows[r] < m.rows) acc[r] += dot_f16(m, rows[r], u, xv);
-        break;
-    default:
-        for (int u = j; u < U; u += lpr)
-#pragma unroll
-            for (int r = 0; r < R; r++)
-                if (rows[r] < m.rows) acc[r] += dot_f32(m, rows[r], u, xv);
-        break;
-    }
+        for (int r = 0; r < R; r++)
+            if (rows[r] < m.rows) acc[r] += dot_unit(m, rows[r], u, xv);
 }
-
 
 // Workgroup tile: 4 waves; each wave holds 64/lpr lane groups; each group
 // owns R consecutive rows and lpr lanes that split the row's units.

@@ -9,25 +9,29 @@ namespace oi {
 // ggml type ids (reference ggml/gguf.odin:27-42)
 enum : int32_t { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14 };
 
-// A weight matrix resident in HBM, in the GEMV layout.  Every matrix is cut
-// into "units" of 64 consecutive weights of one row; a unit is the work of
-// one lane.  Per type:
-//   Q4_K  q: the GGUF super-blocks unchanged (144 B = 16 B header + 128 B of
-//         nibbles; 144 is a multiple of 16, so every 16 B piece is aligned).
-//         Unit u of a row = super-block u/4, group pair u%4.
-//   Q6_K  q: per super-block the 128 B of ql then the 64 B of qh (192 B);
-//         s: the 16 int8 scales per super-block; d: f16 d per super-block.
-//         (The GGUF 210 B block is only 2 B aligned; this split keeps the
-//         byte count and makes every load a naturally aligned 16 B piece.)
-//         Unit u = super-block u/4, half h=(u%4)/2, columns l0=16*(u%2).
-//   Q8_0  q: 32 B of int8 per block; d: f16 d per block.  Unit = 2 blocks.
-//   F32/F16  q: the values.
+// A weight matrix resident in HBM, in the GEMV layout.  Every row is cut into
+// U = cols/64 "units" of 64 consecutive weights; a unit is the work of one
+// lane.  The bytes of a unit are split into 16-byte pieces, and piece k of
+// every (row, unit) is stored in plane k in (row, unit) order, so the 64
+// lanes of a wave reading piece k of 64 consecutive units read one
+// contiguous 1 KB.  The byte count equals the GGUF one.  Per type:
+//   Q4_K  plane 0: qs[32p .. 32p+15] and plane 1: qs[32p+16 .. 32p+31] of
+//         super-block u/4, group pair p = u%4;  s: the 16-byte super-block
+//         header (f16 d, f16 dmin, 12 bytes of 6-bit scales/mins) per (row, sb).
+//   Q6_K  unit u = super-block u/4, half h = (u/2)%2, columns l0 = 16(u%2):
+//         plane 0: ql[64h+l0 ..+15], plane 1: ql[64h+32+l0 ..+15],
+//         plane 2: qh[32h+l0 ..+15];  s: 16 int8 scales per (row, sb);
+//         d: f16 d per (row, sb).
+//   Q8_0  unit u = blocks 2u, 2u+1: plane c = int8 values 16c .. 16c+15 of
+//         the unit;  d: f16 d per (row, block).
+//   F32/F16  q: the values, row-major.
 struct DMat {
     int32_t type;
     int32_t rows;
     int32_t cols;
     int32_t pad;
-    const uint8_t *q;
+    const uint8_t *q;   // plane 0
+    int64_t plane;      // bytes from one plane to the next (rows * U * 16)
     const uint8_t *s;
     const uint16_t *d;
 };
