@@ -293,12 +293,12 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     *out = nullptr;
     if (!opts->use_hip) return fail(OI_E_ARG, "use_hip must be set: this library has no CPU path");
     if (opts->max_ctx <= 0) return fail(OI_E_ARG, "max_ctx must be positive");
-    int rc = check_device(opts->device);
-    if (rc) return rc;
 
+    // the file and the model are checked first, as the reference builds the
+    // transformer before it initialises the GPU (infer/engine.odin:21-25)
     GgufFile g;
     std::string err;
-    rc = g.open(path, err);
+    int rc = g.open(path, err);
     if (rc) return fail(rc, err);
 
     // load_config (infer/model.odin:99-139)
@@ -382,6 +382,7 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
         wbytes += ((size_t)w.t->nbytes + 255) & ~(size_t)255;
     }
     e->weight_bytes = wbytes;
+    if ((rc = check_device(opts->device))) return rc;
 
     // device memory plan
     e->chunk = attn_chunk((int)c.head_dim);

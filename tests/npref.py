@@ -1,0 +1,213 @@
+"""Independent numpy restatements used to pin the CPU oracle (oracle/refcpu.c).
+
+They are written from the block formats and the model mathematics, in a
+different form from the oracle (vectorised, element-wise, float64 where the
+reference is float32), so that a dropped term, a wrong sign or a transposed
+index in the oracle fails a comparison:
+
+  * dequant_*_elem: the reference's element-wise decoders k4_dequant_elem
+    (qwen3_5/metal.odin:476-486) and k6_dequant_elem (:542-555), vectorised in
+    float32 with the same operation order, so they must agree bit-for-bit
+    with the row decoders of ggml/quant.odin;
+  * scale_min_unpack: 6-bit (scale, min) fields read by bit position;
+  * forward_f64: a float64 dense-Qwen3 forward (RMSNorm, per-head q/k norm,
+    NEOX RoPE, grouped-query attention, SwiGLU) from the dequantized weights.
+"""
+import numpy as np
+
+F32 = np.float32
+
+
+def f16(b2):
+    """little-endian byte pairs (..., 2) -> float32"""
+    return np.ascontiguousarray(b2).view(np.uint16).astype(np.uint16).view(np.float16).astype(F32)
+
+
+def scale_min_unpack(q12):
+    """(n, 12) uint8 -> sc (n, 8), m (n, 8): bit-field layout of the Q4_K
+    scales: entries 0-3 are the low 6 bits of bytes 0-3 (scales) and 4-7
+    (mins); entries 4-7 take their low 4 bits from the nibbles of bytes 8-11
+    (scale: low nibble, min: high nibble) and their top 2 bits from the top 2
+    bits of bytes 0-3 (scales) and 4-7 (mins)."""
+    q = q12.astype(np.int64)
+    sc = np.zeros((q.shape[0], 8), np.int64)
+    m = np.zeros_like(sc)
+    for j in range(4):
+        sc[:, j] = q[:, j] & 0x3F
+        m[:, j] = q[:, 4 + j] & 0x3F
+        sc[:, 4 + j] = (q[:, 8 + j] & 0x0F) + 16 * (q[:, j] >> 6)
+        m[:, 4 + j] = (q[:, 8 + j] >> 4) + 16 * (q[:, 4 + j] >> 6)
+    return sc, m
+
+
+def dequant_q4k_elem(blocks):
+    """(nb*144,) uint8 -> (nb*256,) float32, element-wise form."""
+    b = blocks.reshape(-1, 144)
+    d, dmin = f16(b[:, 0:2])[:, 0], f16(b[:, 2:4])[:, 0]
+    sc, m = scale_min_unpack(b[:, 4:16])
+    qs = b[:, 16:].astype(np.int64)
+    e = np.arange(256)
+    sup, ws = e >> 6, e & 63
+    hf, l = ws >> 5, ws & 31
+    is_ = sup * 2 + hf
+    nib = (qs[:, sup * 32 + l] >> (4 * hf)) & 0xF
+    # d * sc * nib - dmin * m, left to right, each op rounded to float32
+    t = (d[:, None] * sc[:, is_].astype(F32)).astype(F32)
+    t = (t * nib.astype(F32)).astype(F32)
+    mm = (dmin[:, None] * m[:, is_].astype(F32)).astype(F32)
+    return (t - mm).astype(F32).reshape(-1)
+
+
+def dequant_q6k_elem(blocks):
+    b = blocks.reshape(-1, 210)
+    ql, qh = b[:, :128].astype(np.int64), b[:, 128:192].astype(np.int64)
+    sc = b[:, 192:208].view(np.int8).astype(np.int64)
+    d = f16(b[:, 208:210])[:, 0]
+    e = np.arange(256)
+    hf, within = e >> 7, e & 127
+    l, sub = within & 31, within >> 5
+    is_ = l >> 4
+    qloff, qhoff, scoff = hf * 64, hf * 32, hf * 8
+    lo_idx = qloff + l + 32 * (sub & 1)
+    lo = (ql[:, lo_idx] >> (4 * (sub >> 1))) & 0xF
+    hi = (qh[:, qhoff + l] >> (2 * sub)) & 3
+    q = (lo | (hi << 4)) - 32
+    s = sc[:, scoff + is_ + 2 * sub]
+    t = (d[:, None] * s.astype(F32)).astype(F32)
+    return (t * q.astype(F32)).astype(F32).reshape(-1)
+
+
+def dequant_q8_0_elem(blocks):
+    b = blocks.reshape(-1, 34)
+    d = f16(b[:, 0:2])[:, 0]
+    q = b[:, 2:].view(np.int8).astype(F32)
+    return (d[:, None] * q).astype(F32).reshape(-1)
+
+
+def dequant(kind, blocks, n):
+    if kind == 0:
+        return np.ascontiguousarray(blocks).view(F32)[:n].copy()
+    if kind == 1:
+        return f16(np.ascontiguousarray(blocks).reshape(-1, 2))[:, 0][:n]
+    return {8: dequant_q8_0_elem, 12: dequant_q4k_elem, 14: dequant_q6k_elem}[kind](blocks)[:n]
+
+
+# ------------------------------------------------------------ float64 model --
+
+class GGUFWeights:
+    """Minimal GGUF reader for the tests (independent of both parsers under
+    test): returns float64 dequantized weights by tensor name."""
+
+    def __init__(self, path):
+        import struct
+        data = np.fromfile(path, np.uint8)
+        self.data = data
+        pos = 0
+
+        def rd(fmt):
+            nonlocal pos
+            v = struct.unpack_from("<" + fmt, data, pos)
+            pos += struct.calcsize("<" + fmt)
+            return v[0]
+
+        def rstr():
+            nonlocal pos
+            n = rd("Q")
+            s = bytes(data[pos:pos + n]).decode()
+            pos += n
+            return s
+
+        assert rd("I") == 0x46554747
+        rd("I")
+        nt, nm = rd("Q"), rd("Q")
+        self.meta = {}
+        scalar = {0: "B", 1: "b", 2: "H", 3: "h", 4: "I", 5: "i", 6: "f", 7: "B", 10: "Q", 11: "q", 12: "d"}
+        for _ in range(nm):
+            k = rstr()
+            t = rd("I")
+            if t == 8:
+                self.meta[k] = rstr()
+            elif t in scalar:
+                self.meta[k] = rd(scalar[t])
+            else:
+                raise ValueError("array metadata not expected in synthetic files")
+        self.tensors = {}
+        for _ in range(nt):
+            name = rstr()
+            nd = rd("I")
+            dims = [rd("Q") for _ in range(nd)]
+            kind = rd("I")
+            off = rd("Q")
+            self.tensors[name] = (dims, kind, off)
+        align = self.meta.get("general.alignment", 32)
+        self.base = (pos + align - 1) // align * align
+
+    def get(self, name):
+        dims, kind, off = self.tensors[name]
+        n = int(np.prod(dims))
+        e, b = {0: (1, 4), 1: (1, 2), 8: (32, 34), 12: (256, 144), 14: (256, 210)}[kind]
+        raw = self.data[self.base + off: self.base + off + n // e * b]
+        w = dequant(kind, raw, n).astype(np.float64)
+        return w.reshape(dims[::-1]) if len(dims) > 1 else w
+
+
+def forward_f64(W, tokens, f16_kv=True):
+    """Logits (float64) after each token of `tokens` at positions 0.. ."""
+    m = W.meta
+    D = m["qwen3.embedding_length"]
+    L = m["qwen3.block_count"]
+    H = m["qwen3.attention.head_count"]
+    KVH = m["qwen3.attention.head_count_kv"]
+    hd = m["qwen3.attention.key_length"]
+    theta = m.get("qwen3.rope.freq_base", 1e6)
+    eps = m.get("qwen3.attention.layer_norm_rms_epsilon", 1e-6)
+    emb = W.get("token_embd.weight")
+    out_w = W.get("output.weight") if "output.weight" in W.tensors else emb
+
+    def rms(x, w):
+        return w * x / np.sqrt(np.mean(x * x) + eps)
+
+    def rope(v, pos):  # NEOX pairs (i, i + hd/2)
+        i = np.arange(hd // 2)
+        ang = pos * theta ** (-(i / (hd // 2)))
+        c, s = np.cos(ang), np.sin(ang)
+        a, b = v[..., : hd // 2], v[..., hd // 2:]
+        return np.concatenate([a * c - b * s, a * s + b * c], axis=-1)
+
+    def r16(v):
+        return v.astype(np.float16).astype(np.float64) if f16_kv else v
+
+    layers = []
+    for l in range(L):
+        p = "blk.%d." % l
+        layers.append({k: W.get(p + k + ".weight") for k in
+                       ["attn_norm", "ffn_norm", "attn_q_norm", "attn_k_norm", "attn_q", "attn_k", "attn_v",
+                        "attn_output", "ffn_gate", "ffn_down", "ffn_up"]})
+    kc = [[] for _ in range(L)]
+    vc = [[] for _ in range(L)]
+    outs = []
+    for pos, tok in enumerate(tokens):
+        x = emb[tok].copy()
+        for l, lw in enumerate(layers):
+            xb = rms(x, lw["attn_norm"])
+            q = (lw["attn_q"] @ xb).reshape(H, hd)
+            k = (lw["attn_k"] @ xb).reshape(KVH, hd)
+            v = (lw["attn_v"] @ xb).reshape(KVH, hd)
+            q = rope(np.stack([rms(qh, lw["attn_q_norm"]) for qh in q]), pos)
+            k = rope(np.stack([rms(kh, lw["attn_k_norm"]) for kh in k]), pos)
+            kc[l].append(r16(k))
+            vc[l].append(r16(v))
+            K, V = np.stack(kc[l]), np.stack(vc[l])  # (t, KVH, hd)
+            o = np.zeros((H, hd))
+            for h in range(H):
+                g = h // (H // KVH)
+                sc = K[:, g, :] @ q[h] / np.sqrt(hd)
+                p_ = np.exp(sc - sc.max())
+                p_ /= p_.sum()
+                o[h] = p_ @ V[:, g, :]
+            x = x + lw["attn_output"] @ o.reshape(-1)
+            xb = rms(x, lw["ffn_norm"])
+            gt, up = lw["ffn_gate"] @ xb, lw["ffn_up"] @ xb
+            x = x + lw["ffn_down"] @ (gt / (1 + np.exp(-gt)) * up)
+        outs.append(out_w @ rms(x, W.get("output_norm.weight")))
+    return outs

@@ -1,0 +1,180 @@
+"""Pins the CPU oracle (oracle/refcpu.c) -- the checker of every GPU parity
+test -- against closed forms, exhaustive small domains, the reference's own
+known-answer tests (qwen3_5/tests.odin) and independent numpy restatements
+(tests/npref.py).  CPU only."""
+import numpy as np
+import pytest
+
+import npref
+import refcpu
+from helpers import random_blocks, same_bits
+
+F32 = np.float32
+
+
+def test_f16_to_f32_all_patterns():
+    bits = np.arange(65536, dtype=np.uint16)
+    got = np.array([refcpu.lib().ref_f16_to_f32(int(b)) for b in bits], F32)
+    assert same_bits(got, bits.view(np.float16).astype(F32))
+
+
+def test_f32_to_f16_round_to_nearest_even():
+    rng = np.random.default_rng(0)
+    xs = np.concatenate([rng.standard_normal(4000).astype(F32) * s for s in (1e-8, 1e-6, 1e-4, 1, 1e3, 6e4)] +
+                        [np.array([2 ** -25, 2 ** -24 * 1.5, 2 ** -24 * 2.5, 65504, 65519.99, 65520, 1e9,
+                                   np.inf, -np.inf, 0.0, -0.0, 1 + 2 ** -11, 1 + 3 * 2 ** -11], F32)])
+    got = np.array([refcpu.lib().ref_f32_to_f16(float(v)) for v in xs], np.uint16)
+    with np.errstate(over="ignore"):
+        assert np.array_equal(got, xs.astype(np.float16).view(np.uint16))
+
+
+@pytest.mark.parametrize("j", range(8))
+def test_get_scale_min_k4_exhaustive(j):
+    """All 2^12 patterns of the 12 bits that entry j reads (the other bits random)."""
+    rng = np.random.default_rng(j)
+    q = rng.integers(0, 256, size=(4096, 12), dtype=np.uint8)
+    pat = np.arange(4096)
+    if j < 4:
+        q[:, j] = (q[:, j] & 0xC0) | (pat & 0x3F)
+        q[:, j + 4] = (q[:, j + 4] & 0xC0) | (pat >> 6)
+    else:
+        q[:, j + 4] = pat & 0xFF
+        q[:, j - 4] = (q[:, j - 4] & 0x3F) | (((pat >> 8) & 3) << 6)
+        q[:, j] = (q[:, j] & 0x3F) | (((pat >> 10) & 3) << 6)
+    sc_ref, m_ref = npref.scale_min_unpack(q)
+    got = np.array([refcpu.get_scale_min_k4(j, row) for row in q])
+    assert np.array_equal(got[:, 0], sc_ref[:, j]) and np.array_equal(got[:, 1], m_ref[:, j])
+    assert len(set(zip(got[:, 0], got[:, 1]))) == 4096  # 12 bits -> 4096 distinct (sc, m)
+
+
+@pytest.mark.parametrize("kind,e,b", [(12, 256, 144), (14, 256, 210), (8, 32, 34), (1, 1, 2), (0, 1, 4)])
+def test_dequant_matches_elementwise_form(kind, e, b):
+    rng = np.random.default_rng(kind)
+    n = 256 * 40
+    blocks = random_blocks(kind, n // e, rng)
+    assert same_bits(refcpu.dequant_row(kind, blocks, n), npref.dequant(kind, blocks, n))
+
+
+def test_dequant_known_answers():
+    # Q4_K: d=1, dmin=0.5, every (sc, m) = (1, 2): value = q - 1
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = np.array([1.0], np.float16).view(np.uint8)
+    blk[2:4] = np.array([0.5], np.float16).view(np.uint8)
+    blk[4:8], blk[8:12], blk[12:16] = 1, 2, 0x21
+    blk[16:] = np.tile(np.arange(16, dtype=np.uint8), 8) | (np.uint8(15) << 4)
+    y = refcpu.dequant_row(12, blk, 256)
+    expect = np.concatenate([np.concatenate([np.tile(np.arange(16), 2), np.full(32, 15)]) for _ in range(4)]) - 1.0
+    assert np.array_equal(y, expect.astype(F32))
+    # Q6_K: d=0.25, all scales 4 -> value = q - 32 over ql/qh bit fields
+    blk = np.zeros(210, np.uint8)
+    blk[192:208] = 4
+    blk[208:210] = np.array([0.25], np.float16).view(np.uint8)
+    blk[0:128] = 0x5A  # low nibble 10, high nibble 5
+    blk[128:192] = 0b11100100  # qh 2-bit fields 0,1,2,3 for sub-blocks 0..3
+    y = refcpu.dequant_row(14, blk, 256).reshape(2, 4, 32)
+    for k, (lo, hi) in enumerate([(10, 0), (10, 1), (5, 2), (5, 3)]):
+        assert np.all(y[:, k, :] == (lo + 16 * hi) - 32)
+    # Q8_0: d = -2 -> -2 * q
+    blk = np.zeros(34, np.uint8)
+    blk[0:2] = np.array([-2.0], np.float16).view(np.uint8)
+    blk[2:] = np.arange(-16, 16, dtype=np.int8).view(np.uint8)
+    assert np.array_equal(refcpu.dequant_row(8, blk, 32), (-2.0 * np.arange(-16, 16)).astype(F32))
+
+
+def test_dot_f32():
+    a = np.arange(1, 49, dtype=F32)
+    b = np.ones(48, F32)
+    assert refcpu.dot_f32(a, b) == 48 * 49 / 2  # exact in float32
+    rng = np.random.default_rng(1)
+    for n in (16, 100, 4096, 12288, 7):
+        a, b = rng.standard_normal(n).astype(F32), rng.standard_normal(n).astype(F32)
+        ref = float(np.dot(a.astype(np.float64), b))
+        assert abs(refcpu.dot_f32(a, b) - ref) <= 1e-5 * float(np.abs(a).dot(np.abs(b)))
+
+
+@pytest.mark.parametrize("kind", [12, 14, 8])
+def test_matmul_t_f64_and_thread_invariance(kind):
+    from oi import synth
+    rows, cols = 300, 1024
+    w = synth.tensor_f32(3, "mm", rows, cols)
+    blocks = synth.quantize_rows(kind, w)
+    x = np.random.default_rng(2).standard_normal(cols).astype(F32)
+    y1 = refcpu.matmul_t(blocks, kind, x, rows, 1)
+    for t in (3, 8):
+        assert np.array_equal(refcpu.matmul_t(blocks, kind, x, rows, t), y1)  # one thread per row
+    wd = npref.dequant(kind, blocks, rows * cols).reshape(rows, cols).astype(np.float64)
+    ref = wd @ x.astype(np.float64)
+    assert np.max(np.abs(y1 - ref)) <= 1e-5 * np.max(np.abs(ref))
+
+
+def test_rmsnorm_known_answer():
+    # qwen3_5/tests.odin:127-139: x=[3,4], w=1 -> x / sqrt(12.5)
+    o = refcpu.rmsnorm([3.0, 4.0], [1.0, 1.0], 1e-8)
+    assert np.allclose(o, np.array([3, 4]) / np.sqrt(12.5), atol=1e-5)
+    rng = np.random.default_rng(4)
+    x, w = rng.standard_normal(4096), rng.standard_normal(4096)
+    ref = w * x / np.sqrt(np.mean(x * x) + 1e-6)
+    assert np.max(np.abs(refcpu.rmsnorm(x, w, 1e-6) - ref)) <= 1e-5 * np.max(np.abs(ref))
+
+
+def test_softmax_and_argmax():
+    x = np.array([1.0, 2.0, 3.0], F32)
+    ref = np.exp(x - 3) / np.exp(x - 3).sum()
+    assert np.allclose(refcpu.softmax(x), ref, rtol=1e-6)
+    assert refcpu.softmax(np.zeros(4, F32)).tolist() == [0.25] * 4
+    # sampler/sampler.odin:79-89: strict '>' keeps the first maximum
+    assert refcpu.argmax(np.array([1, 3, 3, 2], F32)) == 1
+    assert refcpu.argmax(np.zeros(10, F32)) == 0
+    assert refcpu.argmax(np.array([-5, -1, -1], F32)) == 1
+
+
+@pytest.mark.parametrize("name", ["tiny-q4_k", "tiny-q8_0", "tiny-f32"])
+def test_forward_vs_float64_model(make_model, name):
+    """The oracle's whole forward (f16 KV mode) against an independent
+    float64 model on the same weights."""
+    path = make_model(name)
+    W = npref.GGUFWeights(path)
+    tokens = [0, 7, 123, 5, 1000 % 1024, 42]
+    ref = npref.forward_f64(W, tokens, f16_kv=True)
+    r = refcpu.RefEngine(path, max_ctx=64, num_threads=4, kv_f16=True)
+    try:
+        for pos, t in enumerate(tokens):
+            got = r.forward(t, pos)
+            err = np.max(np.abs(got - ref[pos])) / np.max(np.abs(ref[pos]))
+            assert err <= 2e-4, (pos, err)
+    finally:
+        r.close()
+
+
+def test_forward_f32_kv_mode(make_model):
+    path = make_model("tiny-q8_0")
+    W = npref.GGUFWeights(path)
+    tokens = [0, 3, 9]
+    ref = npref.forward_f64(W, tokens, f16_kv=False)
+    r = refcpu.RefEngine(path, max_ctx=16, num_threads=2, kv_f16=False)
+    try:
+        for pos, t in enumerate(tokens):
+            got = r.forward(t, pos)
+            assert np.max(np.abs(got - ref[pos])) / np.max(np.abs(ref[pos])) <= 2e-4
+    finally:
+        r.close()
+
+
+def test_forward_range_and_load_errors(make_model, tmp_path):
+    path = make_model("tiny-q8_0")
+    r = refcpu.RefEngine(path, max_ctx=16)
+    try:
+        for tok, pos in [(-1, 0), (10 ** 7, 0), (0, -1), (0, 16)]:
+            with pytest.raises(RuntimeError, match="out of range"):
+                r.forward(tok, pos)
+    finally:
+        r.close()
+    bad = tmp_path / "bad.gguf"
+    bad.write_bytes(b"GGUX" + bytes(60))
+    with pytest.raises(RuntimeError, match="not a GGUF"):
+        refcpu.RefEngine(str(bad))
+    data = open(path, "rb").read()
+    trunc = tmp_path / "trunc.gguf"
+    trunc.write_bytes(data[: len(data) // 2])
+    with pytest.raises(RuntimeError, match="past end|corrupt|truncated"):
+        refcpu.RefEngine(str(trunc))
