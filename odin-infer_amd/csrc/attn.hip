@@ -59,6 +59,24 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
     uint16_t *kc = a.kc + (size_t)kvh * a.seq_len * HD;
     uint16_t *vc = a.vc + (size_t)kvh * a.seq_len * HD;
 
+    // 0. this token's q (and k, v at pos) first: vector loads return in order,
+    //    so they must not queue behind the tile loads
+    const bool has_pos = pos >= t0 && pos < t1;
+    constexpr int QPT = (G * HD + WG - 1) / WG;
+    float qreg[QPT];
+#pragma unroll
+    for (int i = 0; i < QPT; i++) {
+        const int idx = tid + i * WG;
+        qreg[i] = idx < G * HD ? a.q[(size_t)kvh * G * HD + idx] : 0.f;
+    }
+    float kraw = 0.f, vraw = 0.f;
+    if (has_pos && tid < HD) {
+        kraw = a.k[(size_t)kvh * HD + tid];
+        vraw = a.v[(size_t)kvh * HD + tid];
+    }
+    const float2 *cs = a.rope_cs + (size_t)pos * (HD / 2);
+    const float2 csr = tid < HD / 2 ? cs[tid] : make_float2(0.f, 0.f);
+
     // 1. K and V tile loads
     u32x4 kr[S::NLD], vr[S::NLD];
 #pragma unroll
@@ -75,14 +93,17 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
 
     // 2. RMSNorm + RoPE of the G query heads (and of k at pos): ops.odin:7-19,
     //    forward.odin:117-145; cos/sin come from the host-built table
-    const bool has_pos = pos >= t0 && pos < t1;
-    const float2 *cs = a.rope_cs + (size_t)pos * (HD / 2);
-    for (int i = tid; i < G * HD; i += WG) qr[i / HD][i % HD] = a.q[(size_t)kvh * G * HD + i];
-    if (has_pos)
-        for (int i = tid; i < HD; i += WG) {
-            kp[i] = a.k[(size_t)kvh * HD + i];
-            vp[i] = a.v[(size_t)kvh * HD + i];
-        }
+#pragma unroll
+    for (int i = 0; i < QPT; i++) {
+        const int idx = tid + i * WG;
+        if (idx < G * HD) qr[idx / HD][idx % HD] = qreg[i];
+    }
+    if (has_pos && tid < HD) {
+        kp[tid] = kraw;
+        vp[tid] = vraw;
+    }
+    __shared__ float2 csl[HD / 2];
+    if (tid < HD / 2) csl[tid] = csr;
     __syncthreads();
     const int nvec = G + (has_pos ? 1 : 0);
     for (int g = wave; g < nvec; g += WG / WAVE) {
@@ -101,7 +122,7 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
         const float s = nrm[g];
         const float x = w[i] * (s * v[i]);
         const float y = w[i + HD / 2] * (s * v[i + HD / 2]);
-        const float c = cs[i].x, sn = cs[i].y;
+        const float c = csl[i].x, sn = csl[i].y;
         v[i] = x * c - y * sn;
         v[i + HD / 2] = x * sn + y * c;
     }

@@ -22,29 +22,45 @@ static __device__ __forceinline__ T ldg_nt(const T *p) {
     return __builtin_nontemporal_load(p);
 }
 
-// byte i (0..11) of the packed Q4_K scales held in three words
-static __device__ __forceinline__ uint32_t sbyte(const uint32_t sw[3], int i) {
-    uint32_t w = i < 4 ? sw[0] : (i < 8 ? sw[1] : sw[2]);
-    return (w >> ((i & 3) * 8)) & 0xFFu;
+// (sc, m) of groups 2p and 2p+1 of a Q4_K super-block from the device header
+// words hw1..hw3 (bits 24p..24p+23 of the 96-bit tail, see DMat)
+static __device__ __forceinline__ void q4k_scales(int p, uint32_t hw1, uint32_t hw2, uint32_t hw3, uint32_t &sc0,
+                                                  uint32_t &m0, uint32_t &sc1, uint32_t &m1) {
+    const uint32_t lo = p == 0 || p == 1 ? hw1 : (p == 2 ? hw2 : hw3), hi = p < 2 ? hw2 : hw3;
+    const uint32_t f = __builtin_amdgcn_alignbit(hi, lo, (uint32_t)((24 * p) & 31));
+    sc0 = f & 63u;
+    m0 = (f >> 6) & 63u;
+    sc1 = (f >> 12) & 63u;
+    m1 = (f >> 18) & 63u;
 }
 
-// get_scale_min_k4 (ggml/quant.odin:64-73)
-static __device__ __forceinline__ void scale_min_k4(int j, const uint32_t sw[3], uint32_t &sc, uint32_t &m) {
-    if (j < 4) {
-        sc = sbyte(sw, j) & 63u;
-        m = sbyte(sw, j + 4) & 63u;
-    } else {
-        sc = (sbyte(sw, j + 4) & 0xFu) | ((sbyte(sw, j - 4) >> 6) << 4);
-        m = (sbyte(sw, j + 4) >> 4) | ((sbyte(sw, j) >> 6) << 4);
-    }
+// Cross-lane moves within rows of 16 lanes (DPP), cheaper than LDS-routed
+// shuffles: quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror (lane i of
+// each 8 <-> 7-i) and row_mirror (lane i of each 16 <-> 15-i).
+#define OI_DPP(v, ctrl) \
+    __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (v)), (ctrl), 0xF, 0xF, false))
+static __device__ __forceinline__ float dpp_sum4(float v) {  // sum over aligned groups of 4 lanes
+    v += OI_DPP(v, 0xB1);
+    return v + OI_DPP(v, 0x4E);
 }
-
-
-static __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+static __device__ __forceinline__ float dpp_mirror8(float v) { return OI_DPP(v, 0x141); }
+static __device__ __forceinline__ float dpp_max8(float v) {  // max over aligned groups of 8 lanes
+    v = fmaxf(v, OI_DPP(v, 0xB1));
+    v = fmaxf(v, OI_DPP(v, 0x4E));
+    return fmaxf(v, OI_DPP(v, 0x141));
+}
+// sum over aligned groups of n lanes (n a power of two <= 64); every lane of
+// a group ends with the group's sum
+static __device__ __forceinline__ float lane_group_sum(float v, int n) {
+    if (n >= 2) v += OI_DPP(v, 0xB1);
+    if (n >= 4) v += OI_DPP(v, 0x4E);
+    if (n >= 8) v += OI_DPP(v, 0x141);
+    if (n >= 16) v += OI_DPP(v, 0x140);
+    if (n >= 32) v += __shfl_xor(v, 16, WAVE);
+    if (n >= 64) v += __shfl_xor(v, 32, WAVE);
     return v;
 }
+static __device__ __forceinline__ float wave_sum(float v) { return lane_group_sum(v, WAVE); }
 
 // (value, index) order of a greedy argmax that keeps the first maximum
 // (sampler/sampler.odin:79-89 scans with a strict '>')

@@ -81,6 +81,38 @@ bool matrix_bytes(uint32_t type, int64_t rows, int64_t cols, size_t &bytes) {
     return true;
 }
 
+// Q4_K super-block header in the device form: d, dmin, then the 6-bit
+// (scale, min) of each group pair p as one 24-bit field at bits 24p of the
+// tail.  The values are those of get_scale_min_k4 (ggml/quant.odin:64-73).
+void q4k_header(const uint8_t *blk, uint8_t *out) {
+    const uint8_t *q = blk + 4;
+    uint8_t sc[8], mn[8];
+    for (int j = 0; j < 8; j++) {
+        if (j < 4) {
+            sc[j] = q[j] & 63;
+            mn[j] = q[j + 4] & 63;
+        } else {
+            sc[j] = (uint8_t)((q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4));
+            mn[j] = (uint8_t)((q[j + 4] >> 4) | ((q[j] >> 6) << 4));
+        }
+    }
+    std::memcpy(out, blk, 4);
+    uint64_t lo = 0, hi = 0;  // 96-bit tail as two words
+    for (int p = 0; p < 4; p++) {
+        const uint64_t f = (uint64_t)sc[2 * p] | (uint64_t)mn[2 * p] << 6 | (uint64_t)sc[2 * p + 1] << 12 |
+                           (uint64_t)mn[2 * p + 1] << 18;
+        const int bit = 24 * p;
+        if (bit >= 64) {
+            hi |= f << (bit - 64);
+        } else {
+            lo |= f << bit;
+            if (bit + 24 > 64) hi |= f >> (64 - bit);
+        }
+    }
+    std::memcpy(out + 4, &lo, 8);
+    std::memcpy(out + 12, &hi, 4);
+}
+
 // Repack one GGUF matrix into the device layout (see DMat in oi_kernels.h).
 // Writes into `dst` (bytes from matrix_bytes) and returns the region offsets.
 struct Regions { size_t q = 0, plane = 0, s = 0, d = 0; };
@@ -93,7 +125,7 @@ Regions repack(uint32_t type, const uint8_t *src, int64_t rows, int64_t cols, ui
         for (int64_t row = 0; row < rows; row++)
             for (int64_t sb = 0; sb < NSB; sb++) {
                 const uint8_t *b = src + (row * NSB + sb) * 144;
-                std::memcpy(dst + r.s + (row * NSB + sb) * 16, b, 16);
+                q4k_header(b, dst + r.s + (row * NSB + sb) * 16);
                 for (int p = 0; p < 4; p++) {
                     const size_t u = (size_t)(row * U + 4 * sb + p);
                     std::memcpy(dst + u * 16, b + 16 + 32 * p, 16);

@@ -87,11 +87,11 @@ static __device__ __forceinline__ float wdot(const WQ4K &w, int u, const XU4K &x
     }
     const int p = u & 3;
     const float d = h2f(w.h.x & 0xFFFFu), dmin = h2f(w.h.x >> 16);
-    const uint32_t sw[3] = {w.h.y, w.h.z, w.h.w};
     uint32_t sc0, m0, sc1, m1;
-    scale_min_k4(2 * p, sw, sc0, m0);
-    scale_min_k4(2 * p + 1, sw, sc1, m1);
-    const float q0 = plane_sum(ah0, am0, al0) * x.xs0, q1 = plane_sum(ah1, am1, al1) * x.xs1;
+    q4k_scales(p, w.h.y, w.h.z, w.h.w, sc0, m0, sc1, m1);
+    // |ah| <= 32*15*128, so the 22-bit combination fits in int32
+    const float q0 = (float)((ah0 << 14) + (am0 << 7) + al0) * x.xs0;
+    const float q1 = (float)((ah1 << 14) + (am1 << 7) + al1) * x.xs1;
     return d * ((float)sc0 * q0 + (float)sc1 * q1) - dmin * ((float)m0 * x.s0 + (float)m1 * x.s1);
 }
 
@@ -197,12 +197,9 @@ static __device__ __forceinline__ void quant4(float4 v, int c, uint32_t *hw, uin
                                               float *s32, float *s16) {
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     const float sum = (v.x + v.y) + (v.z + v.w);
-    float sum16 = sum + __shfl_xor(sum, 1, WAVE);
-    sum16 += __shfl_xor(sum16, 2, WAVE);
-    const float sum32 = sum16 + __shfl_xor(sum16, 4, WAVE);
-    amax = fmaxf(amax, __shfl_xor(amax, 1, WAVE));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, WAVE));
-    amax = fmaxf(amax, __shfl_xor(amax, 4, WAVE));
+    const float sum16 = dpp_sum4(sum);             // 4 lanes = 16 elements
+    const float sum32 = sum16 + dpp_mirror8(sum16);  // 8 lanes = 32 elements
+    amax = dpp_max8(amax);
     const float inv = amax > 0.f ? XQ_MAX / amax : 0.f;
     const int q0 = (int)rintf(v.x * inv), q1 = (int)rintf(v.y * inv), q2 = (int)rintf(v.z * inv),
               q3 = (int)rintf(v.w * inv);
@@ -223,72 +220,76 @@ static __device__ __forceinline__ void quant4(float4 v, int c, uint32_t *hw, uin
     if ((c & 3) == 0) s16[c >> 2] = sum16;
 }
 
-// x -> (optional RMSNorm, ops.odin:7-19) -> 15-bit integers in LDS.  With a
-// norm and K <= 8192 the vector is read once into registers; K/4 is a
-// multiple of 8, so the 8-lane groups of quant4 are always whole.
-static __device__ void quantize_x(const GemvArgs &a, u32x4 *xhi, u32x4 *xmid, u32x4 *xlo, float *xs, float *s32,
-                                  float *s16, float *red) {
-    constexpr int NXR = 8;  // float4 per thread held in registers (K <= 8192)
+// x -> (optional RMSNorm, ops.odin:7-19) -> 22-bit integers in LDS, in two
+// phases so that the x loads are issued before the weight prefetch (vector
+// loads return in order: x must not queue behind the weights).  XR float4 of
+// x (and of the norm weight) per thread are held in registers; XR == 0 means
+// K is too long for that and both passes read x from memory after the
+// prefetch.  K/4 is a multiple of 8, so the 8-lane groups of quant4 are whole.
+template <int XR>
+struct XPre {
+    float4 x[XR > 0 ? XR : 1], w[XR > 0 ? XR : 1];
+};
+
+template <int XR>
+static __device__ __forceinline__ void xpre_load(const GemvArgs &a, XPre<XR> &p) {
+    const int tid = threadIdx.x;
+    const float4 *gx = (const float4 *)a.x, *nw = (const float4 *)a.norm_w;
+#pragma unroll
+    for (int i = 0; i < XR; i++) {
+        const int c = tid + i * WG;
+        if (c < a.K / 4) {
+            p.x[i] = gx[c];
+            if (nw) p.w[i] = nw[c];
+        }
+    }
+}
+
+template <int XR>
+static __device__ void xpre_finish(const GemvArgs &a, const XPre<XR> &p, u32x4 *xhi, u32x4 *xmid, u32x4 *xlo,
+                                   float *xs, float *s32, float *s16, float *red) {
     const int K = a.K, tid = threadIdx.x;
     const float4 *gx = (const float4 *)a.x;
     const float4 *nw = (const float4 *)a.norm_w;
     uint32_t *hw = (uint32_t *)xhi, *mw = (uint32_t *)xmid, *lw = (uint32_t *)xlo;
-    if (nw && K <= 4 * WG * NXR) {
-        float4 xv[NXR], wv[NXR];
+    float s = 1.f;
+    if (nw) {
         float ss = 0.f;
+        if (XR > 0) {
 #pragma unroll
-        for (int i = 0; i < NXR; i++) {
-            const int c = tid + i * WG;
-            if (c < K / 4) {
-                xv[i] = gx[c];
-                wv[i] = nw[c];
-                ss += xv[i].x * xv[i].x + xv[i].y * xv[i].y + xv[i].z * xv[i].z + xv[i].w * xv[i].w;
+            for (int i = 0; i < XR; i++)
+                if (tid + i * WG < K / 4)
+                    ss += p.x[i].x * p.x[i].x + p.x[i].y * p.x[i].y + p.x[i].z * p.x[i].z + p.x[i].w * p.x[i].w;
+        } else {
+            for (int c = tid; c < K / 4; c += WG) {
+                const float4 v = gx[c];
+                ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
             }
         }
         ss = wave_sum(ss);
         if ((tid & (WAVE - 1)) == 0) red[tid / WAVE] = ss;
         __syncthreads();
         ss = (red[0] + red[1]) + (red[2] + red[3]);
-        const float s = 1.0f / sqrtf(ss / (float)K + a.eps);
-#pragma unroll
-        for (int i = 0; i < NXR; i++) {
-            const int c = tid + i * WG;
-            if (c < K / 4) {
+        s = 1.0f / sqrtf(ss / (float)K + a.eps);
+    }
+    auto one = [&](float4 v, float4 w, int c) {
+        if (nw) {
 #pragma clang fp contract(off)
-                float4 v;
-                v.x = wv[i].x * (s * xv[i].x);
-                v.y = wv[i].y * (s * xv[i].y);
-                v.z = wv[i].z * (s * xv[i].z);
-                v.w = wv[i].w * (s * xv[i].w);
-                quant4(v, c, hw, mw, lw, xs, s32, s16);
-            }
+            v.x = w.x * (s * v.x);
+            v.y = w.y * (s * v.y);
+            v.z = w.z * (s * v.z);
+            v.w = w.w * (s * v.w);
+        }
+        quant4(v, c, hw, mw, lw, xs, s32, s16);
+    };
+    if (XR > 0) {
+#pragma unroll
+        for (int i = 0; i < XR; i++) {
+            const int c = tid + i * WG;
+            if (c < K / 4) one(p.x[i], p.w[i], c);
         }
     } else {
-        float s = 1.f;
-        if (nw) {
-            float ss = 0.f;
-            for (int c = tid; c < K / 4; c += WG) {
-                const float4 v = gx[c];
-                ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-            }
-            ss = wave_sum(ss);
-            if ((tid & (WAVE - 1)) == 0) red[tid / WAVE] = ss;
-            __syncthreads();
-            ss = (red[0] + red[1]) + (red[2] + red[3]);
-            s = 1.0f / sqrtf(ss / (float)K + a.eps);
-        }
-        for (int c = tid; c < K / 4; c += WG) {
-            float4 v = gx[c];
-            if (nw) {
-#pragma clang fp contract(off)
-                const float4 w = nw[c];
-                v.x = w.x * (s * v.x);
-                v.y = w.y * (s * v.y);
-                v.z = w.z * (s * v.z);
-                v.w = w.w * (s * v.w);
-            }
-            quant4(v, c, hw, mw, lw, xs, s32, s16);
-        }
+        for (int c = tid; c < K / 4; c += WG) one(gx[c], nw ? nw[c] : gx[c], c);
     }
     __syncthreads();
 }
@@ -296,8 +297,12 @@ static __device__ void quantize_x(const GemvArgs &a, u32x4 *xhi, u32x4 *xmid, u3
 // One workgroup: tiles [tb, te) of segment `seg`, all of weight type T.
 // A step is one unit per lane for the R rows (x NM matrices) of a tile; the
 // weights of step s+P-1 are requested before step s is computed (a ring of
-// P register stages), the first P-1 before the x prologue.
-template <int T, int R, int NM, int P>
+// P register stages), the first P-1 right after the x loads.  When a row is
+// at most 64 units long (XU1) a lane's unit is the same in every step, and
+// its slice of x stays in registers for the whole workgroup.  Rows past the
+// end of the matrix are clamped to the last row (computed, not stored), so
+// the hot loop has no row branches.
+template <int T, int R, int NM, int P, int XR, bool XU1>
 static __device__ void gemv_run(const GemvArgs &a, int seg, int tb, int te, int wg) {
     using W = typename Types<T>::W;
     using X = typename Types<T>::X;
@@ -308,31 +313,33 @@ static __device__ void gemv_run(const GemvArgs &a, int seg, int tb, int te, int 
     const DMat &m0 = a.seg[seg].m;
     const DMat &m1 = a.seg[NM == 2 ? 1 : seg].m;
     const int lpr = a.lpr, gpw = WAVE / lpr, grp = lane / lpr, j = lane & (lpr - 1);
-    const int U = K >> 6, upl = U / lpr;
+    const int U = K >> 6, upl = XU1 ? 1 : U / lpr;
     const int rows_m = m0.rows;
     const int nsteps = (te - tb) * upl;
     const int rbase = (wave * gpw + grp) * R;
 
     W ring[P][NM][R];
     auto issue = [&](int step, W (&w)[NM][R]) {
-        const int tile = tb + step / upl, u = j + (step % upl) * lpr;
+        const int tile = XU1 ? tb + step : tb + step / upl, u = XU1 ? j : j + (step % upl) * lpr;
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            const int row = tile * a.rows_per_wg + rbase + r;
-            if (row < rows_m) {
-                wload(m0, row, u, w[0][r]);
-                if (NM == 2) wload(m1, row, u, w[NM - 1][r]);
-            }
+            const int row = min(tile * a.rows_per_wg + rbase + r, rows_m - 1);
+            wload(m0, row, u, w[0][r]);
+            if (NM == 2) wload(m1, row, u, w[NM - 1][r]);
         }
     };
+    XPre<XR> xp;
+    xpre_load<XR>(a, xp);  // x first, then the weights (loads return in order)
 #pragma unroll
     for (int i = 0; i < P - 1; i++)
         if (i < nsteps) issue(i, ring[i]);
 
     u32x4 *xhi = smem, *xmid = smem + K / 16, *xlo = smem + 2 * (K / 16);
     float *xs = (float *)(smem + 3 * (K / 16)), *s32 = xs + K / 32, *s16 = s32 + K / 32;
-    quantize_x(a, xhi, xmid, xlo, xs, s32, s16, red);
+    xpre_finish<XR>(a, xp, xhi, xmid, xlo, xs, s32, s16, red);
     const XQ xq{xhi, xmid, xlo, xs, s32, s16};
+    X xu;
+    if (XU1) xload(xq, j, xu);
 
     float bv = -INFINITY;
     int bi = 0x7FFFFFFF;
@@ -348,24 +355,22 @@ static __device__ void gemv_run(const GemvArgs &a, int seg, int tb, int te, int 
             const int step = base + k;
             if (step >= nsteps) break;
             if (step + P - 1 < nsteps) issue(step + P - 1, ring[(k + P - 1) % P]);
-            const int tile = tb + step / upl, ui = step % upl, u = j + ui * lpr;
+            const int tile = XU1 ? tb + step : tb + step / upl, ui = XU1 ? 0 : step % upl;
+            const int u = j + ui * lpr;
             const int row0 = tile * a.rows_per_wg + rbase;
-            X xu;
-            xload(xq, u, xu);
+            if (!XU1) xload(xq, u, xu);
 #pragma unroll
-            for (int r = 0; r < R; r++)
-                if (row0 + r < rows_m) {
-                    acc[0][r] += wdot(ring[k][0][r], u, xu);
-                    if (NM == 2) acc[NM - 1][r] += wdot(ring[k][NM - 1][r], u, xu);
-                }
-            if (ui == upl - 1) {
+            for (int r = 0; r < R; r++) {
+                acc[0][r] += wdot(ring[k][0][r], u, xu);
+                if (NM == 2) acc[NM - 1][r] += wdot(ring[k][NM - 1][r], u, xu);
+            }
+            if (XU1 || ui == upl - 1) {
                 // reduce over the lanes of the row, then the epilogue
-                for (int o = lpr >> 1; o > 0; o >>= 1)
 #pragma unroll
-                    for (int r = 0; r < R; r++) {
-                        acc[0][r] += __shfl_xor(acc[0][r], o, WAVE);
-                        if (NM == 2) acc[NM - 1][r] += __shfl_xor(acc[NM - 1][r], o, WAVE);
-                    }
+                for (int r = 0; r < R; r++) {
+                    acc[0][r] = lane_group_sum(acc[0][r], lpr);
+                    if (NM == 2) acc[NM - 1][r] = lane_group_sum(acc[NM - 1][r], lpr);
+                }
                 if (j == 0) {
 #pragma unroll
                     for (int r = 0; r < R; r++) {
@@ -425,7 +430,7 @@ static __device__ void gemv_run(const GemvArgs &a, int seg, int tb, int te, int 
     }
 }
 
-template <int R, int NM, int P>
+template <int R, int NM, int P, int XR, bool XU1>
 __global__ __launch_bounds__(WG) void gemv_q_kernel(GemvArgs a) {
     const int wg = blockIdx.x;
     int seg = 0;
@@ -438,28 +443,53 @@ __global__ __launch_bounds__(WG) void gemv_q_kernel(GemvArgs a) {
     const int ntiles = a.seg[seg].ntiles;
     const int tb = (int)((long)ntiles * w / nwg), te = (int)((long)ntiles * (w + 1) / nwg);
     switch (a.seg[seg].m.type) {
-    case T_Q4_K: gemv_run<T_Q4_K, R, NM, P>(a, seg, tb, te, wg); break;
-    case T_Q6_K: gemv_run<T_Q6_K, R, NM, P>(a, seg, tb, te, wg); break;
-    default: gemv_run<T_Q8_0, R, NM, P>(a, seg, tb, te, wg); break;
+    case T_Q4_K: gemv_run<T_Q4_K, R, NM, P, XR, XU1>(a, seg, tb, te, wg); break;
+    case T_Q6_K: gemv_run<T_Q6_K, R, NM, P, XR, XU1>(a, seg, tb, te, wg); break;
+    default: gemv_run<T_Q8_0, R, NM, P, XR, XU1>(a, seg, tb, te, wg); break;
     }
 }
 
-// kernel configurations: (R, NM, P)
-#define GEMV_Q_MAIN gemv_q_kernel<2, 1, 3>
-#define GEMV_Q_SWIGLU gemv_q_kernel<1, 2, 3>
-constexpr int R_MAIN = 2, R_SWIGLU = 1;
+// kernel configurations: (R, NM, P, XR, XU1); XR = float4 of x per thread
+// held in registers by the prologue (K <= 1024 * XR), 0 = x read twice from
+// memory; XU1 = one unit per lane per row (K <= 4096), x kept in registers
+#ifndef OI_GEMV_R
+#define OI_GEMV_R 2
+#endif
+#ifndef OI_GEMV_P
+#define OI_GEMV_P 2
+#endif
+#ifndef OI_GEMV_XREG
+#define OI_GEMV_XREG 1
+#endif
+constexpr int R_MAIN = OI_GEMV_R, R_SWIGLU = 1, P_MAIN = OI_GEMV_P;  // measured best: R=2, P=2
+constexpr bool XREG = OI_GEMV_XREG != 0;
+static const void *gemv_q_fn(bool swiglu, int K) {
+    // one unit per lane per row when the row's unit count is a power of two <= 64
+    const int U = K / 64;
+    const bool xu1 = XREG && U <= 64 && (U & (U - 1)) == 0;
+    if (swiglu) {
+        if (K <= 4096 && xu1) return (const void *)gemv_q_kernel<R_SWIGLU, 2, P_MAIN, 4, true>;
+        if (K <= 4096) return (const void *)gemv_q_kernel<R_SWIGLU, 2, P_MAIN, 4, false>;
+        return (const void *)gemv_q_kernel<R_SWIGLU, 2, P_MAIN, 0, false>;
+    }
+    if (K <= 4096 && xu1) return (const void *)gemv_q_kernel<R_MAIN, 1, P_MAIN, 4, true>;
+    if (K <= 4096) return (const void *)gemv_q_kernel<R_MAIN, 1, P_MAIN, 4, false>;
+    if (K <= 12288) return (const void *)gemv_q_kernel<R_MAIN, 1, P_MAIN, 12, false>;
+    return (const void *)gemv_q_kernel<R_MAIN, 1, P_MAIN, 0, false>;
+}
 
 static int resident_wgs(const void *fn, size_t lds) {
-    static int cache[2] = {0, 0};
-    const int slot = fn == (const void *)GEMV_Q_SWIGLU ? 1 : 0;
-    if (!cache[slot]) {
-        int per_cu = 0, cus = 256, dev = 0;
-        hipGetDevice(&dev);
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, WG, lds) != hipSuccess || per_cu < 1) per_cu = 1;
-        cache[slot] = per_cu * cus;
-    }
-    return cache[slot];
+    struct Entry { const void *fn; size_t lds; int n; };
+    static Entry cache[16];
+    static int ncache = 0;
+    for (int i = 0; i < ncache; i++)
+        if (cache[i].fn == fn && cache[i].lds == lds) return cache[i].n;
+    int per_cu = 0, cus = 256, dev = 0;
+    hipGetDevice(&dev);
+    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, WG, lds) != hipSuccess || per_cu < 1) per_cu = 1;
+    if (ncache < 16) cache[ncache++] = {fn, lds, per_cu * cus};
+    return per_cu * cus;
 }
 
 static size_t gemv_q_lds(int K) { return (size_t)K / 16 * 48 + (size_t)K / 32 * 8 + (size_t)K / 16 * 4; }
@@ -491,7 +521,7 @@ void plan_gemv_q(GemvArgs &a) {
         a.seg[i].ntiles = (a.seg[i].m.rows + a.rows_per_wg - 1) / a.rows_per_wg;
         total_tiles += a.seg[i].ntiles;
     }
-    const long slots = resident_wgs(sw ? (const void *)GEMV_Q_SWIGLU : (const void *)GEMV_Q_MAIN, gemv_q_lds(a.K));
+    const long slots = resident_wgs(gemv_q_fn(sw, a.K), gemv_q_lds(a.K));
     const long k = (total_tiles + slots - 1) / slots;  // tiles per workgroup
     int wg = 0;
     for (int i = 0; i < nseg; i++) {
@@ -507,12 +537,9 @@ void plan_gemv_q(GemvArgs &a) {
 }
 
 hipError_t launch_gemv_q(const GemvArgs &a, hipStream_t st) {
-    dim3 grid(a.total_wgs), block(WG);
-    if (a.mode == GEMV_SWIGLU)
-        hipLaunchKernelGGL(GEMV_Q_SWIGLU, grid, block, gemv_q_lds(a.K), st, a);
-    else
-        hipLaunchKernelGGL(GEMV_Q_MAIN, grid, block, gemv_q_lds(a.K), st, a);
-    return hipGetLastError();
+    const void *fn = gemv_q_fn(a.mode == GEMV_SWIGLU, a.K);
+    void *args[] = {(void *)&a};
+    return hipLaunchKernel(fn, dim3(a.total_wgs), dim3(WG), args, gemv_q_lds(a.K), st);
 }
 
 }  // namespace oi

@@ -29,10 +29,8 @@ __device__ void decode_unit_q4k(const DMat &m, int row, int u, float *out) {
     const u32x4 q0 = *(const u32x4 *)(m.q + ui * 16);
     const u32x4 q1 = *(const u32x4 *)(m.q + m.plane + ui * 16);
     const float d = h2f(hdr.x & 0xFFFFu), dmin = h2f(hdr.x >> 16);
-    const uint32_t sw[3] = {hdr.y, hdr.z, hdr.w};
     uint32_t sc0, m0, sc1, m1;
-    scale_min_k4(2 * p, sw, sc0, m0);
-    scale_min_k4(2 * p + 1, sw, sc1, m1);
+    q4k_scales(p, hdr.y, hdr.z, hdr.w, sc0, m0, sc1, m1);
     const float d1 = d * (float)sc0, mm1 = dmin * (float)m0;
     const float d2 = d * (float)sc1, mm2 = dmin * (float)m1;
     const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};

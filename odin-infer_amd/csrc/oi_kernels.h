@@ -16,8 +16,12 @@ enum : int32_t { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14 };
 // lanes of a wave reading piece k of 64 consecutive units read one
 // contiguous 1 KB.  The byte count equals the GGUF one.  Per type:
 //   Q4_K  plane 0: qs[32p .. 32p+15] and plane 1: qs[32p+16 .. 32p+31] of
-//         super-block u/4, group pair p = u%4;  s: the 16-byte super-block
-//         header (f16 d, f16 dmin, 12 bytes of 6-bit scales/mins) per (row, sb).
+//         super-block u/4, group pair p = u%4;  s: a 16-byte header per
+//         (row, sb): f16 d, f16 dmin, then the eight 6-bit scales and mins
+//         regrouped as four 24-bit fields, field p = sc(2p) | m(2p) << 6 |
+//         sc(2p+1) << 12 | m(2p+1) << 18 at bits 24p.. of the 96-bit tail
+//         (the GGUF packing, ggml/quant.odin:64-73, spread one group pair's
+//         values over three bytes; the values are unchanged).
 //   Q6_K  unit u = super-block u/4, half h = (u/2)%2, columns l0 = 16(u%2):
 //         plane 0: ql[64h+l0 ..+15], plane 1: ql[64h+32+l0 ..+15],
 //         plane 2: qh[32h+l0 ..+15];  s: 16 int8 scales per (row, sb);

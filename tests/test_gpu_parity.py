@@ -80,7 +80,8 @@ def _gemv_case(kind, rows, cols, seed):
 
 
 @pytest.mark.parametrize("kind", [12, 14, 8, 1, 0])
-@pytest.mark.parametrize("rows,cols", [(512, 4096), (300, 1024), (64, 12288), (1000, 512), (7, 2048)])
+@pytest.mark.parametrize("rows,cols", [(512, 4096), (300, 1024), (64, 12288), (1000, 512), (7, 2048), (96, 1536),
+                                       (130, 3072), (40, 768), (33, 5120)])
 def test_gemv_small(kind, rows, cols):
     blocks, x = _gemv_case(kind, rows, cols, 5 + rows + cols)
     got = ggml.gemv(kind, blocks, rows, cols, x)
