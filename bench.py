@@ -93,7 +93,19 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--model-path", default=None, help="reuse an existing synthetic GGUF")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a device-to-device copy of MIB MiB (3 times), to calibrate HBM counters")
     args = ap.parse_args()
+    if args.copy_calibration:
+        import torch
+        n = args.copy_calibration << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_per_dispatch": n}))
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU only: the token loop runs on a single MI355X "
               "(multi-GPU sharding is a design note, not built); got --gpus %d" % args.gpus, file=sys.stderr)
