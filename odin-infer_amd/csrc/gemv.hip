@@ -19,6 +19,9 @@
 // rounding error is <= 2^-22 of the group maximum, below f32 accumulation
 // noise, so greedy picks agree with an f32 reference down to ~1e-6 margins.
 
+#include <algorithm>
+#include <climits>
+
 #include "device_common.h"
 
 namespace oi {
@@ -226,34 +229,38 @@ static __device__ __forceinline__ void quant4(float4 v, int c, uint32_t *hw, uin
 // x (and of the norm weight) per thread are held in registers; XR == 0 means
 // K is too long for that and both passes read x from memory after the
 // prefetch.  K/4 is a multiple of 8, so the 8-lane groups of quant4 are whole.
-template <int XR>
+template <int XR, bool NORM>
 struct XPre {
-    float4 x[XR > 0 ? XR : 1], w[XR > 0 ? XR : 1];
+    float4 x[XR > 0 ? XR : 1], w[XR > 0 && NORM ? XR : 1];
 };
 
-template <int XR>
-static __device__ __forceinline__ void xpre_load(const GemvArgs &a, XPre<XR> &p) {
-    const int tid = threadIdx.x;
-    const float4 *gx = (const float4 *)a.x, *nw = (const float4 *)a.norm_w;
+template <int XR, bool NORM, bool REV = false>
+static __device__ __forceinline__ void xpre_load(const GemvArgs &a, XPre<XR, NORM> &p) {
+    // unconditional loads (indices clamped to the last float4, duplicates are
+    // ignored by xpre_finish): a branch-free sequence lets the compiler wait
+    // for exactly these loads later, not for the weight loads issued after
+    const int tid = threadIdx.x, last = a.K / 4 - 1;
+    const float4 *gx = (const float4 *)a.x;
+    const float4 *nw = (const float4 *)a.norm_w;
 #pragma unroll
-    for (int i = 0; i < XR; i++) {
-        const int c = tid + i * WG;
-        if (c < a.K / 4) {
-            p.x[i] = gx[c];
-            if (nw) p.w[i] = nw[c];
-        }
+    for (int ii = 0; ii < XR; ii++) {
+        const int i = REV ? XR - 1 - ii : ii;  // REV: same loads in another order (see gemv_q_kernel)
+        const int c = min(tid + i * WG, last);
+        p.x[i] = gx[c];
+        if (NORM) p.w[i] = nw[c];
     }
 }
 
-template <int XR>
-static __device__ void xpre_finish(const GemvArgs &a, const XPre<XR> &p, u32x4 *xhi, u32x4 *xmid, u32x4 *xlo,
-                                   float *xs, float *s32, float *s16, float *red) {
+template <int XR, bool NORM>
+static __device__ __forceinline__ void xpre_finish(const GemvArgs &a, const XPre<XR, NORM> &p, u32x4 *xhi,
+                                                   u32x4 *xmid, u32x4 *xlo, float *xs, float *s32, float *s16,
+                                                   float *red) {
     const int K = a.K, tid = threadIdx.x;
     const float4 *gx = (const float4 *)a.x;
     const float4 *nw = (const float4 *)a.norm_w;
     uint32_t *hw = (uint32_t *)xhi, *mw = (uint32_t *)xmid, *lw = (uint32_t *)xlo;
     float s = 1.f;
-    if (nw) {
+    if (NORM) {
         float ss = 0.f;
         if (XR > 0) {
 #pragma unroll
@@ -273,7 +280,7 @@ static __device__ void xpre_finish(const GemvArgs &a, const XPre<XR> &p, u32x4 *
         s = 1.0f / sqrtf(ss / (float)K + a.eps);
     }
     auto one = [&](float4 v, float4 w, int c) {
-        if (nw) {
+        if (NORM) {
 #pragma clang fp contract(off)
             v.x = w.x * (s * v.x);
             v.y = w.y * (s * v.y);
@@ -286,10 +293,10 @@ static __device__ void xpre_finish(const GemvArgs &a, const XPre<XR> &p, u32x4 *
 #pragma unroll
         for (int i = 0; i < XR; i++) {
             const int c = tid + i * WG;
-            if (c < K / 4) one(p.x[i], p.w[i], c);
+            if (c < K / 4) one(p.x[i], p.w[NORM ? i : 0], c);
         }
     } else {
-        for (int c = tid; c < K / 4; c += WG) one(gx[c], nw ? nw[c] : gx[c], c);
+        for (int c = tid; c < K / 4; c += WG) one(gx[c], NORM ? nw[c] : gx[c], c);
     }
     __syncthreads();
 }
@@ -302,8 +309,9 @@ static __device__ void xpre_finish(const GemvArgs &a, const XPre<XR> &p, u32x4 *
 // its slice of x stays in registers for the whole workgroup.  Rows past the
 // end of the matrix are clamped to the last row (computed, not stored), so
 // the hot loop has no row branches.
-template <int T, int R, int NM, int P, int XR, bool XU1>
-static __device__ void gemv_run(const GemvArgs &a, int seg, int tb, int te, int wg) {
+template <int T, int R, int NM, int P, int XR, bool XU1, bool NORM>
+static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int tb, int te, int wg,
+                                                const XPre<XR, NORM> &xp) {
     using W = typename Types<T>::W;
     using X = typename Types<T>::X;
     extern __shared__ u32x4 smem[];
@@ -318,25 +326,31 @@ static __device__ void gemv_run(const GemvArgs &a, int seg, int tb, int te, int 
     const int nsteps = (te - tb) * upl;
     const int rbase = (wave * gpw + grp) * R;
 
+    // Every call issues the same loads: a step past the end reads row 0's
+    // first units (cached; the result is never used).  With no branch around
+    // the loads the compiler can count them, and waits for exactly the stage
+    // it consumes instead of for everything in flight.
     W ring[P][NM][R];
     auto issue = [&](int step, W (&w)[NM][R]) {
+        const bool live = step < nsteps;
         const int tile = XU1 ? tb + step : tb + step / upl, u = XU1 ? j : j + (step % upl) * lpr;
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            const int row = min(tile * a.rows_per_wg + rbase + r, rows_m - 1);
-            wload(m0, row, u, w[0][r]);
-            if (NM == 2) wload(m1, row, u, w[NM - 1][r]);
+            const int row = live ? min(tile * a.rows_per_wg + rbase + r, rows_m - 1) : 0;
+            wload(m0, row, live ? u : j, w[0][r]);
+            if (NM == 2) wload(m1, row, live ? u : j, w[NM - 1][r]);
         }
     };
-    XPre<XR> xp;
-    xpre_load<XR>(a, xp);  // x first, then the weights (loads return in order)
+    // x was requested by the caller; the weights follow (loads return in order)
 #pragma unroll
-    for (int i = 0; i < P - 1; i++)
-        if (i < nsteps) issue(i, ring[i]);
+    for (int i = 0; i < P - 1; i++) issue(i, ring[i]);
+    __builtin_amdgcn_sched_barrier(0);
 
     u32x4 *xhi = smem, *xmid = smem + K / 16, *xlo = smem + 2 * (K / 16);
     float *xs = (float *)(smem + 3 * (K / 16)), *s32 = xs + K / 32, *s16 = s32 + K / 32;
-    xpre_finish<XR>(a, xp, xhi, xmid, xlo, xs, s32, s16, red);
+    float *yo = s16 + K / 16;  // this workgroup's outputs, [tiles_per_wg * rows_per_wg]
+    const int wrow0 = tb * a.rows_per_wg, wrow1 = min(te * a.rows_per_wg, rows_m);
+    xpre_finish<XR, NORM>(a, xp, xhi, xmid, xlo, xs, s32, s16, red);
     const XQ xq{xhi, xmid, xlo, xs, s32, s16};
     X xu;
     if (XU1) xload(xq, j, xu);
@@ -349,60 +363,75 @@ static __device__ void gemv_run(const GemvArgs &a, int seg, int tb, int te, int 
 #pragma unroll
         for (int r = 0; r < R; r++) acc[i][r] = 0.f;
 
-    for (int base = 0; base < nsteps; base += P) {
+    // step `step` consumes ring slot k = step % P; with `issue` first the
+    // next P-1 stages stay in flight while this one is computed
+    auto do_step = [&](int step, int k, bool prefetch) {
+        if (prefetch) {
+            issue(step + P - 1, ring[(k + P - 1) % P]);
+            __builtin_amdgcn_sched_barrier(0);  // the loads go out before this step's arithmetic
+        }
+        const int tile = XU1 ? tb + step : tb + step / upl, ui = XU1 ? 0 : step % upl;
+        const int u = j + ui * lpr;
+        const int row0 = tile * a.rows_per_wg + rbase;
+        if (!XU1) xload(xq, u, xu);
 #pragma unroll
-        for (int k = 0; k < P; k++) {
-            const int step = base + k;
-            if (step >= nsteps) break;
-            if (step + P - 1 < nsteps) issue(step + P - 1, ring[(k + P - 1) % P]);
-            const int tile = XU1 ? tb + step : tb + step / upl, ui = XU1 ? 0 : step % upl;
-            const int u = j + ui * lpr;
-            const int row0 = tile * a.rows_per_wg + rbase;
-            if (!XU1) xload(xq, u, xu);
+        for (int r = 0; r < R; r++) {
+            acc[0][r] += wdot(ring[k][0][r], u, xu);
+            if (NM == 2) acc[NM - 1][r] += wdot(ring[k][NM - 1][r], u, xu);
+        }
+        if (XU1 || ui == upl - 1) {
+            // reduce over the lanes of the row; results go to LDS (no
+            // global memory traffic in the loop but the weight loads)
 #pragma unroll
             for (int r = 0; r < R; r++) {
-                acc[0][r] += wdot(ring[k][0][r], u, xu);
-                if (NM == 2) acc[NM - 1][r] += wdot(ring[k][NM - 1][r], u, xu);
+                acc[0][r] = lane_group_sum(acc[0][r], lpr);
+                if (NM == 2) acc[NM - 1][r] = lane_group_sum(acc[NM - 1][r], lpr);
             }
-            if (XU1 || ui == upl - 1) {
-                // reduce over the lanes of the row, then the epilogue
+            if (j == 0) {
 #pragma unroll
                 for (int r = 0; r < R; r++) {
-                    acc[0][r] = lane_group_sum(acc[0][r], lpr);
-                    if (NM == 2) acc[NM - 1][r] = lane_group_sum(acc[NM - 1][r], lpr);
-                }
-                if (j == 0) {
-#pragma unroll
-                    for (int r = 0; r < R; r++) {
-                        const int row = row0 + r;
-                        if (row >= rows_m) continue;
-                        float *y = a.seg[seg].y;
-                        if (NM == 2) {  // infer/forward.odin:188-193
+                    const int row = row0 + r;
+                    float val = acc[0][r];
+                    if (NM == 2) {  // infer/forward.odin:188-193
 #pragma clang fp contract(off)
-                            float val = acc[0][r];
-                            val *= 1.0f / (1.0f + expf(-val));
-                            val *= acc[NM - 1][r];
-                            y[row] = val;
-                        } else if (a.mode == GEMV_ADD) {
-                            y[row] += acc[0][r];
-                        } else {
-                            y[row] = acc[0][r];
-                            if (a.mode == GEMV_ARGMAX && better(acc[0][r], row, bv, bi)) {
-                                bv = acc[0][r];
-                                bi = row;
-                            }
-                        }
+                        val *= 1.0f / (1.0f + expf(-val));
+                        val *= acc[NM - 1][r];
+                    }
+                    yo[row - wrow0] = val;  // rows past the matrix land in the slack of yo
+                    if (NM == 1 && a.mode == GEMV_ARGMAX && row < rows_m && better(val, row, bv, bi)) {
+                        bv = val;
+                        bi = row;
                     }
                 }
-#pragma unroll
-                for (int i = 0; i < NM; i++)
-#pragma unroll
-                    for (int r = 0; r < R; r++) acc[i][r] = 0.f;
             }
+#pragma unroll
+            for (int i = 0; i < NM; i++)
+#pragma unroll
+                for (int r = 0; r < R; r++) acc[i][r] = 0.f;
+        }
+    };
+    // whole groups of P steps, then the rest without prefetch: no loop exit
+    // in the middle of a group, so every pass through the loop has the same
+    // loads in flight and the compiler waits for exactly one stage
+    const int nfull = nsteps / P;
+    for (int c = 0; c < nfull; c++) {
+#pragma unroll
+        for (int k = 0; k < P; k++) do_step(c * P + k, k, true);
+    }
+#pragma unroll
+    for (int k = 0; k < P - 1; k++)
+        if (nfull * P + k < nsteps) do_step(nfull * P + k, k, false);
+
+    // write back the workgroup's contiguous rows (coalesced)
+    __syncthreads();
+    {
+        float *y = a.seg[seg].y;
+        for (int i = tid; i < wrow1 - wrow0; i += WG) {
+            if (NM == 1 && a.mode == GEMV_ADD) y[wrow0 + i] = y[wrow0 + i] + yo[i];
+            else y[wrow0 + i] = yo[i];
         }
     }
-
-    if (a.mode == GEMV_ARGMAX) {  // this workgroup's best (value, lowest row)
+    if (NM == 1 && a.mode == GEMV_ARGMAX) {  // this workgroup's best (value, lowest row)
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) {
             const float ov = __shfl_xor(bv, o, WAVE);
@@ -430,9 +459,15 @@ static __device__ void gemv_run(const GemvArgs &a, int seg, int tb, int te, int 
     }
 }
 
-template <int R, int NM, int P, int XR, bool XU1>
+// Weight types are template parameters: T for every segment but the last,
+// TL for the last (TL == T: one type).  A runtime switch over all types would
+// let the compiler merge the code paths, and at the merge it can no longer
+// count the loads in flight, so it waits for all of them; the two arms here
+// issue their x loads in different orders so that they are not merged.  Other
+// type mixes are issued as one launch per type (wg_base).
+template <int T, int TL, int R, int NM, int P, int XR, bool XU1, bool NORM>
 __global__ __launch_bounds__(WG) void gemv_q_kernel(GemvArgs a) {
-    const int wg = blockIdx.x;
+    const int wg = blockIdx.x + a.wg_base;
     int seg = 0;
     if (NM == 1) {
         if (a.nseg > 1 && wg >= a.seg[1].wg_begin) seg = 1;
@@ -442,10 +477,16 @@ __global__ __launch_bounds__(WG) void gemv_q_kernel(GemvArgs a) {
     const int nwg = seg_end - a.seg[seg].wg_begin, w = wg - a.seg[seg].wg_begin;
     const int ntiles = a.seg[seg].ntiles;
     const int tb = (int)((long)ntiles * w / nwg), te = (int)((long)ntiles * (w + 1) / nwg);
-    switch (a.seg[seg].m.type) {
-    case T_Q4_K: gemv_run<T_Q4_K, R, NM, P, XR, XU1>(a, seg, tb, te, wg); break;
-    case T_Q6_K: gemv_run<T_Q6_K, R, NM, P, XR, XU1>(a, seg, tb, te, wg); break;
-    default: gemv_run<T_Q8_0, R, NM, P, XR, XU1>(a, seg, tb, te, wg); break;
+    if (TL != T && seg == a.nseg - 1) {
+        XPre<XR, NORM> xp;
+        xpre_load<XR, NORM, true>(a, xp);  // x first, then the weights (loads return in order)
+        __builtin_amdgcn_sched_barrier(0);  // keep every x load ahead of the weight loads
+        gemv_run<TL, R, NM, P, XR, XU1, NORM>(a, seg, tb, te, wg, xp);
+    } else {
+        XPre<XR, NORM> xp;
+        xpre_load<XR, NORM>(a, xp);
+        __builtin_amdgcn_sched_barrier(0);
+        gemv_run<T, R, NM, P, XR, XU1, NORM>(a, seg, tb, te, wg, xp);
     }
 }
 
@@ -463,19 +504,47 @@ __global__ __launch_bounds__(WG) void gemv_q_kernel(GemvArgs a) {
 #endif
 constexpr int R_MAIN = OI_GEMV_R, R_SWIGLU = 1, P_MAIN = OI_GEMV_P;  // measured best: R=2, P=2
 constexpr bool XREG = OI_GEMV_XREG != 0;
-static const void *gemv_q_fn(bool swiglu, int K) {
+template <int T, bool NORM>
+static const void *gemv_q_fn_t(bool swiglu, bool xu1, int K) {
+    if (swiglu) {
+        if (K <= 4096 && xu1) return (const void *)gemv_q_kernel<T, T, R_SWIGLU, 2, P_MAIN, 4, true, NORM>;
+        if (K <= 4096) return (const void *)gemv_q_kernel<T, T, R_SWIGLU, 2, P_MAIN, 4, false, NORM>;
+        return (const void *)gemv_q_kernel<T, T, R_SWIGLU, 2, P_MAIN, 0, false, NORM>;
+    }
+    if (K <= 4096 && xu1) return (const void *)gemv_q_kernel<T, T, R_MAIN, 1, P_MAIN, 4, true, NORM>;
+    if (K <= 4096) return (const void *)gemv_q_kernel<T, T, R_MAIN, 1, P_MAIN, 4, false, NORM>;
+    if (K <= 12288) return (const void *)gemv_q_kernel<T, T, R_MAIN, 1, P_MAIN, 12, false, NORM>;
+    return (const void *)gemv_q_kernel<T, T, R_MAIN, 1, P_MAIN, 0, false, NORM>;
+}
+// two-type kernels (first segments T, last segment TL; RMSNorm prologue,
+// K <= 4096): the projection GEMVs of a layer
+template <int T, int TL>
+static const void *gemv_q_fn_mixed(bool xu1, int K) {
+    if (K > 4096) return nullptr;
+    if (xu1) return (const void *)gemv_q_kernel<T, TL, R_MAIN, 1, P_MAIN, 4, true, true>;
+    return (const void *)gemv_q_kernel<T, TL, R_MAIN, 1, P_MAIN, 4, false, true>;
+}
+static const void *gemv_q_fn_mixed(int t, int tl, bool norm, int K) {
+    const int U = K / 64;
+    const bool xu1 = XREG && U <= 64 && (U & (U - 1)) == 0;
+    if (!norm) return nullptr;
+    if (t == T_Q4_K && tl == T_Q6_K) return gemv_q_fn_mixed<T_Q4_K, T_Q6_K>(xu1, K);
+    if (t == T_Q6_K && tl == T_Q4_K) return gemv_q_fn_mixed<T_Q6_K, T_Q4_K>(xu1, K);
+    if (t == T_Q4_K && tl == T_Q8_0) return gemv_q_fn_mixed<T_Q4_K, T_Q8_0>(xu1, K);
+    if (t == T_Q8_0 && tl == T_Q4_K) return gemv_q_fn_mixed<T_Q8_0, T_Q4_K>(xu1, K);
+    if (t == T_Q8_0 && tl == T_Q6_K) return gemv_q_fn_mixed<T_Q8_0, T_Q6_K>(xu1, K);
+    if (t == T_Q6_K && tl == T_Q8_0) return gemv_q_fn_mixed<T_Q6_K, T_Q8_0>(xu1, K);
+    return nullptr;
+}
+static const void *gemv_q_fn(int type, bool swiglu, bool norm, int K) {
     // one unit per lane per row when the row's unit count is a power of two <= 64
     const int U = K / 64;
     const bool xu1 = XREG && U <= 64 && (U & (U - 1)) == 0;
-    if (swiglu) {
-        if (K <= 4096 && xu1) return (const void *)gemv_q_kernel<R_SWIGLU, 2, P_MAIN, 4, true>;
-        if (K <= 4096) return (const void *)gemv_q_kernel<R_SWIGLU, 2, P_MAIN, 4, false>;
-        return (const void *)gemv_q_kernel<R_SWIGLU, 2, P_MAIN, 0, false>;
+    switch (type) {
+    case T_Q4_K: return norm ? gemv_q_fn_t<T_Q4_K, true>(swiglu, xu1, K) : gemv_q_fn_t<T_Q4_K, false>(swiglu, xu1, K);
+    case T_Q6_K: return norm ? gemv_q_fn_t<T_Q6_K, true>(swiglu, xu1, K) : gemv_q_fn_t<T_Q6_K, false>(swiglu, xu1, K);
+    default: return norm ? gemv_q_fn_t<T_Q8_0, true>(swiglu, xu1, K) : gemv_q_fn_t<T_Q8_0, false>(swiglu, xu1, K);
     }
-    if (K <= 4096 && xu1) return (const void *)gemv_q_kernel<R_MAIN, 1, P_MAIN, 4, true>;
-    if (K <= 4096) return (const void *)gemv_q_kernel<R_MAIN, 1, P_MAIN, 4, false>;
-    if (K <= 12288) return (const void *)gemv_q_kernel<R_MAIN, 1, P_MAIN, 12, false>;
-    return (const void *)gemv_q_kernel<R_MAIN, 1, P_MAIN, 0, false>;
 }
 
 static int resident_wgs(const void *fn, size_t lds) {
@@ -492,7 +561,20 @@ static int resident_wgs(const void *fn, size_t lds) {
     return per_cu * cus;
 }
 
-static size_t gemv_q_lds(int K) { return (size_t)K / 16 * 48 + (size_t)K / 32 * 8 + (size_t)K / 16 * 4; }
+static size_t gemv_q_lds(int K, int out_rows) {
+    return (size_t)K / 16 * 48 + (size_t)K / 32 * 8 + (size_t)K / 16 * 4 + (size_t)out_rows * 4;
+}
+
+// One launch when the segments are of one type, or of one type but the
+// last; otherwise one launch per run of consecutive segments of one type.
+static const void *gemv_q_fn_all(const GemvArgs &a) {
+    if (a.mode == GEMV_SWIGLU || a.nseg < 2) return nullptr;
+    for (int i = 1; i < a.nseg - 1; i++)
+        if (a.seg[i].m.type != a.seg[0].m.type) return nullptr;
+    const int t = a.seg[0].m.type, tl = a.seg[a.nseg - 1].m.type;
+    if (tl == t) return gemv_q_fn(t, false, a.norm_w != nullptr, a.K);
+    return gemv_q_fn_mixed(t, tl, a.norm_w != nullptr, a.K);
+}
 
 bool gemv_q_supported(const GemvArgs &a) {
     const int n = a.mode == GEMV_SWIGLU ? 2 : a.nseg;
@@ -521,8 +603,15 @@ void plan_gemv_q(GemvArgs &a) {
         a.seg[i].ntiles = (a.seg[i].m.rows + a.rows_per_wg - 1) / a.rows_per_wg;
         total_tiles += a.seg[i].ntiles;
     }
-    const long slots = resident_wgs(gemv_q_fn(sw, a.K), gemv_q_lds(a.K));
-    const long k = (total_tiles + slots - 1) / slots;  // tiles per workgroup
+    // resident capacity of the slowest-occupancy kernel of the launch (the
+    // output buffer is sized for one tile here, which the check below keeps)
+    long slots = LONG_MAX;
+    const void *fall = gemv_q_fn_all(a);
+    for (int i = 0; i < nseg; i++) {
+        const void *fn = fall ? fall : gemv_q_fn(a.seg[i].m.type, sw, a.norm_w != nullptr, a.K);
+        slots = std::min(slots, (long)resident_wgs(fn, gemv_q_lds(a.K, a.rows_per_wg * 4)));
+    }
+    long k = (total_tiles + slots - 1) / slots;  // tiles per workgroup
     int wg = 0;
     for (int i = 0; i < nseg; i++) {
         a.seg[i].wg_begin = wg;
@@ -533,13 +622,33 @@ void plan_gemv_q(GemvArgs &a) {
         a.seg[1].ntiles = a.seg[0].ntiles;
     }
     a.total_wgs = wg;
+    a.tiles_per_wg = (int)k;
     a.kernel = 1;
 }
 
 hipError_t launch_gemv_q(const GemvArgs &a, hipStream_t st) {
-    const void *fn = gemv_q_fn(a.mode == GEMV_SWIGLU, a.K);
-    void *args[] = {(void *)&a};
-    return hipLaunchKernel(fn, dim3(a.total_wgs), dim3(WG), args, gemv_q_lds(a.K), st);
+    const bool sw = a.mode == GEMV_SWIGLU;
+    const int nseg = sw ? 1 : a.nseg;
+    const size_t lds = gemv_q_lds(a.K, a.tiles_per_wg * a.rows_per_wg);
+    if (const void *fn = gemv_q_fn_all(a)) {
+        GemvArgs b = a;
+        b.wg_base = 0;
+        void *args[] = {(void *)&b};
+        return hipLaunchKernel(fn, dim3(a.total_wgs), dim3(WG), args, lds, st);
+    }
+    for (int i = 0; i < nseg;) {
+        int j = i + 1;
+        while (j < nseg && a.seg[j].m.type == a.seg[i].m.type) j++;
+        GemvArgs b = a;
+        b.wg_base = a.seg[i].wg_begin;
+        const int end = j < nseg ? a.seg[j].wg_begin : a.total_wgs;
+        const void *fn = gemv_q_fn(a.seg[i].m.type, sw, a.norm_w != nullptr, a.K);
+        void *args[] = {(void *)&b};
+        const hipError_t e = hipLaunchKernel(fn, dim3(end - b.wg_base), dim3(WG), args, lds, st);
+        if (e != hipSuccess) return e;
+        i = j;
+    }
+    return hipSuccess;
 }
 
 }  // namespace oi

@@ -71,6 +71,8 @@ struct GemvArgs {
     float *am_val;         // [total_wgs]
     int32_t *am_idx;       // [total_wgs]
     int32_t *state;
+    int32_t wg_base;       // gemv_q_kernel: workgroup index of blockIdx.x 0 (one launch per weight type)
+    int32_t tiles_per_wg;  // gemv_q_kernel: most tiles any workgroup takes (sizes its output buffer)
 };
 
 // Device state of the token loop (int32 x 8):
