@@ -5,18 +5,25 @@
 // positions of one KV head and serves all G = n_heads / n_kv_heads query
 // heads of the group, so each K/V row is read from HBM once per token (the
 // reference re-reads it for every query head).  Per workgroup:
-//   1. issue the loads of its K and V tiles (16 B per lane, coalesced),
-//   2. meanwhile RMSNorm + RoPE the G query heads (and, in the split that
-//      holds `pos`, the new key; K/V[pos] are rounded to f16 and stored),
+//   1. request this token's q (G heads), k, v, cos/sin and norm weights,
+//      then its K and V tiles (16 B per lane, coalesced); every load is
+//      unconditional (rows past the range re-read a valid row and are zeroed
+//      later), so the compiler waits for the small loads alone while the
+//      tiles stream,
+//   2. RMSNorm + RoPE the G query heads (and, in the split that holds `pos`,
+//      the new key; K/V[pos] are rounded to f16 and stored),
 //   3. stage K (rows padded against bank conflicts) and V in LDS,
-//   4. scores: lane t computes q_g . k_t over a quarter of the dimensions,
-//      one quarter per wave; divided by sqrt(hd) (forward.odin:158),
+//   4. scores: lane l takes positions l, l+64, ... over a quarter of the
+//      dimensions (one quarter per wave); divided by sqrt(hd) (forward.odin:158),
 //   5. split max / exp-sum per head, o = sum_t p v_t (2 dims per lane),
-//   6. write (o, m, l) to a partial buffer.
+//   6. write (o, m, l) to the partial buffer.
 // attn_combine_kernel merges the splits of each query head with
 // exp(m_s - M) weights; the kernel boundary orders the partial writes before
-// the reads, so no fences or atomics are needed.  The current position is
-// used from LDS, so no workgroup reads a cache entry written in this launch.
+// the reads, so no fences or atomics are needed.  (Merging in the last
+// arriving split instead costs a store-completion wait, an atomic and the
+// partial reads in series, which measured slower than the kernel boundary.)
+// The current position is used from LDS, so no workgroup reads a cache
+// entry written in this launch.
 
 #include "device_common.h"
 
@@ -24,12 +31,13 @@ namespace oi {
 
 template <int HD>
 struct AttnShape {
-    static constexpr int CH = 8192 / HD;              // positions per workgroup (64 at hd 128)
+    static constexpr int CH = 64;                     // positions per workgroup (one per lane)
     static constexpr int KPAD = HD + 8;               // LDS row stride of K, in halves
     static constexpr int CPR = HD / 8;                // 16-byte chunks per row
     static constexpr int NLD = CH * CPR / WG;         // loads per thread per tensor
     static constexpr int DPW = HD / 4;                // score dimensions per wave
     static constexpr int DPL = HD / WAVE;             // o dimensions per lane
+    static constexpr int PPL = CH / WAVE;             // score positions per lane
 };
 constexpr int ATTN_MAX_SPLITS = 1024;
 
@@ -45,51 +53,39 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t ks[S::CH * S::KPAD];
     __shared__ __attribute__((aligned(16))) uint16_t vs[S::CH * HD];
     __shared__ __attribute__((aligned(16))) float qr[G][HD];
-    __shared__ float kp[HD], vp[HD];
+    __shared__ float kp[HD], vp[HD], qn[HD], kn[HD];
     __shared__ float sp[4][G][S::CH];  // per-wave partial scores, then p in sp[0]
     __shared__ float ob[4][G][HD];
     __shared__ float mx[G], sm[G], nrm[G + 1];
+    __shared__ float2 csl[HD / 2];
 
     const int split = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
     const int lane = tid & (WAVE - 1), wave = tid / WAVE;
-    const int pos = a.state[1];
+    const int pos = a.state[ST_POS];
     const int t0 = split * S::CH;
     if (t0 > pos) return;
     const int t1 = min(t0 + S::CH, pos + 1), n = t1 - t0;
     uint16_t *kc = a.kc + (size_t)kvh * a.seq_len * HD;
     uint16_t *vc = a.vc + (size_t)kvh * a.seq_len * HD;
+    const bool has_pos = pos < t1;
 
-    // 0. this token's q (and k, v at pos) first: vector loads return in order,
-    //    so they must not queue behind the tile loads
-    const bool has_pos = pos >= t0 && pos < t1;
+    // 1. small loads first (vector loads return in order), then the tiles
     constexpr int QPT = (G * HD + WG - 1) / WG;
     float qreg[QPT];
 #pragma unroll
-    for (int i = 0; i < QPT; i++) {
-        const int idx = tid + i * WG;
-        qreg[i] = idx < G * HD ? a.q[(size_t)kvh * G * HD + idx] : 0.f;
-    }
-    float kraw = 0.f, vraw = 0.f;
-    if (has_pos && tid < HD) {
-        kraw = a.k[(size_t)kvh * HD + tid];
-        vraw = a.v[(size_t)kvh * HD + tid];
-    }
-    const float2 *cs = a.rope_cs + (size_t)pos * (HD / 2);
-    const float2 csr = tid < HD / 2 ? cs[tid] : make_float2(0.f, 0.f);
-
-    // 1. K and V tile loads
+    for (int i = 0; i < QPT; i++) qreg[i] = a.q[(size_t)kvh * G * HD + min(tid + i * WG, G * HD - 1)];
+    const int hi = min(tid, HD - 1);
+    const float kraw = a.k[(size_t)kvh * HD + hi], vraw = a.v[(size_t)kvh * HD + hi];
+    const float2 csr = a.rope_cs[(size_t)pos * (HD / 2) + min(tid, HD / 2 - 1)];
+    const float qnr = a.q_norm[hi], knr = a.k_norm[hi];
     u32x4 kr[S::NLD], vr[S::NLD];
 #pragma unroll
     for (int j = 0; j < S::NLD; j++) {
-        const int c = tid + j * WG, tl = c / S::CPR, ch = c % S::CPR;
-        if (tl < n && t0 + tl != pos) {
-            kr[j] = ldg_nt((const u32x4 *)(kc + (size_t)(t0 + tl) * HD) + ch);
-            vr[j] = ldg_nt((const u32x4 *)(vc + (size_t)(t0 + tl) * HD) + ch);
-        } else {
-            kr[j] = u32x4{0u, 0u, 0u, 0u};
-            vr[j] = u32x4{0u, 0u, 0u, 0u};
-        }
+        const int c = tid + j * WG, tl = min(c / S::CPR, n - 1), ch = c % S::CPR;
+        kr[j] = ldg_nt((const u32x4 *)(kc + (size_t)(t0 + tl) * HD) + ch);
+        vr[j] = ldg_nt((const u32x4 *)(vc + (size_t)(t0 + tl) * HD) + ch);
     }
+    __builtin_amdgcn_sched_barrier(0);
 
     // 2. RMSNorm + RoPE of the G query heads (and of k at pos): ops.odin:7-19,
     //    forward.odin:117-145; cos/sin come from the host-built table
@@ -98,11 +94,12 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
         const int idx = tid + i * WG;
         if (idx < G * HD) qr[idx / HD][idx % HD] = qreg[i];
     }
-    if (has_pos && tid < HD) {
+    if (tid < HD) {
         kp[tid] = kraw;
         vp[tid] = vraw;
+        qn[tid] = qnr;
+        kn[tid] = knr;
     }
-    __shared__ float2 csl[HD / 2];
     if (tid < HD / 2) csl[tid] = csr;
     __syncthreads();
     const int nvec = G + (has_pos ? 1 : 0);
@@ -118,7 +115,7 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
 #pragma clang fp contract(off)
         const int g = idx / (HD / 2), i = idx % (HD / 2);
         float *v = g < G ? qr[g] : kp;
-        const float *w = g < G ? a.q_norm : a.k_norm;
+        const float *w = g < G ? qn : kn;
         const float s = nrm[g];
         const float x = w[i] * (s * v[i]);
         const float y = w[i + HD / 2] * (s * v[i + HD / 2]);
@@ -127,12 +124,14 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
         v[i + HD / 2] = x * sn + y * c;
     }
 
-    // 3. stage the tiles in LDS (rows beyond n are zero; row pos-t0 is set below)
+    // 3. stage the tiles in LDS (rows at or past n are zero; row pos-t0 is set below)
 #pragma unroll
     for (int j = 0; j < S::NLD; j++) {
         const int c = tid + j * WG, tl = c / S::CPR, ch = c % S::CPR;
-        *(u32x4 *)(ks + tl * S::KPAD + ch * 8) = kr[j];
-        *(u32x4 *)(vs + tl * HD + ch * 8) = vr[j];
+        const bool ok = tl < n && t0 + tl != pos;
+        const u32x4 z = {0u, 0u, 0u, 0u};
+        *(u32x4 *)(ks + tl * S::KPAD + ch * 8) = ok ? kr[j] : z;
+        *(u32x4 *)(vs + tl * HD + ch * 8) = ok ? vr[j] : z;
     }
     __syncthreads();
     if (has_pos) {
@@ -147,44 +146,61 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
         __syncthreads();
     }
 
-    // 4. partial scores: lane = position, wave = quarter of the dimensions
-    if (lane < S::CH) {
-        float acc[G];
+    // 4. partial scores: lane = positions lane + 64 p, wave = quarter of the dimensions
+    {
+        float acc[G][S::PPL];
 #pragma unroll
-        for (int g = 0; g < G; g++) acc[g] = 0.f;
-        const uint16_t *krow = ks + lane * S::KPAD + wave * S::DPW;
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int p = 0; p < S::PPL; p++) acc[g][p] = 0.f;
 #pragma unroll
         for (int c = 0; c < S::DPW / 8; c++) {
-            const u32x4 w = *(const u32x4 *)(krow + 8 * c);
-            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-            float kv[8];
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                kv[2 * e] = h2f(ws[e] & 0xFFFFu);
-                kv[2 * e + 1] = h2f(ws[e] >> 16);
-            }
+            for (int p = 0; p < S::PPL; p++) {
+                const u32x4 w = *(const u32x4 *)(ks + (lane + WAVE * p) * S::KPAD + wave * S::DPW + 8 * c);
+                const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+                float kv[8];
 #pragma unroll
-            for (int g = 0; g < G; g++) {
-                const float4 q0 = *(const float4 *)&qr[g][wave * S::DPW + 8 * c];
-                const float4 q1 = *(const float4 *)&qr[g][wave * S::DPW + 8 * c + 4];
-                acc[g] += q0.x * kv[0] + q0.y * kv[1] + q0.z * kv[2] + q0.w * kv[3] + q1.x * kv[4] +
-                          q1.y * kv[5] + q1.z * kv[6] + q1.w * kv[7];
+                for (int e = 0; e < 4; e++) {
+                    kv[2 * e] = h2f(ws[e] & 0xFFFFu);
+                    kv[2 * e + 1] = h2f(ws[e] >> 16);
+                }
+#pragma unroll
+                for (int g = 0; g < G; g++) {
+                    const float4 q0 = *(const float4 *)&qr[g][wave * S::DPW + 8 * c];
+                    const float4 q1 = *(const float4 *)&qr[g][wave * S::DPW + 8 * c + 4];
+                    acc[g][p] += q0.x * kv[0] + q0.y * kv[1] + q0.z * kv[2] + q0.w * kv[3] + q1.x * kv[4] +
+                                 q1.y * kv[5] + q1.z * kv[6] + q1.w * kv[7];
+                }
             }
         }
 #pragma unroll
-        for (int g = 0; g < G; g++) sp[wave][g][lane] = acc[g];
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int p = 0; p < S::PPL; p++) sp[wave][g][lane + WAVE * p] = acc[g][p];
     }
     __syncthreads();
 
     // 5. scores, split-local max and exp-sum (ops.odin:21-37), one wave per head
     const float div = sqrtf((float)HD);
     for (int g = wave; g < G; g += WG / WAVE) {
-        float sc = -INFINITY;
-        if (lane < n) sc = ((sp[0][g][lane] + sp[1][g][lane]) + (sp[2][g][lane] + sp[3][g][lane])) / div;
-        const float m = wave_max(sc);
-        const float e = lane < n ? expf(sc - m) : 0.f;
-        const float l = wave_sum(e);
-        if (lane < S::CH) sp[0][g][lane] = e;
+        float sc[S::PPL], m = -INFINITY;
+#pragma unroll
+        for (int p = 0; p < S::PPL; p++) {
+            const int t = lane + WAVE * p;
+            sc[p] = t < n ? ((sp[0][g][t] + sp[1][g][t]) + (sp[2][g][t] + sp[3][g][t])) / div : -INFINITY;
+            m = fmaxf(m, sc[p]);
+        }
+        m = wave_max(m);
+        float l = 0.f;
+#pragma unroll
+        for (int p = 0; p < S::PPL; p++) {
+            const int t = lane + WAVE * p;
+            const float e = t < n ? expf(sc[p] - m) : 0.f;
+            sp[0][g][t] = e;
+            l += e;
+        }
+        l = wave_sum(l);
         if (lane == 0) {
             mx[g] = m;
             sm[g] = l;
@@ -193,34 +209,36 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
     __syncthreads();
 
     // o_g = sum_t p_g(t) v(t): lane holds DPL dims, wave w takes t = w, w+4, ...
-    float acc[G][S::DPL];
+    {
+        float acc[G][S::DPL];
 #pragma unroll
-    for (int g = 0; g < G; g++)
+        for (int g = 0; g < G; g++)
 #pragma unroll
-        for (int e = 0; e < S::DPL; e++) acc[g][e] = 0.f;
-    for (int tl = wave; tl < n; tl += WG / WAVE) {
-        float vv[S::DPL];
-        if (S::DPL == 2) {
-            const uint32_t w = *(const uint32_t *)(vs + tl * HD + 2 * lane);
-            vv[0] = h2f(w & 0xFFFFu);
-            vv[S::DPL - 1] = h2f(w >> 16);
-        } else {
-            const u32x2 w = *(const u32x2 *)(vs + tl * HD + S::DPL * lane);
-            const uint32_t ws[2] = {w.x, w.y};
+            for (int e = 0; e < S::DPL; e++) acc[g][e] = 0.f;
+        for (int tl = wave; tl < n; tl += WG / WAVE) {
+            float vv[S::DPL];
+            if (S::DPL == 2) {
+                const uint32_t w = *(const uint32_t *)(vs + tl * HD + 2 * lane);
+                vv[0] = h2f(w & 0xFFFFu);
+                vv[S::DPL - 1] = h2f(w >> 16);
+            } else {
+                const u32x2 w = *(const u32x2 *)(vs + tl * HD + S::DPL * lane);
+                const uint32_t ws[2] = {w.x, w.y};
 #pragma unroll
-            for (int e = 0; e < S::DPL; e++) vv[e] = h2f((ws[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+                for (int e = 0; e < S::DPL; e++) vv[e] = h2f((ws[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+            }
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                const float p = sp[0][g][tl];
+#pragma unroll
+                for (int e = 0; e < S::DPL; e++) acc[g][e] += p * vv[e];
+            }
         }
 #pragma unroll
-        for (int g = 0; g < G; g++) {
-            const float p = sp[0][g][tl];
+        for (int g = 0; g < G; g++)
 #pragma unroll
-            for (int e = 0; e < S::DPL; e++) acc[g][e] += p * vv[e];
-        }
+            for (int e = 0; e < S::DPL; e++) ob[wave][g][S::DPL * lane + e] = acc[g][e];
     }
-#pragma unroll
-    for (int g = 0; g < G; g++)
-#pragma unroll
-        for (int e = 0; e < S::DPL; e++) ob[wave][g][S::DPL * lane + e] = acc[g][e];
     __syncthreads();
 
     // 6. partial (o, m, l) of this split
@@ -247,7 +265,7 @@ __global__ __launch_bounds__(WG) void attn_combine_kernel(AttnArgs a) {
     __shared__ float Ls;
     const int h = blockIdx.x, i = blockIdx.y * WAVE + (threadIdx.x & (WAVE - 1));
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid / WAVE;
-    const int pos = a.state[1];
+    const int pos = a.state[ST_POS];
     const int nsplit = pos / S::CH + 1;
     const int stride = HD + 2;
     const float *pb = a.part + (size_t)h * a.max_splits * stride;
