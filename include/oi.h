@@ -114,7 +114,9 @@ enum {
     OI_KERNEL_WO = 2,      /* attention output GEMV + residual */
     OI_KERNEL_GATEUP = 3,  /* RMSNorm + gate/up GEMV + SwiGLU */
     OI_KERNEL_DOWN = 4,    /* down GEMV + residual */
-    OI_KERNEL_OUTPUT = 5   /* final RMSNorm + vocab GEMV + greedy argmax */
+    OI_KERNEL_OUTPUT = 5,  /* final RMSNorm + vocab GEMV + greedy argmax */
+    OI_KERNEL_TOKEN = 6    /* one whole token step (the persistent token kernel when the
+                              engine uses it, else the multi-kernel graph) */
 };
 
 /* Launch one kernel of the token loop `iters` times on the engine's stream,
@@ -122,7 +124,10 @@ enum {
  * duration per launch measured with HIP events on that stream (*avg_us) and
  * the algorithmic HBM bytes of one launch (*bytes).  The attention kernel is
  * timed at the position of the last forward/decode call.  Leaves the
- * activations and the KV entry at that position modified. */
+ * activations and the KV entry at that position modified.
+ * OI_KERNEL_TOKEN times `iters` consecutive greedy token steps from the last
+ * forward/decode position (moved back so they fit the context); *bytes is
+ * then the whole step's algorithmic bytes at the mean position. */
 int oi_engine_time_kernel(oi_engine *e, int32_t kernel, int32_t iters, double *avg_us, double *bytes);
 
 /* --------------------------------------------------- kernels (test, bench) --- */

@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <array>
 #include <climits>
 #include <cmath>
 #include <cstdio>
@@ -22,7 +23,10 @@
 
 #include "gguf.h"
 #include "oi.h"
+#include "oi_debug.h"
 #include "oi_kernels.h"
+#include "stream.h"
+#include "stream_plan.h"
 
 using namespace oi;
 
@@ -81,6 +85,9 @@ bool matrix_bytes(uint32_t type, int64_t rows, int64_t cols, size_t &bytes) {
     return true;
 }
 
+}  // namespace
+
+namespace oi {
 // Q4_K super-block header in the device form: d, dmin, then the 6-bit
 // (scale, min) of each group pair p as one 24-bit field at bits 24p of the
 // tail.  The values are those of get_scale_min_k4 (ggml/quant.odin:64-73).
@@ -112,6 +119,10 @@ void q4k_header(const uint8_t *blk, uint8_t *out) {
     std::memcpy(out + 4, &lo, 8);
     std::memcpy(out + 12, &hi, 4);
 }
+
+}  // namespace oi
+
+namespace {
 
 // Repack one GGUF matrix into the device layout (see DMat in oi_kernels.h).
 // Writes into `dst` (bytes from matrix_bytes) and returns the region offsets.
@@ -213,7 +224,7 @@ struct LayerDev {
 
 }  // namespace
 
-enum { K_QKV = 0, K_ATTN = 1, K_WO = 2, K_GATEUP = 3, K_DOWN = 4, K_OUTPUT = 5 };
+enum { K_QKV = 0, K_ATTN = 1, K_WO = 2, K_GATEUP = 3, K_DOWN = 4, K_OUTPUT = 5, K_TOKEN = 6 };
 
 struct oi_engine {
     oi_config cfg{};
@@ -239,6 +250,11 @@ struct oi_engine {
     hipGraphExec_t gexec = nullptr;
     int last_pos = 0;
     size_t weight_bytes = 0;
+    // persistent token kernel (stream.hip); the multi-kernel path above is
+    // used when it cannot run the model
+    bool use_stream = false;
+    StreamArgs sa{};
+    int64_t stream_seq = 0;   // launches so far (the device keeps its own copy)
 };
 
 namespace {
@@ -259,7 +275,7 @@ int enqueue_token(oi_engine *e) {
 }
 
 int ensure_graph(oi_engine *e) {
-    if (e->gexec || !e->use_graph) return OI_OK;
+    if (e->use_stream || e->gexec || !e->use_graph) return OI_OK;
     HIP_TRY(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
     int rc = enqueue_token(e);
     hipGraph_t g = nullptr;
@@ -281,9 +297,24 @@ int set_state(oi_engine *e, int32_t token, int32_t pos, int32_t cap) {
     return OI_OK;
 }
 
-// One token step: the captured graph, or the same launches issued directly
-// (OI_NO_GRAPH=1, e.g. under tools that do not follow graph capture).
+// A barrier timeout inside the token kernel leaves ST_ERR set; the launch
+// sequence of the grid barrier is then unreliable and the engine is unusable.
+int check_stream_error(oi_engine *e) {
+    if (!e->use_stream) return OI_OK;
+    int32_t err = 0;
+    HIP_TRY(hipMemcpy(&err, e->state + ST_ERR, 4, hipMemcpyDeviceToHost));
+    if (err) return fail(OI_E_DEVICE, "token kernel: grid barrier timed out (engine unusable)");
+    return OI_OK;
+}
+
+// One token step: the persistent token kernel; or the captured graph of the
+// multi-kernel path, or its launches issued directly (OI_NO_GRAPH=1, e.g.
+// under tools that do not follow graph capture).
 int run_token(oi_engine *e) {
+    if (e->use_stream) {
+        HIP_TRY(launch_stream(e->sa, e->stream));
+        return OI_OK;
+    }
     if (e->use_graph) {
         HIP_TRY(hipGraphLaunch(e->gexec, e->stream));
         return OI_OK;
@@ -301,6 +332,269 @@ GemvArgs gemv_args(int mode, int K, const float *x, const float *norm_w, float e
     return a;
 }
 
+
+// ---------------------------------------------------- token kernel plan --
+struct StreamPlanAll {
+    std::vector<PlanKind> plans;
+    std::vector<std::array<int, 4>> layer_plan;
+    int vocab_plan = -1;
+    std::vector<size_t> stage_off;  // per (layer, kind) and the vocab stage: offset in the stage region
+    size_t stage_bytes = 0;
+    int G = 0, rD = 0, rH = 0, rQ = 0, yo = 0;
+    size_t lds = 0;
+};
+
+int plan_index(StreamPlanAll &sp, int kind, const int *types, int nseg, const int *rows, int K, int own,
+               std::string &why) {
+    for (size_t i = 0; i < sp.plans.size(); i++) {
+        const SKind &k = sp.plans[i].kind;
+        bool same = k.K == K && (k.pair != 0) == (kind == SK_GU) && k.nseg == (kind == SK_GU ? 1 : nseg);
+        for (int s = 0; same && s < k.nseg; s++) same = k.seg[s].type == types[s] && k.seg[s].rows == rows[s];
+        if (same && (int)sp.plans[i].wgrows.size() == sp.G && kind != SK_QKV && kind != SK_VOCAB) {
+            // owned-row plans also depend on `own`: compare the first workgroup
+            same = sp.plans[i].wgrows[0].v1 - sp.plans[i].wgrows[0].v0 == std::min(own, rows[0]);
+        }
+        if (same) return (int)i;
+    }
+    PlanKind pk;
+    if (!plan_stream_kind(kind, types, nseg, rows, K, sp.G, own, pk, why)) return -1;
+    sp.yo = std::max(sp.yo, pk.max_wg_rows);
+    sp.plans.push_back(std::move(pk));
+    return (int)sp.plans.size() - 1;
+}
+
+// Can the token kernel run this model on this device?  Fills the plan.
+bool plan_stream_all(GgufFile &g, const oi_config &c, bool tied, int dev, StreamPlanAll &sp, std::string &why) {
+    const int G8 = (int)(c.n_heads / c.n_kv_heads);
+    if (c.head_dim != 128 || G8 > 4) {
+        why = "head_dim 128 and at most 4 query heads per KV head";
+        return false;
+    }
+    int coop = 0, cus = 0, lds_max = 0;
+    hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev);
+    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+    if (!coop || cus <= 0) {
+        why = "cooperative launch not available";
+        return false;
+    }
+    sp.G = cus;
+    if ((2 * sp.G) % c.n_kv_heads) {
+        why = "KV heads do not divide the attention slots";
+        return false;
+    }
+    const int64_t D = c.dim, H = c.hidden_dim, QD = c.n_heads * c.head_dim, KVD = c.n_kv_heads * c.head_dim;
+    auto own = [&](int64_t n) { return (int)(16 * ((n + 16 * sp.G - 1) / (16 * sp.G))); };
+    sp.rD = own(D);
+    sp.rH = own(H);
+    sp.rQ = own(QD);
+    if (sp.rD > 256 || sp.rH > 256 || sp.rQ > 256) {
+        why = "vectors too long for the workgroup row ownership";
+        return false;
+    }
+    auto ty = [&](const std::string &n) { return (int)g.tensor(n)->kind; };
+    sp.layer_plan.resize((size_t)c.n_layers);
+    for (int64_t l = 0; l < c.n_layers; l++) {
+        const std::string p = "blk." + std::to_string(l) + ".";
+        const int tq[3] = {ty(p + "attn_q.weight"), ty(p + "attn_k.weight"), ty(p + "attn_v.weight")};
+        const int rq[3] = {(int)QD, (int)KVD, (int)KVD};
+        const int to[1] = {ty(p + "attn_output.weight")}, ro[1] = {(int)D};
+        const int tg[2] = {ty(p + "ffn_gate.weight"), ty(p + "ffn_up.weight")}, rg[2] = {(int)H, (int)H};
+        const int td[1] = {ty(p + "ffn_down.weight")}, rd[1] = {(int)D};
+        auto &lp = sp.layer_plan[(size_t)l];
+        if ((lp[SK_QKV] = plan_index(sp, SK_QKV, tq, 3, rq, (int)D, 0, why)) < 0) return false;
+        if ((lp[SK_WO] = plan_index(sp, SK_WO, to, 1, ro, (int)QD, sp.rD, why)) < 0) return false;
+        if ((lp[SK_GU] = plan_index(sp, SK_GU, tg, 2, rg, (int)D, sp.rH, why)) < 0) return false;
+        if ((lp[SK_DOWN] = plan_index(sp, SK_DOWN, td, 1, rd, (int)H, sp.rD, why)) < 0) return false;
+    }
+    const int tv[1] = {ty(tied ? "token_embd.weight" : "output.weight")}, rv[1] = {(int)c.vocab_size};
+    if ((sp.vocab_plan = plan_index(sp, SK_VOCAB, tv, 1, rv, (int)D, 0, why)) < 0) return false;
+    sp.yo = std::max(sp.yo, std::max(sp.rQ, 16));
+    sp.lds = stream_lds_bytes((int)std::max(D, std::max(H, QD)), sp.yo);
+    if ((int64_t)sp.lds > lds_max) {
+        why = "token kernel needs " + std::to_string(sp.lds) + " bytes of LDS, device has " + std::to_string(lds_max);
+        return false;
+    }
+    size_t off = 0;
+    for (int64_t l = 0; l < c.n_layers; l++)
+        for (int k = 0; k < 4; k++) {
+            sp.stage_off.push_back(off);
+            off += ((size_t)sp.plans[(size_t)sp.layer_plan[(size_t)l][(size_t)k]].kind.bytes + 255) & ~(size_t)255;
+        }
+    sp.stage_off.push_back(off);
+    off += ((size_t)sp.plans[(size_t)sp.vocab_plan].kind.bytes + 255) & ~(size_t)255;
+    sp.stage_bytes = off;
+    return true;
+}
+
+
+template <class T>
+T *upload_table(oi_engine *e, const std::vector<T> &v) {
+    T *d = (T *)e->arena.take(v.size() * sizeof(T));
+    if (!d || hipMemcpyAsync(d, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice, e->stream) != hipSuccess ||
+        hipStreamSynchronize(e->stream) != hipSuccess)
+        return nullptr;
+    return d;
+}
+
+// Stage buffers in the stream layout, the plan tables and the token kernel's
+// arguments.
+int upload_stream(oi_engine *e, GgufFile &g, bool tied, const StreamPlanAll &sp) {
+    const oi_config &c = e->cfg;
+    uint8_t *stages = e->arena.take(sp.stage_bytes);
+    if (!stages) return fail(OI_E_NOMEM, "arena exhausted (token kernel weights)");
+    std::vector<uint8_t> host;
+    auto put = [&](const PlanKind &pk, const uint8_t *const *src, size_t off) -> int {
+        host.resize((size_t)pk.kind.bytes);
+        repack_stream_kind(pk, src, sp.G, host.data());
+        HIP_TRY(hipMemcpyAsync(stages + off, host.data(), host.size(), hipMemcpyHostToDevice, e->stream));
+        HIP_TRY(hipStreamSynchronize(e->stream));
+        return OI_OK;
+    };
+    std::vector<SLayer> layers((size_t)c.n_layers);
+    int rc;
+    for (int64_t l = 0; l < c.n_layers; l++) {
+        const std::string p = "blk." + std::to_string(l) + ".";
+        auto d = [&](const char *n) { return (const uint8_t *)g.tensor(p + n)->data; };
+        const uint8_t *qkv[3] = {d("attn_q.weight"), d("attn_k.weight"), d("attn_v.weight")};
+        const uint8_t *wo[1] = {d("attn_output.weight")};
+        const uint8_t *gu[2] = {d("ffn_gate.weight"), d("ffn_up.weight")};
+        const uint8_t *dn[1] = {d("ffn_down.weight")};
+        const uint8_t *const *srcs[4] = {qkv, wo, gu, dn};
+        SLayer &L = layers[(size_t)l];
+        for (int k = 0; k < 4; k++) {
+            const size_t off = sp.stage_off[(size_t)l * 4 + (size_t)k];
+            const int pi = sp.layer_plan[(size_t)l][(size_t)k];
+            if ((rc = put(sp.plans[(size_t)pi], srcs[k], off))) return rc;
+            L.w[k] = stages + off;
+            L.plan[k] = pi;
+        }
+        const LayerDev &LD = e->layers[(size_t)l];
+        L.attn_norm = LD.attn_norm;
+        L.ffn_norm = LD.ffn_norm;
+        L.q_norm = LD.q_norm;
+        L.k_norm = LD.k_norm;
+        L.kc = LD.kc;
+        L.vc = LD.vc;
+    }
+    {
+        const uint8_t *voc[1] = {(const uint8_t *)g.tensor(tied ? "token_embd.weight" : "output.weight")->data};
+        if ((rc = put(sp.plans[(size_t)sp.vocab_plan], voc, sp.stage_off.back()))) return rc;
+    }
+    std::vector<SKind> kinds;
+    std::vector<SWave> waves;
+    std::vector<SWgRows> wgrows;
+    for (const PlanKind &pk : sp.plans) {
+        kinds.push_back(pk.kind);
+        waves.insert(waves.end(), pk.waves.begin(), pk.waves.end());
+        wgrows.insert(wgrows.end(), pk.wgrows.begin(), pk.wgrows.end());
+    }
+    StreamArgs &A = e->sa;
+    A = StreamArgs{};
+    A.layers = upload_table(e, layers);
+    A.kinds = upload_table(e, kinds);
+    A.waves = upload_table(e, waves);
+    A.wgrows = upload_table(e, wgrows);
+    if (!A.layers || !A.kinds || !A.waves || !A.wgrows) return fail(OI_E_DEVICE, "token kernel tables upload failed");
+    const int64_t QD = c.n_heads * c.head_dim;
+    auto qv = [](int64_t K) { return ((size_t)qvec_bytes(K) + 2047) & ~(size_t)1023; };
+    A.xq = e->arena.take(qv(c.dim));
+    A.attq = e->arena.take(qv(QD));
+    A.hbq = e->arena.take(qv(c.hidden_dim));
+    A.ssq = (float *)e->arena.take((size_t)sp.G * 4);
+    A.bar = (uint64_t *)e->arena.take(S_NC * 256);
+    if (!A.xq || !A.attq || !A.hbq || !A.ssq || !A.bar) return fail(OI_E_NOMEM, "arena exhausted (token kernel)");
+    A.n_layers = (int32_t)c.n_layers;
+    if (const char *ev = std::getenv("OI_STREAM_LAYERS"))  // debugging: run only the first layers
+        A.n_layers = (int32_t)std::max<int64_t>(1, std::min<int64_t>(c.n_layers, std::atoll(ev)));
+    A.G = sp.G;
+    A.vocab_w = stages + sp.stage_off.back();
+    A.vocab_plan = sp.vocab_plan;
+    A.output_norm = e->output_norm;
+    A.emb = e->tok_embd;
+    A.D = (int32_t)c.dim;
+    A.H = (int32_t)c.hidden_dim;
+    A.QD = (int32_t)QD;
+    A.KVD = (int32_t)(c.n_kv_heads * c.head_dim);
+    A.HD = (int32_t)c.head_dim;
+    A.n_heads = (int32_t)c.n_heads;
+    A.n_kv = (int32_t)c.n_kv_heads;
+    A.vocab = (int32_t)c.vocab_size;
+    A.seq_len = (int32_t)c.seq_len;
+    A.rD = sp.rD;
+    A.rH = sp.rH;
+    A.rQ = sp.rQ;
+    A.eps = c.rms_eps;
+    A.rope_cs = e->rope_cs;
+    A.q = e->q;
+    A.k = e->k;
+    A.v = e->v;
+    A.part = e->part;
+    A.max_chunks = e->max_splits;
+    A.logits = e->logits;
+    A.am_val = e->am_val;
+    A.am_idx = e->am_idx;
+    A.state = e->state;
+    A.tokens = e->tokens;
+    A.finalize_only = 0;
+    A.yo_floats = sp.yo;
+    A.trace = nullptr;
+    if (const char *ev = std::getenv("OI_STREAM_TRACE")) {
+        if (ev[0] == '1') {
+            const size_t tb = (size_t)(2 + 6 * c.n_layers) * sp.G * 8 * 8;
+            HIP_TRY(hipMalloc(&A.trace, tb));  // freed with the engine
+            HIP_TRY(hipMemset(A.trace, 0, tb));
+        }
+    }
+    return OI_OK;
+}
+
+
+// Mean time of one token step (the token kernel, or the multi-kernel graph)
+// over `iters` consecutive greedy steps from the last forward/decode position
+// (moved back so the steps stay inside the context), HIP events on the
+// engine stream.  *bytes: algorithmic HBM bytes of one step at the mean
+// position (weights read once, f16 K/V read and written, logits written).
+int time_token(oi_engine *e, int iters, double *avg_us, double *bytes) {
+    const oi_config &c = e->cfg;
+    if (iters >= c.seq_len) return fail(OI_E_ARG, "iters exceeds the context");
+    const int start = (int)std::min<int64_t>(e->last_pos, c.seq_len - 1 - iters);
+    int rc = ensure_graph(e);
+    if (rc) return rc;
+    hipEvent_t e0, e1;
+    HIP_TRY(hipEventCreate(&e0));
+    HIP_TRY(hipEventCreate(&e1));
+    for (int pass = 0; pass < 2; pass++) {  // warm-up pass, then the timed pass
+        if ((rc = set_state(e, 0, start, 0))) return rc;
+        if (pass) HIP_TRY(hipEventRecord(e0, e->stream));
+        for (int i = 0; i < iters; i++)
+            if ((rc = run_token(e))) return rc;
+        if (pass) HIP_TRY(hipEventRecord(e1, e->stream));
+    }
+    HIP_TRY(hipEventSynchronize(e1));
+    if ((rc = check_stream_error(e))) return rc;
+    float ms = 0;
+    HIP_TRY(hipEventElapsedTime(&ms, e0, e1));
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    *avg_us = ms * 1000.0 / iters;
+    auto mb = [](const DMat &m) {
+        size_t b = 0;
+        matrix_bytes((uint32_t)m.type, m.rows, m.cols, b);
+        return (double)b;
+    };
+    double w = mb(e->output) + 4.0 * c.dim;  // + output_norm
+    size_t erow = 0;
+    matrix_bytes((uint32_t)e->tok_embd.type, 1, e->tok_embd.cols, erow);
+    w += (double)erow;
+    for (const LayerDev &L : e->layers)
+        w += mb(L.wq) + mb(L.wk) + mb(L.wv) + mb(L.wo) + mb(L.w1) + mb(L.w2) + mb(L.w3) + 4.0 * (2 * c.dim + 2 * c.head_dim);
+    const double kvd = (double)(c.n_kv_heads * c.head_dim), mean_pos = start + (iters - 1) / 2.0;
+    *bytes = w + c.n_layers * 2 * kvd * 2 * (mean_pos + 1) + c.n_layers * 2 * kvd * 2 + 4.0 * c.vocab_size;
+    e->last_pos = start + iters - 1;
+    return OI_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -314,6 +608,7 @@ void oi_engine_destroy(oi_engine *e) {
     if (e->gexec) hipGraphExecDestroy(e->gexec);
     if (e->graph) hipGraphDestroy(e->graph);
     if (e->arena.base) hipFree(e->arena.base);
+    if (e->sa.trace) hipFree(e->sa.trace);
     if (e->logits_host) hipHostFree(e->logits_host);
     if (e->state_host) hipHostFree(e->state_host);
     if (e->stream) hipStreamDestroy(e->stream);
@@ -416,6 +711,26 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     e->weight_bytes = wbytes;
     if ((rc = check_device(opts->device))) return rc;
 
+    // persistent token kernel (OI_STREAM=1; the multi-kernel path otherwise)
+    StreamPlanAll sp;
+    {
+        const char *ev = std::getenv("OI_STREAM");
+        const bool want = ev && ev[0] == '1';
+        std::string why;
+        e->use_stream = want && plan_stream_all(g, c, tied, opts->device, sp, why);
+        if (want && !e->use_stream)
+            std::fprintf(stderr, "note: token kernel not used (%s); multi-kernel path\n", why.c_str());
+    }
+    size_t stream_extra = 0;
+    const int64_t QDs = c.n_heads * c.head_dim;
+    auto qv = [](int64_t K) { return ((size_t)qvec_bytes(K) + 2047) & ~(size_t)1023; };
+    if (e->use_stream) {
+        const size_t np = sp.plans.size(), NW = (size_t)sp.G * S_NCW;
+        stream_extra = sp.stage_bytes + np * (sizeof(SKind) + 256) + np * NW * sizeof(SWave) +
+                       np * (size_t)sp.G * sizeof(SWgRows) + (size_t)c.n_layers * sizeof(SLayer) + qv(c.dim) +
+                       qv(QDs) + qv(c.hidden_dim) + (size_t)sp.G * 8 + S_NC * 256 + 16 * 256;
+    }
+
     // device memory plan
     e->chunk = attn_chunk((int)c.head_dim);
     e->max_splits = (int)((c.seq_len + e->chunk - 1) / e->chunk);
@@ -433,9 +748,10 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     plan_gemv(probe);
     size_t act = al(D * 4) + al(QD * 4) + 2 * al(KVD * 4) + al(QD * 4) + al(H * 4) + al(out_rows * 4) +
                  al((size_t)c.n_heads * e->max_splits * (c.head_dim + 2) * 4) + 2 * al((size_t)probe.total_wgs * 4) +
-                 al(ST_WORDS * 4) + al((size_t)(c.seq_len + 1) * 4) +
+                 2 * al((size_t)std::max(probe.total_wgs, sp.G) * 4) + al(ST_SWORDS * 4) +
+                 al((size_t)(c.seq_len + 1) * 4) +
                  al((size_t)c.seq_len * (c.head_dim / 2) * 8);
-    e->arena.size = wbytes + 2 * kv_layer * c.n_layers + act + 4096;
+    e->arena.size = wbytes + 2 * kv_layer * c.n_layers + act + stream_extra + 4096;
     hipError_t he = hipMalloc(&e->arena.base, e->arena.size);
     if (he != hipSuccess) return fail(OI_E_NOMEM, "hipMalloc of " + std::to_string(e->arena.size) + " bytes failed");
     HIP_TRY(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking));
@@ -483,9 +799,9 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     e->hb = (float *)e->arena.take(H * 4);
     e->logits = (float *)e->arena.take(out_rows * 4);
     e->part = (float *)e->arena.take((size_t)c.n_heads * e->max_splits * (c.head_dim + 2) * 4);
-    e->am_val = (float *)e->arena.take((size_t)probe.total_wgs * 4);
-    e->am_idx = (int32_t *)e->arena.take((size_t)probe.total_wgs * 4);
-    e->state = (int32_t *)e->arena.take(ST_WORDS * 4);
+    e->am_val = (float *)e->arena.take((size_t)std::max(probe.total_wgs, sp.G) * 4);
+    e->am_idx = (int32_t *)e->arena.take((size_t)std::max(probe.total_wgs, sp.G) * 4);
+    e->state = (int32_t *)e->arena.take(ST_SWORDS * 4);
     e->tokens = (int32_t *)e->arena.take((size_t)(c.seq_len + 1) * 4);
     e->rope_cs = (float2 *)e->arena.take((size_t)c.seq_len * (c.head_dim / 2) * 8);
     if (!e->rope_cs) return fail(OI_E_NOMEM, "arena exhausted (activations)");
@@ -504,6 +820,7 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
         HIP_TRY(hipMemcpyAsync(e->rope_cs, cs.data(), cs.size() * 8, hipMemcpyHostToDevice, e->stream));
         HIP_TRY(hipStreamSynchronize(e->stream));
     }
+    if (e->use_stream && (rc = upload_stream(e.get(), g, tied, sp))) return rc;
     HIP_TRY(hipHostMalloc((void **)&e->logits_host, out_rows * 4, hipHostMallocDefault));
     HIP_TRY(hipHostMalloc((void **)&e->state_host, ST_WORDS * 4, hipHostMallocDefault));
 
@@ -608,6 +925,7 @@ const float *oi_engine_forward(oi_engine *e, int32_t token, int32_t pos) {
         fail(OI_E_DEVICE, std::string("forward: ") + hipGetErrorString(r));
         return nullptr;
     }
+    if (check_stream_error(e)) return nullptr;
     e->last_pos = pos;
     return e->logits_host;
 }
@@ -626,10 +944,17 @@ int oi_engine_decode_greedy(oi_engine *e, int32_t token, int32_t pos, int32_t n_
     for (int i = 0; i < n_steps; i++)
         if ((rc = run_token(e))) return rc;
     // the last step's argmax is still pending: reduce it
-    HIP_TRY(launch_embed(e->tok_embd, e->state, e->x, (int32_t)e->cfg.vocab_size, e->am_val, e->am_idx, e->tokens, 1,
-                         e->stream));
+    if (e->use_stream) {
+        StreamArgs f = e->sa;
+        f.finalize_only = 1;
+        HIP_TRY(launch_stream(f, e->stream));
+    } else {
+        HIP_TRY(launch_embed(e->tok_embd, e->state, e->x, (int32_t)e->cfg.vocab_size, e->am_val, e->am_idx,
+                             e->tokens, 1, e->stream));
+    }
     HIP_TRY(hipMemcpyAsync(out_tokens, e->tokens, (size_t)n_steps * 4, hipMemcpyDeviceToHost, e->stream));
     HIP_TRY(hipStreamSynchronize(e->stream));
+    if ((rc = check_stream_error(e))) return rc;
     e->last_pos = pos + n_steps - 1;
     return OI_OK;
 }
@@ -660,8 +985,9 @@ const float *oi_engine_logits_device(oi_engine *e) { return e ? e->logits : null
 void *oi_engine_stream(oi_engine *e) { return e ? (void *)e->stream : nullptr; }
 
 int oi_engine_time_kernel(oi_engine *e, int32_t kernel, int32_t iters, double *avg_us, double *bytes) {
-    if (!e || !avg_us || !bytes || iters <= 0 || kernel < K_QKV || kernel > K_OUTPUT)
+    if (!e || !avg_us || !bytes || iters <= 0 || kernel < K_QKV || kernel > K_TOKEN)
         return fail(OI_E_ARG, "bad argument");
+    if (kernel == K_TOKEN) return time_token(e, iters, avg_us, bytes);
     HIP_TRY(hipSetDevice(e->device));
     const oi_config &c = e->cfg;
     const size_t L = e->layers.size();
@@ -810,6 +1136,37 @@ int oi_dequant(int32_t type, const void *blocks, int64_t n, float *out) {
     oi_weights_free(w);
     if (r != hipSuccess) return fail(OI_E_DEVICE, std::string("dequant: ") + hipGetErrorString(r));
     return OI_OK;
+}
+
+int64_t oi_engine_debug_buffer(oi_engine *e, int32_t which, void *dst, int64_t bytes) {
+    if (!e || !dst || bytes < 0) return fail(OI_E_ARG, "bad argument");
+    const oi_config &c = e->cfg;
+    const int64_t QD = c.n_heads * c.head_dim, KVD = c.n_kv_heads * c.head_dim;
+    auto qv = [](int64_t K) { return (int64_t)qvec_bytes(K); };
+    const void *src = nullptr;
+    int64_t n = 0;
+    switch (which) {
+    case OI_BUF_XQ: src = e->sa.xq, n = qv(c.dim); break;
+    case OI_BUF_ATTQ: src = e->sa.attq, n = qv(QD); break;
+    case OI_BUF_HBQ: src = e->sa.hbq, n = qv(c.hidden_dim); break;
+    case OI_BUF_SSQ: src = e->sa.ssq, n = (int64_t)e->sa.G * 4; break;
+    case OI_BUF_Q: src = e->q, n = QD * 4; break;
+    case OI_BUF_K: src = e->k, n = KVD * 4; break;
+    case OI_BUF_V: src = e->v, n = KVD * 4; break;
+    case OI_BUF_PART: src = e->part, n = c.n_heads * (int64_t)e->max_splits * (c.head_dim + 2) * 4; break;
+    case OI_BUF_LOGITS: src = e->logits, n = c.vocab_size * 4; break;
+    case OI_BUF_STATE: src = e->state, n = ST_SWORDS * 4; break;
+    case OI_BUF_AMVAL: src = e->am_val, n = (int64_t)std::max(e->sa.G, 1) * 4; break;
+    case OI_BUF_AMIDX: src = e->am_idx, n = (int64_t)std::max(e->sa.G, 1) * 4; break;
+    case OI_BUF_TRACE: src = e->sa.trace, n = (int64_t)(2 + 6 * c.n_layers) * e->sa.G * 64; break;
+    default: return fail(OI_E_ARG, "unknown buffer");
+    }
+    if (!src) return fail(OI_E_ARG, "buffer not used by this engine");
+    n = std::min(n, bytes);
+    HIP_TRY(hipSetDevice(e->device));
+    HIP_TRY(hipStreamSynchronize(e->stream));
+    HIP_TRY(hipMemcpy(dst, src, (size_t)n, hipMemcpyDeviceToHost));
+    return n;
 }
 
 }  // extern "C"
