@@ -23,7 +23,8 @@ enum {
     OI_BUF_Q = 4,       /* q, k, v projections of the last layer */
     OI_BUF_K = 5,
     OI_BUF_V = 6,
-    OI_BUF_PART = 7,    /* attention partials [n_heads][chunks][head_dim + 2] */
+    OI_BUF_PART = 7,    /* attention partials [n_heads][chunks][head_dim + 4]: o, m, l, pad (token kernel;
+                           the multi-kernel path uses a stride of head_dim + 2) */
     OI_BUF_LOGITS = 8,
     OI_BUF_STATE = 9,
     OI_BUF_AMVAL = 10,

@@ -338,8 +338,8 @@ struct StreamPlanAll {
     std::vector<PlanKind> plans;
     std::vector<std::array<int, 4>> layer_plan;
     int vocab_plan = -1;
-    std::vector<size_t> stage_off;  // per (layer, kind) and the vocab stage: offset in the stage region
-    size_t stage_bytes = 0;
+    std::vector<int32_t> wpieces;  // [G * S_NCW] 1 KB pieces of each compute wave's weight stream
+    size_t wstride = 0;            // bytes between consecutive waves' streams
     int G = 0, rD = 0, rH = 0, rQ = 0, yo = 0;
     size_t lds = 0;
 };
@@ -409,21 +409,26 @@ bool plan_stream_all(GgufFile &g, const oi_config &c, bool tied, int dev, Stream
     }
     const int tv[1] = {ty(tied ? "token_embd.weight" : "output.weight")}, rv[1] = {(int)c.vocab_size};
     if ((sp.vocab_plan = plan_index(sp, SK_VOCAB, tv, 1, rv, (int)D, 0, why)) < 0) return false;
+    if ((c.seq_len + 63) / 64 > 512) {  // the combine gathers at most 8 x 64 chunks in LDS
+        why = "context longer than 32768 positions";
+        return false;
+    }
     sp.yo = std::max(sp.yo, std::max(sp.rQ, 16));
     sp.lds = stream_lds_bytes((int)std::max(D, std::max(H, QD)), sp.yo);
     if ((int64_t)sp.lds > lds_max) {
         why = "token kernel needs " + std::to_string(sp.lds) + " bytes of LDS, device has " + std::to_string(lds_max);
         return false;
     }
-    size_t off = 0;
+    const int NW = sp.G * S_NCW;
+    sp.wpieces.assign((size_t)NW, 0);
+    auto add = [&](int pi) {
+        for (int w = 0; w < NW; w++) sp.wpieces[(size_t)w] += sp.plans[(size_t)pi].waves[(size_t)w].npieces;
+    };
     for (int64_t l = 0; l < c.n_layers; l++)
-        for (int k = 0; k < 4; k++) {
-            sp.stage_off.push_back(off);
-            off += ((size_t)sp.plans[(size_t)sp.layer_plan[(size_t)l][(size_t)k]].kind.bytes + 255) & ~(size_t)255;
-        }
-    sp.stage_off.push_back(off);
-    off += ((size_t)sp.plans[(size_t)sp.vocab_plan].kind.bytes + 255) & ~(size_t)255;
-    sp.stage_bytes = off;
+        for (int k = 0; k < 4; k++) add(sp.layer_plan[(size_t)l][(size_t)k]);
+    add(sp.vocab_plan);
+    const int32_t most = *std::max_element(sp.wpieces.begin(), sp.wpieces.end());
+    sp.wstride = ((size_t)most * 1024 + 4095) & ~(size_t)4095;
     return true;
 }
 
@@ -437,37 +442,29 @@ T *upload_table(oi_engine *e, const std::vector<T> &v) {
     return d;
 }
 
-// Stage buffers in the stream layout, the plan tables and the token kernel's
-// arguments.
+// The compute waves' weight streams, the plan tables and the token kernel's
+// arguments.  Streams are built on the host for blocks of waves at a time
+// (each wave's stages in consumption order) and copied whole.
 int upload_stream(oi_engine *e, GgufFile &g, bool tied, const StreamPlanAll &sp) {
     const oi_config &c = e->cfg;
-    uint8_t *stages = e->arena.take(sp.stage_bytes);
-    if (!stages) return fail(OI_E_NOMEM, "arena exhausted (token kernel weights)");
-    std::vector<uint8_t> host;
-    auto put = [&](const PlanKind &pk, const uint8_t *const *src, size_t off) -> int {
-        host.resize((size_t)pk.kind.bytes);
-        repack_stream_kind(pk, src, sp.G, host.data());
-        HIP_TRY(hipMemcpyAsync(stages + off, host.data(), host.size(), hipMemcpyHostToDevice, e->stream));
-        HIP_TRY(hipStreamSynchronize(e->stream));
-        return OI_OK;
-    };
+    const int NW = sp.G * S_NCW;
+    uint8_t *wstream = e->arena.take(sp.wstride * (size_t)NW);
+    if (!wstream) return fail(OI_E_NOMEM, "arena exhausted (token kernel weights)");
     std::vector<SLayer> layers((size_t)c.n_layers);
-    int rc;
+    // sources and plan of every stage of a token, in stream order
+    std::vector<std::array<const uint8_t *, 3>> srcs;
+    std::vector<int> plan_of;
     for (int64_t l = 0; l < c.n_layers; l++) {
         const std::string p = "blk." + std::to_string(l) + ".";
         auto d = [&](const char *n) { return (const uint8_t *)g.tensor(p + n)->data; };
-        const uint8_t *qkv[3] = {d("attn_q.weight"), d("attn_k.weight"), d("attn_v.weight")};
-        const uint8_t *wo[1] = {d("attn_output.weight")};
-        const uint8_t *gu[2] = {d("ffn_gate.weight"), d("ffn_up.weight")};
-        const uint8_t *dn[1] = {d("ffn_down.weight")};
-        const uint8_t *const *srcs[4] = {qkv, wo, gu, dn};
+        srcs.push_back({d("attn_q.weight"), d("attn_k.weight"), d("attn_v.weight")});
+        srcs.push_back({d("attn_output.weight"), nullptr, nullptr});
+        srcs.push_back({d("ffn_gate.weight"), d("ffn_up.weight"), nullptr});
+        srcs.push_back({d("ffn_down.weight"), nullptr, nullptr});
         SLayer &L = layers[(size_t)l];
         for (int k = 0; k < 4; k++) {
-            const size_t off = sp.stage_off[(size_t)l * 4 + (size_t)k];
-            const int pi = sp.layer_plan[(size_t)l][(size_t)k];
-            if ((rc = put(sp.plans[(size_t)pi], srcs[k], off))) return rc;
-            L.w[k] = stages + off;
-            L.plan[k] = pi;
+            L.plan[k] = sp.layer_plan[(size_t)l][(size_t)k];
+            plan_of.push_back(L.plan[k]);
         }
         const LayerDev &LD = e->layers[(size_t)l];
         L.attn_norm = LD.attn_norm;
@@ -477,9 +474,24 @@ int upload_stream(oi_engine *e, GgufFile &g, bool tied, const StreamPlanAll &sp)
         L.kc = LD.kc;
         L.vc = LD.vc;
     }
+    srcs.push_back({(const uint8_t *)g.tensor(tied ? "token_embd.weight" : "output.weight")->data, nullptr, nullptr});
+    plan_of.push_back(sp.vocab_plan);
     {
-        const uint8_t *voc[1] = {(const uint8_t *)g.tensor(tied ? "token_embd.weight" : "output.weight")->data};
-        if ((rc = put(sp.plans[(size_t)sp.vocab_plan], voc, sp.stage_off.back()))) return rc;
+        const int WB = std::max(1, std::min(NW, (int)((size_t)1 << 30) / (int)std::max<size_t>(sp.wstride, 1)));
+        std::vector<uint8_t> host((size_t)WB * sp.wstride);
+        std::vector<uint8_t *> cur((size_t)WB);
+        for (int w0 = 0; w0 < NW; w0 += WB) {
+            const int w1 = std::min(NW, w0 + WB);
+            for (int w = w0; w < w1; w++) cur[(size_t)(w - w0)] = host.data() + (size_t)(w - w0) * sp.wstride;
+            for (size_t i = 0; i < plan_of.size(); i++) {
+                const PlanKind &pk = sp.plans[(size_t)plan_of[i]];
+                repack_stream_kind(pk, srcs[i].data(), w0, w1, cur.data());
+                for (int w = w0; w < w1; w++) cur[(size_t)(w - w0)] += (size_t)pk.waves[(size_t)w].npieces * 1024;
+            }
+            HIP_TRY(hipMemcpyAsync(wstream + (size_t)w0 * sp.wstride, host.data(), (size_t)(w1 - w0) * sp.wstride,
+                                   hipMemcpyHostToDevice, e->stream));
+            HIP_TRY(hipStreamSynchronize(e->stream));
+        }
     }
     std::vector<SKind> kinds;
     std::vector<SWave> waves;
@@ -508,7 +520,10 @@ int upload_stream(oi_engine *e, GgufFile &g, bool tied, const StreamPlanAll &sp)
     if (const char *ev = std::getenv("OI_STREAM_LAYERS"))  // debugging: run only the first layers
         A.n_layers = (int32_t)std::max<int64_t>(1, std::min<int64_t>(c.n_layers, std::atoll(ev)));
     A.G = sp.G;
-    A.vocab_w = stages + sp.stage_off.back();
+    A.wstream = wstream;
+    A.wstride = (int64_t)sp.wstride;
+    A.wpieces = upload_table(e, sp.wpieces);
+    if (!A.wpieces) return fail(OI_E_DEVICE, "token kernel tables upload failed");
     A.vocab_plan = sp.vocab_plan;
     A.output_norm = e->output_norm;
     A.emb = e->tok_embd;
@@ -726,7 +741,7 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     auto qv = [](int64_t K) { return ((size_t)qvec_bytes(K) + 2047) & ~(size_t)1023; };
     if (e->use_stream) {
         const size_t np = sp.plans.size(), NW = (size_t)sp.G * S_NCW;
-        stream_extra = sp.stage_bytes + np * (sizeof(SKind) + 256) + np * NW * sizeof(SWave) +
+        stream_extra = sp.wstride * NW + NW * 4 + 256 + np * (sizeof(SKind) + 256) + np * NW * sizeof(SWave) +
                        np * (size_t)sp.G * sizeof(SWgRows) + (size_t)c.n_layers * sizeof(SLayer) + qv(c.dim) +
                        qv(QDs) + qv(c.hidden_dim) + (size_t)sp.G * 8 + S_NC * 256 + 16 * 256;
     }
@@ -747,7 +762,7 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     probe.seg[0].m.cols = (int32_t)D;
     plan_gemv(probe);
     size_t act = al(D * 4) + al(QD * 4) + 2 * al(KVD * 4) + al(QD * 4) + al(H * 4) + al(out_rows * 4) +
-                 al((size_t)c.n_heads * e->max_splits * (c.head_dim + 2) * 4) + 2 * al((size_t)probe.total_wgs * 4) +
+                 al((size_t)c.n_heads * e->max_splits * (c.head_dim + 4) * 4) + 2 * al((size_t)probe.total_wgs * 4) +
                  2 * al((size_t)std::max(probe.total_wgs, sp.G) * 4) + al(ST_SWORDS * 4) +
                  al((size_t)(c.seq_len + 1) * 4) +
                  al((size_t)c.seq_len * (c.head_dim / 2) * 8);
@@ -798,7 +813,7 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     e->att = (float *)e->arena.take(QD * 4);
     e->hb = (float *)e->arena.take(H * 4);
     e->logits = (float *)e->arena.take(out_rows * 4);
-    e->part = (float *)e->arena.take((size_t)c.n_heads * e->max_splits * (c.head_dim + 2) * 4);
+    e->part = (float *)e->arena.take((size_t)c.n_heads * e->max_splits * (c.head_dim + 4) * 4);
     e->am_val = (float *)e->arena.take((size_t)std::max(probe.total_wgs, sp.G) * 4);
     e->am_idx = (int32_t *)e->arena.take((size_t)std::max(probe.total_wgs, sp.G) * 4);
     e->state = (int32_t *)e->arena.take(ST_SWORDS * 4);
@@ -1153,7 +1168,7 @@ int64_t oi_engine_debug_buffer(oi_engine *e, int32_t which, void *dst, int64_t b
     case OI_BUF_Q: src = e->q, n = QD * 4; break;
     case OI_BUF_K: src = e->k, n = KVD * 4; break;
     case OI_BUF_V: src = e->v, n = KVD * 4; break;
-    case OI_BUF_PART: src = e->part, n = c.n_heads * (int64_t)e->max_splits * (c.head_dim + 2) * 4; break;
+    case OI_BUF_PART: src = e->part, n = c.n_heads * (int64_t)e->max_splits * (c.head_dim + 4) * 4; break;
     case OI_BUF_LOGITS: src = e->logits, n = c.vocab_size * 4; break;
     case OI_BUF_STATE: src = e->state, n = ST_SWORDS * 4; break;
     case OI_BUF_AMVAL: src = e->am_val, n = (int64_t)std::max(e->sa.G, 1) * 4; break;

@@ -4,19 +4,25 @@
 // One launch computes one token: embedding, every layer, logits and the
 // greedy-argmax partials (reference: infer/forward.odin:17-146 and
 // sampler/sampler.odin:79-89).  The grid is one workgroup per CU, all
-// resident at once (cooperative launch).  A workgroup has S_NCW compute waves
-// and one I/O wave:
-//   * compute waves stream their share of every weight matrix of the token,
-//     in consumption order, through a per-wave LDS ring with direct-to-LDS
-//     loads (global_load_lds_dwordx4, 1 KB per wave instruction), and issue
-//     no other global memory traffic except the attention K/V tile loads;
+// resident at once (cooperative launch).  A workgroup has S_NCW compute
+// waves, S_NLD loader waves and one I/O wave:
+//   * every compute wave has its share of every weight matrix of the token
+//     laid out contiguously in consumption order (its stream); the loader
+//     waves copy the streams into per-compute-wave LDS rings with 16-byte
+//     register loads (many in flight) and publish fill counters in LDS, so
+//     the compute waves read weights from LDS only and the loads run ahead
+//     of the computation across stage barriers;
+//   * compute waves issue no global memory traffic except the attention
+//     K/V tile loads;
 //   * the I/O wave does the coherent traffic: it loads each stage's input
 //     vector (written by other workgroups in this launch) with device-scope
 //     loads, stores the workgroup's outputs with device-scope stores, and
 //     takes part in the grid barrier between stages (device-scope atomic
 //     counters, no cache flushes).
 // Weight loads run ahead of the computation by up to the ring size, across
-// barriers, so HBM keeps streaming while a stage waits for its input.
+// barriers, so HBM keeps streaming while a stage waits for its input.  (On
+// gfx950, direct-to-LDS loads measured at most ~3.7 TB/s with 8 issuing
+// waves per CU, 16-byte register loads ~7 TB/s: hence loader waves.)
 #pragma once
 #include <stdint.h>
 
@@ -25,9 +31,11 @@
 namespace oi {
 
 constexpr int S_NCW = 8;                   // compute waves per workgroup
-constexpr int S_THREADS = 64 * (S_NCW + 1);
+constexpr int S_NLD = 2;                   // loader waves per workgroup (fill the compute waves' rings)
+constexpr int S_THREADS = 64 * (S_NCW + S_NLD + 1);  // + the I/O wave
 constexpr int S_RING = 13;                 // ring pieces (1 KB) per compute wave
 constexpr int S_RING_BYTES = S_RING * 1024;
+constexpr int S_CP = 2;                    // pieces per loader request (chunk)
 constexpr int S_NC = 32;                   // barrier counters (each in its own 256-byte line)
 constexpr int S_MAXRUN = 4;                // row runs per compute wave per stage
 
@@ -58,8 +66,8 @@ struct SKind {
     int32_t K;       // row length
     int32_t lpr;     // lanes per row (power of two <= 64 dividing K/64)
     int32_t pair;    // 1: SwiGLU pairs (gate, up); a virtual row is one pair
-    int64_t region;  // bytes between the stream regions of consecutive compute waves
-    int64_t bytes;   // bytes of one layer's stage buffer
+    int64_t region;  // most bytes of one compute wave's stream in this stage (whole pieces)
+    int64_t pad2;
     SSeg seg[3];
 };
 
@@ -73,7 +81,7 @@ struct SRun {
 // Work of one compute wave in one stage kind.
 struct SWave {
     int32_t nruns;
-    int32_t npieces;  // 1 KB pieces of the wave's stream region
+    int32_t npieces;  // 1 KB pieces of the wave's stream in this stage
     int32_t pad[2];
     SRun run[S_MAXRUN];
 };
@@ -84,24 +92,25 @@ struct SWgRows {
 };
 
 struct SLayer {
-    const uint8_t *w[4];   // stage buffers QKV, WO, GU, DOWN (region of compute wave 0)
     int32_t plan[4];       // plan index (kinds / waves / wgrows) of each stage
     const float *attn_norm, *ffn_norm, *q_norm, *k_norm;
     uint16_t *kc, *vc;     // [n_kv_heads][seq_len][head_dim] f16
 };
 
-// Quantized activation vector (the inter-stage format), the LDS image of
-// gemv_q_kernel's x: per 16 elements (chunk C) a 22-bit integer
-// q = 2^14 hi + 2^7 mid + lo per element (hi int8, mid/lo 0..127) in three
-// byte planes at chunk slot cslot(C), a float scale xs[C] and the float sum
-// s16[C] of the values.  K * 3.5 bytes.
-constexpr int64_t qvec_bytes(int64_t K) { return K / 16 * 56; }
+// Quantized activation vector (the inter-stage format), the LDS image the
+// GEMV reads: per 16 elements (chunk C) a 16-bit integer q = 256 hi + lo per
+// element (hi int8, lo 0..255) in two byte planes at chunk slot cslot(C), a
+// float scale xs[C] (value = q * xs) and the float sum s16[C] of the values.
+// 2.5 bytes per element.
+constexpr int64_t qvec_bytes(int64_t K) { return K / 16 * 40; }
 
 struct StreamArgs {
     const SLayer *layers;
     int32_t n_layers;
     int32_t G;                 // workgroups (= CUs)
-    const uint8_t *vocab_w;    // VOCAB stage buffer
+    const uint8_t *wstream;    // weight streams: compute wave w's at wstream + w * wstride
+    int64_t wstride;
+    const int32_t *wpieces;    // [G * S_NCW] 1 KB pieces of each compute wave's stream
     int32_t vocab_plan;
     const float *output_norm;
     DMat emb;                  // token embedding (GEMV plane layout)
@@ -113,7 +122,7 @@ struct StreamArgs {
     float eps;
     const float2 *rope_cs;     // [seq_len][HD/2]
     float *q, *k, *v;          // raw projections of this token
-    float *part;               // [n_heads][max_chunks][HD + 2] attention partials
+    float *part;               // [n_heads][max_chunks][HD + 4] attention partials (o, m, l, pad)
     int32_t max_chunks;
     uint8_t *xq, *attq, *hbq;  // quantized vectors (qvec_bytes(D), (QD), (H))
     float *ssq;                // [G] partial sums of squares of the residual stream

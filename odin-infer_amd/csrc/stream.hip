@@ -35,8 +35,8 @@
 
 namespace oi {
 
-constexpr float XQ_MAX_S = 2097151.0f;  // 2^21 - 1
-constexpr int NTOT_IO = S_NCW;          // index of the I/O wave
+constexpr float XQ_MAX_S = 32767.0f;  // 2^15 - 1: 16-bit activations
+constexpr int NTOT_IO = S_NCW + S_NLD;  // index of the I/O wave
 constexpr uint64_t SPIN_TICKS = 200000000ull;  // 2 s of the 100 MHz real-time clock
 
 #define LDS_PTR(p) ((__attribute__((address_space(3))) void *)(p))
@@ -64,29 +64,25 @@ static __device__ __forceinline__ uint64_t ld_u64(const uint64_t *p) {
 }
 static __device__ __forceinline__ void vm_wait_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// wait until at most n vector memory operations of this wave are in flight
-// (they complete in issue order); n is at most S_RING
-static __device__ __forceinline__ void vm_wait_n(uint32_t n) {
-    switch (n) {
-    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
-    case 1: asm volatile("s_waitcnt vmcnt(1)" ::: "memory"); break;
-    case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
-    case 3: asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); break;
-    case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
-    case 5: asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
-    case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
-    case 7: asm volatile("s_waitcnt vmcnt(7)" ::: "memory"); break;
-    case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
-    case 9: asm volatile("s_waitcnt vmcnt(9)" ::: "memory"); break;
-    case 10: asm volatile("s_waitcnt vmcnt(10)" ::: "memory"); break;
-    case 11: asm volatile("s_waitcnt vmcnt(11)" ::: "memory"); break;
-    case 12: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
-    default: asm volatile("s_waitcnt vmcnt(13)" ::: "memory"); break;
-    }
-}
-static_assert(S_RING == 13, "vm_wait_n covers counts up to S_RING");
-
 static __device__ __forceinline__ uint32_t uni(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// Barrier of the compute waves and the I/O wave (the loader waves never
+// wait for them, so s_barrier cannot be used): a counter in LDS.  Each
+// wave's LDS writes are complete before it arrives (lgkmcnt(0)); LDS
+// accesses are performed in order, so a wave that sees the count sees them.
+static __device__ __forceinline__ void lds_bar(uint32_t *ctr, uint32_t &target) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    target += S_NCW + 1;
+    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) __builtin_amdgcn_s_sleep(1);
+    asm volatile("" ::: "memory");
+}
+static __device__ __forceinline__ uint32_t lds_ld(const uint32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+static __device__ __forceinline__ void lds_st(uint32_t *p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
 
 // Read-only plan tables through the constant address space: with a uniform
 // index these become scalar loads, which do not touch vmcnt (a vector load
@@ -106,7 +102,10 @@ constexpr int TR_SLOTS = 8;
     } while (0)
 
 // ------------------------------------------------------------ LDS layout --
-struct Misc {
+struct __attribute__((aligned(16))) Misc {
+    uint32_t filled[S_NCW];    // pieces of each compute wave's stream written into its ring
+    uint32_t consumed[S_NCW];  // stream bytes each compute wave has consumed
+    uint32_t bar;              // barrier counter of the compute and I/O waves
     float s_norm;            // RMSNorm scale of the current stage's input
     int32_t abort;
     int32_t token, pos;
@@ -115,7 +114,7 @@ struct Misc {
     int32_t redi[16];
     float xres[256];         // this workgroup's rows of the residual stream x
     float yo_pad[4];
-    uint8_t qstage[16 * 48]; // producer quantization staging (16 chunks)
+    uint8_t qstage[16 * 32]; // producer quantization staging (16 chunks)
 };
 
 struct Lds {
@@ -128,57 +127,44 @@ struct Lds {
 static __device__ __forceinline__ int cslot(int C) { return (C & ~3) | ((C & 3) ^ ((C >> 4) & 3)); }
 
 // ----------------------------------------------------- weight stream ring --
+// Compute wave's view of its ring: piece p of its stream (1 KB) sits at
+// ring slot p % S_RING once filled >= p + 1; the wave publishes the stream
+// bytes it has consumed so the loader can reuse their slots.
 struct Ring {
-    uint32_t issued;     // pieces issued this launch
     uint32_t consumed;   // stream bytes consumed
-    int32_t seg;         // segment (layer x stage kind) of the next piece
-    int32_t seg_piece, seg_n;
-    const uint8_t *seg_addr;
-    uint8_t *lds;        // this wave's ring
+    uint8_t *lds;        // the compute wave's ring
+    const uint32_t *filled;
+    uint32_t *consumed_p;
+    uint32_t *abort_p;   // the workgroup's abort flag (LDS)
+    int32_t *err_p;      // the launch's error word (state)
 };
 
-// segment i: layer i/4, stage kind i%4 (QKV, WO, GU, DOWN); i == 4L: VOCAB
-static __device__ __forceinline__ void seg_open(const StreamArgs &a, int cw, Ring &r) {
-    const int nseg = 4 * a.n_layers + 1;
-    int seg = (int)uni((uint32_t)r.seg);
-    while (seg < nseg) {
-        const bool voc = seg == 4 * a.n_layers;
-        const int pl = (int)uni(voc ? a.vocab_plan : CST(a.layers)[seg >> 2].plan[seg & 3]);
-        const uint8_t *base = voc ? a.vocab_w : CST(a.layers)[seg >> 2].w[seg & 3];
-        r.seg_addr = base + (size_t)cw * CST(a.kinds)[pl].region;
-        r.seg_n = (int)uni((uint32_t)CST(a.waves)[(size_t)pl * a.G * S_NCW + cw].npieces);
-        r.seg_piece = 0;
-        if (r.seg_n > 0) break;
-        seg++;
-    }
-    r.seg = seg;
-    if (seg >= nseg) r.seg_n = 0;
-}
-
-static __device__ __forceinline__ void ring_topup(const StreamArgs &a, int cw, Ring &r) {
-    const int lane = threadIdx.x & 63;
-    const int nseg = 4 * a.n_layers + 1;
-    uint32_t issued = uni(r.issued);
-    const uint32_t limit = uni(r.consumed) / 1024 + S_RING;
-    while (r.seg < nseg && issued < limit) {
-        const uint8_t *src = r.seg_addr + (size_t)r.seg_piece * 1024 + lane * 16;
-        __builtin_amdgcn_global_load_lds((const void *)src, LDS_PTR(r.lds + (issued % S_RING) * 1024), 16, 0,
-                                         2 /* nontemporal */);
-        issued++;
-        if (++r.seg_piece == r.seg_n) {
-            r.seg++;
-            seg_open(a, cw, r);
+// compute wave: bytes [.., end) of its stream are in its ring once this returns
+// (on an abort, or after SPIN_TICKS without progress, which aborts the
+// launch: the stage then completes on stale ring data and the host reports
+// the error)
+static __device__ __forceinline__ void ring_wait(const Ring &r, uint32_t end) {
+    const uint32_t need = uni((end + 1023) / 1024);
+    if (lds_ld(r.filled) < need) {
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        while (lds_ld(r.filled) < need && !lds_ld(r.abort_p)) {
+            if (__builtin_amdgcn_s_memrealtime() - t0 > SPIN_TICKS) {
+                if ((threadIdx.x & 63) == 0) {
+                    lds_st(r.abort_p, 1u);
+                    __hip_atomic_store(r.err_p, (int32_t)S_ERR_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
         }
     }
-    r.issued = issued;
+    asm volatile("" ::: "memory");
 }
-
-// bytes [.., end) of the stream are in LDS once this returns
-static __device__ __forceinline__ void ring_wait(const StreamArgs &a, int cw, Ring &r, uint32_t end) {
-    const uint32_t need = uni((end + 1023) / 1024);
-    ring_topup(a, cw, r);
-    const uint32_t issued = uni(r.issued);
-    vm_wait_n(issued > need ? issued - need : 0);
+// compute wave: stream bytes before `off` are consumed (their ring slots may be refilled)
+static __device__ __forceinline__ void ring_release(Ring &r, uint32_t off) {
+    asm volatile("" ::: "memory");  // the ring reads are issued first (LDS performs a wave's accesses in order)
+    r.consumed = off;
+    if ((threadIdx.x & 63) == 0) lds_st(r.consumed_p, off);
 }
 
 // 16-byte read at stream offset `base + off` (off < S_RING_BYTES)
@@ -192,23 +178,31 @@ static __device__ __forceinline__ const uint8_t *rp(const Ring &r, uint32_t bmod
 static __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
-static __device__ __forceinline__ float psum(int h, int m, int l) {
-    return (float)((h << 14) + (m << 7) + l);
+static __device__ __forceinline__ uint32_t udot4(uint32_t a, uint32_t b, uint32_t c) {
+    return __builtin_amdgcn_udot4(a, b, c, false);
 }
+// first product of a chain: the three-operand form with an inline zero
+// (the compiler would otherwise zero a register for the accumulate form)
+static __device__ __forceinline__ int sdot4z(uint32_t a, uint32_t b) {
+    int d;
+    asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(d) : "v"(a), "v"(b));
+    return d;
+}
+// sum of w * q over a chunk part from the hi (signed) and lo (unsigned) planes
+static __device__ __forceinline__ float psum(int h, uint32_t l) { return (float)((h << 8) + (int)l); }
 
 // x slice of one lane: 4 chunks of 16 elements
 struct XS {
-    u32x4 h[4], m[4], l[4];
+    u32x4 h[4], l[4];
     float xs[4], s[4];
 };
 static __device__ __forceinline__ void x_load(const uint8_t *xr, int K, const int (&C)[4], XS &x) {
     const int nch = K / 16;
-    const u32x4 *hi = (const u32x4 *)xr, *mid = hi + nch, *lo = mid + nch;
+    const u32x4 *hi = (const u32x4 *)xr, *lo = hi + nch;
     const float *xs = (const float *)(lo + nch), *s16 = xs + nch;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
         x.h[c] = hi[cslot(C[c])];
-        x.m[c] = mid[cslot(C[c])];
         x.l[c] = lo[cslot(C[c])];
         x.xs[c] = xs[C[c]];
         x.s[c] = s16[C[c]];
@@ -225,51 +219,65 @@ static __device__ __forceinline__ void unit_chunks(int u, int (&C)[4]) {
 
 // Q4_K: lane's unit = group pair p = l & 3 of super-block; chunks 0,1 low
 // nibbles (group 2p), 2,3 high nibbles (group 2p+1)
-static __device__ __forceinline__ float dot_q4k(const Ring &r, uint32_t bm, int lane, const XS &x) {
-    const u32x4 q0 = *(const u32x4 *)rp(r, bm, 16 * lane);
-    const u32x4 q1 = *(const u32x4 *)rp(r, bm, 1024 + 16 * lane);
-    const u32x4 hd = *(const u32x4 *)rp(r, bm, 2048 + 16 * (lane >> 2));
+template <class RD>
+static __device__ __forceinline__ float dot_q4k(const RD &rp, int lane, const XS &x) {
+    const u32x4 q0 = *(const u32x4 *)rp(16 * lane);
+    const u32x4 q1 = *(const u32x4 *)rp(1024 + 16 * lane);
+    const u32x4 hd = *(const u32x4 *)rp(2048 + 16 * (lane >> 2));
     const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-    int ah[4] = {0, 0, 0, 0}, am[4] = {0, 0, 0, 0}, al[4] = {0, 0, 0, 0};
+    int ah[4];
+    uint32_t al[4];
 #pragma unroll
     for (int k = 0; k < 8; k++) {
         const uint32_t lo = qw[k] & 0x0F0F0F0Fu, hi = (qw[k] >> 4) & 0x0F0F0F0Fu;
         const int c0 = k >> 2, c1 = 2 + (k >> 2), e = k & 3;
-        ah[c0] = sdot4(lo, x.h[c0][e], ah[c0]);
-        am[c0] = sdot4(lo, x.m[c0][e], am[c0]);
-        al[c0] = sdot4(lo, x.l[c0][e], al[c0]);
-        ah[c1] = sdot4(hi, x.h[c1][e], ah[c1]);
-        am[c1] = sdot4(hi, x.m[c1][e], am[c1]);
-        al[c1] = sdot4(hi, x.l[c1][e], al[c1]);
+        if (e == 0) {
+            ah[c0] = sdot4z(lo, x.h[c0][e]);
+            ah[c1] = sdot4z(hi, x.h[c1][e]);
+            al[c0] = udot4(lo, x.l[c0][e], 0u);
+            al[c1] = udot4(hi, x.l[c1][e], 0u);
+        } else {
+            ah[c0] = sdot4(lo, x.h[c0][e], ah[c0]);
+            ah[c1] = sdot4(hi, x.h[c1][e], ah[c1]);
+            al[c0] = udot4(lo, x.l[c0][e], al[c0]);
+            al[c1] = udot4(hi, x.l[c1][e], al[c1]);
+        }
     }
     const float d = h2f(hd.x & 0xFFFFu), dmin = h2f(hd.x >> 16);
     uint32_t sc0, m0, sc1, m1;
     q4k_scales(lane & 3, hd.y, hd.z, hd.w, sc0, m0, sc1, m1);
-    const float dA = psum(ah[0], am[0], al[0]) * x.xs[0] + psum(ah[1], am[1], al[1]) * x.xs[1];
-    const float dB = psum(ah[2], am[2], al[2]) * x.xs[2] + psum(ah[3], am[3], al[3]) * x.xs[3];
+    const float dA = psum(ah[0], al[0]) * x.xs[0] + psum(ah[1], al[1]) * x.xs[1];
+    const float dB = psum(ah[2], al[2]) * x.xs[2] + psum(ah[3], al[3]) * x.xs[3];
     return d * ((float)sc0 * dA + (float)sc1 * dB) - dmin * ((float)m0 * (x.s[0] + x.s[1]) + (float)m1 * (x.s[2] + x.s[3]));
 }
 
-static __device__ __forceinline__ float dot_q6k(const Ring &r, uint32_t bm, int lane, const XS &x) {
-    const u32x4 a0 = *(const u32x4 *)rp(r, bm, 16 * lane);
-    const u32x4 a1 = *(const u32x4 *)rp(r, bm, 1024 + 16 * lane);
-    const u32x4 qv = *(const u32x4 *)rp(r, bm, 2048 + 16 * lane);
-    const u32x2 scw = *(const u32x2 *)rp(r, bm, 3072 + 16 * (lane >> 2) + 8 * ((lane >> 1) & 1));
-    const uint32_t dd = *(const uint16_t *)rp(r, bm, 3328 + 2 * (lane >> 2));
+template <class RD>
+static __device__ __forceinline__ float dot_q6k(const RD &rp, int lane, const XS &x) {
+    const u32x4 a0 = *(const u32x4 *)rp(16 * lane);
+    const u32x4 a1 = *(const u32x4 *)rp(1024 + 16 * lane);
+    const u32x4 qv = *(const u32x4 *)rp(2048 + 16 * lane);
+    const u32x2 scw = *(const u32x2 *)rp(3072 + 16 * (lane >> 2) + 8 * ((lane >> 1) & 1));
+    const uint32_t dd = *(const uint16_t *)rp(3328 + 2 * (lane >> 2));
     const uint32_t l0[4] = {a0.x, a0.y, a0.z, a0.w}, l1[4] = {a1.x, a1.y, a1.z, a1.w};
     const uint32_t qh[4] = {qv.x, qv.y, qv.z, qv.w};
-    int ah[4] = {0, 0, 0, 0}, am[4] = {0, 0, 0, 0}, al[4] = {0, 0, 0, 0};
+    int ah[4];
+    uint32_t al[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
+        // 6-bit values v = q + 32 (0..63) of the four 16-element runs, 4 per word
         const uint32_t v[4] = {(l0[i] & 0x0F0F0F0Fu) | ((qh[i] & 0x03030303u) << 4),
                                (l1[i] & 0x0F0F0F0Fu) | (((qh[i] >> 2) & 0x03030303u) << 4),
                                ((l0[i] >> 4) & 0x0F0F0F0Fu) | (((qh[i] >> 4) & 0x03030303u) << 4),
                                ((l1[i] >> 4) & 0x0F0F0F0Fu) | (((qh[i] >> 6) & 0x03030303u) << 4)};
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            ah[k] = sdot4(v[k], x.h[k][i], ah[k]);
-            am[k] = sdot4(v[k], x.m[k][i], am[k]);
-            al[k] = sdot4(v[k], x.l[k][i], al[k]);
+            if (i == 0) {
+                ah[k] = sdot4z(v[k], x.h[k][i]);
+                al[k] = udot4(v[k], x.l[k][i], 0u);
+            } else {
+                ah[k] = sdot4(v[k], x.h[k][i], ah[k]);
+                al[k] = udot4(v[k], x.l[k][i], al[k]);
+            }
         }
     }
     const uint32_t sw[2] = {scw.x, scw.y};
@@ -279,34 +287,63 @@ static __device__ __forceinline__ float dot_q6k(const Ring &r, uint32_t bm, int 
     for (int k = 0; k < 4; k++) {
         const int bi = bsh + 2 * k;
         const float s = (float)(int8_t)((sw[bi >> 2] >> ((bi & 3) * 8)) & 0xFFu);
-        acc += s * (psum(ah[k], am[k], al[k]) * x.xs[k] - 32.f * x.s[k]);
+        acc += s * (psum(ah[k], al[k]) * x.xs[k] - 32.f * x.s[k]);
     }
     return h2f(dd) * acc;
 }
 
-static __device__ __forceinline__ float dot_q80(const Ring &r, uint32_t bm, int lane, const XS &x) {
-    int ah[4] = {0, 0, 0, 0}, am[4] = {0, 0, 0, 0}, al[4] = {0, 0, 0, 0};
+// Q8_0: signed weights against the unsigned lo plane as (w + 128) . lo - 128 sum(lo)
+template <class RD>
+static __device__ __forceinline__ float dot_q80(const RD &rp, int lane, const XS &x) {
+    int ah[4];
+    uint32_t al[4], ls[4];
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-        const u32x4 w = *(const u32x4 *)rp(r, bm, 1024 * c + 16 * lane);
+        const u32x4 w = *(const u32x4 *)rp(1024 * c + 16 * lane);
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            ah[c] = sdot4(w[e], x.h[c][e], ah[c]);
-            am[c] = sdot4(w[e], x.m[c][e], am[c]);
-            al[c] = sdot4(w[e], x.l[c][e], al[c]);
+            const uint32_t wu = w[e] ^ 0x80808080u;
+            if (e == 0) {
+                ah[c] = sdot4z(w[e], x.h[c][e]);
+                al[c] = udot4(wu, x.l[c][e], 0u);
+                ls[c] = udot4(0x01010101u, x.l[c][e], 0u);
+            } else {
+                ah[c] = sdot4(w[e], x.h[c][e], ah[c]);
+                al[c] = udot4(wu, x.l[c][e], al[c]);
+                ls[c] = udot4(0x01010101u, x.l[c][e], ls[c]);
+            }
         }
     }
-    const uint32_t dw = *(const uint32_t *)rp(r, bm, 4096 + 4 * lane);
-    return h2f(dw & 0xFFFFu) * (psum(ah[0], am[0], al[0]) * x.xs[0] + psum(ah[1], am[1], al[1]) * x.xs[1]) +
-           h2f(dw >> 16) * (psum(ah[2], am[2], al[2]) * x.xs[2] + psum(ah[3], am[3], al[3]) * x.xs[3]);
+    const uint32_t dw = *(const uint32_t *)rp(4096 + 4 * lane);
+    float p[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) p[c] = (float)((ah[c] << 8) + (int)al[c] - 128 * (int)ls[c]);
+    return h2f(dw & 0xFFFFu) * (p[0] * x.xs[0] + p[1] * x.xs[1]) + h2f(dw >> 16) * (p[2] * x.xs[2] + p[3] * x.xs[3]);
 }
 
-template <int T>
-static __device__ __forceinline__ float dot_t(const Ring &r, uint32_t bm, int lane, const XS &x) {
-    if (T == T_Q4_K) return dot_q4k(r, bm, lane, x);
-    if (T == T_Q6_K) return dot_q6k(r, bm, lane, x);
-    return dot_q80(r, bm, lane, x);
+template <int T, class RD>
+static __device__ __forceinline__ float dot_t(const RD &rp, int lane, const XS &x) {
+    if (T == T_Q4_K) return dot_q4k(rp, lane, x);
+    if (T == T_Q6_K) return dot_q6k(rp, lane, x);
+    return dot_q80(rp, lane, x);
 }
+
+// Reads of a step at ring offset bm: contiguous when the step does not
+// cross the ring end (one address add, then immediate offsets), wrapped
+// per read otherwise.
+struct RdLin {
+    const uint8_t *p;
+    __device__ __forceinline__ const uint8_t *operator()(uint32_t off) const { return p + off; }
+};
+struct RdWrap {
+    const uint8_t *lds;
+    uint32_t bm;
+    __device__ __forceinline__ const uint8_t *operator()(uint32_t off) const {
+        uint32_t o = bm + off;
+        if (o >= (uint32_t)S_RING_BYTES) o -= S_RING_BYTES;
+        return lds + o;
+    }
+};
 
 // One run of rows [row0, row0+nrows) of one segment: steps of NR = 64/lpr
 // rows x lpr units; `soff` is the stream offset of the run's first step.
@@ -315,10 +352,12 @@ template <int T, bool PAIR>
 static __device__ void gemv_run(const StreamArgs &a, int cw, Ring &r, uint32_t &soff, const SKind &kd, const SRun &run,
                                 const uint8_t *xr, float *yo, int v0, float scale, int tst) {
     const int lane = threadIdx.x & 63;
-    const int lpr = kd.lpr, K = kd.K, nb = (K >> 6) / lpr, NR = 64 / lpr;
+    const int lpr = (int)uni((uint32_t)kd.lpr), K = (int)uni((uint32_t)kd.K);
+    const int nb = (K >> 6) / lpr, NR = 64 / lpr;
     const int j = lane & (lpr - 1), rsub = lane / lpr;
-    constexpr uint32_t SB = (uint32_t)step_bytes(T) * (PAIR ? 2 : 1);
-    const int nrs = (run.nrows + NR - 1) / NR;
+    constexpr uint32_t SB1 = (uint32_t)step_bytes(T), SB = SB1 * (PAIR ? 2 : 1);
+    const int nrows = (int)uni((uint32_t)run.nrows);
+    const int nrs = (nrows + NR - 1) / NR;
     XS x;
     int C[4];
     if (nb == 1) {
@@ -333,22 +372,27 @@ static __device__ void gemv_run(const StreamArgs &a, int cw, Ring &r, uint32_t &
                 unit_chunks<T>(b * lpr + j, C);
                 x_load(xr, K, C, x);
             }
-            ring_wait(a, cw, r, soff + SB);
-            if (tst >= 0 && rs == 0 && b == 0 && cw % S_NCW == 0) TRACE(a, tst, 3);
+            ring_wait(r, soff + SB);
             const uint32_t bm = uni(soff % (uint32_t)S_RING_BYTES);
-            acc0 += dot_t<T>(r, bm, lane, x);
-            if (PAIR) {
-                uint32_t bm1 = bm + (uint32_t)step_bytes(T);
-                if (bm1 >= (uint32_t)S_RING_BYTES) bm1 -= S_RING_BYTES;
-                acc1 += dot_t<T>(r, bm1, lane, x);
+            if (bm + SB <= (uint32_t)S_RING_BYTES) {
+                const RdLin rd{r.lds + bm};
+                acc0 += dot_t<T>(rd, lane, x);
+                if (PAIR) acc1 += dot_t<T>(RdLin{r.lds + bm + SB1}, lane, x);
+            } else {
+                acc0 += dot_t<T>(RdWrap{r.lds, bm}, lane, x);
+                if (PAIR) {
+                    uint32_t bm1 = bm + SB1;
+                    if (bm1 >= (uint32_t)S_RING_BYTES) bm1 -= S_RING_BYTES;
+                    acc1 += dot_t<T>(RdWrap{r.lds, bm1}, lane, x);
+                }
             }
             soff += SB;
-            r.consumed = soff;
+            ring_release(r, soff);  // per step: a row step of nb steps may exceed the ring
         }
         acc0 = lane_group_sum(acc0, lpr);
         if (PAIR) acc1 = lane_group_sum(acc1, lpr);
         const int rr = rs * NR + rsub;
-        if (j == 0 && rr < run.nrows) {
+        if (j == 0 && rr < nrows) {
             float v = acc0 * scale;
             if (PAIR) {  // infer/forward.odin:128-133
 #pragma clang fp contract(off)
@@ -357,7 +401,6 @@ static __device__ void gemv_run(const StreamArgs &a, int cw, Ring &r, uint32_t &
             }
             yo[run.vrow + rr - v0] = v;
         }
-        ring_topup(a, cw, r);
     }
 }
 
@@ -374,6 +417,7 @@ static __device__ void gemv_stage(const StreamArgs &a, int cw, Ring &r, uint32_t
     for (int i = 0; i < nruns; i++) {
         const SRun run = wv->run[i];
         const int type = kd.seg[run.seg].type;
+        if (i == 0 && cw % S_NCW == 0 && type >= 0) TRACE(a, tst, 3);
         if (kd.pair) {
             if (type == T_Q4_K) gemv_run<T_Q4_K, true>(a, cw, r, soff, kd, run, xr, yo, v0, scale, i == 0 ? tst : -1);
             else if (type == T_Q6_K) gemv_run<T_Q6_K, true>(a, cw, r, soff, kd, run, xr, yo, v0, scale, i == 0 ? tst : -1);
@@ -387,7 +431,7 @@ static __device__ void gemv_stage(const StreamArgs &a, int cw, Ring &r, uint32_t
         }
     }
     soff = start + (uint32_t)npieces * 1024u;
-    r.consumed = soff;
+    ring_release(r, soff);
 }
 
 // Grid barrier over cumulative counters: workgroup w adds 1 to counter
@@ -421,8 +465,18 @@ static __device__ bool grid_wait(const StreamArgs &a, uint64_t seq, int nb, int 
 static __device__ __forceinline__ void io_dma(const uint8_t *src, uint8_t *dst, int bytes) {
     const int lane = threadIdx.x & 63;
     for (int off = 0; off < bytes; off += 1024)
-        __builtin_amdgcn_global_load_lds((const void *)(src + off + lane * 16), LDS_PTR(dst + off), 16, 0,
-                                         16 /* sc1 */);
+        if (off + lane * 16 < bytes)
+            __builtin_amdgcn_global_load_lds((const void *)(src + off + lane * 16), LDS_PTR(dst + off), 16, 0,
+                                             16 /* sc1 */);
+}
+
+// 512 bytes (lanes 0..31); aux 16: device-scope (written in this launch), 0: read-only data
+static __device__ __forceinline__ void io_dma_half(const uint8_t *src, uint8_t *dst, int aux) {
+    const int lane = threadIdx.x & 63;
+    if (lane < 32) {
+        if (aux) __builtin_amdgcn_global_load_lds((const void *)(src + lane * 16), LDS_PTR(dst), 16, 0, 16);
+        else __builtin_amdgcn_global_load_lds((const void *)(src + lane * 16), LDS_PTR(dst), 16, 0, 0);
+    }
 }
 
 // RMSNorm scale from the partial sums of squares (ops.odin:7-19 computes
@@ -463,21 +517,20 @@ static __device__ float io_quantize(const float *vals, const float *w, int n, in
         const float inv = amax > 0.f ? XQ_MAX_S / amax : 0.f;
         const int q = (int)rintf(v * inv);
         const int cc = lane >> 4, k = lane & 15;  // chunk of this pass, element within the chunk
-        stage[cc * 48 + k] = (uint8_t)((q >> 14) & 0xFF);
-        stage[cc * 48 + 16 + k] = (uint8_t)((q >> 7) & 0x7F);
-        stage[cc * 48 + 32 + k] = (uint8_t)(q & 0x7F);
+        stage[cc * 32 + k] = (uint8_t)((q >> 8) & 0xFF);
+        stage[cc * 32 + 16 + k] = (uint8_t)(q & 0xFF);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // one wave: LDS accesses complete in order
         const int nc = min(4, (n - b) / 16);
-        if (lane < nc * 12) {  // 12 words (3 planes x 16 bytes) per chunk
-            const int c2 = lane / 12, pl = (lane % 12) / 4, wd = lane & 3;
+        if (lane < nc * 8) {  // 8 words (2 planes x 16 bytes) per chunk
+            const int c2 = lane / 8, pl = (lane % 8) / 4, wd = lane & 3;
             const int C = (e0 + b) / 16 + c2;
-            const uint32_t word = *(const uint32_t *)(stage + c2 * 48 + pl * 16 + wd * 4);
+            const uint32_t word = *(const uint32_t *)(stage + c2 * 32 + pl * 16 + wd * 4);
             st_u((uint32_t *)(dst + (size_t)pl * nch * 16 + (size_t)cslot(C) * 16 + wd * 4), word);
         }
         if (ok && k == 0) {
             const int C = (e0 + i) / 16;
-            st_f((float *)(dst + (size_t)nch * 48) + C, amax / XQ_MAX_S);
-            st_f((float *)(dst + (size_t)nch * 52) + C, sum);
+            st_f((float *)(dst + (size_t)nch * 32) + C, amax / XQ_MAX_S);
+            st_f((float *)(dst + (size_t)nch * 36) + C, sum);
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
@@ -548,6 +601,7 @@ static __device__ float emb_elem(const DMat &m, int row, int col) {
 // Per half workgroup (4 compute waves), LDS scratch for head_dim 128, G <= 4.
 constexpr int AHD = 128;
 constexpr int AG = 4;
+constexpr int PST = AHD + 4;  // floats per attention partial: o[AHD], m, l, 2 pad (16-byte rows)
 struct __attribute__((aligned(16))) AttnLds {
     float qr[AG][AHD];      // raw q heads (I/O wave)
     float qT[AHD][AG];      // normalized + rotated q, [dim][head]
@@ -575,17 +629,22 @@ static __device__ __forceinline__ int attn_chunk_of(const StreamArgs &a, int h, 
 
 // K/V tile loads of chunk c for thread (wave w of the half, lane l):
 // K row t0 + l, dims [32w, 32w+32); V rows t0 + 16w + i, dims 2l, 2l+1
+#if defined(__HIP_DEVICE_COMPILE__)
+#define GLB(T, p) ((const __attribute__((address_space(1))) T *)(p))
+#else
+#define GLB(T, p) ((const T *)(p))
+#endif
 static __device__ __forceinline__ void attn_issue(const StreamArgs &a, const SLayer &L, int kvh, int c, int pos,
                                                   KVReg &kv) {
     const int w = (threadIdx.x >> 6) & 3, lane = threadIdx.x & 63;
     const int t0 = 64 * c, n = min(64, pos + 1 - t0);
     const uint16_t *kc = L.kc + (size_t)kvh * a.seq_len * AHD, *vc = L.vc + (size_t)kvh * a.seq_len * AHD;
-    const u32x4 *kr = (const u32x4 *)(kc + (size_t)(t0 + min(lane, n - 1)) * AHD + 32 * w);
+    const auto kr = GLB(u32x4, kc + (size_t)(t0 + min(lane, n - 1)) * AHD + 32 * w);
 #pragma unroll
-    for (int i = 0; i < 4; i++) kv.k[i] = ldg_nt(kr + i);
+    for (int i = 0; i < 4; i++) kv.k[i] = __builtin_nontemporal_load(kr + i);
 #pragma unroll
     for (int i = 0; i < 16; i++)
-        kv.v[i] = ldg_nt((const uint32_t *)(vc + (size_t)(t0 + min(16 * w + i, n - 1)) * AHD) + lane);
+        kv.v[i] = __builtin_nontemporal_load(GLB(uint32_t, vc + (size_t)(t0 + min(16 * w + i, n - 1)) * AHD) + lane);
 }
 
 // ------------------------------------------------------------------ kernel --
@@ -627,6 +686,7 @@ static __device__ void io_main(const StreamArgs &a, const Ctx &cx) {
     const uint64_t seq = cx.seq;
     const int nbt = cx.nb_total;
     int stage = 0;
+    uint32_t bt = 0;  // barrier target
     // wait for the barrier of the previous stage; false: abort the launch
     auto wait_prev = [&]() -> bool {
         if (grid_wait(a, seq, nbt, stage - 1)) {
@@ -703,9 +763,9 @@ static __device__ void io_main(const StreamArgs &a, const Ctx &cx) {
             }
         }
         TRACE(a, stage, 1);
-        __syncthreads();  // A
+        lds_bar(&ms.bar, bt);  // A
         if (ms.abort) return;
-        __syncthreads();  // B
+        lds_bar(&ms.bar, bt);  // B
         TRACE(a, stage, 5);
         {
             const SWgRows wr = a.wgrows[(size_t)L.plan[SK_QKV] * G + wg];
@@ -716,45 +776,47 @@ static __device__ void io_main(const StreamArgs &a, const Ctx &cx) {
                 else st_f(a.v + (v - a.QD - a.KVD), y);
             }
         }
+        lds_bar(&ms.bar, bt);  // C: the stores are issued ahead of the compute waves' K/V tile loads
         arrive();
         stage++;
 
         // ------------------------------------------------------ ATTN --
         AttnLds *al = (AttnLds *)s.xr;
         if (wait_prev()) {
+            // this token's q heads, k and v of each half's KV head (device-scope
+            // direct-to-LDS loads), the head norms and the RoPE row of pos
             for (int h = 0; h < 2; h++) {
                 int kvh;
                 attn_chunk_of(a, h, 0, 1 << 30, kvh);
                 AttnLds &A = al[h];
-                for (int i = lane; i < Gq * AHD; i += 64) A.qr[i / AHD][i % AHD] = ld_f(a.q + (size_t)kvh * Gq * AHD + i);
-                for (int i = lane; i < AHD; i += 64) {
-                    A.kp[i] = ld_f(a.k + (size_t)kvh * AHD + i);
-                    A.vp[i] = ld_f(a.v + (size_t)kvh * AHD + i);
-                    A.qn[i] = L.q_norm[i];
-                    A.kn[i] = L.k_norm[i];
-                }
-                if (lane < AHD / 2) A.cs[lane] = a.rope_cs[(size_t)pos * (AHD / 2) + lane];
+                io_dma((const uint8_t *)(a.q + (size_t)kvh * Gq * AHD), (uint8_t *)A.qr, Gq * AHD * 4);
+                io_dma_half((const uint8_t *)(a.k + (size_t)kvh * AHD), (uint8_t *)A.kp, 16);
+                io_dma_half((const uint8_t *)(a.v + (size_t)kvh * AHD), (uint8_t *)A.vp, 16);
+                io_dma_half((const uint8_t *)L.q_norm, (uint8_t *)A.qn, 0);
+                io_dma_half((const uint8_t *)L.k_norm, (uint8_t *)A.kn, 0);
+                io_dma_half((const uint8_t *)(a.rope_cs + (size_t)pos * (AHD / 2)), (uint8_t *)A.cs, 0);
             }
+            vm_wait_all();
         }
         TRACE(a, stage, 1);
-        __syncthreads();  // A
+        lds_bar(&ms.bar, bt);  // A
         if (ms.abort) return;
-        __syncthreads();  // head norms
-        __syncthreads();  // RoPE
-        __syncthreads();  // f16 k/v of pos
+        lds_bar(&ms.bar, bt);  // head norms
+        lds_bar(&ms.bar, bt);  // RoPE
+        lds_bar(&ms.bar, bt);  // f16 k/v of pos
         const int rounds = attn_rounds(a, nchunk);
         for (int rd = 0; rd < rounds; rd++) {
-            __syncthreads();  // scores
-            __syncthreads();  // softmax
-            __syncthreads();  // o partials
-            __syncthreads();  // o reduced
+            lds_bar(&ms.bar, bt);  // scores
+            lds_bar(&ms.bar, bt);  // softmax
+            lds_bar(&ms.bar, bt);  // o partials
+            lds_bar(&ms.bar, bt);  // o reduced
             for (int h = 0; h < 2; h++) {  // partials of both halves, and K/V[pos]
                 int kvh;
                 const int ch = attn_chunk_of(a, h, rd, nchunk, kvh);
                 if (ch < 0) continue;
                 const AttnLds &B = al[h];
                 for (int g = 0; g < Gq; g++) {
-                    float *pp = a.part + ((size_t)(kvh * Gq + g) * a.max_chunks + ch) * (AHD + 2);
+                    float *pp = a.part + ((size_t)(kvh * Gq + g) * a.max_chunks + ch) * PST;
                     for (int i = lane; i < AHD; i += 64) st_f(pp + i, B.ob[0][g][i]);
                     if (lane == 0) {
                         st_f(pp + AHD, B.mx[g]);
@@ -776,23 +838,43 @@ static __device__ void io_main(const StreamArgs &a, const Ctx &cx) {
 
         // ------------------------------------------------------ COMB --
         if (wait_prev()) {
-            // this workgroup's rQ dims of att, 16 at a time (one head each)
+            // this workgroup's rQ dims of att, 16 at a time (one head each):
+            // O = sum_c exp(m_c - M) o_c / sum_c exp(m_c - M) l_c over the chunks
             const int e0 = wg * a.rQ, n = max(0, min(a.rQ, a.QD - e0));
+            float *cb = (float *)s.xr;  // [pass of 64 chunks][5][64 lanes][4]: o[d0..d0+16), (m, l, -, -)
             for (int b0 = 0; b0 < n; b0 += 16) {
                 const int e = e0 + b0, hh = e / AHD, d0 = e % AHD;
-                const float *pb = a.part + (size_t)hh * a.max_chunks * (AHD + 2);
+                const float *pb = a.part + (size_t)hh * a.max_chunks * PST;
+                const int npass = (nchunk + 63) / 64;
+                for (int ps = 0; ps < npass; ps++) {
+                    const int cc = min(ps * 64 + lane, nchunk - 1);
+                    const float *pc = pb + (size_t)cc * PST;
+                    for (int q = 0; q < 4; q++)
+                        __builtin_amdgcn_global_load_lds((const void *)(pc + d0 + 4 * q), LDS_PTR(cb + (ps * 5 + q) * 256),
+                                                         16, 0, 16);
+                    __builtin_amdgcn_global_load_lds((const void *)(pc + AHD), LDS_PTR(cb + (ps * 5 + 4) * 256), 16, 0,
+                                                     16);
+                }
+                vm_wait_all();
                 float M = -INFINITY;
-                for (int cc = lane; cc < nchunk; cc += 64) M = fmaxf(M, ld_f(pb + (size_t)cc * (AHD + 2) + AHD));
+                for (int ps = 0; ps < npass; ps++)
+                    if (ps * 64 + lane < nchunk) M = fmaxf(M, cb[(ps * 5 + 4) * 256 + 4 * lane]);
                 M = wave_max(M);
                 float Ls = 0.f, O[16];
 #pragma unroll
                 for (int i = 0; i < 16; i++) O[i] = 0.f;
-                for (int cc = lane; cc < nchunk; cc += 64) {
-                    const float *pc = pb + (size_t)cc * (AHD + 2);
-                    const float f = expf(ld_f(pc + AHD) - M);
-                    Ls += f * ld_f(pc + AHD + 1);
+                for (int ps = 0; ps < npass; ps++) {
+                    if (ps * 64 + lane >= nchunk) continue;
+                    const float f = expf(cb[(ps * 5 + 4) * 256 + 4 * lane] - M);
+                    Ls += f * cb[(ps * 5 + 4) * 256 + 4 * lane + 1];
 #pragma unroll
-                    for (int i = 0; i < 16; i++) O[i] += f * ld_f(pc + d0 + i);
+                    for (int q = 0; q < 4; q++) {
+                        const float4 o4 = *(const float4 *)(cb + (ps * 5 + q) * 256 + 4 * lane);
+                        O[4 * q] += f * o4.x;
+                        O[4 * q + 1] += f * o4.y;
+                        O[4 * q + 2] += f * o4.z;
+                        O[4 * q + 3] += f * o4.w;
+                    }
                 }
                 Ls = wave_sum(Ls);
 #pragma unroll
@@ -800,13 +882,14 @@ static __device__ void io_main(const StreamArgs &a, const Ctx &cx) {
                     const float oi = wave_sum(O[i]);
                     if (lane == i) s.yo[b0 + i] = oi / Ls;
                 }
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             if (n > 0) io_quantize(s.yo, nullptr, n, e0, a.QD, a.attq, ms.qstage);
             arrive();
         }
         TRACE(a, stage, 1);
-        __syncthreads();  // A
+        lds_bar(&ms.bar, bt);  // A
         if (ms.abort) return;
         stage++;
 
@@ -816,9 +899,9 @@ static __device__ void io_main(const StreamArgs &a, const Ctx &cx) {
             vm_wait_all();
         }
         TRACE(a, stage, 1);
-        __syncthreads();  // A
+        lds_bar(&ms.bar, bt);  // A
         if (ms.abort) return;
-        __syncthreads();  // B
+        lds_bar(&ms.bar, bt);  // B
         TRACE(a, stage, 5);
         {
             const int r0 = wg * a.rD, n = max(0, min(a.rD, a.D - r0));
@@ -840,9 +923,9 @@ static __device__ void io_main(const StreamArgs &a, const Ctx &cx) {
             if (lane == 0) ms.s_norm = sc;
         }
         TRACE(a, stage, 1);
-        __syncthreads();  // A
+        lds_bar(&ms.bar, bt);  // A
         if (ms.abort) return;
-        __syncthreads();  // B
+        lds_bar(&ms.bar, bt);  // B
         TRACE(a, stage, 5);
         {
             const int r0 = wg * a.rH, n = max(0, min(a.rH, a.H - r0));
@@ -857,9 +940,9 @@ static __device__ void io_main(const StreamArgs &a, const Ctx &cx) {
             vm_wait_all();
         }
         TRACE(a, stage, 1);
-        __syncthreads();  // A
+        lds_bar(&ms.bar, bt);  // A
         if (ms.abort) return;
-        __syncthreads();  // B
+        lds_bar(&ms.bar, bt);  // B
         TRACE(a, stage, 5);
         {
             const int r0 = wg * a.rD, n = max(0, min(a.rD, a.D - r0));
@@ -883,9 +966,9 @@ static __device__ void io_main(const StreamArgs &a, const Ctx &cx) {
         if (lane == 0) ms.s_norm = sc;
     }
     TRACE(a, stage, 1);
-    __syncthreads();  // A
+    lds_bar(&ms.bar, bt);  // A
     if (ms.abort) return;
-    __syncthreads();  // B
+    lds_bar(&ms.bar, bt);  // B
     TRACE(a, stage, 5);
     const SWgRows wr = a.wgrows[(size_t)a.vocab_plan * G + wg];
     float bv = -INFINITY;
@@ -911,8 +994,9 @@ static __device__ void io_main(const StreamArgs &a, const Ctx &cx) {
 
 // --------------------------------------------------------- compute waves --
 static __device__ void attn_compute(const StreamArgs &a, const SLayer &L, const Ctx &cx, int wave, int pos,
-                                    int nchunk, KVReg &kv) {
+                                    int nchunk, KVReg (&kvr)[2], uint32_t &bt) {
     const int tid = threadIdx.x, lane = tid & 63, half = wave >> 2, tw = wave & 3, th = tid & 255;
+    Misc &ms = *cx.s.misc;
     AttnLds &A = ((AttnLds *)cx.s.xr)[half];
     const int Gq = a.n_heads / a.n_kv;
     // q heads and k: RMSNorm (ops.odin:7-19), then RoPE (forward.odin:117-145)
@@ -923,7 +1007,7 @@ static __device__ void attn_compute(const StreamArgs &a, const SLayer &L, const 
         ss = wave_sum(ss);
         if (lane == 0) A.nrm[g] = 1.0f / sqrtf(ss / (float)AHD + a.eps);
     }
-    __syncthreads();  // head norms
+    lds_bar(&ms.bar, bt);  // head norms
     for (int idx = th; idx < AG * (AHD / 2); idx += 256) {
 #pragma clang fp contract(off)
         const int g = idx / (AHD / 2), i = idx % (AHD / 2);
@@ -952,13 +1036,13 @@ static __device__ void attn_compute(const StreamArgs &a, const SLayer &L, const 
         A.vpos[i] = f2h(A.vp[i]);
         A.vpos[i + AHD / 2] = f2h(A.vp[i + AHD / 2]);
     }
-    __syncthreads();  // RoPE
-    __syncthreads();  // (kept: the I/O wave mirrors three barriers here)
+    lds_bar(&ms.bar, bt);  // RoPE
+    lds_bar(&ms.bar, bt);  // (kept: the I/O wave mirrors three barriers here)
     const int rounds = attn_rounds(a, nchunk);
     for (int rd = 0; rd < rounds; rd++) {
         int kvh;
         const int c = attn_chunk_of(a, half, rd, nchunk, kvh);
-        if (rd > 0 && c >= 0) attn_issue(a, L, kvh, c, pos, kv);
+        KVReg &kv = kvr[rd & 1];  // rounds rd and rd+1 were requested before this one
         const int t0 = 64 * max(c, 0), n = c >= 0 ? min(64, pos + 1 - t0) : 0;
         // scores: thread (tw, lane) = position t0 + lane, dims [32 tw, 32 tw + 32)
         if (c >= 0) {
@@ -982,7 +1066,7 @@ static __device__ void attn_compute(const StreamArgs &a, const SLayer &L, const 
             for (int g = 0; g < AG; g++)
                 if (g < Gq) A.sp[tw][g][lane] = acc[g];
         }
-        __syncthreads();  // scores
+        lds_bar(&ms.bar, bt);  // scores
         if (c >= 0) {     // split-local softmax (ops.odin:21-37), one wave per head
             const float div = sqrtf((float)AHD);
             for (int g = tw; g < AG; g += 4) {
@@ -1002,7 +1086,7 @@ static __device__ void attn_compute(const StreamArgs &a, const SLayer &L, const 
                 A.pT[t][g] = e;
             }
         }
-        __syncthreads();  // softmax
+        lds_bar(&ms.bar, bt);  // softmax
         // o = sum_t p(t) v(t): thread (tw, lane) = positions 16 tw .. +15, dims 2 lane, 2 lane + 1
         if (c >= 0) {
             float o0[AG] = {0.f, 0.f, 0.f, 0.f}, o1[AG] = {0.f, 0.f, 0.f, 0.f};
@@ -1029,13 +1113,18 @@ static __device__ void attn_compute(const StreamArgs &a, const SLayer &L, const 
                     A.ob[tw][g][2 * lane + 1] = o1[g];
                 }
         }
-        __syncthreads();  // o partials
+        {  // round rd + 2 reuses this round's registers
+            int kvh2;
+            const int c2 = attn_chunk_of(a, half, rd + 2, nchunk, kvh2);
+            if (c2 >= 0) attn_issue(a, L, kvh2, c2, pos, kv);
+        }
+        lds_bar(&ms.bar, bt);  // o partials
         if (c >= 0)
             for (int idx = th; idx < Gq * AHD; idx += 256) {
                 const int g = idx / AHD, i = idx % AHD;
                 A.ob[0][g][i] = (A.ob[0][g][i] + A.ob[1][g][i]) + (A.ob[2][g][i] + A.ob[3][g][i]);
             }
-        __syncthreads();  // o reduced
+        lds_bar(&ms.bar, bt);  // o reduced
     }
 }
 
@@ -1044,15 +1133,16 @@ static __device__ void attn_compute(const StreamArgs &a, const SLayer &L, const 
 static __device__ void compute_main(const StreamArgs &a, const Ctx &cx, int wave) {
     const int cw = blockIdx.x * S_NCW + wave;
     const Lds &s = cx.s;
-    const Misc &ms = *s.misc;
+    Misc &ms = *s.misc;
+    uint32_t bt = 0;  // barrier target
     Ring r;
-    r.issued = 0;
     r.consumed = 0;
-    r.seg = 0;
     r.lds = s.ring + wave * S_RING_BYTES;
+    r.filled = &ms.filled[wave];
+    r.consumed_p = &ms.consumed[wave];
+    r.abort_p = (uint32_t *)&ms.abort;
+    r.err_p = a.state + ST_ERR;
     uint32_t soff = 0;
-    seg_open(a, cw, r);
-    ring_topup(a, cw, r);
     const int nst = 6 * a.n_layers + 1;
     for (int st = 0; st < nst; st++) {
         const int l = st / 6, k = st % 6;  // k: 0 QKV, 1 ATTN, 2 COMB, 3 WO, 4 GU, 5 DOWN; l == n_layers: VOCAB
@@ -1061,37 +1151,151 @@ static __device__ void compute_main(const StreamArgs &a, const Ctx &cx, int wave
         if (k == 1 && !voc) {
             // the K/V tiles of the first round do not depend on this token:
             // requested while the I/O wave waits for the QKV results
-            KVReg kv;
-            int kvh;
-            const int c0 = attn_chunk_of(a, wave >> 2, 0, nchunk, kvh);
-            if (c0 >= 0) attn_issue(a, a.layers[l], kvh, c0, pos, kv);
-            __syncthreads();  // A
+            KVReg kv[2];
+            for (int rd = 0; rd < 2; rd++) {
+                int kvh;
+                const int c0 = attn_chunk_of(a, wave >> 2, rd, nchunk, kvh);
+                if (c0 >= 0) attn_issue(a, a.layers[l], kvh, c0, pos, kv[rd]);
+            }
+            lds_bar(&ms.bar, bt);  // A
             if (ms.abort) break;
             if (wave == 0) TRACE(a, st + 1, 2);
-            attn_compute(a, a.layers[l], cx, wave, pos, nchunk, kv);
+            attn_compute(a, a.layers[l], cx, wave, pos, nchunk, kv, bt);
             if (wave == 0) TRACE(a, st + 1, 4);
             continue;
         }
-        ring_topup(a, cw, r);
-        __syncthreads();  // A
+        // the stage's plan tables, requested before the barrier wait so the
+        // loads after it hit the scalar cache
+        const int pl = (k == 2 && !voc) ? -1 : voc ? a.vocab_plan : CST(a.layers)[l].plan[k == 0 ? SK_QKV : k - 2];
+        int touch = 0;
+        if (pl >= 0) {
+            const auto *kp = CST(a.kinds) + pl;
+            const auto *wp = CST(a.waves) + (size_t)pl * a.G * S_NCW + cw;
+            touch = kp->nseg + kp->seg[2].rows + wp->nruns + wp->run[S_MAXRUN - 1].nrows +
+                    CST(a.wgrows)[(size_t)pl * a.G + blockIdx.x].v0;
+        }
+        lds_bar(&ms.bar, bt);  // A
         if (ms.abort) break;
         if (wave == 0) TRACE(a, st + 1, 2);
         if (k == 2 && !voc) continue;
-        const int pl = voc ? a.vocab_plan : CST(a.layers)[l].plan[k == 0 ? SK_QKV : k - 2];
+        if (touch == INT32_MIN) break;  // never: keeps the early loads
         const float scale = (voc || k == 0 || k == 4) ? ms.s_norm : 1.0f;
         gemv_stage(a, cw, r, soff, pl, s.xr, s.yo, scale, st + 1);
         if (wave == 0) TRACE(a, st + 1, 4);
-        __syncthreads();  // B
+        lds_bar(&ms.bar, bt);  // B
+        if (k == 0 && !voc) lds_bar(&ms.bar, bt);  // C (QKV): the I/O wave's stores go first
     }
-    vm_wait_all();  // no direct-to-LDS load may be in flight when the wave ends
+}
+
+// ---------------------------------------------------------- loader waves --
+// Loader L fills the rings of compute waves LS*L .. LS*L + LS-1 (LS =
+// LSTREAMS) with 16-byte nontemporal loads: one wave instruction moves a
+// 1 KB piece.  Its registers hold NGRP groups of LS slots, slot j of a group
+// being one chunk (CP pieces) of stream j.  The groups are handled in turn:
+// a group's chunks are written to the rings (one LDS wait, then the fill
+// counters), and each slot is refilled with the next chunk of its stream if
+// the ring has room for it (piece p may be loaded once the compute wave has
+// consumed piece p - S_RING).  The other groups' loads stay in flight
+// meanwhile.  A slot with nothing to load re-reads a small resident buffer
+// (the data is dropped), so the count of loads in flight stays exact.
+// Streams are padded to whole chunks (wstride is a multiple of 4 KB); pieces
+// past a stream's end land in ring slots its compute wave no longer reads.
+constexpr int LSTREAMS = S_NCW / S_NLD;
+constexpr int CP = S_CP;
+constexpr int NGRP = 4;
+
+static __device__ __forceinline__ void loader_main(const StreamArgs &a, const Ctx &cx, int L) {
+    const int lane = threadIdx.x & 63;
+    Misc &ms = *cx.s.misc;
+    const int w0 = L * LSTREAMS;
+    const u32x4 *base[LSTREAMS];
+    uint32_t n[LSTREAMS], issued[LSTREAMS];  // pieces of the stream, chunks requested
+#pragma unroll
+    for (int j = 0; j < LSTREAMS; j++) {
+        const int cw = blockIdx.x * S_NCW + w0 + j;
+        base[j] = (const u32x4 *)(a.wstream + (size_t)cw * a.wstride) + lane;
+        n[j] = uni((uint32_t)CST(a.wpieces)[cw]);
+        issued[j] = 0;
+    }
+    const u32x4 *dummy = (const u32x4 *)a.xq + lane;
+    u32x4 data[NGRP][LSTREAMS][CP];
+    uint32_t sc[NGRP][LSTREAMS];  // chunk + 1 held by the slot, 0: none
+#pragma unroll
+    for (int g = 0; g < NGRP; g++)
+#pragma unroll
+        for (int j = 0; j < LSTREAMS; j++) {
+#pragma unroll
+            for (int k = 0; k < CP; k++) data[g][j][k] = __builtin_nontemporal_load(dummy);
+            sc[g][j] = 0;
+        }
+    const uint32_t *abort_p = (const uint32_t *)&ms.abort;
+    while (true) {
+        bool any = false;
+#pragma unroll
+        for (int g = 0; g < NGRP; g++) {
+            bool ret = false;
+#pragma unroll
+            for (int j = 0; j < LSTREAMS; j++)
+                if (sc[g][j]) {
+                    uint8_t *ring = cx.s.ring + (w0 + j) * S_RING_BYTES + lane * 16;
+                    const uint32_t p0 = (sc[g][j] - 1) * CP;
+#pragma unroll
+                    for (int k = 0; k < CP; k++) *(u32x4 *)(ring + ((p0 + k) % S_RING) * 1024) = data[g][j][k];
+                    ret = true;
+                }
+            if (ret) {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                if (lane == 0) {
+#pragma unroll
+                    for (int j = 0; j < LSTREAMS; j++)
+                        if (sc[g][j]) lds_st(&ms.filled[w0 + j], sc[g][j] * CP);
+                }
+                any = true;
+            }
+            uint32_t cons[LSTREAMS];
+#pragma unroll
+            for (int j = 0; j < LSTREAMS; j++) cons[j] = lds_ld(&ms.consumed[w0 + j]);
+#pragma unroll
+            for (int j = 0; j < LSTREAMS; j++) {
+                const uint32_t c = issued[j];
+                const bool ok = uni(c * CP < n[j] && (c + 1) * CP <= cons[j] / 1024 + S_RING);
+                const u32x4 *src = ok ? base[j] + (size_t)c * (CP * 64) : dummy;
+#pragma unroll
+                for (int k = 0; k < CP; k++) data[g][j][k] = __builtin_nontemporal_load(ok ? src + k * 64 : dummy);
+                sc[g][j] = ok ? c + 1 : 0;
+                issued[j] = c + (ok ? 1 : 0);
+                any = any || ok;
+            }
+        }
+        if (!any) {
+            bool done = true;
+#pragma unroll
+            for (int j = 0; j < LSTREAMS; j++) done = done && issued[j] * CP >= n[j];
+            if (done || lds_ld(abort_p)) break;
+            __builtin_amdgcn_s_sleep(2);  // all rings full: let the compute waves catch up
+        }
+        if (lds_ld(abort_p)) break;
+    }
+    vm_wait_all();
 }
 
 __global__ __launch_bounds__(S_THREADS) void stream_kernel(StreamArgs a) {
     const Ctx cx = make_ctx(a);
     const int wave = (int)uni(threadIdx.x >> 6);  // wave-uniform: the role branch is scalar
-    if (wave == S_NCW) {
+    if (threadIdx.x < S_NCW) {
+        cx.s.misc->filled[threadIdx.x] = 0;
+        cx.s.misc->consumed[threadIdx.x] = 0;
+    }
+    if (threadIdx.x == 0) {
+        cx.s.misc->bar = 0;
+        cx.s.misc->abort = 0;
+    }
+    __syncthreads();  // the only barrier of all waves: the counters above are set
+    if (wave == NTOT_IO) {
         io_main(a, cx);
         vm_wait_all();
+    } else if (wave >= S_NCW) {
+        loader_main(a, cx, wave - S_NCW);
     } else {
         compute_main(a, cx, wave);
     }

@@ -1,6 +1,6 @@
 // stream_plan.cpp -- host planning for the persistent token kernel
 // (stream.hip): which rows every compute wave computes in every weight stage,
-// and the repack of the GGUF blocks into per-wave stream regions.
+// and the repack of the GGUF blocks into the compute waves' weight streams.
 //
 // Row assignment.  Stages whose output feeds the next GEMV through the
 // producer-quantized vector (WO, GU, DOWN) give each workgroup the rows it
@@ -10,10 +10,12 @@
 // to bytes (Q6_K rows are 1.46x Q4_K rows), so every wave streams about the
 // same amount.
 //
-// Stream region of a compute wave: for each of its runs, for each step of
-// NR = 64/lpr rows, for each block of lpr units of those rows, the step bytes
-// of stream.h (SwiGLU pairs: gate step, then up step), padded to whole 1 KB
-// pieces.  Rows past the end of a run inside a step are zero blocks.
+// A compute wave's part of one stage in its stream: for each of its runs,
+// for each step of NR = 64/lpr rows, for each block of lpr units of those
+// rows, the step bytes of stream.h (SwiGLU pairs: gate step, then up step),
+// padded to whole 1 KB pieces.  Rows past the end of a run inside a step are
+// zero blocks.  The stream is the concatenation of these parts over the
+// stages of a token (per layer QKV, WO, GU, DOWN, then VOCAB).
 #include <algorithm>
 #include <cstring>
 #include <string>
@@ -40,7 +42,7 @@ static int64_t run_bytes(const SKind &k, const SRun &r) {
     return steps * step_bytes(k.seg[r.seg].type) * (k.pair ? 2 : 1);
 }
 
-static void finish_kind(PlanKind &pk, int G) {
+static void finish_kind(PlanKind &pk) {
     int64_t maxp = 0;
     for (SWave &w : pk.waves) {
         int64_t b = 0;
@@ -49,7 +51,6 @@ static void finish_kind(PlanKind &pk, int G) {
         maxp = std::max<int64_t>(maxp, w.npieces);
     }
     pk.kind.region = maxp * 1024;
-    pk.kind.bytes = pk.kind.region * (int64_t)G * S_NCW;
 }
 
 // push rows [v0, v1) of the stage's virtual rows as runs of wave w
@@ -141,6 +142,13 @@ bool plan_stream_kind(int kind, const int *types, int nseg, const int *rows, int
             why = "weight type not supported by the token kernel";
             return false;
         }
+        // a compute wave holds one step in its ring while the loader needs
+        // room for a whole chunk beyond it
+        const int sb = step_bytes(types[s]) * (k.pair ? 2 : 1);
+        if ((sb + 1023) / 1024 + S_CP > S_RING) {
+            why = "weight step larger than the token kernel's ring";
+            return false;
+        }
         k.seg[s].type = types[s];
         k.seg[s].rows = rows[s];
         k.seg[s].vrow0 = vrow;
@@ -155,7 +163,7 @@ bool plan_stream_kind(int kind, const int *types, int nseg, const int *rows, int
         why = "row plan needs more runs per wave than supported";
         return false;
     }
-    finish_kind(pk, G);
+    finish_kind(pk);
     return true;
 }
 
@@ -203,13 +211,13 @@ static void write_step(int type, const uint8_t *src, int K, int lpr, int r0, int
     }
 }
 
-void repack_stream_kind(const PlanKind &pk, const uint8_t *const *src, int G, uint8_t *dst) {
+void repack_stream_kind(const PlanKind &pk, const uint8_t *const *src, int w0, int w1, uint8_t *const *wdst) {
     const SKind &k = pk.kind;
     const int NR = 64 / k.lpr, nb = (k.K / 64) / k.lpr;
-    std::memset(dst, 0, (size_t)k.bytes);
-    for (int w = 0; w < G * S_NCW; w++) {
+    for (int w = w0; w < w1; w++) {
         const SWave &wv = pk.waves[(size_t)w];
-        uint8_t *out = dst + (size_t)w * k.region;
+        uint8_t *out = wdst[w - w0];
+        std::memset(out, 0, (size_t)wv.npieces * 1024);
         for (int i = 0; i < wv.nruns; i++) {
             const SRun &r = wv.run[i];
             const int type = k.seg[r.seg].type, sb = step_bytes(type);

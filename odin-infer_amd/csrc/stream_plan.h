@@ -21,8 +21,9 @@ struct PlanKind {
 bool plan_stream_kind(int kind, const int *types, int nseg, const int *rows, int K, int G, int own, PlanKind &pk,
                       std::string &why);
 
-// Stage buffer of one layer (pk.kind.bytes bytes): src[s] = GGUF blocks of
-// segment s (GU: src[0] gate, src[1] up).
-void repack_stream_kind(const PlanKind &pk, const uint8_t *const *src, int G, uint8_t *dst);
+// One stage of the streams of compute waves [w0, w1): wave w's
+// pk.waves[w].npieces KB at wdst[w - w0].  src[s] = GGUF blocks of segment s
+// (GU: src[0] gate, src[1] up).
+void repack_stream_kind(const PlanKind &pk, const uint8_t *const *src, int w0, int w1, uint8_t *const *wdst);
 
 }  // namespace oi
