@@ -556,7 +556,7 @@ int upload_stream(oi_engine *e, GgufFile &g, bool tied, const StreamPlanAll &sp)
     A.trace = nullptr;
     if (const char *ev = std::getenv("OI_STREAM_TRACE")) {
         if (ev[0] == '1') {
-            const size_t tb = (size_t)(2 + 6 * c.n_layers) * sp.G * 8 * 8;
+            const size_t tb = (size_t)(2 + 6 * c.n_layers) * sp.G * S_TR_SLOTS * 8;
             HIP_TRY(hipMalloc(&A.trace, tb));  // freed with the engine
             HIP_TRY(hipMemset(A.trace, 0, tb));
         }
@@ -1173,7 +1173,7 @@ int64_t oi_engine_debug_buffer(oi_engine *e, int32_t which, void *dst, int64_t b
     case OI_BUF_STATE: src = e->state, n = ST_SWORDS * 4; break;
     case OI_BUF_AMVAL: src = e->am_val, n = (int64_t)std::max(e->sa.G, 1) * 4; break;
     case OI_BUF_AMIDX: src = e->am_idx, n = (int64_t)std::max(e->sa.G, 1) * 4; break;
-    case OI_BUF_TRACE: src = e->sa.trace, n = (int64_t)(2 + 6 * c.n_layers) * e->sa.G * 64; break;
+    case OI_BUF_TRACE: src = e->sa.trace, n = (int64_t)(2 + 6 * c.n_layers) * e->sa.G * S_TR_SLOTS * 8; break;
     default: return fail(OI_E_ARG, "unknown buffer");
     }
     if (!src) return fail(OI_E_ARG, "buffer not used by this engine");

@@ -38,6 +38,7 @@ constexpr int S_RING_BYTES = S_RING * 1024;
 constexpr int S_CP = 2;                    // pieces per loader request (chunk)
 constexpr int S_NC = 32;                   // barrier counters (each in its own 256-byte line)
 constexpr int S_MAXRUN = 4;                // row runs per compute wave per stage
+constexpr int S_TR_SLOTS = 24;             // debugging trace words per (stage, workgroup)
 
 // Stages that stream weights, in the order of a layer (+ the vocab projection).
 enum StageKind : int32_t { SK_QKV = 0, SK_WO = 1, SK_GU = 2, SK_DOWN = 3, SK_VOCAB = 4, SK_N = 5 };
@@ -134,7 +135,7 @@ struct StreamArgs {
     uint64_t *bar;             // [S_NC * 32] barrier counters
     int32_t finalize_only;     // reduce the pending argmax and stop
     int32_t yo_floats;         // most stage outputs of one workgroup
-    uint64_t *trace;           // debugging (null: off): [stage][G][8] real-time clock stamps
+    uint64_t *trace;           // debugging (null: off): [stage][G][S_TR_SLOTS] clock stamps and counters
 };
 
 // state words used by the stream kernel beyond ST_*: launch sequence (64-bit

@@ -37,6 +37,13 @@ namespace oi {
 
 constexpr float XQ_MAX_S = 32767.0f;  // 2^15 - 1: 16-bit activations
 constexpr int NTOT_IO = S_NCW + S_NLD;  // index of the I/O wave
+// Pieces of the next weight stage the loaders may request before the compute
+// waves start it.  Loads run ahead of a stage barrier only this far: the
+// I/O wave's stores, barrier atomics and gathers queue behind loads in flight.
+#ifndef OI_STREAM_LEAD
+#define OI_STREAM_LEAD 4
+#endif
+constexpr uint32_t S_LEAD = OI_STREAM_LEAD;
 constexpr uint64_t SPIN_TICKS = 200000000ull;  // 2 s of the 100 MHz real-time clock
 
 #define LDS_PTR(p) ((__attribute__((address_space(3))) void *)(p))
@@ -93,18 +100,22 @@ static __device__ __forceinline__ void lds_st(uint32_t *p, uint32_t v) {
 #define CST(p) (p)  // host pass of the same source: no address spaces
 #endif
 
-// debugging trace (StreamArgs::trace): slot k of (stage, workgroup), lane 0
-constexpr int TR_SLOTS = 8;
-#define TRACE(a, stage, k)                                                                                  \
+// debugging trace (StreamArgs::trace), lane 0: slots 0..7 of (stage,
+// workgroup) are clock stamps (TRACE), 8 + w the ticks compute wave w spent
+// waiting for its ring in the stage, 16 + 4 L .. of the last stage loader
+// L's counts of pieces loaded, idle slots and sleeps (TRACE_SET)
+#define TRACE_SET(a, stage, k, v)                                                                          \
     do {                                                                                                    \
         if ((a).trace && (threadIdx.x & 63) == 0)                                                           \
-            (a).trace[((size_t)(stage) * (a).G + blockIdx.x) * TR_SLOTS + (k)] = __builtin_amdgcn_s_memrealtime(); \
+            (a).trace[((size_t)(stage) * (a).G + blockIdx.x) * S_TR_SLOTS + (k)] = (v);                     \
     } while (0)
+#define TRACE(a, stage, k) TRACE_SET(a, stage, k, __builtin_amdgcn_s_memrealtime())
 
 // ------------------------------------------------------------ LDS layout --
 struct __attribute__((aligned(16))) Misc {
     uint32_t filled[S_NCW];    // pieces of each compute wave's stream written into its ring
     uint32_t consumed[S_NCW];  // stream bytes each compute wave has consumed
+    uint32_t allow[S_NCW];     // pieces of each stream the loaders may request so far
     uint32_t bar;              // barrier counter of the compute and I/O waves
     float s_norm;            // RMSNorm scale of the current stage's input
     int32_t abort;
@@ -113,6 +124,7 @@ struct __attribute__((aligned(16))) Misc {
     float red[16];
     int32_t redi[16];
     float xres[256];         // this workgroup's rows of the residual stream x
+    float nrm[256];          // the next norm weights of those rows (requested a stage ahead)
     float yo_pad[4];
     uint8_t qstage[16 * 32]; // producer quantization staging (16 chunks)
 };
@@ -135,15 +147,18 @@ struct Ring {
     uint8_t *lds;        // the compute wave's ring
     const uint32_t *filled;
     uint32_t *consumed_p;
+    uint32_t *allow_p;   // loader limit of this stream (pieces)
     uint32_t *abort_p;   // the workgroup's abort flag (LDS)
     int32_t *err_p;      // the launch's error word (state)
+    bool trace;          // debugging: count the ticks spent waiting
+    uint64_t wait_ticks;
 };
 
 // compute wave: bytes [.., end) of its stream are in its ring once this returns
 // (on an abort, or after SPIN_TICKS without progress, which aborts the
 // launch: the stage then completes on stale ring data and the host reports
 // the error)
-static __device__ __forceinline__ void ring_wait(const Ring &r, uint32_t end) {
+static __device__ __forceinline__ void ring_wait(Ring &r, uint32_t end) {
     const uint32_t need = uni((end + 1023) / 1024);
     if (lds_ld(r.filled) < need) {
         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
@@ -157,6 +172,7 @@ static __device__ __forceinline__ void ring_wait(const Ring &r, uint32_t end) {
             }
             __builtin_amdgcn_s_sleep(1);
         }
+        if (r.trace) r.wait_ticks += __builtin_amdgcn_s_memrealtime() - t0;
     }
     asm volatile("" ::: "memory");
 }
@@ -414,6 +430,7 @@ static __device__ void gemv_stage(const StreamArgs &a, int cw, Ring &r, uint32_t
     const int v0 = CST(a.wgrows)[(size_t)pl * a.G + blockIdx.x].v0;
     const uint32_t start = soff;
     const int nruns = wv->nruns, npieces = wv->npieces;
+    if ((threadIdx.x & 63) == 0) lds_st(r.allow_p, start / 1024 + (uint32_t)npieces + S_LEAD);
     for (int i = 0; i < nruns; i++) {
         const SRun run = wv->run[i];
         const int type = kd.seg[run.seg].type;
@@ -782,9 +799,17 @@ static __device__ void io_main(const StreamArgs &a, const Ctx &cx) {
 
         // ------------------------------------------------------ ATTN --
         AttnLds *al = (AttnLds *)s.xr;
+        // the head norms and the RoPE row of pos (read-only: requested before
+        // the barrier; the QKV input in this LDS area is no longer read)
+        for (int h = 0; h < 2; h++) {
+            AttnLds &A = al[h];
+            io_dma_half((const uint8_t *)L.q_norm, (uint8_t *)A.qn, 0);
+            io_dma_half((const uint8_t *)L.k_norm, (uint8_t *)A.kn, 0);
+            io_dma_half((const uint8_t *)(a.rope_cs + (size_t)pos * (AHD / 2)), (uint8_t *)A.cs, 0);
+        }
         if (wait_prev()) {
             // this token's q heads, k and v of each half's KV head (device-scope
-            // direct-to-LDS loads), the head norms and the RoPE row of pos
+            // direct-to-LDS loads)
             for (int h = 0; h < 2; h++) {
                 int kvh;
                 attn_chunk_of(a, h, 0, 1 << 30, kvh);
@@ -792,9 +817,6 @@ static __device__ void io_main(const StreamArgs &a, const Ctx &cx) {
                 io_dma((const uint8_t *)(a.q + (size_t)kvh * Gq * AHD), (uint8_t *)A.qr, Gq * AHD * 4);
                 io_dma_half((const uint8_t *)(a.k + (size_t)kvh * AHD), (uint8_t *)A.kp, 16);
                 io_dma_half((const uint8_t *)(a.v + (size_t)kvh * AHD), (uint8_t *)A.vp, 16);
-                io_dma_half((const uint8_t *)L.q_norm, (uint8_t *)A.qn, 0);
-                io_dma_half((const uint8_t *)L.k_norm, (uint8_t *)A.kn, 0);
-                io_dma_half((const uint8_t *)(a.rope_cs + (size_t)pos * (AHD / 2)), (uint8_t *)A.cs, 0);
             }
             vm_wait_all();
         }
@@ -894,6 +916,10 @@ static __device__ void io_main(const StreamArgs &a, const Ctx &cx) {
         stage++;
 
         // -------------------------------------------------------- WO --
+        {  // ffn_norm rows for this stage's epilogue: requested now, complete with the gather
+            const int r0 = wg * a.rD, n = max(0, min(a.rD, a.D - r0));
+            io_dma((const uint8_t *)(L.ffn_norm + r0), (uint8_t *)ms.nrm, 4 * n);
+        }
         if (wait_prev()) {
             io_dma(a.attq, s.xr, (int)qvec_bytes(a.QD));
             vm_wait_all();
@@ -908,7 +934,7 @@ static __device__ void io_main(const StreamArgs &a, const Ctx &cx) {
             for (int i = lane; i < n; i += 64) ms.xres[i] = ms.xres[i] + s.yo[i];  // forward.odin:117-121
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             if (n > 0) {
-                const float ss = io_quantize(ms.xres, L.ffn_norm + r0, n, r0, a.D, a.xq, ms.qstage);
+                const float ss = io_quantize(ms.xres, ms.nrm, n, r0, a.D, a.xq, ms.qstage);
                 if (lane == 0) st_f(a.ssq + wg, ss);
             }
         }
@@ -935,6 +961,11 @@ static __device__ void io_main(const StreamArgs &a, const Ctx &cx) {
         stage++;
 
         // ------------------------------------------------------ DOWN --
+        {  // the next norm's rows (next layer's attn_norm, or output_norm)
+            const int r0 = wg * a.rD, n = max(0, min(a.rD, a.D - r0));
+            const float *nw = l + 1 < a.n_layers ? a.layers[l + 1].attn_norm : a.output_norm;
+            io_dma((const uint8_t *)(nw + r0), (uint8_t *)ms.nrm, 4 * n);
+        }
         if (wait_prev()) {
             io_dma(a.hbq, s.xr, (int)qvec_bytes(a.H));
             vm_wait_all();
@@ -948,9 +979,8 @@ static __device__ void io_main(const StreamArgs &a, const Ctx &cx) {
             const int r0 = wg * a.rD, n = max(0, min(a.rD, a.D - r0));
             for (int i = lane; i < n; i += 64) ms.xres[i] = ms.xres[i] + s.yo[i];  // forward.odin:134-139
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            const float *nw = l + 1 < a.n_layers ? a.layers[l + 1].attn_norm : a.output_norm;
             if (n > 0) {
-                const float ss = io_quantize(ms.xres, nw + r0, n, r0, a.D, a.xq, ms.qstage);
+                const float ss = io_quantize(ms.xres, ms.nrm, n, r0, a.D, a.xq, ms.qstage);
                 if (lane == 0) st_f(a.ssq + wg, ss);
             }
         }
@@ -1140,8 +1170,11 @@ static __device__ void compute_main(const StreamArgs &a, const Ctx &cx, int wave
     r.lds = s.ring + wave * S_RING_BYTES;
     r.filled = &ms.filled[wave];
     r.consumed_p = &ms.consumed[wave];
+    r.allow_p = &ms.allow[wave];
     r.abort_p = (uint32_t *)&ms.abort;
     r.err_p = a.state + ST_ERR;
+    r.trace = a.trace != nullptr;
+    r.wait_ticks = 0;
     uint32_t soff = 0;
     const int nst = 6 * a.n_layers + 1;
     for (int st = 0; st < nst; st++) {
@@ -1182,6 +1215,8 @@ static __device__ void compute_main(const StreamArgs &a, const Ctx &cx, int wave
         const float scale = (voc || k == 0 || k == 4) ? ms.s_norm : 1.0f;
         gemv_stage(a, cw, r, soff, pl, s.xr, s.yo, scale, st + 1);
         if (wave == 0) TRACE(a, st + 1, 4);
+        TRACE_SET(a, st + 1, 8 + wave, r.wait_ticks);
+        r.wait_ticks = 0;
         lds_bar(&ms.bar, bt);  // B
         if (k == 0 && !voc) lds_bar(&ms.bar, bt);  // C (QKV): the I/O wave's stores go first
     }
@@ -1229,6 +1264,7 @@ static __device__ __forceinline__ void loader_main(const StreamArgs &a, const Ct
             sc[g][j] = 0;
         }
     const uint32_t *abort_p = (const uint32_t *)&ms.abort;
+    uint32_t n_real = 0, n_idle = 0, n_sleep = 0;  // debugging counts
     while (true) {
         bool any = false;
 #pragma unroll
@@ -1255,16 +1291,22 @@ static __device__ __forceinline__ void loader_main(const StreamArgs &a, const Ct
             uint32_t cons[LSTREAMS];
 #pragma unroll
             for (int j = 0; j < LSTREAMS; j++) cons[j] = lds_ld(&ms.consumed[w0 + j]);
+            uint32_t allow[LSTREAMS];
+#pragma unroll
+            for (int j = 0; j < LSTREAMS; j++) allow[j] = lds_ld(&ms.allow[w0 + j]);
 #pragma unroll
             for (int j = 0; j < LSTREAMS; j++) {
                 const uint32_t c = issued[j];
-                const bool ok = uni(c * CP < n[j] && (c + 1) * CP <= cons[j] / 1024 + S_RING);
+                const bool ok =
+                    uni(c * CP < n[j] && (c + 1) * CP <= min(cons[j] / 1024 + S_RING, allow[j] + CP - 1));
                 const u32x4 *src = ok ? base[j] + (size_t)c * (CP * 64) : dummy;
 #pragma unroll
                 for (int k = 0; k < CP; k++) data[g][j][k] = __builtin_nontemporal_load(ok ? src + k * 64 : dummy);
                 sc[g][j] = ok ? c + 1 : 0;
                 issued[j] = c + (ok ? 1 : 0);
                 any = any || ok;
+                n_real += ok ? 1 : 0;
+                n_idle += ok ? 0 : 1;
             }
         }
         if (!any) {
@@ -1273,10 +1315,14 @@ static __device__ __forceinline__ void loader_main(const StreamArgs &a, const Ct
             for (int j = 0; j < LSTREAMS; j++) done = done && issued[j] * CP >= n[j];
             if (done || lds_ld(abort_p)) break;
             __builtin_amdgcn_s_sleep(2);  // all rings full: let the compute waves catch up
+            n_sleep++;
         }
         if (lds_ld(abort_p)) break;
     }
     vm_wait_all();
+    TRACE_SET(a, 6 * a.n_layers + 1, 16 + 4 * L, n_real);
+    TRACE_SET(a, 6 * a.n_layers + 1, 17 + 4 * L, n_idle);
+    TRACE_SET(a, 6 * a.n_layers + 1, 18 + 4 * L, n_sleep);
 }
 
 __global__ __launch_bounds__(S_THREADS) void stream_kernel(StreamArgs a) {
@@ -1285,6 +1331,7 @@ __global__ __launch_bounds__(S_THREADS) void stream_kernel(StreamArgs a) {
     if (threadIdx.x < S_NCW) {
         cx.s.misc->filled[threadIdx.x] = 0;
         cx.s.misc->consumed[threadIdx.x] = 0;
+        cx.s.misc->allow[threadIdx.x] = S_LEAD;
     }
     if (threadIdx.x == 0) {
         cx.s.misc->bar = 0;
