@@ -7,10 +7,11 @@
 // Layout of the work:
 //   * a row is cut into units of 64 weights; a lane owns units j, j+lpr, ...
 //     of its row (lpr lanes per row, a power of two <= 64);
-//   * a tile is R rows per lane group x (64/lpr) groups per wave x 4 waves;
-//   * every workgroup takes a contiguous range of tiles of ONE segment
-//     (so one weight type per workgroup), requests the weights of its first
-//     tile before the x prologue, and double-buffers the rest in registers.
+//   * a tile is R rows per lane group x (64/lpr) groups: one wave's rows;
+//   * one workgroup of 16 waves per CU takes a contiguous range of tiles of
+//     ONE segment (so one weight type per workgroup); its waves take the
+//     tiles from a counter in LDS, request the weights of their first tile
+//     before the x prologue, and double-buffer the rest in registers.
 // Activations: x (after RMSNorm if asked) is quantized per 32 elements to a
 // 22-bit integer q = 2^14*hi + 2^7*mid + lo (hi int8, mid and lo 0..127) with
 // a float scale, so the products run on v_dot4_i32_i8 (three chains, one per
@@ -223,6 +224,12 @@ static __device__ __forceinline__ void quant4(float4 v, int c, uint32_t *hw, uin
     if ((c & 3) == 0) s16[c >> 2] = sum16;
 }
 
+// One workgroup per CU of GW threads (GNW waves): the x prologue is done once
+// per CU, and the waves of a CU take the row tiles of the workgroup's range
+// from a counter in LDS, so waves that started late (their first loads queue
+// behind the other waves') take fewer tiles and the CU finishes together.
+constexpr int GW = 1024, GNW = GW / WAVE;
+
 // x -> (optional RMSNorm, ops.odin:7-19) -> 22-bit integers in LDS, in two
 // phases so that the x loads are issued before the weight prefetch (vector
 // loads return in order: x must not queue behind the weights).  XR float4 of
@@ -245,7 +252,7 @@ static __device__ __forceinline__ void xpre_load(const GemvArgs &a, XPre<XR, NOR
 #pragma unroll
     for (int ii = 0; ii < XR; ii++) {
         const int i = REV ? XR - 1 - ii : ii;  // REV: same loads in another order (see gemv_q_kernel)
-        const int c = min(tid + i * WG, last);
+        const int c = min(tid + i * GW, last);
         p.x[i] = gx[c];
         if (NORM) p.w[i] = nw[c];
     }
@@ -265,10 +272,10 @@ static __device__ __forceinline__ void xpre_finish(const GemvArgs &a, const XPre
         if (XR > 0) {
 #pragma unroll
             for (int i = 0; i < XR; i++)
-                if (tid + i * WG < K / 4)
+                if (tid + i * GW < K / 4)
                     ss += p.x[i].x * p.x[i].x + p.x[i].y * p.x[i].y + p.x[i].z * p.x[i].z + p.x[i].w * p.x[i].w;
         } else {
-            for (int c = tid; c < K / 4; c += WG) {
+            for (int c = tid; c < K / 4; c += GW) {
                 const float4 v = gx[c];
                 ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
             }
@@ -276,7 +283,14 @@ static __device__ __forceinline__ void xpre_finish(const GemvArgs &a, const XPre
         ss = wave_sum(ss);
         if ((tid & (WAVE - 1)) == 0) red[tid / WAVE] = ss;
         __syncthreads();
-        ss = (red[0] + red[1]) + (red[2] + red[3]);
+        float t[GNW / 2];
+#pragma unroll
+        for (int i = 0; i < GNW / 2; i++) t[i] = red[2 * i] + red[2 * i + 1];
+#pragma unroll
+        for (int w = GNW / 4; w >= 1; w >>= 1)
+#pragma unroll
+            for (int i = 0; i < w; i++) t[i] = t[2 * i] + t[2 * i + 1];
+        ss = t[0];
         s = 1.0f / sqrtf(ss / (float)K + a.eps);
     }
     auto one = [&](float4 v, float4 w, int c) {
@@ -292,64 +306,65 @@ static __device__ __forceinline__ void xpre_finish(const GemvArgs &a, const XPre
     if (XR > 0) {
 #pragma unroll
         for (int i = 0; i < XR; i++) {
-            const int c = tid + i * WG;
+            const int c = tid + i * GW;
             if (c < K / 4) one(p.x[i], p.w[NORM ? i : 0], c);
         }
     } else {
-        for (int c = tid; c < K / 4; c += WG) one(gx[c], NORM ? nw[c] : gx[c], c);
+        for (int c = tid; c < K / 4; c += GW) one(gx[c], NORM ? nw[c] : gx[c], c);
     }
     __syncthreads();
 }
 
-// One workgroup: tiles [tb, te) of segment `seg`, all of weight type T.
-// A step is one unit per lane for the R rows (x NM matrices) of a tile; the
-// weights of step s+P-1 are requested before step s is computed (a ring of
-// P register stages), the first P-1 right after the x loads.  When a row is
-// at most 64 units long (XU1) a lane's unit is the same in every step, and
-// its slice of x stays in registers for the whole workgroup.  Rows past the
-// end of the matrix are clamped to the last row (computed, not stored), so
-// the hot loop has no row branches.
-template <int T, int R, int NM, int P, int XR, bool XU1, bool NORM>
+// One workgroup: row tiles [tb, te) of segment `seg`, all of weight type T.
+// A tile is R rows per lane group x (64/lpr) groups: the rows one wave
+// computes together, in upl = U/lpr steps of one unit per lane (one step
+// when a row is at most 64 units long, XU1; then a lane's unit is the same
+// in every step and its slice of x stays in registers).  A wave starts with
+// tile `wave` and then takes the next free tile of the workgroup from the
+// LDS counter.  The weights of a step are requested before the previous step
+// is computed (two register stages); every pass issues the same loads (a
+// step past the end reads row 0's first units, unused), so the compiler
+// waits for exactly the stage it consumes.  Rows past the end of the matrix
+// are clamped to the last row (computed, not stored).
+template <int T, int R, int NM, int XR, bool XU1, bool NORM>
 static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int tb, int te, int wg,
                                                 const XPre<XR, NORM> &xp) {
     using W = typename Types<T>::W;
     using X = typename Types<T>::X;
     extern __shared__ u32x4 smem[];
-    __shared__ float red[WG / WAVE];
-    __shared__ int redi[WG / WAVE];
+    __shared__ float red[GNW];
+    __shared__ int redi[GNW];
+    __shared__ uint32_t tile_ctr;
     const int K = a.K, tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid / WAVE;
     const DMat &m0 = a.seg[seg].m;
     const DMat &m1 = a.seg[NM == 2 ? 1 : seg].m;
-    const int lpr = a.lpr, gpw = WAVE / lpr, grp = lane / lpr, j = lane & (lpr - 1);
+    const int lpr = a.lpr, grp = lane / lpr, j = lane & (lpr - 1);
     const int U = K >> 6, upl = XU1 ? 1 : U / lpr;
-    const int rows_m = m0.rows;
-    const int nsteps = (te - tb) * upl;
-    const int rbase = (wave * gpw + grp) * R;
+    const int rows_m = m0.rows, rpt = a.rows_per_wg;
+    const int ntl = te - tb;
+    const int rsub = grp * R;
 
-    // Every call issues the same loads: a step past the end reads row 0's
-    // first units (cached; the result is never used).  With no branch around
-    // the loads the compiler can count them, and waits for exactly the stage
-    // it consumes instead of for everything in flight.
-    W ring[P][NM][R];
-    auto issue = [&](int step, W (&w)[NM][R]) {
-        const bool live = step < nsteps;
-        const int tile = XU1 ? tb + step : tb + step / upl, u = XU1 ? j : j + (step % upl) * lpr;
+    W ring[2][NM][R];
+    auto issue = [&](int t, int ui, W (&w)[NM][R]) {
+        const bool live = t < ntl;
+        const int u = XU1 ? j : j + ui * lpr;
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            const int row = live ? min(tile * a.rows_per_wg + rbase + r, rows_m - 1) : 0;
+            const int row = live ? min((tb + t) * rpt + rsub + r, rows_m - 1) : 0;
             wload(m0, row, live ? u : j, w[0][r]);
             if (NM == 2) wload(m1, row, live ? u : j, w[NM - 1][r]);
         }
     };
-    // x was requested by the caller; the weights follow (loads return in order)
-#pragma unroll
-    for (int i = 0; i < P - 1; i++) issue(i, ring[i]);
+    // x was requested by the caller; the first weights follow (loads return in order)
+    int ct = wave, cu = 0;
+    issue(ct, cu, ring[0]);
     __builtin_amdgcn_sched_barrier(0);
 
     u32x4 *xhi = smem, *xmid = smem + K / 16, *xlo = smem + 2 * (K / 16);
     float *xs = (float *)(smem + 3 * (K / 16)), *s32 = xs + K / 32, *s16 = s32 + K / 32;
-    float *yo = s16 + K / 16;  // this workgroup's outputs, [tiles_per_wg * rows_per_wg]
-    const int wrow0 = tb * a.rows_per_wg, wrow1 = min(te * a.rows_per_wg, rows_m);
+    float *yo = s16 + K / 16;  // this workgroup's outputs
+    const int wrow0 = tb * rpt, wrow1 = min(te * rpt, rows_m);
+    if (tid == 0) tile_ctr = 0;  // read after the prologue's barriers
     xpre_finish<XR, NORM>(a, xp, xhi, xmid, xlo, xs, s32, s16, red);
     const XQ xq{xhi, xmid, xlo, xs, s32, s16};
     X xu;
@@ -363,25 +378,29 @@ static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int 
 #pragma unroll
         for (int r = 0; r < R; r++) acc[i][r] = 0.f;
 
-    // step `step` consumes ring slot k = step % P; with `issue` first the
-    // next P-1 stages stay in flight while this one is computed
-    auto do_step = [&](int step, int k, bool prefetch) {
-        if (prefetch) {
-            issue(step + P - 1, ring[(k + P - 1) % P]);
-            __builtin_amdgcn_sched_barrier(0);  // the loads go out before this step's arithmetic
+    // the step after (t, ui): the next unit of the tile, or the next free tile
+    auto next = [&](int t, int ui, int &nt, int &nu) {
+        if (ui + 1 < upl) {
+            nt = t;
+            nu = ui + 1;
+        } else {
+            uint32_t v = 0;
+            if (lane == 0) v = __hip_atomic_fetch_add(&tile_ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            nt = GNW + (int)__builtin_amdgcn_readfirstlane(v);
+            nu = 0;
         }
-        const int tile = XU1 ? tb + step : tb + step / upl, ui = XU1 ? 0 : step % upl;
-        const int u = j + ui * lpr;
-        const int row0 = tile * a.rows_per_wg + rbase;
+    };
+    auto compute = [&](int t, int ui, const W (&w)[NM][R]) {
+        const int u = XU1 ? j : j + ui * lpr;
         if (!XU1) xload(xq, u, xu);
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            acc[0][r] += wdot(ring[k][0][r], u, xu);
-            if (NM == 2) acc[NM - 1][r] += wdot(ring[k][NM - 1][r], u, xu);
+            acc[0][r] += wdot(w[0][r], u, xu);
+            if (NM == 2) acc[NM - 1][r] += wdot(w[NM - 1][r], u, xu);
         }
         if (XU1 || ui == upl - 1) {
-            // reduce over the lanes of the row; results go to LDS (no
-            // global memory traffic in the loop but the weight loads)
+            // reduce over the lanes of the row; results go to LDS (no global
+            // memory traffic in the loop but the weight loads)
 #pragma unroll
             for (int r = 0; r < R; r++) {
                 acc[0][r] = lane_group_sum(acc[0][r], lpr);
@@ -390,7 +409,7 @@ static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int 
             if (j == 0) {
 #pragma unroll
                 for (int r = 0; r < R; r++) {
-                    const int row = row0 + r;
+                    const int row = (tb + t) * rpt + rsub + r;
                     float val = acc[0][r];
                     if (NM == 2) {  // infer/forward.odin:188-193
 #pragma clang fp contract(off)
@@ -410,23 +429,29 @@ static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int 
                 for (int r = 0; r < R; r++) acc[i][r] = 0.f;
         }
     };
-    // whole groups of P steps, then the rest without prefetch: no loop exit
-    // in the middle of a group, so every pass through the loop has the same
-    // loads in flight and the compiler waits for exactly one stage
-    const int nfull = nsteps / P;
-    for (int c = 0; c < nfull; c++) {
-#pragma unroll
-        for (int k = 0; k < P; k++) do_step(c * P + k, k, true);
+    // two steps per pass, so the ring stage of each step is static
+    while (ct < ntl) {
+        int nt, nu;
+        next(ct, cu, nt, nu);
+        issue(nt, nu, ring[1]);
+        __builtin_amdgcn_sched_barrier(0);  // the loads go out before this step's arithmetic
+        compute(ct, cu, ring[0]);
+        ct = nt;
+        cu = nu;
+        if (ct >= ntl) break;
+        next(ct, cu, nt, nu);
+        issue(nt, nu, ring[0]);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(ct, cu, ring[1]);
+        ct = nt;
+        cu = nu;
     }
-#pragma unroll
-    for (int k = 0; k < P - 1; k++)
-        if (nfull * P + k < nsteps) do_step(nfull * P + k, k, false);
 
     // write back the workgroup's contiguous rows (coalesced)
     __syncthreads();
     {
         float *y = a.seg[seg].y;
-        for (int i = tid; i < wrow1 - wrow0; i += WG) {
+        for (int i = tid; i < wrow1 - wrow0; i += GW) {
             if (NM == 1 && a.mode == GEMV_ADD) y[wrow0 + i] = y[wrow0 + i] + yo[i];
             else y[wrow0 + i] = yo[i];
         }
@@ -447,7 +472,7 @@ static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int 
         }
         __syncthreads();
         if (tid == 0) {
-            for (int w = 1; w < WG / WAVE; w++)
+            for (int w = 1; w < GNW; w++)
                 if (better(red[w], redi[w], bv, bi)) {
                     bv = red[w];
                     bi = redi[w];
@@ -465,8 +490,8 @@ static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int 
 // count the loads in flight, so it waits for all of them; the two arms here
 // issue their x loads in different orders so that they are not merged.  Other
 // type mixes are issued as one launch per type (wg_base).
-template <int T, int TL, int R, int NM, int P, int XR, bool XU1, bool NORM>
-__global__ __launch_bounds__(WG) void gemv_q_kernel(GemvArgs a) {
+template <int T, int TL, int R, int NM, int XR, bool XU1, bool NORM>
+__global__ __launch_bounds__(GW) void gemv_q_kernel(GemvArgs a) {
     const int wg = blockIdx.x + a.wg_base;
     int seg = 0;
     if (NM == 1) {
@@ -481,89 +506,72 @@ __global__ __launch_bounds__(WG) void gemv_q_kernel(GemvArgs a) {
         XPre<XR, NORM> xp;
         xpre_load<XR, NORM, true>(a, xp);  // x first, then the weights (loads return in order)
         __builtin_amdgcn_sched_barrier(0);  // keep every x load ahead of the weight loads
-        gemv_run<TL, R, NM, P, XR, XU1, NORM>(a, seg, tb, te, wg, xp);
+        gemv_run<TL, R, NM, XR, XU1, NORM>(a, seg, tb, te, wg, xp);
     } else {
         XPre<XR, NORM> xp;
         xpre_load<XR, NORM>(a, xp);
         __builtin_amdgcn_sched_barrier(0);
-        gemv_run<T, R, NM, P, XR, XU1, NORM>(a, seg, tb, te, wg, xp);
+        gemv_run<T, R, NM, XR, XU1, NORM>(a, seg, tb, te, wg, xp);
     }
 }
 
-// kernel configurations: (R, NM, P, XR, XU1); XR = float4 of x per thread
-// held in registers by the prologue (K <= 1024 * XR), 0 = x read twice from
+// kernel configurations: (R, NM, XR, XU1); XR = float4 of x per thread held
+// in registers by the prologue (K <= 4 * GW * XR), 0 = x read twice from
 // memory; XU1 = one unit per lane per row (K <= 4096), x kept in registers
-#ifndef OI_GEMV_R
-#define OI_GEMV_R 2
-#endif
-#ifndef OI_GEMV_P
-#define OI_GEMV_P 2
-#endif
-#ifndef OI_GEMV_XREG
-#define OI_GEMV_XREG 1
-#endif
-constexpr int R_MAIN = OI_GEMV_R, R_SWIGLU = 1, P_MAIN = OI_GEMV_P;  // measured best: R=2, P=2
-constexpr bool XREG = OI_GEMV_XREG != 0;
-template <int T, bool NORM>
-static const void *gemv_q_fn_t(bool swiglu, bool xu1, int K) {
+template <int T, int R, bool NORM>
+static const void *gemv_q_fn_r(bool swiglu, bool xu1, int K) {
     if (swiglu) {
-        if (K <= 4096 && xu1) return (const void *)gemv_q_kernel<T, T, R_SWIGLU, 2, P_MAIN, 4, true, NORM>;
-        if (K <= 4096) return (const void *)gemv_q_kernel<T, T, R_SWIGLU, 2, P_MAIN, 4, false, NORM>;
-        return (const void *)gemv_q_kernel<T, T, R_SWIGLU, 2, P_MAIN, 0, false, NORM>;
+        if (K <= 4096 && xu1) return (const void *)gemv_q_kernel<T, T, 1, 2, 1, true, NORM>;
+        if (K <= 4096) return (const void *)gemv_q_kernel<T, T, 1, 2, 1, false, NORM>;
+        return (const void *)gemv_q_kernel<T, T, 1, 2, 0, false, NORM>;
     }
-    if (K <= 4096 && xu1) return (const void *)gemv_q_kernel<T, T, R_MAIN, 1, P_MAIN, 4, true, NORM>;
-    if (K <= 4096) return (const void *)gemv_q_kernel<T, T, R_MAIN, 1, P_MAIN, 4, false, NORM>;
-    if (K <= 12288) return (const void *)gemv_q_kernel<T, T, R_MAIN, 1, P_MAIN, 12, false, NORM>;
-    return (const void *)gemv_q_kernel<T, T, R_MAIN, 1, P_MAIN, 0, false, NORM>;
+    if (K <= 4096 && xu1) return (const void *)gemv_q_kernel<T, T, R, 1, 1, true, NORM>;
+    if (K <= 4096) return (const void *)gemv_q_kernel<T, T, R, 1, 1, false, NORM>;
+    if (K <= 12288) return (const void *)gemv_q_kernel<T, T, R, 1, 3, false, NORM>;
+    return (const void *)gemv_q_kernel<T, T, R, 1, 0, false, NORM>;
+}
+template <int T, bool NORM>
+static const void *gemv_q_fn_t(bool swiglu, bool xu1, int K, int R) {
+    return R == 1 ? gemv_q_fn_r<T, 1, NORM>(swiglu, xu1, K) : nullptr;
 }
 // two-type kernels (first segments T, last segment TL; RMSNorm prologue,
 // K <= 4096): the projection GEMVs of a layer
 template <int T, int TL>
-static const void *gemv_q_fn_mixed(bool xu1, int K) {
-    if (K > 4096) return nullptr;
-    if (xu1) return (const void *)gemv_q_kernel<T, TL, R_MAIN, 1, P_MAIN, 4, true, true>;
-    return (const void *)gemv_q_kernel<T, TL, R_MAIN, 1, P_MAIN, 4, false, true>;
+static const void *gemv_q_fn_mixed(bool xu1, int K, int R) {
+    if (K > 4096 || R != 1) return nullptr;
+    if (xu1) return (const void *)gemv_q_kernel<T, TL, 1, 1, 1, true, true>;
+    return (const void *)gemv_q_kernel<T, TL, 1, 1, 1, false, true>;
 }
-static const void *gemv_q_fn_mixed(int t, int tl, bool norm, int K) {
+static bool xu1_of(int K) {
     const int U = K / 64;
-    const bool xu1 = XREG && U <= 64 && (U & (U - 1)) == 0;
+    return U <= 64 && (U & (U - 1)) == 0;  // one unit per lane per row
+}
+static const void *gemv_q_fn_mixed(int t, int tl, bool norm, int K, int R) {
+    const bool xu1 = xu1_of(K);
     if (!norm) return nullptr;
-    if (t == T_Q4_K && tl == T_Q6_K) return gemv_q_fn_mixed<T_Q4_K, T_Q6_K>(xu1, K);
-    if (t == T_Q6_K && tl == T_Q4_K) return gemv_q_fn_mixed<T_Q6_K, T_Q4_K>(xu1, K);
-    if (t == T_Q4_K && tl == T_Q8_0) return gemv_q_fn_mixed<T_Q4_K, T_Q8_0>(xu1, K);
-    if (t == T_Q8_0 && tl == T_Q4_K) return gemv_q_fn_mixed<T_Q8_0, T_Q4_K>(xu1, K);
-    if (t == T_Q8_0 && tl == T_Q6_K) return gemv_q_fn_mixed<T_Q8_0, T_Q6_K>(xu1, K);
-    if (t == T_Q6_K && tl == T_Q8_0) return gemv_q_fn_mixed<T_Q6_K, T_Q8_0>(xu1, K);
+    if (t == T_Q4_K && tl == T_Q6_K) return gemv_q_fn_mixed<T_Q4_K, T_Q6_K>(xu1, K, R);
+    if (t == T_Q6_K && tl == T_Q4_K) return gemv_q_fn_mixed<T_Q6_K, T_Q4_K>(xu1, K, R);
+    if (t == T_Q4_K && tl == T_Q8_0) return gemv_q_fn_mixed<T_Q4_K, T_Q8_0>(xu1, K, R);
+    if (t == T_Q8_0 && tl == T_Q4_K) return gemv_q_fn_mixed<T_Q8_0, T_Q4_K>(xu1, K, R);
+    if (t == T_Q8_0 && tl == T_Q6_K) return gemv_q_fn_mixed<T_Q8_0, T_Q6_K>(xu1, K, R);
+    if (t == T_Q6_K && tl == T_Q8_0) return gemv_q_fn_mixed<T_Q6_K, T_Q8_0>(xu1, K, R);
     return nullptr;
 }
-static const void *gemv_q_fn(int type, bool swiglu, bool norm, int K) {
-    // one unit per lane per row when the row's unit count is a power of two <= 64
-    const int U = K / 64;
-    const bool xu1 = XREG && U <= 64 && (U & (U - 1)) == 0;
+static const void *gemv_q_fn(int type, bool swiglu, bool norm, int K, int R) {
+    const bool xu1 = xu1_of(K);
     switch (type) {
-    case T_Q4_K: return norm ? gemv_q_fn_t<T_Q4_K, true>(swiglu, xu1, K) : gemv_q_fn_t<T_Q4_K, false>(swiglu, xu1, K);
-    case T_Q6_K: return norm ? gemv_q_fn_t<T_Q6_K, true>(swiglu, xu1, K) : gemv_q_fn_t<T_Q6_K, false>(swiglu, xu1, K);
-    default: return norm ? gemv_q_fn_t<T_Q8_0, true>(swiglu, xu1, K) : gemv_q_fn_t<T_Q8_0, false>(swiglu, xu1, K);
+    case T_Q4_K: return norm ? gemv_q_fn_t<T_Q4_K, true>(swiglu, xu1, K, R) : gemv_q_fn_t<T_Q4_K, false>(swiglu, xu1, K, R);
+    case T_Q6_K: return norm ? gemv_q_fn_t<T_Q6_K, true>(swiglu, xu1, K, R) : gemv_q_fn_t<T_Q6_K, false>(swiglu, xu1, K, R);
+    default: return norm ? gemv_q_fn_t<T_Q8_0, true>(swiglu, xu1, K, R) : gemv_q_fn_t<T_Q8_0, false>(swiglu, xu1, K, R);
     }
-}
-
-static int resident_wgs(const void *fn, size_t lds) {
-    struct Entry { const void *fn; size_t lds; int n; };
-    static Entry cache[16];
-    static int ncache = 0;
-    for (int i = 0; i < ncache; i++)
-        if (cache[i].fn == fn && cache[i].lds == lds) return cache[i].n;
-    int per_cu = 0, cus = 256, dev = 0;
-    hipGetDevice(&dev);
-    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, WG, lds) != hipSuccess || per_cu < 1) per_cu = 1;
-    if (ncache < 16) cache[ncache++] = {fn, lds, per_cu * cus};
-    return per_cu * cus;
 }
 
 static size_t gemv_q_lds(int K, int out_rows) {
     return (size_t)K / 16 * 48 + (size_t)K / 32 * 8 + (size_t)K / 16 * 4 + (size_t)out_rows * 4;
 }
+
+// rows per lane group of a plan (the kernel's R)
+static int plan_r(const GemvArgs &a) { return a.rows_per_wg / (64 / a.lpr); }
 
 // One launch when the segments are of one type, or of one type but the
 // last; otherwise one launch per run of consecutive segments of one type.
@@ -572,8 +580,8 @@ static const void *gemv_q_fn_all(const GemvArgs &a) {
     for (int i = 1; i < a.nseg - 1; i++)
         if (a.seg[i].m.type != a.seg[0].m.type) return nullptr;
     const int t = a.seg[0].m.type, tl = a.seg[a.nseg - 1].m.type;
-    if (tl == t) return gemv_q_fn(t, false, a.norm_w != nullptr, a.K);
-    return gemv_q_fn_mixed(t, tl, a.norm_w != nullptr, a.K);
+    if (tl == t) return gemv_q_fn(t, false, a.norm_w != nullptr, a.K, plan_r(a));
+    return gemv_q_fn_mixed(t, tl, a.norm_w != nullptr, a.K, plan_r(a));
 }
 
 bool gemv_q_supported(const GemvArgs &a) {
@@ -583,46 +591,72 @@ bool gemv_q_supported(const GemvArgs &a) {
         if (t != T_Q4_K && t != T_Q6_K && t != T_Q8_0) return false;
     }
     if (a.mode == GEMV_SWIGLU && a.seg[0].m.type != a.seg[1].m.type) return false;
+    // the x prologue holds K/16 chunks of three planes in LDS
+    if (gemv_q_lds(a.K, 0) > 96 * 1024) return false;
     return a.K % 256 == 0 || (a.K % 64 == 0 && a.seg[0].m.type == T_Q8_0 && n == 1);
 }
 
-// Plan for gemv_q_kernel: workgroups spread over the segments in proportion
-// to their tiles, each with a whole number of tiles, no more workgroups than
-// can be resident at once.
+static int device_cus() {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+    }
+    return cus;
+}
+
+static double weight_bytes(int type) { return type == T_Q4_K ? 0.5625 : type == T_Q6_K ? 0.8203125 : 1.0625; }
+
+// Plan for gemv_q_kernel: one workgroup per CU.  A tile is the rows of one
+// wave (64/lpr lane groups x R rows).  Workgroups go to the segments in
+// proportion to their bytes, each with a contiguous range of tiles of one
+// segment.
 void plan_gemv_q(GemvArgs &a) {
     const int U = a.K / 64;
     int lpr = 1;
     while (lpr < 64 && U % (lpr * 2) == 0) lpr *= 2;
     a.lpr = lpr;
     const bool sw = a.mode == GEMV_SWIGLU;
-    const int gpw = 64 / lpr, R = sw ? R_SWIGLU : R_MAIN;
-    a.rows_per_wg = 4 * gpw * R;
+    const int gpw = 64 / lpr, G = device_cus();
     const int nseg = sw ? 1 : a.nseg;
+    long rows = 0;
+    for (int i = 0; i < nseg; i++) rows += a.seg[i].m.rows;
+    // (R = 2 measured no faster and does not fit 128 registers for every type)
+    const int R = 1;
+    (void)rows;
+    a.rows_per_wg = gpw * R;
+    double bytes[3], total = 0;
     long total_tiles = 0;
     for (int i = 0; i < nseg; i++) {
         a.seg[i].ntiles = (a.seg[i].m.rows + a.rows_per_wg - 1) / a.rows_per_wg;
         total_tiles += a.seg[i].ntiles;
+        bytes[i] = (double)a.seg[i].m.rows * a.K * weight_bytes(a.seg[i].m.type);
+        total += bytes[i];
     }
-    // resident capacity of the slowest-occupancy kernel of the launch (the
-    // output buffer is sized for one tile here, which the check below keeps)
-    long slots = LONG_MAX;
-    const void *fall = gemv_q_fn_all(a);
-    for (int i = 0; i < nseg; i++) {
-        const void *fn = fall ? fall : gemv_q_fn(a.seg[i].m.type, sw, a.norm_w != nullptr, a.K);
-        slots = std::min(slots, (long)resident_wgs(fn, gemv_q_lds(a.K, a.rows_per_wg * 4)));
-    }
-    long k = (total_tiles + slots - 1) / slots;  // tiles per workgroup
-    int wg = 0;
+    // at least one workgroup per segment, at most one tile per wave short of a full workgroup
+    const int nwg = (int)std::max<long>(nseg, std::min<long>(G, (total_tiles + GNW - 1) / GNW));
+    int wg = 0, left = nwg;
     for (int i = 0; i < nseg; i++) {
         a.seg[i].wg_begin = wg;
-        wg += (int)((a.seg[i].ntiles + k - 1) / k);
+        int n = i == nseg - 1 ? left : (int)std::lround(nwg * bytes[i] / total);
+        n = std::max(1, std::min(n, left - (nseg - 1 - i)));
+        wg += n;
+        left -= n;
     }
     if (sw) {
         a.seg[1].wg_begin = 0;
         a.seg[1].ntiles = a.seg[0].ntiles;
     }
     a.total_wgs = wg;
-    a.tiles_per_wg = (int)k;
+    int most = 0;
+    for (int i = 0; i < nseg; i++) {
+        const int end = i + 1 < nseg ? a.seg[i + 1].wg_begin : wg;
+        const int n = end - a.seg[i].wg_begin;
+        most = std::max(most, (a.seg[i].ntiles + n - 1) / n);
+    }
+    a.tiles_per_wg = most;
     a.kernel = 1;
 }
 
@@ -630,11 +664,12 @@ hipError_t launch_gemv_q(const GemvArgs &a, hipStream_t st) {
     const bool sw = a.mode == GEMV_SWIGLU;
     const int nseg = sw ? 1 : a.nseg;
     const size_t lds = gemv_q_lds(a.K, a.tiles_per_wg * a.rows_per_wg);
+    const int R = plan_r(a);
     if (const void *fn = gemv_q_fn_all(a)) {
         GemvArgs b = a;
         b.wg_base = 0;
         void *args[] = {(void *)&b};
-        return hipLaunchKernel(fn, dim3(a.total_wgs), dim3(WG), args, lds, st);
+        return hipLaunchKernel(fn, dim3(a.total_wgs), dim3(GW), args, lds, st);
     }
     for (int i = 0; i < nseg;) {
         int j = i + 1;
@@ -642,9 +677,9 @@ hipError_t launch_gemv_q(const GemvArgs &a, hipStream_t st) {
         GemvArgs b = a;
         b.wg_base = a.seg[i].wg_begin;
         const int end = j < nseg ? a.seg[j].wg_begin : a.total_wgs;
-        const void *fn = gemv_q_fn(a.seg[i].m.type, sw, a.norm_w != nullptr, a.K);
+        const void *fn = gemv_q_fn(a.seg[i].m.type, sw, a.norm_w != nullptr, a.K, R);
         void *args[] = {(void *)&b};
-        const hipError_t e = hipLaunchKernel(fn, dim3(end - b.wg_base), dim3(WG), args, lds, st);
+        const hipError_t e = hipLaunchKernel(fn, dim3(end - b.wg_base), dim3(GW), args, lds, st);
         if (e != hipSuccess) return e;
         i = j;
     }
