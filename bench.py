@@ -85,6 +85,73 @@ def cpu_baseline(path, k, v, cfg, gpu_tokens, budget_s):
         r.close()
 
 
+PEAK_F16_TFLOPS = 2500.0  # MI355X dense f16 MFMA
+
+
+def prefill_gemm(iters=50):
+    """Batched projection (oi_gemm_launch, the prefill GEMM on the matrix cores)
+    at the reference harness's projection shapes with 64 tokens: weights
+    resident in HBM, f16 activations, f32 output; mean launch time from HIP
+    events on the null stream (the stream of the launches) over `iters`
+    back-to-back launches.  Device buffers and events come from the HIP runtime
+    the library itself is linked against (libamdhip64)."""
+    import ctypes
+    import numpy as np
+    from oi import ggml
+    hip = ctypes.CDLL("libamdhip64.so")
+    vp = ctypes.c_void_p
+
+    def ok(rc, what):
+        if rc != 0:
+            raise RuntimeError("%s failed (%d)" % (what, rc))
+
+    rng = np.random.default_rng(7)
+    out = []
+    for kind, m, k in ((12, 4096, 4096), (12, 12288, 4096), (14, 4096, 12288)):
+        n = 64
+        e, b = {12: (256, 144), 14: (256, 210)}[kind]
+        nb = m * (k // e)
+        raw = rng.integers(0, 256, size=(nb, b), dtype=np.uint8)
+        d = (rng.random(nb) * 0.18 + 0.02).astype(np.float16).view(np.uint8).reshape(nb, 2)
+        if kind == 12:
+            raw[:, 0:2] = d
+            raw[:, 2:4] = (rng.random(nb) * 0.05).astype(np.float16).view(np.uint8).reshape(nb, 2)
+        else:
+            raw[:, 208:210] = d
+        w = ggml.DeviceWeights(kind, raw.reshape(-1), m, k)
+        xh = np.ascontiguousarray(rng.uniform(-1, 1, size=(n, k)).astype(np.float16))
+        x, c = vp(), vp()
+        ok(hip.hipMalloc(ctypes.byref(x), ctypes.c_size_t(xh.nbytes)), "hipMalloc")
+        ok(hip.hipMalloc(ctypes.byref(c), ctypes.c_size_t(n * m * 4)), "hipMalloc")
+        ok(hip.hipMemcpy(x, xh.ctypes.data_as(vp), ctypes.c_size_t(xh.nbytes), 1), "hipMemcpy")
+        e0, e1 = vp(), vp()
+        ok(hip.hipEventCreate(ctypes.byref(e0)), "hipEventCreate")
+        ok(hip.hipEventCreate(ctypes.byref(e1)), "hipEventCreate")
+        for _ in range(3):
+            w.launch_gemm(x.value, n, c.value)
+        ok(hip.hipDeviceSynchronize(), "hipDeviceSynchronize")
+        ok(hip.hipEventRecord(e0, None), "hipEventRecord")
+        for _ in range(iters):
+            w.launch_gemm(x.value, n, c.value)
+        ok(hip.hipEventRecord(e1, None), "hipEventRecord")
+        ok(hip.hipEventSynchronize(e1), "hipEventSynchronize")
+        ms = ctypes.c_float()
+        ok(hip.hipEventElapsedTime(ctypes.byref(ms), e0, e1), "hipEventElapsedTime")
+        us = ms.value * 1000.0 / iters
+        hip.hipEventDestroy(e0)
+        hip.hipEventDestroy(e1)
+        hip.hipFree(x)
+        hip.hipFree(c)
+        flops = 2.0 * m * n * k
+        byts = w.nbytes + n * k * 2 + n * m * 4
+        out.append({"type": "Q4_K" if kind == 12 else "Q6_K", "rows": m, "cols": k, "tokens": n,
+                    "avg_us": round(us, 3), "TFLOPs": round(flops / us / 1e6, 1),
+                    "frac_f16_peak": round(flops / us / 1e6 / PEAK_F16_TFLOPS, 4),
+                    "GBps": round(byts / us / 1e3, 1), "frac_hbm_peak": round(byts / us / 1e3 / PEAK_HBM_GBPS, 4)})
+        w.free()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -93,6 +160,7 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--model-path", default=None, help="reuse an existing synthetic GGUF")
+    ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM measurement")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (3 times), to calibrate HBM counters")
     args = ap.parse_args()
@@ -169,6 +237,12 @@ def main():
             with open(traffic_file) as f:
                 roofline["traffic"] = json.load(f).get("traffic_bytes_per_launch")
 
+        gemm = None
+        if not args.no_gemm:
+            gemm = prefill_gemm()
+            log("prefill GEMM: " + ", ".join("%s %dx64x%d %.1f us %.0f TFLOP/s" % (
+                g["type"], g["rows"], g["cols"], g["avg_us"], g["TFLOPs"]) for g in gemm))
+
         cpu = None
         if not args.no_cpu:
             log("CPU baseline (oracle) for up to %.0fs ..." % args.cpu_budget)
@@ -191,6 +265,7 @@ def main():
                            "roofline_tok_s": round(PEAK_HBM_GBPS * 1e9 / bpt, 1)},
             "kernels": {n: {"avg_us": round(d["us"], 3), "GBps": round(d["GBps"], 1)} for n, d in kern.items()},
             "cpu_baseline": cpu,
+            "prefill_gemm": gemm,
         }
         print(json.dumps(out), flush=True)
         infer.engine_destroy(e)

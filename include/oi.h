@@ -153,6 +153,19 @@ int oi_gemv_launch(const oi_weights *w, const float *x_dev, float *y_dev, void *
 int oi_gemv(int32_t type, const void *host_blocks, int64_t rows, int64_t cols, const float *x,
             float *y);
 
+/* Batched projection for prefill: the reference's MMQ kernels
+ * (qwen3_5/metal.odin:493-609 gemm_q4k_f32 / gemm_q6k_f32; gemm_harness/
+ * gemm_test.odin:97-135, 297-337): c[t][r] = sum_k f16(dequant(W)[r][k]) * x[t][k]
+ * for n tokens, f32 accumulation, on the matrix cores.  x_dev: n x cols f16
+ * (token-major), c_dev: n x rows f32 (token-major) -- the transposes of the
+ * harness's B[K][N] and C[M][N].  Types Q4_K, Q6_K (cols % 256 == 0), Q8_0
+ * (cols % 64 == 0).  Enqueued on `stream`. */
+int oi_gemm_launch(const oi_weights *w, const uint16_t *x_dev, int32_t n, float *c_dev, void *stream);
+
+/* Host-memory convenience form of oi_gemm_launch (synchronous). */
+int oi_gemm(int32_t type, const void *host_blocks, int64_t rows, int64_t cols, const uint16_t *x, int32_t n,
+            float *c);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1109,6 +1109,39 @@ int oi_gemv_launch(const oi_weights *w, const float *x_dev, float *y_dev, void *
     return OI_OK;
 }
 
+int oi_gemm_launch(const oi_weights *w, const uint16_t *x_dev, int32_t n, float *c_dev, void *stream) {
+    if (!w || !x_dev || !c_dev) return fail(OI_E_ARG, "null argument");
+    if (n <= 0) return fail(OI_E_ARG, "n must be positive");
+    if (!gemm_supported(w->m)) return fail(OI_E_UNSUPPORTED, "type / row length not supported by the GEMM kernel");
+    hipError_t r = launch_gemm(w->m, x_dev, n, c_dev, (hipStream_t)stream);
+    if (r != hipSuccess) return fail(OI_E_DEVICE, std::string("gemm launch: ") + hipGetErrorString(r));
+    return OI_OK;
+}
+
+int oi_gemm(int32_t type, const void *host_blocks, int64_t rows, int64_t cols, const uint16_t *x, int32_t n,
+            float *c) {
+    if (!x || !c) return fail(OI_E_ARG, "null argument");
+    if (n <= 0) return fail(OI_E_ARG, "n must be positive");
+    oi_weights *w = nullptr;
+    int rc = oi_weights_upload(type, host_blocks, rows, cols, &w);
+    if (rc) return rc;
+    uint16_t *dx = nullptr;
+    float *dc = nullptr;
+    hipError_t r = hipMalloc(&dx, (size_t)n * cols * 2);
+    if (r == hipSuccess) r = hipMalloc(&dc, (size_t)n * rows * 4);
+    if (r == hipSuccess) r = hipMemcpy(dx, x, (size_t)n * cols * 2, hipMemcpyHostToDevice);
+    if (r == hipSuccess) {
+        rc = oi_gemm_launch(w, dx, n, dc, nullptr);
+        if (!rc) r = hipMemcpy(c, dc, (size_t)n * rows * 4, hipMemcpyDeviceToHost);
+    }
+    if (dx) hipFree(dx);
+    if (dc) hipFree(dc);
+    oi_weights_free(w);
+    if (rc) return rc;
+    if (r != hipSuccess) return fail(OI_E_DEVICE, std::string("gemm: ") + hipGetErrorString(r));
+    return OI_OK;
+}
+
 int oi_gemv(int32_t type, const void *host_blocks, int64_t rows, int64_t cols, const float *x, float *y) {
     if (!x || !y) return fail(OI_E_ARG, "null argument");
     oi_weights *w = nullptr;

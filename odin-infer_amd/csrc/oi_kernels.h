@@ -114,4 +114,8 @@ bool gemv_q_supported(const GemvArgs &a);
 void plan_gemv_q(GemvArgs &a);
 hipError_t launch_gemv_q(const GemvArgs &a, hipStream_t st);
 
+// gemm.hip: batched projection c[t][r] = sum_k f16(deq(W))[r][k] x[t][k]
+bool gemm_supported(const DMat &m);
+hipError_t launch_gemm(const DMat &m, const uint16_t *x, int32_t n, float *c, hipStream_t st);
+
 }  // namespace oi

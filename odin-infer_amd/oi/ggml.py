@@ -68,6 +68,18 @@ def gemv(kind, w_blocks, rows, cols, x):
     return y
 
 
+def gemm(kind, w_blocks, rows, cols, x16):
+    """Batched projection on the matrix cores (host in, host out):
+    c[t][r] = sum_k f16(dequant(W)[r][k]) * x16[t][k], f32 accumulation.
+    x16: uint16 (f16 bits) [n][cols] -> float32 [n][rows]."""
+    w = np.ascontiguousarray(w_blocks, np.uint8)
+    x = np.ascontiguousarray(x16, np.uint16)
+    n = x.shape[0]
+    c = np.empty((n, rows), np.float32)
+    check(_native.hip().oi_gemm(int(kind), w.ctypes.data, int(rows), int(cols), x.ctypes.data, int(n), c.ctypes.data))
+    return c
+
+
 class DeviceWeights:
     """A matrix resident in HBM in the GEMV layout (oi_weights_upload)."""
 
@@ -81,6 +93,9 @@ class DeviceWeights:
 
     def launch(self, x_dev_ptr, y_dev_ptr, stream=None):
         check(_native.hip().oi_gemv_launch(self.h, x_dev_ptr, y_dev_ptr, stream))
+
+    def launch_gemm(self, x_dev_ptr, n, c_dev_ptr, stream=None):
+        check(_native.hip().oi_gemm_launch(self.h, x_dev_ptr, int(n), c_dev_ptr, stream))
 
     def free(self):
         if self.h:

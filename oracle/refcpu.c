@@ -32,6 +32,10 @@
  *   ref_argmax            ties go to the lowest index (sampler/sampler.odin:79-89)
  *   forward               float64 re-computation of one layer on a tiny model;
  *                         position-0 attention identity; committed logits fixture
+ *   ref_gemm_f16          batched prefill projection: all-ones / identity / row-
+ *                         and column-distinct ladder (gemm_harness/gemm_test.odin
+ *                         :1058-1067) with closed-form results; numpy float64
+ *                         matmul of the f16-rounded dequantized rows
  * Bit-level equality with the Odin binary (its simd/libm lowering) stays
  * unpinned: parity is stated at tolerance level (1e-3) and greedy ids.
  */
@@ -992,3 +996,42 @@ EXPORT const float *ref_engine_forward(void *h, int token, int pos) {
 
 /* Hidden state after the final norm (test hook for layer-level checks). */
 EXPORT const float *ref_engine_hidden(void *h) { return ((ref_engine *)h)->x; }
+
+/* Batched prefill projection as the reference's MMQ kernels compute it
+ * (gemm_harness/gemm_test.odin:97-135 gemm_q4k_f32, :297-337 gemm_q6k_f32,
+ * qwen3_5/metal.odin:493-609): each weight row is dequantized (ggml/quant.odin,
+ * dequant_row), rounded to f16 (the kernels stage A in half), multiplied by f16
+ * activations and summed; the sum is taken in float64 here, as the harness's
+ * CPU reference does (gemm_test.odin:838-851), so the GPU's f32 accumulation
+ * is compared against the exact product of the staged operands.
+ * x: [n][k] f16 bits (token-major), c: [n][m] (token-major). */
+EXPORT int ref_gemm_f16(int kind, const uint8_t *w, int64_t m, int64_t k, const uint16_t *x, int64_t n,
+                        double *c) {
+    const int64_t rb = ref_row_byte_size(kind, k);
+    if (rb <= 0) {
+        snprintf(g_err, sizeof g_err, "gemm: unsupported type %d or row length %lld", kind, (long long)k);
+        return -1;
+    }
+    float *row = malloc((size_t)k * sizeof(float));
+    double *xd = malloc((size_t)(n * k) * sizeof(double));
+    if (!row || !xd) {
+        free(row);
+        free(xd);
+        snprintf(g_err, sizeof g_err, "gemm: out of memory");
+        return -1;
+    }
+    for (int64_t i = 0; i < n * k; i++) xd[i] = ref_f16_to_f32(x[i]);
+    for (int64_t r = 0; r < m; r++) {
+        ref_dequant_row(kind, w + r * rb, k, row);
+        for (int64_t j = 0; j < k; j++) row[j] = ref_f16_to_f32(ref_f32_to_f16(row[j]));
+        for (int64_t t = 0; t < n; t++) {
+            const double *xt = xd + t * k;
+            double s = 0.0;
+            for (int64_t j = 0; j < k; j++) s += (double)row[j] * xt[j];
+            c[t * m + r] = s;
+        }
+    }
+    free(row);
+    free(xd);
+    return 0;
+}

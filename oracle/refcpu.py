@@ -53,6 +53,7 @@ def lib():
         L.ref_engine_kv_fill.argtypes = [c_vp, c_int, c_int, c_int, c_vp, c_vp]
         L.ref_engine_hidden.restype = ctypes.POINTER(c_f)
         L.ref_engine_hidden.argtypes = [c_vp]
+        L.ref_gemm_f16.argtypes = [c_int, c_vp, c_i64, c_i64, c_vp, c_i64, c_vp]
         _lib = L
     return _lib
 
@@ -85,6 +86,18 @@ def matmul_t(w_blocks, kind, x, d, nthreads=1):
     out = np.empty(d, np.float32)
     rc = lib().ref_matmul_t(_p(out), _p(x), kind, _p(w), len(x), d, nthreads)
     if rc:
+        raise RuntimeError(lib().ref_last_error().decode())
+    return out
+
+
+def gemm_f16(w_blocks, kind, m, k, x16):
+    """C[t][r] = sum_j f16(dequant(W)[r][j]) * x16[t][j] in float64 (x16: uint16 [n][k])."""
+    w = np.ascontiguousarray(np.frombuffer(bytes(w_blocks), np.uint8) if not isinstance(w_blocks, np.ndarray)
+                             else w_blocks.view(np.uint8))
+    x = np.ascontiguousarray(x16, np.uint16)
+    n = x.shape[0]
+    out = np.zeros((n, m), np.float64)
+    if lib().ref_gemm_f16(kind, _p(w), m, k, _p(x), n, _p(out)) != 0:
         raise RuntimeError(lib().ref_last_error().decode())
     return out
 
