@@ -91,10 +91,12 @@ PEAK_F16_TFLOPS = 2500.0  # MI355X dense f16 MFMA
 def prefill_gemm(iters=50):
     """Batched projection (oi_gemm_launch, the prefill GEMM on the matrix cores)
     at the reference harness's projection shapes with 64 tokens: weights
-    resident in HBM, f16 activations, f32 output; mean launch time from HIP
-    events on the null stream (the stream of the launches) over `iters`
-    back-to-back launches.  Device buffers and events come from the HIP runtime
-    the library itself is linked against (libamdhip64)."""
+    resident in HBM, f16 activations, f32 output.  `iters` launches (the K-split
+    kernel and, when K is split, the reduction of the partial products) are
+    captured in one HIP graph, so that the time is the device's and not the
+    Python launch loop's; mean time per projection from HIP events around the
+    graph launch.  Device buffers, streams, graphs and events come from the HIP
+    runtime the library itself is linked against (libamdhip64)."""
     import ctypes
     import numpy as np
     from oi import ggml
@@ -120,28 +122,44 @@ def prefill_gemm(iters=50):
             raw[:, 208:210] = d
         w = ggml.DeviceWeights(kind, raw.reshape(-1), m, k)
         xh = np.ascontiguousarray(rng.uniform(-1, 1, size=(n, k)).astype(np.float16))
-        x, c = vp(), vp()
+        wsb = w.gemm_workspace_bytes(n)
+        x, c, ws, st = vp(), vp(), vp(), vp()
         ok(hip.hipMalloc(ctypes.byref(x), ctypes.c_size_t(xh.nbytes)), "hipMalloc")
         ok(hip.hipMalloc(ctypes.byref(c), ctypes.c_size_t(n * m * 4)), "hipMalloc")
+        if wsb:
+            ok(hip.hipMalloc(ctypes.byref(ws), ctypes.c_size_t(wsb)), "hipMalloc")
         ok(hip.hipMemcpy(x, xh.ctypes.data_as(vp), ctypes.c_size_t(xh.nbytes), 1), "hipMemcpy")
+        ok(hip.hipStreamCreate(ctypes.byref(st)), "hipStreamCreate")
+        for _ in range(3):
+            w.launch_gemm(x.value, n, c.value, ws.value, wsb, st.value)
+        ok(hip.hipStreamSynchronize(st), "hipStreamSynchronize")
+        graph, exe = vp(), vp()
+        ok(hip.hipStreamBeginCapture(st, 0), "hipStreamBeginCapture")
+        for _ in range(iters):
+            w.launch_gemm(x.value, n, c.value, ws.value, wsb, st.value)
+        ok(hip.hipStreamEndCapture(st, ctypes.byref(graph)), "hipStreamEndCapture")
+        ok(hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, ctypes.c_size_t(0)), "hipGraphInstantiate")
+        ok(hip.hipGraphLaunch(exe, st), "hipGraphLaunch")
+        ok(hip.hipStreamSynchronize(st), "hipStreamSynchronize")
         e0, e1 = vp(), vp()
         ok(hip.hipEventCreate(ctypes.byref(e0)), "hipEventCreate")
         ok(hip.hipEventCreate(ctypes.byref(e1)), "hipEventCreate")
-        for _ in range(3):
-            w.launch_gemm(x.value, n, c.value)
-        ok(hip.hipDeviceSynchronize(), "hipDeviceSynchronize")
-        ok(hip.hipEventRecord(e0, None), "hipEventRecord")
-        for _ in range(iters):
-            w.launch_gemm(x.value, n, c.value)
-        ok(hip.hipEventRecord(e1, None), "hipEventRecord")
+        ok(hip.hipEventRecord(e0, st), "hipEventRecord")
+        ok(hip.hipGraphLaunch(exe, st), "hipGraphLaunch")
+        ok(hip.hipEventRecord(e1, st), "hipEventRecord")
         ok(hip.hipEventSynchronize(e1), "hipEventSynchronize")
         ms = ctypes.c_float()
         ok(hip.hipEventElapsedTime(ctypes.byref(ms), e0, e1), "hipEventElapsedTime")
         us = ms.value * 1000.0 / iters
         hip.hipEventDestroy(e0)
         hip.hipEventDestroy(e1)
+        hip.hipGraphExecDestroy(exe)
+        hip.hipGraphDestroy(graph)
+        hip.hipStreamDestroy(st)
         hip.hipFree(x)
         hip.hipFree(c)
+        if wsb:
+            hip.hipFree(ws)
         flops = 2.0 * m * n * k
         byts = w.nbytes + n * k * 2 + n * m * 4
         out.append({"type": "Q4_K" if kind == 12 else "Q6_K", "rows": m, "cols": k, "tokens": n,

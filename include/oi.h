@@ -158,9 +158,15 @@ int oi_gemv(int32_t type, const void *host_blocks, int64_t rows, int64_t cols, c
  * gemm_test.odin:97-135, 297-337): c[t][r] = sum_k f16(dequant(W)[r][k]) * x[t][k]
  * for n tokens, f32 accumulation, on the matrix cores.  x_dev: n x cols f16
  * (token-major), c_dev: n x rows f32 (token-major) -- the transposes of the
- * harness's B[K][N] and C[M][N].  Types Q4_K, Q6_K (cols % 256 == 0), Q8_0
- * (cols % 64 == 0).  Enqueued on `stream`. */
-int oi_gemm_launch(const oi_weights *w, const uint16_t *x_dev, int32_t n, float *c_dev, void *stream);
+ * harness's B[K][N] and C[M][N].  Types Q4_K, Q6_K and Q8_0 with cols % 256 == 0
+ * (the reference's K % 256 condition, BATCHED_PREFILL.md:205-207).  Enqueued on
+ * `stream`.  `workspace` (device memory, may be NULL) holds the partial
+ * products when K is split over workgroups; with less than
+ * oi_gemm_workspace_bytes(w, n) bytes the split is reduced to what fits (none
+ * needs no workspace).  Calls that overlap on one workspace race. */
+int64_t oi_gemm_workspace_bytes(const oi_weights *w, int32_t n);
+int oi_gemm_launch(const oi_weights *w, const uint16_t *x_dev, int32_t n, float *c_dev, void *workspace,
+                   int64_t workspace_bytes, void *stream);
 
 /* Host-memory convenience form of oi_gemm_launch (synchronous). */
 int oi_gemm(int32_t type, const void *host_blocks, int64_t rows, int64_t cols, const uint16_t *x, int32_t n,

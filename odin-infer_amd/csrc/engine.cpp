@@ -1109,11 +1109,20 @@ int oi_gemv_launch(const oi_weights *w, const float *x_dev, float *y_dev, void *
     return OI_OK;
 }
 
-int oi_gemm_launch(const oi_weights *w, const uint16_t *x_dev, int32_t n, float *c_dev, void *stream) {
+int64_t oi_gemm_workspace_bytes(const oi_weights *w, int32_t n) {
+    if (!w || n <= 0 || !gemm_supported(w->m)) return 0;
+    const int split = gemm_split(w->m, n, SIZE_MAX);
+    return split > 1 ? (int64_t)split * n * w->m.rows * 4 : 0;
+}
+
+int oi_gemm_launch(const oi_weights *w, const uint16_t *x_dev, int32_t n, float *c_dev, void *workspace,
+                   int64_t workspace_bytes, void *stream) {
     if (!w || !x_dev || !c_dev) return fail(OI_E_ARG, "null argument");
     if (n <= 0) return fail(OI_E_ARG, "n must be positive");
+    if (workspace_bytes < 0) return fail(OI_E_ARG, "negative workspace size");
     if (!gemm_supported(w->m)) return fail(OI_E_UNSUPPORTED, "type / row length not supported by the GEMM kernel");
-    hipError_t r = launch_gemm(w->m, x_dev, n, c_dev, (hipStream_t)stream);
+    const hipError_t r = launch_gemm(w->m, x_dev, n, c_dev, (float *)workspace, workspace ? (size_t)workspace_bytes : 0,
+                                     (hipStream_t)stream);
     if (r != hipSuccess) return fail(OI_E_DEVICE, std::string("gemm launch: ") + hipGetErrorString(r));
     return OI_OK;
 }
@@ -1127,15 +1136,19 @@ int oi_gemm(int32_t type, const void *host_blocks, int64_t rows, int64_t cols, c
     if (rc) return rc;
     uint16_t *dx = nullptr;
     float *dc = nullptr;
+    void *ws = nullptr;
+    const int64_t wsb = oi_gemm_workspace_bytes(w, n);
     hipError_t r = hipMalloc(&dx, (size_t)n * cols * 2);
     if (r == hipSuccess) r = hipMalloc(&dc, (size_t)n * rows * 4);
+    if (r == hipSuccess && wsb) r = hipMalloc(&ws, (size_t)wsb);
     if (r == hipSuccess) r = hipMemcpy(dx, x, (size_t)n * cols * 2, hipMemcpyHostToDevice);
     if (r == hipSuccess) {
-        rc = oi_gemm_launch(w, dx, n, dc, nullptr);
+        rc = oi_gemm_launch(w, dx, n, dc, ws, wsb, nullptr);
         if (!rc) r = hipMemcpy(c, dc, (size_t)n * rows * 4, hipMemcpyDeviceToHost);
     }
     if (dx) hipFree(dx);
     if (dc) hipFree(dc);
+    if (ws) hipFree(ws);
     oi_weights_free(w);
     if (rc) return rc;
     if (r != hipSuccess) return fail(OI_E_DEVICE, std::string("gemm: ") + hipGetErrorString(r));

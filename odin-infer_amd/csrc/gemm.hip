@@ -6,15 +6,19 @@
 // X is token-major f16 [n][K], C token-major f32 [n][M] (the transposes of the
 // reference harness's B[K][N] and C[M][N]; same products).
 //
-// Work layout: a workgroup computes 128 rows x 64 tokens over a slice of K:
-// wave w holds rows 16w .. 16w+15 in four v_mfma_f32_16x16x32_f16
-// accumulators (16 tokens each) and walks the slice chunk by chunk (a chunk
-// is one GEMV unit of 64 weights; two units = one super-block half for
-// Q6_K); the chunk's activations are shared through LDS.  Every lane
-// dequantizes the weights it feeds to
-// the matrix cores straight from the plane layout (no LDS staging of W): for
-// 16x16x32 the A operand of lane l is row l%16, k = 8(l/16) .. +7 of the
-// 32-wide K step, and in the plane layout those are 8 consecutive bytes.
+// Work layout: a workgroup of 8 waves (two per SIMD, so that one wave's
+// dequantization overlaps the other's matrix and LDS work) computes 128 rows x
+// 64 tokens over a slice of K; wave w holds rows 16w .. 16w+15 in four
+// v_mfma_f32_16x16x32_f16 accumulators (16 tokens each).  K is walked in
+// chunks of 256 (one Q4_K / Q6_K super-block, eight Q8_0 blocks); the chunk's
+// 64 x 256 activations are staged in LDS once per workgroup and read by all
+// four waves.  Every lane dequantizes the weights it feeds to the matrix cores
+// straight from the plane layout (no LDS staging of W): lane quarter q owns one
+// 64-weight unit of the chunk (16-byte plane loads), and the chunk's eight
+// 32-wide K steps take 8 of its weights each.  The K order inside a chunk is a
+// permutation chosen so that each lane's bytes are contiguous; the activation
+// octets are placed by the same permutation (omap), so every product pairs
+// the right weight with the right activation.
 // Dequantization follows ggml/quant.odin exactly (separately rounded products,
 // (d*sc)*q for Q6_K), then rounds to f16 (RNE), as the reference's staging.
 //
@@ -31,13 +35,27 @@ namespace oi {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
-constexpr int GM_WAVES = 8, GM_ROWS = 16 * GM_WAVES, GM_TOK = 64, GM_THREADS = GM_WAVES * WAVE;
-constexpr int GM_PD = 4;  // weight chunks in the register ring (GM_PD - 1 in flight)
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+// raw buffer descriptors (data format 32, the gfx9 value for untyped access):
+// 32-bit per-lane offsets and a uniform per-chunk offset, so the loads need no
+// 64-bit address arithmetic; reads past `bytes` return zero
+static __device__ __forceinline__ rsrc_t make_rsrc(const void *p, size_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)(uint32_t)bytes, 0x00020000);
+}
+static __device__ __forceinline__ u32x4 bld16(rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+}
+
+constexpr int GM_WAVES = 8, GM_RT = 1, GM_ROWS = 16 * GM_RT * GM_WAVES, GM_TOK = 64, GM_THREADS = GM_WAVES * WAVE;
+constexpr int GM_KC = 256;                  // K per chunk
+constexpr int GM_XV = GM_TOK * GM_KC / 8;   // 16-byte activation pieces per chunk
+constexpr int GM_XPT = GM_XV / GM_THREADS;  // ... per thread
+constexpr int GM_WD = 2;                    // weight chunks in the register ring (1 in flight)
 
 struct GemmArgs {
-    DMat m;           // weights [M][K], device plane layout
+    DMat m;             // weights [M][K], device plane layout
     const uint16_t *x;  // [n][K] f16
-    float *c;         // [n][M]
+    float *c;           // [n][M], or [split][n][M] partial products when K is split
     int32_t n;
 };
 
@@ -47,241 +65,356 @@ static __device__ __forceinline__ h8 cvt8(const float (&v)[8]) {
     for (int e = 0; e < 8; e++) r[e] = (_Float16)v[e];
     return r;
 }
-
-// ---- A operands of one chunk, per type --------------------------------------
-// Each type has a raw load (the bytes a lane needs for one chunk, issued
-// several chunks ahead) and a dequantization of those bytes into the chunk's
-// A operands.
-//
-// Q4_K unit u (64 weights): K step 0 = low nibbles of bytes 0..31 (group 2p),
-// step 1 = high nibbles (group 2p + 1); lane quarter q reads bytes 8q .. 8q+7
-// (plane q/2, offset 8 (q%2)) and the super-block header.  ggml/quant.odin:178-209.
-struct RawQ4K {
-    u32x4 hdr;
-    u32x2 b;
-};
-static __device__ __forceinline__ void raw_q4k(const DMat &m, int row, int u, int q, RawQ4K &r) {
-    const size_t ui = (size_t)row * (m.cols >> 6) + u;
-    r.hdr = *(const u32x4 *)(m.s + ((size_t)row * (m.cols >> 8) + (u >> 2)) * 16);
-    r.b = *(const u32x2 *)(m.q + (q >> 1) * m.plane + ui * 16 + 8 * (q & 1));
+static __device__ __forceinline__ uint32_t byte_of(uint32_t lo, uint32_t hi, int e) {
+    return ((e < 4 ? lo : hi) >> (8 * (e & 3))) & 0xFFu;
 }
-static __device__ __forceinline__ void deq_q4k(const RawQ4K &r, int u, h8 *A) {
-#pragma clang fp contract(off)
-    const float d = h2f(r.hdr.x & 0xFFFFu), dmin = h2f(r.hdr.x >> 16);
-    uint32_t sc0, m0, sc1, m1;
-    q4k_scales(u & 3, r.hdr.y, r.hdr.z, r.hdr.w, sc0, m0, sc1, m1);
-    const float d1 = d * (float)sc0, mm1 = dmin * (float)m0;
-    const float d2 = d * (float)sc1, mm2 = dmin * (float)m1;
-    float lo[8], hi[8];
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-        const uint32_t by = ((e < 4 ? r.b.x : r.b.y) >> (8 * (e & 3))) & 0xFFu;
-        lo[e] = d1 * (float)(by & 0xFu) - mm1;
-        hi[e] = d2 * (float)(by >> 4) - mm2;
+// keeps a masked word opaque, so that its bytes convert with v_cvt_f32_ubyte{0..3}
+// instead of being re-extracted one by one from the unmasked word
+static __device__ __forceinline__ uint32_t opaque(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+// ---- per-type raw loads and step dequantization ------------------------------
+// raw(): the bytes lane quarter q needs for chunk c of one row (issued chunks
+// ahead); deq(): the 8 weights of K step st as the A operand; omap(q, st): the
+// activation octet (8 consecutive K) those weights multiply.
+
+// Lane offsets: Off holds the per-lane byte offsets of one row's streams,
+// computed once; raw() adds the chunk's uniform offset.
+
+// Q4_K, chunk = super-block c; quarter q owns unit 4c + q (bytes 0-15 in plane
+// 0, 16-31 in plane 1).  Step st = 4h + 2p + b: nibble h (group 2q + h), plane
+// p, bytes 8b .. 8b+7 of that plane; weight = 64q + 32h + 16p + 8b + e, so the
+// octet is 8q + st.  ggml/quant.odin:178-209.
+struct GQ4K {
+    struct Src {
+        rsrc_t q, s;
+        uint32_t plane;
+    };
+    struct Off {
+        uint32_t q, s;
+    };
+    struct Raw {
+        u32x4 p0, p1, hdr;
+    };
+    static __device__ __forceinline__ Src src(const DMat &m) {
+        return Src{make_rsrc(m.q, 2 * m.plane), make_rsrc(m.s, (size_t)m.rows * (m.cols >> 8) * 16), (uint32_t)m.plane};
     }
-    A[0] = cvt8(lo);
-    A[1] = cvt8(hi);
-}
-
-// Q8_0 unit u: K step s covers block 2u + s; lane quarter q reads plane
-// 2s + q/2 at offset 8 (q%2).  ggml/quant.odin:87-96.
-struct RawQ80 {
-    u32x2 b[2];
-    uint32_t d;  // the two blocks' f16 scales
-};
-static __device__ __forceinline__ void raw_q80(const DMat &m, int row, int u, int q, RawQ80 &r) {
-    const size_t ui = (size_t)row * (m.cols >> 6) + u;
-    r.d = *(const uint32_t *)(m.d + (size_t)row * (m.cols >> 5) + 2 * u);
-#pragma unroll
-    for (int s = 0; s < 2; s++) r.b[s] = *(const u32x2 *)(m.q + (2 * s + (q >> 1)) * m.plane + ui * 16 + 8 * (q & 1));
-}
-static __device__ __forceinline__ void deq_q80(const RawQ80 &r, int, h8 *A) {
-#pragma clang fp contract(off)
-#pragma unroll
-    for (int s = 0; s < 2; s++) {
-        const float d = h2f(s ? r.d >> 16 : r.d & 0xFFFFu);
+    static __device__ __forceinline__ Off off(const DMat &m, int row, int q) {
+        return Off{(uint32_t)((row * (m.cols >> 6) + q) * 16), (uint32_t)(row * (m.cols >> 8) * 16)};
+    }
+    static __device__ __forceinline__ void raw(const Src &g, const Off &o, int c, Raw &r) {
+        r.p0 = bld16(g.q, o.q, 64 * c);
+        r.p1 = bld16(g.q, o.q + g.plane, 64 * c);
+        r.hdr = bld16(g.s, o.s, 16 * c);
+    }
+    struct Pre {
+        float d1[2], mm[2];
+    };
+    static __device__ __forceinline__ Pre pre(const Raw &r, int q) {
+        Pre p;
+        const float d = h2f(r.hdr.x & 0xFFFFu), dmin = h2f(r.hdr.x >> 16);
+        uint32_t sc0, m0, sc1, m1;
+        q4k_scales(q, r.hdr.y, r.hdr.z, r.hdr.w, sc0, m0, sc1, m1);
+        p.d1[0] = d * (float)sc0;
+        p.mm[0] = dmin * (float)m0;
+        p.d1[1] = d * (float)sc1;
+        p.mm[1] = dmin * (float)m1;
+        return p;
+    }
+    // d1 * nib is exact in f32 (at most 11 + 6 + 4 significant bits), so the
+    // fused d1 * nib - mm rounds exactly as the separate product and difference
+    static __device__ __forceinline__ h8 deq(const Raw &r, const Pre &p, int st) {
+        const int h = st >> 2, pl = (st >> 1) & 1, b = st & 1;
+        const u32x4 &w = pl ? r.p1 : r.p0;
+        const uint32_t lo = opaque(((b ? w.z : w.x) >> (4 * h)) & 0x0F0F0F0Fu);
+        const uint32_t hi = opaque(((b ? w.w : w.y) >> (4 * h)) & 0x0F0F0F0Fu);
         float v[8];
 #pragma unroll
-        for (int e = 0; e < 8; e++)
-            v[e] = d * (float)(int8_t)(((e < 4 ? r.b[s].x : r.b[s].y) >> (8 * (e & 3))) & 0xFFu);
-        A[s] = cvt8(v);
+        for (int e = 0; e < 8; e++) v[e] = __builtin_fmaf(p.d1[h], (float)byte_of(lo, hi, e), -p.mm[h]);
+        return cvt8(v);
     }
-}
-
-// Q6_K chunk c = half h = c%2 of super-block sb = c/2 (units 4sb+2h, 4sb+2h+1):
-// K step s is the 32 elements 128h + 32s + [0,32) (run s of both units); lane
-// quarter q reads unit q/2 at byte offset 8 (q%2) of its ql-low, ql-high and
-// qh planes; scale index 8h + q/2 + 2s.  ggml/quant.odin:212-247.
-struct RawQ6K {
-    u32x2 qa, qb, qh, scw;
-    uint32_t d;
+    static __device__ __forceinline__ int omap(int q, int st) { return 8 * q + st; }
 };
-static __device__ __forceinline__ void raw_q6k(const DMat &m, int row, int c, int q, RawQ6K &r) {
-    const int sb = c >> 1, h = c & 1, nsb = m.cols >> 8;
-    const int u = 4 * sb + 2 * h + (q >> 1), off = 8 * (q & 1);
-    const size_t ui = (size_t)row * (m.cols >> 6) + u, sbi = (size_t)row * nsb + sb;
-    r.qa = *(const u32x2 *)(m.q + ui * 16 + off);
-    r.qb = *(const u32x2 *)(m.q + m.plane + ui * 16 + off);
-    r.qh = *(const u32x2 *)(m.q + 2 * m.plane + ui * 16 + off);
-    r.scw = *(const u32x2 *)(m.s + sbi * 16 + 8 * h);
-    r.d = m.d[sbi];
-}
-static __device__ __forceinline__ void deq_q6k(const RawQ6K &r, int, h8 *A, int q) {
-#pragma clang fp contract(off)
-    const float d = h2f(r.d);
+
+// Q6_K, chunk = super-block c; quarter q owns unit 4c + q = unit u' = q % 2 of
+// half h = q / 2, bytes 0-15 of its ql-low, ql-high and qh planes.  Step
+// st = 2s + b: run s (ql-low/high nibble and qh bits 2s, scale 8h + u' + 2s),
+// bytes 8b .. 8b+7; weight = 128h + 32s + 16u' + 8b + e, octet
+// 16h + 4s + 2u' + b.  ggml/quant.odin:212-247.
+struct GQ6K {
+    struct Src {
+        rsrc_t q, s, d;
+        uint32_t plane;
+    };
+    struct Off {
+        uint32_t q, s, d;
+    };
+    struct Raw {
+        u32x4 qa, qb, qh;
+        u32x2 scw;
+        uint32_t d;
+    };
+    static __device__ __forceinline__ Src src(const DMat &m) {
+        const size_t nsb = (size_t)m.rows * (m.cols >> 8);
+        return Src{make_rsrc(m.q, 3 * m.plane), make_rsrc(m.s, nsb * 16), make_rsrc(m.d, nsb * 2), (uint32_t)m.plane};
+    }
+    static __device__ __forceinline__ Off off(const DMat &m, int row, int q) {
+        const int nsb = m.cols >> 8;
+        return Off{(uint32_t)((row * (m.cols >> 6) + q) * 16), (uint32_t)(row * nsb * 16 + 8 * (q >> 1)),
+                   (uint32_t)(row * nsb * 2)};
+    }
+    static __device__ __forceinline__ void raw(const Src &g, const Off &o, int c, Raw &r) {
+        r.qa = bld16(g.q, o.q, 64 * c);
+        r.qb = bld16(g.q, o.q + g.plane, 64 * c);
+        r.qh = bld16(g.q, o.q + 2 * g.plane, 64 * c);
+        r.scw = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(g.s, o.s, 16 * c, 0));
+        r.d = __builtin_amdgcn_raw_buffer_load_b16(g.d, o.d, 2 * c, 0);
+    }
+    struct Pre {
+        float ds[4], off[4];
+    };
+    static __device__ __forceinline__ Pre pre(const Raw &r, int q) {
+        Pre p;
+        const float d = h2f(r.d);
 #pragma unroll
-    for (int s = 0; s < 4; s++) {
-        const int is = (q >> 1) + 2 * s;
-        const float ds = d * (float)(int8_t)(((is < 4 ? r.scw.x : r.scw.y) >> (8 * (is & 3))) & 0xFFu);
-        float v[8];
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const uint32_t la = ((e < 4 ? r.qa.x : r.qa.y) >> (8 * (e & 3))) & 0xFFu;
-            const uint32_t lb = ((e < 4 ? r.qb.x : r.qb.y) >> (8 * (e & 3))) & 0xFFu;
-            const uint32_t hb = ((e < 4 ? r.qh.x : r.qh.y) >> (8 * (e & 3))) & 0xFFu;
-            const uint32_t l4 = s == 0 ? (la & 0xF) : s == 1 ? (lb & 0xF) : s == 2 ? (la >> 4) : (lb >> 4);
-            const int qv = (int)(l4 | (((hb >> (2 * s)) & 3u) << 4)) - 32;
-            v[e] = ds * (float)qv;
+        for (int s = 0; s < 4; s++) {
+            const int is = (q & 1) + 2 * s;
+            p.ds[s] = d * (float)(int8_t)byte_of(r.scw.x, r.scw.y, is);
+            p.off[s] = -32.f * p.ds[s];
         }
-        A[s] = cvt8(v);
+        return p;
     }
-}
-
-template <int T> struct GemmType;
-template <> struct GemmType<T_Q4_K> {
-    using Raw = RawQ4K;
-    static constexpr int SPC = 2;
-    static __device__ void raw(const DMat &m, int row, int c, int q, Raw &r) { raw_q4k(m, row, c, q, r); }
-    static __device__ void deq(const Raw &r, int c, int, h8 *A) { deq_q4k(r, c, A); }
-};
-template <> struct GemmType<T_Q8_0> {
-    using Raw = RawQ80;
-    static constexpr int SPC = 2;
-    static __device__ void raw(const DMat &m, int row, int c, int q, Raw &r) { raw_q80(m, row, c, q, r); }
-    static __device__ void deq(const Raw &r, int c, int, h8 *A) { deq_q80(r, c, A); }
-};
-template <> struct GemmType<T_Q6_K> {
-    using Raw = RawQ6K;
-    static constexpr int SPC = 4;
-    static __device__ void raw(const DMat &m, int row, int c, int q, Raw &r) { raw_q6k(m, row, c, q, r); }
-    static __device__ void deq(const Raw &r, int c, int q, h8 *A) { deq_q6k(r, c, A, q); }
+    // ds * (code - 32) as one fused ds * code - 32 ds: the exact value is the
+    // same and the fma rounds it once, as the reference's single product
+    static __device__ __forceinline__ h8 deq(const Raw &r, const Pre &p, int st) {
+        const int s = st >> 1, b = st & 1;
+        const u32x4 &l = (s & 1) ? r.qb : r.qa;
+        const uint32_t llo = ((b ? l.z : l.x) >> (4 * (s >> 1))) & 0x0F0F0F0Fu;
+        const uint32_t lhi = ((b ? l.w : l.y) >> (4 * (s >> 1))) & 0x0F0F0F0Fu;
+        const uint32_t hlo = (((b ? r.qh.z : r.qh.x) >> (2 * s)) & 0x03030303u) << 4;
+        const uint32_t hhi = (((b ? r.qh.w : r.qh.y) >> (2 * s)) & 0x03030303u) << 4;
+        const uint32_t wlo = opaque(llo | hlo), whi = opaque(lhi | hhi);  // 6-bit codes, one per byte
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = __builtin_fmaf(p.ds[s], (float)byte_of(wlo, whi, e), p.off[s]);
+        return cvt8(v);
+    }
+    static __device__ __forceinline__ int omap(int q, int st) {
+        return 16 * (q >> 1) + 4 * (st >> 1) + 2 * (q & 1) + (st & 1);
+    }
 };
 
-// One workgroup: rows [128 bx, +128) (wave w: rows 16w .. 16w+15), tokens
-// [64 by, +64), chunks [bz * cps, +cps) of K.  The 64 x KC activation chunk is
-// staged in LDS once per workgroup (double-buffered, the next chunk's load in
-// flight while this one is computed) and read by all 8 waves; each wave
-// dequantizes its own rows.  With more than one K slice the partial products
-// are added into c (zeroed by the launcher) with device-scope float atomics.
-template <int T>
-__global__ __launch_bounds__(GM_THREADS) void gemm_q_kernel(GemmArgs a, int cps, int split) {
-    using G = GemmType<T>;
-    constexpr int SPC = G::SPC;               // 32-wide K steps per chunk
-    constexpr int KC = 32 * SPC;              // weights per chunk
-    constexpr int XV = GM_TOK * KC / 8;       // 16-byte pieces of an activation chunk
-    constexpr int XPT = XV / GM_THREADS;      // ... per thread
-    __shared__ __attribute__((aligned(16))) u32x4 xs[2][XV];
+// Q8_0, chunk = blocks 8c .. 8c+7; quarter q owns unit 4c + q (blocks 8c + 2q
+// and 8c + 2q + 1); plane 2 blk + half holds bytes 16 half .. +15 of block blk.
+// Step st = 4 blk + 2 half + b: weight 64q + 8st + e, octet 8q + st.
+// ggml/quant.odin:87-96.
+struct GQ80 {
+    struct Src {
+        rsrc_t q, d;
+        uint32_t plane;
+    };
+    struct Off {
+        uint32_t q, d;
+    };
+    struct Raw {
+        u32x4 pl[4];
+        uint32_t d;
+    };
+    static __device__ __forceinline__ Src src(const DMat &m) {
+        return Src{make_rsrc(m.q, 4 * m.plane), make_rsrc(m.d, (size_t)m.rows * (m.cols >> 5) * 2), (uint32_t)m.plane};
+    }
+    static __device__ __forceinline__ Off off(const DMat &m, int row, int q) {
+        return Off{(uint32_t)((row * (m.cols >> 6) + q) * 16), (uint32_t)((row * (m.cols >> 5) + 2 * q) * 2)};
+    }
+    static __device__ __forceinline__ void raw(const Src &g, const Off &o, int c, Raw &r) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) r.pl[k] = bld16(g.q, o.q + k * g.plane, 64 * c);
+        r.d = __builtin_amdgcn_raw_buffer_load_b32(g.d, o.d, 16 * c, 0);
+    }
+    struct Pre {
+        float d[2];
+    };
+    static __device__ __forceinline__ Pre pre(const Raw &r, int) {
+        return Pre{{h2f(r.d & 0xFFFFu), h2f(r.d >> 16)}};
+    }
+    static __device__ __forceinline__ h8 deq(const Raw &r, const Pre &p, int st) {
+#pragma clang fp contract(off)
+        const u32x4 &w = r.pl[st >> 1];
+        const int b = st & 1;
+        const uint32_t lo = b ? w.z : w.x, hi = b ? w.w : w.y;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = p.d[st >> 2] * (float)(int8_t)byte_of(lo, hi, e);
+        return cvt8(v);
+    }
+    static __device__ __forceinline__ int omap(int q, int st) { return 8 * q + st; }
+};
+
+// One workgroup: rows [128 bx, +128), tokens [64 by, +64), chunks
+// [bz * cps, +cps) of K.  Activations: chunk c + 1 is loaded into registers
+// while chunk c is computed, then stored to the LDS buffer of its parity
+// (piece (token j, octet o) at slot 64 o + (j ^ (o % 8)): conflict-free stores
+// of 8 consecutive octets and conflict-free 16-lane operand reads); weights
+// run GM_WD - 1 chunks ahead in a register ring.  With more than one K slice
+// (split > 1) slice z writes its partial products to c + z n M; gemm_reduce
+// sums them in slice order.
+template <class G>
+__global__ __launch_bounds__(GM_THREADS) void gemm_q_kernel(GemmArgs a, int cps) {
+    __shared__ __attribute__((aligned(16))) u32x4 xs[2][GM_XV];
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
     const int q = lane >> 4, li = lane & 15;
     const int M = a.m.rows, K = a.m.cols;
-    const int row = min((int)blockIdx.x * GM_ROWS + 16 * wave + li, M - 1);  // rows past M: recomputed, not stored
+    const int rbase = (int)blockIdx.x * GM_ROWS + 16 * GM_RT * wave;
+    const typename G::Src src = G::src(a.m);
+    typename G::Off off[GM_RT];
+#pragma unroll
+    for (int rt = 0; rt < GM_RT; rt++) off[rt] = G::off(a.m, min(rbase + 16 * rt + li, M - 1), q);  // rows past M: not stored
     const int t0 = (int)blockIdx.y * GM_TOK;
-    const int nchunk = K / KC;
+    const int nchunk = K / GM_KC;
     const int c0 = (int)blockIdx.z * cps, c1 = min(nchunk, c0 + cps);
 
-    // piece p of a chunk: token p / (KC / 8), 8 activations at (p % (KC / 8)) * 8;
-    // LDS slot of piece (token j, k-octet o): o * 64 + j (the B operand of lane
-    // (j, q) for step s is octet 4s + q: consecutive lanes, consecutive slots)
-    auto xfetch = [&](int c, u32x4 (&xr)[XPT]) {
+    const rsrc_t xsrc = make_rsrc(a.x, (size_t)a.n * K * 2);
+    uint32_t xoff[GM_XPT];
 #pragma unroll
-        for (int i = 0; i < XPT; i++) {
-            const int p = threadIdx.x + i * GM_THREADS, j = p / (KC / 8), o = p % (KC / 8);
-            const int tok = min(t0 + j, a.n - 1);
-            xr[i] = *(const u32x4 *)(a.x + (size_t)tok * K + (size_t)c * KC + 8 * o);
-        }
+    for (int i = 0; i < GM_XPT; i++) {
+        const int p = threadIdx.x + i * GM_THREADS, j = p >> 5, o = p & 31;
+        xoff[i] = (uint32_t)(min(t0 + j, a.n - 1) * K * 2 + 16 * o);
+    }
+    u32x4 xr[GM_XPT];
+    auto xfetch = [&](int c) {
+#pragma unroll
+        for (int i = 0; i < GM_XPT; i++) xr[i] = bld16(xsrc, xoff[i], c * GM_KC * 2);
     };
-    auto xstore = [&](int buf, const u32x4 (&xr)[XPT]) {
+    auto xstore = [&](int buf) {
 #pragma unroll
-        for (int i = 0; i < XPT; i++) {
-            const int p = threadIdx.x + i * GM_THREADS, j = p / (KC / 8), o = p % (KC / 8);
-            xs[buf][o * GM_TOK + j] = xr[i];
+        for (int i = 0; i < GM_XPT; i++) {
+            const int p = threadIdx.x + i * GM_THREADS, j = p >> 5, o = p & 31;
+            xs[buf][o * GM_TOK + (j ^ (o & 7))] = xr[i];
         }
     };
 
-    f32x4v acc[4];
+    f32x4v acc[GM_RT][4];
 #pragma unroll
-    for (int t = 0; t < 4; t++) acc[t] = f32x4v{0.f, 0.f, 0.f, 0.f};
-    // weights and activations GM_PD - 1 chunks ahead in register rings
-    // (unconditional loads: chunks past the slice re-read its first, unused)
-    typename G::Raw ring[GM_PD];
-    u32x4 xr[GM_PD][XPT];
+    for (int rt = 0; rt < GM_RT; rt++)
 #pragma unroll
-    for (int r = 0; r < GM_PD - 1; r++) {
-        const int c = c0 + r < c1 ? c0 + r : c0;
-        G::raw(a.m, row, c, q, ring[r]);
-        xfetch(c, xr[r]);
-    }
-    for (int cb = c0; cb < c1; cb += GM_PD) {
+        for (int t = 0; t < 4; t++) acc[rt][t] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    // unconditional loads: chunks past the slice re-read its first, unused
+    typename G::Raw ring[GM_WD][GM_RT];
 #pragma unroll
-        for (int r = 0; r < GM_PD; r++) {
+    for (int r = 0; r < GM_WD - 1; r++)
+#pragma unroll
+        for (int rt = 0; rt < GM_RT; rt++) G::raw(src, off[rt], c0 + r < c1 ? c0 + r : c0, ring[r][rt]);
+    if (c0 < c1) xfetch(c0);
+    for (int cb = c0; cb < c1; cb += GM_WD) {
+#pragma unroll
+        for (int r = 0; r < GM_WD; r++) {
             const int c = cb + r;
             if (c >= c1) break;
-            const int cn = c + GM_PD - 1 < c1 ? c + GM_PD - 1 : c0, rn = (r + GM_PD - 1) % GM_PD;
-            G::raw(a.m, row, cn, q, ring[rn]);
-            xfetch(cn, xr[rn]);
+            const int cn = c + GM_WD - 1 < c1 ? c + GM_WD - 1 : c0;
+#pragma unroll
+            for (int rt = 0; rt < GM_RT; rt++) G::raw(src, off[rt], cn, ring[(r + GM_WD - 1) % GM_WD][rt]);
             const int buf = (c - c0) & 1;
-            xstore(buf, xr[r]);
+            xstore(buf);
+            if (c + 1 < c1) xfetch(c + 1);
             __syncthreads();  // chunk c staged; every wave is done with chunk c - 2's buffer
-            h8 A[SPC];
-            G::deq(ring[r], c, q, A);
+            typename G::Pre pre[GM_RT];
 #pragma unroll
-            for (int s = 0; s < SPC; s++)
+            for (int rt = 0; rt < GM_RT; rt++) pre[rt] = G::pre(ring[r][rt], q);
 #pragma unroll
-                for (int t = 0; t < 4; t++)
-                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                        A[s], __builtin_bit_cast(h8, xs[buf][(4 * s + q) * GM_TOK + 16 * t + li]), acc[t], 0, 0, 0);
+            for (int st = 0; st < 8; st++) {
+                const int o = G::omap(q, st);
+                h8 B[4];
+#pragma unroll
+                for (int t = 0; t < 4; t++) B[t] = __builtin_bit_cast(h8, xs[buf][o * GM_TOK + ((16 * t + li) ^ (o & 7))]);
+#pragma unroll
+                for (int rt = 0; rt < GM_RT; rt++) {
+                    const h8 A = G::deq(ring[r][rt], pre[rt], st);
+#pragma unroll
+                    for (int t = 0; t < 4; t++)
+                        acc[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[t], acc[rt][t], 0, 0, 0);
+                }
+            }
         }
     }
-    // D of token tile t: lane (j, g) holds rows 4g .. 4g+3 of column (token) j
+    // D of tile (rt, t): lane (j, g) holds rows 4g .. 4g+3 of column (token) j
+    float *out = a.c + (size_t)blockIdx.z * a.n * M;
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-        const int tk = t0 + 16 * t + li;
+    for (int rt = 0; rt < GM_RT; rt++) {
+        const int r0 = rbase + 16 * rt + 4 * q;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int r = (int)blockIdx.x * GM_ROWS + 16 * wave + 4 * q + e;
-            if (r < M && tk < a.n) {
-                float *dst = a.c + (size_t)tk * M + r;
-                if (split > 1) __hip_atomic_fetch_add(dst, acc[t][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                else *dst = acc[t][e];
+        for (int t = 0; t < 4; t++) {
+            const int tk = t0 + 16 * t + li;
+            if (tk >= a.n) continue;
+            float *dst = out + (size_t)tk * M + r0;
+            if (r0 + 3 < M && (M & 3) == 0) {
+                *(f32x4v *)dst = acc[rt][t];
+                continue;
             }
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (r0 + e < M) dst[e] = acc[rt][t][e];
+        }
+    }
+}
+
+// c[i] = sum over slices z (in order) of part[z][i]
+__global__ __launch_bounds__(WG) void gemm_reduce(const float *part, float *c, int64_t total, int split) {
+    const int64_t i = (int64_t)blockIdx.x * WG + threadIdx.x;
+    if (4 * i + 3 < total) {
+        f32x4v s = *(const f32x4v *)(part + 4 * i);
+        for (int z = 1; z < split; z++) s += *(const f32x4v *)(part + z * total + 4 * i);
+        *(f32x4v *)(c + 4 * i) = s;
+    } else {
+        for (int64_t k = 4 * i; k < total; k++) {
+            float s = part[k];
+            for (int z = 1; z < split; z++) s += part[z * total + k];
+            c[k] = s;
         }
     }
 }
 
 bool gemm_supported(const DMat &m) {
-    return (m.type == T_Q4_K || m.type == T_Q6_K) ? m.cols % 256 == 0 : m.type == T_Q8_0 && m.cols % 64 == 0;
+    return (m.type == T_Q4_K || m.type == T_Q6_K || m.type == T_Q8_0) && m.cols % GM_KC == 0;
 }
 
-// K is split so that about 192 workgroups run (each slice at least 4 chunks;
-// measured best on 4096/12288 x 64 x 4096/12288); with more than one slice c is
-// zeroed first and the slices add into it.
-hipError_t launch_gemm(const DMat &m, const uint16_t *x, int32_t n, float *c, hipStream_t st) {
-    if (!gemm_supported(m) || n <= 0) return hipErrorInvalidValue;
-    GemmArgs a{m, x, c, n};
-    const int kc = m.type == T_Q6_K ? 128 : 64, nchunk = m.cols / kc;
-    const int tiles = ((m.rows + GM_ROWS - 1) / GM_ROWS) * ((n + GM_TOK - 1) / GM_TOK);
-    int split = std::max(1, std::min((192 + tiles / 2) / tiles, nchunk / 4));  // ~192 workgroups (measured)
+static int normalize_split(int nchunk, int split) {
     const int cps = (nchunk + split - 1) / split;
-    split = (nchunk + cps - 1) / cps;
-    if (split > 1) {
-        const hipError_t e = hipMemsetAsync(c, 0, (size_t)n * m.rows * 4, st);
-        if (e != hipSuccess) return e;
-    }
+    return (nchunk + cps - 1) / cps;
+}
+
+// K is split so that about 256 workgroups run (one per CU; each slice at least
+// two chunks; measured best on 4096/12288 x 64 x 4096/12288), and no further
+// than the partial-product buffer holds.
+int gemm_split(const DMat &m, int32_t n, size_t part_bytes) {
+    const int nchunk = m.cols / GM_KC;
+    const int tiles = ((m.rows + GM_ROWS - 1) / GM_ROWS) * ((n + GM_TOK - 1) / GM_TOK);
+    int split = std::max(1, std::min((256 + tiles / 2) / tiles, nchunk / 2));
+    const size_t per = (size_t)n * m.rows * 4;
+    split = (int)std::min<size_t>(split, std::max<size_t>(1, part_bytes / per));
+    return normalize_split(nchunk, split);
+}
+
+// With split > 1 the slices' partial products go to `part` (split * n * rows
+// floats) and gemm_reduce sums them into c.
+hipError_t launch_gemm(const DMat &m, const uint16_t *x, int32_t n, float *c, float *part, size_t part_bytes,
+                       hipStream_t st) {
+    if (!gemm_supported(m) || n <= 0) return hipErrorInvalidValue;
+    const int nchunk = m.cols / GM_KC;
+    const int split = gemm_split(m, n, part ? part_bytes : 0);
+    const int cps = (nchunk + split - 1) / split;
+    GemmArgs a{m, x, split > 1 ? part : c, n};
     dim3 grid((m.rows + GM_ROWS - 1) / GM_ROWS, (n + GM_TOK - 1) / GM_TOK, split), block(GM_THREADS);
     switch (m.type) {
-    case T_Q4_K: hipLaunchKernelGGL(gemm_q_kernel<T_Q4_K>, grid, block, 0, st, a, cps, split); break;
-    case T_Q6_K: hipLaunchKernelGGL(gemm_q_kernel<T_Q6_K>, grid, block, 0, st, a, cps, split); break;
-    default: hipLaunchKernelGGL(gemm_q_kernel<T_Q8_0>, grid, block, 0, st, a, cps, split); break;
+    case T_Q4_K: hipLaunchKernelGGL(gemm_q_kernel<GQ4K>, grid, block, 0, st, a, cps); break;
+    case T_Q6_K: hipLaunchKernelGGL(gemm_q_kernel<GQ6K>, grid, block, 0, st, a, cps); break;
+    default: hipLaunchKernelGGL(gemm_q_kernel<GQ80>, grid, block, 0, st, a, cps); break;
+    }
+    if (split > 1) {
+        const int64_t total = (int64_t)n * m.rows;
+        const int64_t nb = ((total + 3) / 4 + WG - 1) / WG;
+        hipLaunchKernelGGL(gemm_reduce, dim3((unsigned)nb), dim3(WG), 0, st, part, c, total, split);
     }
     return hipGetLastError();
 }

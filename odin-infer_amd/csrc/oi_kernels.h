@@ -116,6 +116,11 @@ hipError_t launch_gemv_q(const GemvArgs &a, hipStream_t st);
 
 // gemm.hip: batched projection c[t][r] = sum_k f16(deq(W))[r][k] x[t][k]
 bool gemm_supported(const DMat &m);
-hipError_t launch_gemm(const DMat &m, const uint16_t *x, int32_t n, float *c, hipStream_t st);
+// K slices for n tokens when part_bytes of partial products fit (1 = none)
+int gemm_split(const DMat &m, int32_t n, size_t part_bytes);
+// part: room for the K slices' partial products (split * n * rows floats);
+// null or small: fewer slices
+hipError_t launch_gemm(const DMat &m, const uint16_t *x, int32_t n, float *c, float *part, size_t part_bytes,
+                       hipStream_t st);
 
 }  // namespace oi

@@ -46,7 +46,8 @@ HIP_SYMBOLS = {
     "oi_weights_bytes": (c_i64, [c_vp]),
     "oi_gemv_launch": (c_i32, [c_vp, c_vp, c_vp, c_vp]),
     "oi_gemv": (c_i32, [c_i32, c_vp, c_i64, c_i64, c_vp, c_vp]),
-    "oi_gemm_launch": (c_i32, [c_vp, c_vp, c_i32, c_vp, c_vp]),
+    "oi_gemm_workspace_bytes": (c_i64, [c_vp, c_i32]),
+    "oi_gemm_launch": (c_i32, [c_vp, c_vp, c_i32, c_vp, c_vp, c_i64, c_vp]),
     "oi_gemm": (c_i32, [c_i32, c_vp, c_i64, c_i64, c_vp, c_i32, c_vp]),
     # include/oi_debug.h
     "oi_engine_debug_buffer": (c_i64, [c_vp, c_i32, c_vp, c_i64]),

@@ -94,8 +94,11 @@ class DeviceWeights:
     def launch(self, x_dev_ptr, y_dev_ptr, stream=None):
         check(_native.hip().oi_gemv_launch(self.h, x_dev_ptr, y_dev_ptr, stream))
 
-    def launch_gemm(self, x_dev_ptr, n, c_dev_ptr, stream=None):
-        check(_native.hip().oi_gemm_launch(self.h, x_dev_ptr, int(n), c_dev_ptr, stream))
+    def gemm_workspace_bytes(self, n):
+        return int(_native.hip().oi_gemm_workspace_bytes(self.h, int(n)))
+
+    def launch_gemm(self, x_dev_ptr, n, c_dev_ptr, ws_dev_ptr=None, ws_bytes=0, stream=None):
+        check(_native.hip().oi_gemm_launch(self.h, x_dev_ptr, int(n), c_dev_ptr, ws_dev_ptr, int(ws_bytes), stream))
 
     def free(self):
         if self.h:

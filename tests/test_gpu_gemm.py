@@ -16,26 +16,26 @@ pytestmark = pytest.mark.gpu
 
 
 def test_ladder_exact():
-    m, k, n = 16, 64, 8
+    m, k, n = 16, 256, 8
     c = ggml.gemm(8, q8_const_blocks(np.ones((m, k))), m, k, x16(np.ones((n, k))))
     assert np.array_equal(c, np.full((n, m), float(k), np.float32))
     rng = np.random.default_rng(3)
-    x = rng.uniform(-1, 1, size=(5, 64))
-    c = ggml.gemm(8, q8_const_blocks(np.eye(64)), 64, 64, x16(x))
-    assert np.array_equal(c, x.astype(np.float16).astype(np.float32))
-    rows = np.repeat(np.arange(1, 33)[:, None], 128, axis=1)
-    c = ggml.gemm(8, q8_const_blocks(rows), 32, 128, x16(np.ones((3, 128))))
-    assert np.array_equal(c, np.tile(128 * np.arange(1, 33, dtype=np.float32), (3, 1)))
-    xc = np.repeat(np.arange(1, 71)[:, None] / 64.0, 128, axis=1)  # 70 tokens: two token tiles
-    c = ggml.gemm(8, q8_const_blocks(np.ones((32, 128))), 32, 128, x16(xc))
-    assert np.array_equal(c, np.repeat((2 * np.arange(1, 71, dtype=np.float32))[:, None], 32, axis=1))
+    x = rng.uniform(-1, 1, size=(5, 256))
+    c = ggml.gemm(8, q8_const_blocks(np.eye(256)[:64]), 64, 256, x16(x))
+    assert np.array_equal(c, x[:, :64].astype(np.float16).astype(np.float32))
+    rows = np.repeat(np.arange(1, 33)[:, None], 256, axis=1)
+    c = ggml.gemm(8, q8_const_blocks(rows), 32, 256, x16(np.ones((3, 256))))
+    assert np.array_equal(c, np.tile(256 * np.arange(1, 33, dtype=np.float32), (3, 1)))
+    xc = np.repeat(np.arange(1, 71)[:, None] / 64.0, 256, axis=1)  # 70 tokens: two token tiles
+    c = ggml.gemm(8, q8_const_blocks(np.ones((32, 256))), 32, 256, x16(xc))
+    assert np.array_equal(c, np.repeat((4 * np.arange(1, 71, dtype=np.float32))[:, None], 32, axis=1))
 
 
 CASES = [
     (12, 8, 8, 256, 2e-3), (12, 16, 16, 512, 2e-3), (12, 32, 32, 256, 2e-3), (12, 64, 64, 512, 2e-3),
     (12, 256, 64, 4096, 5e-3), (12, 4096, 64, 4096, 1e-2), (12, 12288, 64, 4096, 1e-2),
     (14, 8, 8, 256, 2e-3), (14, 64, 64, 512, 2e-3), (14, 256, 64, 4096, 5e-3), (14, 4096, 64, 12288, 1e-2),
-    (8, 8, 8, 256, 2e-3), (8, 64, 64, 512, 2e-3), (8, 1024, 64, 3072, 1e-2),
+    (8, 8, 8, 256, 2e-3), (8, 64, 64, 512, 2e-3), (8, 1024, 64, 3072, 1e-2), (8, 130, 64, 1280, 2e-3),
     (12, 40, 1, 512, 2e-3), (12, 40, 65, 512, 2e-3), (14, 24, 130, 256, 2e-3),
 ]
 
@@ -56,3 +56,70 @@ def test_gemm_rejects_bad_shapes():
     w = gemm_blocks(12, 8, 256, rng)
     with pytest.raises(Exception):
         ggml.gemm(12, w, 8, 256, np.zeros((0, 256), np.uint16))
+    w8 = gemm_blocks(8, 8, 128, rng)  # K must be a multiple of 256 (one chunk), as the reference's MMQ
+    with pytest.raises(Exception):
+        ggml.gemm(8, w8, 8, 128, np.zeros((4, 128), np.uint16))
+
+
+class _Hip:
+    """Device buffers from the HIP runtime the library is linked against."""
+
+    def __init__(self):
+        import ctypes
+        self.ct = ctypes
+        self.lib = ctypes.CDLL("libamdhip64.so")
+        self.bufs = []
+
+    def alloc(self, nbytes):
+        p = self.ct.c_void_p()
+        assert self.lib.hipMalloc(self.ct.byref(p), self.ct.c_size_t(max(nbytes, 16))) == 0
+        self.bufs.append(p)
+        return p.value
+
+    def put(self, arr):
+        p = self.alloc(arr.nbytes)
+        assert self.lib.hipMemcpy(self.ct.c_void_p(p), arr.ctypes.data_as(self.ct.c_void_p),
+                                  self.ct.c_size_t(arr.nbytes), 1) == 0
+        return p
+
+    def get(self, p, shape, dtype):
+        out = np.empty(shape, dtype)
+        assert self.lib.hipDeviceSynchronize() == 0
+        assert self.lib.hipMemcpy(out.ctypes.data_as(self.ct.c_void_p), self.ct.c_void_p(p),
+                                  self.ct.c_size_t(out.nbytes), 2) == 0
+        return out
+
+    def close(self):
+        for p in self.bufs:
+            self.lib.hipFree(p)
+
+
+@pytest.mark.parametrize("kind,m,n,k", [(12, 4096, 64, 4096), (14, 1024, 40, 12288)])
+def test_gemm_workspace_split(kind, m, n, k):
+    """K split over workgroups (partial products in the caller's workspace,
+    summed in slice order) and unsplit (no workspace) both match the oracle;
+    the split result is bit-identical from run to run (no atomics)."""
+    rng = np.random.default_rng(kind + m + n)
+    wb = gemm_blocks(kind, m, k, rng)
+    x = x16(rng.uniform(-1, 1, size=(n, k)))
+    ref = refcpu.gemm_f16(wb, kind, m, k, x)
+    w = ggml.DeviceWeights(kind, wb, m, k)
+    hip = _Hip()
+    try:
+        wsb = w.gemm_workspace_bytes(n)
+        assert wsb > 0, "this shape is expected to split K"
+        xd, cd, ws = hip.put(np.ascontiguousarray(x)), hip.alloc(n * m * 4), hip.alloc(wsb)
+        w.launch_gemm(xd, n, cd, ws, wsb)
+        split1 = hip.get(cd, (n, m), np.float32)
+        w.launch_gemm(xd, n, cd, ws, wsb)
+        split2 = hip.get(cd, (n, m), np.float32)
+        w.launch_gemm(xd, n, cd, None, 0)
+        whole = hip.get(cd, (n, m), np.float32)
+        w.launch_gemm(xd, n, cd, ws, wsb // 2)  # room for fewer slices
+        fewer = hip.get(cd, (n, m), np.float32)
+    finally:
+        hip.close()
+        w.free()
+    assert np.array_equal(split1, split2)
+    for got in (split1, whole, fewer):
+        assert scaled_err(got, ref) <= 1e-2
