@@ -79,6 +79,20 @@ void oi_engine_destroy(oi_engine *e);
  * the same). */
 const float *oi_engine_forward(oi_engine *e, int32_t token, int32_t pos);
 
+/* engine_forward_batch (qwen3_5/engine.odin:61-93 -> metal.odin:1472-1654
+ * forward_gpu_batch): consume tokens[0..n) at positions pos0 .. pos0+n-1 and
+ * return the logits of the last one (engine-owned pinned host memory, as
+ * oi_engine_forward).  Chunks of up to 512 tokens, cut to a multiple of 8, run
+ * batched: the seven projections of each layer on the matrix cores with f16
+ * operands and f32 accumulation (the reference's MMQ), the per-token operations
+ * (norms, RoPE, cache store, causal attention, SwiGLU, residuals) in f32; the
+ * trailing 1-7 tokens go through oi_engine_forward's path.  A model whose
+ * projections the batched kernels cannot take (type other than Q4_K / Q6_K /
+ * Q8_0, or a row length not a multiple of 256) runs every token through that
+ * path, as the reference's non-Metal fallback (engine.odin:86-91).  NULL on
+ * error: n <= 0, positions past seq_len, or a token out of range. */
+const float *oi_engine_prefill(oi_engine *e, const int32_t *tokens, int32_t n, int32_t pos0);
+
 /* engine_config (infer/engine.odin:54-56). */
 int oi_engine_config(const oi_engine *e, oi_config *out);
 

@@ -255,6 +255,14 @@ struct oi_engine {
     bool use_stream = false;
     StreamArgs sa{};
     int64_t stream_seq = 0;   // launches so far (the device keeps its own copy)
+    // batched prefill buffers (allocated on the first prefill): token ids,
+    // residual [T][dim], rotated q [T][q_dim], f16 projection inputs
+    // [T][max(dim, q_dim, hidden)], and three buffers of partial products
+    void *pf_mem = nullptr;
+    int32_t *pf_tok = nullptr;
+    float *pf_x = nullptr, *pf_q = nullptr, *pf_p[3] = {nullptr, nullptr, nullptr};
+    size_t pf_pbytes[3] = {0, 0, 0};
+    uint16_t *pf_xb = nullptr;
 };
 
 namespace {
@@ -623,6 +631,7 @@ void oi_engine_destroy(oi_engine *e) {
     if (e->gexec) hipGraphExecDestroy(e->gexec);
     if (e->graph) hipGraphDestroy(e->graph);
     if (e->arena.base) hipFree(e->arena.base);
+    if (e->pf_mem) hipFree(e->pf_mem);
     if (e->sa.trace) hipFree(e->sa.trace);
     if (e->logits_host) hipHostFree(e->logits_host);
     if (e->state_host) hipHostFree(e->state_host);
@@ -942,6 +951,166 @@ const float *oi_engine_forward(oi_engine *e, int32_t token, int32_t pos) {
     }
     if (check_stream_error(e)) return nullptr;
     e->last_pos = pos;
+    return e->logits_host;
+}
+
+// ------------------------------------------------------ batched prefill --
+// Max tokens per batched chunk and the chunking rule of the reference
+// (qwen3_5/metal.odin:22 MAX_BATCH_T; engine.odin:66-93: chunks of a multiple
+// of 8 tokens, the trailing 1-7 tokens one at a time).
+constexpr int PF_MAX_T = 512;
+
+namespace {
+
+bool prefill_batched_ok(const oi_engine *e) {
+    if (e->cfg.head_dim != 128 && e->cfg.head_dim != 256) return false;
+    for (const LayerDev &L : e->layers)
+        for (const DMat *m : {&L.wq, &L.wk, &L.wv, &L.wo, &L.w1, &L.w2, &L.w3})
+            if (!gemm_supported(*m)) return false;
+    return true;
+}
+
+size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+int prefill_alloc(oi_engine *e) {
+    if (e->pf_mem) return OI_OK;
+    const oi_config &c = e->cfg;
+    const size_t D = (size_t)c.dim, QD = (size_t)c.n_heads * c.head_dim, H = (size_t)c.hidden_dim;
+    // partial products: buffer 0 takes q, wo, gate and down, buffer 1 k and
+    // up, buffer 2 v; each sized for the largest K split of any chunk length
+    size_t need[3] = {0, 0, 0};
+    for (const LayerDev &L : e->layers) {
+        const std::pair<const DMat *, int> uses[] = {{&L.wq, 0}, {&L.wo, 0}, {&L.w1, 0}, {&L.w2, 0},
+                                                     {&L.wk, 1}, {&L.w3, 1}, {&L.wv, 2}};
+        for (const auto &u : uses)
+            for (int T = 8; T <= PF_MAX_T; T += 8)
+                need[u.second] = std::max(need[u.second],
+                                          (size_t)gemm_split(*u.first, T, SIZE_MAX) * T * u.first->rows * 4);
+    }
+    const size_t xb = (size_t)PF_MAX_T * std::max({D, QD, H}) * 2;
+    size_t total = al256(PF_MAX_T * 4) + al256(PF_MAX_T * D * 4) + al256(PF_MAX_T * QD * 4) + al256(xb);
+    for (size_t b : need) total += al256(b);
+    HIP_TRY(hipMalloc(&e->pf_mem, total));
+    uint8_t *p = (uint8_t *)e->pf_mem;
+    auto take = [&](size_t b) {
+        uint8_t *r = p;
+        p += al256(b);
+        return r;
+    };
+    e->pf_tok = (int32_t *)take(PF_MAX_T * 4);
+    e->pf_x = (float *)take(PF_MAX_T * D * 4);
+    e->pf_q = (float *)take(PF_MAX_T * QD * 4);
+    e->pf_xb = (uint16_t *)take(xb);
+    for (int i = 0; i < 3; i++) {
+        e->pf_p[i] = (float *)take(need[i]);
+        e->pf_pbytes[i] = need[i];
+    }
+    return OI_OK;
+}
+
+// One batched chunk of T tokens at positions pos .. pos+T-1 (forward_gpu_batch,
+// qwen3_5/metal.odin:1472-1654, for the dense decoder of infer/forward.odin):
+// per layer the three attention projections, q/k norm + RoPE + cache store,
+// causal attention, wo + residual, then the MLP projections, SwiGLU, down +
+// residual, all over the T tokens; at the end the final norm and classifier
+// of the last token.
+int prefill_chunk(oi_engine *e, const int32_t *tokens, int T, int pos) {
+    const hipStream_t st = e->stream;
+    const oi_config &c = e->cfg;
+    const int D = (int)c.dim, QD = (int)(c.n_heads * c.head_dim), H = (int)c.hidden_dim, hd = (int)c.head_dim;
+    const float eps = c.rms_eps;
+    HIP_TRY(hipMemcpyAsync(e->pf_tok, tokens, (size_t)T * 4, hipMemcpyHostToDevice, st));
+    HIP_TRY(launch_embed_rows(e->tok_embd, e->pf_tok, T, e->pf_x, st));
+    float *const *P = e->pf_p;
+    const size_t *PB = e->pf_pbytes;
+    for (const LayerDev &L : e->layers) {
+        int qs = 1, ks = 1, vs = 1, s0 = 1, s1 = 1;
+        HIP_TRY(launch_pf_rmsnorm16(e->pf_x, L.attn_norm, eps, D, T, e->pf_xb, st));
+        HIP_TRY(launch_gemm_parts(L.wq, e->pf_xb, T, P[0], PB[0], &qs, st));
+        HIP_TRY(launch_gemm_parts(L.wk, e->pf_xb, T, P[1], PB[1], &ks, st));
+        HIP_TRY(launch_gemm_parts(L.wv, e->pf_xb, T, P[2], PB[2], &vs, st));
+        PfQkvArgs qa{P[0], P[1], P[2], qs, ks, vs, L.q_norm, L.k_norm, eps, e->rope_cs, L.kc, L.vc, e->pf_q,
+                     T, pos, (int32_t)c.seq_len, (int32_t)c.n_heads, (int32_t)c.n_kv_heads};
+        HIP_TRY(launch_pf_qkv(qa, hd, st));
+        HIP_TRY(launch_pf_attn(e->pf_q, L.kc, L.vc, e->pf_xb, T, pos, (int)c.seq_len, (int)c.n_heads,
+                               (int)c.n_kv_heads, hd, st));
+        HIP_TRY(launch_gemm_parts(L.wo, e->pf_xb, T, P[0], PB[0], &s0, st));
+        HIP_TRY(launch_pf_add(e->pf_x, P[0], s0, (int64_t)T * D, st));
+        HIP_TRY(launch_pf_rmsnorm16(e->pf_x, L.ffn_norm, eps, D, T, e->pf_xb, st));
+        HIP_TRY(launch_gemm_parts(L.w1, e->pf_xb, T, P[0], PB[0], &s0, st));
+        HIP_TRY(launch_gemm_parts(L.w3, e->pf_xb, T, P[1], PB[1], &s1, st));
+        HIP_TRY(launch_pf_swiglu16(P[0], s0, P[1], s1, (int64_t)T * H, e->pf_xb, st));
+        HIP_TRY(launch_gemm_parts(L.w2, e->pf_xb, T, P[0], PB[0], &s0, st));
+        HIP_TRY(launch_pf_add(e->pf_x, P[0], s0, (int64_t)T * D, st));
+    }
+    GemvArgs a = gemv_args(GEMV_STORE, D, e->pf_x + (size_t)(T - 1) * D, e->output_norm, eps);
+    a.nseg = 1;
+    a.seg[0].m = e->output;
+    a.seg[0].y = e->logits;
+    if (!plan_gemv(a)) return fail(OI_E_DEVICE, "internal: classifier plan");
+    HIP_TRY(launch_gemv(a, st));
+    (void)QD;
+    return OI_OK;
+}
+
+}  // namespace
+
+const float *oi_engine_prefill(oi_engine *e, const int32_t *tokens, int32_t n, int32_t pos0) {
+    if (!e || !tokens) {
+        fail(OI_E_ARG, "null argument");
+        return nullptr;
+    }
+    if (n <= 0) {
+        fail(OI_E_ARG, "prefill: no tokens");
+        return nullptr;
+    }
+    if (pos0 < 0 || (int64_t)pos0 + n > e->cfg.seq_len) {
+        fail(OI_E_RANGE, "prefill: positions [" + std::to_string(pos0) + ", " + std::to_string((int64_t)pos0 + n) +
+                             ") out of range (seq_len=" + std::to_string(e->cfg.seq_len) + ")");
+        return nullptr;
+    }
+    for (int32_t i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= e->cfg.vocab_size) {
+            fail(OI_E_RANGE, "prefill: token=" + std::to_string(tokens[i]) + " out of range (vocab=" +
+                                 std::to_string(e->cfg.vocab_size) + ")");
+            return nullptr;
+        }
+    if (hipSetDevice(e->device) != hipSuccess) {
+        fail(OI_E_DEVICE, "hipSetDevice failed");
+        return nullptr;
+    }
+    const bool batched = prefill_batched_ok(e);
+    if (batched && prefill_alloc(e)) return nullptr;
+    if (ensure_graph(e)) return nullptr;
+    int i = 0;
+    while (i < n) {
+        const int rem = n - i;
+        if (batched && rem >= 8) {
+            int chunk = std::min(PF_MAX_T, rem);
+            chunk -= chunk % 8;
+            if (prefill_chunk(e, tokens + i, chunk, pos0 + i)) return nullptr;
+            i += chunk;
+        } else {  // one token through the decode path
+            if (set_state(e, tokens[i], pos0 + i, 0) || run_token(e)) return nullptr;
+            // the state copy reads pinned host memory when the stream reaches
+            // it: the next token's state must not be written before that
+            const hipError_t r = hipStreamSynchronize(e->stream);
+            if (r != hipSuccess) {
+                fail(OI_E_DEVICE, std::string("prefill: ") + hipGetErrorString(r));
+                return nullptr;
+            }
+            i += 1;
+        }
+    }
+    hipError_t r = hipMemcpyAsync(e->logits_host, e->logits, (size_t)e->cfg.vocab_size * 4, hipMemcpyDeviceToHost,
+                                  e->stream);
+    if (r == hipSuccess) r = hipStreamSynchronize(e->stream);
+    if (r != hipSuccess) {
+        fail(OI_E_DEVICE, std::string("prefill: ") + hipGetErrorString(r));
+        return nullptr;
+    }
+    if (check_stream_error(e)) return nullptr;
+    e->last_pos = pos0 + n - 1;
     return e->logits_host;
 }
 

@@ -419,4 +419,20 @@ hipError_t launch_gemm(const DMat &m, const uint16_t *x, int32_t n, float *c, fl
     return hipGetLastError();
 }
 
+hipError_t launch_gemm_parts(const DMat &m, const uint16_t *x, int32_t n, float *part, size_t part_bytes, int *split,
+                             hipStream_t st) {
+    if (!gemm_supported(m) || n <= 0 || !part || part_bytes < (size_t)n * m.rows * 4) return hipErrorInvalidValue;
+    const int nchunk = m.cols / GM_KC;
+    *split = gemm_split(m, n, part_bytes);
+    const int cps = (nchunk + *split - 1) / *split;
+    GemmArgs a{m, x, part, n};
+    dim3 grid((m.rows + GM_ROWS - 1) / GM_ROWS, (n + GM_TOK - 1) / GM_TOK, *split), block(GM_THREADS);
+    switch (m.type) {
+    case T_Q4_K: hipLaunchKernelGGL(gemm_q_kernel<GQ4K>, grid, block, 0, st, a, cps); break;
+    case T_Q6_K: hipLaunchKernelGGL(gemm_q_kernel<GQ6K>, grid, block, 0, st, a, cps); break;
+    default: hipLaunchKernelGGL(gemm_q_kernel<GQ80>, grid, block, 0, st, a, cps); break;
+    }
+    return hipGetLastError();
+}
+
 }  // namespace oi

@@ -118,6 +118,18 @@ __global__ __launch_bounds__(WG) void dequant_kernel(DMat m, float *out) {
 }
 
 // ------------------------------------------------------------- embedding --
+// x[t] = dequant(token_embd[tokens[t]]) for the tokens of a prefill batch
+// (forward_gpu_batch's get_embedding_row per token, metal.odin:1499-1501).
+// Grid (ceil(units / WG), n): one unit of 64 weights per thread.
+__global__ __launch_bounds__(WG) void embed_rows_kernel(DMat emb, const int32_t *tokens, float *x) {
+    const int units = emb.cols / 64, u = (int)blockIdx.x * WG + threadIdx.x, t = blockIdx.y;
+    if (u >= units) return;
+    float v[64];
+    decode_unit(emb, tokens[t], u, v);
+    float *o = x + (size_t)t * emb.cols;
+    for (int j = 0; j < 64; j++) o[unit_elem(emb.type, u, j)] = v[j];
+}
+
 static // x = dequant(token_embd[token]) (infer/forward.odin:72-75, 103)
 __global__ __launch_bounds__(WG) void embed_kernel(DMat emb, int32_t *state, float *x, int32_t vocab,
                                                    const float *am_val, const int32_t *am_idx, int32_t *tokens_out,
@@ -407,6 +419,13 @@ hipError_t launch_embed(const DMat &emb, int32_t *state, float *x, int32_t vocab
                         const int32_t *am_idx, int32_t *tokens_out, int finalize_only, hipStream_t st) {
     hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(WG), 0, st, emb, state, x, vocab, am_val, am_idx, tokens_out,
                        finalize_only);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_rows(const DMat &emb, const int32_t *tokens, int n, float *x, hipStream_t st) {
+    const int units = emb.cols / 64;
+    hipLaunchKernelGGL(embed_rows_kernel, dim3((unsigned)((units + WG - 1) / WG), (unsigned)n), dim3(WG), 0, st, emb,
+                       tokens, x);
     return hipGetLastError();
 }
 

@@ -123,4 +123,31 @@ int gemm_split(const DMat &m, int32_t n, size_t part_bytes);
 hipError_t launch_gemm(const DMat &m, const uint16_t *x, int32_t n, float *c, float *part, size_t part_bytes,
                        hipStream_t st);
 
+// gemm.hip, for consumers that sum the K slices themselves: the partial
+// products go to part ([split][n][rows]; with split 1 the product itself)
+hipError_t launch_gemm_parts(const DMat &m, const uint16_t *x, int32_t n, float *part, size_t part_bytes, int *split,
+                             hipStream_t st);
+
+// prefill.hip: the per-token operations of batched prefill
+struct PfQkvArgs {
+    const float *q, *k, *v;     // projections' partial products [split][T][rows]
+    int32_t qs, ks, vs;         // their K slices
+    const float *q_norm, *k_norm;
+    float eps;
+    const float2 *rope_cs;      // [seq_len][head_dim / 2]
+    uint16_t *kc, *vc;          // this layer's cache
+    float *qout;                // [T][n_heads * head_dim]
+    int32_t T, pos0, seq_len, n_heads, n_kv_heads;
+};
+hipError_t launch_pf_rmsnorm16(const float *x, const float *w, float eps, int dim, int T, uint16_t *out,
+                               hipStream_t st);
+hipError_t launch_pf_qkv(const PfQkvArgs &a, int head_dim, hipStream_t st);
+hipError_t launch_pf_attn(const float *q, const uint16_t *kc, const uint16_t *vc, uint16_t *out, int T, int pos0,
+                          int seq_len, int n_heads, int n_kv_heads, int head_dim, hipStream_t st);
+hipError_t launch_pf_add(float *x, const float *part, int split, int64_t total, hipStream_t st);
+hipError_t launch_pf_swiglu16(const float *g, int gs, const float *u, int us, int64_t total, uint16_t *out,
+                              hipStream_t st);
+// kernels.hip: x[t] = dequant(emb[tokens[t]]) for n tokens
+hipError_t launch_embed_rows(const DMat &emb, const int32_t *tokens, int n, float *x, hipStream_t st);
+
 }  // namespace oi

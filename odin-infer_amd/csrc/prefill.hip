@@ -1,0 +1,244 @@
+// prefill.hip -- the per-token operations of batched prefill for T tokens at
+// once (reference: qwen3_5/metal.odin:1472-1654 forward_gpu_batch; the per-token
+// math is infer/forward.odin:17-146).  The projections between them run on the
+// matrix cores (gemm.hip) with f16-staged operands, as the reference's MMQ; the
+// kernels here take the projections' K-slice partial products directly and sum
+// them in slice order, so no separate reduction runs.
+//
+// Layouts: activations token-major, x [T][dim] f32; the inputs of the
+// projections f16 [T][K]; the KV cache f16 [n_kv_heads][seq_len][head_dim] per
+// layer, shared with the decode path.  Token t sits at position pos0 + t.
+
+#include "device_common.h"
+
+namespace oi {
+
+static __device__ __forceinline__ float block_sum(float v, float *red) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    __syncthreads();  // red reusable
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < WG / WAVE; w++) s += red[w];
+    return s;
+}
+
+// sum of the K-slice partial products of element i
+static __device__ __forceinline__ float parts_at(const float *p, int split, size_t slice, size_t i) {
+    float s = p[i];
+    for (int z = 1; z < split; z++) s += p[(size_t)z * slice + i];
+    return s;
+}
+
+// out[t][i] = f16(w[i] * (s * x[t][i])), s = 1 / sqrt(sum x^2 / dim + eps)
+// (ops.odin rmsnorm; the reference converts the f32 result to half for the
+// projection, metal.odin:1236-1242).  Grid: T.
+__global__ __launch_bounds__(WG) void pf_rmsnorm16_kernel(const float *x, const float *w, float eps, int dim,
+                                                          uint16_t *out) {
+#pragma clang fp contract(off)
+    __shared__ float red[WG / WAVE];
+    const size_t t = blockIdx.x;
+    const float *xt = x + t * dim;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < dim; i += WG) ss += xt[i] * xt[i];
+    ss = block_sum(ss, red);
+    const float s = 1.0f / sqrtf(ss / (float)dim + eps);
+    for (int i = threadIdx.x; i < dim; i += WG) out[t * dim + i] = f2h(w[i] * (s * xt[i]));
+}
+
+// Per token (grid T) and head (one wave each): q and k heads RMSNorm'd with
+// q_norm / k_norm and rotated at pos0 + t (forward.odin:57-85, pairs i and
+// i + hd/2); k and v rounded to f16 into the cache at pos0 + t; q kept in f32.
+// Lane l holds dimensions l + 64 e, so the RoPE pair of e is e + DPL/2.
+template <int HD>
+__global__ __launch_bounds__(WG) void pf_qkv_kernel(PfQkvArgs a) {
+#pragma clang fp contract(off)
+    constexpr int DPL = HD / WAVE;
+    const int t = blockIdx.x, lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    const int pos = a.pos0 + t, QD = a.n_heads * HD, KVD = a.n_kv_heads * HD;
+    for (int hh = wave; hh < a.n_heads + 2 * a.n_kv_heads; hh += WG / WAVE) {
+        const bool isq = hh < a.n_heads, isk = !isq && hh < a.n_heads + a.n_kv_heads;
+        const int h = isq ? hh : isk ? hh - a.n_heads : hh - a.n_heads - a.n_kv_heads;
+        const float *src = isq ? a.q : isk ? a.k : a.v;
+        const int split = isq ? a.qs : isk ? a.ks : a.vs;
+        const int rows = isq ? QD : KVD;
+        float v[DPL];
+#pragma unroll
+        for (int e = 0; e < DPL; e++)
+            v[e] = parts_at(src, split, (size_t)a.T * rows, (size_t)t * rows + h * HD + lane + WAVE * e);
+        if (isq || isk) {
+            const float *nw = isq ? a.q_norm : a.k_norm;
+            float ss = 0.f;
+#pragma unroll
+            for (int e = 0; e < DPL; e++) ss += v[e] * v[e];
+            ss = wave_sum(ss);
+            const float s = 1.0f / sqrtf(ss / (float)HD + a.eps);
+#pragma unroll
+            for (int e = 0; e < DPL; e++) v[e] = nw[lane + WAVE * e] * (s * v[e]);
+#pragma unroll
+            for (int e = 0; e < DPL / 2; e++) {
+                const float2 cs = a.rope_cs[(size_t)pos * (HD / 2) + lane + WAVE * e];
+                const float x = v[e], y = v[e + DPL / 2];
+                v[e] = x * cs.x - y * cs.y;
+                v[e + DPL / 2] = x * cs.y + y * cs.x;
+            }
+        }
+        if (isq) {
+#pragma unroll
+            for (int e = 0; e < DPL; e++) a.qout[(size_t)t * QD + h * HD + lane + WAVE * e] = v[e];
+        } else {
+            uint16_t *c = (isk ? a.kc : a.vc) + ((size_t)h * a.seq_len + pos) * HD;
+#pragma unroll
+            for (int e = 0; e < DPL; e++) c[lane + WAVE * e] = f2h(v[e]);
+        }
+    }
+}
+
+struct PfAttnArgs {
+    const float *q;             // [T][n_heads * head_dim]
+    const uint16_t *kc, *vc;    // this layer's cache
+    uint16_t *out;              // [T][n_heads * head_dim] f16 (the wo projection's input)
+    int32_t pos0, seq_len, n_heads, n_kv_heads;
+};
+
+// Causal attention of token t (query head h, grid (n_heads, T)) over positions
+// 0 .. pos0 + t of the f16 cache (forward.odin:87-115: scores q.k / sqrt(hd),
+// softmax, weighted sum of v).  Each wave takes blocks of 64 positions (lane =
+// position) with a running max and sum; the four waves' (m, l, o) are merged
+// at the end.  Lane l accumulates dimensions DPL l .. DPL l + DPL-1.
+template <int HD>
+__global__ __launch_bounds__(WG) void pf_attn_kernel(PfAttnArgs a) {
+    constexpr int DPL = HD / WAVE, NW = WG / WAVE;
+    __shared__ float qs[HD];
+    __shared__ float mw[NW], lw[NW];
+    __shared__ float ow[NW][HD];
+    const int h = blockIdx.x, t = blockIdx.y;
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    const int QD = a.n_heads * HD, kvh = h / (a.n_heads / a.n_kv_heads), L = a.pos0 + t + 1;
+    for (int i = threadIdx.x; i < HD; i += WG) qs[i] = a.q[(size_t)t * QD + h * HD + i];
+    __syncthreads();
+    const uint16_t *kc = a.kc + (size_t)kvh * a.seq_len * HD, *vc = a.vc + (size_t)kvh * a.seq_len * HD;
+    const float rs = sqrtf((float)HD);
+    float m = -INFINITY, l = 0.f, o[DPL];
+#pragma unroll
+    for (int e = 0; e < DPL; e++) o[e] = 0.f;
+    for (int base = WAVE * wave; base < L; base += WG) {
+        const int p = base + lane;
+        float s = -INFINITY;
+        if (p < L) {
+            const u32x4 *kr = (const u32x4 *)(kc + (size_t)p * HD);
+            float acc = 0.f;
+            for (int c = 0; c < HD / 8; c++) {
+                const u32x4 w = kr[c];
+#pragma unroll
+                for (int e = 0; e < 8; e++) acc += qs[8 * c + e] * h2f((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+            }
+            s = acc / rs;
+        }
+        float bm = s;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) bm = fmaxf(bm, __shfl_xor(bm, off, WAVE));
+        const float mn = fmaxf(m, bm), alpha = expf(m - mn);
+        const float pj = p < L ? expf(s - mn) : 0.f;
+        l = l * alpha + wave_sum(pj);
+#pragma unroll
+        for (int e = 0; e < DPL; e++) o[e] *= alpha;
+        const int nj = min(WAVE, L - base);
+        for (int j = 0; j < nj; j++) {
+            const float pb = __shfl(pj, j, WAVE);
+            const uint16_t *vr = vc + (size_t)(base + j) * HD + DPL * lane;
+            if constexpr (DPL == 2) {
+                const uint32_t w = *(const uint32_t *)vr;
+                o[0] += pb * h2f(w & 0xFFFFu);
+                o[1] += pb * h2f(w >> 16);
+            } else {
+                const u32x2 w = *(const u32x2 *)vr;
+#pragma unroll
+                for (int e = 0; e < DPL; e++) o[e] += pb * h2f((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+            }
+        }
+        m = mn;
+    }
+    if (lane == 0) {
+        mw[wave] = m;
+        lw[wave] = l;
+    }
+#pragma unroll
+    for (int e = 0; e < DPL; e++) ow[wave][DPL * lane + e] = o[e];
+    __syncthreads();
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; w++) M = fmaxf(M, mw[w]);
+    float lt = 0.f, sc[NW];
+#pragma unroll
+    for (int w = 0; w < NW; w++) {
+        sc[w] = mw[w] == -INFINITY ? 0.f : expf(mw[w] - M);  // a wave with no positions adds nothing
+        lt += lw[w] * sc[w];
+    }
+    for (int i = threadIdx.x; i < HD; i += WG) {
+        float acc = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) acc += ow[w][i] * sc[w];
+        a.out[(size_t)t * QD + h * HD + i] = f2h(acc / lt);
+    }
+}
+
+// x[i] += sum of the partial products of element i (the residual adds,
+// forward.odin:117-119, 137-139)
+__global__ __launch_bounds__(WG) void pf_add_kernel(float *x, const float *part, int split, int64_t total) {
+    const int64_t i = (int64_t)blockIdx.x * WG + threadIdx.x;
+    if (i < total) x[i] += parts_at(part, split, (size_t)total, (size_t)i);
+}
+
+// out[i] = f16(silu(g[i]) * u[i]) from the gate and up projections' partial
+// products (forward.odin:128-133, separately rounded as the reference)
+__global__ __launch_bounds__(WG) void pf_swiglu16_kernel(const float *g, int gs, const float *u, int us, int64_t total,
+                                                         uint16_t *out) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t)blockIdx.x * WG + threadIdx.x;
+    if (i >= total) return;
+    float val = parts_at(g, gs, (size_t)total, (size_t)i);
+    val *= 1.0f / (1.0f + expf(-val));
+    val *= parts_at(u, us, (size_t)total, (size_t)i);
+    out[i] = f2h(val);
+}
+
+static unsigned blocks(int64_t n) { return (unsigned)((n + WG - 1) / WG); }
+
+hipError_t launch_pf_rmsnorm16(const float *x, const float *w, float eps, int dim, int T, uint16_t *out,
+                               hipStream_t st) {
+    hipLaunchKernelGGL(pf_rmsnorm16_kernel, dim3(T), dim3(WG), 0, st, x, w, eps, dim, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_pf_qkv(const PfQkvArgs &a, int head_dim, hipStream_t st) {
+    if (head_dim == 128) hipLaunchKernelGGL(pf_qkv_kernel<128>, dim3(a.T), dim3(WG), 0, st, a);
+    else if (head_dim == 256) hipLaunchKernelGGL(pf_qkv_kernel<256>, dim3(a.T), dim3(WG), 0, st, a);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_pf_attn(const float *q, const uint16_t *kc, const uint16_t *vc, uint16_t *out, int T, int pos0,
+                          int seq_len, int n_heads, int n_kv_heads, int head_dim, hipStream_t st) {
+    PfAttnArgs a{q, kc, vc, out, pos0, seq_len, n_heads, n_kv_heads};
+    const dim3 grid((unsigned)n_heads, (unsigned)T);
+    if (head_dim == 128) hipLaunchKernelGGL(pf_attn_kernel<128>, grid, dim3(WG), 0, st, a);
+    else if (head_dim == 256) hipLaunchKernelGGL(pf_attn_kernel<256>, grid, dim3(WG), 0, st, a);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_pf_add(float *x, const float *part, int split, int64_t total, hipStream_t st) {
+    hipLaunchKernelGGL(pf_add_kernel, dim3(blocks(total)), dim3(WG), 0, st, x, part, split, total);
+    return hipGetLastError();
+}
+
+hipError_t launch_pf_swiglu16(const float *g, int gs, const float *u, int us, int64_t total, uint16_t *out,
+                              hipStream_t st) {
+    hipLaunchKernelGGL(pf_swiglu16_kernel, dim3(blocks(total)), dim3(WG), 0, st, g, gs, u, us, total, out);
+    return hipGetLastError();
+}
+
+}  // namespace oi

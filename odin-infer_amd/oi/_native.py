@@ -33,6 +33,7 @@ HIP_SYMBOLS = {
     "oi_engine_load": (c_i32, [ctypes.c_char_p, ctypes.POINTER(Opts), ctypes.POINTER(c_vp)]),
     "oi_engine_destroy": (None, [c_vp]),
     "oi_engine_forward": (ctypes.POINTER(c_f), [c_vp, c_i32, c_i32]),
+    "oi_engine_prefill": (ctypes.POINTER(c_f), [c_vp, c_vp, c_i32, c_i32]),
     "oi_engine_config": (c_i32, [c_vp, ctypes.POINTER(Config)]),
     "oi_last_error": (ctypes.c_char_p, []),
     "oi_engine_decode_greedy": (c_i32, [c_vp, c_i32, c_i32, c_i32, c_vp]),

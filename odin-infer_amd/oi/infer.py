@@ -91,6 +91,19 @@ def engine_forward(e, token, pos):
     return np.ctypeslib.as_array(p, shape=(e.config.vocab_size,))
 
 
+def engine_forward_batch(e, tokens, pos_start):
+    """qwen3_5/engine.odin:61-93: consume `tokens` from `pos_start` (batched
+    chunks of a multiple of 8, up to 512; the trailing 1-7 one at a time);
+    returns the last token's logits (a view of engine memory)."""
+    t = np.ascontiguousarray(tokens, np.int32)
+    p = _native.hip().oi_engine_prefill(e.handle, t.ctypes.data, int(t.size), int(pos_start))
+    if not p:
+        L = _native.hip()
+        msg = L.oi_last_error().decode()
+        raise OIError(OI_E_RANGE if "out of range" in msg else -1 if "no tokens" in msg else -7, msg)
+    return np.ctypeslib.as_array(p, shape=(e.config.vocab_size,))
+
+
 def engine_config(e):
     """infer/engine.odin:54-56."""
     return e.config

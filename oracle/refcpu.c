@@ -733,6 +733,11 @@ typedef struct {
     int kv_f16;
     gfile g;
     mm_pool *pool;
+    /* f16-rounded dequantized projection weights of the batched path, per
+     * tensor, made on first use (ref_engine_prefill) */
+    const uint8_t **stg_key;
+    float **stg_w;
+    int n_stg;
 } ref_engine;
 
 static int require(ref_engine *e, const char *name, gtensor **out) { /* model.odin:82-97 */
@@ -761,6 +766,8 @@ EXPORT void ref_engine_destroy(void *h) {
     free(e->x); free(e->xb); free(e->xb2); free(e->xb3); free(e->hb); free(e->hb2);
     free(e->q); free(e->att); free(e->logits); free(e->key_cache); free(e->value_cache);
     free(e->ktmp); free(e->vtmp);
+    for (int i = 0; i < e->n_stg; i++) free(e->stg_w[i]);
+    free(e->stg_key); free(e->stg_w);
     free(e->layers);
     pool_destroy(e->pool);
     gfile_free(&e->g);
@@ -887,10 +894,53 @@ EXPORT int ref_engine_kv_fill(void *h, int layer, int pos0, int npos, const uint
     return 0;
 }
 
-/* forward (infer/forward.odin:17-146).  Returns the engine-owned logits, or
- * NULL (with ref_last_error) where the reference prints and exits. */
-EXPORT const float *ref_engine_forward(void *h, int token, int pos) {
-    ref_engine *e = (ref_engine *)h;
+/* The projection of the batched prefill path (forward_gpu_batch's MMQ,
+ * qwen3_5/metal.odin:1236-1243, 493-609): weights dequantized and rounded to
+ * f16, the input rounded to f16, products summed (in float64 here, as
+ * ref_gemm_f16).  xout[d] = W[d][n] x[n]. */
+static const float *staged_weights(ref_engine *e, int kind, const uint8_t *w, int64_t n, int64_t d) {
+    for (int i = 0; i < e->n_stg; i++)
+        if (e->stg_key[i] == w) return e->stg_w[i];
+    float *sw = malloc((size_t)(n * d) * sizeof(float));
+    const uint8_t **nk = realloc(e->stg_key, (size_t)(e->n_stg + 1) * sizeof *nk);
+    float **nw = realloc(e->stg_w, (size_t)(e->n_stg + 1) * sizeof *nw);
+    if (nk) e->stg_key = nk;
+    if (nw) e->stg_w = nw;
+    if (!sw || !nk || !nw) { free(sw); return NULL; }
+    const int64_t rb = ref_row_byte_size(kind, n);
+    for (int64_t r = 0; r < d; r++) {
+        ref_dequant_row(kind, w + r * rb, n, sw + r * n);
+        for (int64_t j = 0; j < n; j++) sw[r * n + j] = ref_f16_to_f32(ref_f32_to_f16(sw[r * n + j]));
+    }
+    e->stg_key[e->n_stg] = w;
+    e->stg_w[e->n_stg++] = sw;
+    return sw;
+}
+
+static int matmul_staged(ref_engine *e, float *xout, const float *x, int kind, const uint8_t *w, int64_t n,
+                         int64_t d) {
+    const float *sw = staged_weights(e, kind, w, n, d);
+    double *xs = malloc((size_t)n * sizeof(double));
+    if (!sw || !xs) {
+        free(xs);
+        snprintf(g_err, sizeof g_err, "prefill: out of memory");
+        return -1;
+    }
+    for (int64_t j = 0; j < n; j++) xs[j] = ref_f16_to_f32(ref_f32_to_f16(x[j]));
+    for (int64_t r = 0; r < d; r++) {
+        double acc = 0.0;
+        for (int64_t j = 0; j < n; j++) acc += (double)sw[r * n + j] * xs[j];
+        xout[r] = (float)acc;
+    }
+    free(xs);
+    return 0;
+}
+
+/* forward (infer/forward.odin:17-146); with `staged` the seven projections of
+ * each layer are the batched path's (matmul_staged), and without `logits` the
+ * final norm and classifier are skipped (forward_gpu_batch computes them for
+ * the last token only, metal.odin:1637-1641). */
+static const float *forward_impl(ref_engine *e, int token, int pos, int staged, int logits) {
     if (pos < 0 || pos >= e->seq_len) {
         snprintf(g_err, sizeof g_err, "forward: pos=%d out of range (seq_len=%lld)", pos, (long long)e->seq_len);
         return NULL;
@@ -919,9 +969,14 @@ EXPORT const float *ref_engine_forward(void *h, int token, int pos) {
         float *vv = e->kv_f16 ? e->vtmp : v_slice;
 
         ref_rmsnorm(e->xb, e->x, lw->attn_norm, dim, eps);
-        matmul_t(P, e->q, e->xb, lw->wq.kind, lw->wq.data, dim, att_head_dim);
-        matmul_t(P, kk, e->xb, lw->wk.kind, lw->wk.data, dim, kv_dim);
-        matmul_t(P, vv, e->xb, lw->wv.kind, lw->wv.data, dim, kv_dim);
+#define MM(out, in, t, n, d)                                                      \
+    do {                                                                          \
+        if (!staged) matmul_t(P, out, in, (t).kind, (t).data, n, d);              \
+        else if (matmul_staged(e, out, in, (t).kind, (t).data, n, d)) return NULL; \
+    } while (0)
+        MM(e->q, e->xb, lw->wq, dim, att_head_dim);
+        MM(kk, e->xb, lw->wk, dim, kv_dim);
+        MM(vv, e->xb, lw->wv, dim, kv_dim);
 
         /* RoPE + per-head Q/K RMSNorm, forward.odin:57-85 */
         for (int64_t h = 0; h < n_heads; h++) {
@@ -973,25 +1028,62 @@ EXPORT const float *ref_engine_forward(void *h, int token, int pos) {
             }
         }
 
-        matmul_t(P, e->xb2, e->xb3, lw->wo.kind, lw->wo.data, att_head_dim, dim);
+        MM(e->xb2, e->xb3, lw->wo, att_head_dim, dim);
         for (int64_t i = 0; i < dim; i++) e->x[i] += e->xb2[i];
 
         ref_rmsnorm(e->xb, e->x, lw->ffn_norm, dim, eps);
-        matmul_t(P, e->hb, e->xb, lw->w1.kind, lw->w1.data, dim, hidden_dim);
-        matmul_t(P, e->hb2, e->xb, lw->w3.kind, lw->w3.data, dim, hidden_dim);
+        MM(e->hb, e->xb, lw->w1, dim, hidden_dim);
+        MM(e->hb2, e->xb, lw->w3, dim, hidden_dim);
         for (int64_t i = 0; i < hidden_dim; i++) { /* forward.odin:128-133 */
             float val = e->hb[i];
             val *= 1.0f / (1.0f + expf(-val));
             val *= e->hb2[i];
             e->hb2[i] = val;
         }
-        matmul_t(P, e->xb, e->hb2, lw->w2.kind, lw->w2.data, hidden_dim, dim);
+        MM(e->xb, e->hb2, lw->w2, hidden_dim, dim);
+#undef MM
         for (int64_t i = 0; i < dim; i++) e->x[i] += e->xb[i];
     }
 
+    if (!logits) return e->logits;
     ref_rmsnorm(e->x, e->x, e->output_norm, dim, eps);
     matmul_t(P, e->logits, e->x, e->output.kind, e->output.data, dim, e->vocab_size);
     return e->logits;
+}
+
+/* forward (infer/forward.odin:17-146).  Returns the engine-owned logits, or
+ * NULL (with ref_last_error) where the reference prints and exits. */
+EXPORT const float *ref_engine_forward(void *h, int token, int pos) {
+    return forward_impl((ref_engine *)h, token, pos, 0, 1);
+}
+
+/* engine_forward_batch (qwen3_5/engine.odin:61-93): chunks of up to
+ * MAX_BATCH_T = 512 tokens (metal.odin:22), cut to a multiple of 8, through
+ * the batched path (staged projections, logits of the chunk's last token);
+ * the trailing 1-7 tokens one at a time through forward.  Returns the last
+ * token's logits, or NULL. */
+EXPORT const float *ref_engine_prefill(void *h, const int *tokens, int n, int pos0) {
+    ref_engine *e = (ref_engine *)h;
+    if (n <= 0) {
+        snprintf(g_err, sizeof g_err, "prefill: no tokens");
+        return NULL;
+    }
+    const float *out = NULL;
+    int i = 0;
+    while (i < n) {
+        int rem = n - i;
+        if (rem >= 8) {
+            int chunk = rem < 512 ? rem : 512;
+            chunk -= chunk % 8;
+            for (int t = 0; t < chunk; t++)
+                if (!(out = forward_impl(e, tokens[i + t], pos0 + i + t, 1, t == chunk - 1))) return NULL;
+            i += chunk;
+        } else {
+            if (!(out = forward_impl(e, tokens[i], pos0 + i, 0, 1))) return NULL;
+            i += 1;
+        }
+    }
+    return out;
 }
 
 /* Hidden state after the final norm (test hook for layer-level checks). */

@@ -48,6 +48,8 @@ def lib():
         L.ref_engine_load.argtypes = [ctypes.c_char_p, c_int, c_int, c_int]
         L.ref_engine_forward.restype = ctypes.POINTER(c_f)
         L.ref_engine_forward.argtypes = [c_vp, c_int, c_int]
+        L.ref_engine_prefill.restype = ctypes.POINTER(c_f)
+        L.ref_engine_prefill.argtypes = [c_vp, c_vp, c_int, c_int]
         L.ref_engine_destroy.argtypes = [c_vp]
         L.ref_engine_config.argtypes = [c_vp, c_vp, c_vp]
         L.ref_engine_kv_fill.argtypes = [c_vp, c_int, c_int, c_int, c_vp, c_vp]
@@ -148,6 +150,15 @@ class RefEngine:
 
     def forward(self, token, pos):
         p = lib().ref_engine_forward(self.h, token, pos)
+        if not p:
+            raise RuntimeError(lib().ref_last_error().decode())
+        return np.ctypeslib.as_array(p, shape=(self.vocab_size,)).copy()
+
+    def prefill(self, tokens, pos0):
+        """engine_forward_batch: the last token's logits (batched chunks with
+        f16-staged projections, trailing tokens per token)."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        p = lib().ref_engine_prefill(self.h, _p(t), int(t.size), int(pos0))
         if not p:
             raise RuntimeError(lib().ref_last_error().decode())
         return np.ctypeslib.as_array(p, shape=(self.vocab_size,)).copy()

@@ -151,8 +151,11 @@ class GGUFWeights:
         return w.reshape(dims[::-1]) if len(dims) > 1 else w
 
 
-def forward_f64(W, tokens, f16_kv=True):
-    """Logits (float64) after each token of `tokens` at positions 0.. ."""
+def forward_f64(W, tokens, f16_kv=True, staged=()):
+    """Logits (float64) after each token of `tokens` at positions 0.. .
+    Positions in `staged` take the batched prefill path's projections: the
+    seven layer matrices and their inputs rounded to f16 before the product
+    (qwen3_5/metal.odin:1236-1243, 493-609)."""
     m = W.meta
     D = m["qwen3.embedding_length"]
     L = m["qwen3.block_count"]
@@ -183,16 +186,29 @@ def forward_f64(W, tokens, f16_kv=True):
         layers.append({k: W.get(p + k + ".weight") for k in
                        ["attn_norm", "ffn_norm", "attn_q_norm", "attn_k_norm", "attn_q", "attn_k", "attn_v",
                         "attn_output", "ffn_gate", "ffn_down", "ffn_up"]})
+    h16 = {}
+
+    def s16(a):
+        return a.astype(np.float16).astype(np.float64)
+
+    def mm(name, lw, l, x, st):
+        if not st:
+            return lw[name] @ x
+        if (l, name) not in h16:
+            h16[(l, name)] = s16(lw[name])
+        return h16[(l, name)] @ s16(x)
+
     kc = [[] for _ in range(L)]
     vc = [[] for _ in range(L)]
     outs = []
     for pos, tok in enumerate(tokens):
         x = emb[tok].copy()
+        st = pos in staged
         for l, lw in enumerate(layers):
             xb = rms(x, lw["attn_norm"])
-            q = (lw["attn_q"] @ xb).reshape(H, hd)
-            k = (lw["attn_k"] @ xb).reshape(KVH, hd)
-            v = (lw["attn_v"] @ xb).reshape(KVH, hd)
+            q = mm("attn_q", lw, l, xb, st).reshape(H, hd)
+            k = mm("attn_k", lw, l, xb, st).reshape(KVH, hd)
+            v = mm("attn_v", lw, l, xb, st).reshape(KVH, hd)
             q = rope(np.stack([rms(qh, lw["attn_q_norm"]) for qh in q]), pos)
             k = rope(np.stack([rms(kh, lw["attn_k_norm"]) for kh in k]), pos)
             kc[l].append(r16(k))
@@ -205,9 +221,9 @@ def forward_f64(W, tokens, f16_kv=True):
                 p_ = np.exp(sc - sc.max())
                 p_ /= p_.sum()
                 o[h] = p_ @ V[:, g, :]
-            x = x + lw["attn_output"] @ o.reshape(-1)
+            x = x + mm("attn_output", lw, l, o.reshape(-1), st)
             xb = rms(x, lw["ffn_norm"])
-            gt, up = lw["ffn_gate"] @ xb, lw["ffn_up"] @ xb
-            x = x + lw["ffn_down"] @ (gt / (1 + np.exp(-gt)) * up)
+            gt, up = mm("ffn_gate", lw, l, xb, st), mm("ffn_up", lw, l, xb, st)
+            x = x + mm("ffn_down", lw, l, gt / (1 + np.exp(-gt)) * up, st)
         outs.append(out_w @ rms(x, W.get("output_norm.weight")))
     return outs

@@ -146,6 +146,36 @@ def test_forward_vs_float64_model(make_model, name):
         r.close()
 
 
+@pytest.mark.parametrize("name", ["tiny-q4_k", "tiny-q8_0"])
+def test_prefill_vs_float64_model(make_model, name):
+    """The oracle's batched prefill (engine_forward_batch: a chunk of 8 with
+    f16-staged projections, then 3 tokens one at a time) against the float64
+    model with the same positions staged.  Staging moves these logits by
+    6.6e-4 / 8.3e-4 (scaled) while the oracle sits within 2.4e-4 of the staged
+    float64 model, so an unstaged chunk fails the bound below.  The
+    oracle-to-float64 distance is larger than for the per-token path (2e-4):
+    the f16 rounding of f32 and of float64 inputs lands apart near half-way
+    points."""
+    path = make_model(name)
+    W = npref.GGUFWeights(path)
+    tokens = [3, 7, 123, 5, 900, 42, 11, 0, 8, 64, 1]
+    ref = npref.forward_f64(W, tokens, f16_kv=True, staged=set(range(8)))
+    plain = npref.forward_f64(W, tokens, f16_kv=True)
+    r = refcpu.RefEngine(path, max_ctx=64, num_threads=4, kv_f16=True)
+    try:
+        got8 = r.prefill(tokens[:8], 0)
+        err8 = np.max(np.abs(got8 - ref[7])) / np.max(np.abs(ref[7]))
+        gap = np.max(np.abs(plain[7] - ref[7])) / np.max(np.abs(ref[7]))
+        assert err8 <= 3e-4 and gap >= 2.5 * err8, (err8, gap)
+        got = r.prefill(tokens[8:], 8)  # 3 tokens: per-token path after the staged chunk
+        err = np.max(np.abs(got - ref[-1])) / np.max(np.abs(ref[-1]))
+        assert err <= 2e-4, err
+        with pytest.raises(RuntimeError):
+            r.prefill([], 0)
+    finally:
+        r.close()
+
+
 def test_forward_f32_kv_mode(make_model):
     path = make_model("tiny-q8_0")
     W = npref.GGUFWeights(path)
