@@ -179,6 +179,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--model-path", default=None, help="reuse an existing synthetic GGUF")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM measurement")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the batched prefill measurement")
+    ap.add_argument("--prefill-tokens", type=int, default=512)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (3 times), to calibrate HBM counters")
     args = ap.parse_args()
@@ -261,6 +263,25 @@ def main():
             log("prefill GEMM: " + ", ".join("%s %dx64x%d %.1f us %.0f TFLOP/s" % (
                 g["type"], g["rows"], g["cols"], g["avg_us"], g["TFLOPs"]) for g in gemm))
 
+        prefill = None
+        if not args.no_prefill:
+            # batched prefill of a prompt at position 0 (overwrites the synthetic
+            # cache from position 0; the decode measurement is done)
+            n = args.prefill_tokens
+            ptoks = np.random.default_rng(99).integers(0, cfg.vocab_size, size=n).astype(np.int32)
+            infer.engine_forward_batch(e, ptoks, 0)  # warm (allocates the prefill buffers)
+            reps = 3
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                infer.engine_forward_batch(e, ptoks, 0)  # synchronous
+            pel = (time.perf_counter() - t0) / reps
+            D, QD, KVD, H = cfg.dim, cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim, cfg.hidden_dim
+            proj_flop = 2.0 * n * cfg.n_layers * (2 * D * QD + 2 * D * KVD + 3 * D * H)
+            prefill = {"tokens": n, "tok_s": round(n / pel, 1), "ms": round(1000 * pel, 3),
+                       "projection_TFLOPs": round(proj_flop / pel / 1e12, 1),
+                       "note": "host wall clock around oi_engine_prefill (synchronous), chunks of <=512 tokens"}
+            log("prefill: %d tokens in %.2f ms -> %.0f tok/s" % (n, 1000 * pel, n / pel))
+
         cpu = None
         if not args.no_cpu:
             log("CPU baseline (oracle) for up to %.0fs ..." % args.cpu_budget)
@@ -284,6 +305,7 @@ def main():
             "kernels": {n: {"avg_us": round(d["us"], 3), "GBps": round(d["GBps"], 1)} for n, d in kern.items()},
             "cpu_baseline": cpu,
             "prefill_gemm": gemm,
+            "prefill": prefill,
         }
         print(json.dumps(out), flush=True)
         infer.engine_destroy(e)

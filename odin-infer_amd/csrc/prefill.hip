@@ -13,6 +13,9 @@
 
 namespace oi {
 
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
 static __device__ __forceinline__ float block_sum(float v, float *red) {
     v = wave_sum(v);
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
@@ -185,6 +188,150 @@ __global__ __launch_bounds__(WG) void pf_attn_kernel(PfAttnArgs a) {
     }
 }
 
+// Causal attention on the matrix cores for head_dim 128, grid (n_heads,
+// ceil(T / 64)): a workgroup takes 64 queries of one head (wave w: queries
+// 16w .. 16w+15) and walks the keys in blocks of 64 up to its last query's
+// position.  Per block, K (rows padded to 136 halves) and V transposed (V^T,
+// rows of 68 halves) are staged in LDS; then per wave
+//   S^T[key][query] = K Q^T  (v_mfma_f32_16x16x32_f16; A = K rows, B = Q),
+//   online softmax per query (running max, exp, running sum),
+//   O^T[d][query] += V^T P^T (A = V^T rows, B = P).
+// In the S^T result lane (q, g) holds keys 4g+e of each 16-key tile for query
+// q, which is, without any lane exchange, the B operand of the second product
+// when its K index k = 8g + e stands for key 4g + e (e < 4) or 16 + 4g + e - 4
+// of a 32-key chunk; V^T is read with the same map.  Precision: q and p are
+// split into f16 hi + lo halves (two products each), K and V are exact f16,
+// accumulation is f32, so scores and weights keep about 22 bits, close to the
+// reference's f32 arithmetic (forward.odin:87-115).
+constexpr int FA_KP = 136, FA_VP = 68;  // LDS row strides (halves) of K and V^T
+
+static __device__ __forceinline__ void split16(const float (&v)[8], h8 &hi, h8 &lo) {
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        hi[e] = (_Float16)v[e];
+        lo[e] = (_Float16)(v[e] - (float)hi[e]);
+    }
+}
+
+__global__ __launch_bounds__(WG) void pf_fattn128_kernel(PfAttnArgs a, int T) {
+    constexpr int HD = 128;
+    __shared__ __attribute__((aligned(16))) uint16_t ks[64 * FA_KP];
+    __shared__ __attribute__((aligned(16))) uint16_t vt[HD * FA_VP];
+    const int h = blockIdx.x, t0 = 64 * (int)blockIdx.y;
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    const int q = lane & 15, g = lane >> 4;
+    const int QD = a.n_heads * HD, kvh = h / (a.n_heads / a.n_kv_heads);
+    const int tq = t0 + 16 * wave + q;                    // this lane's query (token)
+    const int qpos = a.pos0 + min(tq, T - 1);             // its position
+    const int last = a.pos0 + min(t0 + 63, T - 1);        // the workgroup's last query position
+    const int lmax = a.pos0 + T;                          // cache rows written so far
+    const uint16_t *kc = a.kc + (size_t)kvh * a.seq_len * HD, *vc = a.vc + (size_t)kvh * a.seq_len * HD;
+
+    // B operand of S^T: Q[query q][d = 32c + 8g + e], hi and lo halves
+    h8 qh[4], ql[4];
+    {
+        const float *qr = a.q + (size_t)min(tq, T - 1) * QD + h * HD;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            float v[8];
+            const float4 v0 = *(const float4 *)(qr + 32 * c + 8 * g), v1 = *(const float4 *)(qr + 32 * c + 8 * g + 4);
+            v[0] = v0.x; v[1] = v0.y; v[2] = v0.z; v[3] = v0.w;
+            v[4] = v1.x; v[5] = v1.y; v[6] = v1.z; v[7] = v1.w;
+            split16(v, qh[c], ql[c]);
+        }
+    }
+    const float rs = sqrtf((float)HD);
+    float m = -INFINITY, lsum = 0.f;
+    f32x4v o[8];
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++) o[dt] = f32x4v{0.f, 0.f, 0.f, 0.f};
+
+    for (int kb = 0; 64 * kb <= last; kb++) {
+        // stage K and V^T of keys 64 kb .. +63 (rows past the written range
+        // re-read the last written row; their scores are masked)
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int piece = threadIdx.x + WG * i, r = piece >> 4, c8 = piece & 15;  // row r, 8 halves at 8 c8
+            const int p = min(64 * kb + r, lmax - 1);
+            const u32x4 kv = *(const u32x4 *)(kc + (size_t)p * HD + 8 * c8);
+            *(u32x4 *)(ks + r * FA_KP + 8 * c8) = kv;
+            const u32x4 vv = *(const u32x4 *)(vc + (size_t)p * HD + 8 * c8);
+#pragma unroll
+            for (int e = 0; e < 8; e++) vt[(8 * c8 + e) * FA_VP + r] = (uint16_t)((vv[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+        }
+        __syncthreads();
+        // S^T tiles kt (keys 16 kt + 4g + e for query q)
+        float s[4][4];
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++) {
+            f32x4v acc = f32x4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const h8 kA = __builtin_bit_cast(h8, *(const u32x4 *)(ks + (16 * kt + q) * FA_KP + 32 * c + 8 * g));
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kA, qh[c], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kA, ql[c], acc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int p = 64 * kb + 16 * kt + 4 * g + e;
+                s[kt][e] = p <= qpos ? acc[e] / rs : -INFINITY;
+            }
+        }
+        float bm = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) bm = fmaxf(bm, s[kt][e]);
+        bm = fmaxf(bm, __shfl_xor(bm, 16, WAVE));
+        bm = fmaxf(bm, __shfl_xor(bm, 32, WAVE));
+        const float mn = fmaxf(m, bm), alpha = expf(m - mn);
+        m = mn;
+        float ps = 0.f;
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                s[kt][e] = expf(s[kt][e] - mn);
+                ps += s[kt][e];
+            }
+        lsum = lsum * alpha + ps;
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) o[dt] *= alpha;
+        // O^T += V^T P^T over the two 32-key chunks
+#pragma unroll
+        for (int kc2 = 0; kc2 < 2; kc2++) {
+            float pv[8];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                pv[e] = s[2 * kc2][e];
+                pv[4 + e] = s[2 * kc2 + 1][e];
+            }
+            h8 ph, pl;
+            split16(pv, ph, pl);
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) {
+                const uint16_t *vr = vt + (16 * dt + q) * FA_VP + 32 * kc2 + 4 * g;
+                const u32x2 v0 = *(const u32x2 *)vr, v1 = *(const u32x2 *)(vr + 16);
+                const h8 vA = __builtin_bit_cast(h8, u32x4{v0.x, v0.y, v1.x, v1.y});
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vA, ph, o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vA, pl, o[dt], 0, 0, 0);
+            }
+        }
+    }
+    lsum += __shfl_xor(lsum, 16, WAVE);
+    lsum += __shfl_xor(lsum, 32, WAVE);
+    if (tq < T) {
+        uint16_t *dst = a.out + (size_t)tq * QD + h * HD + 4 * g;
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) {
+            uint32_t w0 = (uint32_t)f2h(o[dt][0] / lsum) | ((uint32_t)f2h(o[dt][1] / lsum) << 16);
+            uint32_t w1 = (uint32_t)f2h(o[dt][2] / lsum) | ((uint32_t)f2h(o[dt][3] / lsum) << 16);
+            *(u32x2 *)(dst + 16 * dt) = u32x2{w0, w1};
+        }
+    }
+}
+
 // x[i] += sum of the partial products of element i (the residual adds,
 // forward.odin:117-119, 137-139)
 __global__ __launch_bounds__(WG) void pf_add_kernel(float *x, const float *part, int split, int64_t total) {
@@ -224,7 +371,9 @@ hipError_t launch_pf_attn(const float *q, const uint16_t *kc, const uint16_t *vc
                           int seq_len, int n_heads, int n_kv_heads, int head_dim, hipStream_t st) {
     PfAttnArgs a{q, kc, vc, out, pos0, seq_len, n_heads, n_kv_heads};
     const dim3 grid((unsigned)n_heads, (unsigned)T);
-    if (head_dim == 128) hipLaunchKernelGGL(pf_attn_kernel<128>, grid, dim3(WG), 0, st, a);
+    if (head_dim == 128)
+        hipLaunchKernelGGL(pf_fattn128_kernel, dim3((unsigned)n_heads, (unsigned)((T + 63) / 64)), dim3(WG), 0, st, a,
+                           T);
     else if (head_dim == 256) hipLaunchKernelGGL(pf_attn_kernel<256>, grid, dim3(WG), 0, st, a);
     else return hipErrorInvalidValue;
     return hipGetLastError();
