@@ -170,6 +170,27 @@ def prefill_gemm(iters=50):
     return out
 
 
+def measure_prefill(e, cfg, n, reps=3):
+    """Batched prefill of an n-token prompt at position 0 (engine_forward_batch,
+    synchronous): host wall clock per call after one warm call (which also
+    allocates the prefill buffers)."""
+    import numpy as np
+    from oi import infer
+    ptoks = np.random.default_rng(99).integers(0, cfg.vocab_size, size=n).astype(np.int32)
+    infer.engine_forward_batch(e, ptoks, 0)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        infer.engine_forward_batch(e, ptoks, 0)
+    pel = (time.perf_counter() - t0) / reps
+    D, QD, KVD, H = cfg.dim, cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim, cfg.hidden_dim
+    proj_flop = 2.0 * n * cfg.n_layers * (2 * D * QD + 2 * D * KVD + 3 * D * H)
+    log("prefill: %d tokens in %.2f ms -> %.0f tok/s" % (n, 1000 * pel, n / pel))
+    return {"tokens": n, "tok_s": round(n / pel, 1), "ms": round(1000 * pel, 3),
+            "projection_TFLOPs": round(proj_flop / pel / 1e12, 1),
+            "note": "host wall clock around oi_engine_prefill (synchronous), chunks of <=512 tokens; "
+                    "the prompt overwrites the cache from position 0 after the decode measurement"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -181,6 +202,8 @@ def main():
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM measurement")
     ap.add_argument("--no-prefill", action="store_true", help="skip the batched prefill measurement")
     ap.add_argument("--prefill-tokens", type=int, default=512)
+    ap.add_argument("--only", choices=["prefill", "gemm"], default=None,
+                    help="run one secondary measurement alone (for profiling) and print its JSON")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (3 times), to calibrate HBM counters")
     args = ap.parse_args()
@@ -204,6 +227,10 @@ def main():
     from oi import infer, synth
     import numpy as np
 
+    if args.only == "gemm":
+        print(json.dumps({"prefill_gemm": prefill_gemm()}), flush=True)
+        return
+
     tmpdir = None
     path = args.model_path
     spec = dict(synth.CONFIGS[MODEL])
@@ -219,6 +246,10 @@ def main():
         e, _ = infer.engine_load(path, infer.Engine_Opts(max_ctx=max_ctx))
         cfg = infer.engine_config(e)
         log("engine loaded in %.1fs (seq_len %d)" % (time.time() - t, cfg.seq_len))
+        if args.only == "prefill":
+            print(json.dumps({"prefill": measure_prefill(e, cfg, args.prefill_tokens)}), flush=True)
+            infer.engine_destroy(e)
+            return
         k, v = synth.kv_prefill(4242, cfg.n_layers, cfg.n_kv_heads, CONTEXT, cfg.head_dim)
         infer.engine_kv_fill(e, 0, 0, k, v)
         log("KV pre-filled to %d" % CONTEXT)
@@ -263,24 +294,7 @@ def main():
             log("prefill GEMM: " + ", ".join("%s %dx64x%d %.1f us %.0f TFLOP/s" % (
                 g["type"], g["rows"], g["cols"], g["avg_us"], g["TFLOPs"]) for g in gemm))
 
-        prefill = None
-        if not args.no_prefill:
-            # batched prefill of a prompt at position 0 (overwrites the synthetic
-            # cache from position 0; the decode measurement is done)
-            n = args.prefill_tokens
-            ptoks = np.random.default_rng(99).integers(0, cfg.vocab_size, size=n).astype(np.int32)
-            infer.engine_forward_batch(e, ptoks, 0)  # warm (allocates the prefill buffers)
-            reps = 3
-            t0 = time.perf_counter()
-            for _ in range(reps):
-                infer.engine_forward_batch(e, ptoks, 0)  # synchronous
-            pel = (time.perf_counter() - t0) / reps
-            D, QD, KVD, H = cfg.dim, cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim, cfg.hidden_dim
-            proj_flop = 2.0 * n * cfg.n_layers * (2 * D * QD + 2 * D * KVD + 3 * D * H)
-            prefill = {"tokens": n, "tok_s": round(n / pel, 1), "ms": round(1000 * pel, 3),
-                       "projection_TFLOPs": round(proj_flop / pel / 1e12, 1),
-                       "note": "host wall clock around oi_engine_prefill (synchronous), chunks of <=512 tokens"}
-            log("prefill: %d tokens in %.2f ms -> %.0f tok/s" % (n, 1000 * pel, n / pel))
+        prefill = None if args.no_prefill else measure_prefill(e, cfg, args.prefill_tokens)
 
         cpu = None
         if not args.no_cpu:
