@@ -170,6 +170,86 @@ def prefill_gemm(iters=50):
     return out
 
 
+def deltanet_step(iters=200):
+    """Gated DeltaNet token step (oi_deltanet_step_launch) at the Qwen3.5 shape
+    of the measurement plan: 16 k heads, 32 v heads, head dims 128, conv kernel
+    4.  Inputs and states resident in HBM; `iters` steps captured in one HIP
+    graph (the states carry from step to step); mean time per step from HIP
+    events around the graph launch.  Bytes: the recurrent state read and
+    written (2 * 32*128*128*4) plus the conv window read and written and the
+    step's vectors."""
+    import ctypes
+    import numpy as np
+    from oi import _native
+    hip = ctypes.CDLL("libamdhip64.so")
+    vp = ctypes.c_void_p
+    L = _native.hip()
+
+    def ok(rc, what):
+        if rc != 0:
+            raise RuntimeError("%s failed (%d)" % (what, rc))
+
+    n_kh, n_vh, hk, hv, kern = 16, 32, 128, 128, 4
+    kd, vd = n_kh * hk, n_vh * hv
+    cd = 2 * kd + vd
+    rng = np.random.default_rng(3)
+    f = np.float32
+    host = {"qkv": rng.standard_normal(cd).astype(f), "z": rng.standard_normal(vd).astype(f),
+            "b": rng.standard_normal(n_vh).astype(f), "a": rng.standard_normal(n_vh).astype(f),
+            "conv_w": (rng.standard_normal(cd * kern) * 0.5).astype(f),
+            "a_decay": (-np.exp(rng.standard_normal(n_vh) * 0.5)).astype(f),
+            "dt_bias": (rng.standard_normal(n_vh) * 0.5).astype(f), "norm_w": np.ones(hv, f),
+            "conv_state": rng.standard_normal(cd * (kern - 1)).astype(f),
+            "rec_state": (rng.standard_normal(n_vh * hk * hv) * 0.1).astype(f),
+            "scratch": np.zeros(cd, f), "out": np.zeros(vd, f)}
+    dev = {}
+    for k, arr in host.items():
+        p = vp()
+        ok(hip.hipMalloc(ctypes.byref(p), ctypes.c_size_t(arr.nbytes)), "hipMalloc")
+        ok(hip.hipMemcpy(p, arr.ctypes.data_as(vp), ctypes.c_size_t(arr.nbytes), 1), "hipMemcpy")
+        dev[k] = p
+    d = _native.DeltaNetDims(n_kh, n_vh, hk, hv, kern, 1e-6)
+    st = vp()
+    ok(hip.hipStreamCreate(ctypes.byref(st)), "hipStreamCreate")
+    order = ("qkv", "z", "b", "a", "conv_w", "a_decay", "dt_bias", "norm_w", "conv_state", "rec_state", "scratch",
+             "out")
+
+    def launch():
+        ok(L.oi_deltanet_step_launch(ctypes.byref(d), *[dev[k] for k in order], st), "oi_deltanet_step_launch")
+
+    launch()
+    ok(hip.hipStreamSynchronize(st), "hipStreamSynchronize")
+    graph, exe = vp(), vp()
+    ok(hip.hipStreamBeginCapture(st, 0), "hipStreamBeginCapture")
+    for _ in range(iters):
+        launch()
+    ok(hip.hipStreamEndCapture(st, ctypes.byref(graph)), "hipStreamEndCapture")
+    ok(hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, ctypes.c_size_t(0)), "hipGraphInstantiate")
+    ok(hip.hipGraphLaunch(exe, st), "hipGraphLaunch")
+    ok(hip.hipStreamSynchronize(st), "hipStreamSynchronize")
+    e0, e1 = vp(), vp()
+    ok(hip.hipEventCreate(ctypes.byref(e0)), "hipEventCreate")
+    ok(hip.hipEventCreate(ctypes.byref(e1)), "hipEventCreate")
+    ok(hip.hipEventRecord(e0, st), "hipEventRecord")
+    ok(hip.hipGraphLaunch(exe, st), "hipGraphLaunch")
+    ok(hip.hipEventRecord(e1, st), "hipEventRecord")
+    ok(hip.hipEventSynchronize(e1), "hipEventSynchronize")
+    ms = ctypes.c_float()
+    ok(hip.hipEventElapsedTime(ctypes.byref(ms), e0, e1), "hipEventElapsedTime")
+    us = ms.value * 1000.0 / iters
+    for h in (e0, e1):
+        hip.hipEventDestroy(h)
+    hip.hipGraphExecDestroy(exe)
+    hip.hipGraphDestroy(graph)
+    hip.hipStreamDestroy(st)
+    for p in dev.values():
+        hip.hipFree(p)
+    byts = 2 * n_vh * hk * hv * 4 + 2 * cd * (kern - 1) * 4 + cd * kern * 4 + (cd + 2 * vd + 2 * n_vh) * 4
+    return {"shape": "n_k_heads 16, n_v_heads 32, head dims 128, conv kernel 4", "avg_us": round(us, 3),
+            "bytes": byts, "GBps": round(byts / us / 1e3, 1), "frac_hbm_peak": round(byts / us / 1e3 / PEAK_HBM_GBPS, 4),
+            "kernels": "dn_conv_kernel + dn_delta_kernel"}
+
+
 def measure_prefill(e, cfg, n, reps=3):
     """Batched prefill of an n-token prompt at position 0 (engine_forward_batch,
     synchronous): host wall clock per call after one warm call (which also
@@ -202,7 +282,7 @@ def main():
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM measurement")
     ap.add_argument("--no-prefill", action="store_true", help="skip the batched prefill measurement")
     ap.add_argument("--prefill-tokens", type=int, default=512)
-    ap.add_argument("--only", choices=["prefill", "gemm"], default=None,
+    ap.add_argument("--only", choices=["prefill", "gemm", "deltanet"], default=None,
                     help="run one secondary measurement alone (for profiling) and print its JSON")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (3 times), to calibrate HBM counters")
@@ -229,6 +309,9 @@ def main():
 
     if args.only == "gemm":
         print(json.dumps({"prefill_gemm": prefill_gemm()}), flush=True)
+        return
+    if args.only == "deltanet":
+        print(json.dumps({"deltanet_step": deltanet_step()}), flush=True)
         return
 
     tmpdir = None
@@ -295,6 +378,9 @@ def main():
                 g["type"], g["rows"], g["cols"], g["avg_us"], g["TFLOPs"]) for g in gemm))
 
         prefill = None if args.no_prefill else measure_prefill(e, cfg, args.prefill_tokens)
+        dn = None if args.no_gemm else deltanet_step()
+        if dn:
+            log("deltanet step: %.2f us, %.0f GB/s" % (dn["avg_us"], dn["GBps"]))
 
         cpu = None
         if not args.no_cpu:
@@ -320,6 +406,7 @@ def main():
             "cpu_baseline": cpu,
             "prefill_gemm": gemm,
             "prefill": prefill,
+            "deltanet_step": dn,
         }
         print(json.dumps(out), flush=True)
         infer.engine_destroy(e)

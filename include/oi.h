@@ -186,6 +186,41 @@ int oi_gemm_launch(const oi_weights *w, const uint16_t *x_dev, int32_t n, float 
 int oi_gemm(int32_t type, const void *host_blocks, int64_t rows, int64_t cols, const uint16_t *x, int32_t n,
             float *c);
 
+/* ------------------------------------------- Qwen3.5 linear-attention step --- */
+
+/* Shape of a gated DeltaNet layer (qwen3_5/model.odin: lin_n_k_heads,
+ * lin_n_v_heads, lin_head_k_dim, lin_head_v_dim, lin_conv_kernel; rms_eps).
+ * conv_dim = 2 * n_k_heads * head_k_dim + n_v_heads * head_v_dim. */
+typedef struct {
+    int32_t n_k_heads, n_v_heads, head_k_dim, head_v_dim, conv_kernel;
+    float eps;
+} oi_deltanet_dims;
+
+/* One token of forward_linear_layer (qwen3_5/forward.odin:172-219) between the
+ * input projections and the output projection: conv1d_step + silu over the
+ * in_qkv projection (ops.odin:97-117), l2norm of q and k per k head with q
+ * scaled by 1/sqrt(head_k_dim), beta = sigmoid(b), decay = exp(ssm_a *
+ * softplus(a + dt_bias)) (ssm_a already -exp(A_log)), the gated delta rule on
+ * each value head's state with k head vh % n_k_heads (ops.odin:120-153), and
+ * the gated RMSNorm rmsnorm(o) * norm_w * silu(z).  Device pointers:
+ * qkv [conv_dim], z [n_v_heads*head_v_dim], b and a [n_v_heads], conv_w
+ * [conv_dim][conv_kernel], a_decay (ssm_a) and dt_bias [n_v_heads], norm_w
+ * [head_v_dim]; conv_state [conv_dim][conv_kernel-1] and rec_state
+ * [n_v_heads][head_k_dim][head_v_dim] are updated in place; scratch holds
+ * conv_dim floats; out [n_v_heads*head_v_dim].  head_k_dim and head_v_dim
+ * must be 128.  Enqueued on `stream`. */
+int oi_deltanet_step_launch(const oi_deltanet_dims *d, const float *qkv, const float *z, const float *b,
+                            const float *a, const float *conv_w, const float *a_decay, const float *dt_bias,
+                            const float *norm_w, float *conv_state, float *rec_state, float *scratch, float *out,
+                            void *stream);
+
+/* Host-memory form over a trajectory of n_tokens steps (synchronous): inputs
+ * qkv [n][conv_dim], z [n][n_v*head_v_dim], b and a [n][n_v_heads]; states in
+ * and out in host memory; out [n][n_v_heads*head_v_dim]. */
+int oi_deltanet_steps(const oi_deltanet_dims *d, int32_t n_tokens, const float *qkv, const float *z, const float *b,
+                      const float *a, const float *conv_w, const float *a_decay, const float *dt_bias,
+                      const float *norm_w, float *conv_state, float *rec_state, float *out);
+
 #ifdef __cplusplus
 }
 #endif

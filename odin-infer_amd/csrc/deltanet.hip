@@ -1,0 +1,160 @@
+// deltanet.hip -- the gated DeltaNet (linear attention) token step of the
+// Qwen3.5 hybrid decoder, between its input projections (in_qkv, in_z, in_b,
+// in_a) and its output projection (reference: qwen3_5/forward.odin:137-225
+// forward_linear_layer; ops.odin:7-37 sigmoid / silu / softplus / l2norm,
+// ops.odin:97-161 conv1d_step and delta_recurrent_step).
+//
+// dn_conv_kernel: depthwise causal conv over the kernel window (current input
+//   last, history oldest first), silu, history slide; one thread per channel.
+// dn_delta_kernel: one workgroup per value head vh (k head vh % n_kh,
+//   forward.odin:193): l2-normalize q and k of the k head (q also scaled by
+//   1/sqrt(head_k_dim)), beta = sigmoid(b), decay = exp(ssm_a * softplus(a +
+//   dt_bias)) (ssm_a already holds -exp(A_log)), then the delta rule on the
+//   head's state S [head_k_dim][head_v_dim] (k outer, v inner):
+//     S *= decay;  delta = (v - S^T k) beta;  S += k delta^T;  o = S^T q
+//   and the gated RMSNorm o = rmsnorm(o) * norm_w * silu(z).
+//   Thread t owns column j = t % head_v_dim over rows rg*R .. rg*R+R-1
+//   (rg = t / head_v_dim), so S is read once and written once per token
+//   (coalesced: consecutive threads, consecutive columns); the two column
+//   sums S^T k and S^T q are reduced over the row groups through LDS.
+// The state is HBM-bound: 4 * head_k_dim * head_v_dim bytes read and written
+// per value head and token.
+
+#include "device_common.h"
+
+namespace oi {
+
+// ops.odin:7-15: the branch keeps exp's argument <= 0
+static __device__ __forceinline__ float sigmoid_ref(float x) {
+#pragma clang fp contract(off)
+    if (x >= 0.0f) {
+        const float z = expf(-x);
+        return 1.0f / (1.0f + z);
+    }
+    const float z = expf(x);
+    return z / (1.0f + z);
+}
+static __device__ __forceinline__ float silu_ref(float x) { return x * sigmoid_ref(x); }
+// ops.odin:21-25 (the logarithm in double precision, as the reference)
+static __device__ __forceinline__ float softplus_ref(float x) {
+    if (x > 20.0f) return x;
+    if (x < -20.0f) return 0.0f;
+    return (float)log((double)(1.0f + expf(x)));
+}
+
+__global__ __launch_bounds__(WG) void dn_conv_kernel(DnArgs a) {
+#pragma clang fp contract(off)
+    const int c = (int)blockIdx.x * WG + threadIdx.x;
+    const int conv_dim = 2 * a.n_kh * a.hk + a.n_vh * a.hv, km1 = a.kernel - 1;
+    if (c >= conv_dim) return;
+    const float *w = a.conv_w + (size_t)c * a.kernel;
+    float *st = a.conv_state + (size_t)c * km1;
+    const float x = a.qkv[c];
+    float acc = w[km1] * x;
+    for (int k = 0; k < km1; k++) acc += w[k] * st[k];
+    a.conv_out[c] = silu_ref(acc);
+    for (int k = 0; k < km1 - 1; k++) st[k] = st[k + 1];
+    if (km1 > 0) st[km1 - 1] = x;
+}
+
+template <int HK, int HV>
+__global__ __launch_bounds__(1024) void dn_delta_kernel(DnArgs a) {
+#pragma clang fp contract(off)
+    constexpr int NT = 1024, RG = NT / HV, R = HK / RG;  // row groups, rows per thread
+    static_assert(HK % RG == 0 && NT % HV == 0, "head shape");
+    __shared__ float qn[HK], kn[HK];
+    __shared__ float part[2][RG][HV];
+    __shared__ float red[NT / WAVE];
+    __shared__ float sc[4];
+    const int vh = blockIdx.x, kh = vh % a.n_kh, t = threadIdx.x;
+    const int lane = t & (WAVE - 1), wave = t / WAVE;
+    const int key_dim = a.n_kh * HK;
+    // l2norm of q and k of the k head (ops.odin:27-37), eps 1e-6 a floor on the norm
+    const float *qr = a.conv_out + kh * HK, *kr = a.conv_out + key_dim + kh * HK;
+    float sq = 0.f, sk = 0.f;
+    if (t < HK) {
+        sq = qr[t] * qr[t];
+        sk = kr[t] * kr[t];
+    }
+    sq = wave_sum(sq);
+    sk = wave_sum(sk);
+    if (lane == 0) red[wave] = sq;
+    __syncthreads();
+    if (t == 0) {
+        float s = 0.f;
+        for (int w = 0; w < (HK + WAVE - 1) / WAVE; w++) s += red[w];
+        sc[0] = s;
+    }
+    __syncthreads();
+    if (lane == 0) red[wave] = sk;
+    __syncthreads();
+    if (t == 0) {
+        float s = 0.f;
+        for (int w = 0; w < (HK + WAVE - 1) / WAVE; w++) s += red[w];
+        sc[1] = s;
+        const float b = a.b[vh];
+        sc[2] = sigmoid_ref(b);
+        sc[3] = expf(a.a_decay[vh] * softplus_ref(a.a[vh] + a.dt_bias[vh]));
+    }
+    __syncthreads();
+    if (t < HK) {
+        const float iq = 1.0f / fmaxf(sqrtf(sc[0]), 1e-6f), ik = 1.0f / fmaxf(sqrtf(sc[1]), 1e-6f);
+        qn[t] = qr[t] * iq * (1.0f / sqrtf((float)HK));
+        kn[t] = kr[t] * ik;
+    }
+    __syncthreads();
+    const float beta = sc[2], decay = sc[3];
+    const int j = t % HV, rg = t / HV, i0 = rg * R;
+    float *S = a.state + (size_t)vh * HK * HV;
+    float s[R];
+    float kv = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        s[r] = S[(size_t)(i0 + r) * HV + j] * decay;
+        kv += s[r] * kn[i0 + r];
+    }
+    part[0][rg][j] = kv;
+    __syncthreads();
+    float kvmem = 0.f;
+#pragma unroll
+    for (int g = 0; g < RG; g++) kvmem += part[0][g][j];
+    const float v = a.conv_out[2 * key_dim + vh * HV + j];
+    const float delta = (v - kvmem) * beta;
+    float o = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        s[r] += kn[i0 + r] * delta;
+        S[(size_t)(i0 + r) * HV + j] = s[r];
+        o += s[r] * qn[i0 + r];
+    }
+    part[1][rg][j] = o;
+    __syncthreads();
+    // gated RMSNorm over the head's outputs (forward.odin:211-218)
+    float oj = 0.f;
+    if (rg == 0) {
+#pragma unroll
+        for (int g = 0; g < RG; g++) oj += part[1][g][j];
+    }
+    float ss = rg == 0 ? oj * oj : 0.f;
+    ss = wave_sum(ss);
+    __syncthreads();
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    if (rg == 0) {
+        float tot = 0.f;
+        for (int w = 0; w < (HV + WAVE - 1) / WAVE; w++) tot += red[w];
+        const float inv = 1.0f / sqrtf(tot / (float)HV + a.eps);
+        const float z = a.z[vh * HV + j];
+        a.out[vh * HV + j] = a.norm_w[j] * (inv * oj) * silu_ref(z);
+    }
+}
+
+hipError_t launch_deltanet(const DnArgs &a, hipStream_t st) {
+    if (a.hk != 128 || a.hv != 128 || a.kernel < 1 || a.n_kh <= 0 || a.n_vh <= 0) return hipErrorInvalidValue;
+    const int conv_dim = 2 * a.n_kh * a.hk + a.n_vh * a.hv;
+    hipLaunchKernelGGL(dn_conv_kernel, dim3((unsigned)((conv_dim + WG - 1) / WG)), dim3(WG), 0, st, a);
+    hipLaunchKernelGGL((dn_delta_kernel<128, 128>), dim3((unsigned)a.n_vh), dim3(1024), 0, st, a);
+    return hipGetLastError();
+}
+
+}  // namespace oi

@@ -1400,3 +1400,87 @@ int64_t oi_engine_debug_buffer(oi_engine *e, int32_t which, void *dst, int64_t b
 }
 
 }  // extern "C"
+
+// ------------------------------------------------- gated DeltaNet step --
+namespace {
+bool dn_dims_ok(const oi_deltanet_dims *d) {
+    return d && d->n_k_heads > 0 && d->n_v_heads > 0 && d->n_v_heads % d->n_k_heads == 0 && d->head_k_dim == 128 &&
+           d->head_v_dim == 128 && d->conv_kernel >= 1 && d->conv_kernel <= 16;
+}
+DnArgs dn_args(const oi_deltanet_dims *d) {
+    DnArgs a{};
+    a.eps = d->eps;
+    a.n_kh = d->n_k_heads;
+    a.n_vh = d->n_v_heads;
+    a.hk = d->head_k_dim;
+    a.hv = d->head_v_dim;
+    a.kernel = d->conv_kernel;
+    return a;
+}
+}  // namespace
+
+int oi_deltanet_step_launch(const oi_deltanet_dims *d, const float *qkv, const float *z, const float *b,
+                            const float *a, const float *conv_w, const float *a_decay, const float *dt_bias,
+                            const float *norm_w, float *conv_state, float *rec_state, float *scratch, float *out,
+                            void *stream) {
+    if (!dn_dims_ok(d)) return fail(OI_E_ARG, "deltanet: head dims must be 128, n_v_heads a multiple of n_k_heads");
+    if (!qkv || !z || !b || !a || !conv_w || !a_decay || !dt_bias || !norm_w || !rec_state || !scratch || !out ||
+        (d->conv_kernel > 1 && !conv_state))
+        return fail(OI_E_ARG, "null argument");
+    DnArgs g = dn_args(d);
+    g.qkv = qkv; g.z = z; g.b = b; g.a = a;
+    g.conv_w = conv_w; g.a_decay = a_decay; g.dt_bias = dt_bias; g.norm_w = norm_w;
+    g.conv_state = conv_state; g.state = rec_state; g.conv_out = scratch; g.out = out;
+    HIP_TRY(launch_deltanet(g, (hipStream_t)stream));
+    return OI_OK;
+}
+
+int oi_deltanet_steps(const oi_deltanet_dims *d, int32_t n_tokens, const float *qkv, const float *z, const float *b,
+                      const float *a, const float *conv_w, const float *a_decay, const float *dt_bias,
+                      const float *norm_w, float *conv_state, float *rec_state, float *out) {
+    if (!dn_dims_ok(d)) return fail(OI_E_ARG, "deltanet: head dims must be 128, n_v_heads a multiple of n_k_heads");
+    if (n_tokens <= 0 || !qkv || !z || !b || !a || !conv_w || !a_decay || !dt_bias || !norm_w || !rec_state || !out ||
+        (d->conv_kernel > 1 && !conv_state))
+        return fail(OI_E_ARG, "bad argument");
+    const size_t kd = (size_t)d->n_k_heads * d->head_k_dim, vd = (size_t)d->n_v_heads * d->head_v_dim;
+    const size_t cd = 2 * kd + vd, nvh = (size_t)d->n_v_heads, km1 = (size_t)d->conv_kernel - 1;
+    const size_t st_n = nvh * d->head_k_dim * d->head_v_dim;
+    // one device block: inputs of all tokens, parameters, states, scratch, outputs
+    const size_t n = (size_t)n_tokens;
+    const size_t floats = n * (cd + vd + 2 * nvh) + cd * d->conv_kernel + 2 * nvh + d->head_v_dim + cd * km1 + st_n +
+                          cd + n * vd;
+    float *dev = nullptr;
+    HIP_TRY(hipMalloc(&dev, floats * 4));
+    float *p = dev;
+    auto put = [&](const float *src, size_t cnt) {
+        float *r = p;
+        p += cnt;
+        return std::make_pair(r, src ? hipMemcpy(r, src, cnt * 4, hipMemcpyHostToDevice) : hipSuccess);
+    };
+    hipError_t r = hipSuccess;
+    float *dq, *dz, *db, *da, *dcw, *dad, *ddt, *dnw, *dcs, *drs, *dsc, *dout;
+    {
+        auto t = put(qkv, n * cd); dq = t.first; r = t.second;
+        if (r == hipSuccess) { t = put(z, n * vd); dz = t.first; r = t.second; }
+        if (r == hipSuccess) { t = put(b, n * nvh); db = t.first; r = t.second; }
+        if (r == hipSuccess) { t = put(a, n * nvh); da = t.first; r = t.second; }
+        if (r == hipSuccess) { t = put(conv_w, cd * d->conv_kernel); dcw = t.first; r = t.second; }
+        if (r == hipSuccess) { t = put(a_decay, nvh); dad = t.first; r = t.second; }
+        if (r == hipSuccess) { t = put(dt_bias, nvh); ddt = t.first; r = t.second; }
+        if (r == hipSuccess) { t = put(norm_w, d->head_v_dim); dnw = t.first; r = t.second; }
+        if (r == hipSuccess) { t = put(km1 ? conv_state : nullptr, cd * km1); dcs = t.first; r = t.second; }
+        if (r == hipSuccess) { t = put(rec_state, st_n); drs = t.first; r = t.second; }
+        if (r == hipSuccess) { dsc = p; p += cd; dout = p; }
+    }
+    int rc = OI_OK;
+    for (size_t i = 0; r == hipSuccess && !rc && i < n; i++)
+        rc = oi_deltanet_step_launch(d, dq + i * cd, dz + i * vd, db + i * nvh, da + i * nvh, dcw, dad, ddt, dnw, dcs,
+                                     drs, dsc, dout + i * vd, nullptr);
+    if (r == hipSuccess && !rc) r = hipMemcpy(out, dout, n * vd * 4, hipMemcpyDeviceToHost);
+    if (r == hipSuccess && !rc && km1) r = hipMemcpy(conv_state, dcs, cd * km1 * 4, hipMemcpyDeviceToHost);
+    if (r == hipSuccess && !rc) r = hipMemcpy(rec_state, drs, st_n * 4, hipMemcpyDeviceToHost);
+    hipFree(dev);
+    if (rc) return rc;
+    if (r != hipSuccess) return fail(OI_E_DEVICE, std::string("deltanet: ") + hipGetErrorString(r));
+    return OI_OK;
+}

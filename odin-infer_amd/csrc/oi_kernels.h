@@ -147,6 +147,23 @@ hipError_t launch_pf_attn(const float *q, const uint16_t *kc, const uint16_t *vc
 hipError_t launch_pf_add(float *x, const float *part, int split, int64_t total, hipStream_t st);
 hipError_t launch_pf_swiglu16(const float *g, int gs, const float *u, int us, int64_t total, uint16_t *out,
                               hipStream_t st);
+// deltanet.hip: the gated DeltaNet token step (between the input and output
+// projections of a Qwen3.5 linear-attention layer)
+struct DnArgs {
+    const float *qkv;              // in_qkv projection [conv_dim], conv_dim = 2 n_kh hk + n_vh hv
+    const float *z, *b, *a;        // in_z [n_vh hv], in_b [n_vh], in_a [n_vh]
+    const float *conv_w;           // [conv_dim][kernel]
+    const float *a_decay, *dt_bias;  // [n_vh] (a_decay = ssm_a = -exp(A_log))
+    const float *norm_w;           // [hv]
+    float eps;
+    float *conv_state;             // [conv_dim][kernel - 1], oldest first
+    float *state;                  // [n_vh][hk][hv]
+    float *conv_out;               // scratch [conv_dim]
+    float *out;                    // [n_vh hv]
+    int32_t n_kh, n_vh, hk, hv, kernel;
+};
+hipError_t launch_deltanet(const DnArgs &a, hipStream_t st);
+
 // kernels.hip: x[t] = dequant(emb[tokens[t]]) for n tokens
 hipError_t launch_embed_rows(const DMat &emb, const int32_t *tokens, int n, float *x, hipStream_t st);
 

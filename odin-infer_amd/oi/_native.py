@@ -18,6 +18,11 @@ class OIError(RuntimeError):
         self.code = code
 
 
+class DeltaNetDims(ctypes.Structure):
+    _fields_ = [("n_k_heads", c_i32), ("n_v_heads", c_i32), ("head_k_dim", c_i32), ("head_v_dim", c_i32),
+                ("conv_kernel", c_i32), ("eps", c_f)]
+
+
 class Opts(ctypes.Structure):
     _fields_ = [("max_ctx", c_i32), ("use_hip", c_i32), ("num_threads", c_i32), ("device", c_i32)]
 
@@ -50,6 +55,8 @@ HIP_SYMBOLS = {
     "oi_gemm_workspace_bytes": (c_i64, [c_vp, c_i32]),
     "oi_gemm_launch": (c_i32, [c_vp, c_vp, c_i32, c_vp, c_vp, c_i64, c_vp]),
     "oi_gemm": (c_i32, [c_i32, c_vp, c_i64, c_i64, c_vp, c_i32, c_vp]),
+    "oi_deltanet_step_launch": (c_i32, [c_vp] * 13 + [c_vp]),
+    "oi_deltanet_steps": (c_i32, [c_vp, c_i32] + [c_vp] * 11),
     # include/oi_debug.h
     "oi_engine_debug_buffer": (c_i64, [c_vp, c_i32, c_vp, c_i64]),
 }

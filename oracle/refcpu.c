@@ -1127,3 +1127,113 @@ EXPORT int ref_gemm_f16(int kind, const uint8_t *w, int64_t m, int64_t k, const 
     free(xd);
     return 0;
 }
+
+/* ---------------------------------------------- Qwen3.5 gated DeltaNet --- */
+
+/* ops.odin:7-15 */
+static float ref_sigmoid(float x) {
+    if (x >= 0.0f) {
+        float z = expf(-x);
+        return 1.0f / (1.0f + z);
+    }
+    float z = expf(x);
+    return z / (1.0f + z);
+}
+static float ref_silu(float x) { return x * ref_sigmoid(x); }
+/* ops.odin:21-25 */
+static float ref_softplus(float x) {
+    if (x > 20.0f) return x;
+    if (x < -20.0f) return 0.0f;
+    return (float)log((double)(1.0f + expf(x)));
+}
+/* ops.odin:27-37: eps is a floor on the norm */
+static void ref_l2norm(float *o, const float *x, int64_t n, float eps) {
+    float ss = 0.0f;
+    for (int64_t i = 0; i < n; i++) ss += x[i] * x[i];
+    float nrm = sqrtf(ss);
+    float inv = 1.0f / (nrm > eps ? nrm : eps);
+    for (int64_t i = 0; i < n; i++) o[i] = x[i] * inv;
+}
+/* ops.odin:97-117 */
+static void ref_conv1d_step(float *out, const float *in, float *state, const float *w, int64_t conv_dim, int kernel) {
+    int km1 = kernel - 1;
+    for (int64_t c = 0; c < conv_dim; c++) {
+        const float *wr = w + c * kernel;
+        float *sb = state + c * km1;
+        float acc = wr[km1] * in[c];
+        for (int k = 0; k < km1; k++) acc += wr[k] * sb[k];
+        out[c] = ref_silu(acc);
+        for (int k = 0; k < km1 - 1; k++) sb[k] = sb[k + 1];
+        if (km1 > 0) sb[km1 - 1] = in[c];
+    }
+}
+/* ops.odin:120-153 */
+EXPORT void ref_delta_step(float *out, float *state, const float *q, const float *k, const float *v, float beta,
+                           float decay, int hk, int hv) {
+    for (int64_t i = 0; i < (int64_t)hk * hv; i++) state[i] *= decay;
+    float *delta = malloc((size_t)hv * sizeof(float));
+    for (int j = 0; j < hv; j++) {
+        float s = 0.0f;
+        for (int i = 0; i < hk; i++) s += state[(int64_t)i * hv + j] * k[i];
+        delta[j] = (v[j] - s) * beta;
+    }
+    for (int i = 0; i < hk; i++) {
+        float ki = k[i];
+        for (int j = 0; j < hv; j++) state[(int64_t)i * hv + j] += ki * delta[j];
+    }
+    for (int j = 0; j < hv; j++) {
+        float s = 0.0f;
+        for (int i = 0; i < hk; i++) s += state[(int64_t)i * hv + j] * q[i];
+        out[j] = s;
+    }
+    free(delta);
+}
+EXPORT void ref_conv1d(float *out, const float *in, float *state, const float *w, int64_t conv_dim, int kernel) {
+    ref_conv1d_step(out, in, state, w, conv_dim, kernel);
+}
+EXPORT void ref_l2norm_into(float *o, const float *x, int64_t n, float eps) { ref_l2norm(o, x, n, eps); }
+
+/* forward_linear_layer (qwen3_5/forward.odin:172-219) from the projections
+ * to the gated RMSNorm, for n_tokens consecutive tokens (states carried). */
+EXPORT int ref_deltanet_steps(int n_kh, int n_vh, int hk, int hv, int kernel, float eps, int n_tokens,
+                              const float *qkv, const float *z, const float *b, const float *a, const float *conv_w,
+                              const float *a_decay, const float *dt_bias, const float *norm_w, float *conv_state,
+                              float *rec_state, float *out) {
+    if (n_kh <= 0 || n_vh <= 0 || hk <= 0 || hv <= 0 || kernel < 1 || n_tokens <= 0) {
+        snprintf(g_err, sizeof g_err, "deltanet: bad dims");
+        return -1;
+    }
+    int64_t key_dim = (int64_t)n_kh * hk, value_dim = (int64_t)n_vh * hv, conv_dim = 2 * key_dim + value_dim;
+    float scale = 1.0f / sqrtf((float)hk);
+    float *co = malloc((size_t)conv_dim * sizeof(float));
+    float *ql = malloc((size_t)key_dim * sizeof(float));
+    float *kl = malloc((size_t)key_dim * sizeof(float));
+    for (int t = 0; t < n_tokens; t++) {
+        const float *in = qkv + (int64_t)t * conv_dim;
+        float *o = out + (int64_t)t * value_dim;
+        ref_conv1d_step(co, in, conv_state, conv_w, conv_dim, kernel);
+        for (int kh = 0; kh < n_kh; kh++) {
+            ref_l2norm(ql + (int64_t)kh * hk, co + (int64_t)kh * hk, hk, 1e-6f);
+            ref_l2norm(kl + (int64_t)kh * hk, co + key_dim + (int64_t)kh * hk, hk, 1e-6f);
+            for (int i = 0; i < hk; i++) ql[(int64_t)kh * hk + i] *= scale;
+        }
+        for (int vh = 0; vh < n_vh; vh++) {
+            int kh = vh % n_kh;
+            float beta = ref_sigmoid(b[(int64_t)t * n_vh + vh]);
+            float g = a_decay[vh] * ref_softplus(a[(int64_t)t * n_vh + vh] + dt_bias[vh]);
+            float decay = expf(g);
+            ref_delta_step(o + (int64_t)vh * hv, rec_state + (int64_t)vh * hk * hv, ql + (int64_t)kh * hk,
+                           kl + (int64_t)kh * hk, co + 2 * key_dim + (int64_t)vh * hv, beta, decay, hk, hv);
+        }
+        for (int vh = 0; vh < n_vh; vh++) {
+            float *oh = o + (int64_t)vh * hv;
+            const float *zh = z + (int64_t)t * value_dim + (int64_t)vh * hv;
+            ref_rmsnorm(oh, oh, norm_w, hv, eps);
+            for (int i = 0; i < hv; i++) oh[i] *= ref_silu(zh[i]);
+        }
+    }
+    free(co);
+    free(ql);
+    free(kl);
+    return 0;
+}

@@ -56,6 +56,10 @@ def lib():
         L.ref_engine_hidden.restype = ctypes.POINTER(c_f)
         L.ref_engine_hidden.argtypes = [c_vp]
         L.ref_gemm_f16.argtypes = [c_int, c_vp, c_i64, c_i64, c_vp, c_i64, c_vp]
+        L.ref_delta_step.argtypes = [c_vp, c_vp, c_vp, c_vp, c_vp, c_f, c_f, c_int, c_int]
+        L.ref_conv1d.argtypes = [c_vp, c_vp, c_vp, c_vp, c_i64, c_int]
+        L.ref_l2norm_into.argtypes = [c_vp, c_vp, c_i64, c_f]
+        L.ref_deltanet_steps.argtypes = [c_int] * 5 + [c_f, c_int] + [c_vp] * 11
         _lib = L
     return _lib
 
@@ -182,3 +186,47 @@ class RefEngine:
             self.close()
         except Exception:
             pass
+
+
+def delta_step(state, q, k, v, beta, decay):
+    """qwen3_5/ops.odin:120-153 on a copy of state [hk][hv]; returns (out, state)."""
+    st = np.ascontiguousarray(state, np.float32).copy()
+    hk, hv = st.shape
+    q, k, v = (np.ascontiguousarray(x, np.float32) for x in (q, k, v))
+    out = np.empty(hv, np.float32)
+    lib().ref_delta_step(_p(out), _p(st), _p(q), _p(k), _p(v), float(beta), float(decay), hk, hv)
+    return out, st
+
+
+def conv1d(x, state, w, kernel):
+    """qwen3_5/ops.odin:97-117; returns (out, new state)."""
+    x = np.ascontiguousarray(x, np.float32)
+    st = np.ascontiguousarray(state, np.float32).copy()
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.empty_like(x)
+    lib().ref_conv1d(_p(out), _p(x), _p(st), _p(w), x.size, kernel)
+    return out, st
+
+
+def l2norm(x, eps=1e-6):
+    x = np.ascontiguousarray(x, np.float32)
+    o = np.empty_like(x)
+    lib().ref_l2norm_into(_p(o), _p(x), x.size, eps)
+    return o
+
+
+def deltanet_steps(n_kh, n_vh, hk, hv, kernel, eps, qkv, z, b, a, conv_w, a_decay, dt_bias, norm_w, conv_state,
+                   rec_state):
+    """forward_linear_layer from the projections to the gated RMSNorm over
+    len(qkv) tokens; returns (out [T, n_vh*hv], conv_state, rec_state)."""
+    f = lambda x: np.ascontiguousarray(x, np.float32)
+    qkv, z, b, a = f(np.atleast_2d(qkv)), f(np.atleast_2d(z)), f(np.atleast_2d(b)), f(np.atleast_2d(a))
+    conv_w, a_decay, dt_bias, norm_w = f(conv_w), f(a_decay), f(dt_bias), f(norm_w)
+    cs, rs = f(conv_state).copy(), f(rec_state).copy()
+    T = qkv.shape[0]
+    out = np.empty((T, n_vh * hv), np.float32)
+    rc = lib().ref_deltanet_steps(n_kh, n_vh, hk, hv, kernel, float(eps), T, _p(qkv), _p(z), _p(b), _p(a),
+                                  _p(conv_w), _p(a_decay), _p(dt_bias), _p(norm_w), _p(cs), _p(rs), _p(out))
+    if rc:
+        raise RuntimeError(lib().ref_last_error().decode())
+    return out, cs, rs

@@ -227,3 +227,47 @@ def forward_f64(W, tokens, f16_kv=True, staged=()):
             x = x + mm("ffn_down", lw, l, gt / (1 + np.exp(-gt)) * up, st)
         outs.append(out_w @ rms(x, W.get("output_norm.weight")))
     return outs
+
+
+def deltanet_f64(n_kh, n_vh, hk, hv, kernel, eps, qkv, z, b, a, conv_w, a_decay, dt_bias, norm_w, conv_state,
+                 rec_state, kv_from_q=False):
+    """Float64 restatement of the gated DeltaNet token step over a trajectory
+    (qwen3_5/forward.odin:172-219 with ops.odin's conv1d_step, l2norm,
+    delta_recurrent_step).  kv_from_q=True reproduces the golden of
+    delta_harness/delta_ref.odin:61, which reads the memory with q instead of
+    k (a known mistake there), for tests that must tell the two apart."""
+    f = lambda x: np.array(x, np.float64)
+    qkv, z, b, a = f(np.atleast_2d(qkv)), f(np.atleast_2d(z)), f(np.atleast_2d(b)), f(np.atleast_2d(a))
+    conv_w, a_decay, dt_bias, norm_w = f(conv_w), f(a_decay), f(dt_bias), f(norm_w)
+    cs, S = f(conv_state).reshape(-1, kernel - 1) if kernel > 1 else None, f(rec_state).reshape(n_vh, hk, hv)
+    kd, vd = n_kh * hk, n_vh * hv
+    cw = conv_w.reshape(-1, kernel)
+    outs = []
+    sig = lambda x: 1.0 / (1.0 + np.exp(-x))
+    for t in range(qkv.shape[0]):
+        x = qkv[t]
+        win = np.concatenate([cs, x[:, None]], axis=1) if kernel > 1 else x[:, None]
+        acc = (cw * win).sum(axis=1)
+        co = acc * sig(acc)
+        if kernel > 1:
+            cs = win[:, 1:]
+        q = co[:kd].reshape(n_kh, hk)
+        k = co[kd:2 * kd].reshape(n_kh, hk)
+        v = co[2 * kd:].reshape(n_vh, hv)
+        q = q / np.maximum(np.linalg.norm(q, axis=1, keepdims=True), 1e-6) / np.sqrt(hk)
+        k = k / np.maximum(np.linalg.norm(k, axis=1, keepdims=True), 1e-6)
+        o = np.empty((n_vh, hv))
+        for vh in range(n_vh):
+            kh = vh % n_kh
+            beta = sig(b[t, vh])
+            sp = a[t, vh] + dt_bias[vh]
+            sp = sp if sp > 20 else (0.0 if sp < -20 else np.log1p(np.exp(sp)))
+            S[vh] *= np.exp(a_decay[vh] * sp)
+            mem = S[vh].T @ (q[kh] if kv_from_q else k[kh])
+            delta = (v[vh] - mem) * beta
+            S[vh] += np.outer(k[kh], delta)
+            o[vh] = S[vh].T @ q[kh]
+        o = o / np.sqrt(np.mean(o * o, axis=1, keepdims=True) + eps) * norm_w
+        zz = z[t].reshape(n_vh, hv)
+        outs.append((o * zz * sig(zz)).reshape(-1))
+    return np.array(outs), (cs.reshape(-1) if kernel > 1 else np.zeros(0)), S.reshape(-1)
