@@ -250,6 +250,94 @@ def deltanet_step(iters=200):
             "kernels": "dn_conv_kernel + dn_delta_kernel"}
 
 
+def _graph_us(hip, st, launch, iters):
+    """Mean device time of `launch` over `iters` launches captured in one HIP
+    graph on stream st (HIP events around a second graph launch)."""
+    import ctypes
+    vp = ctypes.c_void_p
+
+    def ok(rc, what):
+        if rc != 0:
+            raise RuntimeError("%s failed (%d)" % (what, rc))
+
+    launch()
+    ok(hip.hipStreamSynchronize(st), "hipStreamSynchronize")
+    graph, exe = vp(), vp()
+    ok(hip.hipStreamBeginCapture(st, 0), "hipStreamBeginCapture")
+    for _ in range(iters):
+        launch()
+    ok(hip.hipStreamEndCapture(st, ctypes.byref(graph)), "hipStreamEndCapture")
+    ok(hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, ctypes.c_size_t(0)), "hipGraphInstantiate")
+    ok(hip.hipGraphLaunch(exe, st), "hipGraphLaunch")
+    ok(hip.hipStreamSynchronize(st), "hipStreamSynchronize")
+    e0, e1 = vp(), vp()
+    ok(hip.hipEventCreate(ctypes.byref(e0)), "hipEventCreate")
+    ok(hip.hipEventCreate(ctypes.byref(e1)), "hipEventCreate")
+    ok(hip.hipEventRecord(e0, st), "hipEventRecord")
+    ok(hip.hipGraphLaunch(exe, st), "hipGraphLaunch")
+    ok(hip.hipEventRecord(e1, st), "hipEventRecord")
+    ok(hip.hipEventSynchronize(e1), "hipEventSynchronize")
+    ms = ctypes.c_float()
+    ok(hip.hipEventElapsedTime(ctypes.byref(ms), e0, e1), "hipEventElapsedTime")
+    for h in (e0, e1):
+        hip.hipEventDestroy(h)
+    hip.hipGraphExecDestroy(exe)
+    hip.hipGraphDestroy(graph)
+    return ms.value * 1000.0 / iters
+
+
+def qwen35_attn_step(iters=100, seq_len=4096):
+    """Attention of a Qwen3.5 full-attention layer for one token
+    (oi_qwen35_attn_step_launch) at the measurement-plan shape: 16 q heads of
+    256 with gate, 2 kv heads, partial RoPE over 64 dimensions, at the last
+    position of a 4096-token f16 cache.  Bytes: the K and V rows read
+    (2 * 2 * 4096 * 256 * 2) plus q/gate, k, v and the output."""
+    import ctypes
+    import numpy as np
+    from oi import _native
+    hip = ctypes.CDLL("libamdhip64.so")
+    vp = ctypes.c_void_p
+    L = _native.hip()
+
+    def ok(rc, what):
+        if rc != 0:
+            raise RuntimeError("%s failed (%d)" % (what, rc))
+
+    nh, nkv, hd, rd = 16, 2, 256, 64
+    rng = np.random.default_rng(4)
+    f = np.float32
+    d = _native.Qwen35AttnDims(nh, nkv, hd, rd, seq_len, 1e-6)
+    host = {"qproj": rng.standard_normal(nh * 2 * hd).astype(f), "k": rng.standard_normal(nkv * hd).astype(f),
+            "v": rng.standard_normal(nkv * hd).astype(f), "q_norm": np.ones(hd, f), "k_norm": np.ones(hd, f),
+            "inv_freq": (1e7 ** (-(np.arange(rd // 2) / (rd / 2.0)))).astype(f),
+            "kc": rng.standard_normal(nkv * seq_len * hd).astype(np.float16),
+            "vc": rng.standard_normal(nkv * seq_len * hd).astype(np.float16),
+            "ws": np.zeros(L.oi_qwen35_attn_workspace_bytes(ctypes.byref(d)) // 4, f), "out": np.zeros(nh * hd, f)}
+    dev = {}
+    for k, arr in host.items():
+        p = vp()
+        ok(hip.hipMalloc(ctypes.byref(p), ctypes.c_size_t(arr.nbytes)), "hipMalloc")
+        ok(hip.hipMemcpy(p, arr.ctypes.data_as(vp), ctypes.c_size_t(arr.nbytes), 1), "hipMemcpy")
+        dev[k] = p
+    st = vp()
+    ok(hip.hipStreamCreate(ctypes.byref(st)), "hipStreamCreate")
+    order = ("qproj", "k", "v", "q_norm", "k_norm", "inv_freq", "kc", "vc", "ws", "out")
+
+    def launch():
+        ok(L.oi_qwen35_attn_step_launch(ctypes.byref(d), seq_len - 1, *[dev[k] for k in order], st),
+           "oi_qwen35_attn_step_launch")
+
+    us = _graph_us(hip, st, launch, iters)
+    hip.hipStreamDestroy(st)
+    for p in dev.values():
+        hip.hipFree(p)
+    byts = 2 * 2 * nkv * seq_len * hd + 4 * (nh * 2 * hd + 2 * nkv * hd + nh * hd)
+    return {"shape": "16 q heads x 256 (+gate), 2 kv heads, rotary 64, position 4095 of a 4096 f16 cache",
+            "avg_us": round(us, 3), "bytes": byts, "GBps": round(byts / us / 1e3, 1),
+            "frac_hbm_peak": round(byts / us / 1e3 / PEAK_HBM_GBPS, 4),
+            "kernels": "q35_prep_kernel + q35_attn_kernel (2 kv heads x 64 splits) + q35_combine_kernel"}
+
+
 def measure_prefill(e, cfg, n, reps=3):
     """Batched prefill of an n-token prompt at position 0 (engine_forward_batch,
     synchronous): host wall clock per call after one warm call (which also
@@ -282,7 +370,7 @@ def main():
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM measurement")
     ap.add_argument("--no-prefill", action="store_true", help="skip the batched prefill measurement")
     ap.add_argument("--prefill-tokens", type=int, default=512)
-    ap.add_argument("--only", choices=["prefill", "gemm", "deltanet"], default=None,
+    ap.add_argument("--only", choices=["prefill", "gemm", "deltanet", "qwen35_attn"], default=None,
                     help="run one secondary measurement alone (for profiling) and print its JSON")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (3 times), to calibrate HBM counters")
@@ -312,6 +400,9 @@ def main():
         return
     if args.only == "deltanet":
         print(json.dumps({"deltanet_step": deltanet_step()}), flush=True)
+        return
+    if args.only == "qwen35_attn":
+        print(json.dumps({"qwen35_attn_step": qwen35_attn_step()}), flush=True)
         return
 
     tmpdir = None
@@ -379,8 +470,10 @@ def main():
 
         prefill = None if args.no_prefill else measure_prefill(e, cfg, args.prefill_tokens)
         dn = None if args.no_gemm else deltanet_step()
+        q35 = None if args.no_gemm else qwen35_attn_step()
         if dn:
-            log("deltanet step: %.2f us, %.0f GB/s" % (dn["avg_us"], dn["GBps"]))
+            log("deltanet step: %.2f us, %.0f GB/s; qwen3.5 attention step: %.2f us, %.0f GB/s" % (
+                dn["avg_us"], dn["GBps"], q35["avg_us"], q35["GBps"]))
 
         cpu = None
         if not args.no_cpu:
@@ -407,6 +500,7 @@ def main():
             "prefill_gemm": gemm,
             "prefill": prefill,
             "deltanet_step": dn,
+            "qwen35_attn_step": q35,
         }
         print(json.dumps(out), flush=True)
         infer.engine_destroy(e)

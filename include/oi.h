@@ -221,6 +221,39 @@ int oi_deltanet_steps(const oi_deltanet_dims *d, int32_t n_tokens, const float *
                       const float *a, const float *conv_w, const float *a_decay, const float *dt_bias,
                       const float *norm_w, float *conv_state, float *rec_state, float *out);
 
+/* ------------------------------------------ Qwen3.5 full-attention step --- */
+
+/* Shape of a Qwen3.5 full-attention layer (qwen3_5/model.odin: n_heads,
+ * n_kv_heads, head_dim, rotary_dim; seq_len of the cache; rms_eps). */
+typedef struct {
+    int32_t n_heads, n_kv_heads, head_dim, rotary_dim, seq_len;
+    float eps;
+} oi_qwen35_attn_dims;
+
+/* Device scratch bytes that oi_qwen35_attn_step_launch needs. */
+int64_t oi_qwen35_attn_workspace_bytes(const oi_qwen35_attn_dims *d);
+
+/* The attention of forward_full_layer (qwen3_5/forward.odin:69-127) for one
+ * token at `pos`, between the q/k/v projections and wo: per head q = the first
+ * head_dim values of its [q | gate] slice of qproj, RMSNorm with q_norm; k
+ * heads RMSNorm with k_norm; RoPE on the first rotary_dim dimensions only
+ * (pairs i, i + rotary_dim/2; angle pos * inv_freq[i], ops.odin:77-89); k and v
+ * stored as f16 in the cache [n_kv_heads][seq_len][head_dim] at pos; scores
+ * q.k * (1/sqrt(head_dim)) over positions 0..pos, softmax, weighted sum of v;
+ * out = that sum * sigmoid(gate).  head_dim 128 or 256.  Device pointers;
+ * enqueued on `stream`. */
+int oi_qwen35_attn_step_launch(const oi_qwen35_attn_dims *d, int32_t pos, const float *qproj, const float *k,
+                               const float *v, const float *q_norm, const float *k_norm, const float *inv_freq,
+                               uint16_t *k_cache, uint16_t *v_cache, void *workspace, float *out, void *stream);
+
+/* Host-memory form over n_tokens consecutive positions pos0.. (synchronous):
+ * qproj [n][n_heads*2*head_dim], k and v [n][n_kv_heads*head_dim]; the caches
+ * (f16 bits, [n_kv_heads][seq_len][head_dim]) in and out in host memory;
+ * out [n][n_heads*head_dim]. */
+int oi_qwen35_attn_steps(const oi_qwen35_attn_dims *d, int32_t n_tokens, int32_t pos0, const float *qproj,
+                         const float *k, const float *v, const float *q_norm, const float *k_norm,
+                         const float *inv_freq, uint16_t *k_cache, uint16_t *v_cache, float *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1484,3 +1484,85 @@ int oi_deltanet_steps(const oi_deltanet_dims *d, int32_t n_tokens, const float *
     if (r != hipSuccess) return fail(OI_E_DEVICE, std::string("deltanet: ") + hipGetErrorString(r));
     return OI_OK;
 }
+
+// ------------------------------------------------ Qwen3.5 full attention --
+namespace {
+bool q35_dims_ok(const oi_qwen35_attn_dims *d) {
+    return d && d->n_heads > 0 && d->n_kv_heads > 0 && d->n_heads % d->n_kv_heads == 0 &&
+           (d->head_dim == 128 || d->head_dim == 256) && d->rotary_dim >= 0 && d->rotary_dim <= d->head_dim &&
+           d->rotary_dim % 2 == 0 && d->seq_len > 0;
+}
+}  // namespace
+
+int64_t oi_qwen35_attn_workspace_bytes(const oi_qwen35_attn_dims *d) {
+    if (!q35_dims_ok(d)) return 0;
+    return ((int64_t)d->n_heads * d->head_dim + (int64_t)d->n_heads * q35_max_splits(d->seq_len) * (d->head_dim + 2)) *
+           4;
+}
+
+int oi_qwen35_attn_step_launch(const oi_qwen35_attn_dims *d, int32_t pos, const float *qproj, const float *k,
+                               const float *v, const float *q_norm, const float *k_norm, const float *inv_freq,
+                               uint16_t *k_cache, uint16_t *v_cache, void *workspace, float *out, void *stream) {
+    if (!q35_dims_ok(d)) return fail(OI_E_ARG, "qwen35 attention: bad dims");
+    if (pos < 0 || pos >= d->seq_len)
+        return fail(OI_E_RANGE, "qwen35 attention: pos=" + std::to_string(pos) + " out of range (seq_len=" +
+                                    std::to_string(d->seq_len) + ")");
+    if (!qproj || !k || !v || !q_norm || !k_norm || (d->rotary_dim && !inv_freq) || !k_cache || !v_cache ||
+        !workspace || !out)
+        return fail(OI_E_ARG, "null argument");
+    Q35Args a{};
+    a.qproj = qproj; a.k = k; a.v = v; a.q_norm = q_norm; a.k_norm = k_norm; a.inv_freq = inv_freq;
+    a.eps = d->eps; a.rotary_dim = d->rotary_dim; a.pos = pos; a.seq_len = d->seq_len;
+    a.n_heads = d->n_heads; a.n_kv_heads = d->n_kv_heads; a.max_splits = q35_max_splits(d->seq_len);
+    a.kc = k_cache; a.vc = v_cache;
+    a.qbuf = (float *)workspace;
+    a.part = a.qbuf + (size_t)d->n_heads * d->head_dim;
+    a.out = out;
+    HIP_TRY(launch_q35_attn(a, d->head_dim, (hipStream_t)stream));
+    return OI_OK;
+}
+
+int oi_qwen35_attn_steps(const oi_qwen35_attn_dims *d, int32_t n_tokens, int32_t pos0, const float *qproj,
+                         const float *k, const float *v, const float *q_norm, const float *k_norm,
+                         const float *inv_freq, uint16_t *k_cache, uint16_t *v_cache, float *out) {
+    if (!q35_dims_ok(d)) return fail(OI_E_ARG, "qwen35 attention: bad dims");
+    if (n_tokens <= 0 || pos0 < 0 || (int64_t)pos0 + n_tokens > d->seq_len)
+        return fail(OI_E_RANGE, "qwen35 attention: positions out of range");
+    if (!qproj || !k || !v || !q_norm || !k_norm || (d->rotary_dim && !inv_freq) || !k_cache || !v_cache || !out)
+        return fail(OI_E_ARG, "null argument");
+    const size_t n = (size_t)n_tokens, hd = (size_t)d->head_dim, qd = (size_t)d->n_heads * hd,
+                 kvd = (size_t)d->n_kv_heads * hd, cache = kvd * (size_t)d->seq_len;
+    const size_t ws = (size_t)oi_qwen35_attn_workspace_bytes(d);
+    const size_t fl = n * (2 * qd + 2 * kvd) + 2 * hd + (size_t)d->rotary_dim / 2 + n * qd;
+    uint8_t *dev = nullptr;
+    HIP_TRY(hipMalloc((void **)&dev, fl * 4 + 2 * cache * 2 + ws + 256));
+    float *p = (float *)dev;
+    float *dq = p; p += n * 2 * qd;
+    float *dk = p; p += n * kvd;
+    float *dv = p; p += n * kvd;
+    float *dqn = p; p += hd;
+    float *dkn = p; p += hd;
+    float *dif = p; p += d->rotary_dim / 2;
+    float *dout = p; p += n * qd;
+    uint16_t *dkc = (uint16_t *)p, *dvc = dkc + cache;
+    void *dws = (void *)(((uintptr_t)(dvc + cache) + 255) & ~(uintptr_t)255);
+    hipError_t r = hipMemcpy(dq, qproj, n * 2 * qd * 4, hipMemcpyHostToDevice);
+    if (r == hipSuccess) r = hipMemcpy(dk, k, n * kvd * 4, hipMemcpyHostToDevice);
+    if (r == hipSuccess) r = hipMemcpy(dv, v, n * kvd * 4, hipMemcpyHostToDevice);
+    if (r == hipSuccess) r = hipMemcpy(dqn, q_norm, hd * 4, hipMemcpyHostToDevice);
+    if (r == hipSuccess) r = hipMemcpy(dkn, k_norm, hd * 4, hipMemcpyHostToDevice);
+    if (r == hipSuccess && d->rotary_dim) r = hipMemcpy(dif, inv_freq, (size_t)d->rotary_dim / 2 * 4, hipMemcpyHostToDevice);
+    if (r == hipSuccess) r = hipMemcpy(dkc, k_cache, cache * 2, hipMemcpyHostToDevice);
+    if (r == hipSuccess) r = hipMemcpy(dvc, v_cache, cache * 2, hipMemcpyHostToDevice);
+    int rc = OI_OK;
+    for (size_t i = 0; r == hipSuccess && !rc && i < n; i++)
+        rc = oi_qwen35_attn_step_launch(d, pos0 + (int32_t)i, dq + i * 2 * qd, dk + i * kvd, dv + i * kvd, dqn, dkn,
+                                        dif, dkc, dvc, dws, dout + i * qd, nullptr);
+    if (r == hipSuccess && !rc) r = hipMemcpy(out, dout, n * qd * 4, hipMemcpyDeviceToHost);
+    if (r == hipSuccess && !rc) r = hipMemcpy(k_cache, dkc, cache * 2, hipMemcpyDeviceToHost);
+    if (r == hipSuccess && !rc) r = hipMemcpy(v_cache, dvc, cache * 2, hipMemcpyDeviceToHost);
+    hipFree(dev);
+    if (rc) return rc;
+    if (r != hipSuccess) return fail(OI_E_DEVICE, std::string("qwen35 attention: ") + hipGetErrorString(r));
+    return OI_OK;
+}

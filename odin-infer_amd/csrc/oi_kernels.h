@@ -164,6 +164,22 @@ struct DnArgs {
 };
 hipError_t launch_deltanet(const DnArgs &a, hipStream_t st);
 
+// qwen35_attn.hip: attention of a Qwen3.5 full-attention layer for one token
+struct Q35Args {
+    const float *qproj;            // [n_heads][2][head_dim]: q then gate per head
+    const float *k, *v;            // [n_kv_heads * head_dim]
+    const float *q_norm, *k_norm;  // [head_dim]
+    const float *inv_freq;         // [rotary_dim / 2]
+    float eps;
+    int32_t rotary_dim, pos, seq_len, n_heads, n_kv_heads, max_splits;
+    uint16_t *kc, *vc;             // [n_kv_heads][seq_len][head_dim] f16
+    float *qbuf;                   // scratch [n_heads * head_dim]
+    float *part;                   // scratch [n_heads][max_splits][head_dim + 2]
+    float *out;                    // [n_heads * head_dim]
+};
+int q35_max_splits(int seq_len);
+hipError_t launch_q35_attn(const Q35Args &a, int head_dim, hipStream_t st);
+
 // kernels.hip: x[t] = dequant(emb[tokens[t]]) for n tokens
 hipError_t launch_embed_rows(const DMat &emb, const int32_t *tokens, int n, float *x, hipStream_t st);
 

@@ -23,6 +23,11 @@ class DeltaNetDims(ctypes.Structure):
                 ("conv_kernel", c_i32), ("eps", c_f)]
 
 
+class Qwen35AttnDims(ctypes.Structure):
+    _fields_ = [("n_heads", c_i32), ("n_kv_heads", c_i32), ("head_dim", c_i32), ("rotary_dim", c_i32),
+                ("seq_len", c_i32), ("eps", c_f)]
+
+
 class Opts(ctypes.Structure):
     _fields_ = [("max_ctx", c_i32), ("use_hip", c_i32), ("num_threads", c_i32), ("device", c_i32)]
 
@@ -57,6 +62,9 @@ HIP_SYMBOLS = {
     "oi_gemm": (c_i32, [c_i32, c_vp, c_i64, c_i64, c_vp, c_i32, c_vp]),
     "oi_deltanet_step_launch": (c_i32, [c_vp] * 13 + [c_vp]),
     "oi_deltanet_steps": (c_i32, [c_vp, c_i32] + [c_vp] * 11),
+    "oi_qwen35_attn_workspace_bytes": (c_i64, [c_vp]),
+    "oi_qwen35_attn_step_launch": (c_i32, [c_vp, c_i32] + [c_vp] * 11),
+    "oi_qwen35_attn_steps": (c_i32, [c_vp, c_i32, c_i32] + [c_vp] * 9),
     # include/oi_debug.h
     "oi_engine_debug_buffer": (c_i64, [c_vp, c_i32, c_vp, c_i64]),
 }

@@ -1,5 +1,6 @@
 """Qwen3.5 hybrid-decoder pieces on the device: the gated DeltaNet token step
-of a linear-attention layer (qwen3_5/forward.odin:137-225)."""
+of a linear-attention layer (qwen3_5/forward.odin:137-225) and the attention
+of a full-attention layer (forward.odin:46-135)."""
 import ctypes
 
 import numpy as np
@@ -27,3 +28,22 @@ def deltanet_steps(n_k_heads, n_v_heads, head_k_dim, head_v_dim, conv_kernel, ep
     check(_native.hip().oi_deltanet_steps(ctypes.byref(d), T, p(qkv), p(z), p(b), p(a), p(conv_w), p(a_decay),
                                           p(dt_bias), p(norm_w), p(cs), p(rs), p(out)))
     return out, cs, rs
+
+
+def attn_steps(n_heads, n_kv_heads, head_dim, rotary_dim, seq_len, eps, pos0, qproj, k, v, q_norm, k_norm, inv_freq,
+               k_cache16, v_cache16):
+    """Run len(qproj) tokens from pos0 through oi_qwen35_attn_steps.  qproj
+    [T, n_heads*2*head_dim] ([q | gate] per head), k, v [T, n_kv*head_dim];
+    caches uint16 f16 bits [n_kv, seq_len, head_dim].  Returns (out [T,
+    n_heads*head_dim], k_cache16, v_cache16) (copies)."""
+    d = _native.Qwen35AttnDims(n_heads, n_kv_heads, head_dim, rotary_dim, seq_len, eps)
+    qproj, k, v = _f32(np.atleast_2d(qproj)), _f32(np.atleast_2d(k)), _f32(np.atleast_2d(v))
+    q_norm, k_norm, inv_freq = _f32(q_norm), _f32(k_norm), _f32(inv_freq)
+    kc = np.ascontiguousarray(k_cache16, np.uint16).copy()
+    vc = np.ascontiguousarray(v_cache16, np.uint16).copy()
+    T = qproj.shape[0]
+    out = np.empty((T, n_heads * head_dim), np.float32)
+    p = lambda x: x.ctypes.data
+    check(_native.hip().oi_qwen35_attn_steps(ctypes.byref(d), T, int(pos0), p(qproj), p(k), p(v), p(q_norm),
+                                             p(k_norm), p(inv_freq), p(kc), p(vc), p(out)))
+    return out, kc, vc

@@ -1237,3 +1237,76 @@ EXPORT int ref_deltanet_steps(int n_kh, int n_vh, int hk, int hv, int kernel, fl
     free(kl);
     return 0;
 }
+
+/* ---------------------------------------- Qwen3.5 full-attention layer --- */
+
+/* ops.odin:163-168 */
+EXPORT void ref_inv_freq(float theta, int rotary_dim, float *out) {
+    float rd = (float)rotary_dim;
+    for (int i = 0; i < rotary_dim / 2; i++) out[i] = 1.0f / powf(theta, (float)i / (rd / 2.0f));
+}
+/* ops.odin:77-89: pairs (i, i + rotary_dim/2); dimensions past rotary_dim pass */
+EXPORT void ref_mrope(float *v, int pos, const float *inv_freq, int rotary_dim) {
+    int half = rotary_dim / 2;
+    float pf = (float)pos;
+    for (int i = 0; i < half; i++) {
+        float angle = pf * inv_freq[i];
+        float c = cosf(angle), s = sinf(angle);
+        float x = v[i], y = v[i + half];
+        v[i] = x * c - y * s;
+        v[i + half] = x * s + y * c;
+    }
+}
+
+/* The attention of forward_full_layer (qwen3_5/forward.odin:69-127) for
+ * n_tokens tokens at pos0.. over an f16 cache (k/v rounded on store, as the
+ * GPU path keeps them); caches are binary16 bits [n_kv][seq_len][head_dim]. */
+EXPORT int ref_qwen35_attn_steps(int n_heads, int n_kv, int hd, int rotary_dim, int seq_len, float eps, int n_tokens,
+                                 int pos0, const float *qproj, const float *k, const float *v, const float *q_norm,
+                                 const float *k_norm, const float *inv_freq, uint16_t *kc, uint16_t *vc, float *out) {
+    if (n_heads <= 0 || n_kv <= 0 || n_heads % n_kv || hd <= 0 || rotary_dim < 0 || rotary_dim > hd ||
+        n_tokens <= 0 || pos0 < 0 || pos0 + n_tokens > seq_len) {
+        snprintf(g_err, sizeof g_err, "qwen35 attention: bad arguments");
+        return -1;
+    }
+    int kv_mul = n_heads / n_kv;
+    float att_scale = 1.0f / sqrtf((float)hd);
+    float *q = malloc((size_t)n_heads * hd * sizeof(float));
+    float *kk = malloc((size_t)n_kv * hd * sizeof(float));
+    float *att = malloc((size_t)seq_len * sizeof(float));
+    float *row = malloc((size_t)hd * sizeof(float));
+    for (int t = 0; t < n_tokens; t++) {
+        int pos = pos0 + t;
+        const float *qp = qproj + (int64_t)t * n_heads * 2 * hd;
+        for (int h = 0; h < n_heads; h++) ref_rmsnorm(q + (int64_t)h * hd, qp + (int64_t)h * 2 * hd, q_norm, hd, eps);
+        for (int h = 0; h < n_kv; h++)
+            ref_rmsnorm(kk + (int64_t)h * hd, k + ((int64_t)t * n_kv + h) * hd, k_norm, hd, eps);
+        for (int h = 0; h < n_heads; h++) ref_mrope(q + (int64_t)h * hd, pos, inv_freq, rotary_dim);
+        for (int h = 0; h < n_kv; h++) ref_mrope(kk + (int64_t)h * hd, pos, inv_freq, rotary_dim);
+        for (int h = 0; h < n_kv; h++)
+            for (int i = 0; i < hd; i++) {
+                int64_t off = ((int64_t)h * seq_len + pos) * hd + i;
+                kc[off] = ref_f32_to_f16(kk[(int64_t)h * hd + i]);
+                vc[off] = ref_f32_to_f16(v[((int64_t)t * n_kv + h) * hd + i]);
+            }
+        for (int h = 0; h < n_heads; h++) {
+            const float *qh = q + (int64_t)h * hd;
+            int kh = h / kv_mul;
+            for (int tt = 0; tt <= pos; tt++) {
+                for (int i = 0; i < hd; i++) row[i] = ref_f16_to_f32(kc[((int64_t)kh * seq_len + tt) * hd + i]);
+                att[tt] = ref_dot_f32(qh, row, hd) * att_scale;
+            }
+            ref_softmax(att, (int64_t)pos + 1);
+            float *o = out + ((int64_t)t * n_heads + h) * hd;
+            for (int i = 0; i < hd; i++) o[i] = 0.0f;
+            for (int tt = 0; tt <= pos; tt++) {
+                float a = att[tt];
+                for (int i = 0; i < hd; i++) o[i] += a * ref_f16_to_f32(vc[((int64_t)kh * seq_len + tt) * hd + i]);
+            }
+            const float *gate = qp + (int64_t)h * 2 * hd + hd;
+            for (int i = 0; i < hd; i++) o[i] *= ref_sigmoid(gate[i]);
+        }
+    }
+    free(q); free(kk); free(att); free(row);
+    return 0;
+}

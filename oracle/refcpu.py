@@ -60,6 +60,9 @@ def lib():
         L.ref_conv1d.argtypes = [c_vp, c_vp, c_vp, c_vp, c_i64, c_int]
         L.ref_l2norm_into.argtypes = [c_vp, c_vp, c_i64, c_f]
         L.ref_deltanet_steps.argtypes = [c_int] * 5 + [c_f, c_int] + [c_vp] * 11
+        L.ref_inv_freq.argtypes = [c_f, c_int, c_vp]
+        L.ref_mrope.argtypes = [c_vp, c_int, c_vp, c_int]
+        L.ref_qwen35_attn_steps.argtypes = [c_int] * 5 + [c_f, c_int, c_int] + [c_vp] * 9
         _lib = L
     return _lib
 
@@ -230,3 +233,33 @@ def deltanet_steps(n_kh, n_vh, hk, hv, kernel, eps, qkv, z, b, a, conv_w, a_deca
     if rc:
         raise RuntimeError(lib().ref_last_error().decode())
     return out, cs, rs
+
+
+def inv_freq(theta, rotary_dim):
+    out = np.empty(rotary_dim // 2, np.float32)
+    lib().ref_inv_freq(float(theta), rotary_dim, _p(out))
+    return out
+
+
+def mrope(v, pos, inv_f, rotary_dim):
+    v = np.ascontiguousarray(v, np.float32).copy()
+    lib().ref_mrope(_p(v), int(pos), _p(np.ascontiguousarray(inv_f, np.float32)), rotary_dim)
+    return v
+
+
+def qwen35_attn_steps(n_heads, n_kv, hd, rotary_dim, seq_len, eps, pos0, qproj, k, v, q_norm, k_norm, inv_f,
+                      kc16, vc16):
+    """forward_full_layer's attention over len(qproj) tokens from pos0;
+    returns (out [T, n_heads*hd], kc16, vc16)."""
+    f = lambda x: np.ascontiguousarray(x, np.float32)
+    qproj, k, v = f(np.atleast_2d(qproj)), f(np.atleast_2d(k)), f(np.atleast_2d(v))
+    kc = np.ascontiguousarray(kc16, np.uint16).copy()
+    vc = np.ascontiguousarray(vc16, np.uint16).copy()
+    T = qproj.shape[0]
+    out = np.empty((T, n_heads * hd), np.float32)
+    rc = lib().ref_qwen35_attn_steps(n_heads, n_kv, hd, rotary_dim, seq_len, float(eps), T, int(pos0), _p(qproj),
+                                     _p(k), _p(v), _p(f(q_norm)), _p(f(k_norm)), _p(f(inv_f)), _p(kc), _p(vc),
+                                     _p(out))
+    if rc:
+        raise RuntimeError(lib().ref_last_error().decode())
+    return out, kc, vc

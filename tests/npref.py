@@ -271,3 +271,48 @@ def deltanet_f64(n_kh, n_vh, hk, hv, kernel, eps, qkv, z, b, a, conv_w, a_decay,
         zz = z[t].reshape(n_vh, hv)
         outs.append((o * zz * sig(zz)).reshape(-1))
     return np.array(outs), (cs.reshape(-1) if kernel > 1 else np.zeros(0)), S.reshape(-1)
+
+
+def qwen35_attn_f64(n_heads, n_kv, hd, rotary_dim, seq_len, eps, pos0, qproj, k, v, q_norm, k_norm, theta,
+                    kc16, vc16, full_rotary=False, gate=True):
+    """Float64 restatement of forward_full_layer's attention (qwen3_5/
+    forward.odin:69-127) over tokens from pos0 with an f16 cache (k/v rounded
+    on store).  full_rotary / gate=False give the variants a mistake would
+    produce (RoPE over the whole head, no output gate)."""
+    f = lambda x: np.array(x, np.float64)
+    qproj, k, v = f(np.atleast_2d(qproj)), f(np.atleast_2d(k)), f(np.atleast_2d(v))
+    q_norm, k_norm = f(q_norm), f(k_norm)
+    K = np.array(kc16, np.uint16).view(np.float16).astype(np.float64).reshape(n_kv, seq_len, hd)
+    V = np.array(vc16, np.uint16).view(np.float16).astype(np.float64).reshape(n_kv, seq_len, hd)
+    rd = hd if full_rotary else rotary_dim
+    half = rd // 2
+    inv = theta ** (-(np.arange(half) / (rd / 2.0)))
+
+    def rms(x, w):
+        return w * x / np.sqrt(np.mean(x * x) + eps)
+
+    def rope(x, pos):
+        x = x.copy()
+        a, b = x[:half].copy(), x[half:rd].copy()
+        c, s = np.cos(pos * inv), np.sin(pos * inv)
+        x[:half], x[half:rd] = a * c - b * s, a * s + b * c
+        return x
+
+    outs = []
+    for t in range(qproj.shape[0]):
+        pos = pos0 + t
+        qp = qproj[t].reshape(n_heads, 2, hd)
+        q = np.stack([rope(rms(qp[h, 0], q_norm), pos) for h in range(n_heads)])
+        kk = np.stack([rope(rms(k[t].reshape(n_kv, hd)[h], k_norm), pos) for h in range(n_kv)])
+        K[:, pos] = kk.astype(np.float16).astype(np.float64)
+        V[:, pos] = v[t].reshape(n_kv, hd).astype(np.float16).astype(np.float64)
+        o = np.empty((n_heads, hd))
+        for h in range(n_heads):
+            g = h // (n_heads // n_kv)
+            sc = K[g, :pos + 1] @ q[h] / np.sqrt(hd)
+            p = np.exp(sc - sc.max())
+            o[h] = (p / p.sum()) @ V[g, :pos + 1]
+            if gate:
+                o[h] *= 1.0 / (1.0 + np.exp(-qp[h, 1]))
+        outs.append(o.reshape(-1))
+    return np.array(outs)

@@ -38,6 +38,27 @@ def test_library_exports_every_declared_symbol(header, lib):
         assert set(declared("oi.h")) | set(declared("oi_debug.h")) == set(_native.HIP_SYMBOLS)
 
 
+def prototypes(header):
+    """name -> number of parameters of every function declared in header."""
+    text = open(os.path.join(REPO, "include", header)).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(oi_[a-z0-9_]+)\s*\(([^()]*)\)\s*;", text):
+        params = m.group(2).strip()
+        out[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+@pytest.mark.parametrize("header", ["oi.h", "oi_debug.h"])
+def test_binding_arity_matches_header(header):
+    """The ctypes argument lists have as many entries as the C prototypes
+    (a short list silently passes garbage in the missing registers)."""
+    protos = prototypes(header)
+    assert protos
+    for name, n in protos.items():
+        assert len(_native.HIP_SYMBOLS[name][1]) == n, (name, n, len(_native.HIP_SYMBOLS[name][1]))
+
+
 def _load_rc(path, max_ctx=64):
     L = _native.hip()
     o = _native.Opts(max_ctx, 1, 1, 0)
