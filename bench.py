@@ -338,6 +338,57 @@ def qwen35_attn_step(iters=100, seq_len=4096):
             "kernels": "q35_prep_kernel + q35_attn_kernel (2 kv heads x 64 splits) + q35_combine_kernel"}
 
 
+def moe_step(iters=100):
+    """Routed-expert FFN for one token (oi_moe_ffn_launch) at the config-4
+    shape: 128 experts, top 8, dim 2048, expert inner 768, Q4_K experts, F32
+    router; weights resident in HBM, experts chosen on the device.  Bytes: the
+    router and the 8 chosen experts' gate, up and down matrices."""
+    import ctypes
+    import numpy as np
+    from oi import _native, ggml, synth
+    hip = ctypes.CDLL("libamdhip64.so")
+    vp = ctypes.c_void_p
+    L = _native.hip()
+
+    def ok(rc, what):
+        if rc != 0:
+            raise RuntimeError("%s failed (%d)" % (what, rc))
+
+    E, k, dim, inter = 128, 8, 2048, 768
+    rng = np.random.default_rng(8)
+    router = (rng.standard_normal((E, dim)) * 0.1).astype(np.float32)
+    mats = [synth.quantize_rows(12, (rng.standard_normal((E * inter, dim)) * 0.05).astype(np.float32)),
+            synth.quantize_rows(12, (rng.standard_normal((E * inter, dim)) * 0.05).astype(np.float32)),
+            synth.quantize_rows(12, (rng.standard_normal((E * dim, inter)) * 0.05).astype(np.float32))]
+    wr = ggml.DeviceWeights(0, router.view(np.uint8).reshape(-1), E, dim)
+    wg = ggml.DeviceWeights(12, mats[0], E * inter, dim)
+    wu = ggml.DeviceWeights(12, mats[1], E * inter, dim)
+    wd = ggml.DeviceWeights(12, mats[2], E * dim, inter)
+    d = _native.MoeDims(E, k, dim, inter, 1)
+    x, y, ws, st = vp(), vp(), vp(), vp()
+    xh = rng.standard_normal(dim).astype(np.float32)
+    ok(hip.hipMalloc(ctypes.byref(x), ctypes.c_size_t(dim * 4)), "hipMalloc")
+    ok(hip.hipMalloc(ctypes.byref(y), ctypes.c_size_t(dim * 4)), "hipMalloc")
+    ok(hip.hipMalloc(ctypes.byref(ws), ctypes.c_size_t(L.oi_moe_workspace_bytes(ctypes.byref(d)))), "hipMalloc")
+    ok(hip.hipMemcpy(x, xh.ctypes.data_as(vp), ctypes.c_size_t(dim * 4), 1), "hipMemcpy")
+    ok(hip.hipStreamCreate(ctypes.byref(st)), "hipStreamCreate")
+
+    def launch():
+        ok(L.oi_moe_ffn_launch(ctypes.byref(d), wr.h, wg.h, wu.h, wd.h, x, ws, y, st), "oi_moe_ffn_launch")
+
+    us = _graph_us(hip, st, launch, iters)
+    hip.hipStreamDestroy(st)
+    for p in (x, y, ws):
+        hip.hipFree(p)
+    per_expert = (wg.nbytes + wu.nbytes + wd.nbytes) / E
+    byts = wr.nbytes + k * per_expert
+    for w in (wr, wg, wu, wd):
+        w.free()
+    return {"shape": "128 experts, top 8, dim 2048, inter 768, Q4_K experts, F32 router", "avg_us": round(us, 3),
+            "bytes": int(byts), "GBps": round(byts / us / 1e3, 1), "frac_hbm_peak": round(byts / us / 1e3 / PEAK_HBM_GBPS, 4),
+            "kernels": "router GEMV + moe_topk_kernel + moe_gateup_kernel + moe_down_kernel"}
+
+
 def measure_prefill(e, cfg, n, reps=3):
     """Batched prefill of an n-token prompt at position 0 (engine_forward_batch,
     synchronous): host wall clock per call after one warm call (which also
@@ -370,7 +421,7 @@ def main():
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM measurement")
     ap.add_argument("--no-prefill", action="store_true", help="skip the batched prefill measurement")
     ap.add_argument("--prefill-tokens", type=int, default=512)
-    ap.add_argument("--only", choices=["prefill", "gemm", "deltanet", "qwen35_attn"], default=None,
+    ap.add_argument("--only", choices=["prefill", "gemm", "deltanet", "qwen35_attn", "moe"], default=None,
                     help="run one secondary measurement alone (for profiling) and print its JSON")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (3 times), to calibrate HBM counters")
@@ -403,6 +454,9 @@ def main():
         return
     if args.only == "qwen35_attn":
         print(json.dumps({"qwen35_attn_step": qwen35_attn_step()}), flush=True)
+        return
+    if args.only == "moe":
+        print(json.dumps({"moe_step": moe_step()}), flush=True)
         return
 
     tmpdir = None
@@ -471,6 +525,7 @@ def main():
         prefill = None if args.no_prefill else measure_prefill(e, cfg, args.prefill_tokens)
         dn = None if args.no_gemm else deltanet_step()
         q35 = None if args.no_gemm else qwen35_attn_step()
+        moe = None if args.no_gemm else moe_step()
         if dn:
             log("deltanet step: %.2f us, %.0f GB/s; qwen3.5 attention step: %.2f us, %.0f GB/s" % (
                 dn["avg_us"], dn["GBps"], q35["avg_us"], q35["GBps"]))
@@ -501,6 +556,7 @@ def main():
             "prefill": prefill,
             "deltanet_step": dn,
             "qwen35_attn_step": q35,
+            "moe_step": moe,
         }
         print(json.dumps(out), flush=True)
         infer.engine_destroy(e)

@@ -254,6 +254,37 @@ int oi_qwen35_attn_steps(const oi_qwen35_attn_dims *d, int32_t n_tokens, int32_t
                          const float *k, const float *v, const float *q_norm, const float *k_norm,
                          const float *inv_freq, uint16_t *k_cache, uint16_t *v_cache, float *out);
 
+/* --------------------------------------------------- mixture of experts --- */
+
+/* Shape of a routed-expert FFN: n_experts, experts per token, model dim,
+ * expert inner dim, and whether the chosen router probabilities are
+ * renormalized to sum 1. */
+typedef struct {
+    int32_t n_experts, top_k, dim, inter, norm_topk_prob;
+} oi_moe_dims;
+
+/* Device scratch bytes that oi_moe_ffn_launch needs. */
+int64_t oi_moe_workspace_bytes(const oi_moe_dims *d);
+
+/* One token through a routed-expert SwiGLU FFN.  No counterpart in the
+ * reference (its Qwen3.5 MLP is dense, qwen3_5/model.odin:80-82,
+ * forward.odin:227-243); the convention is HF Qwen3-MoE's: logits = router x,
+ * p = softmax over all experts, the top_k largest p (ties to the lower id),
+ * weights p or p / sum (norm_topk_prob), y = sum_k w_k down_e(silu(gate_e x) *
+ * up_e x).  router [n_experts][dim]; gate and up stacked [n_experts*inter][dim];
+ * down stacked [n_experts*dim][inter] (oi_weights of any GEMV type).  The
+ * experts are chosen on the device; only the chosen experts' rows are read.
+ * x_dev, y_dev [dim]; workspace of oi_moe_workspace_bytes.  Enqueued on
+ * `stream`. */
+int oi_moe_ffn_launch(const oi_moe_dims *d, const oi_weights *router, const oi_weights *gate, const oi_weights *up,
+                      const oi_weights *down, const float *x_dev, void *workspace, float *y_dev, void *stream);
+
+/* Host-memory form (synchronous); also returns the chosen ids and weights
+ * (ids_out, w_out: top_k each, may be NULL). */
+int oi_moe_ffn(const oi_moe_dims *d, int32_t router_type, const void *router_blocks, int32_t expert_type,
+               const void *gate_blocks, const void *up_blocks, const void *down_blocks, const float *x, float *y,
+               int32_t *ids_out, float *w_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1566,3 +1566,85 @@ int oi_qwen35_attn_steps(const oi_qwen35_attn_dims *d, int32_t n_tokens, int32_t
     if (r != hipSuccess) return fail(OI_E_DEVICE, std::string("qwen35 attention: ") + hipGetErrorString(r));
     return OI_OK;
 }
+
+// ---------------------------------------------------- mixture of experts --
+namespace {
+bool moe_dims_ok(const oi_moe_dims *d) {
+    return d && d->n_experts > 0 && d->n_experts <= MOE_MAX_EXPERTS && d->top_k >= 1 && d->top_k <= MOE_MAX_K &&
+           d->top_k <= d->n_experts && d->dim > 0 && d->dim % 64 == 0 && d->inter > 0 && d->inter % 64 == 0 &&
+           d->inter <= 64 * MOE_MAX_K * 4 && d->dim <= 15360;
+}
+size_t moe_ws_floats(const oi_moe_dims *d) {
+    return (size_t)d->n_experts + 2 * (size_t)d->top_k + (size_t)d->top_k * d->inter;
+}
+}  // namespace
+
+int64_t oi_moe_workspace_bytes(const oi_moe_dims *d) { return moe_dims_ok(d) ? (int64_t)moe_ws_floats(d) * 4 : 0; }
+
+int oi_moe_ffn_launch(const oi_moe_dims *d, const oi_weights *router, const oi_weights *gate, const oi_weights *up,
+                      const oi_weights *down, const float *x_dev, void *workspace, float *y_dev, void *stream) {
+    if (!moe_dims_ok(d)) return fail(OI_E_ARG, "moe: bad dims (dim and inter multiples of 64, top_k <= 32)");
+    if (!router || !gate || !up || !down || !x_dev || !workspace || !y_dev) return fail(OI_E_ARG, "null argument");
+    const int64_t E = d->n_experts;
+    if (router->m.rows != E || router->m.cols != d->dim || gate->m.rows != E * d->inter || gate->m.cols != d->dim ||
+        up->m.rows != E * d->inter || up->m.cols != d->dim || down->m.rows != E * d->dim || down->m.cols != d->inter ||
+        gate->m.type != up->m.type)
+        return fail(OI_E_ARG, "moe: weight shapes do not match the dims");
+    float *ws = (float *)workspace;
+    MoeArgs a{};
+    a.gate = gate->m; a.up = up->m; a.down = down->m;
+    a.x = x_dev;
+    a.logits = ws;
+    a.ids = (int32_t *)(ws + E);
+    a.w = ws + E + d->top_k;
+    a.h = ws + E + 2 * d->top_k;
+    a.y = y_dev;
+    a.n_experts = d->n_experts; a.top_k = d->top_k; a.dim = d->dim; a.inter = d->inter;
+    a.norm_topk = d->norm_topk_prob;
+    GemvArgs g = gemv_args(GEMV_STORE, d->dim, x_dev, nullptr, 0.f);
+    g.nseg = 1;
+    g.seg[0].m = router->m;
+    g.seg[0].y = ws;
+    if (!plan_gemv(g)) return fail(OI_E_UNSUPPORTED, "moe: router row length not supported");
+    HIP_TRY(launch_moe(a, g, (hipStream_t)stream));
+    return OI_OK;
+}
+
+int oi_moe_ffn(const oi_moe_dims *d, int32_t router_type, const void *router_blocks, int32_t expert_type,
+               const void *gate_blocks, const void *up_blocks, const void *down_blocks, const float *x, float *y,
+               int32_t *ids_out, float *w_out) {
+    if (!moe_dims_ok(d)) return fail(OI_E_ARG, "moe: bad dims (dim and inter multiples of 64, top_k <= 32)");
+    if (!router_blocks || !gate_blocks || !up_blocks || !down_blocks || !x || !y) return fail(OI_E_ARG, "null argument");
+    const int64_t E = d->n_experts;
+    oi_weights *wr = nullptr, *wg = nullptr, *wu = nullptr, *wd = nullptr;
+    int rc = oi_weights_upload(router_type, router_blocks, E, d->dim, &wr);
+    if (!rc) rc = oi_weights_upload(expert_type, gate_blocks, E * d->inter, d->dim, &wg);
+    if (!rc) rc = oi_weights_upload(expert_type, up_blocks, E * d->inter, d->dim, &wu);
+    if (!rc) rc = oi_weights_upload(expert_type, down_blocks, E * d->dim, d->inter, &wd);
+    float *dx = nullptr, *dy = nullptr, *dws = nullptr;
+    hipError_t r = hipSuccess;
+    if (!rc) {
+        r = hipMalloc(&dx, (size_t)d->dim * 4);
+        if (r == hipSuccess) r = hipMalloc(&dy, (size_t)d->dim * 4);
+        if (r == hipSuccess) r = hipMalloc(&dws, moe_ws_floats(d) * 4);
+        if (r == hipSuccess) r = hipMemcpy(dx, x, (size_t)d->dim * 4, hipMemcpyHostToDevice);
+        if (r == hipSuccess) {
+            rc = oi_moe_ffn_launch(d, wr, wg, wu, wd, dx, dws, dy, nullptr);
+            if (!rc) r = hipMemcpy(y, dy, (size_t)d->dim * 4, hipMemcpyDeviceToHost);
+            if (!rc && r == hipSuccess && ids_out)
+                r = hipMemcpy(ids_out, dws + E, (size_t)d->top_k * 4, hipMemcpyDeviceToHost);
+            if (!rc && r == hipSuccess && w_out)
+                r = hipMemcpy(w_out, dws + E + d->top_k, (size_t)d->top_k * 4, hipMemcpyDeviceToHost);
+        }
+    }
+    if (dx) hipFree(dx);
+    if (dy) hipFree(dy);
+    if (dws) hipFree(dws);
+    oi_weights_free(wr);
+    oi_weights_free(wg);
+    oi_weights_free(wu);
+    oi_weights_free(wd);
+    if (rc) return rc;
+    if (r != hipSuccess) return fail(OI_E_DEVICE, std::string("moe: ") + hipGetErrorString(r));
+    return OI_OK;
+}

@@ -422,6 +422,171 @@ hipError_t launch_embed(const DMat &emb, int32_t *state, float *x, int32_t vocab
     return hipGetLastError();
 }
 
+// ------------------------------------------------------------------- MoE --
+// Router top-k and the selected experts' SwiGLU FFN for one token, with the
+// expert ids chosen on the device.  The reference has no MoE code
+// (qwen3_5/model.odin:80-82 and forward.odin:227-243 are dense); the
+// convention is HF Qwen3-MoE's: softmax over all router logits, the top k
+// (ties to the lower id), optionally renormalized to sum 1; expert e:
+// down_e(silu(gate_e x) * up_e x); output sum_k w_k y_k.  Expert matrices are
+// stacked: gate and up [n_experts * inter][dim], down [n_experts * dim][inter].
+
+// rows [r0, r0 + n) of m as a matrix of its own (same planes)
+__device__ __forceinline__ DMat sub_rows(const DMat &m, int r0, int n) {
+    DMat s = m;
+    s.rows = n;
+    const size_t r = (size_t)r0;
+    switch (m.type) {
+    case T_Q4_K: s.q += r * (m.cols >> 6) * 16; s.s += r * (m.cols >> 8) * 16; break;
+    case T_Q6_K: s.q += r * (m.cols >> 6) * 16; s.s += r * (m.cols >> 8) * 16; s.d += r * (m.cols >> 8); break;
+    case T_Q8_0: s.q += r * (m.cols >> 6) * 16; s.d += r * (m.cols >> 5); break;
+    case T_F16: s.q += r * m.cols * 2; break;
+    default: s.q += r * m.cols * 4; break;
+    }
+    return s;
+}
+
+// one wave: softmax of the n router logits (lane l holds logits l, l + 64,
+// ...), k rounds of argmax (first maximum wins), weights p_i or p_i / sum of
+// the chosen p
+__global__ __launch_bounds__(WAVE) void moe_topk_kernel(MoeArgs a) {
+#pragma clang fp contract(off)
+    constexpr int PL = MOE_MAX_EXPERTS / WAVE;
+    const int n = a.n_experts, lane = threadIdx.x;
+    float p[PL];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < PL; i++) {
+        const int e = lane + WAVE * i;
+        p[i] = e < n ? a.logits[e] : -INFINITY;
+        mx = fmaxf(mx, p[i]);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, WAVE));
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < PL; i++) {
+        p[i] = lane + WAVE * i < n ? expf(p[i] - mx) : 0.f;
+        sum += p[i];
+    }
+    sum = wave_sum(sum);
+#pragma unroll
+    for (int i = 0; i < PL; i++) p[i] = lane + WAVE * i < n ? p[i] / sum : -1.f;
+    float chosen = 0.f, wk = 0.f;
+    for (int k = 0; k < a.top_k; k++) {
+        float bv = -1.f;
+        int bi = 0x7FFFFFFF;
+#pragma unroll
+        for (int i = 0; i < PL; i++)
+            if (p[i] >= 0.f && better(p[i], lane + WAVE * i, bv, bi)) {
+                bv = p[i];
+                bi = lane + WAVE * i;
+            }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(bv, off, WAVE);
+            const int oi = __shfl_xor(bi, off, WAVE);
+            if (better(ov, oi, bv, bi)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < PL; i++)
+            if (lane + WAVE * i == bi) p[i] = -1.f;  // taken
+        if (lane == k) wk = bv;
+        chosen += bv;
+        if (lane == 0) a.ids[k] = bi;
+    }
+    if (lane < a.top_k) a.w[lane] = a.norm_topk ? wk / chosen : wk;
+}
+
+// x (n floats) into LDS in the swizzled layout of XView
+__device__ __forceinline__ void moe_stage_x(const float *x, int n, float4 *x4) {
+    for (int c = threadIdx.x; c < n / 4; c += WG) x4[xswz(c)] = ((const float4 *)x)[c];
+}
+
+// h[k][r] = silu(gate_e x)[r] * (up_e x)[r], e = ids[k]; grid (top_k,
+// ceil(inter / 4)), one row per wave: the lanes take the (matrix, unit) pairs
+// of the row's gate and up dot products, so all of the row's loads are in
+// flight at once
+__global__ __launch_bounds__(WG) void moe_gateup_kernel(MoeArgs a) {
+#pragma clang fp contract(off)
+    extern __shared__ float4 smem[];
+    const int k = blockIdx.x, e = a.ids[k], lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    moe_stage_x(a.x, a.dim, smem);
+    __syncthreads();
+    const int r = (int)blockIdx.y * 4 + wave;
+    if (r >= a.inter) return;
+    const XView xv{smem, nullptr};
+    const DMat g = sub_rows(a.gate, e * a.inter, a.inter), u = sub_rows(a.up, e * a.inter, a.inter);
+    const int U = a.dim >> 6;
+    float sg = 0.f, su = 0.f;
+    for (int j = lane; j < 2 * U; j += WAVE) {
+        if (j < U) sg += dot_unit(g, r, j, xv);
+        else su += dot_unit(u, r, j - U, xv);
+    }
+    sg = wave_sum(sg);
+    su = wave_sum(su);
+    if (lane == 0) {
+        const float sig = sg >= 0.f ? 1.0f / (1.0f + expf(-sg)) : expf(sg) / (1.0f + expf(sg));
+        a.h[(size_t)k * a.inter + r] = sg * sig * su;
+    }
+}
+
+// y[r] = sum_k w_k (down_{ids[k]} h_k)[r]; grid ceil(dim / 4), one row per
+// wave, the lanes taking the (expert, unit) pairs so that all of the row's
+// loads are in flight at once; the pair products go through LDS and are
+// summed per expert, then weighted, in expert order
+__global__ __launch_bounds__(WG) void moe_down_kernel(MoeArgs a) {
+    extern __shared__ float4 smem[];
+    __shared__ float part[WG / WAVE][MOE_MAX_K * 4];
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    const int X4 = a.inter / 4;  // float4 slots per expert vector
+    for (int k = 0; k < a.top_k; k++) moe_stage_x(a.h + (size_t)k * a.inter, a.inter, smem + (size_t)k * X4);
+    __syncthreads();
+    const int r = (int)blockIdx.x * 4 + wave;
+    if (r >= a.dim) return;
+    const int U = a.inter >> 6, P = a.top_k * U, NB = (MOE_MAX_K * 4 / U) * U;  // batches end on experts
+    float y = 0.f;
+    for (int p0 = 0; p0 < P; p0 += NB) {
+        const int np = min(P - p0, NB);
+        for (int j = lane; j < np; j += WAVE) {
+            const int pr = p0 + j, k = pr / U, u = pr % U;
+            const DMat d = sub_rows(a.down, a.ids[k] * a.dim, a.dim);
+            part[wave][j] = dot_unit(d, r, u, XView{smem + (size_t)k * X4, nullptr});
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
+        __builtin_amdgcn_wave_barrier();
+        if (lane == 0) {
+            float s = 0.f;
+            for (int j = 0; j < np; j++) {
+                s += part[wave][j];
+                if ((j + 1) % U == 0) {
+                    y += a.w[(p0 + j) / U] * s;
+                    s = 0.f;
+                }
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    if (lane == 0) a.y[r] = y;
+}
+
+hipError_t launch_moe(const MoeArgs &a, const GemvArgs &router, hipStream_t st) {
+    if (a.n_experts > MOE_MAX_EXPERTS || a.top_k > MOE_MAX_K || a.top_k < 1 || a.top_k > a.n_experts ||
+        a.dim % 64 || a.inter % 64 || a.inter > 64 * MOE_MAX_K * 4)
+        return hipErrorInvalidValue;
+    hipError_t r = launch_gemv(router, st);
+    if (r != hipSuccess) return r;
+    hipLaunchKernelGGL(moe_topk_kernel, dim3(1), dim3(WAVE), 0, st, a);
+    hipLaunchKernelGGL(moe_gateup_kernel, dim3((unsigned)a.top_k, (unsigned)((a.inter + 3) / 4)), dim3(WG),
+                       (size_t)a.dim * 4, st, a);
+    hipLaunchKernelGGL(moe_down_kernel, dim3((unsigned)((a.dim + 3) / 4)), dim3(WG),
+                       (size_t)a.top_k * a.inter * 4, st, a);
+    return hipGetLastError();
+}
+
 hipError_t launch_embed_rows(const DMat &emb, const int32_t *tokens, int n, float *x, hipStream_t st) {
     const int units = emb.cols / 64;
     hipLaunchKernelGGL(embed_rows_kernel, dim3((unsigned)((units + WG - 1) / WG), (unsigned)n), dim3(WG), 0, st, emb,

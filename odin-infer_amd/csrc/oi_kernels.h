@@ -180,6 +180,21 @@ struct Q35Args {
 int q35_max_splits(int seq_len);
 hipError_t launch_q35_attn(const Q35Args &a, int head_dim, hipStream_t st);
 
+// kernels.hip: router top-k and selected-expert SwiGLU FFN for one token
+constexpr int MOE_MAX_EXPERTS = 1024, MOE_MAX_K = 32;
+struct MoeArgs {
+    DMat gate, up, down;       // stacked expert matrices
+    const float *x;            // [dim]
+    const float *logits;       // router output [n_experts]
+    int32_t *ids;              // [top_k]
+    float *w;                  // [top_k]
+    float *h;                  // [top_k][inter]
+    float *y;                  // [dim]
+    int32_t n_experts, top_k, dim, inter, norm_topk;
+};
+// router: a planned GEMV writing `logits`
+hipError_t launch_moe(const MoeArgs &a, const GemvArgs &router, hipStream_t st);
+
 // kernels.hip: x[t] = dequant(emb[tokens[t]]) for n tokens
 hipError_t launch_embed_rows(const DMat &emb, const int32_t *tokens, int n, float *x, hipStream_t st);
 

@@ -28,6 +28,10 @@ class Qwen35AttnDims(ctypes.Structure):
                 ("seq_len", c_i32), ("eps", c_f)]
 
 
+class MoeDims(ctypes.Structure):
+    _fields_ = [("n_experts", c_i32), ("top_k", c_i32), ("dim", c_i32), ("inter", c_i32), ("norm_topk_prob", c_i32)]
+
+
 class Opts(ctypes.Structure):
     _fields_ = [("max_ctx", c_i32), ("use_hip", c_i32), ("num_threads", c_i32), ("device", c_i32)]
 
@@ -65,6 +69,9 @@ HIP_SYMBOLS = {
     "oi_qwen35_attn_workspace_bytes": (c_i64, [c_vp]),
     "oi_qwen35_attn_step_launch": (c_i32, [c_vp, c_i32] + [c_vp] * 11),
     "oi_qwen35_attn_steps": (c_i32, [c_vp, c_i32, c_i32] + [c_vp] * 9),
+    "oi_moe_workspace_bytes": (c_i64, [c_vp]),
+    "oi_moe_ffn_launch": (c_i32, [c_vp] * 9),
+    "oi_moe_ffn": (c_i32, [c_vp, c_i32, c_vp, c_i32] + [c_vp] * 7),
     # include/oi_debug.h
     "oi_engine_debug_buffer": (c_i64, [c_vp, c_i32, c_vp, c_i64]),
 }

@@ -1310,3 +1310,59 @@ EXPORT int ref_qwen35_attn_steps(int n_heads, int n_kv, int hd, int rotary_dim, 
     free(q); free(kk); free(att); free(row);
     return 0;
 }
+
+/* ------------------------------------------------- mixture of experts --- */
+
+/* Routed-expert SwiGLU FFN for one token.  The reference has no MoE code; the
+ * convention restated is HF Qwen3-MoE's: logits = router x (rows dequantized,
+ * dot_f32 as matmul_t), p = softmax (ops.odin:51-68 form), the top_k largest
+ * (strict '>' scan: ties to the lower id, as sampler.odin:79-89), weights p or
+ * p / sum, y = sum_k w_k down_e(silu(gate_e x) * up_e x), k in selection order. */
+EXPORT int ref_moe_ffn(int E, int top_k, int dim, int inter, int norm, int rtype, const uint8_t *router, int etype,
+                       const uint8_t *gate, const uint8_t *up, const uint8_t *down, const float *x, float *y,
+                       int *ids, float *wout) {
+    if (E <= 0 || top_k <= 0 || top_k > E || dim <= 0 || inter <= 0) {
+        snprintf(g_err, sizeof g_err, "moe: bad dims");
+        return -1;
+    }
+    int64_t rb = ref_row_byte_size(rtype, dim), gb = ref_row_byte_size(etype, dim), db = ref_row_byte_size(etype, inter);
+    float *p = malloc((size_t)E * sizeof(float)), *row = malloc((size_t)(dim > inter ? dim : inter) * sizeof(float));
+    float *h = malloc((size_t)top_k * inter * sizeof(float)), *w = malloc((size_t)top_k * sizeof(float));
+    for (int e = 0; e < E; e++) {
+        ref_dequant_row(rtype, router + e * rb, dim, row);
+        p[e] = ref_dot_f32(row, x, dim);
+    }
+    ref_softmax(p, E);
+    float sum = 0.0f;
+    for (int k = 0; k < top_k; k++) {
+        int best = -1;
+        for (int e = 0; e < E; e++)
+            if (p[e] >= 0.0f && (best < 0 || p[e] > p[best])) best = e;
+        ids[k] = best;
+        w[k] = p[best];
+        sum += p[best];
+        p[best] = -1.0f;
+    }
+    for (int k = 0; k < top_k; k++) wout[k] = norm ? w[k] / sum : w[k];
+    for (int k = 0; k < top_k; k++) {
+        int64_t e = ids[k];
+        for (int r = 0; r < inter; r++) {
+            ref_dequant_row(etype, gate + (e * inter + r) * gb, dim, row);
+            float g = ref_dot_f32(row, x, dim);
+            ref_dequant_row(etype, up + (e * inter + r) * gb, dim, row);
+            float u = ref_dot_f32(row, x, dim);
+            h[(int64_t)k * inter + r] = ref_silu(g) * u;
+        }
+    }
+    for (int r = 0; r < dim; r++) {
+        float acc = 0.0f;
+        for (int k = 0; k < top_k; k++) {
+            int64_t e = ids[k];
+            ref_dequant_row(etype, down + (e * dim + r) * db, inter, row);
+            acc += wout[k] * ref_dot_f32(row, h + (int64_t)k * inter, inter);
+        }
+        y[r] = acc;
+    }
+    free(p); free(row); free(h); free(w);
+    return 0;
+}

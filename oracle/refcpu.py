@@ -63,6 +63,7 @@ def lib():
         L.ref_inv_freq.argtypes = [c_f, c_int, c_vp]
         L.ref_mrope.argtypes = [c_vp, c_int, c_vp, c_int]
         L.ref_qwen35_attn_steps.argtypes = [c_int] * 5 + [c_f, c_int, c_int] + [c_vp] * 9
+        L.ref_moe_ffn.argtypes = [c_int] * 6 + [c_vp, c_int] + [c_vp] * 7
         _lib = L
     return _lib
 
@@ -263,3 +264,18 @@ def qwen35_attn_steps(n_heads, n_kv, hd, rotary_dim, seq_len, eps, pos0, qproj, 
     if rc:
         raise RuntimeError(lib().ref_last_error().decode())
     return out, kc, vc
+
+
+def moe_ffn(E, top_k, dim, inter, norm, rtype, router, etype, gate, up, down, x):
+    """Routed-expert FFN for one token; returns (y, ids, weights)."""
+    b = lambda a: np.ascontiguousarray(a, np.uint8)
+    router, gate, up, down = b(router), b(gate), b(up), b(down)
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(dim, np.float32)
+    ids = np.empty(top_k, np.int32)
+    w = np.empty(top_k, np.float32)
+    rc = lib().ref_moe_ffn(E, top_k, dim, inter, int(norm), rtype, _p(router), etype, _p(gate), _p(up), _p(down),
+                           _p(x), _p(y), _p(ids), _p(w))
+    if rc:
+        raise RuntimeError(lib().ref_last_error().decode())
+    return y, ids, w
