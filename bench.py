@@ -88,7 +88,7 @@ def cpu_baseline(path, k, v, cfg, gpu_tokens, budget_s):
 PEAK_F16_TFLOPS = 2500.0  # MI355X dense f16 MFMA
 
 
-def prefill_gemm(iters=50):
+def prefill_gemm(iters=50, cpu=True):
     """Batched projection (oi_gemm_launch, the prefill GEMM on the matrix cores)
     at the reference harness's projection shapes with 64 tokens: weights
     resident in HBM, f16 activations, f32 output.  `iters` launches (the K-split
@@ -167,10 +167,26 @@ def prefill_gemm(iters=50):
                     "frac_f16_peak": round(flops / us / 1e6 / PEAK_F16_TFLOPS, 4),
                     "GBps": round(byts / us / 1e3, 1), "frac_hbm_peak": round(byts / us / 1e3 / PEAK_HBM_GBPS, 4)})
         w.free()
+        if cpu:
+            rc = _oracle()
+            rows = 128
+            t0 = time.perf_counter()
+            rc.gemm_f16(raw.reshape(m, -1)[:rows].reshape(-1), kind, rows, k, xh.view(np.uint16))
+            el = (time.perf_counter() - t0) * m / rows
+            out[-1]["cpu_baseline"] = {
+                "value": round(1e6 * el, 1), "unit": "us/projection", "cores": 1, "kind": "port",
+                "sample": "oracle/refcpu.c ref_gemm_f16 (f16-staged operands, float64 sums, as the reference "
+                          "harness's CPU check) on the first %d rows, scaled to %d" % (rows, m)}
     return out
 
 
-def deltanet_step(iters=200):
+def _oracle():
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import refcpu  # the oracle, timed as the CPU baseline
+    return refcpu
+
+
+def deltanet_step(iters=200, cpu=True):
     """Gated DeltaNet token step (oi_deltanet_step_launch) at the Qwen3.5 shape
     of the measurement plan: 16 k heads, 32 v heads, head dims 128, conv kernel
     4.  Inputs and states resident in HBM; `iters` steps captured in one HIP
@@ -245,9 +261,21 @@ def deltanet_step(iters=200):
     for p in dev.values():
         hip.hipFree(p)
     byts = 2 * n_vh * hk * hv * 4 + 2 * cd * (kern - 1) * 4 + cd * kern * 4 + (cd + 2 * vd + 2 * n_vh) * 4
-    return {"shape": "n_k_heads 16, n_v_heads 32, head dims 128, conv kernel 4", "avg_us": round(us, 3),
-            "bytes": byts, "GBps": round(byts / us / 1e3, 1), "frac_hbm_peak": round(byts / us / 1e3 / PEAK_HBM_GBPS, 4),
-            "kernels": "dn_conv_kernel + dn_delta_kernel"}
+    out = {"shape": "n_k_heads 16, n_v_heads 32, head dims 128, conv kernel 4", "avg_us": round(us, 3),
+           "bytes": byts, "GBps": round(byts / us / 1e3, 1), "frac_hbm_peak": round(byts / us / 1e3 / PEAK_HBM_GBPS, 4),
+           "kernels": "dn_conv_kernel + dn_delta_kernel"}
+    if cpu:
+        rc = _oracle()
+        n = 20
+        t0 = time.perf_counter()
+        rc.deltanet_steps(n_kh, n_vh, hk, hv, kern, 1e-6, np.tile(host["qkv"], (n, 1)), np.tile(host["z"], (n, 1)),
+                          np.tile(host["b"], (n, 1)), np.tile(host["a"], (n, 1)), host["conv_w"], host["a_decay"],
+                          host["dt_bias"], host["norm_w"], host["conv_state"], host["rec_state"])
+        el = time.perf_counter() - t0
+        out["cpu_baseline"] = {"value": round(1e6 * el / n, 3), "unit": "us/step", "cores": 1, "kind": "port",
+                               "sample": "%d steps of oracle/refcpu.c ref_deltanet_steps (restated qwen3_5/ops.odin "
+                                         "and forward.odin:172-219), same shape" % n}
+    return out
 
 
 def _graph_us(hip, st, launch, iters):
@@ -286,7 +314,7 @@ def _graph_us(hip, st, launch, iters):
     return ms.value * 1000.0 / iters
 
 
-def qwen35_attn_step(iters=100, seq_len=4096):
+def qwen35_attn_step(iters=100, seq_len=4096, cpu=True):
     """Attention of a Qwen3.5 full-attention layer for one token
     (oi_qwen35_attn_step_launch) at the measurement-plan shape: 16 q heads of
     256 with gate, 2 kv heads, partial RoPE over 64 dimensions, at the last
@@ -332,13 +360,25 @@ def qwen35_attn_step(iters=100, seq_len=4096):
     for p in dev.values():
         hip.hipFree(p)
     byts = 2 * 2 * nkv * seq_len * hd + 4 * (nh * 2 * hd + 2 * nkv * hd + nh * hd)
-    return {"shape": "16 q heads x 256 (+gate), 2 kv heads, rotary 64, position 4095 of a 4096 f16 cache",
-            "avg_us": round(us, 3), "bytes": byts, "GBps": round(byts / us / 1e3, 1),
-            "frac_hbm_peak": round(byts / us / 1e3 / PEAK_HBM_GBPS, 4),
-            "kernels": "q35_prep_kernel + q35_attn_kernel (2 kv heads x 64 splits) + q35_combine_kernel"}
+    out = {"shape": "16 q heads x 256 (+gate), 2 kv heads, rotary 64, position 4095 of a 4096 f16 cache",
+           "avg_us": round(us, 3), "bytes": byts, "GBps": round(byts / us / 1e3, 1),
+           "frac_hbm_peak": round(byts / us / 1e3 / PEAK_HBM_GBPS, 4),
+           "kernels": "q35_prep_kernel + q35_attn_kernel (2 kv heads x 64 splits) + q35_combine_kernel"}
+    if cpu:
+        rc = _oracle()
+        kc16 = host["kc"].view(np.uint16).reshape(nkv, seq_len, hd)
+        vc16 = host["vc"].view(np.uint16).reshape(nkv, seq_len, hd)
+        t0 = time.perf_counter()
+        rc.qwen35_attn_steps(nh, nkv, hd, rd, seq_len, 1e-6, seq_len - 1, host["qproj"], host["k"], host["v"],
+                             host["q_norm"], host["k_norm"], host["inv_freq"], kc16, vc16)
+        el = time.perf_counter() - t0
+        out["cpu_baseline"] = {"value": round(1e6 * el, 1), "unit": "us/step", "cores": 1, "kind": "port",
+                               "sample": "1 step at position 4095 of oracle/refcpu.c ref_qwen35_attn_steps "
+                                         "(restated qwen3_5/forward.odin:69-127), same shape and cache"}
+    return out
 
 
-def moe_step(iters=100):
+def moe_step(iters=100, cpu=True):
     """Routed-expert FFN for one token (oi_moe_ffn_launch) at the config-4
     shape: 128 experts, top 8, dim 2048, expert inner 768, Q4_K experts, F32
     router; weights resident in HBM, experts chosen on the device.  Bytes: the
@@ -384,9 +424,18 @@ def moe_step(iters=100):
     byts = wr.nbytes + k * per_expert
     for w in (wr, wg, wu, wd):
         w.free()
-    return {"shape": "128 experts, top 8, dim 2048, inter 768, Q4_K experts, F32 router", "avg_us": round(us, 3),
-            "bytes": int(byts), "GBps": round(byts / us / 1e3, 1), "frac_hbm_peak": round(byts / us / 1e3 / PEAK_HBM_GBPS, 4),
-            "kernels": "router GEMV + moe_topk_kernel + moe_gateup_kernel + moe_down_kernel"}
+    out = {"shape": "128 experts, top 8, dim 2048, inter 768, Q4_K experts, F32 router", "avg_us": round(us, 3),
+           "bytes": int(byts), "GBps": round(byts / us / 1e3, 1), "frac_hbm_peak": round(byts / us / 1e3 / PEAK_HBM_GBPS, 4),
+           "kernels": "router GEMV + moe_topk_kernel + moe_gateup_kernel + moe_down_kernel"}
+    if cpu:
+        rc = _oracle()
+        t0 = time.perf_counter()
+        rc.moe_ffn(E, k, dim, inter, 1, 0, router.view(np.uint8).reshape(-1), 12, mats[0], mats[1], mats[2], xh)
+        el = time.perf_counter() - t0
+        out["cpu_baseline"] = {"value": round(1e6 * el, 1), "unit": "us/token", "cores": 1, "kind": "port",
+                               "sample": "1 token of oracle/refcpu.c ref_moe_ffn (HF Qwen3-MoE convention restated), "
+                                         "same weights and input"}
+    return out
 
 
 def measure_prefill(e, cfg, n, reps=3):
@@ -518,14 +567,14 @@ def main():
 
         gemm = None
         if not args.no_gemm:
-            gemm = prefill_gemm()
+            gemm = prefill_gemm(cpu=not args.no_cpu)
             log("prefill GEMM: " + ", ".join("%s %dx64x%d %.1f us %.0f TFLOP/s" % (
                 g["type"], g["rows"], g["cols"], g["avg_us"], g["TFLOPs"]) for g in gemm))
 
         prefill = None if args.no_prefill else measure_prefill(e, cfg, args.prefill_tokens)
-        dn = None if args.no_gemm else deltanet_step()
-        q35 = None if args.no_gemm else qwen35_attn_step()
-        moe = None if args.no_gemm else moe_step()
+        dn = None if args.no_gemm else deltanet_step(cpu=not args.no_cpu)
+        q35 = None if args.no_gemm else qwen35_attn_step(cpu=not args.no_cpu)
+        moe = None if args.no_gemm else moe_step(cpu=not args.no_cpu)
         if dn:
             log("deltanet step: %.2f us, %.0f GB/s; qwen3.5 attention step: %.2f us, %.0f GB/s" % (
                 dn["avg_us"], dn["GBps"], q35["avg_us"], q35["GBps"]))
@@ -535,6 +584,12 @@ def main():
             log("CPU baseline (oracle) for up to %.0fs ..." % args.cpu_budget)
             cpu = cpu_baseline(path, k, v, cfg, list(toks), args.cpu_budget)
             log("CPU baseline: %.3f tok/s, greedy ids match: %s" % (cpu["value"], cpu["greedy_ids_match_gpu"]))
+            if prefill:
+                # the reference's CPU engine has no batched path: a prompt is
+                # forward() token by token (qwen3_5/engine.odin:86-91)
+                prefill["cpu_baseline"] = {
+                    "value": round(cpu["value"], 3), "unit": "tok/s", "cores": cpu["cores"], "kind": "port",
+                    "sample": "the decode sample above: the reference's CPU prefill runs forward per token"}
 
         out = {
             "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
