@@ -446,59 +446,55 @@ __device__ __forceinline__ DMat sub_rows(const DMat &m, int r0, int n) {
     return s;
 }
 
-// one wave: softmax of the n router logits (lane l holds logits l, l + 64,
-// ...), k rounds of argmax (first maximum wins), weights p_i or p_i / sum of
-// the chosen p
-__global__ __launch_bounds__(WAVE) void moe_topk_kernel(MoeArgs a) {
+// one workgroup: softmax of the n router logits, then every expert's rank
+// (the number of experts with a larger p, or an equal p and a lower id:
+// the order of k rounds of first-maximum argmax) computed in parallel; the
+// experts of rank < k write their id and weight (p or p / sum of the chosen)
+__global__ __launch_bounds__(WG) void moe_topk_kernel(MoeArgs a) {
 #pragma clang fp contract(off)
-    constexpr int PL = MOE_MAX_EXPERTS / WAVE;
-    const int n = a.n_experts, lane = threadIdx.x;
-    float p[PL];
+    __shared__ float p[MOE_MAX_EXPERTS];
+    __shared__ float red[WG / WAVE];
+    __shared__ float sel[MOE_MAX_K];
+    const int n = a.n_experts, t = threadIdx.x, lane = t & (WAVE - 1), wave = t / WAVE;
     float mx = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < PL; i++) {
-        const int e = lane + WAVE * i;
-        p[i] = e < n ? a.logits[e] : -INFINITY;
-        mx = fmaxf(mx, p[i]);
-    }
+    for (int i = t; i < n; i += WG) mx = fmaxf(mx, a.logits[i]);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, WAVE));
-    float sum = 0.f;
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    float M = red[0];
 #pragma unroll
-    for (int i = 0; i < PL; i++) {
-        p[i] = lane + WAVE * i < n ? expf(p[i] - mx) : 0.f;
-        sum += p[i];
+    for (int w = 1; w < WG / WAVE; w++) M = fmaxf(M, red[w]);
+    __syncthreads();
+    float sum = 0.f;
+    for (int i = t; i < n; i += WG) {
+        const float e = expf(a.logits[i] - M);
+        p[i] = e;
+        sum += e;
     }
     sum = wave_sum(sum);
+    if (lane == 0) red[wave] = sum;
+    __syncthreads();
+    float tot = 0.f;
 #pragma unroll
-    for (int i = 0; i < PL; i++) p[i] = lane + WAVE * i < n ? p[i] / sum : -1.f;
-    float chosen = 0.f, wk = 0.f;
-    for (int k = 0; k < a.top_k; k++) {
-        float bv = -1.f;
-        int bi = 0x7FFFFFFF;
-#pragma unroll
-        for (int i = 0; i < PL; i++)
-            if (p[i] >= 0.f && better(p[i], lane + WAVE * i, bv, bi)) {
-                bv = p[i];
-                bi = lane + WAVE * i;
-            }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            const float ov = __shfl_xor(bv, off, WAVE);
-            const int oi = __shfl_xor(bi, off, WAVE);
-            if (better(ov, oi, bv, bi)) {
-                bv = ov;
-                bi = oi;
-            }
+    for (int w = 0; w < WG / WAVE; w++) tot += red[w];
+    for (int i = t; i < n; i += WG) p[i] = p[i] / tot;
+    __syncthreads();
+    for (int i = t; i < n; i += WG) {
+        const float pi = p[i];
+        int rank = 0;
+        for (int j = 0; j < n; j++) rank += better(p[j], j, pi, i) ? 1 : 0;
+        if (rank < a.top_k) {
+            a.ids[rank] = i;
+            sel[rank] = pi;
         }
-#pragma unroll
-        for (int i = 0; i < PL; i++)
-            if (lane + WAVE * i == bi) p[i] = -1.f;  // taken
-        if (lane == k) wk = bv;
-        chosen += bv;
-        if (lane == 0) a.ids[k] = bi;
     }
-    if (lane < a.top_k) a.w[lane] = a.norm_topk ? wk / chosen : wk;
+    __syncthreads();
+    if (t < a.top_k) {
+        float s = 0.f;
+        for (int k = 0; k < a.top_k; k++) s += sel[k];  // in rank order, as the sequential selection
+        a.w[t] = a.norm_topk ? sel[t] / s : sel[t];
+    }
 }
 
 // x (n floats) into LDS in the swizzled layout of XView
@@ -579,7 +575,7 @@ hipError_t launch_moe(const MoeArgs &a, const GemvArgs &router, hipStream_t st) 
         return hipErrorInvalidValue;
     hipError_t r = launch_gemv(router, st);
     if (r != hipSuccess) return r;
-    hipLaunchKernelGGL(moe_topk_kernel, dim3(1), dim3(WAVE), 0, st, a);
+    hipLaunchKernelGGL(moe_topk_kernel, dim3(1), dim3(WG), 0, st, a);
     hipLaunchKernelGGL(moe_gateup_kernel, dim3((unsigned)a.top_k, (unsigned)((a.inter + 3) / 4)), dim3(WG),
                        (size_t)a.dim * 4, st, a);
     hipLaunchKernelGGL(moe_down_kernel, dim3((unsigned)((a.dim + 3) / 4)), dim3(WG),
