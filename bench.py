@@ -86,16 +86,18 @@ def cpu_baseline(path, k, v, cfg, gpu_tokens, budget_s):
 
 
 PEAK_F16_TFLOPS = 2500.0  # MI355X dense f16 MFMA
+ROTATE_BYTES = 1 << 30  # secondary benches cycle through >= 1 GiB of weights / state
 
 
 def prefill_gemm(iters=50, cpu=True):
     """Batched projection (oi_gemm_launch, the prefill GEMM on the matrix cores)
     at the reference harness's projection shapes with 64 tokens: weights
-    resident in HBM, f16 activations, f32 output.  `iters` launches (the K-split
-    kernel and, when K is split, the reduction of the partial products) are
-    captured in one HIP graph, so that the time is the device's and not the
-    Python launch loop's; mean time per projection from HIP events around the
-    graph launch.  Device buffers, streams, graphs and events come from the HIP
+    resident in HBM (copies totalling >= 1 GiB, cycled, so the Infinity Cache
+    cannot serve repeats), f16 activations, f32 output.  max(iters, copies)
+    launches (the K-split kernel and, when K is split, the reduction of the
+    partial products) are captured in one HIP graph, so that the time is the
+    device's and not the Python launch loop's; mean time per projection from
+    HIP events around the graph launch.  Device buffers, streams, graphs and events come from the HIP
     runtime the library itself is linked against (libamdhip64)."""
     import ctypes
     import numpy as np
@@ -120,7 +122,13 @@ def prefill_gemm(iters=50, cpu=True):
             raw[:, 2:4] = (rng.random(nb) * 0.05).astype(np.float16).view(np.uint8).reshape(nb, 2)
         else:
             raw[:, 208:210] = d
-        w = ggml.DeviceWeights(kind, raw.reshape(-1), m, k)
+        # copies of the weights totalling >= 1 GiB, launch i reads copy i mod
+        # ncopy, so the 256 MB Infinity Cache cannot serve repeats
+        w0 = ggml.DeviceWeights(kind, raw.reshape(-1), m, k)
+        ncopy = max(1, -(-ROTATE_BYTES // w0.nbytes))
+        nlaunch = max(iters, ncopy)
+        ws_list = [w0] + [ggml.DeviceWeights(kind, raw.reshape(-1), m, k) for _ in range(ncopy - 1)]
+        w = w0
         xh = np.ascontiguousarray(rng.uniform(-1, 1, size=(n, k)).astype(np.float16))
         wsb = w.gemm_workspace_bytes(n)
         x, c, ws, st = vp(), vp(), vp(), vp()
@@ -135,8 +143,8 @@ def prefill_gemm(iters=50, cpu=True):
         ok(hip.hipStreamSynchronize(st), "hipStreamSynchronize")
         graph, exe = vp(), vp()
         ok(hip.hipStreamBeginCapture(st, 0), "hipStreamBeginCapture")
-        for _ in range(iters):
-            w.launch_gemm(x.value, n, c.value, ws.value, wsb, st.value)
+        for i in range(nlaunch):
+            ws_list[i % ncopy].launch_gemm(x.value, n, c.value, ws.value, wsb, st.value)
         ok(hip.hipStreamEndCapture(st, ctypes.byref(graph)), "hipStreamEndCapture")
         ok(hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, ctypes.c_size_t(0)), "hipGraphInstantiate")
         ok(hip.hipGraphLaunch(exe, st), "hipGraphLaunch")
@@ -150,7 +158,7 @@ def prefill_gemm(iters=50, cpu=True):
         ok(hip.hipEventSynchronize(e1), "hipEventSynchronize")
         ms = ctypes.c_float()
         ok(hip.hipEventElapsedTime(ctypes.byref(ms), e0, e1), "hipEventElapsedTime")
-        us = ms.value * 1000.0 / iters
+        us = ms.value * 1000.0 / nlaunch
         hip.hipEventDestroy(e0)
         hip.hipEventDestroy(e1)
         hip.hipGraphExecDestroy(exe)
@@ -166,7 +174,9 @@ def prefill_gemm(iters=50, cpu=True):
                     "avg_us": round(us, 3), "TFLOPs": round(flops / us / 1e6, 1),
                     "frac_f16_peak": round(flops / us / 1e6 / PEAK_F16_TFLOPS, 4),
                     "GBps": round(byts / us / 1e3, 1), "frac_hbm_peak": round(byts / us / 1e3 / PEAK_HBM_GBPS, 4)})
-        w.free()
+        for wc in ws_list:
+            wc.free()
+        out[-1]["weight_copies"] = ncopy
         if cpu:
             rc = _oracle()
             rows = 128
@@ -189,9 +199,11 @@ def _oracle():
 def deltanet_step(iters=200, cpu=True):
     """Gated DeltaNet token step (oi_deltanet_step_launch) at the Qwen3.5 shape
     of the measurement plan: 16 k heads, 32 v heads, head dims 128, conv kernel
-    4.  Inputs and states resident in HBM; `iters` steps captured in one HIP
-    graph (the states carry from step to step); mean time per step from HIP
-    events around the graph launch.  Bytes: the recurrent state read and
+    4.  Inputs resident in HBM; the recurrent and conv states cycle through
+    copies totalling >= 1 GiB (as the 36 layers' states do between two visits
+    of one layer), so the Infinity Cache cannot serve them; the steps are
+    captured in one HIP graph; mean time per step from HIP events around the
+    graph launch.  Bytes: the recurrent state read and
     written (2 * 32*128*128*4) plus the conv window read and written and the
     step's vectors."""
     import ctypes
@@ -225,44 +237,39 @@ def deltanet_step(iters=200, cpu=True):
         ok(hip.hipMemcpy(p, arr.ctypes.data_as(vp), ctypes.c_size_t(arr.nbytes), 1), "hipMemcpy")
         dev[k] = p
     d = _native.DeltaNetDims(n_kh, n_vh, hk, hv, kern, 1e-6)
+    # one layer's states per copy, >= 1 GiB cycled (a decode step visits each
+    # layer's state once, with the weights of every layer in between)
+    st_bytes = host["rec_state"].nbytes + host["conv_state"].nbytes
+    ncopy = -(-ROTATE_BYTES // st_bytes)
+    big = {}
+    for k in ("rec_state", "conv_state"):
+        p = vp()
+        nb = host[k].nbytes
+        ok(hip.hipMalloc(ctypes.byref(p), ctypes.c_size_t(nb * ncopy)), "hipMalloc")
+        for c in range(ncopy):
+            ok(hip.hipMemcpy(vp(p.value + c * nb), host[k].ctypes.data_as(vp), ctypes.c_size_t(nb), 1), "hipMemcpy")
+        big[k] = (p, nb)
     st = vp()
     ok(hip.hipStreamCreate(ctypes.byref(st)), "hipStreamCreate")
-    order = ("qkv", "z", "b", "a", "conv_w", "a_decay", "dt_bias", "norm_w", "conv_state", "rec_state", "scratch",
-             "out")
+    order = ("qkv", "z", "b", "a", "conv_w", "a_decay", "dt_bias", "norm_w")
 
-    def launch():
-        ok(L.oi_deltanet_step_launch(ctypes.byref(d), *[dev[k] for k in order], st), "oi_deltanet_step_launch")
+    def launch(i):
+        c = i % ncopy
+        cs = vp(big["conv_state"][0].value + c * big["conv_state"][1])
+        rs = vp(big["rec_state"][0].value + c * big["rec_state"][1])
+        ok(L.oi_deltanet_step_launch(ctypes.byref(d), *[dev[k] for k in order], cs, rs, dev["scratch"], dev["out"],
+                                     st), "oi_deltanet_step_launch")
 
-    launch()
-    ok(hip.hipStreamSynchronize(st), "hipStreamSynchronize")
-    graph, exe = vp(), vp()
-    ok(hip.hipStreamBeginCapture(st, 0), "hipStreamBeginCapture")
-    for _ in range(iters):
-        launch()
-    ok(hip.hipStreamEndCapture(st, ctypes.byref(graph)), "hipStreamEndCapture")
-    ok(hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, ctypes.c_size_t(0)), "hipGraphInstantiate")
-    ok(hip.hipGraphLaunch(exe, st), "hipGraphLaunch")
-    ok(hip.hipStreamSynchronize(st), "hipStreamSynchronize")
-    e0, e1 = vp(), vp()
-    ok(hip.hipEventCreate(ctypes.byref(e0)), "hipEventCreate")
-    ok(hip.hipEventCreate(ctypes.byref(e1)), "hipEventCreate")
-    ok(hip.hipEventRecord(e0, st), "hipEventRecord")
-    ok(hip.hipGraphLaunch(exe, st), "hipGraphLaunch")
-    ok(hip.hipEventRecord(e1, st), "hipEventRecord")
-    ok(hip.hipEventSynchronize(e1), "hipEventSynchronize")
-    ms = ctypes.c_float()
-    ok(hip.hipEventElapsedTime(ctypes.byref(ms), e0, e1), "hipEventElapsedTime")
-    us = ms.value * 1000.0 / iters
-    for h in (e0, e1):
-        hip.hipEventDestroy(h)
-    hip.hipGraphExecDestroy(exe)
-    hip.hipGraphDestroy(graph)
+    iters = max(iters, ncopy)
+    us = _graph_us(hip, st, launch, iters)
     hip.hipStreamDestroy(st)
     for p in dev.values():
         hip.hipFree(p)
+    for p, _ in big.values():
+        hip.hipFree(p)
     byts = 2 * n_vh * hk * hv * 4 + 2 * cd * (kern - 1) * 4 + cd * kern * 4 + (cd + 2 * vd + 2 * n_vh) * 4
     out = {"shape": "n_k_heads 16, n_v_heads 32, head dims 128, conv kernel 4", "avg_us": round(us, 3),
-           "bytes": byts, "GBps": round(byts / us / 1e3, 1), "frac_hbm_peak": round(byts / us / 1e3 / PEAK_HBM_GBPS, 4),
+           "state_copies": ncopy, "bytes": byts, "GBps": round(byts / us / 1e3, 1), "frac_hbm_peak": round(byts / us / 1e3 / PEAK_HBM_GBPS, 4),
            "kernels": "dn_conv_kernel + dn_delta_kernel"}
     if cpu:
         rc = _oracle()
@@ -279,8 +286,9 @@ def deltanet_step(iters=200, cpu=True):
 
 
 def _graph_us(hip, st, launch, iters):
-    """Mean device time of `launch` over `iters` launches captured in one HIP
-    graph on stream st (HIP events around a second graph launch)."""
+    """Mean device time of `launch(i)` over `iters` launches (i = 0..iters-1)
+    captured in one HIP graph on stream st (HIP events around a second graph
+    launch)."""
     import ctypes
     vp = ctypes.c_void_p
 
@@ -288,12 +296,12 @@ def _graph_us(hip, st, launch, iters):
         if rc != 0:
             raise RuntimeError("%s failed (%d)" % (what, rc))
 
-    launch()
+    launch(0)
     ok(hip.hipStreamSynchronize(st), "hipStreamSynchronize")
     graph, exe = vp(), vp()
     ok(hip.hipStreamBeginCapture(st, 0), "hipStreamBeginCapture")
-    for _ in range(iters):
-        launch()
+    for i in range(iters):
+        launch(i)
     ok(hip.hipStreamEndCapture(st, ctypes.byref(graph)), "hipStreamEndCapture")
     ok(hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, ctypes.c_size_t(0)), "hipGraphInstantiate")
     ok(hip.hipGraphLaunch(exe, st), "hipGraphLaunch")
@@ -318,7 +326,8 @@ def qwen35_attn_step(iters=100, seq_len=4096, cpu=True):
     """Attention of a Qwen3.5 full-attention layer for one token
     (oi_qwen35_attn_step_launch) at the measurement-plan shape: 16 q heads of
     256 with gate, 2 kv heads, partial RoPE over 64 dimensions, at the last
-    position of a 4096-token f16 cache.  Bytes: the K and V rows read
+    position of a 4096-token f16 cache; the launches cycle through cache copies
+    totalling >= 1 GiB (one per layer, as a decode step visits them).  Bytes: the K and V rows read
     (2 * 2 * 4096 * 256 * 2) plus q/gate, k, v and the output."""
     import ctypes
     import numpy as np
@@ -347,21 +356,33 @@ def qwen35_attn_step(iters=100, seq_len=4096, cpu=True):
         ok(hip.hipMalloc(ctypes.byref(p), ctypes.c_size_t(arr.nbytes)), "hipMalloc")
         ok(hip.hipMemcpy(p, arr.ctypes.data_as(vp), ctypes.c_size_t(arr.nbytes), 1), "hipMemcpy")
         dev[k] = p
+    # one layer's K and V cache per copy, >= 1 GiB cycled
+    cb = host["kc"].nbytes
+    ncopy = -(-ROTATE_BYTES // (2 * cb))
+    big = vp()
+    ok(hip.hipMalloc(ctypes.byref(big), ctypes.c_size_t(2 * cb * ncopy)), "hipMalloc")
+    for c in range(ncopy):
+        ok(hip.hipMemcpy(vp(big.value + 2 * c * cb), host["kc"].ctypes.data_as(vp), ctypes.c_size_t(cb), 1), "hipMemcpy")
+        ok(hip.hipMemcpy(vp(big.value + (2 * c + 1) * cb), host["vc"].ctypes.data_as(vp), ctypes.c_size_t(cb), 1),
+           "hipMemcpy")
     st = vp()
     ok(hip.hipStreamCreate(ctypes.byref(st)), "hipStreamCreate")
-    order = ("qproj", "k", "v", "q_norm", "k_norm", "inv_freq", "kc", "vc", "ws", "out")
+    order = ("qproj", "k", "v", "q_norm", "k_norm", "inv_freq")
 
-    def launch():
-        ok(L.oi_qwen35_attn_step_launch(ctypes.byref(d), seq_len - 1, *[dev[k] for k in order], st),
-           "oi_qwen35_attn_step_launch")
+    def launch(i):
+        c = i % ncopy
+        kc, vc = vp(big.value + 2 * c * cb), vp(big.value + (2 * c + 1) * cb)
+        ok(L.oi_qwen35_attn_step_launch(ctypes.byref(d), seq_len - 1, *[dev[k] for k in order], kc, vc, dev["ws"],
+                                        dev["out"], st), "oi_qwen35_attn_step_launch")
 
-    us = _graph_us(hip, st, launch, iters)
+    us = _graph_us(hip, st, launch, max(iters, ncopy))
     hip.hipStreamDestroy(st)
     for p in dev.values():
         hip.hipFree(p)
+    hip.hipFree(big)
     byts = 2 * 2 * nkv * seq_len * hd + 4 * (nh * 2 * hd + 2 * nkv * hd + nh * hd)
     out = {"shape": "16 q heads x 256 (+gate), 2 kv heads, rotary 64, position 4095 of a 4096 f16 cache",
-           "avg_us": round(us, 3), "bytes": byts, "GBps": round(byts / us / 1e3, 1),
+           "avg_us": round(us, 3), "cache_copies": ncopy, "bytes": byts, "GBps": round(byts / us / 1e3, 1),
            "frac_hbm_peak": round(byts / us / 1e3 / PEAK_HBM_GBPS, 4),
            "kernels": "q35_prep_kernel + q35_attn_kernel (2 kv heads x 64 splits) + q35_combine_kernel"}
     if cpu:
@@ -381,7 +402,9 @@ def qwen35_attn_step(iters=100, seq_len=4096, cpu=True):
 def moe_step(iters=100, cpu=True):
     """Routed-expert FFN for one token (oi_moe_ffn_launch) at the config-4
     shape: 128 experts, top 8, dim 2048, expert inner 768, Q4_K experts, F32
-    router; weights resident in HBM, experts chosen on the device.  Bytes: the
+    router; weights resident in HBM (whole weight sets cycled, >= 1 GiB, so the
+    Infinity Cache cannot serve the chosen experts again), experts chosen on
+    the device.  Bytes: the
     router and the 8 chosen experts' gate, up and down matrices."""
     import ctypes
     import numpy as np
@@ -400,10 +423,15 @@ def moe_step(iters=100, cpu=True):
     mats = [synth.quantize_rows(12, (rng.standard_normal((E * inter, dim)) * 0.05).astype(np.float32)),
             synth.quantize_rows(12, (rng.standard_normal((E * inter, dim)) * 0.05).astype(np.float32)),
             synth.quantize_rows(12, (rng.standard_normal((E * dim, inter)) * 0.05).astype(np.float32))]
-    wr = ggml.DeviceWeights(0, router.view(np.uint8).reshape(-1), E, dim)
-    wg = ggml.DeviceWeights(12, mats[0], E * inter, dim)
-    wu = ggml.DeviceWeights(12, mats[1], E * inter, dim)
-    wd = ggml.DeviceWeights(12, mats[2], E * dim, inter)
+    # whole weight sets (router + all experts) cycled, >= 1 GiB in total
+    sets = []
+    while True:
+        sets.append((ggml.DeviceWeights(0, router.view(np.uint8).reshape(-1), E, dim),
+                     ggml.DeviceWeights(12, mats[0], E * inter, dim), ggml.DeviceWeights(12, mats[1], E * inter, dim),
+                     ggml.DeviceWeights(12, mats[2], E * dim, inter)))
+        if len(sets) * sum(w.nbytes for w in sets[0]) >= ROTATE_BYTES:
+            break
+    wr, wg, wu, wd = sets[0]
     d = _native.MoeDims(E, k, dim, inter, 1)
     x, y, ws, st = vp(), vp(), vp(), vp()
     xh = rng.standard_normal(dim).astype(np.float32)
@@ -413,18 +441,21 @@ def moe_step(iters=100, cpu=True):
     ok(hip.hipMemcpy(x, xh.ctypes.data_as(vp), ctypes.c_size_t(dim * 4), 1), "hipMemcpy")
     ok(hip.hipStreamCreate(ctypes.byref(st)), "hipStreamCreate")
 
-    def launch():
-        ok(L.oi_moe_ffn_launch(ctypes.byref(d), wr.h, wg.h, wu.h, wd.h, x, ws, y, st), "oi_moe_ffn_launch")
+    def launch(i):
+        r, g, u, dn = sets[i % len(sets)]
+        ok(L.oi_moe_ffn_launch(ctypes.byref(d), r.h, g.h, u.h, dn.h, x, ws, y, st), "oi_moe_ffn_launch")
 
-    us = _graph_us(hip, st, launch, iters)
+    us = _graph_us(hip, st, launch, max(iters, len(sets)))
     hip.hipStreamDestroy(st)
     for p in (x, y, ws):
         hip.hipFree(p)
     per_expert = (wg.nbytes + wu.nbytes + wd.nbytes) / E
     byts = wr.nbytes + k * per_expert
-    for w in (wr, wg, wu, wd):
-        w.free()
+    for ws_ in sets:
+        for w in ws_:
+            w.free()
     out = {"shape": "128 experts, top 8, dim 2048, inter 768, Q4_K experts, F32 router", "avg_us": round(us, 3),
+           "weight_sets": len(sets),
            "bytes": int(byts), "GBps": round(byts / us / 1e3, 1), "frac_hbm_peak": round(byts / us / 1e3 / PEAK_HBM_GBPS, 4),
            "kernels": "router GEMV + moe_topk_kernel + moe_gateup_kernel + moe_down_kernel"}
     if cpu:
