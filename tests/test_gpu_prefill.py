@@ -144,3 +144,23 @@ def test_prefill_errors(make_model):
         assert np.isfinite(infer.engine_forward_batch(e, np.arange(8, dtype=np.int32), 0)).all()
     finally:
         infer.engine_destroy(e)
+
+
+def test_prefill_with_token_kernel_decode(make_model, monkeypatch):
+    """With the persistent token kernel (OI_STREAM=1) the batched prompt, its
+    per-token tail and the decode after it share one KV cache: the greedy ids
+    after a 45-token prompt (40 batched + 5 per token) match the oracle."""
+    monkeypatch.setenv("OI_STREAM", "1")
+    path = make_model("tiny-q4_k")
+    e, r = _engines(path, 256)
+    try:
+        toks = _tokens(21, 45, r.vocab_size)
+        got = infer.engine_forward_batch(e, toks, 0).copy()
+        ref = r.prefill(toks, 0)
+        assert scaled_err(got, ref) <= TOL
+        first = int(np.argmax(got))
+        dev = infer.engine_decode_greedy(e, first, len(toks), 16)
+        assert np.array_equal(dev, _greedy_ref(r, first, len(toks), 16))
+    finally:
+        infer.engine_destroy(e)
+        r.close()
