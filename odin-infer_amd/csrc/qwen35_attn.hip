@@ -7,13 +7,15 @@
 // pos * inv_freq[i] computed in f32), scores are dot * (1/sqrt(head_dim)), and
 // the attention output is multiplied by sigmoid(gate).
 //
-// q35_prep_kernel (grid n_heads + n_kv_heads): RMSNorm + partial RoPE of one
-//   q head (to qbuf) or one k head (to the f16 cache at pos, with v).
-// q35_attn_kernel (grid (n_kv_heads, splits)): positions [s CH, (s+1) CH) of
-//   one kv head for all its query heads, one partial (m, l, o[head_dim]) per
-//   query head and split.
+// q35_attn_kernel (grid (kv head x group of its query heads, splits)):
+//   RMSNorm + partial RoPE of the group's q heads (and, in the split holding
+//   pos, of the new k, stored with v to the f16 cache), then positions
+//   [s CH, (s+1) CH) of the kv head for the group: one partial
+//   (m, l, o[head_dim]) per query head and split.
 // q35_combine_kernel (grid n_heads): merge of the splits, o / l, times
 //   sigmoid(gate).  Kernel boundaries order the cache store and the partials.
+
+#include <type_traits>
 
 #include "device_common.h"
 
@@ -33,123 +35,177 @@ static __device__ __forceinline__ float q35_sigmoid(float x) {
     return z / (1.0f + z);
 }
 
-template <int HD>
-__global__ __launch_bounds__(WG) void q35_prep_kernel(Q35Args a) {
-#pragma clang fp contract(off)
-    __shared__ float red[WG / WAVE];
-    __shared__ float xs[HD];
-    const int hh = blockIdx.x, t = threadIdx.x;
-    const bool isq = hh < a.n_heads;
-    const int h = isq ? hh : hh - a.n_heads;
-    const float *src = isq ? a.qproj + (size_t)h * 2 * HD : a.k + (size_t)h * HD;
-    const float *nw = isq ? a.q_norm : a.k_norm;
-    float ss = 0.f;
-    for (int i = t; i < HD; i += WG) ss += src[i] * src[i];
-    ss = wave_sum(ss);
-    if ((t & (WAVE - 1)) == 0) red[t / WAVE] = ss;
-    __syncthreads();
-    float tot = 0.f;
-#pragma unroll
-    for (int w = 0; w < WG / WAVE; w++) tot += red[w];
-    const float inv = 1.0f / sqrtf(tot / (float)HD + a.eps);
-    for (int i = t; i < HD; i += WG) xs[i] = nw[i] * (inv * src[i]);
-    __syncthreads();
-    const int half = a.rotary_dim / 2;
-    float vout[(HD + WG - 1) / WG];
-#pragma unroll
-    for (int r = 0; r < (HD + WG - 1) / WG; r++) {
-        const int i = t + WG * r;
-        if (i >= HD) continue;
-        float v = xs[i];
-        if (i < a.rotary_dim) {  // ops.odin:77-89
-            const int p = i < half ? i : i - half;
-            const float ang = (float)a.pos * a.inv_freq[p];
-            const float c = cosf(ang), s = sinf(ang);
-            v = i < half ? xs[i] * c - xs[i + half] * s : xs[i - half] * s + xs[i] * c;
-        }
-        vout[r] = v;
-    }
-#pragma unroll
-    for (int r = 0; r < (HD + WG - 1) / WG; r++) {
-        const int i = t + WG * r;
-        if (i >= HD) continue;
-        if (isq) a.qbuf[(size_t)h * HD + i] = vout[r];
-        else {
-            const size_t off = ((size_t)h * a.seq_len + a.pos) * HD + i;
-            a.kc[off] = f2h(vout[r]);
-            a.vc[off] = f2h(a.v[(size_t)h * HD + i]);
-        }
-    }
-}
-
-// One workgroup per (kv head, split of Q35_CH positions): the split's K and V
-// rows are staged in LDS once and serve all G = n_heads / n_kv_heads query
-// heads of the group (the cache is read once per token, not G times).  Wave w
-// takes query heads w, w + 4, ...; lane = position for the scores, then
-// o[d] += p_j v_j[d] with lane l holding dimensions DPL l .. DPL l + DPL-1.
-template <int HD>
+// One workgroup per (kv head, group of GW (4, 2 or 1) of its query heads, split of
+// Q35_CH positions).  The split's K (rows padded against bank conflicts) and
+// V rows and the group's rotated q are staged in LDS; then
+//   scores: lane = position, wave = quarter of the dimensions, each K value
+//           read once for all the group's heads, partial sums through LDS;
+//   softmax of the split, one wave per head;
+//   o = sum_t p_t v_t: lane holds DPL dimensions, wave takes positions
+//           w, w + 4, ..., each V value read once for all heads;
+// and one partial (m, l, o[head_dim]) per query head and split.
+template <int HD, int GW>
 __global__ __launch_bounds__(WG) void q35_attn_kernel(Q35Args a) {
-    constexpr int DPL = HD / WAVE, NW = WG / WAVE, KP = HD + 8;  // K rows padded against bank conflicts
-    __shared__ __attribute__((aligned(16))) uint16_t ks[Q35_CH * KP];
+    constexpr int NW = WG / WAVE, DPW = HD / NW, DPL = HD / WAVE, KP = HD + 8;
+    __shared__ __attribute__((aligned(16))) uint16_t ks[Q35_CH * KP];  // later: o partials [NW][GW][HD] f32
     __shared__ __attribute__((aligned(16))) uint16_t vs[Q35_CH * HD];
-    __shared__ float qs[Q35_GMAX][HD];
-    const int kvh = blockIdx.x, sp = blockIdx.y, G = a.n_heads / a.n_kv_heads;
-    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
-    const int L = a.pos + 1, t0 = sp * Q35_CH, n = min(Q35_CH, L - t0);
+    __shared__ __attribute__((aligned(16))) float qs[GW][HD];
+    __shared__ float sp[NW][GW][Q35_CH];
+    __shared__ float mx[GW], sm[GW];
+    static_assert(NW * GW * HD * 4 <= Q35_CH * KP * 2, "o partials fit in the K tile");
+    const int G = a.n_heads / a.n_kv_heads, ngrp = G / GW;
+    const int kvh = blockIdx.x / ngrp, h0 = kvh * G + (blockIdx.x % ngrp) * GW, sp_i = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid / WAVE;
+    const int L = a.pos + 1, t0 = sp_i * Q35_CH, n = min(Q35_CH, L - t0);
     const uint16_t *kc = a.kc + (size_t)kvh * a.seq_len * HD, *vc = a.vc + (size_t)kvh * a.seq_len * HD;
-    for (int i = threadIdx.x; i < Q35_CH * HD / 8; i += WG) {
-        const int r = i / (HD / 8), c = i % (HD / 8), row = t0 + min(r, n - 1);
-        *(u32x4 *)(ks + r * KP + 8 * c) = *(const u32x4 *)(kc + (size_t)row * HD + 8 * c);
-        *(u32x4 *)(vs + r * HD + 8 * c) = *(const u32x4 *)(vc + (size_t)row * HD + 8 * c);
+    // every tile load is issued before the first LDS store, so the loads
+    // stream instead of waiting one by one
+    constexpr int NLD = Q35_CH * HD / 8 / WG;
+    u32x4 kr[NLD], vr[NLD];
+#pragma unroll
+    for (int j = 0; j < NLD; j++) {
+        const int i = tid + j * WG, r = i / (HD / 8), c = i % (HD / 8), row = t0 + min(r, n - 1);
+        kr[j] = ldg_nt((const u32x4 *)(kc + (size_t)row * HD + 8 * c));
+        vr[j] = ldg_nt((const u32x4 *)(vc + (size_t)row * HD + 8 * c));
     }
-    for (int i = threadIdx.x; i < G * HD; i += WG) qs[i / HD][i % HD] = a.qbuf[(size_t)kvh * G * HD + i];
+    // this workgroup's q heads, and in the split that holds pos the new k and
+    // v: RMSNorm (ops.odin rmsnorm) and partial RoPE (ops.odin:77-89); the
+    // new k / v go to the cache and to the LDS tile row pos - t0
+    const bool has_pos = a.pos < t0 + Q35_CH;
+    for (int i = tid; i < GW * HD; i += WG) qs[i / HD][i % HD] = a.qproj[(size_t)(h0 + i / HD) * 2 * HD + i % HD];
+    __shared__ float kn[HD], vn[HD];
+    if (has_pos)
+        for (int i = tid; i < HD; i += WG) {
+            kn[i] = a.k[(size_t)kvh * HD + i];
+            vn[i] = a.v[(size_t)kvh * HD + i];
+        }
+#pragma unroll
+    for (int j = 0; j < NLD; j++) {
+        const int i = tid + j * WG, r = i / (HD / 8), c = i % (HD / 8);
+        *(u32x4 *)(ks + r * KP + 8 * c) = kr[j];
+        *(u32x4 *)(vs + r * HD + 8 * c) = vr[j];
+    }
+    __syncthreads();
+    for (int g = wave; g < GW + (has_pos ? 1 : 0); g += NW) {
+#pragma clang fp contract(off)
+        float *x = g < GW ? qs[g] : kn;
+        const float *w = g < GW ? a.q_norm : a.k_norm;
+        float ss = 0.f;
+        for (int i = lane; i < HD; i += WAVE) ss += x[i] * x[i];
+        ss = wave_sum(ss);
+        const float inv = 1.0f / sqrtf(ss / (float)HD + a.eps);
+        float xv[DPL];
+#pragma unroll
+        for (int e = 0; e < DPL; e++) xv[e] = w[lane + WAVE * e] * (inv * x[lane + WAVE * e]);
+#pragma unroll
+        for (int e = 0; e < DPL; e++) x[lane + WAVE * e] = xv[e];
+        const int half = a.rotary_dim / 2;
+        float yv[DPL];
+#pragma unroll
+        for (int e = 0; e < DPL; e++) {
+            const int i = lane + WAVE * e;
+            float v = xv[e];
+            if (i < a.rotary_dim) {
+                const int pr = i < half ? i : i - half;
+                const float ang = (float)a.pos * a.inv_freq[pr];
+                const float c = cosf(ang), sn = sinf(ang);
+                v = i < half ? x[i] * c - x[i + half] * sn : x[i - half] * sn + x[i] * c;
+            }
+            yv[e] = v;
+        }
+#pragma unroll
+        for (int e = 0; e < DPL; e++) x[lane + WAVE * e] = yv[e];
+    }
+    __syncthreads();
+    if (has_pos) {
+        const int tl = a.pos - t0;
+        for (int i = tid; i < HD; i += WG) {
+            const uint16_t kb = f2h(kn[i]), vb = f2h(vn[i]);
+            ks[tl * KP + i] = kb;
+            vs[tl * HD + i] = vb;
+            if (blockIdx.x % ngrp == 0) {
+                a.kc[((size_t)kvh * a.seq_len + a.pos) * HD + i] = kb;
+                a.vc[((size_t)kvh * a.seq_len + a.pos) * HD + i] = vb;
+            }
+        }
+    }
+    __syncthreads();
+    {
+        float acc[GW];
+#pragma unroll
+        for (int g = 0; g < GW; g++) acc[g] = 0.f;
+        const uint16_t *kr = ks + lane * KP + wave * DPW;
+#pragma unroll 4
+        for (int c = 0; c < DPW / 8; c++) {
+            const u32x4 w = *(const u32x4 *)(kr + 8 * c);
+            float kv[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) kv[e] = h2f((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+#pragma unroll
+            for (int g = 0; g < GW; g++) {
+                const float4 q0 = *(const float4 *)&qs[g][wave * DPW + 8 * c];
+                const float4 q1 = *(const float4 *)&qs[g][wave * DPW + 8 * c + 4];
+                acc[g] += q0.x * kv[0] + q0.y * kv[1] + q0.z * kv[2] + q0.w * kv[3] + q1.x * kv[4] + q1.y * kv[5] +
+                          q1.z * kv[6] + q1.w * kv[7];
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < GW; g++) sp[wave][g][lane] = acc[g];
+    }
     __syncthreads();
     const float scale = 1.0f / sqrtf((float)HD);
-    for (int g = wave; g < G; g += NW) {
-        const int h = kvh * G + g;
-        float m = -INFINITY, l = 0.f, o[DPL];
+    for (int g = wave; g < GW; g += NW) {
+        const float s = lane < n ? ((sp[0][g][lane] + sp[1][g][lane]) + (sp[2][g][lane] + sp[3][g][lane])) * scale
+                                 : -INFINITY;
+        float m = s;
 #pragma unroll
-        for (int e = 0; e < DPL; e++) o[e] = 0.f;
-        for (int base = 0; base < n; base += WAVE) {
-            const int r = base + lane;
-            float s = -INFINITY;
-            if (r < n) {
-                const uint16_t *kr = ks + r * KP;
-                float acc = 0.f;
-                for (int c = 0; c < HD / 8; c++) {
-                    const u32x4 w = *(const u32x4 *)(kr + 8 * c);
-#pragma unroll
-                    for (int e = 0; e < 8; e++) acc += qs[g][8 * c + e] * h2f((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
-                }
-                s = acc * scale;
-            }
-            float bm = s;
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) bm = fmaxf(bm, __shfl_xor(bm, off, WAVE));
-            const float mn = fmaxf(m, bm), alpha = expf(m - mn);
-            const float pj = r < n ? expf(s - mn) : 0.f;
-            l = l * alpha + wave_sum(pj);
-#pragma unroll
-            for (int e = 0; e < DPL; e++) o[e] *= alpha;
-            const int nj = min(WAVE, n - base);
-            for (int j = 0; j < nj; j++) {
-                const float pb = __shfl(pj, j, WAVE);
-                const uint16_t *vr = vs + (base + j) * HD + DPL * lane;
-#pragma unroll
-                for (int e = 0; e < DPL; e += 2) {
-                    const uint32_t w = *(const uint32_t *)(vr + e);
-                    o[e] += pb * h2f(w & 0xFFFFu);
-                    o[e + 1] += pb * h2f(w >> 16);
-                }
-            }
-            m = mn;
-        }
-        float *pt = a.part + ((size_t)h * a.max_splits + sp) * (HD + 2);
-#pragma unroll
-        for (int e = 0; e < DPL; e++) pt[DPL * lane + e] = o[e];
+        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, WAVE));
+        const float e = lane < n ? expf(s - m) : 0.f;
+        sp[0][g][lane] = e;
+        const float l = wave_sum(e);
         if (lane == 0) {
-            pt[HD] = m;
-            pt[HD + 1] = l;
+            mx[g] = m;
+            sm[g] = l;
+        }
+    }
+    __syncthreads();
+    float *ob = (float *)ks;  // [NW][GW][HD]; the K tile is no longer read
+    {
+        float acc[GW][DPL];
+#pragma unroll
+        for (int g = 0; g < GW; g++)
+#pragma unroll
+            for (int e = 0; e < DPL; e++) acc[g][e] = 0.f;
+        for (int t = wave; t < n; t += NW) {
+            float vv[DPL];
+            const uint16_t *vr = vs + t * HD + DPL * lane;
+#pragma unroll
+            for (int e = 0; e < DPL; e += 2) {
+                const uint32_t w = *(const uint32_t *)(vr + e);
+                vv[e] = h2f(w & 0xFFFFu);
+                vv[e + 1] = h2f(w >> 16);
+            }
+#pragma unroll
+            for (int g = 0; g < GW; g++) {
+                const float p = sp[0][g][t];
+#pragma unroll
+                for (int e = 0; e < DPL; e++) acc[g][e] += p * vv[e];
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < GW; g++)
+#pragma unroll
+            for (int e = 0; e < DPL; e++) ob[(wave * GW + g) * HD + DPL * lane + e] = acc[g][e];
+    }
+    __syncthreads();
+    for (int i = tid; i < GW * HD; i += WG) {
+        const int g = i / HD, d = i % HD;
+        float *pt = a.part + ((size_t)(h0 + g) * a.max_splits + sp_i) * (HD + 2);
+        pt[d] = (ob[(0 * GW + g) * HD + d] + ob[(1 * GW + g) * HD + d]) +
+                (ob[(2 * GW + g) * HD + d] + ob[(3 * GW + g) * HD + d]);
+        if (d == 0) {
+            pt[HD] = mx[g];
+            pt[HD + 1] = sm[g];
         }
     }
 }
@@ -165,8 +221,13 @@ __global__ __launch_bounds__(WG) void q35_combine_kernel(Q35Args a) {
     const int h = blockIdx.x, ns = (a.pos + Q35_CH) / Q35_CH, t = threadIdx.x;
     const int lane = t & (WAVE - 1), wave = t / WAVE;
     const float *pb = a.part + (size_t)h * a.max_splits * (HD + 2);
+    __shared__ float msp[Q35_MAXS], lsp[Q35_MAXS];
     float mx = -INFINITY;
-    for (int s = t; s < ns; s += WG) mx = fmaxf(mx, pb[(size_t)s * (HD + 2) + HD]);
+    for (int s = t; s < ns; s += WG) {  // one memory round trip for every split's (m, l)
+        msp[s] = pb[(size_t)s * (HD + 2) + HD];
+        lsp[s] = pb[(size_t)s * (HD + 2) + HD + 1];
+        mx = fmaxf(mx, msp[s]);
+    }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, WAVE));
     if (lane == 0) red[wave] = mx;
@@ -177,10 +238,10 @@ __global__ __launch_bounds__(WG) void q35_combine_kernel(Q35Args a) {
     __syncthreads();
     float lp = 0.f;
     for (int s = t; s < ns; s += WG) {
-        const float ms = pb[(size_t)s * (HD + 2) + HD];
+        const float ms = msp[s];
         const float w = ms == -INFINITY ? 0.f : expf(ms - M);
         wsp[s] = w;
-        lp += pb[(size_t)s * (HD + 2) + HD + 1] * w;
+        lp += lsp[s] * w;
     }
     lp = wave_sum(lp);
     if (lane == 0) red[wave] = lp;
@@ -204,18 +265,18 @@ hipError_t launch_q35_attn(const Q35Args &a, int head_dim, hipStream_t st) {
     if (ns > a.max_splits || a.rotary_dim < 0 || a.rotary_dim > head_dim || a.rotary_dim % 2 ||
         a.n_heads / a.n_kv_heads > Q35_GMAX || ns > Q35_MAXS)
         return hipErrorInvalidValue;
-    const dim3 g1((unsigned)(a.n_heads + a.n_kv_heads)), g2((unsigned)a.n_kv_heads, (unsigned)ns), g3((unsigned)a.n_heads);
-    if (head_dim == 256) {
-        hipLaunchKernelGGL(q35_prep_kernel<256>, g1, dim3(WG), 0, st, a);
-        hipLaunchKernelGGL(q35_attn_kernel<256>, g2, dim3(WG), 0, st, a);
-        hipLaunchKernelGGL(q35_combine_kernel<256>, g3, dim3(WG), 0, st, a);
-    } else if (head_dim == 128) {
-        hipLaunchKernelGGL(q35_prep_kernel<128>, g1, dim3(WG), 0, st, a);
-        hipLaunchKernelGGL(q35_attn_kernel<128>, g2, dim3(WG), 0, st, a);
-        hipLaunchKernelGGL(q35_combine_kernel<128>, g3, dim3(WG), 0, st, a);
-    } else {
-        return hipErrorInvalidValue;
-    }
+    const int G = a.n_heads / a.n_kv_heads, gw = G % 4 == 0 ? 4 : G % 2 == 0 ? 2 : 1;
+    const dim3 g2((unsigned)(a.n_kv_heads * (G / gw)), (unsigned)ns), g3((unsigned)a.n_heads);
+    auto attn = [&](auto hd_tag) {
+        constexpr int HD = decltype(hd_tag)::value;
+        if (gw == 4) hipLaunchKernelGGL((q35_attn_kernel<HD, 4>), g2, dim3(WG), 0, st, a);
+        else if (gw == 2) hipLaunchKernelGGL((q35_attn_kernel<HD, 2>), g2, dim3(WG), 0, st, a);
+        else hipLaunchKernelGGL((q35_attn_kernel<HD, 1>), g2, dim3(WG), 0, st, a);
+        hipLaunchKernelGGL(q35_combine_kernel<HD>, g3, dim3(WG), 0, st, a);
+    };
+    if (head_dim == 256) attn(std::integral_constant<int, 256>{});
+    else if (head_dim == 128) attn(std::integral_constant<int, 128>{});
+    else return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
