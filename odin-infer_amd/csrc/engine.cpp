@@ -963,7 +963,7 @@ constexpr int PF_MAX_T = 512;
 namespace {
 
 bool prefill_batched_ok(const oi_engine *e) {
-    if (e->cfg.head_dim != 128 && e->cfg.head_dim != 256) return false;
+    if ((e->cfg.head_dim != 128 && e->cfg.head_dim != 256) || e->cfg.dim > 16384) return false;
     for (const LayerDev &L : e->layers)
         for (const DMat *m : {&L.wq, &L.wk, &L.wv, &L.wo, &L.w1, &L.w2, &L.w3})
             if (!gemm_supported(*m)) return false;
@@ -1023,9 +1023,11 @@ int prefill_chunk(oi_engine *e, const int32_t *tokens, int T, int pos) {
     HIP_TRY(launch_embed_rows(e->tok_embd, e->pf_tok, T, e->pf_x, st));
     float *const *P = e->pf_p;
     const size_t *PB = e->pf_pbytes;
-    for (const LayerDev &L : e->layers) {
+    // each residual add is fused with the next sublayer's RMSNorm
+    HIP_TRY(launch_pf_addnorm16(e->pf_x, nullptr, 1, e->layers[0].attn_norm, eps, D, T, e->pf_xb, st));
+    for (size_t l = 0; l < e->layers.size(); l++) {
+        const LayerDev &L = e->layers[l];
         int qs = 1, ks = 1, vs = 1, s0 = 1, s1 = 1;
-        HIP_TRY(launch_pf_rmsnorm16(e->pf_x, L.attn_norm, eps, D, T, e->pf_xb, st));
         HIP_TRY(launch_gemm_parts(L.wq, e->pf_xb, T, P[0], PB[0], &qs, st));
         HIP_TRY(launch_gemm_parts(L.wk, e->pf_xb, T, P[1], PB[1], &ks, st));
         HIP_TRY(launch_gemm_parts(L.wv, e->pf_xb, T, P[2], PB[2], &vs, st));
@@ -1035,13 +1037,15 @@ int prefill_chunk(oi_engine *e, const int32_t *tokens, int T, int pos) {
         HIP_TRY(launch_pf_attn(e->pf_q, L.kc, L.vc, e->pf_xb, T, pos, (int)c.seq_len, (int)c.n_heads,
                                (int)c.n_kv_heads, hd, st));
         HIP_TRY(launch_gemm_parts(L.wo, e->pf_xb, T, P[0], PB[0], &s0, st));
-        HIP_TRY(launch_pf_add(e->pf_x, P[0], s0, (int64_t)T * D, st));
-        HIP_TRY(launch_pf_rmsnorm16(e->pf_x, L.ffn_norm, eps, D, T, e->pf_xb, st));
+        HIP_TRY(launch_pf_addnorm16(e->pf_x, P[0], s0, L.ffn_norm, eps, D, T, e->pf_xb, st));
         HIP_TRY(launch_gemm_parts(L.w1, e->pf_xb, T, P[0], PB[0], &s0, st));
         HIP_TRY(launch_gemm_parts(L.w3, e->pf_xb, T, P[1], PB[1], &s1, st));
         HIP_TRY(launch_pf_swiglu16(P[0], s0, P[1], s1, (int64_t)T * H, e->pf_xb, st));
         HIP_TRY(launch_gemm_parts(L.w2, e->pf_xb, T, P[0], PB[0], &s0, st));
-        HIP_TRY(launch_pf_add(e->pf_x, P[0], s0, (int64_t)T * D, st));
+        if (l + 1 < e->layers.size())
+            HIP_TRY(launch_pf_addnorm16(e->pf_x, P[0], s0, e->layers[l + 1].attn_norm, eps, D, T, e->pf_xb, st));
+        else
+            HIP_TRY(launch_pf_add(e->pf_x, P[0], s0, (int64_t)T * D, st));
     }
     GemvArgs a = gemv_args(GEMV_STORE, D, e->pf_x + (size_t)(T - 1) * D, e->output_norm, eps);
     a.nseg = 1;

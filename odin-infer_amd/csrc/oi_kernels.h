@@ -145,6 +145,9 @@ hipError_t launch_pf_qkv(const PfQkvArgs &a, int head_dim, hipStream_t st);
 hipError_t launch_pf_attn(const float *q, const uint16_t *kc, const uint16_t *vc, uint16_t *out, int T, int pos0,
                           int seq_len, int n_heads, int n_kv_heads, int head_dim, hipStream_t st);
 hipError_t launch_pf_add(float *x, const float *part, int split, int64_t total, hipStream_t st);
+// x += partial-product sums (part may be null), then out = f16(rmsnorm(x) * w); dim <= 16384
+hipError_t launch_pf_addnorm16(float *x, const float *part, int split, const float *w, float eps, int dim, int T,
+                               uint16_t *out, hipStream_t st);
 hipError_t launch_pf_swiglu16(const float *g, int gs, const float *u, int us, int64_t total, uint16_t *out,
                               hipStream_t st);
 // deltanet.hip: the gated DeltaNet token step (between the input and output

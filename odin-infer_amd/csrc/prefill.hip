@@ -51,7 +51,68 @@ __global__ __launch_bounds__(WG) void pf_rmsnorm16_kernel(const float *x, const 
     for (int i = threadIdx.x; i < dim; i += WG) out[t * dim + i] = f2h(w[i] * (s * xt[i]));
 }
 
-// Per token (grid T) and head (one wave each): q and k heads RMSNorm'd with
+// x[t] += (sum of the K-slice partial products) when part is set, then
+// out[t] = f16 of x[t]'s RMSNorm with w (the residual add of one sublayer
+// fused with the next sublayer's norm; x read once, kept in registers).
+// Grid: T; dim <= WG * PF_NPT.
+constexpr int PF_NPT = 64;
+__global__ __launch_bounds__(WG) void pf_addnorm16_kernel(float *x, const float *part, int split, const float *w,
+                                                          float eps, int dim, int T, uint16_t *out) {
+#pragma clang fp contract(off)
+    constexpr int NV = PF_NPT / 4;  // float4 per thread
+    __shared__ float red[WG / WAVE];
+    const size_t t = blockIdx.x;
+    const int d4 = dim / 4;
+    float4 *xt = (float4 *)(x + t * dim);
+    float4 v[NV];
+#pragma unroll
+    for (int r = 0; r < NV; r++) {  // every load of the row issued before any use
+        const int i = threadIdx.x + WG * r;
+        if (i < d4) v[r] = xt[i];
+    }
+    if (part) {
+        const float4 *p4 = (const float4 *)part + t * d4;
+        const size_t slice = (size_t)T * d4;
+        for (int z = 0; z < split; z++) {
+            float4 pz[NV];
+#pragma unroll
+            for (int r = 0; r < NV; r++) {
+                const int i = threadIdx.x + WG * r;
+                if (i < d4) pz[r] = p4[z * slice + i];
+            }
+#pragma unroll
+            for (int r = 0; r < NV; r++) {
+                const int i = threadIdx.x + WG * r;
+                if (i < d4) {
+                    v[r].x += pz[r].x; v[r].y += pz[r].y; v[r].z += pz[r].z; v[r].w += pz[r].w;
+                }
+            }
+        }
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int r = 0; r < NV; r++) {
+        const int i = threadIdx.x + WG * r;
+        if (i < d4) ss += v[r].x * v[r].x + v[r].y * v[r].y + v[r].z * v[r].z + v[r].w * v[r].w;
+    }
+    ss = block_sum(ss, red);
+    const float s = 1.0f / sqrtf(ss / (float)dim + eps);
+    const float4 *w4 = (const float4 *)w;
+    uint2 *o4 = (uint2 *)(out + t * dim);
+#pragma unroll
+    for (int r = 0; r < NV; r++) {
+        const int i = threadIdx.x + WG * r;
+        if (i < d4) {
+            if (part) xt[i] = v[r];
+            const float4 wv = w4[i];
+            o4[i] = uint2{(uint32_t)f2h(wv.x * (s * v[r].x)) | ((uint32_t)f2h(wv.y * (s * v[r].y)) << 16),
+                          (uint32_t)f2h(wv.z * (s * v[r].z)) | ((uint32_t)f2h(wv.w * (s * v[r].w)) << 16)};
+        }
+    }
+}
+
+// Per token and head (grid (T, ceil(heads / 4)), one wave per head; q, k
+// and v heads in that order): q and k heads RMSNorm'd with
 // q_norm / k_norm and rotated at pos0 + t (forward.odin:57-85, pairs i and
 // i + hd/2); k and v rounded to f16 into the cache at pos0 + t; q kept in f32.
 // Lane l holds dimensions l + 64 e, so the RoPE pair of e is e + DPL/2.
@@ -61,7 +122,9 @@ __global__ __launch_bounds__(WG) void pf_qkv_kernel(PfQkvArgs a) {
     constexpr int DPL = HD / WAVE;
     const int t = blockIdx.x, lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
     const int pos = a.pos0 + t, QD = a.n_heads * HD, KVD = a.n_kv_heads * HD;
-    for (int hh = wave; hh < a.n_heads + 2 * a.n_kv_heads; hh += WG / WAVE) {
+    {
+        const int hh = (int)blockIdx.y * (WG / WAVE) + wave;
+        if (hh >= a.n_heads + 2 * a.n_kv_heads) return;
         const bool isq = hh < a.n_heads, isk = !isq && hh < a.n_heads + a.n_kv_heads;
         const int h = isq ? hh : isk ? hh - a.n_heads : hh - a.n_heads - a.n_kv_heads;
         const float *src = isq ? a.q : isk ? a.k : a.v;
@@ -361,8 +424,9 @@ hipError_t launch_pf_rmsnorm16(const float *x, const float *w, float eps, int di
 }
 
 hipError_t launch_pf_qkv(const PfQkvArgs &a, int head_dim, hipStream_t st) {
-    if (head_dim == 128) hipLaunchKernelGGL(pf_qkv_kernel<128>, dim3(a.T), dim3(WG), 0, st, a);
-    else if (head_dim == 256) hipLaunchKernelGGL(pf_qkv_kernel<256>, dim3(a.T), dim3(WG), 0, st, a);
+    const dim3 grid((unsigned)a.T, (unsigned)((a.n_heads + 2 * a.n_kv_heads + WG / WAVE - 1) / (WG / WAVE)));
+    if (head_dim == 128) hipLaunchKernelGGL(pf_qkv_kernel<128>, grid, dim3(WG), 0, st, a);
+    else if (head_dim == 256) hipLaunchKernelGGL(pf_qkv_kernel<256>, grid, dim3(WG), 0, st, a);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }
@@ -376,6 +440,13 @@ hipError_t launch_pf_attn(const float *q, const uint16_t *kc, const uint16_t *vc
                            T);
     else if (head_dim == 256) hipLaunchKernelGGL(pf_attn_kernel<256>, grid, dim3(WG), 0, st, a);
     else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_pf_addnorm16(float *x, const float *part, int split, const float *w, float eps, int dim, int T,
+                               uint16_t *out, hipStream_t st) {
+    if (dim > WG * PF_NPT) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(pf_addnorm16_kernel, dim3(T), dim3(WG), 0, st, x, part, split, w, eps, dim, T, out);
     return hipGetLastError();
 }
 
