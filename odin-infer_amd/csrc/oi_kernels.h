@@ -139,8 +139,6 @@ struct PfQkvArgs {
     float *qout;                // [T][n_heads * head_dim]
     int32_t T, pos0, seq_len, n_heads, n_kv_heads;
 };
-hipError_t launch_pf_rmsnorm16(const float *x, const float *w, float eps, int dim, int T, uint16_t *out,
-                               hipStream_t st);
 hipError_t launch_pf_qkv(const PfQkvArgs &a, int head_dim, hipStream_t st);
 hipError_t launch_pf_attn(const float *q, const uint16_t *kc, const uint16_t *vc, uint16_t *out, int T, int pos0,
                           int seq_len, int n_heads, int n_kv_heads, int head_dim, hipStream_t st);

@@ -35,25 +35,12 @@ static __device__ __forceinline__ float parts_at(const float *p, int split, size
     return s;
 }
 
-// out[t][i] = f16(w[i] * (s * x[t][i])), s = 1 / sqrt(sum x^2 / dim + eps)
-// (ops.odin rmsnorm; the reference converts the f32 result to half for the
-// projection, metal.odin:1236-1242).  Grid: T.
-__global__ __launch_bounds__(WG) void pf_rmsnorm16_kernel(const float *x, const float *w, float eps, int dim,
-                                                          uint16_t *out) {
-#pragma clang fp contract(off)
-    __shared__ float red[WG / WAVE];
-    const size_t t = blockIdx.x;
-    const float *xt = x + t * dim;
-    float ss = 0.f;
-    for (int i = threadIdx.x; i < dim; i += WG) ss += xt[i] * xt[i];
-    ss = block_sum(ss, red);
-    const float s = 1.0f / sqrtf(ss / (float)dim + eps);
-    for (int i = threadIdx.x; i < dim; i += WG) out[t * dim + i] = f2h(w[i] * (s * xt[i]));
-}
-
 // x[t] += (sum of the K-slice partial products) when part is set, then
-// out[t] = f16 of x[t]'s RMSNorm with w (the residual add of one sublayer
-// fused with the next sublayer's norm; x read once, kept in registers).
+// out[t] = f16 of x[t]'s RMSNorm with w: w[i] * (s * x[i]), s = 1 / sqrt(sum
+// x^2 / dim + eps) (ops.odin rmsnorm; the reference converts the f32 result
+// to half for the projection, metal.odin:1236-1242).  The residual add of one
+// sublayer fused with the next sublayer's norm; x read once, kept in
+// registers.
 // Grid: T; dim <= WG * PF_NPT.
 constexpr int PF_NPT = 64;
 __global__ __launch_bounds__(WG) void pf_addnorm16_kernel(float *x, const float *part, int split, const float *w,
@@ -416,12 +403,6 @@ __global__ __launch_bounds__(WG) void pf_swiglu16_kernel(const float *g, int gs,
 }
 
 static unsigned blocks(int64_t n) { return (unsigned)((n + WG - 1) / WG); }
-
-hipError_t launch_pf_rmsnorm16(const float *x, const float *w, float eps, int dim, int T, uint16_t *out,
-                               hipStream_t st) {
-    hipLaunchKernelGGL(pf_rmsnorm16_kernel, dim3(T), dim3(WG), 0, st, x, w, eps, dim, out);
-    return hipGetLastError();
-}
 
 hipError_t launch_pf_qkv(const PfQkvArgs &a, int head_dim, hipStream_t st) {
     const dim3 grid((unsigned)a.T, (unsigned)((a.n_heads + 2 * a.n_kv_heads + WG / WAVE - 1) / (WG / WAVE)));
