@@ -89,7 +89,7 @@ PEAK_F16_TFLOPS = 2500.0  # MI355X dense f16 MFMA
 ROTATE_BYTES = 1 << 30  # secondary benches cycle through >= 1 GiB of weights / state
 
 
-def prefill_gemm(iters=50, cpu=True):
+def prefill_gemm(iters=50, cpu=True, tokens=64, shapes=((12, 4096, 4096), (12, 12288, 4096), (14, 4096, 12288))):
     """Batched projection (oi_gemm_launch, the prefill GEMM on the matrix cores)
     at the reference harness's projection shapes with 64 tokens: weights
     resident in HBM (copies totalling >= 1 GiB, cycled, so the Infinity Cache
@@ -111,8 +111,8 @@ def prefill_gemm(iters=50, cpu=True):
 
     rng = np.random.default_rng(7)
     out = []
-    for kind, m, k in ((12, 4096, 4096), (12, 12288, 4096), (14, 4096, 12288)):
-        n = 64
+    for kind, m, k in shapes:
+        n = tokens
         e, b = {12: (256, 144), 14: (256, 210)}[kind]
         nb = m * (k // e)
         raw = rng.integers(0, 256, size=(nb, b), dtype=np.uint8)

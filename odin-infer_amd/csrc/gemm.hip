@@ -59,10 +59,12 @@ struct GemmArgs {
     int32_t n;
 };
 
+// f32 -> f16 (RNE) of values already rounded to f32 (f2h: the conversion is
+// kept apart from the fma that produced the value)
 static __device__ __forceinline__ h8 cvt8(const float (&v)[8]) {
     h8 r;
 #pragma unroll
-    for (int e = 0; e < 8; e++) r[e] = (_Float16)v[e];
+    for (int e = 0; e < 8; e++) r[e] = __builtin_bit_cast(_Float16, f2h(v[e]));
     return r;
 }
 static __device__ __forceinline__ uint32_t byte_of(uint32_t lo, uint32_t hi, int e) {

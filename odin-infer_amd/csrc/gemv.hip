@@ -488,7 +488,11 @@ static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int 
 // TL for the last (TL == T: one type).  A runtime switch over all types would
 // let the compiler merge the code paths, and at the merge it can no longer
 // count the loads in flight, so it waits for all of them; the two arms here
-// issue their x loads in different orders so that they are not merged.  Other
+// issue their x loads in different orders so that they are not merged.
+// Every wave waits for its x loads before it requests weights: x was written
+// by the previous kernel and is read from the shared cache level, where it
+// would otherwise queue behind the other CUs' weight requests (the prologue
+// then ends later than the first weights arrive).  Other
 // type mixes are issued as one launch per type (wg_base).
 template <int T, int TL, int R, int NM, int XR, bool XU1, bool NORM>
 __global__ __launch_bounds__(GW) void gemv_q_kernel(GemvArgs a) {
@@ -506,10 +510,14 @@ __global__ __launch_bounds__(GW) void gemv_q_kernel(GemvArgs a) {
         XPre<XR, NORM> xp;
         xpre_load<XR, NORM, true>(a, xp);  // x first, then the weights (loads return in order)
         __builtin_amdgcn_sched_barrier(0);  // keep every x load ahead of the weight loads
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        __builtin_amdgcn_sched_barrier(0);
         gemv_run<TL, R, NM, XR, XU1, NORM>(a, seg, tb, te, wg, xp);
     } else {
         XPre<XR, NORM> xp;
         xpre_load<XR, NORM>(a, xp);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): x has arrived before any weight request goes out
         __builtin_amdgcn_sched_barrier(0);
         gemv_run<T, R, NM, XR, XU1, NORM>(a, seg, tb, te, wg, xp);
     }

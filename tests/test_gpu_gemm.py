@@ -51,6 +51,55 @@ def test_gemm_vs_oracle(kind, m, n, k, tol):
     assert err <= tol, "%s %dx%dx%d scaled error %.3g" % (kind, m, n, k, err)
 
 
+def _q4k_wide_range_blocks(rows, rng):
+    """Q4_K rows of one super-block with d in [0.5, 2) and dmin in [2^-16, 2^-12):
+    d*sc*q - dmin*m then spans more than 24 bits, so the f32 dequantization
+    rounds, and rounding that value to f16 differs from rounding the exact
+    value to f16 once in about 1 of 8000 weights."""
+    raw = rng.integers(0, 256, size=(rows, 144), dtype=np.uint8)
+    raw[:, 0:2] = (0.5 + 1.5 * rng.random(rows)).astype(np.float16).view(np.uint8).reshape(rows, 2)
+    raw[:, 2:4] = (2.0 ** rng.uniform(-16, -12, rows)).astype(np.float16).view(np.uint8).reshape(rows, 2)
+    return raw
+
+
+def _q4k_double_rounding_sensitive(raw):
+    """Weights whose f16 value depends on rounding to f32 first (float64 stands in
+    for the exact value, close enough to count them)."""
+    d = raw[:, 0:2].copy().view(np.float16)[:, 0].astype(np.float64)
+    dmin = raw[:, 2:4].copy().view(np.float16)[:, 0].astype(np.float64)
+    n = 0
+    for r in range(raw.shape[0]):
+        q12 = raw[r, 4:16]
+        for j in range(8):
+            sc, mc = refcpu.get_scale_min_k4(j, q12)
+            qs = raw[r, 16 + 32 * (j // 2):16 + 32 * (j // 2) + 32]
+            q = (qs & 15) if j % 2 == 0 else (qs >> 4)
+            d1, m = np.float32(d[r] * sc), np.float32(dmin[r] * mc)  # exact products
+            x = float(d1) * q.astype(np.float64) - float(m)
+            once = x.astype(np.float16)
+            twice = x.astype(np.float32).astype(np.float16)
+            n += int(np.count_nonzero(once != twice))
+    return n
+
+
+def test_gemm_staged_weights_bit_exact():
+    """One-hot activations (token t has 1.0 at column t and zeros elsewhere) make
+    C[t][r] the staged weight f16(dequant(W)[r][t]) itself: one exact product,
+    every other term zero.  The staging (dequantize in f32 as ggml/quant.odin
+    does, then round to f16) is compared bit for bit over 4096 Q4_K rows drawn
+    so that the f32 dequantization rounds; the rows hold weights where rounding
+    the exact value to f16 in one step (v_fma_mix*_f16) would differ."""
+    rng = np.random.default_rng(2024)
+    m, k = 4096, 256
+    raw = _q4k_wide_range_blocks(m, rng)
+    assert _q4k_double_rounding_sensitive(raw[:512]) >= 5  # the draw exercises the distinction
+    x = x16(np.eye(k))
+    got = ggml.gemm(12, raw.reshape(-1), m, k, x)
+    ref = refcpu.gemm_f16(raw.reshape(-1), 12, m, k, x)
+    bad = np.flatnonzero(got.astype(np.float64).ravel() != ref.ravel())
+    assert bad.size == 0, "%d staged weights differ, first at %s" % (bad.size, np.unravel_index(bad[:4], got.shape))
+
+
 def test_gemm_rejects_bad_shapes():
     rng = np.random.default_rng(0)
     w = gemm_blocks(12, 8, 256, rng)
