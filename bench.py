@@ -457,7 +457,8 @@ def moe_step(iters=100, cpu=True):
     out = {"shape": "128 experts, top 8, dim 2048, inter 768, Q4_K experts, F32 router", "avg_us": round(us, 3),
            "weight_sets": len(sets),
            "bytes": int(byts), "GBps": round(byts / us / 1e3, 1), "frac_hbm_peak": round(byts / us / 1e3 / PEAK_HBM_GBPS, 4),
-           "kernels": "router GEMV + moe_topk_kernel + moe_gateup_kernel + moe_down_kernel"}
+           "kernels": "router GEMV + gemv_q_kernel rows mode (routing in its prologue, gate/up) + "
+                      "gemv_q_kernel columns mode (down)"}
     if cpu:
         rc = _oracle()
         t0 = time.perf_counter()

@@ -1610,7 +1610,36 @@ int oi_moe_ffn_launch(const oi_moe_dims *d, const oi_weights *router, const oi_w
     g.seg[0].m = router->m;
     g.seg[0].y = ws;
     if (!plan_gemv(g)) return fail(OI_E_UNSUPPORTED, "moe: router row length not supported");
-    HIP_TRY(launch_moe(a, g, (hipStream_t)stream));
+    // gate/up and down on the quantized GEMV kernel with the experts chosen on
+    // the device, where the type and shapes allow; the generic kernels otherwise
+    GemvArgs gu = gemv_args(GEMV_SWIGLU, d->dim, x_dev, nullptr, 0.f);
+    gu.nseg = 2;
+    gu.seg[0].m = gate->m;
+    gu.seg[1].m = up->m;
+    gu.seg[0].m.rows = gu.seg[1].m.rows = d->top_k * d->inter;  // the chosen experts' rows
+    gu.seg[0].y = gu.seg[1].y = a.h;
+    gu.moe_logits = a.logits;  // routed inside the gate/up kernel
+    gu.moe_ids_out = a.ids;
+    gu.moe_w_out = a.w;
+    gu.moe_norm = d->norm_topk_prob;
+    gu.moe_k = d->top_k;
+    gu.moe_n = d->n_experts;
+    gu.moe_blk = d->inter;
+    const bool gu_ok = gemv_q_moe_supported(gu, MOE_ROWS);
+    if (gu_ok) plan_gemv_q(gu);
+    GemvArgs dn = gemv_args(GEMV_STORE, d->top_k * d->inter, a.h, nullptr, 0.f);
+    dn.nseg = 1;
+    dn.seg[0].m = down->m;
+    dn.seg[0].m.rows = d->dim;  // row r of every expert
+    dn.seg[0].y = y_dev;
+    dn.moe_ids = a.ids;
+    dn.moe_w = a.w;
+    dn.moe_k = d->top_k;
+    dn.moe_n = d->n_experts;
+    dn.moe_blk = d->inter / 64;
+    const bool dn_ok = gemv_q_moe_supported(dn, MOE_COLS);
+    if (dn_ok) plan_gemv_q(dn);
+    HIP_TRY(launch_moe(a, g, gu_ok ? &gu : nullptr, dn_ok ? &dn : nullptr, (hipStream_t)stream));
     return OI_OK;
 }
 

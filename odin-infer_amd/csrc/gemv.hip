@@ -326,9 +326,9 @@ static __device__ __forceinline__ void xpre_finish(const GemvArgs &a, const XPre
 // step past the end reads row 0's first units, unused), so the compiler
 // waits for exactly the stage it consumes.  Rows past the end of the matrix
 // are clamped to the last row (computed, not stored).
-template <int T, int R, int NM, int XR, bool XU1, bool NORM>
+template <int T, int R, int NM, int XR, bool XU1, bool NORM, int MOE = 0>
 static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int tb, int te, int wg,
-                                                const XPre<XR, NORM> &xp) {
+                                                const XPre<XR, NORM> &xp, int idv = 0, float wv = 0.f) {
     using W = typename Types<T>::W;
     using X = typename Types<T>::X;
     extern __shared__ u32x4 smem[];
@@ -351,8 +351,17 @@ static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int 
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const int row = live ? min((tb + t) * rpt + rsub + r, rows_m - 1) : 0;
-            wload(m0, row, live ? u : j, w[0][r]);
-            if (NM == 2) wload(m1, row, live ? u : j, w[NM - 1][r]);
+            int prow = row, pu = live ? u : j;  // the stored row and unit
+            if (MOE == MOE_ROWS) {  // virtual row -> row of the chosen expert
+                const int k = row / a.moe_blk;
+                prow = __shfl(idv, k, WAVE) * a.moe_blk + (row - k * a.moe_blk);
+            } else if (MOE == MOE_COLS) {  // unit of the concatenation -> unit of the chosen expert's row
+                const int k = pu / a.moe_blk;
+                prow = __shfl(idv, k, WAVE) * rows_m + row;
+                pu -= k * a.moe_blk;
+            }
+            wload(m0, prow, pu, w[0][r]);
+            if (NM == 2) wload(m1, prow, pu, w[NM - 1][r]);
         }
     };
     // x was requested by the caller; the first weights follow (loads return in order)
@@ -393,9 +402,13 @@ static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int 
     auto compute = [&](int t, int ui, const W (&w)[NM][R]) {
         const int u = XU1 ? j : j + ui * lpr;
         if (!XU1) xload(xq, u, xu);
+        // (MOE_COLS: the unit's expert weight; units keep their position in the
+        // super-block, as each expert's part is a whole number of super-blocks)
+        const float uw = MOE == MOE_COLS ? __shfl(wv, u / a.moe_blk, WAVE) : 1.f;
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            acc[0][r] += wdot(w[0][r], u, xu);
+            if (MOE == MOE_COLS) acc[0][r] += uw * wdot(w[0][r], u, xu);
+            else acc[0][r] += wdot(w[0][r], u, xu);
             if (NM == 2) acc[NM - 1][r] += wdot(w[NM - 1][r], u, xu);
         }
         if (XU1 || ui == upl - 1) {
@@ -484,6 +497,69 @@ static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int 
     }
 }
 
+// Routing of one token inside the workgroup (MoE rows mode): the router
+// logits l[0..n) (n <= GW) -> softmax (max, exp(l - max), sum, divide: the
+// oracle's ref_softmax) -> each expert's rank (the number of experts with a
+// larger p, or an equal p and a lower id, i.e. the order of k rounds of
+// first-maximum selection) -> lane k < moe_k of every wave gets the id of rank
+// k and its weight (p, or p / the sum of the chosen in rank order).  Workgroup
+// 0 also writes them out for the down projection and the caller.  The loads
+// were issued by the caller before the weights'.
+static __device__ __forceinline__ void moe_route(const GemvArgs &a, float lg, int &idv, float &wv, int wg) {
+    __shared__ __attribute__((aligned(16))) float p[GW];
+    __shared__ float rmax[GNW], rsum[GNW];
+    __shared__ int sid[WAVE];
+    __shared__ float sw[WAVE];
+    const int n = a.moe_n, t = threadIdx.x, lane = t & (WAVE - 1), wave = t / WAVE;
+    float m = t < n ? lg : -INFINITY;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, WAVE));
+    if (lane == 0) rmax[wave] = m;
+    __syncthreads();
+    float M = rmax[0];
+#pragma unroll
+    for (int w = 1; w < GNW; w++) M = fmaxf(M, rmax[w]);
+    float e = 0.f;
+    if (t < n) {
+#pragma clang fp contract(off)
+        e = expf(lg - M);
+    }
+    const float es = wave_sum(e);
+    if (lane == 0) rsum[wave] = es;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < GNW; w++) tot += rsum[w];
+    const float pi = e / tot;
+    if (t < n) p[t] = pi;
+    __syncthreads();
+    if (t < n) {
+        int rank = 0, j = 0;
+#pragma unroll 4
+        for (; j + 4 <= n; j += 4) {
+            const float4 q = *(const float4 *)&p[j];
+            rank += (better(q.x, j, pi, t) ? 1 : 0) + (better(q.y, j + 1, pi, t) ? 1 : 0) +
+                    (better(q.z, j + 2, pi, t) ? 1 : 0) + (better(q.w, j + 3, pi, t) ? 1 : 0);
+        }
+        for (; j < n; j++) rank += better(p[j], j, pi, t) ? 1 : 0;
+        if (rank < a.moe_k) {
+            sid[rank] = t;
+            sw[rank] = pi;
+        }
+    }
+    __syncthreads();
+    float s = 0.f;
+    for (int k = 0; k < a.moe_k; k++) s += sw[k];  // in rank order, as the sequential selection
+    if (lane < a.moe_k) {
+        idv = sid[lane];
+        wv = a.moe_norm ? sw[lane] / s : sw[lane];
+        if (wg == 0 && wave == 0) {
+            a.moe_ids_out[lane] = idv;
+            a.moe_w_out[lane] = wv;
+        }
+    }
+}
+
 // Weight types are template parameters: T for every segment but the last,
 // TL for the last (TL == T: one type).  A runtime switch over all types would
 // let the compiler merge the code paths, and at the merge it can no longer
@@ -494,7 +570,7 @@ static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int 
 // would otherwise queue behind the other CUs' weight requests (the prologue
 // then ends later than the first weights arrive).  Other
 // type mixes are issued as one launch per type (wg_base).
-template <int T, int TL, int R, int NM, int XR, bool XU1, bool NORM>
+template <int T, int TL, int R, int NM, int XR, bool XU1, bool NORM, int MOE = 0>
 __global__ __launch_bounds__(GW) void gemv_q_kernel(GemvArgs a) {
     const int wg = blockIdx.x + a.wg_base;
     int seg = 0;
@@ -516,10 +592,25 @@ __global__ __launch_bounds__(GW) void gemv_q_kernel(GemvArgs a) {
     } else {
         XPre<XR, NORM> xp;
         xpre_load<XR, NORM>(a, xp);
+        // routed experts: lane l < moe_k holds expert l's id (and weight)
+        int idv = 0;
+        float wv = 0.f;
+        float lg = 0.f;
+        const bool route = MOE == MOE_ROWS && a.moe_logits != nullptr;
+        if (MOE) {
+            const int l = threadIdx.x & (WAVE - 1);
+            if (route) {
+                if ((int)threadIdx.x < a.moe_n) lg = a.moe_logits[threadIdx.x];
+            } else if (l < a.moe_k) {
+                idv = min(max(a.moe_ids[l], 0), a.moe_n - 1);  // ids come from the device
+                if (MOE == MOE_COLS) wv = a.moe_w[l];
+            }
+        }
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): x has arrived before any weight request goes out
         __builtin_amdgcn_sched_barrier(0);
-        gemv_run<T, R, NM, XR, XU1, NORM>(a, seg, tb, te, wg, xp);
+        if (route) moe_route(a, lg, idv, wv, wg);
+        gemv_run<T, R, NM, XR, XU1, NORM, MOE>(a, seg, tb, te, wg, xp, idv, wv);
     }
 }
 
@@ -666,6 +757,57 @@ void plan_gemv_q(GemvArgs &a) {
     }
     a.tiles_per_wg = most;
     a.kernel = 1;
+}
+
+// routed experts: one weight type, no RMSNorm; MOE_ROWS is the SwiGLU pair,
+// MOE_COLS a single matrix whose experts' parts are whole super-blocks
+template <int T, int MOE>
+static const void *gemv_q_moe_fn(int K) {
+    const bool xu1 = xu1_of(K);
+    if (MOE == MOE_ROWS) {
+        if (K > 4096) return nullptr;
+        if (xu1) return (const void *)gemv_q_kernel<T, T, 1, 2, 1, true, false, MOE_ROWS>;
+        return (const void *)gemv_q_kernel<T, T, 1, 2, 1, false, false, MOE_ROWS>;
+    }
+    if (K <= 4096 && xu1) return (const void *)gemv_q_kernel<T, T, 1, 1, 1, true, false, MOE_COLS>;
+    if (K <= 4096) return (const void *)gemv_q_kernel<T, T, 1, 1, 1, false, false, MOE_COLS>;
+    if (K <= 12288) return (const void *)gemv_q_kernel<T, T, 1, 1, 3, false, false, MOE_COLS>;
+    return nullptr;
+}
+static const void *gemv_q_moe_fn(int type, int moe, int K) {
+    switch (type) {
+    case T_Q4_K: return moe == MOE_ROWS ? gemv_q_moe_fn<T_Q4_K, MOE_ROWS>(K) : gemv_q_moe_fn<T_Q4_K, MOE_COLS>(K);
+    case T_Q6_K: return moe == MOE_ROWS ? gemv_q_moe_fn<T_Q6_K, MOE_ROWS>(K) : gemv_q_moe_fn<T_Q6_K, MOE_COLS>(K);
+    case T_Q8_0: return moe == MOE_ROWS ? gemv_q_moe_fn<T_Q8_0, MOE_ROWS>(K) : gemv_q_moe_fn<T_Q8_0, MOE_COLS>(K);
+    default: return nullptr;
+    }
+}
+
+bool gemv_q_moe_supported(const GemvArgs &a, int moe) {
+    if (a.norm_w || a.moe_k < 1 || a.moe_k > WAVE || a.moe_n < 1 || a.moe_blk < 1) return false;
+    if (moe == MOE_ROWS) {
+        if (a.mode != GEMV_SWIGLU || a.seg[0].m.rows != a.moe_k * a.moe_blk) return false;
+        if (a.moe_logits ? (a.moe_n > GW || a.moe_k > a.moe_n || !a.moe_ids_out || !a.moe_w_out) : !a.moe_ids)
+            return false;
+    } else if (moe == MOE_COLS) {
+        if (a.mode != GEMV_STORE || a.nseg != 1 || !a.moe_ids || !a.moe_w || a.moe_blk % 4 ||
+            a.K != a.moe_k * 64 * a.moe_blk ||
+            a.seg[0].m.cols != 64 * a.moe_blk)
+            return false;
+    } else {
+        return false;
+    }
+    return gemv_q_supported(a) && gemv_q_moe_fn(a.seg[0].m.type, moe, a.K) != nullptr;
+}
+
+hipError_t launch_gemv_q_moe(const GemvArgs &a, int moe, hipStream_t st) {
+    const void *fn = gemv_q_moe_supported(a, moe) ? gemv_q_moe_fn(a.seg[0].m.type, moe, a.K) : nullptr;
+    if (!fn) return hipErrorInvalidValue;
+    GemvArgs b = a;
+    b.wg_base = 0;
+    void *args[] = {(void *)&b};
+    const size_t lds = gemv_q_lds(a.K, a.tiles_per_wg * a.rows_per_wg);
+    return hipLaunchKernel(fn, dim3(a.total_wgs), dim3(GW), args, lds, st);
 }
 
 hipError_t launch_gemv_q(const GemvArgs &a, hipStream_t st) {

@@ -569,17 +569,28 @@ __global__ __launch_bounds__(WG) void moe_down_kernel(MoeArgs a) {
     if (lane == 0) a.y[r] = y;
 }
 
-hipError_t launch_moe(const MoeArgs &a, const GemvArgs &router, hipStream_t st) {
+hipError_t launch_moe(const MoeArgs &a, const GemvArgs &router, const GemvArgs *gu, const GemvArgs *dn,
+                      hipStream_t st) {
     if (a.n_experts > MOE_MAX_EXPERTS || a.top_k > MOE_MAX_K || a.top_k < 1 || a.top_k > a.n_experts ||
         a.dim % 64 || a.inter % 64 || a.inter > 64 * MOE_MAX_K * 4)
         return hipErrorInvalidValue;
     hipError_t r = launch_gemv(router, st);
     if (r != hipSuccess) return r;
-    hipLaunchKernelGGL(moe_topk_kernel, dim3(1), dim3(WG), 0, st, a);
-    hipLaunchKernelGGL(moe_gateup_kernel, dim3((unsigned)a.top_k, (unsigned)((a.inter + 3) / 4)), dim3(WG),
-                       (size_t)a.dim * 4, st, a);
-    hipLaunchKernelGGL(moe_down_kernel, dim3((unsigned)((a.dim + 3) / 4)), dim3(WG),
-                       (size_t)a.top_k * a.inter * 4, st, a);
+    if (!gu || !gu->moe_logits) hipLaunchKernelGGL(moe_topk_kernel, dim3(1), dim3(WG), 0, st, a);
+    if (gu) {
+        r = launch_gemv_q_moe(*gu, MOE_ROWS, st);
+        if (r != hipSuccess) return r;
+    } else {
+        hipLaunchKernelGGL(moe_gateup_kernel, dim3((unsigned)a.top_k, (unsigned)((a.inter + 3) / 4)), dim3(WG),
+                           (size_t)a.dim * 4, st, a);
+    }
+    if (dn) {
+        r = launch_gemv_q_moe(*dn, MOE_COLS, st);
+        if (r != hipSuccess) return r;
+    } else {
+        hipLaunchKernelGGL(moe_down_kernel, dim3((unsigned)((a.dim + 3) / 4)), dim3(WG),
+                           (size_t)a.top_k * a.inter * 4, st, a);
+    }
     return hipGetLastError();
 }
 

@@ -73,6 +73,21 @@ struct GemvArgs {
     int32_t *state;
     int32_t wg_base;       // gemv_q_kernel: workgroup index of blockIdx.x 0 (one launch per weight type)
     int32_t tiles_per_wg;  // gemv_q_kernel: most tiles any workgroup takes (sizes its output buffer)
+    // routed experts (launch_gemv_q_moe): moe_ids[moe_k] are the experts chosen on
+    // the device (of moe_n).  Rows mode: virtual row v is row v % moe_blk of expert
+    // ids[v / moe_blk] (seg m.rows = moe_k * moe_blk).  Columns mode: the row is the
+    // concatenation over k of row r of expert ids[k] (moe_blk units each, K =
+    // moe_k * 64 * moe_blk), each expert's part weighted by moe_w[k].
+    const int32_t *moe_ids;
+    const float *moe_w;
+    int32_t moe_k, moe_n, moe_blk;
+    // rows mode with moe_logits set: every workgroup routes itself from the
+    // router logits (softmax, top moe_k, weights renormalized if moe_norm) and
+    // workgroup 0 writes the ids and weights to moe_ids_out / moe_w_out
+    const float *moe_logits;
+    int32_t *moe_ids_out;
+    float *moe_w_out;
+    int32_t moe_norm;
 };
 
 // Device state of the token loop (int32 x 8):
@@ -113,6 +128,12 @@ bool plan_gemv(GemvArgs &a);
 bool gemv_q_supported(const GemvArgs &a);
 void plan_gemv_q(GemvArgs &a);
 hipError_t launch_gemv_q(const GemvArgs &a, hipStream_t st);
+// routed-expert GEMV (moe = MOE_ROWS: SwiGLU over the chosen experts' gate/up
+// rows; MOE_COLS: down over the chosen experts' rows, weighted); a planned by
+// plan_gemv_q; false from gemv_q_moe_supported means the generic kernels
+enum { MOE_ROWS = 1, MOE_COLS = 2 };
+bool gemv_q_moe_supported(const GemvArgs &a, int moe);
+hipError_t launch_gemv_q_moe(const GemvArgs &a, int moe, hipStream_t st);
 
 // gemm.hip: batched projection c[t][r] = sum_k f16(deq(W))[r][k] x[t][k]
 bool gemm_supported(const DMat &m);
@@ -193,8 +214,10 @@ struct MoeArgs {
     float *y;                  // [dim]
     int32_t n_experts, top_k, dim, inter, norm_topk;
 };
-// router: a planned GEMV writing `logits`
-hipError_t launch_moe(const MoeArgs &a, const GemvArgs &router, hipStream_t st);
+// router: a planned GEMV writing `logits`; gu / dn: planned routed-expert
+// GEMVs (launch_gemv_q_moe) for gate/up and down, or null for the generic kernels
+hipError_t launch_moe(const MoeArgs &a, const GemvArgs &router, const GemvArgs *gu, const GemvArgs *dn,
+                      hipStream_t st);
 
 // kernels.hip: x[t] = dequant(emb[tokens[t]]) for n tokens
 hipError_t launch_embed_rows(const DMat &emb, const int32_t *tokens, int n, float *x, hipStream_t st);

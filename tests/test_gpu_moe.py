@@ -30,15 +30,21 @@ def test_moe_vs_oracle(E, k, dim, inter, etype, norm):
     assert err <= 1e-4, err
 
 
-def test_moe_ties():
+@pytest.mark.parametrize("dim,inter", [(128, 64), (256, 256)])
+def test_moe_ties(dim, inter):
+    """Equal router rows 5 and 2: rank order puts the lower id first.  128/64
+    runs the generic kernels (moe_topk_kernel), 256/256 the routing inside the
+    gate/up GEMV and the columns-mode down GEMV."""
     rng = np.random.default_rng(3)
-    E, k, dim, inter = 8, 3, 128, 64
+    E, k = 8, 3
     rb, gb, ub, db = make_moe(rng, E, dim, inter, 8, tie=(5, 2))
     x = np.ones(dim, np.float32)
     y, ids, w = moe.moe_ffn(E, k, dim, inter, 0, 0, rb, 8, gb, ub, db, x)
     assert list(ids[:2]) == [2, 5]
-    ry, rids, _ = refcpu.moe_ffn(E, k, dim, inter, 0, 0, rb, 8, gb, ub, db, x)
+    ry, rids, rw = refcpu.moe_ffn(E, k, dim, inter, 0, 0, rb, 8, gb, ub, db, x)
     assert np.array_equal(ids, rids)
+    assert np.allclose(w, rw, rtol=1e-5, atol=0)
+    assert np.max(np.abs(np.float64(y) - ry)) / np.max(np.abs(ry)) <= 1e-4
 
 
 def test_moe_rejects_bad_dims():
