@@ -270,7 +270,7 @@ def deltanet_step(iters=200, cpu=True):
     byts = 2 * n_vh * hk * hv * 4 + 2 * cd * (kern - 1) * 4 + cd * kern * 4 + (cd + 2 * vd + 2 * n_vh) * 4
     out = {"shape": "n_k_heads 16, n_v_heads 32, head dims 128, conv kernel 4", "avg_us": round(us, 3),
            "state_copies": ncopy, "bytes": byts, "GBps": round(byts / us / 1e3, 1), "frac_hbm_peak": round(byts / us / 1e3 / PEAK_HBM_GBPS, 4),
-           "kernels": "dn_conv_kernel + dn_delta_kernel"}
+           "kernels": "dn_step_kernel (conv, gates and delta rule in one launch)"}
     if cpu:
         rc = _oracle()
         n = 20

@@ -18,7 +18,8 @@
 //   (coalesced: consecutive threads, consecutive columns); the two column
 //   sums S^T k and S^T q are reduced over the row groups through LDS.
 // The state is HBM-bound: 4 * head_k_dim * head_v_dim bytes read and written
-// per value head and token.
+// per value head and token.  dn_step_kernel does both in one launch when the
+// value heads are one or two per k head (below).
 
 #include "device_common.h"
 
@@ -149,8 +150,141 @@ __global__ __launch_bounds__(1024) void dn_delta_kernel(DnArgs a) {
     }
 }
 
+// The whole step in one launch: one workgroup per k head kh and its G value
+// heads vh = kh + g n_kh (vh % n_kh == kh), so that the workgroup owns the
+// conv windows of every channel it reads (its q and k channels and its value
+// heads' v channels) and can slide them without racing another workgroup.
+// The conv and the gates are computed as in dn_conv_kernel / dn_delta_kernel;
+// then the G heads' states are updated side by side, 1024 / G threads each
+// (thread owns column j over R = HK G / 8 rows).
+template <int HK, int HV, int G>
+__global__ __launch_bounds__(1024) void dn_step_kernel(DnArgs a) {
+#pragma clang fp contract(off)
+    constexpr int NT = 1024, TPH = NT / G, RG = TPH / HV, R = HK / RG;
+    static_assert(TPH % HV == 0 && HK % RG == 0 && 2 * HK + G * HV <= NT, "head shape");
+    __shared__ float qn[HK], kn[HK], vv[G][HV];
+    __shared__ float part[2][G][RG][HV];
+    __shared__ float red[NT / WAVE];
+    __shared__ float sc[2 + 2 * G];
+    const int kh = blockIdx.x, t = threadIdx.x, lane = t & (WAVE - 1), wave = t / WAVE;
+    const int key_dim = a.n_kh * HK, km1 = a.kernel - 1;
+    // this thread's part of its head's state, requested first: the loads
+    // overlap the conv and the gates, which do not depend on them
+    const int g = t / TPH, tt = t % TPH, j = tt % HV, rg = tt / HV, i0 = rg * R;
+    const int vh = kh + g * a.n_kh;
+    float *S = a.state + (size_t)vh * HK * HV;
+    float s[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) s[r] = S[(size_t)(i0 + r) * HV + j];
+    // conv1d_step + silu of the workgroup's channels (ops.odin:97-116)
+    if (t < 2 * HK + G * HV) {
+        int c;
+        if (t < HK) c = kh * HK + t;
+        else if (t < 2 * HK) c = key_dim + kh * HK + (t - HK);
+        else c = 2 * key_dim + (kh + ((t - 2 * HK) / HV) * a.n_kh) * HV + (t - 2 * HK) % HV;
+        const float *w = a.conv_w + (size_t)c * a.kernel;
+        float *st = a.conv_state + (size_t)c * km1;
+        const float x = a.qkv[c];
+        float acc = w[km1] * x;
+        for (int k = 0; k < km1; k++) acc += w[k] * st[k];
+        const float o = silu_ref(acc);
+        for (int k = 0; k < km1 - 1; k++) st[k] = st[k + 1];
+        if (km1 > 0) st[km1 - 1] = x;
+        if (t < HK) qn[t] = o;
+        else if (t < 2 * HK) kn[t - HK] = o;
+        else vv[(t - 2 * HK) / HV][(t - 2 * HK) % HV] = o;
+    }
+    __syncthreads();
+    // l2norm of q and k (ops.odin:27-37), the gates of the G heads
+    float sq = 0.f, sk = 0.f;
+    if (t < HK) {
+        sq = qn[t] * qn[t];
+        sk = kn[t] * kn[t];
+    }
+    sq = wave_sum(sq);
+    sk = wave_sum(sk);
+    if (lane == 0) red[wave] = sq;
+    __syncthreads();
+    if (t == 0) {
+        float s = 0.f;
+        for (int w = 0; w < (HK + WAVE - 1) / WAVE; w++) s += red[w];
+        sc[0] = s;
+    }
+    __syncthreads();
+    if (lane == 0) red[wave] = sk;
+    __syncthreads();
+    if (t == 0) {
+        float s = 0.f;
+        for (int w = 0; w < (HK + WAVE - 1) / WAVE; w++) s += red[w];
+        sc[1] = s;
+    }
+    if (t < G) {
+        const int vh = kh + t * a.n_kh;
+        sc[2 + t] = sigmoid_ref(a.b[vh]);
+        sc[2 + G + t] = expf(a.a_decay[vh] * softplus_ref(a.a[vh] + a.dt_bias[vh]));
+    }
+    __syncthreads();
+    if (t < HK) {
+        const float iq = 1.0f / fmaxf(sqrtf(sc[0]), 1e-6f), ik = 1.0f / fmaxf(sqrtf(sc[1]), 1e-6f);
+        qn[t] = qn[t] * iq * (1.0f / sqrtf((float)HK));
+        kn[t] = kn[t] * ik;
+    }
+    __syncthreads();
+    // delta rule of head g on its state (forward.odin:193-209)
+    const float beta = sc[2 + g], decay = sc[2 + G + g];
+    float kv = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        s[r] = s[r] * decay;
+        kv += s[r] * kn[i0 + r];
+    }
+    part[0][g][rg][j] = kv;
+    __syncthreads();
+    float kvmem = 0.f;
+#pragma unroll
+    for (int q = 0; q < RG; q++) kvmem += part[0][g][q][j];
+    const float delta = (vv[g][j] - kvmem) * beta;
+    float o = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        s[r] += kn[i0 + r] * delta;
+        S[(size_t)(i0 + r) * HV + j] = s[r];
+        o += s[r] * qn[i0 + r];
+    }
+    part[1][g][rg][j] = o;
+    __syncthreads();
+    // gated RMSNorm over each head's outputs (forward.odin:211-218)
+    float oj = 0.f;
+    if (rg == 0) {
+#pragma unroll
+        for (int q = 0; q < RG; q++) oj += part[1][g][q][j];
+    }
+    float ss = rg == 0 ? oj * oj : 0.f;
+    ss = wave_sum(ss);
+    __syncthreads();
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    if (rg == 0) {
+        float tot = 0.f;
+        const int w0 = g * TPH / WAVE;
+        for (int w = 0; w < (HV + WAVE - 1) / WAVE; w++) tot += red[w0 + w];
+        const float inv = 1.0f / sqrtf(tot / (float)HV + a.eps);
+        const float z = a.z[vh * HV + j];
+        a.out[vh * HV + j] = a.norm_w[j] * (inv * oj) * silu_ref(z);
+    }
+}
+
 hipError_t launch_deltanet(const DnArgs &a, hipStream_t st) {
     if (a.hk != 128 || a.hv != 128 || a.kernel < 1 || a.n_kh <= 0 || a.n_vh <= 0) return hipErrorInvalidValue;
+    if (a.n_vh == a.n_kh) {
+        hipLaunchKernelGGL((dn_step_kernel<128, 128, 1>), dim3((unsigned)a.n_kh), dim3(1024), 0, st, a);
+        return hipGetLastError();
+    }
+    if (a.n_vh == 2 * a.n_kh) {
+        hipLaunchKernelGGL((dn_step_kernel<128, 128, 2>), dim3((unsigned)a.n_kh), dim3(1024), 0, st, a);
+        return hipGetLastError();
+    }
+    // other head ratios: the conv pass, then one workgroup per value head
     const int conv_dim = 2 * a.n_kh * a.hk + a.n_vh * a.hv;
     hipLaunchKernelGGL(dn_conv_kernel, dim3((unsigned)((conv_dim + WG - 1) / WG)), dim3(WG), 0, st, a);
     hipLaunchKernelGGL((dn_delta_kernel<128, 128>), dim3((unsigned)a.n_vh), dim3(1024), 0, st, a);
