@@ -532,6 +532,10 @@ static __device__ __forceinline__ void moe_route(const GemvArgs &a, float lg, in
     for (int w = 0; w < GNW; w++) tot += rsum[w];
     const float pi = e / tot;
     if (t < n) p[t] = pi;
+    if (t < a.moe_k) {  // defined ids even if NaN logits leave a rank unfilled
+        sid[t] = 0;
+        sw[t] = 0.f;
+    }
     __syncthreads();
     if (t < n) {
         int rank = 0, j = 0;
@@ -551,7 +555,7 @@ static __device__ __forceinline__ void moe_route(const GemvArgs &a, float lg, in
     float s = 0.f;
     for (int k = 0; k < a.moe_k; k++) s += sw[k];  // in rank order, as the sequential selection
     if (lane < a.moe_k) {
-        idv = sid[lane];
+        idv = min(max(sid[lane], 0), n - 1);
         wv = a.moe_norm ? sw[lane] / s : sw[lane];
         if (wg == 0 && wave == 0) {
             a.moe_ids_out[lane] = idv;

@@ -479,6 +479,7 @@ __global__ __launch_bounds__(WG) void moe_topk_kernel(MoeArgs a) {
 #pragma unroll
     for (int w = 0; w < WG / WAVE; w++) tot += red[w];
     for (int i = t; i < n; i += WG) p[i] = p[i] / tot;
+    if (t < a.top_k) sel[t] = 0.f;  // defined weights even if NaN logits leave a rank unfilled
     __syncthreads();
     for (int i = t; i < n; i += WG) {
         const float pi = p[i];
@@ -509,7 +510,8 @@ __device__ __forceinline__ void moe_stage_x(const float *x, int n, float4 *x4) {
 __global__ __launch_bounds__(WG) void moe_gateup_kernel(MoeArgs a) {
 #pragma clang fp contract(off)
     extern __shared__ float4 smem[];
-    const int k = blockIdx.x, e = a.ids[k], lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    const int k = blockIdx.x, e = min(max(a.ids[k], 0), a.n_experts - 1);  // ids come from the device
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
     moe_stage_x(a.x, a.dim, smem);
     __syncthreads();
     const int r = (int)blockIdx.y * 4 + wave;
@@ -549,7 +551,7 @@ __global__ __launch_bounds__(WG) void moe_down_kernel(MoeArgs a) {
         const int np = min(P - p0, NB);
         for (int j = lane; j < np; j += WAVE) {
             const int pr = p0 + j, k = pr / U, u = pr % U;
-            const DMat d = sub_rows(a.down, a.ids[k] * a.dim, a.dim);
+            const DMat d = sub_rows(a.down, min(max(a.ids[k], 0), a.n_experts - 1) * a.dim, a.dim);
             part[wave][j] = dot_unit(d, r, u, XView{smem + (size_t)k * X4, nullptr});
         }
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
