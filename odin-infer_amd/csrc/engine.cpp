@@ -1038,10 +1038,18 @@ int prefill_chunk(oi_engine *e, const int32_t *tokens, int T, int pos) {
                                (int)c.n_kv_heads, hd, st));
         HIP_TRY(launch_gemm_parts(L.wo, e->pf_xb, T, P[0], PB[0], &s0, st));
         HIP_TRY(launch_pf_addnorm16(e->pf_x, P[0], s0, L.ffn_norm, eps, D, T, e->pf_xb, st));
-        HIP_TRY(launch_gemm_parts(L.w1, e->pf_xb, T, P[0], PB[0], &s0, st));
-        HIP_TRY(launch_gemm_parts(L.w3, e->pf_xb, T, P[1], PB[1], &s1, st));
-        HIP_TRY(launch_pf_swiglu16(P[0], s0, P[1], s1, (int64_t)T * H, e->pf_xb, st));
-        HIP_TRY(launch_gemm_parts(L.w2, e->pf_xb, T, P[0], PB[0], &s0, st));
+        if (gemm_swiglu_supported(L.w1, L.w3, T)) {
+            // gate and up in one pass, SwiGLU in its epilogue; h goes to the up
+            // partials' buffer (unsplit, it holds T x H floats)
+            uint16_t *hb = (uint16_t *)P[1];
+            HIP_TRY(launch_gemm_swiglu(L.w1, L.w3, e->pf_xb, T, hb, st));
+            HIP_TRY(launch_gemm_parts(L.w2, hb, T, P[0], PB[0], &s0, st));
+        } else {
+            HIP_TRY(launch_gemm_parts(L.w1, e->pf_xb, T, P[0], PB[0], &s0, st));
+            HIP_TRY(launch_gemm_parts(L.w3, e->pf_xb, T, P[1], PB[1], &s1, st));
+            HIP_TRY(launch_pf_swiglu16(P[0], s0, P[1], s1, (int64_t)T * H, e->pf_xb, st));
+            HIP_TRY(launch_gemm_parts(L.w2, e->pf_xb, T, P[0], PB[0], &s0, st));
+        }
         if (l + 1 < e->layers.size())
             HIP_TRY(launch_pf_addnorm16(e->pf_x, P[0], s0, e->layers[l + 1].attn_norm, eps, D, T, e->pf_xb, st));
         else

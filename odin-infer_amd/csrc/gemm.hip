@@ -57,6 +57,8 @@ struct GemmArgs {
     const uint16_t *x;  // [n][K] f16
     float *c;           // [n][M], or [split][n][M] partial products when K is split
     int32_t n;
+    DMat m2;            // NP == 2: the up matrix (m is gate), same type and shape
+    uint16_t *h;        // NP == 2: [n][M] f16 silu(gate x) * (up x)
 };
 
 // f32 -> f16 (RNE) of values already rounded to f32 (f2h: the conversion is
@@ -262,14 +264,22 @@ struct GQ80 {
 // run GM_WD - 1 chunks ahead in a register ring.  With more than one K slice
 // (split > 1) slice z writes its partial products to c + z n M; gemm_reduce
 // sums them in slice order.
-template <class G>
+//
+// NP == 2 (gate and up of the FFN, one K slice): both matrices' rows are
+// computed against the same staged activations, each B operand read from LDS
+// feeding both products, and the epilogue writes the f16 SwiGLU of the pair
+// (infer/forward.odin:188-193: v *= 1/(1+exp(-v)); v *= up; then the half
+// staging of the next projection's input).
+template <class G, int NP = 1>
 __global__ __launch_bounds__(GM_THREADS) void gemm_q_kernel(GemmArgs a, int cps) {
     __shared__ __attribute__((aligned(16))) u32x4 xs[2][GM_XV];
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
     const int q = lane >> 4, li = lane & 15;
     const int M = a.m.rows, K = a.m.cols;
     const int rbase = (int)blockIdx.x * GM_ROWS + 16 * GM_RT * wave;
-    const typename G::Src src = G::src(a.m);
+    typename G::Src src[NP];
+    src[0] = G::src(a.m);
+    if (NP == 2) src[NP - 1] = G::src(a.m2);  // same shape: the same lane offsets
     typename G::Off off[GM_RT];
 #pragma unroll
     for (int rt = 0; rt < GM_RT; rt++) off[rt] = G::off(a.m, min(rbase + 16 * rt + li, M - 1), q);  // rows past M: not stored
@@ -297,17 +307,22 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_q_kernel(GemmArgs a, int cps)
         }
     };
 
-    f32x4v acc[GM_RT][4];
+    f32x4v acc[NP][GM_RT][4];
 #pragma unroll
-    for (int rt = 0; rt < GM_RT; rt++)
+    for (int mp = 0; mp < NP; mp++)
 #pragma unroll
-        for (int t = 0; t < 4; t++) acc[rt][t] = f32x4v{0.f, 0.f, 0.f, 0.f};
+        for (int rt = 0; rt < GM_RT; rt++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) acc[mp][rt][t] = f32x4v{0.f, 0.f, 0.f, 0.f};
     // unconditional loads: chunks past the slice re-read its first, unused
-    typename G::Raw ring[GM_WD][GM_RT];
+    typename G::Raw ring[GM_WD][NP][GM_RT];
 #pragma unroll
     for (int r = 0; r < GM_WD - 1; r++)
 #pragma unroll
-        for (int rt = 0; rt < GM_RT; rt++) G::raw(src, off[rt], c0 + r < c1 ? c0 + r : c0, ring[r][rt]);
+        for (int mp = 0; mp < NP; mp++)
+#pragma unroll
+            for (int rt = 0; rt < GM_RT; rt++)
+                G::raw(src[mp], off[rt], c0 + r < c1 ? c0 + r : c0, ring[r][mp][rt]);
     if (c0 < c1) xfetch(c0);
     for (int cb = c0; cb < c1; cb += GM_WD) {
 #pragma unroll
@@ -316,14 +331,18 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_q_kernel(GemmArgs a, int cps)
             if (c >= c1) break;
             const int cn = c + GM_WD - 1 < c1 ? c + GM_WD - 1 : c0;
 #pragma unroll
-            for (int rt = 0; rt < GM_RT; rt++) G::raw(src, off[rt], cn, ring[(r + GM_WD - 1) % GM_WD][rt]);
+            for (int mp = 0; mp < NP; mp++)
+#pragma unroll
+                for (int rt = 0; rt < GM_RT; rt++) G::raw(src[mp], off[rt], cn, ring[(r + GM_WD - 1) % GM_WD][mp][rt]);
             const int buf = (c - c0) & 1;
             xstore(buf);
             if (c + 1 < c1) xfetch(c + 1);
             __syncthreads();  // chunk c staged; every wave is done with chunk c - 2's buffer
-            typename G::Pre pre[GM_RT];
+            typename G::Pre pre[NP][GM_RT];
 #pragma unroll
-            for (int rt = 0; rt < GM_RT; rt++) pre[rt] = G::pre(ring[r][rt], q);
+            for (int mp = 0; mp < NP; mp++)
+#pragma unroll
+                for (int rt = 0; rt < GM_RT; rt++) pre[mp][rt] = G::pre(ring[r][mp][rt], q);
 #pragma unroll
             for (int st = 0; st < 8; st++) {
                 const int o = G::omap(q, st);
@@ -331,16 +350,48 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_q_kernel(GemmArgs a, int cps)
 #pragma unroll
                 for (int t = 0; t < 4; t++) B[t] = __builtin_bit_cast(h8, xs[buf][o * GM_TOK + ((16 * t + li) ^ (o & 7))]);
 #pragma unroll
-                for (int rt = 0; rt < GM_RT; rt++) {
-                    const h8 A = G::deq(ring[r][rt], pre[rt], st);
+                for (int mp = 0; mp < NP; mp++)
 #pragma unroll
-                    for (int t = 0; t < 4; t++)
-                        acc[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[t], acc[rt][t], 0, 0, 0);
-                }
+                    for (int rt = 0; rt < GM_RT; rt++) {
+                        const h8 A = G::deq(ring[r][mp][rt], pre[mp][rt], st);
+#pragma unroll
+                        for (int t = 0; t < 4; t++)
+                            acc[mp][rt][t] =
+                                __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[t], acc[mp][rt][t], 0, 0, 0);
+                    }
             }
         }
     }
     // D of tile (rt, t): lane (j, g) holds rows 4g .. 4g+3 of column (token) j
+    if (NP == 2) {
+#pragma unroll
+        for (int rt = 0; rt < GM_RT; rt++) {
+            const int r0 = rbase + 16 * rt + 4 * q;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int tk = t0 + 16 * t + li;
+                if (tk >= a.n) continue;
+                uint16_t hv[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+#pragma clang fp contract(off)
+                    float v = acc[0][rt][t][e];
+                    v *= 1.0f / (1.0f + expf(-v));
+                    v *= acc[NP - 1][rt][t][e];
+                    hv[e] = f2h(v);
+                }
+                uint16_t *dst = a.h + (size_t)tk * M + r0;
+                if (r0 + 3 < M && (M & 3) == 0) {
+                    *(u32x2 *)dst = u32x2{(uint32_t)hv[0] | ((uint32_t)hv[1] << 16), (uint32_t)hv[2] | ((uint32_t)hv[3] << 16)};
+                    continue;
+                }
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (r0 + e < M) dst[e] = hv[e];
+            }
+        }
+        return;
+    }
     float *out = a.c + (size_t)blockIdx.z * a.n * M;
 #pragma unroll
     for (int rt = 0; rt < GM_RT; rt++) {
@@ -351,12 +402,12 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_q_kernel(GemmArgs a, int cps)
             if (tk >= a.n) continue;
             float *dst = out + (size_t)tk * M + r0;
             if (r0 + 3 < M && (M & 3) == 0) {
-                *(f32x4v *)dst = acc[rt][t];
+                *(f32x4v *)dst = acc[0][rt][t];
                 continue;
             }
 #pragma unroll
             for (int e = 0; e < 4; e++)
-                if (r0 + e < M) dst[e] = acc[rt][t][e];
+                if (r0 + e < M) dst[e] = acc[0][rt][t][e];
         }
     }
 }
@@ -406,7 +457,7 @@ hipError_t launch_gemm(const DMat &m, const uint16_t *x, int32_t n, float *c, fl
     const int nchunk = m.cols / GM_KC;
     const int split = gemm_split(m, n, part ? part_bytes : 0);
     const int cps = (nchunk + split - 1) / split;
-    GemmArgs a{m, x, split > 1 ? part : c, n};
+    GemmArgs a{m, x, split > 1 ? part : c, n, DMat{}, nullptr};
     dim3 grid((m.rows + GM_ROWS - 1) / GM_ROWS, (n + GM_TOK - 1) / GM_TOK, split), block(GM_THREADS);
     switch (m.type) {
     case T_Q4_K: hipLaunchKernelGGL(gemm_q_kernel<GQ4K>, grid, block, 0, st, a, cps); break;
@@ -421,13 +472,34 @@ hipError_t launch_gemm(const DMat &m, const uint16_t *x, int32_t n, float *c, fl
     return hipGetLastError();
 }
 
+// h[t][r] = f16(silu(gate x)[t][r] * (up x)[t][r]) in one pass over K: only
+// when the projection needs no K split (gemm_split == 1 for this n)
+bool gemm_swiglu_supported(const DMat &gate, const DMat &up, int32_t n) {
+    return gemm_supported(gate) && up.type == gate.type && up.rows == gate.rows && up.cols == gate.cols && n > 0 &&
+           gemm_split(gate, n, SIZE_MAX) == 1;
+}
+
+hipError_t launch_gemm_swiglu(const DMat &gate, const DMat &up, const uint16_t *x, int32_t n, uint16_t *h,
+                              hipStream_t st) {
+    if (!gemm_swiglu_supported(gate, up, n) || !h) return hipErrorInvalidValue;
+    GemmArgs a{gate, x, nullptr, n, up, h};
+    dim3 grid((gate.rows + GM_ROWS - 1) / GM_ROWS, (n + GM_TOK - 1) / GM_TOK, 1), block(GM_THREADS);
+    const int cps = gate.cols / GM_KC;
+    switch (gate.type) {
+    case T_Q4_K: hipLaunchKernelGGL((gemm_q_kernel<GQ4K, 2>), grid, block, 0, st, a, cps); break;
+    case T_Q6_K: hipLaunchKernelGGL((gemm_q_kernel<GQ6K, 2>), grid, block, 0, st, a, cps); break;
+    default: hipLaunchKernelGGL((gemm_q_kernel<GQ80, 2>), grid, block, 0, st, a, cps); break;
+    }
+    return hipGetLastError();
+}
+
 hipError_t launch_gemm_parts(const DMat &m, const uint16_t *x, int32_t n, float *part, size_t part_bytes, int *split,
                              hipStream_t st) {
     if (!gemm_supported(m) || n <= 0 || !part || part_bytes < (size_t)n * m.rows * 4) return hipErrorInvalidValue;
     const int nchunk = m.cols / GM_KC;
     *split = gemm_split(m, n, part_bytes);
     const int cps = (nchunk + *split - 1) / *split;
-    GemmArgs a{m, x, part, n};
+    GemmArgs a{m, x, part, n, DMat{}, nullptr};
     dim3 grid((m.rows + GM_ROWS - 1) / GM_ROWS, (n + GM_TOK - 1) / GM_TOK, *split), block(GM_THREADS);
     switch (m.type) {
     case T_Q4_K: hipLaunchKernelGGL(gemm_q_kernel<GQ4K>, grid, block, 0, st, a, cps); break;

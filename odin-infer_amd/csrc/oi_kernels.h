@@ -146,6 +146,10 @@ hipError_t launch_gemm(const DMat &m, const uint16_t *x, int32_t n, float *c, fl
 
 // gemm.hip, for consumers that sum the K slices themselves: the partial
 // products go to part ([split][n][rows]; with split 1 the product itself)
+// gemm.hip: gate and up in one pass with the SwiGLU epilogue, h [n][rows] f16
+bool gemm_swiglu_supported(const DMat &gate, const DMat &up, int32_t n);
+hipError_t launch_gemm_swiglu(const DMat &gate, const DMat &up, const uint16_t *x, int32_t n, uint16_t *h,
+                              hipStream_t st);
 hipError_t launch_gemm_parts(const DMat &m, const uint16_t *x, int32_t n, float *part, size_t part_bytes, int *split,
                              hipStream_t st);
 
