@@ -470,25 +470,30 @@ def moe_step(iters=100, cpu=True):
     return out
 
 
-def measure_prefill(e, cfg, n, reps=3):
+def measure_prefill(e, cfg, n, reps=7):
     """Batched prefill of an n-token prompt at position 0 (engine_forward_batch,
     synchronous): host wall clock per call after one warm call (which also
-    allocates the prefill buffers)."""
+    allocates the prefill buffers); the median of `reps` calls (single calls
+    vary by several percent), with the fastest and slowest."""
     import numpy as np
     from oi import infer
     ptoks = np.random.default_rng(99).integers(0, cfg.vocab_size, size=n).astype(np.int32)
     infer.engine_forward_batch(e, ptoks, 0)
-    t0 = time.perf_counter()
+    times = []
     for _ in range(reps):
+        t0 = time.perf_counter()
         infer.engine_forward_batch(e, ptoks, 0)
-    pel = (time.perf_counter() - t0) / reps
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    pel = times[len(times) // 2]
     D, QD, KVD, H = cfg.dim, cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim, cfg.hidden_dim
     proj_flop = 2.0 * n * cfg.n_layers * (2 * D * QD + 2 * D * KVD + 3 * D * H)
     log("prefill: %d tokens in %.2f ms -> %.0f tok/s" % (n, 1000 * pel, n / pel))
     return {"tokens": n, "tok_s": round(n / pel, 1), "ms": round(1000 * pel, 3),
+            "ms_min": round(1000 * times[0], 3), "ms_max": round(1000 * times[-1], 3), "calls": reps,
             "projection_TFLOPs": round(proj_flop / pel / 1e12, 1),
-            "note": "host wall clock around oi_engine_prefill (synchronous), chunks of <=512 tokens; "
-                    "the prompt overwrites the cache from position 0 after the decode measurement"}
+            "note": "host wall clock around oi_engine_prefill (synchronous), median of the calls, chunks of "
+                    "<=512 tokens; the prompt overwrites the cache from position 0 after the decode measurement"}
 
 
 def main():
