@@ -22,6 +22,10 @@
 // Dequantization follows ggml/quant.odin exactly (separately rounded products,
 // (d*sc)*q for Q6_K), then rounds to f16 (RNE), as the reference's staging.
 //
+// The FFN's gate and up projections can run as one pass (gemm_q_kernel<G, 2>,
+// launch_gemm_swiglu) that writes the f16 SwiGLU of the pair instead of two
+// f32 products.
+//
 // Operand layout of v_mfma_f32_16x16x32_f16 (per lane l, 8 halves each):
 //   A[i][k]: i = l % 16, k = 8 (l / 16) + e;  B[k][j]: j = l % 16, k = 8 (l / 16) + e
 //   D[i][j] (4 floats): j = l % 16, i = 4 (l / 16) + e.
@@ -382,7 +386,8 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_q_kernel(GemmArgs a, int cps)
                 }
                 uint16_t *dst = a.h + (size_t)tk * M + r0;
                 if (r0 + 3 < M && (M & 3) == 0) {
-                    *(u32x2 *)dst = u32x2{(uint32_t)hv[0] | ((uint32_t)hv[1] << 16), (uint32_t)hv[2] | ((uint32_t)hv[3] << 16)};
+                    *(u32x2 *)dst = u32x2{(uint32_t)hv[0] | ((uint32_t)hv[1] << 16),
+                                          (uint32_t)hv[2] | ((uint32_t)hv[3] << 16)};
                     continue;
                 }
 #pragma unroll
