@@ -129,8 +129,7 @@ enum {
     OI_KERNEL_GATEUP = 3,  /* RMSNorm + gate/up GEMV + SwiGLU */
     OI_KERNEL_DOWN = 4,    /* down GEMV + residual */
     OI_KERNEL_OUTPUT = 5,  /* final RMSNorm + vocab GEMV + greedy argmax */
-    OI_KERNEL_TOKEN = 6    /* one whole token step (the persistent token kernel when the
-                              engine uses it, else the multi-kernel graph) */
+    OI_KERNEL_TOKEN = 6    /* one whole token step (the captured graph) */
 };
 
 /* Launch one kernel of the token loop `iters` times on the engine's stream,

@@ -37,12 +37,12 @@ def build(verbose=False):
     os.makedirs(BUILD, exist_ok=True)
     jobs = []
     objs = []
-    for src in ["kernels.hip", "gemv.hip", "attn.hip", "stream.hip", "gemm.hip", "prefill.hip", "deltanet.hip", "qwen35_attn.hip"]:
+    for src in ["kernels.hip", "gemv.hip", "attn.hip", "gemm.hip", "prefill.hip", "deltanet.hip", "qwen35_attn.hip"]:
         obj = os.path.join(BUILD, src + ".o")
         objs.append(obj)
         jobs.append([HIPCC, "--offload-arch=" + ARCH, *COMMON, *DEVICE_FLAGS, "-x", "hip", "-c",
                      os.path.join(CSRC, src), "-o", obj])
-    for src in ["engine.cpp", "gguf.cpp", "stream_plan.cpp"]:
+    for src in ["engine.cpp", "gguf.cpp"]:
         obj = os.path.join(BUILD, src + ".o")
         objs.append(obj)
         jobs.append([HIPCC, *COMMON, "-D__HIP_PLATFORM_AMD__", "-c", os.path.join(CSRC, src), "-o", obj])

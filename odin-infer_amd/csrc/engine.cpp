@@ -23,10 +23,7 @@
 
 #include "gguf.h"
 #include "oi.h"
-#include "oi_debug.h"
 #include "oi_kernels.h"
-#include "stream.h"
-#include "stream_plan.h"
 
 using namespace oi;
 
@@ -250,11 +247,6 @@ struct oi_engine {
     hipGraphExec_t gexec = nullptr;
     int last_pos = 0;
     size_t weight_bytes = 0;
-    // persistent token kernel (stream.hip); the multi-kernel path above is
-    // used when it cannot run the model
-    bool use_stream = false;
-    StreamArgs sa{};
-    int64_t stream_seq = 0;   // launches so far (the device keeps its own copy)
     // batched prefill buffers (allocated on the first prefill): token ids,
     // residual [T][dim], rotated q [T][q_dim], f16 projection inputs
     // [T][max(dim, q_dim, hidden)], and three buffers of partial products
@@ -263,6 +255,7 @@ struct oi_engine {
     float *pf_x = nullptr, *pf_q = nullptr, *pf_p[3] = {nullptr, nullptr, nullptr};
     size_t pf_pbytes[3] = {0, 0, 0};
     uint16_t *pf_xb = nullptr;
+    bool pf_fused = true;  // gate/up GEMM with the SwiGLU epilogue where it applies (OI_PREFILL_UNFUSED=1: off)
 };
 
 namespace {
@@ -283,7 +276,7 @@ int enqueue_token(oi_engine *e) {
 }
 
 int ensure_graph(oi_engine *e) {
-    if (e->use_stream || e->gexec || !e->use_graph) return OI_OK;
+    if (e->gexec || !e->use_graph) return OI_OK;
     HIP_TRY(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
     int rc = enqueue_token(e);
     hipGraph_t g = nullptr;
@@ -305,24 +298,9 @@ int set_state(oi_engine *e, int32_t token, int32_t pos, int32_t cap) {
     return OI_OK;
 }
 
-// A barrier timeout inside the token kernel leaves ST_ERR set; the launch
-// sequence of the grid barrier is then unreliable and the engine is unusable.
-int check_stream_error(oi_engine *e) {
-    if (!e->use_stream) return OI_OK;
-    int32_t err = 0;
-    HIP_TRY(hipMemcpy(&err, e->state + ST_ERR, 4, hipMemcpyDeviceToHost));
-    if (err) return fail(OI_E_DEVICE, "token kernel: grid barrier timed out (engine unusable)");
-    return OI_OK;
-}
-
-// One token step: the persistent token kernel; or the captured graph of the
-// multi-kernel path, or its launches issued directly (OI_NO_GRAPH=1, e.g.
-// under tools that do not follow graph capture).
+// One token step: the captured graph, or its launches issued directly
+// (OI_NO_GRAPH=1, e.g. under tools that do not follow graph capture).
 int run_token(oi_engine *e) {
-    if (e->use_stream) {
-        HIP_TRY(launch_stream(e->sa, e->stream));
-        return OI_OK;
-    }
     if (e->use_graph) {
         HIP_TRY(hipGraphLaunch(e->gexec, e->stream));
         return OI_OK;
@@ -338,238 +316,6 @@ GemvArgs gemv_args(int mode, int K, const float *x, const float *norm_w, float e
     a.norm_w = norm_w;
     a.eps = eps;
     return a;
-}
-
-
-// ---------------------------------------------------- token kernel plan --
-struct StreamPlanAll {
-    std::vector<PlanKind> plans;
-    std::vector<std::array<int, 4>> layer_plan;
-    int vocab_plan = -1;
-    std::vector<int32_t> wpieces;  // [G * S_NCW] 1 KB pieces of each compute wave's weight stream
-    size_t wstride = 0;            // bytes between consecutive waves' streams
-    int G = 0, rD = 0, rH = 0, rQ = 0, yo = 0;
-    size_t lds = 0;
-};
-
-int plan_index(StreamPlanAll &sp, int kind, const int *types, int nseg, const int *rows, int K, int own,
-               std::string &why) {
-    for (size_t i = 0; i < sp.plans.size(); i++) {
-        const SKind &k = sp.plans[i].kind;
-        bool same = k.K == K && (k.pair != 0) == (kind == SK_GU) && k.nseg == (kind == SK_GU ? 1 : nseg);
-        for (int s = 0; same && s < k.nseg; s++) same = k.seg[s].type == types[s] && k.seg[s].rows == rows[s];
-        if (same && (int)sp.plans[i].wgrows.size() == sp.G && kind != SK_QKV && kind != SK_VOCAB) {
-            // owned-row plans also depend on `own`: compare the first workgroup
-            same = sp.plans[i].wgrows[0].v1 - sp.plans[i].wgrows[0].v0 == std::min(own, rows[0]);
-        }
-        if (same) return (int)i;
-    }
-    PlanKind pk;
-    if (!plan_stream_kind(kind, types, nseg, rows, K, sp.G, own, pk, why)) return -1;
-    sp.yo = std::max(sp.yo, pk.max_wg_rows);
-    sp.plans.push_back(std::move(pk));
-    return (int)sp.plans.size() - 1;
-}
-
-// Can the token kernel run this model on this device?  Fills the plan.
-bool plan_stream_all(GgufFile &g, const oi_config &c, bool tied, int dev, StreamPlanAll &sp, std::string &why) {
-    const int G8 = (int)(c.n_heads / c.n_kv_heads);
-    if (c.head_dim != 128 || G8 > 4) {
-        why = "head_dim 128 and at most 4 query heads per KV head";
-        return false;
-    }
-    int coop = 0, cus = 0, lds_max = 0;
-    hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev);
-    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
-    if (!coop || cus <= 0) {
-        why = "cooperative launch not available";
-        return false;
-    }
-    sp.G = cus;
-    if ((2 * sp.G) % c.n_kv_heads) {
-        why = "KV heads do not divide the attention slots";
-        return false;
-    }
-    const int64_t D = c.dim, H = c.hidden_dim, QD = c.n_heads * c.head_dim, KVD = c.n_kv_heads * c.head_dim;
-    auto own = [&](int64_t n) { return (int)(16 * ((n + 16 * sp.G - 1) / (16 * sp.G))); };
-    sp.rD = own(D);
-    sp.rH = own(H);
-    sp.rQ = own(QD);
-    if (sp.rD > 256 || sp.rH > 256 || sp.rQ > 256) {
-        why = "vectors too long for the workgroup row ownership";
-        return false;
-    }
-    auto ty = [&](const std::string &n) { return (int)g.tensor(n)->kind; };
-    sp.layer_plan.resize((size_t)c.n_layers);
-    for (int64_t l = 0; l < c.n_layers; l++) {
-        const std::string p = "blk." + std::to_string(l) + ".";
-        const int tq[3] = {ty(p + "attn_q.weight"), ty(p + "attn_k.weight"), ty(p + "attn_v.weight")};
-        const int rq[3] = {(int)QD, (int)KVD, (int)KVD};
-        const int to[1] = {ty(p + "attn_output.weight")}, ro[1] = {(int)D};
-        const int tg[2] = {ty(p + "ffn_gate.weight"), ty(p + "ffn_up.weight")}, rg[2] = {(int)H, (int)H};
-        const int td[1] = {ty(p + "ffn_down.weight")}, rd[1] = {(int)D};
-        auto &lp = sp.layer_plan[(size_t)l];
-        if ((lp[SK_QKV] = plan_index(sp, SK_QKV, tq, 3, rq, (int)D, 0, why)) < 0) return false;
-        if ((lp[SK_WO] = plan_index(sp, SK_WO, to, 1, ro, (int)QD, sp.rD, why)) < 0) return false;
-        if ((lp[SK_GU] = plan_index(sp, SK_GU, tg, 2, rg, (int)D, sp.rH, why)) < 0) return false;
-        if ((lp[SK_DOWN] = plan_index(sp, SK_DOWN, td, 1, rd, (int)H, sp.rD, why)) < 0) return false;
-    }
-    const int tv[1] = {ty(tied ? "token_embd.weight" : "output.weight")}, rv[1] = {(int)c.vocab_size};
-    if ((sp.vocab_plan = plan_index(sp, SK_VOCAB, tv, 1, rv, (int)D, 0, why)) < 0) return false;
-    if ((c.seq_len + 63) / 64 > 512) {  // the combine gathers at most 8 x 64 chunks in LDS
-        why = "context longer than 32768 positions";
-        return false;
-    }
-    sp.yo = std::max(sp.yo, std::max(sp.rQ, 16));
-    sp.lds = stream_lds_bytes((int)std::max(D, std::max(H, QD)), sp.yo);
-    if ((int64_t)sp.lds > lds_max) {
-        why = "token kernel needs " + std::to_string(sp.lds) + " bytes of LDS, device has " + std::to_string(lds_max);
-        return false;
-    }
-    const int NW = sp.G * S_NCW;
-    sp.wpieces.assign((size_t)NW, 0);
-    auto add = [&](int pi) {
-        for (int w = 0; w < NW; w++) sp.wpieces[(size_t)w] += sp.plans[(size_t)pi].waves[(size_t)w].npieces;
-    };
-    for (int64_t l = 0; l < c.n_layers; l++)
-        for (int k = 0; k < 4; k++) add(sp.layer_plan[(size_t)l][(size_t)k]);
-    add(sp.vocab_plan);
-    const int32_t most = *std::max_element(sp.wpieces.begin(), sp.wpieces.end());
-    sp.wstride = ((size_t)most * 1024 + 4095) & ~(size_t)4095;
-    return true;
-}
-
-
-template <class T>
-T *upload_table(oi_engine *e, const std::vector<T> &v) {
-    T *d = (T *)e->arena.take(v.size() * sizeof(T));
-    if (!d || hipMemcpyAsync(d, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice, e->stream) != hipSuccess ||
-        hipStreamSynchronize(e->stream) != hipSuccess)
-        return nullptr;
-    return d;
-}
-
-// The compute waves' weight streams, the plan tables and the token kernel's
-// arguments.  Streams are built on the host for blocks of waves at a time
-// (each wave's stages in consumption order) and copied whole.
-int upload_stream(oi_engine *e, GgufFile &g, bool tied, const StreamPlanAll &sp) {
-    const oi_config &c = e->cfg;
-    const int NW = sp.G * S_NCW;
-    uint8_t *wstream = e->arena.take(sp.wstride * (size_t)NW);
-    if (!wstream) return fail(OI_E_NOMEM, "arena exhausted (token kernel weights)");
-    std::vector<SLayer> layers((size_t)c.n_layers);
-    // sources and plan of every stage of a token, in stream order
-    std::vector<std::array<const uint8_t *, 3>> srcs;
-    std::vector<int> plan_of;
-    for (int64_t l = 0; l < c.n_layers; l++) {
-        const std::string p = "blk." + std::to_string(l) + ".";
-        auto d = [&](const char *n) { return (const uint8_t *)g.tensor(p + n)->data; };
-        srcs.push_back({d("attn_q.weight"), d("attn_k.weight"), d("attn_v.weight")});
-        srcs.push_back({d("attn_output.weight"), nullptr, nullptr});
-        srcs.push_back({d("ffn_gate.weight"), d("ffn_up.weight"), nullptr});
-        srcs.push_back({d("ffn_down.weight"), nullptr, nullptr});
-        SLayer &L = layers[(size_t)l];
-        for (int k = 0; k < 4; k++) {
-            L.plan[k] = sp.layer_plan[(size_t)l][(size_t)k];
-            plan_of.push_back(L.plan[k]);
-        }
-        const LayerDev &LD = e->layers[(size_t)l];
-        L.attn_norm = LD.attn_norm;
-        L.ffn_norm = LD.ffn_norm;
-        L.q_norm = LD.q_norm;
-        L.k_norm = LD.k_norm;
-        L.kc = LD.kc;
-        L.vc = LD.vc;
-    }
-    srcs.push_back({(const uint8_t *)g.tensor(tied ? "token_embd.weight" : "output.weight")->data, nullptr, nullptr});
-    plan_of.push_back(sp.vocab_plan);
-    {
-        const int WB = std::max(1, std::min(NW, (int)((size_t)1 << 30) / (int)std::max<size_t>(sp.wstride, 1)));
-        std::vector<uint8_t> host((size_t)WB * sp.wstride);
-        std::vector<uint8_t *> cur((size_t)WB);
-        for (int w0 = 0; w0 < NW; w0 += WB) {
-            const int w1 = std::min(NW, w0 + WB);
-            for (int w = w0; w < w1; w++) cur[(size_t)(w - w0)] = host.data() + (size_t)(w - w0) * sp.wstride;
-            for (size_t i = 0; i < plan_of.size(); i++) {
-                const PlanKind &pk = sp.plans[(size_t)plan_of[i]];
-                repack_stream_kind(pk, srcs[i].data(), w0, w1, cur.data());
-                for (int w = w0; w < w1; w++) cur[(size_t)(w - w0)] += (size_t)pk.waves[(size_t)w].npieces * 1024;
-            }
-            HIP_TRY(hipMemcpyAsync(wstream + (size_t)w0 * sp.wstride, host.data(), (size_t)(w1 - w0) * sp.wstride,
-                                   hipMemcpyHostToDevice, e->stream));
-            HIP_TRY(hipStreamSynchronize(e->stream));
-        }
-    }
-    std::vector<SKind> kinds;
-    std::vector<SWave> waves;
-    std::vector<SWgRows> wgrows;
-    for (const PlanKind &pk : sp.plans) {
-        kinds.push_back(pk.kind);
-        waves.insert(waves.end(), pk.waves.begin(), pk.waves.end());
-        wgrows.insert(wgrows.end(), pk.wgrows.begin(), pk.wgrows.end());
-    }
-    StreamArgs &A = e->sa;
-    A = StreamArgs{};
-    A.layers = upload_table(e, layers);
-    A.kinds = upload_table(e, kinds);
-    A.waves = upload_table(e, waves);
-    A.wgrows = upload_table(e, wgrows);
-    if (!A.layers || !A.kinds || !A.waves || !A.wgrows) return fail(OI_E_DEVICE, "token kernel tables upload failed");
-    const int64_t QD = c.n_heads * c.head_dim;
-    auto qv = [](int64_t K) { return ((size_t)qvec_bytes(K) + 2047) & ~(size_t)1023; };
-    A.xq = e->arena.take(qv(c.dim));
-    A.attq = e->arena.take(qv(QD));
-    A.hbq = e->arena.take(qv(c.hidden_dim));
-    A.ssq = (float *)e->arena.take((size_t)sp.G * 4);
-    A.bar = (uint64_t *)e->arena.take(S_NC * 256);
-    if (!A.xq || !A.attq || !A.hbq || !A.ssq || !A.bar) return fail(OI_E_NOMEM, "arena exhausted (token kernel)");
-    A.n_layers = (int32_t)c.n_layers;
-    if (const char *ev = std::getenv("OI_STREAM_LAYERS"))  // debugging: run only the first layers
-        A.n_layers = (int32_t)std::max<int64_t>(1, std::min<int64_t>(c.n_layers, std::atoll(ev)));
-    A.G = sp.G;
-    A.wstream = wstream;
-    A.wstride = (int64_t)sp.wstride;
-    A.wpieces = upload_table(e, sp.wpieces);
-    if (!A.wpieces) return fail(OI_E_DEVICE, "token kernel tables upload failed");
-    A.vocab_plan = sp.vocab_plan;
-    A.output_norm = e->output_norm;
-    A.emb = e->tok_embd;
-    A.D = (int32_t)c.dim;
-    A.H = (int32_t)c.hidden_dim;
-    A.QD = (int32_t)QD;
-    A.KVD = (int32_t)(c.n_kv_heads * c.head_dim);
-    A.HD = (int32_t)c.head_dim;
-    A.n_heads = (int32_t)c.n_heads;
-    A.n_kv = (int32_t)c.n_kv_heads;
-    A.vocab = (int32_t)c.vocab_size;
-    A.seq_len = (int32_t)c.seq_len;
-    A.rD = sp.rD;
-    A.rH = sp.rH;
-    A.rQ = sp.rQ;
-    A.eps = c.rms_eps;
-    A.rope_cs = e->rope_cs;
-    A.q = e->q;
-    A.k = e->k;
-    A.v = e->v;
-    A.part = e->part;
-    A.max_chunks = e->max_splits;
-    A.logits = e->logits;
-    A.am_val = e->am_val;
-    A.am_idx = e->am_idx;
-    A.state = e->state;
-    A.tokens = e->tokens;
-    A.finalize_only = 0;
-    A.yo_floats = sp.yo;
-    A.trace = nullptr;
-    if (const char *ev = std::getenv("OI_STREAM_TRACE")) {
-        if (ev[0] == '1') {
-            const size_t tb = (size_t)(2 + 6 * c.n_layers) * sp.G * S_TR_SLOTS * 8;
-            HIP_TRY(hipMalloc(&A.trace, tb));  // freed with the engine
-            HIP_TRY(hipMemset(A.trace, 0, tb));
-        }
-    }
-    return OI_OK;
 }
 
 
@@ -595,7 +341,6 @@ int time_token(oi_engine *e, int iters, double *avg_us, double *bytes) {
         if (pass) HIP_TRY(hipEventRecord(e1, e->stream));
     }
     HIP_TRY(hipEventSynchronize(e1));
-    if ((rc = check_stream_error(e))) return rc;
     float ms = 0;
     HIP_TRY(hipEventElapsedTime(&ms, e0, e1));
     hipEventDestroy(e0);
@@ -632,7 +377,6 @@ void oi_engine_destroy(oi_engine *e) {
     if (e->graph) hipGraphDestroy(e->graph);
     if (e->arena.base) hipFree(e->arena.base);
     if (e->pf_mem) hipFree(e->pf_mem);
-    if (e->sa.trace) hipFree(e->sa.trace);
     if (e->logits_host) hipHostFree(e->logits_host);
     if (e->state_host) hipHostFree(e->state_host);
     if (e->stream) hipStreamDestroy(e->stream);
@@ -735,26 +479,6 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     e->weight_bytes = wbytes;
     if ((rc = check_device(opts->device))) return rc;
 
-    // persistent token kernel (OI_STREAM=1; the multi-kernel path otherwise)
-    StreamPlanAll sp;
-    {
-        const char *ev = std::getenv("OI_STREAM");
-        const bool want = ev && ev[0] == '1';
-        std::string why;
-        e->use_stream = want && plan_stream_all(g, c, tied, opts->device, sp, why);
-        if (want && !e->use_stream)
-            std::fprintf(stderr, "note: token kernel not used (%s); multi-kernel path\n", why.c_str());
-    }
-    size_t stream_extra = 0;
-    const int64_t QDs = c.n_heads * c.head_dim;
-    auto qv = [](int64_t K) { return ((size_t)qvec_bytes(K) + 2047) & ~(size_t)1023; };
-    if (e->use_stream) {
-        const size_t np = sp.plans.size(), NW = (size_t)sp.G * S_NCW;
-        stream_extra = sp.wstride * NW + NW * 4 + 256 + np * (sizeof(SKind) + 256) + np * NW * sizeof(SWave) +
-                       np * (size_t)sp.G * sizeof(SWgRows) + (size_t)c.n_layers * sizeof(SLayer) + qv(c.dim) +
-                       qv(QDs) + qv(c.hidden_dim) + (size_t)sp.G * 8 + S_NC * 256 + 16 * 256;
-    }
-
     // device memory plan
     e->chunk = attn_chunk((int)c.head_dim);
     e->max_splits = (int)((c.seq_len + e->chunk - 1) / e->chunk);
@@ -772,10 +496,10 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     plan_gemv(probe);
     size_t act = al(D * 4) + al(QD * 4) + 2 * al(KVD * 4) + al(QD * 4) + al(H * 4) + al(out_rows * 4) +
                  al((size_t)c.n_heads * e->max_splits * (c.head_dim + 4) * 4) + 2 * al((size_t)probe.total_wgs * 4) +
-                 2 * al((size_t)std::max(probe.total_wgs, sp.G) * 4) + al(ST_SWORDS * 4) +
+                 2 * al((size_t)probe.total_wgs * 4) + al(ST_WORDS * 4) +
                  al((size_t)(c.seq_len + 1) * 4) +
                  al((size_t)c.seq_len * (c.head_dim / 2) * 8);
-    e->arena.size = wbytes + 2 * kv_layer * c.n_layers + act + stream_extra + 4096;
+    e->arena.size = wbytes + 2 * kv_layer * c.n_layers + act + 4096;
     hipError_t he = hipMalloc(&e->arena.base, e->arena.size);
     if (he != hipSuccess) return fail(OI_E_NOMEM, "hipMalloc of " + std::to_string(e->arena.size) + " bytes failed");
     HIP_TRY(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking));
@@ -823,9 +547,9 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     e->hb = (float *)e->arena.take(H * 4);
     e->logits = (float *)e->arena.take(out_rows * 4);
     e->part = (float *)e->arena.take((size_t)c.n_heads * e->max_splits * (c.head_dim + 4) * 4);
-    e->am_val = (float *)e->arena.take((size_t)std::max(probe.total_wgs, sp.G) * 4);
-    e->am_idx = (int32_t *)e->arena.take((size_t)std::max(probe.total_wgs, sp.G) * 4);
-    e->state = (int32_t *)e->arena.take(ST_SWORDS * 4);
+    e->am_val = (float *)e->arena.take((size_t)probe.total_wgs * 4);
+    e->am_idx = (int32_t *)e->arena.take((size_t)probe.total_wgs * 4);
+    e->state = (int32_t *)e->arena.take(ST_WORDS * 4);
     e->tokens = (int32_t *)e->arena.take((size_t)(c.seq_len + 1) * 4);
     e->rope_cs = (float2 *)e->arena.take((size_t)c.seq_len * (c.head_dim / 2) * 8);
     if (!e->rope_cs) return fail(OI_E_NOMEM, "arena exhausted (activations)");
@@ -844,7 +568,6 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
         HIP_TRY(hipMemcpyAsync(e->rope_cs, cs.data(), cs.size() * 8, hipMemcpyHostToDevice, e->stream));
         HIP_TRY(hipStreamSynchronize(e->stream));
     }
-    if (e->use_stream && (rc = upload_stream(e.get(), g, tied, sp))) return rc;
     HIP_TRY(hipHostMalloc((void **)&e->logits_host, out_rows * 4, hipHostMallocDefault));
     HIP_TRY(hipHostMalloc((void **)&e->state_host, ST_WORDS * 4, hipHostMallocDefault));
 
@@ -906,6 +629,8 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     e->g_out = a;
     const char *ng = std::getenv("OI_NO_GRAPH");
     e->use_graph = !(ng && ng[0] == '1');
+    const char *pu = std::getenv("OI_PREFILL_UNFUSED");
+    e->pf_fused = !(pu && pu[0] == '1');
 
     std::printf("model: dim=%lld layers=%lld heads=%lld/%lld hidden=%lld vocab=%lld ctx=%lld/%lld  weights=%.0f MB  "
                 "KV cache (f16)=%.0f MB  [gfx950]\n",
@@ -949,7 +674,6 @@ const float *oi_engine_forward(oi_engine *e, int32_t token, int32_t pos) {
         fail(OI_E_DEVICE, std::string("forward: ") + hipGetErrorString(r));
         return nullptr;
     }
-    if (check_stream_error(e)) return nullptr;
     e->last_pos = pos;
     return e->logits_host;
 }
@@ -1038,7 +762,7 @@ int prefill_chunk(oi_engine *e, const int32_t *tokens, int T, int pos) {
                                (int)c.n_kv_heads, hd, st));
         HIP_TRY(launch_gemm_parts(L.wo, e->pf_xb, T, P[0], PB[0], &s0, st));
         HIP_TRY(launch_pf_addnorm16(e->pf_x, P[0], s0, L.ffn_norm, eps, D, T, e->pf_xb, st));
-        if (gemm_swiglu_supported(L.w1, L.w3, T)) {
+        if (e->pf_fused && gemm_swiglu_supported(L.w1, L.w3, T)) {
             // gate and up in one pass, SwiGLU in its epilogue; h goes to the up
             // partials' buffer (unsplit, it holds T x H floats)
             uint16_t *hb = (uint16_t *)P[1];
@@ -1121,7 +845,6 @@ const float *oi_engine_prefill(oi_engine *e, const int32_t *tokens, int32_t n, i
         fail(OI_E_DEVICE, std::string("prefill: ") + hipGetErrorString(r));
         return nullptr;
     }
-    if (check_stream_error(e)) return nullptr;
     e->last_pos = pos0 + n - 1;
     return e->logits_host;
 }
@@ -1140,17 +863,10 @@ int oi_engine_decode_greedy(oi_engine *e, int32_t token, int32_t pos, int32_t n_
     for (int i = 0; i < n_steps; i++)
         if ((rc = run_token(e))) return rc;
     // the last step's argmax is still pending: reduce it
-    if (e->use_stream) {
-        StreamArgs f = e->sa;
-        f.finalize_only = 1;
-        HIP_TRY(launch_stream(f, e->stream));
-    } else {
-        HIP_TRY(launch_embed(e->tok_embd, e->state, e->x, (int32_t)e->cfg.vocab_size, e->am_val, e->am_idx,
-                             e->tokens, 1, e->stream));
-    }
+    HIP_TRY(launch_embed(e->tok_embd, e->state, e->x, (int32_t)e->cfg.vocab_size, e->am_val, e->am_idx, e->tokens,
+                         1, e->stream));
     HIP_TRY(hipMemcpyAsync(out_tokens, e->tokens, (size_t)n_steps * 4, hipMemcpyDeviceToHost, e->stream));
     HIP_TRY(hipStreamSynchronize(e->stream));
-    if ((rc = check_stream_error(e))) return rc;
     e->last_pos = pos + n_steps - 1;
     return OI_OK;
 }
@@ -1380,36 +1096,6 @@ int oi_dequant(int32_t type, const void *blocks, int64_t n, float *out) {
     return OI_OK;
 }
 
-int64_t oi_engine_debug_buffer(oi_engine *e, int32_t which, void *dst, int64_t bytes) {
-    if (!e || !dst || bytes < 0) return fail(OI_E_ARG, "bad argument");
-    const oi_config &c = e->cfg;
-    const int64_t QD = c.n_heads * c.head_dim, KVD = c.n_kv_heads * c.head_dim;
-    auto qv = [](int64_t K) { return (int64_t)qvec_bytes(K); };
-    const void *src = nullptr;
-    int64_t n = 0;
-    switch (which) {
-    case OI_BUF_XQ: src = e->sa.xq, n = qv(c.dim); break;
-    case OI_BUF_ATTQ: src = e->sa.attq, n = qv(QD); break;
-    case OI_BUF_HBQ: src = e->sa.hbq, n = qv(c.hidden_dim); break;
-    case OI_BUF_SSQ: src = e->sa.ssq, n = (int64_t)e->sa.G * 4; break;
-    case OI_BUF_Q: src = e->q, n = QD * 4; break;
-    case OI_BUF_K: src = e->k, n = KVD * 4; break;
-    case OI_BUF_V: src = e->v, n = KVD * 4; break;
-    case OI_BUF_PART: src = e->part, n = c.n_heads * (int64_t)e->max_splits * (c.head_dim + 4) * 4; break;
-    case OI_BUF_LOGITS: src = e->logits, n = c.vocab_size * 4; break;
-    case OI_BUF_STATE: src = e->state, n = ST_SWORDS * 4; break;
-    case OI_BUF_AMVAL: src = e->am_val, n = (int64_t)std::max(e->sa.G, 1) * 4; break;
-    case OI_BUF_AMIDX: src = e->am_idx, n = (int64_t)std::max(e->sa.G, 1) * 4; break;
-    case OI_BUF_TRACE: src = e->sa.trace, n = (int64_t)(2 + 6 * c.n_layers) * e->sa.G * S_TR_SLOTS * 8; break;
-    default: return fail(OI_E_ARG, "unknown buffer");
-    }
-    if (!src) return fail(OI_E_ARG, "buffer not used by this engine");
-    n = std::min(n, bytes);
-    HIP_TRY(hipSetDevice(e->device));
-    HIP_TRY(hipStreamSynchronize(e->stream));
-    HIP_TRY(hipMemcpy(dst, src, (size_t)n, hipMemcpyDeviceToHost));
-    return n;
-}
 
 }  // extern "C"
 

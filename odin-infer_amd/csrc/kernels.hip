@@ -479,7 +479,10 @@ __global__ __launch_bounds__(WG) void moe_topk_kernel(MoeArgs a) {
 #pragma unroll
     for (int w = 0; w < WG / WAVE; w++) tot += red[w];
     for (int i = t; i < n; i += WG) p[i] = p[i] / tot;
-    if (t < a.top_k) sel[t] = 0.f;  // defined weights even if NaN logits leave a rank unfilled
+    if (t < a.top_k) {  // defined ids and weights even if NaN logits leave a rank unfilled
+        sel[t] = 0.f;
+        a.ids[t] = 0;
+    }
     __syncthreads();
     for (int i = t; i < n; i += WG) {
         const float pi = p[i];

@@ -72,8 +72,6 @@ HIP_SYMBOLS = {
     "oi_moe_workspace_bytes": (c_i64, [c_vp]),
     "oi_moe_ffn_launch": (c_i32, [c_vp] * 9),
     "oi_moe_ffn": (c_i32, [c_vp, c_i32, c_vp, c_i32] + [c_vp] * 7),
-    # include/oi_debug.h
-    "oi_engine_debug_buffer": (c_i64, [c_vp, c_i32, c_vp, c_i64]),
 }
 
 

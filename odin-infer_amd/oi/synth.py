@@ -33,6 +33,8 @@ CONFIGS = {
     "tiny-q8_0": _spec(256, 768, 2, 4, 2, 128, 2048, 1024, T.Q8_0, T.Q8_0, T.Q8_0, T.Q8_0, -1, seed=11),
     "tiny-f32": _spec(256, 512, 1, 2, 1, 128, 1024, 512, T.F32, T.F32, T.F32, T.F32, T.F16, seed=3),
     "small-q4_k": _spec(1024, 3072, 4, 16, 4, 128, 8192, 4096, T.Q4_K, T.Q6_K, T.Q4_K, T.Q4_K, T.Q6_K, seed=21),
+    # one layer of the Qwen3-8B shape (projection shapes of the batched prefill at full size)
+    "8b-1layer-q4_k": _spec(4096, 12288, 1, 32, 8, 128, 4096, 4096, T.Q4_K, T.Q6_K, T.Q4_K, T.Q4_K, T.Q6_K, seed=5),
 }
 
 

@@ -340,12 +340,27 @@ EXPORT void ref_dequant_row(int k, const uint8_t *src, int64_t n, float *dst) {
     }
 }
 
+/* Summation order of ref_dot_f32: 0 = the reference's (16-element steps from
+ * the start of the row); 1 = the same steps taken from the end of the row.
+ * Order 1 is a second, equally valid f32 evaluation of the same algorithm: the
+ * tests use the difference of the two to measure how far f32 rounding alone
+ * moves the oracle's logits (its "reordering noise") at a greedy near-tie. */
+static volatile int g_dot_order;
+EXPORT void ref_set_dot_order(int order) { g_dot_order = order; }
+
 /* ggml/quant.odin:250-269: acc0/acc1 are 8-lane vectors updated with FMA over
  * 16-element steps; the lanes of acc0+acc1 are summed in order; scalar tail. */
 EXPORT float ref_dot_f32(const float *a, const float *b, int64_t n) {
     float acc0[8] = {0}, acc1[8] = {0};
     int64_t i = 0;
-    for (; i + 16 <= n; i += 16) {
+    if (g_dot_order == 1) {
+        for (int64_t j = (n / 16) * 16 - 16; j >= 0; j -= 16) {
+            for (int k = 0; k < 8; k++) acc0[k] = fmaf(a[j + k], b[j + k], acc0[k]);
+            for (int k = 0; k < 8; k++) acc1[k] = fmaf(a[j + 8 + k], b[j + 8 + k], acc1[k]);
+        }
+        i = (n / 16) * 16;
+    }
+    for (; g_dot_order != 1 && i + 16 <= n; i += 16) {
         for (int k = 0; k < 8; k++) acc0[k] = fmaf(a[i + k], b[i + k], acc0[k]);
         for (int k = 0; k < 8; k++) acc1[k] = fmaf(a[i + 8 + k], b[i + 8 + k], acc1[k]);
     }

@@ -39,6 +39,7 @@ def lib():
         L.ref_dequant_row.argtypes = [c_int, c_vp, c_i64, c_vp]
         L.ref_dot_f32.restype = c_f
         L.ref_dot_f32.argtypes = [c_vp, c_vp, c_i64]
+        L.ref_set_dot_order.argtypes = [c_int]
         L.ref_matmul_t.argtypes = [c_vp, c_vp, c_int, c_vp, c_i64, c_i64, c_int]
         L.ref_rmsnorm.argtypes = [c_vp, c_vp, c_vp, c_i64, c_f]
         L.ref_softmax.argtypes = [c_vp, c_i64]
@@ -87,6 +88,13 @@ def dot_f32(a, b):
     a = np.ascontiguousarray(a, np.float32)
     b = np.ascontiguousarray(b, np.float32)
     return lib().ref_dot_f32(_p(a), _p(b), len(a))
+
+
+def set_dot_order(order):
+    """0: the reference's summation order in dot_f32; 1: the same 16-element
+    steps taken from the end of the row (a second valid f32 evaluation, used
+    to measure the oracle's own rounding noise)."""
+    lib().ref_set_dot_order(int(order))
 
 
 def matmul_t(w_blocks, kind, x, d, nthreads=1):

@@ -2,9 +2,11 @@
 the oracle (refcpu.ref_moe_ffn, pinned by a float64 brute force): the same
 expert ids in the same order, outputs within a
 scaled error of 1e-4 (weights within 1e-5: the router logits are summed in
-another order), at the measurement-plan shape of config 4 (128 experts,
-top 8, dim 2048, expert inner 768, Q4_K experts, F32 router) and small shapes
-with Q8_0 / Q6_K experts, ties, and no renormalization."""
+another order), at the measurement-plan shapes of config 4 (128 experts,
+top 8, dim 2048, expert inner 768) and config 5 (512 experts, top 10, dim
+2048, inner 512), with F32 and Q4_K routers (config 4 and 5 quantize the
+router Q4_K), and small shapes with Q8_0 / Q6_K experts, ties, and no
+renormalization."""
 import numpy as np
 import pytest
 
@@ -15,15 +17,17 @@ from test_moe_oracle import make_moe
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("E,k,dim,inter,etype,norm", [
-    (128, 8, 2048, 768, 12, 1),   # config 4 shape
-    (16, 4, 256, 128, 8, 1), (8, 8, 256, 256, 14, 0), (32, 10, 512, 512, 12, 1)])
-def test_moe_vs_oracle(E, k, dim, inter, etype, norm):
+@pytest.mark.parametrize("E,k,dim,inter,etype,norm,rtype", [
+    (128, 8, 2048, 768, 12, 1, 0), (128, 8, 2048, 768, 12, 1, 12),    # config 4 shape, F32 / Q4_K router
+    (512, 10, 2048, 512, 12, 1, 12),                                  # config 5 shape, Q4_K router
+    (16, 4, 256, 128, 8, 1, 0), (8, 8, 256, 256, 14, 0, 0), (32, 10, 512, 512, 12, 1, 0),
+    (64, 6, 1024, 256, 8, 1, 8)])
+def test_moe_vs_oracle(E, k, dim, inter, etype, norm, rtype):
     rng = np.random.default_rng(E + k + dim)
-    rb, gb, ub, db = make_moe(rng, E, dim, inter, etype)
+    rb, gb, ub, db = make_moe(rng, E, dim, inter, etype, rtype=rtype)
     x = rng.standard_normal(dim).astype(np.float32)
-    y, ids, w = moe.moe_ffn(E, k, dim, inter, norm, 0, rb, etype, gb, ub, db, x)
-    ry, rids, rw = refcpu.moe_ffn(E, k, dim, inter, norm, 0, rb, etype, gb, ub, db, x)
+    y, ids, w = moe.moe_ffn(E, k, dim, inter, norm, rtype, rb, etype, gb, ub, db, x)
+    ry, rids, rw = refcpu.moe_ffn(E, k, dim, inter, norm, rtype, rb, etype, gb, ub, db, x)
     assert np.array_equal(ids, rids), (ids, rids)
     assert np.allclose(w, rw, rtol=1e-5, atol=0)  # router logits summed in another order
     err = np.max(np.abs(np.float64(y) - ry)) / np.max(np.abs(ry))
@@ -45,6 +49,24 @@ def test_moe_ties(dim, inter):
     assert np.array_equal(ids, rids)
     assert np.allclose(w, rw, rtol=1e-5, atol=0)
     assert np.max(np.abs(np.float64(y) - ry)) / np.max(np.abs(ry)) <= 1e-4
+
+
+@pytest.mark.parametrize("dim,inter", [(128, 64), (256, 256)])
+def test_moe_nan_router_logit_leaves_defined_ids(dim, inter):
+    """A NaN router logit makes every probability NaN, so no expert ranks
+    below the first: the unfilled ranks must still name a valid expert (id 0,
+    weight 0) rather than whatever an earlier call left.  128/64 runs the
+    generic top-k kernel, 256/256 the routing inside the gate/up GEMV."""
+    rng = np.random.default_rng(4)
+    E, k = 8, 3
+    rb, gb, ub, db = make_moe(rng, E, dim, inter, 8)
+    x = rng.standard_normal(dim).astype(np.float32)
+    moe.moe_ffn(E, k, dim, inter, 1, 0, rb, 8, gb, ub, db, x)  # a normal call first
+    r = rb.view(np.float32).copy()
+    r[3 * dim + 7] = np.nan
+    y, ids, w = moe.moe_ffn(E, k, dim, inter, 1, 0, r.view(np.uint8), 8, gb, ub, db, x)
+    assert np.all((ids >= 0) & (ids < E)), ids
+    assert np.all(ids[1:] == 0), ids
 
 
 def test_moe_rejects_bad_dims():

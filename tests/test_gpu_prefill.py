@@ -51,6 +51,44 @@ def test_prefill_logits_vs_oracle(make_model, name, n):
         r.close()
 
 
+def test_prefill_512_tokens_fused_gate_up(make_model):
+    """512 batched tokens on small-q4_k: 24 row tiles x 8 token tiles of the
+    gate/up GEMM need no K split, so the fused gate/up pass with the SwiGLU
+    epilogue runs (the 8B-shape prefill's path); logits and argmax vs the
+    oracle."""
+    path = make_model("small-q4_k")
+    e, r = _engines(path, 1024)
+    try:
+        toks = _tokens(512, 512, r.vocab_size)
+        got = infer.engine_forward_batch(e, toks, 0).copy()
+        ref = r.prefill(toks, 0)
+        err = scaled_err(got, ref)
+        assert err <= TOL, "scaled error %.3g" % err
+        assert int(np.argmax(got)) == refcpu.argmax(ref)
+    finally:
+        infer.engine_destroy(e)
+        r.close()
+
+
+def test_prefill_fused_gate_up_equals_unfused_at_8b_shape(make_model, monkeypatch):
+    """One layer of the Qwen3-8B shape (gate/up 12288 x 4096, 16 K chunks),
+    512 tokens: the fused gate/up pass (SwiGLU in its epilogue) gives the same
+    last-token logits as the two projections + SwiGLU kernel (OI_PREFILL_UNFUSED=1):
+    both compute f16(silu(g) * u) from the same f32 accumulators."""
+    path = make_model("8b-1layer-q4_k")
+    toks = _tokens(3, 512, 4096)
+    out = []
+    for unfused in ("0", "1"):
+        monkeypatch.setenv("OI_PREFILL_UNFUSED", unfused)
+        e, ok = infer.engine_load(path, infer.Engine_Opts(max_ctx=1024))
+        assert ok
+        try:
+            out.append(infer.engine_forward_batch(e, toks, 0).copy())
+        finally:
+            infer.engine_destroy(e)
+    assert np.array_equal(out[0].view(np.uint32), out[1].view(np.uint32)), scaled_err(out[0], out[1])
+
+
 def _greedy_ref(r, token, pos, n):
     out = []
     for i in range(n):
@@ -144,23 +182,3 @@ def test_prefill_errors(make_model):
         assert np.isfinite(infer.engine_forward_batch(e, np.arange(8, dtype=np.int32), 0)).all()
     finally:
         infer.engine_destroy(e)
-
-
-def test_prefill_with_token_kernel_decode(make_model, monkeypatch):
-    """With the persistent token kernel (OI_STREAM=1) the batched prompt, its
-    per-token tail and the decode after it share one KV cache: the greedy ids
-    after a 45-token prompt (40 batched + 5 per token) match the oracle."""
-    monkeypatch.setenv("OI_STREAM", "1")
-    path = make_model("tiny-q4_k")
-    e, r = _engines(path, 256)
-    try:
-        toks = _tokens(21, 45, r.vocab_size)
-        got = infer.engine_forward_batch(e, toks, 0).copy()
-        ref = r.prefill(toks, 0)
-        assert scaled_err(got, ref) <= TOL
-        first = int(np.argmax(got))
-        dev = infer.engine_decode_greedy(e, first, len(toks), 16)
-        assert np.array_equal(dev, _greedy_ref(r, first, len(toks), 16))
-    finally:
-        infer.engine_destroy(e)
-        r.close()

@@ -10,15 +10,18 @@ import refcpu
 from oi import synth
 
 
-def make_moe(rng, E, dim, inter, etype, tie=None):
+def make_moe(rng, E, dim, inter, etype, tie=None, rtype=0):
+    """Router (F32, or quantized to rtype), gate, up, down weights."""
     router = (rng.standard_normal((E, dim)) * 0.1).astype(np.float32)
     if tie is not None:  # experts tie[0] and tie[1] share the largest router row
         router[list(tie)] = router[0] * 0 + 0.5 / np.sqrt(dim)
-    gate = rng.standard_normal((E * inter, dim)).astype(np.float32) * 0.05
-    up = rng.standard_normal((E * inter, dim)).astype(np.float32) * 0.05
-    down = rng.standard_normal((E * dim, inter)).astype(np.float32) * 0.05
+    seed = int(rng.integers(1, 2 ** 31))  # expert matrices from the seeded C generator (fast at 512 experts)
+    gate = synth.tensor_f32(seed, "gate", E * inter, dim, sigma=0.05)
+    up = synth.tensor_f32(seed, "up", E * inter, dim, sigma=0.05)
+    down = synth.tensor_f32(seed, "down", E * dim, inter, sigma=0.05)
     q = lambda m: synth.quantize_rows(etype, m)
-    return router.view(np.uint8).reshape(-1), q(gate), q(up), q(down)
+    rb = router.view(np.uint8).reshape(-1) if rtype == 0 else synth.quantize_rows(rtype, router)
+    return rb, q(gate), q(up), q(down)
 
 
 def moe_f64(E, k, dim, inter, norm, rtype, rb, etype, gb, ub, db, x, renorm=True):
@@ -40,18 +43,19 @@ def moe_f64(E, k, dim, inter, norm, rtype, rb, etype, gb, ub, db, x, renorm=True
     return y, np.array(ids), w
 
 
-@pytest.mark.parametrize("E,k,dim,inter,etype", [(16, 4, 256, 128, 8), (8, 2, 256, 256, 12), (6, 6, 128, 64, 8)])
-def test_moe_vs_float64(E, k, dim, inter, etype):
+@pytest.mark.parametrize("E,k,dim,inter,etype,rtype", [(16, 4, 256, 128, 8, 0), (8, 2, 256, 256, 12, 0),
+                                                        (6, 6, 128, 64, 8, 0), (32, 8, 512, 256, 12, 12)])
+def test_moe_vs_float64(E, k, dim, inter, etype, rtype):
     rng = np.random.default_rng(E * 13 + k)
-    rb, gb, ub, db = make_moe(rng, E, dim, inter, etype)
+    rb, gb, ub, db = make_moe(rng, E, dim, inter, etype, rtype=rtype)
     x = rng.standard_normal(dim).astype(np.float32)
-    y, ids, w = refcpu.moe_ffn(E, k, dim, inter, 1, 0, rb, etype, gb, ub, db, x)
-    ry, rids, rw = moe_f64(E, k, dim, inter, 1, 0, rb, etype, gb, ub, db, x)
+    y, ids, w = refcpu.moe_ffn(E, k, dim, inter, 1, rtype, rb, etype, gb, ub, db, x)
+    ry, rids, rw = moe_f64(E, k, dim, inter, 1, rtype, rb, etype, gb, ub, db, x)
     assert np.array_equal(ids, rids)
     assert np.allclose(w, rw, rtol=1e-5) and abs(w.sum() - 1.0) < 1e-5
     assert np.max(np.abs(y - ry)) / np.max(np.abs(ry)) <= 1e-5
     if k < E:  # without renormalization the result moves well past the bound
-        bad, _, _ = moe_f64(E, k, dim, inter, 1, 0, rb, etype, gb, ub, db, x, renorm=False)
+        bad, _, _ = moe_f64(E, k, dim, inter, 1, rtype, rb, etype, gb, ub, db, x, renorm=False)
         assert np.max(np.abs(y - bad)) / np.max(np.abs(ry)) > 100 * 1e-5
 
 

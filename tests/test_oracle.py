@@ -92,6 +92,32 @@ def test_dot_f32():
         assert abs(refcpu.dot_f32(a, b) - ref) <= 1e-5 * float(np.abs(a).dot(np.abs(b)))
 
 
+def test_dot_f32_reversed_order_is_another_valid_sum():
+    """The second summation order (steps from the end of the row) sums the same
+    products: exact on exact integer data, within f32 rounding of the float64
+    sum on random data, and not always bit-equal to the reference order (so it
+    measures rounding noise)."""
+    rng = np.random.default_rng(2)
+    a = np.arange(1, 97, dtype=F32)
+    try:
+        refcpu.set_dot_order(1)
+        assert refcpu.dot_f32(a, np.ones(96, F32)) == 96 * 97 / 2
+        assert refcpu.dot_f32(a[:40], np.ones(40, F32)) == 40 * 41 / 2  # tail after the steps
+        diffs = 0
+        for n in (16, 100, 4096, 12288):
+            x, y = rng.standard_normal(n).astype(F32), rng.standard_normal(n).astype(F32)
+            refcpu.set_dot_order(1)
+            r1 = refcpu.dot_f32(x, y)
+            refcpu.set_dot_order(0)
+            r0 = refcpu.dot_f32(x, y)
+            ref = float(np.dot(x.astype(np.float64), y))
+            assert abs(r1 - ref) <= 1e-5 * float(np.abs(x).dot(np.abs(y)))
+            diffs += r1 != r0
+        assert diffs >= 1
+    finally:
+        refcpu.set_dot_order(0)
+
+
 @pytest.mark.parametrize("kind", [12, 14, 8])
 def test_matmul_t_f64_and_thread_invariance(kind):
     from oi import synth

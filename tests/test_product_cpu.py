@@ -25,17 +25,16 @@ def declared(header):
     return sorted(set(re.findall(r"\b(oi_[a-z0-9_]+)\s*\(", text)))
 
 
-@pytest.mark.parametrize("header,lib", [("oi.h", _native.LIB_HIP), ("oi_debug.h", _native.LIB_HIP),
-                                        ("oi_synth.h", _native.LIB_SYNTH)])
+@pytest.mark.parametrize("header,lib", [("oi.h", _native.LIB_HIP), ("oi_synth.h", _native.LIB_SYNTH)])
 def test_library_exports_every_declared_symbol(header, lib):
     names = declared(header)
-    assert len(names) >= (5 if header != "oi_debug.h" else 1)
+    assert len(names) >= 5
     L = ctypes.CDLL(lib)
     missing = [n for n in names if not hasattr(L, n)]
     assert not missing, missing
-    if header in ("oi.h", "oi_debug.h"):
-        # the Python binding covers exactly the C ABI headers of the HIP library
-        assert set(declared("oi.h")) | set(declared("oi_debug.h")) == set(_native.HIP_SYMBOLS)
+    if header == "oi.h":
+        # the Python binding covers exactly the C ABI header of the HIP library
+        assert set(declared("oi.h")) == set(_native.HIP_SYMBOLS)
 
 
 def prototypes(header):
@@ -49,7 +48,7 @@ def prototypes(header):
     return out
 
 
-@pytest.mark.parametrize("header", ["oi.h", "oi_debug.h"])
+@pytest.mark.parametrize("header", ["oi.h"])
 def test_binding_arity_matches_header(header):
     """The ctypes argument lists have as many entries as the C prototypes
     (a short list silently passes garbage in the missing registers)."""
