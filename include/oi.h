@@ -278,6 +278,18 @@ int64_t oi_moe_workspace_bytes(const oi_moe_dims *d);
 int oi_moe_ffn_launch(const oi_moe_dims *d, const oi_weights *router, const oi_weights *gate, const oi_weights *up,
                       const oi_weights *down, const float *x_dev, void *workspace, float *y_dev, void *stream);
 
+/* oi_moe_ffn_launch for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  Same arguments and result as
+ * oi_moe_ffn_launch without the workspace: the library uses a fixed 512 KiB
+ * device array of its own, one per GPU, held until the process ends, and
+ * rejects dims whose oi_moe_workspace_bytes exceed it (OI_E_ARG).  It calls
+ * no hipMalloc/hipFree.  Calls on one GPU share the array, so calls that
+ * overlap on one GPU (two streams or two threads) race. */
+int oi_moe_ffn_launch_noalloc(const oi_moe_dims *d, const oi_weights *router, const oi_weights *gate,
+                              const oi_weights *up, const oi_weights *down, const float *x_dev, float *y_dev,
+                              void *stream);
+
 /* Host-memory form (synchronous); also returns the chosen ids and weights
  * (ids_out, w_out: top_k each, may be NULL). */
 int oi_moe_ffn(const oi_moe_dims *d, int32_t router_type, const void *router_blocks, int32_t expert_type,

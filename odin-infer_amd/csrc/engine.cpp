@@ -117,6 +117,9 @@ void q4k_header(const uint8_t *blk, uint8_t *out) {
     std::memcpy(out + 12, &hi, 4);
 }
 
+// Records a failure for oi_last_error() from the library's other sources.
+int set_error(int code, const char *msg) { return fail(code, msg); }
+
 }  // namespace oi
 
 namespace {

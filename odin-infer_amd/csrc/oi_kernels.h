@@ -223,6 +223,9 @@ struct MoeArgs {
 hipError_t launch_moe(const MoeArgs &a, const GemvArgs &router, const GemvArgs *gu, const GemvArgs *dn,
                       hipStream_t st);
 
+// engine.cpp: records a failure for oi_last_error(); returns code
+int set_error(int code, const char *msg);
+
 // kernels.hip: x[t] = dequant(emb[tokens[t]]) for n tokens
 hipError_t launch_embed_rows(const DMat &emb, const int32_t *tokens, int n, float *x, hipStream_t st);
 

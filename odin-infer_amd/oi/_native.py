@@ -71,6 +71,7 @@ HIP_SYMBOLS = {
     "oi_qwen35_attn_steps": (c_i32, [c_vp, c_i32, c_i32] + [c_vp] * 9),
     "oi_moe_workspace_bytes": (c_i64, [c_vp]),
     "oi_moe_ffn_launch": (c_i32, [c_vp] * 9),
+    "oi_moe_ffn_launch_noalloc": (c_i32, [c_vp] * 8),
     "oi_moe_ffn": (c_i32, [c_vp, c_i32, c_vp, c_i32] + [c_vp] * 7),
 }
 
