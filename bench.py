@@ -55,10 +55,22 @@ def weight_bytes(spec):
     return L * per_layer + out + 4 * D + row_byte_size(spec["type_embd"], D)
 
 
-def cpu_baseline(path, k, v, cfg, gpu_tokens, budget_s):
+def cpu_threads():
+    """Threads for the CPU baseline: the host's cores (nproc), capped at the
+    worker-pool share the GPU box grants one GPU (OMP_NUM_THREADS there)."""
+    nproc = os.cpu_count() or 1
+    cap = int(os.environ.get("OMP_NUM_THREADS", nproc) or nproc)
+    return max(1, min(nproc, cap)), nproc
+
+
+def cpu_baseline(path, k, v, cfg, gpu_tokens, budget_s, max_steps=64):
+    """The oracle (restated reference CPU forward) on the host's cores: greedy
+    steps from pos 4096 of the same model and pre-filled f16 KV, up to
+    max_steps or budget_s; its ids are compared with the GPU's.  Then a
+    1-thread figure on one step."""
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import refcpu  # the oracle, timed here as the CPU baseline
-    threads = min(16, os.cpu_count() or 1)
+    threads, nproc = cpu_threads()
     r = refcpu.RefEngine(path, max_ctx=cfg.seq_len, num_threads=threads, kv_f16=True)
     try:
         for layer in range(cfg.n_layers):
@@ -69,20 +81,144 @@ def cpu_baseline(path, k, v, cfg, gpu_tokens, budget_s):
             tok = refcpu.argmax(logits)
             ids.append(tok)
             el = time.perf_counter() - t0
-            if el > budget_s or len(ids) >= len(gpu_tokens):
+            if el > budget_s or len(ids) >= min(max_steps, len(gpu_tokens)):
                 break
         n = len(ids)
-        return {
-            "value": n / el, "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": "%d greedy decode steps from pos %d of the same model and pre-filled f16 KV, "
-                      "oracle/refcpu.c (restated reference CPU forward, row work queue over %d threads)"
-                      % (n, CONTEXT, threads),
-            "ms_per_token": 1000 * el / n,
-            "greedy_ids_match_gpu": bool(list(gpu_tokens[:n]) == ids),
-            "compared_steps": n,
-        }
     finally:
         r.close()
+    # 1 thread, one step (the same forward at the next position)
+    r1 = refcpu.RefEngine(path, max_ctx=cfg.seq_len, num_threads=1, kv_f16=True)
+    try:
+        for layer in range(cfg.n_layers):
+            r1.kv_fill(layer, 0, k[layer], v[layer])
+        t1 = time.perf_counter()
+        r1.forward(0, CONTEXT)
+        el1 = time.perf_counter() - t1
+    finally:
+        r1.close()
+    match = 0
+    while match < n and gpu_tokens[match] == ids[match]:
+        match += 1
+    return {
+        "value": n / el, "unit": "tok/s", "cores": threads, "kind": "port", "nproc": nproc,
+        "sample": "%d greedy decode steps from pos %d of the same model and pre-filled f16 KV, "
+                  "oracle/refcpu.c (restated reference CPU forward, row work queue over %d threads; the host "
+                  "reports nproc=%d, the box grants one GPU a %d-thread share)" % (n, CONTEXT, threads, nproc, threads),
+        "ms_per_token": 1000 * el / n,
+        "one_thread": {"value": 1.0 / el1, "unit": "tok/s", "ms_per_token": 1000 * el1, "sample": "1 step"},
+        "greedy_ids_match_gpu": bool(match == n), "compared_steps": n, "matching_prefix": match,
+    }
+
+
+def c1_cpu_run(budget_s=60.0):
+    """Qwen3-0.6B shape, Q8_0, f32 KV cache, max_ctx 4096,
+    token 0 then 256 greedy steps on the CPU reference path (the oracle, host
+    cores), and the same workload on the GPU (f16 KV) beside it."""
+    from oi import infer, synth
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import refcpu
+    threads, nproc = cpu_threads()
+    d = tempfile.mkdtemp(prefix="oi_c1_")
+    try:
+        path = os.path.join(d, "c1.gguf")
+        synth.write_gguf(path, "qwen3-0.6b-q8_0")
+        spec = synth.CONFIGS["qwen3-0.6b-q8_0"]
+        r = refcpu.RefEngine(path, max_ctx=4096, num_threads=threads, kv_f16=False)
+        try:
+            tok, ids, t0 = 0, [], time.perf_counter()
+            for pos in range(256):
+                tok = refcpu.argmax(r.forward(tok, pos))
+                ids.append(tok)
+                if time.perf_counter() - t0 > budget_s:
+                    break
+            el = time.perf_counter() - t0
+        finally:
+            r.close()
+        n = len(ids)
+        e, _ = infer.engine_load(path, infer.Engine_Opts(max_ctx=4096))
+        try:
+            infer.engine_decode_greedy(e, 0, 0, 16)  # warm
+            g0 = time.perf_counter()
+            gids = infer.engine_decode_greedy(e, 0, 0, 256)
+            gel = time.perf_counter() - g0
+        finally:
+            infer.engine_destroy(e)
+        match = 0
+        while match < n and gids[match] == ids[match]:
+            match += 1
+        wb = weight_bytes(spec)
+        return {"workload": "Qwen3-0.6B shape Q8_0, token 0 + %d greedy steps, f32 KV (CPU) / f16 KV (GPU), "
+                            "max_ctx 4096" % n,
+                "cpu": {"value": round(n / el, 2), "unit": "tok/s", "cores": threads, "nproc": nproc, "kind": "port",
+                        "ms_per_token": round(1000 * el / n, 2),
+                        "GBps": round(wb * n / el / 1e9, 2)},
+                "gpu": {"value": round(256 / gel, 1), "unit": "tok/s", "ms_per_token": round(1000 * gel / 256, 4),
+                        "GBps": round(wb * 256 / gel / 1e9, 1)},
+                "greedy_matching_prefix": match, "compared_steps": n}
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+
+
+def gemv_microbench(iters=100, cpu=True):
+    """the quantized GEMV alone at batch 1 for Q4_K, Q6_K
+    and Q8_0 at 12288x4096, 4096x12288, 4096x4096 and 151936x4096, weights
+    N(0,0.02) quantized, x ~ N(0,1) f32.  Copies of the weights totalling
+    >= 1 GiB are cycled (the 256 MB Infinity Cache cannot serve repeats);
+    max(iters, copies) launches of oi_gemv_launch in one HIP graph, HIP events
+    around the graph launch; the median of 3 graph launches of the mean time
+    per GEMV.  Bytes: weights + 4 in + 4 out."""
+    import ctypes
+    import numpy as np
+    from oi import ggml, synth
+    hip = ctypes.CDLL("libamdhip64.so")
+    vp = ctypes.c_void_p
+
+    def ok(rc, what):
+        if rc != 0:
+            raise RuntimeError("%s failed (%d)" % (what, rc))
+
+    threads, _ = cpu_threads()
+    out = []
+    names = {12: "Q4_K", 14: "Q6_K", 8: "Q8_0"}
+    for rows, cols in ((12288, 4096), (4096, 12288), (4096, 4096), (151936, 4096)):
+        w32 = synth.tensor_f32(9, "microbench.%dx%d" % (rows, cols), rows, cols, sigma=0.02)
+        x = np.random.default_rng(rows + cols).standard_normal(cols).astype(np.float32)
+        for kind in (12, 14, 8):
+            blocks = synth.quantize_rows(kind, w32)
+            w0 = ggml.DeviceWeights(kind, blocks, rows, cols)
+            ncopy = max(1, -(-ROTATE_BYTES // w0.nbytes))
+            ws = [w0] + [ggml.DeviceWeights(kind, blocks, rows, cols) for _ in range(ncopy - 1)]
+            xd, yd, st = vp(), vp(), vp()
+            ok(hip.hipMalloc(ctypes.byref(xd), ctypes.c_size_t(cols * 4)), "hipMalloc")
+            ok(hip.hipMalloc(ctypes.byref(yd), ctypes.c_size_t(rows * 4)), "hipMalloc")
+            ok(hip.hipMemcpy(xd, x.ctypes.data_as(vp), ctypes.c_size_t(cols * 4), 1), "hipMemcpy")
+            ok(hip.hipStreamCreate(ctypes.byref(st)), "hipStreamCreate")
+            n = max(iters, ncopy)
+            runs = sorted(_graph_us(hip, st, lambda i: ws[i % ncopy].launch(xd.value, yd.value, st.value), n)
+                          for _ in range(3))
+            us = runs[1]
+            hip.hipStreamDestroy(st)
+            hip.hipFree(xd)
+            hip.hipFree(yd)
+            byts = w0.nbytes + 4 * cols + 4 * rows
+            rec = {"type": names[kind], "rows": rows, "cols": cols, "median_us": round(us, 3),
+                   "runs_us": [round(u, 3) for u in runs], "launches": n, "weight_copies": ncopy,
+                   "bytes": int(byts), "GBps": round(byts / us / 1e3, 1),
+                   "frac_hbm_peak": round(byts / us / 1e3 / PEAK_HBM_GBPS, 4)}
+            for wc in ws:
+                wc.free()
+            if cpu:
+                rc = _oracle()
+                t0 = time.perf_counter()
+                rc.matmul_t(blocks, kind, x, rows, threads)
+                el = time.perf_counter() - t0
+                rec["cpu_baseline"] = {"value": round(1e6 * el, 1), "unit": "us/GEMV", "cores": threads,
+                                       "kind": "port", "sample": "one oracle/refcpu.c matmul_t (restated "
+                                       "infer/matmul.odin:77-109) of the same matrix and x"}
+            out.append(rec)
+            log("GEMV %s %dx%d: %.2f us, %.0f GB/s" % (names[kind], rows, cols, us, byts / us / 1e3))
+        del w32
+    return out
 
 
 PEAK_F16_TFLOPS = 2500.0  # MI355X dense f16 MFMA
@@ -470,6 +606,131 @@ def moe_step(iters=100, cpu=True):
     return out
 
 
+def _free_gb(path):
+    st = os.statvfs(path)
+    return st.f_bavail * st.f_frsize / 1e9
+
+
+def model_decode(name, context, steps, warmup=8, prompt=0, cpu=True, cpu_budget=20.0):
+    """A whole-model decode measurement at batch 1 for the routed-expert and
+    hybrid configurations: the synthetic model `name` (full size), then either
+    the f16 KV cache pre-filled with N(0,1) to `context` positions (config 4)
+    or a `prompt`-token random-id prompt through engine_forward_batch (config
+    5, the hybrid's DeltaNet states need the prompt itself), then `steps`
+    greedy steps of the device-side loop.  Bytes per token: every launch's
+    algorithmic bytes (routed experts: only the chosen ones) from the engine's
+    own accounting at the mean position.  CPU baseline: the oracle on a bounded
+    sample of the same decode."""
+    import numpy as np
+    from oi import infer, synth
+    spec = synth.CONFIGS[name]
+    d = tempfile.mkdtemp(prefix="oi_%s_" % name)
+    try:
+        need = 1.2 * weight_bytes_any(spec) / 1e9 + 1
+        if _free_gb(d) < need:
+            return {"skipped": "needs %.0f GB of temporary disk, %.0f GB free" % (need, _free_gb(d))}
+        path = os.path.join(d, name + ".gguf")
+        t = time.time()
+        synth.write_gguf(path, name)
+        log("wrote synthetic %s (%.2f GB) in %.1fs" % (name, os.path.getsize(path) / 1e9, time.time() - t))
+        start = context if not prompt else prompt
+        e, _ = infer.engine_load(path, infer.Engine_Opts(max_ctx=start + steps + warmup + 8))
+        cfg = infer.engine_config(e)
+        out = {"model": name, "layers": cfg.n_layers, "dim": cfg.dim, "vocab": cfg.vocab_size}
+        try:
+            if prompt:
+                toks = np.random.default_rng(5).integers(0, cfg.vocab_size, size=prompt).astype(np.int32)
+                t0 = time.perf_counter()
+                logits = infer.engine_forward_batch(e, toks, 0)
+                pel = time.perf_counter() - t0
+                first = int(np.argmax(logits))
+                out["prefill"] = {"tokens": prompt, "ms": round(1000 * pel, 1), "tok_s": round(prompt / pel, 1),
+                                  "path": "per-token decode steps (the hybrid has no batched path here yet)"}
+                log("%s prefill: %d tokens in %.1f ms" % (name, prompt, 1000 * pel))
+                snap = None
+            else:
+                k, v = synth.kv_prefill(777, cfg.n_layers, cfg.n_kv_heads, context, cfg.head_dim)
+                infer.engine_kv_fill(e, 0, 0, k, v)
+                first = 0
+                snap = (k, v)
+            if warmup and not prompt:
+                infer.engine_decode_greedy(e, first, start, warmup)
+            t0 = time.perf_counter()
+            toks = infer.engine_decode_greedy(e, first, start, steps)
+            el = time.perf_counter() - t0
+            tok_s = steps / el
+            infer.engine_forward(e, int(toks[-1]), start + steps - 1)
+            us, bpt = infer.engine_time_kernel(e, "token", min(steps, 64))
+            kern = {}
+            for kn in ("qkv", "attn", "wo", "router", "gateup", "down", "shared", "linear_in", "deltanet",
+                       "linear_out", "output"):
+                try:
+                    infer.engine_time_kernel(e, kn, 16)
+                    ku, kb = infer.engine_time_kernel(e, kn, 64)
+                    kern[kn] = {"avg_us": round(ku, 3), "GBps": round(kb / ku / 1e3, 1)}
+                except Exception:
+                    pass
+            gbps = bpt * tok_s / 1e9
+            out.update({"decode_tok_s": round(tok_s, 2), "ms_per_token": round(1000 * el / steps, 4),
+                        "steps": steps, "from_pos": start, "bytes_per_token": int(bpt),
+                        "achieved_GBps": round(gbps, 1), "frac_hbm_peak": round(gbps / PEAK_HBM_GBPS, 4),
+                        "kernels_us": kern})
+            log("%s decode: %.1f tok/s, %.0f GB/s (%.1f%% of peak)" % (name, tok_s, gbps,
+                                                                        100 * gbps / PEAK_HBM_GBPS))
+        finally:
+            infer.engine_destroy(e)
+        if cpu:
+            sys.path.insert(0, os.path.join(REPO, "oracle"))
+            import refcpu
+            threads, nproc = cpu_threads()
+            r = refcpu.RefEngine(path, max_ctx=start + 64, num_threads=threads, kv_f16=True)
+            try:
+                if snap is not None:
+                    for layer in range(cfg.n_layers):
+                        r.kv_fill(layer, 0, snap[0][layer], snap[1][layer])
+                    tok, n, t0 = first, 0, time.perf_counter()
+                    while True:
+                        tok = refcpu.argmax(r.forward(tok, start + n))
+                        n += 1
+                        if time.perf_counter() - t0 > cpu_budget or n >= 16:
+                            break
+                    el = time.perf_counter() - t0
+                    sample = "%d greedy steps from pos %d of the same model and pre-filled cache" % (n, start)
+                else:
+                    # the hybrid's state needs the prompt: time the oracle's first prompt tokens
+                    n, t0 = 0, time.perf_counter()
+                    ptoks = np.random.default_rng(5).integers(0, cfg.vocab_size, size=16)
+                    for t in ptoks:
+                        r.forward(int(t), n)
+                        n += 1
+                        if time.perf_counter() - t0 > cpu_budget:
+                            break
+                    el = time.perf_counter() - t0
+                    sample = "%d forward steps from position 0 (the prompt's first tokens) of the same model" % n
+                out["cpu_baseline"] = {"value": round(n / el, 4), "unit": "tok/s", "cores": threads, "nproc": nproc,
+                                       "kind": "port", "sample": sample + ", oracle/refcpu.c"}
+            finally:
+                r.close()
+        return out
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+
+
+def weight_bytes_any(spec):
+    """GGUF bytes of a synthetic model of any architecture (for disk checks)."""
+    from oi.ggml import row_byte_size
+    D, L, V = spec["dim"], spec["n_layers"], spec["vocab_size"]
+    QD, KVD = spec["n_heads"] * spec["head_dim"], spec["n_kv_heads"] * spec["head_dim"]
+    t = spec["type_default"]
+    per = row_byte_size(t, D) * (2 * QD + 2 * KVD) + row_byte_size(t, QD) * D
+    if spec["n_experts"]:
+        per += 3 * spec["n_experts"] * spec["expert_ffn"] * row_byte_size(t, D)
+        per += 3 * spec.get("shared_expert_ffn", 0) * row_byte_size(t, D)
+    else:
+        per += 3 * spec["hidden_dim"] * row_byte_size(t, D)
+    return L * per + 2 * V * row_byte_size(t, D)
+
+
 def measure_prefill(e, cfg, n, reps=7):
     """Batched prefill of an n-token prompt at position 0 (engine_forward_batch,
     synchronous): host wall clock per call after one warm call (which also
@@ -501,13 +762,17 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=512)
     ap.add_argument("--warmup", type=int, default=16)
-    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
+    ap.add_argument("--cpu-budget", type=float, default=40.0, help="seconds of CPU baseline work (decode sample)")
+    ap.add_argument("--no-microbench", action="store_true", help="skip the config-2 GEMV microbench")
+    ap.add_argument("--no-models", action="store_true", help="skip the config-4 / config-5 whole-model decodes")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--model-path", default=None, help="reuse an existing synthetic GGUF")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM measurement")
     ap.add_argument("--no-prefill", action="store_true", help="skip the batched prefill measurement")
     ap.add_argument("--prefill-tokens", type=int, default=512)
-    ap.add_argument("--only", choices=["prefill", "gemm", "deltanet", "qwen35_attn", "moe"], default=None,
+    ap.add_argument("--only", choices=["prefill", "gemm", "deltanet", "qwen35_attn", "moe", "gemv", "c1", "decode",
+                                       "c4", "c5"],
+                    default=None,
                     help="run one secondary measurement alone (for profiling) and print its JSON")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (3 times), to calibrate HBM counters")
@@ -543,6 +808,19 @@ def main():
         return
     if args.only == "moe":
         print(json.dumps({"moe_step": moe_step()}), flush=True)
+        return
+    if args.only == "gemv":
+        print(json.dumps({"gemv_microbench": gemv_microbench(cpu=not args.no_cpu)}), flush=True)
+        return
+    if args.only == "c1":
+        print(json.dumps({"c1": c1_cpu_run()}), flush=True)
+        return
+    if args.only == "c4":
+        print(json.dumps({"c4": model_decode("qwen3-30b-a3b-q4_k", 2048, 256, cpu=not args.no_cpu)}), flush=True)
+        return
+    if args.only == "c5":
+        print(json.dumps({"c5": model_decode("qwen35-hybrid-moe", 0, 256, prompt=2048, cpu=not args.no_cpu)}),
+              flush=True)
         return
 
     tmpdir = None
@@ -590,6 +868,12 @@ def main():
             infer.engine_time_kernel(e, name, iters)  # warm
             us, b = infer.engine_time_kernel(e, name, iters)
             kern[name] = {"us": us, "bytes": b, "GBps": b / us / 1e3}
+        if args.only == "decode":
+            print(json.dumps({"decode_tok_s": round(tok_s, 2), "ms_per_step": round(1000 * el / args.steps, 4),
+                              "kernels": {n: {"avg_us": round(d["us"], 3), "GBps": round(d["GBps"], 1)}
+                                          for n, d in kern.items()}}), flush=True)
+            infer.engine_destroy(e)
+            return
         dom = "gateup"
         roofline = {
             "bound": "hbm", "kernel": "gemv_kernel gate/up Q4_K (RMSNorm prologue, SwiGLU epilogue)",
@@ -616,6 +900,17 @@ def main():
             log("deltanet step: %.2f us, %.0f GB/s; qwen3.5 attention step: %.2f us, %.0f GB/s" % (
                 dn["avg_us"], dn["GBps"], q35["avg_us"], q35["GBps"]))
 
+        micro = None if args.no_microbench else gemv_microbench(cpu=not args.no_cpu)
+        c4 = c5 = None
+        if not args.no_models:
+            c4 = model_decode("qwen3-30b-a3b-q4_k", 2048, 256, cpu=not args.no_cpu)
+            c5 = model_decode("qwen35-hybrid-moe", 0, 256, prompt=2048, cpu=not args.no_cpu)
+        c1 = None if args.no_cpu else c1_cpu_run()
+        if c1:
+            log("C1: CPU %.2f tok/s (%d threads), GPU %.1f tok/s, greedy prefix %d/%d" % (
+                c1["cpu"]["value"], c1["cpu"]["cores"], c1["gpu"]["value"], c1["greedy_matching_prefix"],
+                c1["compared_steps"]))
+
         cpu = None
         if not args.no_cpu:
             log("CPU baseline (oracle) for up to %.0fs ..." % args.cpu_budget)
@@ -631,7 +926,10 @@ def main():
         out = {
             "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(1000 * el / args.steps, 4), "higher_is_better": True,
-            "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+            "scaling": "weak", "vs_baseline": None, "dtype": "q4k/q6k x i22 dot4, f32",
+            "dtype_note": "weights Q4_K/Q6_K decoded in registers; activations quantized per 32 elements to 22-bit "
+                          "integers (three int8 planes) for v_dot4_i32_i8, f32 scales, sums and accumulation; "
+                          "norms, RoPE, softmax and attention in f32 over an f16 KV cache",
             "data": "synthetic (seeded N(0,0.02) weights quantized Q4_K/Q6_K; N(0,1) f16 KV prefill)",
             "config": {"workload": "Qwen3-8B-shape dense decode, bs1, greedy, f16 KV pre-filled to 4096, "
                                    "%d steps from pos 4096" % args.steps,
@@ -649,6 +947,10 @@ def main():
             "deltanet_step": dn,
             "qwen35_attn_step": q35,
             "moe_step": moe,
+            "gemv_microbench": micro,
+            "c1": c1,
+            "c4_moe_decode": c4,
+            "c5_hybrid": c5,
         }
         print(json.dumps(out), flush=True)
         infer.engine_destroy(e)

@@ -63,9 +63,17 @@ typedef struct oi_weights oi_weights;
 /* ------------------------------------------------------------ engine API --- */
 
 /* engine_load (infer/engine.odin:18-34 -> infer/model.odin:216-242):
- * parse the GGUF at `path`, check the tensors the dense Qwen3 loader requires
- * (infer/model.odin:99-179), upload weights to HBM and allocate the f16 KV
- * cache [layer][kv_head][seq_len][head_dim].  Returns 0 and *out on success. */
+ * parse the GGUF at `path`, check the tensors the loader of its architecture
+ * requires, upload weights to HBM and allocate the f16 KV cache
+ * [layer][kv_head][seq_len][head_dim].  Architectures (general.architecture):
+ * "qwen3" (the dense loader, infer/model.odin:99-179), "qwen35" (the hybrid
+ * loader, qwen3_5/model.odin:225-364: full-attention layers with a KV cache,
+ * gated DeltaNet layers with conv and recurrent states) and, with no reference
+ * loader, routed-expert FFNs ("qwen3moe", and "qwen35" files with
+ * expert_count): ffn_gate_inp + ffn_{gate,up,down}_exps, optionally a shared
+ * expert (ffn_*_shexp).  Config: for routed experts hidden_dim is the expert
+ * inner size; for "qwen35" n_heads / n_kv_heads / head_dim are the
+ * full-attention layers'.  Returns 0 and *out on success. */
 int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out);
 
 /* engine_destroy (infer/engine.odin:36-43). NULL is allowed. */
@@ -115,6 +123,12 @@ int oi_engine_decode_greedy(oi_engine *e, int32_t token, int32_t pos, int32_t n_
 int oi_engine_kv_fill(oi_engine *e, int32_t layer0, int32_t nlayers, int32_t pos0, int32_t npos,
                       const uint16_t *k_f16, const uint16_t *v_f16);
 
+/* engine_reset_state (qwen3_5/engine.odin:108-132): zero every
+ * position-evolving state -- the KV cache of the attention layers, the conv
+ * and recurrent states of the DeltaNet layers -- so a new prompt can start at
+ * position 0 (the DeltaNet recurrence cannot be rewound). */
+int oi_engine_reset_state(oi_engine *e);
+
 /* Device pointer to the engine's last logits (vocab_size floats). */
 const float *oi_engine_logits_device(oi_engine *e);
 
@@ -129,7 +143,12 @@ enum {
     OI_KERNEL_GATEUP = 3,  /* RMSNorm + gate/up GEMV + SwiGLU */
     OI_KERNEL_DOWN = 4,    /* down GEMV + residual */
     OI_KERNEL_OUTPUT = 5,  /* final RMSNorm + vocab GEMV + greedy argmax */
-    OI_KERNEL_TOKEN = 6    /* one whole token step (the captured graph) */
+    OI_KERNEL_TOKEN = 6,   /* one whole token step (the captured graph) */
+    OI_KERNEL_ROUTER = 7,  /* MoE router GEMV (+ the shared expert's gate row) */
+    OI_KERNEL_LINEAR_IN = 8,   /* Qwen3.5 DeltaNet input projections (qkv, z, b, a) */
+    OI_KERNEL_DELTANET = 9,    /* Qwen3.5 gated DeltaNet token step */
+    OI_KERNEL_LINEAR_OUT = 10, /* Qwen3.5 DeltaNet output projection + residual */
+    OI_KERNEL_SHARED = 11      /* MoE shared expert: gate/up, then down + gated residual */
 };
 
 /* Launch one kernel of the token loop `iters` times on the engine's stream,

@@ -34,9 +34,21 @@ typedef struct oi_synth_spec {
     float norm_sigma;      /* stddev around 1.0 of F32 norm weights */
     uint64_t seed;
     int32_t n_threads;
+    /* Architecture: 0 = dense Qwen3 ("qwen3"); 1 = Qwen3-MoE ("qwen3moe": the
+     * FFN of every layer is n_experts routed experts of expert_ffn, top
+     * n_experts_used, router ffn_gate_inp); 2 = Qwen3.5 hybrid ("qwen35", the
+     * layout qwen3_5/model.odin:225-364 reads: every full_attn_interval-th layer
+     * full attention with [q | gate] heads and partial RoPE, the others gated
+     * DeltaNet; the FFN dense, or routed experts plus a shared expert of
+     * shared_expert_ffn with a sigmoid gate when n_experts > 0). */
+    int32_t arch;
+    int32_t n_experts, n_experts_used, expert_ffn, shared_expert_ffn;
+    int32_t type_router;   /* ggml type of ffn_gate_inp (and ffn_gate_inp_shexp) */
+    int32_t full_attn_interval, rotary_dim;
+    int32_t lin_n_k_heads, lin_n_v_heads, lin_head_k_dim, lin_head_v_dim, lin_conv_kernel;
 } oi_synth_spec;
 
-/* Write a dense Qwen3 GGUF v3 file. Returns 0 or a negative code. */
+/* Write a GGUF v3 file of spec->arch. Returns 0 or a negative code. */
 int oi_synth_write_gguf(const char *path, const oi_synth_spec *spec);
 
 /* Quantize nrows x ncols f32 (row-major) to `type` blocks (GGUF layout).

@@ -44,7 +44,8 @@ int fail(int code, const std::string &msg) {
     } while (0)
 
 bool device_type_ok(uint32_t t) {
-    return t == T_F32 || t == T_F16 || t == T_Q8_0 || t == T_Q4_K || t == T_Q6_K;
+    return t == T_F32 || t == T_F16 || t == T_Q8_0 || t == T_Q4_K || t == T_Q6_K || t == T_Q4_0 || t == T_Q4_1 ||
+           t == T_Q5_0 || t == T_Q5_1;
 }
 
 const char *type_name(uint32_t t) {
@@ -216,15 +217,38 @@ struct Arena {
     }
 };
 
+// Layer kinds: Qwen3 attention (infer/forward.odin:45-121), Qwen3.5 full
+// attention (qwen3_5/forward.odin:46-135), Qwen3.5 gated DeltaNet (:137-225).
+enum { LK_QWEN3 = 0, LK_FULL = 1, LK_LINEAR = 2 };
+
 struct LayerDev {
-    DMat wq, wk, wv, wo, w1, w2, w3;
-    const float *attn_norm, *ffn_norm, *q_norm, *k_norm;
-    uint16_t *kc, *vc;
+    int kind = LK_QWEN3;
+    bool moe = false, shared = false;  // routed-expert FFN (with a shared expert)
+    DMat wq{}, wk{}, wv{}, wo{}, w1{}, w2{}, w3{};
+    const float *attn_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+    uint16_t *kc = nullptr, *vc = nullptr;
+    DMat router{}, gexp{}, uexp{}, dexp{}, sh_inp{}, sh_gate{}, sh_up{}, sh_down{};
+    DMat in_qkv{}, in_z{}, in_b{}, in_a{}, ssm_out{};
+    const float *conv_w = nullptr, *dt_bias = nullptr, *ssm_a = nullptr, *ssm_norm = nullptr;
+    float *conv_state = nullptr, *rec_state = nullptr;
+};
+
+// One launch of the token step: a GEMV (dense or routed-expert), an attention
+// or a DeltaNet step.  `role` is the kernel id of oi_engine_time_kernel.
+enum { OP_GEMV = 0, OP_MOE_ROWS, OP_MOE_COLS, OP_ATTN, OP_Q35, OP_DN };
+struct Op {
+    int kind = OP_GEMV, role = 0;
+    double bytes = 0;  // algorithmic HBM bytes per launch (attention: without the cache rows)
+    GemvArgs g{};
+    AttnArgs at{};
+    Q35Args q{};
+    DnArgs dn{};
 };
 
 }  // namespace
 
-enum { K_QKV = 0, K_ATTN = 1, K_WO = 2, K_GATEUP = 3, K_DOWN = 4, K_OUTPUT = 5, K_TOKEN = 6 };
+enum { K_QKV = 0, K_ATTN = 1, K_WO = 2, K_GATEUP = 3, K_DOWN = 4, K_OUTPUT = 5, K_TOKEN = 6, K_ROUTER = 7,
+       K_LIN_IN = 8, K_DELTANET = 9, K_LIN_OUT = 10, K_SHARED = 11, K_LAST = 11 };
 
 struct oi_engine {
     oi_config cfg{};
@@ -243,9 +267,11 @@ struct oi_engine {
     float *logits_host = nullptr;
     int32_t *state_host = nullptr;
     int chunk = 64, max_splits = 0;
-    std::vector<GemvArgs> g_qkv, g_wo, g_gateup, g_down;
+    int arch = 0;  // 0 qwen3, 1 qwen3moe, 2 qwen35
+    int64_t n_experts = 0, top_k = 0, expert_ffn = 0, shared_ffn = 0;
+    int64_t rotary_dim = 0, lin_nk = 0, lin_nv = 0, lin_hk = 0, lin_hv = 0, lin_kernel = 0, full_interval = 0;
+    std::vector<std::vector<Op>> ops;  // per layer, in launch order
     GemvArgs g_out{};
-    std::vector<AttnArgs> a_attn;
     hipGraph_t graph = nullptr;
     hipGraphExec_t gexec = nullptr;
     int last_pos = 0;
@@ -263,17 +289,23 @@ struct oi_engine {
 
 namespace {
 
+hipError_t launch_op(const oi_engine *e, const Op &o, hipStream_t st) {
+    switch (o.kind) {
+    case OP_MOE_ROWS: return launch_gemv_q_moe(o.g, MOE_ROWS, st);
+    case OP_MOE_COLS: return launch_gemv_q_moe(o.g, MOE_COLS, st);
+    case OP_ATTN: return launch_attn(o.at, (int)e->cfg.head_dim, st);
+    case OP_Q35: return launch_q35_attn(o.q, (int)e->cfg.head_dim, st);
+    case OP_DN: return launch_deltanet(o.dn, st);
+    default: return launch_gemv(o.g, st);
+    }
+}
+
 int enqueue_token(oi_engine *e) {
     const hipStream_t st = e->stream;
     HIP_TRY(launch_embed(e->tok_embd, e->state, e->x, (int32_t)e->cfg.vocab_size, e->am_val, e->am_idx, e->tokens,
                          0, st));
-    for (size_t l = 0; l < e->layers.size(); l++) {
-        HIP_TRY(launch_gemv(e->g_qkv[l], st));
-        HIP_TRY(launch_attn(e->a_attn[l], (int)e->cfg.head_dim, st));
-        HIP_TRY(launch_gemv(e->g_wo[l], st));
-        HIP_TRY(launch_gemv(e->g_gateup[l], st));
-        HIP_TRY(launch_gemv(e->g_down[l], st));
-    }
+    for (const auto &layer : e->ops)
+        for (const Op &o : layer) HIP_TRY(launch_op(e, o, st));
     HIP_TRY(launch_gemv(e->g_out, st));
     return OI_OK;
 }
@@ -349,19 +381,21 @@ int time_token(oi_engine *e, int iters, double *avg_us, double *bytes) {
     hipEventDestroy(e0);
     hipEventDestroy(e1);
     *avg_us = ms * 1000.0 / iters;
-    auto mb = [](const DMat &m) {
-        size_t b = 0;
-        matrix_bytes((uint32_t)m.type, m.rows, m.cols, b);
-        return (double)b;
-    };
-    double w = mb(e->output) + 4.0 * c.dim;  // + output_norm
+    // every launch's algorithmic bytes (weights read once: routed experts only
+    // the chosen ones), the cache rows read at the mean position, the classifier
+    size_t b = 0;
+    matrix_bytes((uint32_t)e->output.type, e->output.rows, e->output.cols, b);
+    double w = (double)b + 4.0 * c.dim + 4.0 * c.vocab_size;  // + output_norm, logits
     size_t erow = 0;
     matrix_bytes((uint32_t)e->tok_embd.type, 1, e->tok_embd.cols, erow);
     w += (double)erow;
-    for (const LayerDev &L : e->layers)
-        w += mb(L.wq) + mb(L.wk) + mb(L.wv) + mb(L.wo) + mb(L.w1) + mb(L.w2) + mb(L.w3) + 4.0 * (2 * c.dim + 2 * c.head_dim);
     const double kvd = (double)(c.n_kv_heads * c.head_dim), mean_pos = start + (iters - 1) / 2.0;
-    *bytes = w + c.n_layers * 2 * kvd * 2 * (mean_pos + 1) + c.n_layers * 2 * kvd * 2 + 4.0 * c.vocab_size;
+    for (const auto &layer : e->ops)
+        for (const Op &o : layer) {
+            w += o.bytes;
+            if (o.kind == OP_ATTN || o.kind == OP_Q35) w += 2 * kvd * 2 * (mean_pos + 1);
+        }
+    *bytes = w;
     e->last_pos = start + iters - 1;
     return OI_OK;
 }
@@ -399,32 +433,48 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     int rc = g.open(path, err);
     if (rc) return fail(rc, err);
 
-    // load_config (infer/model.odin:99-139)
-    auto *arch = g.meta("general.architecture");
-    if (!arch || arch->str != "qwen3")
-        std::fprintf(stderr, "warning: architecture is '%s', expected 'qwen3'\n", arch ? arch->str.c_str() : "");
-    const char *keys[7] = {"qwen3.embedding_length", "qwen3.feed_forward_length", "qwen3.block_count",
-                           "qwen3.attention.head_count", "qwen3.attention.head_count_kv", "qwen3.context_length",
-                           "qwen3.attention.key_length"};
-    int64_t kv[7];
-    for (int i = 0; i < 7; i++) {
-        auto *m = g.meta(keys[i]);
-        if (!m) return fail(OI_E_MODEL, std::string("missing metadata key: ") + keys[i]);
-        kv[i] = (int64_t)m->u;
-    }
+    // load_config (infer/model.odin:99-139; qwen3_5/model.odin:225-304): the
+    // metadata keys carry the architecture name as their prefix
+    auto *am = g.meta("general.architecture");
+    const std::string arch = am ? am->str : "";
     std::unique_ptr<oi_engine> e(new oi_engine());
+    e->arch = arch == "qwen3moe" ? 1 : arch == "qwen35" ? 2 : 0;
+    if (e->arch == 0 && arch != "qwen3")
+        std::fprintf(stderr, "warning: architecture is '%s', expected 'qwen3'\n", arch.c_str());
+    const std::string a = (e->arch == 0 ? std::string("qwen3") : arch) + ".";
+    auto key = [&](const char *k, int64_t &v) -> int {
+        auto *m = g.meta(a + k);
+        if (!m) return fail(OI_E_MODEL, "missing metadata key: " + a + k);
+        v = (int64_t)m->u;
+        return OI_OK;
+    };
     e->device = opts->device;
     oi_config &c = e->cfg;
-    c.dim = kv[0];
-    c.hidden_dim = kv[1];
-    c.n_layers = kv[2];
-    c.n_heads = kv[3];
-    c.n_kv_heads = kv[4];
-    c.max_seq = kv[5];
-    c.head_dim = kv[6];
-    auto *rf = g.meta("qwen3.rope.freq_base");
-    c.rope_freq = rf ? (float)rf->f : 1000000.0f;
-    auto *re = g.meta("qwen3.attention.layer_norm_rms_epsilon");
+    if ((rc = key("embedding_length", c.dim)) || (rc = key("feed_forward_length", c.hidden_dim)) ||
+        (rc = key("block_count", c.n_layers)) || (rc = key("attention.head_count", c.n_heads)) ||
+        (rc = key("attention.head_count_kv", c.n_kv_heads)) || (rc = key("context_length", c.max_seq)) ||
+        (rc = key("attention.key_length", c.head_dim)))
+        return rc;
+    const bool moe = e->arch == 1 || (e->arch == 2 && g.meta(a + "expert_count"));
+    if (moe) {
+        if ((rc = key("expert_count", e->n_experts)) || (rc = key("expert_used_count", e->top_k)) ||
+            (rc = key("expert_feed_forward_length", e->expert_ffn)))
+            return rc;
+        if (auto *m = g.meta(a + "expert_shared_feed_forward_length")) e->shared_ffn = (int64_t)m->u;
+        c.hidden_dim = e->expert_ffn;
+    }
+    if (e->arch == 2) {
+        int64_t inner = 0;
+        if ((rc = key("ssm.group_count", e->lin_nk)) || (rc = key("ssm.time_step_rank", e->lin_nv)) ||
+            (rc = key("ssm.state_size", e->lin_hk)) || (rc = key("ssm.inner_size", inner)) ||
+            (rc = key("ssm.conv_kernel", e->lin_kernel)) || (rc = key("full_attention_interval", e->full_interval)) ||
+            (rc = key("rope.dimension_count", e->rotary_dim)))
+            return rc;
+        e->lin_hv = e->lin_nv > 0 ? inner / e->lin_nv : 0;
+    }
+    auto *rf = g.meta(a + "rope.freq_base");
+    c.rope_freq = rf ? (float)rf->f : (e->arch == 2 ? 10000000.0f : 1000000.0f);
+    auto *re = g.meta(a + "attention.layer_norm_rms_epsilon");
     c.rms_eps = re ? (float)re->f : 1e-6f;
 
     auto require = [&](const std::string &name, const GgufTensor *&t) -> int {
@@ -432,7 +482,7 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
         if (!t) return fail(OI_E_MODEL, "missing required tensor: " + name);
         if (!device_type_ok(t->kind))
             return fail(OI_E_UNSUPPORTED, "tensor " + name + " has quant type " + type_name(t->kind) +
-                                              " (supported on this path: F32, F16, Q8_0, Q4_K, Q6_K)");
+                                              " (supported on this path: F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q4_K, Q6_K)");
         return OI_OK;
     };
     const GgufTensor *emb;
@@ -448,28 +498,70 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     if (!((c.head_dim == 128 || c.head_dim == 256) && (G == 1 || G == 2 || G == 4 || G == 8)))
         return fail(OI_E_UNSUPPORTED, "head_dim / GQA group not supported (head_dim 128 or 256, group 1, 2, 4 or 8)");
     if (c.n_heads * c.head_dim > 15360) return fail(OI_E_MODEL, "n_heads*head_dim too large");
+    if (moe && (e->n_experts < 1 || e->n_experts > 1024 || e->top_k < 1 || e->top_k > 32 ||
+                e->top_k > e->n_experts || e->shared_ffn % 256 || e->shared_ffn > 15360))
+        return fail(OI_E_UNSUPPORTED, "expert configuration not supported (<= 1024 experts, top_k <= 32, "
+                                      "inner sizes multiples of 256)");
+    if (e->arch == 2 && (e->full_interval < 1 || e->lin_hk != 128 || e->lin_hv != 128 || e->lin_nk < 1 ||
+                         e->lin_nv < 1 || e->lin_nv % e->lin_nk || e->lin_kernel < 1 || e->lin_kernel > 8 ||
+                         e->rotary_dim < 0 || e->rotary_dim > c.head_dim || e->rotary_dim % 2))
+        return fail(OI_E_UNSUPPORTED, "hybrid configuration not supported (DeltaNet head dims 128, value heads a "
+                                      "multiple of key heads, conv kernel <= 8)");
 
-    // tensors (model.odin:141-179): shapes checked against the config
+    // tensors (infer/model.odin:141-179; qwen3_5/model.odin:306-364): shapes checked against the config
     struct Want { std::string name; int64_t rows, cols; bool f32; const GgufTensor *t; };
     std::vector<Want> want;
     const int64_t D = c.dim, H = c.hidden_dim, QD = c.n_heads * c.head_dim, KVD = c.n_kv_heads * c.head_dim;
+    const int64_t E = e->n_experts, EF = e->expert_ffn, SF = e->shared_ffn;
+    const int64_t KD = e->lin_nk * e->lin_hk, VD = e->lin_nv * e->lin_hv, CD = 2 * KD + VD;
     want.push_back({"token_embd.weight", c.vocab_size, D, false, nullptr});
     want.push_back({"output_norm.weight", 1, D, true, nullptr});
     const bool tied = g.tensor("output.weight") == nullptr;  // model.odin:149-158
     if (!tied) want.push_back({"output.weight", c.vocab_size, D, false, nullptr});
+    std::vector<int> kinds((size_t)c.n_layers);
+    std::vector<char> shared((size_t)c.n_layers, 0);
     for (int64_t l = 0; l < c.n_layers; l++) {
         const std::string p = "blk." + std::to_string(l) + ".";
+        // qwen3_5/model.odin:289-300: full attention at layers interval-1, 2 interval-1, ...
+        const int kind = e->arch != 2 ? LK_QWEN3 : ((l + 1) % e->full_interval == 0 ? LK_FULL : LK_LINEAR);
+        kinds[(size_t)l] = kind;
         want.push_back({p + "attn_norm.weight", 1, D, true, nullptr});
-        want.push_back({p + "ffn_norm.weight", 1, D, true, nullptr});
-        want.push_back({p + "attn_q_norm.weight", 1, c.head_dim, true, nullptr});
-        want.push_back({p + "attn_k_norm.weight", 1, c.head_dim, true, nullptr});
-        want.push_back({p + "attn_q.weight", QD, D, false, nullptr});
-        want.push_back({p + "attn_k.weight", KVD, D, false, nullptr});
-        want.push_back({p + "attn_v.weight", KVD, D, false, nullptr});
-        want.push_back({p + "attn_output.weight", D, QD, false, nullptr});
-        want.push_back({p + "ffn_gate.weight", H, D, false, nullptr});
-        want.push_back({p + "ffn_down.weight", D, H, false, nullptr});
-        want.push_back({p + "ffn_up.weight", H, D, false, nullptr});
+        want.push_back({p + (e->arch == 2 ? "post_attention_norm.weight" : "ffn_norm.weight"), 1, D, true, nullptr});
+        if (kind != LK_LINEAR) {
+            want.push_back({p + "attn_q_norm.weight", 1, c.head_dim, true, nullptr});
+            want.push_back({p + "attn_k_norm.weight", 1, c.head_dim, true, nullptr});
+            want.push_back({p + "attn_q.weight", kind == LK_FULL ? 2 * QD : QD, D, false, nullptr});
+            want.push_back({p + "attn_k.weight", KVD, D, false, nullptr});
+            want.push_back({p + "attn_v.weight", KVD, D, false, nullptr});
+            want.push_back({p + "attn_output.weight", D, QD, false, nullptr});
+        } else {
+            want.push_back({p + "attn_qkv.weight", CD, D, false, nullptr});
+            want.push_back({p + "attn_gate.weight", VD, D, false, nullptr});
+            want.push_back({p + "ssm_beta.weight", e->lin_nv, D, false, nullptr});
+            want.push_back({p + "ssm_alpha.weight", e->lin_nv, D, false, nullptr});
+            want.push_back({p + "ssm_conv1d.weight", CD, e->lin_kernel, true, nullptr});
+            want.push_back({p + "ssm_dt.bias", 1, e->lin_nv, true, nullptr});
+            want.push_back({p + "ssm_a", 1, e->lin_nv, true, nullptr});
+            want.push_back({p + "ssm_norm.weight", 1, e->lin_hv, true, nullptr});
+            want.push_back({p + "ssm_out.weight", D, VD, false, nullptr});
+        }
+        if (!moe) {
+            want.push_back({p + "ffn_gate.weight", H, D, false, nullptr});
+            want.push_back({p + "ffn_down.weight", D, H, false, nullptr});
+            want.push_back({p + "ffn_up.weight", H, D, false, nullptr});
+        } else {
+            want.push_back({p + "ffn_gate_inp.weight", E, D, false, nullptr});
+            want.push_back({p + "ffn_gate_exps.weight", E * EF, D, false, nullptr});
+            want.push_back({p + "ffn_up_exps.weight", E * EF, D, false, nullptr});
+            want.push_back({p + "ffn_down_exps.weight", E * D, EF, false, nullptr});
+            if (SF > 0 && g.tensor(p + "ffn_gate_inp_shexp.weight")) {
+                shared[(size_t)l] = 1;
+                want.push_back({p + "ffn_gate_inp_shexp.weight", 1, D, false, nullptr});
+                want.push_back({p + "ffn_gate_shexp.weight", SF, D, false, nullptr});
+                want.push_back({p + "ffn_up_shexp.weight", SF, D, false, nullptr});
+                want.push_back({p + "ffn_down_shexp.weight", D, SF, false, nullptr});
+            }
+        }
     }
     size_t wbytes = 0;
     for (auto &w : want) {
@@ -480,15 +572,21 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
         wbytes += ((size_t)w.t->nbytes + 255) & ~(size_t)255;
     }
     e->weight_bytes = wbytes;
+    e->n_experts = E;
     if ((rc = check_device(opts->device))) return rc;
 
     // device memory plan
+    int n_attn = 0, n_lin = 0;
+    for (int k : kinds) (k == LK_LINEAR ? n_lin : n_attn)++;
     e->chunk = attn_chunk((int)c.head_dim);
     e->max_splits = (int)((c.seq_len + e->chunk - 1) / e->chunk);
     if (e->max_splits > attn_max_splits())
         return fail(OI_E_UNSUPPORTED, "seq_len " + std::to_string(c.seq_len) + " exceeds the attention kernel's " +
                                           std::to_string(attn_max_splits() * e->chunk) + " positions");
+    const int q35_splits = e->arch == 2 ? q35_max_splits((int)c.seq_len) : 0;
     const size_t kv_layer = (size_t)c.n_kv_heads * c.seq_len * c.head_dim * 2;
+    const size_t conv_layer = (size_t)CD * (e->lin_kernel > 0 ? e->lin_kernel - 1 : 0) * 4;
+    const size_t rec_layer = (size_t)e->lin_nv * e->lin_hk * e->lin_hv * 4;
     auto al = [](size_t n) { return (n + 255) & ~(size_t)255; };
     const size_t out_rows = (size_t)c.vocab_size;
     GemvArgs probe = gemv_args(GEMV_ARGMAX, (int)D, nullptr, nullptr, 0.f);
@@ -497,12 +595,18 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     probe.seg[0].m.rows = (int32_t)out_rows;
     probe.seg[0].m.cols = (int32_t)D;
     plan_gemv(probe);
-    size_t act = al(D * 4) + al(QD * 4) + 2 * al(KVD * 4) + al(QD * 4) + al(H * 4) + al(out_rows * 4) +
-                 al((size_t)c.n_heads * e->max_splits * (c.head_dim + 4) * 4) + 2 * al((size_t)probe.total_wgs * 4) +
-                 2 * al((size_t)probe.total_wgs * 4) + al(ST_WORDS * 4) +
-                 al((size_t)(c.seq_len + 1) * 4) +
+    const size_t hb_n = std::max<size_t>({(size_t)H, (size_t)(e->top_k * EF), (size_t)SF, 1});
+    const size_t part_n = std::max((size_t)c.n_heads * e->max_splits * (c.head_dim + 4),
+                                   (size_t)c.n_heads * q35_splits * (c.head_dim + 2));
+    size_t act = al(D * 4) + al(2 * QD * 4) + 2 * al(KVD * 4) + al(QD * 4) + al(hb_n * 4) + al(out_rows * 4) +
+                 al(part_n * 4) + 2 * al((size_t)probe.total_wgs * 4) +
+                 al(ST_WORDS * 4) + al((size_t)(c.seq_len + 1) * 4) +
                  al((size_t)c.seq_len * (c.head_dim / 2) * 8);
-    e->arena.size = wbytes + 2 * kv_layer * c.n_layers + act + 4096;
+    if (e->arch == 2)
+        act += al(QD * 4) + al((size_t)(e->rotary_dim / 2 + 1) * 4) + 2 * al((size_t)CD * 4) + 2 * al((size_t)VD * 4) +
+               2 * al((size_t)e->lin_nv * 4);
+    if (moe) act += al((size_t)E * 4) + 3 * al(64 * 4) + al((size_t)SF * 4 + 4);
+    e->arena.size = wbytes + 2 * kv_layer * n_attn + (conv_layer + rec_layer + 512) * n_lin + act + 8192;
     hipError_t he = hipMalloc(&e->arena.base, e->arena.size);
     if (he != hipSuccess) return fail(OI_E_NOMEM, "hipMalloc of " + std::to_string(e->arena.size) + " bytes failed");
     HIP_TRY(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking));
@@ -525,37 +629,93 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     e->output_norm = f32s[wi++];
     e->output = tied ? e->tok_embd : mats[wi++];
     e->layers.resize((size_t)c.n_layers);
-    for (auto &L : e->layers) {
+    for (size_t l = 0; l < e->layers.size(); l++) {
+        LayerDev &L = e->layers[l];
+        L.kind = kinds[l];
+        L.moe = moe;
+        L.shared = shared[l] != 0;
         L.attn_norm = f32s[wi++];
         L.ffn_norm = f32s[wi++];
-        L.q_norm = f32s[wi++];
-        L.k_norm = f32s[wi++];
-        L.wq = mats[wi++];
-        L.wk = mats[wi++];
-        L.wv = mats[wi++];
-        L.wo = mats[wi++];
-        L.w1 = mats[wi++];
-        L.w2 = mats[wi++];
-        L.w3 = mats[wi++];
+        if (L.kind != LK_LINEAR) {
+            L.q_norm = f32s[wi++];
+            L.k_norm = f32s[wi++];
+            L.wq = mats[wi++];
+            L.wk = mats[wi++];
+            L.wv = mats[wi++];
+            L.wo = mats[wi++];
+        } else {
+            L.in_qkv = mats[wi++];
+            L.in_z = mats[wi++];
+            L.in_b = mats[wi++];
+            L.in_a = mats[wi++];
+            L.conv_w = f32s[wi++];
+            L.dt_bias = f32s[wi++];
+            L.ssm_a = f32s[wi++];
+            L.ssm_norm = f32s[wi++];
+            L.ssm_out = mats[wi++];
+        }
+        if (!moe) {
+            L.w1 = mats[wi++];
+            L.w2 = mats[wi++];
+            L.w3 = mats[wi++];
+        } else {
+            L.router = mats[wi++];
+            L.gexp = mats[wi++];
+            L.uexp = mats[wi++];
+            L.dexp = mats[wi++];
+            if (L.shared) {
+                L.sh_inp = mats[wi++];
+                L.sh_gate = mats[wi++];
+                L.sh_up = mats[wi++];
+                L.sh_down = mats[wi++];
+            }
+        }
     }
     for (auto &L : e->layers) {
-        L.kc = (uint16_t *)e->arena.take(kv_layer);
-        L.vc = (uint16_t *)e->arena.take(kv_layer);
+        if (L.kind != LK_LINEAR) {
+            L.kc = (uint16_t *)e->arena.take(kv_layer);
+            L.vc = (uint16_t *)e->arena.take(kv_layer);
+        } else {
+            L.conv_state = (float *)e->arena.take(conv_layer + 4);
+            L.rec_state = (float *)e->arena.take(rec_layer);
+        }
     }
     e->x = (float *)e->arena.take(D * 4);
-    e->q = (float *)e->arena.take(QD * 4);
+    e->q = (float *)e->arena.take(2 * QD * 4);  // q, or [q | gate] per head (Qwen3.5)
     e->k = (float *)e->arena.take(KVD * 4);
     e->v = (float *)e->arena.take(KVD * 4);
     e->att = (float *)e->arena.take(QD * 4);
-    e->hb = (float *)e->arena.take(H * 4);
+    e->hb = (float *)e->arena.take(hb_n * 4);
     e->logits = (float *)e->arena.take(out_rows * 4);
-    e->part = (float *)e->arena.take((size_t)c.n_heads * e->max_splits * (c.head_dim + 4) * 4);
+    e->part = (float *)e->arena.take(part_n * 4);
     e->am_val = (float *)e->arena.take((size_t)probe.total_wgs * 4);
     e->am_idx = (int32_t *)e->arena.take((size_t)probe.total_wgs * 4);
     e->state = (int32_t *)e->arena.take(ST_WORDS * 4);
     e->tokens = (int32_t *)e->arena.take((size_t)(c.seq_len + 1) * 4);
     e->rope_cs = (float2 *)e->arena.take((size_t)c.seq_len * (c.head_dim / 2) * 8);
-    if (!e->rope_cs) return fail(OI_E_NOMEM, "arena exhausted (activations)");
+    float *qbuf = nullptr, *inv_freq = nullptr, *lin_qkv = nullptr, *lin_conv = nullptr, *lin_z = nullptr;
+    float *lin_out = nullptr, *lin_b = nullptr, *lin_a = nullptr;
+    if (e->arch == 2) {
+        qbuf = (float *)e->arena.take(QD * 4);
+        inv_freq = (float *)e->arena.take((size_t)(e->rotary_dim / 2 + 1) * 4);
+        lin_qkv = (float *)e->arena.take((size_t)CD * 4);
+        lin_conv = (float *)e->arena.take((size_t)CD * 4);
+        lin_z = (float *)e->arena.take((size_t)VD * 4);
+        lin_out = (float *)e->arena.take((size_t)VD * 4);
+        lin_b = (float *)e->arena.take((size_t)e->lin_nv * 4);
+        lin_a = (float *)e->arena.take((size_t)e->lin_nv * 4);
+    }
+    float *mo_logits = nullptr, *mo_w = nullptr, *mo_sg = nullptr;
+    int32_t *mo_ids = nullptr;
+    if (moe) {
+        mo_logits = (float *)e->arena.take((size_t)E * 4);
+        mo_ids = (int32_t *)e->arena.take(64 * 4);
+        mo_w = (float *)e->arena.take(64 * 4);
+        mo_sg = (float *)e->arena.take(64 * 4);
+    }
+    float *sh_h = moe ? (float *)e->arena.take((size_t)SF * 4 + 4) : nullptr;
+    if (!e->rope_cs || (e->arch == 2 && !lin_a) || (moe && !sh_h))
+        return fail(OI_E_NOMEM, "arena exhausted (activations)");
 
     // RoPE table, same f32 formula as infer/forward.odin:127-130
     {
@@ -571,75 +731,222 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
         HIP_TRY(hipMemcpyAsync(e->rope_cs, cs.data(), cs.size() * 8, hipMemcpyHostToDevice, e->stream));
         HIP_TRY(hipStreamSynchronize(e->stream));
     }
+    if (e->arch == 2) {  // partial-rotary inverse frequencies (qwen3_5/ops.odin:163-168)
+        const int half = (int)e->rotary_dim / 2;
+        std::vector<float> inv((size_t)half + 1, 0.f);
+        const float rd = (float)e->rotary_dim;
+        for (int i = 0; i < half; i++) inv[(size_t)i] = 1.0f / powf(c.rope_freq, (float)i / (rd / 2.0f));
+        HIP_TRY(hipMemcpyAsync(inv_freq, inv.data(), inv.size() * 4, hipMemcpyHostToDevice, e->stream));
+        HIP_TRY(hipStreamSynchronize(e->stream));
+    }
     HIP_TRY(hipHostMalloc((void **)&e->logits_host, out_rows * 4, hipHostMallocDefault));
     HIP_TRY(hipHostMalloc((void **)&e->state_host, ST_WORDS * 4, hipHostMallocDefault));
 
     // launch plans
     const float eps = c.rms_eps;
+    auto mbytes = [](const DMat &m) {
+        size_t b = 0;
+        matrix_bytes((uint32_t)m.type, m.rows, m.cols, b);
+        return (double)b;
+    };
+    auto gemv_op = [&](int role, GemvArgs ga) -> Op {
+        Op o;
+        o.kind = OP_GEMV;
+        o.role = role;
+        if (!plan_gemv(ga)) fail(OI_E_DEVICE, "internal: GEMV plan");
+        o.g = ga;
+        const int n = ga.mode == GEMV_SWIGLU ? 2 : ga.nseg;
+        double rows = 0;
+        for (int i = 0; i < n; i++) {
+            o.bytes += mbytes(ga.seg[i].m);
+            rows += ga.seg[i].m.rows;
+        }
+        o.bytes += 4.0 * ga.K + (ga.norm_w ? 4.0 * ga.K : 0) + 4.0 * (ga.mode == GEMV_SWIGLU ? rows / 2 : rows) *
+                                                               (ga.mode == GEMV_ADD ? 2 : 1);
+        return o;
+    };
+    e->ops.assign((size_t)c.n_layers, {});
     for (size_t l = 0; l < e->layers.size(); l++) {
         LayerDev &L = e->layers[l];
-        GemvArgs a = gemv_args(GEMV_STORE, (int)D, e->x, L.attn_norm, eps);
-        a.nseg = 3;
-        a.seg[0].m = L.wq; a.seg[0].y = e->q;
-        a.seg[1].m = L.wk; a.seg[1].y = e->k;
-        a.seg[2].m = L.wv; a.seg[2].y = e->v;
-        plan_gemv(a);
-        e->g_qkv.push_back(a);
-
-        AttnArgs t{};
-        t.q = e->q; t.k = e->k; t.v = e->v;
-        t.q_norm = L.q_norm; t.k_norm = L.k_norm; t.eps = eps;
-        t.seq_len = (int32_t)c.seq_len;
-        t.rope_cs = e->rope_cs;
-        t.kc = L.kc; t.vc = L.vc;
-        t.state = e->state;
-        t.chunk = e->chunk;
-        t.max_splits = e->max_splits;
-        t.part = e->part;
-        t.out = e->att;
-        t.n_heads = (int32_t)c.n_heads;
-        t.n_kv_heads = (int32_t)c.n_kv_heads;
-        e->a_attn.push_back(t);
-
-        a = gemv_args(GEMV_ADD, (int)QD, e->att, nullptr, eps);
-        a.nseg = 1;
-        a.seg[0].m = L.wo; a.seg[0].y = e->x;
-        plan_gemv(a);
-        e->g_wo.push_back(a);
-
-        a = gemv_args(GEMV_SWIGLU, (int)D, e->x, L.ffn_norm, eps);
-        a.nseg = 2;
-        a.seg[0].m = L.w1; a.seg[0].y = e->hb;
-        a.seg[1].m = L.w3; a.seg[1].y = e->hb;
-        plan_gemv(a);
-        e->g_gateup.push_back(a);
-
-        a = gemv_args(GEMV_ADD, (int)H, e->hb, nullptr, eps);
-        a.nseg = 1;
-        a.seg[0].m = L.w2; a.seg[0].y = e->x;
-        plan_gemv(a);
-        e->g_down.push_back(a);
+        std::vector<Op> &ops = e->ops[l];
+        if (L.kind == LK_QWEN3 || L.kind == LK_FULL) {
+            GemvArgs q = gemv_args(GEMV_STORE, (int)D, e->x, L.attn_norm, eps);
+            q.nseg = 3;
+            q.seg[0].m = L.wq; q.seg[0].y = e->q;
+            q.seg[1].m = L.wk; q.seg[1].y = e->k;
+            q.seg[2].m = L.wv; q.seg[2].y = e->v;
+            ops.push_back(gemv_op(K_QKV, q));
+            Op at;
+            at.role = K_ATTN;
+            at.bytes = (QD * 2.0 + 2 * KVD) * 4 + 2.0 * c.head_dim * 4 + 2.0 * KVD * 2;
+            if (L.kind == LK_QWEN3) {
+                at.kind = OP_ATTN;
+                AttnArgs &t = at.at;
+                t.q = e->q; t.k = e->k; t.v = e->v;
+                t.q_norm = L.q_norm; t.k_norm = L.k_norm; t.eps = eps;
+                t.seq_len = (int32_t)c.seq_len;
+                t.rope_cs = e->rope_cs;
+                t.kc = L.kc; t.vc = L.vc;
+                t.state = e->state;
+                t.chunk = e->chunk;
+                t.max_splits = e->max_splits;
+                t.part = e->part;
+                t.out = e->att;
+                t.n_heads = (int32_t)c.n_heads;
+                t.n_kv_heads = (int32_t)c.n_kv_heads;
+            } else {
+                at.kind = OP_Q35;
+                Q35Args &t = at.q;
+                t.qproj = e->q; t.k = e->k; t.v = e->v;
+                t.q_norm = L.q_norm; t.k_norm = L.k_norm;
+                t.inv_freq = inv_freq;
+                t.eps = eps;
+                t.rotary_dim = (int32_t)e->rotary_dim;
+                t.pos = 0;
+                t.state = e->state;  // pos from the device state
+                t.seq_len = (int32_t)c.seq_len;
+                t.n_heads = (int32_t)c.n_heads;
+                t.n_kv_heads = (int32_t)c.n_kv_heads;
+                t.max_splits = q35_splits;
+                t.kc = L.kc; t.vc = L.vc;
+                t.qbuf = qbuf;
+                t.part = e->part;
+                t.out = e->att;
+            }
+            ops.push_back(at);
+            GemvArgs o = gemv_args(GEMV_ADD, (int)QD, e->att, nullptr, eps);
+            o.nseg = 1;
+            o.seg[0].m = L.wo; o.seg[0].y = e->x;
+            ops.push_back(gemv_op(K_WO, o));
+        } else {
+            GemvArgs in = gemv_args(GEMV_STORE, (int)D, e->x, L.attn_norm, eps);
+            in.nseg = 4;
+            in.seg[0].m = L.in_qkv; in.seg[0].y = lin_qkv;
+            in.seg[1].m = L.in_z; in.seg[1].y = lin_z;
+            in.seg[2].m = L.in_b; in.seg[2].y = lin_b;
+            in.seg[3].m = L.in_a; in.seg[3].y = lin_a;
+            ops.push_back(gemv_op(K_LIN_IN, in));
+            Op dn;
+            dn.kind = OP_DN;
+            dn.role = K_DELTANET;
+            DnArgs &t = dn.dn;
+            t.qkv = lin_qkv; t.z = lin_z; t.b = lin_b; t.a = lin_a;
+            t.conv_w = L.conv_w; t.a_decay = L.ssm_a; t.dt_bias = L.dt_bias; t.norm_w = L.ssm_norm;
+            t.eps = eps;
+            t.conv_state = L.conv_state;
+            t.state = L.rec_state;
+            t.conv_out = lin_conv;
+            t.out = lin_out;
+            t.n_kh = (int32_t)e->lin_nk; t.n_vh = (int32_t)e->lin_nv;
+            t.hk = (int32_t)e->lin_hk; t.hv = (int32_t)e->lin_hv; t.kernel = (int32_t)e->lin_kernel;
+            dn.bytes = 2.0 * rec_layer + 2.0 * conv_layer + (double)CD * e->lin_kernel * 4 + (CD + 3.0 * VD) * 4;
+            ops.push_back(dn);
+            GemvArgs o = gemv_args(GEMV_ADD, (int)VD, lin_out, nullptr, eps);
+            o.nseg = 1;
+            o.seg[0].m = L.ssm_out; o.seg[0].y = e->x;
+            ops.push_back(gemv_op(K_LIN_OUT, o));
+        }
+        if (!L.moe) {
+            GemvArgs gu = gemv_args(GEMV_SWIGLU, (int)D, e->x, L.ffn_norm, eps);
+            gu.nseg = 2;
+            gu.seg[0].m = L.w1; gu.seg[0].y = e->hb;
+            gu.seg[1].m = L.w3; gu.seg[1].y = e->hb;
+            ops.push_back(gemv_op(K_GATEUP, gu));
+            GemvArgs dw = gemv_args(GEMV_ADD, (int)H, e->hb, nullptr, eps);
+            dw.nseg = 1;
+            dw.seg[0].m = L.w2; dw.seg[0].y = e->x;
+            ops.push_back(gemv_op(K_DOWN, dw));
+            continue;
+        }
+        // routed experts: router (+ the shared expert's gate row), the chosen
+        // experts' gate/up with the routing in its prologue, the shared expert's
+        // gate/up, then the two down projections adding into x (the shared one
+        // scaled by sigmoid of its gate)
+        GemvArgs r = gemv_args(GEMV_STORE, (int)D, e->x, L.ffn_norm, eps);
+        r.nseg = L.shared ? 2 : 1;
+        r.seg[0].m = L.router; r.seg[0].y = mo_logits;
+        if (L.shared) { r.seg[1].m = L.sh_inp; r.seg[1].y = mo_sg; }
+        ops.push_back(gemv_op(K_ROUTER, r));
+        Op gu;
+        gu.kind = OP_MOE_ROWS;
+        gu.role = K_GATEUP;
+        GemvArgs &ga = gu.g;
+        ga = gemv_args(GEMV_SWIGLU, (int)D, e->x, L.ffn_norm, eps);
+        ga.nseg = 2;
+        ga.seg[0].m = L.gexp; ga.seg[1].m = L.uexp;
+        ga.seg[0].m.rows = ga.seg[1].m.rows = (int32_t)(e->top_k * EF);  // the chosen experts' rows
+        ga.seg[0].y = ga.seg[1].y = e->hb;
+        ga.moe_logits = mo_logits;
+        ga.moe_ids_out = mo_ids;
+        ga.moe_w_out = mo_w;
+        ga.moe_norm = 1;  // Qwen3-MoE / Qwen3-Next renormalize the chosen weights
+        ga.moe_k = (int32_t)e->top_k;
+        ga.moe_n = (int32_t)E;
+        ga.moe_blk = (int32_t)EF;
+        if (!gemv_q_moe_supported(ga, MOE_ROWS))
+            return fail(OI_E_UNSUPPORTED, "routed experts: type or shape not supported by the expert GEMV "
+                                          "(Q4_K / Q6_K / Q8_0, dim <= 4096, inner a multiple of 256)");
+        plan_gemv_q(ga);
+        gu.bytes = 2.0 * e->top_k * mbytes(L.gexp) / E + mbytes(L.router) * 0 + 4.0 * D + 4.0 * E + 4.0 * e->top_k * EF;
+        ops.push_back(gu);
+        // the shared expert's gate/up reads the same normalized x, so it runs
+        // before either down projection adds into x
+        if (L.shared) {
+            GemvArgs su = gemv_args(GEMV_SWIGLU, (int)D, e->x, L.ffn_norm, eps);
+            su.nseg = 2;
+            su.seg[0].m = L.sh_gate; su.seg[0].y = sh_h;
+            su.seg[1].m = L.sh_up; su.seg[1].y = sh_h;
+            ops.push_back(gemv_op(K_SHARED, su));
+        }
+        Op dn;
+        dn.kind = OP_MOE_COLS;
+        dn.role = K_DOWN;
+        GemvArgs &gd = dn.g;
+        gd = gemv_args(GEMV_ADD, (int)(e->top_k * EF), e->hb, nullptr, eps);
+        gd.nseg = 1;
+        gd.seg[0].m = L.dexp;
+        gd.seg[0].m.rows = (int32_t)D;  // row r of every expert
+        gd.seg[0].y = e->x;
+        gd.moe_ids = mo_ids;
+        gd.moe_w = mo_w;
+        gd.moe_k = (int32_t)e->top_k;
+        gd.moe_n = (int32_t)E;
+        gd.moe_blk = (int32_t)(EF / 64);
+        if (!gemv_q_moe_supported(gd, MOE_COLS))
+            return fail(OI_E_UNSUPPORTED, "routed experts: down projection not supported by the expert GEMV");
+        plan_gemv_q(gd);
+        dn.bytes = e->top_k * mbytes(L.dexp) / E + 4.0 * e->top_k * EF + 8.0 * D;
+        ops.push_back(dn);
+        if (L.shared) {
+            GemvArgs sd = gemv_args(GEMV_ADD, (int)SF, sh_h, nullptr, eps);
+            sd.nseg = 1;
+            sd.seg[0].m = L.sh_down; sd.seg[0].y = e->x;
+            sd.ygate = mo_sg;  // x += sigmoid(gate . x) * shared(x)
+            ops.push_back(gemv_op(K_SHARED, sd));
+        }
     }
-    GemvArgs a = gemv_args(GEMV_ARGMAX, (int)D, e->x, e->output_norm, eps);
-    a.nseg = 1;
-    a.seg[0].m = e->output; a.seg[0].y = e->logits;
-    plan_gemv(a);
-    a.am_val = e->am_val;
-    a.am_idx = e->am_idx;
-    a.state = e->state;
-    if (a.total_wgs != probe.total_wgs) return fail(OI_E_DEVICE, "internal: output plan mismatch");
-    e->n_partials = a.total_wgs;
-    e->g_out = a;
+    if (!g_err.empty() && g_err == "internal: GEMV plan") return OI_E_DEVICE;
+    GemvArgs ao = gemv_args(GEMV_ARGMAX, (int)D, e->x, e->output_norm, eps);
+    ao.nseg = 1;
+    ao.seg[0].m = e->output; ao.seg[0].y = e->logits;
+    plan_gemv(ao);
+    ao.am_val = e->am_val;
+    ao.am_idx = e->am_idx;
+    ao.state = e->state;
+    if (ao.total_wgs != probe.total_wgs) return fail(OI_E_DEVICE, "internal: output plan mismatch");
+    e->n_partials = ao.total_wgs;
+    e->g_out = ao;
     const char *ng = std::getenv("OI_NO_GRAPH");
     e->use_graph = !(ng && ng[0] == '1');
     const char *pu = std::getenv("OI_PREFILL_UNFUSED");
     e->pf_fused = !(pu && pu[0] == '1');
 
-    std::printf("model: dim=%lld layers=%lld heads=%lld/%lld hidden=%lld vocab=%lld ctx=%lld/%lld  weights=%.0f MB  "
-                "KV cache (f16)=%.0f MB  [gfx950]\n",
-                (long long)c.dim, (long long)c.n_layers, (long long)c.n_heads, (long long)c.n_kv_heads,
-                (long long)c.hidden_dim, (long long)c.vocab_size, (long long)c.seq_len, (long long)c.max_seq,
-                wbytes / 1048576.0, 2.0 * kv_layer * c.n_layers / 1048576.0);
+    std::printf("model: %s dim=%lld layers=%lld (attention %d, linear %d) heads=%lld/%lld hidden=%lld vocab=%lld "
+                "ctx=%lld/%lld experts=%lld/%lld  weights=%.0f MB  KV cache (f16)=%.0f MB  [gfx950]\n",
+                e->arch == 0 ? "qwen3" : arch.c_str(), (long long)c.dim, (long long)c.n_layers, n_attn, n_lin,
+                (long long)c.n_heads, (long long)c.n_kv_heads, (long long)c.hidden_dim, (long long)c.vocab_size,
+                (long long)c.seq_len, (long long)c.max_seq, (long long)e->top_k, (long long)E, wbytes / 1048576.0,
+                2.0 * kv_layer * n_attn / 1048576.0);
     HIP_TRY(hipStreamSynchronize(e->stream));
     *out = e.release();
     return OI_OK;
@@ -690,6 +997,10 @@ constexpr int PF_MAX_T = 512;
 namespace {
 
 bool prefill_batched_ok(const oi_engine *e) {
+    // the batched path covers the dense decoder; the routed-expert and hybrid
+    // layouts run their prompts token by token (the reference's fallback,
+    // qwen3_5/engine.odin:86-91)
+    if (e->arch != 0) return false;
     if ((e->cfg.head_dim != 128 && e->cfg.head_dim != 256) || e->cfg.dim > 16384) return false;
     for (const LayerDev &L : e->layers)
         for (const DMat *m : {&L.wq, &L.wk, &L.wv, &L.wo, &L.w1, &L.w2, &L.w3})
@@ -884,7 +1195,7 @@ int oi_engine_kv_fill(oi_engine *e, int32_t layer0, int32_t nlayers, int32_t pos
     HIP_TRY(hipSetDevice(e->device));
     const size_t hd = (size_t)c.head_dim;
     for (int l = 0; l < nlayers; l++)
-        for (int h = 0; h < c.n_kv_heads; h++) {
+        for (int h = 0; h < c.n_kv_heads && e->layers[(size_t)(layer0 + l)].kc; h++) {  // DeltaNet layers: no cache
             const size_t src = (((size_t)l * c.n_kv_heads + h) * npos) * hd;
             const size_t dst = ((size_t)h * c.seq_len + pos0) * hd;
             HIP_TRY(hipMemcpyAsync(e->layers[(size_t)(layer0 + l)].kc + dst, k + src, (size_t)npos * hd * 2,
@@ -896,50 +1207,64 @@ int oi_engine_kv_fill(oi_engine *e, int32_t layer0, int32_t nlayers, int32_t pos
     return OI_OK;
 }
 
+int oi_engine_reset_state(oi_engine *e) {
+    if (!e) return fail(OI_E_ARG, "null engine");
+    HIP_TRY(hipSetDevice(e->device));
+    const oi_config &c = e->cfg;
+    const size_t kv_layer = (size_t)c.n_kv_heads * c.seq_len * c.head_dim * 2;
+    const size_t conv_layer = (size_t)(2 * e->lin_nk * e->lin_hk + e->lin_nv * e->lin_hv) *
+                              (e->lin_kernel > 0 ? e->lin_kernel - 1 : 0) * 4;
+    const size_t rec_layer = (size_t)e->lin_nv * e->lin_hk * e->lin_hv * 4;
+    for (const LayerDev &L : e->layers) {
+        if (L.kc) HIP_TRY(hipMemsetAsync(L.kc, 0, kv_layer, e->stream));
+        if (L.vc) HIP_TRY(hipMemsetAsync(L.vc, 0, kv_layer, e->stream));
+        if (L.conv_state && conv_layer) HIP_TRY(hipMemsetAsync(L.conv_state, 0, conv_layer, e->stream));
+        if (L.rec_state) HIP_TRY(hipMemsetAsync(L.rec_state, 0, rec_layer, e->stream));
+    }
+    HIP_TRY(hipStreamSynchronize(e->stream));
+    e->last_pos = 0;
+    return OI_OK;
+}
+
 const float *oi_engine_logits_device(oi_engine *e) { return e ? e->logits : nullptr; }
 void *oi_engine_stream(oi_engine *e) { return e ? (void *)e->stream : nullptr; }
 
 int oi_engine_time_kernel(oi_engine *e, int32_t kernel, int32_t iters, double *avg_us, double *bytes) {
-    if (!e || !avg_us || !bytes || iters <= 0 || kernel < K_QKV || kernel > K_TOKEN)
+    if (!e || !avg_us || !bytes || iters <= 0 || kernel < K_QKV || kernel > K_LAST)
         return fail(OI_E_ARG, "bad argument");
     if (kernel == K_TOKEN) return time_token(e, iters, avg_us, bytes);
     HIP_TRY(hipSetDevice(e->device));
     const oi_config &c = e->cfg;
-    const size_t L = e->layers.size();
-    auto mat_bytes = [](const DMat &m) {
+    // the launches of this role in every layer, in layer order
+    std::vector<const Op *> sel;
+    for (const auto &layer : e->ops)
+        for (const Op &o : layer)
+            if (o.role == kernel) sel.push_back(&o);
+    Op out;
+    if (kernel == K_OUTPUT) {
+        out.g = e->g_out;
         size_t b = 0;
-        matrix_bytes((uint32_t)m.type, m.rows, m.cols, b);
-        return (double)b;
-    };
-    double per = 0;
-    const double D = (double)c.dim, H = (double)c.hidden_dim, QD = (double)(c.n_heads * c.head_dim),
-                 KVD = (double)(c.n_kv_heads * c.head_dim);
+        matrix_bytes((uint32_t)e->output.type, e->output.rows, e->output.cols, b);
+        out.bytes = (double)b + 8.0 * c.dim + 4.0 * c.vocab_size;
+        sel.push_back(&out);
+    }
+    if (sel.empty()) return fail(OI_E_ARG, "this model has no launch of that kernel");
     const double pos = e->last_pos;
     hipEvent_t e0, e1;
     HIP_TRY(hipEventCreate(&e0));
     HIP_TRY(hipEventCreate(&e1));
-    int rc = OI_OK;
-    auto run = [&](bool timed) -> int {
+    auto run = [&]() -> int {
         for (int it = 0; it < iters; it++) {
-            const size_t l = (size_t)it % L;
-            hipError_t r = hipSuccess;
-            switch (kernel) {
-            case K_QKV: r = launch_gemv(e->g_qkv[l], e->stream); break;
-            case K_ATTN: r = launch_attn(e->a_attn[l], (int)c.head_dim, e->stream); break;
-            case K_WO: r = launch_gemv(e->g_wo[l], e->stream); break;
-            case K_GATEUP: r = launch_gemv(e->g_gateup[l], e->stream); break;
-            case K_DOWN: r = launch_gemv(e->g_down[l], e->stream); break;
-            default: r = launch_gemv(e->g_out, e->stream); break;
-            }
+            const hipError_t r = launch_op(e, *sel[(size_t)it % sel.size()], e->stream);
             if (r != hipSuccess) return fail(OI_E_DEVICE, std::string("launch: ") + hipGetErrorString(r));
         }
-        (void)timed;
         return OI_OK;
     };
+    int rc;
     if ((rc = set_state(e, 0, e->last_pos, 0))) return rc;
-    if ((rc = run(false))) return rc;
+    if ((rc = run())) return rc;
     HIP_TRY(hipEventRecord(e0, e->stream));
-    if ((rc = run(true))) return rc;
+    if ((rc = run())) return rc;
     HIP_TRY(hipEventRecord(e1, e->stream));
     HIP_TRY(hipEventSynchronize(e1));
     float ms = 0;
@@ -947,16 +1272,16 @@ int oi_engine_time_kernel(oi_engine *e, int32_t kernel, int32_t iters, double *a
     hipEventDestroy(e0);
     hipEventDestroy(e1);
     *avg_us = ms * 1000.0 / iters;
-    const LayerDev &L0 = e->layers[0];
-    switch (kernel) {
-    case K_QKV: per = mat_bytes(L0.wq) + mat_bytes(L0.wk) + mat_bytes(L0.wv) + D * 8 + (QD + 2 * KVD) * 4; break;
-    case K_ATTN: per = 2.0 * KVD * 2 * (pos + 1) + (QD * 2 + 2 * KVD) * 4 + 2 * (c.head_dim + c.head_dim) * 4; break;
-    case K_WO: per = mat_bytes(L0.wo) + QD * 4 + D * 8; break;
-    case K_GATEUP: per = mat_bytes(L0.w1) + mat_bytes(L0.w3) + D * 8 + H * 4; break;
-    case K_DOWN: per = mat_bytes(L0.w2) + H * 4 + D * 8; break;
-    default: per = mat_bytes(e->output) + D * 8 + (double)c.vocab_size * 4; break;
+    // mean algorithmic bytes over the launches timed; attention adds the
+    // cache rows read at the timed position
+    double total = 0;
+    for (int it = 0; it < iters; it++) {
+        const Op &o = *sel[(size_t)it % sel.size()];
+        double b = o.bytes;
+        if (o.kind == OP_ATTN || o.kind == OP_Q35) b += 2.0 * c.n_kv_heads * c.head_dim * 2 * (pos + 1);
+        total += b;
     }
-    *bytes = per;
+    *bytes = total / iters;
     return OI_OK;
 }
 

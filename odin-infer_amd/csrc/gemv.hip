@@ -464,8 +464,10 @@ static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int 
     __syncthreads();
     {
         float *y = a.seg[seg].y;
+        // shared-expert gate: y += sigmoid(g) * Wx (the product first, then the scale)
+        const float gs = NM == 1 && a.mode == GEMV_ADD && a.ygate ? 1.0f / (1.0f + expf(-a.ygate[0])) : 1.f;
         for (int i = tid; i < wrow1 - wrow0; i += GW) {
-            if (NM == 1 && a.mode == GEMV_ADD) y[wrow0 + i] = y[wrow0 + i] + yo[i];
+            if (NM == 1 && a.mode == GEMV_ADD) y[wrow0 + i] = y[wrow0 + i] + (a.ygate ? yo[i] * gs : yo[i]);
             else y[wrow0 + i] = yo[i];
         }
     }
@@ -578,10 +580,9 @@ template <int T, int TL, int R, int NM, int XR, bool XU1, bool NORM, int MOE = 0
 __global__ __launch_bounds__(GW) void gemv_q_kernel(GemvArgs a) {
     const int wg = blockIdx.x + a.wg_base;
     int seg = 0;
-    if (NM == 1) {
-        if (a.nseg > 1 && wg >= a.seg[1].wg_begin) seg = 1;
-        if (a.nseg > 2 && wg >= a.seg[2].wg_begin) seg = 2;
-    }
+    if (NM == 1)
+        for (int i = 1; i < a.nseg; i++)
+            if (wg >= a.seg[i].wg_begin) seg = i;
     const int seg_end = (NM == 1 && seg + 1 < a.nseg) ? a.seg[seg + 1].wg_begin : a.total_wgs;
     const int nwg = seg_end - a.seg[seg].wg_begin, w = wg - a.seg[seg].wg_begin;
     const int ntiles = a.seg[seg].ntiles;
@@ -730,7 +731,7 @@ void plan_gemv_q(GemvArgs &a) {
     const int R = 1;
     (void)rows;
     a.rows_per_wg = gpw * R;
-    double bytes[3], total = 0;
+    double bytes[GEMV_MAX_SEG], total = 0;
     long total_tiles = 0;
     for (int i = 0; i < nseg; i++) {
         a.seg[i].ntiles = (a.seg[i].m.rows + a.rows_per_wg - 1) / a.rows_per_wg;
@@ -763,49 +764,59 @@ void plan_gemv_q(GemvArgs &a) {
     a.kernel = 1;
 }
 
-// routed experts: one weight type, no RMSNorm; MOE_ROWS is the SwiGLU pair,
-// MOE_COLS a single matrix whose experts' parts are whole super-blocks
+// routed experts: one weight type; MOE_ROWS is the SwiGLU pair (optionally
+// with the RMSNorm prologue), MOE_COLS a single matrix whose experts' parts
+// are whole super-blocks (store or residual add)
 template <int T, int MOE>
-static const void *gemv_q_moe_fn(int K) {
+static const void *gemv_q_moe_fn(int K, bool norm) {
     const bool xu1 = xu1_of(K);
     if (MOE == MOE_ROWS) {
         if (K > 4096) return nullptr;
+        if (norm) {
+            if (xu1) return (const void *)gemv_q_kernel<T, T, 1, 2, 1, true, true, MOE_ROWS>;
+            return (const void *)gemv_q_kernel<T, T, 1, 2, 1, false, true, MOE_ROWS>;
+        }
         if (xu1) return (const void *)gemv_q_kernel<T, T, 1, 2, 1, true, false, MOE_ROWS>;
         return (const void *)gemv_q_kernel<T, T, 1, 2, 1, false, false, MOE_ROWS>;
     }
+    if (norm) return nullptr;
     if (K <= 4096 && xu1) return (const void *)gemv_q_kernel<T, T, 1, 1, 1, true, false, MOE_COLS>;
     if (K <= 4096) return (const void *)gemv_q_kernel<T, T, 1, 1, 1, false, false, MOE_COLS>;
     if (K <= 12288) return (const void *)gemv_q_kernel<T, T, 1, 1, 3, false, false, MOE_COLS>;
     return nullptr;
 }
-static const void *gemv_q_moe_fn(int type, int moe, int K) {
+static const void *gemv_q_moe_fn(int type, int moe, int K, bool norm) {
     switch (type) {
-    case T_Q4_K: return moe == MOE_ROWS ? gemv_q_moe_fn<T_Q4_K, MOE_ROWS>(K) : gemv_q_moe_fn<T_Q4_K, MOE_COLS>(K);
-    case T_Q6_K: return moe == MOE_ROWS ? gemv_q_moe_fn<T_Q6_K, MOE_ROWS>(K) : gemv_q_moe_fn<T_Q6_K, MOE_COLS>(K);
-    case T_Q8_0: return moe == MOE_ROWS ? gemv_q_moe_fn<T_Q8_0, MOE_ROWS>(K) : gemv_q_moe_fn<T_Q8_0, MOE_COLS>(K);
+    case T_Q4_K:
+        return moe == MOE_ROWS ? gemv_q_moe_fn<T_Q4_K, MOE_ROWS>(K, norm) : gemv_q_moe_fn<T_Q4_K, MOE_COLS>(K, norm);
+    case T_Q6_K:
+        return moe == MOE_ROWS ? gemv_q_moe_fn<T_Q6_K, MOE_ROWS>(K, norm) : gemv_q_moe_fn<T_Q6_K, MOE_COLS>(K, norm);
+    case T_Q8_0:
+        return moe == MOE_ROWS ? gemv_q_moe_fn<T_Q8_0, MOE_ROWS>(K, norm) : gemv_q_moe_fn<T_Q8_0, MOE_COLS>(K, norm);
     default: return nullptr;
     }
 }
 
 bool gemv_q_moe_supported(const GemvArgs &a, int moe) {
-    if (a.norm_w || a.moe_k < 1 || a.moe_k > WAVE || a.moe_n < 1 || a.moe_blk < 1) return false;
+    if ((a.norm_w && moe != MOE_ROWS) || a.moe_k < 1 || a.moe_k > WAVE || a.moe_n < 1 || a.moe_blk < 1) return false;
     if (moe == MOE_ROWS) {
         if (a.mode != GEMV_SWIGLU || a.seg[0].m.rows != a.moe_k * a.moe_blk) return false;
         if (a.moe_logits ? (a.moe_n > GW || a.moe_k > a.moe_n || !a.moe_ids_out || !a.moe_w_out) : !a.moe_ids)
             return false;
     } else if (moe == MOE_COLS) {
-        if (a.mode != GEMV_STORE || a.nseg != 1 || !a.moe_ids || !a.moe_w || a.moe_blk % 4 ||
+        if ((a.mode != GEMV_STORE && a.mode != GEMV_ADD) || a.nseg != 1 || !a.moe_ids || !a.moe_w || a.moe_blk % 4 ||
             a.K != a.moe_k * 64 * a.moe_blk ||
             a.seg[0].m.cols != 64 * a.moe_blk)
             return false;
     } else {
         return false;
     }
-    return gemv_q_supported(a) && gemv_q_moe_fn(a.seg[0].m.type, moe, a.K) != nullptr;
+    return gemv_q_supported(a) && gemv_q_moe_fn(a.seg[0].m.type, moe, a.K, a.norm_w != nullptr) != nullptr;
 }
 
 hipError_t launch_gemv_q_moe(const GemvArgs &a, int moe, hipStream_t st) {
-    const void *fn = gemv_q_moe_supported(a, moe) ? gemv_q_moe_fn(a.seg[0].m.type, moe, a.K) : nullptr;
+    const void *fn = gemv_q_moe_supported(a, moe) ? gemv_q_moe_fn(a.seg[0].m.type, moe, a.K, a.norm_w != nullptr)
+                                                   : nullptr;
     if (!fn) return hipErrorInvalidValue;
     GemvArgs b = a;
     b.wg_base = 0;

@@ -1,6 +1,7 @@
 // kernels.hip -- gfx950 kernels of the decode token loop.
 //
-//   gemv_kernel    GEMV for any device type (F32, F16, Q8_0, Q4_K, Q6_K) in
+//   gemv_kernel    GEMV for any device type (F32, F16, Q8_0, Q4_0, Q4_1, Q5_0,
+//                  Q5_1, Q4_K, Q6_K) in
 //                  float arithmetic, with the same fused prologue/epilogues as
 //                  gemv_q_kernel (gemv.hip), used where that one does not apply
 //                  (reference: infer/matmul.odin:77-109, ggml/quant.odin:76-282)
@@ -67,10 +68,54 @@ __device__ void decode_unit_q6k(const DMat &m, int row, int u, float *out) {
     }
 }
 
+// The 32-element block types kept in their GGUF layout (rows of cols/32
+// blocks of bb bytes): unit u is blocks 2u and 2u+1 of the row,
+// ggml/quant.odin:98-162 (separately rounded mul then add; element j and
+// j + 16 from the low and high nibble of byte j).
+__device__ void decode_unit_legacy(const DMat &m, int row, int u, float *out) {
+#pragma clang fp contract(off)
+    const int bb = m.type == T_Q4_0 ? 18 : m.type == T_Q4_1 ? 20 : m.type == T_Q5_0 ? 22 : 24;
+    const uint8_t *rowp = m.q + (size_t)row * (m.cols >> 5) * bb;
+    for (int h = 0; h < 2; h++) {
+        const uint8_t *b = rowp + (size_t)(2 * u + h) * bb;
+        const float d = h2f((uint32_t)b[0] | ((uint32_t)b[1] << 8));
+        float *o = out + 32 * h;
+        if (m.type == T_Q4_0) {
+            for (int j = 0; j < 16; j++) {
+                o[j] = (float)((int)(b[2 + j] & 0xF) - 8) * d;
+                o[j + 16] = (float)((int)(b[2 + j] >> 4) - 8) * d;
+            }
+        } else if (m.type == T_Q4_1) {
+            const float mn = h2f((uint32_t)b[2] | ((uint32_t)b[3] << 8));
+            for (int j = 0; j < 16; j++) {
+                o[j] = (float)(b[4 + j] & 0xF) * d + mn;
+                o[j + 16] = (float)(b[4 + j] >> 4) * d + mn;
+            }
+        } else {
+            const bool q51 = m.type == T_Q5_1;
+            const float mn = q51 ? h2f((uint32_t)b[2] | ((uint32_t)b[3] << 8)) : 0.f;
+            const uint8_t *qhp = b + (q51 ? 4 : 2), *qs = b + (q51 ? 8 : 6);
+            const uint32_t qh = (uint32_t)qhp[0] | (uint32_t)qhp[1] << 8 | (uint32_t)qhp[2] << 16 | (uint32_t)qhp[3] << 24;
+            for (int j = 0; j < 16; j++) {
+                const uint32_t xh0 = ((qh >> j) << 4) & 0x10u, xh1 = (qh >> (j + 12)) & 0x10u;
+                const int x0 = (int)((qs[j] & 0xFu) | xh0), x1 = (int)((qs[j] >> 4) | xh1);
+                if (q51) {
+                    o[j] = (float)x0 * d + mn;
+                    o[j + 16] = (float)x1 * d + mn;
+                } else {
+                    o[j] = (float)(x0 - 16) * d;
+                    o[j + 16] = (float)(x1 - 16) * d;
+                }
+            }
+        }
+    }
+}
+
 // Any type: decode unit u of `row` into out[64] (order: see unit_elem).
 __device__ void decode_unit(const DMat &m, int row, int u, float *out) {
 #pragma clang fp contract(off)
     switch (m.type) {
+    case T_Q4_0: case T_Q4_1: case T_Q5_0: case T_Q5_1: decode_unit_legacy(m, row, u, out); break;
     case T_Q4_K: decode_unit_q4k(m, row, u, out); break;
     case T_Q6_K: decode_unit_q6k(m, row, u, out); break;
     case T_Q8_0: {  // ggml/quant.odin:87-96
@@ -304,7 +349,8 @@ __global__ __launch_bounds__(WG) void gemv_kernel(GemvArgs a) {
     const int wg = blockIdx.x;
     int seg = 0;
     if (a.nseg > 1 && a.mode != GEMV_SWIGLU && wg >= a.seg[1].wg_begin) seg = 1;
-    if (a.nseg > 2 && wg >= a.seg[2].wg_begin) seg = 2;
+    for (int i = 2; i < a.nseg; i++)
+        if (wg >= a.seg[i].wg_begin) seg = i;
     const GemvSeg &S = a.seg[seg];
     const int lane = tid & (WAVE - 1), wave = tid / WAVE;
     const int lpr = a.lpr, gpw = WAVE / lpr;
@@ -338,7 +384,7 @@ __global__ __launch_bounds__(WG) void gemv_kernel(GemvArgs a) {
             const int row = rows[r];
             if (row >= S.m.rows) continue;
             if (a.mode == GEMV_ADD) {
-                S.y[row] += acc[r];
+                S.y[row] += a.ygate ? acc[r] * (1.0f / (1.0f + expf(-a.ygate[0]))) : acc[r];
             } else if (a.mode == GEMV_SWIGLU) {  // infer/forward.odin:188-193
                 float val = acc[r];
                 val *= 1.0f / (1.0f + expf(-val));
@@ -371,7 +417,7 @@ __global__ __launch_bounds__(WG) void gemv_kernel(GemvArgs a) {
 }
 
 bool plan_gemv(GemvArgs &a) {
-    if (a.K <= 0 || a.K % 64) return false;
+    if (a.K <= 0 || a.K % 64 || a.nseg < 1 || a.nseg > GEMV_MAX_SEG) return false;
     if (gemv_q_supported(a)) {
         plan_gemv_q(a);
         return true;
@@ -441,6 +487,10 @@ __device__ __forceinline__ DMat sub_rows(const DMat &m, int r0, int n) {
     case T_Q6_K: s.q += r * (m.cols >> 6) * 16; s.s += r * (m.cols >> 8) * 16; s.d += r * (m.cols >> 8); break;
     case T_Q8_0: s.q += r * (m.cols >> 6) * 16; s.d += r * (m.cols >> 5); break;
     case T_F16: s.q += r * m.cols * 2; break;
+    case T_Q4_0: s.q += r * (m.cols >> 5) * 18; break;
+    case T_Q4_1: s.q += r * (m.cols >> 5) * 20; break;
+    case T_Q5_0: s.q += r * (m.cols >> 5) * 22; break;
+    case T_Q5_1: s.q += r * (m.cols >> 5) * 24; break;
     default: s.q += r * m.cols * 4; break;
     }
     return s;

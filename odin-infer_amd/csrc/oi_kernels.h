@@ -7,7 +7,8 @@
 namespace oi {
 
 // ggml type ids (reference ggml/gguf.odin:27-42)
-enum : int32_t { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14 };
+enum : int32_t { T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q4_1 = 3, T_Q5_0 = 6, T_Q5_1 = 7, T_Q8_0 = 8, T_Q4_K = 12,
+                 T_Q6_K = 14 };
 
 // A weight matrix resident in HBM, in the GEMV layout.  Every row is cut into
 // U = cols/64 "units" of 64 consecutive weights; a unit is the work of one
@@ -29,6 +30,8 @@ enum : int32_t { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14 };
 //   Q8_0  unit u = blocks 2u, 2u+1: plane c = int8 values 16c .. 16c+15 of
 //         the unit;  d: f16 d per (row, block).
 //   F32/F16  q: the values, row-major.
+//   Q4_0/Q4_1/Q5_0/Q5_1  q: the GGUF blocks, row-major (decoded by the generic
+//         GEMV; the reference's CPU path reads them, ggml/quant.odin:98-162).
 struct DMat {
     int32_t type;
     int32_t rows;
@@ -42,7 +45,7 @@ struct DMat {
 
 enum GemvMode : int32_t {
     GEMV_STORE = 0,   // y[r] = W x
-    GEMV_ADD = 1,     // y[r] += W x            (residual epilogue)
+    GEMV_ADD = 1,     // y[r] += W x            (residual epilogue; y[r] += sigmoid(ygate[0]) W x with ygate)
     GEMV_SWIGLU = 2,  // y[r] = silu(Wg x) * (Wu x); seg[0]=gate, seg[1]=up
     GEMV_ARGMAX = 3   // y[r] = W x, then greedy argmax over all rows
 };
@@ -54,8 +57,10 @@ struct GemvSeg {
     int32_t ntiles;    // row tiles of this segment (gemv_q_kernel)
 };
 
+constexpr int GEMV_MAX_SEG = 4;
+
 struct GemvArgs {
-    GemvSeg seg[3];
+    GemvSeg seg[GEMV_MAX_SEG];
     int32_t nseg;
     int32_t mode;
     int32_t K;             // row length (all segments)
@@ -88,6 +93,9 @@ struct GemvArgs {
     int32_t *moe_ids_out;
     float *moe_w_out;
     int32_t moe_norm;
+    // GEMV_ADD: if set, the product is scaled by sigmoid(ygate[0]) before the add
+    // (the shared expert's gate of a Qwen3-Next-style MoE layer)
+    const float *ygate;
 };
 
 // Device state of the token loop (int32 x 8):
@@ -105,7 +113,7 @@ struct AttnArgs {
     const int32_t *state;      // pos = state[1]
     int32_t chunk;             // positions per split
     int32_t max_splits;
-    float *part;               // [n_heads][max_splits][head_dim + 2]
+    float *part;               // [n_kv_heads][max_splits][group][head_dim + 2]
     float *out;                // [n_heads * head_dim]
     int32_t n_heads, n_kv_heads;
 };
@@ -202,6 +210,7 @@ struct Q35Args {
     float *qbuf;                   // scratch [n_heads * head_dim]
     float *part;                   // scratch [n_heads][max_splits][head_dim + 2]
     float *out;                    // [n_heads * head_dim]
+    const int32_t *state;          // if set, pos = state[ST_POS] (the token loop's device state) instead of pos
 };
 int q35_max_splits(int seq_len);
 hipError_t launch_q35_attn(const Q35Args &a, int head_dim, hipStream_t st);

@@ -56,7 +56,9 @@ __global__ __launch_bounds__(WG) void q35_attn_kernel(Q35Args a) {
     const int G = a.n_heads / a.n_kv_heads, ngrp = G / GW;
     const int kvh = blockIdx.x / ngrp, h0 = kvh * G + (blockIdx.x % ngrp) * GW, sp_i = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid / WAVE;
-    const int L = a.pos + 1, t0 = sp_i * Q35_CH, n = min(Q35_CH, L - t0);
+    const int pos = a.state ? a.state[ST_POS] : a.pos;  // the token loop keeps pos on the device
+    const int L = pos + 1, t0 = sp_i * Q35_CH, n = min(Q35_CH, L - t0);
+    if (t0 > pos) return;  // a split past pos (graph launches size the grid for seq_len)
     const uint16_t *kc = a.kc + (size_t)kvh * a.seq_len * HD, *vc = a.vc + (size_t)kvh * a.seq_len * HD;
     // every tile load is issued before the first LDS store, so the loads
     // stream instead of waiting one by one
@@ -71,7 +73,7 @@ __global__ __launch_bounds__(WG) void q35_attn_kernel(Q35Args a) {
     // this workgroup's q heads, and in the split that holds pos the new k and
     // v: RMSNorm (ops.odin rmsnorm) and partial RoPE (ops.odin:77-89); the
     // new k / v go to the cache and to the LDS tile row pos - t0
-    const bool has_pos = a.pos < t0 + Q35_CH;
+    const bool has_pos = pos < t0 + Q35_CH;
     for (int i = tid; i < GW * HD; i += WG) qs[i / HD][i % HD] = a.qproj[(size_t)(h0 + i / HD) * 2 * HD + i % HD];
     __shared__ float kn[HD], vn[HD];
     if (has_pos)
@@ -107,7 +109,7 @@ __global__ __launch_bounds__(WG) void q35_attn_kernel(Q35Args a) {
             float v = xv[e];
             if (i < a.rotary_dim) {
                 const int pr = i < half ? i : i - half;
-                const float ang = (float)a.pos * a.inv_freq[pr];
+                const float ang = (float)pos * a.inv_freq[pr];
                 const float c = cosf(ang), sn = sinf(ang);
                 v = i < half ? x[i] * c - x[i + half] * sn : x[i - half] * sn + x[i] * c;
             }
@@ -118,14 +120,14 @@ __global__ __launch_bounds__(WG) void q35_attn_kernel(Q35Args a) {
     }
     __syncthreads();
     if (has_pos) {
-        const int tl = a.pos - t0;
+        const int tl = pos - t0;
         for (int i = tid; i < HD; i += WG) {
             const uint16_t kb = f2h(kn[i]), vb = f2h(vn[i]);
             ks[tl * KP + i] = kb;
             vs[tl * HD + i] = vb;
             if (blockIdx.x % ngrp == 0) {
-                a.kc[((size_t)kvh * a.seq_len + a.pos) * HD + i] = kb;
-                a.vc[((size_t)kvh * a.seq_len + a.pos) * HD + i] = vb;
+                a.kc[((size_t)kvh * a.seq_len + pos) * HD + i] = kb;
+                a.vc[((size_t)kvh * a.seq_len + pos) * HD + i] = vb;
             }
         }
     }
@@ -218,7 +220,8 @@ __global__ __launch_bounds__(WG) void q35_combine_kernel(Q35Args a) {
 #pragma clang fp contract(off)
     __shared__ float wsp[Q35_MAXS];
     __shared__ float red[WG / WAVE];
-    const int h = blockIdx.x, ns = (a.pos + Q35_CH) / Q35_CH, t = threadIdx.x;
+    const int pos = a.state ? a.state[ST_POS] : a.pos;
+    const int h = blockIdx.x, ns = (pos + Q35_CH) / Q35_CH, t = threadIdx.x;
     const int lane = t & (WAVE - 1), wave = t / WAVE;
     const float *pb = a.part + (size_t)h * a.max_splits * (HD + 2);
     __shared__ float msp[Q35_MAXS], lsp[Q35_MAXS];
@@ -261,7 +264,8 @@ __global__ __launch_bounds__(WG) void q35_combine_kernel(Q35Args a) {
 int q35_max_splits(int seq_len) { return (seq_len + Q35_CH - 1) / Q35_CH; }
 
 hipError_t launch_q35_attn(const Q35Args &a, int head_dim, hipStream_t st) {
-    const int ns = (a.pos + Q35_CH) / Q35_CH;
+    // with a device-side pos the grid covers every split of the cache
+    const int ns = a.state ? a.max_splits : (a.pos + Q35_CH) / Q35_CH;
     if (ns > a.max_splits || a.rotary_dim < 0 || a.rotary_dim > head_dim || a.rotary_dim % 2 ||
         a.n_heads / a.n_kv_heads > Q35_GMAX || ns > Q35_MAXS)
         return hipErrorInvalidValue;

@@ -1,4 +1,5 @@
-// synth.cpp -- seeded synthetic dense-Qwen3 GGUF writer and block quantizers.
+// synth.cpp -- seeded synthetic GGUF writer (dense Qwen3, Qwen3-MoE, Qwen3.5
+// hybrid) and block quantizers.
 //
 // New code: the reference only reads GGUF (ggml/gguf.odin:167-229) and only
 // dequantizes (ggml/quant.odin:76-282).  Block layouts written here are the
@@ -363,9 +364,10 @@ struct Writer {
 struct TensorPlan {
     std::string name;
     int type;
-    int ndim;
-    int64_t rows, cols;  // 1-D tensors: rows = 1
+    std::vector<uint64_t> dims;  // GGUF order: dims[0] is the row length
+    int64_t rows, cols;          // generated as rows x cols (rows = product of dims[1..])
     float sigma, mean;
+    int transform;               // 0: as drawn; 1: -exp(v) (ssm_a = -exp(A_log))
     uint64_t offset, bytes;
 };
 
@@ -422,33 +424,79 @@ void oi_synth_tensor_f32(uint64_t seed, const char *name, int64_t rows, int64_t 
 
 int oi_synth_write_gguf(const char *path, const oi_synth_spec *s) {
     if (!path || !s || s->dim <= 0 || s->n_layers <= 0 || s->n_heads <= 0 || s->n_kv_heads <= 0 ||
-        s->head_dim <= 0 || s->vocab_size <= 0 || s->hidden_dim <= 0)
+        s->head_dim <= 0 || s->vocab_size <= 0 || s->hidden_dim <= 0 || s->arch < 0 || s->arch > 2)
+        return -1;
+    const bool moe = s->arch == 1 || (s->arch == 2 && s->n_experts > 0);
+    if (moe && (s->n_experts <= 0 || s->n_experts_used <= 0 || s->n_experts_used > s->n_experts ||
+                s->expert_ffn <= 0))
+        return -1;
+    if (s->arch == 2 && (s->full_attn_interval <= 0 || s->rotary_dim <= 0 || s->lin_n_k_heads <= 0 ||
+                         s->lin_n_v_heads <= 0 || s->lin_head_k_dim <= 0 || s->lin_head_v_dim <= 0 ||
+                         s->lin_conv_kernel <= 0))
         return -1;
     const int nt = s->n_threads > 0 ? s->n_threads : 1;
     std::vector<TensorPlan> plan;
     auto add2 = [&](const std::string &nm, int type, int64_t rows, int64_t cols) {
-        plan.push_back({nm, type, 2, rows, cols, s->sigma, 0.0f, 0, 0});
+        plan.push_back({nm, type, {(uint64_t)cols, (uint64_t)rows}, rows, cols, s->sigma, 0.0f, 0, 0, 0});
     };
-    auto add1 = [&](const std::string &nm, int64_t n) {
-        plan.push_back({nm, OI_T_F32, 1, 1, n, s->norm_sigma, 1.0f, 0, 0});
+    auto add3 = [&](const std::string &nm, int type, int64_t n_exp, int64_t rows, int64_t cols) {
+        plan.push_back({nm, type, {(uint64_t)cols, (uint64_t)rows, (uint64_t)n_exp}, n_exp * rows, cols, s->sigma,
+                        0.0f, 0, 0, 0});
+    };
+    auto add1 = [&](const std::string &nm, int64_t n) {  // F32 norm weight, 1 + N(0, norm_sigma)
+        plan.push_back({nm, OI_T_F32, {(uint64_t)n}, 1, n, s->norm_sigma, 1.0f, 0, 0, 0});
+    };
+    auto add1v = [&](const std::string &nm, int64_t n, float sigma, float mean, int transform) {
+        plan.push_back({nm, OI_T_F32, {(uint64_t)n}, 1, n, sigma, mean, transform, 0, 0});
     };
     const int64_t D = s->dim, H = s->hidden_dim, Q = s->n_heads * s->head_dim, KV = s->n_kv_heads * s->head_dim;
+    const int64_t E = s->n_experts, EF = s->expert_ffn, SF = s->shared_expert_ffn;
+    const int64_t KD = (int64_t)s->lin_n_k_heads * s->lin_head_k_dim, VD = (int64_t)s->lin_n_v_heads * s->lin_head_v_dim;
+    const int64_t CD = 2 * KD + VD;
     add2("token_embd.weight", s->type_embd, s->vocab_size, D);
     add1("output_norm.weight", D);
     if (s->type_output >= 0) add2("output.weight", s->type_output, s->vocab_size, D);
     for (int64_t l = 0; l < s->n_layers; l++) {
         std::string p = "blk." + std::to_string(l) + ".";
         add1(p + "attn_norm.weight", D);
-        add1(p + "ffn_norm.weight", D);
-        add1(p + "attn_q_norm.weight", s->head_dim);
-        add1(p + "attn_k_norm.weight", s->head_dim);
-        add2(p + "attn_q.weight", s->type_default, Q, D);
-        add2(p + "attn_k.weight", s->type_default, KV, D);
-        add2(p + "attn_v.weight", s->type_attn_v, KV, D);
-        add2(p + "attn_output.weight", s->type_default, D, Q);
-        add2(p + "ffn_gate.weight", s->type_default, H, D);
-        add2(p + "ffn_down.weight", s->type_ffn_down, D, H);
-        add2(p + "ffn_up.weight", s->type_default, H, D);
+        // the Qwen3.5 loader calls the FFN norm post_attention_norm (qwen3_5/model.odin:325)
+        add1(p + (s->arch == 2 ? "post_attention_norm.weight" : "ffn_norm.weight"), D);
+        const bool full = s->arch != 2 || (l + 1) % s->full_attn_interval == 0;  // qwen3_5/model.odin:289-300
+        if (full) {
+            add1(p + "attn_q_norm.weight", s->head_dim);
+            add1(p + "attn_k_norm.weight", s->head_dim);
+            add2(p + "attn_q.weight", s->type_default, s->arch == 2 ? 2 * Q : Q, D);  // [q | gate] per head
+            add2(p + "attn_k.weight", s->type_default, KV, D);
+            add2(p + "attn_v.weight", s->type_attn_v, KV, D);
+            add2(p + "attn_output.weight", s->type_default, D, Q);
+        } else {  // gated DeltaNet (qwen3_5/model.odin:346-360)
+            add2(p + "attn_qkv.weight", s->type_default, CD, D);
+            add2(p + "attn_gate.weight", s->type_default, VD, D);
+            add2(p + "ssm_beta.weight", s->type_default, s->lin_n_v_heads, D);
+            add2(p + "ssm_alpha.weight", s->type_default, s->lin_n_v_heads, D);
+            plan.push_back({p + "ssm_conv1d.weight", OI_T_F32,
+                            {(uint64_t)s->lin_conv_kernel, (uint64_t)CD}, CD, s->lin_conv_kernel, 0.25f, 0.0f, 0, 0, 0});
+            add1v(p + "ssm_dt.bias", s->lin_n_v_heads, 0.5f, 0.0f, 0);
+            add1v(p + "ssm_a", s->lin_n_v_heads, 0.5f, 0.0f, 1);
+            add1(p + "ssm_norm.weight", s->lin_head_v_dim);
+            add2(p + "ssm_out.weight", s->type_default, D, VD);
+        }
+        if (!moe) {
+            add2(p + "ffn_gate.weight", s->type_default, H, D);
+            add2(p + "ffn_down.weight", s->type_ffn_down, D, H);
+            add2(p + "ffn_up.weight", s->type_default, H, D);
+        } else {
+            add2(p + "ffn_gate_inp.weight", s->type_router, E, D);
+            add3(p + "ffn_gate_exps.weight", s->type_default, E, EF, D);
+            add3(p + "ffn_up_exps.weight", s->type_default, E, EF, D);
+            add3(p + "ffn_down_exps.weight", s->type_ffn_down, E, D, EF);
+            if (s->arch == 2 && SF > 0) {
+                add2(p + "ffn_gate_inp_shexp.weight", s->type_router, 1, D);
+                add2(p + "ffn_gate_shexp.weight", s->type_default, SF, D);
+                add2(p + "ffn_up_shexp.weight", s->type_default, SF, D);
+                add2(p + "ffn_down_shexp.weight", s->type_ffn_down, D, SF);
+            }
+        }
     }
     const uint64_t align = 32;
     uint64_t off = 0;
@@ -462,39 +510,65 @@ int oi_synth_write_gguf(const char *path, const oi_synth_spec *s) {
     Writer w;
     w.f = std::fopen(path, "wb");
     if (!w.f) return -3;
+    const char *arch = s->arch == 0 ? "qwen3" : s->arch == 1 ? "qwen3moe" : "qwen35";
+    const std::string a = std::string(arch) + ".";
+    // metadata: the keys the loaders read (infer/model.odin:103-134;
+    // qwen3_5/model.odin:245-282), plus the expert counts of routed-expert models
+    struct MetaKV {
+        std::string k;
+        int kind;  // 4 u32, 6 f32, 8 string
+        uint32_t u;
+        float f;
+        std::string str;
+    };
+    std::vector<MetaKV> meta;
+    auto kv_u32 = [&](const std::string &k, int64_t v) { meta.push_back({k, 4, (uint32_t)v, 0.f, ""}); };
+    auto kv_f32 = [&](const std::string &k, float v) { meta.push_back({k, 6, 0, v, ""}); };
+    meta.push_back({"general.architecture", 8, 0, 0.f, arch});
+    meta.push_back({"general.name", 8, 0, 0.f, "odin-infer-amd synthetic"});
+    kv_u32("general.alignment", (int64_t)align);
+    kv_u32(a + "embedding_length", D);
+    kv_u32(a + "feed_forward_length", moe ? EF : H);
+    kv_u32(a + "block_count", s->n_layers);
+    kv_u32(a + "attention.head_count", s->n_heads);
+    kv_u32(a + "attention.head_count_kv", s->n_kv_heads);
+    kv_u32(a + "context_length", s->context_length);
+    kv_u32(a + "attention.key_length", s->head_dim);
+    kv_u32(a + "attention.value_length", s->head_dim);
+    kv_f32(a + "rope.freq_base", s->rope_theta);
+    kv_f32(a + "attention.layer_norm_rms_epsilon", s->rms_eps);
+    if (moe) {
+        kv_u32(a + "expert_count", E);
+        kv_u32(a + "expert_used_count", s->n_experts_used);
+        kv_u32(a + "expert_feed_forward_length", EF);
+        if (s->arch == 2 && SF > 0) kv_u32(a + "expert_shared_feed_forward_length", SF);
+    }
+    if (s->arch == 2) {
+        kv_u32(a + "ssm.group_count", s->lin_n_k_heads);
+        kv_u32(a + "ssm.time_step_rank", s->lin_n_v_heads);
+        kv_u32(a + "ssm.state_size", s->lin_head_k_dim);
+        kv_u32(a + "ssm.inner_size", VD);
+        kv_u32(a + "ssm.conv_kernel", s->lin_conv_kernel);
+        kv_u32(a + "full_attention_interval", s->full_attn_interval);
+        kv_u32(a + "rope.dimension_count", s->rotary_dim);
+    }
     // header (ggml/gguf.odin:177-189)
     w.u32(0x46554747u);
     w.u32(3);
     w.u64(plan.size());
-    const int n_meta = 12;
-    w.u64(n_meta);
-    auto kv_str = [&](const char *k, const char *v) { w.str(k); w.u32(8); w.str(v); };
-    auto kv_u32 = [&](const char *k, uint32_t v) { w.str(k); w.u32(4); w.u32(v); };
-    auto kv_f32 = [&](const char *k, float v) { w.str(k); w.u32(6); w.raw(&v, 4); };
-    // metadata the dense loader reads (infer/model.odin:103-134)
-    kv_str("general.architecture", "qwen3");
-    kv_str("general.name", "odin-infer-amd synthetic");
-    kv_u32("general.alignment", (uint32_t)align);
-    kv_u32("qwen3.embedding_length", (uint32_t)D);
-    kv_u32("qwen3.feed_forward_length", (uint32_t)H);
-    kv_u32("qwen3.block_count", (uint32_t)s->n_layers);
-    kv_u32("qwen3.attention.head_count", (uint32_t)s->n_heads);
-    kv_u32("qwen3.attention.head_count_kv", (uint32_t)s->n_kv_heads);
-    kv_u32("qwen3.context_length", (uint32_t)s->context_length);
-    kv_u32("qwen3.attention.key_length", (uint32_t)s->head_dim);
-    kv_f32("qwen3.rope.freq_base", s->rope_theta);
-    kv_f32("qwen3.attention.layer_norm_rms_epsilon", s->rms_eps);
+    w.u64(meta.size());
+    for (auto &m : meta) {
+        w.str(m.k);
+        w.u32((uint32_t)m.kind);
+        if (m.kind == 4) w.u32(m.u);
+        else if (m.kind == 6) w.raw(&m.f, 4);
+        else w.str(m.str);
+    }
     // tensor infos (ggml/gguf.odin:198-212): dims[0] is the row length
     for (auto &t : plan) {
         w.str(t.name);
-        if (t.ndim == 1) {
-            w.u32(1);
-            w.u64((uint64_t)t.cols);
-        } else {
-            w.u32(2);
-            w.u64((uint64_t)t.cols);
-            w.u64((uint64_t)t.rows);
-        }
+        w.u32((uint32_t)t.dims.size());
+        for (uint64_t d : t.dims) w.u64(d);
         w.u32((uint32_t)t.type);
         w.u64(t.offset);
     }
@@ -507,16 +581,18 @@ int oi_synth_write_gguf(const char *path, const oi_synth_spec *s) {
         if (t.offset > written) w.raw(pad.data(), (size_t)(t.offset - written));
         written = t.offset;
         buf.assign(t.bytes, 0);
-        int e, b;
+        int e = 1, b = 4;
         block_info(t.type, &e, &b);
         const int64_t rb = t.cols / e * b;
         const uint64_t h = fnv1a(t.name.c_str());
         bool bad = false;
-        parallel_for(t.rows, nt, [&](int64_t a, int64_t z) {
+        parallel_for(t.rows, nt, [&](int64_t a0, int64_t z) {
             std::vector<float> row((size_t)t.cols);
-            for (int64_t r = a; r < z; r++) {
+            for (int64_t r = a0; r < z; r++) {
                 Xoshiro g(row_seed(s->seed, h, r));
                 fill_normal(g, row.data(), t.cols, t.sigma, t.mean);
+                if (t.transform == 1)
+                    for (auto &v : row) v = -std::exp(v);
                 if (quantize_row(t.type, row.data(), t.cols, buf.data() + r * rb)) bad = true;
             }
         });

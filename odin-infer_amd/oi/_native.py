@@ -52,6 +52,7 @@ HIP_SYMBOLS = {
     "oi_last_error": (ctypes.c_char_p, []),
     "oi_engine_decode_greedy": (c_i32, [c_vp, c_i32, c_i32, c_i32, c_vp]),
     "oi_engine_kv_fill": (c_i32, [c_vp, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp]),
+    "oi_engine_reset_state": (c_i32, [c_vp]),
     "oi_engine_logits_device": (c_vp, [c_vp]),
     "oi_engine_stream": (c_vp, [c_vp]),
     "oi_engine_time_kernel": (c_i32, [c_vp, c_i32, c_i32, ctypes.POINTER(c_d), ctypes.POINTER(c_d)]),
@@ -81,7 +82,11 @@ class SynthSpec(ctypes.Structure):
                 ("n_kv_heads", c_i64), ("head_dim", c_i64), ("vocab_size", c_i64), ("context_length", c_i64),
                 ("rope_theta", c_f), ("rms_eps", c_f), ("type_default", c_i32), ("type_attn_v", c_i32),
                 ("type_ffn_down", c_i32), ("type_embd", c_i32), ("type_output", c_i32), ("sigma", c_f),
-                ("norm_sigma", c_f), ("seed", ctypes.c_uint64), ("n_threads", c_i32)]
+                ("norm_sigma", c_f), ("seed", ctypes.c_uint64), ("n_threads", c_i32),
+                ("arch", c_i32), ("n_experts", c_i32), ("n_experts_used", c_i32), ("expert_ffn", c_i32),
+                ("shared_expert_ffn", c_i32), ("type_router", c_i32), ("full_attn_interval", c_i32),
+                ("rotary_dim", c_i32), ("lin_n_k_heads", c_i32), ("lin_n_v_heads", c_i32),
+                ("lin_head_k_dim", c_i32), ("lin_head_v_dim", c_i32), ("lin_conv_kernel", c_i32)]
 
 
 SYNTH_SYMBOLS = {

@@ -20,7 +20,8 @@ from . import _native
 from ._native import OIError, check
 
 OI_E_RANGE = -6
-KERNELS = {"qkv": 0, "attn": 1, "wo": 2, "gateup": 3, "down": 4, "output": 5}
+KERNELS = {"qkv": 0, "attn": 1, "wo": 2, "gateup": 3, "down": 4, "output": 5, "token": 6, "router": 7,
+           "linear_in": 8, "deltanet": 9, "linear_out": 10, "shared": 11}
 
 
 @dataclass
@@ -141,6 +142,11 @@ def engine_time_kernel(e, kernel, iters):
 
 def engine_stream(e):
     return _native.hip().oi_engine_stream(e.handle)
+
+
+def engine_reset_state(e):
+    """qwen3_5/engine.odin:108-132: zero the KV cache and the DeltaNet states."""
+    check(_native.hip().oi_engine_reset_state(e.handle))
 
 
 def engine_logits_device(e):

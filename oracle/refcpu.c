@@ -733,6 +733,19 @@ typedef struct { int kind; const uint8_t *data; } tensor;
 typedef struct {
     const float *attn_norm, *ffn_norm, *q_norm, *k_norm;
     tensor wq, wk, wv, wo, w1, w2, w3;
+    /* layer kind: 0 Qwen3 attention (infer/forward.odin), 1 Qwen3.5 full attention,
+     * 2 Qwen3.5 gated DeltaNet (qwen3_5/forward.odin:46-225) */
+    int kind;
+    /* routed-expert FFN (Qwen3-MoE / Qwen3-Next convention; no reference code),
+     * optionally with a sigmoid-gated shared expert */
+    int moe, shared;
+    tensor router, gexp, uexp, dexp, sh_inp, sh_gate, sh_up, sh_down;
+    /* gated DeltaNet (qwen3_5/model.odin:346-360) and its states */
+    tensor in_qkv, in_z, in_b, in_a, ssm_out;
+    const float *conv_w, *dt_bias, *ssm_a, *ssm_norm;
+    float *conv_state, *rec_state;
+    /* Qwen3.5 full attention: f16 cache [n_kv][seq_len][head_dim] (binary16 bits) */
+    uint16_t *kc16, *vc16;
 } layer_w;
 
 typedef struct {
@@ -742,6 +755,14 @@ typedef struct {
     tensor token_embedding, output;
     const float *output_norm;
     layer_w *layers;
+    /* architecture: 0 "qwen3" (infer/model.odin), 1 "qwen3moe", 2 "qwen35" (qwen3_5/model.odin) */
+    int arch;
+    int64_t n_experts, top_k, expert_ffn, shared_ffn;
+    int norm_topk;
+    int64_t rotary_dim, lin_nk, lin_nv, lin_hk, lin_hv, lin_kernel, full_interval;
+    float *inv_freq;
+    /* scratch of the MoE and hybrid layers */
+    float *mo_p, *mo_h, *mo_y, *mo_t, *hy_qproj, *hy_k, *hy_v, *hy_qkv, *hy_z, *hy_b, *hy_a, *hy_out;
     /* Run_State, infer/model.odin:53-65 */
     float *x, *xb, *xb2, *xb3, *hb, *hb2, *q, *att, *logits, *key_cache, *value_cache;
     float *ktmp, *vtmp;
@@ -754,6 +775,17 @@ typedef struct {
     float **stg_w;
     int n_stg;
 } ref_engine;
+
+static float ref_sigmoid(float x);
+static float ref_silu(float x);
+EXPORT void ref_inv_freq(float theta, int rotary_dim, float *out);
+EXPORT int ref_deltanet_steps(int n_kh, int n_vh, int hk, int hv, int kernel, float eps, int n_tokens,
+                              const float *qkv, const float *z, const float *b, const float *a, const float *conv_w,
+                              const float *a_decay, const float *dt_bias, const float *norm_w, float *conv_state,
+                              float *rec_state, float *out);
+EXPORT int ref_qwen35_attn_steps(int n_heads, int n_kv, int hd, int rotary_dim, int seq_len, float eps, int n_tokens,
+                                 int pos0, const float *qproj, const float *k, const float *v, const float *q_norm,
+                                 const float *k_norm, const float *inv_freq, uint16_t *kc, uint16_t *vc, float *out);
 
 static int require(ref_engine *e, const char *name, gtensor **out) { /* model.odin:82-97 */
     gtensor *t = gtensor_get(&e->g, name);
@@ -781,6 +813,13 @@ EXPORT void ref_engine_destroy(void *h) {
     free(e->x); free(e->xb); free(e->xb2); free(e->xb3); free(e->hb); free(e->hb2);
     free(e->q); free(e->att); free(e->logits); free(e->key_cache); free(e->value_cache);
     free(e->ktmp); free(e->vtmp);
+    free(e->inv_freq); free(e->mo_p); free(e->mo_h); free(e->mo_y); free(e->mo_t);
+    free(e->hy_qproj); free(e->hy_k); free(e->hy_v); free(e->hy_qkv); free(e->hy_z); free(e->hy_b);
+    free(e->hy_a); free(e->hy_out);
+    for (int64_t l = 0; e->layers && l < e->n_layers; l++) {
+        free(e->layers[l].conv_state); free(e->layers[l].rec_state);
+        free(e->layers[l].kc16); free(e->layers[l].vc16);
+    }
     for (int i = 0; i < e->n_stg; i++) free(e->stg_w[i]);
     free(e->stg_key); free(e->stg_w);
     free(e->layers);
@@ -798,21 +837,53 @@ EXPORT void *ref_engine_load(const char *path, int max_ctx, int num_threads, int
     int rc = gfile_open(path, &e->g);
     if (rc) { ref_engine_destroy(e); return NULL; }
     gfile *g = &e->g;
-    /* load_config, model.odin:99-139 */
-    const char *keys[7] = {"qwen3.embedding_length", "qwen3.feed_forward_length", "qwen3.block_count",
-                           "qwen3.attention.head_count", "qwen3.attention.head_count_kv",
-                           "qwen3.context_length", "qwen3.attention.key_length"};
-    int64_t vals[7];
-    for (int i = 0; i < 7; i++) {
-        gmeta *m = gmeta_get(g, keys[i]);
-        if (!m) { snprintf(g_err, sizeof g_err, "missing metadata key: %s", keys[i]); ref_engine_destroy(e); return NULL; }
-        vals[i] = (int64_t)m->u;
+    /* load_config (infer/model.odin:99-139; qwen3_5/model.odin:225-304): the
+     * metadata keys carry the architecture name as their prefix */
+    gmeta *am = gmeta_get(g, "general.architecture");
+    char arch[32] = "qwen3";
+    if (am && am->str && am->str_len < sizeof arch) {
+        memcpy(arch, am->str, am->str_len);
+        arch[am->str_len] = 0;
     }
-    e->dim = vals[0]; e->hidden_dim = vals[1]; e->n_layers = vals[2]; e->n_heads = vals[3];
-    e->n_kv_heads = vals[4]; e->max_seq = vals[5]; e->head_dim = vals[6];
-    gmeta *m = gmeta_get(g, "qwen3.rope.freq_base");
-    e->rope_freq = m ? (float)m->f : 1000000.0f;
-    m = gmeta_get(g, "qwen3.attention.layer_norm_rms_epsilon");
+    e->arch = !strcmp(arch, "qwen3moe") ? 1 : !strcmp(arch, "qwen35") ? 2 : 0;
+    char key[128];
+#define META_U(dst, suffix) do { snprintf(key, sizeof key, "%s." suffix, arch); gmeta *m_ = gmeta_get(g, key); \
+        if (!m_) { snprintf(g_err, sizeof g_err, "missing metadata key: %s", key); ref_engine_destroy(e); return NULL; } \
+        dst = (int64_t)m_->u; } while (0)
+    META_U(e->dim, "embedding_length");
+    META_U(e->hidden_dim, "feed_forward_length");
+    META_U(e->n_layers, "block_count");
+    META_U(e->n_heads, "attention.head_count");
+    META_U(e->n_kv_heads, "attention.head_count_kv");
+    META_U(e->max_seq, "context_length");
+    META_U(e->head_dim, "attention.key_length");
+    if (e->arch == 1 || (e->arch == 2 && (snprintf(key, sizeof key, "%s.expert_count", arch), gmeta_get(g, key)))) {
+        META_U(e->n_experts, "expert_count");
+        META_U(e->top_k, "expert_used_count");
+        META_U(e->expert_ffn, "expert_feed_forward_length");
+        e->hidden_dim = e->expert_ffn;
+        e->norm_topk = 1; /* Qwen3-MoE / Qwen3-Next renormalize the chosen weights */
+        snprintf(key, sizeof key, "%s.expert_shared_feed_forward_length", arch);
+        gmeta *sm = gmeta_get(g, key);
+        e->shared_ffn = sm ? (int64_t)sm->u : 0;
+    }
+    if (e->arch == 2) { /* qwen3_5/model.odin:262-300 */
+        META_U(e->lin_nk, "ssm.group_count");
+        META_U(e->lin_nv, "ssm.time_step_rank");
+        META_U(e->lin_hk, "ssm.state_size");
+        int64_t inner;
+        META_U(inner, "ssm.inner_size");
+        e->lin_hv = inner / (e->lin_nv > 0 ? e->lin_nv : 1);
+        META_U(e->lin_kernel, "ssm.conv_kernel");
+        META_U(e->full_interval, "full_attention_interval");
+        META_U(e->rotary_dim, "rope.dimension_count");
+    }
+#undef META_U
+    snprintf(key, sizeof key, "%s.rope.freq_base", arch);
+    gmeta *m = gmeta_get(g, key);
+    e->rope_freq = m ? (float)m->f : (e->arch == 2 ? 10000000.0f : 1000000.0f);
+    snprintf(key, sizeof key, "%s.attention.layer_norm_rms_epsilon", arch);
+    m = gmeta_get(g, key);
     e->rms_eps = m ? (float)m->f : 1e-6f;
     gtensor *emb;
     if (require(e, "token_embd.weight", &emb)) { ref_engine_destroy(e); return NULL; }
@@ -836,6 +907,7 @@ EXPORT void *ref_engine_load(const char *path, int max_ctx, int num_threads, int
     }
     e->layers = (layer_w *)calloc((size_t)e->n_layers, sizeof(layer_w));
     char nm[96];
+    const int64_t conv_dim = 2 * e->lin_nk * e->lin_hk + e->lin_nv * e->lin_hv;
     for (int64_t l = 0; l < e->n_layers; l++) {
         layer_w *lw = &e->layers[l];
         int bad = 0;
@@ -843,19 +915,75 @@ EXPORT void *ref_engine_load(const char *path, int max_ctx, int num_threads, int
 #define QW(field, suffix) { gtensor *t_; snprintf(nm, sizeof nm, "blk.%lld." suffix, (long long)l); \
         if (require(e, nm, &t_)) bad = 1; else lw->field = (tensor){t_->kind, t_->data}; }
         F32W(attn_norm, "attn_norm.weight")
-        F32W(ffn_norm, "ffn_norm.weight")
-        F32W(q_norm, "attn_q_norm.weight")
-        F32W(k_norm, "attn_k_norm.weight")
-        QW(wq, "attn_q.weight")
-        QW(wk, "attn_k.weight")
-        QW(wv, "attn_v.weight")
-        QW(wo, "attn_output.weight")
-        QW(w1, "ffn_gate.weight")
-        QW(w2, "ffn_down.weight")
-        QW(w3, "ffn_up.weight")
+        if (e->arch == 2) { F32W(ffn_norm, "post_attention_norm.weight") } /* qwen3_5/model.odin:325 */
+        else { F32W(ffn_norm, "ffn_norm.weight") }
+        lw->kind = e->arch != 2 ? 0 : ((l + 1) % e->full_interval == 0 ? 1 : 2); /* qwen3_5/model.odin:289-300 */
+        if (lw->kind != 2) {
+            F32W(q_norm, "attn_q_norm.weight")
+            F32W(k_norm, "attn_k_norm.weight")
+            QW(wq, "attn_q.weight")
+            QW(wk, "attn_k.weight")
+            QW(wv, "attn_v.weight")
+            QW(wo, "attn_output.weight")
+        } else {
+            QW(in_qkv, "attn_qkv.weight")
+            QW(in_z, "attn_gate.weight")
+            QW(in_b, "ssm_beta.weight")
+            QW(in_a, "ssm_alpha.weight")
+            F32W(conv_w, "ssm_conv1d.weight")
+            F32W(dt_bias, "ssm_dt.bias")
+            F32W(ssm_a, "ssm_a")
+            F32W(ssm_norm, "ssm_norm.weight")
+            QW(ssm_out, "ssm_out.weight")
+        }
+        if (e->n_experts > 0) {
+            lw->moe = 1;
+            QW(router, "ffn_gate_inp.weight")
+            QW(gexp, "ffn_gate_exps.weight")
+            QW(uexp, "ffn_up_exps.weight")
+            QW(dexp, "ffn_down_exps.weight")
+            snprintf(nm, sizeof nm, "blk.%lld.ffn_gate_inp_shexp.weight", (long long)l);
+            if (gtensor_get(g, nm)) {
+                lw->shared = 1;
+                QW(sh_inp, "ffn_gate_inp_shexp.weight")
+                QW(sh_gate, "ffn_gate_shexp.weight")
+                QW(sh_up, "ffn_up_shexp.weight")
+                QW(sh_down, "ffn_down_shexp.weight")
+            }
+        } else {
+            QW(w1, "ffn_gate.weight")
+            QW(w2, "ffn_down.weight")
+            QW(w3, "ffn_up.weight")
+        }
 #undef F32W
 #undef QW
         if (bad) { ref_engine_destroy(e); return NULL; }
+        if (lw->kind == 2) {
+            lw->conv_state = (float *)calloc((size_t)(conv_dim * (e->lin_kernel - 1) + 1), 4);
+            lw->rec_state = (float *)calloc((size_t)(e->lin_nv * e->lin_hk * e->lin_hv), 4);
+        } else if (lw->kind == 1) {
+            lw->kc16 = (uint16_t *)calloc((size_t)(e->n_kv_heads * e->seq_len * e->head_dim), 2);
+            lw->vc16 = (uint16_t *)calloc((size_t)(e->n_kv_heads * e->seq_len * e->head_dim), 2);
+        }
+    }
+    if (e->arch == 2) {
+        e->inv_freq = (float *)calloc((size_t)(e->rotary_dim / 2 + 1), 4);
+        ref_inv_freq(e->rope_freq, (int)e->rotary_dim, e->inv_freq); /* qwen3_5/model.odin:454-455 */
+        e->hy_qproj = (float *)calloc((size_t)(2 * e->n_heads * e->head_dim), 4);
+        e->hy_k = (float *)calloc((size_t)(e->n_kv_heads * e->head_dim), 4);
+        e->hy_v = (float *)calloc((size_t)(e->n_kv_heads * e->head_dim), 4);
+        e->hy_qkv = (float *)calloc((size_t)(conv_dim + 1), 4);
+        e->hy_z = (float *)calloc((size_t)(e->lin_nv * e->lin_hv + 1), 4);
+        e->hy_b = (float *)calloc((size_t)(e->lin_nv + 1), 4);
+        e->hy_a = (float *)calloc((size_t)(e->lin_nv + 1), 4);
+        e->hy_out = (float *)calloc((size_t)(e->lin_nv * e->lin_hv + e->n_heads * e->head_dim + 1), 4);
+    }
+    if (e->n_experts > 0) {
+        int64_t hmax = e->expert_ffn > e->shared_ffn ? e->expert_ffn : e->shared_ffn;
+        e->mo_p = (float *)calloc((size_t)e->n_experts, 4);
+        e->mo_h = (float *)calloc((size_t)(e->top_k * hmax + 2 * hmax), 4);
+        e->mo_y = (float *)calloc((size_t)e->dim, 4);
+        e->mo_t = (float *)calloc((size_t)e->dim, 4);
     }
     /* malloc_run_state, model.odin:185-200 */
     int64_t att_head_dim = e->n_heads * e->head_dim, kv_dim = e->n_kv_heads * e->head_dim;
@@ -955,6 +1083,97 @@ static int matmul_staged(ref_engine *e, float *xout, const float *x, int kind, c
  * each layer are the batched path's (matmul_staged), and without `logits` the
  * final norm and classifier are skipped (forward_gpu_batch computes them for
  * the last token only, metal.odin:1637-1641). */
+/* Routed-expert SwiGLU FFN of one token (x already normalized) into y, rows on
+ * the row pool: the arithmetic of ref_moe_ffn (each row dequantized and dotted
+ * with dot_f32; softmax; top_k by a strict '>' scan, ties to the lower id;
+ * weights renormalized in selection order; y[r] = sum over the chosen experts
+ * in selection order of w_k * (down_e h_k)[r], h_k = silu(gate_e x) *
+ * up_e x), then the shared expert when the layer has one (HF Qwen3-Next):
+ * y += sigmoid(w_shexp . x) * down_s(silu(gate_s x) * up_s x).  The reference
+ * has no MoE code (qwen3_5/model.odin:80-82 is a dense MLP). */
+static void moe_ffn_layer(ref_engine *e, const layer_w *lw, const float *x, float *y) {
+    const int64_t D = e->dim, E = e->n_experts, K = e->top_k, F = e->expert_ffn, S = e->shared_ffn;
+    mm_pool *P = e->pool;
+    float *p = e->mo_p, *h = e->mo_h, *t = e->mo_t;
+    matmul_t(P, p, x, lw->router.kind, lw->router.data, D, E);
+    ref_softmax(p, E);
+    int ids[64];
+    float w[64], sum = 0.0f;
+    for (int64_t k = 0; k < K; k++) {
+        int best = -1;
+        for (int64_t i = 0; i < E; i++)
+            if (p[i] >= 0.0f && (best < 0 || p[i] > p[best])) best = (int)i;
+        ids[k] = best;
+        w[k] = p[best];
+        sum += p[best];
+        p[best] = -1.0f;
+    }
+    for (int64_t k = 0; k < K; k++) w[k] = e->norm_topk ? w[k] / sum : w[k];
+    const int64_t grb = ref_row_byte_size(lw->gexp.kind, D), drb = ref_row_byte_size(lw->dexp.kind, F);
+    float *hk = h, *hu = h + K * F;
+    for (int64_t k = 0; k < K; k++) {
+        const int64_t ex = ids[k];
+        matmul_t(P, hk + k * F, x, lw->gexp.kind, lw->gexp.data + ex * F * grb, D, F);
+        matmul_t(P, hu, x, lw->uexp.kind, lw->uexp.data + ex * F * grb, D, F);
+        for (int64_t r = 0; r < F; r++) hk[k * F + r] = ref_silu(hk[k * F + r]) * hu[r];
+    }
+    for (int64_t r = 0; r < D; r++) y[r] = 0.0f;
+    for (int64_t k = 0; k < K; k++) {
+        matmul_t(P, t, hk + k * F, lw->dexp.kind, lw->dexp.data + (int64_t)ids[k] * D * drb, F, D);
+        for (int64_t r = 0; r < D; r++) y[r] += w[k] * t[r];
+    }
+    if (!lw->shared) return;
+    float g;
+    matmul_t(P, &g, x, lw->sh_inp.kind, lw->sh_inp.data, D, 1);
+    float *sg = h, *su = h + S;
+    matmul_t(P, sg, x, lw->sh_gate.kind, lw->sh_gate.data, D, S);
+    matmul_t(P, su, x, lw->sh_up.kind, lw->sh_up.data, D, S);
+    for (int64_t r = 0; r < S; r++) sg[r] = ref_silu(sg[r]) * su[r];
+    matmul_t(P, t, sg, lw->sh_down.kind, lw->sh_down.data, S, D);
+    const float gs = ref_sigmoid(g);
+    for (int64_t r = 0; r < D; r++) y[r] += gs * t[r];
+}
+
+/* forward_full_layer (qwen3_5/forward.odin:46-135) up to the residual add:
+ * RMSNorm, the [q | gate], k and v projections, then the attention restated by
+ * ref_qwen35_attn_steps (q/k RMSNorm, partial RoPE, f16 cache at pos, softmax
+ * with dot * 1/sqrt(head_dim), sigmoid gate), wo. */
+static int q35_full_attention(ref_engine *e, layer_w *lw, int pos) {
+    const int64_t D = e->dim, QD = e->n_heads * e->head_dim, KVD = e->n_kv_heads * e->head_dim;
+    mm_pool *P = e->pool;
+    ref_rmsnorm(e->xb, e->x, lw->attn_norm, D, e->rms_eps);
+    matmul_t(P, e->hy_qproj, e->xb, lw->wq.kind, lw->wq.data, D, 2 * QD);
+    matmul_t(P, e->hy_k, e->xb, lw->wk.kind, lw->wk.data, D, KVD);
+    matmul_t(P, e->hy_v, e->xb, lw->wv.kind, lw->wv.data, D, KVD);
+    if (ref_qwen35_attn_steps((int)e->n_heads, (int)e->n_kv_heads, (int)e->head_dim, (int)e->rotary_dim,
+                              (int)e->seq_len, e->rms_eps, 1, pos, e->hy_qproj, e->hy_k, e->hy_v, lw->q_norm,
+                              lw->k_norm, e->inv_freq, lw->kc16, lw->vc16, e->hy_out))
+        return -1;
+    matmul_t(P, e->xb2, e->hy_out, lw->wo.kind, lw->wo.data, QD, D);
+    for (int64_t i = 0; i < D; i++) e->x[i] += e->xb2[i];
+    return 0;
+}
+
+/* forward_linear_layer (qwen3_5/forward.odin:137-225) up to the residual add:
+ * RMSNorm, the in_qkv / in_z / in_b / in_a projections, the conv / l2norm /
+ * delta rule / gated RMSNorm step restated by ref_deltanet_steps, ssm_out. */
+static int q35_linear_attention(ref_engine *e, layer_w *lw) {
+    const int64_t D = e->dim, KD = e->lin_nk * e->lin_hk, VD = e->lin_nv * e->lin_hv, CD = 2 * KD + VD;
+    mm_pool *P = e->pool;
+    ref_rmsnorm(e->xb, e->x, lw->attn_norm, D, e->rms_eps);
+    matmul_t(P, e->hy_qkv, e->xb, lw->in_qkv.kind, lw->in_qkv.data, D, CD);
+    matmul_t(P, e->hy_z, e->xb, lw->in_z.kind, lw->in_z.data, D, VD);
+    matmul_t(P, e->hy_b, e->xb, lw->in_b.kind, lw->in_b.data, D, e->lin_nv);
+    matmul_t(P, e->hy_a, e->xb, lw->in_a.kind, lw->in_a.data, D, e->lin_nv);
+    if (ref_deltanet_steps((int)e->lin_nk, (int)e->lin_nv, (int)e->lin_hk, (int)e->lin_hv, (int)e->lin_kernel,
+                           e->rms_eps, 1, e->hy_qkv, e->hy_z, e->hy_b, e->hy_a, lw->conv_w, lw->ssm_a, lw->dt_bias,
+                           lw->ssm_norm, lw->conv_state, lw->rec_state, e->hy_out))
+        return -1;
+    matmul_t(P, e->xb2, e->hy_out, lw->ssm_out.kind, lw->ssm_out.data, VD, D);
+    for (int64_t i = 0; i < D; i++) e->x[i] += e->xb2[i];
+    return 0;
+}
+
 static const float *forward_impl(ref_engine *e, int token, int pos, int staged, int logits) {
     if (pos < 0 || pos >= e->seq_len) {
         snprintf(g_err, sizeof g_err, "forward: pos=%d out of range (seq_len=%lld)", pos, (long long)e->seq_len);
@@ -976,6 +1195,10 @@ static const float *forward_impl(ref_engine *e, int token, int pos, int staged, 
 
     for (int64_t l = 0; l < e->n_layers; l++) {
         layer_w *lw = &e->layers[l];
+        if (lw->kind == 1 && q35_full_attention(e, lw, pos)) return NULL;
+        if (lw->kind == 2 && q35_linear_attention(e, lw)) return NULL;
+        if (lw->kind != 0) goto ffn;
+        {
         int64_t loff = l * seq_len * kv_dim;
         float *k_slice = e->key_cache + loff + (int64_t)pos * kv_dim;
         float *v_slice = e->value_cache + loff + (int64_t)pos * kv_dim;
@@ -1045,8 +1268,22 @@ static const float *forward_impl(ref_engine *e, int token, int pos, int staged, 
 
         MM(e->xb2, e->xb3, lw->wo, att_head_dim, dim);
         for (int64_t i = 0; i < dim; i++) e->x[i] += e->xb2[i];
-
+        }
+    ffn:
         ref_rmsnorm(e->xb, e->x, lw->ffn_norm, dim, eps);
+        if (lw->moe) { /* routed experts (+ shared expert) */
+            moe_ffn_layer(e, lw, e->xb, e->mo_y);
+            for (int64_t i = 0; i < dim; i++) e->x[i] += e->mo_y[i];
+            continue;
+        }
+        if (e->arch == 2) { /* mlp_layer, qwen3_5/forward.odin:227-243 */
+            matmul_t(P, e->hb, e->xb, lw->w1.kind, lw->w1.data, dim, hidden_dim);
+            matmul_t(P, e->hb2, e->xb, lw->w3.kind, lw->w3.data, dim, hidden_dim);
+            for (int64_t i = 0; i < hidden_dim; i++) e->hb2[i] = ref_silu(e->hb[i]) * e->hb2[i];
+            matmul_t(P, e->xb, e->hb2, lw->w2.kind, lw->w2.data, hidden_dim, dim);
+            for (int64_t i = 0; i < dim; i++) e->x[i] += e->xb[i];
+            continue;
+        }
         MM(e->hb, e->xb, lw->w1, dim, hidden_dim);
         MM(e->hb2, e->xb, lw->w3, dim, hidden_dim);
         for (int64_t i = 0; i < hidden_dim; i++) { /* forward.odin:128-133 */
@@ -1087,7 +1324,7 @@ EXPORT const float *ref_engine_prefill(void *h, const int *tokens, int n, int po
     int i = 0;
     while (i < n) {
         int rem = n - i;
-        if (rem >= 8) {
+        if (rem >= 8 && e->arch == 0) {
             int chunk = rem < 512 ? rem : 512;
             chunk -= chunk % 8;
             for (int t = 0; t < chunk; t++)

@@ -14,7 +14,8 @@ def random_blocks(kind, nblocks, rng):
     """Random bytes for `nblocks` blocks of `kind`, with the f16 scale fields
     set to finite values of assorted magnitude (any byte pattern is a valid
     block for dequant; finite scales keep comparisons free of inf/nan)."""
-    e, b = {8: (32, 34), 12: (256, 144), 14: (256, 210), 1: (1, 2), 0: (1, 4)}[kind]
+    e, b = {8: (32, 34), 12: (256, 144), 14: (256, 210), 1: (1, 2), 0: (1, 4), 2: (32, 18), 3: (32, 20),
+            6: (32, 22), 7: (32, 24)}[kind]
     raw = rng.integers(0, 256, size=(nblocks, b), dtype=np.uint8)
 
     def f16_field(n):
@@ -23,9 +24,9 @@ def random_blocks(kind, nblocks, rng):
         v[rng.random(n) < 0.05] = 0
         return v.view(np.uint16)
 
-    if kind == 8:
+    if kind in (8, 2, 6):  # d
         raw[:, 0:2] = f16_field(nblocks).view(np.uint8).reshape(nblocks, 2)
-    elif kind == 12:
+    elif kind in (12, 3, 7):  # d, then dmin (K) or m (Q4_1 / Q5_1)
         raw[:, 0:2] = f16_field(nblocks).view(np.uint8).reshape(nblocks, 2)
         raw[:, 2:4] = f16_field(nblocks).view(np.uint8).reshape(nblocks, 2)
     elif kind == 14:

@@ -11,7 +11,10 @@ index in the oracle fails a comparison:
     with the row decoders of ggml/quant.odin;
   * scale_min_unpack: 6-bit (scale, min) fields read by bit position;
   * forward_f64: a float64 dense-Qwen3 forward (RMSNorm, per-head q/k norm,
-    NEOX RoPE, grouped-query attention, SwiGLU) from the dequantized weights.
+    NEOX RoPE, grouped-query attention, SwiGLU) from the dequantized weights;
+  * forward_general_f64: the same for the routed-expert (Qwen3-MoE) and
+    hybrid (Qwen3.5: full attention + gated DeltaNet, dense or routed FFN)
+    layouts.
 """
 import numpy as np
 
@@ -84,11 +87,41 @@ def dequant_q8_0_elem(blocks):
     return (d[:, None] * q).astype(F32).reshape(-1)
 
 
+def dequant_legacy_elem(kind, blocks):
+    """Q4_0 / Q4_1 / Q5_0 / Q5_1 (GGML's 32-element blocks; reader:
+    ggml/quant.odin:98-162), element by element: element e of a block takes
+    nibble e // 16 of byte e % 16 of qs, and (Q5) bit e of the 32-bit qh as
+    its fifth bit.  Q4_0 / Q5_0: (q - 8 | 16) * d; Q4_1 / Q5_1: q * d + m,
+    each operation rounded to float32."""
+    bb = {2: 18, 3: 20, 6: 22, 7: 24}[kind]
+    b = blocks.reshape(-1, bb)
+    d = f16(b[:, 0:2])[:, 0]
+    has_m = kind in (3, 7)
+    m = f16(b[:, 2:4])[:, 0] if has_m else None
+    e = np.arange(32)
+    if kind in (6, 7):
+        o = 4 if has_m else 2
+        qh = b[:, o:o + 4].astype(np.int64)
+        qh = qh[:, 0] | qh[:, 1] << 8 | qh[:, 2] << 16 | qh[:, 3] << 24
+        qs = b[:, o + 4:].astype(np.int64)
+        q = ((qs[:, e % 16] >> (4 * (e // 16))) & 0xF) | (((qh[:, None] >> e) & 1) << 4)
+        off = 16
+    else:
+        qs = b[:, 4 if has_m else 2:].astype(np.int64)
+        q = (qs[:, e % 16] >> (4 * (e // 16))) & 0xF
+        off = 8
+    if has_m:
+        return ((q.astype(F32) * d[:, None]).astype(F32) + m[:, None]).astype(F32).reshape(-1)
+    return ((q - off).astype(F32) * d[:, None]).astype(F32).reshape(-1)
+
+
 def dequant(kind, blocks, n):
     if kind == 0:
         return np.ascontiguousarray(blocks).view(F32)[:n].copy()
     if kind == 1:
         return f16(np.ascontiguousarray(blocks).reshape(-1, 2))[:, 0][:n]
+    if kind in (2, 3, 6, 7):
+        return dequant_legacy_elem(kind, blocks)[:n]
     return {8: dequant_q8_0_elem, 12: dequant_q4k_elem, 14: dequant_q6k_elem}[kind](blocks)[:n]
 
 
@@ -145,7 +178,9 @@ class GGUFWeights:
     def get(self, name):
         dims, kind, off = self.tensors[name]
         n = int(np.prod(dims))
-        e, b = {0: (1, 4), 1: (1, 2), 8: (32, 34), 12: (256, 144), 14: (256, 210)}[kind]
+        e, b = {0: (1, 4), 1: (1, 2), 2: (32, 18), 3: (32, 20), 6: (32, 22), 7: (32, 24), 8: (32, 34),
+                12: (256, 144), 14: (256, 210)}[kind]
+        dims = [int(d) for d in dims]
         raw = self.data[self.base + off: self.base + off + n // e * b]
         w = dequant(kind, raw, n).astype(np.float64)
         return w.reshape(dims[::-1]) if len(dims) > 1 else w
@@ -316,3 +351,129 @@ def qwen35_attn_f64(n_heads, n_kv, hd, rotary_dim, seq_len, eps, pos0, qproj, k,
                 o[h] *= 1.0 / (1.0 + np.exp(-qp[h, 1]))
         outs.append(o.reshape(-1))
     return np.array(outs)
+
+
+def forward_general_f64(W, tokens, moe_renorm=True, shared_gate=True, attn_gate=True, ffn_norm=True):
+    """Float64 forward of the routed-expert and hybrid layouts: "qwen3moe"
+    (Qwen3 attention, routed-expert FFN) and "qwen35" (qwen3_5/forward.odin:
+    16-243: every full_attention_interval-th layer full attention with
+    [q | gate] heads, partial RoPE and a sigmoid output gate, the others gated
+    DeltaNet; the FFN dense or routed experts plus a sigmoid-gated shared
+    expert).  Routed experts follow HF Qwen3-MoE / Qwen3-Next: softmax over
+    the router logits, the top k (ties to the lower id), weights renormalized,
+    y = sum_k w_k down_k(silu(gate_k x) * up_k x) [+ sigmoid(s . x) *
+    shared(x)].  The keyword switches give the models a mistake would produce
+    (no renormalization, no shared-expert gate, no attention output gate, the
+    attention norm's weight used for the FFN norm).
+    Logits after each token at positions 0.. (f16-rounded K/V, as the oracle's
+    f16 mode)."""
+    m = W.meta
+    arch = m["general.architecture"]
+    a = arch + "."
+    D, L = m[a + "embedding_length"], m[a + "block_count"]
+    H, KVH, hd = m[a + "attention.head_count"], m[a + "attention.head_count_kv"], m[a + "attention.key_length"]
+    theta = m[a + "rope.freq_base"]
+    eps = m[a + "attention.layer_norm_rms_epsilon"]
+    E, K = m.get(a + "expert_count", 0), m.get(a + "expert_used_count", 0)
+    hybrid = arch == "qwen35"
+    if hybrid:
+        interval, rd = m[a + "full_attention_interval"], m[a + "rope.dimension_count"]
+        nk, nv, hk = m[a + "ssm.group_count"], m[a + "ssm.time_step_rank"], m[a + "ssm.state_size"]
+        hv, kern = m[a + "ssm.inner_size"] // nv, m[a + "ssm.conv_kernel"]
+    else:
+        rd = hd
+    emb = W.get("token_embd.weight")
+    out_w = W.get("output.weight") if "output.weight" in W.tensors else emb
+    sig = lambda v: 1.0 / (1.0 + np.exp(-v))
+
+    def rms(x, w):
+        return w * x / np.sqrt(np.mean(x * x) + eps)
+
+    def rope(v, pos):  # pairs (i, i + rd/2) over the first rd dimensions
+        half = rd // 2
+        inv = theta ** (-(np.arange(half) / (rd / 2.0)))
+        c, s = np.cos(pos * inv), np.sin(pos * inv)
+        v = v.copy()
+        x0, x1 = v[..., :half].copy(), v[..., half:rd].copy()
+        v[..., :half], v[..., half:rd] = x0 * c - x1 * s, x0 * s + x1 * c
+        return v
+
+    def attention(q, kc, vc, l):
+        Kc, Vc = np.stack(kc[l]), np.stack(vc[l])  # (t, KVH, hd)
+        o = np.zeros((H, hd))
+        for h in range(H):
+            g = h // (H // KVH)
+            sc = Kc[:, g, :] @ q[h] / np.sqrt(hd)
+            p = np.exp(sc - sc.max())
+            o[h] = (p / p.sum()) @ Vc[:, g, :]
+        return o
+
+    r16 = lambda v: v.astype(np.float16).astype(np.float64)
+    G = lambda name: W.get(name)
+    kc = [[] for _ in range(L)]
+    vc = [[] for _ in range(L)]
+    conv = {}
+    rec = {}
+    outs = []
+    for pos, tok in enumerate(tokens):
+        x = emb[tok].copy()
+        for l in range(L):
+            p = "blk.%d." % l
+            full = (not hybrid) or (l + 1) % interval == 0
+            xb = rms(x, G(p + "attn_norm.weight"))
+            if not hybrid:
+                q = (G(p + "attn_q.weight") @ xb).reshape(H, hd)
+                k = (G(p + "attn_k.weight") @ xb).reshape(KVH, hd)
+                v = (G(p + "attn_v.weight") @ xb).reshape(KVH, hd)
+                q = rope(np.stack([rms(qh, G(p + "attn_q_norm.weight")) for qh in q]), pos)
+                k = rope(np.stack([rms(kh, G(p + "attn_k_norm.weight")) for kh in k]), pos)
+                kc[l].append(r16(k))
+                vc[l].append(r16(v))
+                x = x + G(p + "attn_output.weight") @ attention(q, kc, vc, l).reshape(-1)
+            elif full:
+                qp = (G(p + "attn_q.weight") @ xb).reshape(H, 2, hd)
+                k = (G(p + "attn_k.weight") @ xb).reshape(KVH, hd)
+                v = (G(p + "attn_v.weight") @ xb).reshape(KVH, hd)
+                q = rope(np.stack([rms(qp[h, 0], G(p + "attn_q_norm.weight")) for h in range(H)]), pos)
+                k = rope(np.stack([rms(kh, G(p + "attn_k_norm.weight")) for kh in k]), pos)
+                kc[l].append(r16(k))
+                vc[l].append(r16(v))
+                o = attention(q, kc, vc, l) * (sig(qp[:, 1, :]) if attn_gate else 1.0)
+                x = x + G(p + "attn_output.weight") @ o.reshape(-1)
+            else:
+                kd, vd = nk * hk, nv * hv
+                if l not in conv:
+                    conv[l] = np.zeros((2 * kd + vd) * (kern - 1))
+                    rec[l] = np.zeros(nv * hk * hv)
+                qkv = G(p + "attn_qkv.weight") @ xb
+                z = G(p + "attn_gate.weight") @ xb
+                bb = G(p + "ssm_beta.weight") @ xb
+                aa = G(p + "ssm_alpha.weight") @ xb
+                o, conv[l], rec[l] = deltanet_f64(nk, nv, hk, hv, kern, eps, qkv, z, bb, aa,
+                                                  G(p + "ssm_conv1d.weight").reshape(-1), G(p + "ssm_a"),
+                                                  G(p + "ssm_dt.bias"), G(p + "ssm_norm.weight"), conv[l], rec[l])
+                x = x + G(p + "ssm_out.weight") @ o[0]
+            nname = ("post_attention_norm.weight" if hybrid else "ffn_norm.weight") if ffn_norm else "attn_norm.weight"
+            xb = rms(x, G(p + nname))
+            if E:
+                pr = G(p + "ffn_gate_inp.weight") @ xb
+                pr = np.exp(pr - pr.max())
+                pr /= pr.sum()
+                ids = sorted(range(E), key=lambda i: (-pr[i], i))[:K]
+                w = pr[ids] / (pr[ids].sum() if moe_renorm else 1.0)
+                Ge, Ue, De = G(p + "ffn_gate_exps.weight"), G(p + "ffn_up_exps.weight"), G(p + "ffn_down_exps.weight")
+                y = np.zeros(D)
+                for wk, ex in zip(w, ids):
+                    gt, up = Ge[ex] @ xb, Ue[ex] @ xb
+                    y += wk * (De[ex] @ (gt * sig(gt) * up))
+                if p + "ffn_gate_inp_shexp.weight" in W.tensors:
+                    gs = float((G(p + "ffn_gate_inp_shexp.weight") @ xb).reshape(-1)[0])
+                    gt, up = G(p + "ffn_gate_shexp.weight") @ xb, G(p + "ffn_up_shexp.weight") @ xb
+                    ys = G(p + "ffn_down_shexp.weight") @ (gt * sig(gt) * up)
+                    y += (sig(gs) if shared_gate else 1.0) * ys
+                x = x + y
+            else:
+                gt, up = G(p + "ffn_gate.weight") @ xb, G(p + "ffn_up.weight") @ xb
+                x = x + G(p + "ffn_down.weight") @ (gt * sig(gt) * up)
+        outs.append(out_w @ rms(x, G("output_norm.weight")))
+    return outs

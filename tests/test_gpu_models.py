@@ -6,7 +6,9 @@ oracle (oracle/refcpu.c, the restated reference forward, infer/forward.odin:
       greedy steps;
   C3  Qwen3-8B shape, Q4_K with Q6_K attn_v and output: f16 KV pre-filled with
       N(0,1) to 4096 positions, token 0 at position 4096, then 64 greedy steps
-      (the first steps of the bench's workload, same model and cache seeds).
+      (the first steps of the bench's workload, same model and cache seeds);
+  C4 / C5 layer shapes (4 layers each) and small models of the routed-expert
+      and hybrid layouts: logits on the oracle's greedy path, then greedy ids.
 
 Bars (the north star's): per-step logits within a scaled error
 max|d|/max|ref| <= 1e-3, and greedy ids identical for 64 steps with ties to
@@ -111,7 +113,15 @@ def _check_greedy(e, path, max_ctx, prefill, token, pos, ref_ids, ref_margins):
         assert margin <= noise, "step %d: gpu %d vs oracle %d, margin %.3g exceeds the oracle's f32 noise %.3g" % (
             i, got[i], ref_ids[i], margin, noise)
         ties.append(i)
-        # continue teacher-forced on the oracle's path from step i + 1
+        # continue teacher-forced on the oracle's path from step i + 1; the
+        # replay from a reset state covers models whose DeltaNet recurrence
+        # cannot be rewound (a dense cache is simply overwritten)
+        if prefill is None:
+            infer.engine_reset_state(e)
+            e_tok = token
+            for j in range(i + 1):
+                infer.engine_forward(e, e_tok, pos + j)
+                e_tok = int(ref_ids[j])
         e_tok = int(ref_ids[i])
         for j in range(i + 1, n):
             lg = infer.engine_forward(e, e_tok, pos + j)
@@ -182,3 +192,61 @@ def test_c3_qwen3_8b_q4_k_m_decode_from_4096(make_model):
     finally:
         infer.engine_destroy(e)
         r.close()
+
+
+def _walk_logits(e, r, n, token=0):
+    """Teacher-forced on the oracle's greedy path from position 0: the worst
+    scaled logit error over n steps and the oracle's ids and margins."""
+    ids, margins, worst = [], [], 0.0
+    for pos in range(n):
+        got = infer.engine_forward(e, token, pos).copy()
+        ref = r.forward(token, pos)
+        worst = max(worst, scaled_err(got, ref))
+        token, m = _top2(ref)
+        ids.append(token)
+        margins.append(m)
+    return worst, np.array(ids, np.int32), margins
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("name,steps", [
+    ("moe-tiny", 48),                 # routed experts (Qwen3-MoE layout), small
+    ("qwen35-tiny", 48),              # hybrid: 3 DeltaNet layers + 1 full-attention layer, dense FFN
+    ("qwen35-moe-tiny", 48),          # hybrid + routed experts + shared expert
+    ("qwen3-30b-a3b-4layer", 32),     # config 4's layer shapes: 128 experts top 8, inner 768, 32/4 heads
+    ("qwen35-hybrid-moe-4layer", 32),  # config 5's layer shapes: 512 experts top 10 + shared, 16/2 heads of 256
+])
+def test_moe_and_hybrid_models_vs_oracle(make_model, name, steps):
+    """Per-step logits within 1e-3 on the oracle's greedy path from token 0 at
+    position 0, then the device-side greedy loop from a reset state against
+    the oracle's ids (a differing step must be a proven f32 tie)."""
+    path = make_model(name)
+    max_ctx = 128
+    e, ok = infer.engine_load(path, infer.Engine_Opts(max_ctx=max_ctx))
+    assert ok
+    r = refcpu.RefEngine(path, max_ctx=max_ctx, num_threads=NTHREADS, kv_f16=True)
+    try:
+        worst, ref_ids, margins = _walk_logits(e, r, steps)
+        print("%s worst scaled logit error over %d steps: %.3g" % (name, steps, worst))
+        assert worst <= TOL
+        infer.engine_reset_state(e)  # the DeltaNet states cannot be rewound
+        ties = _check_greedy(e, path, max_ctx, None, 0, 0, ref_ids, margins)
+        print("%s proven f32 ties:" % name, ties)
+    finally:
+        infer.engine_destroy(e)
+        r.close()
+
+
+def test_reset_state_repeats_the_first_token(make_model):
+    """engine_reset_state (qwen3_5/engine.odin:108-132) zeroes the DeltaNet
+    states and the cache: the same prompt gives the same logits again."""
+    path = make_model("qwen35-tiny")
+    e, ok = infer.engine_load(path, infer.Engine_Opts(max_ctx=64))
+    try:
+        first = [infer.engine_forward(e, t, p).copy() for p, t in enumerate([3, 9, 27])]
+        infer.engine_reset_state(e)
+        again = [infer.engine_forward(e, t, p).copy() for p, t in enumerate([3, 9, 27])]
+        for a, b in zip(first, again):
+            assert np.array_equal(a, b)
+    finally:
+        infer.engine_destroy(e)

@@ -16,10 +16,11 @@ from oi import ggml, infer, synth
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
 NTHREADS = min(16, os.cpu_count() or 1)
-BLOCK = {0: (1, 4), 1: (1, 2), 8: (32, 34), 12: (256, 144), 14: (256, 210)}
+BLOCK = {0: (1, 4), 1: (1, 2), 2: (32, 18), 3: (32, 20), 6: (32, 22), 7: (32, 24), 8: (32, 34), 12: (256, 144),
+         14: (256, 210)}
 
 
-@pytest.mark.parametrize("kind", [8, 12, 14, 1, 0])
+@pytest.mark.parametrize("kind", [8, 12, 14, 1, 0, 2, 3, 6, 7])
 def test_dequant_bit_exact_random(kind):
     rng = np.random.default_rng(100 + kind)
     n = 16384
@@ -79,7 +80,7 @@ def _gemv_case(kind, rows, cols, seed):
     return blocks, x
 
 
-@pytest.mark.parametrize("kind", [12, 14, 8, 1, 0])
+@pytest.mark.parametrize("kind", [12, 14, 8, 1, 0, 2, 3, 6, 7])
 @pytest.mark.parametrize("rows,cols", [(512, 4096), (300, 1024), (64, 12288), (1000, 512), (7, 2048), (96, 1536),
                                        (130, 3072), (40, 768), (33, 5120)])
 def test_gemv_small(kind, rows, cols):
@@ -165,7 +166,7 @@ def _engines(path, max_ctx):
     return e, r
 
 
-@pytest.mark.parametrize("name", ["tiny-q4_k", "tiny-q8_0", "tiny-f32"])
+@pytest.mark.parametrize("name", ["tiny-q4_k", "tiny-q8_0", "tiny-f32", "tiny-legacy"])
 def test_forward_logits_teacher_forced(make_model, name):
     path = make_model(name)
     e, r = _engines(path, 256)
@@ -194,7 +195,8 @@ def _greedy_ref(r, token, pos, n):
     return np.array(out, np.int32)
 
 
-@pytest.mark.parametrize("name,steps", [("tiny-q4_k", 64), ("tiny-q8_0", 64), ("small-q4_k", 64)])
+@pytest.mark.parametrize("name,steps", [("tiny-q4_k", 64), ("tiny-q8_0", 64), ("small-q4_k", 64),
+                                        ("tiny-legacy", 64)])
 def test_greedy_decode_matches_oracle(make_model, name, steps):
     path = make_model(name)
     e, r = _engines(path, 512)

@@ -8,6 +8,7 @@ import pytest
 import npref
 import refcpu
 from helpers import random_blocks, same_bits
+from oi import synth
 
 F32 = np.float32
 
@@ -47,7 +48,8 @@ def test_get_scale_min_k4_exhaustive(j):
     assert len(set(zip(got[:, 0], got[:, 1]))) == 4096  # 12 bits -> 4096 distinct (sc, m)
 
 
-@pytest.mark.parametrize("kind,e,b", [(12, 256, 144), (14, 256, 210), (8, 32, 34), (1, 1, 2), (0, 1, 4)])
+@pytest.mark.parametrize("kind,e,b", [(12, 256, 144), (14, 256, 210), (8, 32, 34), (1, 1, 2), (0, 1, 4), (2, 32, 18),
+                                      (3, 32, 20), (6, 32, 22), (7, 32, 24)])
 def test_dequant_matches_elementwise_form(kind, e, b):
     rng = np.random.default_rng(kind)
     n = 256 * 40
@@ -79,6 +81,42 @@ def test_dequant_known_answers():
     blk[0:2] = np.array([-2.0], np.float16).view(np.uint8)
     blk[2:] = np.arange(-16, 16, dtype=np.int8).view(np.uint8)
     assert np.array_equal(refcpu.dequant_row(8, blk, 32), (-2.0 * np.arange(-16, 16)).astype(F32))
+
+
+def test_dequant_legacy_known_answers():
+    """Hand-built blocks of the 32-element types (ggml/quant.odin:98-162):
+    the low nibbles of qs[0..15] are elements 0-15, the high nibbles 16-31,
+    bit e of qh the fifth bit of element e."""
+    qs = np.arange(16, dtype=np.uint8) | (np.uint8(15) - np.arange(16, dtype=np.uint8)) << 4
+    nib = np.concatenate([np.arange(16), 15 - np.arange(16)])
+    h = lambda v: np.array([v], np.float16).view(np.uint8)
+    # Q4_0: (q - 8) * d
+    blk = np.concatenate([h(0.5), qs])
+    assert np.array_equal(refcpu.dequant_row(2, blk, 32), ((nib - 8) * 0.5).astype(F32))
+    # Q4_1: q * d + m
+    blk = np.concatenate([h(2.0), h(-3.0), qs])
+    assert np.array_equal(refcpu.dequant_row(3, blk, 32), (nib * 2.0 - 3.0).astype(F32))
+    # Q5_0: qh = 0xF0F0F0F0 sets the fifth bit of elements 4-7, 12-15, 20-23, 28-31
+    qh = np.array([0xF0F0F0F0], np.uint32).view(np.uint8)
+    hb = np.array([(0xF0F0F0F0 >> e) & 1 for e in range(32)])
+    blk = np.concatenate([h(-1.0), qh, qs])
+    assert np.array_equal(refcpu.dequant_row(6, blk, 32), (-(nib + 16 * hb - 16)).astype(F32))
+    # Q5_1: every fifth bit set, d = 0.25, m = 1: (q | 16) * 0.25 + 1
+    blk = np.concatenate([h(0.25), h(1.0), np.full(4, 0xFF, np.uint8), qs])
+    assert np.array_equal(refcpu.dequant_row(7, blk, 32), ((nib + 16) * 0.25 + 1.0).astype(F32))
+
+
+@pytest.mark.parametrize("kind,step", [(2, 1 / 8), (3, 1 / 15), (6, 1 / 16), (7, 1 / 31)])
+def test_legacy_quantize_dequant_round_trip(kind, step):
+    """The synthetic writer's quantizers (their own code) and the oracle's
+    readers agree on the layout: a row survives quantize -> dequant within
+    the block's quantization step (a swapped nibble or qh bit would not)."""
+    rng = np.random.default_rng(kind)
+    x = rng.standard_normal((8, 256)).astype(F32)
+    y = refcpu.dequant_row(kind, synth.quantize_rows(kind, x), x.size).reshape(x.shape)
+    rng_blk = np.ptp(x.reshape(-1, 32), axis=1) if kind in (3, 7) else 2 * np.abs(x.reshape(-1, 32)).max(axis=1)
+    err = np.abs(y - x).reshape(-1, 32).max(axis=1)
+    assert np.all(err <= rng_blk * step * 0.51 + 2e-3 * rng_blk)
 
 
 def test_dot_f32():
@@ -154,7 +192,7 @@ def test_softmax_and_argmax():
     assert refcpu.argmax(np.array([-5, -1, -1], F32)) == 1
 
 
-@pytest.mark.parametrize("name", ["tiny-q4_k", "tiny-q8_0", "tiny-f32"])
+@pytest.mark.parametrize("name", ["tiny-q4_k", "tiny-q8_0", "tiny-f32", "tiny-legacy"])
 def test_forward_vs_float64_model(make_model, name):
     """The oracle's whole forward (f16 KV mode) against an independent
     float64 model on the same weights."""

@@ -95,10 +95,11 @@ def test_engine_load_errors(make_model, tmp_path):
     (tmp_path / "notensor.gguf").write_bytes(data.replace(b"blk.1.ffn_up.weight", b"blk.1.ffn_xx.weight"))
     rc, msg = _load_rc(tmp_path / "notensor.gguf")
     assert rc == OI_E_MODEL and "missing required tensor: blk.1.ffn_up.weight" in msg
-    # a quant type the reference reads but this path does not (Q4_0 = 2)
-    q4 = _patch_tensor_type(data, "blk.0.attn_q.weight", 2)
-    (tmp_path / "q4_0.gguf").write_bytes(q4)
-    rc, msg = _load_rc(tmp_path / "q4_0.gguf")
+    # a type the reference's dequant turns into zeros (ggml/quant.odin:170-173)
+    # is refused by name here rather than read as zeros (Q2_K = 10)
+    q2 = _patch_tensor_type(data, "blk.0.attn_q.weight", 10)
+    (tmp_path / "q2_k.gguf").write_bytes(q2)
+    rc, msg = _load_rc(tmp_path / "q2_k.gguf")
     assert rc in (OI_E_UNSUPPORTED, OI_E_FORMAT) and "blk.0.attn_q.weight" in msg
     # norm weights must be F32 (infer/model.odin:74-80)
     (tmp_path / "f16norm.gguf").write_bytes(_patch_tensor_type(data, "output_norm.weight", 1))
