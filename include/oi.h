@@ -129,6 +129,51 @@ int oi_engine_kv_fill(oi_engine *e, int32_t layer0, int32_t nlayers, int32_t pos
  * position 0 (the DeltaNet recurrence cannot be rewound). */
 int oi_engine_reset_state(oi_engine *e);
 
+/* ------------------------------------------------- state persistence ---
+ * The position-evolving state: the K/V cache of the attention layers and the
+ * conv / recurrent states of the DeltaNet layers, in layer order. */
+
+/* engine_save_kv (qwen3_5/kv_persist.odin:365-372, metal_save_kv
+ * qwen3_5/metal.odin:780-862): write the .oikv v1 file -- a 60-byte
+ * little-endian header (magic 0x4F494B56, version 1, arch, FNV-1a 64
+ * fingerprint of dim, n_layers, n_heads, n_kv_heads, head_dim, the four
+ * DeltaNet head counts / dims, conv kernel and vocab_size; n_valid_pos,
+ * seq_len, n_full, n_linear, kv_dim, conv_dim, conv kernel, n_v_heads,
+ * head_k_dim, head_v_dim), then per attention layer K and V as f32
+ * [n_valid_pos][kv_dim], then every conv state and every recurrent state
+ * (f32), then the IEEE CRC-32 of all of it.  arch is 2 for the qwen35 layout
+ * (the reference's value); the qwen3 and qwen3moe layouts, which the
+ * reference does not persist, write 1 and 3.  OI_E_RANGE if n_valid_pos is
+ * outside [0, seq_len]; OI_E_IO on a file error. */
+int oi_engine_save_kv(oi_engine *e, const char *path, int32_t n_valid_pos);
+
+/* engine_load_kv (qwen3_5/kv_persist.odin:374-381, metal_load_kv
+ * metal.odin:864-962): check magic, version, arch, fingerprint, seq_len,
+ * n_valid_pos <= seq_len, the layer dims, the file size and the CRC -- all
+ * before any state changes -- then zero the K/V cache, read the file's
+ * positions (f32 -> f16, round to nearest even) and the DeltaNet states.
+ * *n_valid_pos receives the restored length (the next position to fill).
+ * OI_E_IO (cannot open) or OI_E_FORMAT with the reference's message. */
+int oi_engine_load_kv(oi_engine *e, const char *path, int32_t *n_valid_pos);
+
+/* engine_save_full_state / engine_restore_full_state (qwen3_5/engine.odin:
+ * 139-151, metal.odin:1655-1676): byte copies of the device state in its own
+ * layout -- kv_k and kv_v f16 [n_attention_layers][n_kv_heads][seq_len]
+ * [head_dim], conv f32 [n_linear][conv_dim][kernel-1], rec f32 [n_linear]
+ * [n_v_heads][head_k_dim][head_v_dim].  The buffers are the caller's, in host
+ * or device memory (a prefix snapshot can stay in HBM); sizes in bytes from
+ * oi_engine_state_sizes (a zero size takes a null pointer). */
+int oi_engine_state_sizes(oi_engine *e, int64_t sizes[4]);
+int oi_engine_save_full_state(oi_engine *e, void *kv_k, void *kv_v, void *conv, void *rec);
+int oi_engine_restore_full_state(oi_engine *e, const void *kv_k, const void *kv_v, const void *conv,
+                                 const void *rec);
+
+/* engine_save_spec_state / engine_restore_spec_state (qwen3_5/engine.odin:
+ * 153-165, metal.odin:1678-1700): the conv and recurrent states alone, for a
+ * speculative-decoding rollback. */
+int oi_engine_save_spec_state(oi_engine *e, void *conv, void *rec);
+int oi_engine_restore_spec_state(oi_engine *e, const void *conv, const void *rec);
+
 /* Device pointer to the engine's last logits (vocab_size floats). */
 const float *oi_engine_logits_device(oi_engine *e);
 

@@ -24,6 +24,7 @@
 #include "gguf.h"
 #include "oi.h"
 #include "oi_kernels.h"
+#include "engine_internal.h"
 
 using namespace oi;
 
@@ -206,86 +207,7 @@ int upload_matrix(uint32_t type, const uint8_t *src, int64_t rows, int64_t cols,
     return OI_OK;
 }
 
-struct Arena {
-    uint8_t *base = nullptr;
-    size_t size = 0, used = 0;
-    uint8_t *take(size_t n) {
-        size_t at = (used + 255) & ~(size_t)255;
-        if (at + n > size) return nullptr;
-        used = at + n;
-        return base + at;
-    }
-};
-
-// Layer kinds: Qwen3 attention (infer/forward.odin:45-121), Qwen3.5 full
-// attention (qwen3_5/forward.odin:46-135), Qwen3.5 gated DeltaNet (:137-225).
-enum { LK_QWEN3 = 0, LK_FULL = 1, LK_LINEAR = 2 };
-
-struct LayerDev {
-    int kind = LK_QWEN3;
-    bool moe = false, shared = false;  // routed-expert FFN (with a shared expert)
-    DMat wq{}, wk{}, wv{}, wo{}, w1{}, w2{}, w3{};
-    const float *attn_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
-    uint16_t *kc = nullptr, *vc = nullptr;
-    DMat router{}, gexp{}, uexp{}, dexp{}, sh_inp{}, sh_gate{}, sh_up{}, sh_down{};
-    DMat in_qkv{}, in_z{}, in_b{}, in_a{}, ssm_out{};
-    const float *conv_w = nullptr, *dt_bias = nullptr, *ssm_a = nullptr, *ssm_norm = nullptr;
-    float *conv_state = nullptr, *rec_state = nullptr;
-};
-
-// One launch of the token step: a GEMV (dense or routed-expert), an attention
-// or a DeltaNet step.  `role` is the kernel id of oi_engine_time_kernel.
-enum { OP_GEMV = 0, OP_MOE_ROWS, OP_MOE_COLS, OP_ATTN, OP_Q35, OP_DN };
-struct Op {
-    int kind = OP_GEMV, role = 0;
-    double bytes = 0;  // algorithmic HBM bytes per launch (attention: without the cache rows)
-    GemvArgs g{};
-    AttnArgs at{};
-    Q35Args q{};
-    DnArgs dn{};
-};
-
 }  // namespace
-
-enum { K_QKV = 0, K_ATTN = 1, K_WO = 2, K_GATEUP = 3, K_DOWN = 4, K_OUTPUT = 5, K_TOKEN = 6, K_ROUTER = 7,
-       K_LIN_IN = 8, K_DELTANET = 9, K_LIN_OUT = 10, K_SHARED = 11, K_LAST = 11 };
-
-struct oi_engine {
-    oi_config cfg{};
-    int device = 0;
-    hipStream_t stream = nullptr;
-    Arena arena;
-    std::vector<LayerDev> layers;
-    DMat tok_embd{}, output{};
-    const float *output_norm = nullptr;
-    float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *hb = nullptr;
-    float *logits = nullptr, *part = nullptr, *am_val = nullptr;
-    int32_t *am_idx = nullptr, *state = nullptr, *tokens = nullptr;
-    int n_partials = 0;
-    bool use_graph = true;
-    float2 *rope_cs = nullptr;
-    float *logits_host = nullptr;
-    int32_t *state_host = nullptr;
-    int chunk = 64, max_splits = 0;
-    int arch = 0;  // 0 qwen3, 1 qwen3moe, 2 qwen35
-    int64_t n_experts = 0, top_k = 0, expert_ffn = 0, shared_ffn = 0;
-    int64_t rotary_dim = 0, lin_nk = 0, lin_nv = 0, lin_hk = 0, lin_hv = 0, lin_kernel = 0, full_interval = 0;
-    std::vector<std::vector<Op>> ops;  // per layer, in launch order
-    GemvArgs g_out{};
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t gexec = nullptr;
-    int last_pos = 0;
-    size_t weight_bytes = 0;
-    // batched prefill buffers (allocated on the first prefill): token ids,
-    // residual [T][dim], rotated q [T][q_dim], f16 projection inputs
-    // [T][max(dim, q_dim, hidden)], and three buffers of partial products
-    void *pf_mem = nullptr;
-    int32_t *pf_tok = nullptr;
-    float *pf_x = nullptr, *pf_q = nullptr, *pf_p[3] = {nullptr, nullptr, nullptr};
-    size_t pf_pbytes[3] = {0, 0, 0};
-    uint16_t *pf_xb = nullptr;
-    bool pf_fused = true;  // gate/up GEMM with the SwiGLU epilogue where it applies (OI_PREFILL_UNFUSED=1: off)
-};
 
 namespace {
 

@@ -9,6 +9,9 @@
 //                  reduction of the previous step's argmax partials
 //                  (sampler/sampler.odin:79-89)
 //   dequant_kernel bit-exact dequant of a matrix (test hook)
+//   moe_*          routed-expert FFN for shapes the quantized GEMV does not take
+//   kv_export/import_kernel  f16 head-major cache <-> f32 position-major rows
+//                  (the .oikv state file's layout)
 //
 // Wave64 throughout; workgroups of 256 threads (4 waves).
 
@@ -653,6 +656,42 @@ hipError_t launch_embed_rows(const DMat &emb, const int32_t *tokens, int n, floa
     const int units = emb.cols / 64;
     hipLaunchKernelGGL(embed_rows_kernel, dim3((unsigned)((units + WG - 1) / WG), (unsigned)n), dim3(WG), 0, st, emb,
                        tokens, x);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------- KV conversion --
+// The .oikv state file holds K and V as f32 rows [pos][n_kv * hd]
+// (qwen3_5/kv_persist.odin:210-260); the device cache is f16 head-major
+// [n_kv][seq_len][hd] (infer/metal.odin:443-454).  One thread per element of
+// positions [0, n); consecutive threads take consecutive dimensions of one
+// head, so the f16 side is read or written 128 contiguous bytes per 64 lanes.
+__global__ __launch_bounds__(WG) void kv_export_kernel(const uint16_t *c, float *out, int n, int n_kv, int seq_len,
+                                                       int hd) {
+    const long i = (long)blockIdx.x * WG + threadIdx.x;  // over [n_kv][n][hd]
+    if (i >= (long)n_kv * n * hd) return;
+    const int d = (int)(i % hd), t = (int)((i / hd) % n), h = (int)(i / ((long)hd * n));
+    out[((size_t)t * n_kv + h) * hd + d] = h2f(c[((size_t)h * seq_len + t) * hd + d]);
+}
+
+// f32 -> f16 round to nearest even (the reference's f16(x) cast,
+// qwen3_5/metal.odin:912-940)
+__global__ __launch_bounds__(WG) void kv_import_kernel(const float *in, uint16_t *c, int n, int n_kv, int seq_len,
+                                                       int hd) {
+    const long i = (long)blockIdx.x * WG + threadIdx.x;
+    if (i >= (long)n_kv * n * hd) return;
+    const int d = (int)(i % hd), t = (int)((i / hd) % n), h = (int)(i / ((long)hd * n));
+    c[((size_t)h * seq_len + t) * hd + d] = f2h(in[((size_t)t * n_kv + h) * hd + d]);
+}
+
+hipError_t launch_kv_convert(bool to_f32, uint16_t *cache, float *rows, int n, int n_kv, int seq_len, int hd,
+                             hipStream_t st) {
+    const long total = (long)n_kv * n * hd;
+    if (total <= 0) return hipSuccess;
+    const dim3 grid((unsigned)((total + WG - 1) / WG));
+    if (to_f32)
+        hipLaunchKernelGGL(kv_export_kernel, grid, dim3(WG), 0, st, cache, rows, n, n_kv, seq_len, hd);
+    else
+        hipLaunchKernelGGL(kv_import_kernel, grid, dim3(WG), 0, st, rows, cache, n, n_kv, seq_len, hd);
     return hipGetLastError();
 }
 

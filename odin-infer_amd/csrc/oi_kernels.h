@@ -129,6 +129,10 @@ hipError_t launch_embed(const DMat &emb, int32_t *state, float *x, int32_t vocab
 int attn_chunk(int head_dim);
 int attn_max_splits();
 hipError_t launch_dequant(const DMat &m, float *out, hipStream_t st);
+// f16 head-major cache [n_kv][seq_len][hd], positions [0, n) <-> f32 rows
+// [n][n_kv * hd]; to_f32: cache -> rows, else rows -> cache (RNE)
+hipError_t launch_kv_convert(bool to_f32, uint16_t *cache, float *rows, int n, int n_kv, int seq_len, int hd,
+                             hipStream_t st);
 
 // Plan a GEMV over segments sharing one K: picks the kernel and fills lpr,
 // rows_per_wg, wg_begin, ntiles, total_wgs.  False if K is not a multiple of 64.

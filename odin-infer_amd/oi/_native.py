@@ -53,6 +53,13 @@ HIP_SYMBOLS = {
     "oi_engine_decode_greedy": (c_i32, [c_vp, c_i32, c_i32, c_i32, c_vp]),
     "oi_engine_kv_fill": (c_i32, [c_vp, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp]),
     "oi_engine_reset_state": (c_i32, [c_vp]),
+    "oi_engine_save_kv": (c_i32, [c_vp, ctypes.c_char_p, c_i32]),
+    "oi_engine_load_kv": (c_i32, [c_vp, ctypes.c_char_p, c_vp]),
+    "oi_engine_state_sizes": (c_i32, [c_vp, c_vp]),
+    "oi_engine_save_full_state": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "oi_engine_restore_full_state": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "oi_engine_save_spec_state": (c_i32, [c_vp, c_vp, c_vp]),
+    "oi_engine_restore_spec_state": (c_i32, [c_vp, c_vp, c_vp]),
     "oi_engine_logits_device": (c_vp, [c_vp]),
     "oi_engine_stream": (c_vp, [c_vp]),
     "oi_engine_time_kernel": (c_i32, [c_vp, c_i32, c_i32, ctypes.POINTER(c_d), ctypes.POINTER(c_d)]),

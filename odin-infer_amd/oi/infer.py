@@ -12,6 +12,7 @@ silent CPU fallback when the GPU is missing (engine.odin:23-31) is not
 reproduced: engine_load raises instead.
 """
 import ctypes
+import sys
 from dataclasses import dataclass
 
 import numpy as np
@@ -147,6 +148,72 @@ def engine_stream(e):
 def engine_reset_state(e):
     """qwen3_5/engine.odin:108-132: zero the KV cache and the DeltaNet states."""
     check(_native.hip().oi_engine_reset_state(e.handle))
+
+
+def engine_save_kv(e, path, n_valid_pos):
+    """engine_save_kv (qwen3_5/kv_persist.odin:365-372): write the .oikv v1
+    file of positions [0, n_valid_pos) and the DeltaNet states.  As the
+    reference: the message goes to stderr and the result is False on failure."""
+    rc = _native.hip().oi_engine_save_kv(e.handle, str(path).encode(), int(n_valid_pos))
+    if rc != 0:
+        print(_native.hip().oi_last_error().decode(), file=sys.stderr)
+    return rc == 0
+
+
+def engine_load_kv(e, path):
+    """engine_load_kv (kv_persist.odin:374-381): (n_valid_pos, True), or
+    (0, False) with the reason on stderr when the file is refused."""
+    n = ctypes.c_int32()
+    rc = _native.hip().oi_engine_load_kv(e.handle, str(path).encode(), ctypes.byref(n))
+    if rc != 0:
+        print(_native.hip().oi_last_error().decode(), file=sys.stderr)
+        return 0, False
+    return n.value, True
+
+
+def engine_state_sizes(e):
+    """Byte sizes of (kv_k, kv_v, conv, rec) snapshots."""
+    s = (ctypes.c_int64 * 4)()
+    check(_native.hip().oi_engine_state_sizes(e.handle, s))
+    return tuple(s)
+
+
+def _buf(n):
+    return np.empty(n, np.uint8)
+
+
+def engine_save_full_state(e):
+    """engine_save_full_state (qwen3_5/engine.odin:139-144): host copies
+    (kv_k, kv_v, conv, rec) of the device state, in its layout."""
+    bufs = [_buf(n) for n in engine_state_sizes(e)]
+    check(_native.hip().oi_engine_save_full_state(e.handle, *[b.ctypes.data for b in bufs]))
+    return tuple(bufs)
+
+
+def engine_restore_full_state(e, kv_k, kv_v, conv, rec):
+    """engine_restore_full_state (qwen3_5/engine.odin:146-151)."""
+    bufs = [np.ascontiguousarray(b, np.uint8) for b in (kv_k, kv_v, conv, rec)]
+    for b, n in zip(bufs, engine_state_sizes(e)):
+        if b.size != n:
+            raise OIError(-1, "snapshot size %d, the engine holds %d" % (b.size, n))
+    check(_native.hip().oi_engine_restore_full_state(e.handle, *[b.ctypes.data for b in bufs]))
+
+
+def engine_save_spec_state(e):
+    """engine_save_spec_state (qwen3_5/engine.odin:153-158): (conv, rec)."""
+    _, _, nc, nr = engine_state_sizes(e)
+    conv, rec = _buf(nc), _buf(nr)
+    check(_native.hip().oi_engine_save_spec_state(e.handle, conv.ctypes.data, rec.ctypes.data))
+    return conv, rec
+
+
+def engine_restore_spec_state(e, conv, rec):
+    """engine_restore_spec_state (qwen3_5/engine.odin:160-165)."""
+    _, _, nc, nr = engine_state_sizes(e)
+    conv, rec = np.ascontiguousarray(conv, np.uint8), np.ascontiguousarray(rec, np.uint8)
+    if conv.size != nc or rec.size != nr:
+        raise OIError(-1, "snapshot sizes differ from the engine's")
+    check(_native.hip().oi_engine_restore_spec_state(e.handle, conv.ctypes.data, rec.ctypes.data))
 
 
 def engine_logits_device(e):

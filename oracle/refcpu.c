@@ -1341,6 +1341,220 @@ EXPORT const float *ref_engine_prefill(void *h, const int *tokens, int n, int po
 /* Hidden state after the final norm (test hook for layer-level checks). */
 EXPORT const float *ref_engine_hidden(void *h) { return ((ref_engine *)h)->x; }
 
+/* ------------------------------------------------------ state persistence --
+ * engine_reset_state (qwen3_5/engine.odin:112-132) and the .oikv v1 file of
+ * qwen3_5/kv_persist.odin:1-381: cpu_save_kv (:218-265) / cpu_load_kv
+ * (:267-336) for the f32 caches of the dense layers, metal_save_kv /
+ * metal_load_kv's head-major f16 conversion (qwen3_5/metal.odin:780-962) for
+ * the f16 caches of the Qwen3.5 full-attention layers.  The header is the 60
+ * bytes write_header emits (kv_persist.odin:141-156); the checksum is CRC-32
+ * (IEEE, reflected 0xEDB88320) over header + body, appended last. */
+
+EXPORT void ref_engine_reset_state(void *h) {
+    ref_engine *e = (ref_engine *)h;
+    int64_t kv_dim = e->n_kv_heads * e->head_dim, conv_dim = 2 * e->lin_nk * e->lin_hk + e->lin_nv * e->lin_hv;
+    memset(e->key_cache, 0, (size_t)(e->n_layers * e->seq_len * kv_dim) * 4);
+    memset(e->value_cache, 0, (size_t)(e->n_layers * e->seq_len * kv_dim) * 4);
+    for (int64_t l = 0; l < e->n_layers; l++) {
+        layer_w *lw = &e->layers[l];
+        if (lw->kind == 2) {
+            memset(lw->conv_state, 0, (size_t)(conv_dim * (e->lin_kernel - 1)) * 4);
+            memset(lw->rec_state, 0, (size_t)(e->lin_nv * e->lin_hk * e->lin_hv) * 4);
+        } else if (lw->kind == 1) {
+            memset(lw->kc16, 0, (size_t)(e->n_kv_heads * e->seq_len * e->head_dim) * 2);
+            memset(lw->vc16, 0, (size_t)(e->n_kv_heads * e->seq_len * e->head_dim) * 2);
+        }
+    }
+}
+
+static uint32_t kv_crc_update(uint32_t crc, const uint8_t *p, size_t n) {
+    /* bitwise form of the reflected CRC-32 (crc holds the complemented register) */
+    for (size_t i = 0; i < n; i++) {
+        crc ^= p[i];
+        for (int k = 0; k < 8; k++) crc = (crc >> 1) ^ (0xEDB88320u & (0u - (crc & 1u)));
+    }
+    return crc;
+}
+
+/* model_fingerprint, kv_persist.odin:74-93 */
+static uint64_t kv_fingerprint(const ref_engine *e) {
+    uint64_t h = 0xcbf29ce484222325ull;
+    int64_t f[11] = {e->dim, e->n_layers, e->n_heads, e->n_kv_heads, e->head_dim, e->lin_nk,
+                     e->lin_nv, e->lin_hk, e->lin_hv, e->lin_kernel, e->vocab_size};
+    for (int i = 0; i < 11; i++) h = (h ^ (uint64_t)f[i]) * 0x100000001b3ull;
+    return h;
+}
+
+/* 2 = KV_ARCH_QWEN3_5 (kv_persist.odin:53); 1 and 3 for the layouts the reference does not persist */
+static uint32_t kv_arch(const ref_engine *e) { return e->arch == 2 ? 2u : e->arch == 1 ? 3u : 1u; }
+
+typedef struct { FILE *f; uint32_t crc; int bad; } kv_out;
+
+static void kv_put(kv_out *o, const void *p, size_t n) {
+    o->crc = kv_crc_update(o->crc, (const uint8_t *)p, n);
+    if (fwrite(p, 1, n, o->f) != n) o->bad = 1;
+}
+static void kv_put_u32(kv_out *o, uint32_t v) {
+    uint8_t b[4] = {(uint8_t)v, (uint8_t)(v >> 8), (uint8_t)(v >> 16), (uint8_t)(v >> 24)};
+    kv_put(o, b, 4);
+}
+
+static void kv_header_fields(const ref_engine *e, uint32_t n_valid, uint32_t out[10], int64_t *n_full, int64_t *n_lin) {
+    *n_full = *n_lin = 0;
+    for (int64_t l = 0; l < e->n_layers; l++) {
+        if (e->layers[l].kind == 2) (*n_lin)++;
+        else (*n_full)++;
+    }
+    uint32_t v[10] = {n_valid, (uint32_t)e->seq_len, (uint32_t)*n_full, (uint32_t)*n_lin,
+                      (uint32_t)(e->n_kv_heads * e->head_dim), (uint32_t)(2 * e->lin_nk * e->lin_hk + e->lin_nv * e->lin_hv),
+                      (uint32_t)e->lin_kernel, (uint32_t)e->lin_nv, (uint32_t)e->lin_hk, (uint32_t)e->lin_hv};
+    memcpy(out, v, sizeof v);
+}
+
+/* K or V of attention layer l at positions [0, n) as f32 rows [n][kv_dim] */
+static void kv_layer_rows(const ref_engine *e, int64_t l, int which, int64_t n, float *rows) {
+    const layer_w *lw = &e->layers[l];
+    int64_t kv_dim = e->n_kv_heads * e->head_dim, hd = e->head_dim;
+    if (lw->kind == 0) { /* cpu_save_kv: the layer's [seq_len][kv_dim] slice */
+        const float *src = (which ? e->value_cache : e->key_cache) + l * e->seq_len * kv_dim;
+        memcpy(rows, src, (size_t)(n * kv_dim) * 4);
+        return;
+    }
+    const uint16_t *c = which ? lw->vc16 : lw->kc16; /* metal_save_kv's conversion */
+    for (int64_t kh = 0; kh < e->n_kv_heads; kh++)
+        for (int64_t p = 0; p < n; p++)
+            for (int64_t d = 0; d < hd; d++)
+                rows[p * kv_dim + kh * hd + d] = ref_f16_to_f32(c[(kh * e->seq_len + p) * hd + d]);
+}
+
+EXPORT int ref_engine_save_kv(void *h, const char *path, int n_valid_pos) {
+    ref_engine *e = (ref_engine *)h;
+    if (n_valid_pos < 0 || n_valid_pos > e->seq_len) {
+        snprintf(g_err, sizeof g_err, "kv: n_valid_pos %d > seq_len %lld", n_valid_pos, (long long)e->seq_len);
+        return -1;
+    }
+    kv_out o = {fopen(path, "wb"), 0xFFFFFFFFu, 0};
+    if (!o.f) { snprintf(g_err, sizeof g_err, "kv: cannot open %s for write", path); return -1; }
+    uint32_t f[10];
+    int64_t n_full, n_lin;
+    kv_header_fields(e, (uint32_t)n_valid_pos, f, &n_full, &n_lin);
+    kv_put_u32(&o, 0x4F494B56u);
+    kv_put_u32(&o, 1);
+    kv_put_u32(&o, kv_arch(e));
+    uint64_t fp = kv_fingerprint(e);
+    kv_put_u32(&o, (uint32_t)fp);
+    kv_put_u32(&o, (uint32_t)(fp >> 32));
+    for (int i = 0; i < 10; i++) kv_put_u32(&o, f[i]);
+    int64_t kv_dim = e->n_kv_heads * e->head_dim;
+    float *rows = (float *)malloc((size_t)(n_valid_pos * kv_dim + 1) * 4);
+    for (int64_t l = 0; l < e->n_layers && rows; l++) {
+        if (e->layers[l].kind == 2) continue;
+        for (int which = 0; which < 2; which++) {
+            kv_layer_rows(e, l, which, n_valid_pos, rows);
+            kv_put(&o, rows, (size_t)(n_valid_pos * kv_dim) * 4);
+        }
+    }
+    free(rows);
+    int64_t conv_n = (2 * e->lin_nk * e->lin_hk + e->lin_nv * e->lin_hv) * (e->lin_kernel > 0 ? e->lin_kernel - 1 : 0);
+    int64_t rec_n = e->lin_nv * e->lin_hk * e->lin_hv;
+    for (int64_t l = 0; l < e->n_layers; l++)
+        if (e->layers[l].kind == 2) kv_put(&o, e->layers[l].conv_state, (size_t)conv_n * 4);
+    for (int64_t l = 0; l < e->n_layers; l++)
+        if (e->layers[l].kind == 2) kv_put(&o, e->layers[l].rec_state, (size_t)rec_n * 4);
+    uint32_t crc = o.crc ^ 0xFFFFFFFFu;
+    kv_put_u32(&o, crc);
+    if (fclose(o.f) != 0) o.bad = 1;
+    if (o.bad) { snprintf(g_err, sizeof g_err, "kv: write failed"); return -1; }
+    return 0;
+}
+
+static int kv_fail(FILE *f, const char *msg) {
+    snprintf(g_err, sizeof g_err, "%s", msg);
+    if (f) fclose(f);
+    return -1;
+}
+
+/* Returns the restored n_valid_pos, or -1 (message in ref_last_error). */
+EXPORT int ref_engine_load_kv(void *h, const char *path) {
+    ref_engine *e = (ref_engine *)h;
+    FILE *f = fopen(path, "rb");
+    if (!f) return kv_fail(NULL, "kv: cannot open file");
+    uint8_t hb[60];
+    if (fread(hb, 1, 60, f) != 60) return kv_fail(f, "kv: header truncated");
+    uint32_t w[15];
+    for (int i = 0; i < 15; i++)
+        w[i] = (uint32_t)hb[4 * i] | (uint32_t)hb[4 * i + 1] << 8 | (uint32_t)hb[4 * i + 2] << 16 |
+               (uint32_t)hb[4 * i + 3] << 24;
+    uint64_t fp = (uint64_t)w[3] | (uint64_t)w[4] << 32;
+    uint32_t mine[10];
+    int64_t n_full, n_lin;
+    kv_header_fields(e, 0, mine, &n_full, &n_lin);
+    if (w[0] != 0x4F494B56u) return kv_fail(f, "kv: bad magic");
+    if (w[1] != 1) return kv_fail(f, "kv: version mismatch");
+    if (w[2] != kv_arch(e)) return kv_fail(f, "kv: arch mismatch");
+    if (fp != kv_fingerprint(e)) return kv_fail(f, "kv: fingerprint mismatch");
+    if (w[6] != mine[1]) return kv_fail(f, "kv: seq_len mismatch");
+    if (w[5] > mine[1]) return kv_fail(f, "kv: file n_valid_pos > engine seq_len");
+    for (int i = 2; i < 10; i++)
+        if (w[5 + i] != mine[i]) return kv_fail(f, "kv: layer dimensions differ");
+    /* verify_crc32 over everything but the last 4 bytes, before touching the state */
+    fseek(f, 0, SEEK_END);
+    long size = ftell(f);
+    if (size < 64) return kv_fail(f, "kv: file too short");
+    rewind(f);
+    uint32_t crc = 0xFFFFFFFFu;
+    uint8_t buf[65536];
+    long left = size - 4;
+    while (left > 0) {
+        size_t n = left > (long)sizeof buf ? sizeof buf : (size_t)left;
+        if (fread(buf, 1, n, f) != n) return kv_fail(f, "kv: read failed");
+        crc = kv_crc_update(crc, buf, n);
+        left -= (long)n;
+    }
+    if (fread(buf, 1, 4, f) != 4) return kv_fail(f, "kv: read failed");
+    uint32_t stored = (uint32_t)buf[0] | (uint32_t)buf[1] << 8 | (uint32_t)buf[2] << 16 | (uint32_t)buf[3] << 24;
+    if ((crc ^ 0xFFFFFFFFu) != stored) return kv_fail(f, "kv: CRC mismatch — file corrupted");
+    fseek(f, 60, SEEK_SET);
+    int64_t n = w[5], kv_dim = e->n_kv_heads * e->head_dim, hd = e->head_dim;
+    int64_t conv_dim = 2 * e->lin_nk * e->lin_hk + e->lin_nv * e->lin_hv;
+    int64_t conv_n = conv_dim * (e->lin_kernel > 0 ? e->lin_kernel - 1 : 0), rec_n = e->lin_nv * e->lin_hk * e->lin_hv;
+    if ((uint64_t)size != 60u + 8u * (uint64_t)(n_full * n * kv_dim) + 4u * (uint64_t)(n_lin * (conv_n + rec_n)) + 4u)
+        return kv_fail(f, "kv: file size does not match its header");
+    /* zero the caches, then read (cpu_load_kv :313-333; f16 caches round as metal_load_kv) */
+    memset(e->key_cache, 0, (size_t)(e->n_layers * e->seq_len * kv_dim) * 4);
+    memset(e->value_cache, 0, (size_t)(e->n_layers * e->seq_len * kv_dim) * 4);
+    float *rows = (float *)malloc((size_t)(n * kv_dim + 1) * 4);
+    if (!rows) return kv_fail(f, "kv: out of memory");
+    for (int64_t l = 0; l < e->n_layers; l++) {
+        layer_w *lw = &e->layers[l];
+        if (lw->kind == 2) continue;
+        for (int which = 0; which < 2; which++) {
+            if (fread(rows, 4, (size_t)(n * kv_dim), f) != (size_t)(n * kv_dim)) { free(rows); return kv_fail(f, "kv: read failed"); }
+            if (lw->kind == 0) {
+                float *dst = (which ? e->value_cache : e->key_cache) + l * e->seq_len * kv_dim;
+                for (int64_t i = 0; i < n * kv_dim; i++)
+                    dst[i] = e->kv_f16 ? ref_f16_to_f32(ref_f32_to_f16(rows[i])) : rows[i];
+            } else {
+                uint16_t *c = which ? lw->vc16 : lw->kc16;
+                memset(c, 0, (size_t)(e->n_kv_heads * e->seq_len * hd) * 2);
+                for (int64_t kh = 0; kh < e->n_kv_heads; kh++)
+                    for (int64_t p = 0; p < n; p++)
+                        for (int64_t d = 0; d < hd; d++)
+                            c[(kh * e->seq_len + p) * hd + d] = ref_f32_to_f16(rows[p * kv_dim + kh * hd + d]);
+            }
+        }
+    }
+    free(rows);
+    for (int64_t l = 0; l < e->n_layers; l++)
+        if (e->layers[l].kind == 2 && fread(e->layers[l].conv_state, 4, (size_t)conv_n, f) != (size_t)conv_n)
+            return kv_fail(f, "kv: conv_states read failed");
+    for (int64_t l = 0; l < e->n_layers; l++)
+        if (e->layers[l].kind == 2 && fread(e->layers[l].rec_state, 4, (size_t)rec_n, f) != (size_t)rec_n)
+            return kv_fail(f, "kv: recurrent_states read failed");
+    fclose(f);
+    return (int)n;
+}
+
 /* Batched prefill projection as the reference's MMQ kernels compute it
  * (gemm_harness/gemm_test.odin:97-135 gemm_q4k_f32, :297-337 gemm_q6k_f32,
  * qwen3_5/metal.odin:493-609): each weight row is dequantized (ggml/quant.odin,

@@ -65,6 +65,9 @@ def lib():
         L.ref_mrope.argtypes = [c_vp, c_int, c_vp, c_int]
         L.ref_qwen35_attn_steps.argtypes = [c_int] * 5 + [c_f, c_int, c_int] + [c_vp] * 9
         L.ref_moe_ffn.argtypes = [c_int] * 6 + [c_vp, c_int] + [c_vp] * 7
+        L.ref_engine_reset_state.argtypes = [c_vp]
+        L.ref_engine_save_kv.argtypes = [c_vp, ctypes.c_char_p, c_int]
+        L.ref_engine_load_kv.argtypes = [c_vp, ctypes.c_char_p]
         _lib = L
     return _lib
 
@@ -187,6 +190,23 @@ class RefEngine:
         rc = lib().ref_engine_kv_fill(self.h, layer, pos0, npos, _p(k16), _p(v16))
         if rc:
             raise RuntimeError(lib().ref_last_error().decode())
+
+    def reset_state(self):
+        """engine_reset_state (qwen3_5/engine.odin:112-132)."""
+        lib().ref_engine_reset_state(self.h)
+
+    def save_kv(self, path, n_valid_pos):
+        """cpu_save_kv (qwen3_5/kv_persist.odin:218-265); raises on failure."""
+        if lib().ref_engine_save_kv(self.h, str(path).encode(), int(n_valid_pos)) != 0:
+            raise RuntimeError(lib().ref_last_error().decode())
+
+    def load_kv(self, path):
+        """cpu_load_kv (kv_persist.odin:267-336): the restored n_valid_pos;
+        raises RuntimeError with the reference's message on a refused file."""
+        n = lib().ref_engine_load_kv(self.h, str(path).encode())
+        if n < 0:
+            raise RuntimeError(lib().ref_last_error().decode())
+        return n
 
     def close(self):
         if self.h:

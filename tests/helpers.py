@@ -45,3 +45,28 @@ def same_bits(a, b):
     b = np.asarray(b, np.float32)
     na, nb = np.isnan(a), np.isnan(b)
     return bool(np.array_equal(na, nb) and np.array_equal(a[~na].view(np.uint32), b[~nb].view(np.uint32)))
+
+
+class DeviceBuffer:
+    """Device memory from the HIP runtime the library itself uses
+    (libamdhip64), for tests that hand device pointers to the C ABI."""
+
+    def __init__(self, nbytes):
+        import ctypes
+        self._hip = ctypes.CDLL("libamdhip64.so")
+        self.nbytes = max(int(nbytes), 1)
+        self.ptr = ctypes.c_void_p()
+        if self._hip.hipMalloc(ctypes.byref(self.ptr), ctypes.c_size_t(self.nbytes)) != 0:
+            raise RuntimeError("hipMalloc failed")
+
+    def to_host(self, n=None):
+        import ctypes
+        out = np.empty(self.nbytes if n is None else n, np.uint8)
+        if self._hip.hipMemcpy(out.ctypes.data_as(ctypes.c_void_p), self.ptr, ctypes.c_size_t(out.size), 2) != 0:
+            raise RuntimeError("hipMemcpy failed")
+        return out
+
+    def free(self):
+        if self.ptr:
+            self._hip.hipFree(self.ptr)
+            self.ptr = None
