@@ -854,6 +854,19 @@ def main():
         tok_s = args.steps / el
         log("decode: %d steps in %.3fs -> %.1f tok/s" % (args.steps, el, tok_s))
 
+        # the same loop with the sampler on the device (serve_harness's
+        # temperature and top-p, serve.odin:1544, with a nonzero seed)
+        smp = infer.Sampler(0.6, 0.95, rng_seed=42)
+        infer.engine_decode_sample(e, 0, CONTEXT, min(16, args.steps), smp)  # warm, captures its graph
+        t0 = time.perf_counter()
+        infer.engine_decode_sample(e, 0, CONTEXT, args.steps, smp)
+        el_s = time.perf_counter() - t0
+        sampled = {"temperature": 0.6, "topp": 0.95, "tok_s": round(args.steps / el_s, 2),
+                   "ms_per_token": round(1000 * el_s / args.steps, 4),
+                   "sampler_us_per_token": round(1e6 * (el_s - el) / args.steps, 2)}
+        log("sampled decode (T 0.6, top-p 0.95): %.1f tok/s, sampler %.1f us/token" % (
+            sampled["tok_s"], sampled["sampler_us_per_token"]))
+
         # whole-step algorithmic bytes at the mean position of the timed steps
         wb = weight_bytes(spec)
         mean_pos = CONTEXT + (args.steps - 1) / 2.0
@@ -870,7 +883,7 @@ def main():
             kern[name] = {"us": us, "bytes": b, "GBps": b / us / 1e3}
         if args.only == "decode":
             print(json.dumps({"decode_tok_s": round(tok_s, 2), "ms_per_step": round(1000 * el / args.steps, 4),
-                              "kernels": {n: {"avg_us": round(d["us"], 3), "GBps": round(d["GBps"], 1)}
+                              "sampled_decode": sampled, "kernels": {n: {"avg_us": round(d["us"], 3), "GBps": round(d["GBps"], 1)}
                                           for n, d in kern.items()}}), flush=True)
             infer.engine_destroy(e)
             return
@@ -941,6 +954,7 @@ def main():
                            "frac_of_peak": round(loop_gbps / PEAK_HBM_GBPS, 4),
                            "roofline_tok_s": round(PEAK_HBM_GBPS * 1e9 / bpt, 1)},
             "kernels": {n: {"avg_us": round(d["us"], 3), "GBps": round(d["GBps"], 1)} for n, d in kern.items()},
+            "sampled_decode": sampled,
             "cpu_baseline": cpu,
             "prefill_gemm": gemm,
             "prefill": prefill,

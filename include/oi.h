@@ -117,6 +117,36 @@ const char *oi_last_error(void);
 int oi_engine_decode_greedy(oi_engine *e, int32_t token, int32_t pos, int32_t n_steps,
                             int32_t *out_tokens);
 
+/* Sampler (sampler/sampler.odin:16-29 build_sampler / enable_repeat_penalty,
+ * without the JSON grammar mask).  The state is the caller's and is written
+ * back after each call: rng_state advanced once per draw (xorshift64*,
+ * random_u32 :68-73), and, with record set and repeat_penalty != 1, last[]
+ * extended by each pick and trimmed to the newest 64 (record_token :50-56). */
+typedef struct oi_sampler {
+    float temperature;    /* 0: first maximum (sample_argmax :79-89) */
+    float topp;           /* in (0, 1): sample_topp (:106-139); otherwise sample_mult (:91-100) */
+    float repeat_penalty; /* 1: off; logits of distinct recent tokens divided (> 0) or multiplied */
+    int32_t record;       /* 1: append each pick to last[] as record_token does */
+    uint64_t rng_state;
+    int32_t n_last;       /* tokens in last[], oldest first (<= 64) */
+    int32_t last[64];
+} oi_sampler;
+
+/* Decode loop with sampling on the device (the caller loop of
+ * serve_harness/serve.odin:514-525 with sampler.sample): step i consumes the
+ * current token at pos+i and draws the next as sample() does -- penalty,
+ * temperature, softmax, one coin, multinomial or top-p -- on the device.
+ * Running probabilities are summed exactly (64-bit fixed point, 2^-40), so a
+ * pick differs from the reference's sequential f32 sums only where the coin
+ * lies within their rounding of a boundary.  Writes the n_steps picks to
+ * out_tokens and the advanced sampler state to *s. */
+int oi_engine_decode_sample(oi_engine *e, int32_t token, int32_t pos, int32_t n_steps, oi_sampler *s,
+                            int32_t *out_tokens);
+
+/* One draw of the same sampler on n host logits (synchronous; the logits are
+ * not modified).  *s is advanced as above. */
+int oi_sample(const float *logits, int32_t n, oi_sampler *s, int32_t *out_token);
+
 /* Overwrite positions [pos0, pos0+npos) of layers [layer0, layer0+nlayers) of
  * the f16 KV cache with host data laid out [layer][kv_head][npos][head_dim]
  * (binary16 bits).  Used to pre-fill long contexts for measurement. */

@@ -80,6 +80,12 @@ struct oi_engine {
     oi::GemvArgs g_out{};
     hipGraph_t graph = nullptr;
     hipGraphExec_t gexec = nullptr;
+    // sampled decoding: the sampler's device state, its probability scratch
+    // [vocab], and the token step + sampler graph
+    oi::SampleState *samp = nullptr;
+    float *samp_p = nullptr;
+    hipGraph_t graph_s = nullptr;
+    hipGraphExec_t gexec_s = nullptr;
     int last_pos = 0;
     size_t weight_bytes = 0;
     // batched prefill buffers (allocated on the first prefill): token ids,

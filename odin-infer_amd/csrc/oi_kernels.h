@@ -103,6 +103,18 @@ struct GemvArgs {
 //   [4] argmax pending  [5] number of argmax partials
 enum { ST_TOKEN = 0, ST_POS = 1, ST_STEP = 2, ST_CAP = 3, ST_PENDING = 4, ST_NPART = 5, ST_WORDS = 8 };
 
+// Sampler state in device memory (sampler/sampler.odin:16-29 without the
+// grammar): updated by every draw (rng) and, with `record`, by every pick
+// (record_token, window SAMPLE_WINDOW).
+constexpr int SAMPLE_WINDOW = 64;
+struct SampleState {
+    float temperature, topp, penalty;
+    int32_t record;
+    uint64_t rng;
+    int32_t n_last;
+    int32_t last[SAMPLE_WINDOW];  // oldest first
+};
+
 struct AttnArgs {
     const float *q, *k, *v;    // this token's raw projections
     const float *q_norm, *k_norm;
@@ -129,6 +141,13 @@ hipError_t launch_embed(const DMat &emb, int32_t *state, float *x, int32_t vocab
 int attn_chunk(int head_dim);
 int attn_max_splits();
 hipError_t launch_dequant(const DMat &m, float *out, hipStream_t st);
+// One draw of the sampler (sample.hip) from logits[0, n); p: n floats of
+// scratch.  With `state` set the pick advances the token loop (token, pos,
+// step, pending as the greedy reduction does) and is stored at
+// tokens_out[step]; `pick`, if set, receives it too.
+hipError_t launch_sample(const float *logits, float *p, int n, SampleState *ss, int32_t *state, int32_t *tokens_out,
+                         int32_t *pick, hipStream_t st);
+int sample_max_vocab();  // largest n launch_sample takes
 // f16 head-major cache [n_kv][seq_len][hd], positions [0, n) <-> f32 rows
 // [n][n_kv * hd]; to_f32: cache -> rows, else rows -> cache (RNE)
 hipError_t launch_kv_convert(bool to_f32, uint16_t *cache, float *rows, int n, int n_kv, int seq_len, int hd,

@@ -42,6 +42,12 @@ class Config(ctypes.Structure):
                 ("head_dim", c_i64), ("rope_freq", c_f), ("rms_eps", c_f)]
 
 
+class Sampler(ctypes.Structure):
+    """oi_sampler (include/oi.h): sampler/sampler.odin:16-29 without the grammar."""
+    _fields_ = [("temperature", c_f), ("topp", c_f), ("repeat_penalty", c_f), ("record", c_i32),
+                ("rng_state", ctypes.c_uint64), ("n_last", c_i32), ("last", c_i32 * 64)]
+
+
 # every symbol include/oi.h declares, with (restype, argtypes)
 HIP_SYMBOLS = {
     "oi_engine_load": (c_i32, [ctypes.c_char_p, ctypes.POINTER(Opts), ctypes.POINTER(c_vp)]),
@@ -53,6 +59,8 @@ HIP_SYMBOLS = {
     "oi_engine_decode_greedy": (c_i32, [c_vp, c_i32, c_i32, c_i32, c_vp]),
     "oi_engine_kv_fill": (c_i32, [c_vp, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp]),
     "oi_engine_reset_state": (c_i32, [c_vp]),
+    "oi_engine_decode_sample": (c_i32, [c_vp, c_i32, c_i32, c_i32, ctypes.POINTER(Sampler), c_vp]),
+    "oi_sample": (c_i32, [c_vp, c_i32, ctypes.POINTER(Sampler), ctypes.POINTER(c_i32)]),
     "oi_engine_save_kv": (c_i32, [c_vp, ctypes.c_char_p, c_i32]),
     "oi_engine_load_kv": (c_i32, [c_vp, ctypes.c_char_p, c_vp]),
     "oi_engine_state_sizes": (c_i32, [c_vp, c_vp]),

@@ -123,6 +123,51 @@ def engine_decode_greedy(e, token, pos, n_steps):
     return out
 
 
+class Sampler:
+    """sampler.Sampler (sampler/sampler.odin:16-38) without the grammar:
+    build_sampler's temperature, topp and rng seed, enable_repeat_penalty's
+    penalty, and the recent-token window that record_token keeps."""
+
+    def __init__(self, temperature, topp, rng_seed=0, repeat_penalty=1.0, record=False, last=()):
+        self.temperature, self.topp, self.rng_state = float(temperature), float(topp), int(rng_seed)
+        self.repeat_penalty = max(float(repeat_penalty), 1.0)  # enable_repeat_penalty clamps (:42-44)
+        self.record = bool(record)
+        self.last = [int(t) for t in last][-64:]
+
+    def _c(self):
+        c = _native.Sampler(self.temperature, self.topp, self.repeat_penalty, int(self.record), self.rng_state,
+                            len(self.last))
+        for i, t in enumerate(self.last):
+            c.last[i] = t
+        return c
+
+    def _take(self, c):
+        self.rng_state = c.rng_state
+        self.last = [int(c.last[i]) for i in range(c.n_last)]
+
+
+def sample(s, logits):
+    """sampler.sample (sampler.odin:141-199) on the device for host logits;
+    the logits are not modified.  Advances s."""
+    x = np.ascontiguousarray(logits, np.float32)
+    c = s._c()
+    out = ctypes.c_int32()
+    check(_native.hip().oi_sample(x.ctypes.data, int(x.size), ctypes.byref(c), ctypes.byref(out)))
+    s._take(c)
+    return out.value
+
+
+def engine_decode_sample(e, token, pos, n_steps, s):
+    """Decode loop with the sampler on the device; returns the n_steps picks
+    and advances s."""
+    out = np.empty(n_steps, np.int32)
+    c = s._c()
+    check(_native.hip().oi_engine_decode_sample(e.handle, int(token), int(pos), int(n_steps), ctypes.byref(c),
+                                                out.ctypes.data))
+    s._take(c)
+    return out
+
+
 def engine_kv_fill(e, layer0, pos0, k16, v16):
     """k16, v16: uint16 [nlayers][n_kv_heads][npos][head_dim] binary16 bits."""
     k16 = np.ascontiguousarray(k16, np.uint16)

@@ -1341,6 +1341,105 @@ EXPORT const float *ref_engine_prefill(void *h, const int *tokens, int n, int po
 /* Hidden state after the final norm (test hook for layer-level checks). */
 EXPORT const float *ref_engine_hidden(void *h) { return ((ref_engine *)h)->x; }
 
+/* ---------------------------------------------------------------- sampler --
+ * sampler/sampler.odin:68-199 without the grammar mask.  slice.sort_by
+ * (:118) leaves equal probabilities in an unspecified order; here they keep
+ * index order (the comparator breaks ties by index). */
+
+static uint32_t ref_random_u32(uint64_t *state) { /* :68-73 */
+    *state ^= *state >> 12;
+    *state ^= *state << 25;
+    *state ^= *state >> 27;
+    return (uint32_t)((*state * 0x2545F4914F6CDD1Dull) >> 32);
+}
+
+EXPORT float ref_random_f32(uint64_t *state) { return (float)(ref_random_u32(state) >> 8) / 16777216.0f; }
+
+static int64_t ref_sample_mult(const float *p, int64_t n, float coin) { /* :91-100 */
+    float cdf = 0.0f;
+    for (int64_t i = 0; i < n; i++) {
+        cdf += p[i];
+        if (coin < cdf) return i;
+    }
+    return n - 1;
+}
+
+typedef struct { float prob; int64_t index; } prob_index;
+
+static int prob_index_cmp(const void *a, const void *b) {
+    const prob_index *x = (const prob_index *)a, *y = (const prob_index *)b;
+    if (x->prob > y->prob) return -1;
+    if (x->prob < y->prob) return 1;
+    return x->index < y->index ? -1 : x->index > y->index;
+}
+
+static int64_t ref_sample_topp(const float *p, int64_t n, float topp, prob_index *pi, float coin) { /* :106-139 */
+    int64_t n0 = 0;
+    float cutoff = (1.0f - topp) / (float)(n - 1);
+    for (int64_t i = 0; i < n; i++)
+        if (p[i] >= cutoff) {
+            pi[n0].index = i;
+            pi[n0].prob = p[i];
+            n0++;
+        }
+    qsort(pi, (size_t)n0, sizeof *pi, prob_index_cmp);
+    float cumulative_prob = 0.0f;
+    int64_t last_idx = n0 - 1;
+    for (int64_t i = 0; i < n0; i++) {
+        cumulative_prob += pi[i].prob;
+        if (cumulative_prob > topp) {
+            last_idx = i;
+            break;
+        }
+    }
+    float r = coin * cumulative_prob;
+    float cdf = 0.0f;
+    for (int64_t i = 0; i <= last_idx; i++) {
+        cdf += pi[i].prob;
+        if (r < cdf) return pi[i].index;
+    }
+    return pi[last_idx].index;
+}
+
+/* sample (:141-199): logits are modified in place, as the reference's are. */
+EXPORT int64_t ref_sample(float *logits, int64_t n, float temperature, float topp, float penalty,
+                          const int32_t *last, int n_last, uint64_t *rng) {
+    if (penalty != 1.0f && n_last > 0) {
+        int32_t seen[64];
+        int ns = 0;
+        for (int i = 0; i < n_last; i++) {
+            int32_t tok = last[i];
+            if (tok < 0 || tok >= n) continue;
+            int dup = 0;
+            for (int j = 0; j < ns; j++) dup |= seen[j] == tok;
+            if (dup) continue;
+            if (ns < 64) seen[ns++] = tok;
+            if (logits[tok] > 0) logits[tok] /= penalty;
+            else logits[tok] *= penalty;
+        }
+    }
+    if (temperature == 0.0f) return ref_argmax(logits, n);
+    for (int64_t i = 0; i < n; i++) logits[i] /= temperature;
+    ref_softmax(logits, n);
+    float coin = ref_random_f32(rng);
+    if (topp <= 0 || topp >= 1) return ref_sample_mult(logits, n, coin);
+    prob_index *pi = (prob_index *)malloc((size_t)n * sizeof *pi);
+    if (!pi) return -1;
+    int64_t r = ref_sample_topp(logits, n, topp, pi, coin);
+    free(pi);
+    return r;
+}
+
+/* record_token (:50-56) with its default window 64; last has room for 65 */
+EXPORT void ref_record_token(int32_t *last, int *n_last, int32_t token, float penalty) {
+    if (penalty == 1.0f) return;
+    last[(*n_last)++] = token;
+    while (*n_last > 64) {
+        memmove(last, last + 1, (size_t)(*n_last - 1) * sizeof *last);
+        (*n_last)--;
+    }
+}
+
 /* ------------------------------------------------------ state persistence --
  * engine_reset_state (qwen3_5/engine.odin:112-132) and the .oikv v1 file of
  * qwen3_5/kv_persist.odin:1-381: cpu_save_kv (:218-265) / cpu_load_kv

@@ -66,6 +66,11 @@ def lib():
         L.ref_qwen35_attn_steps.argtypes = [c_int] * 5 + [c_f, c_int, c_int] + [c_vp] * 9
         L.ref_moe_ffn.argtypes = [c_int] * 6 + [c_vp, c_int] + [c_vp] * 7
         L.ref_engine_reset_state.argtypes = [c_vp]
+        L.ref_random_f32.restype = c_f
+        L.ref_random_f32.argtypes = [c_vp]
+        L.ref_sample.restype = c_i64
+        L.ref_sample.argtypes = [c_vp, c_i64, c_f, c_f, c_f, c_vp, c_int, c_vp]
+        L.ref_record_token.argtypes = [c_vp, c_vp, ctypes.c_int32, c_f]
         L.ref_engine_save_kv.argtypes = [c_vp, ctypes.c_char_p, c_int]
         L.ref_engine_load_kv.argtypes = [c_vp, ctypes.c_char_p]
         _lib = L
@@ -148,6 +153,33 @@ def get_scale_min_k4(j, q12):
     m = ctypes.c_uint8()
     lib().ref_get_scale_min_k4(j, _p(q), ctypes.byref(sc), ctypes.byref(m))
     return sc.value, m.value
+
+
+def random_f32(rng_state):
+    """random_f32 (sampler/sampler.odin:75-77): (value, advanced state)."""
+    st = ctypes.c_uint64(rng_state)
+    v = lib().ref_random_f32(ctypes.byref(st))
+    return v, st.value
+
+
+def sample(logits, temperature, topp, penalty=1.0, last=(), rng_state=0):
+    """sampler.sample (sampler/sampler.odin:141-199, no grammar) on a copy of
+    logits: (index, advanced rng state)."""
+    x = np.array(logits, np.float32, copy=True)
+    lt = np.ascontiguousarray(last, np.int32)
+    st = ctypes.c_uint64(rng_state)
+    i = lib().ref_sample(_p(x), x.size, float(temperature), float(topp), float(penalty), _p(lt) if lt.size else None,
+                         int(lt.size), ctypes.byref(st))
+    return int(i), st.value
+
+
+def record_token(last, token, penalty):
+    """record_token (sampler.odin:50-56), window 64: the new window."""
+    buf = np.zeros(65, np.int32)
+    buf[:len(last)] = last
+    n = ctypes.c_int(len(last))
+    lib().ref_record_token(_p(buf), ctypes.byref(n), int(token), float(penalty))
+    return [int(t) for t in buf[:n.value]]
 
 
 class RefEngine:
