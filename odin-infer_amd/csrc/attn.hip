@@ -13,10 +13,11 @@
 //   2. RMSNorm + RoPE the G query heads (and, in the split that holds `pos`,
 //      the new key; K/V[pos] are rounded to f16 and stored),
 //   3. stage K (rows padded against bank conflicts) and V in LDS,
-//   4. scores: lane l takes positions l, l+64, ... over a quarter of the
-//      dimensions (one quarter per wave); divided by sqrt(hd) (forward.odin:158),
-//   5. split max / exp-sum per head, o = sum_t p v_t (2 dims per lane),
-//   6. write (o, m, l) to the partial buffer.
+//   4. one wave per query head, with no workgroup barrier: scores with lane l
+//      taking position l (the whole dot product of its K row), divided by
+//      sqrt(hd) (forward.odin:158); split max / exp-sum by wave reductions;
+//      o = sum_t p v_t with 2 dims per lane and p read from the wave's LDS row,
+//   5. write (o, m, l) to the partial buffer.
 // attn_combine_kernel merges the splits of each query head with
 // exp(m_s - M) weights; the kernel boundary orders the partial writes before
 // the reads, so no fences or atomics are needed.  (Merging in the last
@@ -54,9 +55,8 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t vs[S::CH * HD];
     __shared__ __attribute__((aligned(16))) float qr[G][HD];
     __shared__ float kp[HD], vp[HD], qn[HD], kn[HD];
-    __shared__ float sp[4][G][S::CH];  // per-wave partial scores, then p in sp[0]
-    __shared__ float ob[4][G][HD];
-    __shared__ float mx[G], sm[G], nrm[G + 1];
+    __shared__ __attribute__((aligned(16))) float sp[1][G][S::CH];  // p of each head (its wave's row)
+    __shared__ float nrm[G + 1];
     __shared__ float2 csl[HD / 2];
 
     const int split = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
@@ -146,49 +146,29 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
         __syncthreads();
     }
 
-    // 4. partial scores: lane = positions lane + 64 p, wave = quarter of the dimensions
-    {
-        float acc[G][S::PPL];
-#pragma unroll
-        for (int g = 0; g < G; g++)
-#pragma unroll
-            for (int p = 0; p < S::PPL; p++) acc[g][p] = 0.f;
-#pragma unroll
-        for (int c = 0; c < S::DPW / 8; c++) {
-#pragma unroll
-            for (int p = 0; p < S::PPL; p++) {
-                const u32x4 w = *(const u32x4 *)(ks + (lane + WAVE * p) * S::KPAD + wave * S::DPW + 8 * c);
-                const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-                float kv[8];
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    kv[2 * e] = h2f(ws[e] & 0xFFFFu);
-                    kv[2 * e + 1] = h2f(ws[e] >> 16);
-                }
-#pragma unroll
-                for (int g = 0; g < G; g++) {
-                    const float4 q0 = *(const float4 *)&qr[g][wave * S::DPW + 8 * c];
-                    const float4 q1 = *(const float4 *)&qr[g][wave * S::DPW + 8 * c + 4];
-                    acc[g][p] += q0.x * kv[0] + q0.y * kv[1] + q0.z * kv[2] + q0.w * kv[3] + q1.x * kv[4] +
-                                 q1.y * kv[5] + q1.z * kv[6] + q1.w * kv[7];
-                }
-            }
-        }
-#pragma unroll
-        for (int g = 0; g < G; g++)
-#pragma unroll
-            for (int p = 0; p < S::PPL; p++) sp[wave][g][lane + WAVE * p] = acc[g][p];
-    }
-    __syncthreads();
-
-    // 5. scores, split-local max and exp-sum (ops.odin:21-37), one wave per head
+    // 4-6. one wave per query head, no workgroup barrier: scores with lane =
+    // position (each lane the whole dot product of its row), split max and
+    // exp-sum by wave reductions (ops.odin:21-37), p through this wave's LDS
+    // row, o = sum_t p(t) v(t) with DPL dimensions per lane, then the split's
+    // (o, m, l).  Score = q.k / sqrt(hd) (forward.odin:158 divides).
     const float div = sqrtf((float)HD);
+    const int stride = HD + 2;
     for (int g = wave; g < G; g += WG / WAVE) {
         float sc[S::PPL], m = -INFINITY;
 #pragma unroll
         for (int p = 0; p < S::PPL; p++) {
             const int t = lane + WAVE * p;
-            sc[p] = t < n ? ((sp[0][g][t] + sp[1][g][t]) + (sp[2][g][t] + sp[3][g][t])) / div : -INFINITY;
+            float acc[4] = {0.f, 0.f, 0.f, 0.f};  // four chains over the 8-dimension chunks
+#pragma unroll
+            for (int c = 0; c < HD / 8; c++) {
+                const u32x4 w = *(const u32x4 *)(ks + t * S::KPAD + 8 * c);
+                const float4 q0 = *(const float4 *)&qr[g][8 * c];
+                const float4 q1 = *(const float4 *)&qr[g][8 * c + 4];
+                acc[c & 3] += q0.x * h2f(w.x & 0xFFFFu) + q0.y * h2f(w.x >> 16) + q0.z * h2f(w.y & 0xFFFFu) +
+                              q0.w * h2f(w.y >> 16) + q1.x * h2f(w.z & 0xFFFFu) + q1.y * h2f(w.z >> 16) +
+                              q1.z * h2f(w.w & 0xFFFFu) + q1.w * h2f(w.w >> 16);
+            }
+            sc[p] = t < n ? ((acc[0] + acc[1]) + (acc[2] + acc[3])) / div : -INFINITY;
             m = fmaxf(m, sc[p]);
         }
         m = wave_max(m);
@@ -197,60 +177,44 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
         for (int p = 0; p < S::PPL; p++) {
             const int t = lane + WAVE * p;
             const float e = t < n ? expf(sc[p] - m) : 0.f;
-            sp[0][g][t] = e;
+            sp[0][g][t] = e;  // this wave's row only: DS operations of one wave complete in order
             l += e;
         }
         l = wave_sum(l);
-        if (lane == 0) {
-            mx[g] = m;
-            sm[g] = l;
-        }
-    }
-    __syncthreads();
-
-    // o_g = sum_t p_g(t) v(t): lane holds DPL dims, wave w takes t = w, w+4, ...
-    {
-        float acc[G][S::DPL];
+        __builtin_amdgcn_wave_barrier();
+        float acc[4][S::DPL];
 #pragma unroll
-        for (int g = 0; g < G; g++)
+        for (int j = 0; j < 4; j++)
 #pragma unroll
-            for (int e = 0; e < S::DPL; e++) acc[g][e] = 0.f;
-        for (int tl = wave; tl < n; tl += WG / WAVE) {
-            float vv[S::DPL];
-            if (S::DPL == 2) {
-                const uint32_t w = *(const uint32_t *)(vs + tl * HD + 2 * lane);
-                vv[0] = h2f(w & 0xFFFFu);
-                vv[S::DPL - 1] = h2f(w >> 16);
-            } else {
-                const u32x2 w = *(const u32x2 *)(vs + tl * HD + S::DPL * lane);
-                const uint32_t ws[2] = {w.x, w.y};
+            for (int e = 0; e < S::DPL; e++) acc[j][e] = 0.f;
+#pragma unroll 4
+        for (int t4 = 0; t4 < S::CH; t4 += 4) {
+            const float4 p4 = *(const float4 *)&sp[0][g][t4];  // rows past n hold p = 0 and zero V
+            const float pw[4] = {p4.x, p4.y, p4.z, p4.w};
 #pragma unroll
-                for (int e = 0; e < S::DPL; e++) vv[e] = h2f((ws[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
-            }
+            for (int j = 0; j < 4; j++) {
+                float vv[S::DPL];
+                if (S::DPL == 2) {
+                    const uint32_t w = *(const uint32_t *)(vs + (t4 + j) * HD + 2 * lane);
+                    vv[0] = h2f(w & 0xFFFFu);
+                    vv[S::DPL - 1] = h2f(w >> 16);
+                } else {
+                    const u32x2 w = *(const u32x2 *)(vs + (t4 + j) * HD + S::DPL * lane);
+                    const uint32_t ws[2] = {w.x, w.y};
 #pragma unroll
-            for (int g = 0; g < G; g++) {
-                const float p = sp[0][g][tl];
+                    for (int e = 0; e < S::DPL; e++) vv[e] = h2f((ws[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+                }
 #pragma unroll
-                for (int e = 0; e < S::DPL; e++) acc[g][e] += p * vv[e];
+                for (int e = 0; e < S::DPL; e++) acc[j][e] += pw[j] * vv[e];
             }
         }
-#pragma unroll
-        for (int g = 0; g < G; g++)
-#pragma unroll
-            for (int e = 0; e < S::DPL; e++) ob[wave][g][S::DPL * lane + e] = acc[g][e];
-    }
-    __syncthreads();
-
-    // 6. partial (o, m, l) of this split
-    const int stride = HD + 2;
-    for (int idx = tid; idx < G * HD; idx += WG) {
-        const int g = idx / HD, i = idx % HD;
-        const float o = (ob[0][g][i] + ob[1][g][i]) + (ob[2][g][i] + ob[3][g][i]);
         float *pp = a.part + ((size_t)(kvh * G + g) * a.max_splits + split) * stride;
-        pp[i] = o;
-        if (i == 0) {
-            pp[HD] = mx[g];
-            pp[HD + 1] = sm[g];
+#pragma unroll
+        for (int e = 0; e < S::DPL; e++)
+            pp[S::DPL * lane + e] = (acc[0][e] + acc[1][e]) + (acc[2][e] + acc[3][e]);
+        if (lane == 0) {
+            pp[HD] = m;
+            pp[HD + 1] = l;
         }
     }
 }
