@@ -501,10 +501,10 @@ static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int 
 
 // Routing of one token inside the workgroup (MoE rows mode): the router
 // logits l[0..n) (n <= GW) -> softmax (max, exp(l - max), sum, divide: the
-// oracle's ref_softmax) -> each expert's rank (the number of experts with a
-// larger p, or an equal p and a lower id, i.e. the order of k rounds of
-// first-maximum selection) -> lane k < moe_k of every wave gets the id of rank
-// k and its weight (p, or p / the sum of the chosen in rank order).  Workgroup
+// oracle's ref_softmax) -> the k best experts in the order (p descending, id
+// ascending), i.e. the order of k rounds of first-maximum selection -> lane
+// k < moe_k of every wave gets the id of rank k and its weight (p, or p / the
+// sum of the chosen in rank order).  Workgroup
 // 0 also writes them out for the down projection and the caller.  The loads
 // were issued by the caller before the weights'.
 static __device__ __forceinline__ void moe_route(const GemvArgs &a, float lg, int &idv, float &wv, int wg) {
@@ -512,6 +512,9 @@ static __device__ __forceinline__ void moe_route(const GemvArgs &a, float lg, in
     __shared__ float rmax[GNW], rsum[GNW];
     __shared__ int sid[WAVE];
     __shared__ float sw[WAVE];
+    __shared__ float cv[GNW * WAVE];  // per wave: its k best (value, id), in order
+    __shared__ int ci[GNW * WAVE];
+    __shared__ int wcnt[GNW];         // candidates of each wave
     const int n = a.moe_n, t = threadIdx.x, lane = t & (WAVE - 1), wave = t / WAVE;
     float m = t < n ? lg : -INFINITY;
 #pragma unroll
@@ -533,24 +536,43 @@ static __device__ __forceinline__ void moe_route(const GemvArgs &a, float lg, in
 #pragma unroll
     for (int w = 0; w < GNW; w++) tot += rsum[w];
     const float pi = e / tot;
+    // top k in the order (p descending, id ascending) -- the order of k rounds
+    // of first-maximum selection -- in two levels, both comparisons only: an
+    // expert's rank within its wave's 64; the wave's k best become candidates
+    // (an expert among the k best overall has fewer than k better experts in
+    // its wave); a candidate's rank among the candidates is its rank overall
+    // (every expert better than one of the k best is itself a candidate).  A
+    // NaN p is never a candidate; a rank no expert fills keeps id 0, weight 0.
+    const int k = a.moe_k, nw = (n + WAVE - 1) / WAVE;
+    const bool valid = t < n && pi == pi;
     if (t < n) p[t] = pi;
-    if (t < a.moe_k) {  // defined ids even if NaN logits leave a rank unfilled
+    if (t < k) {
         sid[t] = 0;
         sw[t] = 0.f;
     }
+    const int nvalid = __popcll(__ballot(valid));
+    if (lane == 0) wcnt[wave] = min(nvalid, k);
     __syncthreads();
-    if (t < n) {
-        int rank = 0, j = 0;
+    if (valid) {
+        int rank = 0;
+        const int j0 = wave * WAVE, j1 = min(n, j0 + WAVE);
 #pragma unroll 4
-        for (; j + 4 <= n; j += 4) {
-            const float4 q = *(const float4 *)&p[j];
-            rank += (better(q.x, j, pi, t) ? 1 : 0) + (better(q.y, j + 1, pi, t) ? 1 : 0) +
-                    (better(q.z, j + 2, pi, t) ? 1 : 0) + (better(q.w, j + 3, pi, t) ? 1 : 0);
+        for (int j = j0; j < j1; j++) rank += better(p[j], j, pi, t) ? 1 : 0;
+        if (rank < k) {
+            cv[wave * WAVE + rank] = pi;
+            ci[wave * WAVE + rank] = t;
         }
-        for (; j < n; j++) rank += better(p[j], j, pi, t) ? 1 : 0;
-        if (rank < a.moe_k) {
-            sid[rank] = t;
-            sw[rank] = pi;
+    }
+    __syncthreads();
+    if (t < nw * WAVE && (t & (WAVE - 1)) < wcnt[t / WAVE]) {  // candidate slot t
+        const float cvv = cv[t];
+        const int cii = ci[t];
+        int rank = 0;
+        for (int w = 0; w < nw; w++)
+            for (int r = 0; r < wcnt[w]; r++) rank += better(cv[w * WAVE + r], ci[w * WAVE + r], cvv, cii) ? 1 : 0;
+        if (rank < k) {
+            sid[rank] = cii;
+            sw[rank] = cvv;
         }
     }
     __syncthreads();

@@ -59,6 +59,19 @@ class DeviceBuffer:
         if self._hip.hipMalloc(ctypes.byref(self.ptr), ctypes.c_size_t(self.nbytes)) != 0:
             raise RuntimeError("hipMalloc failed")
 
+    def from_host(self, a):
+        import ctypes
+        a = np.ascontiguousarray(a)
+        if a.nbytes > self.nbytes:
+            raise ValueError("host array larger than the buffer")
+        if self._hip.hipMemcpy(self.ptr, a.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(a.nbytes), 1) != 0:
+            raise RuntimeError("hipMemcpy failed")
+        return self
+
+    def sync(self):
+        if self._hip.hipDeviceSynchronize() != 0:
+            raise RuntimeError("hipDeviceSynchronize failed")
+
     def to_host(self, n=None):
         import ctypes
         out = np.empty(self.nbytes if n is None else n, np.uint8)

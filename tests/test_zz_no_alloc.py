@@ -10,19 +10,13 @@ import pytest
 
 import refcpu
 from oi import _native, ggml
+from helpers import DeviceBuffer
 from test_moe_oracle import make_moe
 
 pytestmark = pytest.mark.gpu
 
 
-def _torch():
-    import torch
-    assert torch.cuda.is_available()
-    return torch
-
-
 def _run(E, k, dim, inter, etype, rtype, seed, norm=1):
-    torch = _torch()
     rng = np.random.default_rng(seed)
     rb, gb, ub, db = make_moe(rng, E, dim, inter, etype, rtype=rtype)
     x = rng.standard_normal(dim).astype(np.float32)
@@ -30,20 +24,22 @@ def _run(E, k, dim, inter, etype, rtype, seed, norm=1):
          ggml.DeviceWeights(etype, ub, E * inter, dim), ggml.DeviceWeights(etype, db, E * dim, inter)]
     d = _native.MoeDims(E, k, dim, inter, norm)
     L = _native.hip()
-    xd = torch.from_numpy(x).cuda()
-    y_ws = torch.full((dim,), float("nan"), device="cuda")
-    y_na = torch.full((dim,), float("nan"), device="cuda")
-    ws = torch.empty(int(L.oi_moe_workspace_bytes(ctypes.byref(d))) // 4, dtype=torch.float32, device="cuda")
-    vp = ctypes.c_void_p
-    _native.check(L.oi_moe_ffn_launch(ctypes.byref(d), *[ww.h for ww in w], vp(xd.data_ptr()), vp(ws.data_ptr()),
-                                      vp(y_ws.data_ptr()), None))
-    _native.check(L.oi_moe_ffn_launch_noalloc(ctypes.byref(d), *[ww.h for ww in w], vp(xd.data_ptr()),
-                                              vp(y_na.data_ptr()), None))
-    torch.cuda.synchronize()
+    nan = np.full(dim, np.nan, np.float32)
+    xd, y_ws, y_na = DeviceBuffer(dim * 4).from_host(x), DeviceBuffer(dim * 4).from_host(nan), \
+        DeviceBuffer(dim * 4).from_host(nan)
+    ws = DeviceBuffer(int(L.oi_moe_workspace_bytes(ctypes.byref(d))))
+    try:
+        _native.check(L.oi_moe_ffn_launch(ctypes.byref(d), *[ww.h for ww in w], xd.ptr, ws.ptr, y_ws.ptr, None))
+        _native.check(L.oi_moe_ffn_launch_noalloc(ctypes.byref(d), *[ww.h for ww in w], xd.ptr, y_na.ptr, None))
+        xd.sync()
+        out_ws, out_na = y_ws.to_host().view(np.float32), y_na.to_host().view(np.float32)
+    finally:
+        for b in (xd, y_ws, y_na, ws):
+            b.free()
+        for ww in w:
+            ww.free()
     ry, _, _ = refcpu.moe_ffn(E, k, dim, inter, norm, rtype, rb, etype, gb, ub, db, x)
-    for ww in w:
-        ww.free()
-    return y_ws.cpu().numpy(), y_na.cpu().numpy(), ry
+    return out_ws, out_na, ry
 
 
 def test_noalloc_equals_workspace_entry_two_calls():
