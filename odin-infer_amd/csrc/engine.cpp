@@ -195,6 +195,26 @@ DMat make_dmat(uint32_t type, int64_t rows, int64_t cols, const uint8_t *dev, co
     return m;
 }
 
+// Rows [r0, r0 + n) of a device matrix as a matrix of its own (the planes
+// keep their stride; the per-row regions move by r0 rows).
+DMat dmat_rows(const DMat &m, int64_t r0, int64_t n) {
+    DMat v = m;
+    v.rows = (int32_t)n;
+    const size_t r = (size_t)r0, c = (size_t)m.cols;
+    switch (m.type) {
+    case T_Q4_K: v.q += r * (c / 64) * 16; v.s += r * (c / 256) * 16; break;
+    case T_Q6_K: v.q += r * (c / 64) * 16; v.s += r * (c / 256) * 16; v.d += r * (c / 256); break;
+    case T_Q8_0: v.q += r * (c / 64) * 16; v.d += r * (c / 32); break;
+    case T_F16: v.q += r * c * 2; break;
+    case T_Q4_0: v.q += r * (c / 32) * 18; break;
+    case T_Q4_1: v.q += r * (c / 32) * 20; break;
+    case T_Q5_0: v.q += r * (c / 32) * 22; break;
+    case T_Q5_1: v.q += r * (c / 32) * 24; break;
+    default: v.q += r * c * 4; break;
+    }
+    return v;
+}
+
 // Host staging of a repacked matrix, then one copy into device memory.
 int upload_matrix(uint32_t type, const uint8_t *src, int64_t rows, int64_t cols, uint8_t *dev, hipStream_t st,
                   std::vector<uint8_t> &stage, DMat &out) {
@@ -434,7 +454,18 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
                                       "multiple of key heads, conv kernel <= 8)");
 
     // tensors (infer/model.odin:141-179; qwen3_5/model.odin:306-364): shapes checked against the config
-    struct Want { std::string name; int64_t rows, cols; bool f32; const GgufTensor *t; };
+    // append: a tensor uploaded as more rows of this one (a shared expert as
+    // expert n_experts of the stacked matrices); merged_into: this tensor is
+    // those rows, a view from row view_r0 of that entry
+    struct Want {
+        std::string name;
+        int64_t rows, cols;
+        bool f32;
+        const GgufTensor *t;
+        const GgufTensor *append = nullptr;
+        int merged_into = -1;
+        int64_t view_r0 = 0;
+    };
     std::vector<Want> want;
     const int64_t D = c.dim, H = c.hidden_dim, QD = c.n_heads * c.head_dim, KVD = c.n_kv_heads * c.head_dim;
     const int64_t E = e->n_experts, EF = e->expert_ffn, SF = e->shared_ffn;
@@ -445,6 +476,7 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     if (!tied) want.push_back({"output.weight", c.vocab_size, D, false, nullptr});
     std::vector<int> kinds((size_t)c.n_layers);
     std::vector<char> shared((size_t)c.n_layers, 0);
+    std::vector<int> exp_at, shx_at;  // want index of each layer's routed / shared gate matrix
     for (int64_t l = 0; l < c.n_layers; l++) {
         const std::string p = "blk." + std::to_string(l) + ".";
         // qwen3_5/model.odin:289-300: full attention at layers interval-1, 2 interval-1, ...
@@ -476,11 +508,13 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
             want.push_back({p + "ffn_up.weight", H, D, false, nullptr});
         } else {
             want.push_back({p + "ffn_gate_inp.weight", E, D, false, nullptr});
+            exp_at.push_back((int)want.size());
             want.push_back({p + "ffn_gate_exps.weight", E * EF, D, false, nullptr});
             want.push_back({p + "ffn_up_exps.weight", E * EF, D, false, nullptr});
             want.push_back({p + "ffn_down_exps.weight", E * D, EF, false, nullptr});
             if (SF > 0 && g.tensor(p + "ffn_gate_inp_shexp.weight")) {
                 shared[(size_t)l] = 1;
+                shx_at.push_back((int)want.size() + 1);
                 want.push_back({p + "ffn_gate_inp_shexp.weight", 1, D, false, nullptr});
                 want.push_back({p + "ffn_gate_shexp.weight", SF, D, false, nullptr});
                 want.push_back({p + "ffn_up_shexp.weight", SF, D, false, nullptr});
@@ -498,6 +532,28 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     }
     e->weight_bytes = wbytes;
     e->n_experts = E;
+    // a shared expert with the routed experts' inner size and types becomes
+    // expert E of the stacked matrices, so the routed gate/up and down launches
+    // take it as one more chosen expert (weight sigmoid of its router row)
+    std::vector<char> merged((size_t)c.n_layers, 0);
+    {
+        size_t si = 0;
+        for (int64_t l = 0, ei = 0; l < c.n_layers && moe; l++, ei++) {
+            if (!shared[(size_t)l]) continue;
+            const int xg = exp_at[(size_t)ei], sg = shx_at[si++];
+            bool ok = SF == EF;
+            for (int m = 0; m < 3 && ok; m++) ok = want[(size_t)(xg + m)].t->kind == want[(size_t)(sg + m)].t->kind;
+            if (!ok) continue;
+            merged[(size_t)l] = 1;
+            for (int m = 0; m < 3; m++) {
+                Want &x = want[(size_t)(xg + m)], &sh = want[(size_t)(sg + m)];
+                sh.merged_into = xg + m;
+                sh.view_r0 = x.rows;  // E * EF (gate, up) or E * D (down)
+                x.append = sh.t;
+                x.rows += sh.rows;
+            }
+        }
+    }
     if ((rc = check_device(opts->device))) return rc;
 
     // device memory plan
@@ -520,7 +576,7 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     probe.seg[0].m.rows = (int32_t)out_rows;
     probe.seg[0].m.cols = (int32_t)D;
     plan_gemv(probe);
-    const size_t hb_n = std::max<size_t>({(size_t)H, (size_t)(e->top_k * EF), (size_t)SF, 1});
+    const size_t hb_n = std::max<size_t>({(size_t)H, (size_t)((e->top_k + 1) * EF), (size_t)SF, 1});
     const size_t part_n = std::max((size_t)c.n_heads * e->max_splits * (c.head_dim + 4),
                                    (size_t)c.n_heads * q35_splits * (c.head_dim + 2));
     size_t act = al(D * 4) + al(2 * QD * 4) + 2 * al(KVD * 4) + al(QD * 4) + al(hb_n * 4) + al(out_rows * 4) +
@@ -542,14 +598,27 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     std::vector<uint8_t> stage;
     std::vector<DMat> mats(want.size());
     std::vector<const float *> f32s(want.size(), nullptr);
+    std::vector<uint8_t> cat;
     for (size_t i = 0; i < want.size(); i++) {
         const GgufTensor *t = want[i].t;
-        uint8_t *dev = e->arena.take((size_t)t->nbytes);
+        if (want[i].merged_into >= 0) continue;  // uploaded with the tensor it extends
+        const size_t nb = (size_t)t->nbytes + (want[i].append ? (size_t)want[i].append->nbytes : 0);
+        uint8_t *dev = e->arena.take(nb);
         if (!dev) return fail(OI_E_NOMEM, "arena exhausted");
-        if ((rc = upload_matrix(t->kind, t->data, want[i].rows, want[i].cols, dev, e->stream, stage, mats[i])))
+        const uint8_t *src = t->data;
+        if (want[i].append) {  // the GGUF rows of both, one after the other
+            cat.resize(nb);
+            std::memcpy(cat.data(), t->data, (size_t)t->nbytes);
+            std::memcpy(cat.data() + t->nbytes, want[i].append->data, (size_t)want[i].append->nbytes);
+            src = cat.data();
+        }
+        if ((rc = upload_matrix(t->kind, src, want[i].rows, want[i].cols, dev, e->stream, stage, mats[i])))
             return rc;
         f32s[i] = (const float *)dev;
     }
+    for (size_t i = 0; i < want.size(); i++)
+        if (want[i].merged_into >= 0) mats[i] = dmat_rows(mats[(size_t)want[i].merged_into], want[i].view_r0, want[i].rows);
+    std::vector<uint8_t>().swap(cat);
     size_t wi = 0;
     e->tok_embd = mats[wi++];
     e->output_norm = f32s[wi++];
@@ -560,6 +629,7 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
         L.kind = kinds[l];
         L.moe = moe;
         L.shared = shared[l] != 0;
+        L.shared_merged = merged[l] != 0;
         L.attn_norm = f32s[wi++];
         L.ffn_norm = f32s[wi++];
         if (L.kind != LK_LINEAR) {
@@ -795,6 +865,9 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
         r.seg[0].m = L.router; r.seg[0].y = mo_logits;
         if (L.shared) { r.seg[1].m = L.sh_inp; r.seg[1].y = mo_sg; }
         ops.push_back(gemv_op(K_ROUTER, r));
+        // a merged shared expert is expert E: one more part of the routed launches
+        const int sx = L.shared_merged ? 1 : 0;
+        const int64_t KP = e->top_k + sx;  // parts: the chosen experts (+ the shared one)
         Op gu;
         gu.kind = OP_MOE_ROWS;
         gu.role = K_GATEUP;
@@ -802,24 +875,29 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
         ga = gemv_args(GEMV_SWIGLU, (int)D, e->x, L.ffn_norm, eps);
         ga.nseg = 2;
         ga.seg[0].m = L.gexp; ga.seg[1].m = L.uexp;
-        ga.seg[0].m.rows = ga.seg[1].m.rows = (int32_t)(e->top_k * EF);  // the chosen experts' rows
+        ga.seg[0].m.rows = ga.seg[1].m.rows = (int32_t)(KP * EF);  // the chosen experts' rows
         ga.seg[0].y = ga.seg[1].y = e->hb;
         ga.moe_logits = mo_logits;
         ga.moe_ids_out = mo_ids;
         ga.moe_w_out = mo_w;
         ga.moe_norm = 1;  // Qwen3-MoE / Qwen3-Next renormalize the chosen weights
-        ga.moe_k = (int32_t)e->top_k;
+        ga.moe_k = (int32_t)KP;
         ga.moe_n = (int32_t)E;
         ga.moe_blk = (int32_t)EF;
+        if (sx) {
+            ga.moe_sel = (int32_t)e->top_k;
+            ga.moe_nblk = (int32_t)E + 1;
+            ga.moe_sgate = mo_sg;
+        }
         if (!gemv_q_moe_supported(ga, MOE_ROWS))
             return fail(OI_E_UNSUPPORTED, "routed experts: type or shape not supported by the expert GEMV "
                                           "(Q4_K / Q6_K / Q8_0, dim <= 4096, inner a multiple of 256)");
         plan_gemv_q(ga);
-        gu.bytes = 2.0 * e->top_k * mbytes(L.gexp) / E + mbytes(L.router) * 0 + 4.0 * D + 4.0 * E + 4.0 * e->top_k * EF;
+        gu.bytes = 2.0 * KP * mbytes(L.gexp) / (E + sx) + 4.0 * D + 4.0 * E + 4.0 * KP * EF;
         ops.push_back(gu);
         // the shared expert's gate/up reads the same normalized x, so it runs
         // before either down projection adds into x
-        if (L.shared) {
+        if (L.shared && !sx) {
             GemvArgs su = gemv_args(GEMV_SWIGLU, (int)D, e->x, L.ffn_norm, eps);
             su.nseg = 2;
             su.seg[0].m = L.sh_gate; su.seg[0].y = sh_h;
@@ -830,22 +908,23 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
         dn.kind = OP_MOE_COLS;
         dn.role = K_DOWN;
         GemvArgs &gd = dn.g;
-        gd = gemv_args(GEMV_ADD, (int)(e->top_k * EF), e->hb, nullptr, eps);
+        gd = gemv_args(GEMV_ADD, (int)(KP * EF), e->hb, nullptr, eps);
         gd.nseg = 1;
         gd.seg[0].m = L.dexp;
         gd.seg[0].m.rows = (int32_t)D;  // row r of every expert
         gd.seg[0].y = e->x;
         gd.moe_ids = mo_ids;
         gd.moe_w = mo_w;
-        gd.moe_k = (int32_t)e->top_k;
+        gd.moe_k = (int32_t)KP;
         gd.moe_n = (int32_t)E;
         gd.moe_blk = (int32_t)(EF / 64);
+        if (sx) gd.moe_nblk = (int32_t)E + 1;
         if (!gemv_q_moe_supported(gd, MOE_COLS))
             return fail(OI_E_UNSUPPORTED, "routed experts: down projection not supported by the expert GEMV");
         plan_gemv_q(gd);
-        dn.bytes = e->top_k * mbytes(L.dexp) / E + 4.0 * e->top_k * EF + 8.0 * D;
+        dn.bytes = KP * mbytes(L.dexp) / (E + sx) + 4.0 * KP * EF + 8.0 * D;
         ops.push_back(dn);
-        if (L.shared) {
+        if (L.shared && !sx) {
             GemvArgs sd = gemv_args(GEMV_ADD, (int)SF, sh_h, nullptr, eps);
             sd.nseg = 1;
             sd.seg[0].m = L.sh_down; sd.seg[0].y = e->x;

@@ -30,6 +30,7 @@ enum { LK_QWEN3 = 0, LK_FULL = 1, LK_LINEAR = 2 };
 struct LayerDev {
     int kind = LK_QWEN3;
     bool moe = false, shared = false;  // routed-expert FFN (with a shared expert)
+    bool shared_merged = false;        // the shared expert stored as expert n_experts of the stacks
     DMat wq{}, wk{}, wv{}, wo{}, w1{}, w2{}, w3{};
     const float *attn_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
     uint16_t *kc = nullptr, *vc = nullptr;

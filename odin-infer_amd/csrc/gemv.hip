@@ -339,7 +339,9 @@ static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int 
     const DMat &m0 = a.seg[seg].m;
     const DMat &m1 = a.seg[NM == 2 ? 1 : seg].m;
     const int lpr = a.lpr, grp = lane / lpr, j = lane & (lpr - 1);
-    const int U = K >> 6, upl = XU1 ? 1 : U / lpr;
+    // (MOE_COLS: lanes per row need not divide the units; a lane's units past
+    // the row are read at the row's last unit and weighted 0)
+    const int U = K >> 6, upl = XU1 ? 1 : (MOE == MOE_COLS ? (U + lpr - 1) / lpr : U / lpr);
     const int rows_m = m0.rows, rpt = a.rows_per_wg;
     const int ntl = te - tb;
     const int rsub = grp * R;
@@ -351,7 +353,7 @@ static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int 
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const int row = live ? min((tb + t) * rpt + rsub + r, rows_m - 1) : 0;
-            int prow = row, pu = live ? u : j;  // the stored row and unit
+            int prow = row, pu = live ? (MOE == MOE_COLS ? min(u, U - 1) : u) : j;  // the stored row and unit
             if (MOE == MOE_ROWS) {  // virtual row -> row of the chosen expert
                 const int k = row / a.moe_blk;
                 prow = __shfl(idv, k, WAVE) * a.moe_blk + (row - k * a.moe_blk);
@@ -400,11 +402,13 @@ static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int 
         }
     };
     auto compute = [&](int t, int ui, const W (&w)[NM][R]) {
-        const int u = XU1 ? j : j + ui * lpr;
+        const int u0 = XU1 ? j : j + ui * lpr;
+        const int u = MOE == MOE_COLS ? min(u0, U - 1) : u0;
         if (!XU1) xload(xq, u, xu);
         // (MOE_COLS: the unit's expert weight; units keep their position in the
         // super-block, as each expert's part is a whole number of super-blocks)
-        const float uw = MOE == MOE_COLS ? __shfl(wv, u / a.moe_blk, WAVE) : 1.f;
+        const float uw0 = MOE == MOE_COLS ? __shfl(wv, u / a.moe_blk, WAVE) : 1.f;
+        const float uw = MOE == MOE_COLS && u0 >= U ? 0.f : uw0;
 #pragma unroll
         for (int r = 0; r < R; r++) {
             if (MOE == MOE_COLS) acc[0][r] += uw * wdot(w[0][r], u, xu);
@@ -507,7 +511,7 @@ static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int 
 // sum of the chosen in rank order).  Workgroup
 // 0 also writes them out for the down projection and the caller.  The loads
 // were issued by the caller before the weights'.
-static __device__ __forceinline__ void moe_route(const GemvArgs &a, float lg, int &idv, float &wv, int wg) {
+static __device__ __forceinline__ void moe_route(const GemvArgs &a, float lg, float sg, int &idv, float &wv, int wg) {
     __shared__ __attribute__((aligned(16))) float p[GW];
     __shared__ float rmax[GNW], rsum[GNW];
     __shared__ int sid[WAVE];
@@ -543,10 +547,10 @@ static __device__ __forceinline__ void moe_route(const GemvArgs &a, float lg, in
     // its wave); a candidate's rank among the candidates is its rank overall
     // (every expert better than one of the k best is itself a candidate).  A
     // NaN p is never a candidate; a rank no expert fills keeps id 0, weight 0.
-    const int k = a.moe_k, nw = (n + WAVE - 1) / WAVE;
+    const int k = a.moe_sel > 0 ? a.moe_sel : a.moe_k, nw = (n + WAVE - 1) / WAVE;
     const bool valid = t < n && pi == pi;
     if (t < n) p[t] = pi;
-    if (t < k) {
+    if (t < a.moe_k) {
         sid[t] = 0;
         sw[t] = 0.f;
     }
@@ -577,10 +581,16 @@ static __device__ __forceinline__ void moe_route(const GemvArgs &a, float lg, in
     }
     __syncthreads();
     float s = 0.f;
-    for (int k = 0; k < a.moe_k; k++) s += sw[k];  // in rank order, as the sequential selection
+    for (int r = 0; r < k; r++) s += sw[r];  // in rank order, as the sequential selection
+    const int nblk = a.moe_nblk > 0 ? a.moe_nblk : n;
     if (lane < a.moe_k) {
-        idv = min(max(sid[lane], 0), n - 1);
-        wv = a.moe_norm ? sw[lane] / s : sw[lane];
+        if (lane < k) {
+            idv = min(max(sid[lane], 0), nblk - 1);
+            wv = a.moe_norm ? sw[lane] / s : sw[lane];
+        } else {  // the shared expert, gated by sigmoid of its router row
+            idv = n;
+            wv = 1.0f / (1.0f + expf(-sg));
+        }
         if (wg == 0 && wave == 0) {
             a.moe_ids_out[lane] = idv;
             a.moe_w_out[lane] = wv;
@@ -622,21 +632,23 @@ __global__ __launch_bounds__(GW) void gemv_q_kernel(GemvArgs a) {
         // routed experts: lane l < moe_k holds expert l's id (and weight)
         int idv = 0;
         float wv = 0.f;
-        float lg = 0.f;
+        float lg = 0.f, sg = 0.f;
         const bool route = MOE == MOE_ROWS && a.moe_logits != nullptr;
         if (MOE) {
             const int l = threadIdx.x & (WAVE - 1);
             if (route) {
                 if ((int)threadIdx.x < a.moe_n) lg = a.moe_logits[threadIdx.x];
+                if (a.moe_sgate) sg = a.moe_sgate[0];
             } else if (l < a.moe_k) {
-                idv = min(max(a.moe_ids[l], 0), a.moe_n - 1);  // ids come from the device
+                // ids come from the device
+                idv = min(max(a.moe_ids[l], 0), (a.moe_nblk > 0 ? a.moe_nblk : a.moe_n) - 1);
                 if (MOE == MOE_COLS) wv = a.moe_w[l];
             }
         }
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): x has arrived before any weight request goes out
         __builtin_amdgcn_sched_barrier(0);
-        if (route) moe_route(a, lg, idv, wv, wg);
+        if (route) moe_route(a, lg, sg, idv, wv, wg);
         gemv_run<T, R, NM, XR, XU1, NORM, MOE>(a, seg, tb, te, wg, xp, idv, wv);
     }
 }
@@ -743,6 +755,9 @@ void plan_gemv_q(GemvArgs &a) {
     const int U = a.K / 64;
     int lpr = 1;
     while (lpr < 64 && U % (lpr * 2) == 0) lpr *= 2;
+    // routed-expert columns mode masks the units past the row, so a long row
+    // takes a whole wave (one row per tile) whatever its unit count
+    if (a.moe_ids && !a.moe_logits && a.mode != GEMV_SWIGLU && U >= 64) lpr = 64;
     a.lpr = lpr;
     const bool sw = a.mode == GEMV_SWIGLU;
     const int gpw = 64 / lpr, G = device_cus();
@@ -823,7 +838,9 @@ bool gemv_q_moe_supported(const GemvArgs &a, int moe) {
     if ((a.norm_w && moe != MOE_ROWS) || a.moe_k < 1 || a.moe_k > WAVE || a.moe_n < 1 || a.moe_blk < 1) return false;
     if (moe == MOE_ROWS) {
         if (a.mode != GEMV_SWIGLU || a.seg[0].m.rows != a.moe_k * a.moe_blk) return false;
-        if (a.moe_logits ? (a.moe_n > GW || a.moe_k > a.moe_n || !a.moe_ids_out || !a.moe_w_out) : !a.moe_ids)
+        const int sel = a.moe_sel > 0 ? a.moe_sel : a.moe_k;
+        if (a.moe_sel > 0 && (a.moe_sel + 1 != a.moe_k || !a.moe_sgate || a.moe_nblk != a.moe_n + 1)) return false;
+        if (a.moe_logits ? (a.moe_n > GW || sel > a.moe_n || !a.moe_ids_out || !a.moe_w_out) : !a.moe_ids)
             return false;
     } else if (moe == MOE_COLS) {
         if ((a.mode != GEMV_STORE && a.mode != GEMV_ADD) || a.nseg != 1 || !a.moe_ids || !a.moe_w || a.moe_blk % 4 ||

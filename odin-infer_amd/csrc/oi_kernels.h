@@ -93,6 +93,12 @@ struct GemvArgs {
     int32_t *moe_ids_out;
     float *moe_w_out;
     int32_t moe_norm;
+    // a shared expert stored as expert moe_n of the stacked matrices (moe_nblk =
+    // moe_n + 1 blocks): routing picks moe_sel (< moe_k) experts and adds
+    // expert moe_n as part moe_sel with weight sigmoid(moe_sgate[0]); 0 / null:
+    // no shared expert (moe_sel = moe_k, moe_nblk = moe_n)
+    int32_t moe_sel, moe_nblk;
+    const float *moe_sgate;
     // GEMV_ADD: if set, the product is scaled by sigmoid(ygate[0]) before the add
     // (the shared expert's gate of a Qwen3-Next-style MoE layer)
     const float *ygate;
