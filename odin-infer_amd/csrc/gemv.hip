@@ -776,8 +776,9 @@ void plan_gemv_q(GemvArgs &a) {
         bytes[i] = (double)a.seg[i].m.rows * a.K * weight_bytes(a.seg[i].m.type);
         total += bytes[i];
     }
-    // at least one workgroup per segment, at most one tile per wave short of a full workgroup
-    const int nwg = (int)std::max<long>(nseg, std::min<long>(G, (total_tiles + GNW - 1) / GNW));
+    // at least one workgroup per segment; small matrices spread over more CUs
+    // (4 tiles per workgroup) rather than filling every wave of a few
+    const int nwg = (int)std::max<long>(nseg, std::min<long>(G, (total_tiles + 3) / 4));
     int wg = 0, left = nwg;
     for (int i = 0; i < nseg; i++) {
         a.seg[i].wg_begin = wg;
