@@ -503,6 +503,13 @@ static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int 
     }
 }
 
+// lane j's 64-bit value, broadcast to the wave (j uniform)
+static __device__ __forceinline__ unsigned long long readlane64(unsigned long long v, int j) {
+    const unsigned lo = __builtin_amdgcn_readlane((int)(unsigned)v, j);
+    const unsigned hi = __builtin_amdgcn_readlane((int)(unsigned)(v >> 32), j);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
 // Routing of one token inside the workgroup (MoE rows mode): the router
 // logits l[0..n) (n <= GW) -> softmax (max, exp(l - max), sum, divide: the
 // oracle's ref_softmax) -> the k best experts in the order (p descending, id
@@ -512,14 +519,17 @@ static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int 
 // 0 also writes them out for the down projection and the caller.  The loads
 // were issued by the caller before the weights'.
 static __device__ __forceinline__ void moe_route(const GemvArgs &a, float lg, float sg, int &idv, float &wv, int wg) {
-    __shared__ __attribute__((aligned(16))) float p[GW];
     __shared__ float rmax[GNW], rsum[GNW];
     __shared__ int sid[WAVE];
     __shared__ float sw[WAVE];
-    __shared__ float cv[GNW * WAVE];  // per wave: its k best (value, id), in order
-    __shared__ int ci[GNW * WAVE];
-    __shared__ int wcnt[GNW];         // candidates of each wave
+    __shared__ unsigned long long cand[GW];  // wave w's k best keys at [w * k, w * k + k)
     const int n = a.moe_n, t = threadIdx.x, lane = t & (WAVE - 1), wave = t / WAVE;
+    const int k = a.moe_sel > 0 ? a.moe_sel : a.moe_k, nw = (n + WAVE - 1) / WAVE;
+    if (t < a.moe_k) {
+        sid[t] = 0;
+        sw[t] = 0.f;
+    }
+    if (wave < nw && lane < k) cand[wave * k + lane] = 0ull;
     float m = t < n ? lg : -INFINITY;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, WAVE));
@@ -541,42 +551,35 @@ static __device__ __forceinline__ void moe_route(const GemvArgs &a, float lg, fl
     for (int w = 0; w < GNW; w++) tot += rsum[w];
     const float pi = e / tot;
     // top k in the order (p descending, id ascending) -- the order of k rounds
-    // of first-maximum selection -- in two levels, both comparisons only: an
-    // expert's rank within its wave's 64; the wave's k best become candidates
-    // (an expert among the k best overall has fewer than k better experts in
-    // its wave); a candidate's rank among the candidates is its rank overall
+    // of first-maximum selection.  p >= +0, so its bits order as unsigned
+    // integers: the key (bits of p, ~id) orders experts by that rule as one
+    // 64-bit comparison; a NaN p (and a lane past n) gets key 0, below every
+    // expert.  Two levels: an expert's rank within its wave's 64 (keys
+    // broadcast from registers); the wave's k best become candidates (an
+    // expert among the k best overall has fewer than k better experts in its
+    // wave); a candidate's rank among the candidates is its rank overall
     // (every expert better than one of the k best is itself a candidate).  A
-    // NaN p is never a candidate; a rank no expert fills keeps id 0, weight 0.
-    const int k = a.moe_sel > 0 ? a.moe_sel : a.moe_k, nw = (n + WAVE - 1) / WAVE;
+    // rank no expert fills keeps id 0, weight 0.
     const bool valid = t < n && pi == pi;
-    if (t < n) p[t] = pi;
-    if (t < a.moe_k) {
-        sid[t] = 0;
-        sw[t] = 0.f;
-    }
-    const int nvalid = __popcll(__ballot(valid));
-    if (lane == 0) wcnt[wave] = min(nvalid, k);
-    __syncthreads();
-    if (valid) {
+    const unsigned long long key = valid ? ((unsigned long long)__float_as_uint(pi) << 32) | (unsigned)~t : 0ull;
+    if (wave < nw) {
         int rank = 0;
-        const int j0 = wave * WAVE, j1 = min(n, j0 + WAVE);
-#pragma unroll 4
-        for (int j = j0; j < j1; j++) rank += better(p[j], j, pi, t) ? 1 : 0;
-        if (rank < k) {
-            cv[wave * WAVE + rank] = pi;
-            ci[wave * WAVE + rank] = t;
-        }
+#pragma unroll
+        for (int j = 0; j < WAVE; j++) rank += readlane64(key, j) > key ? 1 : 0;
+        if (valid && rank < k) cand[wave * k + rank] = key;
     }
     __syncthreads();
-    if (t < nw * WAVE && (t & (WAVE - 1)) < wcnt[t / WAVE]) {  // candidate slot t
-        const float cvv = cv[t];
-        const int cii = ci[t];
-        int rank = 0;
-        for (int w = 0; w < nw; w++)
-            for (int r = 0; r < wcnt[w]; r++) rank += better(cv[w * WAVE + r], ci[w * WAVE + r], cvv, cii) ? 1 : 0;
-        if (rank < k) {
-            sid[rank] = cii;
-            sw[rank] = cvv;
+    const int nc = nw * k;
+    if (t < nc) {
+        const unsigned long long mk = cand[t];
+        if (mk != 0ull) {
+            int rank = 0;
+#pragma unroll 8
+            for (int c = 0; c < nc; c++) rank += cand[c] > mk ? 1 : 0;
+            if (rank < k) {
+                sid[rank] = (int)~(unsigned)mk;
+                sw[rank] = __uint_as_float((unsigned)(mk >> 32));
+            }
         }
     }
     __syncthreads();
