@@ -503,36 +503,75 @@ static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int 
     }
 }
 
-// lane j's 64-bit value, broadcast to the wave (j uniform)
-static __device__ __forceinline__ unsigned long long readlane64(unsigned long long v, int j) {
-    const unsigned lo = __builtin_amdgcn_readlane((int)(unsigned)v, j);
-    const unsigned hi = __builtin_amdgcn_readlane((int)(unsigned)(v >> 32), j);
-    return ((unsigned long long)hi << 32) | lo;
+// lane j's value, broadcast to the wave (j uniform)
+static __device__ __forceinline__ float readlanef(float v, int j) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
+}
+
+// number of set bits of m below this lane
+static __device__ __forceinline__ int lane_prefix(unsigned long long m) {
+    return (int)__builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u));
+}
+
+// Wave max and sum without LDS: DPP within rows of 16 lanes, then the four
+// rows' results read out of lanes 0, 16, 32, 48 (sum: ((r0 + r1) + r2) + r3,
+// the same on every lane).
+static __device__ __forceinline__ float wave_max_dpp(float v) {
+    v = dpp_max8(v);
+    v = fmaxf(v, OI_DPP(v, 0x140));
+    return fmaxf(fmaxf(readlanef(v, 0), readlanef(v, 16)), fmaxf(readlanef(v, 32), readlanef(v, 48)));
+}
+static __device__ __forceinline__ float wave_sum_dpp(float v) {
+    v = lane_group_sum(v, 16);
+    return ((readlanef(v, 0) + readlanef(v, 16)) + readlanef(v, 32)) + readlanef(v, 48);
+}
+
+// Expert keys for routing: bit 41 set for a defined probability p (>= +0,
+// so its bits order as unsigned integers), p's bits at 40..10, 1023 - id at
+// 9..0: one unsigned comparison orders experts by (p descending, id
+// ascending); an undefined expert (NaN p, or past n) has key 0.
+constexpr unsigned long long ROUTE_KEY_VALID = 1ull << 41;
+static_assert(GW <= 1024, "expert ids must fit the key's 10 low bits");
+
+// The k-th largest of the wave's keys v[0..NV) (the caller has checked that
+// more than k are nonzero; nonzero keys are distinct), one bit at a time from
+// the top: the largest T with at least k keys >= T, ending early once exactly
+// k keys are >= T.  Counts are ballots, so every lane of the wave takes part.
+template <int NV>
+static __device__ __forceinline__ unsigned long long wave_kth_key(const unsigned long long (&v)[NV], int k) {
+    unsigned long long T = 0ull;
+#pragma unroll
+    for (int b = 41; b >= 0; b--) {
+        const unsigned long long tr = T | (1ull << b);
+        int cnt = 0;
+#pragma unroll
+        for (int i = 0; i < NV; i++) cnt += __popcll(__ballot(v[i] >= tr));
+        if (cnt >= k) {
+            T = tr;
+            if (cnt == k) break;
+        }
+    }
+    return T;
 }
 
 // Routing of one token inside the workgroup (MoE rows mode): the router
 // logits l[0..n) (n <= GW) -> softmax (max, exp(l - max), sum, divide: the
 // oracle's ref_softmax) -> the k best experts in the order (p descending, id
 // ascending), i.e. the order of k rounds of first-maximum selection -> lane
-// k < moe_k of every wave gets the id of rank k and its weight (p, or p / the
+// r < moe_k of every wave gets the id of rank r and its weight (p, or p / the
 // sum of the chosen in rank order).  Workgroup
 // 0 also writes them out for the down projection and the caller.  The loads
 // were issued by the caller before the weights'.
 static __device__ __forceinline__ void moe_route(const GemvArgs &a, float lg, float sg, int &idv, float &wv, int wg) {
     __shared__ float rmax[GNW], rsum[GNW];
-    __shared__ int sid[WAVE];
-    __shared__ float sw[WAVE];
-    __shared__ unsigned long long cand[GW];  // wave w's k best keys at [w * k, w * k + k)
+    __shared__ unsigned long long cand[GW];     // wave w's best keys at [w * k, w * k + k), then zeros
+    __shared__ unsigned long long stage[WAVE];  // keys moved between the lanes of wave 0
+    __shared__ unsigned long long ordered[WAVE];  // the chosen keys by rank
+    __shared__ int rid[WAVE];                   // the chosen ids and weights, rank order
+    __shared__ float rw[WAVE];
     const int n = a.moe_n, t = threadIdx.x, lane = t & (WAVE - 1), wave = t / WAVE;
     const int k = a.moe_sel > 0 ? a.moe_sel : a.moe_k, nw = (n + WAVE - 1) / WAVE;
-    if (t < a.moe_k) {
-        sid[t] = 0;
-        sw[t] = 0.f;
-    }
-    if (wave < nw && lane < k) cand[wave * k + lane] = 0ull;
-    float m = t < n ? lg : -INFINITY;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, WAVE));
+    const float m = wave_max_dpp(t < n ? lg : -INFINITY);
     if (lane == 0) rmax[wave] = m;
     __syncthreads();
     float M = rmax[0];
@@ -543,61 +582,94 @@ static __device__ __forceinline__ void moe_route(const GemvArgs &a, float lg, fl
 #pragma clang fp contract(off)
         e = expf(lg - M);
     }
-    const float es = wave_sum(e);
+    const float es = wave_sum_dpp(e);
     if (lane == 0) rsum[wave] = es;
     __syncthreads();
     float tot = 0.f;
 #pragma unroll
     for (int w = 0; w < GNW; w++) tot += rsum[w];
     const float pi = e / tot;
-    // top k in the order (p descending, id ascending) -- the order of k rounds
-    // of first-maximum selection.  p >= +0, so its bits order as unsigned
-    // integers: the key (bits of p, ~id) orders experts by that rule as one
-    // 64-bit comparison; a NaN p (and a lane past n) gets key 0, below every
-    // expert.  Two levels: an expert's rank within its wave's 64 (keys
-    // broadcast from registers); the wave's k best become candidates (an
+    // Two levels: each wave's k best of its 64 experts become candidates (an
     // expert among the k best overall has fewer than k better experts in its
-    // wave); a candidate's rank among the candidates is its rank overall
-    // (every expert better than one of the k best is itself a candidate).  A
-    // rank no expert fills keeps id 0, weight 0.
+    // wave); then wave 0 takes the k best candidates (every expert better
+    // than one of the k best overall is itself a candidate) and orders them.
+    // The bit searches run on the CU's one scalar unit, so the second level
+    // is not repeated in every wave.  A rank no expert fills keeps id 0,
+    // weight 0.
     const bool valid = t < n && pi == pi;
-    const unsigned long long key = valid ? ((unsigned long long)__float_as_uint(pi) << 32) | (unsigned)~t : 0ull;
+    const unsigned long long key =
+        valid ? ROUTE_KEY_VALID | ((unsigned long long)__float_as_uint(pi) << 10) | (unsigned)(1023 - t) : 0ull;
     if (wave < nw) {
-        int rank = 0;
-#pragma unroll
-        for (int j = 0; j < WAVE; j++) rank += readlane64(key, j) > key ? 1 : 0;
-        if (valid && rank < k) cand[wave * k + rank] = key;
+        const unsigned long long v[1] = {key};
+        const unsigned long long T = __popcll(__ballot(valid)) > k ? wave_kth_key(v, k) : 0ull;
+        const bool c = valid && key >= T;
+        const unsigned long long cm = __ballot(c);
+        if (c) cand[wave * k + lane_prefix(cm)] = key;
+        if (lane >= __popcll(cm) && lane < k) cand[wave * k + lane] = 0ull;
     }
     __syncthreads();
-    const int nc = nw * k;
-    if (t < nc) {
-        const unsigned long long mk = cand[t];
-        if (mk != 0ull) {
-            int rank = 0;
-#pragma unroll 8
-            for (int c = 0; c < nc; c++) rank += cand[c] > mk ? 1 : 0;
-            if (rank < k) {
-                sid[rank] = (int)~(unsigned)mk;
-                sw[rank] = __uint_as_float((unsigned)(mk >> 32));
+    if (wave == 0) {
+        // the candidates, 64 at a time: lanes < k of A keep the best so far
+        const int nc = nw * k;
+        unsigned long long A = lane < nc ? cand[lane] : 0ull;
+        for (int c0 = WAVE; c0 < nc; c0 += WAVE) {
+            const unsigned long long v[2] = {A, c0 + lane < nc ? cand[c0 + lane] : 0ull};
+            const int nv = __popcll(__ballot(v[0] != 0ull)) + __popcll(__ballot(v[1] != 0ull));
+            const unsigned long long T = nv > k ? wave_kth_key(v, k) : 0ull;
+            const bool w0 = v[0] != 0ull && v[0] >= T, w1 = v[1] != 0ull && v[1] >= T;
+            const unsigned long long b0 = __ballot(w0), b1 = __ballot(w1);
+            if (w0) stage[lane_prefix(b0)] = v[0];
+            if (w1) stage[__popcll(b0) + lane_prefix(b1)] = v[1];
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
+            __builtin_amdgcn_wave_barrier();
+            A = lane < __popcll(b0) + __popcll(b1) ? stage[lane] : 0ull;
+            __builtin_amdgcn_wave_barrier();
+        }
+        // the k best, ordered: lane r gets the key of rank r (0 past the last);
+        // the chosen keys are read back from LDS by every lane (broadcast
+        // reads, all in flight together)
+        const unsigned long long v[1] = {A};
+        const unsigned long long T = __popcll(__ballot(A != 0ull)) > k ? wave_kth_key(v, k) : 0ull;
+        const bool win = A != 0ull && A >= T;
+        const unsigned long long bw = __ballot(win);
+        const int nch = __popcll(bw);
+        if (win) stage[lane_prefix(bw)] = A;
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();
+        const unsigned long long mine = lane < nch ? stage[lane] : 0ull;
+        int rank = 0;
+        for (int j = 0; j < nch; j++) rank += stage[j] > mine ? 1 : 0;
+        if (lane < nch) ordered[rank] = mine;
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();
+        const unsigned long long R = lane < nch ? ordered[lane] : 0ull;
+        const float wr = R != 0ull ? __uint_as_float((unsigned)(R >> 10) & 0x7FFFFFFFu) : 0.f;
+        const int id = R != 0ull ? 1023 - (int)(R & 1023u) : 0;
+        float s = 0.f;  // in rank order, as the sequential selection; ranks past nch weigh 0
+        for (int r = 0; r < nch; r++) s += __uint_as_float((unsigned)(ordered[r] >> 10) & 0x7FFFFFFFu);
+        const int nblk = a.moe_nblk > 0 ? a.moe_nblk : n;
+        if (lane < a.moe_k) {
+            int fi;
+            float fw;
+            if (lane < k) {
+                fi = min(max(id, 0), nblk - 1);
+                fw = a.moe_norm ? wr / s : wr;
+            } else {  // the shared expert, gated by sigmoid of its router row
+                fi = n;
+                fw = 1.0f / (1.0f + expf(-sg));
+            }
+            rid[lane] = fi;
+            rw[lane] = fw;
+            if (wg == 0) {
+                a.moe_ids_out[lane] = fi;
+                a.moe_w_out[lane] = fw;
             }
         }
     }
     __syncthreads();
-    float s = 0.f;
-    for (int r = 0; r < k; r++) s += sw[r];  // in rank order, as the sequential selection
-    const int nblk = a.moe_nblk > 0 ? a.moe_nblk : n;
     if (lane < a.moe_k) {
-        if (lane < k) {
-            idv = min(max(sid[lane], 0), nblk - 1);
-            wv = a.moe_norm ? sw[lane] / s : sw[lane];
-        } else {  // the shared expert, gated by sigmoid of its router row
-            idv = n;
-            wv = 1.0f / (1.0f + expf(-sg));
-        }
-        if (wg == 0 && wave == 0) {
-            a.moe_ids_out[lane] = idv;
-            a.moe_w_out[lane] = wv;
-        }
+        idv = rid[lane];
+        wv = rw[lane];
     }
 }
 
