@@ -640,13 +640,24 @@ def model_decode(name, context, steps, warmup=8, prompt=0, cpu=True, cpu_budget=
         try:
             if prompt:
                 toks = np.random.default_rng(5).integers(0, cfg.vocab_size, size=prompt).astype(np.int32)
-                t0 = time.perf_counter()
-                logits = infer.engine_forward_batch(e, toks, 0)
-                pel = time.perf_counter() - t0
+                infer.engine_forward_batch(e, toks[:64], 0)  # allocates the prefill buffers
+                pf = {"tokens": prompt}
+                for chunk in (64, 512):
+                    best = None
+                    for _ in range(3):
+                        infer.engine_reset_state(e)
+                        t0 = time.perf_counter()
+                        for i in range(0, prompt, chunk):
+                            logits = infer.engine_forward_batch(e, toks[i:i + chunk], i)
+                        pel = time.perf_counter() - t0
+                        best = pel if best is None else min(best, pel)
+                    pf["chunk%d" % chunk] = {"ms": round(1000 * best, 1), "tok_s": round(prompt / best, 1)}
+                    log("%s prefill, %d-token chunks: %d tokens in %.1f ms (%.0f tok/s)" % (
+                        name, chunk, prompt, 1000 * best, prompt / best))
                 first = int(np.argmax(logits))
-                out["prefill"] = {"tokens": prompt, "ms": round(1000 * pel, 1), "tok_s": round(prompt / pel, 1),
-                                  "path": "per-token decode steps (the hybrid has no batched path here yet)"}
-                log("%s prefill: %d tokens in %.1f ms" % (name, prompt, 1000 * pel))
+                pf["note"] = ("batched prefill (oi_engine_prefill) from a reset state, one call per chunk, host "
+                              "wall clock, best of 3; decode continues from the 512-token-chunk run")
+                out["prefill"] = pf
                 snap = None
             else:
                 k, v = synth.kv_prefill(777, cfg.n_layers, cfg.n_kv_heads, context, cfg.head_dim)

@@ -37,7 +37,7 @@ def build(verbose=False):
     os.makedirs(BUILD, exist_ok=True)
     jobs = []
     objs = []
-    for src in ["kernels.hip", "gemv.hip", "attn.hip", "gemm.hip", "prefill.hip", "deltanet.hip", "qwen35_attn.hip", "noalloc.hip", "sample.hip"]:
+    for src in ["kernels.hip", "gemv.hip", "attn.hip", "gemm.hip", "prefill.hip", "deltanet.hip", "qwen35_attn.hip", "noalloc.hip", "sample.hip", "prefill_hybrid.hip"]:
         obj = os.path.join(BUILD, src + ".o")
         objs.append(obj)
         jobs.append([HIPCC, "--offload-arch=" + ARCH, *COMMON, *DEVICE_FLAGS, "-x", "hip", "-c",

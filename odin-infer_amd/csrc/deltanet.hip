@@ -25,24 +25,6 @@
 
 namespace oi {
 
-// ops.odin:7-15: the branch keeps exp's argument <= 0
-static __device__ __forceinline__ float sigmoid_ref(float x) {
-#pragma clang fp contract(off)
-    if (x >= 0.0f) {
-        const float z = expf(-x);
-        return 1.0f / (1.0f + z);
-    }
-    const float z = expf(x);
-    return z / (1.0f + z);
-}
-static __device__ __forceinline__ float silu_ref(float x) { return x * sigmoid_ref(x); }
-// ops.odin:21-25 (the logarithm in double precision, as the reference)
-static __device__ __forceinline__ float softplus_ref(float x) {
-    if (x > 20.0f) return x;
-    if (x < -20.0f) return 0.0f;
-    return (float)log((double)(1.0f + expf(x)));
-}
-
 __global__ __launch_bounds__(WG) void dn_conv_kernel(DnArgs a) {
 #pragma clang fp contract(off)
     const int c = (int)blockIdx.x * WG + threadIdx.x;

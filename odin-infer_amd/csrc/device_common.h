@@ -67,6 +67,33 @@ static __device__ __forceinline__ float lane_group_sum(float v, int n) {
 }
 static __device__ __forceinline__ float wave_sum(float v) { return lane_group_sum(v, WAVE); }
 
+// Qwen3.5 activations (qwen3_5/ops.odin:7-15 sigmoid: the branch keeps exp's
+// argument <= 0; silu = x sigmoid(x))
+static __device__ __forceinline__ float sigmoid_ref(float x) {
+#pragma clang fp contract(off)
+    if (x >= 0.0f) {
+        const float z = expf(-x);
+        return 1.0f / (1.0f + z);
+    }
+    const float z = expf(x);
+    return z / (1.0f + z);
+}
+static __device__ __forceinline__ float silu_ref(float x) { return x * sigmoid_ref(x); }
+// ops.odin:21-25 (the logarithm in double precision, as the reference)
+static __device__ __forceinline__ float softplus_ref(float x) {
+    if (x > 20.0f) return x;
+    if (x < -20.0f) return 0.0f;
+    return (float)log((double)(1.0f + expf(x)));
+}
+
+// sum of the K-slice partial products of element i (a split projection's
+// slices, each `slice` floats, summed in slice order)
+static __device__ __forceinline__ float parts_at(const float *p, int split, size_t slice, size_t i) {
+    float s = p[i];
+    for (int z = 1; z < split; z++) s += p[(size_t)z * slice + i];
+    return s;
+}
+
 // (value, index) order of a greedy argmax that keeps the first maximum
 // (sampler/sampler.odin:79-89 scans with a strict '>')
 static __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {

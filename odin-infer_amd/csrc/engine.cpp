@@ -696,6 +696,7 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     if (e->arch == 2) {
         qbuf = (float *)e->arena.take(QD * 4);
         inv_freq = (float *)e->arena.take((size_t)(e->rotary_dim / 2 + 1) * 4);
+        e->inv_freq = inv_freq;
         lin_qkv = (float *)e->arena.take((size_t)CD * 4);
         lin_conv = (float *)e->arena.take((size_t)CD * 4);
         lin_z = (float *)e->arena.take((size_t)VD * 4);
@@ -1004,14 +1005,33 @@ constexpr int PF_MAX_T = 512;
 namespace {
 
 bool prefill_batched_ok(const oi_engine *e) {
-    // the batched path covers the dense decoder; the routed-expert and hybrid
-    // layouts run their prompts token by token (the reference's fallback,
-    // qwen3_5/engine.odin:86-91)
-    if (e->arch != 0) return false;
-    if ((e->cfg.head_dim != 128 && e->cfg.head_dim != 256) || e->cfg.dim > 16384) return false;
-    for (const LayerDev &L : e->layers)
-        for (const DMat *m : {&L.wq, &L.wk, &L.wv, &L.wo, &L.w1, &L.w2, &L.w3})
+    // every layout of the reference's batched path (the dense decoder and the
+    // Qwen3.5 hybrid, forward_gpu_batch) and the routed-expert FFN; a layout
+    // a kernel here does not take runs its prompt token by token (the
+    // reference's fallback, qwen3_5/engine.odin:86-91)
+    const oi_config &c = e->cfg;
+    if ((c.head_dim != 128 && c.head_dim != 256) || c.dim > 16384) return false;
+    for (const LayerDev &L : e->layers) {
+        std::vector<const DMat *> g;
+        if (L.kind == LK_LINEAR) {
+            if (!pf_dn_supported((int)e->lin_hk, (int)e->lin_hv, (int)e->lin_kernel) || e->lin_nv % e->lin_nk) return false;
+            g = {&L.in_qkv, &L.in_z, &L.in_b, &L.in_a, &L.ssm_out};
+        } else {
+            if (L.kind == LK_FULL && (e->rotary_dim > c.head_dim || e->rotary_dim % 2)) return false;
+            g = {&L.wq, &L.wk, &L.wv, &L.wo};
+        }
+        if (!L.moe) {
+            g.push_back(&L.w1); g.push_back(&L.w2); g.push_back(&L.w3);
+        } else {
+            const int32_t D = (int32_t)c.dim, EF = (int32_t)e->expert_ffn;
+            if ((L.shared && !L.shared_merged) || e->n_experts + 1 > 1024 || e->top_k > MOE_MAX_K) return false;
+            if (!mt_gemv_supported(L.router, D) || !mt_gemv_supported(L.gexp, D) || !mt_gemv_supported(L.uexp, D) ||
+                !mt_gemv_supported(L.dexp, EF) || (L.shared && !mt_gemv_supported(L.sh_inp, D)))
+                return false;
+        }
+        for (const DMat *m : g)
             if (!gemm_supported(*m)) return false;
+    }
     return true;
 }
 
@@ -1020,49 +1040,164 @@ size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
 int prefill_alloc(oi_engine *e) {
     if (e->pf_mem) return OI_OK;
     const oi_config &c = e->cfg;
-    const size_t D = (size_t)c.dim, QD = (size_t)c.n_heads * c.head_dim, H = (size_t)c.hidden_dim;
-    // partial products: buffer 0 takes q, wo, gate and down, buffer 1 k and
-    // up, buffer 2 v; each sized for the largest K split of any chunk length
-    size_t need[3] = {0, 0, 0};
+    const size_t T = PF_MAX_T, D = (size_t)c.dim, QD = (size_t)c.n_heads * c.head_dim, H = (size_t)c.hidden_dim;
+    const size_t KD = (size_t)(e->lin_nk * e->lin_hk), VD = (size_t)(e->lin_nv * e->lin_hv), CD = 2 * KD + VD;
+    bool full = false, lin = false, moe = false;
+    // partial products: buffer 0 takes q, wo, gate, down, in_qkv and ssm_out,
+    // buffer 1 k, up and in_z, buffer 2 v and in_b, buffer 3 in_a; each sized
+    // for the largest K split of any chunk length
+    size_t need[4] = {0, 0, 0, 0};
     for (const LayerDev &L : e->layers) {
-        const std::pair<const DMat *, int> uses[] = {{&L.wq, 0}, {&L.wo, 0}, {&L.w1, 0}, {&L.w2, 0},
-                                                     {&L.wk, 1}, {&L.w3, 1}, {&L.wv, 2}};
+        full |= L.kind == LK_FULL;
+        lin |= L.kind == LK_LINEAR;
+        moe |= L.moe;
+        std::vector<std::pair<const DMat *, int>> uses;
+        if (L.kind == LK_LINEAR) uses = {{&L.in_qkv, 0}, {&L.ssm_out, 0}, {&L.in_z, 1}, {&L.in_b, 2}, {&L.in_a, 3}};
+        else uses = {{&L.wq, 0}, {&L.wo, 0}, {&L.wk, 1}, {&L.wv, 2}};
+        if (!L.moe) {
+            uses.push_back({&L.w1, 0}); uses.push_back({&L.w2, 0}); uses.push_back({&L.w3, 1});
+        }
         for (const auto &u : uses)
-            for (int T = 8; T <= PF_MAX_T; T += 8)
+            for (int n = 8; n <= PF_MAX_T; n += 8)
                 need[u.second] = std::max(need[u.second],
-                                          (size_t)gemm_split(*u.first, T, SIZE_MAX) * T * u.first->rows * 4);
+                                          (size_t)gemm_split(*u.first, n, SIZE_MAX) * n * u.first->rows * 4);
     }
-    const size_t xb = (size_t)PF_MAX_T * std::max({D, QD, H}) * 2;
-    size_t total = al256(PF_MAX_T * 4) + al256(PF_MAX_T * D * 4) + al256(PF_MAX_T * QD * 4) + al256(xb);
-    for (size_t b : need) total += al256(b);
+    need[0] = std::max(need[0], T * D * 4);  // the routed experts' weighted sums
+    const size_t xb = T * std::max({D, QD, H, VD}) * 2;
+    const size_t NE = (size_t)(e->n_experts + 1), KP = (size_t)(e->top_k + 1), EF = (size_t)e->expert_ffn;
+    const int tg = moe ? (int)((EF + mt_gemv_tile_rows((int32_t)D, (int32_t)EF) - 1) / mt_gemv_tile_rows((int32_t)D, (int32_t)EF)) : 0;
+    const int td = moe ? (int)((D + mt_gemv_tile_rows((int32_t)EF, (int32_t)D) - 1) / mt_gemv_tile_rows((int32_t)EF, (int32_t)D)) : 0;
+    const size_t items_per_tile = NE + (T * KP + MT_PAIR_SLICE - 1) / MT_PAIR_SLICE;  // pair slices
+    std::vector<size_t> sizes = {T * 4, T * D * 4, T * QD * 4 * 2, xb, need[0], need[1], need[2], need[3],
+                                 full ? T * QD * 4 : 0,
+                                 lin ? T * CD * 4 : 0, lin ? T * 2 * KD * 4 : 0, lin ? T * 2 * (size_t)e->lin_nv * 4 : 0,
+                                 lin ? T * VD * 4 : 0,
+                                 moe ? T * D * 4 : 0, moe ? T * (size_t)e->n_experts * 4 : 0, moe ? T * 4 : 0,
+                                 moe ? T * KP * 4 : 0, moe ? T * KP * EF * 4 : 0, moe ? T * KP * D * 4 : 0,
+                                 moe ? T * KP * 4 : 0, moe ? T * KP * 4 : 0, moe ? NE * 4 : 0, moe ? NE * 4 : 0,
+                                 moe ? NE * 4 : 0, moe ? 8 * tg * items_per_tile : 0,
+                                 moe ? 8 * td * items_per_tile : 0, moe ? (size_t)8 : 0};
+    size_t total = 0;
+    for (size_t b : sizes) total += al256(b);
     HIP_TRY(hipMalloc(&e->pf_mem, total));
     uint8_t *p = (uint8_t *)e->pf_mem;
-    auto take = [&](size_t b) {
-        uint8_t *r = p;
-        p += al256(b);
+    size_t k = 0;
+    auto take = [&]() {
+        uint8_t *r = sizes[k] ? p : nullptr;
+        p += al256(sizes[k++]);
         return r;
     };
-    e->pf_tok = (int32_t *)take(PF_MAX_T * 4);
-    e->pf_x = (float *)take(PF_MAX_T * D * 4);
-    e->pf_q = (float *)take(PF_MAX_T * QD * 4);
-    e->pf_xb = (uint16_t *)take(xb);
-    for (int i = 0; i < 3; i++) {
-        e->pf_p[i] = (float *)take(need[i]);
-        e->pf_pbytes[i] = need[i];
+    e->pf_tok = (int32_t *)take();
+    e->pf_x = (float *)take();
+    e->pf_q = (float *)take();
+    e->pf_xb = (uint16_t *)take();
+    for (int i = 0; i < 4; i++) {
+        e->pf_pbytes[i] = sizes[k];
+        e->pf_p[i] = (float *)take();
     }
+    e->pf_gate = (float *)take();
+    e->pf_conv = (float *)take();
+    e->pf_qk = (float *)take();
+    e->pf_gates = (float *)take();
+    e->pf_o = (float *)take();
+    e->pf_xn = (float *)take();
+    e->pf_lg = (float *)take();
+    e->pf_sg = (float *)take();
+    e->pf_w = (float *)take();
+    e->pf_h = (float *)take();
+    e->pf_yd = (float *)take();
+    e->pf_ids = (int32_t *)take();
+    e->pf_list = (int32_t *)take();
+    e->pf_off = (int32_t *)take();
+    e->pf_cnt = (int32_t *)take();
+    e->pf_fill = (int32_t *)take();
+    e->pf_items_gu = (int32_t *)take();
+    e->pf_items_dn = (int32_t *)take();
+    e->pf_nitems = (int32_t *)take();
+    return OI_OK;
+}
+
+// The routed-expert FFN of the chunk (no counterpart in the reference: its
+// batched path has a dense MLP), in f32 as the per-token path: router logits
+// (and the shared expert's gate logit) by a multi-token GEMV of the f32 norm
+// output, softmax + top-k per token, the pairs grouped by expert, the chosen
+// experts' SwiGLU rows and down rows per pair, their weighted sum per token
+// into partial-product buffer 0.
+int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
+    const hipStream_t st = e->stream;
+    const int32_t D = (int32_t)e->cfg.dim, E = (int32_t)e->n_experts, EF = (int32_t)e->expert_ffn;
+    const int sx = L.shared_merged ? 1 : 0, KP = (int)e->top_k + sx, NE = E + sx;
+    const int slices = (T + MT_PAIR_SLICE - 1) / MT_PAIR_SLICE, pairs = T * KP;
+    MtGemvArgs r{};
+    r.m = L.router;
+    r.K = D;
+    r.rows = E;
+    r.xdiv = 1;
+    r.tile_rows = mt_gemv_tile_rows(D, E);
+    r.tiles = (E + r.tile_rows - 1) / r.tile_rows;
+    r.dense_n = T;
+    r.pair_slice = MT_PAIR_SLICE;
+    r.x = e->pf_xn;
+    r.y = e->pf_lg;
+    HIP_TRY(launch_mt_gemv(r, r.tiles * slices, st));
+    if (L.shared) {
+        r.m = L.sh_inp;
+        r.rows = 1;
+        r.tile_rows = 1;
+        r.tiles = 1;
+        r.y = e->pf_sg;
+        HIP_TRY(launch_mt_gemv(r, slices, st));
+    }
+    const int tr_gu = mt_gemv_tile_rows(D, EF), tr_dn = mt_gemv_tile_rows(EF, D);
+    PfMoeArgs ma{};
+    ma.logits = e->pf_lg;
+    ma.sgl = L.shared ? e->pf_sg : nullptr;
+    ma.ids = e->pf_ids;
+    ma.w = e->pf_w;
+    ma.list = e->pf_list; ma.off = e->pf_off; ma.cnt = e->pf_cnt; ma.fill = e->pf_fill;
+    ma.items_gu = e->pf_items_gu; ma.items_dn = e->pf_items_dn; ma.nitems = e->pf_nitems;
+    ma.yd = e->pf_yd;
+    ma.out = e->pf_p[0];
+    ma.T = T; ma.n_experts = E; ma.top_k = (int32_t)e->top_k; ma.kp = KP;
+    ma.norm_topk = 1;  // Qwen3-MoE / Qwen3-Next renormalize the chosen weights
+    ma.tiles_gu = (EF + tr_gu - 1) / tr_gu;
+    ma.tiles_dn = (D + tr_dn - 1) / tr_dn;
+    ma.dim = D;
+    ma.pair_slice = MT_PAIR_SLICE;
+    HIP_TRY(launch_pf_moe_route(ma, st));
+    const int item_tiles = NE + (pairs + MT_PAIR_SLICE - 1) / MT_PAIR_SLICE;  // bound on the pair slices
+    MtGemvArgs g{};
+    g.m = L.gexp; g.m2 = L.uexp;
+    g.swiglu = 1;
+    g.K = D; g.rows = EF; g.xdiv = KP; g.tile_rows = tr_gu;
+    g.x = e->pf_xn; g.y = e->pf_h;
+    g.list = e->pf_list; g.off = e->pf_off; g.cnt = e->pf_cnt;
+    g.items = e->pf_items_gu; g.nitems = e->pf_nitems;
+    g.pair_slice = MT_PAIR_SLICE;
+    HIP_TRY(launch_mt_gemv(g, item_tiles * ma.tiles_gu, st));
+    MtGemvArgs d{};
+    d.m = L.dexp;
+    d.K = EF; d.rows = D; d.xdiv = 1; d.tile_rows = tr_dn;
+    d.x = e->pf_h; d.y = e->pf_yd;
+    d.list = e->pf_list; d.off = e->pf_off; d.cnt = e->pf_cnt;
+    d.items = e->pf_items_dn; d.nitems = e->pf_nitems + 1;
+    d.pair_slice = MT_PAIR_SLICE;
+    HIP_TRY(launch_mt_gemv(d, item_tiles * ma.tiles_dn, st));
+    HIP_TRY(launch_pf_moe_combine(ma, st));
     return OI_OK;
 }
 
 // One batched chunk of T tokens at positions pos .. pos+T-1 (forward_gpu_batch,
-// qwen3_5/metal.odin:1472-1654, for the dense decoder of infer/forward.odin):
-// per layer the three attention projections, q/k norm + RoPE + cache store,
-// causal attention, wo + residual, then the MLP projections, SwiGLU, down +
-// residual, all over the T tokens; at the end the final norm and classifier
-// of the last token.
+// qwen3_5/metal.odin:1472-1654): per layer the attention sublayer (Qwen3
+// attention; Qwen3.5 full attention with the [q | gate] projection, partial
+// RoPE and the sigmoid output gate; or the Qwen3.5 DeltaNet: conv, delta
+// rule over the chunk's tokens in order, gated RMSNorm), then the FFN (dense
+// SwiGLU, or routed experts), all over the T tokens; at the end the final
+// norm and classifier of the last token.
 int prefill_chunk(oi_engine *e, const int32_t *tokens, int T, int pos) {
     const hipStream_t st = e->stream;
     const oi_config &c = e->cfg;
-    const int D = (int)c.dim, QD = (int)(c.n_heads * c.head_dim), H = (int)c.hidden_dim, hd = (int)c.head_dim;
+    const int D = (int)c.dim, H = (int)c.hidden_dim, hd = (int)c.head_dim;
     const float eps = c.rms_eps;
     HIP_TRY(hipMemcpyAsync(e->pf_tok, tokens, (size_t)T * 4, hipMemcpyHostToDevice, st));
     HIP_TRY(launch_embed_rows(e->tok_embd, e->pf_tok, T, e->pf_x, st));
@@ -1072,18 +1207,54 @@ int prefill_chunk(oi_engine *e, const int32_t *tokens, int T, int pos) {
     HIP_TRY(launch_pf_addnorm16(e->pf_x, nullptr, 1, e->layers[0].attn_norm, eps, D, T, e->pf_xb, st));
     for (size_t l = 0; l < e->layers.size(); l++) {
         const LayerDev &L = e->layers[l];
-        int qs = 1, ks = 1, vs = 1, s0 = 1, s1 = 1;
-        HIP_TRY(launch_gemm_parts(L.wq, e->pf_xb, T, P[0], PB[0], &qs, st));
-        HIP_TRY(launch_gemm_parts(L.wk, e->pf_xb, T, P[1], PB[1], &ks, st));
-        HIP_TRY(launch_gemm_parts(L.wv, e->pf_xb, T, P[2], PB[2], &vs, st));
-        PfQkvArgs qa{P[0], P[1], P[2], qs, ks, vs, L.q_norm, L.k_norm, eps, e->rope_cs, L.kc, L.vc, e->pf_q,
-                     T, pos, (int32_t)c.seq_len, (int32_t)c.n_heads, (int32_t)c.n_kv_heads};
-        HIP_TRY(launch_pf_qkv(qa, hd, st));
-        HIP_TRY(launch_pf_attn(e->pf_q, L.kc, L.vc, e->pf_xb, T, pos, (int)c.seq_len, (int)c.n_heads,
-                               (int)c.n_kv_heads, hd, st));
-        HIP_TRY(launch_gemm_parts(L.wo, e->pf_xb, T, P[0], PB[0], &s0, st));
-        HIP_TRY(launch_pf_addnorm16(e->pf_x, P[0], s0, L.ffn_norm, eps, D, T, e->pf_xb, st));
-        if (e->pf_fused && gemm_swiglu_supported(L.w1, L.w3, T)) {
+        int qs = 1, ks = 1, vs = 1, s0 = 1, s1 = 1, s2 = 1, s3 = 1;
+        if (L.kind == LK_QWEN3) {
+            HIP_TRY(launch_gemm_parts(L.wq, e->pf_xb, T, P[0], PB[0], &qs, st));
+            HIP_TRY(launch_gemm_parts(L.wk, e->pf_xb, T, P[1], PB[1], &ks, st));
+            HIP_TRY(launch_gemm_parts(L.wv, e->pf_xb, T, P[2], PB[2], &vs, st));
+            PfQkvArgs qa{P[0], P[1], P[2], qs, ks, vs, L.q_norm, L.k_norm, eps, e->rope_cs, L.kc, L.vc, e->pf_q,
+                         T, pos, (int32_t)c.seq_len, (int32_t)c.n_heads, (int32_t)c.n_kv_heads};
+            HIP_TRY(launch_pf_qkv(qa, hd, st));
+            HIP_TRY(launch_pf_attn(e->pf_q, L.kc, L.vc, e->pf_xb, T, pos, (int)c.seq_len, (int)c.n_heads,
+                                   (int)c.n_kv_heads, hd, st));
+            HIP_TRY(launch_gemm_parts(L.wo, e->pf_xb, T, P[0], PB[0], &s0, st));
+        } else if (L.kind == LK_FULL) {
+            HIP_TRY(launch_gemm_parts(L.wq, e->pf_xb, T, P[0], PB[0], &qs, st));
+            HIP_TRY(launch_gemm_parts(L.wk, e->pf_xb, T, P[1], PB[1], &ks, st));
+            HIP_TRY(launch_gemm_parts(L.wv, e->pf_xb, T, P[2], PB[2], &vs, st));
+            PfQ35Args qa{P[0], P[1], P[2], qs, ks, vs, L.q_norm, L.k_norm, e->inv_freq, eps, (int32_t)e->rotary_dim,
+                         L.kc, L.vc, e->pf_q, e->pf_gate, T, pos, (int32_t)c.seq_len, (int32_t)c.n_heads,
+                         (int32_t)c.n_kv_heads};
+            HIP_TRY(launch_pf_q35_qkv(qa, hd, st));
+            HIP_TRY(launch_pf_attn(e->pf_q, L.kc, L.vc, e->pf_xb, T, pos, (int)c.seq_len, (int)c.n_heads,
+                                   (int)c.n_kv_heads, hd, st, e->pf_gate));
+            HIP_TRY(launch_gemm_parts(L.wo, e->pf_xb, T, P[0], PB[0], &s0, st));
+        } else {
+            HIP_TRY(launch_gemm_parts(L.in_qkv, e->pf_xb, T, P[0], PB[0], &s0, st));
+            HIP_TRY(launch_gemm_parts(L.in_z, e->pf_xb, T, P[1], PB[1], &s1, st));
+            HIP_TRY(launch_gemm_parts(L.in_b, e->pf_xb, T, P[2], PB[2], &s2, st));
+            HIP_TRY(launch_gemm_parts(L.in_a, e->pf_xb, T, P[3], PB[3], &s3, st));
+            PfDnArgs da{};
+            da.qkv = P[0]; da.z = P[1]; da.b = P[2]; da.a = P[3];
+            da.qkvs = s0; da.zs = s1; da.bs = s2; da.as = s3;
+            da.conv_w = L.conv_w; da.a_decay = L.ssm_a; da.dt_bias = L.dt_bias; da.norm_w = L.ssm_norm;
+            da.eps = eps;
+            da.conv_state = L.conv_state;
+            da.state = L.rec_state;
+            da.conv_out = e->pf_conv; da.qk = e->pf_qk; da.gates = e->pf_gates; da.o = e->pf_o;
+            da.out16 = e->pf_xb;  // the in_* projections have read it
+            da.T = T;
+            da.n_kh = (int32_t)e->lin_nk; da.n_vh = (int32_t)e->lin_nv;
+            da.hk = (int32_t)e->lin_hk; da.hv = (int32_t)e->lin_hv; da.kernel = (int32_t)e->lin_kernel;
+            HIP_TRY(launch_pf_deltanet(da, st));
+            HIP_TRY(launch_gemm_parts(L.ssm_out, e->pf_xb, T, P[0], PB[0], &s0, st));
+        }
+        HIP_TRY(launch_pf_addnorm16(e->pf_x, P[0], s0, L.ffn_norm, eps, D, T, e->pf_xb, st,
+                                    L.moe ? e->pf_xn : nullptr));
+        if (L.moe) {
+            if (prefill_moe(e, L, T)) return -1;
+            s0 = 1;
+        } else if (e->pf_fused && gemm_swiglu_supported(L.w1, L.w3, T)) {
             // gate and up in one pass, SwiGLU in its epilogue; h goes to the up
             // partials' buffer (unsplit, it holds T x H floats)
             uint16_t *hb = (uint16_t *)P[1];
@@ -1106,7 +1277,6 @@ int prefill_chunk(oi_engine *e, const int32_t *tokens, int T, int pos) {
     a.seg[0].y = e->logits;
     if (!plan_gemv(a)) return fail(OI_E_DEVICE, "internal: classifier plan");
     HIP_TRY(launch_gemv(a, st));
-    (void)QD;
     return OI_OK;
 }
 

@@ -89,14 +89,24 @@ struct oi_engine {
     hipGraphExec_t gexec_s = nullptr;
     int last_pos = 0;
     size_t weight_bytes = 0;
+    float *inv_freq = nullptr;  // Qwen3.5 partial RoPE frequencies [rotary_dim / 2]
     // batched prefill buffers (allocated on the first prefill): token ids,
     // residual [T][dim], rotated q [T][q_dim], f16 projection inputs
-    // [T][max(dim, q_dim, hidden)], and three buffers of partial products
+    // [T][max(dim, q_dim, hidden, value_dim)], four buffers of partial
+    // products; the Qwen3.5 attention gate [T][q_dim]; the DeltaNet scratch
+    // (conv outputs, normalized q / k, gates, outputs); the routed-expert
+    // scratch (normalized x in f32, router logits, chosen ids / weights, pair
+    // lists, work items, SwiGLU rows and down rows per pair)
     void *pf_mem = nullptr;
     int32_t *pf_tok = nullptr;
-    float *pf_x = nullptr, *pf_q = nullptr, *pf_p[3] = {nullptr, nullptr, nullptr};
-    size_t pf_pbytes[3] = {0, 0, 0};
+    float *pf_x = nullptr, *pf_q = nullptr, *pf_p[4] = {nullptr, nullptr, nullptr, nullptr};
+    size_t pf_pbytes[4] = {0, 0, 0, 0};
     uint16_t *pf_xb = nullptr;
+    float *pf_gate = nullptr;
+    float *pf_conv = nullptr, *pf_qk = nullptr, *pf_gates = nullptr, *pf_o = nullptr;
+    float *pf_xn = nullptr, *pf_lg = nullptr, *pf_sg = nullptr, *pf_w = nullptr, *pf_h = nullptr, *pf_yd = nullptr;
+    int32_t *pf_ids = nullptr, *pf_list = nullptr, *pf_off = nullptr, *pf_cnt = nullptr, *pf_fill = nullptr;
+    int32_t *pf_items_gu = nullptr, *pf_items_dn = nullptr, *pf_nitems = nullptr;
     bool pf_fused = true;  // gate/up GEMM with the SwiGLU epilogue where it applies (OI_PREFILL_UNFUSED=1: off)
 };
 

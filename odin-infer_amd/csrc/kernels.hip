@@ -15,6 +15,8 @@
 //
 // Wave64 throughout; workgroups of 256 threads (4 waves).
 
+#include <algorithm>
+
 #include "device_common.h"
 
 namespace oi {
@@ -649,6 +651,307 @@ hipError_t launch_moe(const MoeArgs &a, const GemvArgs &router, const GemvArgs *
         hipLaunchKernelGGL(moe_down_kernel, dim3((unsigned)((a.dim + 3) / 4)), dim3(WG),
                            (size_t)a.top_k * a.inter * 4, st, a);
     }
+    return hipGetLastError();
+}
+
+// --------------------------------------------- routed experts, prefill --
+// The routed-expert FFN of a prefill chunk in f32, the arithmetic of the
+// per-token path (router, softmax, top-k, renormalized weights, the chosen
+// experts' SwiGLU and down projections; the reference has no MoE, so nothing
+// here is staged in f16).  Pairs p = t kp + s (token t, its s-th chosen
+// expert) are grouped by expert, and a multi-token GEMV reads the rows of
+// each chosen expert once for all of its pairs.
+
+constexpr int MT_CMAX = 8;  // pairs per pass of the multi-token GEMV
+
+// the 64 decoded weights w of unit u dotted with x (LDS, XView's swizzle):
+// they are four runs of 16 consecutive row elements (unit_elem)
+__device__ __forceinline__ float dot_unit_x(const float *w, int type, int u, const float4 *x4) {
+    float a = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int c0 = unit_elem(type, u, 16 * k) >> 2;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 x = x4[xswz(c0 + i)];
+            const float *wk = w + 16 * k + 4 * i;
+            a += wk[0] * x.x + wk[1] * x.y + wk[2] * x.z + wk[3] * x.w;
+        }
+    }
+    return a;
+}
+
+// Work item (expert e, pair slice, row tile): rows [tile * tile_rows,
+// +tile_rows) of expert e against pairs [slice * pair_slice, +pair_slice) of
+// e's list, cmax pairs per pass with their x rows in LDS.  Lane groups of lpr lanes (the smallest power of two >= the row's
+// units, at most 64) take one row each and split its units; each unit is
+// decoded once (decode_unit, exact) for all the pass's pairs.
+// y[p][r] = row r . x  or, for a SwiGLU pair of matrices,
+// silu(gate_r . x) * (up_r . x) (forward.odin:128-133).
+__global__ __launch_bounds__(WG) void mt_gemv_kernel(MtGemvArgs a, int cmax) {
+#pragma clang fp contract(off)
+    extern __shared__ float4 smem[];
+    const int it = blockIdx.x;
+    int e = 0, tile, slice, n, base;
+    if (a.dense_n > 0) {
+        tile = it % a.tiles;
+        slice = it / a.tiles;
+        n = a.dense_n;
+        base = 0;
+    } else {
+        if (it >= *a.nitems) return;
+        e = a.items[2 * it];
+        tile = a.items[2 * it + 1] & 0xFFFF;
+        slice = a.items[2 * it + 1] >> 16;
+        n = a.cnt[e];
+        base = a.off[e];
+    }
+    base += slice * a.pair_slice;
+    n = min(a.pair_slice, n - slice * a.pair_slice);
+    const int r0 = tile * a.tile_rows, r1 = min(a.rows, r0 + a.tile_rows);
+    if (r0 >= r1) return;
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    const int U = a.K >> 6, K4 = a.K >> 2;
+    int lpr = 1;
+    while (lpr < U && lpr < WAVE) lpr <<= 1;
+    const int gpw = WAVE / lpr, grp = lane / lpr, gl = lane % lpr;
+    const DMat g = sub_rows(a.m, e * a.rows, a.rows);
+    const DMat up = a.swiglu ? sub_rows(a.m2, e * a.rows, a.rows) : g;
+    for (int c0 = 0; c0 < n; c0 += cmax) {
+        const int nc = min(cmax, n - c0);
+        __syncthreads();  // the previous pass's x reads are done
+        for (int idx = threadIdx.x; idx < nc * K4; idx += WG) {
+            const int j = idx / K4, c = idx % K4;
+            const int p = a.dense_n > 0 ? base + c0 + j : a.list[base + c0 + j];
+            smem[j * K4 + xswz(c)] = ((const float4 *)(a.x + (size_t)(p / a.xdiv) * a.K))[c];
+        }
+        __syncthreads();
+        for (int r = r0 + wave * gpw + grp; r < r1; r += (WG / WAVE) * gpw) {
+            float ag[MT_CMAX], au[MT_CMAX];
+#pragma unroll
+            for (int j = 0; j < MT_CMAX; j++) ag[j] = au[j] = 0.f;
+            for (int u = gl; u < U; u += lpr) {
+                float w[64];
+                decode_unit(g, r, u, w);
+#pragma unroll
+                for (int j = 0; j < MT_CMAX; j++)
+                    if (j < nc) ag[j] += dot_unit_x(w, g.type, u, smem + j * K4);
+                if (a.swiglu) {
+                    decode_unit(up, r, u, w);
+#pragma unroll
+                    for (int j = 0; j < MT_CMAX; j++)
+                        if (j < nc) au[j] += dot_unit_x(w, up.type, u, smem + j * K4);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < MT_CMAX; j++) {
+                if (j < nc) {
+                    ag[j] = lane_group_sum(ag[j], lpr);
+                    if (a.swiglu) au[j] = lane_group_sum(au[j], lpr);
+                }
+            }
+            if (gl == 0) {
+#pragma unroll
+                for (int j = 0; j < MT_CMAX; j++) {
+                    if (j < nc) {
+                        const int p = a.dense_n > 0 ? base + c0 + j : a.list[base + c0 + j];
+                        float v = ag[j];
+                        if (a.swiglu) {
+                            v *= 1.0f / (1.0f + expf(-v));
+                            v *= au[j];
+                        }
+                        a.y[(size_t)p * a.rows + r] = v;
+                    }
+                }
+            }
+        }
+    }
+}
+
+static int mt_lpr(int32_t K) {
+    int lpr = 1;
+    while (lpr < K / 64 && lpr < WAVE) lpr <<= 1;
+    return lpr;
+}
+bool mt_gemv_supported(const DMat &m, int32_t K) {
+    return K > 0 && K % 64 == 0 && K <= 16384 && m.cols == K &&
+           (m.type == T_Q4_K || m.type == T_Q6_K || m.type == T_Q8_0 || m.type == T_F32 || m.type == T_F16 ||
+            m.type == T_Q4_0 || m.type == T_Q4_1 || m.type == T_Q5_0 || m.type == T_Q5_1);
+}
+// eight passes of the workgroup's lane groups
+int mt_gemv_tile_rows(int32_t K, int32_t rows) { return std::min<int32_t>(rows, 8 * (WG / WAVE) * (WAVE / mt_lpr(K))); }
+
+hipError_t launch_mt_gemv(const MtGemvArgs &a, int max_items, hipStream_t st) {
+    if (!mt_gemv_supported(a.m, a.K) || (a.swiglu && !mt_gemv_supported(a.m2, a.K)) || a.tile_rows <= 0 ||
+        a.rows <= 0 || a.xdiv <= 0 || max_items <= 0 || a.pair_slice <= 0 ||
+        (a.dense_n > 0 && (a.tiles != (a.rows + a.tile_rows - 1) / a.tile_rows ||
+                           max_items != a.tiles * ((a.dense_n + a.pair_slice - 1) / a.pair_slice))))
+        return hipErrorInvalidValue;
+    const int cmax = std::max(1, std::min(MT_CMAX, 16384 / a.K));  // <= 64 KB of x in LDS
+    hipLaunchKernelGGL(mt_gemv_kernel, dim3((unsigned)max_items), dim3(WG), (size_t)cmax * a.K * 4, st, a, cmax);
+    return hipGetLastError();
+}
+
+// Router softmax and top-k of every token of the chunk (grid T): the
+// selection of moe_topk_kernel (rank = the number of experts with a larger p,
+// or an equal p and a lower id), then the merged shared expert (id
+// n_experts, weight sigmoid of its gate logit) in slot top_k.
+__global__ __launch_bounds__(WG) void pf_moe_topk_kernel(PfMoeArgs a) {
+#pragma clang fp contract(off)
+    __shared__ float p[MOE_MAX_EXPERTS];
+    __shared__ float red[WG / WAVE];
+    __shared__ float sel[MOE_MAX_K];
+    __shared__ int sid[MOE_MAX_K];
+    const int n = a.n_experts, t = threadIdx.x, lane = t & (WAVE - 1), wave = t / WAVE, tok = blockIdx.x;
+    const float *lg = a.logits + (size_t)tok * n;
+    float mx = -INFINITY;
+    for (int i = t; i < n; i += WG) mx = fmaxf(mx, lg[i]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, WAVE));
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    float M = red[0];
+#pragma unroll
+    for (int w = 1; w < WG / WAVE; w++) M = fmaxf(M, red[w]);
+    __syncthreads();
+    float sum = 0.f;
+    for (int i = t; i < n; i += WG) {
+        const float e = expf(lg[i] - M);
+        p[i] = e;
+        sum += e;
+    }
+    sum = wave_sum(sum);
+    if (lane == 0) red[wave] = sum;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < WG / WAVE; w++) tot += red[w];
+    for (int i = t; i < n; i += WG) p[i] = p[i] / tot;
+    if (t < a.top_k) {  // defined ids and weights even if NaN logits leave a rank unfilled
+        sel[t] = 0.f;
+        sid[t] = 0;
+    }
+    __syncthreads();
+    for (int i = t; i < n; i += WG) {
+        const float pi = p[i];
+        int rank = 0;
+        for (int j = 0; j < n; j++) rank += better(p[j], j, pi, i) ? 1 : 0;
+        if (rank < a.top_k) {
+            sid[rank] = i;
+            sel[rank] = pi;
+        }
+    }
+    __syncthreads();
+    if (t < a.kp) {
+        int id;
+        float w;
+        if (t < a.top_k) {
+            float s = 0.f;
+            for (int k = 0; k < a.top_k; k++) s += sel[k];  // in rank order, as the sequential selection
+            id = sid[t];
+            w = a.norm_topk ? sel[t] / s : sel[t];
+        } else {  // the shared expert
+            id = n;
+            w = 1.0f / (1.0f + expf(-a.sgl[tok]));
+        }
+        a.ids[(size_t)tok * a.kp + t] = id;
+        a.w[(size_t)tok * a.kp + t] = w;
+    }
+}
+
+// exclusive prefix sum of v over threads (one value per thread of the
+// 1024-thread workgroup); *total receives the sum
+__device__ __forceinline__ int block_excl_scan(int v, int *wsum, int *total) {
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE, nw = blockDim.x / WAVE;
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) {
+        const int y = __shfl_up(x, o, WAVE);
+        if (lane >= o) x += y;
+    }
+    __syncthreads();  // wsum reusable
+    if (lane == WAVE - 1) wsum[wave] = x;
+    __syncthreads();
+    int before = 0, all = 0;
+    for (int w = 0; w < nw; w++) {
+        const int s = wsum[w];
+        if (w < wave) before += s;
+        all += s;
+    }
+    *total = all;
+    return before + x - v;
+}
+
+// Pairs grouped by expert (one workgroup of 1024 threads, one expert per
+// thread): counts, offsets, the pair lists (any order within an expert: each
+// pair's result is its own), and the work items (expert; pair slice << 16 |
+// row tile) of the gate/up and down multi-token GEMVs: tiles_gu / tiles_dn
+// row tiles per slice of pair_slice pairs of each chosen expert.
+__global__ __launch_bounds__(1024) void pf_moe_group_kernel(PfMoeArgs a) {
+    __shared__ int cnt[1024], fill[1024], wsum[16];
+    const int ne = a.n_experts + (a.kp > a.top_k ? 1 : 0), P = a.T * a.kp, e = threadIdx.x;
+    if (e < ne) {
+        cnt[e] = 0;
+        fill[e] = 0;
+    }
+    __syncthreads();
+    for (int p = threadIdx.x; p < P; p += blockDim.x) atomicAdd(&cnt[min(max(a.ids[p], 0), ne - 1)], 1);
+    __syncthreads();
+    const int c = e < ne ? cnt[e] : 0, ns = (c + a.pair_slice - 1) / a.pair_slice;
+    int tp, tg, td;
+    const int off = block_excl_scan(c, wsum, &tp);
+    const int og = block_excl_scan(ns * a.tiles_gu, wsum, &tg);
+    const int od = block_excl_scan(ns * a.tiles_dn, wsum, &td);
+    if (e < ne) {
+        a.off[e] = off;
+        a.cnt[e] = c;
+        for (int i = 0; i < ns * a.tiles_gu; i++) {
+            a.items_gu[2 * (og + i)] = e;
+            a.items_gu[2 * (og + i) + 1] = ((i / a.tiles_gu) << 16) | (i % a.tiles_gu);
+        }
+        for (int i = 0; i < ns * a.tiles_dn; i++) {
+            a.items_dn[2 * (od + i)] = e;
+            a.items_dn[2 * (od + i) + 1] = ((i / a.tiles_dn) << 16) | (i % a.tiles_dn);
+        }
+        fill[e] = off;  // the next free slot of e
+    }
+    if (threadIdx.x == 0) {
+        a.nitems[0] = tg;
+        a.nitems[1] = td;
+    }
+    __syncthreads();
+    for (int p = threadIdx.x; p < P; p += blockDim.x) {
+        const int x = min(max(a.ids[p], 0), ne - 1);
+        a.list[atomicAdd(&fill[x], 1)] = p;
+    }
+}
+
+// out[t][r] = sum over the token's slots s (rank order, the shared expert
+// last) of w[t][s] yd[t kp + s][r]
+__global__ __launch_bounds__(WG) void pf_moe_combine_kernel(PfMoeArgs a) {
+#pragma clang fp contract(off)
+    const int t = blockIdx.y, r = (int)blockIdx.x * WG + threadIdx.x;
+    if (r >= a.dim) return;
+    float acc = 0.f;
+    for (int s = 0; s < a.kp; s++)
+        acc += a.w[(size_t)t * a.kp + s] * a.yd[((size_t)t * a.kp + s) * a.dim + r];
+    a.out[(size_t)t * a.dim + r] = acc;
+}
+
+hipError_t launch_pf_moe_route(const PfMoeArgs &a, hipStream_t st) {
+    const int ne = a.n_experts + (a.kp > a.top_k ? 1 : 0);
+    if (a.T <= 0 || a.n_experts <= 0 || ne > 1024 || a.top_k < 1 || a.top_k > MOE_MAX_K || a.top_k > a.n_experts ||
+        a.kp < a.top_k || a.kp > a.top_k + 1 || (a.kp > a.top_k && !a.sgl) || a.tiles_gu > 0xFFFF ||
+        a.tiles_dn > 0xFFFF || a.pair_slice <= 0 || (int64_t)a.T * a.kp / a.pair_slice >= 0x7FFF)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(pf_moe_topk_kernel, dim3((unsigned)a.T), dim3(WG), 0, st, a);
+    hipLaunchKernelGGL(pf_moe_group_kernel, dim3(1), dim3(1024), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_pf_moe_combine(const PfMoeArgs &a, hipStream_t st) {
+    hipLaunchKernelGGL(pf_moe_combine_kernel, dim3((unsigned)((a.dim + WG - 1) / WG), (unsigned)a.T), dim3(WG), 0, st,
+                       a);
     return hipGetLastError();
 }
 

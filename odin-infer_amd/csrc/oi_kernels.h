@@ -202,14 +202,80 @@ struct PfQkvArgs {
     int32_t T, pos0, seq_len, n_heads, n_kv_heads;
 };
 hipError_t launch_pf_qkv(const PfQkvArgs &a, int head_dim, hipStream_t st);
+// gate: null, or [T][n_heads * head_dim] f32, the output multiplied by its
+// sigmoid before rounding (the Qwen3.5 attention's output gate)
 hipError_t launch_pf_attn(const float *q, const uint16_t *kc, const uint16_t *vc, uint16_t *out, int T, int pos0,
-                          int seq_len, int n_heads, int n_kv_heads, int head_dim, hipStream_t st);
+                          int seq_len, int n_heads, int n_kv_heads, int head_dim, hipStream_t st,
+                          const float *gate = nullptr);
 hipError_t launch_pf_add(float *x, const float *part, int split, int64_t total, hipStream_t st);
 // x += partial-product sums (part may be null), then out = f16(rmsnorm(x) * w); dim <= 16384
+// out32: null, or [T][dim] f32 that receives the norm's f32 result as well
 hipError_t launch_pf_addnorm16(float *x, const float *part, int split, const float *w, float eps, int dim, int T,
-                               uint16_t *out, hipStream_t st);
+                               uint16_t *out, hipStream_t st, float *out32 = nullptr);
 hipError_t launch_pf_swiglu16(const float *g, int gs, const float *u, int us, int64_t total, uint16_t *out,
                               hipStream_t st);
+// prefill_hybrid.hip: batched prefill of the Qwen3.5 hybrid layers
+struct PfQ35Args {
+    const float *q, *k, *v;        // projections' partial products [split][T][rows]; q rows [n_heads][q | gate]
+    int32_t qs, ks, vs;            // their K slices
+    const float *q_norm, *k_norm;  // [head_dim]
+    const float *inv_freq;         // [rotary_dim / 2]
+    float eps;
+    int32_t rotary_dim;
+    uint16_t *kc, *vc;             // this layer's cache
+    float *qout, *gate;            // [T][n_heads * head_dim]: rotated q, gate
+    int32_t T, pos0, seq_len, n_heads, n_kv_heads;
+};
+hipError_t launch_pf_q35_qkv(const PfQ35Args &a, int head_dim, hipStream_t st);
+struct PfDnArgs {
+    const float *qkv, *z, *b, *a;  // in_qkv / in_z / in_b / in_a partial products [split][T][rows]
+    int32_t qkvs, zs, bs, as;      // their K slices
+    const float *conv_w;           // [conv_dim][kernel]
+    const float *a_decay, *dt_bias;  // [n_vh]
+    const float *norm_w;           // [hv]
+    float eps;
+    float *conv_state;             // [conv_dim][kernel - 1], oldest first
+    float *state;                  // [n_vh][hk][hv]
+    float *conv_out;               // scratch [T][conv_dim]
+    float *qk;                     // scratch [T][2 n_kh hk]: normalized q (scaled), k
+    float *gates;                  // scratch [T][2 n_vh]: beta, decay
+    float *o;                      // scratch [T][n_vh hv]: delta-rule outputs
+    uint16_t *out16;               // [T][n_vh hv]: gated-normed, f16 (the output projection's input)
+    int32_t T, n_kh, n_vh, hk, hv, kernel;
+};
+bool pf_dn_supported(int hk, int hv, int kernel);
+hipError_t launch_pf_deltanet(const PfDnArgs &a, hipStream_t st);
+// kernels.hip: the routed-expert FFN of a prefill chunk.  Pairs p = t * kp + s
+// (token t, slot s of its kp chosen experts) are grouped by expert; a
+// multi-token GEMV reads each chosen expert's rows once for all of its pairs.
+struct MtGemvArgs {
+    DMat m, m2;                    // stacked matrices [n_exp * rows][K] (m2: up of a SwiGLU pair)
+    int32_t swiglu, K, rows, xdiv, tile_rows, dense_n, pair_slice, tiles;
+    const float *x;                // activation rows [*][K]: pair p reads row p / xdiv
+    float *y;                      // output rows [pairs][rows]
+    const int32_t *list, *off, *cnt;  // pairs by expert: list[off[e] .. off[e] + cnt[e])
+    const int32_t *items, *nitems; // work items [2]: expert, pair slice << 16 | row tile; their count
+};
+// dense_n > 0: one "expert" (e = 0) holding pairs 0 .. dense_n-1, no lists (a
+// plain multi-token GEMV); item it = slice * tiles + row tile, max_items =
+// tiles * ceil(dense_n / pair_slice)
+constexpr int MT_PAIR_SLICE = 32;  // pairs per work item of the routed-expert prefill
+bool mt_gemv_supported(const DMat &m, int32_t K);
+int mt_gemv_tile_rows(int32_t K, int32_t rows);
+hipError_t launch_mt_gemv(const MtGemvArgs &a, int max_items, hipStream_t st);
+struct PfMoeArgs {
+    const float *logits;           // [T][n_experts]
+    const float *sgl;              // [T] shared expert gate logits, or null
+    int32_t *ids;                  // [T][kp] expert (n_experts = the merged shared expert)
+    float *w;                      // [T][kp]
+    int32_t *list, *off, *cnt, *fill;  // [T kp], [n_exp] x 3
+    int32_t *items_gu, *items_dn, *nitems;  // [2 * tiles * (n_exp + T kp / pair_slice)], [2]
+    const float *yd;               // [T kp][dim] down outputs per pair
+    float *out;                    // [T][dim] the weighted sums
+    int32_t T, n_experts, top_k, kp, norm_topk, tiles_gu, tiles_dn, dim, pair_slice;
+};
+hipError_t launch_pf_moe_route(const PfMoeArgs &a, hipStream_t st);
+hipError_t launch_pf_moe_combine(const PfMoeArgs &a, hipStream_t st);
 // deltanet.hip: the gated DeltaNet token step (between the input and output
 // projections of a Qwen3.5 linear-attention layer)
 struct DnArgs {

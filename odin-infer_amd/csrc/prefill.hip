@@ -28,13 +28,6 @@ static __device__ __forceinline__ float block_sum(float v, float *red) {
     return s;
 }
 
-// sum of the K-slice partial products of element i
-static __device__ __forceinline__ float parts_at(const float *p, int split, size_t slice, size_t i) {
-    float s = p[i];
-    for (int z = 1; z < split; z++) s += p[(size_t)z * slice + i];
-    return s;
-}
-
 // x[t] += (sum of the K-slice partial products) when part is set, then
 // out[t] = f16 of x[t]'s RMSNorm with w: w[i] * (s * x[i]), s = 1 / sqrt(sum
 // x^2 / dim + eps) (ops.odin rmsnorm; the reference converts the f32 result
@@ -44,7 +37,7 @@ static __device__ __forceinline__ float parts_at(const float *p, int split, size
 // Grid: T; dim <= WG * PF_NPT.
 constexpr int PF_NPT = 64;
 __global__ __launch_bounds__(WG) void pf_addnorm16_kernel(float *x, const float *part, int split, const float *w,
-                                                          float eps, int dim, int T, uint16_t *out) {
+                                                          float eps, int dim, int T, uint16_t *out, float *out32) {
 #pragma clang fp contract(off)
     constexpr int NV = PF_NPT / 4;  // float4 per thread
     __shared__ float red[WG / WAVE];
@@ -92,8 +85,9 @@ __global__ __launch_bounds__(WG) void pf_addnorm16_kernel(float *x, const float 
         if (i < d4) {
             if (part) xt[i] = v[r];
             const float4 wv = w4[i];
-            o4[i] = uint2{(uint32_t)f2h(wv.x * (s * v[r].x)) | ((uint32_t)f2h(wv.y * (s * v[r].y)) << 16),
-                          (uint32_t)f2h(wv.z * (s * v[r].z)) | ((uint32_t)f2h(wv.w * (s * v[r].w)) << 16)};
+            const float4 n{wv.x * (s * v[r].x), wv.y * (s * v[r].y), wv.z * (s * v[r].z), wv.w * (s * v[r].w)};
+            o4[i] = uint2{(uint32_t)f2h(n.x) | ((uint32_t)f2h(n.y) << 16), (uint32_t)f2h(n.z) | ((uint32_t)f2h(n.w) << 16)};
+            if (out32) ((float4 *)(out32 + t * dim))[i] = n;
         }
     }
 }
@@ -154,7 +148,14 @@ struct PfAttnArgs {
     const uint16_t *kc, *vc;    // this layer's cache
     uint16_t *out;              // [T][n_heads * head_dim] f16 (the wo projection's input)
     int32_t pos0, seq_len, n_heads, n_kv_heads;
+    const float *gate;          // null, or [T][n_heads * head_dim]: out *= sigmoid(gate) (Qwen3.5)
 };
+
+// the attention output of one element, gated when the layer has a gate
+static __device__ __forceinline__ float pf_gated(const PfAttnArgs &a, float o, size_t i) {
+#pragma clang fp contract(off)
+    return a.gate ? o * sigmoid_ref(a.gate[i]) : o;
+}
 
 // Causal attention of token t (query head h, grid (n_heads, T)) over positions
 // 0 .. pos0 + t of the f16 cache (forward.odin:87-115: scores q.k / sqrt(hd),
@@ -234,7 +235,7 @@ __global__ __launch_bounds__(WG) void pf_attn_kernel(PfAttnArgs a) {
         float acc = 0.f;
 #pragma unroll
         for (int w = 0; w < NW; w++) acc += ow[w][i] * sc[w];
-        a.out[(size_t)t * QD + h * HD + i] = f2h(acc / lt);
+        a.out[(size_t)t * QD + h * HD + i] = f2h(pf_gated(a, acc / lt, (size_t)t * QD + h * HD + i));
     }
 }
 
@@ -372,11 +373,15 @@ __global__ __launch_bounds__(WG) void pf_fattn128_kernel(PfAttnArgs a, int T) {
     lsum += __shfl_xor(lsum, 16, WAVE);
     lsum += __shfl_xor(lsum, 32, WAVE);
     if (tq < T) {
-        uint16_t *dst = a.out + (size_t)tq * QD + h * HD + 4 * g;
+        const size_t d0 = (size_t)tq * QD + h * HD + 4 * g;
+        uint16_t *dst = a.out + d0;
 #pragma unroll
         for (int dt = 0; dt < 8; dt++) {
-            uint32_t w0 = (uint32_t)f2h(o[dt][0] / lsum) | ((uint32_t)f2h(o[dt][1] / lsum) << 16);
-            uint32_t w1 = (uint32_t)f2h(o[dt][2] / lsum) | ((uint32_t)f2h(o[dt][3] / lsum) << 16);
+            float r[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) r[e] = pf_gated(a, o[dt][e] / lsum, d0 + 16 * dt + e);
+            const uint32_t w0 = (uint32_t)f2h(r[0]) | ((uint32_t)f2h(r[1]) << 16);
+            const uint32_t w1 = (uint32_t)f2h(r[2]) | ((uint32_t)f2h(r[3]) << 16);
             *(u32x2 *)(dst + 16 * dt) = u32x2{w0, w1};
         }
     }
@@ -413,8 +418,8 @@ hipError_t launch_pf_qkv(const PfQkvArgs &a, int head_dim, hipStream_t st) {
 }
 
 hipError_t launch_pf_attn(const float *q, const uint16_t *kc, const uint16_t *vc, uint16_t *out, int T, int pos0,
-                          int seq_len, int n_heads, int n_kv_heads, int head_dim, hipStream_t st) {
-    PfAttnArgs a{q, kc, vc, out, pos0, seq_len, n_heads, n_kv_heads};
+                          int seq_len, int n_heads, int n_kv_heads, int head_dim, hipStream_t st, const float *gate) {
+    PfAttnArgs a{q, kc, vc, out, pos0, seq_len, n_heads, n_kv_heads, gate};
     const dim3 grid((unsigned)n_heads, (unsigned)T);
     if (head_dim == 128)
         hipLaunchKernelGGL(pf_fattn128_kernel, dim3((unsigned)n_heads, (unsigned)((T + 63) / 64)), dim3(WG), 0, st, a,
@@ -425,9 +430,9 @@ hipError_t launch_pf_attn(const float *q, const uint16_t *kc, const uint16_t *vc
 }
 
 hipError_t launch_pf_addnorm16(float *x, const float *part, int split, const float *w, float eps, int dim, int T,
-                               uint16_t *out, hipStream_t st) {
+                               uint16_t *out, hipStream_t st, float *out32) {
     if (dim > WG * PF_NPT) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(pf_addnorm16_kernel, dim3(T), dim3(WG), 0, st, x, part, split, w, eps, dim, T, out);
+    hipLaunchKernelGGL(pf_addnorm16_kernel, dim3(T), dim3(WG), 0, st, x, part, split, w, eps, dim, T, out, out32);
     return hipGetLastError();
 }
 

@@ -1,0 +1,324 @@
+// prefill_hybrid.hip -- the per-token operations of batched prefill for the
+// Qwen3.5 hybrid layers, T tokens at once (reference: qwen3_5/metal.odin:
+// 1510-1622 forward_gpu_batch; the per-token math is qwen3_5/forward.odin:
+// 46-225 and ops.odin).  The projections between them run on the matrix cores
+// (gemm.hip); the kernels here read the projections' K-slice partial products
+// and sum them in slice order.
+//
+// Full-attention layer (forward_full_layer):
+//   pf_q35_qkv_kernel  [q | gate] split, q / k head RMSNorm, partial RoPE at
+//                      pos0 + t, k and v rounded to f16 into the cache; the
+//                      causal attention with the sigmoid gate is
+//                      prefill.hip's (launch_pf_attn with a gate).
+// Linear-attention layer (forward_linear_layer):
+//   pf_dn_conv_kernel       causal depthwise conv over the chunk (inputs before
+//                           the chunk from the conv state) + silu
+//   pf_dn_conv_state_kernel the conv state after the chunk (its last inputs)
+//   pf_dn_prep_kernel       per token: l2norm of q (times 1/sqrt(head_k_dim))
+//                           and k, beta = sigmoid(b), decay = exp(ssm_a
+//                           softplus(a + dt_bias))
+//   pf_dn_delta_kernel      the delta rule over the chunk's tokens in order,
+//                           the state held in registers for the whole chunk
+//   pf_dn_gnorm_kernel      gated RMSNorm, f16 rows for the output projection
+//
+// Layouts: token-major; partial products [split][T][rows]; the conv state
+// [conv_dim][kernel - 1] oldest first and the recurrent state [n_vh][hk][hv]
+// are the decode path's, so decode continues from the chunk.
+
+#include "device_common.h"
+
+namespace oi {
+
+// Per token and head (grid (T, ceil(heads / 4)), one wave per head; q, k and
+// v heads in that order).  The q projection holds [q | gate] per head
+// (forward.odin:53-60); gate goes out unchanged.  q and k heads: RMSNorm with
+// q_norm / k_norm, then RoPE on the first rotary_dim dimensions (pairs i and
+// i + rotary_dim / 2, angle pos * inv_freq[i] in f32, ops.odin:77-89), as
+// qwen35_attn.hip does for one token.  Lane l holds dimensions l + 64 e.
+template <int HD>
+__global__ __launch_bounds__(WG) void pf_q35_qkv_kernel(PfQ35Args a) {
+#pragma clang fp contract(off)
+    constexpr int DPL = HD / WAVE;
+    __shared__ float xs[WG / WAVE][HD];
+    const int t = blockIdx.x, lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    const int hh = (int)blockIdx.y * (WG / WAVE) + wave;
+    if (hh >= a.n_heads + 2 * a.n_kv_heads) return;  // whole waves; no workgroup barrier below
+    const int pos = a.pos0 + t, QD = a.n_heads * HD, KVD = a.n_kv_heads * HD;
+    const bool isq = hh < a.n_heads, isk = !isq && hh < a.n_heads + a.n_kv_heads;
+    const int h = isq ? hh : isk ? hh - a.n_heads : hh - a.n_heads - a.n_kv_heads;
+    float v[DPL];
+    if (isq) {
+        const size_t slice = (size_t)a.T * 2 * QD, base = (size_t)t * 2 * QD + (size_t)h * 2 * HD;
+#pragma unroll
+        for (int e = 0; e < DPL; e++) {
+            v[e] = parts_at(a.q, a.qs, slice, base + lane + WAVE * e);
+            a.gate[(size_t)t * QD + h * HD + lane + WAVE * e] = parts_at(a.q, a.qs, slice, base + HD + lane + WAVE * e);
+        }
+    } else {
+        const float *src = isk ? a.k : a.v;
+        const int split = isk ? a.ks : a.vs;
+#pragma unroll
+        for (int e = 0; e < DPL; e++)
+            v[e] = parts_at(src, split, (size_t)a.T * KVD, (size_t)t * KVD + h * HD + lane + WAVE * e);
+    }
+    if (isq || isk) {
+        const float *nw = isq ? a.q_norm : a.k_norm;
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < DPL; e++) ss += v[e] * v[e];
+        ss = wave_sum(ss);
+        const float inv = 1.0f / sqrtf(ss / (float)HD + a.eps);
+        float *x = xs[wave];
+#pragma unroll
+        for (int e = 0; e < DPL; e++) {
+            v[e] = nw[lane + WAVE * e] * (inv * v[e]);
+            x[lane + WAVE * e] = v[e];
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes are done
+        __builtin_amdgcn_wave_barrier();
+        const int half = a.rotary_dim / 2;
+#pragma unroll
+        for (int e = 0; e < DPL; e++) {
+            const int i = lane + WAVE * e;
+            if (i < a.rotary_dim) {
+                const int pr = i < half ? i : i - half;
+                const float ang = (float)pos * a.inv_freq[pr];
+                const float c = cosf(ang), sn = sinf(ang);
+                v[e] = i < half ? x[i] * c - x[i + half] * sn : x[i - half] * sn + x[i] * c;
+            }
+        }
+    }
+    if (isq) {
+#pragma unroll
+        for (int e = 0; e < DPL; e++) a.qout[(size_t)t * QD + h * HD + lane + WAVE * e] = v[e];
+    } else {
+        uint16_t *c = (isk ? a.kc : a.vc) + ((size_t)h * a.seq_len + pos) * HD;
+#pragma unroll
+        for (int e = 0; e < DPL; e++) c[lane + WAVE * e] = f2h(v[e]);
+    }
+}
+
+// ---------------------------------------------------------------- DeltaNet --
+
+constexpr int DN_TT = 16;  // tokens per thread of the conv
+
+// in(tau) of channel c: the in_qkv projection of token tau of the chunk, or,
+// before the chunk, the conv state's input (tau in [-(KS-1), 0))
+template <int KS>
+static __device__ __forceinline__ float dn_in(const PfDnArgs &a, int CD, int c, int tau) {
+    if (tau >= 0) return parts_at(a.qkv, a.qkvs, (size_t)a.T * CD, (size_t)tau * CD + c);
+    return a.conv_state[(size_t)c * (KS - 1) + (KS - 1 + tau)];
+}
+
+// conv1d_step + silu (ops.odin:97-116) of channel c for tokens [16 y, 16 y +
+// 16): out = silu(w[KS-1] in(t) + sum_k w[k] in(t - (KS-1) + k)), the order
+// of the decode step.  Grid (ceil(conv_dim / 256), ceil(T / 16)).
+template <int KS>
+__global__ __launch_bounds__(WG) void pf_dn_conv_kernel(PfDnArgs a) {
+#pragma clang fp contract(off)
+    constexpr int KM1 = KS - 1;
+    const int CD = 2 * a.n_kh * a.hk + a.n_vh * a.hv;
+    const int c = (int)blockIdx.x * WG + threadIdx.x;
+    if (c >= CD) return;
+    const int t0 = (int)blockIdx.y * DN_TT, t1 = min(a.T, t0 + DN_TT);
+    float w[KS], win[KM1 > 0 ? KM1 : 1];
+#pragma unroll
+    for (int k = 0; k < KS; k++) w[k] = a.conv_w[(size_t)c * KS + k];
+#pragma unroll
+    for (int k = 0; k < KM1; k++) win[k] = dn_in<KS>(a, CD, c, t0 - KM1 + k);
+    for (int t = t0; t < t1; t++) {
+        const float x = dn_in<KS>(a, CD, c, t);
+        float acc = w[KM1] * x;
+#pragma unroll
+        for (int k = 0; k < KM1; k++) acc += w[k] * win[k];
+        a.conv_out[(size_t)t * CD + c] = silu_ref(acc);
+#pragma unroll
+        for (int k = 0; k + 1 < KM1; k++) win[k] = win[k + 1];
+        if (KM1 > 0) win[KM1 - 1] = x;
+    }
+}
+
+// the conv state after the chunk: its last KS-1 inputs, oldest first (runs
+// after pf_dn_conv_kernel, which reads the state from before the chunk)
+template <int KS>
+__global__ __launch_bounds__(WG) void pf_dn_conv_state_kernel(PfDnArgs a) {
+    const int CD = 2 * a.n_kh * a.hk + a.n_vh * a.hv;
+    const int c = (int)blockIdx.x * WG + threadIdx.x;
+    if (c >= CD) return;
+    float x[KS > 1 ? KS - 1 : 1];
+#pragma unroll
+    for (int k = 0; k < KS - 1; k++) x[k] = dn_in<KS>(a, CD, c, a.T - (KS - 1) + k);
+#pragma unroll
+    for (int k = 0; k < KS - 1; k++) a.conv_state[(size_t)c * (KS - 1) + k] = x[k];
+}
+
+// Per token (grid T): l2norm of each k head's q and k (ops.odin:27-37, eps
+// 1e-6 a floor on the norm; q also times 1/sqrt(head_k_dim),
+// forward.odin:187-192) into qk [T][2 key_dim] (q heads, then k heads); the
+// gates of every value head into gates [T][2 n_vh] (beta, then decay).
+template <int HK>
+__global__ __launch_bounds__(WG) void pf_dn_prep_kernel(PfDnArgs a) {
+#pragma clang fp contract(off)
+    constexpr int E = HK / WAVE;
+    const int t = blockIdx.x, lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    const int KD = a.n_kh * HK, CD = 2 * KD + a.n_vh * a.hv;
+    for (int kh = wave; kh < a.n_kh; kh += WG / WAVE) {
+        const float *q = a.conv_out + (size_t)t * CD + kh * HK, *k = q + KD;
+        float qv[E], kv[E], sq = 0.f, sk = 0.f;
+#pragma unroll
+        for (int e = 0; e < E; e++) {
+            qv[e] = q[lane + WAVE * e];
+            kv[e] = k[lane + WAVE * e];
+            sq += qv[e] * qv[e];
+            sk += kv[e] * kv[e];
+        }
+        sq = wave_sum(sq);
+        sk = wave_sum(sk);
+        const float iq = 1.0f / fmaxf(sqrtf(sq), 1e-6f), ik = 1.0f / fmaxf(sqrtf(sk), 1e-6f);
+        float *o = a.qk + (size_t)t * 2 * KD + kh * HK;
+#pragma unroll
+        for (int e = 0; e < E; e++) {
+            o[lane + WAVE * e] = qv[e] * iq * (1.0f / sqrtf((float)HK));
+            o[KD + lane + WAVE * e] = kv[e] * ik;
+        }
+    }
+    for (int vh = threadIdx.x; vh < a.n_vh; vh += WG) {
+        const size_t slice = (size_t)a.T * a.n_vh, i = (size_t)t * a.n_vh + vh;
+        const float b = parts_at(a.b, a.bs, slice, i), av = parts_at(a.a, a.as, slice, i);
+        a.gates[(size_t)t * 2 * a.n_vh + vh] = sigmoid_ref(b);
+        a.gates[(size_t)t * 2 * a.n_vh + a.n_vh + vh] = expf(a.a_decay[vh] * softplus_ref(av + a.dt_bias[vh]));
+    }
+}
+
+// The delta rule (forward.odin:193-209) over the chunk's tokens in order:
+//   S *= decay;  delta = (v - S^T k) beta;  S += k delta^T;  o = S^T q.
+// Grid (n_vh, hv / 32): a workgroup owns 32 state columns of value head vh
+// (k head vh % n_kh); each wave 8 columns, lane = 8 column + row group, a
+// row group 16 rows, so a lane holds 16 state values for the whole chunk (read
+// once, written once).  The column sums over the 8 row groups are DPP sums
+// inside the lane's group of 8.  Per 32 tokens the workgroup stages the k
+// head's q and k, its v columns and the gates in LDS.
+constexpr int DN_DB = 32;
+template <int HK, int HV>
+__global__ __launch_bounds__(WG) void pf_dn_delta_kernel(PfDnArgs a) {
+#pragma clang fp contract(off)
+    constexpr int RG = 8, RPL = HK / RG, QP = HK + HK / 4;  // rows per lane; row group g at 20 g (16 + 4 pad)
+    static_assert(RPL == 16 && HV % 32 == 0, "head shape");
+    __shared__ __attribute__((aligned(16))) float sq[DN_DB][QP];
+    __shared__ __attribute__((aligned(16))) float sk[DN_DB][QP];
+    __shared__ float sv[DN_DB][32];
+    __shared__ float sg[DN_DB][2];
+    const int vh = blockIdx.x, kh = vh % a.n_kh, c0 = (int)blockIdx.y * 32;
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    const int cl = wave * 8 + (lane >> 3), rg = lane & 7, j = c0 + cl, i0 = rg * RPL;
+    const int KD = a.n_kh * HK, CD = 2 * KD + a.n_vh * HV, VD = a.n_vh * HV;
+    float *S = a.state + (size_t)vh * HK * HV;
+    float s[RPL];
+#pragma unroll
+    for (int r = 0; r < RPL; r++) s[r] = S[(size_t)(i0 + r) * HV + j];
+    for (int tb = 0; tb < a.T; tb += DN_DB) {
+        const int nb = min(DN_DB, a.T - tb);
+        __syncthreads();  // the previous block's LDS reads are done
+        for (int idx = threadIdx.x; idx < nb * 2 * HK; idx += WG) {
+            const int tt = idx / (2 * HK), e = idx % (2 * HK), ee = e % HK;
+            const float val = a.qk[(size_t)(tb + tt) * 2 * KD + (e < HK ? 0 : KD) + kh * HK + ee];
+            (e < HK ? sq : sk)[tt][ee + (ee / RPL) * 4] = val;
+        }
+        for (int idx = threadIdx.x; idx < nb * 32; idx += WG) {
+            const int tt = idx / 32, cc = idx % 32;
+            sv[tt][cc] = a.conv_out[(size_t)(tb + tt) * CD + 2 * KD + vh * HV + c0 + cc];
+        }
+        if (threadIdx.x < 2 * nb) {
+            const int tt = threadIdx.x / 2, g = threadIdx.x % 2;
+            sg[tt][g] = a.gates[(size_t)(tb + tt) * 2 * a.n_vh + g * a.n_vh + vh];
+        }
+        __syncthreads();
+        for (int tt = 0; tt < nb; tt++) {
+            const float beta = sg[tt][0], decay = sg[tt][1];
+            const float4 *k4 = (const float4 *)&sk[tt][rg * (RPL + 4)], *q4 = (const float4 *)&sq[tt][rg * (RPL + 4)];
+            float kn[RPL], qn[RPL];
+#pragma unroll
+            for (int i = 0; i < RPL / 4; i++) {
+                const float4 kk = k4[i], qq = q4[i];
+                kn[4 * i] = kk.x; kn[4 * i + 1] = kk.y; kn[4 * i + 2] = kk.z; kn[4 * i + 3] = kk.w;
+                qn[4 * i] = qq.x; qn[4 * i + 1] = qq.y; qn[4 * i + 2] = qq.z; qn[4 * i + 3] = qq.w;
+            }
+            float kv = 0.f;
+#pragma unroll
+            for (int r = 0; r < RPL; r++) {
+                s[r] = s[r] * decay;
+                kv += s[r] * kn[r];
+            }
+            kv += OI_DPP(kv, 0xB1);  // sum over the lane's group of 8 (the row groups)
+            kv += OI_DPP(kv, 0x4E);
+            kv += dpp_mirror8(kv);
+            const float delta = (sv[tt][cl] - kv) * beta;
+            float o = 0.f;
+#pragma unroll
+            for (int r = 0; r < RPL; r++) {
+                s[r] += kn[r] * delta;
+                o += s[r] * qn[r];
+            }
+            o += OI_DPP(o, 0xB1);
+            o += OI_DPP(o, 0x4E);
+            o += dpp_mirror8(o);
+            if (rg == 0) a.o[(size_t)(tb + tt) * VD + vh * HV + j] = o;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RPL; r++) S[(size_t)(i0 + r) * HV + j] = s[r];
+}
+
+// gated RMSNorm (forward.odin:211-218): per token (grid T) and value head,
+// out = f16(norm_w[j] (inv o[j]) silu(z[j])), inv = 1 / sqrt(sum o^2 / hv +
+// eps); z from the in_z projection's partial products
+template <int HV>
+__global__ __launch_bounds__(WG) void pf_dn_gnorm_kernel(PfDnArgs a) {
+#pragma clang fp contract(off)
+    constexpr int E = HV / WAVE;
+    const int t = blockIdx.x, lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    const int VD = a.n_vh * HV;
+    for (int vh = wave; vh < a.n_vh; vh += WG / WAVE) {
+        float o[E], ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < E; e++) {
+            o[e] = a.o[(size_t)t * VD + vh * HV + lane + WAVE * e];
+            ss += o[e] * o[e];
+        }
+        ss = wave_sum(ss);
+        const float inv = 1.0f / sqrtf(ss / (float)HV + a.eps);
+#pragma unroll
+        for (int e = 0; e < E; e++) {
+            const int j = lane + WAVE * e;
+            const float z = parts_at(a.z, a.zs, (size_t)a.T * VD, (size_t)t * VD + vh * HV + j);
+            a.out16[(size_t)t * VD + vh * HV + j] = f2h(a.norm_w[j] * (inv * o[e]) * silu_ref(z));
+        }
+    }
+}
+
+static unsigned nblk(int64_t n, int per) { return (unsigned)((n + per - 1) / per); }
+
+hipError_t launch_pf_q35_qkv(const PfQ35Args &a, int head_dim, hipStream_t st) {
+    if (a.rotary_dim < 0 || a.rotary_dim > head_dim || a.rotary_dim % 2) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)a.T, nblk(a.n_heads + 2 * a.n_kv_heads, WG / WAVE));
+    if (head_dim == 128) hipLaunchKernelGGL(pf_q35_qkv_kernel<128>, grid, dim3(WG), 0, st, a);
+    else if (head_dim == 256) hipLaunchKernelGGL(pf_q35_qkv_kernel<256>, grid, dim3(WG), 0, st, a);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+bool pf_dn_supported(int hk, int hv, int kernel) { return hk == 128 && hv == 128 && kernel == 4; }
+
+hipError_t launch_pf_deltanet(const PfDnArgs &a, hipStream_t st) {
+    if (!pf_dn_supported(a.hk, a.hv, a.kernel) || a.T < a.kernel - 1 || a.n_kh <= 0 || a.n_vh % a.n_kh)
+        return hipErrorInvalidValue;
+    const int CD = 2 * a.n_kh * a.hk + a.n_vh * a.hv;
+    hipLaunchKernelGGL(pf_dn_conv_kernel<4>, dim3(nblk(CD, WG), nblk(a.T, DN_TT)), dim3(WG), 0, st, a);
+    hipLaunchKernelGGL(pf_dn_conv_state_kernel<4>, dim3(nblk(CD, WG)), dim3(WG), 0, st, a);
+    hipLaunchKernelGGL(pf_dn_prep_kernel<128>, dim3((unsigned)a.T), dim3(WG), 0, st, a);
+    hipLaunchKernelGGL((pf_dn_delta_kernel<128, 128>), dim3((unsigned)a.n_vh, 128 / 32), dim3(WG), 0, st, a);
+    hipLaunchKernelGGL(pf_dn_gnorm_kernel<128>, dim3((unsigned)a.T), dim3(WG), 0, st, a);
+    return hipGetLastError();
+}
+
+}  // namespace oi

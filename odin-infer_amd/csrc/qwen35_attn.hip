@@ -25,16 +25,6 @@ constexpr int Q35_CH = 64;   // positions per attention workgroup
 constexpr int Q35_GMAX = 8;  // query heads per kv head
 constexpr int Q35_MAXS = 2048;  // position splits (contexts up to 131072)
 
-static __device__ __forceinline__ float q35_sigmoid(float x) {
-#pragma clang fp contract(off)
-    if (x >= 0.0f) {
-        const float z = expf(-x);
-        return 1.0f / (1.0f + z);
-    }
-    const float z = expf(x);
-    return z / (1.0f + z);
-}
-
 // One workgroup per (kv head, group of GW (4, 2 or 1) of its query heads, split of
 // Q35_CH positions).  The split's K (rows padded against bank conflicts) and
 // V rows and the group's rotated q are staged in LDS; then
@@ -257,7 +247,7 @@ __global__ __launch_bounds__(WG) void q35_combine_kernel(Q35Args a) {
 #pragma unroll 8
         for (int s = 0; s < ns; s++) acc += pb[(size_t)s * (HD + 2) + i] * wsp[s];
         const float gate = a.qproj[(size_t)h * 2 * HD + HD + i];
-        a.out[(size_t)h * HD + i] = (acc / lt) * q35_sigmoid(gate);
+        a.out[(size_t)h * HD + i] = (acc / lt) * sigmoid_ref(gate);
     }
 }
 

@@ -70,6 +70,11 @@ CONFIGS = {
                                  used=10, eff=512, shared=512),
     "qwen35-hybrid-moe-4layer": _hybrid(2048, 512, 4, 16, 2, 256, 151936, 262144, 64, 16, 32, 128, experts=512,
                                         used=10, eff=512, shared=512, seed=41),
+    # two layers of the config 5 shapes (a DeltaNet layer, then a full-attention layer) and of the
+    # config 4 shapes: batched prefill parity at full per-layer size
+    "qwen35-hybrid-moe-2layer": _hybrid(2048, 512, 2, 16, 2, 256, 151936, 262144, 64, 16, 32, 128, experts=512,
+                                        used=10, eff=512, shared=512, interval=2, seed=43),
+    "qwen3-30b-a3b-2layer": _moe(2048, 2, 32, 4, 151936, 40960, 128, 8, 768, seed=33),
     # small hybrids for tests: dense FFN (the reference's layout) and routed experts + shared expert
     "qwen35-tiny": _hybrid(256, 512, 4, 4, 2, 128, 2048, 1024, 32, 2, 4, 128, seed=17),
     "qwen35-moe-tiny": _hybrid(256, 256, 4, 4, 2, 256, 2048, 1024, 64, 2, 4, 128, experts=8, used=2, eff=256,

@@ -1134,22 +1134,33 @@ static void moe_ffn_layer(ref_engine *e, const layer_w *lw, const float *x, floa
     for (int64_t r = 0; r < D; r++) y[r] += gs * t[r];
 }
 
+/* a projection of the per-token path (matmul_t) or, with `staged`, of the
+ * batched path (matmul_staged) */
+static int matmul_mode(ref_engine *e, int staged, float *out, const float *in, const tensor *t, int64_t n,
+                       int64_t d) {
+    if (!staged) {
+        matmul_t(e->pool, out, in, t->kind, t->data, n, d);
+        return 0;
+    }
+    return matmul_staged(e, out, in, t->kind, t->data, n, d);
+}
+
 /* forward_full_layer (qwen3_5/forward.odin:46-135) up to the residual add:
  * RMSNorm, the [q | gate], k and v projections, then the attention restated by
  * ref_qwen35_attn_steps (q/k RMSNorm, partial RoPE, f16 cache at pos, softmax
  * with dot * 1/sqrt(head_dim), sigmoid gate), wo. */
-static int q35_full_attention(ref_engine *e, layer_w *lw, int pos) {
+static int q35_full_attention(ref_engine *e, layer_w *lw, int pos, int staged) {
     const int64_t D = e->dim, QD = e->n_heads * e->head_dim, KVD = e->n_kv_heads * e->head_dim;
-    mm_pool *P = e->pool;
     ref_rmsnorm(e->xb, e->x, lw->attn_norm, D, e->rms_eps);
-    matmul_t(P, e->hy_qproj, e->xb, lw->wq.kind, lw->wq.data, D, 2 * QD);
-    matmul_t(P, e->hy_k, e->xb, lw->wk.kind, lw->wk.data, D, KVD);
-    matmul_t(P, e->hy_v, e->xb, lw->wv.kind, lw->wv.data, D, KVD);
+    if (matmul_mode(e, staged, e->hy_qproj, e->xb, &lw->wq, D, 2 * QD) ||
+        matmul_mode(e, staged, e->hy_k, e->xb, &lw->wk, D, KVD) ||
+        matmul_mode(e, staged, e->hy_v, e->xb, &lw->wv, D, KVD))
+        return -1;
     if (ref_qwen35_attn_steps((int)e->n_heads, (int)e->n_kv_heads, (int)e->head_dim, (int)e->rotary_dim,
                               (int)e->seq_len, e->rms_eps, 1, pos, e->hy_qproj, e->hy_k, e->hy_v, lw->q_norm,
                               lw->k_norm, e->inv_freq, lw->kc16, lw->vc16, e->hy_out))
         return -1;
-    matmul_t(P, e->xb2, e->hy_out, lw->wo.kind, lw->wo.data, QD, D);
+    if (matmul_mode(e, staged, e->xb2, e->hy_out, &lw->wo, QD, D)) return -1;
     for (int64_t i = 0; i < D; i++) e->x[i] += e->xb2[i];
     return 0;
 }
@@ -1157,19 +1168,19 @@ static int q35_full_attention(ref_engine *e, layer_w *lw, int pos) {
 /* forward_linear_layer (qwen3_5/forward.odin:137-225) up to the residual add:
  * RMSNorm, the in_qkv / in_z / in_b / in_a projections, the conv / l2norm /
  * delta rule / gated RMSNorm step restated by ref_deltanet_steps, ssm_out. */
-static int q35_linear_attention(ref_engine *e, layer_w *lw) {
+static int q35_linear_attention(ref_engine *e, layer_w *lw, int staged) {
     const int64_t D = e->dim, KD = e->lin_nk * e->lin_hk, VD = e->lin_nv * e->lin_hv, CD = 2 * KD + VD;
-    mm_pool *P = e->pool;
     ref_rmsnorm(e->xb, e->x, lw->attn_norm, D, e->rms_eps);
-    matmul_t(P, e->hy_qkv, e->xb, lw->in_qkv.kind, lw->in_qkv.data, D, CD);
-    matmul_t(P, e->hy_z, e->xb, lw->in_z.kind, lw->in_z.data, D, VD);
-    matmul_t(P, e->hy_b, e->xb, lw->in_b.kind, lw->in_b.data, D, e->lin_nv);
-    matmul_t(P, e->hy_a, e->xb, lw->in_a.kind, lw->in_a.data, D, e->lin_nv);
+    if (matmul_mode(e, staged, e->hy_qkv, e->xb, &lw->in_qkv, D, CD) ||
+        matmul_mode(e, staged, e->hy_z, e->xb, &lw->in_z, D, VD) ||
+        matmul_mode(e, staged, e->hy_b, e->xb, &lw->in_b, D, e->lin_nv) ||
+        matmul_mode(e, staged, e->hy_a, e->xb, &lw->in_a, D, e->lin_nv))
+        return -1;
     if (ref_deltanet_steps((int)e->lin_nk, (int)e->lin_nv, (int)e->lin_hk, (int)e->lin_hv, (int)e->lin_kernel,
                            e->rms_eps, 1, e->hy_qkv, e->hy_z, e->hy_b, e->hy_a, lw->conv_w, lw->ssm_a, lw->dt_bias,
                            lw->ssm_norm, lw->conv_state, lw->rec_state, e->hy_out))
         return -1;
-    matmul_t(P, e->xb2, e->hy_out, lw->ssm_out.kind, lw->ssm_out.data, VD, D);
+    if (matmul_mode(e, staged, e->xb2, e->hy_out, &lw->ssm_out, VD, D)) return -1;
     for (int64_t i = 0; i < D; i++) e->x[i] += e->xb2[i];
     return 0;
 }
@@ -1195,8 +1206,8 @@ static const float *forward_impl(ref_engine *e, int token, int pos, int staged, 
 
     for (int64_t l = 0; l < e->n_layers; l++) {
         layer_w *lw = &e->layers[l];
-        if (lw->kind == 1 && q35_full_attention(e, lw, pos)) return NULL;
-        if (lw->kind == 2 && q35_linear_attention(e, lw)) return NULL;
+        if (lw->kind == 1 && q35_full_attention(e, lw, pos, staged)) return NULL;
+        if (lw->kind == 2 && q35_linear_attention(e, lw, staged)) return NULL;
         if (lw->kind != 0) goto ffn;
         {
         int64_t loff = l * seq_len * kv_dim;
@@ -1277,10 +1288,11 @@ static const float *forward_impl(ref_engine *e, int token, int pos, int staged, 
             continue;
         }
         if (e->arch == 2) { /* mlp_layer, qwen3_5/forward.odin:227-243 */
-            matmul_t(P, e->hb, e->xb, lw->w1.kind, lw->w1.data, dim, hidden_dim);
-            matmul_t(P, e->hb2, e->xb, lw->w3.kind, lw->w3.data, dim, hidden_dim);
+            if (matmul_mode(e, staged, e->hb, e->xb, &lw->w1, dim, hidden_dim) ||
+                matmul_mode(e, staged, e->hb2, e->xb, &lw->w3, dim, hidden_dim))
+                return NULL;
             for (int64_t i = 0; i < hidden_dim; i++) e->hb2[i] = ref_silu(e->hb[i]) * e->hb2[i];
-            matmul_t(P, e->xb, e->hb2, lw->w2.kind, lw->w2.data, hidden_dim, dim);
+            if (matmul_mode(e, staged, e->xb, e->hb2, &lw->w2, hidden_dim, dim)) return NULL;
             for (int64_t i = 0; i < dim; i++) e->x[i] += e->xb[i];
             continue;
         }
@@ -1312,8 +1324,12 @@ EXPORT const float *ref_engine_forward(void *h, int token, int pos) {
 /* engine_forward_batch (qwen3_5/engine.odin:61-93): chunks of up to
  * MAX_BATCH_T = 512 tokens (metal.odin:22), cut to a multiple of 8, through
  * the batched path (staged projections, logits of the chunk's last token);
- * the trailing 1-7 tokens one at a time through forward.  Returns the last
- * token's logits, or NULL. */
+ * the trailing 1-7 tokens one at a time through forward.  In the batched path
+ * of every layout the attention / DeltaNet projections and a dense MLP are
+ * staged (forward_gpu_batch, metal.odin:1510-1634); the routed-expert FFN,
+ * which the reference does not have, stays in f32 (router, experts and
+ * shared expert as the per-token path).  Returns the last token's logits, or
+ * NULL. */
 EXPORT const float *ref_engine_prefill(void *h, const int *tokens, int n, int pos0) {
     ref_engine *e = (ref_engine *)h;
     if (n <= 0) {
@@ -1324,7 +1340,7 @@ EXPORT const float *ref_engine_prefill(void *h, const int *tokens, int n, int po
     int i = 0;
     while (i < n) {
         int rem = n - i;
-        if (rem >= 8 && e->arch == 0) {
+        if (rem >= 8) {
             int chunk = rem < 512 ? rem : 512;
             chunk -= chunk % 8;
             for (int t = 0; t < chunk; t++)

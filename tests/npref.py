@@ -353,7 +353,7 @@ def qwen35_attn_f64(n_heads, n_kv, hd, rotary_dim, seq_len, eps, pos0, qproj, k,
     return np.array(outs)
 
 
-def forward_general_f64(W, tokens, moe_renorm=True, shared_gate=True, attn_gate=True, ffn_norm=True):
+def forward_general_f64(W, tokens, moe_renorm=True, shared_gate=True, attn_gate=True, ffn_norm=True, staged=()):
     """Float64 forward of the routed-expert and hybrid layouts: "qwen3moe"
     (Qwen3 attention, routed-expert FFN) and "qwen35" (qwen3_5/forward.odin:
     16-243: every full_attention_interval-th layer full attention with
@@ -366,7 +366,10 @@ def forward_general_f64(W, tokens, moe_renorm=True, shared_gate=True, attn_gate=
     (no renormalization, no shared-expert gate, no attention output gate, the
     attention norm's weight used for the FFN norm).
     Logits after each token at positions 0.. (f16-rounded K/V, as the oracle's
-    f16 mode)."""
+    f16 mode).  Positions in `staged` take the batched prefill path's
+    projections (forward_gpu_batch, qwen3_5/metal.odin:1510-1634): the
+    attention / DeltaNet projections and a dense MLP with weights and inputs
+    rounded to f16; the router, routed experts and shared expert exact."""
     m = W.meta
     arch = m["general.architecture"]
     a = arch + "."
@@ -410,6 +413,14 @@ def forward_general_f64(W, tokens, moe_renorm=True, shared_gate=True, attn_gate=
 
     r16 = lambda v: v.astype(np.float16).astype(np.float64)
     G = lambda name: W.get(name)
+    h16 = {}
+
+    def S(name, st):  # a projection matrix, f16-rounded on a staged position
+        if not st:
+            return G(name)
+        if name not in h16:
+            h16[name] = r16(G(name))
+        return h16[name]
     kc = [[] for _ in range(L)]
     vc = [[] for _ in range(L)]
     conv = {}
@@ -417,42 +428,45 @@ def forward_general_f64(W, tokens, moe_renorm=True, shared_gate=True, attn_gate=
     outs = []
     for pos, tok in enumerate(tokens):
         x = emb[tok].copy()
+        st = pos in staged
         for l in range(L):
             p = "blk.%d." % l
             full = (not hybrid) or (l + 1) % interval == 0
             xb = rms(x, G(p + "attn_norm.weight"))
+            xs = r16(xb) if st else xb
             if not hybrid:
-                q = (G(p + "attn_q.weight") @ xb).reshape(H, hd)
-                k = (G(p + "attn_k.weight") @ xb).reshape(KVH, hd)
-                v = (G(p + "attn_v.weight") @ xb).reshape(KVH, hd)
+                q = (S(p + "attn_q.weight", st) @ xs).reshape(H, hd)
+                k = (S(p + "attn_k.weight", st) @ xs).reshape(KVH, hd)
+                v = (S(p + "attn_v.weight", st) @ xs).reshape(KVH, hd)
                 q = rope(np.stack([rms(qh, G(p + "attn_q_norm.weight")) for qh in q]), pos)
                 k = rope(np.stack([rms(kh, G(p + "attn_k_norm.weight")) for kh in k]), pos)
                 kc[l].append(r16(k))
                 vc[l].append(r16(v))
-                x = x + G(p + "attn_output.weight") @ attention(q, kc, vc, l).reshape(-1)
+                o = attention(q, kc, vc, l).reshape(-1)
+                x = x + S(p + "attn_output.weight", st) @ (r16(o) if st else o)
             elif full:
-                qp = (G(p + "attn_q.weight") @ xb).reshape(H, 2, hd)
-                k = (G(p + "attn_k.weight") @ xb).reshape(KVH, hd)
-                v = (G(p + "attn_v.weight") @ xb).reshape(KVH, hd)
+                qp = (S(p + "attn_q.weight", st) @ xs).reshape(H, 2, hd)
+                k = (S(p + "attn_k.weight", st) @ xs).reshape(KVH, hd)
+                v = (S(p + "attn_v.weight", st) @ xs).reshape(KVH, hd)
                 q = rope(np.stack([rms(qp[h, 0], G(p + "attn_q_norm.weight")) for h in range(H)]), pos)
                 k = rope(np.stack([rms(kh, G(p + "attn_k_norm.weight")) for kh in k]), pos)
                 kc[l].append(r16(k))
                 vc[l].append(r16(v))
-                o = attention(q, kc, vc, l) * (sig(qp[:, 1, :]) if attn_gate else 1.0)
-                x = x + G(p + "attn_output.weight") @ o.reshape(-1)
+                o = (attention(q, kc, vc, l) * (sig(qp[:, 1, :]) if attn_gate else 1.0)).reshape(-1)
+                x = x + S(p + "attn_output.weight", st) @ (r16(o) if st else o)
             else:
                 kd, vd = nk * hk, nv * hv
                 if l not in conv:
                     conv[l] = np.zeros((2 * kd + vd) * (kern - 1))
                     rec[l] = np.zeros(nv * hk * hv)
-                qkv = G(p + "attn_qkv.weight") @ xb
-                z = G(p + "attn_gate.weight") @ xb
-                bb = G(p + "ssm_beta.weight") @ xb
-                aa = G(p + "ssm_alpha.weight") @ xb
+                qkv = S(p + "attn_qkv.weight", st) @ xs
+                z = S(p + "attn_gate.weight", st) @ xs
+                bb = S(p + "ssm_beta.weight", st) @ xs
+                aa = S(p + "ssm_alpha.weight", st) @ xs
                 o, conv[l], rec[l] = deltanet_f64(nk, nv, hk, hv, kern, eps, qkv, z, bb, aa,
                                                   G(p + "ssm_conv1d.weight").reshape(-1), G(p + "ssm_a"),
                                                   G(p + "ssm_dt.bias"), G(p + "ssm_norm.weight"), conv[l], rec[l])
-                x = x + G(p + "ssm_out.weight") @ o[0]
+                x = x + S(p + "ssm_out.weight", st) @ (r16(o[0]) if st else o[0])
             nname = ("post_attention_norm.weight" if hybrid else "ffn_norm.weight") if ffn_norm else "attn_norm.weight"
             xb = rms(x, G(p + nname))
             if E:
@@ -473,7 +487,9 @@ def forward_general_f64(W, tokens, moe_renorm=True, shared_gate=True, attn_gate=
                     y += (sig(gs) if shared_gate else 1.0) * ys
                 x = x + y
             else:
-                gt, up = G(p + "ffn_gate.weight") @ xb, G(p + "ffn_up.weight") @ xb
-                x = x + G(p + "ffn_down.weight") @ (gt * sig(gt) * up)
+                xs = r16(xb) if st else xb
+                gt, up = S(p + "ffn_gate.weight", st) @ xs, S(p + "ffn_up.weight", st) @ xs
+                hh = gt * sig(gt) * up
+                x = x + S(p + "ffn_down.weight", st) @ (r16(hh) if st else hh)
         outs.append(out_w @ rms(x, G("output_norm.weight")))
     return outs

@@ -61,3 +61,36 @@ def test_oracle_hybrid_layer_schedule(make_model):
         full = "blk.%d.attn_q.weight" % l in W.tensors
         lin = "blk.%d.ssm_out.weight" % l in W.tensors
         assert (full, lin) == ((l + 1) % 4 == 0, (l + 1) % 4 != 0)
+
+
+@pytest.mark.parametrize("name,mistake", [("moe-tiny", dict(moe_renorm=False)),
+                                          ("qwen35-tiny", dict(attn_gate=False)),
+                                          ("qwen35-moe-tiny", dict(shared_gate=False))])
+def test_oracle_batched_prefill_vs_float64(make_model, name, mistake):
+    """The oracle's batched prefill for these layouts (a chunk of 8 with the
+    attention / DeltaNet / dense-MLP projections staged in f16, the routed
+    experts exact; then 3 tokens per token) against the float64 model with the
+    same positions staged.  The f16 rounding of the staged inputs makes this
+    comparison noisy: a relative change of 1e-7 in the float64 model's inputs
+    before the rounding (the size of the f32 / float64 difference) moves its
+    chunk logits by 4.5e-4 (moe-tiny) to 6.2e-4 (qwen35-tiny), about as much
+    as the staging itself; so the chunk is held to 1.5e-3 (which a staged
+    model with a planted composition mistake misses by 10x), and the
+    per-token tail after it to the per-token bound.  The staged product itself
+    is pinned exactly by test_gemm_oracle."""
+    path = make_model(name)
+    W = GGUFWeights(path)
+    tokens = TOKENS + [11, 250, 3]
+    ref = forward_general_f64(W, tokens, staged=set(range(8)))
+    bad = forward_general_f64(W, tokens[:8], staged=set(range(8)), **mistake)
+    r = refcpu.RefEngine(path, max_ctx=64, num_threads=min(8, os.cpu_count() or 1), kv_f16=True)
+    try:
+        got8 = np.array(r.prefill(tokens[:8], 0), np.float64)
+        err8 = scaled_err(got8, ref[7])
+        print("%s: oracle vs staged float64 %.3g, vs a planted mistake %.3g" % (name, err8, scaled_err(got8, bad[7])))
+        assert err8 <= 5 * TOL
+        assert scaled_err(got8, bad[7]) > 10 * 5 * TOL
+        got = np.array(r.prefill(tokens[8:], 8), np.float64)
+        assert scaled_err(got, ref[-1]) <= 5 * TOL
+    finally:
+        r.close()
