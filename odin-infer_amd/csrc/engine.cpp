@@ -948,6 +948,8 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     e->use_graph = !(ng && ng[0] == '1');
     const char *pu = std::getenv("OI_PREFILL_UNFUSED");
     e->pf_fused = !(pu && pu[0] == '1');
+    const char *pm = std::getenv("OI_PREFILL_NO_MFMA");
+    e->pf_no_mfma = pm && pm[0] == '1';
 
     std::printf("model: %s dim=%lld layers=%lld (attention %d, linear %d) heads=%lld/%lld hidden=%lld vocab=%lld "
                 "ctx=%lld/%lld experts=%lld/%lld  weights=%.0f MB  KV cache (f16)=%.0f MB  [gfx950]\n",
@@ -1065,9 +1067,15 @@ int prefill_alloc(oi_engine *e) {
     need[0] = std::max(need[0], T * D * 4);  // the routed experts' weighted sums
     const size_t xb = T * std::max({D, QD, H, VD}) * 2;
     const size_t NE = (size_t)(e->n_experts + 1), KP = (size_t)(e->top_k + 1), EF = (size_t)e->expert_ffn;
-    const int tg = moe ? (int)((EF + mt_gemv_tile_rows((int32_t)D, (int32_t)EF) - 1) / mt_gemv_tile_rows((int32_t)D, (int32_t)EF)) : 0;
-    const int td = moe ? (int)((D + mt_gemv_tile_rows((int32_t)EF, (int32_t)D) - 1) / mt_gemv_tile_rows((int32_t)EF, (int32_t)D)) : 0;
-    const size_t items_per_tile = NE + (T * KP + MT_PAIR_SLICE - 1) / MT_PAIR_SLICE;  // pair slices
+    // work items: row tiles x pair slices, for either expert kernel
+    size_t tg = 0, td = 0;
+    if (moe) {
+        const size_t rg = (size_t)mt_gemv_tile_rows((int32_t)D, (int32_t)EF), rd = (size_t)mt_gemv_tile_rows((int32_t)EF, (int32_t)D);
+        tg = std::max((EF + rg - 1) / rg * (NE + (T * KP + MT_PAIR_SLICE - 1) / MT_PAIR_SLICE),
+                      (EF + MT_MFMA_ROWS - 1) / MT_MFMA_ROWS * (NE + (T * KP + MT_MFMA_PAIRS - 1) / MT_MFMA_PAIRS));
+        td = std::max((D + rd - 1) / rd * (NE + (T * KP + MT_PAIR_SLICE - 1) / MT_PAIR_SLICE),
+                      (D + MT_MFMA_ROWS - 1) / MT_MFMA_ROWS * (NE + (T * KP + MT_MFMA_PAIRS - 1) / MT_MFMA_PAIRS));
+    }
     std::vector<size_t> sizes = {T * 4, T * D * 4, T * QD * 4 * 2, xb, need[0], need[1], need[2], need[3],
                                  full ? T * QD * 4 : 0,
                                  lin ? T * CD * 4 : 0, lin ? T * 2 * KD * 4 : 0, lin ? T * 2 * (size_t)e->lin_nv * 4 : 0,
@@ -1075,8 +1083,7 @@ int prefill_alloc(oi_engine *e) {
                                  moe ? T * D * 4 : 0, moe ? T * (size_t)e->n_experts * 4 : 0, moe ? T * 4 : 0,
                                  moe ? T * KP * 4 : 0, moe ? T * KP * EF * 4 : 0, moe ? T * KP * D * 4 : 0,
                                  moe ? T * KP * 4 : 0, moe ? T * KP * 4 : 0, moe ? NE * 4 : 0, moe ? NE * 4 : 0,
-                                 moe ? NE * 4 : 0, moe ? 8 * tg * items_per_tile : 0,
-                                 moe ? 8 * td * items_per_tile : 0, moe ? (size_t)8 : 0};
+                                 moe ? NE * 4 : 0, 8 * tg, 8 * td, moe ? (size_t)8 : 0};
     size_t total = 0;
     for (size_t b : sizes) total += al256(b);
     HIP_TRY(hipMalloc(&e->pf_mem, total));
@@ -1133,7 +1140,7 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
     r.K = D;
     r.rows = E;
     r.xdiv = 1;
-    r.tile_rows = mt_gemv_tile_rows(D, E);
+    r.tile_rows = std::max(1, mt_gemv_tile_rows(D, E) / 8);  // one pass of the lane groups: more workgroups
     r.tiles = (E + r.tile_rows - 1) / r.tile_rows;
     r.dense_n = T;
     r.pair_slice = MT_PAIR_SLICE;
@@ -1148,7 +1155,12 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
         r.y = e->pf_sg;
         HIP_TRY(launch_mt_gemv(r, slices, st));
     }
-    const int tr_gu = mt_gemv_tile_rows(D, EF), tr_dn = mt_gemv_tile_rows(EF, D);
+    // the chosen experts on the matrix cores where their type allows (f32 MFMA),
+    // else the multi-token GEMV
+    const bool mm = !e->pf_no_mfma && mt_mfma_supported(L.gexp, D, EF) && mt_mfma_supported(L.uexp, D, EF) &&
+                    L.gexp.type == L.uexp.type && mt_mfma_supported(L.dexp, EF, D);
+    const int tr_gu = mm ? MT_MFMA_ROWS : mt_gemv_tile_rows(D, EF), tr_dn = mm ? MT_MFMA_ROWS : mt_gemv_tile_rows(EF, D);
+    const int ps = mm ? MT_MFMA_PAIRS : MT_PAIR_SLICE;
     PfMoeArgs ma{};
     ma.logits = e->pf_lg;
     ma.sgl = L.shared ? e->pf_sg : nullptr;
@@ -1163,9 +1175,9 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
     ma.tiles_gu = (EF + tr_gu - 1) / tr_gu;
     ma.tiles_dn = (D + tr_dn - 1) / tr_dn;
     ma.dim = D;
-    ma.pair_slice = MT_PAIR_SLICE;
+    ma.pair_slice = ps;
     HIP_TRY(launch_pf_moe_route(ma, st));
-    const int item_tiles = NE + (pairs + MT_PAIR_SLICE - 1) / MT_PAIR_SLICE;  // bound on the pair slices
+    const int item_tiles = NE + (pairs + ps - 1) / ps;  // bound on the pair slices
     MtGemvArgs g{};
     g.m = L.gexp; g.m2 = L.uexp;
     g.swiglu = 1;
@@ -1173,16 +1185,16 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
     g.x = e->pf_xn; g.y = e->pf_h;
     g.list = e->pf_list; g.off = e->pf_off; g.cnt = e->pf_cnt;
     g.items = e->pf_items_gu; g.nitems = e->pf_nitems;
-    g.pair_slice = MT_PAIR_SLICE;
-    HIP_TRY(launch_mt_gemv(g, item_tiles * ma.tiles_gu, st));
+    g.pair_slice = ps;
+    HIP_TRY(mm ? launch_mt_mfma(g, item_tiles * ma.tiles_gu, st) : launch_mt_gemv(g, item_tiles * ma.tiles_gu, st));
     MtGemvArgs d{};
     d.m = L.dexp;
     d.K = EF; d.rows = D; d.xdiv = 1; d.tile_rows = tr_dn;
     d.x = e->pf_h; d.y = e->pf_yd;
     d.list = e->pf_list; d.off = e->pf_off; d.cnt = e->pf_cnt;
     d.items = e->pf_items_dn; d.nitems = e->pf_nitems + 1;
-    d.pair_slice = MT_PAIR_SLICE;
-    HIP_TRY(launch_mt_gemv(d, item_tiles * ma.tiles_dn, st));
+    d.pair_slice = ps;
+    HIP_TRY(mm ? launch_mt_mfma(d, item_tiles * ma.tiles_dn, st) : launch_mt_gemv(d, item_tiles * ma.tiles_dn, st));
     HIP_TRY(launch_pf_moe_combine(ma, st));
     return OI_OK;
 }

@@ -108,5 +108,6 @@ struct oi_engine {
     int32_t *pf_ids = nullptr, *pf_list = nullptr, *pf_off = nullptr, *pf_cnt = nullptr, *pf_fill = nullptr;
     int32_t *pf_items_gu = nullptr, *pf_items_dn = nullptr, *pf_nitems = nullptr;
     bool pf_fused = true;  // gate/up GEMM with the SwiGLU epilogue where it applies (OI_PREFILL_UNFUSED=1: off)
+    bool pf_no_mfma = false;  // routed experts of a prefill on the multi-token GEMV only (OI_PREFILL_NO_MFMA=1)
 };
 

@@ -792,6 +792,177 @@ hipError_t launch_mt_gemv(const MtGemvArgs &a, int max_items, hipStream_t st) {
     return hipGetLastError();
 }
 
+// ---- the same on the matrix cores (f32 MFMA): Q4_K / Q6_K / Q8_0 experts
+//
+// v_mfma_f32_16x16x4_f32: D[16][16] += A[16][4] B[4][16]; lane l gives
+// A[i][k] with i = l % 16, k = l / 16, and B[k][j] with j = l % 16, k = l / 16,
+// and holds D[i][j] for j = l % 16, i = 4 (l / 16) + e (e < 4).  Lane l takes
+// row i of its wave's 16 and pair j = i of the item's 16; for each 64-weight
+// unit it decodes the quarter g = l / 16 (16 weights, exact), reads the same
+// 16 K positions of its pair's x, and 16 products sum the unit over the four
+// quarters.  f32 operands and accumulation: the arithmetic of mt_gemv_kernel
+// up to the order of the sums.
+constexpr int MM_PAIRS = 16, MM_ROWS = 16 * (WG / WAVE), MM_KC = 256;
+static_assert(MM_PAIRS == MT_MFMA_PAIRS && MM_ROWS == MT_MFMA_ROWS, "item shape");
+
+// Quarter g of unit u of `row`: the weights at row elements
+// unit_elem(type, u, 16 g) + s, s < 16 (decode_unit's values).  load_quarter
+// issues the loads (raw bytes), decode_quarter does the arithmetic, so the
+// loads of later units can be in flight while earlier ones are used.
+struct QRaw {
+    u32x4 a, b;  // Q4_K: quants (plane g & 1), header; Q6_K: ql (plane g & 1), qh; Q8_0: quants (plane g)
+    uint32_t x;  // Q6_K: d | scale << 16; Q8_0: d
+};
+__device__ __forceinline__ QRaw load_quarter(const DMat &m, int row, int u, int g) {
+    const size_t ui = (size_t)row * (m.cols >> 6) + u;
+    QRaw r;
+    if (m.type == T_Q4_K) {
+        r.a = *(const u32x4 *)(m.q + (g & 1) * m.plane + ui * 16);
+        r.b = *(const u32x4 *)(m.s + ((size_t)row * (m.cols >> 8) + (u >> 2)) * 16);
+        r.x = 0;
+    } else if (m.type == T_Q6_K) {
+        const size_t sbi = (size_t)row * (m.cols >> 8) + (u >> 2);
+        r.a = *(const u32x4 *)(m.q + (g & 1) * m.plane + ui * 16);
+        r.b = *(const u32x4 *)(m.q + 2 * m.plane + ui * 16);
+        const uint8_t sc = m.s[sbi * 16 + 8 * ((u >> 1) & 1) + (u & 1) + 2 * g];
+        r.x = (uint32_t)m.d[sbi] | ((uint32_t)sc << 16);
+    } else {
+        r.a = *(const u32x4 *)(m.q + g * m.plane + ui * 16);
+        r.b = u32x4{0u, 0u, 0u, 0u};
+        r.x = m.d[(size_t)row * (m.cols >> 5) + 2 * u + (g >> 1)];
+    }
+    return r;
+}
+__device__ __forceinline__ void decode_quarter(int type, const QRaw &r, int u, int g, float *w) {
+#pragma clang fp contract(off)
+    const uint32_t qw[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+    if (type == T_Q4_K) {  // ggml/quant.odin:178-209
+        const float d = h2f(r.b.x & 0xFFFFu), dmin = h2f(r.b.x >> 16);
+        uint32_t sc0, m0, sc1, m1;
+        q4k_scales(u & 3, r.b.y, r.b.z, r.b.w, sc0, m0, sc1, m1);
+        const bool hi = g >= 2;
+        const float dd = d * (float)(hi ? sc1 : sc0), mm = dmin * (float)(hi ? m1 : m0);
+#pragma unroll
+        for (int l = 0; l < 16; l++) {
+            const uint32_t b = (qw[l >> 2] >> ((l & 3) * 8)) & 0xFFu;
+            w[l] = dd * (float)(hi ? b >> 4 : b & 0xFu) - mm;
+        }
+    } else if (type == T_Q6_K) {  // ggml/quant.odin:212-247
+        const float dsc = h2f(r.x & 0xFFFFu) * (float)(int8_t)(r.x >> 16);
+        const uint32_t hw[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const uint32_t ql = (qw[i >> 2] >> ((i & 3) * 8)) & 0xFFu, qh = (hw[i >> 2] >> ((i & 3) * 8)) & 0xFFu;
+            const int q = (int)((g < 2 ? (ql & 0xFu) : (ql >> 4)) | (((qh >> (2 * g)) & 3u) << 4)) - 32;
+            w[i] = dsc * (float)q;
+        }
+    } else {  // Q8_0, ggml/quant.odin:87-96
+        const float d = h2f(r.x & 0xFFFFu);
+#pragma unroll
+        for (int j = 0; j < 16; j++) w[j] = d * (float)(int8_t)((qw[j >> 2] >> ((j & 3) * 8)) & 0xFFu);
+    }
+}
+
+typedef float mm_f32x4 __attribute__((ext_vector_type(4)));
+
+// Work item (expert e, slice of 16 pairs, tile of 64 rows); the x rows of the
+// slice's pairs staged in LDS, whole when they fit (few pairs), else KC K
+// positions (KC / 256 super-blocks) at a time; rows padded by 4 floats; lanes
+// of pairs past the slice's count give B = 0.  Each lane keeps the raw loads of the next super-block's 4 units in
+// flight while it decodes and multiplies the current one's.
+template <int KC>
+__global__ __launch_bounds__(WG) void mt_mfma_kernel(MtGemvArgs a) {
+#pragma clang fp contract(off)
+    __shared__ __attribute__((aligned(16))) float xs[MM_PAIRS][KC + 4];
+    const int it = blockIdx.x;
+    if (it >= *a.nitems) return;
+    const int e = a.items[2 * it], tile = a.items[2 * it + 1] & 0xFFFF, slice = a.items[2 * it + 1] >> 16;
+    const int base = a.off[e] + slice * MM_PAIRS, n = min(MM_PAIRS, a.cnt[e] - slice * MM_PAIRS);
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE, i16 = lane & 15, g = lane >> 4;
+    const int row0 = tile * MM_ROWS + 16 * wave;
+    const bool active = row0 < a.rows;  // rows % 16 == 0
+    const int row = min(row0 + i16, a.rows - 1);
+    const DMat gm = sub_rows(a.m, e * a.rows, a.rows);
+    const DMat um = a.swiglu ? sub_rows(a.m2, e * a.rows, a.rows) : gm;
+    const int nsb = a.K / MM_KC;  // super-blocks
+    const bool whole = n * (a.K + 4) <= MM_PAIRS * (KC + 4);  // every x row in LDS at once
+    const int xstride = whole ? a.K + 4 : KC + 4;
+    float *xsf = &xs[0][0];
+    mm_f32x4 accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
+    QRaw rg[4], ru[4];
+    if (active) {
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            rg[s] = load_quarter(gm, row, s, g);
+            if (a.swiglu) ru[s] = load_quarter(um, row, s, g);
+        }
+    }
+    for (int c = 0; c < nsb; c++) {
+        const int k0 = whole ? 0 : (c / (KC / MM_KC)) * KC, kw = whole ? a.K : KC;
+        if (whole ? c == 0 : c % (KC / MM_KC) == 0) {
+            __syncthreads();  // the previous chunk's reads are done
+            for (int idx = threadIdx.x; idx < n * kw / 4; idx += WG) {
+                const int j = idx / (kw / 4), q = idx % (kw / 4);
+                *(float4 *)(xsf + j * xstride + 4 * q) =
+                    ((const float4 *)(a.x + (size_t)(a.list[base + j] / a.xdiv) * a.K + k0))[q];
+            }
+            __syncthreads();
+        }
+        if (!active) continue;
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const int u = 4 * c + s;
+            float w[16], wu[16], xv[16];
+            decode_quarter(gm.type, rg[s], u, g, w);
+            if (a.swiglu) decode_quarter(um.type, ru[s], u, g, wu);
+            if (c + 1 < nsb) {  // the next super-block's unit s
+                rg[s] = load_quarter(gm, row, u + 4, g);
+                if (a.swiglu) ru[s] = load_quarter(um, row, u + 4, g);
+            }
+            const float4 *xr = (const float4 *)(xsf + i16 * xstride + unit_elem(gm.type, u, 16 * g) - k0);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (i16 < n) t = xr[q];  // rows past n are not staged
+                xv[4 * q] = t.x; xv[4 * q + 1] = t.y; xv[4 * q + 2] = t.z; xv[4 * q + 3] = t.w;
+            }
+#pragma unroll
+            for (int s2 = 0; s2 < 16; s2++) accg = __builtin_amdgcn_mfma_f32_16x16x4f32(w[s2], xv[s2], accg, 0, 0, 0);
+            if (a.swiglu) {
+#pragma unroll
+                for (int s2 = 0; s2 < 16; s2++)
+                    accu = __builtin_amdgcn_mfma_f32_16x16x4f32(wu[s2], xv[s2], accu, 0, 0, 0);
+            }
+        }
+    }
+    if (!active || i16 >= n) return;
+    const int p = a.list[base + i16];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        float v = accg[r];
+        if (a.swiglu) {
+            v *= 1.0f / (1.0f + expf(-v));
+            v *= accu[r];
+        }
+        a.y[(size_t)p * a.rows + row0 + 4 * g + r] = v;
+    }
+}
+
+bool mt_mfma_supported(const DMat &m, int32_t K, int32_t rows) {
+    return (m.type == T_Q4_K || m.type == T_Q6_K || m.type == T_Q8_0) && m.cols == K && K % MM_KC == 0 &&
+           rows % 16 == 0;
+}
+
+hipError_t launch_mt_mfma(const MtGemvArgs &a, int max_items, hipStream_t st) {
+    if (!mt_mfma_supported(a.m, a.K, a.rows) || (a.swiglu && (!mt_mfma_supported(a.m2, a.K, a.rows) ||
+                                                              a.m2.type != a.m.type)) ||
+        a.tile_rows != MM_ROWS || a.pair_slice != MM_PAIRS || a.xdiv <= 0 || max_items <= 0 || a.dense_n > 0)
+        return hipErrorInvalidValue;
+    if (a.K % 512 == 0) hipLaunchKernelGGL(mt_mfma_kernel<512>, dim3((unsigned)max_items), dim3(WG), 0, st, a);
+    else hipLaunchKernelGGL(mt_mfma_kernel<MM_KC>, dim3((unsigned)max_items), dim3(WG), 0, st, a);
+    return hipGetLastError();
+}
+
 // Router softmax and top-k of every token of the chunk (grid T): the
 // selection of moe_topk_kernel (rank = the number of experts with a larger p,
 // or an equal p and a lower id), then the merged shared expert (id

@@ -263,6 +263,11 @@ constexpr int MT_PAIR_SLICE = 32;  // pairs per work item of the routed-expert p
 bool mt_gemv_supported(const DMat &m, int32_t K);
 int mt_gemv_tile_rows(int32_t K, int32_t rows);
 hipError_t launch_mt_gemv(const MtGemvArgs &a, int max_items, hipStream_t st);
+// the same on the matrix cores (f32 MFMA) for Q4_K / Q6_K / Q8_0 matrices with
+// K % 256 == 0 and rows % 16 == 0: items of 16 pairs x 64 rows
+constexpr int MT_MFMA_PAIRS = 16, MT_MFMA_ROWS = 64;
+bool mt_mfma_supported(const DMat &m, int32_t K, int32_t rows);
+hipError_t launch_mt_mfma(const MtGemvArgs &a, int max_items, hipStream_t st);
 struct PfMoeArgs {
     const float *logits;           // [T][n_experts]
     const float *sgl;              // [T] shared expert gate logits, or null
