@@ -948,8 +948,8 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     e->use_graph = !(ng && ng[0] == '1');
     const char *pu = std::getenv("OI_PREFILL_UNFUSED");
     e->pf_fused = !(pu && pu[0] == '1');
-    const char *pm = std::getenv("OI_PREFILL_NO_MFMA");
-    e->pf_no_mfma = pm && pm[0] == '1';
+    const char *pm = std::getenv("OI_PREFILL_EXPERTS");  // "gemv" / "f32": the other expert kernels (tests)
+    e->pf_experts = !pm ? 0 : std::strcmp(pm, "gemv") == 0 ? 1 : std::strcmp(pm, "f32") == 0 ? 2 : 0;
 
     std::printf("model: %s dim=%lld layers=%lld (attention %d, linear %d) heads=%lld/%lld hidden=%lld vocab=%lld "
                 "ctx=%lld/%lld experts=%lld/%lld  weights=%.0f MB  KV cache (f16)=%.0f MB  [gfx950]\n",
@@ -1080,7 +1080,7 @@ int prefill_alloc(oi_engine *e) {
                                  full ? T * QD * 4 : 0,
                                  lin ? T * CD * 4 : 0, lin ? T * 2 * KD * 4 : 0, lin ? T * 2 * (size_t)e->lin_nv * 4 : 0,
                                  lin ? T * VD * 4 : 0,
-                                 moe ? T * D * 4 : 0, moe ? T * (size_t)e->n_experts * 4 : 0, moe ? T * 4 : 0,
+                                 moe ? T * D * 4 : 0, moe ? T * (size_t)e->n_experts * 4 : 0,
                                  moe ? T * KP * 4 : 0, moe ? T * KP * EF * 4 : 0, moe ? T * KP * D * 4 : 0,
                                  moe ? T * KP * 4 : 0, moe ? T * KP * 4 : 0, moe ? NE * 4 : 0, moe ? NE * 4 : 0,
                                  moe ? NE * 4 : 0, 8 * tg, 8 * td, moe ? (size_t)8 : 0};
@@ -1109,7 +1109,6 @@ int prefill_alloc(oi_engine *e) {
     e->pf_o = (float *)take();
     e->pf_xn = (float *)take();
     e->pf_lg = (float *)take();
-    e->pf_sg = (float *)take();
     e->pf_w = (float *)take();
     e->pf_h = (float *)take();
     e->pf_yd = (float *)take();
@@ -1147,23 +1146,16 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
     r.x = e->pf_xn;
     r.y = e->pf_lg;
     HIP_TRY(launch_mt_gemv(r, r.tiles * slices, st));
-    if (L.shared) {
-        r.m = L.sh_inp;
-        r.rows = 1;
-        r.tile_rows = 1;
-        r.tiles = 1;
-        r.y = e->pf_sg;
-        HIP_TRY(launch_mt_gemv(r, slices, st));
-    }
     // the chosen experts on the matrix cores where their type allows (f32 MFMA),
     // else the multi-token GEMV
-    const bool mm = !e->pf_no_mfma && mt_mfma_supported(L.gexp, D, EF) && mt_mfma_supported(L.uexp, D, EF) &&
+    const bool mm = e->pf_experts != 1 && mt_mfma_supported(L.gexp, D, EF) && mt_mfma_supported(L.uexp, D, EF) &&
                     L.gexp.type == L.uexp.type && mt_mfma_supported(L.dexp, EF, D);
     const int tr_gu = mm ? MT_MFMA_ROWS : mt_gemv_tile_rows(D, EF), tr_dn = mm ? MT_MFMA_ROWS : mt_gemv_tile_rows(EF, D);
     const int ps = mm ? MT_MFMA_PAIRS : MT_PAIR_SLICE;
     PfMoeArgs ma{};
     ma.logits = e->pf_lg;
-    ma.sgl = L.shared ? e->pf_sg : nullptr;
+    if (L.shared) ma.sh_inp = L.sh_inp;
+    ma.xn = e->pf_xn;
     ma.ids = e->pf_ids;
     ma.w = e->pf_w;
     ma.list = e->pf_list; ma.off = e->pf_off; ma.cnt = e->pf_cnt; ma.fill = e->pf_fill;
@@ -1186,7 +1178,8 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
     g.list = e->pf_list; g.off = e->pf_off; g.cnt = e->pf_cnt;
     g.items = e->pf_items_gu; g.nitems = e->pf_nitems;
     g.pair_slice = ps;
-    HIP_TRY(mm ? launch_mt_mfma(g, item_tiles * ma.tiles_gu, st) : launch_mt_gemv(g, item_tiles * ma.tiles_gu, st));
+    HIP_TRY(mm ? launch_mt_mfma(g, item_tiles * ma.tiles_gu, st, e->pf_experts == 2)
+               : launch_mt_gemv(g, item_tiles * ma.tiles_gu, st));
     MtGemvArgs d{};
     d.m = L.dexp;
     d.K = EF; d.rows = D; d.xdiv = 1; d.tile_rows = tr_dn;
@@ -1194,7 +1187,8 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
     d.list = e->pf_list; d.off = e->pf_off; d.cnt = e->pf_cnt;
     d.items = e->pf_items_dn; d.nitems = e->pf_nitems + 1;
     d.pair_slice = ps;
-    HIP_TRY(mm ? launch_mt_mfma(d, item_tiles * ma.tiles_dn, st) : launch_mt_gemv(d, item_tiles * ma.tiles_dn, st));
+    HIP_TRY(mm ? launch_mt_mfma(d, item_tiles * ma.tiles_dn, st, e->pf_experts == 2)
+               : launch_mt_gemv(d, item_tiles * ma.tiles_dn, st));
     HIP_TRY(launch_pf_moe_combine(ma, st));
     return OI_OK;
 }

@@ -104,10 +104,11 @@ struct oi_engine {
     uint16_t *pf_xb = nullptr;
     float *pf_gate = nullptr;
     float *pf_conv = nullptr, *pf_qk = nullptr, *pf_gates = nullptr, *pf_o = nullptr;
-    float *pf_xn = nullptr, *pf_lg = nullptr, *pf_sg = nullptr, *pf_w = nullptr, *pf_h = nullptr, *pf_yd = nullptr;
+    float *pf_xn = nullptr, *pf_lg = nullptr, *pf_w = nullptr, *pf_h = nullptr, *pf_yd = nullptr;
     int32_t *pf_ids = nullptr, *pf_list = nullptr, *pf_off = nullptr, *pf_cnt = nullptr, *pf_fill = nullptr;
     int32_t *pf_items_gu = nullptr, *pf_items_dn = nullptr, *pf_nitems = nullptr;
     bool pf_fused = true;  // gate/up GEMM with the SwiGLU epilogue where it applies (OI_PREFILL_UNFUSED=1: off)
-    bool pf_no_mfma = false;  // routed experts of a prefill on the multi-token GEMV only (OI_PREFILL_NO_MFMA=1)
+    int pf_experts = 0;  // routed experts of a prefill: 0 the default kernels, 1 the multi-token GEMV, 2 f32 MFMA
+                         // only (OI_PREFILL_EXPERTS=gemv / f32)
 };
 

@@ -948,32 +948,236 @@ __global__ __launch_bounds__(WG) void mt_mfma_kernel(MtGemvArgs a) {
     }
 }
 
+// ---- Q4_K experts on f16 MFMA with the weights exact --------------------
+//
+// A Q4_K weight is d1 q - m1 with q in 0..15 and (d1, m1) per 32 weights
+// (one sub-block) and row, so a sub-block's dot product with x is
+//   d1 sum(q x) - m1 sum(x),
+// and sum(q x) runs on v_mfma_f32_16x16x32_f16: q is an exact half, x is
+// split into hi = f16(x) and lo = f16(x - hi) (x to ~2^-22), two products per
+// sub-block with f32 accumulation; sum(x) is the f32 sum of x.  The weights
+// are never rounded (the staged path rounds d1 q - m1 to f16), so this is the
+// f32 arithmetic of mt_gemv_kernel up to the order of the sums and the x split.
+// Operand layout (per lane l, 8 halves): A[i][k], i = l % 16, k = 8 (l / 16) + e;
+// B[k][j], j = l % 16; D[i][j]: j = l % 16, i = 4 (l / 16) + e.  Lane (i, g =
+// l / 16) loads bytes 8g .. 8g+7 of row i's 32 quant bytes of a unit (low
+// nibbles: sub-block 0's K positions 8g + e, high nibbles sub-block 1's), and
+// the x halves of pair i at the same K positions.
+typedef _Float16 mq_h8 __attribute__((ext_vector_type(8)));
+
+// the 8 nibbles (low when hi == false) of 8 bytes as exact halves
+__device__ __forceinline__ mq_h8 nibbles_h8(uint32_t w0, uint32_t w1, bool hi) {
+    const uint32_t n0 = (hi ? w0 >> 4 : w0) & 0x0F0F0F0Fu, n1 = (hi ? w1 >> 4 : w1) & 0x0F0F0F0Fu;
+    // bytes [n, 0x64] form the half 1024 + n; subtract 1024 (exact)
+    u32x4 v;
+    v.x = __builtin_amdgcn_perm(0x64646464u, n0, 0x07010600u);
+    v.y = __builtin_amdgcn_perm(0x64646464u, n0, 0x07030602u);
+    v.z = __builtin_amdgcn_perm(0x64646464u, n1, 0x07010600u);
+    v.w = __builtin_amdgcn_perm(0x64646464u, n1, 0x07030602u);
+    mq_h8 h = __builtin_bit_cast(mq_h8, v);
+    const mq_h8 bias = {1024.f16, 1024.f16, 1024.f16, 1024.f16, 1024.f16, 1024.f16, 1024.f16, 1024.f16};
+    return h - bias;
+}
+
+// Per KC-wide chunk of K: the chunk's weight loads (8 bytes per unit and
+// lane, the row headers) are issued first, then the x rows of the item's
+// pairs are staged (hi / lo halves, f32 sums per 32) while they travel; the
+// header lanes write (d1, m1) of every sub-block of their row to LDS once per
+// chunk.
+template <int KC>
+__global__ __launch_bounds__(WG) void mt_q4mfma_kernel(MtGemvArgs a) {
+#pragma clang fp contract(off)
+    constexpr int XP = KC + 8, NU = KC / 64, NS = KC / 256, NB = KC / 32;  // LDS row stride; units, super-blocks, sub-blocks
+    __shared__ __attribute__((aligned(16))) uint16_t xh[MM_PAIRS][XP];
+    __shared__ __attribute__((aligned(16))) uint16_t xl[MM_PAIRS][XP];
+    __shared__ float sx[MM_PAIRS][NB];
+    __shared__ __attribute__((aligned(16))) float scl[2][WG / WAVE][16][2 * NB];  // (d, m) per sub-block of a row
+    const int it = blockIdx.x;
+    if (it >= *a.nitems) return;
+    const int e = a.items[2 * it], tile = a.items[2 * it + 1] & 0xFFFF, slice = a.items[2 * it + 1] >> 16;
+    const int base = a.off[e] + slice * MM_PAIRS, n = min(MM_PAIRS, a.cnt[e] - slice * MM_PAIRS);
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE, i16 = lane & 15, g = lane >> 4;
+    const int row0 = tile * MM_ROWS + 16 * wave;
+    const bool active = row0 < a.rows;  // rows % 16 == 0
+    const int row = min(row0 + i16, a.rows - 1);
+    const DMat gm = sub_rows(a.m, e * a.rows, a.rows);
+    const DMat um = a.swiglu ? sub_rows(a.m2, e * a.rows, a.rows) : gm;
+    // a runtime count: with a constant 2 the compiler keeps twice the
+    // registers (300 VGPRs, one wave per SIMD)
+    const int nmat = a.swiglu ? 2 : 1;
+    const int U = a.K >> 6;
+    mm_f32x4 accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
+    for (int c0 = 0; c0 < a.K; c0 += KC) {
+        uint32_t qw[2][NU][2];
+        u32x4 hd[2][NS];
+        if (active) {
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++) {
+                if (mi >= nmat) break;
+                const DMat &m = mi ? um : gm;
+#pragma unroll
+                for (int k = 0; k < NU; k++) {
+                    const size_t ui = (size_t)row * U + c0 / 64 + k;
+                    const u32x2 q = *(const u32x2 *)(m.q + (g >> 1) * m.plane + ui * 16 + 8 * (g & 1));
+                    qw[mi][k][0] = q.x;
+                    qw[mi][k][1] = q.y;
+                }
+                if (g == 0) {
+#pragma unroll
+                    for (int k = 0; k < NS; k++)
+                        hd[mi][k] = *(const u32x4 *)(m.s + ((size_t)row * (m.cols >> 8) + c0 / 256 + k) * 16);
+                }
+            }
+        }
+        __syncthreads();  // the previous chunk's LDS reads are done
+        // x rows of the item's pairs, 8 elements per step: hi / lo halves and
+        // the f32 sum of each 32 (four consecutive threads, DPP)
+        for (int idx0 = 0; idx0 < n * (KC / 8); idx0 += WG) {
+            const int idx = idx0 + threadIdx.x, j = idx / (KC / 8), c8 = idx % (KC / 8);
+            float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            if (j < n) {
+                const float4 *xr = (const float4 *)(a.x + (size_t)(a.list[base + j] / a.xdiv) * a.K + c0 + 8 * c8);
+                const float4 p0 = xr[0], p1 = xr[1];
+                v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w;
+                v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
+            }
+            uint32_t hw[4], lw[4];
+            float s8 = 0.f;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const uint16_t h0 = f2h(v[2 * q]), h1 = f2h(v[2 * q + 1]);
+                const uint16_t l0 = f2h(v[2 * q] - h2f(h0)), l1 = f2h(v[2 * q + 1] - h2f(h1));
+                hw[q] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+                lw[q] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+                s8 += v[2 * q] + v[2 * q + 1];
+            }
+            s8 = dpp_sum4(s8);  // the 32 elements of one sub-block (c8 = 4 b .. 4 b + 3)
+            if (j < n) {
+                *(u32x4 *)&xh[j][8 * c8] = u32x4{hw[0], hw[1], hw[2], hw[3]};
+                *(u32x4 *)&xl[j][8 * c8] = u32x4{lw[0], lw[1], lw[2], lw[3]};
+                if ((c8 & 3) == 0) sx[j][c8 / 4] = s8;
+            }
+        }
+        if (active && g == 0) {  // (d1, m1) of every sub-block of this row in the chunk
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++) {
+                if (mi >= nmat) break;
+#pragma unroll
+                for (int k = 0; k < NS; k++) {
+                    const float d = h2f(hd[mi][k].x & 0xFFFFu), dmin = h2f(hd[mi][k].x >> 16);
+#pragma unroll
+                    for (int p = 0; p < 4; p++) {
+                        uint32_t sc0, m0, sc1, m1;
+                        q4k_scales(p, hd[mi][k].y, hd[mi][k].z, hd[mi][k].w, sc0, m0, sc1, m1);
+                        *(float4 *)&scl[mi][wave][i16][2 * (8 * k + 2 * p)] =
+                            make_float4(d * (float)sc0, dmin * (float)m0, d * (float)sc1, dmin * (float)m1);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        if (!active) continue;
+#pragma unroll
+        for (int k = 0; k < NU; k++) {
+#pragma unroll
+            for (int sb = 0; sb < 2; sb++) {
+                const int b = 2 * k + sb, kx = 32 * b + 8 * g;  // sub-block in the chunk; this lane's K positions
+                u32x4 bh = {0u, 0u, 0u, 0u}, bl = {0u, 0u, 0u, 0u};
+                float sxv = 0.f;
+                if (i16 < n) {
+                    bh = *(const u32x4 *)&xh[i16][kx];
+                    bl = *(const u32x4 *)&xl[i16][kx];
+                    sxv = sx[i16][b];
+                }
+                const mq_h8 Bh = __builtin_bit_cast(mq_h8, bh), Bl = __builtin_bit_cast(mq_h8, bl);
+#pragma unroll
+                for (int mi = 0; mi < 2; mi++) {
+                    if (mi >= nmat) break;
+                    const mq_h8 A = nibbles_h8(qw[mi][k][0], qw[mi][k][1], sb == 1);
+                    mm_f32x4 t = {0.f, 0.f, 0.f, 0.f};
+                    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bh, t, 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bl, t, 0, 0, 0);
+                    mm_f32x4 &acc = mi ? accu : accg;
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const float2 dm = *(const float2 *)&scl[mi][wave][4 * g + r][2 * b];
+                        acc[r] += dm.x * t[r] - dm.y * sxv;
+                    }
+                }
+            }
+        }
+    }
+    if (!active || i16 >= n) return;
+    const int p = a.list[base + i16];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        float v = accg[r];
+        if (a.swiglu) {
+            v *= 1.0f / (1.0f + expf(-v));
+            v *= accu[r];
+        }
+        a.y[(size_t)p * a.rows + row0 + 4 * g + r] = v;
+    }
+}
+
 bool mt_mfma_supported(const DMat &m, int32_t K, int32_t rows) {
     return (m.type == T_Q4_K || m.type == T_Q6_K || m.type == T_Q8_0) && m.cols == K && K % MM_KC == 0 &&
            rows % 16 == 0;
 }
 
-hipError_t launch_mt_mfma(const MtGemvArgs &a, int max_items, hipStream_t st) {
+hipError_t launch_mt_mfma(const MtGemvArgs &a, int max_items, hipStream_t st, bool f32_only) {
     if (!mt_mfma_supported(a.m, a.K, a.rows) || (a.swiglu && (!mt_mfma_supported(a.m2, a.K, a.rows) ||
                                                               a.m2.type != a.m.type)) ||
         a.tile_rows != MM_ROWS || a.pair_slice != MM_PAIRS || a.xdiv <= 0 || max_items <= 0 || a.dense_n > 0)
         return hipErrorInvalidValue;
-    if (a.K % 512 == 0) hipLaunchKernelGGL(mt_mfma_kernel<512>, dim3((unsigned)max_items), dim3(WG), 0, st, a);
-    else hipLaunchKernelGGL(mt_mfma_kernel<MM_KC>, dim3((unsigned)max_items), dim3(WG), 0, st, a);
+    if (a.m.type == T_Q4_K && !f32_only) {
+        const dim3 grid((unsigned)max_items);
+        hipLaunchKernelGGL(mt_q4mfma_kernel<MM_KC>, grid, dim3(WG), 0, st, a);  // 512: 256 VGPRs, slower
+    } else if (a.K % 512 == 0) {
+        hipLaunchKernelGGL(mt_mfma_kernel<512>, dim3((unsigned)max_items), dim3(WG), 0, st, a);
+    } else {
+        hipLaunchKernelGGL(mt_mfma_kernel<MM_KC>, dim3((unsigned)max_items), dim3(WG), 0, st, a);
+    }
     return hipGetLastError();
 }
 
 // Router softmax and top-k of every token of the chunk (grid T): the
 // selection of moe_topk_kernel (rank = the number of experts with a larger p,
 // or an equal p and a lower id), then the merged shared expert (id
-// n_experts, weight sigmoid of its gate logit) in slot top_k.
+// n_experts, weight sigmoid of its gate logit, the dot product of its gate
+// row with the token's normed x, computed here) in slot top_k.
 __global__ __launch_bounds__(WG) void pf_moe_topk_kernel(PfMoeArgs a) {
 #pragma clang fp contract(off)
     __shared__ float p[MOE_MAX_EXPERTS];
     __shared__ float red[WG / WAVE];
     __shared__ float sel[MOE_MAX_K];
     __shared__ int sid[MOE_MAX_K];
+    __shared__ float sgl;
     const int n = a.n_experts, t = threadIdx.x, lane = t & (WAVE - 1), wave = t / WAVE, tok = blockIdx.x;
+    if (a.kp > a.top_k) {  // the shared expert's gate logit: one unit per thread, then a block sum
+        const int U = a.sh_inp.cols >> 6;
+        float acc = 0.f;
+        for (int u = t; u < U; u += WG) {
+            float w[64];
+            decode_unit(a.sh_inp, 0, u, w);
+            const float *x = a.xn + (size_t)tok * a.sh_inp.cols;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const float4 *xr = (const float4 *)(x + unit_elem(a.sh_inp.type, u, 16 * k));
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float4 xv = xr[i];
+                    const float *wk = w + 16 * k + 4 * i;
+                    acc += wk[0] * xv.x + wk[1] * xv.y + wk[2] * xv.z + wk[3] * xv.w;
+                }
+            }
+        }
+        acc = wave_sum(acc);
+        if (lane == 0) red[wave] = acc;
+        __syncthreads();
+        if (t == 0) sgl = red[0] + red[1] + red[2] + red[3];
+        __syncthreads();
+    }
     const float *lg = a.logits + (size_t)tok * n;
     float mx = -INFINITY;
     for (int i = t; i < n; i += WG) mx = fmaxf(mx, lg[i]);
@@ -1023,7 +1227,7 @@ __global__ __launch_bounds__(WG) void pf_moe_topk_kernel(PfMoeArgs a) {
             w = a.norm_topk ? sel[t] / s : sel[t];
         } else {  // the shared expert
             id = n;
-            w = 1.0f / (1.0f + expf(-a.sgl[tok]));
+            w = 1.0f / (1.0f + expf(-sgl));
         }
         a.ids[(size_t)tok * a.kp + t] = id;
         a.w[(size_t)tok * a.kp + t] = w;
@@ -1112,7 +1316,9 @@ __global__ __launch_bounds__(WG) void pf_moe_combine_kernel(PfMoeArgs a) {
 hipError_t launch_pf_moe_route(const PfMoeArgs &a, hipStream_t st) {
     const int ne = a.n_experts + (a.kp > a.top_k ? 1 : 0);
     if (a.T <= 0 || a.n_experts <= 0 || ne > 1024 || a.top_k < 1 || a.top_k > MOE_MAX_K || a.top_k > a.n_experts ||
-        a.kp < a.top_k || a.kp > a.top_k + 1 || (a.kp > a.top_k && !a.sgl) || a.tiles_gu > 0xFFFF ||
+        a.kp < a.top_k || a.kp > a.top_k + 1 || (a.kp > a.top_k && (!a.xn || a.sh_inp.rows < 1 ||
+                                                                  a.sh_inp.cols % 64 || a.sh_inp.cols > 16384)) ||
+        a.tiles_gu > 0xFFFF ||
         a.tiles_dn > 0xFFFF || a.pair_slice <= 0 || (int64_t)a.T * a.kp / a.pair_slice >= 0x7FFF)
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(pf_moe_topk_kernel, dim3((unsigned)a.T), dim3(WG), 0, st, a);

@@ -263,14 +263,17 @@ constexpr int MT_PAIR_SLICE = 32;  // pairs per work item of the routed-expert p
 bool mt_gemv_supported(const DMat &m, int32_t K);
 int mt_gemv_tile_rows(int32_t K, int32_t rows);
 hipError_t launch_mt_gemv(const MtGemvArgs &a, int max_items, hipStream_t st);
-// the same on the matrix cores (f32 MFMA) for Q4_K / Q6_K / Q8_0 matrices with
-// K % 256 == 0 and rows % 16 == 0: items of 16 pairs x 64 rows
+// the same on the matrix cores for Q4_K / Q6_K / Q8_0 matrices with K % 256 ==
+// 0 and rows % 16 == 0: items of 16 pairs x 64 rows; Q4_K on f16 MFMA with the
+// weights exact (raw quants, scales per 32 in f32, x split hi + lo) unless
+// f32_only, the others (and f32_only) on f32 MFMA of the decoded weights
 constexpr int MT_MFMA_PAIRS = 16, MT_MFMA_ROWS = 64;
 bool mt_mfma_supported(const DMat &m, int32_t K, int32_t rows);
-hipError_t launch_mt_mfma(const MtGemvArgs &a, int max_items, hipStream_t st);
+hipError_t launch_mt_mfma(const MtGemvArgs &a, int max_items, hipStream_t st, bool f32_only = false);
 struct PfMoeArgs {
     const float *logits;           // [T][n_experts]
-    const float *sgl;              // [T] shared expert gate logits, or null
+    DMat sh_inp;                   // the shared expert's gate row (when kp > top_k)
+    const float *xn;               // [T][dim] the normed x (f32)
     int32_t *ids;                  // [T][kp] expert (n_experts = the merged shared expert)
     float *w;                      // [T][kp]
     int32_t *list, *off, *cnt, *fill;  // [T kp], [n_exp] x 3

@@ -154,13 +154,15 @@ def test_prefill_split_calls_agree(make_model):
 
 @pytest.mark.parametrize("shape", ["c5", "c4"])
 def test_prefill_expert_kernels_agree(tmp_path, monkeypatch, shape):
-    """The routed experts of a chunk on the matrix cores (f32 MFMA, the default
-    for Q4_K / Q6_K / Q8_0 experts) and on the multi-token GEMV
-    (OI_PREFILL_NO_MFMA=1): the same f32 arithmetic up to the order of the
-    sums.  One layer of the config 5 / config 4 shapes, so nothing staged in
-    f16 follows the experts (a later staged projection would turn a 1e-7
-    difference into ~1e-4 at its rounding boundaries): the last logits agree
-    within 1e-5."""
+    """The routed experts of a chunk on the three expert kernels: Q4_K quants
+    on f16 MFMA with the scales applied per 32 weights in f32 and x split
+    hi + lo (the default for Q4_K experts), the decoded weights on f32 MFMA
+    (OI_PREFILL_EXPERTS=f32, the default for Q6_K / Q8_0) and the
+    multi-token GEMV (OI_PREFILL_EXPERTS=gemv): the same f32 arithmetic up to
+    the order of the sums and x to ~2^-22.  One layer of the config 5 /
+    config 4 shapes, so nothing staged in f16 follows the experts (a later
+    staged projection would turn a 1e-7 difference into ~1e-4 at its rounding
+    boundaries): the last logits agree within 1e-5."""
     from oi import synth
     spec = (synth._hybrid(2048, 512, 1, 16, 2, 256, 4096, 4096, 64, 16, 32, 128, experts=512, used=10, eff=512,
                           shared=512, interval=2, seed=47) if shape == "c5" else
@@ -168,15 +170,16 @@ def test_prefill_expert_kernels_agree(tmp_path, monkeypatch, shape):
     path = tmp_path / ("%s.gguf" % shape)
     synth.write_gguf(path, spec)
     toks = _tokens(13, 200, 4096)
-    out = []
-    for off in ("0", "1"):
-        monkeypatch.setenv("OI_PREFILL_NO_MFMA", off)
+    out = {}
+    for kind in ("default", "f32", "gemv"):
+        monkeypatch.setenv("OI_PREFILL_EXPERTS", kind)
         e, ok = infer.engine_load(str(path), infer.Engine_Opts(max_ctx=256))
         assert ok
         try:
-            out.append(infer.engine_forward_batch(e, toks, 0).copy())
+            out[kind] = infer.engine_forward_batch(e, toks, 0).copy()
         finally:
             infer.engine_destroy(e)
-    err = scaled_err(out[0], out[1])
-    print("%s: MFMA vs multi-token GEMV experts %.3g" % (shape, err))
-    assert err <= 1e-5
+    for kind in ("f32", "gemv"):
+        err = scaled_err(out["default"], out[kind])
+        print("%s: default vs %s experts %.3g" % (shape, kind, err))
+        assert err <= 1e-5, kind
