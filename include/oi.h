@@ -314,6 +314,19 @@ int oi_deltanet_steps(const oi_deltanet_dims *d, int32_t n_tokens, const float *
                       const float *a, const float *conv_w, const float *a_decay, const float *dt_bias,
                       const float *norm_w, float *conv_state, float *rec_state, float *out);
 
+/* The same trajectory through the batched prefill kernels, all n_tokens at
+ * once: the conv over the whole trajectory, l2norm and gates per token, the
+ * delta rule token by token in one launch (chunk 0) or in its chunked form
+ * over chunks of 16 or 32 tokens (chunk 16 / 32; qwen3_5/metal.odin:416-468
+ * chunked_delta, which the reference builds but does not dispatch,
+ * metal.odin:1583-1586), the gated norm (metal.odin:1582-1618, the linear
+ * layer of forward_gpu_batch).  Host memory as oi_deltanet_steps; head dims
+ * 128, conv kernel 4, n_tokens >= conv_kernel - 1. */
+int oi_deltanet_steps_batched(const oi_deltanet_dims *d, int32_t n_tokens, int32_t chunk, const float *qkv,
+                              const float *z, const float *b, const float *a, const float *conv_w,
+                              const float *a_decay, const float *dt_bias, const float *norm_w, float *conv_state,
+                              float *rec_state, float *out);
+
 /* ------------------------------------------ Qwen3.5 full-attention step --- */
 
 /* Shape of a Qwen3.5 full-attention layer (qwen3_5/model.odin: n_heads,

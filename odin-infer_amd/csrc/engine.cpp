@@ -950,6 +950,8 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     e->pf_fused = !(pu && pu[0] == '1');
     const char *pm = std::getenv("OI_PREFILL_EXPERTS");  // "gemv" / "f32": the other expert kernels (tests)
     e->pf_experts = !pm ? 0 : std::strcmp(pm, "gemv") == 0 ? 1 : std::strcmp(pm, "f32") == 0 ? 2 : 0;
+    const char *pc = std::getenv("OI_PREFILL_DN_CHUNK");  // "16" / "32": the chunked delta rule in prefill
+    e->pf_dn_chunk = !pc ? 0 : std::strcmp(pc, "16") == 0 ? 16 : std::strcmp(pc, "32") == 0 ? 32 : 0;
 
     std::printf("model: %s dim=%lld layers=%lld (attention %d, linear %d) heads=%lld/%lld hidden=%lld vocab=%lld "
                 "ctx=%lld/%lld experts=%lld/%lld  weights=%.0f MB  KV cache (f16)=%.0f MB  [gfx950]\n",
@@ -1078,7 +1080,7 @@ int prefill_alloc(oi_engine *e) {
     }
     std::vector<size_t> sizes = {T * 4, T * D * 4, T * QD * 4 * 2, xb, need[0], need[1], need[2], need[3],
                                  full ? T * QD * 4 : 0,
-                                 lin ? T * CD * 4 : 0, lin ? T * 2 * KD * 4 : 0, lin ? T * 2 * (size_t)e->lin_nv * 4 : 0,
+                                 lin ? T * CD * 4 : 0, lin ? T * 2 * KD * 4 : 0, lin ? T * 3 * (size_t)e->lin_nv * 4 : 0,
                                  lin ? T * VD * 4 : 0,
                                  moe ? T * D * 4 : 0, moe ? T * (size_t)e->n_experts * 4 : 0,
                                  moe ? T * KP * 4 : 0, moe ? T * KP * EF * 4 : 0, moe ? T * KP * D * 4 : 0,
@@ -1252,6 +1254,7 @@ int prefill_chunk(oi_engine *e, const int32_t *tokens, int T, int pos) {
             da.T = T;
             da.n_kh = (int32_t)e->lin_nk; da.n_vh = (int32_t)e->lin_nv;
             da.hk = (int32_t)e->lin_hk; da.hv = (int32_t)e->lin_hv; da.kernel = (int32_t)e->lin_kernel;
+            da.chunk = e->pf_dn_chunk;
             HIP_TRY(launch_pf_deltanet(da, st));
             HIP_TRY(launch_gemm_parts(L.ssm_out, e->pf_xb, T, P[0], PB[0], &s0, st));
         }
@@ -1762,6 +1765,58 @@ int oi_deltanet_steps(const oi_deltanet_dims *d, int32_t n_tokens, const float *
     hipFree(dev);
     if (rc) return rc;
     if (r != hipSuccess) return fail(OI_E_DEVICE, std::string("deltanet: ") + hipGetErrorString(r));
+    return OI_OK;
+}
+
+int oi_deltanet_steps_batched(const oi_deltanet_dims *d, int32_t n_tokens, int32_t chunk, const float *qkv,
+                              const float *z, const float *b, const float *a, const float *conv_w,
+                              const float *a_decay, const float *dt_bias, const float *norm_w, float *conv_state,
+                              float *rec_state, float *out) {
+    if (!dn_dims_ok(d) || !pf_dn_supported(d->head_k_dim, d->head_v_dim, d->conv_kernel))
+        return fail(OI_E_ARG, "deltanet batched: head dims 128, conv kernel 4, n_v_heads a multiple of n_k_heads");
+    if (chunk != 0 && chunk != 16 && chunk != 32) return fail(OI_E_ARG, "deltanet batched: chunk must be 0, 16 or 32");
+    if (n_tokens < d->conv_kernel - 1 || !qkv || !z || !b || !a || !conv_w || !a_decay || !dt_bias || !norm_w ||
+        !conv_state || !rec_state || !out)
+        return fail(OI_E_ARG, "deltanet batched: bad argument (n_tokens must be at least conv_kernel - 1)");
+    const size_t n = (size_t)n_tokens, nvh = (size_t)d->n_v_heads, kd = (size_t)d->n_k_heads * d->head_k_dim;
+    const size_t vd = nvh * d->head_v_dim, cd = 2 * kd + vd, km1 = (size_t)d->conv_kernel - 1;
+    const size_t st_n = nvh * d->head_k_dim * d->head_v_dim;
+    // inputs, parameters, states, then the kernels' scratch (conv out, q/k, gates, o) and out
+    const size_t in_f[] = {n * cd, n * vd, n * nvh, n * nvh, cd * d->conv_kernel, nvh, nvh, (size_t)d->head_v_dim,
+                           cd * km1, st_n};
+    const float *in_p[] = {qkv, z, b, a, conv_w, a_decay, dt_bias, norm_w, conv_state, rec_state};
+    size_t floats = n * cd + n * 2 * kd + n * 3 * nvh + n * vd + n * vd;
+    for (size_t x : in_f) floats += x;
+    float *dev = nullptr;
+    HIP_TRY(hipMalloc(&dev, floats * 4));
+    float *dp[10], *p = dev;
+    hipError_t r = hipSuccess;
+    for (int i = 0; i < 10; i++) {
+        dp[i] = p;
+        p += in_f[i];
+        if (r == hipSuccess) r = hipMemcpy(dp[i], in_p[i], in_f[i] * 4, hipMemcpyHostToDevice);
+    }
+    PfDnArgs da{};
+    da.qkv = dp[0]; da.z = dp[1]; da.b = dp[2]; da.a = dp[3];
+    da.qkvs = da.zs = da.bs = da.as = 1;
+    da.conv_w = dp[4]; da.a_decay = dp[5]; da.dt_bias = dp[6]; da.norm_w = dp[7];
+    da.eps = d->eps;
+    da.conv_state = dp[8]; da.state = dp[9];
+    da.conv_out = p; p += n * cd;
+    da.qk = p; p += n * 2 * kd;
+    da.gates = p; p += n * 3 * nvh;
+    da.o = p; p += n * vd;
+    da.out32 = p;
+    da.T = n_tokens;
+    da.n_kh = d->n_k_heads; da.n_vh = d->n_v_heads;
+    da.hk = d->head_k_dim; da.hv = d->head_v_dim; da.kernel = d->conv_kernel;
+    da.chunk = chunk;
+    if (r == hipSuccess) r = launch_pf_deltanet(da, nullptr);
+    if (r == hipSuccess) r = hipMemcpy(out, da.out32, n * vd * 4, hipMemcpyDeviceToHost);
+    if (r == hipSuccess) r = hipMemcpy(conv_state, dp[8], cd * km1 * 4, hipMemcpyDeviceToHost);
+    if (r == hipSuccess) r = hipMemcpy(rec_state, dp[9], st_n * 4, hipMemcpyDeviceToHost);
+    hipFree(dev);
+    if (r != hipSuccess) return fail(OI_E_DEVICE, std::string("deltanet batched: ") + hipGetErrorString(r));
     return OI_OK;
 }
 

@@ -238,10 +238,12 @@ struct PfDnArgs {
     float *state;                  // [n_vh][hk][hv]
     float *conv_out;               // scratch [T][conv_dim]
     float *qk;                     // scratch [T][2 n_kh hk]: normalized q (scaled), k
-    float *gates;                  // scratch [T][2 n_vh]: beta, decay
+    float *gates;                  // scratch [T][3 n_vh]: beta, decay, log decay
     float *o;                      // scratch [T][n_vh hv]: delta-rule outputs
     uint16_t *out16;               // [T][n_vh hv]: gated-normed, f16 (the output projection's input)
+    float *out32;                  // or, when set, the same in f32
     int32_t T, n_kh, n_vh, hk, hv, kernel;
+    int32_t chunk;                 // 0: the delta rule token by token; 16 / 32: its chunked form
 };
 bool pf_dn_supported(int hk, int hv, int kernel);
 hipError_t launch_pf_deltanet(const PfDnArgs &a, hipStream_t st);

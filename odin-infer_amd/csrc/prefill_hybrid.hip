@@ -16,10 +16,14 @@
 //   pf_dn_conv_state_kernel the conv state after the chunk (its last inputs)
 //   pf_dn_prep_kernel       per token: l2norm of q (times 1/sqrt(head_k_dim))
 //                           and k, beta = sigmoid(b), decay = exp(ssm_a
-//                           softplus(a + dt_bias))
+//                           softplus(a + dt_bias)) and its log
 //   pf_dn_delta_kernel      the delta rule over the chunk's tokens in order,
 //                           the state held in registers for the whole chunk
+//   pf_dn_chunk_kernel      the same in its chunked form (metal.odin:416-468,
+//                           which the reference does not dispatch): 16 or 32
+//                           tokens per step, decay ratios from log sums
 //   pf_dn_gnorm_kernel      gated RMSNorm, f16 rows for the output projection
+//                           (or f32 rows for the host-memory entry point)
 //
 // Layouts: token-major; partial products [split][T][rows]; the conv state
 // [conv_dim][kernel - 1] oldest first and the recurrent state [n_vh][hk][hv]
@@ -155,7 +159,7 @@ __global__ __launch_bounds__(WG) void pf_dn_conv_state_kernel(PfDnArgs a) {
 // Per token (grid T): l2norm of each k head's q and k (ops.odin:27-37, eps
 // 1e-6 a floor on the norm; q also times 1/sqrt(head_k_dim),
 // forward.odin:187-192) into qk [T][2 key_dim] (q heads, then k heads); the
-// gates of every value head into gates [T][2 n_vh] (beta, then decay).
+// gates of every value head into gates [T][3 n_vh] (beta, decay, log decay).
 template <int HK>
 __global__ __launch_bounds__(WG) void pf_dn_prep_kernel(PfDnArgs a) {
 #pragma clang fp contract(off)
@@ -185,8 +189,10 @@ __global__ __launch_bounds__(WG) void pf_dn_prep_kernel(PfDnArgs a) {
     for (int vh = threadIdx.x; vh < a.n_vh; vh += WG) {
         const size_t slice = (size_t)a.T * a.n_vh, i = (size_t)t * a.n_vh + vh;
         const float b = parts_at(a.b, a.bs, slice, i), av = parts_at(a.a, a.as, slice, i);
-        a.gates[(size_t)t * 2 * a.n_vh + vh] = sigmoid_ref(b);
-        a.gates[(size_t)t * 2 * a.n_vh + a.n_vh + vh] = expf(a.a_decay[vh] * softplus_ref(av + a.dt_bias[vh]));
+        const float lg = a.a_decay[vh] * softplus_ref(av + a.dt_bias[vh]);  // log of the decay
+        a.gates[(size_t)t * 3 * a.n_vh + vh] = sigmoid_ref(b);
+        a.gates[(size_t)t * 3 * a.n_vh + a.n_vh + vh] = expf(lg);
+        a.gates[(size_t)t * 3 * a.n_vh + 2 * a.n_vh + vh] = lg;
     }
 }
 
@@ -230,7 +236,7 @@ __global__ __launch_bounds__(WG) void pf_dn_delta_kernel(PfDnArgs a) {
         }
         if (threadIdx.x < 2 * nb) {
             const int tt = threadIdx.x / 2, g = threadIdx.x % 2;
-            sg[tt][g] = a.gates[(size_t)(tb + tt) * 2 * a.n_vh + g * a.n_vh + vh];
+            sg[tt][g] = a.gates[(size_t)(tb + tt) * 3 * a.n_vh + g * a.n_vh + vh];
         }
         __syncthreads();
         for (int tt = 0; tt < nb; tt++) {
@@ -269,6 +275,126 @@ __global__ __launch_bounds__(WG) void pf_dn_delta_kernel(PfDnArgs a) {
     for (int r = 0; r < RPL; r++) S[(size_t)(i0 + r) * HV + j] = s[r];
 }
 
+// The chunked form of the delta rule (the math of the reference's
+// chunked_delta, qwen3_5/metal.odin:416-468): per chunk of C tokens, with the
+// chunk's entry state S fixed, c[t] = sum of the log decays up to t,
+//   d_t = beta_t v_t - beta_t e^{c[t]} S^T k_t - sum_{i<t} beta_t e^{c[t]-c[i]} (k_t.k_i) d_i
+//   o_t = e^{c[t]} S^T q_t + sum_{i<=t} e^{c[t]-c[i]} (q_t.k_i) d_i
+//   S'  = e^{c[C-1]} S + sum_i e^{c[C-1]-c[i]} k_i d_i^T.
+// The decay ratios are differences of log sums (the reference divides
+// running products, which gives 0/0 once a chunk's product underflows).
+// Same grid and lane layout as pf_dn_delta_kernel: S^T k_t and S^T q_t of
+// all the chunk's tokens are independent products (DPP sums over the 8 row
+// groups), the substitution runs in one lane per column, the state update is
+// one rank-C product per lane.
+template <int HK, int HV, int C>
+__global__ __launch_bounds__(WG) void pf_dn_chunk_kernel(PfDnArgs a) {
+#pragma clang fp contract(off)
+    constexpr int RG = 8, RPL = HK / RG;
+    static_assert(RPL == 16 && HV % 32 == 0, "head shape");
+    __shared__ __attribute__((aligned(16))) float sq[C][HK];
+    __shared__ __attribute__((aligned(16))) float sk[C][HK];
+    __shared__ float sv[C][32];
+    __shared__ float sbeta[C], slc[C];
+    __shared__ float lm[C][C + 1], om[C][C + 1];  // beta_t e^{c[t]-c[i]} k_t.k_i (i < t); e^{c[t]-c[i]} q_t.k_i (i <= t)
+    __shared__ float sik[32][C], siq[32][C], dd[32][C];
+    const int vh = blockIdx.x, kh = vh % a.n_kh, c0 = (int)blockIdx.y * 32;
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    const int cl = wave * 8 + (lane >> 3), rg = lane & 7, j = c0 + cl, i0 = rg * RPL;
+    const int KD = a.n_kh * HK, CD = 2 * KD + a.n_vh * HV, VD = a.n_vh * HV;
+    float *S = a.state + (size_t)vh * HK * HV;
+    float s[RPL];
+#pragma unroll
+    for (int r = 0; r < RPL; r++) s[r] = S[(size_t)(i0 + r) * HV + j];
+    for (int tb = 0; tb < a.T; tb += C) {
+        const int nb = min(C, a.T - tb);
+        __syncthreads();  // the previous chunk's LDS reads are done
+        for (int idx = threadIdx.x; idx < nb * 2 * HK; idx += WG) {
+            const int tt = idx / (2 * HK), e = idx % (2 * HK), ee = e % HK;
+            const float val = a.qk[(size_t)(tb + tt) * 2 * KD + (e < HK ? 0 : KD) + kh * HK + ee];
+            (e < HK ? sq : sk)[tt][ee] = val;
+        }
+        for (int idx = threadIdx.x; idx < nb * 32; idx += WG) {
+            const int tt = idx / 32, cc = idx % 32;
+            sv[tt][cc] = a.conv_out[(size_t)(tb + tt) * CD + 2 * KD + vh * HV + c0 + cc];
+        }
+        if (threadIdx.x < nb) {  // beta, and the running sum of the log decays
+            const int t = threadIdx.x;
+            sbeta[t] = a.gates[(size_t)(tb + t) * 3 * a.n_vh + vh];
+            float c = 0.f;
+            for (int i = 0; i <= t; i++) c += a.gates[(size_t)(tb + i) * 3 * a.n_vh + 2 * a.n_vh + vh];
+            slc[t] = c;
+        }
+        __syncthreads();
+        for (int idx = threadIdx.x; idx < nb * nb; idx += WG) {  // the chunk's k.k and q.k products
+            const int t = idx / nb, i = idx % nb;
+            float dk = 0.f, dq = 0.f;
+            if (i <= t) {
+                const float4 *ki = (const float4 *)sk[i], *kt = (const float4 *)sk[t], *qt = (const float4 *)sq[t];
+                for (int c4 = 0; c4 < HK / 4; c4++) {
+                    const float4 x = ki[c4], y = kt[c4], z = qt[c4];
+                    dk += x.x * y.x + x.y * y.y + x.z * y.z + x.w * y.w;
+                    dq += x.x * z.x + x.y * z.y + x.z * z.z + x.w * z.w;
+                }
+            }
+            const float ratio = i < t ? expf(slc[t] - slc[i]) : 1.0f;
+            lm[t][i] = i < t ? sbeta[t] * ratio * dk : 0.f;
+            om[t][i] = i <= t ? ratio * dq : 0.f;
+        }
+        // S^T k_t and S^T q_t of every token of the chunk (S the entry state)
+        for (int t = 0; t < nb; t++) {
+            const float4 *k4 = (const float4 *)&sk[t][i0], *q4 = (const float4 *)&sq[t][i0];
+            float pk = 0.f, pq = 0.f;
+#pragma unroll
+            for (int c4 = 0; c4 < RPL / 4; c4++) {
+                const float4 kk = k4[c4], qq = q4[c4];
+                pk += s[4 * c4] * kk.x + s[4 * c4 + 1] * kk.y + s[4 * c4 + 2] * kk.z + s[4 * c4 + 3] * kk.w;
+                pq += s[4 * c4] * qq.x + s[4 * c4 + 1] * qq.y + s[4 * c4 + 2] * qq.z + s[4 * c4 + 3] * qq.w;
+            }
+            pk += OI_DPP(pk, 0xB1);
+            pk += OI_DPP(pk, 0x4E);
+            pk += dpp_mirror8(pk);
+            pq += OI_DPP(pq, 0xB1);
+            pq += OI_DPP(pq, 0x4E);
+            pq += dpp_mirror8(pq);
+            if (rg == 0) {
+                sik[cl][t] = pk;
+                siq[cl][t] = pq;
+            }
+        }
+        __syncthreads();
+        if (rg == 0) {  // forward substitution and the outputs, one lane per column
+            for (int t = 0; t < nb; t++) {
+                const float ec = expf(slc[t]);
+                float d = sbeta[t] * sv[t][cl] - sbeta[t] * ec * sik[cl][t];
+                for (int i = 0; i < t; i++) d -= lm[t][i] * dd[cl][i];
+                dd[cl][t] = d;
+                float o = ec * siq[cl][t];
+                for (int i = 0; i <= t; i++) o += om[t][i] * dd[cl][i];
+                a.o[(size_t)(tb + t) * VD + vh * HV + j] = o;
+            }
+        }
+        __syncthreads();
+        const float lcC = slc[nb - 1], ecC = expf(lcC);
+#pragma unroll
+        for (int r = 0; r < RPL; r++) s[r] *= ecC;
+        for (int i = 0; i < nb; i++) {
+            const float f = expf(lcC - slc[i]), di = dd[cl][i];
+            const float4 *k4 = (const float4 *)&sk[i][i0];
+#pragma unroll
+            for (int c4 = 0; c4 < RPL / 4; c4++) {
+                const float4 kk = k4[c4];
+                s[4 * c4] += (f * kk.x) * di;
+                s[4 * c4 + 1] += (f * kk.y) * di;
+                s[4 * c4 + 2] += (f * kk.z) * di;
+                s[4 * c4 + 3] += (f * kk.w) * di;
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RPL; r++) S[(size_t)(i0 + r) * HV + j] = s[r];
+}
+
 // gated RMSNorm (forward.odin:211-218): per token (grid T) and value head,
 // out = f16(norm_w[j] (inv o[j]) silu(z[j])), inv = 1 / sqrt(sum o^2 / hv +
 // eps); z from the in_z projection's partial products
@@ -291,7 +417,9 @@ __global__ __launch_bounds__(WG) void pf_dn_gnorm_kernel(PfDnArgs a) {
         for (int e = 0; e < E; e++) {
             const int j = lane + WAVE * e;
             const float z = parts_at(a.z, a.zs, (size_t)a.T * VD, (size_t)t * VD + vh * HV + j);
-            a.out16[(size_t)t * VD + vh * HV + j] = f2h(a.norm_w[j] * (inv * o[e]) * silu_ref(z));
+            const float v = a.norm_w[j] * (inv * o[e]) * silu_ref(z);
+            if (a.out32) a.out32[(size_t)t * VD + vh * HV + j] = v;
+            else a.out16[(size_t)t * VD + vh * HV + j] = f2h(v);
         }
     }
 }
@@ -310,13 +438,17 @@ hipError_t launch_pf_q35_qkv(const PfQ35Args &a, int head_dim, hipStream_t st) {
 bool pf_dn_supported(int hk, int hv, int kernel) { return hk == 128 && hv == 128 && kernel == 4; }
 
 hipError_t launch_pf_deltanet(const PfDnArgs &a, hipStream_t st) {
-    if (!pf_dn_supported(a.hk, a.hv, a.kernel) || a.T < a.kernel - 1 || a.n_kh <= 0 || a.n_vh % a.n_kh)
+    if (!pf_dn_supported(a.hk, a.hv, a.kernel) || a.T < a.kernel - 1 || a.n_kh <= 0 || a.n_vh % a.n_kh ||
+        (a.chunk != 0 && a.chunk != 16 && a.chunk != 32))
         return hipErrorInvalidValue;
     const int CD = 2 * a.n_kh * a.hk + a.n_vh * a.hv;
     hipLaunchKernelGGL(pf_dn_conv_kernel<4>, dim3(nblk(CD, WG), nblk(a.T, DN_TT)), dim3(WG), 0, st, a);
     hipLaunchKernelGGL(pf_dn_conv_state_kernel<4>, dim3(nblk(CD, WG)), dim3(WG), 0, st, a);
     hipLaunchKernelGGL(pf_dn_prep_kernel<128>, dim3((unsigned)a.T), dim3(WG), 0, st, a);
-    hipLaunchKernelGGL((pf_dn_delta_kernel<128, 128>), dim3((unsigned)a.n_vh, 128 / 32), dim3(WG), 0, st, a);
+    const dim3 dgrid((unsigned)a.n_vh, 128 / 32);
+    if (a.chunk == 16) hipLaunchKernelGGL((pf_dn_chunk_kernel<128, 128, 16>), dgrid, dim3(WG), 0, st, a);
+    else if (a.chunk == 32) hipLaunchKernelGGL((pf_dn_chunk_kernel<128, 128, 32>), dgrid, dim3(WG), 0, st, a);
+    else hipLaunchKernelGGL((pf_dn_delta_kernel<128, 128>), dgrid, dim3(WG), 0, st, a);
     hipLaunchKernelGGL(pf_dn_gnorm_kernel<128>, dim3((unsigned)a.T), dim3(WG), 0, st, a);
     return hipGetLastError();
 }

@@ -82,6 +82,7 @@ HIP_SYMBOLS = {
     "oi_gemm": (c_i32, [c_i32, c_vp, c_i64, c_i64, c_vp, c_i32, c_vp]),
     "oi_deltanet_step_launch": (c_i32, [c_vp] * 13 + [c_vp]),
     "oi_deltanet_steps": (c_i32, [c_vp, c_i32] + [c_vp] * 11),
+    "oi_deltanet_steps_batched": (c_i32, [c_vp, c_i32, c_i32] + [c_vp] * 11),
     "oi_qwen35_attn_workspace_bytes": (c_i64, [c_vp]),
     "oi_qwen35_attn_step_launch": (c_i32, [c_vp, c_i32] + [c_vp] * 11),
     "oi_qwen35_attn_steps": (c_i32, [c_vp, c_i32, c_i32] + [c_vp] * 9),

@@ -30,6 +30,25 @@ def deltanet_steps(n_k_heads, n_v_heads, head_k_dim, head_v_dim, conv_kernel, ep
     return out, cs, rs
 
 
+def deltanet_steps_batched(n_k_heads, n_v_heads, head_k_dim, head_v_dim, conv_kernel, eps, chunk, qkv, z, b, a,
+                           conv_w, a_decay, dt_bias, norm_w, conv_state, rec_state):
+    """The same trajectory through oi_deltanet_steps_batched, the batched
+    prefill kernels: the delta rule token by token (chunk 0) or in its
+    chunked form over chunks of 16 / 32 tokens.  Returns (out, conv_state,
+    rec_state) as deltanet_steps."""
+    d = _native.DeltaNetDims(n_k_heads, n_v_heads, head_k_dim, head_v_dim, conv_kernel, eps)
+    qkv, z, b, a = _f32(np.atleast_2d(qkv)), _f32(np.atleast_2d(z)), _f32(np.atleast_2d(b)), _f32(np.atleast_2d(a))
+    conv_w, a_decay, dt_bias, norm_w = _f32(conv_w), _f32(a_decay), _f32(dt_bias), _f32(norm_w)
+    cs, rs = _f32(conv_state).copy(), _f32(rec_state).copy()
+    T = qkv.shape[0]
+    out = np.empty((T, n_v_heads * head_v_dim), np.float32)
+    p = lambda x: x.ctypes.data
+    check(_native.hip().oi_deltanet_steps_batched(ctypes.byref(d), T, int(chunk), p(qkv), p(z), p(b), p(a),
+                                                  p(conv_w), p(a_decay), p(dt_bias), p(norm_w), p(cs), p(rs),
+                                                  p(out)))
+    return out, cs, rs
+
+
 def attn_steps(n_heads, n_kv_heads, head_dim, rotary_dim, seq_len, eps, pos0, qproj, k, v, q_norm, k_norm, inv_freq,
                k_cache16, v_cache16):
     """Run len(qproj) tokens from pos0 through oi_qwen35_attn_steps.  qproj

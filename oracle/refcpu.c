@@ -1819,6 +1819,140 @@ EXPORT int ref_deltanet_steps(int n_kh, int n_vh, int hk, int hv, int kernel, fl
     return 0;
 }
 
+/* The chunked form of the delta rule for one value head and one chunk of C
+ * tokens (qwen3_5/metal.odin:416-468 chunked_delta, the math of
+ * delta_harness/delta_ref.odin:186-283): with cp[t] = g[0]..g[t] (the decays'
+ * running product) and the chunk's state S at entry,
+ *   d_t = beta_t v_t - beta_t cp[t] S^T k_t - sum_{i<t} beta_t (cp[t]/cp[i]) (k_t.k_i) d_i
+ *   o_t = cp[t] S^T q_t + sum_{i<=t} (cp[t]/cp[i]) (q_t.k_i) d_i      (the i = t factor 1)
+ *   S'  = cp[C-1] S + sum_i (cp[C-1]/cp[i]) k_i d_i^T
+ * which equals C tokenwise steps (S *= g; d = (v - S^T k) beta; S += k d^T;
+ * o = S^T q) up to rounding.  q, k [C][hk]; v, out [C][hv]; state [hk][hv]. */
+EXPORT void ref_delta_chunk(float *out, float *state, const float *q, const float *k, const float *v,
+                            const float *beta, const float *g, int C, int hk, int hv) {
+    if (C <= 0 || hk <= 0 || hv <= 0) return;
+    float *cp = malloc((size_t)C * sizeof(float));
+    float *kkt = malloc((size_t)C * C * sizeof(float)), *kqt = malloc((size_t)C * C * sizeof(float));
+    float *s0k = malloc((size_t)C * hv * sizeof(float)), *s0q = malloc((size_t)C * hv * sizeof(float));
+    float *d = malloc((size_t)C * hv * sizeof(float));
+    float acc = 1.0f;
+    for (int t = 0; t < C; t++) {
+        acc *= g[t];
+        cp[t] = acc;
+    }
+    for (int t = 0; t < C; t++)
+        for (int i = 0; i < C; i++) {
+            float dk = 0.0f, dq = 0.0f;
+            for (int a = 0; a < hk; a++) {
+                dk += k[(int64_t)i * hk + a] * k[(int64_t)t * hk + a];
+                dq += k[(int64_t)i * hk + a] * q[(int64_t)t * hk + a];
+            }
+            kkt[t * C + i] = dk;
+            kqt[t * C + i] = dq;
+        }
+    for (int t = 0; t < C; t++)
+        for (int j = 0; j < hv; j++) {
+            float sk = 0.0f, sq = 0.0f;
+            for (int a = 0; a < hk; a++) {
+                sk += state[(int64_t)a * hv + j] * k[(int64_t)t * hk + a];
+                sq += state[(int64_t)a * hv + j] * q[(int64_t)t * hk + a];
+            }
+            s0k[(int64_t)t * hv + j] = sk;
+            s0q[(int64_t)t * hv + j] = sq;
+        }
+    for (int t = 0; t < C; t++)
+        for (int j = 0; j < hv; j++)
+            d[(int64_t)t * hv + j] = beta[t] * v[(int64_t)t * hv + j] - beta[t] * cp[t] * s0k[(int64_t)t * hv + j];
+    for (int t = 0; t < C; t++)
+        for (int i = 0; i < t; i++) {
+            float L = beta[t] * (cp[t] / cp[i]) * kkt[t * C + i];
+            for (int j = 0; j < hv; j++) d[(int64_t)t * hv + j] -= L * d[(int64_t)i * hv + j];
+        }
+    for (int t = 0; t < C; t++) {
+        float *o = out + (int64_t)t * hv;
+        for (int j = 0; j < hv; j++) o[j] = cp[t] * s0q[(int64_t)t * hv + j];
+        for (int i = 0; i <= t; i++) {
+            float w = (i < t ? cp[t] / cp[i] : 1.0f) * kqt[t * C + i];
+            for (int j = 0; j < hv; j++) o[j] += w * d[(int64_t)i * hv + j];
+        }
+    }
+    float cpC = cp[C - 1];
+    for (int64_t x = 0; x < (int64_t)hk * hv; x++) state[x] *= cpC;
+    for (int i = 0; i < C; i++) {
+        float f = cp[C - 1] / cp[i];
+        for (int a = 0; a < hk; a++) {
+            float ka = f * k[(int64_t)i * hk + a];
+            for (int j = 0; j < hv; j++) state[(int64_t)a * hv + j] += ka * d[(int64_t)i * hv + j];
+        }
+    }
+    free(cp); free(kkt); free(kqt); free(s0k); free(s0q); free(d);
+}
+
+/* ref_deltanet_steps with the delta rule in chunks of `chunk` tokens (the last
+ * chunk may be shorter): per token the conv, l2norm and gates as the tokenwise
+ * form, per chunk and value head ref_delta_chunk, then per token the gated
+ * RMSNorm. */
+EXPORT int ref_deltanet_steps_chunked(int n_kh, int n_vh, int hk, int hv, int kernel, float eps, int n_tokens,
+                                      int chunk, const float *qkv, const float *z, const float *b, const float *a,
+                                      const float *conv_w, const float *a_decay, const float *dt_bias,
+                                      const float *norm_w, float *conv_state, float *rec_state, float *out) {
+    if (n_kh <= 0 || n_vh <= 0 || hk <= 0 || hv <= 0 || kernel < 1 || n_tokens <= 0 || chunk <= 0) {
+        snprintf(g_err, sizeof g_err, "deltanet: bad dims");
+        return -1;
+    }
+    int64_t key_dim = (int64_t)n_kh * hk, value_dim = (int64_t)n_vh * hv, conv_dim = 2 * key_dim + value_dim;
+    float scale = 1.0f / sqrtf((float)hk);
+    float *co = malloc((size_t)conv_dim * sizeof(float));
+    float *ql = malloc((size_t)chunk * key_dim * sizeof(float)), *kl = malloc((size_t)chunk * key_dim * sizeof(float));
+    float *vv = malloc((size_t)chunk * value_dim * sizeof(float));
+    float *bt = malloc((size_t)chunk * n_vh * sizeof(float)), *gt = malloc((size_t)chunk * n_vh * sizeof(float));
+    float *qh = malloc((size_t)chunk * hk * sizeof(float)), *kh_ = malloc((size_t)chunk * hk * sizeof(float));
+    float *vh_ = malloc((size_t)chunk * hv * sizeof(float)), *oh = malloc((size_t)chunk * hv * sizeof(float));
+    float *bh = malloc((size_t)chunk * sizeof(float)), *gh = malloc((size_t)chunk * sizeof(float));
+    for (int t0 = 0; t0 < n_tokens; t0 += chunk) {
+        int C = n_tokens - t0 < chunk ? n_tokens - t0 : chunk;
+        for (int c = 0; c < C; c++) {
+            int t = t0 + c;
+            ref_conv1d_step(co, qkv + (int64_t)t * conv_dim, conv_state, conv_w, conv_dim, kernel);
+            for (int kh = 0; kh < n_kh; kh++) {
+                float *qd = ql + (int64_t)c * key_dim + (int64_t)kh * hk, *kd = kl + (int64_t)c * key_dim + (int64_t)kh * hk;
+                ref_l2norm(qd, co + (int64_t)kh * hk, hk, 1e-6f);
+                ref_l2norm(kd, co + key_dim + (int64_t)kh * hk, hk, 1e-6f);
+                for (int i = 0; i < hk; i++) qd[i] *= scale;
+            }
+            memcpy(vv + (int64_t)c * value_dim, co + 2 * key_dim, (size_t)value_dim * sizeof(float));
+            for (int vh = 0; vh < n_vh; vh++) {
+                bt[c * n_vh + vh] = ref_sigmoid(b[(int64_t)t * n_vh + vh]);
+                gt[c * n_vh + vh] = expf(a_decay[vh] * ref_softplus(a[(int64_t)t * n_vh + vh] + dt_bias[vh]));
+            }
+        }
+        for (int vh = 0; vh < n_vh; vh++) {
+            int kh = vh % n_kh;
+            for (int c = 0; c < C; c++) {
+                memcpy(qh + (int64_t)c * hk, ql + (int64_t)c * key_dim + (int64_t)kh * hk, (size_t)hk * sizeof(float));
+                memcpy(kh_ + (int64_t)c * hk, kl + (int64_t)c * key_dim + (int64_t)kh * hk, (size_t)hk * sizeof(float));
+                memcpy(vh_ + (int64_t)c * hv, vv + (int64_t)c * value_dim + (int64_t)vh * hv, (size_t)hv * sizeof(float));
+                bh[c] = bt[c * n_vh + vh];
+                gh[c] = gt[c * n_vh + vh];
+            }
+            ref_delta_chunk(oh, rec_state + (int64_t)vh * hk * hv, qh, kh_, vh_, bh, gh, C, hk, hv);
+            for (int c = 0; c < C; c++)
+                memcpy(out + (int64_t)(t0 + c) * value_dim + (int64_t)vh * hv, oh + (int64_t)c * hv,
+                       (size_t)hv * sizeof(float));
+        }
+        for (int c = 0; c < C; c++)
+            for (int vh = 0; vh < n_vh; vh++) {
+                float *o = out + (int64_t)(t0 + c) * value_dim + (int64_t)vh * hv;
+                const float *zh = z + (int64_t)(t0 + c) * value_dim + (int64_t)vh * hv;
+                ref_rmsnorm(o, o, norm_w, hv, eps);
+                for (int i = 0; i < hv; i++) o[i] *= ref_silu(zh[i]);
+            }
+    }
+    free(co); free(ql); free(kl); free(vv); free(bt); free(gt);
+    free(qh); free(kh_); free(vh_); free(oh); free(bh); free(gh);
+    return 0;
+}
+
 /* ---------------------------------------- Qwen3.5 full-attention layer --- */
 
 /* ops.odin:163-168 */

@@ -61,6 +61,8 @@ def lib():
         L.ref_conv1d.argtypes = [c_vp, c_vp, c_vp, c_vp, c_i64, c_int]
         L.ref_l2norm_into.argtypes = [c_vp, c_vp, c_i64, c_f]
         L.ref_deltanet_steps.argtypes = [c_int] * 5 + [c_f, c_int] + [c_vp] * 11
+        L.ref_delta_chunk.argtypes = [c_vp] * 7 + [c_int] * 3
+        L.ref_deltanet_steps_chunked.argtypes = [c_int] * 5 + [c_f, c_int, c_int] + [c_vp] * 11
         L.ref_inv_freq.argtypes = [c_f, c_int, c_vp]
         L.ref_mrope.argtypes = [c_vp, c_int, c_vp, c_int]
         L.ref_qwen35_attn_steps.argtypes = [c_int] * 5 + [c_f, c_int, c_int] + [c_vp] * 9
@@ -291,6 +293,37 @@ def deltanet_steps(n_kh, n_vh, hk, hv, kernel, eps, qkv, z, b, a, conv_w, a_deca
     out = np.empty((T, n_vh * hv), np.float32)
     rc = lib().ref_deltanet_steps(n_kh, n_vh, hk, hv, kernel, float(eps), T, _p(qkv), _p(z), _p(b), _p(a),
                                   _p(conv_w), _p(a_decay), _p(dt_bias), _p(norm_w), _p(cs), _p(rs), _p(out))
+    if rc:
+        raise RuntimeError(lib().ref_last_error().decode())
+    return out, cs, rs
+
+
+def delta_chunk(state, q, k, v, beta, g):
+    """ref_delta_chunk: the chunked delta rule (qwen3_5/metal.odin:416-468) for
+    one value head over C tokens; returns (out [C, hv], new state [hk, hv])."""
+    f = lambda x: np.ascontiguousarray(x, np.float32)
+    st = f(state).copy()
+    q, k, v, beta, g = f(q), f(k), f(v), f(beta), f(g)
+    C, hk = k.shape
+    hv = v.shape[1]
+    out = np.empty((C, hv), np.float32)
+    lib().ref_delta_chunk(_p(out), _p(st), _p(q), _p(k), _p(v), _p(beta), _p(g), C, hk, hv)
+    return out, st
+
+
+def deltanet_steps_chunked(n_kh, n_vh, hk, hv, kernel, eps, chunk, qkv, z, b, a, conv_w, a_decay, dt_bias, norm_w,
+                           conv_state, rec_state):
+    """deltanet_steps with the delta rule in chunks of `chunk` tokens
+    (ref_deltanet_steps_chunked); returns (out, conv_state, rec_state)."""
+    f = lambda x: np.ascontiguousarray(x, np.float32)
+    qkv, z, b, a = f(np.atleast_2d(qkv)), f(np.atleast_2d(z)), f(np.atleast_2d(b)), f(np.atleast_2d(a))
+    conv_w, a_decay, dt_bias, norm_w = f(conv_w), f(a_decay), f(dt_bias), f(norm_w)
+    cs, rs = f(conv_state).copy(), f(rec_state).copy()
+    T = qkv.shape[0]
+    out = np.empty((T, n_vh * hv), np.float32)
+    rc = lib().ref_deltanet_steps_chunked(n_kh, n_vh, hk, hv, kernel, float(eps), T, int(chunk), _p(qkv), _p(z),
+                                          _p(b), _p(a), _p(conv_w), _p(a_decay), _p(dt_bias), _p(norm_w), _p(cs),
+                                          _p(rs), _p(out))
     if rc:
         raise RuntimeError(lib().ref_last_error().decode())
     return out, cs, rs

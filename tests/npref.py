@@ -308,6 +308,43 @@ def deltanet_f64(n_kh, n_vh, hk, hv, kernel, eps, qkv, z, b, a, conv_w, a_decay,
     return np.array(outs), (cs.reshape(-1) if kernel > 1 else np.zeros(0)), S.reshape(-1)
 
 
+def delta_tokens_f64(state, q, k, v, beta, g):
+    """Float64 gated delta rule token by token (qwen3_5/ops.odin:120-153):
+    S *= g_t; d = (v_t - S^T k_t) beta_t; S += k_t d^T; o_t = S^T q_t.
+    Returns (out [C, hv], state [hk, hv])."""
+    S = np.array(state, np.float64).copy()
+    out = []
+    for t in range(len(k)):
+        S *= g[t]
+        d = (np.float64(v[t]) - S.T @ np.float64(k[t])) * beta[t]
+        S += np.outer(np.float64(k[t]), d)
+        out.append(S.T @ np.float64(q[t]))
+    return np.array(out), S
+
+
+def delta_chunk_f64(state, q, k, v, beta, g, mistake=None):
+    """Float64 chunked form of the gated delta rule over C tokens (the math of
+    qwen3_5/metal.odin:416-468 chunked_delta), written with matrices: cp the
+    running product of the decays, D[t, i] = cp[t] / cp[i],
+      (I + tril(beta D (K K^T), -1)) Delta = beta v - beta cp (K S)
+      O  = cp (Q S) + tril(D (Q K^T)) Delta
+      S' = cp[C-1] S + (K cp[C-1] / cp)^T Delta.
+    `mistake` plants one error for tests that must catch it: 'no_ratio' (cp[t]
+    for cp[t] / cp[i]), 'o_strict' (O without the i = t term), 'state_ratio'
+    (S' without the per-token factors), 'l_diag' (the diagonal kept in the
+    substitution).  Returns (out [C, hv], state [hk, hv])."""
+    f = lambda x: np.array(x, np.float64)
+    S, q, k, v, beta, g = f(state), f(q), f(k), f(v), f(beta), f(g)
+    cp = np.cumprod(g)
+    D = cp[:, None] / cp[None, :] if mistake != "no_ratio" else np.repeat(cp[:, None], len(cp), 1)
+    L = np.tril(beta[:, None] * D * (k @ k.T), 0 if mistake == "l_diag" else -1)
+    rhs = beta[:, None] * v - (beta * cp)[:, None] * (k @ S)
+    delta = np.linalg.solve(np.eye(len(k)) + L, rhs)
+    O = cp[:, None] * (q @ S) + np.tril(D * (q @ k.T), -1 if mistake == "o_strict" else 0) @ delta
+    w = cp[-1] / cp if mistake != "state_ratio" else np.ones_like(cp)
+    return O, cp[-1] * S + (k * w[:, None]).T @ delta
+
+
 def qwen35_attn_f64(n_heads, n_kv, hd, rotary_dim, seq_len, eps, pos0, qproj, k, v, q_norm, k_norm, theta,
                     kc16, vc16, full_rotary=False, gate=True):
     """Float64 restatement of forward_full_layer's attention (qwen3_5/

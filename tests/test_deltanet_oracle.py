@@ -69,3 +69,113 @@ def test_deltanet_steps_vs_float64(shape):
         assert np.array_equal(cs, rcs.astype(np.float32))  # the window only moves values
     bad, _, _ = npref.deltanet_f64(*args, kv_from_q=True)
     assert np.max(np.abs(out - bad)) / np.max(np.abs(ref)) > 100 * 2e-5
+
+
+# ----- the chunked form of the delta rule (qwen3_5/metal.odin:416-468) -----
+
+def _chunk_case(rng, C, hk, hv, beta=None, g=None):
+    q = rng.standard_normal((C, hk))
+    k = rng.standard_normal((C, hk))
+    q /= np.linalg.norm(q, axis=1, keepdims=True) * np.sqrt(hk)
+    k /= np.linalg.norm(k, axis=1, keepdims=True)
+    v = rng.uniform(-1, 1, (C, hv))
+    beta = rng.uniform(0.2, 0.8, C) if beta is None else np.broadcast_to(np.float64(beta), (C,))
+    g = rng.uniform(0.25, 0.99, C) if g is None else np.broadcast_to(np.float64(g), (C,))
+    S = rng.standard_normal((hk, hv)) * 0.1
+    f = lambda x: np.asarray(x, np.float32).astype(np.float64)  # the f32 values both sides see
+    return f(S), f(q), f(k), f(v), f(beta), f(g)
+
+
+@pytest.mark.parametrize("C,hk,hv", [(1, 8, 8), (2, 16, 8), (5, 16, 16), (16, 32, 16), (33, 16, 24)])
+def test_delta_chunk_f64_equals_tokenwise(C, hk, hv):
+    """The chunked form is an exact rewriting of C token steps: in float64 the
+    two agree to rounding; each planted mistake in the chunked form departs
+    by far more."""
+    case = _chunk_case(np.random.default_rng(C * 31 + hk), C, hk, hv)
+    o_t, s_t = npref.delta_tokens_f64(*case)
+    o_c, s_c = npref.delta_chunk_f64(*case)
+    scale = max(np.max(np.abs(o_t)), 1e-30)
+    assert np.max(np.abs(o_c - o_t)) / scale <= 1e-12
+    assert np.max(np.abs(s_c - s_t)) / np.max(np.abs(s_t)) <= 1e-12
+    for m in ("no_ratio", "o_strict", "state_ratio", "l_diag"):
+        o_m, s_m = npref.delta_chunk_f64(*case, mistake=m)
+        if C == 1 and m in ("no_ratio", "state_ratio"):
+            continue  # one token: the ratios are all 1
+        err = max(np.max(np.abs(o_m - o_t)) / scale, np.max(np.abs(s_m - s_t)) / np.max(np.abs(s_t)))
+        assert err > 1e-3, m
+
+
+@pytest.mark.parametrize("C", [1, 3, 16, 32, 64])
+def test_oracle_delta_chunk_vs_f64(C):
+    """refcpu.ref_delta_chunk (f32) against the float64 chunked form at head
+    dims 128, decays down to 0.25 (a 64-token chunk's running product reaches
+    ~1e-20, still a normal f32)."""
+    case = _chunk_case(np.random.default_rng(C), C, 128, 128)
+    out, st = refcpu.delta_chunk(*case)
+    o64, s64 = npref.delta_chunk_f64(*case)
+    assert np.max(np.abs(out - o64)) / np.max(np.abs(o64)) <= 2e-5
+    assert np.max(np.abs(st - s64)) / np.max(np.abs(s64)) <= 2e-5
+    for m in ("o_strict", "l_diag") + (("no_ratio", "state_ratio") if C > 1 else ()):
+        om, sm = npref.delta_chunk_f64(*case, mistake=m)
+        assert max(np.max(np.abs(out - om)) / np.max(np.abs(o64)), np.max(np.abs(st - sm)) / np.max(np.abs(s64))) > 1e-3
+
+
+def _ladder_beta(kind, t):
+    return {"real": 0.55, "one": 1.0, "tiny": 0.01, "sin": 0.3 + 0.4 * np.sin(t),
+            "saw": 0.2 + 0.6 * ((t * 0.31) % 1.0)}[kind]
+
+
+def _ladder_g(kind, t):
+    return {"real": 0.99, "slow": 0.999, "strong": 0.1, "one": 1.0, "cos": 0.4 + 0.4 * np.cos(t * 0.7),
+            "saw": 0.25 + 0.6 * ((t * 0.47) % 1.0)}[kind]
+
+
+@pytest.mark.parametrize("C,T,bk,gk", [(1, 256, "real", "real"), (2, 256, "real", "real"), (4, 256, "real", "real"),
+                                       (8, 256, "real", "real"), (16, 256, "real", "real"),
+                                       (16, 1024, "real", "slow"), (16, 1024, "one", "real"),
+                                       (16, 256, "sin", "cos"), (16, 256, "saw", "saw"), (16, 256, "tiny", "real"),
+                                       (16, 256, "real", "strong"), (16, 256, "real", "one")])
+def test_oracle_chunked_ladder(C, T, bk, gk):
+    """The reference's chunked-vs-tokenwise ladder (delta_ref.odin:288-399:
+    head dims 128, l2-normalized q (times 1/sqrt(128)) and k, v in [-1, 1],
+    zero initial state, the listed beta / decay schedules, chunks of C): the
+    oracle's chunked form against its token steps, output within the
+    reference's 1e-2 absolute bound and, tighter, 1e-4 of the output scale;
+    the state too."""
+    rng = np.random.default_rng(C * 7 + T)
+    t = np.arange(T)
+    beta = np.array([_ladder_beta(bk, x) for x in t], np.float32)
+    g = np.array([_ladder_g(gk, x) for x in t], np.float32)
+    _, q, k, v, _, _ = _chunk_case(rng, T, 128, 128)
+    s_tok = np.zeros((128, 128), np.float32)
+    out_tok = np.empty((T, 128), np.float32)
+    for i in range(T):
+        out_tok[i], s_tok = refcpu.delta_step(s_tok, q[i], k[i], v[i], float(beta[i]), float(g[i]))
+    s_ch = np.zeros((128, 128), np.float32)
+    out_ch = np.empty((T, 128), np.float32)
+    for lo in range(0, T, C):
+        out_ch[lo:lo + C], s_ch = refcpu.delta_chunk(s_ch, q[lo:lo + C], k[lo:lo + C], v[lo:lo + C],
+                                                     beta[lo:lo + C], g[lo:lo + C])
+    d = np.max(np.abs(np.float64(out_ch) - out_tok))
+    assert d < 1e-2
+    assert d <= 1e-4 * np.max(np.abs(out_tok)), d
+    assert np.max(np.abs(np.float64(s_ch) - s_tok)) <= 1e-4 * np.max(np.abs(s_tok))
+
+
+@pytest.mark.parametrize("chunk,T", [(1, 7), (3, 10), (16, 37), (64, 37), (16, 64)])
+def test_deltanet_steps_chunked_vs_tokenwise(chunk, T):
+    """The whole step with the delta rule in chunks (ragged last chunk) against
+    the oracle's token steps and the float64 model; a planted mistake in the
+    float64 model still fails the bound."""
+    c = _case(np.random.default_rng(chunk * 100 + T), 2, 4, 16, 16, 4, T)
+    args = [c[k] for k in ("n_kh", "n_vh", "hk", "hv", "kernel", "eps", "qkv", "z", "b", "a", "conv_w", "a_decay",
+                           "dt_bias", "norm_w", "conv_state", "rec_state")]
+    out, cs, rs = refcpu.deltanet_steps_chunked(*args[:6], chunk, *args[6:])
+    tok, tcs, trs = refcpu.deltanet_steps(*args)
+    ref, rcs, rrs = npref.deltanet_f64(*args)
+    assert np.array_equal(cs, tcs)
+    for got, want in ((out, ref), (rs, rrs)):
+        assert np.max(np.abs(got - want)) / np.max(np.abs(want)) <= 2e-5
+    assert np.max(np.abs(out - tok)) / np.max(np.abs(tok)) <= 2e-5
+    bad, _, _ = npref.deltanet_f64(*args, kv_from_q=True)
+    assert np.max(np.abs(out - bad)) / np.max(np.abs(ref)) > 100 * 2e-5

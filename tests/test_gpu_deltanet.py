@@ -76,3 +76,45 @@ def test_deltanet_rejects_head_dims():
     args = _case(np.random.default_rng(0), 1, 1, 64, 64, 2, 1)
     with pytest.raises(_native.OIError):
         qwen35.deltanet_steps(*args)
+
+
+def _moderate(args):
+    """Decays of 0.2-0.9 per token: a 32-token chunk's running product stays a
+    normal f32 (the oracle's chunked form divides running products, which
+    turns to 0/0 once one underflows; the kernels work with sums of logs)."""
+    rng = np.random.default_rng(len(args[6]))
+    T, n_vh = args[8].shape
+    args[9] = (rng.standard_normal((T, n_vh)) * 0.5 - 1.0).astype(np.float32)  # a
+    args[11] = (-np.exp(rng.standard_normal(n_vh) * 0.25)).astype(np.float32)  # a_decay
+    return args
+
+
+@pytest.mark.parametrize("chunk,T", [(0, 3), (0, 37), (16, 3), (16, 37), (16, 200), (32, 37), (32, 200)])
+def test_deltanet_batched_vs_oracle(chunk, T):
+    """oi_deltanet_steps_batched (the prefill kernels: conv over the whole
+    trajectory, then the delta rule token by token or in chunks of 16 / 32
+    with a ragged last chunk) against the oracle's same form
+    (ref_deltanet_steps / ref_deltanet_steps_chunked) within 1e-5, and against
+    the oracle's token steps within 1e-4 (the chunked form sums in another
+    order); the conv window moves values only, bit-identical."""
+    args = _moderate(_case(np.random.default_rng(T * 3 + chunk), 16, 32, 128, 128, 4, T))
+    print("case chunk=%d T=%d" % (chunk, T), flush=True)
+    out, cs, rs = qwen35.deltanet_steps_batched(*args[:6], chunk, *args[6:])
+    tok, tcs, trs = refcpu.deltanet_steps(*args)
+    rout, rcs, rrs = refcpu.deltanet_steps_chunked(*args[:6], chunk, *args[6:]) if chunk else (tok, tcs, trs)
+    print("chunk %d T %d: vs oracle %.3g / state %.3g; vs token steps %.3g" %
+          (chunk, T, _err(out, rout), _err(rs, rrs), _err(out, tok)))
+    assert _err(out, rout) <= 1e-5, _err(out, rout)
+    assert _err(rs, rrs) <= 1e-5, _err(rs, rrs)
+    assert _err(out, tok) <= 1e-4 and _err(rs, trs) <= 1e-4
+    assert np.array_equal(cs, rcs)
+
+
+def test_deltanet_batched_rejects_bad_chunk():
+    args = _case(np.random.default_rng(1), 2, 2, 128, 128, 4, 8)
+    for chunk in (8, 64, -1):
+        with pytest.raises(RuntimeError, match="chunk"):
+            qwen35.deltanet_steps_batched(*args[:6], chunk, *args[6:])
+    with pytest.raises(RuntimeError, match="n_tokens"):
+        short = _case(np.random.default_rng(1), 2, 2, 128, 128, 4, 2)
+        qwen35.deltanet_steps_batched(*short[:6], 16, *short[6:])

@@ -183,3 +183,35 @@ def test_prefill_expert_kernels_agree(tmp_path, monkeypatch, shape):
         err = scaled_err(out["default"], out[kind])
         print("%s: default vs %s experts %.3g" % (shape, kind, err))
         assert err <= 1e-5, kind
+
+
+@pytest.mark.parametrize("chunk", ["16", "32"])
+@pytest.mark.parametrize("name,n", [("qwen35-tiny", 40), ("qwen35-hybrid-moe-2layer", 200)])
+def test_prefill_chunked_delta_vs_oracle(make_model, monkeypatch, chunk, name, n):
+    """Prefill with the delta rule of the DeltaNet layers in its chunked form
+    (OI_PREFILL_DN_CHUNK=16 / 32) against the oracle's prefill (the delta
+    rule token by token): the same bars as the default path, and the same
+    greedy continuation on the tiny model."""
+    monkeypatch.setenv("OI_PREFILL_DN_CHUNK", chunk)
+    path = make_model(name)
+    e, r = _engines(path, 256)
+    try:
+        toks = _tokens(17, n, r.vocab_size)
+        print("case %s n=%d chunk %s" % (name, n, chunk), flush=True)
+        got = infer.engine_forward_batch(e, toks, 0).copy()
+        ref = r.prefill(toks, 0)
+        err = scaled_err(got, ref)
+        print("%s n=%d chunk %s: scaled error %.3g" % (name, n, chunk, err))
+        assert err <= TOL
+        first = int(np.argmax(got))
+        assert first == refcpu.argmax(ref)
+        if name == "qwen35-tiny":
+            got_g = infer.engine_decode_greedy(e, first, n, 8)
+            ref_g, tok = [], first
+            for i in range(8):
+                tok = refcpu.argmax(r.forward(tok, n + i))
+                ref_g.append(tok)
+            assert np.array_equal(got_g, np.array(ref_g, np.int32))
+    finally:
+        infer.engine_destroy(e)
+        r.close()
