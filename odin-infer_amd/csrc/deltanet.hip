@@ -19,7 +19,10 @@
 //   sums S^T k and S^T q are reduced over the row groups through LDS.
 // The state is HBM-bound: 4 * head_k_dim * head_v_dim bytes read and written
 // per value head and token.  dn_step_kernel does both in one launch when the
-// value heads are one or two per k head (below).
+// value heads are one or two per k head (below).  The engine's token loop
+// uses dn_cols_kernel instead: the conv in the in_qkv GEMV's epilogue, the
+// delta rule over many more workgroups, the gated norm in the output GEMV's
+// prologue.
 
 #include "device_common.h"
 
@@ -256,8 +259,97 @@ __global__ __launch_bounds__(1024) void dn_step_kernel(DnArgs a) {
     }
 }
 
+// The delta rule alone (the token loop's form: the in_qkv GEMV has applied
+// the conv, the output GEMV's prologue finishes the gated norm from the
+// outputs times silu(z) and the per-workgroup sums of squares written here).  Grid (n_vh,
+// hv / 32): a workgroup owns 32 state columns of value head vh, so the state
+// is spread over n_vh * hv / 32 workgroups (128 at 32 value heads) and every
+// row segment a workgroup reads is one 128-byte line.  Lane = 8 column +
+// row group, a row group 16 rows: a lane holds 16 state values; the column
+// sums over the 8 row groups are DPP sums inside the lane's group of 8.  Each
+// lane normalizes its 16 rows of q and k itself (the sums of squares over the
+// same groups of 8).
+template <int HK, int HV>
+__global__ __launch_bounds__(WG) void dn_cols_kernel(DnArgs a) {
+#pragma clang fp contract(off)
+    constexpr int RPL = HK / 8;
+    static_assert(RPL == 16 && HV % 32 == 0, "head shape");
+    const int vh = blockIdx.x, kh = vh % a.n_kh, c0 = (int)blockIdx.y * 32;
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    const int cl = wave * 8 + (lane >> 3), rg = lane & 7, j = c0 + cl, i0 = rg * RPL;
+    const int KD = a.n_kh * HK;
+    float *S = a.state + (size_t)vh * HK * HV;
+    float s[RPL];
+#pragma unroll
+    for (int r = 0; r < RPL; r++) s[r] = S[(size_t)(i0 + r) * HV + j];
+    const float4 *q4 = (const float4 *)(a.conv_out + kh * HK + i0);
+    const float4 *k4 = (const float4 *)(a.conv_out + KD + kh * HK + i0);
+    float qn[RPL], kn[RPL];
+#pragma unroll
+    for (int i = 0; i < RPL / 4; i++) {
+        const float4 qq = q4[i], kk = k4[i];
+        qn[4 * i] = qq.x; qn[4 * i + 1] = qq.y; qn[4 * i + 2] = qq.z; qn[4 * i + 3] = qq.w;
+        kn[4 * i] = kk.x; kn[4 * i + 1] = kk.y; kn[4 * i + 2] = kk.z; kn[4 * i + 3] = kk.w;
+    }
+    const float v = a.conv_out[2 * KD + vh * HV + j];
+    const float beta = sigmoid_ref(a.b[vh]);
+    const float decay = expf(a.a_decay[vh] * softplus_ref(a.a[vh] + a.dt_bias[vh]));
+    // l2norm of q and k (ops.odin:27-37), eps 1e-6 a floor on the norm
+    float sq = 0.f, sk = 0.f;
+#pragma unroll
+    for (int r = 0; r < RPL; r++) {
+        sq += qn[r] * qn[r];
+        sk += kn[r] * kn[r];
+    }
+    sq += OI_DPP(sq, 0xB1);
+    sq += OI_DPP(sq, 0x4E);
+    sq += dpp_mirror8(sq);
+    sk += OI_DPP(sk, 0xB1);
+    sk += OI_DPP(sk, 0x4E);
+    sk += dpp_mirror8(sk);
+    const float iq = 1.0f / fmaxf(sqrtf(sq), 1e-6f), ik = 1.0f / fmaxf(sqrtf(sk), 1e-6f);
+#pragma unroll
+    for (int r = 0; r < RPL; r++) {
+        qn[r] = qn[r] * iq * (1.0f / sqrtf((float)HK));
+        kn[r] = kn[r] * ik;
+    }
+    // delta rule (forward.odin:193-209)
+    float kv = 0.f;
+#pragma unroll
+    for (int r = 0; r < RPL; r++) {
+        s[r] = s[r] * decay;
+        kv += s[r] * kn[r];
+    }
+    kv += OI_DPP(kv, 0xB1);
+    kv += OI_DPP(kv, 0x4E);
+    kv += dpp_mirror8(kv);
+    const float delta = (v - kv) * beta;
+    float o = 0.f;
+#pragma unroll
+    for (int r = 0; r < RPL; r++) {
+        s[r] += kn[r] * delta;
+        S[(size_t)(i0 + r) * HV + j] = s[r];
+        o += s[r] * qn[r];
+    }
+    o += OI_DPP(o, 0xB1);
+    o += OI_DPP(o, 0x4E);
+    o += dpp_mirror8(o);
+    // for the gated norm (forward.odin:211-218) in the output GEMV's prologue:
+    // o silu(z) per column, and this workgroup's part of the head's sum of o^2
+    __shared__ float wss[WG / WAVE];
+    const float ss = wave_sum(rg == 0 ? o * o : 0.f);
+    if (lane == 0) wss[wave] = ss;
+    if (rg == 0) a.out[vh * HV + j] = o * silu_ref(a.z[vh * HV + j]);
+    __syncthreads();
+    if (threadIdx.x == 0) a.ssq[vh * (HV / 32) + blockIdx.y] = (wss[0] + wss[1]) + (wss[2] + wss[3]);
+}
+
 hipError_t launch_deltanet(const DnArgs &a, hipStream_t st) {
     if (a.hk != 128 || a.hv != 128 || a.kernel < 1 || a.n_kh <= 0 || a.n_vh <= 0) return hipErrorInvalidValue;
+    if (a.cols) {
+        hipLaunchKernelGGL((dn_cols_kernel<128, 128>), dim3((unsigned)a.n_vh, 128 / 32), dim3(WG), 0, st, a);
+        return hipGetLastError();
+    }
     if (a.n_vh == a.n_kh) {
         hipLaunchKernelGGL((dn_step_kernel<128, 128, 1>), dim3((unsigned)a.n_kh), dim3(1024), 0, st, a);
         return hipGetLastError();

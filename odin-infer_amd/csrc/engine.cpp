@@ -585,7 +585,7 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
                  al((size_t)c.seq_len * (c.head_dim / 2) * 8);
     if (e->arch == 2)
         act += al(QD * 4) + al((size_t)(e->rotary_dim / 2 + 1) * 4) + 2 * al((size_t)CD * 4) + 2 * al((size_t)VD * 4) +
-               2 * al((size_t)e->lin_nv * 4);
+               2 * al((size_t)e->lin_nv * 4) + al((size_t)e->lin_nv * 16);
     if (moe) act += al((size_t)E * 4) + 3 * al(64 * 4) + al((size_t)SF * 4 + 4);
     act += al(sizeof(SampleState)) + al((size_t)c.vocab_size * 4);  // sampler state and probabilities
     e->arena.size = wbytes + 2 * kv_layer * n_attn + (conv_layer + rec_layer + 512) * n_lin + act + 8192;
@@ -692,7 +692,7 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     e->samp_p = (float *)e->arena.take((size_t)c.vocab_size * 4);
     e->rope_cs = (float2 *)e->arena.take((size_t)c.seq_len * (c.head_dim / 2) * 8);
     float *qbuf = nullptr, *inv_freq = nullptr, *lin_qkv = nullptr, *lin_conv = nullptr, *lin_z = nullptr;
-    float *lin_out = nullptr, *lin_b = nullptr, *lin_a = nullptr;
+    float *lin_out = nullptr, *lin_b = nullptr, *lin_a = nullptr, *lin_ssq = nullptr;
     if (e->arch == 2) {
         qbuf = (float *)e->arena.take(QD * 4);
         inv_freq = (float *)e->arena.take((size_t)(e->rotary_dim / 2 + 1) * 4);
@@ -703,6 +703,7 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
         lin_out = (float *)e->arena.take((size_t)VD * 4);
         lin_b = (float *)e->arena.take((size_t)e->lin_nv * 4);
         lin_a = (float *)e->arena.take((size_t)e->lin_nv * 4);
+        lin_ssq = (float *)e->arena.take((size_t)e->lin_nv * 4 * 4);  // [n_vh][hv / 32] (hv 128 on that path)
     }
     float *mo_logits = nullptr, *mo_w = nullptr, *mo_sg = nullptr;
     int32_t *mo_ids = nullptr;
@@ -713,7 +714,7 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
         mo_sg = (float *)e->arena.take(64 * 4);
     }
     float *sh_h = moe ? (float *)e->arena.take((size_t)SF * 4 + 4) : nullptr;
-    if (!e->rope_cs || (e->arch == 2 && !lin_a) || (moe && !sh_h))
+    if (!e->rope_cs || (e->arch == 2 && !lin_ssq) || (moe && !sh_h))
         return fail(OI_E_NOMEM, "arena exhausted (activations)");
 
     // RoPE table, same f32 formula as infer/forward.odin:127-130
@@ -764,6 +765,7 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
                                                                (ga.mode == GEMV_ADD ? 2 : 1);
         return o;
     };
+    e->dn_fused = std::getenv("OI_DN_FUSED") != nullptr;  // the one-launch DeltaNet step in the token loop
     e->ops.assign((size_t)c.n_layers, {});
     for (size_t l = 0; l < e->layers.size(); l++) {
         LayerDev &L = e->layers[l];
@@ -824,7 +826,19 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
             in.seg[1].m = L.in_z; in.seg[1].y = lin_z;
             in.seg[2].m = L.in_b; in.seg[2].y = lin_b;
             in.seg[3].m = L.in_a; in.seg[3].y = lin_a;
-            ops.push_back(gemv_op(K_LIN_IN, in));
+            GemvArgs o = gemv_args(GEMV_ADD, (int)VD, lin_out, nullptr, eps);
+            o.nseg = 1;
+            o.seg[0].m = L.ssm_out; o.seg[0].y = e->x;
+            // the split step when both GEMVs take their part: the conv as the
+            // in_qkv rows' epilogue, the delta rule on n_vh x 4 workgroups,
+            // the gated norm as the output GEMV's prologue
+            GemvArgs in2 = in, o2 = o;
+            in2.seg[0].y = lin_conv;
+            in2.conv_w = L.conv_w; in2.conv_state = L.conv_state; in2.conv_kernel = (int32_t)e->lin_kernel;
+            o2.norm_w = L.ssm_norm; o2.gss = lin_ssq;
+            const bool split = !e->dn_fused && e->lin_hk == 128 && e->lin_hv == 128 && plan_gemv(in2) &&
+                               in2.kernel == 1 && plan_gemv(o2) && o2.kernel == 1;
+            ops.push_back(gemv_op(K_LIN_IN, split ? in2 : in));
             Op dn;
             dn.kind = OP_DN;
             dn.role = K_DELTANET;
@@ -838,12 +852,12 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
             t.out = lin_out;
             t.n_kh = (int32_t)e->lin_nk; t.n_vh = (int32_t)e->lin_nv;
             t.hk = (int32_t)e->lin_hk; t.hv = (int32_t)e->lin_hv; t.kernel = (int32_t)e->lin_kernel;
-            dn.bytes = 2.0 * rec_layer + 2.0 * conv_layer + (double)CD * e->lin_kernel * 4 + (CD + 3.0 * VD) * 4;
+            t.cols = split ? 1 : 0;
+            t.ssq = lin_ssq;
+            dn.bytes = split ? 2.0 * rec_layer + (2.0 * KD + VD) * 4 + 2.0 * VD * 4
+                             : 2.0 * rec_layer + 2.0 * conv_layer + (double)CD * e->lin_kernel * 4 + (CD + 3.0 * VD) * 4;
             ops.push_back(dn);
-            GemvArgs o = gemv_args(GEMV_ADD, (int)VD, lin_out, nullptr, eps);
-            o.nseg = 1;
-            o.seg[0].m = L.ssm_out; o.seg[0].y = e->x;
-            ops.push_back(gemv_op(K_LIN_OUT, o));
+            ops.push_back(gemv_op(K_LIN_OUT, split ? o2 : o));
         }
         if (!L.moe) {
             GemvArgs gu = gemv_args(GEMV_SWIGLU, (int)D, e->x, L.ffn_norm, eps);

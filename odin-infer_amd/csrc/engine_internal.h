@@ -110,6 +110,7 @@ struct oi_engine {
     bool pf_fused = true;  // gate/up GEMM with the SwiGLU epilogue where it applies (OI_PREFILL_UNFUSED=1: off)
     int pf_experts = 0;  // routed experts of a prefill: 0 the default kernels, 1 the multi-token GEMV, 2 f32 MFMA
                          // only (OI_PREFILL_EXPERTS=gemv / f32)
+    bool dn_fused = false;  // token loop: the one-launch DeltaNet step instead of the split one (OI_DN_FUSED)
     int pf_dn_chunk = 0;  // delta rule of a prefill chunk: 0 token by token, 16 / 32 chunked (OI_PREFILL_DN_CHUNK)
 };
 

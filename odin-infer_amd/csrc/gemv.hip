@@ -236,12 +236,23 @@ constexpr int GW = 1024, GNW = GW / WAVE;
 // x (and of the norm weight) per thread are held in registers; XR == 0 means
 // K is too long for that and both passes read x from memory after the
 // prefetch.  K/4 is a multiple of 8, so the 8-lane groups of quant4 are whole.
-template <int XR, bool NORM>
+// Prologue modes: NORM 0 takes x as it is, XN_RMS replaces it by rmsnorm(x) *
+// norm_w over the whole vector, XN_GATED finishes the gated RMSNorm of a
+// DeltaNet layer's output (qwen3_5/forward.odin:211-218): x holds o silu(z)
+// per head of GN_HV values and gss the head's four partial sums of o^2;
+// x = norm_w[j] (inv_h x), inv_h = 1 / sqrt(sum_h o^2 / GN_HV + eps).
+// XN_RMS_CONV is XN_RMS with the conv epilogue (segment 0's rows are DeltaNet
+// conv channels).
+enum { XN_RMS = 1, XN_GATED = 2, XN_RMS_CONV = 3 };
+constexpr int GN_HV = 128;
+static constexpr bool xn_rms(int n) { return n == XN_RMS || n == XN_RMS_CONV; }
+
+template <int XR, int NORM>
 struct XPre {
-    float4 x[XR > 0 ? XR : 1], w[XR > 0 && NORM ? XR : 1];
+    float4 x[XR > 0 ? XR : 1], w[XR > 0 && NORM ? XR : 1], z[XR > 0 && NORM == XN_GATED ? XR : 1];  // z: gss
 };
 
-template <int XR, bool NORM, bool REV = false>
+template <int XR, int NORM, bool REV = false>
 static __device__ __forceinline__ void xpre_load(const GemvArgs &a, XPre<XR, NORM> &p) {
     // unconditional loads (indices clamped to the last float4, duplicates are
     // ignored by xpre_finish): a branch-free sequence lets the compiler wait
@@ -254,20 +265,44 @@ static __device__ __forceinline__ void xpre_load(const GemvArgs &a, XPre<XR, NOR
         const int i = REV ? XR - 1 - ii : ii;  // REV: same loads in another order (see gemv_q_kernel)
         const int c = min(tid + i * GW, last);
         p.x[i] = gx[c];
-        if (NORM) p.w[i] = nw[c];
+        if (xn_rms(NORM)) p.w[i] = nw[c];
+        if (NORM == XN_GATED) {
+            p.w[i] = nw[c % (GN_HV / 4)];
+            p.z[i] = ((const float4 *)a.gss)[c / (GN_HV / 4)];
+        }
     }
 }
 
-template <int XR, bool NORM>
+template <int XR, int NORM>
 static __device__ __forceinline__ void xpre_finish(const GemvArgs &a, const XPre<XR, NORM> &p, u32x4 *xhi,
                                                    u32x4 *xmid, u32x4 *xlo, float *xs, float *s32, float *s16,
                                                    float *red) {
+    static_assert(NORM != XN_GATED || XR > 0, "the gated norm needs x in registers");
     const int K = a.K, tid = threadIdx.x;
     const float4 *gx = (const float4 *)a.x;
     const float4 *nw = (const float4 *)a.norm_w;
     uint32_t *hw = (uint32_t *)xhi, *mw = (uint32_t *)xmid, *lw = (uint32_t *)xlo;
     float s = 1.f;
-    if (NORM) {
+    if (NORM == XN_GATED) {
+#pragma unroll
+        for (int i = 0; i < XR; i++) {
+            const float4 v = p.x[i], z = p.z[i], w = p.w[i];
+            float4 g;
+            {
+#pragma clang fp contract(off)
+                const float inv = 1.0f / sqrtf(((z.x + z.y) + (z.z + z.w)) / (float)GN_HV + a.eps);
+                g.x = w.x * (inv * v.x);
+                g.y = w.y * (inv * v.y);
+                g.z = w.z * (inv * v.z);
+                g.w = w.w * (inv * v.w);
+            }
+            const int c = tid + i * GW;
+            if (c < K / 4) quant4(g, c, hw, mw, lw, xs, s32, s16);
+        }
+        __syncthreads();
+        return;
+    }
+    if (xn_rms(NORM)) {
         float ss = 0.f;
         if (XR > 0) {
 #pragma unroll
@@ -294,7 +329,7 @@ static __device__ __forceinline__ void xpre_finish(const GemvArgs &a, const XPre
         s = 1.0f / sqrtf(ss / (float)K + a.eps);
     }
     auto one = [&](float4 v, float4 w, int c) {
-        if (NORM) {
+        if (xn_rms(NORM)) {
 #pragma clang fp contract(off)
             v.x = w.x * (s * v.x);
             v.y = w.y * (s * v.y);
@@ -315,6 +350,11 @@ static __device__ __forceinline__ void xpre_finish(const GemvArgs &a, const XPre
     __syncthreads();
 }
 
+// LDS of gemv_q_kernel: the x planes and scales, then the workgroup's outputs
+static size_t gemv_q_lds(int K, int out_rows) {
+    return (size_t)K / 16 * 48 + (size_t)K / 32 * 8 + (size_t)K / 16 * 4 + (size_t)out_rows * 4;
+}
+
 // One workgroup: row tiles [tb, te) of segment `seg`, all of weight type T.
 // A tile is R rows per lane group x (64/lpr) groups: the rows one wave
 // computes together, in upl = U/lpr steps of one unit per lane (one step
@@ -326,7 +366,7 @@ static __device__ __forceinline__ void xpre_finish(const GemvArgs &a, const XPre
 // step past the end reads row 0's first units, unused), so the compiler
 // waits for exactly the stage it consumes.  Rows past the end of the matrix
 // are clamped to the last row (computed, not stored).
-template <int T, int R, int NM, int XR, bool XU1, bool NORM, int MOE = 0>
+template <int T, int R, int NM, int XR, bool XU1, int NORM, int MOE = 0>
 static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int tb, int te, int wg,
                                                 const XPre<XR, NORM> &xp, int idv = 0, float wv = 0.f) {
     using W = typename Types<T>::W;
@@ -369,6 +409,20 @@ static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int 
     // x was requested by the caller; the first weights follow (loads return in order)
     int ct = wave, cu = 0;
     issue(ct, cu, ring[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    // conv epilogue: this thread's row's taps and window (rows past the end
+    // and other segments' workgroups read a valid row, unused), needed only
+    // after the loop, so requested after the first weights (they come from
+    // HBM; the weight requests do not wait for them)
+    float ctap[4] = {0.f, 0.f, 0.f, 0.f}, cwin[3] = {0.f, 0.f, 0.f};
+    if (NORM == XN_RMS_CONV) {
+        const int KS = a.conv_kernel, km1 = KS - 1;
+        const int c = min(tb * a.rows_per_wg + tid, a.seg[0].m.rows - 1);
+#pragma unroll
+        for (int k = 0; k < 4; k++) ctap[k] = a.conv_w[(size_t)c * KS + min(k, km1)];
+#pragma unroll
+        for (int k = 0; k < 3; k++) cwin[k] = a.conv_state[(size_t)c * km1 + min(k, km1 - 1)];
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     u32x4 *xhi = smem, *xmid = smem + K / 16, *xlo = smem + 2 * (K / 16);
@@ -470,9 +524,36 @@ static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int 
         float *y = a.seg[seg].y;
         // shared-expert gate: y += sigmoid(g) * Wx (the product first, then the scale)
         const float gs = NM == 1 && a.mode == GEMV_ADD && a.ygate ? 1.0f / (1.0f + expf(-a.ygate[0])) : 1.f;
-        for (int i = tid; i < wrow1 - wrow0; i += GW) {
-            if (NM == 1 && a.mode == GEMV_ADD) y[wrow0 + i] = y[wrow0 + i] + (a.ygate ? yo[i] * gs : yo[i]);
-            else y[wrow0 + i] = yo[i];
+        if (NORM == XN_RMS_CONV && seg == 0) {
+            // conv epilogue: row c is a channel of the DeltaNet conv
+            // (ops.odin:97-116, as dn_conv_kernel): silu of the window with the
+            // product last, then the window slides (2 <= kernel <= 4)
+            const int KS = a.conv_kernel, km1 = KS - 1;
+            for (int i = tid; i < wrow1 - wrow0; i += GW) {
+#pragma clang fp contract(off)
+                const int c = wrow0 + i;
+                float *cs = a.conv_state + (size_t)c * km1;
+                float tp[4], wn[3];
+#pragma unroll
+                for (int k = 0; k < 4; k++) tp[k] = i == tid ? ctap[k] : a.conv_w[(size_t)c * KS + min(k, km1)];
+#pragma unroll
+                for (int k = 0; k < 3; k++) wn[k] = i == tid ? cwin[k] : cs[min(k, km1 - 1)];
+                const float x = yo[i];
+                float acc = tp[km1] * x;
+#pragma unroll
+                for (int k = 0; k < 3; k++)
+                    if (k < km1) acc += tp[k] * wn[k];
+                y[c] = silu_ref(acc);
+#pragma unroll
+                for (int k = 0; k < 2; k++)
+                    if (k < km1 - 1) cs[k] = wn[k + 1];
+                cs[km1 - 1] = x;
+            }
+        } else {
+            for (int i = tid; i < wrow1 - wrow0; i += GW) {
+                if (NM == 1 && a.mode == GEMV_ADD) y[wrow0 + i] = y[wrow0 + i] + (a.ygate ? yo[i] * gs : yo[i]);
+                else y[wrow0 + i] = yo[i];
+            }
         }
     }
     if (NM == 1 && a.mode == GEMV_ARGMAX) {  // this workgroup's best (value, lowest row)
@@ -683,7 +764,7 @@ static __device__ __forceinline__ void moe_route(const GemvArgs &a, float lg, fl
 // would otherwise queue behind the other CUs' weight requests (the prologue
 // then ends later than the first weights arrive).  Other
 // type mixes are issued as one launch per type (wg_base).
-template <int T, int TL, int R, int NM, int XR, bool XU1, bool NORM, int MOE = 0>
+template <int T, int TL, int R, int NM, int XR, bool XU1, int NORM, int MOE = 0>
 __global__ __launch_bounds__(GW) void gemv_q_kernel(GemvArgs a) {
     const int wg = blockIdx.x + a.wg_base;
     int seg = 0;
@@ -731,19 +812,25 @@ __global__ __launch_bounds__(GW) void gemv_q_kernel(GemvArgs a) {
 // kernel configurations: (R, NM, XR, XU1); XR = float4 of x per thread held
 // in registers by the prologue (K <= 4 * GW * XR), 0 = x read twice from
 // memory; XU1 = one unit per lane per row (K <= 4096), x kept in registers
-template <int T, int R, bool NORM>
+template <int T, int R, int NORM>
 static const void *gemv_q_fn_r(bool swiglu, bool xu1, int K) {
-    if (swiglu) {
-        if (K <= 4096 && xu1) return (const void *)gemv_q_kernel<T, T, 1, 2, 1, true, NORM>;
-        if (K <= 4096) return (const void *)gemv_q_kernel<T, T, 1, 2, 1, false, NORM>;
-        return (const void *)gemv_q_kernel<T, T, 1, 2, 0, false, NORM>;
+    if constexpr (NORM == XN_GATED || NORM == XN_RMS_CONV) {  // x in registers: K <= 4096
+        if (swiglu || K > 4096 || (NORM == XN_GATED && K % GN_HV)) return nullptr;
+        if (xu1) return (const void *)gemv_q_kernel<T, T, R, 1, 1, true, NORM>;
+        return (const void *)gemv_q_kernel<T, T, R, 1, 1, false, NORM>;
+    } else {
+        if (swiglu) {
+            if (K <= 4096 && xu1) return (const void *)gemv_q_kernel<T, T, 1, 2, 1, true, NORM>;
+            if (K <= 4096) return (const void *)gemv_q_kernel<T, T, 1, 2, 1, false, NORM>;
+            return (const void *)gemv_q_kernel<T, T, 1, 2, 0, false, NORM>;
+        }
+        if (K <= 4096 && xu1) return (const void *)gemv_q_kernel<T, T, R, 1, 1, true, NORM>;
+        if (K <= 4096) return (const void *)gemv_q_kernel<T, T, R, 1, 1, false, NORM>;
+        if (K <= 12288) return (const void *)gemv_q_kernel<T, T, R, 1, 3, false, NORM>;
+        return (const void *)gemv_q_kernel<T, T, R, 1, 0, false, NORM>;
     }
-    if (K <= 4096 && xu1) return (const void *)gemv_q_kernel<T, T, R, 1, 1, true, NORM>;
-    if (K <= 4096) return (const void *)gemv_q_kernel<T, T, R, 1, 1, false, NORM>;
-    if (K <= 12288) return (const void *)gemv_q_kernel<T, T, R, 1, 3, false, NORM>;
-    return (const void *)gemv_q_kernel<T, T, R, 1, 0, false, NORM>;
 }
-template <int T, bool NORM>
+template <int T, int NORM>
 static const void *gemv_q_fn_t(bool swiglu, bool xu1, int K, int R) {
     return R == 1 ? gemv_q_fn_r<T, 1, NORM>(swiglu, xu1, K) : nullptr;
 }
@@ -759,9 +846,9 @@ static bool xu1_of(int K) {
     const int U = K / 64;
     return U <= 64 && (U & (U - 1)) == 0;  // one unit per lane per row
 }
-static const void *gemv_q_fn_mixed(int t, int tl, bool norm, int K, int R) {
+static const void *gemv_q_fn_mixed(int t, int tl, int norm, int K, int R) {
     const bool xu1 = xu1_of(K);
-    if (!norm) return nullptr;
+    if (norm != XN_RMS) return nullptr;
     if (t == T_Q4_K && tl == T_Q6_K) return gemv_q_fn_mixed<T_Q4_K, T_Q6_K>(xu1, K, R);
     if (t == T_Q6_K && tl == T_Q4_K) return gemv_q_fn_mixed<T_Q6_K, T_Q4_K>(xu1, K, R);
     if (t == T_Q4_K && tl == T_Q8_0) return gemv_q_fn_mixed<T_Q4_K, T_Q8_0>(xu1, K, R);
@@ -770,18 +857,25 @@ static const void *gemv_q_fn_mixed(int t, int tl, bool norm, int K, int R) {
     if (t == T_Q6_K && tl == T_Q8_0) return gemv_q_fn_mixed<T_Q6_K, T_Q8_0>(xu1, K, R);
     return nullptr;
 }
-static const void *gemv_q_fn(int type, bool swiglu, bool norm, int K, int R) {
+template <int T>
+static const void *gemv_q_fn_n(bool swiglu, int norm, bool xu1, int K, int R) {
+    if (norm == XN_GATED) return gemv_q_fn_t<T, XN_GATED>(swiglu, xu1, K, R);
+    if (norm == XN_RMS_CONV) return gemv_q_fn_t<T, XN_RMS_CONV>(swiglu, xu1, K, R);
+    return norm ? gemv_q_fn_t<T, XN_RMS>(swiglu, xu1, K, R) : gemv_q_fn_t<T, 0>(swiglu, xu1, K, R);
+}
+static const void *gemv_q_fn(int type, bool swiglu, int norm, int K, int R) {
     const bool xu1 = xu1_of(K);
     switch (type) {
-    case T_Q4_K: return norm ? gemv_q_fn_t<T_Q4_K, true>(swiglu, xu1, K, R) : gemv_q_fn_t<T_Q4_K, false>(swiglu, xu1, K, R);
-    case T_Q6_K: return norm ? gemv_q_fn_t<T_Q6_K, true>(swiglu, xu1, K, R) : gemv_q_fn_t<T_Q6_K, false>(swiglu, xu1, K, R);
-    default: return norm ? gemv_q_fn_t<T_Q8_0, true>(swiglu, xu1, K, R) : gemv_q_fn_t<T_Q8_0, false>(swiglu, xu1, K, R);
+    case T_Q4_K: return gemv_q_fn_n<T_Q4_K>(swiglu, norm, xu1, K, R);
+    case T_Q6_K: return gemv_q_fn_n<T_Q6_K>(swiglu, norm, xu1, K, R);
+    default: return gemv_q_fn_n<T_Q8_0>(swiglu, norm, xu1, K, R);
     }
 }
-
-static size_t gemv_q_lds(int K, int out_rows) {
-    return (size_t)K / 16 * 48 + (size_t)K / 32 * 8 + (size_t)K / 16 * 4 + (size_t)out_rows * 4;
+// the prologue mode of a GEMV's arguments
+static int norm_mode(const GemvArgs &a) {
+    return a.gss ? XN_GATED : a.norm_w ? (a.conv_w ? XN_RMS_CONV : XN_RMS) : 0;
 }
+
 
 // rows per lane group of a plan (the kernel's R)
 static int plan_r(const GemvArgs &a) { return a.rows_per_wg / (64 / a.lpr); }
@@ -793,8 +887,8 @@ static const void *gemv_q_fn_all(const GemvArgs &a) {
     for (int i = 1; i < a.nseg - 1; i++)
         if (a.seg[i].m.type != a.seg[0].m.type) return nullptr;
     const int t = a.seg[0].m.type, tl = a.seg[a.nseg - 1].m.type;
-    if (tl == t) return gemv_q_fn(t, false, a.norm_w != nullptr, a.K, plan_r(a));
-    return gemv_q_fn_mixed(t, tl, a.norm_w != nullptr, a.K, plan_r(a));
+    if (tl == t) return gemv_q_fn(t, false, norm_mode(a), a.K, plan_r(a));
+    return gemv_q_fn_mixed(t, tl, norm_mode(a), a.K, plan_r(a));
 }
 
 bool gemv_q_supported(const GemvArgs &a) {
@@ -806,6 +900,11 @@ bool gemv_q_supported(const GemvArgs &a) {
     if (a.mode == GEMV_SWIGLU && a.seg[0].m.type != a.seg[1].m.type) return false;
     // the x prologue holds K/16 chunks of three planes in LDS
     if (gemv_q_lds(a.K, 0) > 96 * 1024) return false;
+    // gated head norm prologue: x in registers, whole heads; conv epilogue: stored rows
+    if (a.gss && (!a.norm_w || a.mode == GEMV_SWIGLU || a.K > 4096 || a.K % GN_HV)) return false;
+    if (a.conv_w && (a.mode != GEMV_STORE || !a.norm_w || !a.conv_state || a.conv_kernel < 2 ||
+                     a.conv_kernel > 4 || a.K > 4096))
+        return false;
     return a.K % 256 == 0 || (a.K % 64 == 0 && a.seg[0].m.type == T_Q8_0 && n == 1);
 }
 
@@ -911,7 +1010,9 @@ static const void *gemv_q_moe_fn(int type, int moe, int K, bool norm) {
 }
 
 bool gemv_q_moe_supported(const GemvArgs &a, int moe) {
-    if ((a.norm_w && moe != MOE_ROWS) || a.moe_k < 1 || a.moe_k > WAVE || a.moe_n < 1 || a.moe_blk < 1) return false;
+    if ((a.norm_w && moe != MOE_ROWS) || a.gss || a.conv_w || a.moe_k < 1 || a.moe_k > WAVE || a.moe_n < 1 ||
+        a.moe_blk < 1)
+        return false;
     if (moe == MOE_ROWS) {
         if (a.mode != GEMV_SWIGLU || a.seg[0].m.rows != a.moe_k * a.moe_blk) return false;
         const int sel = a.moe_sel > 0 ? a.moe_sel : a.moe_k;
@@ -957,7 +1058,8 @@ hipError_t launch_gemv_q(const GemvArgs &a, hipStream_t st) {
         GemvArgs b = a;
         b.wg_base = a.seg[i].wg_begin;
         const int end = j < nseg ? a.seg[j].wg_begin : a.total_wgs;
-        const void *fn = gemv_q_fn(a.seg[i].m.type, sw, a.norm_w != nullptr, a.K, R);
+        const void *fn = gemv_q_fn(a.seg[i].m.type, sw, norm_mode(a), a.K, R);
+        if (!fn) return hipErrorInvalidValue;
         void *args[] = {(void *)&b};
         const hipError_t e = hipLaunchKernel(fn, dim3(end - b.wg_base), dim3(GW), args, lds, st);
         if (e != hipSuccess) return e;

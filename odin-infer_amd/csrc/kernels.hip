@@ -427,6 +427,7 @@ bool plan_gemv(GemvArgs &a) {
         plan_gemv_q(a);
         return true;
     }
+    if (a.gss || a.conv_w) return false;  // prologue / epilogue of gemv_q_kernel only
     a.kernel = 0;
     const int U = a.K / 64;
     int lpr = 1;

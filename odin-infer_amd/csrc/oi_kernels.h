@@ -102,6 +102,17 @@ struct GemvArgs {
     // GEMV_ADD: if set, the product is scaled by sigmoid(ygate[0]) before the add
     // (the shared expert's gate of a Qwen3-Next-style MoE layer)
     const float *ygate;
+    // gemv_q_kernel only.  gss set: the prologue finishes the gated RMSNorm of
+    // a DeltaNet layer's output per head of 128: x holds o silu(z), gss
+    // [heads][4] partial sums of o^2, x = norm_w[j] (inv_h x) with inv_h =
+    // 1 / sqrt(sum / 128 + eps) (norm_w [128]).  conv_w set (GEMV_STORE):
+    // segment 0's rows are the channels of the DeltaNet conv, stored as
+    // silu(conv) with conv_state [rows][conv_kernel - 1] slid (the in_qkv
+    // projection of the token step).
+    const float *gss;
+    const float *conv_w;
+    float *conv_state;
+    int32_t conv_kernel;
 };
 
 // Device state of the token loop (int32 x 8):
@@ -300,6 +311,12 @@ struct DnArgs {
     float *conv_out;               // scratch [conv_dim]
     float *out;                    // [n_vh hv]
     int32_t n_kh, n_vh, hk, hv, kernel;
+    // 1: the delta rule alone over (value head, 32 columns) workgroups, conv_out
+    // already holding the conv (the in_qkv GEMV's epilogue); out gets
+    // o silu(z) and ssq [n_vh][hv / 32] the sums of o^2 per workgroup (the
+    // output GEMV's prologue finishes the gated norm)
+    int32_t cols;
+    float *ssq;
 };
 hipError_t launch_deltanet(const DnArgs &a, hipStream_t st);
 
