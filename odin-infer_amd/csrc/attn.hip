@@ -42,11 +42,6 @@ struct AttnShape {
 };
 constexpr int ATTN_MAX_SPLITS = 1024;
 
-static __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
-    return v;
-}
 
 template <int HD, int G>
 __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
@@ -171,7 +166,7 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
             sc[p] = t < n ? ((acc[0] + acc[1]) + (acc[2] + acc[3])) / div : -INFINITY;
             m = fmaxf(m, sc[p]);
         }
-        m = wave_max(m);
+        m = wave_max_all(m);
         float l = 0.f;
 #pragma unroll
         for (int p = 0; p < S::PPL; p++) {
@@ -220,7 +215,10 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
 }
 
 // O_h = sum_s exp(m_s - M) o_s / sum_s exp(m_s - M) l_s  for one query head and
-// 64 of its dimensions; the 4 waves take every 4th split.
+// 64 of its dimensions; the 4 waves take every 4th split.  The o values of
+// the first 4 CMB_PF splits are requested together with the (m, l) pairs (one
+// memory round trip instead of two); longer caches read the rest afterwards.
+constexpr int CMB_PF = 20;
 template <int HD>
 __global__ __launch_bounds__(WG) void attn_combine_kernel(AttnArgs a) {
     using S = AttnShape<HD>;
@@ -233,6 +231,12 @@ __global__ __launch_bounds__(WG) void attn_combine_kernel(AttnArgs a) {
     const int nsplit = pos / S::CH + 1;
     const int stride = HD + 2;
     const float *pb = a.part + (size_t)h * a.max_splits * stride;
+    float ov[CMB_PF];
+#pragma unroll
+    for (int k = 0; k < CMB_PF; k++) {
+        const int s = wave + (WG / WAVE) * k;
+        ov[k] = s < nsplit ? pb[(size_t)s * stride + i] : 0.f;
+    }
     for (int s = tid; s < nsplit; s += WG) {
         wm[s] = pb[(size_t)s * stride + HD];
         wl[s] = pb[(size_t)s * stride + HD + 1];
@@ -241,7 +245,7 @@ __global__ __launch_bounds__(WG) void attn_combine_kernel(AttnArgs a) {
     if (wave == 0) {
         float M = -INFINITY;
         for (int s = lane; s < nsplit; s += WAVE) M = fmaxf(M, wm[s]);
-        M = wave_max(M);
+        M = wave_max_all(M);
         float L = 0.f;
         for (int s = lane; s < nsplit; s += WAVE) {
             const float f = expf(wm[s] - M);
@@ -253,8 +257,13 @@ __global__ __launch_bounds__(WG) void attn_combine_kernel(AttnArgs a) {
     }
     __syncthreads();
     float O = 0.f;
+#pragma unroll
+    for (int k = 0; k < CMB_PF; k++) {
+        const int s = wave + (WG / WAVE) * k;
+        if (s < nsplit) O += wm[s] * ov[k];
+    }
 #pragma unroll 8
-    for (int s = wave; s < nsplit; s += WG / WAVE) O += wm[s] * pb[(size_t)s * stride + i];
+    for (int s = wave + (WG / WAVE) * CMB_PF; s < nsplit; s += WG / WAVE) O += wm[s] * pb[(size_t)s * stride + i];
     ored[wave][lane] = O;
     __syncthreads();
     if (wave == 0) a.out[(size_t)h * HD + i] = ((ored[0][lane] + ored[1][lane]) + (ored[2][lane] + ored[3][lane])) / Ls;

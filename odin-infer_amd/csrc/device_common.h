@@ -54,18 +54,35 @@ static __device__ __forceinline__ float dpp_max8(float v) {  // max over aligned
     v = fmaxf(v, OI_DPP(v, 0x4E));
     return fmaxf(v, OI_DPP(v, 0x141));
 }
+// lane j's value (j uniform), read into a scalar register
+static __device__ __forceinline__ float lane_value(float v, int j) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
+}
 // sum over aligned groups of n lanes (n a power of two <= 64); every lane of
-// a group ends with the group's sum
+// a group ends with the group's sum.  Rows of 16 by DPP, then the rows' sums
+// read out of lanes 0, 16, 32, 48 and added as (r0 + r1) + (r2 + r3) (the
+// order of the two xor-16 / xor-32 butterfly steps, without their two LDS
+// round trips).  The whole wave must be active.
 static __device__ __forceinline__ float lane_group_sum(float v, int n) {
     if (n >= 2) v += OI_DPP(v, 0xB1);
     if (n >= 4) v += OI_DPP(v, 0x4E);
     if (n >= 8) v += OI_DPP(v, 0x141);
     if (n >= 16) v += OI_DPP(v, 0x140);
-    if (n >= 32) v += __shfl_xor(v, 16, WAVE);
-    if (n >= 64) v += __shfl_xor(v, 32, WAVE);
+    if (n >= 32) {
+        const float lo = lane_value(v, 0) + lane_value(v, 16), hi = lane_value(v, 32) + lane_value(v, 48);
+        v = n >= 64 ? lo + hi : (__lane_id() < 32 ? lo : hi);
+    }
     return v;
 }
 static __device__ __forceinline__ float wave_sum(float v) { return lane_group_sum(v, WAVE); }
+// maximum over the wave (whole wave active)
+static __device__ __forceinline__ float wave_max_all(float v) {
+    v = fmaxf(v, OI_DPP(v, 0xB1));
+    v = fmaxf(v, OI_DPP(v, 0x4E));
+    v = fmaxf(v, OI_DPP(v, 0x141));
+    v = fmaxf(v, OI_DPP(v, 0x140));
+    return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
+}
 
 // Qwen3.5 activations (qwen3_5/ops.odin:7-15 sigmoid: the branch keeps exp's
 // argument <= 0; silu = x sigmoid(x))
