@@ -963,7 +963,11 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     const char *pu = std::getenv("OI_PREFILL_UNFUSED");
     e->pf_fused = !(pu && pu[0] == '1');
     const char *pm = std::getenv("OI_PREFILL_EXPERTS");  // "gemv" / "f32": the other expert kernels (tests)
-    e->pf_experts = !pm ? 0 : std::strcmp(pm, "gemv") == 0 ? 1 : std::strcmp(pm, "f32") == 0 ? 2 : 0;
+    e->pf_experts = !pm                            ? 0
+                    : std::strcmp(pm, "gemv") == 0  ? 1
+                    : std::strcmp(pm, "f32") == 0   ? 2
+                    : std::strcmp(pm, "wide") == 0  ? 3
+                                                    : 0;
     const char *pc = std::getenv("OI_PREFILL_DN_CHUNK");  // "16" / "32": the chunked delta rule in prefill
     e->pf_dn_chunk = !pc ? 0 : std::strcmp(pc, "16") == 0 ? 16 : std::strcmp(pc, "32") == 0 ? 32 : 0;
 
@@ -1088,16 +1092,17 @@ int prefill_alloc(oi_engine *e) {
     if (moe) {
         const size_t rg = (size_t)mt_gemv_tile_rows((int32_t)D, (int32_t)EF), rd = (size_t)mt_gemv_tile_rows((int32_t)EF, (int32_t)D);
         tg = std::max((EF + rg - 1) / rg * (NE + (T * KP + MT_PAIR_SLICE - 1) / MT_PAIR_SLICE),
-                      (EF + MT_MFMA_ROWS - 1) / MT_MFMA_ROWS * (NE + (T * KP + MT_MFMA_PAIRS - 1) / MT_MFMA_PAIRS));
+                      (EF + MT_MFMA_ROWS - 1) / MT_MFMA_ROWS * (NE + (T * KP + MT_MFMA_FEW - 1) / MT_MFMA_FEW));
         td = std::max((D + rd - 1) / rd * (NE + (T * KP + MT_PAIR_SLICE - 1) / MT_PAIR_SLICE),
-                      (D + MT_MFMA_ROWS - 1) / MT_MFMA_ROWS * (NE + (T * KP + MT_MFMA_PAIRS - 1) / MT_MFMA_PAIRS));
+                      (D + MT_MFMA_ROWS - 1) / MT_MFMA_ROWS * (NE + (T * KP + MT_MFMA_FEW - 1) / MT_MFMA_FEW));
     }
     std::vector<size_t> sizes = {T * 4, T * D * 4, T * QD * 4 * 2, xb, need[0], need[1], need[2], need[3],
                                  full ? T * QD * 4 : 0,
                                  lin ? T * CD * 4 : 0, lin ? T * 2 * KD * 4 : 0, lin ? T * 3 * (size_t)e->lin_nv * 4 : 0,
                                  lin ? T * VD * 4 : 0,
                                  moe ? T * D * 4 : 0, moe ? T * (size_t)e->n_experts * 4 : 0,
-                                 moe ? T * KP * 4 : 0, moe ? T * KP * EF * 4 : 0, moe ? T * KP * D * 4 : 0,
+                                 moe ? T * KP * 4 : 0, moe ? T * KP * EF * 4 : 0, moe ? T * KP * EF * 4 : 0,
+                                 moe ? T * KP * D * 4 : 0,
                                  moe ? T * KP * 4 : 0, moe ? T * KP * 4 : 0, moe ? NE * 4 : 0, moe ? NE * 4 : 0,
                                  moe ? NE * 4 : 0, 8 * tg, 8 * td, moe ? (size_t)8 : 0};
     size_t total = 0;
@@ -1127,6 +1132,7 @@ int prefill_alloc(oi_engine *e) {
     e->pf_lg = (float *)take();
     e->pf_w = (float *)take();
     e->pf_h = (float *)take();
+    e->pf_h2 = (float *)take();
     e->pf_yd = (float *)take();
     e->pf_ids = (int32_t *)take();
     e->pf_list = (int32_t *)take();
@@ -1167,7 +1173,12 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
     const bool mm = e->pf_experts != 1 && mt_mfma_supported(L.gexp, D, EF) && mt_mfma_supported(L.uexp, D, EF) &&
                     L.gexp.type == L.uexp.type && mt_mfma_supported(L.dexp, EF, D);
     const int tr_gu = mm ? MT_MFMA_ROWS : mt_gemv_tile_rows(D, EF), tr_dn = mm ? MT_MFMA_ROWS : mt_gemv_tile_rows(EF, D);
-    const int ps = mm ? MT_MFMA_PAIRS : MT_PAIR_SLICE;
+    // few pairs per expert (a short chunk: ~1.4 at 64 tokens of top 10 of 512):
+    // items of MT_MFMA_FEW pairs with the x rows staged once
+    const bool few = mm && e->pf_experts == 0 && L.gexp.type == T_Q4_K && L.dexp.type == T_Q4_K &&
+                     pairs <= MT_MFMA_FEW * NE && D <= 4096 && EF <= 4096 && D % MT_MFMA_ROWS == 0 &&
+                     EF % MT_MFMA_ROWS == 0;
+    const int ps = few ? MT_MFMA_FEW : mm ? MT_MFMA_PAIRS : MT_PAIR_SLICE;
     PfMoeArgs ma{};
     ma.logits = e->pf_lg;
     if (L.shared) ma.sh_inp = L.sh_inp;
@@ -1180,8 +1191,8 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
     ma.out = e->pf_p[0];
     ma.T = T; ma.n_experts = E; ma.top_k = (int32_t)e->top_k; ma.kp = KP;
     ma.norm_topk = 1;  // Qwen3-MoE / Qwen3-Next renormalize the chosen weights
-    ma.tiles_gu = (EF + tr_gu - 1) / tr_gu;
-    ma.tiles_dn = (D + tr_dn - 1) / tr_dn;
+    ma.tiles_gu = few ? 1 : (EF + tr_gu - 1) / tr_gu;  // a few-pair item covers every row tile
+    ma.tiles_dn = few ? 1 : (D + tr_dn - 1) / tr_dn;
     ma.dim = D;
     ma.pair_slice = ps;
     HIP_TRY(launch_pf_moe_route(ma, st));
@@ -1191,6 +1202,10 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
     g.swiglu = 1;
     g.K = D; g.rows = EF; g.xdiv = KP; g.tile_rows = tr_gu;
     g.x = e->pf_xn; g.y = e->pf_h;
+    if (few) {  // gate rows to pf_h, up rows to pf_h2; the down launch applies the SwiGLU
+        g.y2 = e->pf_h2;
+        g.tiles = 1;
+    }
     g.list = e->pf_list; g.off = e->pf_off; g.cnt = e->pf_cnt;
     g.items = e->pf_items_gu; g.nitems = e->pf_nitems;
     g.pair_slice = ps;
@@ -1200,6 +1215,10 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
     d.m = L.dexp;
     d.K = EF; d.rows = D; d.xdiv = 1; d.tile_rows = tr_dn;
     d.x = e->pf_h; d.y = e->pf_yd;
+    if (few) {
+        d.x2 = e->pf_h2;
+        d.tiles = 1;
+    }
     d.list = e->pf_list; d.off = e->pf_off; d.cnt = e->pf_cnt;
     d.items = e->pf_items_dn; d.nitems = e->pf_nitems + 1;
     d.pair_slice = ps;

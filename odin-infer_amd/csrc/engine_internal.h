@@ -105,11 +105,12 @@ struct oi_engine {
     float *pf_gate = nullptr;
     float *pf_conv = nullptr, *pf_qk = nullptr, *pf_gates = nullptr, *pf_o = nullptr;
     float *pf_xn = nullptr, *pf_lg = nullptr, *pf_w = nullptr, *pf_h = nullptr, *pf_yd = nullptr;
+    float *pf_h2 = nullptr;  // up rows of the routed experts (few-pair items)
     int32_t *pf_ids = nullptr, *pf_list = nullptr, *pf_off = nullptr, *pf_cnt = nullptr, *pf_fill = nullptr;
     int32_t *pf_items_gu = nullptr, *pf_items_dn = nullptr, *pf_nitems = nullptr;
     bool pf_fused = true;  // gate/up GEMM with the SwiGLU epilogue where it applies (OI_PREFILL_UNFUSED=1: off)
     int pf_experts = 0;  // routed experts of a prefill: 0 the default kernels, 1 the multi-token GEMV, 2 f32 MFMA
-                         // only (OI_PREFILL_EXPERTS=gemv / f32)
+                         // only, 3 no few-pair items (OI_PREFILL_EXPERTS=gemv / f32 / wide)
     bool dn_fused = false;  // token loop: the one-launch DeltaNet step instead of the split one (OI_DN_FUSED)
     int pf_dn_chunk = 0;  // delta rule of a prefill chunk: 0 token by token, 16 / 32 chunked (OI_PREFILL_DN_CHUNK)
 };

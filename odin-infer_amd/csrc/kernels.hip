@@ -1121,6 +1121,158 @@ __global__ __launch_bounds__(WG) void mt_q4mfma_kernel(MtGemvArgs a) {
     }
 }
 
+// mt_q4mfma_kernel for items of at most MF_PAIRS pairs (a short chunk
+// spreads its pairs over many experts: ~1.4 per expert at 64 tokens of top 10
+// of 512).  An item is (expert, pair slice) and one matrix: the workgroup
+// streams ALL row tiles of that matrix for its pairs (the item's descriptor,
+// pair lists and x rows are read once, then the weights stream without a
+// break: a step is one 256-wide chunk of K of one 64-row tile, and the next
+// step's weights are in flight while the current one is computed, across tile
+// boundaries).  The x rows of the item's pairs are staged in LDS once for the
+// whole K (hi / lo halves and the f32 sums per 32); with x2 set they are
+// silu(x) * x2 (the SwiGLU of separately computed gate and up rows, the
+// reference's order).  A SwiGLU pair runs as two halves of the grid (blocks
+// past mat_items take m2 into y2), so one matrix's registers fit three waves
+// per SIMD.  The sub-block scales of a step go through the wave's own LDS
+// rows (written by the header lanes, read after a wave barrier: a wave's DS
+// operations complete in order).
+constexpr int MF_PAIRS = MT_MFMA_FEW;
+template <int KC>
+__global__ __launch_bounds__(WG) void mt_q4mfma_few_kernel(MtGemvArgs a) {
+#pragma clang fp contract(off)
+    constexpr int NU = KC / 64, NS = KC / 256, NB = KC / 32;
+    extern __shared__ __attribute__((aligned(16))) uint16_t mf_smem[];
+    __shared__ __attribute__((aligned(16))) float scl[WG / WAVE][16][2 * NB];  // (d, m) per sub-block of a row
+    const bool second = a.mat_items > 0 && (int)blockIdx.x >= a.mat_items;
+    const int it = second ? (int)blockIdx.x - a.mat_items : (int)blockIdx.x;
+    if (it >= *a.nitems) return;
+    const int XP = a.K + 8;
+    uint16_t *xh = mf_smem, *xl = mf_smem + MF_PAIRS * XP;
+    float *sx = (float *)(mf_smem + 2 * MF_PAIRS * XP);  // [MF_PAIRS][K / 32]
+    const int e = a.items[2 * it], slice = a.items[2 * it + 1] >> 16;
+    const int base = a.off[e] + slice * MF_PAIRS, n = min(MF_PAIRS, a.cnt[e] - slice * MF_PAIRS);
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE, i16 = lane & 15, g = lane >> 4;
+    const DMat m = sub_rows(second ? a.m2 : a.m, e * a.rows, a.rows);
+    float *y = second ? a.y2 : a.y;
+    const int U = a.K >> 6, nch = a.K / KC, K32 = a.K / 32;
+    const int ntile = a.rows / MM_ROWS, nstep = ntile * nch;  // rows % 64 == 0
+    constexpr int NSTG = 4;  // ring stages: three steps in flight while one is computed
+    uint32_t qw[NSTG][NU][2];  // [stage][unit][word]
+    u32x4 hd[NSTG][NS];
+    // the same loads in every call (a step past the end re-reads the last one),
+    // so that the compiler waits for exactly the stage it consumes
+    auto issue = [&](int st, int stg) {
+        const int ss = min(st, nstep - 1), c = ss % nch, r = (ss / nch) * MM_ROWS + 16 * wave + i16;
+#pragma unroll
+        for (int k = 0; k < NU; k++) {
+            const size_t ui = (size_t)r * U + c * (KC / 64) + k;
+            const u32x2 q = *(const u32x2 *)(m.q + (g >> 1) * m.plane + ui * 16 + 8 * (g & 1));
+            qw[stg][k][0] = q.x;
+            qw[stg][k][1] = q.y;
+        }
+#pragma unroll
+        for (int k = 0; k < NS; k++) hd[stg][k] = *(const u32x4 *)(m.s + ((size_t)r * (m.cols >> 8) + c * NS + k) * 16);
+    };
+#pragma unroll
+    for (int i = 0; i < NSTG - 1; i++) issue(i, i);
+    // x rows of the item's pairs for the whole K, 8 elements per step
+    for (int idx = threadIdx.x; idx < n * (a.K / 8); idx += WG) {
+        const int j = idx / (a.K / 8), c8 = idx % (a.K / 8);
+        const size_t xo = (size_t)(a.list[base + j] / a.xdiv) * a.K + 8 * c8;
+        const float4 *xr = (const float4 *)(a.x + xo);
+        const float4 p0 = xr[0], p1 = xr[1];
+        float v[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+        if (a.x2) {  // SwiGLU: v = silu(gate) * up (infer/forward.odin:188-193)
+            const float4 *ur = (const float4 *)(a.x2 + xo);
+            const float4 u0 = ur[0], u1 = ur[1];
+            const float u[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                v[q] *= 1.0f / (1.0f + expf(-v[q]));
+                v[q] *= u[q];
+            }
+        }
+        uint32_t hw[4], lw[4];
+        float s8 = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint16_t h0 = f2h(v[2 * q]), h1 = f2h(v[2 * q + 1]);
+            const uint16_t l0 = f2h(v[2 * q] - h2f(h0)), l1 = f2h(v[2 * q + 1] - h2f(h1));
+            hw[q] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+            lw[q] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+            s8 += v[2 * q] + v[2 * q + 1];
+        }
+        // the 32 elements of one sub-block: four consecutive c8 of one pair
+        // (n * K / 8 is a multiple of 4, so whole groups of 4 threads run here)
+        s8 = dpp_sum4(s8);
+        *(u32x4 *)&xh[j * XP + 8 * c8] = u32x4{hw[0], hw[1], hw[2], hw[3]};
+        *(u32x4 *)&xl[j * XP + 8 * c8] = u32x4{lw[0], lw[1], lw[2], lw[3]};
+        if ((c8 & 3) == 0) sx[j * K32 + c8 / 4] = s8;
+    }
+    __syncthreads();
+    const int p = i16 < n ? a.list[base + i16] : 0;
+    mm_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](int st, int stg) {
+        const int c = st % nch;
+        if (g == 0) {  // (d1, m1) of every sub-block of this row in the chunk
+#pragma unroll
+            for (int k = 0; k < NS; k++) {
+                const float d = h2f(hd[stg][k].x & 0xFFFFu), dmin = h2f(hd[stg][k].x >> 16);
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    uint32_t sc0, m0, sc1, m1;
+                    q4k_scales(q, hd[stg][k].y, hd[stg][k].z, hd[stg][k].w, sc0, m0, sc1, m1);
+                    *(float4 *)&scl[wave][i16][2 * (8 * k + 2 * q)] =
+                        make_float4(d * (float)sc0, dmin * (float)m0, d * (float)sc1, dmin * (float)m1);
+                }
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int k = 0; k < NU; k++) {
+#pragma unroll
+            for (int sb = 0; sb < 2; sb++) {
+                const int b = 2 * k + sb, kx = c * KC + 32 * b + 8 * g;  // this lane's K positions
+                u32x4 bh = {0u, 0u, 0u, 0u}, bl = {0u, 0u, 0u, 0u};
+                float sxv = 0.f;
+                if (i16 < n) {
+                    bh = *(const u32x4 *)&xh[i16 * XP + kx];
+                    bl = *(const u32x4 *)&xl[i16 * XP + kx];
+                    sxv = sx[i16 * K32 + c * NB + b];
+                }
+                const mq_h8 A = nibbles_h8(qw[stg][k][0], qw[stg][k][1], sb == 1);
+                mm_f32x4 t = {0.f, 0.f, 0.f, 0.f};
+                t = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(mq_h8, bh), t, 0, 0, 0);
+                t = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(mq_h8, bl), t, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float2 dm = *(const float2 *)&scl[wave][4 * g + r][2 * b];
+                    acc[r] += dm.x * t[r] - dm.y * sxv;
+                }
+            }
+        }
+        __builtin_amdgcn_wave_barrier();  // the scale reads are done before the next step writes them
+        if (c == nch - 1) {  // the tile's rows are complete
+            if (i16 < n) {
+                const int row0 = (st / nch) * MM_ROWS + 16 * wave + 4 * g;
+#pragma unroll
+                for (int r = 0; r < 4; r++) y[(size_t)p * a.rows + row0 + r] = acc[r];
+            }
+            acc = mm_f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    // NSTG steps per pass, so each stage index is static; every pass issues
+    // the same loads (clamped to the last step), only the computation stops
+    // at the end
+    for (int st = 0; st < nstep; st += NSTG) {
+#pragma unroll
+        for (int j = 0; j < NSTG; j++) {
+            issue(st + j + NSTG - 1, (j + NSTG - 1) % NSTG);
+            if (st + j < nstep) compute(st + j, j);
+        }
+    }
+}
+
 bool mt_mfma_supported(const DMat &m, int32_t K, int32_t rows) {
     return (m.type == T_Q4_K || m.type == T_Q6_K || m.type == T_Q8_0) && m.cols == K && K % MM_KC == 0 &&
            rows % 16 == 0;
@@ -1129,8 +1281,20 @@ bool mt_mfma_supported(const DMat &m, int32_t K, int32_t rows) {
 hipError_t launch_mt_mfma(const MtGemvArgs &a, int max_items, hipStream_t st, bool f32_only) {
     if (!mt_mfma_supported(a.m, a.K, a.rows) || (a.swiglu && (!mt_mfma_supported(a.m2, a.K, a.rows) ||
                                                               a.m2.type != a.m.type)) ||
-        a.tile_rows != MM_ROWS || a.pair_slice != MM_PAIRS || a.xdiv <= 0 || max_items <= 0 || a.dense_n > 0)
+        a.tile_rows != MM_ROWS || (a.pair_slice != MM_PAIRS && a.pair_slice != MF_PAIRS) || a.xdiv <= 0 ||
+        max_items <= 0 || a.dense_n > 0)
         return hipErrorInvalidValue;
+    if (a.pair_slice == MF_PAIRS) {  // few pairs per item: Q4_K, x staged whole, every row tile per item
+        const size_t lds = (size_t)MF_PAIRS * (a.K + 8) * 4 + (size_t)MF_PAIRS * (a.K / 32) * 4;
+        if (a.m.type != T_Q4_K || f32_only || lds > 96 * 1024 || a.rows % MM_ROWS || a.tiles != 1 ||
+            (a.swiglu && !a.y2))
+            return hipErrorInvalidValue;
+        MtGemvArgs b = a;
+        b.mat_items = a.swiglu ? max_items : 0;  // gate into y, up into y2 (the SwiGLU is the consumer's)
+        const dim3 grid((unsigned)(a.swiglu ? 2 * max_items : max_items));
+        hipLaunchKernelGGL(mt_q4mfma_few_kernel<MM_KC>, grid, dim3(WG), lds, st, b);
+        return hipGetLastError();
+    }
     if (a.m.type == T_Q4_K && !f32_only) {
         const dim3 grid((unsigned)max_items);
         hipLaunchKernelGGL(mt_q4mfma_kernel<MM_KC>, grid, dim3(WG), 0, st, a);  // 512: 256 VGPRs, slower

@@ -268,6 +268,12 @@ struct MtGemvArgs {
     float *y;                      // output rows [pairs][rows]
     const int32_t *list, *off, *cnt;  // pairs by expert: list[off[e] .. off[e] + cnt[e])
     const int32_t *items, *nitems; // work items [2]: expert, pair slice << 16 | row tile; their count
+    // items of MT_MFMA_FEW pairs only: a SwiGLU pair writes gate rows to y and
+    // up rows to y2 (set by the launcher: blocks from mat_items on take m2);
+    // x2 set: the x rows are silu(x) * x2 (the SwiGLU of such gate and up rows)
+    float *y2;
+    const float *x2;
+    int32_t mat_items;
 };
 // dense_n > 0: one "expert" (e = 0) holding pairs 0 .. dense_n-1, no lists (a
 // plain multi-token GEMV); item it = slice * tiles + row tile, max_items =
@@ -281,6 +287,13 @@ hipError_t launch_mt_gemv(const MtGemvArgs &a, int max_items, hipStream_t st);
 // weights exact (raw quants, scales per 32 in f32, x split hi + lo) unless
 // f32_only, the others (and f32_only) on f32 MFMA of the decoded weights
 constexpr int MT_MFMA_PAIRS = 16, MT_MFMA_ROWS = 64;
+// items of at most MT_MFMA_FEW pairs (pair_slice == MT_MFMA_FEW, tiles == 1: an
+// item covers every row tile): Q4_K only, the x rows staged once for the whole
+// K (K <= ~5600), the weights streaming through all row tiles with the next
+// step in flight; for chunks whose pairs spread thinly over the experts.  A
+// SwiGLU pair leaves gate in y and up in y2; the down launch applies the
+// SwiGLU to its x rows (x2 = up)
+constexpr int MT_MFMA_FEW = 4;
 bool mt_mfma_supported(const DMat &m, int32_t K, int32_t rows);
 hipError_t launch_mt_mfma(const MtGemvArgs &a, int max_items, hipStream_t st, bool f32_only = false);
 struct PfMoeArgs {

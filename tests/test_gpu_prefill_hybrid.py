@@ -152,26 +152,28 @@ def test_prefill_split_calls_agree(make_model):
         infer.engine_destroy(e2)
 
 
-@pytest.mark.parametrize("shape", ["c5", "c4"])
-def test_prefill_expert_kernels_agree(tmp_path, monkeypatch, shape):
-    """The routed experts of a chunk on the three expert kernels: Q4_K quants
-    on f16 MFMA with the scales applied per 32 weights in f32 and x split
-    hi + lo (the default for Q4_K experts), the decoded weights on f32 MFMA
-    (OI_PREFILL_EXPERTS=f32, the default for Q6_K / Q8_0) and the
-    multi-token GEMV (OI_PREFILL_EXPERTS=gemv): the same f32 arithmetic up to
-    the order of the sums and x to ~2^-22.  One layer of the config 5 /
-    config 4 shapes, so nothing staged in f16 follows the experts (a later
-    staged projection would turn a 1e-7 difference into ~1e-4 at its rounding
-    boundaries): the last logits agree within 1e-5."""
+@pytest.mark.parametrize("shape,n", [("c5", 200), ("c5", 64), ("c4", 200), ("c4", 48)])
+def test_prefill_expert_kernels_agree(tmp_path, monkeypatch, shape, n):
+    """The routed experts of a chunk on the expert kernels: Q4_K quants on f16
+    MFMA with the scales applied per 32 weights in f32 and x split hi + lo,
+    in items of up to 4 pairs with x staged whole (the default when the
+    chunk's pairs average at most 4 per expert: 64 tokens at C5, 48 at C4) or
+    of up to 16 pairs (the default otherwise; OI_PREFILL_EXPERTS=wide), the
+    decoded weights on f32 MFMA (OI_PREFILL_EXPERTS=f32, the default for
+    Q6_K / Q8_0) and the multi-token GEMV (OI_PREFILL_EXPERTS=gemv): the same
+    f32 arithmetic up to the order of the sums and x to ~2^-22.  One layer of
+    the config 5 / config 4 shapes, so nothing staged in f16 follows the
+    experts (a later staged projection would turn a 1e-7 difference into
+    ~1e-4 at its rounding boundaries): the last logits agree within 1e-5."""
     from oi import synth
     spec = (synth._hybrid(2048, 512, 1, 16, 2, 256, 4096, 4096, 64, 16, 32, 128, experts=512, used=10, eff=512,
                           shared=512, interval=2, seed=47) if shape == "c5" else
             synth._moe(2048, 1, 32, 4, 4096, 4096, 128, 8, 768, seed=37))
     path = tmp_path / ("%s.gguf" % shape)
     synth.write_gguf(path, spec)
-    toks = _tokens(13, 200, 4096)
+    toks = _tokens(13, n, 4096)
     out = {}
-    for kind in ("default", "f32", "gemv"):
+    for kind in ("default", "wide", "f32", "gemv"):
         monkeypatch.setenv("OI_PREFILL_EXPERTS", kind)
         e, ok = infer.engine_load(str(path), infer.Engine_Opts(max_ctx=256))
         assert ok
@@ -179,9 +181,9 @@ def test_prefill_expert_kernels_agree(tmp_path, monkeypatch, shape):
             out[kind] = infer.engine_forward_batch(e, toks, 0).copy()
         finally:
             infer.engine_destroy(e)
-    for kind in ("f32", "gemv"):
+    for kind in ("wide", "f32", "gemv"):
         err = scaled_err(out["default"], out[kind])
-        print("%s: default vs %s experts %.3g" % (shape, kind, err))
+        print("%s n=%d: default vs %s experts %.3g" % (shape, n, kind, err))
         assert err <= 1e-5, kind
 
 
