@@ -967,6 +967,7 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
                     : std::strcmp(pm, "gemv") == 0  ? 1
                     : std::strcmp(pm, "f32") == 0   ? 2
                     : std::strcmp(pm, "wide") == 0  ? 3
+                    : std::strcmp(pm, "fewmfma") == 0 ? 4
                                                     : 0;
     const char *pc = std::getenv("OI_PREFILL_DN_CHUNK");  // "16" / "32": the chunked delta rule in prefill
     e->pf_dn_chunk = !pc ? 0 : std::strcmp(pc, "16") == 0 ? 16 : std::strcmp(pc, "32") == 0 ? 32 : 0;
@@ -1175,7 +1176,8 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
     const int tr_gu = mm ? MT_MFMA_ROWS : mt_gemv_tile_rows(D, EF), tr_dn = mm ? MT_MFMA_ROWS : mt_gemv_tile_rows(EF, D);
     // few pairs per expert (a short chunk: ~1.4 at 64 tokens of top 10 of 512):
     // items of MT_MFMA_FEW pairs with the x rows staged once
-    const bool few = mm && e->pf_experts == 0 && L.gexp.type == T_Q4_K && L.dexp.type == T_Q4_K &&
+    const bool few = mm && (e->pf_experts == 0 || e->pf_experts == 4) && L.gexp.type == T_Q4_K &&
+                     L.dexp.type == T_Q4_K &&
                      pairs <= MT_MFMA_FEW * NE && D <= 4096 && EF <= 4096 && D % MT_MFMA_ROWS == 0 &&
                      EF % MT_MFMA_ROWS == 0;
     const int ps = few ? MT_MFMA_FEW : mm ? MT_MFMA_PAIRS : MT_PAIR_SLICE;
@@ -1209,8 +1211,12 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
     g.list = e->pf_list; g.off = e->pf_off; g.cnt = e->pf_cnt;
     g.items = e->pf_items_gu; g.nitems = e->pf_nitems;
     g.pair_slice = ps;
-    HIP_TRY(mm ? launch_mt_mfma(g, item_tiles * ma.tiles_gu, st, e->pf_experts == 2)
-               : launch_mt_gemv(g, item_tiles * ma.tiles_gu, st));
+    // few pairs: the int8 dot4 kernel where the shapes allow it (not OI_PREFILL_EXPERTS=fewmfma)
+    const bool dot4 = few && e->pf_experts == 0 && mt_dot4_supported(L.gexp, D, EF) &&
+                      mt_dot4_supported(L.uexp, D, EF) && mt_dot4_supported(L.dexp, EF, D);
+    HIP_TRY(dot4 ? launch_mt_dot4(g, item_tiles, st)
+            : mm ? launch_mt_mfma(g, item_tiles * ma.tiles_gu, st, e->pf_experts == 2)
+                 : launch_mt_gemv(g, item_tiles * ma.tiles_gu, st));
     MtGemvArgs d{};
     d.m = L.dexp;
     d.K = EF; d.rows = D; d.xdiv = 1; d.tile_rows = tr_dn;
@@ -1222,8 +1228,9 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
     d.list = e->pf_list; d.off = e->pf_off; d.cnt = e->pf_cnt;
     d.items = e->pf_items_dn; d.nitems = e->pf_nitems + 1;
     d.pair_slice = ps;
-    HIP_TRY(mm ? launch_mt_mfma(d, item_tiles * ma.tiles_dn, st, e->pf_experts == 2)
-               : launch_mt_gemv(d, item_tiles * ma.tiles_dn, st));
+    HIP_TRY(dot4 ? launch_mt_dot4(d, item_tiles, st)
+            : mm ? launch_mt_mfma(d, item_tiles * ma.tiles_dn, st, e->pf_experts == 2)
+                 : launch_mt_gemv(d, item_tiles * ma.tiles_dn, st));
     HIP_TRY(launch_pf_moe_combine(ma, st));
     return OI_OK;
 }

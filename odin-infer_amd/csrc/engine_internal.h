@@ -110,7 +110,8 @@ struct oi_engine {
     int32_t *pf_items_gu = nullptr, *pf_items_dn = nullptr, *pf_nitems = nullptr;
     bool pf_fused = true;  // gate/up GEMM with the SwiGLU epilogue where it applies (OI_PREFILL_UNFUSED=1: off)
     int pf_experts = 0;  // routed experts of a prefill: 0 the default kernels, 1 the multi-token GEMV, 2 f32 MFMA
-                         // only, 3 no few-pair items (OI_PREFILL_EXPERTS=gemv / f32 / wide)
+                         // only, 3 no few-pair items, 4 few-pair items on MFMA (OI_PREFILL_EXPERTS=gemv / f32 /
+                         // wide / fewmfma)
     bool dn_fused = false;  // token loop: the one-launch DeltaNet step instead of the split one (OI_DN_FUSED)
     int pf_dn_chunk = 0;  // delta rule of a prefill chunk: 0 token by token, 16 / 32 chunked (OI_PREFILL_DN_CHUNK)
 };

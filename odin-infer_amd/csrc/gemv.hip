@@ -1068,4 +1068,130 @@ hipError_t launch_gemv_q(const GemvArgs &a, hipStream_t st) {
     return hipSuccess;
 }
 
+// ------------------------------------ routed experts of a short prefill chunk
+// mt_dot4_kernel: the token loop's int8 dot4 arithmetic over the few pairs
+// (<= MT_MFMA_FEW) of one expert slice.  An item is (expert, pair slice, one
+// matrix); its workgroup (4 waves) streams every row of that matrix.  The
+// prologue quantizes each pair's x row (silu(x) * x2 when x2 is set) into the
+// three int8 planes in LDS, as the decode GEMV's prologue does for its one x;
+// then a lane owns one 64-weight unit of MD_R rows per step (lpr = K / 64
+// lanes per row) and dots them with each pair's planes in turn (x read from
+// LDS once per step and pair, for MD_R rows).  The
+// next three steps' weights are in flight while one is computed.
+// Results: the f32 dot product up to the order of the sums and x to 2^-22 of
+// its group maximum (the decode GEMV's bound).
+constexpr int MD_R = 2;
+template <int LPR>
+__global__ __launch_bounds__(WG) void mt_dot4_kernel(MtGemvArgs a) {
+    extern __shared__ __attribute__((aligned(16))) u32x4 md_smem[];
+    constexpr int NP = MT_MFMA_FEW, NWV = WG / WAVE, GPW = WAVE / LPR;  // lane groups per wave
+    const bool second = a.mat_items > 0 && (int)blockIdx.x >= a.mat_items;
+    const int it = second ? (int)blockIdx.x - a.mat_items : (int)blockIdx.x;
+    if (it >= *a.nitems) return;
+    const int K = a.K, U = K >> 6;  // U == LPR: one unit per lane
+    const int e = a.items[2 * it], slice = a.items[2 * it + 1] >> 16;
+    const int base = a.off[e] + slice * NP, n = min(NP, a.cnt[e] - slice * NP);
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid / WAVE, grp = lane / LPR, j = lane % LPR;
+    const DMat m = sub_rows(second ? a.m2 : a.m, e * a.rows, a.rows);
+    float *y = second ? a.y2 : a.y;
+    // per pair: planes [3][K/16] chunks, then xs, s32 [K/32], s16 [K/16]
+    const int pstride = 3 * (K / 16) + (K / 32 * 2 + K / 16) / 4;  // in u32x4
+    auto xq = [&](int pj) {
+        u32x4 *b = md_smem + pj * pstride;
+        float *f = (float *)(b + 3 * (K / 16));
+        return XQ{b, b + K / 16, b + 2 * (K / 16), f, f + K / 32, f + K / 16};
+    };
+    // the first step's weights, then x (the loads are independent)
+    const int rows_step = GPW * MD_R, nstep = a.rows / (rows_step * NWV);  // rows % (rows_step * NWV) == 0
+    constexpr int NSTG = 4;  // ring stages: three steps in flight while one is computed
+    WQ4K ring[NSTG][MD_R];
+    auto issue = [&](int st, WQ4K (&w)[MD_R]) {
+        const int s2 = min(st, nstep - 1), r0 = (s2 * NWV + wave) * rows_step + grp * MD_R;
+#pragma unroll
+        for (int r = 0; r < MD_R; r++) wload(m, r0 + r, j, w[r]);
+    };
+#pragma unroll
+    for (int i = 0; i < NSTG - 1; i++) issue(i, ring[i]);
+    for (int pj = 0; pj < n; pj++) {
+        const XQ q = xq(pj);
+        const size_t xo = (size_t)(a.list[base + pj] / a.xdiv) * K;
+        for (int c = tid; c < K / 4; c += WG) {  // K / 4 float4, groups of 8 threads
+            float4 v = ((const float4 *)(a.x + xo))[c];
+            if (a.x2) {  // SwiGLU (infer/forward.odin:188-193)
+#pragma clang fp contract(off)
+                const float4 u = ((const float4 *)(a.x2 + xo))[c];
+                v.x *= 1.0f / (1.0f + expf(-v.x));
+                v.y *= 1.0f / (1.0f + expf(-v.y));
+                v.z *= 1.0f / (1.0f + expf(-v.z));
+                v.w *= 1.0f / (1.0f + expf(-v.w));
+                v.x *= u.x;
+                v.y *= u.y;
+                v.z *= u.z;
+                v.w *= u.w;
+            }
+            quant4(v, c, (uint32_t *)q.hi, (uint32_t *)q.mid, (uint32_t *)q.lo, (float *)q.xs, (float *)q.s32,
+                   (float *)q.s16);
+        }
+    }
+    // results [pair][row] in LDS, written out coalesced at the end (stores in
+    // the loop would share the memory counter with the weight loads)
+    float *yl = (float *)(md_smem + NP * pstride);
+    __syncthreads();
+    auto compute = [&](int st, const WQ4K (&w)[MD_R]) {
+        const int r0 = (st * NWV + wave) * rows_step + grp * MD_R;
+#pragma unroll 1
+        for (int pj = 0; pj < n; pj++) {  // one pair's x slice live at a time
+            XU4K xu;
+            xload(xq(pj), j, xu);
+            float acc[MD_R];
+#pragma unroll
+            for (int r = 0; r < MD_R; r++) acc[r] = lane_group_sum(wdot(w[r], j, xu), LPR);
+            if (j == 0) {
+#pragma unroll
+                for (int r = 0; r < MD_R; r++) yl[pj * a.rows + r0 + r] = acc[r];
+            }
+        }
+    };
+    // NSTG steps per pass, so each stage index is static; every pass issues
+    // the same loads (clamped to the last step), only the computation stops
+    for (int st = 0; st < nstep; st += NSTG) {
+#pragma unroll
+        for (int i = 0; i < NSTG; i++) {
+            issue(st + i + NSTG - 1, ring[(i + NSTG - 1) % NSTG]);
+            if (st + i < nstep) compute(st + i, ring[i]);
+        }
+    }
+    __syncthreads();
+    for (int pj = 0; pj < n; pj++) {
+        float *yr = y + (size_t)a.list[base + pj] * a.rows;
+        for (int r = tid; r < a.rows; r += WG) yr[r] = yl[pj * a.rows + r];
+    }
+}
+
+bool mt_dot4_supported(const DMat &m, int32_t K, int32_t rows) {
+    const int U = K / 64;
+    return m.type == T_Q4_K && m.cols == K && K % 256 == 0 && (U == 8 || U == 16 || U == 32 || U == 64) &&
+           rows % ((WAVE / U) * MD_R * (WG / WAVE)) == 0 && K <= 4096;
+}
+
+hipError_t launch_mt_dot4(const MtGemvArgs &a, int max_items, hipStream_t st) {
+    if (!mt_dot4_supported(a.m, a.K, a.rows) || (a.swiglu && (!mt_dot4_supported(a.m2, a.K, a.rows) || !a.y2)) ||
+        a.pair_slice != MT_MFMA_FEW || a.tiles != 1 || a.xdiv <= 0 || max_items <= 0 || a.dense_n > 0)
+        return hipErrorInvalidValue;
+    MtGemvArgs b = a;
+    b.mat_items = a.swiglu ? max_items : 0;  // gate into y, up into y2 (the SwiGLU is the consumer's)
+    const int K = a.K;
+    const size_t lds = (size_t)MT_MFMA_FEW * (3 * (K / 16) * 16 + (K / 32) * 8 + (K / 16) * 4) +
+                       (size_t)MT_MFMA_FEW * a.rows * 4;  // x planes, then the results
+    if (lds > 96 * 1024) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)(a.swiglu ? 2 * max_items : max_items));
+    switch (K / 64) {
+    case 8: hipLaunchKernelGGL(mt_dot4_kernel<8>, grid, dim3(WG), lds, st, b); break;
+    case 16: hipLaunchKernelGGL(mt_dot4_kernel<16>, grid, dim3(WG), lds, st, b); break;
+    case 32: hipLaunchKernelGGL(mt_dot4_kernel<32>, grid, dim3(WG), lds, st, b); break;
+    default: hipLaunchKernelGGL(mt_dot4_kernel<64>, grid, dim3(WG), lds, st, b); break;
+    }
+    return hipGetLastError();
+}
+
 }  // namespace oi

@@ -483,24 +483,6 @@ hipError_t launch_embed(const DMat &emb, int32_t *state, float *x, int32_t vocab
 // down_e(silu(gate_e x) * up_e x); output sum_k w_k y_k.  Expert matrices are
 // stacked: gate and up [n_experts * inter][dim], down [n_experts * dim][inter].
 
-// rows [r0, r0 + n) of m as a matrix of its own (same planes)
-__device__ __forceinline__ DMat sub_rows(const DMat &m, int r0, int n) {
-    DMat s = m;
-    s.rows = n;
-    const size_t r = (size_t)r0;
-    switch (m.type) {
-    case T_Q4_K: s.q += r * (m.cols >> 6) * 16; s.s += r * (m.cols >> 8) * 16; break;
-    case T_Q6_K: s.q += r * (m.cols >> 6) * 16; s.s += r * (m.cols >> 8) * 16; s.d += r * (m.cols >> 8); break;
-    case T_Q8_0: s.q += r * (m.cols >> 6) * 16; s.d += r * (m.cols >> 5); break;
-    case T_F16: s.q += r * m.cols * 2; break;
-    case T_Q4_0: s.q += r * (m.cols >> 5) * 18; break;
-    case T_Q4_1: s.q += r * (m.cols >> 5) * 20; break;
-    case T_Q5_0: s.q += r * (m.cols >> 5) * 22; break;
-    case T_Q5_1: s.q += r * (m.cols >> 5) * 24; break;
-    default: s.q += r * m.cols * 4; break;
-    }
-    return s;
-}
 
 // one workgroup: softmax of the n router logits, then every expert's rank
 // (the number of experts with a larger p, or an equal p and a lower id:

@@ -294,6 +294,10 @@ constexpr int MT_MFMA_PAIRS = 16, MT_MFMA_ROWS = 64;
 // SwiGLU pair leaves gate in y and up in y2; the down launch applies the
 // SwiGLU to its x rows (x2 = up)
 constexpr int MT_MFMA_FEW = 4;
+// the same items (<= MT_MFMA_FEW pairs, every row tile) on the decode GEMV's
+// int8 dot4 arithmetic (gemv.hip): Q4_K with K / 64 in {8, 16, 32, 64}
+bool mt_dot4_supported(const DMat &m, int32_t K, int32_t rows);
+hipError_t launch_mt_dot4(const MtGemvArgs &a, int max_items, hipStream_t st);
 bool mt_mfma_supported(const DMat &m, int32_t K, int32_t rows);
 hipError_t launch_mt_mfma(const MtGemvArgs &a, int max_items, hipStream_t st, bool f32_only = false);
 struct PfMoeArgs {
