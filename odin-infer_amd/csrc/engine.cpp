@@ -1156,7 +1156,10 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
     const hipStream_t st = e->stream;
     const int32_t D = (int32_t)e->cfg.dim, E = (int32_t)e->n_experts, EF = (int32_t)e->expert_ffn;
     const int sx = L.shared_merged ? 1 : 0, KP = (int)e->top_k + sx, NE = E + sx;
-    const int slices = (T + MT_PAIR_SLICE - 1) / MT_PAIR_SLICE, pairs = T * KP;
+    // router: slices of 8 tokens (the multi-token GEMV's x staging holds 8 rows
+    // of 2048), so each workgroup stages its x once and the grid fills the GPU
+    const int rps = D <= 2048 ? 8 : MT_PAIR_SLICE;
+    const int slices = (T + rps - 1) / rps, pairs = T * KP;
     MtGemvArgs r{};
     r.m = L.router;
     r.K = D;
@@ -1165,7 +1168,7 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
     r.tile_rows = std::max(1, mt_gemv_tile_rows(D, E) / 8);  // one pass of the lane groups: more workgroups
     r.tiles = (E + r.tile_rows - 1) / r.tile_rows;
     r.dense_n = T;
-    r.pair_slice = MT_PAIR_SLICE;
+    r.pair_slice = rps;
     r.x = e->pf_xn;
     r.y = e->pf_lg;
     HIP_TRY(launch_mt_gemv(r, r.tiles * slices, st));

@@ -614,26 +614,6 @@ static __device__ __forceinline__ float wave_sum_dpp(float v) {
 constexpr unsigned long long ROUTE_KEY_VALID = 1ull << 41;
 static_assert(GW <= 1024, "expert ids must fit the key's 10 low bits");
 
-// The k-th largest of the wave's keys v[0..NV) (the caller has checked that
-// more than k are nonzero; nonzero keys are distinct), one bit at a time from
-// the top: the largest T with at least k keys >= T, ending early once exactly
-// k keys are >= T.  Counts are ballots, so every lane of the wave takes part.
-template <int NV>
-static __device__ __forceinline__ unsigned long long wave_kth_key(const unsigned long long (&v)[NV], int k) {
-    unsigned long long T = 0ull;
-#pragma unroll
-    for (int b = 41; b >= 0; b--) {
-        const unsigned long long tr = T | (1ull << b);
-        int cnt = 0;
-#pragma unroll
-        for (int i = 0; i < NV; i++) cnt += __popcll(__ballot(v[i] >= tr));
-        if (cnt >= k) {
-            T = tr;
-            if (cnt == k) break;
-        }
-    }
-    return T;
-}
 
 // Routing of one token inside the workgroup (MoE rows mode): the router
 // logits l[0..n) (n <= GW) -> softmax (max, exp(l - max), sum, divide: the

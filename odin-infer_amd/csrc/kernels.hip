@@ -1354,13 +1354,49 @@ __global__ __launch_bounds__(WG) void pf_moe_topk_kernel(PfMoeArgs a) {
         sid[t] = 0;
     }
     __syncthreads();
-    for (int i = t; i < n; i += WG) {
-        const float pi = p[i];
-        int rank = 0;
-        for (int j = 0; j < n; j++) rank += better(p[j], j, pi, i) ? 1 : 0;
-        if (rank < a.top_k) {
-            sid[rank] = i;
-            sel[rank] = pi;
+    // The k best in the order (p descending, id ascending), i.e. k rounds of
+    // first-maximum selection.  Keys: bit 41 set for a defined p (>= +0, so its
+    // bits order as unsigned integers), p's bits at 40..10, 1023 - id at 9..0.
+    // Each wave keeps its k best keys as candidates (an expert among the k best
+    // has fewer than k better experts in its wave), then a candidate's rank
+    // among the candidates is its rank among all experts when it is below k
+    // (every expert better than one of the k best is itself a candidate).
+    __shared__ unsigned long long cand[(WG / WAVE) * MOE_MAX_K];
+    {
+        constexpr int NV = MOE_MAX_EXPERTS / WG;
+        const int k = a.top_k;
+        unsigned long long v[NV];
+        int nvalid = 0;
+#pragma unroll
+        for (int q = 0; q < NV; q++) {
+            const int i = t + q * WG;
+            const float pi = i < n ? p[i] : __builtin_nanf("");
+            v[q] = pi >= 0.f ? (1ull << 41) | ((unsigned long long)__float_as_uint(pi) << 10) | (unsigned)(1023 - i)
+                             : 0ull;
+            nvalid += __popcll(__ballot(v[q] != 0ull));
+        }
+        const unsigned long long T = nvalid > k ? wave_kth_key(v, k) : 1ull;
+        int slot = 0;
+#pragma unroll
+        for (int q = 0; q < NV; q++) {
+            const unsigned long long m = __ballot(v[q] >= T);
+            const int at = slot + __builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u));
+            if (v[q] >= T && at < k) cand[wave * k + at] = v[q];
+            slot += __popcll(m);
+        }
+        for (int q = slot + lane; q < k; q += WAVE) cand[wave * k + q] = 0ull;
+        __syncthreads();
+        if (t < (WG / WAVE) * k) {
+            const unsigned long long c = cand[t];
+            if (c != 0ull) {
+                int rank = 0;
+                for (int j = 0; j < (WG / WAVE) * k; j++) rank += cand[j] > c ? 1 : 0;
+                if (rank < k) {
+                    const int id = 1023 - (int)(c & 1023ull);
+                    sid[rank] = id;
+                    sel[rank] = p[id];
+                }
+            }
         }
     }
     __syncthreads();
