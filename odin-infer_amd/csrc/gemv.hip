@@ -1057,7 +1057,7 @@ hipError_t launch_gemv_q(const GemvArgs &a, hipStream_t st) {
 // then a lane owns one 64-weight unit of MD_R rows per step (lpr = K / 64
 // lanes per row) and dots them with each pair's planes in turn (x read from
 // LDS once per step and pair, for MD_R rows).  The
-// next three steps' weights are in flight while one is computed.
+// next step's weights are in flight while the current one is computed.
 // Results: the f32 dot product up to the order of the sums and x to 2^-22 of
 // its group maximum (the decode GEMV's bound).
 constexpr int MD_R = 4;
@@ -1083,7 +1083,7 @@ __global__ __launch_bounds__(WG) void mt_dot4_kernel(MtGemvArgs a) {
     };
     // the first step's weights, then x (the loads are independent)
     const int rows_step = GPW * MD_R, nstep = a.rows / (rows_step * NWV);  // rows % (rows_step * NWV) == 0
-    constexpr int NSTG = 2;  // ring stages: one step in flight while one is computed
+    constexpr int NSTG = 2;  // ring stages: the next step in flight while one is computed
     WQ4K ring[NSTG][MD_R];
     auto issue = [&](int st, WQ4K (&w)[MD_R]) {
         const int s2 = min(st, nstep - 1), r0 = (s2 * NWV + wave) * rows_step + grp * MD_R;
