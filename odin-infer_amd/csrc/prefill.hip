@@ -9,6 +9,9 @@
 // projections f16 [T][K]; the KV cache f16 [n_kv_heads][seq_len][head_dim] per
 // layer, shared with the decode path.  Token t sits at position pos0 + t.
 
+#include <cstdlib>
+#include <cstring>
+
 #include "device_common.h"
 
 namespace oi {
@@ -239,10 +242,10 @@ __global__ __launch_bounds__(WG) void pf_attn_kernel(PfAttnArgs a) {
     }
 }
 
-// Causal attention on the matrix cores for head_dim 128, grid (n_heads,
+// Causal attention on the matrix cores for head_dim 128 or 256, grid (n_heads,
 // ceil(T / 64)): a workgroup takes 64 queries of one head (wave w: queries
 // 16w .. 16w+15) and walks the keys in blocks of 64 up to its last query's
-// position.  Per block, K (rows padded to 136 halves) and V transposed (V^T,
+// position.  Per block, K (rows padded to HD + 8 halves) and V transposed (V^T,
 // rows of 68 halves) are staged in LDS; then per wave
 //   S^T[key][query] = K Q^T  (v_mfma_f32_16x16x32_f16; A = K rows, B = Q),
 //   online softmax per query (running max, exp, running sum),
@@ -254,7 +257,7 @@ __global__ __launch_bounds__(WG) void pf_attn_kernel(PfAttnArgs a) {
 // split into f16 hi + lo halves (two products each), K and V are exact f16,
 // accumulation is f32, so scores and weights keep about 22 bits, close to the
 // reference's f32 arithmetic (forward.odin:87-115).
-constexpr int FA_KP = 136, FA_VP = 68;  // LDS row strides (halves) of K and V^T
+constexpr int FA_VP = 68;  // LDS row stride (halves) of V^T; K rows: HD + 8
 
 static __device__ __forceinline__ void split16(const float (&v)[8], h8 &hi, h8 &lo) {
 #pragma unroll
@@ -264,8 +267,9 @@ static __device__ __forceinline__ void split16(const float (&v)[8], h8 &hi, h8 &
     }
 }
 
-__global__ __launch_bounds__(WG) void pf_fattn128_kernel(PfAttnArgs a, int T) {
-    constexpr int HD = 128;
+template <int HD>
+__global__ __launch_bounds__(WG) void pf_fattn_kernel(PfAttnArgs a, int T) {
+    constexpr int FA_KP = HD + 8, NC = HD / 32, NDT = HD / 16;  // K row stride; 32-wide K chunks; 16-wide d tiles
     __shared__ __attribute__((aligned(16))) uint16_t ks[64 * FA_KP];
     __shared__ __attribute__((aligned(16))) uint16_t vt[HD * FA_VP];
     const int h = blockIdx.x, t0 = 64 * (int)blockIdx.y;
@@ -279,11 +283,11 @@ __global__ __launch_bounds__(WG) void pf_fattn128_kernel(PfAttnArgs a, int T) {
     const uint16_t *kc = a.kc + (size_t)kvh * a.seq_len * HD, *vc = a.vc + (size_t)kvh * a.seq_len * HD;
 
     // B operand of S^T: Q[query q][d = 32c + 8g + e], hi and lo halves
-    h8 qh[4], ql[4];
+    h8 qh[NC], ql[NC];
     {
         const float *qr = a.q + (size_t)min(tq, T - 1) * QD + h * HD;
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
+        for (int c = 0; c < NC; c++) {
             float v[8];
             const float4 v0 = *(const float4 *)(qr + 32 * c + 8 * g), v1 = *(const float4 *)(qr + 32 * c + 8 * g + 4);
             v[0] = v0.x; v[1] = v0.y; v[2] = v0.z; v[3] = v0.w;
@@ -293,17 +297,17 @@ __global__ __launch_bounds__(WG) void pf_fattn128_kernel(PfAttnArgs a, int T) {
     }
     const float rs = sqrtf((float)HD);
     float m = -INFINITY, lsum = 0.f;
-    f32x4v o[8];
+    f32x4v o[NDT];
 #pragma unroll
-    for (int dt = 0; dt < 8; dt++) o[dt] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    for (int dt = 0; dt < NDT; dt++) o[dt] = f32x4v{0.f, 0.f, 0.f, 0.f};
 
     for (int kb = 0; 64 * kb <= last; kb++) {
         // stage K and V^T of keys 64 kb .. +63 (rows past the written range
         // re-read the last written row; their scores are masked)
         __syncthreads();
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int piece = threadIdx.x + WG * i, r = piece >> 4, c8 = piece & 15;  // row r, 8 halves at 8 c8
+        for (int i = 0; i < 64 * (HD / 8) / WG; i++) {
+            const int piece = threadIdx.x + WG * i, r = piece / (HD / 8), c8 = piece % (HD / 8);  // row r, 8 halves at 8 c8
             const int p = min(64 * kb + r, lmax - 1);
             const u32x4 kv = *(const u32x4 *)(kc + (size_t)p * HD + 8 * c8);
             *(u32x4 *)(ks + r * FA_KP + 8 * c8) = kv;
@@ -318,7 +322,7 @@ __global__ __launch_bounds__(WG) void pf_fattn128_kernel(PfAttnArgs a, int T) {
         for (int kt = 0; kt < 4; kt++) {
             f32x4v acc = f32x4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int c = 0; c < 4; c++) {
+            for (int c = 0; c < NC; c++) {
                 const h8 kA = __builtin_bit_cast(h8, *(const u32x4 *)(ks + (16 * kt + q) * FA_KP + 32 * c + 8 * g));
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kA, qh[c], acc, 0, 0, 0);
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kA, ql[c], acc, 0, 0, 0);
@@ -348,7 +352,7 @@ __global__ __launch_bounds__(WG) void pf_fattn128_kernel(PfAttnArgs a, int T) {
             }
         lsum = lsum * alpha + ps;
 #pragma unroll
-        for (int dt = 0; dt < 8; dt++) o[dt] *= alpha;
+        for (int dt = 0; dt < NDT; dt++) o[dt] *= alpha;
         // O^T += V^T P^T over the two 32-key chunks
 #pragma unroll
         for (int kc2 = 0; kc2 < 2; kc2++) {
@@ -361,7 +365,7 @@ __global__ __launch_bounds__(WG) void pf_fattn128_kernel(PfAttnArgs a, int T) {
             h8 ph, pl;
             split16(pv, ph, pl);
 #pragma unroll
-            for (int dt = 0; dt < 8; dt++) {
+            for (int dt = 0; dt < NDT; dt++) {
                 const uint16_t *vr = vt + (16 * dt + q) * FA_VP + 32 * kc2 + 4 * g;
                 const u32x2 v0 = *(const u32x2 *)vr, v1 = *(const u32x2 *)(vr + 16);
                 const h8 vA = __builtin_bit_cast(h8, u32x4{v0.x, v0.y, v1.x, v1.y});
@@ -376,7 +380,7 @@ __global__ __launch_bounds__(WG) void pf_fattn128_kernel(PfAttnArgs a, int T) {
         const size_t d0 = (size_t)tq * QD + h * HD + 4 * g;
         uint16_t *dst = a.out + d0;
 #pragma unroll
-        for (int dt = 0; dt < 8; dt++) {
+        for (int dt = 0; dt < NDT; dt++) {
             float r[4];
 #pragma unroll
             for (int e = 0; e < 4; e++) r[e] = pf_gated(a, o[dt][e] / lsum, d0 + 16 * dt + e);
@@ -409,6 +413,12 @@ __global__ __launch_bounds__(WG) void pf_swiglu16_kernel(const float *g, int gs,
 
 static unsigned blocks(int64_t n) { return (unsigned)((n + WG - 1) / WG); }
 
+// OI_PREFILL_ATTN=lanes: head_dim 256 always on the lane-per-position kernel (tests)
+static bool pf_attn_lanes() {
+    const char *e = std::getenv("OI_PREFILL_ATTN");
+    return e && std::strcmp(e, "lanes") == 0;
+}
+
 hipError_t launch_pf_qkv(const PfQkvArgs &a, int head_dim, hipStream_t st) {
     const dim3 grid((unsigned)a.T, (unsigned)((a.n_heads + 2 * a.n_kv_heads + WG / WAVE - 1) / (WG / WAVE)));
     if (head_dim == 128) hipLaunchKernelGGL(pf_qkv_kernel<128>, grid, dim3(WG), 0, st, a);
@@ -421,9 +431,13 @@ hipError_t launch_pf_attn(const float *q, const uint16_t *kc, const uint16_t *vc
                           int seq_len, int n_heads, int n_kv_heads, int head_dim, hipStream_t st, const float *gate) {
     PfAttnArgs a{q, kc, vc, out, pos0, seq_len, n_heads, n_kv_heads, gate};
     const dim3 grid((unsigned)n_heads, (unsigned)T);
-    if (head_dim == 128)
-        hipLaunchKernelGGL(pf_fattn128_kernel, dim3((unsigned)n_heads, (unsigned)((T + 63) / 64)), dim3(WG), 0, st, a,
-                           T);
+    const dim3 fgrid((unsigned)n_heads, (unsigned)((T + 63) / 64));
+    if (head_dim == 128) hipLaunchKernelGGL(pf_fattn_kernel<128>, fgrid, dim3(WG), 0, st, a, T);
+    // head_dim 256: the matrix cores from 128 tokens on; a shorter chunk gives
+    // them one workgroup per head only (16 at config 5), where one workgroup per
+    // (head, token) on the lane-per-position kernel is faster
+    else if (head_dim == 256 && T >= 128 && !pf_attn_lanes())
+        hipLaunchKernelGGL(pf_fattn_kernel<256>, fgrid, dim3(WG), 0, st, a, T);
     else if (head_dim == 256) hipLaunchKernelGGL(pf_attn_kernel<256>, grid, dim3(WG), 0, st, a);
     else return hipErrorInvalidValue;
     return hipGetLastError();
