@@ -125,17 +125,23 @@ __global__ __launch_bounds__(WG) void pf_dn_conv_kernel(PfDnArgs a) {
     const int c = (int)blockIdx.x * WG + threadIdx.x;
     if (c >= CD) return;
     const int t0 = (int)blockIdx.y * DN_TT, t1 = min(a.T, t0 + DN_TT);
-    float w[KS], win[KM1 > 0 ? KM1 : 1];
+    float w[KS], win[KM1 > 0 ? KM1 : 1], xs[DN_TT];
 #pragma unroll
     for (int k = 0; k < KS; k++) w[k] = a.conv_w[(size_t)c * KS + k];
 #pragma unroll
     for (int k = 0; k < KM1; k++) win[k] = dn_in<KS>(a, CD, c, t0 - KM1 + k);
-    for (int t = t0; t < t1; t++) {
-        const float x = dn_in<KS>(a, CD, c, t);
+    // every token's input requested before the first is used (one memory
+    // round trip for the 16 tokens, not one per token)
+#pragma unroll
+    for (int i = 0; i < DN_TT; i++) xs[i] = t0 + i < t1 ? dn_in<KS>(a, CD, c, t0 + i) : 0.f;
+#pragma unroll
+    for (int i = 0; i < DN_TT; i++) {
+        if (t0 + i >= t1) break;
+        const float x = xs[i];
         float acc = w[KM1] * x;
 #pragma unroll
         for (int k = 0; k < KM1; k++) acc += w[k] * win[k];
-        a.conv_out[(size_t)t * CD + c] = silu_ref(acc);
+        a.conv_out[(size_t)(t0 + i) * CD + c] = silu_ref(acc);
 #pragma unroll
         for (int k = 0; k + 1 < KM1; k++) win[k] = win[k + 1];
         if (KM1 > 0) win[KM1 - 1] = x;
@@ -212,7 +218,7 @@ __global__ __launch_bounds__(WG) void pf_dn_delta_kernel(PfDnArgs a) {
     static_assert(RPL == 16 && HV % 32 == 0, "head shape");
     __shared__ __attribute__((aligned(16))) float sq[DN_DB][QP];
     __shared__ __attribute__((aligned(16))) float sk[DN_DB][QP];
-    __shared__ float sv[DN_DB][32];
+    __shared__ __attribute__((aligned(16))) float sv[DN_DB][32];
     __shared__ float sg[DN_DB][2];
     const int vh = blockIdx.x, kh = vh % a.n_kh, c0 = (int)blockIdx.y * 32;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
@@ -224,20 +230,40 @@ __global__ __launch_bounds__(WG) void pf_dn_delta_kernel(PfDnArgs a) {
     for (int r = 0; r < RPL; r++) s[r] = S[(size_t)(i0 + r) * HV + j];
     for (int tb = 0; tb < a.T; tb += DN_DB) {
         const int nb = min(DN_DB, a.T - tb);
+        // the block's q, k (float4 pieces), v and gates: every load issued
+        // before any is used (a loop of load-then-store would wait for each)
+        constexpr int QK4 = DN_DB * 2 * HK / 4 / WG, V4 = DN_DB * 32 / 4 / WG;
+        static_assert(QK4 * WG * 4 == DN_DB * 2 * HK && V4 >= 1, "staging shape");
+        float4 qk4[QK4], v4[V4];
+        float gv = 0.f;
+#pragma unroll
+        for (int i = 0; i < QK4; i++) {
+            const int idx = threadIdx.x + i * WG, tt = idx / (HK / 2), e4 = idx % (HK / 2);  // HK / 2 float4 per token
+            const int side = e4 / (HK / 4), ee = 4 * (e4 % (HK / 4));
+            qk4[i] = tt < nb ? *(const float4 *)(a.qk + (size_t)(tb + tt) * 2 * KD + side * KD + kh * HK + ee)
+                             : float4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int i = 0; i < V4; i++) {
+            const int idx = threadIdx.x + i * WG, tt = idx / 8, c4 = idx % 8;
+            v4[i] = tt < nb ? *(const float4 *)(a.conv_out + (size_t)(tb + tt) * CD + 2 * KD + vh * HV + c0 + 4 * c4)
+                            : float4{0.f, 0.f, 0.f, 0.f};
+        }
+        if (threadIdx.x < 2 * nb)
+            gv = a.gates[(size_t)(tb + threadIdx.x / 2) * 3 * a.n_vh + (threadIdx.x % 2) * a.n_vh + vh];
         __syncthreads();  // the previous block's LDS reads are done
-        for (int idx = threadIdx.x; idx < nb * 2 * HK; idx += WG) {
-            const int tt = idx / (2 * HK), e = idx % (2 * HK), ee = e % HK;
-            const float val = a.qk[(size_t)(tb + tt) * 2 * KD + (e < HK ? 0 : KD) + kh * HK + ee];
-            (e < HK ? sq : sk)[tt][ee + (ee / RPL) * 4] = val;
+#pragma unroll
+        for (int i = 0; i < QK4; i++) {
+            const int idx = threadIdx.x + i * WG, tt = idx / (HK / 2), e4 = idx % (HK / 2);
+            const int side = e4 / (HK / 4), ee = 4 * (e4 % (HK / 4));
+            *(float4 *)&(side ? sk : sq)[tt][ee + (ee / RPL) * 4] = qk4[i];  // 4 | ee, RPL: one row group
         }
-        for (int idx = threadIdx.x; idx < nb * 32; idx += WG) {
-            const int tt = idx / 32, cc = idx % 32;
-            sv[tt][cc] = a.conv_out[(size_t)(tb + tt) * CD + 2 * KD + vh * HV + c0 + cc];
+#pragma unroll
+        for (int i = 0; i < V4; i++) {
+            const int idx = threadIdx.x + i * WG, tt = idx / 8, c4 = idx % 8;
+            *(float4 *)&sv[tt][4 * c4] = v4[i];
         }
-        if (threadIdx.x < 2 * nb) {
-            const int tt = threadIdx.x / 2, g = threadIdx.x % 2;
-            sg[tt][g] = a.gates[(size_t)(tb + tt) * 3 * a.n_vh + g * a.n_vh + vh];
-        }
+        if (threadIdx.x < 2 * nb) sg[threadIdx.x / 2][threadIdx.x % 2] = gv;
         __syncthreads();
         for (int tt = 0; tt < nb; tt++) {
             const float beta = sg[tt][0], decay = sg[tt][1];
@@ -249,22 +275,26 @@ __global__ __launch_bounds__(WG) void pf_dn_delta_kernel(PfDnArgs a) {
                 kn[4 * i] = kk.x; kn[4 * i + 1] = kk.y; kn[4 * i + 2] = kk.z; kn[4 * i + 3] = kk.w;
                 qn[4 * i] = qq.x; qn[4 * i + 1] = qq.y; qn[4 * i + 2] = qq.z; qn[4 * i + 3] = qq.w;
             }
-            float kv = 0.f;
+            // four partial sums per product (short dependency chains; the
+            // token recurrence is the kernel's critical path)
+            float kp[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int r = 0; r < RPL; r++) {
                 s[r] = s[r] * decay;
-                kv += s[r] * kn[r];
+                kp[r & 3] += s[r] * kn[r];
             }
+            float kv = (kp[0] + kp[1]) + (kp[2] + kp[3]);
             kv += OI_DPP(kv, 0xB1);  // sum over the lane's group of 8 (the row groups)
             kv += OI_DPP(kv, 0x4E);
             kv += dpp_mirror8(kv);
             const float delta = (sv[tt][cl] - kv) * beta;
-            float o = 0.f;
+            float op[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int r = 0; r < RPL; r++) {
                 s[r] += kn[r] * delta;
-                o += s[r] * qn[r];
+                op[r & 3] += s[r] * qn[r];
             }
+            float o = (op[0] + op[1]) + (op[2] + op[3]);
             o += OI_DPP(o, 0xB1);
             o += OI_DPP(o, 0x4E);
             o += dpp_mirror8(o);
@@ -401,25 +431,36 @@ __global__ __launch_bounds__(WG) void pf_dn_chunk_kernel(PfDnArgs a) {
 template <int HV>
 __global__ __launch_bounds__(WG) void pf_dn_gnorm_kernel(PfDnArgs a) {
 #pragma clang fp contract(off)
-    constexpr int E = HV / WAVE;
+    constexpr int E = HV / WAVE, NH = 8;  // dimensions per lane; value heads per wave and pass
     const int t = blockIdx.x, lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
     const int VD = a.n_vh * HV;
-    for (int vh = wave; vh < a.n_vh; vh += WG / WAVE) {
-        float o[E], ss = 0.f;
+    for (int vh0 = wave * NH; vh0 < a.n_vh; vh0 += (WG / WAVE) * NH) {
+        // the pass's o and z values requested before any is used
+        float o[NH][E], z[NH][E];
 #pragma unroll
-        for (int e = 0; e < E; e++) {
-            o[e] = a.o[(size_t)t * VD + vh * HV + lane + WAVE * e];
-            ss += o[e] * o[e];
-        }
-        ss = wave_sum(ss);
-        const float inv = 1.0f / sqrtf(ss / (float)HV + a.eps);
+        for (int h = 0; h < NH; h++)
 #pragma unroll
-        for (int e = 0; e < E; e++) {
-            const int j = lane + WAVE * e;
-            const float z = parts_at(a.z, a.zs, (size_t)a.T * VD, (size_t)t * VD + vh * HV + j);
-            const float v = a.norm_w[j] * (inv * o[e]) * silu_ref(z);
-            if (a.out32) a.out32[(size_t)t * VD + vh * HV + j] = v;
-            else a.out16[(size_t)t * VD + vh * HV + j] = f2h(v);
+            for (int e = 0; e < E; e++) {
+                const int vh = min(vh0 + h, a.n_vh - 1), j = lane + WAVE * e;
+                o[h][e] = a.o[(size_t)t * VD + vh * HV + j];
+                z[h][e] = parts_at(a.z, a.zs, (size_t)a.T * VD, (size_t)t * VD + vh * HV + j);
+            }
+#pragma unroll
+        for (int h = 0; h < NH; h++) {
+            if (vh0 + h >= a.n_vh) break;  // uniform
+            const int vh = vh0 + h;
+            float ss = 0.f;
+#pragma unroll
+            for (int e = 0; e < E; e++) ss += o[h][e] * o[h][e];
+            ss = wave_sum(ss);
+            const float inv = 1.0f / sqrtf(ss / (float)HV + a.eps);
+#pragma unroll
+            for (int e = 0; e < E; e++) {
+                const int j = lane + WAVE * e;
+                const float v = a.norm_w[j] * (inv * o[h][e]) * silu_ref(z[h][e]);
+                if (a.out32) a.out32[(size_t)t * VD + vh * HV + j] = v;
+                else a.out16[(size_t)t * VD + vh * HV + j] = f2h(v);
+            }
         }
     }
 }
