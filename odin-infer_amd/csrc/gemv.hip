@@ -1092,14 +1092,32 @@ __global__ __launch_bounds__(WG) void mt_dot4_kernel(MtGemvArgs a) {
     };
 #pragma unroll
     for (int i = 0; i < NSTG - 1; i++) issue(i, ring[i]);
-    for (int pj = 0; pj < n; pj++) {
+    // every pair's x (and x2) requested before any is used: K / 4 float4 per
+    // pair, XI per thread (a loop of load-then-use would wait for each pair)
+    constexpr int XI = LPR * 64 / 4 / WG > 0 ? LPR * 64 / 4 / WG : 1;
+    float4 xv[NP][XI], uv[NP][XI];
+#pragma unroll
+    for (int pj = 0; pj < NP; pj++) {
+        const size_t xo = (size_t)(a.list[base + min(pj, n - 1)] / a.xdiv) * K;
+#pragma unroll
+        for (int i = 0; i < XI; i++) {
+            const int c = min(tid + i * WG, K / 4 - 1);
+            xv[pj][i] = ((const float4 *)(a.x + xo))[c];
+            uv[pj][i] = a.x2 ? ((const float4 *)(a.x2 + xo))[c] : float4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+#pragma unroll
+    for (int pj = 0; pj < NP; pj++) {
+        if (pj >= n) break;
         const XQ q = xq(pj);
-        const size_t xo = (size_t)(a.list[base + pj] / a.xdiv) * K;
-        for (int c = tid; c < K / 4; c += WG) {  // K / 4 float4, groups of 8 threads
-            float4 v = ((const float4 *)(a.x + xo))[c];
+#pragma unroll
+        for (int i = 0; i < XI; i++) {
+            const int c = tid + i * WG;  // K / 4 float4, groups of 8 threads
+            if (c >= K / 4) break;
+            float4 v = xv[pj][i];
             if (a.x2) {  // SwiGLU (infer/forward.odin:188-193)
 #pragma clang fp contract(off)
-                const float4 u = ((const float4 *)(a.x2 + xo))[c];
+                const float4 u = uv[pj][i];
                 v.x *= 1.0f / (1.0f + expf(-v.x));
                 v.y *= 1.0f / (1.0f + expf(-v.y));
                 v.z *= 1.0f / (1.0f + expf(-v.z));
