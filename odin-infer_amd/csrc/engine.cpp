@@ -1277,8 +1277,10 @@ int prefill_chunk(oi_engine *e, const int32_t *tokens, int T, int pos) {
                          L.kc, L.vc, e->pf_q, e->pf_gate, T, pos, (int32_t)c.seq_len, (int32_t)c.n_heads,
                          (int32_t)c.n_kv_heads};
             HIP_TRY(launch_pf_q35_qkv(qa, hd, st));
+            // the k / v partial products are consumed: their buffer is the
+            // attention's scratch
             HIP_TRY(launch_pf_attn(e->pf_q, L.kc, L.vc, e->pf_xb, T, pos, (int)c.seq_len, (int)c.n_heads,
-                                   (int)c.n_kv_heads, hd, st, e->pf_gate));
+                                   (int)c.n_kv_heads, hd, st, e->pf_gate, P[1], PB[1]));
             HIP_TRY(launch_gemm_parts(L.wo, e->pf_xb, T, P[0], PB[0], &s0, st));
         } else {
             HIP_TRY(launch_gemm_parts(L.in_qkv, e->pf_xb, T, P[0], PB[0], &s0, st));

@@ -215,9 +215,11 @@ struct PfQkvArgs {
 hipError_t launch_pf_qkv(const PfQkvArgs &a, int head_dim, hipStream_t st);
 // gate: null, or [T][n_heads * head_dim] f32, the output multiplied by its
 // sigmoid before rounding (the Qwen3.5 attention's output gate)
+// ws: optional scratch for the key-split form of short chunks (head_dim 256:
+// [splits][T][n_heads][head_dim + 2] floats, splits <= 16); unused if too small
 hipError_t launch_pf_attn(const float *q, const uint16_t *kc, const uint16_t *vc, uint16_t *out, int T, int pos0,
                           int seq_len, int n_heads, int n_kv_heads, int head_dim, hipStream_t st,
-                          const float *gate = nullptr);
+                          const float *gate = nullptr, float *ws = nullptr, size_t ws_bytes = 0);
 hipError_t launch_pf_add(float *x, const float *part, int split, int64_t total, hipStream_t st);
 // x += partial-product sums (part may be null), then out = f16(rmsnorm(x) * w); dim <= 16384
 // out32: null, or [T][dim] f32 that receives the norm's f32 result as well

@@ -9,6 +9,7 @@
 // projections f16 [T][K]; the KV cache f16 [n_kv_heads][seq_len][head_dim] per
 // layer, shared with the decode path.  Token t sits at position pos0 + t.
 
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 
@@ -267,8 +268,12 @@ static __device__ __forceinline__ void split16(const float (&v)[8], h8 &hi, h8 &
     }
 }
 
-template <int HD>
-__global__ __launch_bounds__(WG) void pf_fattn_kernel(PfAttnArgs a, int T) {
+// SPLIT: the key blocks are divided over gridDim.z workgroups (a short chunk
+// has too few query tiles to fill the GPU); each writes its queries'
+// unnormalized (o, m, l) to ws [split][T][n_heads][HD + 2] and
+// pf_fattn_merge_kernel combines them.
+template <int HD, bool SPLIT = false>
+__global__ __launch_bounds__(WG) void pf_fattn_kernel(PfAttnArgs a, int T, float *ws = nullptr) {
     constexpr int FA_KP = HD + 8, NC = HD / 32, NDT = HD / 16;  // K row stride; 32-wide K chunks; 16-wide d tiles
     __shared__ __attribute__((aligned(16))) uint16_t ks[64 * FA_KP];
     __shared__ __attribute__((aligned(16))) uint16_t vt[HD * FA_VP];
@@ -301,7 +306,13 @@ __global__ __launch_bounds__(WG) void pf_fattn_kernel(PfAttnArgs a, int T) {
 #pragma unroll
     for (int dt = 0; dt < NDT; dt++) o[dt] = f32x4v{0.f, 0.f, 0.f, 0.f};
 
-    for (int kb = 0; 64 * kb <= last; kb++) {
+    int kb0 = 0, kb1 = last / 64 + 1;  // this workgroup's key blocks
+    if (SPLIT) {
+        const int nb = kb1, ns = (int)gridDim.z, z = (int)blockIdx.z;
+        kb0 = (int)((long)nb * z / ns);
+        kb1 = (int)((long)nb * (z + 1) / ns);
+    }
+    for (int kb = kb0; kb < kb1; kb++) {
         // stage K and V^T of keys 64 kb .. +63 (rows past the written range
         // re-read the last written row; their scores are masked)
         __syncthreads();
@@ -340,14 +351,16 @@ __global__ __launch_bounds__(WG) void pf_fattn_kernel(PfAttnArgs a, int T) {
             for (int e = 0; e < 4; e++) bm = fmaxf(bm, s[kt][e]);
         bm = fmaxf(bm, __shfl_xor(bm, 16, WAVE));
         bm = fmaxf(bm, __shfl_xor(bm, 32, WAVE));
-        const float mn = fmaxf(m, bm), alpha = expf(m - mn);
+        // (a key-split block may have no key visible to this query yet: m and
+        // mn stay -inf and nothing is added)
+        const float mn = fmaxf(m, bm), alpha = mn == -INFINITY ? 1.f : expf(m - mn);
         m = mn;
         float ps = 0.f;
 #pragma unroll
         for (int kt = 0; kt < 4; kt++)
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                s[kt][e] = expf(s[kt][e] - mn);
+                s[kt][e] = mn == -INFINITY ? 0.f : expf(s[kt][e] - mn);
                 ps += s[kt][e];
             }
         lsum = lsum * alpha + ps;
@@ -376,6 +389,18 @@ __global__ __launch_bounds__(WG) void pf_fattn_kernel(PfAttnArgs a, int T) {
     }
     lsum += __shfl_xor(lsum, 16, WAVE);
     lsum += __shfl_xor(lsum, 32, WAVE);
+    if (SPLIT) {  // this split's (o, m, l) of the lane's query
+        if (tq < T) {
+            float *pp = ws + (((size_t)blockIdx.z * T + tq) * a.n_heads + h) * (HD + 2);
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) *(float4 *)(pp + 16 * dt + 4 * g) = make_float4(o[dt][0], o[dt][1], o[dt][2], o[dt][3]);
+            if (g == 0) {
+                pp[HD] = m;
+                pp[HD + 1] = lsum;
+            }
+        }
+        return;
+    }
     if (tq < T) {
         const size_t d0 = (size_t)tq * QD + h * HD + 4 * g;
         uint16_t *dst = a.out + d0;
@@ -389,6 +414,26 @@ __global__ __launch_bounds__(WG) void pf_fattn_kernel(PfAttnArgs a, int T) {
             *(u32x2 *)(dst + 16 * dt) = u32x2{w0, w1};
         }
     }
+}
+
+// The splits of pf_fattn_kernel<HD, true> for token t and head h (grid (T,
+// n_heads), thread d): O = sum_s e^{m_s - M} o_s / sum_s e^{m_s - M} l_s.
+template <int HD>
+__global__ __launch_bounds__(HD) void pf_fattn_merge_kernel(PfAttnArgs a, int T, const float *ws, int ns) {
+#pragma clang fp contract(off)
+    const int t = blockIdx.x, h = blockIdx.y, d = threadIdx.x, QD = a.n_heads * HD;
+    const size_t stride = (size_t)T * a.n_heads * (HD + 2), base = ((size_t)t * a.n_heads + h) * (HD + 2);
+    float M = -INFINITY;
+    for (int z = 0; z < ns; z++) M = fmaxf(M, ws[z * stride + base + HD]);
+    float L = 0.f, O = 0.f;
+    for (int z = 0; z < ns; z++) {
+        const float mz = ws[z * stride + base + HD];
+        const float f = mz == -INFINITY ? 0.f : expf(mz - M);  // a split with no visible key adds nothing
+        L += f * ws[z * stride + base + HD + 1];
+        O += f * ws[z * stride + base + d];
+    }
+    const size_t i = (size_t)t * QD + h * HD + d;
+    a.out[i] = f2h(pf_gated(a, O / L, i));
 }
 
 // x[i] += sum of the partial products of element i (the residual adds,
@@ -428,16 +473,31 @@ hipError_t launch_pf_qkv(const PfQkvArgs &a, int head_dim, hipStream_t st) {
 }
 
 hipError_t launch_pf_attn(const float *q, const uint16_t *kc, const uint16_t *vc, uint16_t *out, int T, int pos0,
-                          int seq_len, int n_heads, int n_kv_heads, int head_dim, hipStream_t st, const float *gate) {
+                          int seq_len, int n_heads, int n_kv_heads, int head_dim, hipStream_t st, const float *gate,
+                          float *ws, size_t ws_bytes) {
     PfAttnArgs a{q, kc, vc, out, pos0, seq_len, n_heads, n_kv_heads, gate};
     const dim3 grid((unsigned)n_heads, (unsigned)T);
     const dim3 fgrid((unsigned)n_heads, (unsigned)((T + 63) / 64));
-    if (head_dim == 128) hipLaunchKernelGGL(pf_fattn_kernel<128>, fgrid, dim3(WG), 0, st, a, T);
+    // a short chunk at head_dim 256: the key blocks split over workgroups (up
+    // to 16 per query tile, at least 2 blocks each) when the workspace holds
+    // the partials
+    const int nkb = (pos0 + T + 63) / 64, qt = (T + 63) / 64;
+    const size_t per = (size_t)T * n_heads * (head_dim + 2) * 4;
+    int ns = std::min(16, nkb / 2);
+    if (ws && per > 0) ns = std::min<int>(ns, (int)(ws_bytes / per));
+    if (head_dim == 256 && T < 128 && !pf_attn_lanes() && ws && ns >= 2 && qt * n_heads < 256) {
+        hipLaunchKernelGGL((pf_fattn_kernel<256, true>), dim3((unsigned)n_heads, (unsigned)qt, (unsigned)ns), dim3(WG),
+                           0, st, a, T, ws);
+        hipLaunchKernelGGL(pf_fattn_merge_kernel<256>, dim3((unsigned)T, (unsigned)n_heads), dim3(256), 0, st, a, T,
+                           (const float *)ws, ns);
+        return hipGetLastError();
+    }
+    if (head_dim == 128) hipLaunchKernelGGL((pf_fattn_kernel<128>), fgrid, dim3(WG), 0, st, a, T, nullptr);
     // head_dim 256: the matrix cores from 128 tokens on; a shorter chunk gives
     // them one workgroup per head only (16 at config 5), where one workgroup per
     // (head, token) on the lane-per-position kernel is faster
     else if (head_dim == 256 && T >= 128 && !pf_attn_lanes())
-        hipLaunchKernelGGL(pf_fattn_kernel<256>, fgrid, dim3(WG), 0, st, a, T);
+        hipLaunchKernelGGL((pf_fattn_kernel<256>), fgrid, dim3(WG), 0, st, a, T, nullptr);
     else if (head_dim == 256) hipLaunchKernelGGL(pf_attn_kernel<256>, grid, dim3(WG), 0, st, a);
     else return hipErrorInvalidValue;
     return hipGetLastError();
