@@ -111,6 +111,24 @@ static __device__ __forceinline__ float parts_at(const float *p, int split, size
     return s;
 }
 
+// v[j] = parts_at(p, split, slice, idx(j)) for j < N, with the same sums in
+// the same order, but each slice's N loads are requested together: `split`
+// memory round trips instead of one per element and slice (a runtime trip
+// count inside the element loop makes every load wait for the one before)
+template <int N, class F>
+static __device__ __forceinline__ void parts_gather(float (&v)[N], const float *p, int split, size_t slice, F idx) {
+#pragma unroll
+    for (int j = 0; j < N; j++) v[j] = p[idx(j)];
+    for (int z = 1; z < split; z++) {
+        const float *q = p + (size_t)z * slice;
+        float t[N];
+#pragma unroll
+        for (int j = 0; j < N; j++) t[j] = q[idx(j)];
+#pragma unroll
+        for (int j = 0; j < N; j++) v[j] += t[j];
+    }
+}
+
 // (value, index) order of a greedy argmax that keeps the first maximum
 // (sampler/sampler.odin:79-89 scans with a strict '>')
 static __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {

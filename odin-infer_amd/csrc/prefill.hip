@@ -116,9 +116,8 @@ __global__ __launch_bounds__(WG) void pf_qkv_kernel(PfQkvArgs a) {
         const int split = isq ? a.qs : isk ? a.ks : a.vs;
         const int rows = isq ? QD : KVD;
         float v[DPL];
-#pragma unroll
-        for (int e = 0; e < DPL; e++)
-            v[e] = parts_at(src, split, (size_t)a.T * rows, (size_t)t * rows + h * HD + lane + WAVE * e);
+        const size_t base = (size_t)t * rows + h * HD + lane;
+        parts_gather(v, src, split, (size_t)a.T * rows, [&](int e) { return base + WAVE * e; });
         if (isq || isk) {
             const float *nw = isq ? a.q_norm : a.k_norm;
             float ss = 0.f;

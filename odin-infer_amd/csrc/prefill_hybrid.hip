@@ -53,17 +53,18 @@ __global__ __launch_bounds__(WG) void pf_q35_qkv_kernel(PfQ35Args a) {
     float v[DPL];
     if (isq) {
         const size_t slice = (size_t)a.T * 2 * QD, base = (size_t)t * 2 * QD + (size_t)h * 2 * HD;
+        float qg[2 * DPL];  // q, then gate
+        parts_gather(qg, a.q, a.qs, slice, [&](int j) { return base + (j / DPL) * HD + lane + WAVE * (j % DPL); });
 #pragma unroll
         for (int e = 0; e < DPL; e++) {
-            v[e] = parts_at(a.q, a.qs, slice, base + lane + WAVE * e);
-            a.gate[(size_t)t * QD + h * HD + lane + WAVE * e] = parts_at(a.q, a.qs, slice, base + HD + lane + WAVE * e);
+            v[e] = qg[e];
+            a.gate[(size_t)t * QD + h * HD + lane + WAVE * e] = qg[DPL + e];
         }
     } else {
         const float *src = isk ? a.k : a.v;
         const int split = isk ? a.ks : a.vs;
-#pragma unroll
-        for (int e = 0; e < DPL; e++)
-            v[e] = parts_at(src, split, (size_t)a.T * KVD, (size_t)t * KVD + h * HD + lane + WAVE * e);
+        const size_t base = (size_t)t * KVD + h * HD + lane;
+        parts_gather(v, src, split, (size_t)a.T * KVD, [&](int e) { return base + WAVE * e; });
     }
     if (isq || isk) {
         const float *nw = isq ? a.q_norm : a.k_norm;
@@ -104,62 +105,57 @@ __global__ __launch_bounds__(WG) void pf_q35_qkv_kernel(PfQ35Args a) {
 
 // ---------------------------------------------------------------- DeltaNet --
 
-constexpr int DN_TT = 16;  // tokens per thread of the conv
+constexpr int DN_TT = 8;  // tokens per thread of the conv
 
-// in(tau) of channel c: the in_qkv projection of token tau of the chunk, or,
-// before the chunk, the conv state's input (tau in [-(KS-1), 0))
-template <int KS>
-static __device__ __forceinline__ float dn_in(const PfDnArgs &a, int CD, int c, int tau) {
-    if (tau >= 0) return parts_at(a.qkv, a.qkvs, (size_t)a.T * CD, (size_t)tau * CD + c);
-    return a.conv_state[(size_t)c * (KS - 1) + (KS - 1 + tau)];
-}
-
-// conv1d_step + silu (ops.odin:97-116) of channel c for tokens [16 y, 16 y +
-// 16): out = silu(w[KS-1] in(t) + sum_k w[k] in(t - (KS-1) + k)), the order
-// of the decode step.  Grid (ceil(conv_dim / 256), ceil(T / 16)).
+// conv1d_step + silu (ops.odin:97-116) of channel c for tokens [8 y, 8 y +
+// 8): out = silu(w[KS-1] in(t) + sum_k w[k] in(t - (KS-1) + k)), the order
+// of the decode step, where in(tau) is the in_qkv projection of token tau of
+// the chunk or, before the chunk (tau in [-(KS-1), 0)), the conv state's
+// input.  The window and the tokens are gathered together (clamped indices,
+// every load unconditional).  Grid (ceil(conv_dim / 256), ceil(T / 8)).
 template <int KS>
 __global__ __launch_bounds__(WG) void pf_dn_conv_kernel(PfDnArgs a) {
 #pragma clang fp contract(off)
-    constexpr int KM1 = KS - 1;
+    constexpr int KM1 = KS - 1, NX = KM1 + DN_TT;
+    static_assert(DN_TT >= KM1, "only the first block's window reaches before the chunk");
     const int CD = 2 * a.n_kh * a.hk + a.n_vh * a.hv;
     const int c = (int)blockIdx.x * WG + threadIdx.x;
     if (c >= CD) return;
     const int t0 = (int)blockIdx.y * DN_TT, t1 = min(a.T, t0 + DN_TT);
-    float w[KS], win[KM1 > 0 ? KM1 : 1], xs[DN_TT];
+    float w[KS], st[KM1 > 0 ? KM1 : 1], xs[NX];  // xs[j] = in(t0 - KM1 + j)
 #pragma unroll
     for (int k = 0; k < KS; k++) w[k] = a.conv_w[(size_t)c * KS + k];
 #pragma unroll
-    for (int k = 0; k < KM1; k++) win[k] = dn_in<KS>(a, CD, c, t0 - KM1 + k);
-    // every token's input requested before the first is used (one memory
-    // round trip for the 16 tokens, not one per token)
+    for (int k = 0; k < KM1; k++) st[k] = a.conv_state[(size_t)c * KM1 + k];
+    parts_gather(xs, a.qkv, a.qkvs, (size_t)a.T * CD,
+                 [&](int j) { return (size_t)min(max(t0 - KM1 + j, 0), t1 - 1) * CD + c; });
+    if (t0 == 0) {  // t0 is a multiple of DN_TT >= KM1: only the first block reads the state
 #pragma unroll
-    for (int i = 0; i < DN_TT; i++) xs[i] = t0 + i < t1 ? dn_in<KS>(a, CD, c, t0 + i) : 0.f;
+        for (int k = 0; k < KM1; k++) xs[k] = st[k];
+    }
 #pragma unroll
     for (int i = 0; i < DN_TT; i++) {
         if (t0 + i >= t1) break;
-        const float x = xs[i];
-        float acc = w[KM1] * x;
+        float acc = w[KM1] * xs[KM1 + i];
 #pragma unroll
-        for (int k = 0; k < KM1; k++) acc += w[k] * win[k];
+        for (int k = 0; k < KM1; k++) acc += w[k] * xs[i + k];
         a.conv_out[(size_t)(t0 + i) * CD + c] = silu_ref(acc);
-#pragma unroll
-        for (int k = 0; k + 1 < KM1; k++) win[k] = win[k + 1];
-        if (KM1 > 0) win[KM1 - 1] = x;
     }
 }
 
 // the conv state after the chunk: its last KS-1 inputs, oldest first (runs
-// after pf_dn_conv_kernel, which reads the state from before the chunk)
+// after pf_dn_conv_kernel, which reads the state from before the chunk;
+// T >= KS-1, so every one comes from the chunk)
 template <int KS>
 __global__ __launch_bounds__(WG) void pf_dn_conv_state_kernel(PfDnArgs a) {
+    constexpr int KM1 = KS > 1 ? KS - 1 : 1;
     const int CD = 2 * a.n_kh * a.hk + a.n_vh * a.hv;
     const int c = (int)blockIdx.x * WG + threadIdx.x;
-    if (c >= CD) return;
-    float x[KS > 1 ? KS - 1 : 1];
+    if (c >= CD || KS < 2) return;
+    float x[KM1];
+    parts_gather(x, a.qkv, a.qkvs, (size_t)a.T * CD, [&](int k) { return (size_t)(a.T - KM1 + k) * CD + c; });
 #pragma unroll
-    for (int k = 0; k < KS - 1; k++) x[k] = dn_in<KS>(a, CD, c, a.T - (KS - 1) + k);
-#pragma unroll
-    for (int k = 0; k < KS - 1; k++) a.conv_state[(size_t)c * (KS - 1) + k] = x[k];
+    for (int k = 0; k < KM1; k++) a.conv_state[(size_t)c * KM1 + k] = x[k];
 }
 
 // Per token (grid T): l2norm of each k head's q and k (ops.odin:27-37, eps
@@ -425,42 +421,40 @@ __global__ __launch_bounds__(WG) void pf_dn_chunk_kernel(PfDnArgs a) {
     for (int r = 0; r < RPL; r++) S[(size_t)(i0 + r) * HV + j] = s[r];
 }
 
-// gated RMSNorm (forward.odin:211-218): per token (grid T) and value head,
-// out = f16(norm_w[j] (inv o[j]) silu(z[j])), inv = 1 / sqrt(sum o^2 / hv +
-// eps); z from the in_z projection's partial products
+// gated RMSNorm (forward.odin:211-218): per token and value head, out =
+// f16(norm_w[j] (inv o[j]) silu(z[j])), inv = 1 / sqrt(sum o^2 / hv + eps); z
+// from the in_z projection's partial products.  Grid (T, ceil(n_vh / (4
+// GN_NH))): each wave takes GN_NH heads, their o and z requested together.
+constexpr int GN_NH = 2;
 template <int HV>
 __global__ __launch_bounds__(WG) void pf_dn_gnorm_kernel(PfDnArgs a) {
 #pragma clang fp contract(off)
-    constexpr int E = HV / WAVE, NH = 8;  // dimensions per lane; value heads per wave and pass
+    constexpr int E = HV / WAVE, NH = GN_NH, NV = NH * E;  // dimensions per lane; heads per wave
     const int t = blockIdx.x, lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    const int vh0 = ((int)blockIdx.y * (WG / WAVE) + wave) * NH;
+    if (vh0 >= a.n_vh) return;  // whole waves; no workgroup barrier below
     const int VD = a.n_vh * HV;
-    for (int vh0 = wave * NH; vh0 < a.n_vh; vh0 += (WG / WAVE) * NH) {
-        // the pass's o and z values requested before any is used
-        float o[NH][E], z[NH][E];
+    // value v of the wave: head vh0 + v / E (clamped), dimension lane + 64 (v % E)
+    auto at = [&](int v) { return (size_t)t * VD + min(vh0 + v / E, a.n_vh - 1) * HV + lane + WAVE * (v % E); };
+    float o[NV], z[NV];
 #pragma unroll
-        for (int h = 0; h < NH; h++)
+    for (int v = 0; v < NV; v++) o[v] = a.o[at(v)];
+    parts_gather(z, a.z, a.zs, (size_t)a.T * VD, at);
 #pragma unroll
-            for (int e = 0; e < E; e++) {
-                const int vh = min(vh0 + h, a.n_vh - 1), j = lane + WAVE * e;
-                o[h][e] = a.o[(size_t)t * VD + vh * HV + j];
-                z[h][e] = parts_at(a.z, a.zs, (size_t)a.T * VD, (size_t)t * VD + vh * HV + j);
-            }
+    for (int h = 0; h < NH; h++) {
+        if (vh0 + h >= a.n_vh) break;  // uniform
+        const int vh = vh0 + h;
+        float ss = 0.f;
 #pragma unroll
-        for (int h = 0; h < NH; h++) {
-            if (vh0 + h >= a.n_vh) break;  // uniform
-            const int vh = vh0 + h;
-            float ss = 0.f;
+        for (int e = 0; e < E; e++) ss += o[h * E + e] * o[h * E + e];
+        ss = wave_sum(ss);
+        const float inv = 1.0f / sqrtf(ss / (float)HV + a.eps);
 #pragma unroll
-            for (int e = 0; e < E; e++) ss += o[h][e] * o[h][e];
-            ss = wave_sum(ss);
-            const float inv = 1.0f / sqrtf(ss / (float)HV + a.eps);
-#pragma unroll
-            for (int e = 0; e < E; e++) {
-                const int j = lane + WAVE * e;
-                const float v = a.norm_w[j] * (inv * o[h][e]) * silu_ref(z[h][e]);
-                if (a.out32) a.out32[(size_t)t * VD + vh * HV + j] = v;
-                else a.out16[(size_t)t * VD + vh * HV + j] = f2h(v);
-            }
+        for (int e = 0; e < E; e++) {
+            const int j = lane + WAVE * e;
+            const float v = a.norm_w[j] * (inv * o[h * E + e]) * silu_ref(z[h * E + e]);
+            if (a.out32) a.out32[(size_t)t * VD + vh * HV + j] = v;
+            else a.out16[(size_t)t * VD + vh * HV + j] = f2h(v);
         }
     }
 }
@@ -490,7 +484,8 @@ hipError_t launch_pf_deltanet(const PfDnArgs &a, hipStream_t st) {
     if (a.chunk == 16) hipLaunchKernelGGL((pf_dn_chunk_kernel<128, 128, 16>), dgrid, dim3(WG), 0, st, a);
     else if (a.chunk == 32) hipLaunchKernelGGL((pf_dn_chunk_kernel<128, 128, 32>), dgrid, dim3(WG), 0, st, a);
     else hipLaunchKernelGGL((pf_dn_delta_kernel<128, 128>), dgrid, dim3(WG), 0, st, a);
-    hipLaunchKernelGGL(pf_dn_gnorm_kernel<128>, dim3((unsigned)a.T), dim3(WG), 0, st, a);
+    hipLaunchKernelGGL(pf_dn_gnorm_kernel<128>, dim3((unsigned)a.T, nblk(a.n_vh, (WG / WAVE) * GN_NH)), dim3(WG), 0, st,
+                       a);
     return hipGetLastError();
 }
 
