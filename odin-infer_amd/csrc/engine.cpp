@@ -968,6 +968,8 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
                     : std::strcmp(pm, "f32") == 0   ? 2
                     : std::strcmp(pm, "wide") == 0  ? 3
                     : std::strcmp(pm, "fewmfma") == 0 ? 4
+                    : std::strcmp(pm, "dot4") == 0 ? 5
+                    : std::strcmp(pm, "i8") == 0 ? 6
                                                     : 0;
     const char *pc = std::getenv("OI_PREFILL_DN_CHUNK");  // "16" / "32": the chunked delta rule in prefill
     e->pf_dn_chunk = !pc ? 0 : std::strcmp(pc, "16") == 0 ? 16 : std::strcmp(pc, "32") == 0 ? 32 : 0;
@@ -1179,11 +1181,23 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
     const int tr_gu = mm ? MT_MFMA_ROWS : mt_gemv_tile_rows(D, EF), tr_dn = mm ? MT_MFMA_ROWS : mt_gemv_tile_rows(EF, D);
     // few pairs per expert (a short chunk: ~1.4 at 64 tokens of top 10 of 512):
     // items of MT_MFMA_FEW pairs with the x rows staged once
-    const bool few = mm && (e->pf_experts == 0 || e->pf_experts == 4) && L.gexp.type == T_Q4_K &&
+    const int px = e->pf_experts;
+    const bool few = mm && (px == 0 || px == 4 || px == 5 || px == 6) && L.gexp.type == T_Q4_K &&
                      L.dexp.type == T_Q4_K &&
                      pairs <= MT_MFMA_FEW * NE && D <= 4096 && EF <= 4096 && D % MT_MFMA_ROWS == 0 &&
                      EF % MT_MFMA_ROWS == 0;
     const int ps = few ? MT_MFMA_FEW : mm ? MT_MFMA_PAIRS : MT_PAIR_SLICE;
+    // few pairs, where the shapes allow: gate/up on the token loop's int8 dot4
+    // arithmetic, down on int8 planes of x on the matrix cores with items of
+    // half the rows (measured fastest that way round at 64 tokens of config 5);
+    // OI_PREFILL_EXPERTS=dot4 / i8: that kernel for both, fewmfma: f16 MFMA
+    const int tiles_qi = D % 128 == 0 ? 2 : 1;
+    const bool i8_gu = few && mt_q4i8_supported(L.gexp, D, EF) && mt_q4i8_supported(L.uexp, D, EF);
+    const bool d4_gu = few && mt_dot4_supported(L.gexp, D, EF) && mt_dot4_supported(L.uexp, D, EF);
+    const bool gu_i8 = i8_gu && (px == 6 || (px == 0 && !d4_gu));
+    const bool gu_d4 = !gu_i8 && d4_gu && (px == 0 || px == 5);
+    const bool dn_i8 = few && mt_q4i8_supported(L.dexp, EF, D / tiles_qi) && (px == 0 || px == 6);
+    const bool dn_d4 = !dn_i8 && few && mt_dot4_supported(L.dexp, EF, D) && (px == 0 || px == 5);
     PfMoeArgs ma{};
     ma.logits = e->pf_lg;
     if (L.shared) ma.sh_inp = L.sh_inp;
@@ -1197,7 +1211,7 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
     ma.T = T; ma.n_experts = E; ma.top_k = (int32_t)e->top_k; ma.kp = KP;
     ma.norm_topk = 1;  // Qwen3-MoE / Qwen3-Next renormalize the chosen weights
     ma.tiles_gu = few ? 1 : (EF + tr_gu - 1) / tr_gu;  // a few-pair item covers every row tile
-    ma.tiles_dn = few ? 1 : (D + tr_dn - 1) / tr_dn;
+    ma.tiles_dn = dn_i8 ? tiles_qi : few ? 1 : (D + tr_dn - 1) / tr_dn;
     ma.dim = D;
     ma.pair_slice = ps;
     HIP_TRY(launch_pf_moe_route(ma, st));
@@ -1214,10 +1228,8 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
     g.list = e->pf_list; g.off = e->pf_off; g.cnt = e->pf_cnt;
     g.items = e->pf_items_gu; g.nitems = e->pf_nitems;
     g.pair_slice = ps;
-    // few pairs: the int8 dot4 kernel where the shapes allow it (not OI_PREFILL_EXPERTS=fewmfma)
-    const bool dot4 = few && e->pf_experts == 0 && mt_dot4_supported(L.gexp, D, EF) &&
-                      mt_dot4_supported(L.uexp, D, EF) && mt_dot4_supported(L.dexp, EF, D);
-    HIP_TRY(dot4 ? launch_mt_dot4(g, item_tiles, st)
+    HIP_TRY(gu_i8 ? launch_mt_q4i8(g, item_tiles, st)
+            : gu_d4 ? launch_mt_dot4(g, item_tiles, st)
             : mm ? launch_mt_mfma(g, item_tiles * ma.tiles_gu, st, e->pf_experts == 2)
                  : launch_mt_gemv(g, item_tiles * ma.tiles_gu, st));
     MtGemvArgs d{};
@@ -1226,12 +1238,13 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
     d.x = e->pf_h; d.y = e->pf_yd;
     if (few) {
         d.x2 = e->pf_h2;
-        d.tiles = 1;
+        d.tiles = ma.tiles_dn;
     }
     d.list = e->pf_list; d.off = e->pf_off; d.cnt = e->pf_cnt;
     d.items = e->pf_items_dn; d.nitems = e->pf_nitems + 1;
     d.pair_slice = ps;
-    HIP_TRY(dot4 ? launch_mt_dot4(d, item_tiles, st)
+    HIP_TRY(dn_i8 ? launch_mt_q4i8(d, item_tiles * ma.tiles_dn, st)
+            : dn_d4 ? launch_mt_dot4(d, item_tiles, st)
             : mm ? launch_mt_mfma(d, item_tiles * ma.tiles_dn, st, e->pf_experts == 2)
                  : launch_mt_gemv(d, item_tiles * ma.tiles_dn, st));
     HIP_TRY(launch_pf_moe_combine(ma, st));

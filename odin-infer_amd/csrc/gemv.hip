@@ -1192,4 +1192,228 @@ hipError_t launch_mt_dot4(const MtGemvArgs &a, int max_items, hipStream_t st) {
     return hipGetLastError();
 }
 
+// mt_q4i8_kernel: the same few-pair items on the matrix cores
+// (v_mfma_i32_16x16x32_i8).  Each pair's x row (silu(x) * x2 when x2 is set)
+// is scaled by one factor per row, s = max|x| / QI_MAX, to integers below
+// 2^28 (rounded from the f32 product, so within 2^-24 of the row maximum)
+// and split into four 7-bit planes, the top one signed: x = s (2^21 h +
+// 2^14 p2 + 2^7 p1 + p0).  The 16 rows of the MFMA's A operand are (plane,
+// pair); its B operand is 16 weight rows' 4-bit quants of one 32-weight group
+// as they are stored (the low nibbles of a 64-weight unit are its first
+// group, the high nibbles its second), so the weights need two logic
+// operations per 8 bytes.  Per group the integer products are scaled by the
+// row's 6-bit group scale in int32 (|sum| < 2^31 over a super-block), per
+// super-block by d in f32; the min term, dmin m_g sum(x over the group), runs
+// beside it in f32.  An item is (expert, pair slice, row tile of rows /
+// tiles rows, one matrix); a wave takes 16-row tiles of it (lane (n, G): row
+// n; plane G of the four pairs for the products, pair G for the min term) and
+// walks K one super-block per step with the next two steps' weights in
+// flight; the planes are combined across lanes at the end of a tile into
+// one result per lane (row n, pair G), held in registers until the last tile
+// (stores in the loop would share the memory counter with the weight loads).
+constexpr float QI_MAX = 268434432.f;  // 2^28 - 2^10: the rounded product stays below 2^28
+constexpr int QI_MAXT = 16;            // 16-row tiles per wave (rows of an item <= 16 * 16 * 4)
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+template <int XI>
+__global__ __launch_bounds__(WG) void mt_q4i8_kernel(MtGemvArgs a) {
+    extern __shared__ __attribute__((aligned(16))) u32x4 md_smem[];
+    constexpr int NP = MT_MFMA_FEW, NWV = WG / WAVE, NSTG = 3;
+    static_assert(NP == 4, "the A operand's 16 rows are 4 planes x 4 pairs");
+    const bool second = a.mat_items > 0 && (int)blockIdx.x >= a.mat_items;
+    const int it = second ? (int)blockIdx.x - a.mat_items : (int)blockIdx.x;
+    if (it >= *a.nitems) return;
+    const int K = a.K, U = K >> 6, NSB = K >> 8;
+    const int e = a.items[2 * it], slice = a.items[2 * it + 1] >> 16, tile = a.items[2 * it + 1] & 0xFFFF;
+    const int base = a.off[e] + slice * NP, n = min(NP, a.cnt[e] - slice * NP);
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid / WAVE, G = lane >> 4;
+    const int rows = a.rows / a.tiles, row0 = tile * rows;
+    const DMat m = sub_rows(second ? a.m2 : a.m, e * a.rows + row0, rows);
+    float *y = (second ? a.y2 : a.y) + row0;
+    // LDS: the A operand [unit][lane] (16 B per lane: group g = lane / 16 of
+    // the unit's first 32 weights, then of its second), the group sums
+    // [pair][K/32], the scales and the wave maxima
+    u32x4 *xa = md_smem;
+    float *xsum = (float *)(xa + U * WAVE);
+    float *xsc = xsum + NP * (K / 32);  // [NP] scales, then [NWV][NP] wave maxima
+    struct Step {
+        u32x4 h;
+        u32x2 q[4];
+    };
+    const int nstep = (rows / (16 * NWV)) * NSB;  // rows % (16 NWV) == 0
+    auto issue = [&](int s, Step &w) {
+        const int s2 = min(s, nstep - 1), ti = s2 / NSB, sb = s2 - ti * NSB;
+        const int r = (ti * NWV + wave) * 16 + (lane & 15);
+        // cached loads: a step reads 32 of each 128-byte line per row and
+        // plane, the next three instructions and the next step the rest
+        w.h = *(const u32x4 *)(m.s + ((size_t)r * NSB + sb) * 16);
+        const uint8_t *qb = m.q + (size_t)(G >> 1) * m.plane + (G & 1) * 8;
+#pragma unroll
+        for (int k = 0; k < 4; k++) w.q[k] = *(const u32x2 *)(qb + ((size_t)r * U + 4 * sb + k) * 16);
+    };
+    Step ring[NSTG];
+#pragma unroll
+    for (int i = 0; i < NSTG - 1; i++) issue(i, ring[i]);
+    // every pair's x (and x2) requested before any is used
+    float4 xv[NP][XI], uv[NP][XI];
+#pragma unroll
+    for (int pj = 0; pj < NP; pj++) {
+        const size_t xo = (size_t)(a.list[base + min(pj, n - 1)] / a.xdiv) * K;
+#pragma unroll
+        for (int i = 0; i < XI; i++) {
+            const int c = min(tid + i * WG, K / 4 - 1);
+            xv[pj][i] = ((const float4 *)(a.x + xo))[c];
+            uv[pj][i] = a.x2 ? ((const float4 *)(a.x2 + xo))[c] : float4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    float amax[NP];
+#pragma unroll
+    for (int pj = 0; pj < NP; pj++) {
+        amax[pj] = 0.f;
+#pragma unroll
+        for (int i = 0; i < XI; i++) {
+            float4 v = xv[pj][i];
+            if (a.x2) {  // SwiGLU (infer/forward.odin:188-193)
+#pragma clang fp contract(off)
+                const float4 u = uv[pj][i];
+                v.x *= 1.0f / (1.0f + expf(-v.x));
+                v.y *= 1.0f / (1.0f + expf(-v.y));
+                v.z *= 1.0f / (1.0f + expf(-v.z));
+                v.w *= 1.0f / (1.0f + expf(-v.w));
+                v.x *= u.x;
+                v.y *= u.y;
+                v.z *= u.z;
+                v.w *= u.w;
+                xv[pj][i] = v;
+            }
+            if (tid + i * WG < K / 4)
+                amax[pj] = fmaxf(amax[pj], fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
+        amax[pj] = wave_max_all(amax[pj]);
+        if (lane == 0) xsc[NP + wave * NP + pj] = amax[pj];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int pj = 0; pj < NP; pj++) {
+        float mx = 0.f;
+#pragma unroll
+        for (int w = 0; w < NWV; w++) mx = fmaxf(mx, xsc[NP + w * NP + pj]);
+        const float inv = mx > 0.f ? QI_MAX / mx : 0.f;
+#pragma unroll
+        for (int i = 0; i < XI; i++) {
+            const int c = tid + i * WG;  // float4 c: elements 4c..4c+3 (K / 4 is a multiple of 64: whole waves)
+            if (c >= K / 4) break;
+            const float4 v = xv[pj][i];
+            const float sum = (v.x + v.y) + (v.z + v.w);
+            const float sum16 = dpp_sum4(sum);
+            const float sum32 = sum16 + dpp_mirror8(sum16);  // the 8 lanes of one 32-element group
+            if ((c & 7) == 0) xsum[pj * (K / 32) + (c >> 3)] = sum32;
+            const int q[4] = {(int)rintf(v.x * inv), (int)rintf(v.y * inv), (int)rintf(v.z * inv),
+                              (int)rintf(v.w * inv)};
+            // unit c / 16, group g = (c / 2) % 4 of its first (c % 16 < 8) or second half
+            uint32_t *cell = (uint32_t *)(xa + (c >> 4) * WAVE + ((c >> 1) & 3) * 16) + ((c >> 3) & 1) * 2 + (c & 1);
+#pragma unroll
+            for (int pl = 0; pl < 4; pl++) {
+                const int sh = 21 - 7 * pl;
+                uint32_t b = 0;
+#pragma unroll
+                for (int k = 0; k < 4; k++) b |= ((uint32_t)(q[k] >> sh) & (pl == 0 ? 0xFFu : 0x7Fu)) << (8 * k);
+                cell[(4 * pl + pj) * 4] = b;  // A row 4 plane + pair
+            }
+        }
+        if (tid == 0) xsc[pj] = mx / QI_MAX;
+    }
+    __syncthreads();
+    float facc[4] = {0.f, 0.f, 0.f, 0.f}, fmin = 0.f;
+    float res[QI_MAXT];  // tile results, the latest last
+#pragma unroll
+    for (int k = 0; k < QI_MAXT; k++) res[k] = 0.f;
+    const float pw = G == 0 ? 2097152.f : G == 1 ? 16384.f : G == 2 ? 128.f : 1.f;  // plane weight 2^(21 - 7 G)
+    auto compute = [&](int s, const Step &w) {
+        const int ti = s / NSB, sb = s - ti * NSB;
+        const float d = h2f(w.h.x & 0xFFFFu), dmin = h2f(w.h.x >> 16);
+        i32x4 iacc = {0, 0, 0, 0};
+        float mf = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int u = 4 * sb + k;
+            uint32_t sc0, m0, sc1, m1;
+            q4k_scales(k, w.h.y, w.h.z, w.h.w, sc0, m0, sc1, m1);
+            const u32x4 xo = xa[u * WAVE + lane];
+            const uint32_t lo0 = w.q[k].x & 0x0F0F0F0Fu, lo1 = w.q[k].y & 0x0F0F0F0Fu;
+            const uint32_t hi0 = (w.q[k].x >> 4) & 0x0F0F0F0Fu, hi1 = (w.q[k].y >> 4) & 0x0F0F0F0Fu;
+            const i32x4 z = {0, 0, 0, 0};
+            const i32x4 dA = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+                (long)(((uint64_t)xo.y << 32) | xo.x), (long)(((uint64_t)lo1 << 32) | lo0), z, 0, 0, 0);
+            const i32x4 dB = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+                (long)(((uint64_t)xo.w << 32) | xo.z), (long)(((uint64_t)hi1 << 32) | hi0), z, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 4; v++) iacc[v] += __mul24((int)sc0, dA[v]) + __mul24((int)sc1, dB[v]);  // |dA| < 2^23
+            const float2 xs2 = *(const float2 *)&xsum[G * (K / 32) + 2 * u];
+            mf += (float)m0 * xs2.x + (float)m1 * xs2.y;
+        }
+#pragma unroll
+        for (int v = 0; v < 4; v++) facc[v] += d * (float)iacc[v];
+        fmin += dmin * mf;
+        if (sb == NSB - 1) {  // the tile's row n = lane % 16 is done: combine the planes
+            float t[4];
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                t[v] = pw * facc[v];
+                t[v] += __shfl_xor(t[v], 16, WAVE);
+                t[v] += __shfl_xor(t[v], 32, WAVE);
+                facc[v] = 0.f;
+            }
+            const float S = G == 0 ? t[0] : G == 1 ? t[1] : G == 2 ? t[2] : t[3];
+#pragma unroll
+            for (int k = 0; k + 1 < QI_MAXT; k++) res[k] = res[k + 1];
+            res[QI_MAXT - 1] = xsc[G] * S - fmin;
+            fmin = 0.f;
+        }
+    };
+    // NSTG steps per pass, so each stage index is static; every pass issues
+    // the same loads (clamped to the last step), only the computation stops
+    for (int st = 0; st < nstep; st += NSTG) {
+#pragma unroll
+        for (int i = 0; i < NSTG; i++) {
+            issue(st + i + NSTG - 1, ring[(i + NSTG - 1) % NSTG]);
+            if (st + i < nstep) compute(st + i, ring[i]);
+        }
+    }
+    if (G < n) {
+        const int ntl = rows / (16 * NWV);  // the wave's tiles: tile i's result is res[QI_MAXT - ntl + i]
+        float *yr = y + (size_t)a.list[base + G] * a.rows + wave * 16 + (lane & 15);
+#pragma unroll
+        for (int k = 0; k < QI_MAXT; k++) {
+            const int i = k - (QI_MAXT - ntl);
+            if (i >= 0) yr[(size_t)i * NWV * 16] = res[k];
+        }
+    }
+}
+
+static size_t mt_q4i8_lds(int32_t K) {
+    return (size_t)(K / 64) * WAVE * 16 + (size_t)MT_MFMA_FEW * (K / 32) * 4 +
+           (size_t)(MT_MFMA_FEW + (WG / WAVE) * MT_MFMA_FEW) * 4;
+}
+
+// rows: the rows of one row tile
+bool mt_q4i8_supported(const DMat &m, int32_t K, int32_t rows) {
+    return m.type == T_Q4_K && m.cols == K && K % 256 == 0 && K <= 4096 && rows > 0 &&
+           rows % (16 * (WG / WAVE)) == 0 && rows <= QI_MAXT * 16 * (WG / WAVE);
+}
+
+hipError_t launch_mt_q4i8(const MtGemvArgs &a, int max_items, hipStream_t st) {
+    if (a.tiles < 1 || a.rows % a.tiles || !mt_q4i8_supported(a.m, a.K, a.rows / a.tiles) ||
+        (a.swiglu && (!mt_q4i8_supported(a.m2, a.K, a.rows / a.tiles) || !a.y2)) || a.m.rows < a.rows ||
+        a.pair_slice != MT_MFMA_FEW || a.xdiv <= 0 || max_items <= 0 || a.dense_n > 0)
+        return hipErrorInvalidValue;
+    MtGemvArgs b = a;
+    b.mat_items = a.swiglu ? max_items : 0;  // gate into y, up into y2 (the SwiGLU is the consumer's)
+    const size_t lds = mt_q4i8_lds(a.K);
+    const dim3 grid((unsigned)(a.swiglu ? 2 * max_items : max_items));
+    if (a.K <= 1024) hipLaunchKernelGGL(mt_q4i8_kernel<1>, grid, dim3(WG), lds, st, b);
+    else if (a.K <= 2048) hipLaunchKernelGGL(mt_q4i8_kernel<2>, grid, dim3(WG), lds, st, b);
+    else hipLaunchKernelGGL(mt_q4i8_kernel<4>, grid, dim3(WG), lds, st, b);
+    return hipGetLastError();
+}
+
 }  // namespace oi

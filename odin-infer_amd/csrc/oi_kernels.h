@@ -300,6 +300,8 @@ constexpr int MT_MFMA_FEW = 4;
 // int8 dot4 arithmetic (gemv.hip): Q4_K with K / 64 in {8, 16, 32, 64}
 bool mt_dot4_supported(const DMat &m, int32_t K, int32_t rows);
 hipError_t launch_mt_dot4(const MtGemvArgs &a, int max_items, hipStream_t st);
+bool mt_q4i8_supported(const DMat &m, int32_t K, int32_t rows);
+hipError_t launch_mt_q4i8(const MtGemvArgs &a, int max_items, hipStream_t st);
 bool mt_mfma_supported(const DMat &m, int32_t K, int32_t rows);
 hipError_t launch_mt_mfma(const MtGemvArgs &a, int max_items, hipStream_t st, bool f32_only = false);
 struct PfMoeArgs {

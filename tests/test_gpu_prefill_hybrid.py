@@ -155,10 +155,12 @@ def test_prefill_split_calls_agree(make_model):
 @pytest.mark.parametrize("shape,n", [("c5", 200), ("c5", 64), ("c4", 200), ("c4", 48)])
 def test_prefill_expert_kernels_agree(tmp_path, monkeypatch, shape, n):
     """The routed experts of a chunk on the expert kernels: items of up to 4
-    pairs on the decode GEMV's int8 dot4 arithmetic (x quantized to 22 bits
-    per group of 32; the default when the chunk's pairs average at most 4 per
-    expert: 64 tokens at C5, 48 at C4) or on f16 MFMA (OI_PREFILL_EXPERTS=
-    fewmfma); Q4_K quants on f16 MFMA with the scales applied per 32 weights
+    pairs (the default when the chunk's pairs average at most 4 per expert:
+    64 tokens at C5, 48 at C4) with gate/up on the decode GEMV's int8 dot4
+    arithmetic (x quantized to 22 bits per group of 32) and down on int8 MFMA
+    (x scaled per row to 28-bit integers in four planes), both on dot4
+    (OI_PREFILL_EXPERTS=dot4), both on int8 MFMA (i8) or on f16 MFMA
+    (fewmfma); Q4_K quants on f16 MFMA with the scales applied per 32 weights
     in f32 and x split hi + lo in items of up to 16 pairs (the default
     otherwise; OI_PREFILL_EXPERTS=wide), the
     decoded weights on f32 MFMA (OI_PREFILL_EXPERTS=f32, the default for
@@ -175,7 +177,7 @@ def test_prefill_expert_kernels_agree(tmp_path, monkeypatch, shape, n):
     synth.write_gguf(path, spec)
     toks = _tokens(13, n, 4096)
     out = {}
-    for kind in ("default", "fewmfma", "wide", "f32", "gemv"):
+    for kind in ("default", "dot4", "i8", "fewmfma", "wide", "f32", "gemv"):
         monkeypatch.setenv("OI_PREFILL_EXPERTS", kind)
         e, ok = infer.engine_load(str(path), infer.Engine_Opts(max_ctx=256))
         assert ok
@@ -183,7 +185,7 @@ def test_prefill_expert_kernels_agree(tmp_path, monkeypatch, shape, n):
             out[kind] = infer.engine_forward_batch(e, toks, 0).copy()
         finally:
             infer.engine_destroy(e)
-    for kind in ("fewmfma", "wide", "f32", "gemv"):
+    for kind in ("dot4", "i8", "fewmfma", "wide", "f32", "gemv"):
         err = scaled_err(out["default"], out[kind])
         print("%s n=%d: default vs %s experts %.3g" % (shape, n, kind, err))
         assert err <= 1e-5, kind
