@@ -1187,14 +1187,15 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
                      pairs <= MT_MFMA_FEW * NE && D <= 4096 && EF <= 4096 && D % MT_MFMA_ROWS == 0 &&
                      EF % MT_MFMA_ROWS == 0;
     const int ps = few ? MT_MFMA_FEW : mm ? MT_MFMA_PAIRS : MT_PAIR_SLICE;
-    // few pairs, where the shapes allow: gate/up on the token loop's int8 dot4
-    // arithmetic, down on int8 planes of x on the matrix cores with items of
-    // half the rows (measured fastest that way round at 64 tokens of config 5);
-    // OI_PREFILL_EXPERTS=dot4 / i8: that kernel for both, fewmfma: f16 MFMA
+    // few pairs, where the shapes allow: int8 planes of x on the matrix cores
+    // with items of half the rows (64 tokens of config 5: gate/up 120 us, down
+    // 58 us per layer, against 141 / 94 us on the token loop's int8 dot4
+    // arithmetic); OI_PREFILL_EXPERTS=dot4: dot4, fewmfma: f16 MFMA
     const int tiles_qi = D % 128 == 0 ? 2 : 1;
-    const bool i8_gu = few && mt_q4i8_supported(L.gexp, D, EF) && mt_q4i8_supported(L.uexp, D, EF);
+    const int tiles_qg = EF % 128 == 0 ? 2 : 1;
+    const bool i8_gu = few && mt_q4i8_supported(L.gexp, D, EF / tiles_qg) && mt_q4i8_supported(L.uexp, D, EF / tiles_qg);
     const bool d4_gu = few && mt_dot4_supported(L.gexp, D, EF) && mt_dot4_supported(L.uexp, D, EF);
-    const bool gu_i8 = i8_gu && (px == 6 || (px == 0 && !d4_gu));
+    const bool gu_i8 = i8_gu && (px == 0 || px == 6);
     const bool gu_d4 = !gu_i8 && d4_gu && (px == 0 || px == 5);
     const bool dn_i8 = few && mt_q4i8_supported(L.dexp, EF, D / tiles_qi) && (px == 0 || px == 6);
     const bool dn_d4 = !dn_i8 && few && mt_dot4_supported(L.dexp, EF, D) && (px == 0 || px == 5);
@@ -1210,7 +1211,8 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
     ma.out = e->pf_p[0];
     ma.T = T; ma.n_experts = E; ma.top_k = (int32_t)e->top_k; ma.kp = KP;
     ma.norm_topk = 1;  // Qwen3-MoE / Qwen3-Next renormalize the chosen weights
-    ma.tiles_gu = few ? 1 : (EF + tr_gu - 1) / tr_gu;  // a few-pair item covers every row tile
+    // a few-pair item covers every row tile, or half the rows on int8 MFMA
+    ma.tiles_gu = gu_i8 ? tiles_qg : few ? 1 : (EF + tr_gu - 1) / tr_gu;
     ma.tiles_dn = dn_i8 ? tiles_qi : few ? 1 : (D + tr_dn - 1) / tr_dn;
     ma.dim = D;
     ma.pair_slice = ps;
@@ -1223,12 +1225,12 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
     g.x = e->pf_xn; g.y = e->pf_h;
     if (few) {  // gate rows to pf_h, up rows to pf_h2; the down launch applies the SwiGLU
         g.y2 = e->pf_h2;
-        g.tiles = 1;
+        g.tiles = ma.tiles_gu;
     }
     g.list = e->pf_list; g.off = e->pf_off; g.cnt = e->pf_cnt;
     g.items = e->pf_items_gu; g.nitems = e->pf_nitems;
     g.pair_slice = ps;
-    HIP_TRY(gu_i8 ? launch_mt_q4i8(g, item_tiles, st)
+    HIP_TRY(gu_i8 ? launch_mt_q4i8(g, item_tiles * ma.tiles_gu, st)
             : gu_d4 ? launch_mt_dot4(g, item_tiles, st)
             : mm ? launch_mt_mfma(g, item_tiles * ma.tiles_gu, st, e->pf_experts == 2)
                  : launch_mt_gemv(g, item_tiles * ma.tiles_gu, st));

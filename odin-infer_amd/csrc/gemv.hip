@@ -1201,7 +1201,9 @@ hipError_t launch_mt_dot4(const MtGemvArgs &a, int max_items, hipStream_t st) {
 // pair); its B operand is 16 weight rows' 4-bit quants of one 32-weight group
 // as they are stored (the low nibbles of a 64-weight unit are its first
 // group, the high nibbles its second), so the weights need two logic
-// operations per 8 bytes.  Per group the integer products are scaled by the
+// operations per 8 bytes; they pass through a per-wave LDS staging area so
+// that the loads read whole units (16 bytes per lane) while the operand
+// takes 8 bytes of each of four units.  Per group the integer products are scaled by the
 // row's 6-bit group scale in int32 (|sum| < 2^31 over a super-block), per
 // super-block by d in f32; the min term, dmin m_g sum(x over the group), runs
 // beside it in f32.  An item is (expert, pair slice, row tile of rows /
@@ -1214,6 +1216,7 @@ hipError_t launch_mt_dot4(const MtGemvArgs &a, int max_items, hipStream_t st) {
 constexpr float QI_MAX = 268434432.f;  // 2^28 - 2^10: the rounded product stays below 2^28
 constexpr int QI_MAXT = 16;            // 16-row tiles per wave (rows of an item <= 16 * 16 * 4)
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+constexpr int QI_SROW = 144;  // staging row stride in bytes (128 + 16 against bank conflicts)
 template <int XI>
 __global__ __launch_bounds__(WG) void mt_q4i8_kernel(MtGemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) u32x4 md_smem[];
@@ -1235,20 +1238,21 @@ __global__ __launch_bounds__(WG) void mt_q4i8_kernel(MtGemvArgs a) {
     u32x4 *xa = md_smem;
     float *xsum = (float *)(xa + U * WAVE);
     float *xsc = xsum + NP * (K / 32);  // [NP] scales, then [NWV][NP] wave maxima
+    uint8_t *stg = (uint8_t *)(xsc + NP + NWV * NP) + wave * 16 * QI_SROW;  // the wave's weight staging
     struct Step {
-        u32x4 h;
-        u32x2 q[4];
+        u32x4 h, q0, q1;
     };
     const int nstep = (rows / (16 * NWV)) * NSB;  // rows % (16 NWV) == 0
     auto issue = [&](int s, Step &w) {
         const int s2 = min(s, nstep - 1), ti = s2 / NSB, sb = s2 - ti * NSB;
         const int r = (ti * NWV + wave) * 16 + (lane & 15);
-        // cached loads: a step reads 32 of each 128-byte line per row and
-        // plane, the next three instructions and the next step the rest
+        // lane (n, G): both planes of unit 4 sb + G, so each instruction reads
+        // 64 contiguous bytes per row and plane (cached loads: the next step
+        // reads the other half of each 128-byte line)
         w.h = *(const u32x4 *)(m.s + ((size_t)r * NSB + sb) * 16);
-        const uint8_t *qb = m.q + (size_t)(G >> 1) * m.plane + (G & 1) * 8;
-#pragma unroll
-        for (int k = 0; k < 4; k++) w.q[k] = *(const u32x2 *)(qb + ((size_t)r * U + 4 * sb + k) * 16);
+        const size_t ui = (size_t)r * U + 4 * sb + G;
+        w.q0 = *(const u32x4 *)(m.q + ui * 16);
+        w.q1 = *(const u32x4 *)(m.q + m.plane + ui * 16);
     };
     Step ring[NSTG];
 #pragma unroll
@@ -1333,14 +1337,24 @@ __global__ __launch_bounds__(WG) void mt_q4i8_kernel(MtGemvArgs a) {
         const float d = h2f(w.h.x & 0xFFFFu), dmin = h2f(w.h.x >> 16);
         i32x4 iacc = {0, 0, 0, 0};
         float mf = 0.f;
+        // through the wave's LDS rows (one wave's LDS operations complete in
+        // order): lane (n, g) then takes dwords 2g, 2g+1 of each unit, the B
+        // operand layout (group g = the unit's weights 8g .. 8g+7 of each half)
+        u32x2 wq[4];
+        asm volatile("" ::: "memory");  // the previous step's reads stay before these writes
+        uint8_t *sr = stg + (lane & 15) * QI_SROW;
+        *(u32x4 *)(sr + G * 32) = w.q0;
+        *(u32x4 *)(sr + G * 32 + 16) = w.q1;
+#pragma unroll
+        for (int k = 0; k < 4; k++) wq[k] = *(const u32x2 *)(sr + k * 32 + 8 * G);
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             const int u = 4 * sb + k;
             uint32_t sc0, m0, sc1, m1;
             q4k_scales(k, w.h.y, w.h.z, w.h.w, sc0, m0, sc1, m1);
             const u32x4 xo = xa[u * WAVE + lane];
-            const uint32_t lo0 = w.q[k].x & 0x0F0F0F0Fu, lo1 = w.q[k].y & 0x0F0F0F0Fu;
-            const uint32_t hi0 = (w.q[k].x >> 4) & 0x0F0F0F0Fu, hi1 = (w.q[k].y >> 4) & 0x0F0F0F0Fu;
+            const uint32_t lo0 = wq[k].x & 0x0F0F0F0Fu, lo1 = wq[k].y & 0x0F0F0F0Fu;
+            const uint32_t hi0 = (wq[k].x >> 4) & 0x0F0F0F0Fu, hi1 = (wq[k].y >> 4) & 0x0F0F0F0Fu;
             const i32x4 z = {0, 0, 0, 0};
             const i32x4 dA = __builtin_amdgcn_mfma_i32_16x16x32_i8(
                 (long)(((uint64_t)xo.y << 32) | xo.x), (long)(((uint64_t)lo1 << 32) | lo0), z, 0, 0, 0);
@@ -1392,7 +1406,7 @@ __global__ __launch_bounds__(WG) void mt_q4i8_kernel(MtGemvArgs a) {
 
 static size_t mt_q4i8_lds(int32_t K) {
     return (size_t)(K / 64) * WAVE * 16 + (size_t)MT_MFMA_FEW * (K / 32) * 4 +
-           (size_t)(MT_MFMA_FEW + (WG / WAVE) * MT_MFMA_FEW) * 4;
+           (size_t)(MT_MFMA_FEW + (WG / WAVE) * MT_MFMA_FEW) * 4 + (size_t)(WG / WAVE) * 16 * QI_SROW;
 }
 
 // rows: the rows of one row tile

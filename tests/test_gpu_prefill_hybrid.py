@@ -156,11 +156,10 @@ def test_prefill_split_calls_agree(make_model):
 def test_prefill_expert_kernels_agree(tmp_path, monkeypatch, shape, n):
     """The routed experts of a chunk on the expert kernels: items of up to 4
     pairs (the default when the chunk's pairs average at most 4 per expert:
-    64 tokens at C5, 48 at C4) with gate/up on the decode GEMV's int8 dot4
-    arithmetic (x quantized to 22 bits per group of 32) and down on int8 MFMA
-    (x scaled per row to 28-bit integers in four planes), both on dot4
-    (OI_PREFILL_EXPERTS=dot4), both on int8 MFMA (i8) or on f16 MFMA
-    (fewmfma); Q4_K quants on f16 MFMA with the scales applied per 32 weights
+    64 tokens at C5, 48 at C4) on int8 MFMA (x scaled per row to 28-bit
+    integers in four planes; OI_PREFILL_EXPERTS=i8 forces it), on the decode
+    GEMV's int8 dot4 arithmetic (x quantized to 22 bits per group of 32;
+    dot4) or on f16 MFMA (fewmfma); Q4_K quants on f16 MFMA with the scales applied per 32 weights
     in f32 and x split hi + lo in items of up to 16 pairs (the default
     otherwise; OI_PREFILL_EXPERTS=wide), the
     decoded weights on f32 MFMA (OI_PREFILL_EXPERTS=f32, the default for
