@@ -1207,20 +1207,20 @@ hipError_t launch_mt_dot4(const MtGemvArgs &a, int max_items, hipStream_t st) {
 // row's 6-bit group scale in int32 (|sum| < 2^31 over a super-block), per
 // super-block by d in f32; the min term, dmin m_g sum(x over the group), runs
 // beside it in f32.  An item is (expert, pair slice, row tile of rows /
-// tiles rows, one matrix); a wave takes 16-row tiles of it (lane (n, G): row
-// n; plane G of the four pairs for the products, pair G for the min term) and
-// walks K one super-block per step with the next two steps' weights in
-// flight; the planes are combined across lanes at the end of a tile into
+// tiles rows, one matrix); each of its 8 waves takes 16-row tiles of it
+// (lane (n, G): row n; plane G of the four pairs for the products, pair G for
+// the min term) and walks K one super-block per step with the next step's
+// weights in flight (deeper rings measured no faster); the planes are combined across lanes at the end of a tile into
 // one result per lane (row n, pair G), held in registers until the last tile
 // (stores in the loop would share the memory counter with the weight loads).
 constexpr float QI_MAX = 268434432.f;  // 2^28 - 2^10: the rounded product stays below 2^28
-constexpr int QI_MAXT = 16;            // 16-row tiles per wave (rows of an item <= 16 * 16 * 4)
+constexpr int QI_MAXT = 16;            // 16-row tiles per wave (rows of an item <= 16 * 16 * waves)
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 constexpr int QI_SROW = 144;  // staging row stride in bytes (128 + 16 against bank conflicts)
-template <int XI>
-__global__ __launch_bounds__(WG) void mt_q4i8_kernel(MtGemvArgs a) {
+template <int XI, int NWV>
+__global__ __launch_bounds__(NWV * WAVE) void mt_q4i8_kernel(MtGemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) u32x4 md_smem[];
-    constexpr int NP = MT_MFMA_FEW, NWV = WG / WAVE, NSTG = 3;
+    constexpr int NP = MT_MFMA_FEW, QW = NWV * WAVE, NSTG = 2;
     static_assert(NP == 4, "the A operand's 16 rows are 4 planes x 4 pairs");
     const bool second = a.mat_items > 0 && (int)blockIdx.x >= a.mat_items;
     const int it = second ? (int)blockIdx.x - a.mat_items : (int)blockIdx.x;
@@ -1264,7 +1264,7 @@ __global__ __launch_bounds__(WG) void mt_q4i8_kernel(MtGemvArgs a) {
         const size_t xo = (size_t)(a.list[base + min(pj, n - 1)] / a.xdiv) * K;
 #pragma unroll
         for (int i = 0; i < XI; i++) {
-            const int c = min(tid + i * WG, K / 4 - 1);
+            const int c = min(tid + i * QW, K / 4 - 1);
             xv[pj][i] = ((const float4 *)(a.x + xo))[c];
             uv[pj][i] = a.x2 ? ((const float4 *)(a.x2 + xo))[c] : float4{0.f, 0.f, 0.f, 0.f};
         }
@@ -1289,7 +1289,7 @@ __global__ __launch_bounds__(WG) void mt_q4i8_kernel(MtGemvArgs a) {
                 v.w *= u.w;
                 xv[pj][i] = v;
             }
-            if (tid + i * WG < K / 4)
+            if (tid + i * QW < K / 4)
                 amax[pj] = fmaxf(amax[pj], fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
         }
         amax[pj] = wave_max_all(amax[pj]);
@@ -1304,7 +1304,7 @@ __global__ __launch_bounds__(WG) void mt_q4i8_kernel(MtGemvArgs a) {
         const float inv = mx > 0.f ? QI_MAX / mx : 0.f;
 #pragma unroll
         for (int i = 0; i < XI; i++) {
-            const int c = tid + i * WG;  // float4 c: elements 4c..4c+3 (K / 4 is a multiple of 64: whole waves)
+            const int c = tid + i * QW;  // float4 c: elements 4c..4c+3 (K / 4 is a multiple of 64: whole waves)
             if (c >= K / 4) break;
             const float4 v = xv[pj][i];
             const float sum = (v.x + v.y) + (v.z + v.w);
@@ -1404,15 +1404,16 @@ __global__ __launch_bounds__(WG) void mt_q4i8_kernel(MtGemvArgs a) {
     }
 }
 
-static size_t mt_q4i8_lds(int32_t K) {
+constexpr int QI_NW = 8;  // waves per workgroup: the x planes in LDS serve 8 waves (4 measured 2% slower)
+static size_t mt_q4i8_lds(int32_t K, int nw) {
     return (size_t)(K / 64) * WAVE * 16 + (size_t)MT_MFMA_FEW * (K / 32) * 4 +
-           (size_t)(MT_MFMA_FEW + (WG / WAVE) * MT_MFMA_FEW) * 4 + (size_t)(WG / WAVE) * 16 * QI_SROW;
+           (size_t)(MT_MFMA_FEW + nw * MT_MFMA_FEW) * 4 + (size_t)nw * 16 * QI_SROW;
 }
 
 // rows: the rows of one row tile
 bool mt_q4i8_supported(const DMat &m, int32_t K, int32_t rows) {
-    return m.type == T_Q4_K && m.cols == K && K % 256 == 0 && K <= 4096 && rows > 0 &&
-           rows % (16 * (WG / WAVE)) == 0 && rows <= QI_MAXT * 16 * (WG / WAVE);
+    return m.type == T_Q4_K && m.cols == K && K % 256 == 0 && K <= 4096 && rows > 0 && rows % (16 * QI_NW) == 0 &&
+           rows <= QI_MAXT * 16 * QI_NW;
 }
 
 hipError_t launch_mt_q4i8(const MtGemvArgs &a, int max_items, hipStream_t st) {
@@ -1422,11 +1423,10 @@ hipError_t launch_mt_q4i8(const MtGemvArgs &a, int max_items, hipStream_t st) {
         return hipErrorInvalidValue;
     MtGemvArgs b = a;
     b.mat_items = a.swiglu ? max_items : 0;  // gate into y, up into y2 (the SwiGLU is the consumer's)
-    const size_t lds = mt_q4i8_lds(a.K);
-    const dim3 grid((unsigned)(a.swiglu ? 2 * max_items : max_items));
-    if (a.K <= 1024) hipLaunchKernelGGL(mt_q4i8_kernel<1>, grid, dim3(WG), lds, st, b);
-    else if (a.K <= 2048) hipLaunchKernelGGL(mt_q4i8_kernel<2>, grid, dim3(WG), lds, st, b);
-    else hipLaunchKernelGGL(mt_q4i8_kernel<4>, grid, dim3(WG), lds, st, b);
+    const size_t lds = mt_q4i8_lds(a.K, QI_NW);
+    const dim3 grid((unsigned)(a.swiglu ? 2 * max_items : max_items)), block(QI_NW * WAVE);
+    if (a.K <= 4 * QI_NW * WAVE) hipLaunchKernelGGL((mt_q4i8_kernel<1, QI_NW>), grid, block, lds, st, b);
+    else hipLaunchKernelGGL((mt_q4i8_kernel<2, QI_NW>), grid, block, lds, st, b);
     return hipGetLastError();
 }
 
