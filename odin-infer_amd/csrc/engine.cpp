@@ -1182,17 +1182,20 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
     // few pairs per expert (a short chunk: ~1.4 at 64 tokens of top 10 of 512):
     // items of MT_MFMA_FEW pairs with the x rows staged once
     const int px = e->pf_experts;
+    // int8 MFMA items stay ahead of the 16-pair f16 items at any chunk size
+    // (200 tokens of config 5, ~4.3 pairs per expert: 304 against 669 us per
+    // layer), so with it the few-pair items are used whatever the pair count
+    const int tiles_qi = D % 128 == 0 ? 2 : 1, tiles_qg = EF % 128 == 0 ? 2 : 1;
+    const bool i8_all = (px == 0 || px == 6) && mt_q4i8_supported(L.gexp, D, EF / tiles_qg) &&
+                        mt_q4i8_supported(L.uexp, D, EF / tiles_qg) && mt_q4i8_supported(L.dexp, EF, D / tiles_qi);
     const bool few = mm && (px == 0 || px == 4 || px == 5 || px == 6) && L.gexp.type == T_Q4_K &&
-                     L.dexp.type == T_Q4_K &&
-                     pairs <= MT_MFMA_FEW * NE && D <= 4096 && EF <= 4096 && D % MT_MFMA_ROWS == 0 &&
-                     EF % MT_MFMA_ROWS == 0;
+                     L.dexp.type == T_Q4_K && (pairs <= MT_MFMA_FEW * NE || i8_all) && D <= 4096 && EF <= 4096 &&
+                     D % MT_MFMA_ROWS == 0 && EF % MT_MFMA_ROWS == 0;
     const int ps = few ? MT_MFMA_FEW : mm ? MT_MFMA_PAIRS : MT_PAIR_SLICE;
     // few pairs, where the shapes allow: int8 planes of x on the matrix cores
     // with items of half the rows (64 tokens of config 5: gate/up 120 us, down
     // 58 us per layer, against 141 / 94 us on the token loop's int8 dot4
     // arithmetic); OI_PREFILL_EXPERTS=dot4: dot4, fewmfma: f16 MFMA
-    const int tiles_qi = D % 128 == 0 ? 2 : 1;
-    const int tiles_qg = EF % 128 == 0 ? 2 : 1;
     const bool i8_gu = few && mt_q4i8_supported(L.gexp, D, EF / tiles_qg) && mt_q4i8_supported(L.uexp, D, EF / tiles_qg);
     const bool d4_gu = few && mt_dot4_supported(L.gexp, D, EF) && mt_dot4_supported(L.uexp, D, EF);
     const bool gu_i8 = i8_gu && (px == 0 || px == 6);
