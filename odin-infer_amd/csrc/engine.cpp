@@ -1107,7 +1107,8 @@ int prefill_alloc(oi_engine *e) {
                                  moe ? T * KP * 4 : 0, moe ? T * KP * EF * 4 : 0, moe ? T * KP * EF * 4 : 0,
                                  moe ? T * KP * D * 4 : 0,
                                  moe ? T * KP * 4 : 0, moe ? T * KP * 4 : 0, moe ? NE * 4 : 0, moe ? NE * 4 : 0,
-                                 moe ? NE * 4 : 0, 8 * tg, 8 * td, moe ? (size_t)8 : 0};
+                                 moe ? NE * 4 : 0, 8 * tg, 8 * td, moe ? (size_t)8 : 0,
+                                 moe ? (T + 2 * ((T + MT_MFMA_FEW - 1) / MT_MFMA_FEW) * 16 + 4) * 4 : 0};
     size_t total = 0;
     for (size_t b : sizes) total += al256(b);
     HIP_TRY(hipMalloc(&e->pf_mem, total));
@@ -1145,6 +1146,8 @@ int prefill_alloc(oi_engine *e) {
     e->pf_items_gu = (int32_t *)take();
     e->pf_items_dn = (int32_t *)take();
     e->pf_nitems = (int32_t *)take();
+    e->pf_rt = (int32_t *)take();
+    e->pf_rt_T = 0;
     return OI_OK;
 }
 
@@ -1167,13 +1170,33 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
     r.K = D;
     r.rows = E;
     r.xdiv = 1;
-    r.tile_rows = std::max(1, mt_gemv_tile_rows(D, E) / 8);  // one pass of the lane groups: more workgroups
-    r.tiles = (E + r.tile_rows - 1) / r.tile_rows;
-    r.dense_n = T;
-    r.pair_slice = rps;
     r.x = e->pf_xn;
     r.y = e->pf_lg;
-    HIP_TRY(launch_mt_gemv(r, r.tiles * slices, st));
+    // on int8 MFMA (the experts' kernel, x to 2^-25 of its row maximum) in
+    // items of 4 tokens and 128-row tiles where the router allows (200 tokens
+    // of config 5: 62 -> 14 us per layer; the 2048-token prompt 489 -> 477 ms
+    // at 64-token chunks, 198 -> 177 ms at 512), else the multi-token GEMV
+    const int tiles_r = std::max(1, std::min(16, E / 128));
+    const int px0 = e->pf_experts;
+    if ((px0 == 0 || px0 == 6) && E % tiles_r == 0 && T <= 16 * MT_MFMA_FEW * 0x7FF &&
+        mt_q4i8_supported(L.router, D, E / tiles_r)) {
+        const int nsr = (T + MT_MFMA_FEW - 1) / MT_MFMA_FEW;
+        int32_t *rl = e->pf_rt, *ri = rl + T, *rh = ri + 2 * nsr * 16;
+        if (e->pf_rt_T != T) {  // the items depend on T only (tiles_r <= 16 fits the buffer)
+            HIP_TRY(launch_pf_router_items(T, tiles_r, rl, ri, rh, st));
+            e->pf_rt_T = T;
+        }
+        r.tiles = tiles_r;
+        r.pair_slice = MT_MFMA_FEW;
+        r.list = rl; r.items = ri; r.off = rh; r.cnt = rh + 1; r.nitems = rh + 2;
+        HIP_TRY(launch_mt_q4i8(r, nsr * tiles_r, st));
+    } else {
+        r.tile_rows = std::max(1, mt_gemv_tile_rows(D, E) / 8);  // one pass of the lane groups: more workgroups
+        r.tiles = (E + r.tile_rows - 1) / r.tile_rows;
+        r.dense_n = T;
+        r.pair_slice = rps;
+        HIP_TRY(launch_mt_gemv(r, r.tiles * slices, st));
+    }
     // the chosen experts on the matrix cores where their type allows (f32 MFMA),
     // else the multi-token GEMV
     const bool mm = e->pf_experts != 1 && mt_mfma_supported(L.gexp, D, EF) && mt_mfma_supported(L.uexp, D, EF) &&

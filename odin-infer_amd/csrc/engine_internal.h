@@ -108,6 +108,9 @@ struct oi_engine {
     float *pf_h2 = nullptr;  // up rows of the routed experts (few-pair items)
     int32_t *pf_ids = nullptr, *pf_list = nullptr, *pf_off = nullptr, *pf_cnt = nullptr, *pf_fill = nullptr;
     int32_t *pf_items_gu = nullptr, *pf_items_dn = nullptr, *pf_nitems = nullptr;
+    // the router's work items for mt_q4i8_kernel: list, items, then off / cnt / count (filled for pf_rt_T tokens)
+    int32_t *pf_rt = nullptr;
+    int pf_rt_T = 0;
     bool pf_fused = true;  // gate/up GEMM with the SwiGLU epilogue where it applies (OI_PREFILL_UNFUSED=1: off)
     int pf_experts = 0;  // routed experts of a prefill: 0 the default kernels, 1 the multi-token GEMV, 2 f32 MFMA
                          // only, 3 no few-pair items, 4 few-pair items on MFMA (OI_PREFILL_EXPERTS=gemv / f32 /

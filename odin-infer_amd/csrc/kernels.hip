@@ -1509,6 +1509,31 @@ hipError_t launch_pf_moe_route(const PfMoeArgs &a, hipStream_t st) {
     return hipGetLastError();
 }
 
+// The router as one "expert" whose pairs are the chunk's tokens in order
+// (list[t] = t), in slices of MT_MFMA_FEW tokens and `tiles` row tiles: the
+// work items of mt_q4i8_kernel (off, cnt and the item count in the same
+// buffer's tail).  One workgroup.
+__global__ __launch_bounds__(WG) void pf_router_items_kernel(int T, int tiles, int32_t *list, int32_t *items,
+                                                              int32_t *hdr) {
+    const int ns = (T + MT_MFMA_FEW - 1) / MT_MFMA_FEW;
+    for (int t = threadIdx.x; t < T; t += WG) list[t] = t;
+    for (int i = threadIdx.x; i < ns * tiles; i += WG) {
+        items[2 * i] = 0;
+        items[2 * i + 1] = ((i / tiles) << 16) | (i % tiles);
+    }
+    if (threadIdx.x == 0) {
+        hdr[0] = 0;           // off
+        hdr[1] = T;           // cnt
+        hdr[2] = ns * tiles;  // items
+    }
+}
+
+hipError_t launch_pf_router_items(int T, int tiles, int32_t *list, int32_t *items, int32_t *hdr, hipStream_t st) {
+    if (T <= 0 || tiles <= 0 || tiles > 0xFFFF) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(pf_router_items_kernel, dim3(1), dim3(WG), 0, st, T, tiles, list, items, hdr);
+    return hipGetLastError();
+}
+
 hipError_t launch_pf_moe_combine(const PfMoeArgs &a, hipStream_t st) {
     hipLaunchKernelGGL(pf_moe_combine_kernel, dim3((unsigned)((a.dim + WG - 1) / WG), (unsigned)a.T), dim3(WG), 0, st,
                        a);

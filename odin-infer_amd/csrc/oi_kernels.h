@@ -318,6 +318,7 @@ struct PfMoeArgs {
 };
 hipError_t launch_pf_moe_route(const PfMoeArgs &a, hipStream_t st);
 hipError_t launch_pf_moe_combine(const PfMoeArgs &a, hipStream_t st);
+hipError_t launch_pf_router_items(int T, int tiles, int32_t *list, int32_t *items, int32_t *hdr, hipStream_t st);
 // deltanet.hip: the gated DeltaNet token step (between the input and output
 // projections of a Qwen3.5 linear-attention layer)
 struct DnArgs {
