@@ -200,25 +200,28 @@ __global__ __launch_bounds__(WG) void pf_dn_prep_kernel(PfDnArgs a) {
 
 // The delta rule (forward.odin:193-209) over the chunk's tokens in order:
 //   S *= decay;  delta = (v - S^T k) beta;  S += k delta^T;  o = S^T q.
-// Grid (n_vh, hv / 32): a workgroup owns 32 state columns of value head vh
-// (k head vh % n_kh); each wave 8 columns, lane = 8 column + row group, a
-// row group 16 rows, so a lane holds 16 state values for the whole chunk (read
-// once, written once).  The column sums over the 8 row groups are DPP sums
-// inside the lane's group of 8.  Per 32 tokens the workgroup stages the k
+// Grid (n_vh, hv / 16): a workgroup owns 16 state columns of value head vh
+// (k head vh % n_kh); each wave 4 columns, lane = 16 column + row group, a
+// row group 8 rows, so a lane holds 8 state values for the whole chunk (read
+// once, written once).  The column sums over the 16 row groups are DPP sums
+// inside the lane's row of 16.  (With 32 columns and 16 rows per lane half
+// the SIMDs had no wave and the token recurrence, the kernel's critical path,
+// was twice as long per lane.)  Per 32 tokens the workgroup stages the k
 // head's q and k, its v columns and the gates in LDS.
-constexpr int DN_DB = 32;
+constexpr int DN_DB = 32, DN_RG = 16, DN_CW = WG / DN_RG;
 template <int HK, int HV>
 __global__ __launch_bounds__(WG) void pf_dn_delta_kernel(PfDnArgs a) {
 #pragma clang fp contract(off)
-    constexpr int RG = 8, RPL = HK / RG, QP = HK + HK / 4;  // rows per lane; row group g at 20 g (16 + 4 pad)
-    static_assert(RPL == 16 && HV % 32 == 0, "head shape");
+    constexpr int RG = DN_RG, RPL = HK / RG, QP = RG * (RPL + 4);  // rows per lane; row group g at (RPL + 4) g
+    constexpr int CW = DN_CW;                                       // columns per workgroup (4 per wave)
+    static_assert(RPL == 8 && HV % CW == 0 && CW * RG == WG, "head shape");
     __shared__ __attribute__((aligned(16))) float sq[DN_DB][QP];
     __shared__ __attribute__((aligned(16))) float sk[DN_DB][QP];
-    __shared__ __attribute__((aligned(16))) float sv[DN_DB][32];
+    __shared__ __attribute__((aligned(16))) float sv[DN_DB][CW];
     __shared__ float sg[DN_DB][2];
-    const int vh = blockIdx.x, kh = vh % a.n_kh, c0 = (int)blockIdx.y * 32;
+    const int vh = blockIdx.x, kh = vh % a.n_kh, c0 = (int)blockIdx.y * CW;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
-    const int cl = wave * 8 + (lane >> 3), rg = lane & 7, j = c0 + cl, i0 = rg * RPL;
+    const int cl = wave * (WAVE / RG) + lane / RG, rg = lane % RG, j = c0 + cl, i0 = rg * RPL;
     const int KD = a.n_kh * HK, CD = 2 * KD + a.n_vh * HV, VD = a.n_vh * HV;
     float *S = a.state + (size_t)vh * HK * HV;
     float s[RPL];
@@ -228,9 +231,9 @@ __global__ __launch_bounds__(WG) void pf_dn_delta_kernel(PfDnArgs a) {
         const int nb = min(DN_DB, a.T - tb);
         // the block's q, k (float4 pieces), v and gates: every load issued
         // before any is used (a loop of load-then-store would wait for each)
-        constexpr int QK4 = DN_DB * 2 * HK / 4 / WG, V4 = DN_DB * 32 / 4 / WG;
-        static_assert(QK4 * WG * 4 == DN_DB * 2 * HK && V4 >= 1, "staging shape");
-        float4 qk4[QK4], v4[V4];
+        constexpr int QK4 = DN_DB * 2 * HK / 4 / WG, NV4 = DN_DB * CW / 4;  // NV4 <= WG: one float4 of v per thread
+        static_assert(QK4 * WG * 4 == DN_DB * 2 * HK && NV4 <= WG, "staging shape");
+        float4 qk4[QK4], v4;
         float gv = 0.f;
 #pragma unroll
         for (int i = 0; i < QK4; i++) {
@@ -239,11 +242,11 @@ __global__ __launch_bounds__(WG) void pf_dn_delta_kernel(PfDnArgs a) {
             qk4[i] = tt < nb ? *(const float4 *)(a.qk + (size_t)(tb + tt) * 2 * KD + side * KD + kh * HK + ee)
                              : float4{0.f, 0.f, 0.f, 0.f};
         }
-#pragma unroll
-        for (int i = 0; i < V4; i++) {
-            const int idx = threadIdx.x + i * WG, tt = idx / 8, c4 = idx % 8;
-            v4[i] = tt < nb ? *(const float4 *)(a.conv_out + (size_t)(tb + tt) * CD + 2 * KD + vh * HV + c0 + 4 * c4)
-                            : float4{0.f, 0.f, 0.f, 0.f};
+        {
+            const int tt = threadIdx.x / (CW / 4), c4 = threadIdx.x % (CW / 4);
+            v4 = threadIdx.x < NV4 && tt < nb
+                     ? *(const float4 *)(a.conv_out + (size_t)(tb + tt) * CD + 2 * KD + vh * HV + c0 + 4 * c4)
+                     : float4{0.f, 0.f, 0.f, 0.f};
         }
         if (threadIdx.x < 2 * nb)
             gv = a.gates[(size_t)(tb + threadIdx.x / 2) * 3 * a.n_vh + (threadIdx.x % 2) * a.n_vh + vh];
@@ -254,11 +257,7 @@ __global__ __launch_bounds__(WG) void pf_dn_delta_kernel(PfDnArgs a) {
             const int side = e4 / (HK / 4), ee = 4 * (e4 % (HK / 4));
             *(float4 *)&(side ? sk : sq)[tt][ee + (ee / RPL) * 4] = qk4[i];  // 4 | ee, RPL: one row group
         }
-#pragma unroll
-        for (int i = 0; i < V4; i++) {
-            const int idx = threadIdx.x + i * WG, tt = idx / 8, c4 = idx % 8;
-            *(float4 *)&sv[tt][4 * c4] = v4[i];
-        }
+        if (threadIdx.x < NV4) *(float4 *)&sv[threadIdx.x / (CW / 4)][4 * (threadIdx.x % (CW / 4))] = v4;
         if (threadIdx.x < 2 * nb) sg[threadIdx.x / 2][threadIdx.x % 2] = gv;
         __syncthreads();
         for (int tt = 0; tt < nb; tt++) {
@@ -280,9 +279,10 @@ __global__ __launch_bounds__(WG) void pf_dn_delta_kernel(PfDnArgs a) {
                 kp[r & 3] += s[r] * kn[r];
             }
             float kv = (kp[0] + kp[1]) + (kp[2] + kp[3]);
-            kv += OI_DPP(kv, 0xB1);  // sum over the lane's group of 8 (the row groups)
+            kv += OI_DPP(kv, 0xB1);  // sum over the lane's row of 16 (the row groups)
             kv += OI_DPP(kv, 0x4E);
             kv += dpp_mirror8(kv);
+            kv += OI_DPP(kv, 0x140);
             const float delta = (sv[tt][cl] - kv) * beta;
             float op[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -294,6 +294,7 @@ __global__ __launch_bounds__(WG) void pf_dn_delta_kernel(PfDnArgs a) {
             o += OI_DPP(o, 0xB1);
             o += OI_DPP(o, 0x4E);
             o += dpp_mirror8(o);
+            o += OI_DPP(o, 0x140);
             if (rg == 0) a.o[(size_t)(tb + tt) * VD + vh * HV + j] = o;
         }
     }
@@ -483,7 +484,7 @@ hipError_t launch_pf_deltanet(const PfDnArgs &a, hipStream_t st) {
     const dim3 dgrid((unsigned)a.n_vh, 128 / 32);
     if (a.chunk == 16) hipLaunchKernelGGL((pf_dn_chunk_kernel<128, 128, 16>), dgrid, dim3(WG), 0, st, a);
     else if (a.chunk == 32) hipLaunchKernelGGL((pf_dn_chunk_kernel<128, 128, 32>), dgrid, dim3(WG), 0, st, a);
-    else hipLaunchKernelGGL((pf_dn_delta_kernel<128, 128>), dgrid, dim3(WG), 0, st, a);
+    else hipLaunchKernelGGL((pf_dn_delta_kernel<128, 128>), dim3((unsigned)a.n_vh, 128 / DN_CW), dim3(WG), 0, st, a);
     hipLaunchKernelGGL(pf_dn_gnorm_kernel<128>, dim3((unsigned)a.T, nblk(a.n_vh, (WG / WAVE) * GN_NH)), dim3(WG), 0, st,
                        a);
     return hipGetLastError();
