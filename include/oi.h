@@ -101,8 +101,45 @@ const float *oi_engine_forward(oi_engine *e, int32_t token, int32_t pos);
  * error: n <= 0, positions past seq_len, or a token out of range. */
 const float *oi_engine_prefill(oi_engine *e, const int32_t *tokens, int32_t n, int32_t pos0);
 
+/* engine_verify_batch (qwen3_5/engine.odin:166-174: forward_gpu_batch, then
+ * metal_verify_batch_logits, qwen3_5/metal.odin:1707-1747): consume
+ * tokens[0..n) at positions pos0 .. pos0+n-1 exactly as oi_engine_prefill
+ * does (same chunking, same state afterwards) and return the logits of every
+ * position: n rows of vocab_size floats, row i predicting position pos0+i+1
+ * (engine-owned pinned host memory, valid until the next call of this
+ * procedure).  Each row is the final RMSNorm and classifier of that token's
+ * hidden state in f32 (the decode path's GEMV, as the reference's per-row
+ * enc_gemv).  NULL on the errors of oi_engine_prefill, or OI_E_NOMEM when the
+ * n x vocab buffer cannot be allocated. */
+const float *oi_engine_verify_batch(oi_engine *e, const int32_t *tokens, int32_t n, int32_t pos0);
+
+/* engine_batch_max (qwen3_5/engine.odin:96-102): the most tokens one batched
+ * chunk of oi_engine_prefill / oi_engine_verify_batch takes (qwen3_5/metal.odin:22
+ * MAX_BATCH_T). */
+int32_t oi_engine_batch_max(void);
+
 /* engine_config (infer/engine.odin:54-56). */
 int oi_engine_config(const oi_engine *e, oi_config *out);
+
+/* Config of the qwen3_5 package (qwen3_5/model.odin:20-45), its fields in that
+ * order without the layer_types slice (oi_engine_layer_types gives it).  For
+ * a hybrid ("qwen35") file: the partial RoPE width and fraction, the DeltaNet
+ * dimensions and the full-attention interval of the file; for the other
+ * layouts every layer is full attention over the whole head (rotary_dim =
+ * head_dim, partial_rotary = 1, lin_* = 0, full_attn_interval = 1).  n_full and
+ * n_linear count the layers of each kind. */
+typedef struct oi_qwen35_config {
+    int64_t dim, hidden_dim, n_layers, n_heads, n_kv_heads, head_dim, vocab_size, seq_len, max_seq;
+    float rms_eps, rope_theta, partial_rotary;
+    int64_t rotary_dim, lin_n_k_heads, lin_n_v_heads, lin_head_k_dim, lin_head_v_dim, lin_conv_kernel;
+    int64_t full_attn_interval, n_full, n_linear;
+} oi_qwen35_config;
+int oi_engine_config_qwen35(const oi_engine *e, oi_qwen35_config *out);
+
+/* Config.layer_types (qwen3_5/model.odin:288-300): out[l] = 0 for a
+ * full-attention layer, 1 for a gated-DeltaNet layer (the order of the
+ * reference's Layer_Type enum); n must equal n_layers (OI_E_ARG otherwise). */
+int oi_engine_layer_types(const oi_engine *e, int32_t *out, int32_t n);
 
 /* Message of the last failure on this thread. */
 const char *oi_last_error(void);

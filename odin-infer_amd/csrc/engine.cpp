@@ -361,6 +361,8 @@ void oi_engine_destroy(oi_engine *e) {
     if (e->pf_mem) hipFree(e->pf_mem);
     if (e->logits_host) hipHostFree(e->logits_host);
     if (e->state_host) hipHostFree(e->state_host);
+    if (e->vf_dev) hipFree(e->vf_dev);
+    if (e->vf_host) hipHostFree(e->vf_host);
     if (e->stream) hipStreamDestroy(e->stream);
     delete e;
 }
@@ -991,6 +993,51 @@ int oi_engine_config(const oi_engine *e, oi_config *out) {
     return OI_OK;
 }
 
+static_assert(sizeof(oi_qwen35_config) == 160, "oi_qwen35_config layout (the Odin binding mirrors it)");
+
+int oi_engine_config_qwen35(const oi_engine *e, oi_qwen35_config *out) {
+    if (!e || !out) return fail(OI_E_ARG, "null argument");
+    const oi_config &c = e->cfg;
+    oi_qwen35_config q{};
+    q.dim = c.dim;
+    q.hidden_dim = c.hidden_dim;
+    q.n_layers = c.n_layers;
+    q.n_heads = c.n_heads;
+    q.n_kv_heads = c.n_kv_heads;
+    q.head_dim = c.head_dim;
+    q.vocab_size = c.vocab_size;
+    q.seq_len = c.seq_len;
+    q.max_seq = c.max_seq;
+    q.rms_eps = c.rms_eps;
+    q.rope_theta = c.rope_freq;
+    // a hybrid file's partial RoPE (qwen3_5/model.odin:277-286); every other
+    // layout rotates the whole head and has no DeltaNet layers
+    const bool hybrid = e->arch == 2;
+    q.rotary_dim = hybrid ? e->rotary_dim : c.head_dim;
+    q.partial_rotary = (float)q.rotary_dim / (float)std::max<int64_t>(c.head_dim, 1);
+    q.lin_n_k_heads = hybrid ? e->lin_nk : 0;
+    q.lin_n_v_heads = hybrid ? e->lin_nv : 0;
+    q.lin_head_k_dim = hybrid ? e->lin_hk : 0;
+    q.lin_head_v_dim = hybrid ? e->lin_hv : 0;
+    q.lin_conv_kernel = hybrid ? e->lin_kernel : 0;
+    q.full_attn_interval = hybrid ? e->full_interval : 1;
+    for (const LayerDev &L : e->layers) {
+        if (L.kind == LK_LINEAR) q.n_linear++;
+        else q.n_full++;
+    }
+    *out = q;
+    return OI_OK;
+}
+
+int oi_engine_layer_types(const oi_engine *e, int32_t *out, int32_t n) {
+    if (!e || (!out && n > 0)) return fail(OI_E_ARG, "null argument");
+    if (n != (int32_t)e->layers.size())
+        return fail(OI_E_ARG, "layer_types: " + std::to_string(n) + " entries for " +
+                                  std::to_string(e->layers.size()) + " layers");
+    for (int32_t l = 0; l < n; l++) out[l] = e->layers[(size_t)l].kind == LK_LINEAR ? 1 : 0;
+    return OI_OK;
+}
+
 const float *oi_engine_forward(oi_engine *e, int32_t token, int32_t pos) {
     if (!e) {
         fail(OI_E_ARG, "null engine");
@@ -1286,7 +1333,10 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
 // rule over the chunk's tokens in order, gated RMSNorm), then the FFN (dense
 // SwiGLU, or routed experts), all over the T tokens; at the end the final
 // norm and classifier of the last token.
-int prefill_chunk(oi_engine *e, const int32_t *tokens, int T, int pos) {
+// rows != nullptr: the classifier of every token of the chunk, token t's
+// logits to rows + t * vocab (engine_verify_batch); otherwise the last token's
+// logits to e->logits.
+int prefill_chunk(oi_engine *e, const int32_t *tokens, int T, int pos, float *rows = nullptr) {
     const hipStream_t st = e->stream;
     const oi_config &c = e->cfg;
     const int D = (int)c.dim, H = (int)c.hidden_dim, hd = (int)c.head_dim;
@@ -1366,64 +1416,110 @@ int prefill_chunk(oi_engine *e, const int32_t *tokens, int T, int pos) {
         else
             HIP_TRY(launch_pf_add(e->pf_x, P[0], s0, (int64_t)T * D, st));
     }
-    GemvArgs a = gemv_args(GEMV_STORE, D, e->pf_x + (size_t)(T - 1) * D, e->output_norm, eps);
-    a.nseg = 1;
-    a.seg[0].m = e->output;
-    a.seg[0].y = e->logits;
-    if (!plan_gemv(a)) return fail(OI_E_DEVICE, "internal: classifier plan");
-    HIP_TRY(launch_gemv(a, st));
+    // the final norm and classifier (metal.odin:1637-1641 for the last token;
+    // metal_verify_batch_logits, metal.odin:1707-1747, for every token): the
+    // decode path's f32 GEMV with the RMSNorm prologue, one row at a time
+    for (int t = rows ? 0 : T - 1; t < T; t++) {
+        GemvArgs a = gemv_args(GEMV_STORE, D, e->pf_x + (size_t)t * D, e->output_norm, eps);
+        a.nseg = 1;
+        a.seg[0].m = e->output;
+        a.seg[0].y = rows ? rows + (size_t)t * c.vocab_size : e->logits;
+        if (!plan_gemv(a)) return fail(OI_E_DEVICE, "internal: classifier plan");
+        HIP_TRY(launch_gemv(a, st));
+    }
     return OI_OK;
 }
 
 }  // namespace
 
-const float *oi_engine_prefill(oi_engine *e, const int32_t *tokens, int32_t n, int32_t pos0) {
-    if (!e || !tokens) {
-        fail(OI_E_ARG, "null argument");
-        return nullptr;
-    }
-    if (n <= 0) {
-        fail(OI_E_ARG, "prefill: no tokens");
-        return nullptr;
-    }
-    if (pos0 < 0 || (int64_t)pos0 + n > e->cfg.seq_len) {
-        fail(OI_E_RANGE, "prefill: positions [" + std::to_string(pos0) + ", " + std::to_string((int64_t)pos0 + n) +
-                             ") out of range (seq_len=" + std::to_string(e->cfg.seq_len) + ")");
-        return nullptr;
-    }
+namespace {
+
+// engine_forward_batch over tokens[0, n) at pos0 (chunks of a multiple of 8
+// up to PF_MAX_T batched, the trailing 1-7 through the decode path).  rows ==
+// nullptr: the last token's logits in e->logits; otherwise every token's
+// logits, token i at rows + i * vocab (device memory).  Returns 0 or a code.
+int prefill_run(oi_engine *e, const int32_t *tokens, int32_t n, int32_t pos0, float *rows) {
+    const char *what = rows ? "verify_batch" : "prefill";
+    if (n <= 0) return fail(OI_E_ARG, std::string(what) + ": no tokens");
+    if (pos0 < 0 || (int64_t)pos0 + n > e->cfg.seq_len)
+        return fail(OI_E_RANGE, std::string(what) + ": positions [" + std::to_string(pos0) + ", " +
+                                    std::to_string((int64_t)pos0 + n) + ") out of range (seq_len=" +
+                                    std::to_string(e->cfg.seq_len) + ")");
     for (int32_t i = 0; i < n; i++)
-        if (tokens[i] < 0 || tokens[i] >= e->cfg.vocab_size) {
-            fail(OI_E_RANGE, "prefill: token=" + std::to_string(tokens[i]) + " out of range (vocab=" +
-                                 std::to_string(e->cfg.vocab_size) + ")");
-            return nullptr;
-        }
-    if (hipSetDevice(e->device) != hipSuccess) {
-        fail(OI_E_DEVICE, "hipSetDevice failed");
-        return nullptr;
-    }
+        if (tokens[i] < 0 || tokens[i] >= e->cfg.vocab_size)
+            return fail(OI_E_RANGE, std::string(what) + ": token=" + std::to_string(tokens[i]) +
+                                        " out of range (vocab=" + std::to_string(e->cfg.vocab_size) + ")");
+    if (hipSetDevice(e->device) != hipSuccess) return fail(OI_E_DEVICE, "hipSetDevice failed");
     const bool batched = prefill_batched_ok(e);
-    if (batched && prefill_alloc(e)) return nullptr;
-    if (ensure_graph(e)) return nullptr;
+    if (batched && prefill_alloc(e)) return -1;
+    if (ensure_graph(e)) return -1;
+    const size_t V = (size_t)e->cfg.vocab_size;
     int i = 0;
     while (i < n) {
         const int rem = n - i;
         if (batched && rem >= 8) {
             int chunk = std::min(PF_MAX_T, rem);
             chunk -= chunk % 8;
-            if (prefill_chunk(e, tokens + i, chunk, pos0 + i)) return nullptr;
+            if (prefill_chunk(e, tokens + i, chunk, pos0 + i, rows ? rows + (size_t)i * V : nullptr)) return -1;
             i += chunk;
         } else {  // one token through the decode path
-            if (set_state(e, tokens[i], pos0 + i, 0) || run_token(e)) return nullptr;
+            if (set_state(e, tokens[i], pos0 + i, 0) || run_token(e)) return -1;
+            hipError_t r = hipSuccess;
+            if (rows) r = hipMemcpyAsync(rows + (size_t)i * V, e->logits, V * 4, hipMemcpyDeviceToDevice, e->stream);
             // the state copy reads pinned host memory when the stream reaches
             // it: the next token's state must not be written before that
-            const hipError_t r = hipStreamSynchronize(e->stream);
-            if (r != hipSuccess) {
-                fail(OI_E_DEVICE, std::string("prefill: ") + hipGetErrorString(r));
-                return nullptr;
-            }
+            if (r == hipSuccess) r = hipStreamSynchronize(e->stream);
+            if (r != hipSuccess) return fail(OI_E_DEVICE, std::string(what) + ": " + hipGetErrorString(r));
             i += 1;
         }
     }
+    return OI_OK;
+}
+
+}  // namespace
+
+int32_t oi_engine_batch_max(void) { return PF_MAX_T; }
+
+const float *oi_engine_verify_batch(oi_engine *e, const int32_t *tokens, int32_t n, int32_t pos0) {
+    if (!e || !tokens) {
+        fail(OI_E_ARG, "null argument");
+        return nullptr;
+    }
+    if (n > 0 && n > e->vf_rows) {
+        if (hipSetDevice(e->device) != hipSuccess) {
+            fail(OI_E_DEVICE, "hipSetDevice failed");
+            return nullptr;
+        }
+        if (e->vf_dev) hipFree(e->vf_dev);
+        if (e->vf_host) hipHostFree(e->vf_host);
+        e->vf_dev = e->vf_host = nullptr;
+        e->vf_rows = 0;
+        const size_t bytes = (size_t)n * (size_t)e->cfg.vocab_size * 4;
+        if (hipMalloc((void **)&e->vf_dev, bytes) != hipSuccess ||
+            hipHostMalloc((void **)&e->vf_host, bytes, hipHostMallocDefault) != hipSuccess) {
+            fail(OI_E_NOMEM, "verify_batch: cannot allocate the logits of " + std::to_string(n) + " positions");
+            return nullptr;
+        }
+        e->vf_rows = n;
+    }
+    if (prefill_run(e, tokens, n, pos0, e->vf_dev)) return nullptr;
+    const size_t bytes = (size_t)n * (size_t)e->cfg.vocab_size * 4;
+    hipError_t r = hipMemcpyAsync(e->vf_host, e->vf_dev, bytes, hipMemcpyDeviceToHost, e->stream);
+    if (r == hipSuccess) r = hipStreamSynchronize(e->stream);
+    if (r != hipSuccess) {
+        fail(OI_E_DEVICE, std::string("verify_batch: ") + hipGetErrorString(r));
+        return nullptr;
+    }
+    e->last_pos = pos0 + n - 1;
+    return e->vf_host;
+}
+
+const float *oi_engine_prefill(oi_engine *e, const int32_t *tokens, int32_t n, int32_t pos0) {
+    if (!e || !tokens) {
+        fail(OI_E_ARG, "null argument");
+        return nullptr;
+    }
+    if (prefill_run(e, tokens, n, pos0, nullptr)) return nullptr;
     hipError_t r = hipMemcpyAsync(e->logits_host, e->logits, (size_t)e->cfg.vocab_size * 4, hipMemcpyDeviceToHost,
                                   e->stream);
     if (r == hipSuccess) r = hipStreamSynchronize(e->stream);

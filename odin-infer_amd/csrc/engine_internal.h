@@ -117,5 +117,9 @@ struct oi_engine {
                          // wide / fewmfma)
     bool dn_fused = false;  // token loop: the one-launch DeltaNet step instead of the split one (OI_DN_FUSED)
     int pf_dn_chunk = 0;  // delta rule of a prefill chunk: 0 token by token, 16 / 32 chunked (OI_PREFILL_DN_CHUNK)
+    // engine_verify_batch: the logits of every position, [rows][vocab] on the
+    // device and in pinned host memory (allocated on first use, grown as needed)
+    float *vf_dev = nullptr, *vf_host = nullptr;
+    int64_t vf_rows = 0;
 };
 

@@ -42,6 +42,16 @@ class Config(ctypes.Structure):
                 ("head_dim", c_i64), ("rope_freq", c_f), ("rms_eps", c_f)]
 
 
+class Qwen35Config(ctypes.Structure):
+    """oi_qwen35_config: qwen3_5/model.odin:20-45 without layer_types."""
+    _fields_ = [("dim", c_i64), ("hidden_dim", c_i64), ("n_layers", c_i64), ("n_heads", c_i64),
+                ("n_kv_heads", c_i64), ("head_dim", c_i64), ("vocab_size", c_i64), ("seq_len", c_i64),
+                ("max_seq", c_i64), ("rms_eps", c_f), ("rope_theta", c_f), ("partial_rotary", c_f),
+                ("rotary_dim", c_i64), ("lin_n_k_heads", c_i64), ("lin_n_v_heads", c_i64),
+                ("lin_head_k_dim", c_i64), ("lin_head_v_dim", c_i64), ("lin_conv_kernel", c_i64),
+                ("full_attn_interval", c_i64), ("n_full", c_i64), ("n_linear", c_i64)]
+
+
 class Sampler(ctypes.Structure):
     """oi_sampler (include/oi.h): sampler/sampler.odin:16-29 without the grammar."""
     _fields_ = [("temperature", c_f), ("topp", c_f), ("repeat_penalty", c_f), ("record", c_i32),
@@ -55,6 +65,10 @@ HIP_SYMBOLS = {
     "oi_engine_forward": (ctypes.POINTER(c_f), [c_vp, c_i32, c_i32]),
     "oi_engine_prefill": (ctypes.POINTER(c_f), [c_vp, c_vp, c_i32, c_i32]),
     "oi_engine_config": (c_i32, [c_vp, ctypes.POINTER(Config)]),
+    "oi_engine_verify_batch": (ctypes.POINTER(c_f), [c_vp, c_vp, c_i32, c_i32]),
+    "oi_engine_config_qwen35": (c_i32, [c_vp, ctypes.POINTER(Qwen35Config)]),
+    "oi_engine_layer_types": (c_i32, [c_vp, c_vp, c_i32]),
+    "oi_engine_batch_max": (c_i32, []),
     "oi_last_error": (ctypes.c_char_p, []),
     "oi_engine_decode_greedy": (c_i32, [c_vp, c_i32, c_i32, c_i32, c_vp]),
     "oi_engine_kv_fill": (c_i32, [c_vp, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp]),

@@ -106,6 +106,19 @@ def engine_forward_batch(e, tokens, pos_start):
     return np.ctypeslib.as_array(p, shape=(e.config.vocab_size,))
 
 
+def engine_verify_batch(e, tokens, pos_start):
+    """qwen3_5/engine.odin:166-174: consume `tokens` from `pos_start` as
+    engine_forward_batch does and return every position's logits, [n][vocab]
+    (a view of engine memory, valid until the next call)."""
+    t = np.ascontiguousarray(tokens, np.int32)
+    p = _native.hip().oi_engine_verify_batch(e.handle, t.ctypes.data, int(t.size), int(pos_start))
+    if not p:
+        L = _native.hip()
+        msg = L.oi_last_error().decode()
+        raise OIError(OI_E_RANGE if "out of range" in msg else -1 if "no tokens" in msg else -7, msg)
+    return np.ctypeslib.as_array(p, shape=(int(t.size), e.config.vocab_size))
+
+
 def engine_config(e):
     """infer/engine.odin:54-56."""
     return e.config

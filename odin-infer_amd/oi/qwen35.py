@@ -9,6 +9,32 @@ from . import _native
 from ._native import check
 
 
+LAYER_FULL_ATTENTION, LAYER_LINEAR_ATTENTION = 0, 1  # qwen3_5/model.odin:18 Layer_Type
+
+
+def engine_config(e):
+    """The qwen3_5 package's engine_config (qwen3_5/engine.odin:104-106 ->
+    Config, qwen3_5/model.odin:20-45): a dict of its fields in order,
+    layer_types included (0 full attention, 1 gated DeltaNet)."""
+    L = _native.hip()
+    c = _native.Qwen35Config()
+    check(L.oi_engine_config_qwen35(e.handle, ctypes.byref(c)))
+    out = {name: getattr(c, name) for name, _ in c._fields_}
+    types = np.empty(int(c.n_layers), np.int32)
+    check(L.oi_engine_layer_types(e.handle, types.ctypes.data, int(c.n_layers)))
+    keys = list(out)
+    at = keys.index("full_attn_interval") + 1
+    ordered = {k: out[k] for k in keys[:at]}
+    ordered["layer_types"] = [int(t) for t in types]
+    ordered.update({k: out[k] for k in keys[at:]})
+    return ordered
+
+
+def engine_batch_max():
+    """qwen3_5/engine.odin:96-102: tokens per batched chunk (metal.odin:22)."""
+    return int(_native.hip().oi_engine_batch_max())
+
+
 def _f32(x):
     return np.ascontiguousarray(x, np.float32)
 

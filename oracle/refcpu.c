@@ -774,6 +774,14 @@ typedef struct {
     const uint8_t **stg_key;
     float **stg_w;
     int n_stg;
+    /* engine_verify_batch: logits of every position [vf_rows][vocab] */
+    float *vf;
+    int64_t vf_rows;
+    /* test hook: the routing boundary of every (position, layer) a forward
+     * visits, log(p_k / p_k+1) of the k-th chosen and the best unchosen
+     * expert, [seq_len][n_layers] (NAN where no routed FFN ran) */
+    float *rt_margin;
+    int64_t cur_pos, cur_layer;
 } ref_engine;
 
 static float ref_sigmoid(float x);
@@ -822,6 +830,8 @@ EXPORT void ref_engine_destroy(void *h) {
     }
     for (int i = 0; i < e->n_stg; i++) free(e->stg_w[i]);
     free(e->stg_key); free(e->stg_w);
+    free(e->vf);
+    free(e->rt_margin);
     free(e->layers);
     pool_destroy(e->pool);
     gfile_free(&e->g);
@@ -1108,6 +1118,12 @@ static void moe_ffn_layer(ref_engine *e, const layer_w *lw, const float *x, floa
         sum += p[best];
         p[best] = -1.0f;
     }
+    if (e->rt_margin && K > 0) {
+        float nxt = -1.0f;
+        for (int64_t i = 0; i < E; i++)
+            if (p[i] > nxt) nxt = p[i];
+        e->rt_margin[e->cur_pos * e->n_layers + e->cur_layer] = nxt > 0.0f ? logf(w[K - 1] / nxt) : INFINITY;
+    }
     for (int64_t k = 0; k < K; k++) w[k] = e->norm_topk ? w[k] / sum : w[k];
     const int64_t grb = ref_row_byte_size(lw->gexp.kind, D), drb = ref_row_byte_size(lw->dexp.kind, F);
     float *hk = h, *hu = h + K * F;
@@ -1283,6 +1299,8 @@ static const float *forward_impl(ref_engine *e, int token, int pos, int staged, 
     ffn:
         ref_rmsnorm(e->xb, e->x, lw->ffn_norm, dim, eps);
         if (lw->moe) { /* routed experts (+ shared expert) */
+            e->cur_pos = pos;
+            e->cur_layer = l;
             moe_ffn_layer(e, lw, e->xb, e->mo_y);
             for (int64_t i = 0; i < dim; i++) e->x[i] += e->mo_y[i];
             continue;
@@ -1353,6 +1371,62 @@ EXPORT const float *ref_engine_prefill(void *h, const int *tokens, int n, int po
     }
     return out;
 }
+
+/* engine_verify_batch (qwen3_5/engine.odin:166-174): the tokens go through
+ * the path of ref_engine_prefill (batched chunks of a multiple of 8 up to 512
+ * with staged projections, the trailing 1-7 per token), and every position's
+ * logits are kept: each token's final RMSNorm and classifier in f32
+ * (metal_verify_batch_logits, qwen3_5/metal.odin:1707-1747: one enc_rmsnorm +
+ * enc_gemv per row of the batch).  Returns [n][vocab] (engine-owned, valid
+ * until the next call), or NULL. */
+EXPORT const float *ref_engine_verify_batch(void *h, const int *tokens, int n, int pos0) {
+    ref_engine *e = (ref_engine *)h;
+    if (n <= 0) {
+        snprintf(g_err, sizeof g_err, "verify_batch: no tokens");
+        return NULL;
+    }
+    if (n > e->vf_rows) {
+        float *b = (float *)realloc(e->vf, (size_t)n * (size_t)e->vocab_size * sizeof(float));
+        if (!b) {
+            snprintf(g_err, sizeof g_err, "verify_batch: out of memory");
+            return NULL;
+        }
+        e->vf = b;
+        e->vf_rows = n;
+    }
+    int i = 0;
+    while (i < n) {
+        int rem = n - i, chunk = 1, staged = 0;
+        if (rem >= 8) {
+            chunk = rem < 512 ? rem : 512;
+            chunk -= chunk % 8;
+            staged = 1;
+        }
+        for (int t = 0; t < chunk; t++) {
+            const float *out = forward_impl(e, tokens[i + t], pos0 + i + t, staged, 1);
+            if (!out) return NULL;
+            memcpy(e->vf + (size_t)(i + t) * (size_t)e->vocab_size, out, (size_t)e->vocab_size * sizeof(float));
+        }
+        i += chunk;
+    }
+    return e->vf;
+}
+
+/* Test hook: start (on != 0; all margins NAN) or stop recording the routing
+ * boundary margins; ref_engine_route_margins returns the [seq_len][n_layers]
+ * table (NULL when not recording). */
+EXPORT int ref_engine_route_log(void *h, int on) {
+    ref_engine *e = (ref_engine *)h;
+    free(e->rt_margin);
+    e->rt_margin = NULL;
+    if (!on) return 0;
+    const size_t n = (size_t)e->seq_len * (size_t)e->n_layers;
+    e->rt_margin = (float *)malloc(n * sizeof(float));
+    if (!e->rt_margin) return -1;
+    for (size_t i = 0; i < n; i++) e->rt_margin[i] = NAN;
+    return 0;
+}
+EXPORT const float *ref_engine_route_margins(void *h) { return ((ref_engine *)h)->rt_margin; }
 
 /* Hidden state after the final norm (test hook for layer-level checks). */
 EXPORT const float *ref_engine_hidden(void *h) { return ((ref_engine *)h)->x; }

@@ -51,6 +51,11 @@ def lib():
         L.ref_engine_forward.argtypes = [c_vp, c_int, c_int]
         L.ref_engine_prefill.restype = ctypes.POINTER(c_f)
         L.ref_engine_prefill.argtypes = [c_vp, c_vp, c_int, c_int]
+        L.ref_engine_verify_batch.restype = ctypes.POINTER(c_f)
+        L.ref_engine_route_log.argtypes = [c_vp, c_int]
+        L.ref_engine_route_margins.restype = ctypes.POINTER(c_f)
+        L.ref_engine_route_margins.argtypes = [c_vp]
+        L.ref_engine_verify_batch.argtypes = [c_vp, c_vp, c_int, c_int]
         L.ref_engine_destroy.argtypes = [c_vp]
         L.ref_engine_config.argtypes = [c_vp, c_vp, c_vp]
         L.ref_engine_kv_fill.argtypes = [c_vp, c_int, c_int, c_int, c_vp, c_vp]
@@ -215,6 +220,29 @@ class RefEngine:
         if not p:
             raise RuntimeError(lib().ref_last_error().decode())
         return np.ctypeslib.as_array(p, shape=(self.vocab_size,)).copy()
+
+    def verify_batch(self, tokens, pos0):
+        """engine_verify_batch: the prefill path over `tokens` with every
+        position's logits kept, [n][vocab]."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        p = lib().ref_engine_verify_batch(self.h, _p(t), int(t.size), int(pos0))
+        if not p:
+            raise RuntimeError(lib().ref_last_error().decode())
+        return np.ctypeslib.as_array(p, shape=(int(t.size), self.vocab_size)).copy()
+
+    def route_log(self, on=True):
+        """Start (all NaN) or stop recording routing boundary margins."""
+        if lib().ref_engine_route_log(self.h, int(bool(on))):
+            raise MemoryError("route log")
+
+    def route_margins(self):
+        """[seq_len][n_layers]: log(p_k / p_k+1) between the k-th chosen and
+        the best unchosen expert of each (position, layer) forwarded while
+        recording (NaN elsewhere)."""
+        p = lib().ref_engine_route_margins(self.h)
+        if not p:
+            raise RuntimeError("route log is off")
+        return np.ctypeslib.as_array(p, shape=(self.seq_len, self.n_layers)).copy()
 
     def kv_fill(self, layer, pos0, k16, v16):
         """k16, v16: uint16 [n_kv_heads][npos][head_dim] for one layer."""

@@ -194,6 +194,46 @@ def test_c3_qwen3_8b_q4_k_m_decode_from_4096(make_model):
         r.close()
 
 
+@pytest.mark.timeout(900)
+def test_c4_qwen3_moe_decode_from_2048(make_model):
+    """BASELINE config 4 at its own context: the Qwen3-30B-A3B layer shapes
+    (32 query / 4 KV heads, so the attention kernel serves 8 query heads per
+    KV head; 128 experts top 8, expert inner 768) on 4 layers, f16 KV
+    pre-filled with N(0,1) to 2048 positions, token 0 at position 2048: the
+    split attention over 33 splits and their merge, the router and the routed
+    experts against the oracle -- logits of the first 8 steps and the 64
+    greedy ids of the device-side loop (infer/forward.odin:87-115 for the
+    attention; the routed FFN restates the HF Qwen3-MoE convention)."""
+    path = make_model("qwen3-30b-a3b-4layer")
+    L, n, nlog = 2048, 64, 8
+    max_ctx = L + n + 8
+    e, ok = infer.engine_load(path, infer.Engine_Opts(max_ctx=max_ctx))
+    assert ok
+    r = refcpu.RefEngine(path, max_ctx=max_ctx, num_threads=NTHREADS, kv_f16=True)
+    try:
+        cfg = infer.engine_config(e)
+        assert (cfg.dim, cfg.n_layers, cfg.n_heads, cfg.n_kv_heads, cfg.vocab_size) == (2048, 4, 32, 4, 151936)
+        k, v = synth.kv_prefill(4343, cfg.n_layers, cfg.n_kv_heads, L, cfg.head_dim)
+        infer.engine_kv_fill(e, 0, 0, k, v)
+        for l in range(cfg.n_layers):
+            r.kv_fill(l, 0, k[l], v[l])
+        ref_ids, margins, kept = _oracle_path(r, 0, L, n, nlog)
+        print("C4 oracle top-1/top-2 margins:", " ".join("%.2g" % m for m in margins), flush=True)
+        tok, worst = 0, 0.0
+        for i in range(nlog):
+            got = infer.engine_forward(e, tok, L + i).copy()
+            err = scaled_err(got, kept[i])
+            worst = max(worst, err)
+            assert err <= TOL, "step %d scaled error %.3g" % (i, err)
+            tok = int(ref_ids[i])
+        print("C4 worst scaled logit error over %d steps from position %d: %.3g" % (nlog, L, worst))
+        ties = _check_greedy(e, path, max_ctx, (k, v), 0, L, ref_ids, margins)
+        print("C4 proven f32 ties:", ties)
+    finally:
+        infer.engine_destroy(e)
+        r.close()
+
+
 def _walk_logits(e, r, n, token=0):
     """Teacher-forced on the oracle's greedy path from position 0: the worst
     scaled logit error over n steps and the oracle's ids and margins."""

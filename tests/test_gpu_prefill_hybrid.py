@@ -84,6 +84,97 @@ def test_prefill_full_shapes_vs_oracle(make_model, name, n):
         r.close()
 
 
+def _oikv_sections(g, o, name):
+    """Compare two .oikv files (GPU, oracle): header byte for byte, then the
+    K/V, conv and recurrent sections by scaled difference."""
+    assert len(g) == len(o) and g[:60] == o[:60]
+    bg, bo = np.frombuffer(g[60:-4], np.float32), np.frombuffer(o[60:-4], np.float32)
+    n, _, n_full, n_lin, kv_dim, conv_dim, kern, nv, hk, hv = struct.unpack_from("<10I", o, 20)
+    off, errs = 0, {}
+    for what, size in [("K/V", 2 * n_full * n * kv_dim), ("conv", n_lin * conv_dim * max(kern - 1, 0)),
+                       ("recurrent", n_lin * nv * hk * hv)]:
+        if size:
+            errs[what] = scaled_err(bg[off:off + size], bo[off:off + size])
+            print("%s: %s section, scaled difference GPU vs oracle %.3g" % (name, what, errs[what]), flush=True)
+        off += size
+    assert off == bo.size
+    return errs
+
+
+@pytest.mark.timeout(1200)
+def test_c5_prompt_2048_in_64_token_chunks_then_decode(make_model, tmp_path):
+    """BASELINE config 5 as configured, on two layers of its shapes (a
+    DeltaNet layer, then a full-attention layer; 512 experts top 10 + the
+    shared expert): a 2048-token random-id prompt in 64-token chunks (one
+    engine_forward_batch call per chunk, qwen3_5/engine.odin:66-93), so the
+    conv and recurrent states carry across 32 chunks and the key-split
+    prefill attention runs at positions up to 2048; then greedy decoding
+    from position 2048.  Against the oracle's staged prefill over the same
+    prompt (qwen3_5/forward.odin:46-225 per token, projections staged in f16
+    as qwen3_5/metal.odin:493-609): last logits within 1e-3 and the same
+    argmax, the K/V, conv and recurrent state after the prompt within 1e-3
+    (through the .oikv files both sides write), then 32 identical greedy ids."""
+    path = make_model("qwen35-hybrid-moe-2layer")
+    n, chunk, ndec = 2048, 64, 32
+    e, r = _engines(path, n + ndec + 8)
+    try:
+        toks = _tokens(2048, n, r.vocab_size)
+        for i in range(0, n, chunk):
+            got = infer.engine_forward_batch(e, toks[i:i + chunk], i)
+        got = got.copy()
+        print("C5 GPU prompt done (%d chunks of %d)" % (n // chunk, chunk), flush=True)
+        r.route_log(True)
+        for i in range(0, n, 256):  # the oracle's result does not depend on its chunking
+            ref = r.prefill(toks[i:i + 256], i)
+            print("oracle prompt: %d / %d tokens" % (i + 256, n), flush=True)
+        margins = r.route_margins()[:n, 0]  # layer 0's routing, which feeds layer 1's K/V
+        r.route_log(False)
+        err = scaled_err(got, ref)
+        print("C5 last logits after the 2048-token prompt: scaled error %.3g" % err, flush=True)
+        assert err <= TOL
+        first = int(np.argmax(got))
+        assert first == refcpu.argmax(ref)
+        fg, fr = tmp_path / "gpu.oikv", tmp_path / "ref.oikv"
+        assert infer.engine_save_kv(e, fg, n)
+        r.save_kv(fr, n)
+        g, o = fg.read_bytes(), fr.read_bytes()
+        errs = _oikv_sections(g, o, "C5 after 2048 tokens")
+        assert set(errs) == {"K/V", "conv", "recurrent"}
+        assert errs["conv"] <= TOL and errs["recurrent"] <= TOL
+        # K/V per position.  Layer 0's top-10-of-512 routing of a token whose
+        # 10th and 11th experts are closer than the f16 staging noise of its
+        # input (the staged projections round the GPU's f32 and the oracle's
+        # float64-accumulated inputs apart at half-way points) may pick the
+        # other expert on the GPU, which moves that one position's layer-1 K/V
+        # by a few percent.  Such a position is accepted only where the
+        # oracle's own routing margin there, log(p10 / p11), is below
+        # ROUTE_TIE, and at most 1% of the positions may need it; every other
+        # position must be within TOL.
+        ROUTE_TIE = 3e-4
+        n_full, kv_dim = struct.unpack_from("<I", o, 28)[0], struct.unpack_from("<I", o, 36)[0]
+        assert n_full == 1
+        bg = np.frombuffer(g[60:60 + 8 * n * kv_dim], np.float32).reshape(2, n, kv_dim).astype(np.float64)
+        bo = np.frombuffer(o[60:60 + 8 * n * kv_dim], np.float32).reshape(2, n, kv_dim).astype(np.float64)
+        per_pos = np.abs(bg - bo).max(axis=(0, 2)) / np.abs(bo).max()
+        bad = np.nonzero(per_pos > TOL)[0]
+        print("C5 K/V: positions over %.0e: %s; their layer-0 routing margins %s; positions with a margin "
+              "below %.0e: %d; worst elsewhere %.3g" % (
+                  TOL, list(bad), ["%.2g" % margins[p] for p in bad], ROUTE_TIE,
+                  int(np.sum(margins < ROUTE_TIE)), float(np.delete(per_pos, bad).max())), flush=True)
+        assert len(bad) <= n // 100
+        assert all(margins[p] < ROUTE_TIE for p in bad), "a K/V difference at a position routed with a clear margin"
+        got_g = infer.engine_decode_greedy(e, first, n, ndec)
+        ref_g, tok = [], first
+        for i in range(ndec):
+            tok = refcpu.argmax(r.forward(tok, n + i))
+            ref_g.append(tok)
+        print("C5 greedy ids from %d: gpu %s oracle %s" % (n, list(got_g), ref_g), flush=True)
+        assert np.array_equal(got_g, np.array(ref_g, np.int32))
+    finally:
+        infer.engine_destroy(e)
+        r.close()
+
+
 @pytest.mark.parametrize("name", ["qwen35-tiny", "qwen35-moe-tiny"])
 def test_prefill_state_vs_oracle(make_model, tmp_path, name):
     """The state after a 37-token prompt (32 batched + 5 per token) through
@@ -98,19 +189,8 @@ def test_prefill_state_vs_oracle(make_model, tmp_path, name):
         fg, fr = tmp_path / "gpu.oikv", tmp_path / "ref.oikv"
         assert infer.engine_save_kv(e, fg, len(toks))
         r.save_kv(fr, len(toks))
-        g, o = fg.read_bytes(), fr.read_bytes()
-        assert len(g) == len(o) and g[:60] == o[:60]
-        bg, bo = np.frombuffer(g[60:-4], np.float32), np.frombuffer(o[60:-4], np.float32)
-        n, _, n_full, n_lin, kv_dim, conv_dim, kern, nv, hk, hv = struct.unpack_from("<10I", o, 20)
-        off = 0
-        for what, size in [("K/V", 2 * n_full * n * kv_dim), ("conv", n_lin * conv_dim * max(kern - 1, 0)),
-                           ("recurrent", n_lin * nv * hk * hv)]:
-            if size:
-                err = scaled_err(bg[off:off + size], bo[off:off + size])
-                print("%s: %s section, scaled difference GPU vs oracle %.3g" % (name, what, err))
-                assert err <= TOL, what
-            off += size
-        assert off == bo.size
+        for what, v in _oikv_sections(fg.read_bytes(), fr.read_bytes(), name).items():
+            assert v <= TOL, what
     finally:
         infer.engine_destroy(e)
         r.close()
@@ -251,3 +331,49 @@ def test_prefill_attention_kernels_agree(make_model, monkeypatch, n):
     err = scaled_err(out["mfma"], out["lanes"])
     print("head_dim 256 attention: matrix cores vs lanes %.3g" % err)
     assert err <= 1e-4
+
+
+@pytest.mark.parametrize("name,seed", [("tiny-q4_k", 31), ("moe-tiny", 43), ("qwen35-moe-tiny", 194)])
+def test_verify_batch_vs_oracle(make_model, name, seed):
+    """engine_verify_batch (qwen3_5/engine.odin:166-174): after a 20-token
+    prompt, 11 draft tokens (a batched chunk of 8, then 3 through the token
+    path) with every position's logits returned.  Each row within 1e-3 of the
+    oracle's verify_batch with the same argmax; the last row equals
+    engine_forward_batch's result for the same tokens on a second engine, bit
+    for bit (the same kernels); the state afterwards is the prefill's: the
+    next token's logits match the oracle's.  The tiny routed models choose 2
+    of 8 experts, so one routing step whose 2nd and 3rd experts are closer
+    than the f16 staging noise would move every later row by percents; the
+    token seeds are ones whose routing margins log(p2 / p3) in the oracle are
+    all above 5e-3, which the test checks first."""
+    path = make_model(name)
+    e, r = _engines(path, 128)
+    e2, ok = infer.engine_load(path, infer.Engine_Opts(max_ctx=128))
+    assert ok
+    try:
+        t = _tokens(seed, 31, r.vocab_size)
+        prompt, draft = t[:20], t[20:]
+        infer.engine_forward_batch(e, prompt, 0)
+        r.route_log(True)
+        r.prefill(prompt, 0)
+        ref = r.verify_batch(draft, 20)
+        if "moe" in name:
+            assert np.nanmin(r.route_margins()[:31]) > 5e-3
+        r.route_log(False)
+        rows = infer.engine_verify_batch(e, draft, 20).copy()
+        assert rows.shape == ref.shape == (11, r.vocab_size)
+        errs = [scaled_err(rows[i], ref[i]) for i in range(11)]
+        print("%s verify rows, scaled error: %s" % (name, " ".join("%.2g" % x for x in errs)), flush=True)
+        assert max(errs) <= TOL
+        assert [int(np.argmax(x)) for x in rows] == [refcpu.argmax(x) for x in ref]
+        infer.engine_forward_batch(e2, prompt, 0)
+        last = infer.engine_forward_batch(e2, draft, 20).copy()
+        assert np.array_equal(last, rows[-1])
+        got = infer.engine_forward(e, 5, 31).copy()
+        assert scaled_err(got, r.forward(5, 31)) <= TOL
+        with pytest.raises(infer.OIError):
+            infer.engine_verify_batch(e, [], 0)
+    finally:
+        infer.engine_destroy(e)
+        infer.engine_destroy(e2)
+        r.close()

@@ -7,6 +7,7 @@ import pytest
 
 import npref
 import refcpu
+from helpers import scaled_err
 from helpers import random_blocks, same_bits
 from oi import synth
 
@@ -206,6 +207,44 @@ def test_forward_vs_float64_model(make_model, name):
             got = r.forward(t, pos)
             err = np.max(np.abs(got - ref[pos])) / np.max(np.abs(ref[pos]))
             assert err <= 2e-4, (pos, err)
+    finally:
+        r.close()
+
+
+@pytest.mark.parametrize("name", ["tiny-q4_k", "tiny-q8_0"])
+def test_verify_batch_vs_float64_model(make_model, name):
+    """The oracle's engine_verify_batch (qwen3_5/engine.odin:166-174): 11
+    tokens = a staged chunk of 8 and 3 per-token positions, every position's
+    logits kept.  Each row is within the bounds of the prefill test below of
+    the float64 model with the same positions staged; the chunk's rows are
+    staged (the unstaged model is farther than the bound on some row), row i
+    predicts position i + 1 (a one-row shift misses), the last row equals
+    ref_engine_prefill's result and the per-token rows equal
+    ref_engine_forward's, bit for bit."""
+    path = make_model(name)
+    W = npref.GGUFWeights(path)
+    tokens = [3, 7, 123, 5, 900, 42, 11, 0, 8, 64, 1]
+    # (the staged rows' bound is the prefill test's 3e-4 with room for the
+    # chunk's inner rows: 2.3e-4 - 3.04e-4 measured, unstaged 4.7e-4 - 9e-4)
+    ref = np.array(npref.forward_f64(W, tokens, f16_kv=True, staged=set(range(8))))
+    plain = np.array(npref.forward_f64(W, tokens, f16_kv=True))
+    r = refcpu.RefEngine(path, max_ctx=64, num_threads=4, kv_f16=True)
+    try:
+        rows = r.verify_batch(tokens, 0)
+        assert rows.shape == (len(tokens), r.vocab_size)
+        errs = [scaled_err(rows[i], ref[i]) for i in range(len(tokens))]
+        assert max(errs[:8]) <= 3.5e-4 and max(errs[8:]) <= 2e-4, errs
+        assert max(scaled_err(rows[i], plain[i]) for i in range(8)) >= 2.5 * max(errs[:8])
+        assert min(scaled_err(rows[i], ref[i + 1]) for i in range(len(tokens) - 1)) > 10 * max(errs)
+        r.reset_state()
+        last = r.prefill(tokens, 0)
+        assert np.array_equal(last, rows[-1])
+        r.reset_state()
+        r.prefill(tokens[:8], 0)
+        for i in range(8, len(tokens)):
+            assert np.array_equal(r.forward(tokens[i], i), rows[i])
+        with pytest.raises(RuntimeError):
+            r.verify_batch([], 0)
     finally:
         r.close()
 
