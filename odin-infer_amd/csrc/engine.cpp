@@ -561,11 +561,16 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     // device memory plan
     int n_attn = 0, n_lin = 0;
     for (int k : kinds) (k == LK_LINEAR ? n_lin : n_attn)++;
-    e->chunk = attn_chunk((int)c.head_dim);
-    e->max_splits = (int)((c.seq_len + e->chunk - 1) / e->chunk);
+    // decode attention at head_dim 128: the lane-per-position kernel over
+    // splits of 64 (default), or OI_ATTN=mfma, the matrix-core kernel over
+    // splits sized from pos (the same arithmetic; measured no faster at C3)
+    const char *af = std::getenv("OI_ATTN");
+    e->max_splits = attn_plan((int)c.head_dim, (int)c.n_kv_heads, (int)c.seq_len, &e->chunk,
+                              !(af && std::strcmp(af, "mfma") == 0));
     if (e->max_splits > attn_max_splits())
-        return fail(OI_E_UNSUPPORTED, "seq_len " + std::to_string(c.seq_len) + " exceeds the attention kernel's " +
-                                          std::to_string(attn_max_splits() * e->chunk) + " positions");
+        return fail(OI_E_UNSUPPORTED, "seq_len " + std::to_string(c.seq_len) + " needs " +
+                                          std::to_string(e->max_splits) + " attention splits (at most " +
+                                          std::to_string(attn_max_splits()) + ")");
     const int q35_splits = e->arch == 2 ? q35_max_splits((int)c.seq_len) : 0;
     const size_t kv_layer = (size_t)c.n_kv_heads * c.seq_len * c.head_dim * 2;
     const size_t conv_layer = (size_t)CD * (e->lin_kernel > 0 ? e->lin_kernel - 1 : 0) * 4;

@@ -157,6 +157,12 @@ hipError_t launch_embed(const DMat &emb, int32_t *state, float *x, int32_t vocab
                         const int32_t *am_idx, int32_t *tokens_out, int finalize_only, hipStream_t st);
 int attn_chunk(int head_dim);
 int attn_max_splits();
+// Splits of the decode attention at this shape (the grid's first dimension,
+// the partial buffer's split count); *chunk: positions per split, 0 when the
+// kernel sizes its splits from pos at run time.  fixed: splits of 64 on the
+// lane-per-position kernel at every head_dim; otherwise head_dim 128 takes
+// the matrix-core kernel.
+int attn_plan(int head_dim, int n_kv_heads, int seq_len, int *chunk, bool fixed);
 hipError_t launch_dequant(const DMat &m, float *out, hipStream_t st);
 // One draw of the sampler (sample.hip) from logits[0, n); p: n floats of
 // scratch.  With `state` set the pick advances the token loop (token, pos,

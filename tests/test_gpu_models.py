@@ -317,3 +317,39 @@ def test_split_deltanet_step_matches_fused(make_model, monkeypatch, name):
     worst = max(scaled_err(a, b) for a, b in zip(out[False], out[True]))
     print("%s: split vs fused DeltaNet step, worst scaled logit difference %.3g" % (name, worst))
     assert worst <= 2e-4
+
+
+@pytest.mark.parametrize("name,overrides,L", [
+    ("tiny-q4_k", {"n_heads": 2, "n_kv_heads": 2}, 700),  # 1 query head per KV head
+    ("qwen3-0.6b-q8_0", {"n_layers": 2}, 1500),           # 2 (config 1's heads)
+    ("small-q4_k", {}, 3000),                              # 4
+    ("qwen3-30b-a3b-4layer", {}, 2048),                    # 8 (config 4's heads)
+])
+def test_decode_attention_kernels_agree(make_model, monkeypatch, name, overrides, L):
+    """The head_dim-128 decode attention on the lane-per-position kernel over
+    splits of 64 (the default, f32 q) against the matrix-core kernel
+    (OI_ATTN=mfma: splits sized from pos, one 16-key tile per wave, q split
+    into f16 + remainder, f32 sums): the same f32 arithmetic up to the order
+    of the sums and q's ~2^-22 rounding.  8 steps from a KV cache pre-filled
+    with N(0,1) to L positions, logits within 2e-5 (scaled) of each other
+    (the matrix-core kernel without the remainder columns measured 4.1e-4 on
+    small-q4_k); the default is within 1e-3 of the oracle in the tests above."""
+    path = make_model(name, **overrides)
+    out = {}
+    for kind in ("default", "mfma"):
+        if kind == "mfma":
+            monkeypatch.setenv("OI_ATTN", "mfma")
+        e, ok = infer.engine_load(path, infer.Engine_Opts(max_ctx=L + 16))
+        assert ok
+        try:
+            cfg = infer.engine_config(e)
+            k, v = synth.kv_prefill(77, cfg.n_layers, cfg.n_kv_heads, L, cfg.head_dim)
+            infer.engine_kv_fill(e, 0, 0, k, v)
+            toks = [int(t) for t in np.random.default_rng(5).integers(0, cfg.vocab_size, 8)]
+            out[kind] = [infer.engine_forward(e, t, L + i).copy() for i, t in enumerate(toks)]
+        finally:
+            infer.engine_destroy(e)
+    worst = max(scaled_err(a, b) for a, b in zip(out["default"], out["mfma"]))
+    print("%s (L=%d): matrix-core vs lane-per-position attention, worst scaled logit difference %.3g"
+          % (name, L, worst))
+    assert worst <= 2e-5
