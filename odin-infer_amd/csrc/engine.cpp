@@ -235,6 +235,7 @@ namespace {
 hipError_t launch_op(const oi_engine *e, const Op &o, hipStream_t st) {
     switch (o.kind) {
     case OP_MOE_ROWS: return launch_gemv_q_moe(o.g, MOE_ROWS, st);
+    case OP_MOE_ROWS_R: return launch_gemv_q_moe(o.g, MOE_ROWS_R, st);
     case OP_MOE_COLS: return launch_gemv_q_moe(o.g, MOE_COLS, st);
     case OP_ATTN: return launch_attn(o.at, (int)e->cfg.head_dim, st);
     case OP_Q35: return launch_q35_attn(o.q, (int)e->cfg.head_dim, st);
@@ -773,6 +774,10 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
         return o;
     };
     e->dn_fused = std::getenv("OI_DN_FUSED") != nullptr;  // the one-launch DeltaNet step in the token loop
+    {
+        const char *mr = std::getenv("OI_MOE_ROUTER");
+        e->router_fused = mr && std::strcmp(mr, "fused") == 0;
+    }
     e->ops.assign((size_t)c.n_layers, {});
     for (size_t l = 0; l < e->layers.size(); l++) {
         LayerDev &L = e->layers[l];
@@ -882,11 +887,6 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
         // experts' gate/up with the routing in its prologue, the shared expert's
         // gate/up, then the two down projections adding into x (the shared one
         // scaled by sigmoid of its gate)
-        GemvArgs r = gemv_args(GEMV_STORE, (int)D, e->x, L.ffn_norm, eps);
-        r.nseg = L.shared ? 2 : 1;
-        r.seg[0].m = L.router; r.seg[0].y = mo_logits;
-        if (L.shared) { r.seg[1].m = L.sh_inp; r.seg[1].y = mo_sg; }
-        ops.push_back(gemv_op(K_ROUTER, r));
         // a merged shared expert is expert E: one more part of the routed launches
         const int sx = L.shared_merged ? 1 : 0;
         const int64_t KP = e->top_k + sx;  // parts: the chosen experts (+ the shared one)
@@ -914,8 +914,28 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
         if (!gemv_q_moe_supported(ga, MOE_ROWS))
             return fail(OI_E_UNSUPPORTED, "routed experts: type or shape not supported by the expert GEMV "
                                           "(Q4_K / Q6_K / Q8_0, dim <= 4096, inner a multiple of 256)");
-        plan_gemv_q(ga);
         gu.bytes = 2.0 * KP * mbytes(L.gexp) / (E + sx) + 4.0 * D + 4.0 * E + 4.0 * KP * EF;
+        // a router GEMV (+ the shared expert's gate row) first; or, with
+        // OI_MOE_ROUTER=fused, the router inside the gate/up launch (each
+        // workgroup computes the logits from its normalized x) where the router
+        // fits it -- no shared expert, the experts' type.  Config 4: gate/up
+        // 16.7 us fused against 5.6 + 9.8 us as two launches (every workgroup
+        // reads the router and routes before its first expert row is requested)
+        GemvArgs fr = ga;
+        fr.moe_logits = nullptr;
+        fr.moe_router = L.router;
+        if (e->router_fused && !L.shared && gemv_q_moe_supported(fr, MOE_ROWS_R)) {
+            ga = fr;
+            gu.kind = OP_MOE_ROWS_R;
+            gu.bytes += mbytes(L.router);
+        } else {
+            GemvArgs r = gemv_args(GEMV_STORE, (int)D, e->x, L.ffn_norm, eps);
+            r.nseg = L.shared ? 2 : 1;
+            r.seg[0].m = L.router; r.seg[0].y = mo_logits;
+            if (L.shared) { r.seg[1].m = L.sh_inp; r.seg[1].y = mo_sg; }
+            ops.push_back(gemv_op(K_ROUTER, r));
+        }
+        plan_gemv_q(ga);
         ops.push_back(gu);
         // the shared expert's gate/up reads the same normalized x, so it runs
         // before either down projection adds into x

@@ -42,7 +42,7 @@ struct LayerDev {
 
 // One launch of the token step: a GEMV (dense or routed-expert), an attention
 // or a DeltaNet step.  `role` is the kernel id of oi_engine_time_kernel.
-enum { OP_GEMV = 0, OP_MOE_ROWS, OP_MOE_COLS, OP_ATTN, OP_Q35, OP_DN };
+enum { OP_GEMV = 0, OP_MOE_ROWS, OP_MOE_COLS, OP_ATTN, OP_Q35, OP_DN, OP_MOE_ROWS_R };
 struct Op {
     int kind = OP_GEMV, role = 0;
     double bytes = 0;  // algorithmic HBM bytes per launch (attention: without the cache rows)
@@ -116,6 +116,8 @@ struct oi_engine {
                          // only, 3 no few-pair items, 4 few-pair items on MFMA (OI_PREFILL_EXPERTS=gemv / f32 /
                          // wide / fewmfma)
     bool dn_fused = false;  // token loop: the one-launch DeltaNet step instead of the split one (OI_DN_FUSED)
+    bool router_fused = false;  // token loop: the router inside the routed gate/up launch where it applies
+                                // (OI_MOE_ROUTER=fused; measured slower at config 4 than its own launch)
     int pf_dn_chunk = 0;  // delta rule of a prefill chunk: 0 token by token, 16 / 32 chunked (OI_PREFILL_DN_CHUNK)
     // engine_verify_batch: the logits of every position, [rows][vocab] on the
     // device and in pinned host memory (allocated on first use, grown as needed)

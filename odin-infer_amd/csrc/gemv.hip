@@ -394,7 +394,7 @@ static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int 
         for (int r = 0; r < R; r++) {
             const int row = live ? min((tb + t) * rpt + rsub + r, rows_m - 1) : 0;
             int prow = row, pu = live ? (MOE == MOE_COLS ? min(u, U - 1) : u) : j;  // the stored row and unit
-            if (MOE == MOE_ROWS) {  // virtual row -> row of the chosen expert
+            if (MOE == MOE_ROWS || MOE == MOE_ROWS_R) {  // virtual row -> row of the chosen expert
                 const int k = row / a.moe_blk;
                 prow = __shfl(idv, k, WAVE) * a.moe_blk + (row - k * a.moe_blk);
             } else if (MOE == MOE_COLS) {  // unit of the concatenation -> unit of the chosen expert's row
@@ -430,7 +430,8 @@ static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int 
     float *yo = s16 + K / 16;  // this workgroup's outputs
     const int wrow0 = tb * rpt, wrow1 = min(te * rpt, rows_m);
     if (tid == 0) tile_ctr = 0;  // read after the prologue's barriers
-    xpre_finish<XR, NORM>(a, xp, xhi, xmid, xlo, xs, s32, s16, red);
+    if (MOE == MOE_ROWS_R) __syncthreads();  // the kernel built the x planes before routing
+    else xpre_finish<XR, NORM>(a, xp, xhi, xmid, xlo, xs, s32, s16, red);
     const XQ xq{xhi, xmid, xlo, xs, s32, s16};
     X xu;
     if (XU1) xload(xq, j, xu);
@@ -734,6 +735,56 @@ static __device__ __forceinline__ void moe_route(const GemvArgs &a, float lg, fl
     }
 }
 
+// Router of a routed-expert layer fused into the gate/up launch (MOE_ROWS_R):
+// l[r] = router row r . x for r < moe_n, from the x planes in LDS -- the
+// router GEMV's arithmetic (the same 64-weight units, int8 products, per-unit
+// scaling), lanes per row = K / 64 (32 or 64).  The rows of up to RR steps
+// are requested at the kernel's start, before the x prologue (a workgroup
+// reads the router from L2, the first of each XCD from HBM), and consumed
+// after it; longer routers take further passes.
+template <int T>
+struct RouterPre {
+    static constexpr int RR = T == T_Q4_K ? 4 : 2;  // (a Q6_K / Q8_0 unit holds more registers)
+    typename Types<T>::W w[RR];
+};
+// (the waves' rows are rotated by the workgroup index, so the workgroups of
+// an XCD do not request the same router rows at the same moment)
+template <int T>
+static __device__ __forceinline__ void router_row(const GemvArgs &a, int base, int st, int &r, int &j) {
+    const int U = a.K >> 6, lane = threadIdx.x & (WAVE - 1), rpw = WAVE / U;
+    const int wave = ((int)(threadIdx.x / WAVE) + (int)blockIdx.x) & (GNW - 1);
+    j = lane & (U - 1);
+    r = base + (st * GNW + wave) * rpw + lane / U;
+}
+template <int T>
+static __device__ __forceinline__ void router_load(const GemvArgs &a, int base, RouterPre<T> &p) {
+#pragma unroll
+    for (int st = 0; st < RouterPre<T>::RR; st++) {
+        int r, j;
+        router_row<T>(a, base, st, r, j);
+        wload(a.moe_router, min(r, a.moe_n - 1), j, p.w[st]);
+    }
+}
+template <int T>
+static __device__ __forceinline__ void router_logits(const GemvArgs &a, const XQ &xq, RouterPre<T> &p, float *rl) {
+    using X = typename Types<T>::X;
+    constexpr int RR = RouterPre<T>::RR;
+    const int U = a.K >> 6, rpw = WAVE / U, n = a.moe_n;
+    int r, j;
+    router_row<T>(a, 0, 0, r, j);
+    X xu;
+    xload(xq, j, xu);
+    for (int base = 0; base < n; base += GNW * rpw * RR) {
+        if (base > 0) router_load<T>(a, base, p);
+#pragma unroll
+        for (int st = 0; st < RR; st++) {
+            const float v = lane_group_sum(wdot(p.w[st], j, xu), U);
+            router_row<T>(a, base, st, r, j);
+            if (j == 0 && r < n) rl[r] = v;
+        }
+    }
+}
+
 // Weight types are template parameters: T for every segment but the last,
 // TL for the last (TL == T: one type).  A runtime switch over all types would
 // let the compiler merge the code paths, and at the merge it can no longer
@@ -762,6 +813,29 @@ __global__ __launch_bounds__(GW) void gemv_q_kernel(GemvArgs a) {
         __builtin_amdgcn_s_waitcnt(0x0F70);
         __builtin_amdgcn_sched_barrier(0);
         gemv_run<TL, R, NM, XR, XU1, NORM>(a, seg, tb, te, wg, xp);
+    } else if (MOE == MOE_ROWS_R) {
+        // the x prologue here (RMSNorm, the quantized planes in LDS, as
+        // gemv_run's), the router logits from it, the routing, then the
+        // chosen experts' rows
+        XPre<XR, NORM> xp;
+        xpre_load<XR, NORM>(a, xp);
+        __builtin_amdgcn_sched_barrier(0);  // x first: the router rows queue behind it, not before
+        RouterPre<T> rp;
+        router_load<T>(a, 0, rp);
+        __builtin_amdgcn_sched_barrier(0);
+        extern __shared__ u32x4 smem[];
+        __shared__ float red_r[GNW], rl[GW];
+        const int K = a.K;
+        u32x4 *xhi = smem, *xmid = smem + K / 16, *xlo = smem + 2 * (K / 16);
+        float *xs = (float *)(smem + 3 * (K / 16)), *s32 = xs + K / 32, *s16 = s32 + K / 32;
+        xpre_finish<XR, NORM>(a, xp, xhi, xmid, xlo, xs, s32, s16, red_r);
+        const XQ xq{xhi, xmid, xlo, xs, s32, s16};
+        router_logits<T>(a, xq, rp, rl);
+        __syncthreads();
+        int idv = 0;
+        float wv = 0.f;
+        moe_route(a, (int)threadIdx.x < a.moe_n ? rl[threadIdx.x] : 0.f, 0.f, idv, wv, wg);
+        gemv_run<T, R, NM, XR, XU1, NORM, MOE>(a, seg, tb, te, wg, xp, idv, wv);
     } else {
         XPre<XR, NORM> xp;
         xpre_load<XR, NORM>(a, xp);
@@ -971,33 +1045,50 @@ static const void *gemv_q_moe_fn(int K, bool norm) {
         if (xu1) return (const void *)gemv_q_kernel<T, T, 1, 2, 1, true, false, MOE_ROWS>;
         return (const void *)gemv_q_kernel<T, T, 1, 2, 1, false, false, MOE_ROWS>;
     }
+    if (MOE == MOE_ROWS_R) {  // the router needs RMSNorm(x): norm only
+        if ((K != 2048 && K != 4096) || !norm) return nullptr;
+        if (xu1) return (const void *)gemv_q_kernel<T, T, 1, 2, 1, true, true, MOE_ROWS_R>;
+        return (const void *)gemv_q_kernel<T, T, 1, 2, 1, false, true, MOE_ROWS_R>;
+    }
     if (norm) return nullptr;
     if (K <= 4096 && xu1) return (const void *)gemv_q_kernel<T, T, 1, 1, 1, true, false, MOE_COLS>;
     if (K <= 4096) return (const void *)gemv_q_kernel<T, T, 1, 1, 1, false, false, MOE_COLS>;
     if (K <= 12288) return (const void *)gemv_q_kernel<T, T, 1, 1, 3, false, false, MOE_COLS>;
     return nullptr;
 }
+template <int T>
+static const void *gemv_q_moe_fn_t(int moe, int K, bool norm) {
+    switch (moe) {
+    case MOE_ROWS: return gemv_q_moe_fn<T, MOE_ROWS>(K, norm);
+    case MOE_ROWS_R: return gemv_q_moe_fn<T, MOE_ROWS_R>(K, norm);
+    case MOE_COLS: return gemv_q_moe_fn<T, MOE_COLS>(K, norm);
+    default: return nullptr;
+    }
+}
 static const void *gemv_q_moe_fn(int type, int moe, int K, bool norm) {
     switch (type) {
-    case T_Q4_K:
-        return moe == MOE_ROWS ? gemv_q_moe_fn<T_Q4_K, MOE_ROWS>(K, norm) : gemv_q_moe_fn<T_Q4_K, MOE_COLS>(K, norm);
-    case T_Q6_K:
-        return moe == MOE_ROWS ? gemv_q_moe_fn<T_Q6_K, MOE_ROWS>(K, norm) : gemv_q_moe_fn<T_Q6_K, MOE_COLS>(K, norm);
-    case T_Q8_0:
-        return moe == MOE_ROWS ? gemv_q_moe_fn<T_Q8_0, MOE_ROWS>(K, norm) : gemv_q_moe_fn<T_Q8_0, MOE_COLS>(K, norm);
+    case T_Q4_K: return gemv_q_moe_fn_t<T_Q4_K>(moe, K, norm);
+    case T_Q6_K: return gemv_q_moe_fn_t<T_Q6_K>(moe, K, norm);
+    case T_Q8_0: return gemv_q_moe_fn_t<T_Q8_0>(moe, K, norm);
     default: return nullptr;
     }
 }
 
 bool gemv_q_moe_supported(const GemvArgs &a, int moe) {
-    if ((a.norm_w && moe != MOE_ROWS) || a.gss || a.conv_w || a.moe_k < 1 || a.moe_k > WAVE || a.moe_n < 1 ||
-        a.moe_blk < 1)
+    if ((a.norm_w && moe != MOE_ROWS && moe != MOE_ROWS_R) || a.gss || a.conv_w || a.moe_k < 1 ||
+        a.moe_k > WAVE || a.moe_n < 1 || a.moe_blk < 1)
         return false;
     if (moe == MOE_ROWS) {
         if (a.mode != GEMV_SWIGLU || a.seg[0].m.rows != a.moe_k * a.moe_blk) return false;
         const int sel = a.moe_sel > 0 ? a.moe_sel : a.moe_k;
         if (a.moe_sel > 0 && (a.moe_sel + 1 != a.moe_k || !a.moe_sgate || a.moe_nblk != a.moe_n + 1)) return false;
         if (a.moe_logits ? (a.moe_n > GW || sel > a.moe_n || !a.moe_ids_out || !a.moe_w_out) : !a.moe_ids)
+            return false;
+    } else if (moe == MOE_ROWS_R) {
+        // no shared expert; the router in the experts' type, one row per expert
+        if (a.mode != GEMV_SWIGLU || a.seg[0].m.rows != a.moe_k * a.moe_blk || a.moe_sel > 0 || !a.norm_w ||
+            a.moe_n > GW || a.moe_k > a.moe_n || !a.moe_ids_out || !a.moe_w_out || a.moe_router.rows != a.moe_n ||
+            a.moe_router.cols != a.K || a.moe_router.type != a.seg[0].m.type || !a.moe_router.q)
             return false;
     } else if (moe == MOE_COLS) {
         if ((a.mode != GEMV_STORE && a.mode != GEMV_ADD) || a.nseg != 1 || !a.moe_ids || !a.moe_w || a.moe_blk % 4 ||

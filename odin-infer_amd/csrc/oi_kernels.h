@@ -99,6 +99,10 @@ struct GemvArgs {
     // no shared expert (moe_sel = moe_k, moe_nblk = moe_n)
     int32_t moe_sel, moe_nblk;
     const float *moe_sgate;
+    // rows mode, router fused (MOE_ROWS_R): the router matrix (moe_n rows of K,
+    // the experts' weight type); every workgroup computes the router logits
+    // from its RMSNormed x before routing (no router launch, no moe_logits)
+    DMat moe_router;
     // GEMV_ADD: if set, the product is scaled by sigmoid(ygate[0]) before the add
     // (the shared expert's gate of a Qwen3-Next-style MoE layer)
     const float *ygate;
@@ -183,9 +187,11 @@ bool gemv_q_supported(const GemvArgs &a);
 void plan_gemv_q(GemvArgs &a);
 hipError_t launch_gemv_q(const GemvArgs &a, hipStream_t st);
 // routed-expert GEMV (moe = MOE_ROWS: SwiGLU over the chosen experts' gate/up
-// rows; MOE_COLS: down over the chosen experts' rows, weighted); a planned by
-// plan_gemv_q; false from gemv_q_moe_supported means the generic kernels
-enum { MOE_ROWS = 1, MOE_COLS = 2 };
+// rows; MOE_ROWS_R: the same with the router fused into the launch, from
+// GemvArgs::moe_router; MOE_COLS: down over the chosen experts' rows,
+// weighted); a planned by plan_gemv_q; false from gemv_q_moe_supported means
+// the generic kernels
+enum { MOE_ROWS = 1, MOE_COLS = 2, MOE_ROWS_R = 3 };
 bool gemv_q_moe_supported(const GemvArgs &a, int moe);
 hipError_t launch_gemv_q_moe(const GemvArgs &a, int moe, hipStream_t st);
 

@@ -74,3 +74,34 @@ def test_moe_rejects_bad_dims():
     rb, gb, ub, db = make_moe(rng, 4, 128, 64, 8)
     with pytest.raises(_native.OIError):
         moe.moe_ffn(4, 5, 128, 64, 1, 0, rb, 8, gb, ub, db, np.ones(128, np.float32))  # top_k > n_experts
+
+
+def test_fused_router_matches_separate(make_model, monkeypatch):
+    """The token loop's router inside the routed gate/up launch
+    (OI_MOE_ROUTER=fused: each workgroup computes the 128 router logits of
+    config 4's layer from its RMSNormed x) against the router as a launch of
+    its own (the default): the same int8 products up to the order of the lane
+    sums, so the same experts are chosen and 16 steps of logits agree within
+    1e-5, on 4 layers of the Qwen3-30B-A3B shape; the device loop's greedy ids
+    are equal."""
+    import numpy as np
+    from helpers import scaled_err
+    from oi import infer
+    path = make_model("qwen3-30b-a3b-4layer")
+    out, ids = {}, {}
+    for kind in ("separate", "fused"):
+        if kind == "fused":
+            monkeypatch.setenv("OI_MOE_ROUTER", "fused")
+        e, ok = infer.engine_load(path, infer.Engine_Opts(max_ctx=64))
+        assert ok
+        try:
+            toks = [int(t) for t in np.random.default_rng(9).integers(0, 151936, 16)]
+            out[kind] = [infer.engine_forward(e, t, p).copy() for p, t in enumerate(toks)]
+            infer.engine_reset_state(e)
+            ids[kind] = list(infer.engine_decode_greedy(e, 0, 0, 24))
+        finally:
+            infer.engine_destroy(e)
+    worst = max(scaled_err(a, b) for a, b in zip(out["fused"], out["separate"]))
+    print("fused vs separate router, worst scaled logit difference %.3g" % worst)
+    assert worst <= 1e-5
+    assert ids["fused"] == ids["separate"]
