@@ -768,6 +768,37 @@ def measure_prefill(e, cfg, n, reps=7):
                     "<=512 tokens; the prompt overwrites the cache from position 0 after the decode measurement"}
 
 
+def remove_stale_models(min_age_s=120):
+    """Delete the synthetic models that an earlier bench run left in the
+    temporary directory when it ended abnormally (each is up to 45 GB; left
+    behind they make later runs skip the whole-model measurements for lack
+    of disk).  Only this script's directories (oi_bench_*, oi_c1_*, oi_<model>_*
+    holding nothing but .gguf files) older than min_age_s are removed."""
+    root = tempfile.gettempdir()
+    removed = 0
+    try:
+        names = os.listdir(root)
+    except OSError:
+        return 0
+    for name in names:
+        p = os.path.join(root, name)
+        if not name.startswith("oi_") or not os.path.isdir(p) or os.path.islink(p):
+            continue
+        try:
+            files = os.listdir(p)
+            if not files or not all(f.endswith(".gguf") for f in files):
+                continue
+            if time.time() - os.path.getmtime(p) < min_age_s:
+                continue
+            shutil.rmtree(p, ignore_errors=True)
+            removed += 1
+        except OSError:
+            continue
+    if removed:
+        log("removed %d stale synthetic-model directories from %s" % (removed, root))
+    return removed
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -788,6 +819,7 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (3 times), to calibrate HBM counters")
     args = ap.parse_args()
+    remove_stale_models()
     if args.copy_calibration:
         import torch
         n = args.copy_calibration << 20
