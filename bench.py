@@ -417,7 +417,7 @@ def deltanet_step(iters=200, cpu=True):
         el = time.perf_counter() - t0
         out["cpu_baseline"] = {"value": round(1e6 * el / n, 3), "unit": "us/step", "cores": 1, "kind": "port",
                                "sample": "%d steps of oracle/refcpu.c ref_deltanet_steps (restated qwen3_5/ops.odin "
-                                         "and forward.odin:172-219), same shape" % n}
+                                         "and qwen3_5/forward.odin:172-219), same shape" % n}
     return out
 
 
@@ -611,7 +611,7 @@ def _free_gb(path):
     return st.f_bavail * st.f_frsize / 1e9
 
 
-def model_decode(name, context, steps, warmup=8, prompt=0, cpu=True, cpu_budget=20.0):
+def model_decode(name, context, steps, warmup=8, prompt=0, cpu=True, cpu_budget=20.0, chunks=(64, 512)):
     """A whole-model decode measurement at batch 1 for the routed-expert and
     hybrid configurations: the synthetic model `name` (full size), then either
     the f16 KV cache pre-filled with N(0,1) to `context` positions (config 4)
@@ -642,7 +642,7 @@ def model_decode(name, context, steps, warmup=8, prompt=0, cpu=True, cpu_budget=
                 toks = np.random.default_rng(5).integers(0, cfg.vocab_size, size=prompt).astype(np.int32)
                 infer.engine_forward_batch(e, toks[:64], 0)  # allocates the prefill buffers
                 pf = {"tokens": prompt}
-                for chunk in (64, 512):
+                for chunk in chunks:
                     best = None
                     for _ in range(3):
                         infer.engine_reset_state(e)
@@ -651,12 +651,21 @@ def model_decode(name, context, steps, warmup=8, prompt=0, cpu=True, cpu_budget=
                             logits = infer.engine_forward_batch(e, toks[i:i + chunk], i)
                         pel = time.perf_counter() - t0
                         best = pel if best is None else min(best, pel)
-                    pf["chunk%d" % chunk] = {"ms": round(1000 * best, 1), "tok_s": round(prompt / best, 1)}
+                    wk = hybrid_prefill_work(spec, prompt, chunk)
+                    pf["chunk%d" % chunk] = {
+                        "ms": round(1000 * best, 1), "tok_s": round(prompt / best, 1),
+                        "algorithmic_bytes": wk["bytes"], "GBps": round(wk["bytes"] / best / 1e9, 1),
+                        "frac_hbm_peak": round(wk["bytes"] / best / 1e9 / PEAK_HBM_GBPS, 4),
+                        "TFLOPs": round(wk["flops"] / best / 1e12, 2),
+                        "frac_f16_peak": round(wk["flops"] / best / 1e12 / PEAK_F16_TFLOPS, 4),
+                        "distinct_experts_per_call": wk["distinct_experts_per_call"]}
                     log("%s prefill, %d-token chunks: %d tokens in %.1f ms (%.0f tok/s)" % (
                         name, chunk, prompt, 1000 * best, prompt / best))
                 first = int(np.argmax(logits))
                 pf["note"] = ("batched prefill (oi_engine_prefill) from a reset state, one call per chunk, host "
-                              "wall clock, best of 3; decode continues from the 512-token-chunk run")
+                              "wall clock, best of 3; decode continues from the last chunk length's run; bytes and "
+                              "FLOPs from bench.hybrid_prefill_work (routed experts: expected distinct experts "
+                              "per call under uniform routing)")
                 out["prefill"] = pf
                 snap = None
             else:
@@ -725,6 +734,55 @@ def model_decode(name, context, steps, warmup=8, prompt=0, cpu=True, cpu_budget=
         return out
     finally:
         shutil.rmtree(d, ignore_errors=True)
+
+
+def hybrid_prefill_work(spec, prompt, chunk):
+    """Algorithmic HBM bytes and FLOPs of a Qwen3.5 hybrid routed-expert
+    prompt of `prompt` tokens run in `chunk`-token calls (oi_engine_prefill,
+    qwen3_5/forward.odin:46-225 per token).  Per call: every dense weight once
+    (attention / DeltaNet projections, router, shared expert, the output
+    projection for the call's last row), the routed experts that the call's
+    tokens select -- counted as the expected number of distinct experts under
+    uniform routing, E (1 - (1 - k/E)^T) of E, since a call streams each
+    selected expert once -- the K/V of the full-attention layers read up to the
+    call's last position and written for its tokens, and the DeltaNet conv and
+    recurrent states read and written once.  FLOPs: 2 per weight element per
+    token for the dense weights and the k routed experts, plus 4 hd per key
+    per head for attention (scores and values) and 4 hk hv per token per value
+    head for the delta rule."""
+    from oi.ggml import row_byte_size
+    D, V, L = spec["dim"], spec["vocab_size"], spec["n_layers"]
+    Q, KV, hd = spec["n_heads"] * spec["head_dim"], spec["n_kv_heads"] * spec["head_dim"], spec["head_dim"]
+    E, k, EF, SF = spec["n_experts"], spec["n_experts_used"], spec["expert_ffn"], spec["shared_expert_ffn"]
+    nv, hk, hv = spec["lin_n_v_heads"], spec["lin_head_k_dim"], spec["lin_head_v_dim"]
+    KD, VD = spec["lin_n_k_heads"] * hk, nv * hv
+    CD, ck = 2 * KD + VD, spec["lin_conv_kernel"]
+    t, tv, tdn, tr = spec["type_default"], spec["type_attn_v"], spec["type_ffn_down"], spec["type_router"]
+    n_full = sum(1 for l in range(L) if (l + 1) % spec["full_attn_interval"] == 0)
+    n_lin = L - n_full
+    rb = row_byte_size
+    full_w = rb(t, D) * (2 * Q + KV) + rb(tv, D) * KV + rb(t, Q) * D
+    full_p = D * (2 * Q + 2 * KV) + Q * D
+    lin_w = rb(t, D) * (CD + VD + 2 * nv) + rb(t, VD) * D + 4 * CD * ck
+    lin_p = D * (CD + VD + 2 * nv) + VD * D
+    ffn_w = rb(tr, D) * (E + 1) + rb(t, D) * 2 * SF + rb(tdn, SF) * D
+    ffn_p = D * (E + 1) + 3 * SF * D
+    exp_w = rb(t, D) * 2 * EF + rb(tdn, EF) * D
+    exp_p = 3 * EF * D
+    dense_w = n_full * full_w + n_lin * lin_w + L * ffn_w + rb(spec["type_output"], D) * V
+    per_tok_p = n_full * full_p + n_lin * lin_p + L * (ffn_p + k * exp_p)
+    state = n_lin * (nv * hk * hv * 4 + CD * (ck - 1) * 4)
+    byts = flops = 0.0
+    for p0 in range(0, prompt, chunk):
+        T = min(chunk, prompt - p0)
+        distinct = E * (1.0 - (1.0 - k / E) ** T)
+        byts += dense_w + L * distinct * exp_w + T * rb(spec["type_embd"], D)
+        byts += n_full * 2 * KV * 2 * (p0 + T) + n_full * 2 * KV * 2 * T + 2 * state
+        flops += 2.0 * T * per_tok_p + 2.0 * D * V
+        keys = T * p0 + T * (T + 1) / 2  # causal keys over the call's rows
+        flops += n_full * 4.0 * spec["n_heads"] * hd * keys + n_lin * 4.0 * T * nv * hk * hv
+    return {"bytes": int(byts), "flops": flops,
+            "distinct_experts_per_call": round(E * (1.0 - (1.0 - k / E) ** min(chunk, prompt)), 1)}
 
 
 def weight_bytes_any(spec):
@@ -816,6 +874,10 @@ def main():
                                        "c4", "c5"],
                     default=None,
                     help="run one secondary measurement alone (for profiling) and print its JSON")
+    ap.add_argument("--c5-model", default="qwen35-hybrid-moe",
+                    help="synthetic model of --only c5 (a shorter model of the same shapes, such as "
+                         "qwen35-hybrid-moe-4layer, gives the same per-launch kernels for profiling)")
+    ap.add_argument("--c5-chunks", default="64,512", help="prompt chunk lengths of --only c5, comma-separated")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (3 times), to calibrate HBM counters")
     args = ap.parse_args()
@@ -862,8 +924,9 @@ def main():
         print(json.dumps({"c4": model_decode("qwen3-30b-a3b-q4_k", 2048, 256, cpu=not args.no_cpu)}), flush=True)
         return
     if args.only == "c5":
-        print(json.dumps({"c5": model_decode("qwen35-hybrid-moe", 0, 256, prompt=2048, cpu=not args.no_cpu)}),
-              flush=True)
+        chunks = tuple(int(c) for c in args.c5_chunks.split(","))
+        print(json.dumps({"c5": model_decode(args.c5_model, 0, 256, prompt=2048, cpu=not args.no_cpu,
+                                             chunks=chunks)}), flush=True)
         return
 
     tmpdir = None

@@ -83,11 +83,11 @@ void oi_engine_destroy(oi_engine *e);
  * consume `token` at `pos`, write K/V[pos], return vocab_size logits that
  * predict pos+1.  The pointer is engine-owned pinned host memory, valid until
  * the next call on this engine.  NULL on error (token/pos out of range:
- * the reference prints and exits, forward.odin:22-29; the Odin binding does
+ * the reference prints and exits, infer/forward.odin:22-29; the Odin binding does
  * the same). */
 const float *oi_engine_forward(oi_engine *e, int32_t token, int32_t pos);
 
-/* engine_forward_batch (qwen3_5/engine.odin:61-93 -> metal.odin:1472-1654
+/* engine_forward_batch (qwen3_5/engine.odin:61-93 -> qwen3_5/metal.odin:1472-1654
  * forward_gpu_batch): consume tokens[0..n) at positions pos0 .. pos0+n-1 and
  * return the logits of the last one (engine-owned pinned host memory, as
  * oi_engine_forward).  Chunks of up to 512 tokens, cut to a multiple of 8, run
@@ -97,7 +97,7 @@ const float *oi_engine_forward(oi_engine *e, int32_t token, int32_t pos);
  * trailing 1-7 tokens go through oi_engine_forward's path.  A model whose
  * projections the batched kernels cannot take (type other than Q4_K / Q6_K /
  * Q8_0, or a row length not a multiple of 256) runs every token through that
- * path, as the reference's non-Metal fallback (engine.odin:86-91).  NULL on
+ * path, as the reference's non-Metal fallback (qwen3_5/engine.odin:86-91).  NULL on
  * error: n <= 0, positions past seq_len, or a token out of range. */
 const float *oi_engine_prefill(oi_engine *e, const int32_t *tokens, int32_t n, int32_t pos0);
 
@@ -215,7 +215,7 @@ int oi_engine_reset_state(oi_engine *e);
 int oi_engine_save_kv(oi_engine *e, const char *path, int32_t n_valid_pos);
 
 /* engine_load_kv (qwen3_5/kv_persist.odin:374-381, metal_load_kv
- * metal.odin:864-962): check magic, version, arch, fingerprint, seq_len,
+ * qwen3_5/metal.odin:864-962): check magic, version, arch, fingerprint, seq_len,
  * n_valid_pos <= seq_len, the layer dims, the file size and the CRC -- all
  * before any state changes -- then zero the K/V cache, read the file's
  * positions (f32 -> f16, round to nearest even) and the DeltaNet states.
@@ -224,7 +224,7 @@ int oi_engine_save_kv(oi_engine *e, const char *path, int32_t n_valid_pos);
 int oi_engine_load_kv(oi_engine *e, const char *path, int32_t *n_valid_pos);
 
 /* engine_save_full_state / engine_restore_full_state (qwen3_5/engine.odin:
- * 139-151, metal.odin:1655-1676): byte copies of the device state in its own
+ * 139-151, qwen3_5/metal.odin:1655-1676): byte copies of the device state in its own
  * layout -- kv_k and kv_v f16 [n_attention_layers][n_kv_heads][seq_len]
  * [head_dim], conv f32 [n_linear][conv_dim][kernel-1], rec f32 [n_linear]
  * [n_v_heads][head_k_dim][head_v_dim].  The buffers are the caller's, in host
@@ -236,7 +236,7 @@ int oi_engine_restore_full_state(oi_engine *e, const void *kv_k, const void *kv_
                                  const void *rec);
 
 /* engine_save_spec_state / engine_restore_spec_state (qwen3_5/engine.odin:
- * 153-165, metal.odin:1678-1700): the conv and recurrent states alone, for a
+ * 153-165, qwen3_5/metal.odin:1678-1700): the conv and recurrent states alone, for a
  * speculative-decoding rollback. */
 int oi_engine_save_spec_state(oi_engine *e, void *conv, void *rec);
 int oi_engine_restore_spec_state(oi_engine *e, const void *conv, const void *rec);
@@ -328,10 +328,10 @@ typedef struct {
 
 /* One token of forward_linear_layer (qwen3_5/forward.odin:172-219) between the
  * input projections and the output projection: conv1d_step + silu over the
- * in_qkv projection (ops.odin:97-117), l2norm of q and k per k head with q
+ * in_qkv projection (qwen3_5/ops.odin:97-117), l2norm of q and k per k head with q
  * scaled by 1/sqrt(head_k_dim), beta = sigmoid(b), decay = exp(ssm_a *
  * softplus(a + dt_bias)) (ssm_a already -exp(A_log)), the gated delta rule on
- * each value head's state with k head vh % n_k_heads (ops.odin:120-153), and
+ * each value head's state with k head vh % n_k_heads (qwen3_5/ops.odin:120-153), and
  * the gated RMSNorm rmsnorm(o) * norm_w * silu(z).  Device pointers:
  * qkv [conv_dim], z [n_v_heads*head_v_dim], b and a [n_v_heads], conv_w
  * [conv_dim][conv_kernel], a_decay (ssm_a) and dt_bias [n_v_heads], norm_w
@@ -356,7 +356,7 @@ int oi_deltanet_steps(const oi_deltanet_dims *d, int32_t n_tokens, const float *
  * delta rule token by token in one launch (chunk 0) or in its chunked form
  * over chunks of 16 or 32 tokens (chunk 16 / 32; qwen3_5/metal.odin:416-468
  * chunked_delta, which the reference builds but does not dispatch,
- * metal.odin:1583-1586), the gated norm (metal.odin:1582-1618, the linear
+ * qwen3_5/metal.odin:1583-1586), the gated norm (qwen3_5/metal.odin:1582-1618, the linear
  * layer of forward_gpu_batch).  Host memory as oi_deltanet_steps; head dims
  * 128, conv kernel 4, n_tokens >= conv_kernel - 1. */
 int oi_deltanet_steps_batched(const oi_deltanet_dims *d, int32_t n_tokens, int32_t chunk, const float *qkv,
@@ -380,7 +380,7 @@ int64_t oi_qwen35_attn_workspace_bytes(const oi_qwen35_attn_dims *d);
  * token at `pos`, between the q/k/v projections and wo: per head q = the first
  * head_dim values of its [q | gate] slice of qproj, RMSNorm with q_norm; k
  * heads RMSNorm with k_norm; RoPE on the first rotary_dim dimensions only
- * (pairs i, i + rotary_dim/2; angle pos * inv_freq[i], ops.odin:77-89); k and v
+ * (pairs i, i + rotary_dim/2; angle pos * inv_freq[i], qwen3_5/ops.odin:77-89); k and v
  * stored as f16 in the cache [n_kv_heads][seq_len][head_dim] at pos; scores
  * q.k * (1/sqrt(head_dim)) over positions 0..pos, softmax, weighted sum of v;
  * out = that sum * sigmoid(gate).  head_dim 128 or 256.  Device pointers;
@@ -411,7 +411,7 @@ int64_t oi_moe_workspace_bytes(const oi_moe_dims *d);
 
 /* One token through a routed-expert SwiGLU FFN.  No counterpart in the
  * reference (its Qwen3.5 MLP is dense, qwen3_5/model.odin:80-82,
- * forward.odin:227-243); the convention is HF Qwen3-MoE's: logits = router x,
+ * qwen3_5/forward.odin:227-243); the convention is HF Qwen3-MoE's: logits = router x,
  * p = softmax over all experts, the top_k largest p (ties to the lower id),
  * weights p or p / sum (norm_topk_prob), y = sum_k w_k down_e(silu(gate_e x) *
  * up_e x).  router [n_experts][dim]; gate and up stacked [n_experts*inter][dim];

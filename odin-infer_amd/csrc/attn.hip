@@ -1,5 +1,5 @@
 // attn.hip -- split-L grouped-query decode attention over the f16 KV cache
-// (reference: infer/forward.odin:117-175; f16 cache as infer/metal.odin:443-474).
+// (reference: infer/forward.odin:87-115; f16 cache as infer/metal.odin:443-474).
 //
 // attn_kernel, grid (splits, n_kv_heads): a workgroup takes CH consecutive
 // positions of one KV head and serves all G = n_heads / n_kv_heads query
@@ -15,7 +15,7 @@
 //   3. stage K (rows padded against bank conflicts) and V in LDS,
 //   4. one wave per query head, with no workgroup barrier: scores with lane l
 //      taking position l (the whole dot product of its K row), divided by
-//      sqrt(hd) (forward.odin:158); split max / exp-sum by wave reductions;
+//      sqrt(hd) (infer/forward.odin:98); split max / exp-sum by wave reductions;
 //      o = sum_t p v_t with 2 dims per lane and p read from the wave's LDS row,
 //   5. write (o, m, l) to the partial buffer.
 // attn_combine_kernel merges the splits of each query head with
@@ -94,8 +94,8 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // 2. RMSNorm + RoPE of the G query heads (and of k at pos): ops.odin:7-19,
-    //    forward.odin:117-145; cos/sin come from the host-built table
+    // 2. RMSNorm + RoPE of the G query heads (and of k at pos): infer/ops.odin:7-19,
+    //    infer/forward.odin:57-85; cos/sin come from the host-built table
 #pragma unroll
     for (int i = 0; i < QPT; i++) {
         const int idx = tid + i * WG;
@@ -155,9 +155,9 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
 
     // 4-6. one wave per query head, no workgroup barrier: scores with lane =
     // position (each lane the whole dot product of its row), split max and
-    // exp-sum by wave reductions (ops.odin:21-37), p through this wave's LDS
+    // exp-sum by wave reductions (infer/ops.odin:21-37), p through this wave's LDS
     // row, o = sum_t p(t) v(t) with DPL dimensions per lane, then the split's
-    // (o, m, l).  Score = q.k / sqrt(hd) (forward.odin:158 divides).
+    // (o, m, l).  Score = q.k / sqrt(hd) (infer/forward.odin:98 divides).
     const float div = sqrtf((float)HD);
     const int stride = HD + 2;
     for (int g = wave; g < G; g += WG / WAVE) {
@@ -305,7 +305,7 @@ __global__ __launch_bounds__(WG) void attn_combine_kernel(AttnArgs a) {
 //      (so q keeps about 22 bits; K is exact f16, products exact, sums f32);
 //      the two columns are added (a DPP row shift), divided by sqrt(hd)
 //      (infer/forward.odin:98);
-//   4. the wave's softmax over its keys (max, exp, sum: ops.odin:21-37) and
+//   4. the wave's softmax over its keys (max, exp, sum: infer/ops.odin:21-37) and
 //      o = sum_t p_t v_t for its keys, 2 dimensions per lane, all heads;
 //   5. the waves' (o, m, l) merged through LDS with exp(m_w - M) weights
 //      into the split's (o, m, l), which attn_combine_kernel merges across
@@ -377,8 +377,8 @@ __global__ __launch_bounds__(A128_NT) void attn128_kernel(AttnArgs a) {
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // 2. RMSNorm + RoPE of the query heads and of k at pos (ops.odin:7-19,
-    //    forward.odin:57-85; cos/sin from the host-built table)
+    // 2. RMSNorm + RoPE of the query heads and of k at pos (infer/ops.odin:7-19,
+    //    infer/forward.odin:57-85; cos/sin from the host-built table)
     if (tid < NQ4) *(float4 *)&qr[tid / (HD / 4)][4 * (tid % (HD / 4))] = q4;
     if (tid < HD / 4) {
         *(float4 *)&kp[4 * tid] = k4;

@@ -1,13 +1,13 @@
 // deltanet.hip -- the gated DeltaNet (linear attention) token step of the
 // Qwen3.5 hybrid decoder, between its input projections (in_qkv, in_z, in_b,
 // in_a) and its output projection (reference: qwen3_5/forward.odin:137-225
-// forward_linear_layer; ops.odin:7-37 sigmoid / silu / softplus / l2norm,
-// ops.odin:97-161 conv1d_step and delta_recurrent_step).
+// forward_linear_layer; qwen3_5/ops.odin:7-37 sigmoid / silu / softplus / l2norm,
+// qwen3_5/ops.odin:97-161 conv1d_step and delta_recurrent_step).
 //
 // dn_conv_kernel: depthwise causal conv over the kernel window (current input
 //   last, history oldest first), silu, history slide; one thread per channel.
 // dn_delta_kernel: one workgroup per value head vh (k head vh % n_kh,
-//   forward.odin:193): l2-normalize q and k of the k head (q also scaled by
+//   qwen3_5/forward.odin:193): l2-normalize q and k of the k head (q also scaled by
 //   1/sqrt(head_k_dim)), beta = sigmoid(b), decay = exp(ssm_a * softplus(a +
 //   dt_bias)) (ssm_a already holds -exp(A_log)), then the delta rule on the
 //   head's state S [head_k_dim][head_v_dim] (k outer, v inner):
@@ -55,7 +55,7 @@ __global__ __launch_bounds__(1024) void dn_delta_kernel(DnArgs a) {
     const int vh = blockIdx.x, kh = vh % a.n_kh, t = threadIdx.x;
     const int lane = t & (WAVE - 1), wave = t / WAVE;
     const int key_dim = a.n_kh * HK;
-    // l2norm of q and k of the k head (ops.odin:27-37), eps 1e-6 a floor on the norm
+    // l2norm of q and k of the k head (qwen3_5/ops.odin:27-37), eps 1e-6 a floor on the norm
     const float *qr = a.conv_out + kh * HK, *kr = a.conv_out + key_dim + kh * HK;
     float sq = 0.f, sk = 0.f;
     if (t < HK) {
@@ -115,7 +115,7 @@ __global__ __launch_bounds__(1024) void dn_delta_kernel(DnArgs a) {
     }
     part[1][rg][j] = o;
     __syncthreads();
-    // gated RMSNorm over the head's outputs (forward.odin:211-218)
+    // gated RMSNorm over the head's outputs (qwen3_5/forward.odin:211-218)
     float oj = 0.f;
     if (rg == 0) {
 #pragma unroll
@@ -161,7 +161,7 @@ __global__ __launch_bounds__(1024) void dn_step_kernel(DnArgs a) {
     float s[R];
 #pragma unroll
     for (int r = 0; r < R; r++) s[r] = S[(size_t)(i0 + r) * HV + j];
-    // conv1d_step + silu of the workgroup's channels (ops.odin:97-116)
+    // conv1d_step + silu of the workgroup's channels (qwen3_5/ops.odin:97-116)
     if (t < 2 * HK + G * HV) {
         int c;
         if (t < HK) c = kh * HK + t;
@@ -180,7 +180,7 @@ __global__ __launch_bounds__(1024) void dn_step_kernel(DnArgs a) {
         else vv[(t - 2 * HK) / HV][(t - 2 * HK) % HV] = o;
     }
     __syncthreads();
-    // l2norm of q and k (ops.odin:27-37), the gates of the G heads
+    // l2norm of q and k (qwen3_5/ops.odin:27-37), the gates of the G heads
     float sq = 0.f, sk = 0.f;
     if (t < HK) {
         sq = qn[t] * qn[t];
@@ -215,7 +215,7 @@ __global__ __launch_bounds__(1024) void dn_step_kernel(DnArgs a) {
         kn[t] = kn[t] * ik;
     }
     __syncthreads();
-    // delta rule of head g on its state (forward.odin:193-209)
+    // delta rule of head g on its state (qwen3_5/forward.odin:193-209)
     const float beta = sc[2 + g], decay = sc[2 + G + g];
     float kv = 0.f;
 #pragma unroll
@@ -238,7 +238,7 @@ __global__ __launch_bounds__(1024) void dn_step_kernel(DnArgs a) {
     }
     part[1][g][rg][j] = o;
     __syncthreads();
-    // gated RMSNorm over each head's outputs (forward.odin:211-218)
+    // gated RMSNorm over each head's outputs (qwen3_5/forward.odin:211-218)
     float oj = 0.f;
     if (rg == 0) {
 #pragma unroll
@@ -294,7 +294,7 @@ __global__ __launch_bounds__(WG) void dn_cols_kernel(DnArgs a) {
     const float v = a.conv_out[2 * KD + vh * HV + j];
     const float beta = sigmoid_ref(a.b[vh]);
     const float decay = expf(a.a_decay[vh] * softplus_ref(a.a[vh] + a.dt_bias[vh]));
-    // l2norm of q and k (ops.odin:27-37), eps 1e-6 a floor on the norm
+    // l2norm of q and k (qwen3_5/ops.odin:27-37), eps 1e-6 a floor on the norm
     float sq = 0.f, sk = 0.f;
 #pragma unroll
     for (int r = 0; r < RPL; r++) {
@@ -313,7 +313,7 @@ __global__ __launch_bounds__(WG) void dn_cols_kernel(DnArgs a) {
         qn[r] = qn[r] * iq * (1.0f / sqrtf((float)HK));
         kn[r] = kn[r] * ik;
     }
-    // delta rule (forward.odin:193-209)
+    // delta rule (qwen3_5/forward.odin:193-209)
     float kv = 0.f;
 #pragma unroll
     for (int r = 0; r < RPL; r++) {
@@ -334,7 +334,7 @@ __global__ __launch_bounds__(WG) void dn_cols_kernel(DnArgs a) {
     o += OI_DPP(o, 0xB1);
     o += OI_DPP(o, 0x4E);
     o += dpp_mirror8(o);
-    // for the gated norm (forward.odin:211-218) in the output GEMV's prologue:
+    // for the gated norm (qwen3_5/forward.odin:211-218) in the output GEMV's prologue:
     // o silu(z) per column, and this workgroup's part of the head's sum of o^2
     __shared__ float wss[WG / WAVE];
     const float ss = wave_sum(rg == 0 ? o * o : 0.f);

@@ -96,7 +96,7 @@ static __device__ __forceinline__ float sigmoid_ref(float x) {
     return z / (1.0f + z);
 }
 static __device__ __forceinline__ float silu_ref(float x) { return x * sigmoid_ref(x); }
-// ops.odin:21-25 (the logarithm in double precision, as the reference)
+// qwen3_5/ops.odin:20-24 (the logarithm in double precision, as the reference)
 static __device__ __forceinline__ float softplus_ref(float x) {
     if (x > 20.0f) return x;
     if (x < -20.0f) return 0.0f;

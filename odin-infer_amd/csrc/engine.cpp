@@ -435,8 +435,8 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     };
     const GgufTensor *emb;
     if ((rc = require("token_embd.weight", emb))) return rc;
-    c.vocab_size = (int64_t)emb->dims.back();  // model.odin:137-138
-    c.seq_len = std::min<int64_t>(c.max_seq, opts->max_ctx);  // model.odin:220-223
+    c.vocab_size = (int64_t)emb->dims.back();  // infer/model.odin:137-138
+    c.seq_len = std::min<int64_t>(c.max_seq, opts->max_ctx);  // infer/model.odin:220-223
     if (c.seq_len <= 0) c.seq_len = opts->max_ctx;
 
     if (c.dim <= 0 || c.dim % 256 || c.dim > 15360 || c.hidden_dim <= 0 || c.hidden_dim % 256 ||
@@ -475,7 +475,7 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     const int64_t KD = e->lin_nk * e->lin_hk, VD = e->lin_nv * e->lin_hv, CD = 2 * KD + VD;
     want.push_back({"token_embd.weight", c.vocab_size, D, false, nullptr});
     want.push_back({"output_norm.weight", 1, D, true, nullptr});
-    const bool tied = g.tensor("output.weight") == nullptr;  // model.odin:149-158
+    const bool tied = g.tensor("output.weight") == nullptr;  // infer/model.odin:149-158
     if (!tied) want.push_back({"output.weight", c.vocab_size, D, false, nullptr});
     std::vector<int> kinds((size_t)c.n_layers);
     std::vector<char> shared((size_t)c.n_layers, 0);
@@ -1068,7 +1068,7 @@ const float *oi_engine_forward(oi_engine *e, int32_t token, int32_t pos) {
         fail(OI_E_ARG, "null engine");
         return nullptr;
     }
-    // forward.odin:82-89
+    // infer/forward.odin:22-29
     if (pos < 0 || pos >= e->cfg.seq_len) {
         fail(OI_E_RANGE, "forward: pos=" + std::to_string(pos) + " out of range (seq_len=" +
                              std::to_string(e->cfg.seq_len) + ")");
@@ -1095,7 +1095,7 @@ const float *oi_engine_forward(oi_engine *e, int32_t token, int32_t pos) {
 
 // ------------------------------------------------------ batched prefill --
 // Max tokens per batched chunk and the chunking rule of the reference
-// (qwen3_5/metal.odin:22 MAX_BATCH_T; engine.odin:66-93: chunks of a multiple
+// (qwen3_5/metal.odin:22 MAX_BATCH_T; qwen3_5/engine.odin:66-93: chunks of a multiple
 // of 8 tokens, the trailing 1-7 tokens one at a time).
 constexpr int PF_MAX_T = 512;
 
@@ -1441,8 +1441,8 @@ int prefill_chunk(oi_engine *e, const int32_t *tokens, int T, int pos, float *ro
         else
             HIP_TRY(launch_pf_add(e->pf_x, P[0], s0, (int64_t)T * D, st));
     }
-    // the final norm and classifier (metal.odin:1637-1641 for the last token;
-    // metal_verify_batch_logits, metal.odin:1707-1747, for every token): the
+    // the final norm and classifier (qwen3_5/metal.odin:1637-1641 for the last token;
+    // metal_verify_batch_logits, qwen3_5/metal.odin:1707-1747, for every token): the
     // decode path's f32 GEMV with the RMSNorm prologue, one row at a time
     for (int t = rows ? 0 : T - 1; t < T; t++) {
         GemvArgs a = gemv_args(GEMV_STORE, D, e->pf_x + (size_t)t * D, e->output_norm, eps);

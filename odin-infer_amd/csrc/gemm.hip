@@ -272,7 +272,7 @@ struct GQ80 {
 // NP == 2 (gate and up of the FFN, one K slice): both matrices' rows are
 // computed against the same staged activations, each B operand read from LDS
 // feeding both products, and the epilogue writes the f16 SwiGLU of the pair
-// (infer/forward.odin:188-193: v *= 1/(1+exp(-v)); v *= up; then the half
+// (infer/forward.odin:128-132: v *= 1/(1+exp(-v)); v *= up; then the half
 // staging of the next projection's input).
 template <class G, int NP = 1>
 __global__ __launch_bounds__(GM_THREADS) void gemm_q_kernel(GemmArgs a, int cps) {

@@ -1,7 +1,7 @@
 // gemv.hip -- quantized GEMV for Q4_K, Q6_K and Q8_0 weights on gfx950
 // (reference: infer/matmul.odin:77-109 over ggml/quant.odin:76-282), with the
 // token loop's fusions: RMSNorm prologue (infer/ops.odin:7-19), residual add,
-// SwiGLU (infer/forward.odin:185-193) and greedy-argmax partials
+// SwiGLU (infer/forward.odin:128-132) and greedy-argmax partials
 // (sampler/sampler.odin:79-89).
 //
 // Layout of the work:
@@ -230,7 +230,7 @@ static __device__ __forceinline__ void quant4(float4 v, int c, uint32_t *hw, uin
 // behind the other waves') take fewer tiles and the CU finishes together.
 constexpr int GW = 1024, GNW = GW / WAVE;
 
-// x -> (optional RMSNorm, ops.odin:7-19) -> 22-bit integers in LDS, in two
+// x -> (optional RMSNorm, infer/ops.odin:7-19) -> 22-bit integers in LDS, in two
 // phases so that the x loads are issued before the weight prefetch (vector
 // loads return in order: x must not queue behind the weights).  XR float4 of
 // x (and of the norm weight) per thread are held in registers; XR == 0 means
@@ -483,7 +483,7 @@ static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int 
                 for (int r = 0; r < R; r++) {
                     const int row = (tb + t) * rpt + rsub + r;
                     float val = acc[0][r];
-                    if (NM == 2) {  // infer/forward.odin:188-193
+                    if (NM == 2) {  // infer/forward.odin:128-132
 #pragma clang fp contract(off)
                         val *= 1.0f / (1.0f + expf(-val));
                         val *= acc[NM - 1][r];
@@ -527,7 +527,7 @@ static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int 
         const float gs = NM == 1 && a.mode == GEMV_ADD && a.ygate ? 1.0f / (1.0f + expf(-a.ygate[0])) : 1.f;
         if (NORM == XN_RMS_CONV && seg == 0) {
             // conv epilogue: row c is a channel of the DeltaNet conv
-            // (ops.odin:97-116, as dn_conv_kernel): silu of the window with the
+            // (qwen3_5/ops.odin:97-116, as dn_conv_kernel): silu of the window with the
             // product last, then the window slides (2 <= kernel <= 4)
             const int KS = a.conv_kernel, km1 = KS - 1;
             for (int i = tid; i < wrow1 - wrow0; i += GW) {
@@ -1206,7 +1206,7 @@ __global__ __launch_bounds__(WG) void mt_dot4_kernel(MtGemvArgs a) {
             const int c = tid + i * WG;  // K / 4 float4, groups of 8 threads
             if (c >= K / 4) break;
             float4 v = xv[pj][i];
-            if (a.x2) {  // SwiGLU (infer/forward.odin:188-193)
+            if (a.x2) {  // SwiGLU (infer/forward.odin:128-132)
 #pragma clang fp contract(off)
                 const float4 u = uv[pj][i];
                 v.x *= 1.0f / (1.0f + expf(-v.x));
@@ -1367,7 +1367,7 @@ __global__ __launch_bounds__(NWV * WAVE) void mt_q4i8_kernel(MtGemvArgs a) {
 #pragma unroll
         for (int i = 0; i < XI; i++) {
             float4 v = xv[pj][i];
-            if (a.x2) {  // SwiGLU (infer/forward.odin:188-193)
+            if (a.x2) {  // SwiGLU (infer/forward.odin:128-132)
 #pragma clang fp contract(off)
                 const float4 u = uv[pj][i];
                 v.x *= 1.0f / (1.0f + expf(-v.x));

@@ -5,7 +5,7 @@
 //                  float arithmetic, with the same fused prologue/epilogues as
 //                  gemv_q_kernel (gemv.hip), used where that one does not apply
 //                  (reference: infer/matmul.odin:77-109, ggml/quant.odin:76-282)
-//   embed_kernel   token embedding row (forward.odin:72-75), preceded by the
+//   embed_kernel   token embedding row (infer/forward.odin:12-15, 43), preceded by the
 //                  reduction of the previous step's argmax partials
 //                  (sampler/sampler.odin:79-89)
 //   dequant_kernel bit-exact dequant of a matrix (test hook)
@@ -169,7 +169,7 @@ __global__ __launch_bounds__(WG) void dequant_kernel(DMat m, float *out) {
 
 // ------------------------------------------------------------- embedding --
 // x[t] = dequant(token_embd[tokens[t]]) for the tokens of a prefill batch
-// (forward_gpu_batch's get_embedding_row per token, metal.odin:1499-1501).
+// (forward_gpu_batch's get_embedding_row per token, qwen3_5/metal.odin:1499-1501).
 // Grid (ceil(units / WG), n): one unit of 64 weights per thread.
 __global__ __launch_bounds__(WG) void embed_rows_kernel(DMat emb, const int32_t *tokens, float *x) {
     const int units = emb.cols / 64, u = (int)blockIdx.x * WG + threadIdx.x, t = blockIdx.y;
@@ -307,7 +307,7 @@ __global__ __launch_bounds__(WG) void gemv_kernel(GemvArgs a) {
     float4 *x4 = smem;
     float *s16 = (float *)(smem + K / 4);
 
-    // ---- prologue: x (optionally RMS-normalised, ops.odin:7-19) into LDS
+    // ---- prologue: x (optionally RMS-normalised, infer/ops.odin:7-19) into LDS
     const float4 *gx = (const float4 *)a.x;
     float s = 1.f;
     if (a.norm_w) {
@@ -390,7 +390,7 @@ __global__ __launch_bounds__(WG) void gemv_kernel(GemvArgs a) {
             if (row >= S.m.rows) continue;
             if (a.mode == GEMV_ADD) {
                 S.y[row] += a.ygate ? acc[r] * (1.0f / (1.0f + expf(-a.ygate[0]))) : acc[r];
-            } else if (a.mode == GEMV_SWIGLU) {  // infer/forward.odin:188-193
+            } else if (a.mode == GEMV_SWIGLU) {  // infer/forward.odin:128-132
                 float val = acc[r];
                 val *= 1.0f / (1.0f + expf(-val));
                 val *= acc2[r];
@@ -477,7 +477,7 @@ hipError_t launch_embed(const DMat &emb, int32_t *state, float *x, int32_t vocab
 // ------------------------------------------------------------------- MoE --
 // Router top-k and the selected experts' SwiGLU FFN for one token, with the
 // expert ids chosen on the device.  The reference has no MoE code
-// (qwen3_5/model.odin:80-82 and forward.odin:227-243 are dense); the
+// (qwen3_5/model.odin:80-82 and qwen3_5/forward.odin:227-243 are dense); the
 // convention is HF Qwen3-MoE's: softmax over all router logits, the top k
 // (ties to the lower id), optionally renormalized to sum 1; expert e:
 // down_e(silu(gate_e x) * up_e x); output sum_k w_k y_k.  Expert matrices are
@@ -670,7 +670,7 @@ __device__ __forceinline__ float dot_unit_x(const float *w, int type, int u, con
 // units, at most 64) take one row each and split its units; each unit is
 // decoded once (decode_unit, exact) for all the pass's pairs.
 // y[p][r] = row r . x  or, for a SwiGLU pair of matrices,
-// silu(gate_r . x) * (up_r . x) (forward.odin:128-133).
+// silu(gate_r . x) * (up_r . x) (infer/forward.odin:128-132).
 __global__ __launch_bounds__(WG) void mt_gemv_kernel(MtGemvArgs a, int cmax) {
 #pragma clang fp contract(off)
     extern __shared__ float4 smem[];
@@ -1164,7 +1164,7 @@ __global__ __launch_bounds__(WG) void mt_q4mfma_few_kernel(MtGemvArgs a) {
         const float4 *xr = (const float4 *)(a.x + xo);
         const float4 p0 = xr[0], p1 = xr[1];
         float v[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-        if (a.x2) {  // SwiGLU: v = silu(gate) * up (infer/forward.odin:188-193)
+        if (a.x2) {  // SwiGLU: v = silu(gate) * up (infer/forward.odin:128-132)
             const float4 *ur = (const float4 *)(a.x2 + xo);
             const float4 u0 = ur[0], u1 = ur[1];
             const float u[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};

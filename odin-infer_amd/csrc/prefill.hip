@@ -35,7 +35,7 @@ static __device__ __forceinline__ float block_sum(float v, float *red) {
 // x[t] += (sum of the K-slice partial products) when part is set, then
 // out[t] = f16 of x[t]'s RMSNorm with w: w[i] * (s * x[i]), s = 1 / sqrt(sum
 // x^2 / dim + eps) (ops.odin rmsnorm; the reference converts the f32 result
-// to half for the projection, metal.odin:1236-1242).  The residual add of one
+// to half for the projection, qwen3_5/metal.odin:1236-1242).  The residual add of one
 // sublayer fused with the next sublayer's norm; x read once, kept in
 // registers.
 // Grid: T; dim <= WG * PF_NPT.
@@ -98,7 +98,7 @@ __global__ __launch_bounds__(WG) void pf_addnorm16_kernel(float *x, const float 
 
 // Per token and head (grid (T, ceil(heads / 4)), one wave per head; q, k
 // and v heads in that order): q and k heads RMSNorm'd with
-// q_norm / k_norm and rotated at pos0 + t (forward.odin:57-85, pairs i and
+// q_norm / k_norm and rotated at pos0 + t (infer/forward.odin:57-85, pairs i and
 // i + hd/2); k and v rounded to f16 into the cache at pos0 + t; q kept in f32.
 // Lane l holds dimensions l + 64 e, so the RoPE pair of e is e + DPL/2.
 template <int HD>
@@ -161,7 +161,7 @@ static __device__ __forceinline__ float pf_gated(const PfAttnArgs &a, float o, s
 }
 
 // Causal attention of token t (query head h, grid (n_heads, T)) over positions
-// 0 .. pos0 + t of the f16 cache (forward.odin:87-115: scores q.k / sqrt(hd),
+// 0 .. pos0 + t of the f16 cache (infer/forward.odin:87-115: scores q.k / sqrt(hd),
 // softmax, weighted sum of v).  Each wave takes blocks of 64 positions (lane =
 // position) with a running max and sum; the four waves' (m, l, o) are merged
 // at the end.  Lane l accumulates dimensions DPL l .. DPL l + DPL-1.
@@ -256,7 +256,7 @@ __global__ __launch_bounds__(WG) void pf_attn_kernel(PfAttnArgs a) {
 // of a 32-key chunk; V^T is read with the same map.  Precision: q and p are
 // split into f16 hi + lo halves (two products each), K and V are exact f16,
 // accumulation is f32, so scores and weights keep about 22 bits, close to the
-// reference's f32 arithmetic (forward.odin:87-115).
+// reference's f32 arithmetic (infer/forward.odin:87-115).
 constexpr int FA_VP = 68;  // LDS row stride (halves) of V^T; K rows: HD + 8
 
 static __device__ __forceinline__ void split16(const float (&v)[8], h8 &hi, h8 &lo) {
@@ -436,14 +436,14 @@ __global__ __launch_bounds__(HD) void pf_fattn_merge_kernel(PfAttnArgs a, int T,
 }
 
 // x[i] += sum of the partial products of element i (the residual adds,
-// forward.odin:117-119, 137-139)
+// infer/forward.odin:119-121, 137-139)
 __global__ __launch_bounds__(WG) void pf_add_kernel(float *x, const float *part, int split, int64_t total) {
     const int64_t i = (int64_t)blockIdx.x * WG + threadIdx.x;
     if (i < total) x[i] += parts_at(part, split, (size_t)total, (size_t)i);
 }
 
 // out[i] = f16(silu(g[i]) * u[i]) from the gate and up projections' partial
-// products (forward.odin:128-133, separately rounded as the reference)
+// products (infer/forward.odin:128-132, separately rounded as the reference)
 __global__ __launch_bounds__(WG) void pf_swiglu16_kernel(const float *g, int gs, const float *u, int us, int64_t total,
                                                          uint16_t *out) {
 #pragma clang fp contract(off)

@@ -19,7 +19,7 @@
 //                           softplus(a + dt_bias)) and its log
 //   pf_dn_delta_kernel      the delta rule over the chunk's tokens in order,
 //                           the state held in registers for the whole chunk
-//   pf_dn_chunk_kernel      the same in its chunked form (metal.odin:416-468,
+//   pf_dn_chunk_kernel      the same in its chunked form (qwen3_5/metal.odin:416-468,
 //                           which the reference does not dispatch): 16 or 32
 //                           tokens per step, decay ratios from log sums
 //   pf_dn_gnorm_kernel      gated RMSNorm, f16 rows for the output projection
@@ -35,9 +35,9 @@ namespace oi {
 
 // Per token and head (grid (T, ceil(heads / 4)), one wave per head; q, k and
 // v heads in that order).  The q projection holds [q | gate] per head
-// (forward.odin:53-60); gate goes out unchanged.  q and k heads: RMSNorm with
+// (qwen3_5/forward.odin:74-82); gate goes out unchanged.  q and k heads: RMSNorm with
 // q_norm / k_norm, then RoPE on the first rotary_dim dimensions (pairs i and
-// i + rotary_dim / 2, angle pos * inv_freq[i] in f32, ops.odin:77-89), as
+// i + rotary_dim / 2, angle pos * inv_freq[i] in f32, qwen3_5/ops.odin:77-89), as
 // qwen35_attn.hip does for one token.  Lane l holds dimensions l + 64 e.
 template <int HD>
 __global__ __launch_bounds__(WG) void pf_q35_qkv_kernel(PfQ35Args a) {
@@ -107,7 +107,7 @@ __global__ __launch_bounds__(WG) void pf_q35_qkv_kernel(PfQ35Args a) {
 
 constexpr int DN_TT = 8;  // tokens per thread of the conv
 
-// conv1d_step + silu (ops.odin:97-116) of channel c for tokens [8 y, 8 y +
+// conv1d_step + silu (qwen3_5/ops.odin:97-116) of channel c for tokens [8 y, 8 y +
 // 8): out = silu(w[KS-1] in(t) + sum_k w[k] in(t - (KS-1) + k)), the order
 // of the decode step, where in(tau) is the in_qkv projection of token tau of
 // the chunk or, before the chunk (tau in [-(KS-1), 0)), the conv state's
@@ -158,9 +158,9 @@ __global__ __launch_bounds__(WG) void pf_dn_conv_state_kernel(PfDnArgs a) {
     for (int k = 0; k < KM1; k++) a.conv_state[(size_t)c * KM1 + k] = x[k];
 }
 
-// Per token (grid T): l2norm of each k head's q and k (ops.odin:27-37, eps
+// Per token (grid T): l2norm of each k head's q and k (qwen3_5/ops.odin:27-37, eps
 // 1e-6 a floor on the norm; q also times 1/sqrt(head_k_dim),
-// forward.odin:187-192) into qk [T][2 key_dim] (q heads, then k heads); the
+// qwen3_5/forward.odin:177-188) into qk [T][2 key_dim] (q heads, then k heads); the
 // gates of every value head into gates [T][3 n_vh] (beta, decay, log decay).
 template <int HK>
 __global__ __launch_bounds__(WG) void pf_dn_prep_kernel(PfDnArgs a) {
@@ -198,7 +198,7 @@ __global__ __launch_bounds__(WG) void pf_dn_prep_kernel(PfDnArgs a) {
     }
 }
 
-// The delta rule (forward.odin:193-209) over the chunk's tokens in order:
+// The delta rule (qwen3_5/forward.odin:193-209) over the chunk's tokens in order:
 //   S *= decay;  delta = (v - S^T k) beta;  S += k delta^T;  o = S^T q.
 // Grid (n_vh, hv / 16): a workgroup owns 16 state columns of value head vh
 // (k head vh % n_kh); each wave 4 columns, lane = 16 column + row group, a
@@ -422,7 +422,7 @@ __global__ __launch_bounds__(WG) void pf_dn_chunk_kernel(PfDnArgs a) {
     for (int r = 0; r < RPL; r++) S[(size_t)(i0 + r) * HV + j] = s[r];
 }
 
-// gated RMSNorm (forward.odin:211-218): per token and value head, out =
+// gated RMSNorm (qwen3_5/forward.odin:211-218): per token and value head, out =
 // f16(norm_w[j] (inv o[j]) silu(z[j])), inv = 1 / sqrt(sum o^2 / hv + eps); z
 // from the in_z projection's partial products.  Grid (T, ceil(n_vh / (4
 // GN_NH))): each wave takes GN_NH heads, their o and z requested together.

@@ -1,7 +1,7 @@
 // qwen35_attn.hip -- the attention of a Qwen3.5 full-attention layer for one
 // token, between its projections and its output projection (reference:
-// qwen3_5/forward.odin:46-135 forward_full_layer; ops.odin:77-89
-// apply_mrope_text_head, ops.odin:163-168 inv_freq_default).  What differs from
+// qwen3_5/forward.odin:46-135 forward_full_layer; qwen3_5/ops.odin:77-89
+// apply_mrope_text_head, qwen3_5/ops.odin:163-168 inv_freq_default).  What differs from
 // the Qwen3 decoder: the q projection holds [q | gate] per head, RoPE rotates
 // only the first rotary_dim dimensions (pairs i and i + rotary_dim/2, angles
 // pos * inv_freq[i] computed in f32), scores are dot * (1/sqrt(head_dim)), and
@@ -61,7 +61,7 @@ __global__ __launch_bounds__(WG) void q35_attn_kernel(Q35Args a) {
         vr[j] = ldg_nt((const u32x4 *)(vc + (size_t)row * HD + 8 * c));
     }
     // this workgroup's q heads, and in the split that holds pos the new k and
-    // v: RMSNorm (ops.odin rmsnorm) and partial RoPE (ops.odin:77-89); the
+    // v: RMSNorm (ops.odin rmsnorm) and partial RoPE (qwen3_5/ops.odin:77-89); the
     // new k / v go to the cache and to the LDS tile row pos - t0
     const bool has_pos = pos < t0 + Q35_CH;
     for (int i = tid; i < GW * HD; i += WG) qs[i / HD][i % HD] = a.qproj[(size_t)(h0 + i / HD) * 2 * HD + i % HD];

@@ -6,9 +6,9 @@
 
 Same names, argument meaning and error behaviour as the reference: the
 returned logits alias engine-owned memory valid until the next call
-(forward.odin:145); an out-of-range token or pos is fatal in the reference
-(forward.odin:22-29) and raises OIError(OI_E_RANGE) here.  The reference's
-silent CPU fallback when the GPU is missing (engine.odin:23-31) is not
+(infer/forward.odin:145); an out-of-range token or pos is fatal in the reference
+(infer/forward.odin:22-29) and raises OIError(OI_E_RANGE) here.  The reference's
+silent CPU fallback when the GPU is missing (infer/engine.odin:23-31) is not
 reproduced: engine_load raises instead.
 """
 import ctypes

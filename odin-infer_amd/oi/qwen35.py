@@ -1,6 +1,6 @@
 """Qwen3.5 hybrid-decoder pieces on the device: the gated DeltaNet token step
 of a linear-attention layer (qwen3_5/forward.odin:137-225) and the attention
-of a full-attention layer (forward.odin:46-135)."""
+of a full-attention layer (qwen3_5/forward.odin:46-135)."""
 import ctypes
 
 import numpy as np
@@ -31,7 +31,7 @@ def engine_config(e):
 
 
 def engine_batch_max():
-    """qwen3_5/engine.odin:96-102: tokens per batched chunk (metal.odin:22)."""
+    """qwen3_5/engine.odin:96-102: tokens per batched chunk (qwen3_5/metal.odin:22)."""
     return int(_native.hip().oi_engine_batch_max())
 
 

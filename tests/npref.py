@@ -347,8 +347,8 @@ def delta_chunk_f64(state, q, k, v, beta, g, mistake=None):
 
 def qwen35_attn_f64(n_heads, n_kv, hd, rotary_dim, seq_len, eps, pos0, qproj, k, v, q_norm, k_norm, theta,
                     kc16, vc16, full_rotary=False, gate=True):
-    """Float64 restatement of forward_full_layer's attention (qwen3_5/
-    forward.odin:69-127) over tokens from pos0 with an f16 cache (k/v rounded
+    """Float64 restatement of forward_full_layer's attention
+    (qwen3_5/forward.odin:69-127) over tokens from pos0 with an f16 cache (k/v rounded
     on store).  full_rotary / gate=False give the variants a mistake would
     produce (RoPE over the whole head, no output gate)."""
     f = lambda x: np.array(x, np.float64)

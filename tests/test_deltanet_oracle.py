@@ -1,5 +1,5 @@
 """The oracle's gated DeltaNet step (refcpu.c, restating qwen3_5/ops.odin and
-forward.odin:172-219) pinned by the reference's own known answers
+qwen3_5/forward.odin:172-219) pinned by the reference's own known answers
 (qwen3_5/tests.odin:13-95, 141-150) and by an independent float64 model of
 the whole step; the float64 model with the mistake of the reference's
 delta_harness golden (memory read with q, delta_ref.odin:61) must fail the

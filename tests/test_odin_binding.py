@@ -31,7 +31,7 @@ engine_save_full_state, engine_restore_full_state; :1525-1548 engine_load
 with Engine_Opts{max_ctx, use_metal, num_threads}, engine_destroy,
 destroy_matmul_pool, engine_config, metal_ready.  Plus the package's own
 public procedures (qwen3_5/engine.odin:7-174, kv_persist.odin:365-381,
-matmul.odin:28-61).
+infer/matmul.odin:28-61).
 """
 import os
 import re

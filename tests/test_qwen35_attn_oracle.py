@@ -1,5 +1,5 @@
 """The oracle's Qwen3.5 full-attention step (refcpu.c, restating
-qwen3_5/forward.odin:69-127 and ops.odin:77-89, 163-168) pinned by the
+qwen3_5/forward.odin:69-127 and qwen3_5/ops.odin:77-89, 163-168) pinned by the
 reference's RoPE known answers (qwen3_5/tests.odin:97-125), the inv_freq
 closed form, and an independent float64 model of the step; the float64
 variants with RoPE over the whole head or without the output gate must fail
