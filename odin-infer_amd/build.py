@@ -42,7 +42,7 @@ def build(verbose=False):
         objs.append(obj)
         jobs.append([HIPCC, "--offload-arch=" + ARCH, *COMMON, *DEVICE_FLAGS, "-x", "hip", "-c",
                      os.path.join(CSRC, src), "-o", obj])
-    for src in ["engine.cpp", "gguf.cpp", "state.cpp"]:
+    for src in ["engine.cpp", "gguf.cpp", "oikv.cpp", "state.cpp"]:
         obj = os.path.join(BUILD, src + ".o")
         objs.append(obj)
         jobs.append([HIPCC, *COMMON, "-D__HIP_PLATFORM_AMD__", "-c", os.path.join(CSRC, src), "-o", obj])

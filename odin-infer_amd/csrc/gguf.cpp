@@ -197,9 +197,27 @@ int GgufFile::open(const std::string &path, std::string &err) {
             err = "tensor " + t.name + " has unknown type " + std::to_string(t.kind);
             return OI_E_FORMAT;
         }
-        t.nbytes = t.nelems() / (uint64_t)e * (uint64_t)b;
+        // the element count must not wrap and the row must hold whole blocks
+        uint64_t n = 1;
+        for (uint64_t d : t.dims)
+            if (d != 0 && n > UINT64_MAX / d) {
+                err = "tensor " + t.name + " has an element count beyond 2^64";
+                return OI_E_FORMAT;
+            } else {
+                n *= d;
+            }
+        if (t.dims[0] % (uint64_t)e != 0) {
+            err = "tensor " + t.name + " has rows of " + std::to_string(t.dims[0]) + " elements, not a multiple of " +
+                  std::to_string(e);
+            return OI_E_FORMAT;
+        }
+        if (n / (uint64_t)e > UINT64_MAX / (uint64_t)b || t.offset > len_ || base > len_ - t.offset) {
+            err = "tensor " + t.name + " extends past the end of the file";
+            return OI_E_FORMAT;
+        }
+        t.nbytes = n / (uint64_t)e * (uint64_t)b;
         const uint64_t start = base + t.offset;
-        if (start > len_ || t.nbytes > len_ - start) {
+        if (t.nbytes > len_ - start) {
             err = "tensor " + t.name + " extends past the end of the file";
             return OI_E_FORMAT;
         }

@@ -1,7 +1,7 @@
 // state.cpp -- persistence of the engine's position-evolving state: the
 // .oikv v1 file (reference: qwen3_5/kv_persist.odin:1-381 and the Metal
 // conversion qwen3_5/metal.odin:780-962) and in-memory snapshots
-// (qwen3_5/engine.odin:139-165, metal.odin:1655-1700).
+// (qwen3_5/engine.odin:139-165, qwen3_5/metal.odin:1655-1700).
 //
 // The state lives in HBM: per attention layer an f16 head-major cache
 // [n_kv][seq_len][hd] for K and for V, per DeltaNet layer its conv window
@@ -22,6 +22,7 @@
 #include <vector>
 
 #include "engine_internal.h"
+#include "oikv.h"
 
 using namespace oi;
 
@@ -35,85 +36,6 @@ int fail(int code, const std::string &msg) { return set_error(code, msg.c_str())
         if (e_ != hipSuccess)                                                             \
             return fail(OI_E_DEVICE, std::string(#expr) + ": " + hipGetErrorString(e_)); \
     } while (0)
-
-constexpr uint32_t KV_MAGIC = 0x4F494B56u;  // 'O','I','K','V' little-endian
-constexpr uint32_t KV_VERSION = 1;
-constexpr size_t HEADER_BYTES = 60;  // the fields as written by write_header (kv_persist.odin:141-156)
-
-// IEEE 802.3 CRC-32 (reflected polynomial 0xEDB88320, initial and final
-// complement), the checksum of core:hash crc32 over header + body.
-struct Crc32 {
-    uint32_t table[256];
-    uint32_t v = 0xFFFFFFFFu;
-    Crc32() {
-        for (uint32_t i = 0; i < 256; i++) {
-            uint32_t c = i;
-            for (int k = 0; k < 8; k++) c = (c & 1) ? 0xEDB88320u ^ (c >> 1) : c >> 1;
-            table[i] = c;
-        }
-    }
-    void add(const void *p, size_t n) {
-        const uint8_t *b = (const uint8_t *)p;
-        for (size_t i = 0; i < n; i++) v = table[(v ^ b[i]) & 0xFF] ^ (v >> 8);
-    }
-    uint32_t value() const { return v ^ 0xFFFFFFFFu; }
-};
-
-// Header fields in file order (kv_persist.odin:55-70, 95-113).
-struct Header {
-    uint32_t magic, version, arch;
-    uint64_t fingerprint;
-    uint32_t n_valid_pos, seq_len, n_full, n_linear, kv_dim, conv_dim, conv_kernel, n_v_heads, head_k_dim,
-        head_v_dim;
-};
-
-void put_u32(uint8_t *&p, uint32_t v) {
-    for (int i = 0; i < 4; i++) *p++ = (uint8_t)(v >> (8 * i));
-}
-void put_u64(uint8_t *&p, uint64_t v) {
-    for (int i = 0; i < 8; i++) *p++ = (uint8_t)(v >> (8 * i));
-}
-uint32_t get_u32(const uint8_t *&p) {
-    uint32_t v = 0;
-    for (int i = 0; i < 4; i++) v |= (uint32_t)*p++ << (8 * i);
-    return v;
-}
-uint64_t get_u64(const uint8_t *&p) {
-    uint64_t v = 0;
-    for (int i = 0; i < 8; i++) v |= (uint64_t)*p++ << (8 * i);
-    return v;
-}
-
-void encode(const Header &h, uint8_t out[HEADER_BYTES]) {
-    uint8_t *p = out;
-    put_u32(p, h.magic);
-    put_u32(p, h.version);
-    put_u32(p, h.arch);
-    put_u64(p, h.fingerprint);
-    for (uint32_t v : {h.n_valid_pos, h.seq_len, h.n_full, h.n_linear, h.kv_dim, h.conv_dim, h.conv_kernel,
-                       h.n_v_heads, h.head_k_dim, h.head_v_dim})
-        put_u32(p, v);
-}
-
-Header decode(const uint8_t in[HEADER_BYTES]) {
-    const uint8_t *p = in;
-    Header h{};
-    h.magic = get_u32(p);
-    h.version = get_u32(p);
-    h.arch = get_u32(p);
-    h.fingerprint = get_u64(p);
-    h.n_valid_pos = get_u32(p);
-    h.seq_len = get_u32(p);
-    h.n_full = get_u32(p);
-    h.n_linear = get_u32(p);
-    h.kv_dim = get_u32(p);
-    h.conv_dim = get_u32(p);
-    h.conv_kernel = get_u32(p);
-    h.n_v_heads = get_u32(p);
-    h.head_k_dim = get_u32(p);
-    h.head_v_dim = get_u32(p);
-    return h;
-}
 
 // What the engine holds, in the header's terms.
 struct Shape {
@@ -151,10 +73,10 @@ uint64_t fingerprint(const oi_engine *e) {
 // arch field: the reference's KV_ARCH_QWEN3_5 = 2 for the hybrid layout
 uint32_t arch_code(const oi_engine *e) { return e->arch == 2 ? 2u : e->arch == 1 ? 3u : 1u; }
 
-Header header_of(const oi_engine *e, const Shape &s, uint32_t n_valid) {
-    Header h{};
-    h.magic = KV_MAGIC;
-    h.version = KV_VERSION;
+OikvHeader header_of(const oi_engine *e, const Shape &s, uint32_t n_valid) {
+    OikvHeader h{};
+    h.magic = OIKV_MAGIC;
+    h.version = OIKV_VERSION;
     h.arch = arch_code(e);
     h.fingerprint = fingerprint(e);
     h.n_valid_pos = n_valid;
@@ -168,14 +90,6 @@ Header header_of(const oi_engine *e, const Shape &s, uint32_t n_valid) {
     h.head_k_dim = (uint32_t)e->lin_hk;
     h.head_v_dim = (uint32_t)e->lin_hv;
     return h;
-}
-
-// body bytes after the header (kv_bytes / conv_bytes / rec_bytes, kv_persist.odin:116-128)
-uint64_t body_bytes(const Header &h) {
-    const uint64_t kv = 2ull * h.n_full * h.n_valid_pos * h.kv_dim * 4;
-    const uint64_t conv = h.conv_kernel == 0 ? 0 : (uint64_t)h.n_linear * h.conv_dim * (h.conv_kernel - 1) * 4;
-    const uint64_t rec = (uint64_t)h.n_linear * h.n_v_heads * h.head_k_dim * h.head_v_dim * 4;
-    return kv + conv + rec;
 }
 
 struct FileCloser {
@@ -212,7 +126,7 @@ int oi_engine_save_kv(oi_engine *e, const char *path, int32_t n_valid_pos) {
                                     std::to_string(c.seq_len));
     HIP_TRY(hipSetDevice(e->device));
     const Shape s = shape_of(e);
-    const Header h = header_of(e, s, (uint32_t)n_valid_pos);
+    const OikvHeader h = header_of(e, s, (uint32_t)n_valid_pos);
     File f(std::fopen(path, "wb"));
     if (!f) return fail(OI_E_IO, std::string("kv: cannot open ") + path + " for write");
     Crc32 crc;
@@ -220,8 +134,8 @@ int oi_engine_save_kv(oi_engine *e, const char *path, int32_t n_valid_pos) {
         crc.add(p, n);
         return std::fwrite(p, 1, n, f.get()) == n;
     };
-    uint8_t hb[HEADER_BYTES];
-    encode(h, hb);
+    uint8_t hb[OIKV_HEADER_BYTES];
+    oikv_encode(h, hb);
     if (!put(hb, sizeof hb)) return fail(OI_E_IO, "kv: header write failed");
 
     const size_t rows = (size_t)n_valid_pos * s.kv_dim * 4;
@@ -252,7 +166,7 @@ int oi_engine_save_kv(oi_engine *e, const char *path, int32_t n_valid_pos) {
                 return fail(OI_E_IO, part == 0 ? "kv: conv_states write failed" : "kv: recurrent_states write failed");
         }
     uint8_t cb[4], *p = cb;
-    put_u32(p, crc.value());
+    oikv_put_u32(p, crc.value());
     if (std::fwrite(cb, 1, 4, f.get()) != 4 || std::fflush(f.get()) != 0)
         return fail(OI_E_IO, "kv: crc append failed");
     if (std::fclose(f.release()) != 0) return fail(OI_E_IO, "kv: close failed");
@@ -265,78 +179,28 @@ int oi_engine_load_kv(oi_engine *e, const char *path, int32_t *n_valid_pos) {
     HIP_TRY(hipSetDevice(e->device));
     File f(std::fopen(path, "rb"));
     if (!f) return fail(OI_E_IO, std::string("kv: cannot open ") + path);
-    uint8_t hb[HEADER_BYTES];
+    uint8_t hb[OIKV_HEADER_BYTES];
     if (std::fread(hb, 1, sizeof hb, f.get()) != sizeof hb) return fail(OI_E_FORMAT, "kv: header truncated");
-    const Header h = decode(hb);
+    const OikvHeader h = oikv_decode(hb);
     const Shape s = shape_of(e);
-    const Header mine = header_of(e, s, 0);
-    char msg[160];
-    // the reference's checks, in its order (kv_persist.odin:278-305)
-    if (h.magic != KV_MAGIC) {
-        std::snprintf(msg, sizeof msg, "kv: bad magic 0x%08x", h.magic);
-        return fail(OI_E_FORMAT, msg);
-    }
-    if (h.version != KV_VERSION) {
-        std::snprintf(msg, sizeof msg, "kv: version mismatch (file=%u, supported=%u)", h.version, KV_VERSION);
-        return fail(OI_E_FORMAT, msg);
-    }
-    if (h.arch != mine.arch) {
-        std::snprintf(msg, sizeof msg, "kv: arch mismatch (file=%u, expected %u)", h.arch, mine.arch);
-        return fail(OI_E_FORMAT, msg);
-    }
-    if (h.fingerprint != mine.fingerprint) {
-        std::snprintf(msg, sizeof msg, "kv: fingerprint mismatch (file=0x%016llx, model=0x%016llx) — wrong model?",
-                      (unsigned long long)h.fingerprint, (unsigned long long)mine.fingerprint);
-        return fail(OI_E_FORMAT, msg);
-    }
-    if (h.seq_len != mine.seq_len) {
-        std::snprintf(msg, sizeof msg, "kv: seq_len mismatch (file=%u, engine=%u) — use same -c", h.seq_len,
-                      mine.seq_len);
-        return fail(OI_E_FORMAT, msg);
-    }
-    if (h.n_valid_pos > mine.seq_len) {
-        std::snprintf(msg, sizeof msg, "kv: file n_valid_pos %u > engine seq_len %u", h.n_valid_pos, mine.seq_len);
-        return fail(OI_E_FORMAT, msg);
-    }
-    // layer dims (the fingerprint implies them; a file that disagrees is corrupt)
-    if (h.n_full != mine.n_full || h.n_linear != mine.n_linear || h.kv_dim != mine.kv_dim ||
-        h.conv_dim != mine.conv_dim || h.conv_kernel != mine.conv_kernel || h.n_v_heads != mine.n_v_heads ||
-        h.head_k_dim != mine.head_k_dim || h.head_v_dim != mine.head_v_dim)
-        return fail(OI_E_FORMAT, "kv: layer dimensions differ from the engine's");
-    const uint64_t body = body_bytes(h);
     if (std::fseek(f.get(), 0, SEEK_END) != 0) return fail(OI_E_IO, "kv: seek failed");
     const long size = std::ftell(f.get());
-    if (size < 0 || (uint64_t)size != HEADER_BYTES + body + 4) {
-        std::snprintf(msg, sizeof msg, "kv: file is %ld bytes, the header implies %llu", size,
-                      (unsigned long long)(HEADER_BYTES + body + 4));
-        return fail(OI_E_FORMAT, msg);
-    }
-    // CRC over header + body before any state changes (kv_persist.odin:307-310)
-    {
-        Crc32 crc;
-        std::vector<uint8_t> buf(8u << 20);
-        std::rewind(f.get());
-        uint64_t left = HEADER_BYTES + body;
-        while (left) {
-            const size_t n = (size_t)std::min<uint64_t>(left, buf.size());
-            if (std::fread(buf.data(), 1, n, f.get()) != n) return fail(OI_E_IO, "kv: read failed");
-            crc.add(buf.data(), n);
-            left -= n;
-        }
-        uint8_t cb[4];
-        if (std::fread(cb, 1, 4, f.get()) != 4) return fail(OI_E_IO, "kv: read failed");
-        const uint8_t *p = cb;
-        if (get_u32(p) != crc.value()) return fail(OI_E_FORMAT, "kv: CRC mismatch — file corrupted");
-    }
-    if (std::fseek(f.get(), (long)HEADER_BYTES, SEEK_SET) != 0) return fail(OI_E_IO, "kv: seek failed");
+    if (size < 0) return fail(OI_E_IO, "kv: tell failed");
+    std::string msg;
+    // the reference's checks, in its order, then the size and the CRC over
+    // header + body before any state changes (kv_persist.odin:278-310)
+    int rc = oikv_check_header(h, header_of(e, s, 0), (uint64_t)size, msg);
+    if (rc == OI_OK) rc = oikv_verify_crc(f.get(), OIKV_HEADER_BYTES + oikv_body_bytes(h), msg);
+    if (rc != OI_OK) return fail(rc, msg);
+    if (std::fseek(f.get(), (long)OIKV_HEADER_BYTES, SEEK_SET) != 0) return fail(OI_E_IO, "kv: seek failed");
 
     const int n = (int)h.n_valid_pos;
     const size_t rows = (size_t)n * s.kv_dim * 4;
     const size_t conv_b = (size_t)(s.conv_dim * s.km1) * 4, rec_b = (size_t)s.rec_floats * 4;
     Staging st;
-    int rc = st.alloc(std::max(rows, std::max(conv_b, rec_b)));
+    rc = st.alloc(std::max(rows, std::max(conv_b, rec_b)));
     if (rc) return rc;
-    // everything past n_valid_pos is stale: zero the caches first (metal.odin:912-916)
+    // everything past n_valid_pos is stale: zero the caches first (qwen3_5/metal.odin:912-916)
     for (const LayerDev *L : s.attn) {
         HIP_TRY(hipMemsetAsync(L->kc, 0, s.kv_layer_bytes, e->stream));
         HIP_TRY(hipMemsetAsync(L->vc, 0, s.kv_layer_bytes, e->stream));

@@ -593,8 +593,8 @@ typedef struct {
 
 typedef struct { const uint8_t *d; size_t len, pos; int bad; } rdr;
 
-static int need(rdr *r, size_t n) {
-    if (r->bad || r->pos + n > r->len) { r->bad = 1; return 0; }
+static int need(rdr *r, uint64_t n) {
+    if (r->bad || n > r->len - r->pos) { r->bad = 1; return 0; } /* no wrap: pos <= len always */
     return 1;
 }
 static uint64_t rd_le(rdr *r, int n) {
@@ -608,7 +608,7 @@ static const char *rd_str(rdr *r, uint64_t *len) {
     uint64_t l = rd_le(r, 8);
     if (!need(r, l)) return NULL;
     const char *s = (const char *)r->d + r->pos;
-    r->pos += l;
+    r->pos += (size_t)l;
     *len = l;
     return s;
 }
@@ -643,7 +643,11 @@ static int gfile_open(const char *path, gfile *g) { /* gguf.odin:167-229 */
     int fd = open(path, O_RDONLY);
     if (fd < 0) { snprintf(g_err, sizeof g_err, "mmap failed for %s: %s", path, strerror(errno)); return -1; }
     struct stat st;
-    fstat(fd, &st);
+    if (fstat(fd, &st) != 0 || st.st_size < 24) {
+        close(fd);
+        snprintf(g_err, sizeof g_err, "not a GGUF file (too short): %s", path);
+        return -1;
+    }
     g->map_len = (size_t)st.st_size;
     g->map = (uint8_t *)mmap(NULL, g->map_len, PROT_READ, MAP_PRIVATE, fd, 0);
     close(fd);
@@ -661,7 +665,7 @@ static int gfile_open(const char *path, gfile *g) { /* gguf.odin:167-229 */
         uint64_t kl;
         const char *k = rd_str(&r, &kl);
         if (!k) break;
-        snprintf(m->key, sizeof m->key, "%.*s", (int)kl, k);
+        snprintf(m->key, sizeof m->key, "%.*s", (int)(kl < sizeof m->key ? kl : sizeof m->key - 1), k);
         m->type = (int)rd_le(&r, 4);
         switch (m->type) { /* gguf.odin:135-161 */
         case G_U8: case G_I8: case G_BOOL: m->u = rd_le(&r, 1); break;
@@ -686,7 +690,7 @@ static int gfile_open(const char *path, gfile *g) { /* gguf.odin:167-229 */
         uint64_t nl;
         const char *nm = rd_str(&r, &nl);
         if (!nm) break;
-        snprintf(t->name, sizeof t->name, "%.*s", (int)nl, nm);
+        snprintf(t->name, sizeof t->name, "%.*s", (int)(nl < sizeof t->name ? nl : sizeof t->name - 1), nm);
         t->n_dims = (int)rd_le(&r, 4);
         if (t->n_dims < 1 || t->n_dims > 4) { r.bad = 1; break; }
         for (int d = 0; d < t->n_dims; d++) t->dims[d] = rd_le(&r, 8);
@@ -701,15 +705,25 @@ static int gfile_open(const char *path, gfile *g) { /* gguf.odin:167-229 */
     uint64_t data_base = (r.pos + alignment - 1) & ~(alignment - 1);
     for (int i = 0; i < g->n_tensors; i++) {
         gtensor *t = &g->tensors[i];
+        /* element counts, sizes and offsets checked for wrap-around before use */
         uint64_t ne = 1;
-        for (int d = 0; d < t->n_dims; d++) ne *= t->dims[d];
+        int e, b;
+        ref_block_info(t->kind, &e, &b);
+        for (int d = 0; d < t->n_dims; d++) {
+            if (t->dims[d] && ne > (uint64_t)INT64_MAX / t->dims[d]) ne = UINT64_MAX;
+            else ne *= t->dims[d];
+        }
+        if (ne == UINT64_MAX || ne / (uint64_t)e > (uint64_t)INT64_MAX / (uint64_t)b) {
+            snprintf(g_err, sizeof g_err, "tensor %s: element count overflows", t->name);
+            return -7;
+        }
         t->size = (uint64_t)ref_row_byte_size(t->kind, (int64_t)ne);
-        uint64_t start = data_base + t->offset;
-        if (start + t->size > g->map_len) {
+        if (t->offset > g->map_len || data_base > g->map_len - t->offset ||
+            t->size > g->map_len - (data_base + t->offset)) {
             snprintf(g_err, sizeof g_err, "tensor %s extends past end of file", t->name);
             return -7;
         }
-        t->data = g->map + start;
+        t->data = g->map + data_base + t->offset;
     }
     return 0;
 }
@@ -795,7 +809,7 @@ EXPORT int ref_qwen35_attn_steps(int n_heads, int n_kv, int hd, int rotary_dim, 
                                  int pos0, const float *qproj, const float *k, const float *v, const float *q_norm,
                                  const float *k_norm, const float *inv_freq, uint16_t *kc, uint16_t *vc, float *out);
 
-static int require(ref_engine *e, const char *name, gtensor **out) { /* model.odin:82-97 */
+static int require(ref_engine *e, const char *name, gtensor **out) { /* infer/model.odin:82-97 */
     gtensor *t = gtensor_get(&e->g, name);
     if (!t) { snprintf(g_err, sizeof g_err, "missing required tensor: %s", name); return -10; }
     if (!ref_is_supported_quant(t->kind)) {
@@ -806,13 +820,28 @@ static int require(ref_engine *e, const char *name, gtensor **out) { /* model.od
     return 0;
 }
 
-static int as_f32(ref_engine *e, const char *name, const float **out) { /* model.odin:74-80 */
+static int as_f32(ref_engine *e, const char *name, const float **out) { /* infer/model.odin:74-80 */
     gtensor *t;
     int rc = require(e, name, &t);
     if (rc) return rc;
     if (t->kind != T_F32) { snprintf(g_err, sizeof g_err, "expected F32 tensor for %s", name); return -12; }
     *out = (const float *)t->data;
     return 0;
+}
+
+/* Shape checks the reference leaves to Odin's bounds-checked slices: a
+ * weight's rows hold `cols` elements and it has `rows` of them (3-D expert
+ * stacks count every expert's rows), so the forward pass never reads past a
+ * tensor.  Not a reference step; malformed files fail here instead. */
+static int shape_ok(ref_engine *e, const gtensor *t, int64_t cols, int64_t rows) {
+    uint64_t ne = 1;
+    for (int d = 0; d < t->n_dims; d++) ne *= t->dims[d]; /* bounded by the reader's overflow check */
+    if (t->dims[0] != (uint64_t)cols || ne != (uint64_t)cols * (uint64_t)rows) {
+        snprintf(g_err, sizeof g_err, "tensor %s: shape does not match the model's dimensions", t->name);
+        (void)e;
+        return 0;
+    }
+    return 1;
 }
 
 EXPORT void ref_engine_destroy(void *h) {
@@ -838,7 +867,7 @@ EXPORT void ref_engine_destroy(void *h) {
     free(e);
 }
 
-/* engine_load (infer/engine.odin:18-34) -> build_transformer (model.odin:216-242).
+/* engine_load (infer/engine.odin:18-34) -> build_transformer (infer/model.odin:216-242).
  * kv_f16 != 0 selects the f16 KV mode: K and V at each position are rounded to
  * binary16 (round-to-nearest-even) when stored, as the reference GPU path's
  * store_kv does (infer/metal.odin:443-454), and attention reads them back. */
@@ -895,15 +924,44 @@ EXPORT void *ref_engine_load(const char *path, int max_ctx, int num_threads, int
     snprintf(key, sizeof key, "%s.attention.layer_norm_rms_epsilon", arch);
     m = gmeta_get(g, key);
     e->rms_eps = m ? (float)m->f : 1e-6f;
+    /* dimensions in range before anything is sized by them (not a reference
+     * step: the reference trusts the file) */
+    {
+        const int64_t lim = 1 << 20;
+        int ok = e->dim > 0 && e->dim <= lim && e->hidden_dim > 0 && e->hidden_dim <= lim && e->n_layers > 0 &&
+                 e->n_layers <= 4096 && e->n_heads > 0 && e->n_heads <= 4096 && e->n_kv_heads > 0 &&
+                 e->n_heads % e->n_kv_heads == 0 && e->head_dim > 0 && e->head_dim <= 4096 && max_ctx > 0;
+        if (e->n_experts > 0 || e->arch == 1)
+            ok = ok && e->n_experts > 0 && e->n_experts <= 4096 && e->top_k > 0 && e->top_k <= e->n_experts &&
+                 e->expert_ffn > 0 && e->expert_ffn <= lim && e->shared_ffn >= 0 && e->shared_ffn <= lim;
+        if (e->arch == 2)
+            ok = ok && e->lin_nk > 0 && e->lin_nk <= 4096 && e->lin_nv > 0 && e->lin_nv <= 4096 && e->lin_hk > 0 &&
+                 e->lin_hk <= 4096 && e->lin_hv > 0 && e->lin_hv <= 4096 && e->lin_kernel > 0 && e->lin_kernel <= 64 &&
+                 e->full_interval > 0 && e->rotary_dim >= 0 && e->rotary_dim <= e->head_dim && e->rotary_dim % 2 == 0;
+        if (!ok) {
+            snprintf(g_err, sizeof g_err, "model dimensions out of range");
+            ref_engine_destroy(e);
+            return NULL;
+        }
+    }
     gtensor *emb;
     if (require(e, "token_embd.weight", &emb)) { ref_engine_destroy(e); return NULL; }
     e->vocab_size = (int64_t)emb->dims[emb->n_dims - 1];
-    /* model.odin:220-223 */
+    if (e->vocab_size <= 0 || e->vocab_size > (1 << 24) || !shape_ok(e, emb, e->dim, e->vocab_size)) {
+        if (e->vocab_size <= 0 || e->vocab_size > (1 << 24))
+            snprintf(g_err, sizeof g_err, "vocabulary size out of range");
+        ref_engine_destroy(e);
+        return NULL;
+    }
+    /* infer/model.odin:220-223 */
     e->seq_len = e->max_seq < max_ctx ? e->max_seq : max_ctx;
     if (e->seq_len <= 0) e->seq_len = max_ctx;
-    /* memory_map_weights, model.odin:141-179 */
+    /* memory_map_weights, infer/model.odin:141-179 */
     e->token_embedding = (tensor){emb->kind, emb->data};
-    if (as_f32(e, "output_norm.weight", &e->output_norm)) { ref_engine_destroy(e); return NULL; }
+    if (as_f32(e, "output_norm.weight", &e->output_norm) || !shape_ok(e, gtensor_get(g, "output_norm.weight"), e->dim, 1)) {
+        ref_engine_destroy(e);
+        return NULL;
+    }
     gtensor *out = gtensor_get(g, "output.weight");
     if (out) {
         if (!ref_is_supported_quant(out->kind)) {
@@ -911,59 +969,68 @@ EXPORT void *ref_engine_load(const char *path, int max_ctx, int num_threads, int
             ref_engine_destroy(e);
             return NULL;
         }
+        if (!shape_ok(e, out, e->dim, e->vocab_size)) { ref_engine_destroy(e); return NULL; }
         e->output = (tensor){out->kind, out->data};
     } else {
         e->output = e->token_embedding; /* tied classifier */
     }
     e->layers = (layer_w *)calloc((size_t)e->n_layers, sizeof(layer_w));
+    if (!e->layers) { snprintf(g_err, sizeof g_err, "out of memory"); ref_engine_destroy(e); return NULL; }
     char nm[96];
     const int64_t conv_dim = 2 * e->lin_nk * e->lin_hk + e->lin_nv * e->lin_hv;
+    const int64_t D = e->dim, QD = e->n_heads * e->head_dim, KVD = e->n_kv_heads * e->head_dim;
+    const int64_t VD = e->lin_nv * e->lin_hv, HD = e->head_dim;
     for (int64_t l = 0; l < e->n_layers; l++) {
         layer_w *lw = &e->layers[l];
         int bad = 0;
-#define F32W(field, suffix) snprintf(nm, sizeof nm, "blk.%lld." suffix, (long long)l); bad |= as_f32(e, nm, &lw->field);
-#define QW(field, suffix) { gtensor *t_; snprintf(nm, sizeof nm, "blk.%lld." suffix, (long long)l); \
-        if (require(e, nm, &t_)) bad = 1; else lw->field = (tensor){t_->kind, t_->data}; }
-        F32W(attn_norm, "attn_norm.weight")
-        if (e->arch == 2) { F32W(ffn_norm, "post_attention_norm.weight") } /* qwen3_5/model.odin:325 */
-        else { F32W(ffn_norm, "ffn_norm.weight") }
+#define F32W(field, suffix, n) { snprintf(nm, sizeof nm, "blk.%lld." suffix, (long long)l); \
+        if (as_f32(e, nm, &lw->field) || !shape_ok(e, gtensor_get(g, nm), n, 1)) bad = 1; }
+#define QW(field, suffix, cols, rows) { gtensor *t_; snprintf(nm, sizeof nm, "blk.%lld." suffix, (long long)l); \
+        if (require(e, nm, &t_) || !shape_ok(e, t_, cols, rows)) bad = 1; else lw->field = (tensor){t_->kind, t_->data}; }
+        F32W(attn_norm, "attn_norm.weight", D)
+        if (e->arch == 2) { F32W(ffn_norm, "post_attention_norm.weight", D) } /* qwen3_5/model.odin:325 */
+        else { F32W(ffn_norm, "ffn_norm.weight", D) }
         lw->kind = e->arch != 2 ? 0 : ((l + 1) % e->full_interval == 0 ? 1 : 2); /* qwen3_5/model.odin:289-300 */
         if (lw->kind != 2) {
-            F32W(q_norm, "attn_q_norm.weight")
-            F32W(k_norm, "attn_k_norm.weight")
-            QW(wq, "attn_q.weight")
-            QW(wk, "attn_k.weight")
-            QW(wv, "attn_v.weight")
-            QW(wo, "attn_output.weight")
+            F32W(q_norm, "attn_q_norm.weight", HD)
+            F32W(k_norm, "attn_k_norm.weight", HD)
+            QW(wq, "attn_q.weight", D, lw->kind == 1 ? 2 * QD : QD)
+            QW(wk, "attn_k.weight", D, KVD)
+            QW(wv, "attn_v.weight", D, KVD)
+            QW(wo, "attn_output.weight", QD, D)
         } else {
-            QW(in_qkv, "attn_qkv.weight")
-            QW(in_z, "attn_gate.weight")
-            QW(in_b, "ssm_beta.weight")
-            QW(in_a, "ssm_alpha.weight")
-            F32W(conv_w, "ssm_conv1d.weight")
-            F32W(dt_bias, "ssm_dt.bias")
-            F32W(ssm_a, "ssm_a")
-            F32W(ssm_norm, "ssm_norm.weight")
-            QW(ssm_out, "ssm_out.weight")
+            QW(in_qkv, "attn_qkv.weight", D, conv_dim)
+            QW(in_z, "attn_gate.weight", D, VD)
+            QW(in_b, "ssm_beta.weight", D, e->lin_nv)
+            QW(in_a, "ssm_alpha.weight", D, e->lin_nv)
+            { /* [conv_dim][kernel] F32 */
+                snprintf(nm, sizeof nm, "blk.%lld.ssm_conv1d.weight", (long long)l);
+                if (as_f32(e, nm, &lw->conv_w) || !shape_ok(e, gtensor_get(g, nm), e->lin_kernel, conv_dim)) bad = 1;
+            }
+            F32W(dt_bias, "ssm_dt.bias", e->lin_nv)
+            F32W(ssm_a, "ssm_a", e->lin_nv)
+            F32W(ssm_norm, "ssm_norm.weight", e->lin_hv)
+            QW(ssm_out, "ssm_out.weight", VD, D)
         }
         if (e->n_experts > 0) {
             lw->moe = 1;
-            QW(router, "ffn_gate_inp.weight")
-            QW(gexp, "ffn_gate_exps.weight")
-            QW(uexp, "ffn_up_exps.weight")
-            QW(dexp, "ffn_down_exps.weight")
+            QW(router, "ffn_gate_inp.weight", D, e->n_experts)
+            QW(gexp, "ffn_gate_exps.weight", D, e->n_experts * e->expert_ffn)
+            QW(uexp, "ffn_up_exps.weight", D, e->n_experts * e->expert_ffn)
+            QW(dexp, "ffn_down_exps.weight", e->expert_ffn, e->n_experts * D)
             snprintf(nm, sizeof nm, "blk.%lld.ffn_gate_inp_shexp.weight", (long long)l);
             if (gtensor_get(g, nm)) {
                 lw->shared = 1;
-                QW(sh_inp, "ffn_gate_inp_shexp.weight")
-                QW(sh_gate, "ffn_gate_shexp.weight")
-                QW(sh_up, "ffn_up_shexp.weight")
-                QW(sh_down, "ffn_down_shexp.weight")
+                if (e->shared_ffn <= 0) bad = 1;
+                QW(sh_inp, "ffn_gate_inp_shexp.weight", D, 1)
+                QW(sh_gate, "ffn_gate_shexp.weight", D, e->shared_ffn)
+                QW(sh_up, "ffn_up_shexp.weight", D, e->shared_ffn)
+                QW(sh_down, "ffn_down_shexp.weight", e->shared_ffn, D)
             }
         } else {
-            QW(w1, "ffn_gate.weight")
-            QW(w2, "ffn_down.weight")
-            QW(w3, "ffn_up.weight")
+            QW(w1, "ffn_gate.weight", D, e->hidden_dim)
+            QW(w2, "ffn_down.weight", e->hidden_dim, D)
+            QW(w3, "ffn_up.weight", D, e->hidden_dim)
         }
 #undef F32W
 #undef QW
@@ -995,7 +1062,7 @@ EXPORT void *ref_engine_load(const char *path, int max_ctx, int num_threads, int
         e->mo_y = (float *)calloc((size_t)e->dim, 4);
         e->mo_t = (float *)calloc((size_t)e->dim, 4);
     }
-    /* malloc_run_state, model.odin:185-200 */
+    /* malloc_run_state, infer/model.odin:185-200 */
     int64_t att_head_dim = e->n_heads * e->head_dim, kv_dim = e->n_kv_heads * e->head_dim;
     e->x = (float *)calloc((size_t)e->dim, 4);
     e->xb = (float *)calloc((size_t)e->dim, 4);
@@ -1011,8 +1078,22 @@ EXPORT void *ref_engine_load(const char *path, int max_ctx, int num_threads, int
     e->ktmp = (float *)calloc((size_t)kv_dim, 4);
     e->vtmp = (float *)calloc((size_t)kv_dim, 4);
     if (!e->key_cache || !e->value_cache) { snprintf(g_err, sizeof g_err, "KV cache allocation failed"); ref_engine_destroy(e); return NULL; }
+    {
+        int missing = !e->x || !e->xb || !e->xb2 || !e->xb3 || !e->hb || !e->hb2 || !e->q || !e->att || !e->logits ||
+                      !e->ktmp || !e->vtmp;
+        if (e->arch == 2)
+            missing |= !e->inv_freq || !e->hy_qproj || !e->hy_k || !e->hy_v || !e->hy_qkv || !e->hy_z || !e->hy_b ||
+                       !e->hy_a || !e->hy_out;
+        if (e->n_experts > 0) missing |= !e->mo_p || !e->mo_h || !e->mo_y || !e->mo_t;
+        for (int64_t l = 0; l < e->n_layers; l++) {
+            const layer_w *lw = &e->layers[l];
+            if (lw->kind == 2) missing |= !lw->conv_state || !lw->rec_state;
+            if (lw->kind == 1) missing |= !lw->kc16 || !lw->vc16;
+        }
+        if (missing) { snprintf(g_err, sizeof g_err, "out of memory"); ref_engine_destroy(e); return NULL; }
+    }
     e->kv_f16 = kv_f16;
-    e->pool = pool_create(num_threads < 1 ? 1 : num_threads); /* engine.odin:20 */
+    e->pool = pool_create(num_threads < 1 ? 1 : num_threads); /* infer/engine.odin:20 */
     return e;
 }
 
@@ -1092,7 +1173,7 @@ static int matmul_staged(ref_engine *e, float *xout, const float *x, int kind, c
 /* forward (infer/forward.odin:17-146); with `staged` the seven projections of
  * each layer are the batched path's (matmul_staged), and without `logits` the
  * final norm and classifier are skipped (forward_gpu_batch computes them for
- * the last token only, metal.odin:1637-1641). */
+ * the last token only, qwen3_5/metal.odin:1637-1641). */
 /* Routed-expert SwiGLU FFN of one token (x already normalized) into y, rows on
  * the row pool: the arithmetic of ref_moe_ffn (each row dequantized and dotted
  * with dot_f32; softmax; top_k by a strict '>' scan, ties to the lower id;
@@ -1216,7 +1297,7 @@ static const float *forward_impl(ref_engine *e, int token, int pos, int staged, 
     float eps = e->rms_eps;
     mm_pool *P = e->pool;
 
-    /* get_embedding_row, forward.odin:12-15 */
+    /* get_embedding_row, infer/forward.odin:12-15 */
     int64_t rb = ref_row_byte_size(e->token_embedding.kind, dim);
     ref_dequant_row(e->token_embedding.kind, e->token_embedding.data + (int64_t)token * rb, dim, e->x);
 
@@ -1243,7 +1324,7 @@ static const float *forward_impl(ref_engine *e, int token, int pos, int staged, 
         MM(kk, e->xb, lw->wk, dim, kv_dim);
         MM(vv, e->xb, lw->wv, dim, kv_dim);
 
-        /* RoPE + per-head Q/K RMSNorm, forward.odin:57-85 */
+        /* RoPE + per-head Q/K RMSNorm, infer/forward.odin:57-85 */
         for (int64_t h = 0; h < n_heads; h++) {
             float *q = e->q + h * head_dim;
             ref_rmsnorm(q, q, lw->q_norm, head_dim, eps);
@@ -1273,7 +1354,7 @@ static const float *forward_impl(ref_engine *e, int token, int pos, int staged, 
             }
         }
 
-        /* multihead attention, forward.odin:87-115 */
+        /* multihead attention, infer/forward.odin:87-115 */
         for (int64_t h = 0; h < n_heads; h++) {
             float *q = e->q + h * head_dim;
             float *att = e->att + h * seq_len;
@@ -1316,7 +1397,7 @@ static const float *forward_impl(ref_engine *e, int token, int pos, int staged, 
         }
         MM(e->hb, e->xb, lw->w1, dim, hidden_dim);
         MM(e->hb2, e->xb, lw->w3, dim, hidden_dim);
-        for (int64_t i = 0; i < hidden_dim; i++) { /* forward.odin:128-133 */
+        for (int64_t i = 0; i < hidden_dim; i++) { /* infer/forward.odin:128-132 */
             float val = e->hb[i];
             val *= 1.0f / (1.0f + expf(-val));
             val *= e->hb2[i];
@@ -1340,11 +1421,11 @@ EXPORT const float *ref_engine_forward(void *h, int token, int pos) {
 }
 
 /* engine_forward_batch (qwen3_5/engine.odin:61-93): chunks of up to
- * MAX_BATCH_T = 512 tokens (metal.odin:22), cut to a multiple of 8, through
+ * MAX_BATCH_T = 512 tokens (qwen3_5/metal.odin:22), cut to a multiple of 8, through
  * the batched path (staged projections, logits of the chunk's last token);
  * the trailing 1-7 tokens one at a time through forward.  In the batched path
  * of every layout the attention / DeltaNet projections and a dense MLP are
- * staged (forward_gpu_batch, metal.odin:1510-1634); the routed-expert FFN,
+ * staged (forward_gpu_batch, qwen3_5/metal.odin:1510-1634); the routed-expert FFN,
  * which the reference does not have, stays in f32 (router, experts and
  * shared expert as the per-token path).  Returns the last token's logits, or
  * NULL. */
@@ -1785,7 +1866,7 @@ EXPORT int ref_gemm_f16(int kind, const uint8_t *w, int64_t m, int64_t k, const 
 
 /* ---------------------------------------------- Qwen3.5 gated DeltaNet --- */
 
-/* ops.odin:7-15 */
+/* qwen3_5/ops.odin:7-14 */
 static float ref_sigmoid(float x) {
     if (x >= 0.0f) {
         float z = expf(-x);
@@ -1795,13 +1876,13 @@ static float ref_sigmoid(float x) {
     return z / (1.0f + z);
 }
 static float ref_silu(float x) { return x * ref_sigmoid(x); }
-/* ops.odin:21-25 */
+/* qwen3_5/ops.odin:20-24 */
 static float ref_softplus(float x) {
     if (x > 20.0f) return x;
     if (x < -20.0f) return 0.0f;
     return (float)log((double)(1.0f + expf(x)));
 }
-/* ops.odin:27-37: eps is a floor on the norm */
+/* qwen3_5/ops.odin:26-37: eps is a floor on the norm */
 static void ref_l2norm(float *o, const float *x, int64_t n, float eps) {
     float ss = 0.0f;
     for (int64_t i = 0; i < n; i++) ss += x[i] * x[i];
@@ -1809,7 +1890,7 @@ static void ref_l2norm(float *o, const float *x, int64_t n, float eps) {
     float inv = 1.0f / (nrm > eps ? nrm : eps);
     for (int64_t i = 0; i < n; i++) o[i] = x[i] * inv;
 }
-/* ops.odin:97-117 */
+/* qwen3_5/ops.odin:97-117 */
 static void ref_conv1d_step(float *out, const float *in, float *state, const float *w, int64_t conv_dim, int kernel) {
     int km1 = kernel - 1;
     for (int64_t c = 0; c < conv_dim; c++) {
@@ -1822,7 +1903,7 @@ static void ref_conv1d_step(float *out, const float *in, float *state, const flo
         if (km1 > 0) sb[km1 - 1] = in[c];
     }
 }
-/* ops.odin:120-153 */
+/* qwen3_5/ops.odin:120-153 */
 EXPORT void ref_delta_step(float *out, float *state, const float *q, const float *k, const float *v, float beta,
                            float decay, int hk, int hv) {
     for (int64_t i = 0; i < (int64_t)hk * hv; i++) state[i] *= decay;
@@ -2029,12 +2110,12 @@ EXPORT int ref_deltanet_steps_chunked(int n_kh, int n_vh, int hk, int hv, int ke
 
 /* ---------------------------------------- Qwen3.5 full-attention layer --- */
 
-/* ops.odin:163-168 */
+/* qwen3_5/ops.odin:163-168 */
 EXPORT void ref_inv_freq(float theta, int rotary_dim, float *out) {
     float rd = (float)rotary_dim;
     for (int i = 0; i < rotary_dim / 2; i++) out[i] = 1.0f / powf(theta, (float)i / (rd / 2.0f));
 }
-/* ops.odin:77-89: pairs (i, i + rotary_dim/2); dimensions past rotary_dim pass */
+/* qwen3_5/ops.odin:77-89: pairs (i, i + rotary_dim/2); dimensions past rotary_dim pass */
 EXPORT void ref_mrope(float *v, int pos, const float *inv_freq, int rotary_dim) {
     int half = rotary_dim / 2;
     float pf = (float)pos;
@@ -2104,7 +2185,7 @@ EXPORT int ref_qwen35_attn_steps(int n_heads, int n_kv, int hd, int rotary_dim, 
 
 /* Routed-expert SwiGLU FFN for one token.  The reference has no MoE code; the
  * convention restated is HF Qwen3-MoE's: logits = router x (rows dequantized,
- * dot_f32 as matmul_t), p = softmax (ops.odin:51-68 form), the top_k largest
+ * dot_f32 as matmul_t), p = softmax (qwen3_5/ops.odin:51-68 form), the top_k largest
  * (strict '>' scan: ties to the lower id, as sampler.odin:79-89), weights p or
  * p / sum, y = sum_k w_k down_e(silu(gate_e x) * up_e x), k in selection order. */
 EXPORT int ref_moe_ffn(int E, int top_k, int dim, int inter, int norm, int rtype, const uint8_t *router, int etype,
