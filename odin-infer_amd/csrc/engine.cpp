@@ -230,6 +230,16 @@ int upload_matrix(uint32_t type, const uint8_t *src, int64_t rows, int64_t cols,
 
 }  // namespace
 
+namespace oi {
+int repack_matrix_host(uint32_t type, const uint8_t *src, int64_t rows, int64_t cols, std::vector<uint8_t> &stage) {
+    size_t bytes;
+    if (!matrix_bytes(type, rows, cols, bytes)) return fail(OI_E_ARG, "matrix size not a whole number of blocks");
+    stage.resize(bytes);
+    (void)repack(type, src, rows, cols, stage.data());
+    return OI_OK;
+}
+}  // namespace oi
+
 namespace {
 
 hipError_t launch_op(const oi_engine *e, const Op &o, hipStream_t st) {
@@ -440,7 +450,8 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     if (c.seq_len <= 0) c.seq_len = opts->max_ctx;
 
     if (c.dim <= 0 || c.dim % 256 || c.dim > 15360 || c.hidden_dim <= 0 || c.hidden_dim % 256 ||
-        c.hidden_dim > 15360 || c.n_layers <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads)
+        c.hidden_dim > 15360 || c.n_layers <= 0 || c.n_layers > 4096 || c.n_heads <= 0 || c.n_heads > 4096 ||
+        c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads)
         return fail(OI_E_MODEL, "model dimensions outside what this path supports");
     const int G = (int)(c.n_heads / c.n_kv_heads);
     if (!((c.head_dim == 128 || c.head_dim == 256) && (G == 1 || G == 2 || G == 4 || G == 8)))
@@ -451,7 +462,7 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
         return fail(OI_E_UNSUPPORTED, "expert configuration not supported (<= 1024 experts, top_k <= 32, "
                                       "inner sizes multiples of 256)");
     if (e->arch == 2 && (e->full_interval < 1 || e->lin_hk != 128 || e->lin_hv != 128 || e->lin_nk < 1 ||
-                         e->lin_nv < 1 || e->lin_nv % e->lin_nk || e->lin_kernel < 1 || e->lin_kernel > 8 ||
+                         e->lin_nk > 4096 || e->lin_nv < 1 || e->lin_nv > 4096 || e->lin_nv % e->lin_nk || e->lin_kernel < 1 || e->lin_kernel > 8 ||
                          e->rotary_dim < 0 || e->rotary_dim > c.head_dim || e->rotary_dim % 2))
         return fail(OI_E_UNSUPPORTED, "hybrid configuration not supported (DeltaNet head dims 128, value heads a "
                                       "multiple of key heads, conv kernel <= 8)");

@@ -52,6 +52,12 @@ struct Op {
     DnArgs dn{};
 };
 
+// The host half of a weight upload: the GGUF matrix `src` (rows x cols of
+// `type`) repacked into the device layout in `stage`.  OI_OK, or OI_E_ARG
+// when a row is not a whole number of blocks.  Separate so that the sanitizer
+// build can run it on files without a device.
+int repack_matrix_host(uint32_t type, const uint8_t *src, int64_t rows, int64_t cols, std::vector<uint8_t> &stage);
+
 }  // namespace oi
 
 enum { K_QKV = 0, K_ATTN = 1, K_WO = 2, K_GATEUP = 3, K_DOWN = 4, K_OUTPUT = 5, K_TOKEN = 6, K_ROUTER = 7,

@@ -186,7 +186,7 @@ int GgufFile::open(const std::string &path, std::string &err) {
     }
     uint64_t align = 32;
     if (auto *a = meta("general.alignment")) align = a->u;
-    if (align == 0 || (align & (align - 1))) {
+    if (align == 0 || (align & (align - 1)) || align > len_) {
         err = "bad general.alignment";
         return OI_E_FORMAT;
     }
@@ -209,6 +209,12 @@ int GgufFile::open(const std::string &path, std::string &err) {
         if (t.dims[0] % (uint64_t)e != 0) {
             err = "tensor " + t.name + " has rows of " + std::to_string(t.dims[0]) + " elements, not a multiple of " +
                   std::to_string(e);
+            return OI_E_FORMAT;
+        }
+        // GGUF places every tensor at a multiple of the alignment (the
+        // reference does not check it; f32 and f16 data must be aligned)
+        if (t.offset % align != 0) {
+            err = "tensor " + t.name + " is not aligned to " + std::to_string(align) + " bytes";
             return OI_E_FORMAT;
         }
         if (n / (uint64_t)e > UINT64_MAX / (uint64_t)b || t.offset > len_ || base > len_ - t.offset) {

@@ -156,4 +156,30 @@ int oikv_verify_crc(FILE *f, uint64_t covered, std::string &msg) {
     return OI_OK;
 }
 
+int oikv_open_checked(FILE *f, const OikvHeader &mine, OikvHeader &h, std::string &msg) {
+    uint8_t hb[OIKV_HEADER_BYTES];
+    if (std::fread(hb, 1, sizeof hb, f) != sizeof hb) {
+        msg = "kv: header truncated";
+        return OI_E_FORMAT;
+    }
+    h = oikv_decode(hb);
+    if (std::fseek(f, 0, SEEK_END) != 0) {
+        msg = "kv: seek failed";
+        return OI_E_IO;
+    }
+    const long size = std::ftell(f);
+    if (size < 0) {
+        msg = "kv: tell failed";
+        return OI_E_IO;
+    }
+    int rc = oikv_check_header(h, mine, (uint64_t)size, msg);
+    if (rc == OI_OK) rc = oikv_verify_crc(f, OIKV_HEADER_BYTES + oikv_body_bytes(h), msg);
+    if (rc != OI_OK) return rc;
+    if (std::fseek(f, (long)OIKV_HEADER_BYTES, SEEK_SET) != 0) {
+        msg = "kv: seek failed";
+        return OI_E_IO;
+    }
+    return OI_OK;
+}
+
 }  // namespace oi

@@ -53,4 +53,9 @@ int oikv_check_header(const OikvHeader &file, const OikvHeader &mine, uint64_t f
 // start; OI_OK, OI_E_IO or OI_E_FORMAT with `msg` set.
 int oikv_verify_crc(FILE *f, uint64_t covered, std::string &msg);
 
+// Everything a load does before it touches state: read and decode the
+// header, the checks above against `mine`, the CRC, then position `f` at the
+// body.  OI_OK with `h` filled, else OI_E_FORMAT / OI_E_IO with `msg` set.
+int oikv_open_checked(FILE *f, const OikvHeader &mine, OikvHeader &h, std::string &msg);
+
 }  // namespace oi

@@ -179,20 +179,13 @@ int oi_engine_load_kv(oi_engine *e, const char *path, int32_t *n_valid_pos) {
     HIP_TRY(hipSetDevice(e->device));
     File f(std::fopen(path, "rb"));
     if (!f) return fail(OI_E_IO, std::string("kv: cannot open ") + path);
-    uint8_t hb[OIKV_HEADER_BYTES];
-    if (std::fread(hb, 1, sizeof hb, f.get()) != sizeof hb) return fail(OI_E_FORMAT, "kv: header truncated");
-    const OikvHeader h = oikv_decode(hb);
     const Shape s = shape_of(e);
-    if (std::fseek(f.get(), 0, SEEK_END) != 0) return fail(OI_E_IO, "kv: seek failed");
-    const long size = std::ftell(f.get());
-    if (size < 0) return fail(OI_E_IO, "kv: tell failed");
-    std::string msg;
     // the reference's checks, in its order, then the size and the CRC over
     // header + body before any state changes (kv_persist.odin:278-310)
-    int rc = oikv_check_header(h, header_of(e, s, 0), (uint64_t)size, msg);
-    if (rc == OI_OK) rc = oikv_verify_crc(f.get(), OIKV_HEADER_BYTES + oikv_body_bytes(h), msg);
+    OikvHeader h;
+    std::string msg;
+    int rc = oikv_open_checked(f.get(), header_of(e, s, 0), h, msg);
     if (rc != OI_OK) return fail(rc, msg);
-    if (std::fseek(f.get(), (long)OIKV_HEADER_BYTES, SEEK_SET) != 0) return fail(OI_E_IO, "kv: seek failed");
 
     const int n = (int)h.n_valid_pos;
     const size_t rows = (size_t)n * s.kv_dim * 4;

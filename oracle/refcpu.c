@@ -580,6 +580,7 @@ typedef struct {
     uint64_t offset;
     const uint8_t *data;
     uint64_t size;
+    uint8_t *copy; /* an aligned private copy when the file places data off 4-byte boundaries */
 } gtensor;
 
 typedef struct {
@@ -633,6 +634,7 @@ static void skip_val(rdr *r, int t, int depth) { /* gguf.odin:113-133 */
 
 static void gfile_free(gfile *g) {
     if (g->map) munmap(g->map, g->map_len);
+    for (int i = 0; g->tensors && i < g->n_tensors; i++) free(g->tensors[i].copy);
     free(g->meta);
     free(g->tensors);
     memset(g, 0, sizeof *g);
@@ -701,7 +703,7 @@ static int gfile_open(const char *path, gfile *g) { /* gguf.odin:167-229 */
     uint64_t alignment = 32;
     for (int i = 0; i < g->n_meta; i++)
         if (!strcmp(g->meta[i].key, "general.alignment")) alignment = g->meta[i].u;
-    if (alignment == 0 || (alignment & (alignment - 1))) { snprintf(g_err, sizeof g_err, "bad alignment"); return -6; }
+    if (alignment == 0 || (alignment & (alignment - 1)) || alignment > g->map_len) { snprintf(g_err, sizeof g_err, "bad alignment"); return -6; }
     uint64_t data_base = (r.pos + alignment - 1) & ~(alignment - 1);
     for (int i = 0; i < g->n_tensors; i++) {
         gtensor *t = &g->tensors[i];
@@ -717,6 +719,10 @@ static int gfile_open(const char *path, gfile *g) { /* gguf.odin:167-229 */
             snprintf(g_err, sizeof g_err, "tensor %s: element count overflows", t->name);
             return -7;
         }
+        if (t->offset % alignment) { /* spec placement; the reference does not check it */
+            snprintf(g_err, sizeof g_err, "tensor %s is not aligned", t->name);
+            return -7;
+        }
         t->size = (uint64_t)ref_row_byte_size(t->kind, (int64_t)ne);
         if (t->offset > g->map_len || data_base > g->map_len - t->offset ||
             t->size > g->map_len - (data_base + t->offset)) {
@@ -724,6 +730,14 @@ static int gfile_open(const char *path, gfile *g) { /* gguf.odin:167-229 */
             return -7;
         }
         t->data = g->map + data_base + t->offset;
+        /* general.alignment 1 or 2 is legal GGUF but leaves f32/f16 data
+         * misaligned for direct loads: read such a tensor from a copy */
+        if (((uintptr_t)t->data & 3) && t->size) {
+            t->copy = (uint8_t *)malloc((size_t)t->size);
+            if (!t->copy) { snprintf(g_err, sizeof g_err, "out of memory"); return -7; }
+            memcpy(t->copy, t->data, (size_t)t->size);
+            t->data = t->copy;
+        }
     }
     return 0;
 }
@@ -1194,6 +1208,11 @@ static void moe_ffn_layer(ref_engine *e, const layer_w *lw, const float *x, floa
         int best = -1;
         for (int64_t i = 0; i < E; i++)
             if (p[i] >= 0.0f && (best < 0 || p[i] > p[best])) best = (int)i;
+        if (best < 0) { /* NaN probabilities rank nothing: expert 0 at weight 0, as the device does */
+            ids[k] = 0;
+            w[k] = 0.0f;
+            continue;
+        }
         ids[k] = best;
         w[k] = p[best];
         sum += p[best];
@@ -2208,6 +2227,11 @@ EXPORT int ref_moe_ffn(int E, int top_k, int dim, int inter, int norm, int rtype
         int best = -1;
         for (int e = 0; e < E; e++)
             if (p[e] >= 0.0f && (best < 0 || p[e] > p[best])) best = e;
+        if (best < 0) { /* NaN probabilities rank nothing: expert 0 at weight 0, as the device does */
+            ids[k] = 0;
+            w[k] = 0.0f;
+            continue;
+        }
         ids[k] = best;
         w[k] = p[best];
         sum += p[best];
