@@ -429,7 +429,10 @@ int oi_moe_ffn_launch(const oi_moe_dims *d, const oi_weights *router, const oi_w
  * device array of its own, one per GPU, held until the process ends, and
  * rejects dims whose oi_moe_workspace_bytes exceed it (OI_E_ARG).  It calls
  * no hipMalloc/hipFree.  Calls on one GPU share the array, so calls that
- * overlap on one GPU (two streams or two threads) race. */
+ * overlap on one GPU (two streams or two threads) race.  The array's device
+ * address is looked up once per GPU and kept: do not call it across a
+ * hipDeviceReset of that GPU (the code object, and the array with it, may
+ * move). */
 int oi_moe_ffn_launch_noalloc(const oi_moe_dims *d, const oi_weights *router, const oi_weights *gate,
                               const oi_weights *up, const oi_weights *down, const float *x_dev, float *y_dev,
                               void *stream);

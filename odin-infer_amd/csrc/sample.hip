@@ -41,7 +41,9 @@ namespace {
 constexpr int SWG = 1024, SWAVES = SWG / WAVE;
 constexpr int SAMPLE_MAX_VOCAB = 1 << 18;  // LDS penalty bitmap: 32 KB
 
-__device__ __forceinline__ uint64_t fix40(float p) { return (uint64_t)(p * 1099511627776.0f); }
+// p * 2^40 rounded to the nearest integer (the scaling is exact in f32, rintf
+// rounds the fraction), so the fixed-point total is unbiased against the f32 sum
+__device__ __forceinline__ uint64_t fix40(float p) { return (uint64_t)rintf(p * 1099511627776.0f); }
 
 struct Hist {
     uint32_t cnt[256];
@@ -356,7 +358,9 @@ __global__ __launch_bounds__(SWG) void sample_kernel(const float *logits, float 
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), w = tid / WAVE;
     const int W = ((n + SWAVES - 1) / SWAVES + BATCH - 1) / BATCH * BATCH;
     const Range r{min(n, w * W), min(n, (w + 1) * W)};
-    const float T = ss->temperature, topp = ss->topp, pen = ss->penalty;
+    // enable_repeat_penalty's clamp (sampler.odin:42-44) applied here too, so a
+    // C caller's penalty below 1 acts as 1 (off) rather than dividing by it
+    const float T = ss->temperature, topp = ss->topp, pen = ss->penalty < 1.0f ? 1.0f : ss->penalty;
     for (int i = tid; i < (n + 31) / 32; i += SWG) s.pen_bits[i] = 0;
     __syncthreads();
     if (tid == 0) {  // distinct recent tokens and their penalised logits

@@ -100,6 +100,45 @@ def test_temperature_zero_and_penalty_match_the_oracle_exactly():
     assert infer.sample(infer.Sampler(0.0, 0.0, repeat_penalty=2.0, last=[0]), np.array([-1, -1.5], F32)) == 1
 
 
+def test_penalty_below_one_is_clamped_at_the_c_abi():
+    """enable_repeat_penalty clamps penalties below 1 to 1 (sampler.odin:42-44);
+    a C caller that writes 0.5 or 0 into oi_sampler directly gets the same
+    pick as the clamped reference (no division by 0, no inverted penalty)."""
+    rng = np.random.default_rng(11)
+    logits = (rng.standard_normal(2048) * 2).astype(F32)
+    last = list(rng.integers(0, 2048, 30))
+    for t, topp in ((0.0, 0.9), (0.7, 0.9)):
+        for raw in (0.5, 0.0):
+            s = infer.Sampler(t, topp, rng_seed=77, last=last)
+            s.repeat_penalty = raw  # past the wrapper's clamp: the value reaches the C ABI
+            got = infer.sample(s, logits)
+            want, st = refcpu.sample(logits, t, topp, 1.0, last, rng_state=77)
+            assert got == want and s.rng_state == st
+
+
+def test_coin_near_one_matches_exact_picks():
+    """Coins within 2^-24 of 1 (the largest the 24-bit coin takes): the pick is
+    the float64 one, so rounding the fixed-point masses keeps the running
+    total from falling short of the coin and the draw from falling through
+    to the last vocabulary id."""
+    from refcpu import random_f32
+    rng = np.random.default_rng(12)
+    logits = (rng.standard_normal(151936) * 0.5).astype(F32)  # flat: many small masses
+    # xorshift64* states whose next coin is the largest, found by search on the CPU
+    states, st = [], 1
+    while len(states) < 3:
+        coin, nxt = random_f32(st)
+        if coin >= 1.0 - 2.0 ** -20:
+            states.append(st)
+        st = (st * 6364136223846793005 + 1442695040888963407) % 2 ** 64 or 1
+    for st in states:
+        coin, _ = random_f32(st)
+        for t, topp in ((1.0, 0.0), (0.9, 0.95)):
+            want, margin = exact_pick(logits, t, topp, coin)
+            got = infer.sample(infer.Sampler(t, topp, rng_seed=st), logits)
+            assert got == want or margin <= 1e-6, (st, coin, t, topp, got, want)
+
+
 def test_zero_coin_matches_the_oracle_exactly():
     """seed 0 (serve.odin:1544): every coin is 0."""
     rng = np.random.default_rng(2)
