@@ -354,7 +354,8 @@ int oi_deltanet_steps(const oi_deltanet_dims *d, int32_t n_tokens, const float *
 /* The same trajectory through the batched prefill kernels, all n_tokens at
  * once: the conv over the whole trajectory, l2norm and gates per token, the
  * delta rule token by token in one launch (chunk 0) or in its chunked form
- * over chunks of 16 or 32 tokens (chunk 16 / 32; qwen3_5/metal.odin:416-468
+ * over chunks of 16, 32 or 64 tokens (chunk 16 / 32 / 64, the last on the
+ * matrix cores; qwen3_5/metal.odin:416-468
  * chunked_delta, which the reference builds but does not dispatch,
  * qwen3_5/metal.odin:1583-1586), the gated norm (qwen3_5/metal.odin:1582-1618, the linear
  * layer of forward_gpu_batch).  Host memory as oi_deltanet_steps; head dims

@@ -1009,8 +1009,15 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
                     : std::strcmp(pm, "dot4") == 0 ? 5
                     : std::strcmp(pm, "i8") == 0 ? 6
                                                     : 0;
-    const char *pc = std::getenv("OI_PREFILL_DN_CHUNK");  // "16" / "32": the chunked delta rule in prefill
-    e->pf_dn_chunk = !pc ? 0 : std::strcmp(pc, "16") == 0 ? 16 : std::strcmp(pc, "32") == 0 ? 32 : 0;
+    // the delta rule of a prefill chunk: in its chunked form over 64 tokens on
+    // the matrix cores (default), token by token ("0"), or the lane-level
+    // chunked form over 16 / 32 tokens
+    const char *pc = std::getenv("OI_PREFILL_DN_CHUNK");
+    e->pf_dn_chunk = !pc                          ? 64
+                     : std::strcmp(pc, "16") == 0 ? 16
+                     : std::strcmp(pc, "32") == 0 ? 32
+                     : std::strcmp(pc, "0") == 0  ? 0
+                                                  : 64;
 
     std::printf("model: %s dim=%lld layers=%lld (attention %d, linear %d) heads=%lld/%lld hidden=%lld vocab=%lld "
                 "ctx=%lld/%lld experts=%lld/%lld  weights=%.0f MB  KV cache (f16)=%.0f MB  [gfx950]\n",
@@ -1186,6 +1193,7 @@ int prefill_alloc(oi_engine *e) {
                                  full ? T * QD * 4 : 0,
                                  lin ? T * CD * 4 : 0, lin ? T * 2 * KD * 4 : 0, lin ? T * 3 * (size_t)e->lin_nv * 4 : 0,
                                  lin ? T * VD * 4 : 0,
+                                 lin ? pf_dc_scratch_floats((int)e->lin_nv, (int)T) * 4 : 0,
                                  moe ? T * D * 4 : 0, moe ? T * (size_t)e->n_experts * 4 : 0,
                                  moe ? T * KP * 4 : 0, moe ? T * KP * EF * 4 : 0, moe ? T * KP * EF * 4 : 0,
                                  moe ? T * KP * D * 4 : 0,
@@ -1215,6 +1223,7 @@ int prefill_alloc(oi_engine *e) {
     e->pf_qk = (float *)take();
     e->pf_gates = (float *)take();
     e->pf_o = (float *)take();
+    e->pf_dc = (float *)take();
     e->pf_xn = (float *)take();
     e->pf_lg = (float *)take();
     e->pf_w = (float *)take();
@@ -1427,6 +1436,7 @@ int prefill_chunk(oi_engine *e, const int32_t *tokens, int T, int pos, float *ro
             da.n_kh = (int32_t)e->lin_nk; da.n_vh = (int32_t)e->lin_nv;
             da.hk = (int32_t)e->lin_hk; da.hv = (int32_t)e->lin_hv; da.kernel = (int32_t)e->lin_kernel;
             da.chunk = e->pf_dn_chunk;
+            da.dc = e->pf_dc;
             HIP_TRY(launch_pf_deltanet(da, st));
             HIP_TRY(launch_gemm_parts(L.ssm_out, e->pf_xb, T, P[0], PB[0], &s0, st));
         }
@@ -1992,7 +2002,8 @@ int oi_deltanet_steps_batched(const oi_deltanet_dims *d, int32_t n_tokens, int32
                               float *rec_state, float *out) {
     if (!dn_dims_ok(d) || !pf_dn_supported(d->head_k_dim, d->head_v_dim, d->conv_kernel))
         return fail(OI_E_ARG, "deltanet batched: head dims 128, conv kernel 4, n_v_heads a multiple of n_k_heads");
-    if (chunk != 0 && chunk != 16 && chunk != 32) return fail(OI_E_ARG, "deltanet batched: chunk must be 0, 16 or 32");
+    if (chunk != 0 && chunk != 16 && chunk != 32 && chunk != 64)
+        return fail(OI_E_ARG, "deltanet batched: chunk must be 0, 16, 32 or 64");
     if (n_tokens < d->conv_kernel - 1 || !qkv || !z || !b || !a || !conv_w || !a_decay || !dt_bias || !norm_w ||
         !conv_state || !rec_state || !out)
         return fail(OI_E_ARG, "deltanet batched: bad argument (n_tokens must be at least conv_kernel - 1)");
@@ -2003,7 +2014,8 @@ int oi_deltanet_steps_batched(const oi_deltanet_dims *d, int32_t n_tokens, int32
     const size_t in_f[] = {n * cd, n * vd, n * nvh, n * nvh, cd * d->conv_kernel, nvh, nvh, (size_t)d->head_v_dim,
                            cd * km1, st_n};
     const float *in_p[] = {qkv, z, b, a, conv_w, a_decay, dt_bias, norm_w, conv_state, rec_state};
-    size_t floats = n * cd + n * 2 * kd + n * 3 * nvh + n * vd + n * vd;
+    const size_t dcf = chunk == 64 ? pf_dc_scratch_floats((int)nvh, (int)n) : 0;
+    size_t floats = n * cd + n * 2 * kd + n * 3 * nvh + n * vd + n * vd + dcf;
     for (size_t x : in_f) floats += x;
     float *dev = nullptr;
     HIP_TRY(hipMalloc(&dev, floats * 4));
@@ -2024,6 +2036,7 @@ int oi_deltanet_steps_batched(const oi_deltanet_dims *d, int32_t n_tokens, int32
     da.qk = p; p += n * 2 * kd;
     da.gates = p; p += n * 3 * nvh;
     da.o = p; p += n * vd;
+    da.dc = dcf ? p : nullptr; p += dcf;
     da.out32 = p;
     da.T = n_tokens;
     da.n_kh = d->n_k_heads; da.n_vh = d->n_v_heads;

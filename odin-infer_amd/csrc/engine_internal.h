@@ -110,6 +110,7 @@ struct oi_engine {
     uint16_t *pf_xb = nullptr;
     float *pf_gate = nullptr;
     float *pf_conv = nullptr, *pf_qk = nullptr, *pf_gates = nullptr, *pf_o = nullptr;
+    float *pf_dc = nullptr;  // the chunked delta rule's Tb and M per value head and 64-token chunk
     float *pf_xn = nullptr, *pf_lg = nullptr, *pf_w = nullptr, *pf_h = nullptr, *pf_yd = nullptr;
     float *pf_h2 = nullptr;  // up rows of the routed experts (few-pair items)
     int32_t *pf_ids = nullptr, *pf_list = nullptr, *pf_off = nullptr, *pf_cnt = nullptr, *pf_fill = nullptr;
@@ -124,7 +125,7 @@ struct oi_engine {
     bool dn_fused = false;  // token loop: the one-launch DeltaNet step instead of the split one (OI_DN_FUSED)
     bool router_fused = false;  // token loop: the router inside the routed gate/up launch where it applies
                                 // (OI_MOE_ROUTER=fused; measured slower at config 4 than its own launch)
-    int pf_dn_chunk = 0;  // delta rule of a prefill chunk: 0 token by token, 16 / 32 chunked (OI_PREFILL_DN_CHUNK)
+    int pf_dn_chunk = 64;  // delta rule of a prefill chunk: 0 token by token, 16 / 32 / 64 chunked (OI_PREFILL_DN_CHUNK)
     // engine_verify_batch: the logits of every position, [rows][vocab] on the
     // device and in pinned host memory (allocated on first use, grown as needed)
     float *vf_dev = nullptr, *vf_host = nullptr;

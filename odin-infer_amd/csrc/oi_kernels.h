@@ -268,9 +268,11 @@ struct PfDnArgs {
     uint16_t *out16;               // [T][n_vh hv]: gated-normed, f16 (the output projection's input)
     float *out32;                  // or, when set, the same in f32
     int32_t T, n_kh, n_vh, hk, hv, kernel;
-    int32_t chunk;                 // 0: the delta rule token by token; 16 / 32: its chunked form
+    int32_t chunk;                 // 0: the delta rule token by token; 16 / 32 / 64: its chunked form
+    float *dc;                     // chunk 64: scratch of pf_dc_scratch_floats(n_vh, T) floats
 };
 bool pf_dn_supported(int hk, int hv, int kernel);
+size_t pf_dc_scratch_floats(int n_vh, int T);
 hipError_t launch_pf_deltanet(const PfDnArgs &a, hipStream_t st);
 // kernels.hip: the routed-expert FFN of a prefill chunk.  Pairs p = t * kp + s
 // (token t, slot s of its kp chosen experts) are grouped by expert; a

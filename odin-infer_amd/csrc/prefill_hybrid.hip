@@ -22,6 +22,10 @@
 //   pf_dn_chunk_kernel      the same in its chunked form (qwen3_5/metal.odin:416-468,
 //                           which the reference does not dispatch): 16 or 32
 //                           tokens per step, decay ratios from log sums
+//   pf_dc_prep_kernel,      the chunked form in chunks of 64 on the matrix
+//   pf_dc_state_kernel      cores: the state-free C x C matrices of every
+//                           chunk at once, then the state carried through them
+//   pf_dc_single_kernel     the same for a prompt of one chunk, in one launch
 //   pf_dn_gnorm_kernel      gated RMSNorm, f16 rows for the output projection
 //                           (or f32 rows for the host-memory entry point)
 //
@@ -422,6 +426,636 @@ __global__ __launch_bounds__(WG) void pf_dn_chunk_kernel(PfDnArgs a) {
     for (int r = 0; r < RPL; r++) S[(size_t)(i0 + r) * HV + j] = s[r];
 }
 
+// ---- the chunked delta rule on the matrix cores (chunks of 64 tokens) ----
+//
+// The same math as pf_dn_chunk_kernel in matrix form.  Per value head and
+// chunk, with K, Q [64][hk] (q already scaled), V [64][hv], c the running sum
+// of the log decays, G_t = e^{c_t}, F_t = e^{c_63 - c_t} (padded tokens past
+// the end of the prompt have k = q = v = 0, beta = 0 and log decay 0):
+//   L_ti = beta_t e^{c_t - c_i} k_t.k_i (i < t)    M_ti = e^{c_t - c_i} q_t.k_i (i <= t)
+//   T = (I + L)^-1,  Tb = T diag(beta)
+//   X = V - diag(G) K S,  D = Tb X,  O = diag(G) Q S + M D
+//   S' = G_63 S + (diag(F) K)^T D
+// (I + L) D = diag(beta) X is the forward substitution of the token form.
+// pf_dc_prep_kernel forms Tb, M and c per (value head, chunk) -- they do not
+// depend on the state, so every chunk of the call runs at once; the inverse
+// is blocked by 16: the diagonal blocks by substitution (a lane per column),
+// then T_ba = -T_bb sum_{m=a}^{b-1} L_bm T_ma on the matrix cores.
+// pf_dc_state_kernel carries one value head's state through the chunks, a
+// workgroup per 32 state columns.  Every product is v_mfma_f32_16x16x4_f32
+// (f32 operands, f32 sums): D[16][16] += A[16][4] B[4][16], lane l giving
+// A[l % 16][kk] and B[kk][l % 16] for kk = l / 16 and holding
+// D[4 (l / 16) + e][l % 16].  Which physical index of the contraction an
+// instruction's kk stands for is free as long as A and B agree; it is chosen
+// so that a lane's operands over consecutive instructions are consecutive in
+// LDS (one 16-byte read per four instructions, all issued before the first).
+constexpr int DC = 64;         // tokens per chunk
+constexpr int DC_CB = 32;      // state columns per workgroup of pf_dc_state_kernel
+constexpr int DC_WG = 512;     // threads of both kernels (two waves per SIMD)
+constexpr int DC_WAVES = DC_WG / WAVE;
+typedef float dc_f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ dc_f32x4 dc_mfma(float a, float b, dc_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+// Four instructions over a lane's four consecutive operands, into four
+// independent accumulators: a chain of dependent matrix instructions waits
+// for each result, four chains keep the matrix core busy.
+__device__ __forceinline__ void dc_mfma4(float4 a, float4 b, dc_f32x4 (&c)[4]) {
+    c[0] = dc_mfma(a.x, b.x, c[0]);
+    c[1] = dc_mfma(a.y, b.y, c[1]);
+    c[2] = dc_mfma(a.z, b.z, c[2]);
+    c[3] = dc_mfma(a.w, b.w, c[3]);
+}
+__device__ __forceinline__ dc_f32x4 dc_sum4(const dc_f32x4 (&c)[4]) { return (c[0] + c[1]) + (c[2] + c[3]); }
+
+// x = hi + lo in halves (to ~2^-22 of x) for the products of l2-normalised
+// rows, whose elements lie in [-1, 1]: hi.hi + hi.lo + lo.hi on
+// v_mfma_f32_16x16x32_f16 (exact half products, f32 sums), lo.lo dropped.
+// Lane l gives A[l % 16][8 (l / 16) + e] and B[8 (l / 16) + e][l % 16], e < 8.
+typedef _Float16 dc_h8 __attribute__((ext_vector_type(8)));
+#define DC_ZERO4 {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}}
+
+// [n_vh][n_chunks] of DC_REC floats: Tb [64][64], M [64][64] (lower 16-blocks
+// only), c [64] (the running sums of the log decays), the chunk's q | k rows
+// [64][2 hk] (written only in the records of value heads vh < n_kh, i.e. of
+// k head vh), and the value head's v in column blocks [hv / 16][64][16]: the
+// state kernel reads each of its inputs as one contiguous run (q, k and v
+// rows in the projection layout are 32 KB apart, so the same few memory
+// channels would serve all of a chunk's rows)
+constexpr int DC_C = 2 * DC * DC, DC_QKO = DC_C + DC, DC_VO = DC_QKO + DC * 2 * 128;
+constexpr int DC_REC = DC_VO + DC * 128;
+size_t pf_dc_scratch_floats(int n_vh, int T) { return (size_t)n_vh * ((T + DC - 1) / DC) * DC_REC; }
+
+// inclusive prefix sum over a wave (lane order)
+__device__ __forceinline__ float dc_wave_scan(float v) {
+    const int lane = threadIdx.x & (WAVE - 1);
+#pragma unroll
+    for (int d = 1; d < WAVE; d <<= 1) {
+        const float o = __shfl_up(v, d, WAVE);
+        if (lane >= d) v += o;
+    }
+    return v;
+}
+
+// lower 16-blocks (bi, bj), bj <= bi, in row order
+__device__ __forceinline__ void dc_lower_block(int p, int &bi, int &bj) {
+    bi = p >= 6 ? 3 : p >= 3 ? 2 : p >= 1 ? 1 : 0;
+    bj = p - bi * (bi + 1) / 2;
+}
+
+// The chunk's q and k rows of k head kh (zeros past nb) as float4 pieces:
+// loaded into registers all at once, then stored to LDS rows of pitch HK + 4
+// (a loop that stores each piece as it arrives waits for every load in turn).
+constexpr int DC_QK4 = DC * 128 / 2 / DC_WG;
+template <int HK>
+__device__ __forceinline__ void dc_load_qk(const PfDnArgs &a, dc_f32x4 (&v)[DC_QK4], int tb, int nb, int kh) {
+    static_assert(DC * HK / 2 == DC_QK4 * DC_WG, "staging shape");
+    const int KD = a.n_kh * HK;
+#pragma unroll
+    for (int i = 0; i < DC_QK4; i++) {
+        const int idx = threadIdx.x + i * DC_WG, t = idx / (HK / 2), e4 = idx % (HK / 2);
+        const int side = e4 / (HK / 4), ee = 4 * (e4 % (HK / 4));
+        v[i] = t < nb ? *(const dc_f32x4 *)(a.qk + (size_t)(tb + t) * 2 * KD + side * KD + kh * HK + ee)
+                      : dc_f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+}
+template <int HK>
+__device__ __forceinline__ void dc_store_qk(const dc_f32x4 (&v)[DC_QK4], float (*sq)[HK + 4], float (*sk)[HK + 4]) {
+#pragma unroll
+    for (int i = 0; i < DC_QK4; i++) {
+        const int idx = threadIdx.x + i * DC_WG, t = idx / (HK / 2), e4 = idx % (HK / 2);
+        const int side = e4 / (HK / 4), ee = 4 * (e4 % (HK / 4));
+        *(dc_f32x4 *)&(side ? sk : sq)[t][ee] = v[i];
+    }
+}
+
+// (I + L_bb)^-1 of diagonal block b (one wave; lane < 16 = column) by
+// substitution, each row's sum in four fused chains (the critical path)
+template <int LP>
+__device__ __forceinline__ void dc_invert_diag(const float (*sl)[LP], float (*stt)[LP], int b, int lane) {
+    if (lane >= 16) return;
+    const int o = 16 * b, j = lane;
+    float col[16];
+#pragma unroll
+    for (int t = 0; t < 16; t++) {
+        float p4[4] = {t == j ? 1.f : 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < t; i++) p4[i & 3] = fmaf(-sl[o + t][o + i], col[i], p4[i & 3]);
+        col[t] = (p4[0] + p4[1]) + (p4[2] + p4[3]);
+    }
+#pragma unroll
+    for (int t = 0; t < 16; t++) stt[o + t][o + j] = col[t];
+}
+
+// The blocks below the diagonal, block row by block row (called by every
+// thread of the workgroup after the diagonal blocks; ends with a barrier):
+// T_ba = -T_bb sum_{m=a}^{b-1} L_bm T_ma, waves a < b one block each.
+template <int LP>
+__device__ __forceinline__ void dc_invert_below(const float (*sl)[LP], float (*stt)[LP], float (*sz)[16][17], int wave,
+                                                int r, int kq) {
+    for (int b = 1; b < 4; b++) {
+        const int ab = wave;
+        if (ab < b) {
+            dc_f32x4 zc[4] = DC_ZERO4;
+            for (int m = ab; m < b; m++)
+#pragma unroll
+                for (int k0 = 0; k0 < 16; k0 += 4)
+                    zc[k0 / 4] = dc_mfma(sl[16 * b + r][16 * m + k0 + kq], stt[16 * m + k0 + kq][16 * ab + r], zc[k0 / 4]);
+            const dc_f32x4 z = dc_sum4(zc);
+#pragma unroll
+            for (int e = 0; e < 4; e++) sz[wave][4 * kq + e][r] = z[e];
+            dc_f32x4 yc[4] = DC_ZERO4;
+#pragma unroll
+            for (int k0 = 0; k0 < 16; k0 += 4)
+                yc[k0 / 4] = dc_mfma(stt[16 * b + r][16 * b + k0 + kq], sz[wave][k0 + kq][r], yc[k0 / 4]);
+            const dc_f32x4 y = dc_sum4(yc);
+#pragma unroll
+            for (int e = 0; e < 4; e++) stt[16 * b + 4 * kq + e][16 * ab + r] = -y[e];
+        }
+        __syncthreads();
+    }
+}
+
+template <int HK>
+__global__ __launch_bounds__(DC_WG) void pf_dc_prep_kernel(PfDnArgs a) {
+#pragma clang fp contract(off)
+    constexpr int HP = HK + 8;  // row pitch in halves: 16-byte aligned rows, 4 banks apart
+    static_assert(HK % 128 == 0, "k rows in four 32-element lane slices");
+    // q and k rows split once into f16 hi and lo parts, as the matrix cores take them
+    __shared__ __attribute__((aligned(16))) _Float16 skh[DC][HP], skl[DC][HP], sqh[DC][HP], sql[DC][HP];
+    __shared__ float sl[DC][DC + 1], stt[DC][DC + 1], sz[4][16][17];
+    __shared__ float slg[DC], slc[DC], sbeta[DC];
+    const int vh = blockIdx.x, ch = blockIdx.y, nch = (int)gridDim.y, kh = vh % a.n_kh;
+    const int tb = ch * DC, nb = min(DC, a.T - tb);
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE, r = lane & 15, kq = lane >> 4;
+    float *out = a.dc + ((size_t)vh * nch + ch) * DC_REC;
+    {  // q and k rows, v rows and the gates: every load issued before any is stored
+        static_assert(HK == 128, "record layout");
+        constexpr int V4 = DC * 128 / 4 / DC_WG;
+        const int CD = 2 * a.n_kh * HK + a.n_vh * 128;
+        dc_f32x4 qk4[DC_QK4], v4[V4];
+        dc_load_qk<HK>(a, qk4, tb, nb, kh);
+#pragma unroll
+        for (int i = 0; i < V4; i++) {
+            const int idx = threadIdx.x + i * DC_WG, t = idx / 32, c4 = 4 * (idx % 32);
+            v4[i] = t < nb ? *(const dc_f32x4 *)(a.conv_out + (size_t)(tb + t) * CD + 2 * a.n_kh * HK + vh * 128 + c4)
+                           : dc_f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        const int t = threadIdx.x;
+        const float b = t < nb ? a.gates[(size_t)(tb + t) * 3 * a.n_vh + vh] : 0.f;
+        const float g = t < nb ? a.gates[(size_t)(tb + t) * 3 * a.n_vh + 2 * a.n_vh + vh] : 0.f;
+#pragma unroll
+        for (int i = 0; i < DC_QK4; i++) {
+            const int idx = threadIdx.x + i * DC_WG, tt = idx / (HK / 2), e4 = idx % (HK / 2);
+            const int side = e4 / (HK / 4), ee = 4 * (e4 % (HK / 4));
+            typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+            h4 hi, lo;
+#pragma unroll
+            for (int x = 0; x < 4; x++) {
+                hi[x] = (_Float16)qk4[i][x];
+                lo[x] = (_Float16)(qk4[i][x] - (float)hi[x]);
+            }
+            *(h4 *)&(side ? skh : sqh)[tt][ee] = hi;
+            *(h4 *)&(side ? skl : sql)[tt][ee] = lo;
+        }
+        if (vh < a.n_kh)  // this record carries k head vh's q | k rows
+#pragma unroll
+            for (int i = 0; i < DC_QK4; i++) *(dc_f32x4 *)(out + DC_QKO + 4 * (threadIdx.x + i * DC_WG)) = qk4[i];
+#pragma unroll
+        for (int i = 0; i < V4; i++) {
+            const int idx = threadIdx.x + i * DC_WG, tt = idx / 32, c4 = 4 * (idx % 32);
+            *(dc_f32x4 *)(out + DC_VO + (c4 / 16) * DC * 16 + tt * 16 + c4 % 16) = v4[i];
+        }
+        if (t < DC) {
+            sbeta[t] = b;
+            slg[t] = g;
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {  // the running sum of the log decays (kept for the state kernel)
+        const float c = dc_wave_scan(slg[lane]);
+        slc[lane] = c;
+        out[DC_C + lane] = c;
+    }
+    __syncthreads();
+    // k_t.k_i (then q_t.k_i) over the lower 16-blocks, 10 tiles each: lane
+    // slice s of a row is its elements 32 s + 8 kq .. + 7
+    auto tile = [&](bool isq, int p) {
+        int bi, bj;
+        dc_lower_block(p, bi, bj);
+        const _Float16 *xh = (isq ? sqh : skh)[16 * bi + r] + 8 * kq, *xl = (isq ? sql : skl)[16 * bi + r] + 8 * kq;
+        const _Float16 *yh = skh[16 * bj + r] + 8 * kq, *yl = skl[16 * bj + r] + 8 * kq;
+        dc_h8 ah[HK / 32], al[HK / 32], bh[HK / 32], bl[HK / 32];
+#pragma unroll
+        for (int m = 0; m < HK / 32; m++) {
+            ah[m] = *(const dc_h8 *)(xh + 32 * m);
+            al[m] = *(const dc_h8 *)(xl + 32 * m);
+            bh[m] = *(const dc_h8 *)(yh + 32 * m);
+            bl[m] = *(const dc_h8 *)(yl + 32 * m);
+        }
+        float ct[4], bt[4];  // the epilogue's operands, read while the products run
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            ct[e] = slc[16 * bi + 4 * kq + e];
+            bt[e] = sbeta[16 * bi + 4 * kq + e];
+        }
+        const float ci = slc[16 * bj + r];
+        dc_f32x4 c3[3] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int m = 0; m < HK / 32; m++) {
+            c3[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[m], bh[m], c3[0], 0, 0, 0);
+            c3[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[m], bl[m], c3[1], 0, 0, 0);
+            c3[2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[m], bh[m], c3[2], 0, 0, 0);
+        }
+        const dc_f32x4 acc = c3[0] + (c3[1] + c3[2]);
+        float val[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {  // selects, not branches (exp of a positive difference is discarded)
+            const int t = 16 * bi + 4 * kq + e, i = 16 * bj + r;
+            const float ratio = expf(ct[e] - ci);
+            val[e] = isq ? (i <= t ? ratio * acc[e] : 0.f) : (i < t ? bt[e] * ratio * acc[e] : 0.f);
+        }
+        if (isq) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) out[DC * DC + (16 * bi + 4 * kq + e) * DC + 16 * bj + r] = val[e];
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++) sl[16 * bi + 4 * kq + e][16 * bj + r] = val[e];
+        }
+    };
+    for (int p = wave; p < 10; p += DC_WAVES) tile(false, p);
+    __syncthreads();
+    if (wave < 4) {
+        dc_invert_diag<DC + 1>(sl, stt, wave, lane);
+    } else {  // meanwhile the q.k tiles, which the inverse does not need
+        for (int p = wave - 4; p < 10; p += 4) tile(true, p);
+    }
+    __syncthreads();
+    dc_invert_below<DC + 1>(sl, stt, sz, wave, r, kq);
+    for (int idx = threadIdx.x; idx < DC * DC; idx += DC_WG) {  // Tb = T diag(beta), lower blocks
+        const int t = idx / DC, i = idx % DC;
+        if (i / 16 <= t / 16) out[idx] = stt[t][i] * sbeta[i];
+    }
+}
+
+// The state kernel's inputs of one chunk, held in registers from the load
+// (issued while the previous chunk is computed) to the LDS stores: q / k rows,
+// Tb and M (whole 64 x 64; only the lower blocks are read), the workgroup's
+// v columns and c.
+constexpr int DC_TM4 = DC * DC / 4 / DC_WG, DC_V4 = DC * DC_CB / 4 / DC_WG;
+static_assert(DC_TM4 * DC_WG * 4 == DC * DC && DC_V4 * DC_WG * 4 == DC * DC_CB, "staging shape");
+struct DcStage {
+    dc_f32x4 qk4[DC_QK4], tb4[DC_TM4], m4[DC_TM4], v4[DC_V4];
+    float lg;
+};
+__device__ __forceinline__ void dc_stage_load(const PfDnArgs &a, DcStage &g, int vh, int kh, int ch, int nch, int c0) {
+    const float *tm = a.dc + ((size_t)vh * nch + ch) * DC_REC;
+    const float *qkr = a.dc + ((size_t)kh * nch + ch) * DC_REC + DC_QKO;
+#pragma unroll
+    for (int i = 0; i < DC_QK4; i++) g.qk4[i] = *(const dc_f32x4 *)(qkr + 4 * (threadIdx.x + i * DC_WG));
+#pragma unroll
+    for (int i = 0; i < DC_TM4; i++) {
+        g.tb4[i] = *(const dc_f32x4 *)(tm + 4 * (threadIdx.x + i * DC_WG));
+        g.m4[i] = *(const dc_f32x4 *)(tm + DC * DC + 4 * (threadIdx.x + i * DC_WG));
+    }
+#pragma unroll
+    for (int i = 0; i < DC_V4; i++) {  // the record's 16-column blocks c0 / 16 and c0 / 16 + 1, [64][16] each
+        const int idx = threadIdx.x + i * DC_WG, blk = idx / (DC * 4), w4 = idx % (DC * 4);
+        g.v4[i] = *(const dc_f32x4 *)(tm + DC_VO + (c0 / 16 + blk) * DC * 16 + 4 * w4);
+    }
+    g.lg = threadIdx.x < DC ? tm[DC_C + threadIdx.x] : 0.f;
+}
+
+// A workgroup carries 32 state columns (two 16-column tiles).  Waves 0-3
+// form K S for token rows 16 w (then X), waves 4-7 Q S for token rows
+// 16 (w - 4) (then O); wave w forms D for token rows 16 (w / 2), column tile
+// w % 2; every wave owns state rows 16 w .. 16 w + 15 of both column tiles
+// (8 values per lane for the whole prompt).  X, D and the state are kept
+// transposed in LDS ([column][row]) so that a lane reads its B operands 16
+// bytes at a time.
+template <int HK, int HV>
+__global__ __launch_bounds__(DC_WG) void pf_dc_state_kernel(PfDnArgs a) {
+#pragma clang fp contract(off)
+    constexpr int KP = HK + 4, TP = DC + 4;
+    static_assert(HK == 16 * DC_WAVES && HV % DC_CB == 0 && DC_CB == 32, "a state row tile per wave");
+    __shared__ __attribute__((aligned(16))) float sk[DC][KP];
+    __shared__ __attribute__((aligned(16))) float sq[DC][KP];
+    __shared__ __attribute__((aligned(16))) float stb[DC][TP];
+    __shared__ __attribute__((aligned(16))) float sm[DC][TP];
+    __shared__ __attribute__((aligned(16))) float sst[DC_CB][KP];  // S^T
+    __shared__ __attribute__((aligned(16))) float sxt[DC_CB][TP];  // X^T
+    __shared__ __attribute__((aligned(16))) float sdt[DC_CB][TP];  // D^T
+    __shared__ __attribute__((aligned(16))) float sv[DC][DC_CB];
+    __shared__ float slg[DC];  // c
+    const int vh = blockIdx.x, kh = vh % a.n_kh, c0 = (int)blockIdx.y * DC_CB, nch = (a.T + DC - 1) / DC;
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE, r = lane & 15, kq = lane >> 4;
+    const int VD = a.n_vh * HV;
+    float *S = a.state + (size_t)vh * HK * HV;
+    dc_f32x4 st[2];  // state rows 16 wave + 4 kq + e, columns c0 + 16 ct + r
+#pragma unroll
+    for (int ct = 0; ct < 2; ct++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) st[ct][e] = S[(size_t)(16 * wave + 4 * kq + e) * HV + c0 + 16 * ct + r];
+    // the inputs of chunk ch + 1 are loaded into registers at the start of
+    // chunk ch and stored to LDS after its last LDS read (so no register array
+    // lives across iterations)
+    auto put = [&](const DcStage &g) __attribute__((always_inline)) {
+        dc_store_qk<HK>(g.qk4, sq, sk);
+#pragma unroll
+        for (int i = 0; i < DC_TM4; i++) {
+            const int idx = 4 * (threadIdx.x + i * DC_WG);
+            *(dc_f32x4 *)&stb[idx / DC][idx % DC] = g.tb4[i];
+            *(dc_f32x4 *)&sm[idx / DC][idx % DC] = g.m4[i];
+        }
+#pragma unroll
+        for (int i = 0; i < DC_V4; i++) {
+            const int idx = threadIdx.x + i * DC_WG, blk = idx / (DC * 4), w4 = idx % (DC * 4);
+            *(dc_f32x4 *)&sv[w4 / 4][16 * blk + 4 * (w4 % 4)] = g.v4[i];
+        }
+        if (threadIdx.x < DC) slg[threadIdx.x] = g.lg;
+#pragma unroll
+        for (int ct = 0; ct < 2; ct++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) sst[16 * ct + r][16 * wave + 4 * kq + e] = st[ct][e];
+    };
+    {
+        DcStage g;
+        dc_stage_load(a, g, vh, kh, 0, nch, c0);
+        put(g);
+    }
+    for (int ch = 0; ch < nch; ch++) {
+        const int tb = ch * DC, nb = min(DC, a.T - tb);
+        DcStage g;  // chunk ch + 1
+        if (ch + 1 < nch) dc_stage_load(a, g, vh, kh, ch + 1, nch, c0);
+        __syncthreads();
+        // K S (waves 0-3) or Q S (waves 4-7) for token rows 16 rt, both
+        // column tiles; instruction 4 m + x of a lane sums state row 32 kq + 4 m + x
+        const int rt = wave & 3;
+        dc_f32x4 u[2];
+        {
+            const float *xr = (wave < 4 ? sk : sq)[16 * rt + r] + 32 * kq;
+            float4 xa[8];
+#pragma unroll
+            for (int m = 0; m < 8; m++) xa[m] = *(const float4 *)(xr + 4 * m);
+#pragma unroll
+            for (int ct = 0; ct < 2; ct++) {
+                const float *yr = sst[16 * ct + r] + 32 * kq;
+                float4 yb[8];
+#pragma unroll
+                for (int m = 0; m < 8; m++) yb[m] = *(const float4 *)(yr + 4 * m);
+                dc_f32x4 uc[4] = DC_ZERO4;
+#pragma unroll
+                for (int m = 0; m < 8; m++) dc_mfma4(xa[m], yb[m], uc);
+                u[ct] = dc_sum4(uc);
+            }
+        }
+        if (wave < 4)  // X = V - G (K S), transposed
+#pragma unroll
+            for (int ct = 0; ct < 2; ct++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int t = 16 * rt + 4 * kq + e;
+                    sxt[16 * ct + r][t] = sv[t][16 * ct + r] - expf(slg[t]) * u[ct][e];
+                }
+        __syncthreads();
+        {  // D = Tb X for token rows 16 (wave / 2), column tile wave % 2:
+           // instruction 4 bj + x sums token 16 bj + 4 kq + x
+            const int dr = wave >> 1, dcol = 16 * (wave & 1) + r;
+            dc_f32x4 dc[4] = DC_ZERO4;
+            for (int bj = 0; bj <= dr; bj++)
+                dc_mfma4(*(const float4 *)&stb[16 * dr + r][16 * bj + 4 * kq],
+                         *(const float4 *)&sxt[dcol][16 * bj + 4 * kq], dc);
+            const dc_f32x4 d = dc_sum4(dc);
+#pragma unroll
+            for (int e = 0; e < 4; e++) sdt[dcol][16 * dr + 4 * kq + e] = d[e];
+        }
+        __syncthreads();
+        if (wave >= 4) {  // O = G (Q S) + M D for token rows 16 rt, both column tiles
+#pragma unroll
+            for (int ct = 0; ct < 2; ct++) {
+                dc_f32x4 oc[4] = DC_ZERO4;
+                for (int bj = 0; bj <= rt; bj++)
+                    dc_mfma4(*(const float4 *)&sm[16 * rt + r][16 * bj + 4 * kq],
+                             *(const float4 *)&sdt[16 * ct + r][16 * bj + 4 * kq], oc);
+                const dc_f32x4 o = dc_sum4(oc);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int t = 16 * rt + 4 * kq + e;
+                    if (t < nb) a.o[(size_t)(tb + t) * VD + vh * HV + c0 + 16 * ct + r] = expf(slg[t]) * u[ct][e] + o[e];
+                }
+            }
+        }
+        {  // S' = G_63 S + (diag(F) K)^T D for state rows 16 wave: instruction
+           // 4 m + x sums token 16 m + 4 kq + x
+            const float c63 = slg[DC - 1];
+            float4 ka[4];
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                const int k0 = 16 * m + 4 * kq;
+                ka[m].x = expf(c63 - slg[k0]) * sk[k0][16 * wave + r];
+                ka[m].y = expf(c63 - slg[k0 + 1]) * sk[k0 + 1][16 * wave + r];
+                ka[m].z = expf(c63 - slg[k0 + 2]) * sk[k0 + 2][16 * wave + r];
+                ka[m].w = expf(c63 - slg[k0 + 3]) * sk[k0 + 3][16 * wave + r];
+            }
+            const float g63 = expf(c63);
+#pragma unroll
+            for (int ct = 0; ct < 2; ct++) {
+                dc_f32x4 sc[4] = DC_ZERO4;
+                sc[0] = st[ct] * g63;
+#pragma unroll
+                for (int m = 0; m < 4; m++) dc_mfma4(ka[m], *(const float4 *)&sdt[16 * ct + r][16 * m + 4 * kq], sc);
+                st[ct] = dc_sum4(sc);
+            }
+        }
+        __syncthreads();  // every read of this chunk's LDS inputs is done
+        if (ch + 1 < nch) put(g);
+    }
+#pragma unroll
+    for (int ct = 0; ct < 2; ct++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) S[(size_t)(16 * wave + 4 * kq + e) * HV + c0 + 16 * ct + r] = st[ct][e];
+}
+
+// A prompt of at most 64 tokens is one chunk: pf_dc_single_kernel does the
+// prep kernel's work and the state kernel's in one launch, per (value head,
+// 32 state columns), with every intermediate in LDS (the four workgroups of
+// a value head each form its L, M and inverse).  The state-free products
+// k.k and q.k run in f32 here; K S and Q S, which do not depend on the
+// inverse, run while waves 0-3 invert the diagonal blocks.
+template <int HK, int HV>
+__global__ __launch_bounds__(DC_WG) void pf_dc_single_kernel(PfDnArgs a) {
+#pragma clang fp contract(off)
+    constexpr int KP = HK + 4, TP = DC + 4;
+    static_assert(HK == 16 * DC_WAVES && HV % DC_CB == 0 && DC_CB == 32, "a state row tile per wave");
+    __shared__ __attribute__((aligned(16))) float sk[DC][KP];
+    __shared__ __attribute__((aligned(16))) float sq[DC][KP];
+    __shared__ __attribute__((aligned(16))) float sl[DC][TP];   // L; then X^T and D^T
+    __shared__ __attribute__((aligned(16))) float stt[DC][TP];  // T
+    __shared__ __attribute__((aligned(16))) float sm[DC][TP];   // M
+    __shared__ __attribute__((aligned(16))) float sst[DC_CB][KP];  // S^T
+    __shared__ __attribute__((aligned(16))) float sv[DC][DC_CB];
+    __shared__ float sz[4][16][17], slg[DC], slc[DC];
+    __shared__ __attribute__((aligned(16))) float sbeta[DC];  // read 16 bytes at a time
+    static_assert(2 * DC_CB <= DC, "X^T and D^T fit where L was");
+    float(*sxt)[TP] = sl;
+    float(*sdt)[TP] = sl + DC_CB;
+    const int vh = blockIdx.x, kh = vh % a.n_kh, c0 = (int)blockIdx.y * DC_CB, nb = a.T;
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE, r = lane & 15, kq = lane >> 4;
+    const int KD = a.n_kh * HK, CD = 2 * KD + a.n_vh * HV, VD = a.n_vh * HV;
+    float *S = a.state + (size_t)vh * HK * HV;
+    dc_f32x4 st[2];  // state rows 16 wave + 4 kq + e, columns c0 + 16 ct + r
+    {  // every load issued before any is stored
+        constexpr int V4 = DC * DC_CB / 4 / DC_WG;
+        static_assert(V4 == 1, "one v piece per thread");
+        dc_f32x4 qk4[DC_QK4];
+        dc_load_qk<HK>(a, qk4, 0, nb, kh);
+        const int vt = threadIdx.x / (DC_CB / 4), vc = 4 * (threadIdx.x % (DC_CB / 4));
+        const dc_f32x4 v4 = vt < nb ? *(const dc_f32x4 *)(a.conv_out + (size_t)vt * CD + 2 * KD + vh * HV + c0 + vc)
+                                    : dc_f32x4{0.f, 0.f, 0.f, 0.f};
+        const int t = threadIdx.x;
+        const float b = t < nb ? a.gates[(size_t)t * 3 * a.n_vh + vh] : 0.f;
+        const float g = t < nb ? a.gates[(size_t)t * 3 * a.n_vh + 2 * a.n_vh + vh] : 0.f;
+#pragma unroll
+        for (int ct = 0; ct < 2; ct++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) st[ct][e] = S[(size_t)(16 * wave + 4 * kq + e) * HV + c0 + 16 * ct + r];
+        dc_store_qk<HK>(qk4, sq, sk);
+        *(dc_f32x4 *)&sv[vt][vc] = v4;
+        if (t < DC) {
+            sbeta[t] = b;
+            slg[t] = g;
+        }
+#pragma unroll
+        for (int ct = 0; ct < 2; ct++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) sst[16 * ct + r][16 * wave + 4 * kq + e] = st[ct][e];
+    }
+    __syncthreads();
+    if (wave == 0) slc[lane] = dc_wave_scan(slg[lane]);
+    __syncthreads();
+    // k_t.k_i (into L) or q_t.k_i (into M) of lower 16-block p; instruction
+    // 4 m + x of a lane sums element 32 kq + 4 m + x of the rows
+    auto tile = [&](bool isq, int p) __attribute__((always_inline)) {
+        int bi, bj;
+        dc_lower_block(p, bi, bj);
+        const float *xr = (isq ? sq : sk)[16 * bi + r] + 32 * kq, *yr = sk[16 * bj + r] + 32 * kq;
+        float4 xa[8], yb[8];
+#pragma unroll
+        for (int m = 0; m < 8; m++) {
+            xa[m] = *(const float4 *)(xr + 4 * m);
+            yb[m] = *(const float4 *)(yr + 4 * m);
+        }
+        float ct4[4], bt4[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            ct4[e] = slc[16 * bi + 4 * kq + e];
+            bt4[e] = sbeta[16 * bi + 4 * kq + e];
+        }
+        const float ci = slc[16 * bj + r];
+        dc_f32x4 c4[4] = DC_ZERO4;
+#pragma unroll
+        for (int m = 0; m < 8; m++) dc_mfma4(xa[m], yb[m], c4);
+        const dc_f32x4 acc = dc_sum4(c4);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int t = 16 * bi + 4 * kq + e, i = 16 * bj + r;
+            const float ratio = expf(ct4[e] - ci);
+            if (isq) sm[t][i] = i <= t ? ratio * acc[e] : 0.f;
+            else sl[t][i] = i < t ? bt4[e] * ratio * acc[e] : 0.f;
+        }
+    };
+    for (int p = wave; p < 10; p += DC_WAVES) tile(false, p);
+    __syncthreads();
+    if (wave < 4) dc_invert_diag<TP>(sl, stt, wave, lane);
+    else
+        for (int p = wave - 4; p < 10; p += 4) tile(true, p);
+    // K S (waves 0-3) or Q S (waves 4-7) for token rows 16 rt, both column
+    // tiles; instruction 4 m + x of a lane sums state row 32 kq + 4 m + x
+    const int rt = wave & 3;
+    dc_f32x4 u[2];
+    {
+        const float *xr = (wave < 4 ? sk : sq)[16 * rt + r] + 32 * kq;
+        float4 xa[8];
+#pragma unroll
+        for (int m = 0; m < 8; m++) xa[m] = *(const float4 *)(xr + 4 * m);
+#pragma unroll
+        for (int ct = 0; ct < 2; ct++) {
+            const float *yr = sst[16 * ct + r] + 32 * kq;
+            float4 yb[8];
+#pragma unroll
+            for (int m = 0; m < 8; m++) yb[m] = *(const float4 *)(yr + 4 * m);
+            dc_f32x4 uc[4] = DC_ZERO4;
+#pragma unroll
+            for (int m = 0; m < 8; m++) dc_mfma4(xa[m], yb[m], uc);
+            u[ct] = dc_sum4(uc);
+        }
+    }
+    __syncthreads();
+    dc_invert_below<TP>(sl, stt, sz, wave, r, kq);  // ends with a barrier: L is free
+    if (wave < 4)  // X = V - G (K S), transposed
+#pragma unroll
+        for (int ct = 0; ct < 2; ct++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int t = 16 * rt + 4 * kq + e;
+                sxt[16 * ct + r][t] = sv[t][16 * ct + r] - expf(slc[t]) * u[ct][e];
+            }
+    __syncthreads();
+    {  // D = T diag(beta) X for token rows 16 (wave / 2), column tile wave % 2
+        const int dr = wave >> 1, dcol = 16 * (wave & 1) + r;
+        dc_f32x4 dc[4] = DC_ZERO4;
+        for (int bj = 0; bj <= dr; bj++) {
+            const float4 tr = *(const float4 *)&stt[16 * dr + r][16 * bj + 4 * kq];
+            const float4 bb = *(const float4 *)&sbeta[16 * bj + 4 * kq];
+            dc_mfma4(float4{tr.x * bb.x, tr.y * bb.y, tr.z * bb.z, tr.w * bb.w},
+                     *(const float4 *)&sxt[dcol][16 * bj + 4 * kq], dc);
+        }
+        const dc_f32x4 d = dc_sum4(dc);
+#pragma unroll
+        for (int e = 0; e < 4; e++) sdt[dcol][16 * dr + 4 * kq + e] = d[e];
+    }
+    __syncthreads();
+    if (wave >= 4) {  // O = G (Q S) + M D for token rows 16 rt, both column tiles
+#pragma unroll
+        for (int ct = 0; ct < 2; ct++) {
+            dc_f32x4 oc[4] = DC_ZERO4;
+            for (int bj = 0; bj <= rt; bj++)
+                dc_mfma4(*(const float4 *)&sm[16 * rt + r][16 * bj + 4 * kq],
+                         *(const float4 *)&sdt[16 * ct + r][16 * bj + 4 * kq], oc);
+            const dc_f32x4 o = dc_sum4(oc);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int t = 16 * rt + 4 * kq + e;
+                if (t < nb) a.o[(size_t)t * VD + vh * HV + c0 + 16 * ct + r] = expf(slc[t]) * u[ct][e] + o[e];
+            }
+        }
+    }
+    {  // S' = G_63 S + (diag(F) K)^T D for state rows 16 wave
+        const float c63 = slc[DC - 1];
+        float4 ka[4];
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const int k0 = 16 * m + 4 * kq;
+            ka[m].x = expf(c63 - slc[k0]) * sk[k0][16 * wave + r];
+            ka[m].y = expf(c63 - slc[k0 + 1]) * sk[k0 + 1][16 * wave + r];
+            ka[m].z = expf(c63 - slc[k0 + 2]) * sk[k0 + 2][16 * wave + r];
+            ka[m].w = expf(c63 - slc[k0 + 3]) * sk[k0 + 3][16 * wave + r];
+        }
+        const float g63 = expf(c63);
+#pragma unroll
+        for (int ct = 0; ct < 2; ct++) {
+            dc_f32x4 sc[4] = DC_ZERO4;
+            sc[0] = st[ct] * g63;
+#pragma unroll
+            for (int m = 0; m < 4; m++) dc_mfma4(ka[m], *(const float4 *)&sdt[16 * ct + r][16 * m + 4 * kq], sc);
+            st[ct] = dc_sum4(sc);
+#pragma unroll
+            for (int e = 0; e < 4; e++) S[(size_t)(16 * wave + 4 * kq + e) * HV + c0 + 16 * ct + r] = st[ct][e];
+        }
+    }
+}
+
 // gated RMSNorm (qwen3_5/forward.odin:211-218): per token and value head, out =
 // f16(norm_w[j] (inv o[j]) silu(z[j])), inv = 1 / sqrt(sum o^2 / hv + eps); z
 // from the in_z projection's partial products.  Grid (T, ceil(n_vh / (4
@@ -475,14 +1109,21 @@ bool pf_dn_supported(int hk, int hv, int kernel) { return hk == 128 && hv == 128
 
 hipError_t launch_pf_deltanet(const PfDnArgs &a, hipStream_t st) {
     if (!pf_dn_supported(a.hk, a.hv, a.kernel) || a.T < a.kernel - 1 || a.n_kh <= 0 || a.n_vh % a.n_kh ||
-        (a.chunk != 0 && a.chunk != 16 && a.chunk != 32))
+        (a.chunk != 0 && a.chunk != 16 && a.chunk != 32 && a.chunk != 64) || (a.chunk == 64 && !a.dc))
         return hipErrorInvalidValue;
     const int CD = 2 * a.n_kh * a.hk + a.n_vh * a.hv;
     hipLaunchKernelGGL(pf_dn_conv_kernel<4>, dim3(nblk(CD, WG), nblk(a.T, DN_TT)), dim3(WG), 0, st, a);
     hipLaunchKernelGGL(pf_dn_conv_state_kernel<4>, dim3(nblk(CD, WG)), dim3(WG), 0, st, a);
     hipLaunchKernelGGL(pf_dn_prep_kernel<128>, dim3((unsigned)a.T), dim3(WG), 0, st, a);
     const dim3 dgrid((unsigned)a.n_vh, 128 / 32);
-    if (a.chunk == 16) hipLaunchKernelGGL((pf_dn_chunk_kernel<128, 128, 16>), dgrid, dim3(WG), 0, st, a);
+    if (a.chunk == 64 && a.T <= DC) {
+        hipLaunchKernelGGL((pf_dc_single_kernel<128, 128>), dim3((unsigned)a.n_vh, 128 / DC_CB), dim3(DC_WG), 0, st,
+                           a);
+    } else if (a.chunk == 64) {
+        hipLaunchKernelGGL(pf_dc_prep_kernel<128>, dim3((unsigned)a.n_vh, nblk(a.T, DC)), dim3(DC_WG), 0, st, a);
+        hipLaunchKernelGGL((pf_dc_state_kernel<128, 128>), dim3((unsigned)a.n_vh, 128 / DC_CB), dim3(DC_WG), 0, st,
+                           a);
+    } else if (a.chunk == 16) hipLaunchKernelGGL((pf_dn_chunk_kernel<128, 128, 16>), dgrid, dim3(WG), 0, st, a);
     else if (a.chunk == 32) hipLaunchKernelGGL((pf_dn_chunk_kernel<128, 128, 32>), dgrid, dim3(WG), 0, st, a);
     else hipLaunchKernelGGL((pf_dn_delta_kernel<128, 128>), dim3((unsigned)a.n_vh, 128 / DN_CW), dim3(WG), 0, st, a);
     hipLaunchKernelGGL(pf_dn_gnorm_kernel<128>, dim3((unsigned)a.T, nblk(a.n_vh, (WG / WAVE) * GN_NH)), dim3(WG), 0, st,

@@ -60,7 +60,7 @@ def deltanet_steps_batched(n_k_heads, n_v_heads, head_k_dim, head_v_dim, conv_ke
                            conv_w, a_decay, dt_bias, norm_w, conv_state, rec_state):
     """The same trajectory through oi_deltanet_steps_batched, the batched
     prefill kernels: the delta rule token by token (chunk 0) or in its
-    chunked form over chunks of 16 / 32 tokens.  Returns (out, conv_state,
+    chunked form over chunks of 16 / 32 / 64 tokens.  Returns (out, conv_state,
     rec_state) as deltanet_steps."""
     d = _native.DeltaNetDims(n_k_heads, n_v_heads, head_k_dim, head_v_dim, conv_kernel, eps)
     qkv, z, b, a = _f32(np.atleast_2d(qkv)), _f32(np.atleast_2d(z)), _f32(np.atleast_2d(b)), _f32(np.atleast_2d(a))

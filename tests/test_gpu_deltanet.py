@@ -89,11 +89,13 @@ def _moderate(args):
     return args
 
 
-@pytest.mark.parametrize("chunk,T", [(0, 3), (0, 37), (16, 3), (16, 37), (16, 200), (32, 37), (32, 200)])
+@pytest.mark.parametrize("chunk,T", [(0, 3), (0, 37), (16, 3), (16, 37), (16, 200), (32, 37), (32, 200),
+                                     (64, 3), (64, 37), (64, 64), (64, 200), (64, 512)])
 def test_deltanet_batched_vs_oracle(chunk, T):
     """oi_deltanet_steps_batched (the prefill kernels: conv over the whole
-    trajectory, then the delta rule token by token or in chunks of 16 / 32
-    with a ragged last chunk) against the oracle's same form
+    trajectory, then the delta rule token by token or in chunks of 16 / 32 /
+    64 -- the last on the matrix cores -- with a ragged last chunk) against
+    the oracle's same form
     (ref_deltanet_steps / ref_deltanet_steps_chunked) within 1e-5, and against
     the oracle's token steps within 1e-4 (the chunked form sums in another
     order); the conv window moves values only, bit-identical."""
@@ -112,7 +114,7 @@ def test_deltanet_batched_vs_oracle(chunk, T):
 
 def test_deltanet_batched_rejects_bad_chunk():
     args = _case(np.random.default_rng(1), 2, 2, 128, 128, 4, 8)
-    for chunk in (8, 64, -1):
+    for chunk in (8, 48, -1):
         with pytest.raises(RuntimeError, match="chunk"):
             qwen35.deltanet_steps_batched(*args[:6], chunk, *args[6:])
     with pytest.raises(RuntimeError, match="n_tokens"):

@@ -215,9 +215,18 @@ def test_prefill_then_greedy_matches_oracle(make_model, name):
         r.close()
 
 
-def test_prefill_split_calls_agree(make_model):
+@pytest.mark.parametrize("chunk,bar", [("0", 1e-4), (None, TOL)])
+def test_prefill_split_calls_agree(make_model, monkeypatch, chunk, bar):
     """48 tokens in one call and in two (24 + 24) on the hybrid: the
-    recurrent and conv states carry across chunks as across tokens."""
+    recurrent and conv states carry across chunks as across tokens.  With
+    the delta rule token by token (OI_PREFILL_DN_CHUNK=0) both partitions do
+    the same arithmetic (1e-4); in the default chunked form one 48-token
+    chunk and two 24-token chunks sum in different orders, and the f16
+    staging of the next projections turns those roundings into differences
+    of the size of the oracle bar, which each partition also meets against
+    the oracle (test_prefill_logits_vs_oracle)."""
+    if chunk is not None:
+        monkeypatch.setenv("OI_PREFILL_DN_CHUNK", chunk)
     path = make_model("qwen35-moe-tiny")
     toks = _tokens(11, 48, 2048)
     e, _ = infer.engine_load(path, infer.Engine_Opts(max_ctx=128))
@@ -226,7 +235,9 @@ def test_prefill_split_calls_agree(make_model):
         whole = infer.engine_forward_batch(e, toks, 0).copy()
         infer.engine_forward_batch(e2, toks[:24], 0)
         parts = infer.engine_forward_batch(e2, toks[24:], 24).copy()
-        assert scaled_err(parts, whole) <= 1e-4
+        err = scaled_err(parts, whole)
+        print("split calls, chunk %s: scaled difference %.3g" % (chunk or "default", err))
+        assert err <= bar
     finally:
         infer.engine_destroy(e)
         infer.engine_destroy(e2)
@@ -270,18 +281,20 @@ def test_prefill_expert_kernels_agree(tmp_path, monkeypatch, shape, n):
         assert err <= 1e-5, kind
 
 
-@pytest.mark.parametrize("chunk", ["16", "32"])
+@pytest.mark.parametrize("chunk", ["0", "16", "32"])
 @pytest.mark.parametrize("name,n", [("qwen35-tiny", 40), ("qwen35-hybrid-moe-2layer", 200)])
 def test_prefill_chunked_delta_vs_oracle(make_model, monkeypatch, chunk, name, n):
-    """Prefill with the delta rule of the DeltaNet layers in its chunked form
-    (OI_PREFILL_DN_CHUNK=16 / 32) against the oracle's prefill (the delta
-    rule token by token): the same bars as the default path, and the same
-    greedy continuation on the tiny model."""
+    """Prefill with the delta rule of the DeltaNet layers token by token
+    (OI_PREFILL_DN_CHUNK=0) or in the lane-level chunked form over 16 / 32
+    tokens, instead of the default 64-token chunks on the matrix cores,
+    against the oracle's prefill (the delta rule token by token): the same
+    bars as the default path, and the same greedy continuation on the tiny
+    model."""
     monkeypatch.setenv("OI_PREFILL_DN_CHUNK", chunk)
     path = make_model(name)
     e, r = _engines(path, 256)
     try:
-        toks = _tokens(17, n, r.vocab_size)
+        toks = _tokens(n + 1, n, r.vocab_size)  # the inputs of test_prefill_logits_vs_oracle
         print("case %s n=%d chunk %s" % (name, n, chunk), flush=True)
         got = infer.engine_forward_batch(e, toks, 0).copy()
         ref = r.prefill(toks, 0)
