@@ -366,8 +366,10 @@ void oi_engine_destroy(oi_engine *e) {
     if (e->stream) hipStreamSynchronize(e->stream);
     if (e->gexec) hipGraphExecDestroy(e->gexec);
     if (e->graph) hipGraphDestroy(e->graph);
-    if (e->gexec_s) hipGraphExecDestroy(e->gexec_s);
-    if (e->graph_s) hipGraphDestroy(e->graph_s);
+    for (int m = 0; m < 3; m++) {
+        if (e->gexec_s[m]) hipGraphExecDestroy(e->gexec_s[m]);
+        if (e->graph_s[m]) hipGraphDestroy(e->graph_s[m]);
+    }
     if (e->arena.base) hipFree(e->arena.base);
     if (e->pf_mem) hipFree(e->pf_mem);
     if (e->logits_host) hipHostFree(e->logits_host);
@@ -606,7 +608,7 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
         act += al(QD * 4) + al((size_t)(e->rotary_dim / 2 + 1) * 4) + 2 * al((size_t)CD * 4) + 2 * al((size_t)VD * 4) +
                2 * al((size_t)e->lin_nv * 4) + al((size_t)e->lin_nv * 16);
     if (moe) act += al((size_t)E * 4) + 3 * al(64 * 4) + al((size_t)SF * 4 + 4);
-    act += al(sizeof(SampleState)) + al((size_t)c.vocab_size * 4);  // sampler state and probabilities
+    act += al(sizeof(SampleState)) + al((size_t)c.vocab_size * 4) + al(sample_work_bytes());  // the sampler
     e->arena.size = wbytes + 2 * kv_layer * n_attn + (conv_layer + rec_layer + 512) * n_lin + act + 8192;
     hipError_t he = hipMalloc(&e->arena.base, e->arena.size);
     if (he != hipSuccess) return fail(OI_E_NOMEM, "hipMalloc of " + std::to_string(e->arena.size) + " bytes failed");
@@ -709,6 +711,7 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     e->tokens = (int32_t *)e->arena.take((size_t)(c.seq_len + 1) * 4);
     e->samp = (SampleState *)e->arena.take(sizeof(SampleState));
     e->samp_p = (float *)e->arena.take((size_t)c.vocab_size * 4);
+    e->samp_work = e->arena.take(sample_work_bytes());
     e->rope_cs = (float2 *)e->arena.take((size_t)c.seq_len * (c.head_dim / 2) * 8);
     float *qbuf = nullptr, *inv_freq = nullptr, *lin_qkv = nullptr, *lin_conv = nullptr, *lin_z = nullptr;
     float *lin_out = nullptr, *lin_b = nullptr, *lin_a = nullptr, *lin_ssq = nullptr;
@@ -1617,29 +1620,33 @@ int oi_engine_decode_sample(oi_engine *e, int32_t token, int32_t pos, int32_t n_
     if (n_steps == 0) return OI_OK;
     HIP_TRY(hipSetDevice(e->device));
     const int V = (int)e->cfg.vocab_size;
-    // the token step followed by the sampler, captured once
-    if (e->use_graph && !e->gexec_s) {
+    // the token step followed by the sampler's launches for this mode,
+    // captured once per mode
+    const int mode = sample_mode(s->temperature, s->topp, V);
+    if (e->use_graph && !e->gexec_s[mode]) {
         HIP_TRY(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
         int rc = enqueue_token(e);
-        const hipError_t le =
-            rc ? hipSuccess : launch_sample(e->logits, e->samp_p, V, e->samp, e->state, e->tokens, nullptr, e->stream);
+        const hipError_t le = rc ? hipSuccess
+                                 : launch_sample(e->logits, e->samp_p, V, e->samp, mode, e->samp_work, e->state,
+                                                 e->tokens, nullptr, e->stream);
         hipGraph_t g = nullptr;
         const hipError_t ec = hipStreamEndCapture(e->stream, &g);
         if (rc) return rc;
         if (le != hipSuccess) return fail(OI_E_DEVICE, std::string("launch_sample: ") + hipGetErrorString(le));
         if (ec != hipSuccess) return fail(OI_E_DEVICE, std::string("hipStreamEndCapture: ") + hipGetErrorString(ec));
-        e->graph_s = g;
-        HIP_TRY(hipGraphInstantiate(&e->gexec_s, g, nullptr, nullptr, 0));
+        e->graph_s[mode] = g;
+        HIP_TRY(hipGraphInstantiate(&e->gexec_s[mode], g, nullptr, nullptr, 0));
     }
     HIP_TRY(hipMemcpyAsync(e->samp, s, sizeof(SampleState), hipMemcpyHostToDevice, e->stream));
     int rc = set_state(e, token, pos, n_steps);
     if (rc) return rc;
     for (int i = 0; i < n_steps; i++) {
         if (e->use_graph) {
-            HIP_TRY(hipGraphLaunch(e->gexec_s, e->stream));
+            HIP_TRY(hipGraphLaunch(e->gexec_s[mode], e->stream));
         } else {
             if ((rc = enqueue_token(e))) return rc;
-            HIP_TRY(launch_sample(e->logits, e->samp_p, V, e->samp, e->state, e->tokens, nullptr, e->stream));
+            HIP_TRY(launch_sample(e->logits, e->samp_p, V, e->samp, mode, e->samp_work, e->state, e->tokens, nullptr,
+                                  e->stream));
         }
     }
     HIP_TRY(hipMemcpyAsync(out_tokens, e->tokens, (size_t)n_steps * 4, hipMemcpyDeviceToHost, e->stream));
@@ -1655,16 +1662,18 @@ int oi_sample(const float *logits, int32_t n, oi_sampler *s, int32_t *out_token)
     if (s->n_last < 0 || s->n_last > SAMPLE_WINDOW) return fail(OI_E_ARG, "sampler: n_last outside [0, 64]");
     int dev = 0;
     HIP_TRY(hipGetDevice(&dev));
-    const size_t lb = (size_t)n * 4, al = (lb + 255) & ~(size_t)255;
+    const size_t lb = (size_t)n * 4, al = (lb + 255) & ~(size_t)255, wb = (sample_work_bytes() + 255) & ~(size_t)255;
     uint8_t *buf = nullptr;
-    HIP_TRY(hipMalloc((void **)&buf, 2 * al + sizeof(SampleState) + 256));
+    HIP_TRY(hipMalloc((void **)&buf, 2 * al + wb + sizeof(SampleState) + 256));
     std::unique_ptr<uint8_t, void (*)(uint8_t *)> guard(buf, [](uint8_t *b) { (void)hipFree(b); });
     float *dl = (float *)buf, *dp = (float *)(buf + al);
-    SampleState *ds = (SampleState *)(buf + 2 * al);
-    int32_t *dpick = (int32_t *)(buf + 2 * al + sizeof(SampleState));
+    void *work = buf + 2 * al;
+    SampleState *ds = (SampleState *)(buf + 2 * al + wb);
+    int32_t *dpick = (int32_t *)(buf + 2 * al + wb + sizeof(SampleState));
     HIP_TRY(hipMemcpy(dl, logits, lb, hipMemcpyHostToDevice));
     HIP_TRY(hipMemcpy(ds, s, sizeof(SampleState), hipMemcpyHostToDevice));
-    HIP_TRY(launch_sample(dl, dp, n, ds, nullptr, nullptr, dpick, nullptr));
+    HIP_TRY(launch_sample(dl, dp, n, ds, sample_mode(s->temperature, s->topp, n), work, nullptr, nullptr, dpick,
+                          nullptr));
     HIP_TRY(hipMemcpy(out_token, dpick, 4, hipMemcpyDeviceToHost));
     HIP_TRY(hipMemcpy(s, ds, sizeof(SampleState), hipMemcpyDeviceToHost));
     return OI_OK;

@@ -91,8 +91,9 @@ struct oi_engine {
     // [vocab], and the token step + sampler graph
     oi::SampleState *samp = nullptr;
     float *samp_p = nullptr;
-    hipGraph_t graph_s = nullptr;
-    hipGraphExec_t gexec_s = nullptr;
+    void *samp_work = nullptr;
+    hipGraph_t graph_s[3] = {nullptr, nullptr, nullptr};  // the step + sampler, per sample_mode
+    hipGraphExec_t gexec_s[3] = {nullptr, nullptr, nullptr};
     int last_pos = 0;
     size_t weight_bytes = 0;
     float *inv_freq = nullptr;  // Qwen3.5 partial RoPE frequencies [rotary_dim / 2]

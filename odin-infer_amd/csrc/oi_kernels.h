@@ -169,11 +169,16 @@ int attn_max_splits();
 int attn_plan(int head_dim, int n_kv_heads, int seq_len, int *chunk, bool fixed);
 hipError_t launch_dequant(const DMat &m, float *out, hipStream_t st);
 // One draw of the sampler (sample.hip) from logits[0, n); p: n floats of
-// scratch.  With `state` set the pick advances the token loop (token, pos,
-// step, pending as the greedy reduction does) and is stored at
-// tokens_out[step]; `pick`, if set, receives it too.
-hipError_t launch_sample(const float *logits, float *p, int n, SampleState *ss, int32_t *state, int32_t *tokens_out,
-                         int32_t *pick, hipStream_t st);
+// scratch, work: sample_work_bytes() of scratch.  mode: sample_mode() of the
+// state's temperature and topp (the launch sequence depends on it).  With
+// `state` set the pick advances the token loop (token, pos, step, pending as
+// the greedy reduction does) and is stored at tokens_out[step]; `pick`, if
+// set, receives it too.
+enum { SAMPLE_GREEDY = 0, SAMPLE_MULT = 1, SAMPLE_TOPP = 2 };
+int sample_mode(float temperature, float topp, int n);
+size_t sample_work_bytes();
+hipError_t launch_sample(const float *logits, float *p, int n, SampleState *ss, int mode, void *work, int32_t *state,
+                         int32_t *tokens_out, int32_t *pick, hipStream_t st);
 int sample_max_vocab();  // largest n launch_sample takes
 // f16 head-major cache [n_kv][seq_len][hd], positions [0, n) <-> f32 rows
 // [n][n_kv * hd]; to_f32: cache -> rows, else rows -> cache (RNE)

@@ -2,16 +2,16 @@
 // 68-199, without the JSON grammar mask), so a sampled decode loop needs no
 // logits on the host.
 //
-// One workgroup of 1024 threads (16 waves) per draw.  Wave w owns the index
-// range [w*W, (w+1)*W) (W a multiple of 1024) and walks it 1024 elements at a
-// time, each lane loading four 16-byte groups, so every pass is coalesced and
-// per-wave totals come in index order.  (One workgroup streams the 600 KB of
-// a 150k vocabulary at ~25 GB/s -- the logits come from the other XCDs' L2
-// through the MALL -- so a draw costs 50 us at temperature 0 and ~400 us with
-// top-p on the Qwen3 vocabulary.)  Steps, in the reference's order:
+// A draw is a short sequence of launches over G workgroups, each owning a
+// contiguous slice of SLICE = 2048 logits (75 workgroups at the Qwen3
+// vocabulary), so every pass over the vocabulary is spread over the chip
+// instead of one CU (one workgroup reads the 600 KB of logits, written by the
+// vocabulary GEMV on all eight XCDs, at ~25 GB/s).  Values that one launch
+// hands to the next (per-workgroup partials, histograms, the selection in
+// progress) live in a SampleWork record in device memory.  Steps, in the
+// reference's order:
 //   1. repetition penalty on each distinct recent token (positive logits
-//      divided, others multiplied), sampler.odin:142-160 -- the tokens are
-//      marked in an LDS bitmap so the pass over the logits stays one read;
+//      divided, others multiplied), sampler.odin:142-160;
 //   2. temperature 0: first maximum (sample_argmax :79-89); otherwise
 //      x / temperature, softmax (max, exp(x - max), sum, divide; ops.odin
 //      :21-37), one xorshift draw (random_u32 / random_f32 :68-77);
@@ -21,16 +21,21 @@
 //      first), cut after the first prefix whose mass exceeds topp, and the
 //      coin times that mass located in the same order (sample_topp :106-139).
 // Running masses are exact: each probability is taken as a 64-bit fixed-point
-// number (p * 2^40, truncated) and summed in integers, so the result does not
+// number (p * 2^40, rounded) and summed in integers, so the result does not
 // depend on the summation order (the reference's sequential f32 sums carry
 // ~1e-5 of rounding over 150k terms; picks can differ from it only when the
-// target lies within that rounding of a boundary).  The top-p order is never
+// target lies within that rounding of a boundary).  The softmax sum is an f32
+// sum in a fixed order (per workgroup, then the workgroups in order), the
+// same in every workgroup that needs it.  The top-p order is never
 // materialised: the boundary element is found by radix selection over the
 // float bits of p (positive floats order as their bit patterns), four 8-bit
-// digits from the top, with per-bucket count, mass and lowest index in LDS.
-// A lane adds runs of equal buckets before touching LDS, so the flat
-// distributions that put most elements in one bucket do not serialise on one
-// address.  The first digit's histogram is shared by both selections.
+// digits from the top, one launch per digit, each workgroup adding its
+// candidates' per-bucket count, mass and lowest index to a device histogram
+// and every workgroup walking the previous digit's histogram the same way.
+//
+// Launches per draw: temperature 0: 2; multinomial: 4; top-p: 11.  The
+// sequence depends only on the mode (sample_mode), which the caller knows,
+// so a captured graph holds one mode's sequence.
 
 #include "device_common.h"
 
@@ -38,8 +43,10 @@ namespace oi {
 
 namespace {
 
-constexpr int SWG = 1024, SWAVES = SWG / WAVE;
-constexpr int SAMPLE_MAX_VOCAB = 1 << 18;  // LDS penalty bitmap: 32 KB
+constexpr int SB = 256, SBW = SB / WAVE;   // threads per workgroup, waves
+constexpr int SLICE = 2048;                // logits per workgroup: two blocks of 4 per thread
+constexpr int SAMPLE_MAX_VOCAB = 1 << 18;
+constexpr int MAXG = SAMPLE_MAX_VOCAB / SLICE;
 
 // p * 2^40 rounded to the nearest integer (the scaling is exact in f32, rintf
 // rounds the fraction), so the fixed-point total is unbiased against the f32 sum
@@ -51,118 +58,217 @@ struct Hist {
     unsigned long long mass[256];
 };
 
-struct Smem {
-    uint32_t pen_bits[SAMPLE_MAX_VOCAB / 32];
-    Hist h, h3;  // the current digit's histogram; the first digit's, kept
-    uint64_t wtot[SWAVES];
-    float fv[SWAVES];
-    int iv[SWAVES];
-    int pen_tok[SAMPLE_WINDOW];
-    float pen_val[SAMPLE_WINDOW];
-    uint64_t total, above, u64b;
-    int n_pen, sel, pick, ib;
-    float fb;
+// The selection in progress, handed from one digit's launch to the next
+// (stage k reads slot k and writes slot k + 1, so no launch overwrites what
+// another workgroup of the same launch still has to read).
+struct Sel {
+    uint32_t prefix, mask, tie_lo, tie_cnt;
+    unsigned long long above, target, c1;
+    int32_t all, done, pad0, pad1;  // all: the candidates' whole mass within topp; done: pick made
+};
+
+constexpr int NHIST = 7;  // digit histograms: boundary 3..0 -> 0..3, coin 2..0 -> 4..6
+constexpr int NSEL = 12;
+struct SampleWork {
+    Hist h[NHIST];
+    float pmax[MAXG], psum[MAXG];
+    int32_t pidx[MAXG];
+    uint32_t pties[MAXG];
+    unsigned long long pmass[MAXG];
+    Sel sel[NSEL];
     uint32_t coin_k;
 };
 
-// sums over waves in wave order (a wave's value from its lane 0)
-__device__ uint64_t waves_excl_scan(uint64_t v, Smem &s, uint64_t *total) {
-    const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
-    if (lane == 0) s.wtot[w] = v;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint64_t run = 0;
-        for (int i = 0; i < SWAVES; i++) {
-            const uint64_t t = s.wtot[i];
-            s.wtot[i] = run;
-            run += t;
+__host__ __device__ __forceinline__ int wg_count(int n) { return (n + SLICE - 1) / SLICE; }
+
+// The thread's elements: block k (0, 1) holds base + 1024 k + 4 tid + x, so
+// in index order a workgroup's elements are block 0 by thread, then block 1.
+__device__ __forceinline__ int elem(int base, int k, int x) { return base + 1024 * k + 4 * (int)threadIdx.x + x; }
+
+__device__ __forceinline__ void load8(const float *src, int base, int n, float (&v)[2][4]) {
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int i = elem(base, k, 0);
+        if (i + 3 < n) {
+            const float4 q = *(const float4 *)(src + i);
+            v[k][0] = q.x;
+            v[k][1] = q.y;
+            v[k][2] = q.z;
+            v[k][3] = q.w;
+        } else {
+#pragma unroll
+            for (int x = 0; x < 4; x++) v[k][x] = i + x < n ? src[i + x] : 0.f;
         }
-        s.total = run;
     }
-    __syncthreads();
-    const uint64_t r = s.wtot[w];
-    if (total) *total = s.total;
-    __syncthreads();
-    return r;
 }
-
-__device__ float wave_max_f(float v) {
+__device__ __forceinline__ void store8(float *dst, int base, int n, const float (&v)[2][4]) {
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
-    return v;
-}
-
-__device__ float block_max(float v, Smem &s) {
-    v = wave_max_f(v);
-    if ((threadIdx.x & (WAVE - 1)) == 0) s.fv[threadIdx.x / WAVE] = v;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float m = s.fv[0];
-        for (int i = 1; i < SWAVES; i++) m = fmaxf(m, s.fv[i]);
-        s.fb = m;
+    for (int k = 0; k < 2; k++) {
+        const int i = elem(base, k, 0);
+        if (i + 3 < n) *(float4 *)(dst + i) = float4{v[k][0], v[k][1], v[k][2], v[k][3]};
+        else
+#pragma unroll
+            for (int x = 0; x < 4; x++)
+                if (i + x < n) dst[i + x] = v[k][x];
     }
-    __syncthreads();
-    const float r = s.fb;
-    __syncthreads();
-    return r;
 }
 
-// sum in a fixed order: lanes by a butterfly, waves in order
-__device__ float block_sum(float v, Smem &s) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
-    if ((threadIdx.x & (WAVE - 1)) == 0) s.fv[threadIdx.x / WAVE] = v;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float m = 0.f;
-        for (int i = 0; i < SWAVES; i++) m += s.fv[i];
-        s.fb = m;
-    }
-    __syncthreads();
-    const float r = s.fb;
-    __syncthreads();
-    return r;
-}
-
-__device__ uint64_t wave_sum_u64(uint64_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
-    return v;
-}
+struct Lds {
+    Hist h;
+    float fv[SBW];
+    int iv[SBW];
+    unsigned long long uv[SBW];
+    uint32_t pen_bits[SLICE / 32];
+    int pen_tok[SAMPLE_WINDOW];
+    float pen_val[SAMPLE_WINDOW];
+    int n_pen, pick;
+    Sel s;
+};
 
 // (value, index) maximum with the lower index on ties; NaN never wins
-__device__ int block_argmax(float v, int i, Smem &s) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(v, o, WAVE);
-        const int oi = __shfl_xor(i, o, WAVE);
-        if (ov > v || (ov == v && oi < i)) {
-            v = ov;
-            i = oi;
-        }
+__device__ __forceinline__ void argmax_combine(float &v, int &i, float ov, int oi) {
+    if (ov > v || (ov == v && oi < i)) {
+        v = ov;
+        i = oi;
     }
+}
+__device__ void block_argmax(float &v, int &i, Lds &s) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) argmax_combine(v, i, __shfl_xor(v, o, WAVE), __shfl_xor(i, o, WAVE));
     if ((threadIdx.x & (WAVE - 1)) == 0) {
         s.fv[threadIdx.x / WAVE] = v;
         s.iv[threadIdx.x / WAVE] = i;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        float bv = s.fv[0];
-        int bi = s.iv[0];
-        for (int w = 1; w < SWAVES; w++)
-            if (s.fv[w] > bv || (s.fv[w] == bv && s.iv[w] < bi)) {
-                bv = s.fv[w];
-                bi = s.iv[w];
-            }
-        s.pick = bi == 0x7FFFFFFF ? 0 : bi;
+    v = s.fv[0];
+    i = s.iv[0];
+    for (int w = 1; w < SBW; w++) argmax_combine(v, i, s.fv[w], s.iv[w]);
+    __syncthreads();
+}
+// f32 sum in a fixed order: the thread's own elements in order, lanes by a
+// butterfly, waves in order
+__device__ float block_sum(float v, Lds &s) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    if ((threadIdx.x & (WAVE - 1)) == 0) s.fv[threadIdx.x / WAVE] = v;
+    __syncthreads();
+    float r = 0.f;
+    for (int w = 0; w < SBW; w++) r += s.fv[w];
+    __syncthreads();
+    return r;
+}
+__device__ unsigned long long block_sum_u64(unsigned long long v, Lds &s) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    if ((threadIdx.x & (WAVE - 1)) == 0) s.uv[threadIdx.x / WAVE] = v;
+    __syncthreads();
+    unsigned long long r = 0;
+    for (int w = 0; w < SBW; w++) r += s.uv[w];
+    __syncthreads();
+    return r;
+}
+// exclusive prefix over the threads in thread order (and the total)
+__device__ unsigned long long block_excl_scan(unsigned long long v, Lds &s, unsigned long long *total) {
+    const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+    unsigned long long incl = v;
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) {
+        const unsigned long long y = __shfl_up(incl, o, WAVE);
+        if (lane >= o) incl += y;
+    }
+    if (lane == WAVE - 1) s.uv[w] = incl;
+    __syncthreads();
+    unsigned long long before = 0, tot = 0;
+    for (int i = 0; i < SBW; i++) {
+        if (i < w) before += s.uv[i];
+        tot += s.uv[i];
     }
     __syncthreads();
+    *total = tot;
+    return before + incl - v;
+}
+
+// The first element of the workgroup's slice, in index order, at which
+// carry + running weight exceeds target (weights wt[k][x] of the thread's
+// elements); -1 if none.  Every thread gets the result.
+__device__ int block_find(const unsigned long long (&wt)[2][4], int base, unsigned long long carry,
+                          unsigned long long target, Lds &s) {
+    if (threadIdx.x == 0) s.pick = -1;
+    __syncthreads();
+    for (int k = 0; k < 2; k++) {
+        const unsigned long long mine = wt[k][0] + wt[k][1] + wt[k][2] + wt[k][3];
+        unsigned long long tot;
+        const unsigned long long before = block_excl_scan(mine, s, &tot);
+        if (carry + before <= target && target < carry + before + mine) {  // exactly one thread
+            unsigned long long run = carry + before;
+            for (int x = 0; x < 4; x++) {
+                run += wt[k][x];
+                if (run > target) {
+                    s.pick = elem(base, k, x);
+                    break;
+                }
+            }
+        }
+        __syncthreads();
+        if (s.pick >= 0) break;
+        carry += tot;
+    }
     const int r = s.pick;
     __syncthreads();
     return r;
 }
 
-// A lane's run of equal buckets, added to LDS when the bucket changes.
+// Bucket of h where the running mass from the top, starting at *above, first
+// exceeds target; -1 if none.  *above becomes the mass of the higher buckets.
+// One wave (wave 0) walks; the result goes to every thread.
+__device__ int walk_buckets(const Hist &h, unsigned long long target, unsigned long long *above, Lds &s) {
+    const int lane = threadIdx.x & (WAVE - 1);
+    if (threadIdx.x < WAVE) {
+        unsigned long long m[4], sum = 0;  // buckets 255 - 4 lane - x, descending
+#pragma unroll
+        for (int x = 0; x < 4; x++) {
+            m[x] = h.mass[255 - 4 * lane - x];
+            sum += m[x];
+        }
+        unsigned long long incl = sum;
+#pragma unroll
+        for (int o = 1; o < WAVE; o <<= 1) {
+            const unsigned long long y = __shfl_up(incl, o, WAVE);
+            if (lane >= o) incl += y;
+        }
+        const unsigned long long base = *above + incl - sum;
+        const unsigned long long bal = __ballot(base + sum > target);
+        if (bal == 0) {
+            if (lane == 0) {
+                s.pick = -1;
+                s.s.above = *above + __shfl(incl, WAVE - 1, WAVE);
+            }
+        } else {
+            const int L = __ffsll((long long)bal) - 1;
+            if (lane == L) {
+                unsigned long long run = base;
+                int sel = -1;
+                for (int x = 0; x < 4; x++) {
+                    if (run + m[x] > target) {
+                        sel = 255 - 4 * lane - x;
+                        break;
+                    }
+                    run += m[x];
+                }
+                s.pick = sel;
+                s.s.above = run;
+            }
+        }
+    }
+    __syncthreads();
+    const int sel = s.pick;
+    *above = s.s.above;
+    __syncthreads();
+    return sel;
+}
+
+// A thread's run of equal buckets, added to LDS when the bucket changes
+// (flat distributions put most elements of a slice in one bucket).
 struct Run {
     int b = -1;
     uint32_t c = 0, lo = 0;
@@ -179,7 +285,7 @@ struct Run {
             b = bucket;
             c = 0;
             m = 0;
-            lo = (uint32_t)i;  // elements come in increasing index order per lane
+            lo = (uint32_t)i;  // a thread's elements come in increasing index order
         }
         c++;
         m += mass;
@@ -187,316 +293,403 @@ struct Run {
 };
 
 __device__ void hist_clear(Hist &h) {
-    for (int i = threadIdx.x; i < 256; i += SWG) {
+    for (int i = threadIdx.x; i < 256; i += SB) {
         h.cnt[i] = 0;
         h.lo[i] = 0xFFFFFFFFu;
         h.mass[i] = 0;
     }
 }
 
-struct Range {
-    int b0, b1;  // this wave's index range
+// digit d histogram of the slice's candidates whose bits match prefix under
+// mask, added to the device histogram g
+__device__ void hist_digit(const float *p, int base, int n, float cutoff, int d, uint32_t prefix, uint32_t mask,
+                           Hist *g, Lds &s) {
+    hist_clear(s.h);
+    float v[2][4];
+    load8(p, base, n, v);
+    __syncthreads();
+    Run run;
+#pragma unroll
+    for (int k = 0; k < 2; k++)
+#pragma unroll
+        for (int x = 0; x < 4; x++) {
+            const int i = elem(base, k, x);
+            const uint32_t key = __float_as_uint(v[k][x]);
+            if (i < n && v[k][x] >= cutoff && (key & mask) == prefix)
+                run.add(s.h, (int)((key >> (8 * d)) & 255u), i, fix40(v[k][x]));
+        }
+    run.flush(s.h);
+    __syncthreads();
+    for (int b = threadIdx.x; b < 256; b += SB)
+        if (s.h.cnt[b]) {
+            atomicAdd(&g->cnt[b], s.h.cnt[b]);
+            atomicAdd(&g->mass[b], s.h.mass[b]);
+            atomicMin(&g->lo[b], s.h.lo[b]);
+        }
+}
+
+__device__ __forceinline__ float cutoff_of(const SampleState *ss, int n) {
+    return (1.0f - ss->topp) / (float)(n - 1);
+}
+
+// The pick: record_token (sampler.odin:50-56) and the token loop's state.
+// One thread.
+__device__ void finalize(int pick, SampleState *ss, int32_t *state, int32_t *tokens_out, int32_t *pick_out) {
+    const float pen = ss->penalty < 1.0f ? 1.0f : ss->penalty;
+    if (ss->record && pen != 1.0f) {
+        int nl = min(ss->n_last, SAMPLE_WINDOW);
+        if (nl == SAMPLE_WINDOW) {
+            for (int i = 1; i < SAMPLE_WINDOW; i++) ss->last[i - 1] = ss->last[i];
+            nl--;
+        }
+        ss->last[nl] = pick;
+        ss->n_last = nl + 1;
+    }
+    if (state) {  // advance the token loop as the greedy reduction does
+        const int step = state[ST_STEP];
+        if (tokens_out && step >= 0 && step < state[ST_CAP]) tokens_out[step] = pick;
+        state[ST_STEP] = step + 1;
+        state[ST_TOKEN] = pick;
+        state[ST_POS] = state[ST_POS] + 1;
+        state[ST_PENDING] = 0;
+    }
+    if (pick_out) *pick_out = pick;
+}
+
+struct SArgs {
+    const float *logits;
+    float *p;
+    int n;
+    SampleState *ss;
+    SampleWork *w;
+    int32_t *state, *tokens_out, *pick_out;
 };
 
-// Calls f(i, src[i]) for the wave's range in increasing index order per
-// lane.  A lane takes 4 consecutive elements of each 256-element group and
-// loads 4 groups (16 values) at once, so 4 16-byte loads are in flight.
-constexpr int GROUP = 4 * WAVE, BATCH = 4 * GROUP;
-
-template <class F>
-__device__ __forceinline__ void for_each(const float *src, Range r, F f) {
-    const int lane = threadIdx.x & (WAVE - 1);
-    for (int base = r.b0; base < r.b1; base += BATCH) {
-        float v[16];
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int i = base + GROUP * u + 4 * lane;
-            if (i + 3 < r.b1) {
-                const float4 q = *(const float4 *)(src + i);
-                v[4 * u] = q.x;
-                v[4 * u + 1] = q.y;
-                v[4 * u + 2] = q.z;
-                v[4 * u + 3] = q.w;
-            } else {
-#pragma unroll
-                for (int k = 0; k < 4; k++) v[4 * u + k] = i + k < r.b1 ? src[i + k] : 0.f;
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < 4; u++)
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const int i = base + GROUP * u + 4 * lane + k;
-                if (i < r.b1) f(i, v[4 * u + k]);
-            }
-    }
-}
-
-// digit d histogram of the candidates whose key matches prefix under mask
-__device__ void hist_pass(const float *p, Range r, float cutoff, int d, uint32_t prefix, uint32_t mask, Hist &h) {
-    Run run;
-    for_each(p, r, [&](int i, float v) {
-        const uint32_t k = __float_as_uint(v);
-        if (v >= cutoff && (k & mask) == prefix) run.add(h, (int)((k >> (8 * d)) & 255u), i, fix40(v));
-    });
-    run.flush(h);
-}
-
-// Index order within a 1024-element batch: group u, lane, element k.  The
-// first element of the wave's range, in index order, at which
-// carry + running weight(i) exceeds target, where weight(i, v) is given;
-// -1 if none.  *carry: the weight before the range on entry.
-template <class Wt>
-__device__ int wave_find(const float *src, Range r, uint64_t carry, uint64_t target, Wt weight) {
-    const int lane = threadIdx.x & (WAVE - 1);
-    for (int base = r.b0; base < r.b1; base += GROUP) {
-        const int i0 = base + 4 * lane;
-        uint64_t wk[4], lsum = 0;
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            wk[k] = i0 + k < r.b1 ? weight(i0 + k, src[i0 + k]) : 0;
-            lsum += wk[k];
-        }
-        uint64_t incl = lsum;
-#pragma unroll
-        for (int o = 1; o < WAVE; o <<= 1) {
-            const uint64_t y = __shfl_up(incl, o, WAVE);
-            if (lane >= o) incl += y;
-        }
-        const uint64_t bal = __ballot(carry + incl > target);
-        if (bal) {
-            const int L = __ffsll((long long)bal) - 1;
-            uint64_t run = carry + __shfl(incl - lsum, L, WAVE);
-            int found = -1;
-            if (lane == L)
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    run += wk[k];
-                    if (found < 0 && run > target) found = i0 + k;
-                }
-            return __shfl(found, L, WAVE);
-        }
-        carry += __shfl(incl, WAVE - 1, WAVE);
-    }
-    return -1;
-}
-
-// Bucket of digit d (from the top) where the running mass, starting at
-// *above, first exceeds target; -1 if none.  *above becomes the mass of the
-// higher buckets.  One thread; the result is broadcast through s.
-__device__ int walk_buckets(const Hist &h, uint64_t target, uint64_t *above, Smem &s) {
-    if (threadIdx.x == 0) {
-        uint64_t run = *above;
-        int sel = -1;
-        for (int b = 255; b >= 0; b--) {
-            if (!h.cnt[b]) continue;
-            if (run + h.mass[b] > target) {
-                sel = b;
-                break;
-            }
-            run += h.mass[b];
-        }
-        s.sel = sel;
-        s.above = run;
-    }
-    __syncthreads();
-    const int sel = s.sel;
-    *above = s.above;
-    __syncthreads();
-    return sel;
-}
-
-// The first element, in the order (p descending, index ascending) over the
-// candidates p >= cutoff, at which the running mass exceeds `target`; -1 if
-// the candidates' whole mass does not.  *through: the running mass including
-// that element.  h3: the candidates' first-digit histogram.
-__device__ int select_desc(const float *p, Range r, float cutoff, uint64_t target, const Hist &h3, Smem &s,
-                           uint64_t *through) {
-    const int lane = threadIdx.x & (WAVE - 1);
-    uint64_t above = 0;
-    int sel = walk_buckets(h3, target, &above, s);
-    if (sel < 0) return -1;
-    uint32_t prefix = (uint32_t)sel << 24, mask = 0xFF000000u;
-    uint32_t tie_lo = h3.lo[sel], tie_cnt = h3.cnt[sel];
-    for (int d = 2; d >= 0; d--) {
-        hist_clear(s.h);
-        __syncthreads();
-        hist_pass(p, r, cutoff, d, prefix, mask, s.h);
-        __syncthreads();
-        sel = walk_buckets(s.h, target, &above, s);
-        if (sel < 0) return -1;  // unreachable: the bucket above held the crossing
-        prefix |= (uint32_t)sel << (8 * d);
-        mask |= 255u << (8 * d);
-        tie_lo = s.h.lo[sel];
-        tie_cnt = s.h.cnt[sel];
-        __syncthreads();
-    }
-    // equal probabilities in index order: the j-th crosses
-    const uint64_t P = fix40(__uint_as_float(prefix));
-    const uint64_t j = P ? (target - above) / P : 0;
-    *through = above + (j + 1) * P;
-    if (j == 0 || tie_cnt <= 1) return (int)tie_lo;
-    // rank j among the ties: per-wave counts, then the wave holding it
-    uint64_t c = 0;
-    for_each(p, r, [&](int, float v) { c += __float_as_uint(v) == prefix; });
-    const uint64_t mine = wave_sum_u64(c);
-    const uint64_t before = waves_excl_scan(mine, s, nullptr);
-    if (before <= j && j < before + mine) {
-        const int f = wave_find(p, r, before, j, [&](int, float v) -> uint64_t { return __float_as_uint(v) == prefix; });
-        if (lane == 0) s.pick = f;
-    }
-    __syncthreads();
-    const int res = s.pick;
-    __syncthreads();
-    return res;
-}
-
-__global__ __launch_bounds__(SWG) void sample_kernel(const float *logits, float *p, int n, SampleState *ss,
-                                                     int32_t *state, int32_t *tokens_out, int32_t *pick_out) {
+// 1. Penalty (distinct recent tokens, each once) and temperature into p; the
+// slice's first maximum.  Workgroup 0 also clears the digit histograms.
+__global__ __launch_bounds__(SB) void sample_penalty_kernel(SArgs a) {
 #pragma clang fp contract(off)
-    __shared__ Smem s;
-    const int tid = threadIdx.x, lane = tid & (WAVE - 1), w = tid / WAVE;
-    const int W = ((n + SWAVES - 1) / SWAVES + BATCH - 1) / BATCH * BATCH;
-    const Range r{min(n, w * W), min(n, (w + 1) * W)};
+    __shared__ Lds s;
+    const int base = blockIdx.x * SLICE, tid = threadIdx.x;
+    const SampleState *ss = a.ss;
     // enable_repeat_penalty's clamp (sampler.odin:42-44) applied here too, so a
     // C caller's penalty below 1 acts as 1 (off) rather than dividing by it
-    const float T = ss->temperature, topp = ss->topp, pen = ss->penalty < 1.0f ? 1.0f : ss->penalty;
-    for (int i = tid; i < (n + 31) / 32; i += SWG) s.pen_bits[i] = 0;
-    __syncthreads();
-    if (tid == 0) {  // distinct recent tokens and their penalised logits
-        int np = 0;
-        if (pen != 1.0f)
-            for (int i = 0; i < ss->n_last && i < SAMPLE_WINDOW; i++) {
-                const int tok = ss->last[i];
-                if (tok < 0 || tok >= n) continue;
-                bool dup = false;
-                for (int j = 0; j < np; j++) dup |= s.pen_tok[j] == tok;
-                if (dup) continue;
-                const float v = logits[tok];
-                s.pen_tok[np] = tok;
-                s.pen_val[np] = v > 0.f ? v / pen : v * pen;
-                s.pen_bits[tok >> 5] |= 1u << (tok & 31);
-                np++;
+    const float T = ss->temperature, pen = ss->penalty < 1.0f ? 1.0f : ss->penalty;
+    if (blockIdx.x == 0)
+        for (int h = 0; h < NHIST; h++)
+            for (int i = tid; i < 256; i += SB) {
+                a.w->h[h].cnt[i] = 0;
+                a.w->h[h].lo[i] = 0xFFFFFFFFu;
+                a.w->h[h].mass[i] = 0;
             }
-        s.n_pen = np;
-        s.pick = 0;
+    for (int i = tid; i < SLICE / 32; i += SB) s.pen_bits[i] = 0;
+    if (tid == 0) s.n_pen = 0;
+    __syncthreads();
+    const int nl = min(ss->n_last, SAMPLE_WINDOW);
+    if (pen != 1.0f && tid < nl) {
+        const int tok = ss->last[tid];
+        bool dup = false;
+        for (int j = 0; j < tid; j++) dup |= ss->last[j] == tok;
+        if (!dup && tok >= base && tok < base + SLICE && tok < a.n) {
+            const float v = a.logits[tok];
+            const int slot = atomicAdd(&s.n_pen, 1);
+            s.pen_tok[slot] = tok;
+            s.pen_val[slot] = v > 0.f ? v / pen : v * pen;
+            atomicOr(&s.pen_bits[(tok - base) >> 5], 1u << ((tok - base) & 31));
+        }
     }
     __syncthreads();
+    float v[2][4];
+    load8(a.logits, base, a.n, v);
     const bool greedy = T == 0.0f;
-    // x = value (/ T) into p; the lane's maximum (first index on ties)
     float m = -INFINITY;
     int mi = 0x7FFFFFFF;
-    for_each(logits, r, [&](int i, float v) {
-        if (s.pen_bits[i >> 5] & (1u << (i & 31)))
-            for (int k = 0; k < s.n_pen; k++)
-                if (s.pen_tok[k] == i) v = s.pen_val[k];
-        if (!greedy) v = v / T;
-        p[i] = v;
-        if (v > m) {
-            m = v;
-            mi = i;
+#pragma unroll
+    for (int k = 0; k < 2; k++)
+#pragma unroll
+        for (int x = 0; x < 4; x++) {
+            const int i = elem(base, k, x);
+            if (i >= a.n) continue;
+            float x0 = v[k][x];
+            if (s.pen_bits[(i - base) >> 5] & (1u << ((i - base) & 31)))
+                for (int q = 0; q < s.n_pen; q++)
+                    if (s.pen_tok[q] == i) x0 = s.pen_val[q];
+            if (!greedy) x0 = x0 / T;
+            v[k][x] = x0;
+            argmax_combine(m, mi, x0, i);
         }
-    });
-    int pick;
-    if (greedy) {
-        pick = block_argmax(m, mi, s);
-    } else {
-        const float mx = block_max(m, s);
-        float sum = 0.f;
-        for_each(p, r, [&](int i, float x) {
-            const float e = expf(x - mx);
-            p[i] = e;
-            sum += e;
-        });
-        const float tot = block_sum(sum, s);
-        if (tid == 0) {  // random_f32 (sampler.odin:68-77)
-            uint64_t x = ss->rng;
-            x ^= x >> 12;
-            x ^= x << 25;
-            x ^= x >> 27;
-            ss->rng = x;
-            s.coin_k = (uint32_t)((x * 0x2545F4914F6CDD1Dull) >> 32) >> 8;  // coin = coin_k / 2^24
-        }
-        const bool mult = !(topp > 0.f && topp < 1.f) || n == 1;
-        const float cutoff = mult ? 0.f : (1.0f - topp) / (float)(n - 1);
-        if (!mult) hist_clear(s.h3);
-        __syncthreads();
-        const uint64_t coin_k = s.coin_k;
-        // p = e / sum; the wave's mass (index order) or the first digit's histogram
-        uint64_t wm = 0;
-        Run run;
-        for_each(p, r, [&](int i, float e) {
-            const float q = e / tot;
-            p[i] = q;
-            if (mult) wm += fix40(q);
-            else if (q >= cutoff) run.add(s.h3, (int)(__float_as_uint(q) >> 24), i, fix40(q));
-        });
-        if (!mult) run.flush(s.h3);
-        __syncthreads();
-        if (mult) {
-            // sample_mult: the first index whose running mass exceeds the coin
-            const uint64_t mine = wave_sum_u64(wm);
-            const uint64_t before = waves_excl_scan(mine, s, nullptr);
-            const uint64_t target = coin_k << 16;  // coin * 2^40, exact
-            if (tid == 0) s.pick = n - 1;          // no crossing: the last index
-            __syncthreads();
-            if (before <= target && target < before + mine) {
-                const int f = wave_find(p, r, before, target, [](int, float q) -> uint64_t { return fix40(q); });
-                if (lane == 0 && f >= 0) s.pick = f;
-            }
-            __syncthreads();
-            pick = s.pick;
-        } else {
-            uint64_t c1 = 0;
-            const int last = select_desc(p, r, cutoff, fix40(topp), s.h3, s, &c1);
-            if (last < 0) {
-                // the candidates' whole mass is within topp: all of them
-                uint64_t tot3 = 0;
-                if (tid == 0)
-                    for (int b = 0; b < 256; b++) tot3 += s.h3.mass[b];
-                if (tid == 0) s.u64b = tot3;
-                __syncthreads();
-                c1 = s.u64b;
-                __syncthreads();
-            }
-            // r = coin * cumulative: (c1 * coin_k) >> 24 without overflow
-            const uint64_t lo = c1 * coin_k, hi = __umul64hi(c1, coin_k);
-            const uint64_t rr = (hi << 40) | (lo >> 24);
-            uint64_t dummy;
-            pick = select_desc(p, r, cutoff, rr, s.h3, s, &dummy);
-            if (pick < 0) pick = 0;  // unreachable: rr < c1
-        }
-    }
+    store8(a.p, base, a.n, v);
+    block_argmax(m, mi, s);
     if (tid == 0) {
-        if (ss->record && pen != 1.0f) {  // record_token (sampler.odin:50-56)
-            int nl = min(ss->n_last, SAMPLE_WINDOW);
-            if (nl == SAMPLE_WINDOW) {
-                for (int i = 1; i < SAMPLE_WINDOW; i++) ss->last[i - 1] = ss->last[i];
-                nl--;
-            }
-            ss->last[nl] = pick;
-            ss->n_last = nl + 1;
-        }
-        if (state) {  // advance the token loop as the greedy reduction does
-            const int step = state[ST_STEP];
-            if (tokens_out && step >= 0 && step < state[ST_CAP]) tokens_out[step] = pick;
-            state[ST_STEP] = step + 1;
-            state[ST_TOKEN] = pick;
-            state[ST_POS] = state[ST_POS] + 1;
-            state[ST_PENDING] = 0;
-        }
-        if (pick_out) *pick_out = pick;
+        a.w->pmax[blockIdx.x] = m;
+        a.w->pidx[blockIdx.x] = mi;
     }
+}
+
+// 2. The maximum over the slices.  Temperature 0: workgroup 0 picks it.
+// Otherwise exp(x - max) into p and the slice's sum.
+__global__ __launch_bounds__(SB) void sample_exp_kernel(SArgs a, int greedy) {
+#pragma clang fp contract(off)
+    __shared__ Lds s;
+    const int G = wg_count(a.n), base = blockIdx.x * SLICE;
+    float mx = a.w->pmax[0];
+    int mi = a.w->pidx[0];
+    for (int g = 1; g < G; g++) argmax_combine(mx, mi, a.w->pmax[g], a.w->pidx[g]);
+    if (greedy) {
+        if (blockIdx.x == 0 && threadIdx.x == 0)
+            finalize(mi == 0x7FFFFFFF ? 0 : mi, a.ss, a.state, a.tokens_out, a.pick_out);
+        return;
+    }
+    float v[2][4], sum = 0.f;
+    load8(a.p, base, a.n, v);
+#pragma unroll
+    for (int k = 0; k < 2; k++)
+#pragma unroll
+        for (int x = 0; x < 4; x++)
+            if (elem(base, k, x) < a.n) {
+                v[k][x] = expf(v[k][x] - mx);
+                sum += v[k][x];
+            }
+    store8(a.p, base, a.n, v);
+    sum = block_sum(sum, s);
+    if (threadIdx.x == 0) a.w->psum[blockIdx.x] = sum;
+}
+
+// 3. p / sum (the sum over the slices in order), then the slice's fixed-point
+// mass (multinomial) or its candidates' first-digit histogram (top-p).
+// Workgroup 0 draws the coin (random_f32, sampler.odin:68-77).
+__global__ __launch_bounds__(SB) void sample_norm_kernel(SArgs a, int topp_mode) {
+#pragma clang fp contract(off)
+    __shared__ Lds s;
+    const int G = wg_count(a.n), base = blockIdx.x * SLICE;
+    float tot = 0.f;
+    for (int g = 0; g < G; g++) tot += a.w->psum[g];
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        uint64_t x = a.ss->rng;
+        x ^= x >> 12;
+        x ^= x << 25;
+        x ^= x >> 27;
+        a.ss->rng = x;
+        a.w->coin_k = (uint32_t)((x * 0x2545F4914F6CDD1Dull) >> 32) >> 8;  // coin = coin_k / 2^24
+    }
+    float v[2][4];
+    load8(a.p, base, a.n, v);
+#pragma unroll
+    for (int k = 0; k < 2; k++)
+#pragma unroll
+        for (int x = 0; x < 4; x++) v[k][x] = v[k][x] / tot;
+    store8(a.p, base, a.n, v);
+    if (!topp_mode) {
+        unsigned long long m = 0;
+#pragma unroll
+        for (int k = 0; k < 2; k++)
+#pragma unroll
+            for (int x = 0; x < 4; x++)
+                if (elem(base, k, x) < a.n) m += fix40(v[k][x]);
+        m = block_sum_u64(m, s);
+        if (threadIdx.x == 0) a.w->pmass[blockIdx.x] = m;
+        return;
+    }
+    const float cutoff = cutoff_of(a.ss, a.n);
+    hist_clear(s.h);
+    __syncthreads();
+    Run run;
+#pragma unroll
+    for (int k = 0; k < 2; k++)
+#pragma unroll
+        for (int x = 0; x < 4; x++) {
+            const int i = elem(base, k, x);
+            if (i < a.n && v[k][x] >= cutoff) run.add(s.h, (int)(__float_as_uint(v[k][x]) >> 24), i, fix40(v[k][x]));
+        }
+    run.flush(s.h);
+    __syncthreads();
+    for (int b = threadIdx.x; b < 256; b += SB)
+        if (s.h.cnt[b]) {
+            atomicAdd(&a.w->h[0].cnt[b], s.h.cnt[b]);
+            atomicAdd(&a.w->h[0].mass[b], s.h.mass[b]);
+            atomicMin(&a.w->h[0].lo[b], s.h.lo[b]);
+        }
+}
+
+// 4 (multinomial, sample_mult): the first index whose running mass exceeds
+// the coin; the last index when none does.
+__global__ __launch_bounds__(SB) void sample_mult_kernel(SArgs a) {
+    __shared__ Lds s;
+    const int G = wg_count(a.n), base = blockIdx.x * SLICE;
+    unsigned long long before = 0, total = 0;
+    for (int g = 0; g < G; g++) {
+        if (g < (int)blockIdx.x) before += a.w->pmass[g];
+        total += a.w->pmass[g];
+    }
+    const unsigned long long target = (unsigned long long)a.w->coin_k << 16;  // coin * 2^40, exact
+    if (total <= target) {
+        if (blockIdx.x == 0 && threadIdx.x == 0) finalize(a.n - 1, a.ss, a.state, a.tokens_out, a.pick_out);
+        return;
+    }
+    if (!(before <= target && target < before + a.w->pmass[blockIdx.x])) return;
+    float v[2][4];
+    load8(a.p, base, a.n, v);
+    unsigned long long wt[2][4];
+#pragma unroll
+    for (int k = 0; k < 2; k++)
+#pragma unroll
+        for (int x = 0; x < 4; x++) wt[k][x] = elem(base, k, x) < a.n ? fix40(v[k][x]) : 0;
+    const int f = block_find(wt, base, before, target, s);
+    if (threadIdx.x == 0) finalize(f < 0 ? a.n - 1 : f, a.ss, a.state, a.tokens_out, a.pick_out);
+}
+
+// Top-p digit rounds.  Stage k (0-based) reads a.w->sel[k] (stage 0: none)
+// and writes sel[k + 1]:
+//   stage 0: boundary target fix40(topp): walk digit 3 (h[0]), histogram digit 2 -> h[1]
+//   stages 1, 2: walk h[stage], histogram the next digit -> h[stage + 1]
+//   stage 3: walk h[3] -> the boundary value; c1 = the mass through it; coin
+//            target r = coin * c1: walk h[0] again, histogram digit 2 -> h[4]
+//   stages 4, 5: walk h[stage], histogram -> h[stage + 1]
+//   stage 6: walk h[6] -> the pick value; if its rank among equal
+//            probabilities is 0 (or it has no equal), the pick; otherwise
+//            each slice counts its equal elements
+//   stage 7: the slice holding that rank finds it
+__global__ __launch_bounds__(SB) void sample_topp_kernel(SArgs a, int stage) {
+    __shared__ Lds s;
+    const int base = blockIdx.x * SLICE, tid = threadIdx.x;
+    const float cutoff = cutoff_of(a.ss, a.n);
+    SampleWork *w = a.w;
+    Sel cur;
+    if (stage == 0) {
+        cur = Sel{};
+        cur.target = fix40(a.ss->topp);
+    } else {
+        cur = w->sel[stage];
+    }
+    if (cur.done) {  // the pick is made: later stages pass it on
+        if (blockIdx.x == 0 && tid == 0) w->sel[stage + 1] = cur;
+        return;
+    }
+    auto walk_digit = [&](const Hist &gh, int d) -> int {
+        unsigned long long above = cur.above;
+        const int sel = walk_buckets(gh, cur.target, &above, s);
+        if (sel >= 0) {
+            cur.above = above;
+            cur.prefix |= (uint32_t)sel << (8 * d);
+            cur.mask |= 255u << (8 * d);
+            cur.tie_lo = gh.lo[sel];
+            cur.tie_cnt = gh.cnt[sel];
+        }
+        return sel;
+    };
+    if (stage == 0 || stage == 1 || stage == 2 || stage == 4 || stage == 5) {
+        const int hin = stage == 0 ? 0 : stage, d = stage >= 4 ? 6 - stage : 3 - stage;  // digit walked
+        const int sel = walk_digit(w->h[hin], d);
+        if (sel < 0) {
+            // boundary: the candidates' whole mass is within topp, so all of
+            // them are kept (the coin stage then takes c1 = that mass);
+            // coin: unreachable (r < c1), pick 0 as the reference's fallback
+            if (stage < 3) cur.all = 1;
+            else {
+                cur.done = 1;
+                if (blockIdx.x == 0 && tid == 0) finalize(0, a.ss, a.state, a.tokens_out, a.pick_out);
+            }
+        } else {
+            hist_digit(a.p, base, a.n, cutoff, d - 1, cur.prefix, cur.mask, &w->h[hin + 1], s);
+        }
+        if (blockIdx.x == 0 && tid == 0) w->sel[stage + 1] = cur;
+        return;
+    }
+    if (stage == 3) {
+        if (!cur.all) {
+            walk_digit(w->h[3], 0);
+            // equal probabilities in index order: the j-th crosses
+            const uint64_t P = fix40(__uint_as_float(cur.prefix));
+            const uint64_t j = P ? (cur.target - cur.above) / P : 0;
+            cur.c1 = cur.above + (j + 1) * P;
+        } else {
+            unsigned long long t = 0;
+            for (int b = 0; b < 256; b++) t += w->h[0].mass[b];
+            cur.c1 = t;
+        }
+        // r = coin * c1: (c1 * coin_k) >> 24 without overflow
+        const unsigned long long ck = w->coin_k, lo = cur.c1 * ck, hi = __umul64hi(cur.c1, ck);
+        Sel nxt{};
+        nxt.target = (hi << 40) | (lo >> 24);
+        cur = nxt;
+        const int sel = walk_digit(w->h[0], 3);
+        if (sel < 0) {  // unreachable: r < c1
+            cur.done = 1;
+            if (blockIdx.x == 0 && tid == 0) finalize(0, a.ss, a.state, a.tokens_out, a.pick_out);
+        } else {
+            hist_digit(a.p, base, a.n, cutoff, 2, cur.prefix, cur.mask, &w->h[4], s);
+        }
+        if (blockIdx.x == 0 && tid == 0) w->sel[stage + 1] = cur;
+        return;
+    }
+    if (stage == 6) {
+        const int sel = walk_digit(w->h[6], 0);
+        if (sel < 0) {  // unreachable
+            cur.done = 1;
+            if (blockIdx.x == 0 && tid == 0) finalize(0, a.ss, a.state, a.tokens_out, a.pick_out);
+            if (blockIdx.x == 0 && tid == 0) w->sel[stage + 1] = cur;
+            return;
+        }
+        const uint64_t P = fix40(__uint_as_float(cur.prefix));
+        const uint64_t j = P ? (cur.target - cur.above) / P : 0;
+        if (j == 0 || cur.tie_cnt <= 1) {
+            cur.done = 1;
+            if (blockIdx.x == 0 && tid == 0) finalize((int)cur.tie_lo, a.ss, a.state, a.tokens_out, a.pick_out);
+        } else {
+            cur.c1 = j;  // the rank, for stage 7
+            float v[2][4];
+            load8(a.p, base, a.n, v);
+            unsigned long long c = 0;
+#pragma unroll
+            for (int k = 0; k < 2; k++)
+#pragma unroll
+                for (int x = 0; x < 4; x++) c += elem(base, k, x) < a.n && __float_as_uint(v[k][x]) == cur.prefix;
+            c = block_sum_u64(c, s);
+            if (tid == 0) w->pties[blockIdx.x] = (uint32_t)c;
+        }
+        if (blockIdx.x == 0 && tid == 0) w->sel[stage + 1] = cur;
+        return;
+    }
+    // stage 7: rank j among the equal probabilities, in index order
+    unsigned long long before = 0;
+    for (int g = 0; g < (int)blockIdx.x; g++) before += w->pties[g];
+    const unsigned long long j = cur.c1;
+    if (!(before <= j && j < before + w->pties[blockIdx.x])) return;
+    float v[2][4];
+    load8(a.p, base, a.n, v);
+    unsigned long long wt[2][4];
+#pragma unroll
+    for (int k = 0; k < 2; k++)
+#pragma unroll
+        for (int x = 0; x < 4; x++) wt[k][x] = elem(base, k, x) < a.n && __float_as_uint(v[k][x]) == cur.prefix;
+    const int f = block_find(wt, base, before, j, s);
+    if (tid == 0) finalize(f < 0 ? (int)cur.tie_lo : f, a.ss, a.state, a.tokens_out, a.pick_out);
 }
 
 }  // namespace
 
 int sample_max_vocab() { return SAMPLE_MAX_VOCAB; }
+size_t sample_work_bytes() { return sizeof(SampleWork); }
+int sample_mode(float temperature, float topp, int n) {
+    if (temperature == 0.0f) return SAMPLE_GREEDY;
+    return !(topp > 0.f && topp < 1.f) || n == 1 ? SAMPLE_MULT : SAMPLE_TOPP;
+}
 
-hipError_t launch_sample(const float *logits, float *p, int n, SampleState *ss, int32_t *state, int32_t *tokens_out,
-                         int32_t *pick, hipStream_t st) {
-    if (n <= 0 || n > SAMPLE_MAX_VOCAB) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(sample_kernel, dim3(1), dim3(SWG), 0, st, logits, p, n, ss, state, tokens_out, pick);
+hipError_t launch_sample(const float *logits, float *p, int n, SampleState *ss, int mode, void *work, int32_t *state,
+                         int32_t *tokens_out, int32_t *pick, hipStream_t st) {
+    if (n <= 0 || n > SAMPLE_MAX_VOCAB || !work || mode < SAMPLE_GREEDY || mode > SAMPLE_TOPP)
+        return hipErrorInvalidValue;
+    const SArgs a{logits, p, n, ss, (SampleWork *)work, state, tokens_out, pick};
+    const dim3 grid((unsigned)wg_count(n));
+    hipLaunchKernelGGL(sample_penalty_kernel, grid, dim3(SB), 0, st, a);
+    hipLaunchKernelGGL(sample_exp_kernel, grid, dim3(SB), 0, st, a, (int)(mode == SAMPLE_GREEDY));
+    if (mode == SAMPLE_GREEDY) return hipGetLastError();
+    hipLaunchKernelGGL(sample_norm_kernel, grid, dim3(SB), 0, st, a, (int)(mode == SAMPLE_TOPP));
+    if (mode == SAMPLE_MULT) {
+        hipLaunchKernelGGL(sample_mult_kernel, grid, dim3(SB), 0, st, a);
+        return hipGetLastError();
+    }
+    for (int stage = 0; stage < 8; stage++) hipLaunchKernelGGL(sample_topp_kernel, grid, dim3(SB), 0, st, a, stage);
     return hipGetLastError();
 }
 

@@ -139,6 +139,25 @@ def test_coin_near_one_matches_exact_picks():
             assert got == want or margin <= 1e-6, (st, coin, t, topp, got, want)
 
 
+@pytest.mark.parametrize("topp", [0.9, 0.0])
+def test_equal_probabilities_across_slices(topp):
+    """A run of 12000 equal logits spanning several of the sampler's
+    2048-logit workgroup slices: the top-p boundary and the coin fall inside
+    the run, so the pick is the j-th equal probability in index order,
+    counted across slices (top-p), or the first index past the coin's mass
+    (multinomial)."""
+    n = 20000
+    logits = np.full(n, -2.0, F32)
+    logits[3000:15000] = 1.0
+    for seed in range(1, 13):
+        coin, _ = refcpu.random_f32(seed)
+        want, margin = exact_pick(logits, 1.0, topp, coin)
+        got = infer.sample(infer.Sampler(1.0, topp, rng_seed=seed), logits)
+        assert got == want or margin <= 1e-6, (seed, got, want)
+        if topp:
+            assert 3000 <= got < 15000
+
+
 def test_zero_coin_matches_the_oracle_exactly():
     """seed 0 (serve.odin:1544): every coin is 0."""
     rng = np.random.default_rng(2)
