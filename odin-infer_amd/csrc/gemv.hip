@@ -1292,31 +1292,46 @@ hipError_t launch_mt_dot4(const MtGemvArgs &a, int max_items, hipStream_t st) {
 // pair); its B operand is 16 weight rows' 4-bit quants of one 32-weight group
 // as they are stored (the low nibbles of a 64-weight unit are its first
 // group, the high nibbles its second), so the weights need two logic
-// operations per 8 bytes; they pass through a per-wave LDS staging area so
-// that the loads read whole units (16 bytes per lane) while the operand
-// takes 8 bytes of each of four units.  Per group the integer products are scaled by the
+// operations per 8 bytes.  Per group the integer products are scaled by the
 // row's 6-bit group scale in int32 (|sum| < 2^31 over a super-block), per
 // super-block by d in f32; the min term, dmin m_g sum(x over the group), runs
 // beside it in f32.  An item is (expert, pair slice, row tile of rows /
 // tiles rows, one matrix); each of its 8 waves takes 16-row tiles of it
 // (lane (n, G): row n; plane G of the four pairs for the products, pair G for
-// the min term) and walks K one super-block per step with the next step's
-// weights in flight (deeper rings measured no faster); the planes are combined across lanes at the end of a tile into
-// one result per lane (row n, pair G), held in registers until the last tile
-// (stores in the loop would share the memory counter with the weight loads).
+// the min term) and walks K SBS super-blocks per step with the next step's
+// weights in flight.  The quants pass through a per-wave LDS staging area, so
+// the loads follow the memory rather than the operand: with SBS = 2 a row's
+// two super-blocks are one 128-byte line per quant plane, and each load
+// instruction reads 8 such lines whole (8 lanes per line; 2 x 64 bytes per
+// line at SBS = 1, which left half of each line to a second request and held
+// the loads alone to ~4 TB/s), while the operand takes 8 bytes of each of four
+// units.  The super-block headers of a tile (16 rows x NSB x 16 contiguous
+// bytes) are loaded whole, one tile ahead, NSB dwords per lane (HT = NSB, when
+// NSB divides 4 SBS, so that each step's headers sit in fixed registers of
+// known lanes), and each step takes its rows' headers from those lanes by
+// ds_bpermute; loaded per step instead (16 rows x 32 bytes, a quarter of 16
+// lines) they cost a fifth of the stream's time for a ninth of its bytes.
+// Otherwise (HT = 0) the headers pass through the staging rows.  The planes are combined across lanes at the
+// end of a tile into one result per lane (row n, pair G), held in registers
+// until the last tile (stores in the loop would share the memory counter with
+// the weight loads).
 constexpr float QI_MAX = 268434432.f;  // 2^28 - 2^10: the rounded product stays below 2^28
 constexpr int QI_MAXT = 16;            // 16-row tiles per wave (rows of an item <= 16 * 16 * waves)
 typedef int i32x4 __attribute__((ext_vector_type(4)));
-constexpr int QI_SROW = 144;  // staging row stride in bytes (128 + 16 against bank conflicts)
-template <int XI, int NWV>
+// staging row stride in bytes: SBS x 4 units of 32 quant bytes (plane 0, then
+// plane 1), SBS x 16 header bytes (when HT = 0), 16 bytes against bank conflicts
+__host__ __device__ constexpr int qi_srow(int sbs, int ht) { return sbs * (ht ? 128 : 144) + 16; }
+template <int XI, int NWV, int SBS, int HT>
 __global__ __launch_bounds__(NWV * WAVE) void mt_q4i8_kernel(MtGemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) u32x4 md_smem[];
-    constexpr int NP = MT_MFMA_FEW, QW = NWV * WAVE, NSTG = 2;
+    constexpr int NP = MT_MFMA_FEW, QW = NWV * WAVE, NSTG = 2, SROW = qi_srow(SBS, HT), RPI = 16 / SBS;
     static_assert(NP == 4, "the A operand's 16 rows are 4 planes x 4 pairs");
+    static_assert(SBS == 1 || SBS == 2, "one or two super-blocks per step");
+    static_assert(HT == 0 || ((4 * SBS) % HT == 0 && HT % 2 == 0), "a step's headers in fixed registers");
     const bool second = a.mat_items > 0 && (int)blockIdx.x >= a.mat_items;
     const int it = second ? (int)blockIdx.x - a.mat_items : (int)blockIdx.x;
     if (it >= *a.nitems) return;
-    const int K = a.K, U = K >> 6, NSB = K >> 8;
+    const int K = a.K, U = K >> 6, NSB = K >> 8, NSS = NSB / SBS;  // NSB % SBS == 0
     const int e = a.items[2 * it], slice = a.items[2 * it + 1] >> 16, tile = a.items[2 * it + 1] & 0xFFFF;
     const int base = a.off[e] + slice * NP, n = min(NP, a.cnt[e] - slice * NP);
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid / WAVE, G = lane >> 4;
@@ -1325,30 +1340,80 @@ __global__ __launch_bounds__(NWV * WAVE) void mt_q4i8_kernel(MtGemvArgs a) {
     float *y = (second ? a.y2 : a.y) + row0;
     // LDS: the A operand [unit][lane] (16 B per lane: group g = lane / 16 of
     // the unit's first 32 weights, then of its second), the group sums
-    // [pair][K/32], the scales and the wave maxima
+    // [pair][K/32], the scales and the wave maxima, the waves' staging rows
     u32x4 *xa = md_smem;
     float *xsum = (float *)(xa + U * WAVE);
     float *xsc = xsum + NP * (K / 32);  // [NP] scales, then [NWV][NP] wave maxima
-    uint8_t *stg = (uint8_t *)(xsc + NP + NWV * NP) + wave * 16 * QI_SROW;  // the wave's weight staging
+    uint8_t *stg = (uint8_t *)(xsc + NP + NWV * NP) + wave * 16 * SROW;  // the wave's weight staging
     struct Step {
-        u32x4 h, q0, q1;
+        u32x4 q[2 * SBS];  // [plane][instruction]
+        uint32_t h[HT > 0 ? 1 : SBS];
     };
-    const int nstep = (rows / (16 * NWV)) * NSB;  // rows % (16 NWV) == 0
+    const int nstep = (rows / (16 * NWV)) * NSS;  // rows % (16 NWV) == 0
+    // load lanes: row ln of each instruction's RPI rows, 16-byte unit lc of the
+    // row's SBS super-blocks; header lanes: row lane / 4, SBS dwords (lane % 4)
+    // of its SBS x 16 header bytes
+    const int ln = lane % RPI, lc = lane / RPI;
     auto issue = [&](int s, Step &w) {
-        const int s2 = min(s, nstep - 1), ti = s2 / NSB, sb = s2 - ti * NSB;
-        const int r = (ti * NWV + wave) * 16 + (lane & 15);
-        // lane (n, G): both planes of unit 4 sb + G, so each instruction reads
-        // 64 contiguous bytes per row and plane (cached loads: the next step
-        // reads the other half of each 128-byte line)
-        w.h = *(const u32x4 *)(m.s + ((size_t)r * NSB + sb) * 16);
-        const size_t ui = (size_t)r * U + 4 * sb + G;
-        w.q0 = *(const u32x4 *)(m.q + ui * 16);
-        w.q1 = *(const u32x4 *)(m.q + m.plane + ui * 16);
+        const int s2 = min(s, nstep - 1), ti = s2 / NSS, ss = s2 - ti * NSS;
+        const int rb = (ti * NWV + wave) * 16;
+#pragma unroll
+        for (int i = 0; i < SBS; i++) {
+            const size_t ui = (size_t)(rb + i * RPI + ln) * U + 4 * SBS * ss + lc;
+            w.q[i] = *(const u32x4 *)(m.q + ui * 16);
+            w.q[SBS + i] = *(const u32x4 *)(m.q + m.plane + ui * 16);
+        }
+        if constexpr (HT == 0) {
+            const uint32_t *hp =
+                (const uint32_t *)(m.s + ((size_t)(rb + (lane >> 2)) * NSB + SBS * ss) * 16) + (lane & 3) * SBS;
+            if constexpr (SBS == 2) {
+                const u32x2 hv = *(const u32x2 *)hp;
+                w.h[0] = hv.x;
+                w.h[1] = hv.y;
+            } else {
+                w.h[0] = *hp;
+            }
+        }
+    };
+    // the tile headers (HT > 0): lane l holds row l / 4's dwords [(l % 4) HT, (l % 4 + 1) HT)
+    const int ntl = rows / (16 * NWV);
+    uint32_t hreg[HT > 0 ? HT : 1];
+    auto hload = [&](int ti) {
+        if constexpr (HT > 0) {
+            const uint32_t *hp =
+                (const uint32_t *)(m.s + (size_t)((min(ti, ntl - 1) * NWV + wave) * 16) * HT * 16) + lane * HT;
+#pragma unroll
+            for (int j = 0; j < HT; j += 4) {
+                if (HT - j >= 4) {
+                    const u32x4 v = *(const u32x4 *)(hp + j);
+                    hreg[j] = v.x; hreg[j + 1] = v.y; hreg[j + 2] = v.z; hreg[j + 3] = v.w;
+                } else {
+                    const u32x2 v = *(const u32x2 *)(hp + j);
+                    hreg[j] = v.x; hreg[j + 1] = v.y;
+                }
+            }
+        }
+    };
+    // a step's headers (HT > 0): dword c of super-block sb of row n is held by
+    // lane 4 n + (4 sb + c) / HT, in hreg[(4 sb + c) % HT]
+    auto gather = [&](int s, u32x4 (&hv)[SBS]) {
+        if constexpr (HT > 0) {
+            const int ss = s % NSS, src = 4 * (lane & 15) + (4 * SBS * ss) / HT;
+#pragma unroll
+            for (int hb = 0; hb < SBS; hb++) {
+                uint32_t d4[4];
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+                    d4[c] = (uint32_t)__builtin_amdgcn_ds_bpermute((src + (4 * hb + c) / HT) << 2,
+                                                                   (int)hreg[(4 * hb + c) % HT]);
+                hv[hb] = u32x4{d4[0], d4[1], d4[2], d4[3]};
+            }
+        }
     };
     Step ring[NSTG];
-#pragma unroll
-    for (int i = 0; i < NSTG - 1; i++) issue(i, ring[i]);
-    // every pair's x (and x2) requested before any is used
+    // every pair's x (and x2) requested before any is used, and before the
+    // first weights (the loads return in order: behind the weights, the x
+    // rows of 8 waves took ~7 us to arrive, ~4 us ahead of them)
     float4 xv[NP][XI], uv[NP][XI];
 #pragma unroll
     for (int pj = 0; pj < NP; pj++) {
@@ -1360,6 +1425,9 @@ __global__ __launch_bounds__(NWV * WAVE) void mt_q4i8_kernel(MtGemvArgs a) {
             uv[pj][i] = a.x2 ? ((const float4 *)(a.x2 + xo))[c] : float4{0.f, 0.f, 0.f, 0.f};
         }
     }
+    hload(0);
+#pragma unroll
+    for (int i = 0; i < NSTG - 1; i++) issue(i, ring[i]);
     float amax[NP];
 #pragma unroll
     for (int pj = 0; pj < NP; pj++) {
@@ -1423,43 +1491,57 @@ __global__ __launch_bounds__(NWV * WAVE) void mt_q4i8_kernel(MtGemvArgs a) {
 #pragma unroll
     for (int k = 0; k < QI_MAXT; k++) res[k] = 0.f;
     const float pw = G == 0 ? 2097152.f : G == 1 ? 16384.f : G == 2 ? 128.f : 1.f;  // plane weight 2^(21 - 7 G)
-    auto compute = [&](int s, const Step &w) {
-        const int ti = s / NSB, sb = s - ti * NSB;
-        const float d = h2f(w.h.x & 0xFFFFu), dmin = h2f(w.h.x >> 16);
-        i32x4 iacc = {0, 0, 0, 0};
-        float mf = 0.f;
+    auto compute = [&](int s, const Step &w, const u32x4 (&hg)[SBS]) {
+        const int ti = s / NSS, ss = s - ti * NSS;
         // through the wave's LDS rows (one wave's LDS operations complete in
         // order): lane (n, g) then takes dwords 2g, 2g+1 of each unit, the B
         // operand layout (group g = the unit's weights 8g .. 8g+7 of each half)
-        u32x2 wq[4];
         asm volatile("" ::: "memory");  // the previous step's reads stay before these writes
-        uint8_t *sr = stg + (lane & 15) * QI_SROW;
-        *(u32x4 *)(sr + G * 32) = w.q0;
-        *(u32x4 *)(sr + G * 32 + 16) = w.q1;
 #pragma unroll
-        for (int k = 0; k < 4; k++) wq[k] = *(const u32x2 *)(sr + k * 32 + 8 * G);
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int u = 4 * sb + k;
-            uint32_t sc0, m0, sc1, m1;
-            q4k_scales(k, w.h.y, w.h.z, w.h.w, sc0, m0, sc1, m1);
-            const u32x4 xo = xa[u * WAVE + lane];
-            const uint32_t lo0 = wq[k].x & 0x0F0F0F0Fu, lo1 = wq[k].y & 0x0F0F0F0Fu;
-            const uint32_t hi0 = (wq[k].x >> 4) & 0x0F0F0F0Fu, hi1 = (wq[k].y >> 4) & 0x0F0F0F0Fu;
-            const i32x4 z = {0, 0, 0, 0};
-            const i32x4 dA = __builtin_amdgcn_mfma_i32_16x16x32_i8(
-                (long)(((uint64_t)xo.y << 32) | xo.x), (long)(((uint64_t)lo1 << 32) | lo0), z, 0, 0, 0);
-            const i32x4 dB = __builtin_amdgcn_mfma_i32_16x16x32_i8(
-                (long)(((uint64_t)xo.w << 32) | xo.z), (long)(((uint64_t)hi1 << 32) | hi0), z, 0, 0, 0);
-#pragma unroll
-            for (int v = 0; v < 4; v++) iacc[v] += __mul24((int)sc0, dA[v]) + __mul24((int)sc1, dB[v]);  // |dA| < 2^23
-            const float2 xs2 = *(const float2 *)&xsum[G * (K / 32) + 2 * u];
-            mf += (float)m0 * xs2.x + (float)m1 * xs2.y;
+        for (int i = 0; i < SBS; i++) {
+            uint8_t *wr = stg + (i * RPI + ln) * SROW + lc * 32;
+            *(u32x4 *)wr = w.q[i];
+            *(u32x4 *)(wr + 16) = w.q[SBS + i];
         }
+        if constexpr (HT == 0) {
+            uint8_t *wh = stg + (lane >> 2) * SROW + SBS * 128 + (lane & 3) * SBS * 4;
+            if constexpr (SBS == 2) *(u32x2 *)wh = u32x2{w.h[0], w.h[1]};
+            else *(uint32_t *)wh = w.h[0];
+        }
+        const uint8_t *sr = stg + (lane & 15) * SROW;
 #pragma unroll
-        for (int v = 0; v < 4; v++) facc[v] += d * (float)iacc[v];
-        fmin += dmin * mf;
-        if (sb == NSB - 1) {  // the tile's row n = lane % 16 is done: combine the planes
+        for (int hb = 0; hb < SBS; hb++) {
+            const int sb = SBS * ss + hb;
+            const u32x4 hv = HT > 0 ? hg[hb] : *(const u32x4 *)(sr + SBS * 128 + hb * 16);
+            u32x2 wq[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) wq[k] = *(const u32x2 *)(sr + (4 * hb + k) * 32 + 8 * G);
+            const float d = h2f(hv.x & 0xFFFFu), dmin = h2f(hv.x >> 16);
+            i32x4 iacc = {0, 0, 0, 0};
+            float mf = 0.f;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int u = 4 * sb + k;
+                uint32_t sc0, m0, sc1, m1;
+                q4k_scales(k, hv.y, hv.z, hv.w, sc0, m0, sc1, m1);
+                const u32x4 xo = xa[u * WAVE + lane];
+                const uint32_t lo0 = wq[k].x & 0x0F0F0F0Fu, lo1 = wq[k].y & 0x0F0F0F0Fu;
+                const uint32_t hi0 = (wq[k].x >> 4) & 0x0F0F0F0Fu, hi1 = (wq[k].y >> 4) & 0x0F0F0F0Fu;
+                const i32x4 z = {0, 0, 0, 0};
+                const i32x4 dA = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+                    (long)(((uint64_t)xo.y << 32) | xo.x), (long)(((uint64_t)lo1 << 32) | lo0), z, 0, 0, 0);
+                const i32x4 dB = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+                    (long)(((uint64_t)xo.w << 32) | xo.z), (long)(((uint64_t)hi1 << 32) | hi0), z, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 4; v++) iacc[v] += __mul24((int)sc0, dA[v]) + __mul24((int)sc1, dB[v]);  // |dA| < 2^23
+                const float2 xs2 = *(const float2 *)&xsum[G * (K / 32) + 2 * u];
+                mf += (float)m0 * xs2.x + (float)m1 * xs2.y;
+            }
+#pragma unroll
+            for (int v = 0; v < 4; v++) facc[v] += d * (float)iacc[v];
+            fmin += dmin * mf;
+        }
+        if (ss == NSS - 1) {  // the tile's row n = lane % 16 is done: combine the planes
             float t[4];
 #pragma unroll
             for (int v = 0; v < 4; v++) {
@@ -1477,15 +1559,22 @@ __global__ __launch_bounds__(NWV * WAVE) void mt_q4i8_kernel(MtGemvArgs a) {
     };
     // NSTG steps per pass, so each stage index is static; every pass issues
     // the same loads (clamped to the last step), only the computation stops
+    // (HT > 0: a step's headers are taken before the next tile's are requested
+    // into the same registers, at the tile's last step)
     for (int st = 0; st < nstep; st += NSTG) {
 #pragma unroll
         for (int i = 0; i < NSTG; i++) {
-            issue(st + i + NSTG - 1, ring[(i + NSTG - 1) % NSTG]);
-            if (st + i < nstep) compute(st + i, ring[i]);
+            const int s = st + i;
+            u32x4 hg[SBS];
+            if (HT > 0 && s < nstep) {
+                gather(s, hg);
+                if (s % NSS == NSS - 1) hload(s / NSS + 1);
+            }
+            issue(s + NSTG - 1, ring[(i + NSTG - 1) % NSTG]);
+            if (s < nstep) compute(s, ring[i], hg);
         }
     }
-    if (G < n) {
-        const int ntl = rows / (16 * NWV);  // the wave's tiles: tile i's result is res[QI_MAXT - ntl + i]
+    if (G < n) {  // the wave's tiles: tile i's result is res[QI_MAXT - ntl + i]
         float *yr = y + (size_t)a.list[base + G] * a.rows + wave * 16 + (lane & 15);
 #pragma unroll
         for (int k = 0; k < QI_MAXT; k++) {
@@ -1496,9 +1585,17 @@ __global__ __launch_bounds__(NWV * WAVE) void mt_q4i8_kernel(MtGemvArgs a) {
 }
 
 constexpr int QI_NW = 8;  // waves per workgroup: the x planes in LDS serve 8 waves (4 measured 2% slower)
+static int qi_sbs(int32_t K) { return (K / 256) % 2 == 0 ? 2 : 1; }
+// headers per tile when a tile takes more than one step and NSB divides 4 SBS
+// (NSB = 4, 8 here), else per step (at NSB = 2 a step's headers are already
+// 512 contiguous bytes, and the permutes only cost)
+static int qi_ht(int32_t K) {
+    const int nsb = K / 256;
+    return qi_sbs(K) == 2 && (nsb == 4 || nsb == 8) ? nsb : 0;
+}
 static size_t mt_q4i8_lds(int32_t K, int nw) {
     return (size_t)(K / 64) * WAVE * 16 + (size_t)MT_MFMA_FEW * (K / 32) * 4 +
-           (size_t)(MT_MFMA_FEW + nw * MT_MFMA_FEW) * 4 + (size_t)nw * 16 * QI_SROW;
+           (size_t)(MT_MFMA_FEW + nw * MT_MFMA_FEW) * 4 + (size_t)nw * 16 * qi_srow(qi_sbs(K), qi_ht(K));
 }
 
 // rows: the rows of one row tile
@@ -1516,8 +1613,19 @@ hipError_t launch_mt_q4i8(const MtGemvArgs &a, int max_items, hipStream_t st) {
     b.mat_items = a.swiglu ? max_items : 0;  // gate into y, up into y2 (the SwiGLU is the consumer's)
     const size_t lds = mt_q4i8_lds(a.K, QI_NW);
     const dim3 grid((unsigned)(a.swiglu ? 2 * max_items : max_items)), block(QI_NW * WAVE);
-    if (a.K <= 4 * QI_NW * WAVE) hipLaunchKernelGGL((mt_q4i8_kernel<1, QI_NW>), grid, block, lds, st, b);
-    else hipLaunchKernelGGL((mt_q4i8_kernel<2, QI_NW>), grid, block, lds, st, b);
+    const bool x1 = a.K <= 4 * QI_NW * WAVE;  // K <= 2048: NSB <= 8
+    switch (x1 ? qi_ht(a.K) : -1) {
+    case 8: hipLaunchKernelGGL((mt_q4i8_kernel<1, QI_NW, 2, 8>), grid, block, lds, st, b); break;
+    case 4: hipLaunchKernelGGL((mt_q4i8_kernel<1, QI_NW, 2, 4>), grid, block, lds, st, b); break;
+    case 0:
+        if (qi_sbs(a.K) == 2) hipLaunchKernelGGL((mt_q4i8_kernel<1, QI_NW, 2, 0>), grid, block, lds, st, b);
+        else hipLaunchKernelGGL((mt_q4i8_kernel<1, QI_NW, 1, 0>), grid, block, lds, st, b);
+        break;
+    default:
+        if (qi_sbs(a.K) == 2) hipLaunchKernelGGL((mt_q4i8_kernel<2, QI_NW, 2, 0>), grid, block, lds, st, b);
+        else hipLaunchKernelGGL((mt_q4i8_kernel<2, QI_NW, 1, 0>), grid, block, lds, st, b);
+        break;
+    }
     return hipGetLastError();
 }
 

@@ -1,4 +1,6 @@
 """Shared helpers for the tests."""
+import struct
+
 import numpy as np
 
 
@@ -83,3 +85,74 @@ class DeviceBuffer:
         if self.ptr:
             self._hip.hipFree(self.ptr)
             self.ptr = None
+
+
+def gguf_fields(data):
+    """Offsets of a GGUF v3 header's fields: a list of (name, offset, size)."""
+    out = [("magic", 0, 4), ("version", 4, 4), ("n_tensors", 8, 8), ("n_meta", 16, 8)]
+    n_tensors, n_meta = struct.unpack_from("<QQ", data, 8)
+    pos = 24
+    sizes = {0: 1, 1: 1, 2: 2, 3: 2, 4: 4, 5: 4, 6: 4, 7: 1, 10: 8, 11: 8, 12: 8}
+
+    def value(t, pos, name):
+        if t in sizes:
+            out.append((name + ".value", pos, sizes[t]))
+            return pos + sizes[t]
+        if t == 8:
+            (n,) = struct.unpack_from("<Q", data, pos)
+            out.append((name + ".strlen", pos, 8))
+            return pos + 8 + n
+        if t == 9:
+            (et,) = struct.unpack_from("<I", data, pos)
+            (cnt,) = struct.unpack_from("<Q", data, pos + 4)
+            out.append((name + ".atype", pos, 4))
+            out.append((name + ".count", pos + 4, 8))
+            pos += 12
+            for _ in range(cnt):
+                pos = value(et, pos, name + "[]")
+            return pos
+        raise ValueError(t)
+
+    for _ in range(n_meta):
+        (kl,) = struct.unpack_from("<Q", data, pos)
+        key = data[pos + 8:pos + 8 + kl].decode()
+        out.append(("meta:%s.keylen" % key, pos, 8))
+        pos += 8 + kl
+        (t,) = struct.unpack_from("<I", data, pos)
+        out.append(("meta:%s.type" % key, pos, 4))
+        pos = value(t, pos + 4, "meta:" + key)
+    for _ in range(n_tensors):
+        (nl,) = struct.unpack_from("<Q", data, pos)
+        name = data[pos + 8:pos + 8 + nl].decode()
+        out.append(("tensor:%s.namelen" % name, pos, 8))
+        pos += 8 + nl
+        (nd,) = struct.unpack_from("<I", data, pos)
+        out.append(("tensor:%s.n_dims" % name, pos, 4))
+        pos += 4
+        for d in range(nd):
+            out.append(("tensor:%s.dim%d" % (name, d), pos, 8))
+            pos += 8
+        out.append(("tensor:%s.type" % name, pos, 4))
+        out.append(("tensor:%s.offset" % name, pos + 4, 8))
+        pos += 12
+    out.append(("end", pos, 0))
+    return out
+
+
+def gguf_tensor_data(data):
+    """{tensor name: (absolute byte offset of its data, GGML type)} of a GGUF v3
+    file held in `data` (the data section starts at the first multiple of
+    general.alignment, default 32, after the tensor infos)."""
+    fields = gguf_fields(data)
+    align = 32
+    for name, off, size in fields:
+        if name == "meta:general.alignment.value":
+            align = int.from_bytes(data[off:off + size], "little")
+    start = -(-fields[-1][1] // align) * align
+    out = {}
+    for name, off, size in fields:
+        if name.startswith("tensor:") and name.endswith(".offset"):
+            t = name[len("tensor:"):-len(".offset")]
+            out[t] = (start + int.from_bytes(data[off:off + 8], "little"),
+                      int.from_bytes(data[off - 4:off], "little"))
+    return out

@@ -19,7 +19,7 @@ import numpy as np
 import pytest
 
 import refcpu
-from helpers import scaled_err
+from helpers import gguf_tensor_data, scaled_err
 from oi import infer
 
 pytestmark = pytest.mark.gpu
@@ -279,6 +279,52 @@ def test_prefill_expert_kernels_agree(tmp_path, monkeypatch, shape, n):
         err = scaled_err(out["default"], out[kind])
         print("%s n=%d: default vs %s experts %.3g" % (shape, n, kind, err))
         assert err <= 1e-5, kind
+
+
+@pytest.mark.parametrize("mode", ["massive", "group"])
+def test_prefill_int8_experts_outlier_activations(tmp_path, mode):
+    """The routed experts of a 64-token chunk on the int8 matrix cores (the
+    default at config 5's shapes) scale each pair's x row once, by its
+    largest element, into four 7-bit planes: 28 bits relative to the row's
+    maximum, so a row holding a 10^3..10^4 outlier keeps far fewer bits for
+    its small elements.  The FFN norm weight of a one-layer config-5-shape
+    model (a DeltaNet layer, 512 experts top 10 + the shared expert) is
+    patched so that every token's expert input carries outliers: four massive
+    channels at 1.5e3..1.2e4 times the rest (the residual-stream pattern of
+    Qwen models) or one element of every 32 at 10^2..10^4 times the rest.
+    The last logits against the oracle's prefill (its routed experts in
+    float64 from f32 x, qwen3_5/forward.odin:227-243): scaled error 1e-3 and
+    the same argmax."""
+    from oi import synth
+    spec = synth._hybrid(2048, 512, 1, 16, 2, 256, 4096, 4096, 64, 16, 32, 128, experts=512, used=10, eff=512,
+                         shared=512, interval=2, seed=53)
+    path = tmp_path / "c5l1.gguf"
+    synth.write_gguf(path, spec)
+    data = bytearray(path.read_bytes())
+    off, typ = gguf_tensor_data(bytes(data))["blk.0.post_attention_norm.weight"]
+    assert typ == 0  # F32
+    w = np.frombuffer(data, np.float32, 2048, off).copy()
+    rng = np.random.default_rng(11)
+    if mode == "massive":
+        w[[3, 777, 1029, 2039]] *= np.array([3.1e3, -8.7e3, 1.2e4, -1.5e3], np.float32)
+    else:
+        pos = np.arange(64) * 32 + rng.integers(0, 32, size=64)
+        w[pos] *= (10.0 ** rng.uniform(2, 4, size=64)).astype(np.float32)
+    data[off:off + w.nbytes] = w.tobytes()
+    path.write_bytes(bytes(data))
+    e, r = _engines(str(path), 256)
+    try:
+        toks = _tokens(19, 64, r.vocab_size)
+        print("case outliers %s" % mode, flush=True)
+        got = infer.engine_forward_batch(e, toks, 0).copy()
+        ref = r.prefill(toks, 0)
+        err = scaled_err(got, ref)
+        print("outliers %s: scaled error %.3g" % (mode, err))
+        assert err <= TOL
+        assert int(np.argmax(got)) == refcpu.argmax(ref)
+    finally:
+        infer.engine_destroy(e)
+        r.close()
 
 
 @pytest.mark.parametrize("chunk", ["0", "16", "32"])

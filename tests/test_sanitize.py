@@ -22,6 +22,8 @@ import sys
 import numpy as np
 import pytest
 
+from helpers import gguf_fields
+
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 SAN = os.path.join(REPO, "tests", "sanitize")
 EXE = os.path.join(SAN, "_build", "san_readers")
@@ -69,58 +71,6 @@ def _run(exe, args):
         parts = line.split(" ", 3 if args[0] == "gguf" else 2)
         rows[parts[-1]] = tuple(int(x) for x in parts[:-1])
     return rows
-
-
-def gguf_fields(data):
-    """Offsets of a GGUF v3 header's fields: a list of (name, offset, size)."""
-    out = [("magic", 0, 4), ("version", 4, 4), ("n_tensors", 8, 8), ("n_meta", 16, 8)]
-    n_tensors, n_meta = struct.unpack_from("<QQ", data, 8)
-    pos = 24
-    sizes = {0: 1, 1: 1, 2: 2, 3: 2, 4: 4, 5: 4, 6: 4, 7: 1, 10: 8, 11: 8, 12: 8}
-
-    def value(t, pos, name):
-        if t in sizes:
-            out.append((name + ".value", pos, sizes[t]))
-            return pos + sizes[t]
-        if t == 8:
-            (n,) = struct.unpack_from("<Q", data, pos)
-            out.append((name + ".strlen", pos, 8))
-            return pos + 8 + n
-        if t == 9:
-            (et,) = struct.unpack_from("<I", data, pos)
-            (cnt,) = struct.unpack_from("<Q", data, pos + 4)
-            out.append((name + ".atype", pos, 4))
-            out.append((name + ".count", pos + 4, 8))
-            pos += 12
-            for _ in range(cnt):
-                pos = value(et, pos, name + "[]")
-            return pos
-        raise ValueError(t)
-
-    for _ in range(n_meta):
-        (kl,) = struct.unpack_from("<Q", data, pos)
-        key = data[pos + 8:pos + 8 + kl].decode()
-        out.append(("meta:%s.keylen" % key, pos, 8))
-        pos += 8 + kl
-        (t,) = struct.unpack_from("<I", data, pos)
-        out.append(("meta:%s.type" % key, pos, 4))
-        pos = value(t, pos + 4, "meta:" + key)
-    for _ in range(n_tensors):
-        (nl,) = struct.unpack_from("<Q", data, pos)
-        name = data[pos + 8:pos + 8 + nl].decode()
-        out.append(("tensor:%s.namelen" % name, pos, 8))
-        pos += 8 + nl
-        (nd,) = struct.unpack_from("<I", data, pos)
-        out.append(("tensor:%s.n_dims" % name, pos, 4))
-        pos += 4
-        for d in range(nd):
-            out.append(("tensor:%s.dim%d" % (name, d), pos, 8))
-            pos += 8
-        out.append(("tensor:%s.type" % name, pos, 4))
-        out.append(("tensor:%s.offset" % name, pos + 4, 8))
-        pos += 12
-    out.append(("end", pos, 0))
-    return out
 
 
 def _put(data, off, size, v):
