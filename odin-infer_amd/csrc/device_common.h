@@ -106,26 +106,47 @@ static __device__ __forceinline__ float softplus_ref(float x) {
 // sum of the K-slice partial products of element i (a split projection's
 // slices, each `slice` floats, summed in slice order)
 static __device__ __forceinline__ float parts_at(const float *p, int split, size_t slice, size_t i) {
+    // slices requested 8 at a time (a runtime trip count would make every
+    // load wait for the sum before it), summed in slice order
     float s = p[i];
-    for (int z = 1; z < split; z++) s += p[(size_t)z * slice + i];
+    for (int z0 = 1; z0 < split; z0 += 8) {
+        float t[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            if (z0 + k < split) t[k] = p[(size_t)(z0 + k) * slice + i];
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            if (z0 + k < split) s += t[k];
+    }
     return s;
 }
 
 // v[j] = parts_at(p, split, slice, idx(j)) for j < N, with the same sums in
-// the same order, but each slice's N loads are requested together: `split`
-// memory round trips instead of one per element and slice (a runtime trip
-// count inside the element loop makes every load wait for the one before)
+// the same order, but the loads of max(1, 16 / N) slices are requested
+// together: ceil(split / that) memory round trips instead of one per element
+// and slice (a runtime trip count inside the element loop makes every load
+// wait for the one before)
 template <int N, class F>
 static __device__ __forceinline__ void parts_gather(float (&v)[N], const float *p, int split, size_t slice, F idx) {
+    constexpr int B = N >= 16 ? 1 : 16 / N;
 #pragma unroll
     for (int j = 0; j < N; j++) v[j] = p[idx(j)];
-    for (int z = 1; z < split; z++) {
-        const float *q = p + (size_t)z * slice;
-        float t[N];
+    for (int z0 = 1; z0 < split; z0 += B) {
+        float t[B][N];
 #pragma unroll
-        for (int j = 0; j < N; j++) t[j] = q[idx(j)];
+        for (int k = 0; k < B; k++) {
+            const float *q = p + (size_t)(z0 + k) * slice;
+            if (z0 + k < split) {
 #pragma unroll
-        for (int j = 0; j < N; j++) v[j] += t[j];
+                for (int j = 0; j < N; j++) t[k][j] = q[idx(j)];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < B; k++)
+            if (z0 + k < split) {
+#pragma unroll
+                for (int j = 0; j < N; j++) v[j] += t[k][j];
+            }
     }
 }
 
