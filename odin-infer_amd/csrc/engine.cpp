@@ -1252,7 +1252,9 @@ int prefill_alloc(oi_engine *e) {
 // output, softmax + top-k per token, the pairs grouped by expert, the chosen
 // experts' SwiGLU rows and down rows per pair, their weighted sum per token
 // into partial-product buffer 0.
-int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
+// combine = false: the pair rows and weights stay in pf_yd / pf_w for the next
+// residual add + norm, which sums them (launch_pf_addnorm16's myd)
+int prefill_moe(oi_engine *e, const LayerDev &L, int T, bool combine = true) {
     const hipStream_t st = e->stream;
     const int32_t D = (int32_t)e->cfg.dim, E = (int32_t)e->n_experts, EF = (int32_t)e->expert_ffn;
     const int sx = L.shared_merged ? 1 : 0, KP = (int)e->top_k + sx, NE = E + sx;
@@ -1370,7 +1372,7 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T) {
             : dn_d4 ? launch_mt_dot4(d, item_tiles, st)
             : mm ? launch_mt_mfma(d, item_tiles * ma.tiles_dn, st, e->pf_experts == 2)
                  : launch_mt_gemv(d, item_tiles * ma.tiles_dn, st));
-    HIP_TRY(launch_pf_moe_combine(ma, st));
+    if (combine) HIP_TRY(launch_pf_moe_combine(ma, st));
     return OI_OK;
 }
 
@@ -1445,9 +1447,16 @@ int prefill_chunk(oi_engine *e, const int32_t *tokens, int T, int pos, float *ro
         }
         HIP_TRY(launch_pf_addnorm16(e->pf_x, P[0], s0, L.ffn_norm, eps, D, T, e->pf_xb, st,
                                     L.moe ? e->pf_xn : nullptr));
+        const bool last = l + 1 == e->layers.size();
         if (L.moe) {
-            if (prefill_moe(e, L, T)) return -1;
+            if (prefill_moe(e, L, T, last)) return -1;
             s0 = 1;
+            if (!last) {  // the expert combine summed in the next layer's residual add + norm
+                const int KP = (int)e->top_k + (L.shared_merged ? 1 : 0);
+                HIP_TRY(launch_pf_addnorm16(e->pf_x, nullptr, 1, e->layers[l + 1].attn_norm, eps, D, T, e->pf_xb, st,
+                                            nullptr, e->pf_w, e->pf_yd, KP));
+                continue;
+            }
         } else if (e->pf_fused && gemm_swiglu_supported(L.w1, L.w3, T)) {
             // gate and up in one pass, SwiGLU in its epilogue; h goes to the up
             // partials' buffer (unsplit, it holds T x H floats)

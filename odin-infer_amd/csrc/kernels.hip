@@ -1491,8 +1491,15 @@ __global__ __launch_bounds__(WG) void pf_moe_combine_kernel(PfMoeArgs a) {
     const int t = blockIdx.y, r = (int)blockIdx.x * WG + threadIdx.x;
     if (r >= a.dim) return;
     float acc = 0.f;
-    for (int s = 0; s < a.kp; s++)
-        acc += a.w[(size_t)t * a.kp + s] * a.yd[((size_t)t * a.kp + s) * a.dim + r];
+    for (int s0 = 0; s0 < a.kp; s0 += 8) {  // 8 slots' rows requested together, summed in slot order
+        float y[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            if (s0 + k < a.kp) y[k] = a.yd[((size_t)t * a.kp + s0 + k) * a.dim + r];
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            if (s0 + k < a.kp) acc += a.w[(size_t)t * a.kp + s0 + k] * y[k];
+    }
     a.out[(size_t)t * a.dim + r] = acc;
 }
 

@@ -240,8 +240,10 @@ hipError_t launch_pf_attn(const float *q, const uint16_t *kc, const uint16_t *vc
 hipError_t launch_pf_add(float *x, const float *part, int split, int64_t total, hipStream_t st);
 // x += partial-product sums (part may be null), then out = f16(rmsnorm(x) * w); dim <= 16384
 // out32: null, or [T][dim] f32 that receives the norm's f32 result as well
+// myd (with part null): x += sum_s mw[t kp + s] myd[(t kp + s) dim ..], a routed FFN's pair rows
 hipError_t launch_pf_addnorm16(float *x, const float *part, int split, const float *w, float eps, int dim, int T,
-                               uint16_t *out, hipStream_t st, float *out32 = nullptr);
+                               uint16_t *out, hipStream_t st, float *out32 = nullptr, const float *mw = nullptr,
+                               const float *myd = nullptr, int kp = 0);
 hipError_t launch_pf_swiglu16(const float *g, int gs, const float *u, int us, int64_t total, uint16_t *out,
                               hipStream_t st);
 // prefill_hybrid.hip: batched prefill of the Qwen3.5 hybrid layers

@@ -39,12 +39,16 @@ static __device__ __forceinline__ float block_sum(float v, float *red) {
 // sublayer fused with the next sublayer's norm; x read once, kept in
 // registers (NV float4 per thread).  The row, the norm weights and the first
 // 16 / NV slices are requested together, the slices summed in order (one
-// memory round trip per slice took ~9 us at 64 tokens and 8 slices).
+// memory round trip per slice took ~9 us at 64 tokens and 8 slices).  With
+// myd set, the addend is instead a routed-expert FFN's output, the weighted
+// sum of the token's kp pair rows in slot order, sum_s mw[t kp + s] myd[t kp
+// + s] (the sum of pf_moe_combine_kernel, which this replaces ahead of a norm).
 // Grid: T; dim <= WG * 4 * NV.
 constexpr int PF_NPT = 64;
 template <int NV>
 __global__ __launch_bounds__(WG) void pf_addnorm16_kernel(float *x, const float *part, int split, const float *w,
-                                                          float eps, int dim, int T, uint16_t *out, float *out32) {
+                                                          float eps, int dim, int T, uint16_t *out, float *out32,
+                                                          const float *mw, const float *myd, int kp) {
 #pragma clang fp contract(off)
     constexpr int PB = NV >= 16 ? 1 : 16 / NV;  // slices per round trip
     __shared__ float red[WG / WAVE];
@@ -88,6 +92,39 @@ __global__ __launch_bounds__(WG) void pf_addnorm16_kernel(float *x, const float 
                 }
         }
     }
+    if (myd) {
+        float4 acc[NV];
+#pragma unroll
+        for (int r = 0; r < NV; r++) acc[r] = float4{0.f, 0.f, 0.f, 0.f};
+        const float4 *y4 = (const float4 *)myd + t * kp * d4;
+        for (int s0 = 0; s0 < kp; s0 += PB) {
+            float4 yz[PB][NV];
+            float wz[PB];
+#pragma unroll
+            for (int k = 0; k < PB; k++)
+                if (s0 + k < kp) {
+                    wz[k] = mw[t * kp + s0 + k];
+#pragma unroll
+                    for (int r = 0; r < NV; r++) {
+                        const int i = threadIdx.x + WG * r;
+                        if (i < d4) yz[k][r] = y4[(s0 + k) * d4 + i];
+                    }
+                }
+#pragma unroll
+            for (int k = 0; k < PB; k++)
+                if (s0 + k < kp) {
+#pragma unroll
+                    for (int r = 0; r < NV; r++) {
+                        acc[r].x += wz[k] * yz[k][r].x; acc[r].y += wz[k] * yz[k][r].y;
+                        acc[r].z += wz[k] * yz[k][r].z; acc[r].w += wz[k] * yz[k][r].w;
+                    }
+                }
+        }
+#pragma unroll
+        for (int r = 0; r < NV; r++) {
+            v[r].x += acc[r].x; v[r].y += acc[r].y; v[r].z += acc[r].z; v[r].w += acc[r].w;
+        }
+    }
     float ss = 0.f;
 #pragma unroll
     for (int r = 0; r < NV; r++) {
@@ -101,7 +138,7 @@ __global__ __launch_bounds__(WG) void pf_addnorm16_kernel(float *x, const float 
     for (int r = 0; r < NV; r++) {
         const int i = threadIdx.x + WG * r;
         if (i < d4) {
-            if (part) xt[i] = v[r];
+            if (part || myd) xt[i] = v[r];
             const float4 n{wv[r].x * (s * v[r].x), wv[r].y * (s * v[r].y), wv[r].z * (s * v[r].z),
                            wv[r].w * (s * v[r].w)};
             o4[i] = uint2{(uint32_t)f2h(n.x) | ((uint32_t)f2h(n.y) << 16), (uint32_t)f2h(n.z) | ((uint32_t)f2h(n.w) << 16)};
@@ -517,10 +554,12 @@ hipError_t launch_pf_attn(const float *q, const uint16_t *kc, const uint16_t *vc
 }
 
 hipError_t launch_pf_addnorm16(float *x, const float *part, int split, const float *w, float eps, int dim, int T,
-                               uint16_t *out, hipStream_t st, float *out32) {
-    if (dim > WG * PF_NPT) return hipErrorInvalidValue;
+                               uint16_t *out, hipStream_t st, float *out32, const float *mw, const float *myd, int kp) {
+    if (dim > WG * PF_NPT || (myd && (part || !mw || kp < 1))) return hipErrorInvalidValue;
     const int nv = (dim / 4 + WG - 1) / WG;
-#define PF_AN(NV) hipLaunchKernelGGL(pf_addnorm16_kernel<NV>, dim3(T), dim3(WG), 0, st, x, part, split, w, eps, dim, T, out, out32)
+#define PF_AN(NV)                                                                                              \
+    hipLaunchKernelGGL(pf_addnorm16_kernel<NV>, dim3(T), dim3(WG), 0, st, x, part, split, w, eps, dim, T, out, out32, \
+                       mw, myd, kp)
     if (nv <= 1) PF_AN(1);
     else if (nv <= 2) PF_AN(2);
     else if (nv <= 4) PF_AN(4);

@@ -12,8 +12,8 @@
 //                      prefill.hip's (launch_pf_attn with a gate).
 // Linear-attention layer (forward_linear_layer):
 //   pf_dn_conv_kernel       causal depthwise conv over the chunk (inputs before
-//                           the chunk from the conv state) + silu
-//   pf_dn_conv_state_kernel the conv state after the chunk (its last inputs)
+//                           the chunk from the conv state) + silu; the conv
+//                           state after the chunk (its last inputs)
 //   pf_dn_prep_kernel       per token: l2norm of q (times 1/sqrt(head_k_dim))
 //                           and k, beta = sigmoid(b), decay = exp(ssm_a
 //                           softplus(a + dt_bias)) and its log
@@ -116,7 +116,11 @@ constexpr int DN_TT = 8;  // tokens per thread of the conv
 // of the decode step, where in(tau) is the in_qkv projection of token tau of
 // the chunk or, before the chunk (tau in [-(KS-1), 0)), the conv state's
 // input.  The window and the tokens are gathered together (clamped indices,
-// every load unconditional).  Grid (ceil(conv_dim / 256), ceil(T / 8)).
+// every load unconditional).  The first token block, the only one that reads
+// the conv state, also writes the state after the chunk: its last KS-1
+// inputs, oldest first (T >= KS-1, so every one comes from the chunk; the
+// same thread reads the old state first).  Grid (ceil(conv_dim / 256),
+// ceil(T / 8)).
 template <int KS>
 __global__ __launch_bounds__(WG) void pf_dn_conv_kernel(PfDnArgs a) {
 #pragma clang fp contract(off)
@@ -134,8 +138,14 @@ __global__ __launch_bounds__(WG) void pf_dn_conv_kernel(PfDnArgs a) {
     parts_gather(xs, a.qkv, a.qkvs, (size_t)a.T * CD,
                  [&](int j) { return (size_t)min(max(t0 - KM1 + j, 0), t1 - 1) * CD + c; });
     if (t0 == 0) {  // t0 is a multiple of DN_TT >= KM1: only the first block reads the state
+        float tail[KM1 > 0 ? KM1 : 1];
+        if constexpr (KM1 > 0)
+            parts_gather(tail, a.qkv, a.qkvs, (size_t)a.T * CD, [&](int k) { return (size_t)(a.T - KM1 + k) * CD + c; });
 #pragma unroll
-        for (int k = 0; k < KM1; k++) xs[k] = st[k];
+        for (int k = 0; k < KM1; k++) {
+            xs[k] = st[k];
+            a.conv_state[(size_t)c * KM1 + k] = tail[k];
+        }
     }
 #pragma unroll
     for (int i = 0; i < DN_TT; i++) {
@@ -145,21 +155,6 @@ __global__ __launch_bounds__(WG) void pf_dn_conv_kernel(PfDnArgs a) {
         for (int k = 0; k < KM1; k++) acc += w[k] * xs[i + k];
         a.conv_out[(size_t)(t0 + i) * CD + c] = silu_ref(acc);
     }
-}
-
-// the conv state after the chunk: its last KS-1 inputs, oldest first (runs
-// after pf_dn_conv_kernel, which reads the state from before the chunk;
-// T >= KS-1, so every one comes from the chunk)
-template <int KS>
-__global__ __launch_bounds__(WG) void pf_dn_conv_state_kernel(PfDnArgs a) {
-    constexpr int KM1 = KS > 1 ? KS - 1 : 1;
-    const int CD = 2 * a.n_kh * a.hk + a.n_vh * a.hv;
-    const int c = (int)blockIdx.x * WG + threadIdx.x;
-    if (c >= CD || KS < 2) return;
-    float x[KM1];
-    parts_gather(x, a.qkv, a.qkvs, (size_t)a.T * CD, [&](int k) { return (size_t)(a.T - KM1 + k) * CD + c; });
-#pragma unroll
-    for (int k = 0; k < KM1; k++) a.conv_state[(size_t)c * KM1 + k] = x[k];
 }
 
 // Per token (grid T): l2norm of each k head's q and k (qwen3_5/ops.odin:27-37, eps
@@ -1113,7 +1108,6 @@ hipError_t launch_pf_deltanet(const PfDnArgs &a, hipStream_t st) {
         return hipErrorInvalidValue;
     const int CD = 2 * a.n_kh * a.hk + a.n_vh * a.hv;
     hipLaunchKernelGGL(pf_dn_conv_kernel<4>, dim3(nblk(CD, WG), nblk(a.T, DN_TT)), dim3(WG), 0, st, a);
-    hipLaunchKernelGGL(pf_dn_conv_state_kernel<4>, dim3(nblk(CD, WG)), dim3(WG), 0, st, a);
     hipLaunchKernelGGL(pf_dn_prep_kernel<128>, dim3((unsigned)a.T), dim3(WG), 0, st, a);
     const dim3 dgrid((unsigned)a.n_vh, 128 / 32);
     if (a.chunk == 64 && a.T <= DC) {
