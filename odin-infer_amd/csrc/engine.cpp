@@ -1386,6 +1386,26 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T, bool combine = true) {
 // rows != nullptr: the classifier of every token of the chunk, token t's
 // logits to rows + t * vocab (engine_verify_batch); otherwise the last token's
 // logits to e->logits.
+// Projections of the same f16 input into partial-product buffers P[idx[i]]
+// (slice counts to split[i]): consecutive matrices of one type share a launch
+// (launch_gemm_parts_multi; the same blocks and results as a launch each).
+int prefill_projections(oi_engine *e, const DMat *const *m, const int *idx, int n, int T, int *split) {
+    for (int i = 0; i < n;) {
+        int j = i + 1;
+        while (j < n && j - i < 4 && m[j]->type == m[i]->type && m[j]->cols == m[i]->cols) j++;
+        float *part[4];
+        size_t pb[4];
+        for (int k = i; k < j; k++) {
+            part[k - i] = e->pf_p[idx[k]];
+            pb[k - i] = e->pf_pbytes[idx[k]];
+        }
+        if (j - i == 1) HIP_TRY(launch_gemm_parts(*m[i], e->pf_xb, T, part[0], pb[0], &split[i], e->stream));
+        else HIP_TRY(launch_gemm_parts_multi(m + i, part, pb, j - i, e->pf_xb, T, split + i, e->stream));
+        i = j;
+    }
+    return OI_OK;
+}
+
 int prefill_chunk(oi_engine *e, const int32_t *tokens, int T, int pos, float *rows = nullptr) {
     const hipStream_t st = e->stream;
     const oi_config &c = e->cfg;
@@ -1400,10 +1420,14 @@ int prefill_chunk(oi_engine *e, const int32_t *tokens, int T, int pos, float *ro
     for (size_t l = 0; l < e->layers.size(); l++) {
         const LayerDev &L = e->layers[l];
         int qs = 1, ks = 1, vs = 1, s0 = 1, s1 = 1, s2 = 1, s3 = 1;
+        if (L.kind == LK_QWEN3 || L.kind == LK_FULL) {
+            const DMat *pm[3] = {&L.wq, &L.wk, &L.wv};
+            const int pi[3] = {0, 1, 2};
+            int sp[3];
+            if (prefill_projections(e, pm, pi, 3, T, sp)) return -1;
+            qs = sp[0]; ks = sp[1]; vs = sp[2];
+        }
         if (L.kind == LK_QWEN3) {
-            HIP_TRY(launch_gemm_parts(L.wq, e->pf_xb, T, P[0], PB[0], &qs, st));
-            HIP_TRY(launch_gemm_parts(L.wk, e->pf_xb, T, P[1], PB[1], &ks, st));
-            HIP_TRY(launch_gemm_parts(L.wv, e->pf_xb, T, P[2], PB[2], &vs, st));
             PfQkvArgs qa{P[0], P[1], P[2], qs, ks, vs, L.q_norm, L.k_norm, eps, e->rope_cs, L.kc, L.vc, e->pf_q,
                          T, pos, (int32_t)c.seq_len, (int32_t)c.n_heads, (int32_t)c.n_kv_heads};
             HIP_TRY(launch_pf_qkv(qa, hd, st));
@@ -1411,9 +1435,6 @@ int prefill_chunk(oi_engine *e, const int32_t *tokens, int T, int pos, float *ro
                                    (int)c.n_kv_heads, hd, st));
             HIP_TRY(launch_gemm_parts(L.wo, e->pf_xb, T, P[0], PB[0], &s0, st));
         } else if (L.kind == LK_FULL) {
-            HIP_TRY(launch_gemm_parts(L.wq, e->pf_xb, T, P[0], PB[0], &qs, st));
-            HIP_TRY(launch_gemm_parts(L.wk, e->pf_xb, T, P[1], PB[1], &ks, st));
-            HIP_TRY(launch_gemm_parts(L.wv, e->pf_xb, T, P[2], PB[2], &vs, st));
             PfQ35Args qa{P[0], P[1], P[2], qs, ks, vs, L.q_norm, L.k_norm, e->inv_freq, eps, (int32_t)e->rotary_dim,
                          L.kc, L.vc, e->pf_q, e->pf_gate, T, pos, (int32_t)c.seq_len, (int32_t)c.n_heads,
                          (int32_t)c.n_kv_heads};
@@ -1424,10 +1445,11 @@ int prefill_chunk(oi_engine *e, const int32_t *tokens, int T, int pos, float *ro
                                    (int)c.n_kv_heads, hd, st, e->pf_gate, P[1], PB[1]));
             HIP_TRY(launch_gemm_parts(L.wo, e->pf_xb, T, P[0], PB[0], &s0, st));
         } else {
-            HIP_TRY(launch_gemm_parts(L.in_qkv, e->pf_xb, T, P[0], PB[0], &s0, st));
-            HIP_TRY(launch_gemm_parts(L.in_z, e->pf_xb, T, P[1], PB[1], &s1, st));
-            HIP_TRY(launch_gemm_parts(L.in_b, e->pf_xb, T, P[2], PB[2], &s2, st));
-            HIP_TRY(launch_gemm_parts(L.in_a, e->pf_xb, T, P[3], PB[3], &s3, st));
+            const DMat *pm[4] = {&L.in_qkv, &L.in_z, &L.in_b, &L.in_a};
+            const int pi[4] = {0, 1, 2, 3};
+            int sp[4];
+            if (prefill_projections(e, pm, pi, 4, T, sp)) return -1;
+            s0 = sp[0]; s1 = sp[1]; s2 = sp[2]; s3 = sp[3];
             PfDnArgs da{};
             da.qkv = P[0]; da.z = P[1]; da.b = P[2]; da.a = P[3];
             da.qkvs = s0; da.zs = s1; da.bs = s2; da.as = s3;

@@ -217,6 +217,10 @@ hipError_t launch_gemm_swiglu(const DMat &gate, const DMat &up, const uint16_t *
                               hipStream_t st);
 hipError_t launch_gemm_parts(const DMat &m, const uint16_t *x, int32_t n, float *part, size_t part_bytes, int *split,
                              hipStream_t st);
+// launch_gemm_parts of up to 4 projections of the same x (same type and K) in
+// one launch: matrix i's partial products to part[i], its slice count to split[i]
+hipError_t launch_gemm_parts_multi(const DMat *const *m, float *const *part, const size_t *part_bytes, int nseg,
+                                   const uint16_t *x, int32_t n, int *split, hipStream_t st);
 
 // prefill.hip: the per-token operations of batched prefill
 struct PfQkvArgs {
