@@ -28,12 +28,14 @@
 // sum in a fixed order (per workgroup, then the workgroups in order), the
 // same in every workgroup that needs it.  The top-p order is never
 // materialised: the boundary element is found by radix selection over the
-// float bits of p (positive floats order as their bit patterns), four 8-bit
-// digits from the top, one launch per digit, each workgroup adding its
-// candidates' per-bucket count, mass and lowest index to a device histogram
-// and every workgroup walking the previous digit's histogram the same way.
+// float bits of p (positive floats order as their bit patterns; the sign bit
+// is 0), three digits from the top (bits 30..20, 19..9, 8..0: 2048, 2048 and
+// 512 buckets), one launch per digit, each workgroup adding its candidates'
+// per-bucket count, mass and lowest index to a device histogram and every
+// workgroup walking the previous digit's histogram the same way (four 8-bit
+// digits took two launches more per draw: 63.5 us against ~50).
 //
-// Launches per draw: temperature 0: 2; multinomial: 4; top-p: 11.  The
+// Launches per draw: temperature 0: 2; multinomial: 4; top-p: 9.  The
 // sequence depends only on the mode (sample_mode), which the caller knows,
 // so a captured graph holds one mode's sequence.
 
@@ -52,10 +54,14 @@ constexpr int MAXG = SAMPLE_MAX_VOCAB / SLICE;
 // rounds the fraction), so the fixed-point total is unbiased against the f32 sum
 __device__ __forceinline__ uint64_t fix40(float p) { return (uint64_t)rintf(p * 1099511627776.0f); }
 
+constexpr int NB = 2048;  // buckets of a digit
+// digit t from the top: bits [SH[t], SH[t] + WD[t])
+__device__ __forceinline__ int dshift(int t) { return t == 0 ? 20 : t == 1 ? 9 : 0; }
+__device__ __forceinline__ uint32_t dmask(int t) { return t == 2 ? 511u : 2047u; }
 struct Hist {
-    uint32_t cnt[256];
-    uint32_t lo[256];  // lowest index in the bucket
-    unsigned long long mass[256];
+    uint32_t cnt[NB];
+    uint32_t lo[NB];  // lowest index in the bucket
+    unsigned long long mass[NB];
 };
 
 // The selection in progress, handed from one digit's launch to the next
@@ -67,8 +73,8 @@ struct Sel {
     int32_t all, done, pad0, pad1;  // all: the candidates' whole mass within topp; done: pick made
 };
 
-constexpr int NHIST = 7;  // digit histograms: boundary 3..0 -> 0..3, coin 2..0 -> 4..6
-constexpr int NSEL = 12;
+constexpr int NHIST = 5;  // digit histograms: boundary digits 0..2 -> 0..2, coin digits 1, 2 -> 3, 4
+constexpr int NSEL = 8;
 struct SampleWork {
     Hist h[NHIST];
     float pmax[MAXG], psum[MAXG];
@@ -220,49 +226,35 @@ __device__ int block_find(const unsigned long long (&wt)[2][4], int base, unsign
 
 // Bucket of h where the running mass from the top, starting at *above, first
 // exceeds target; -1 if none.  *above becomes the mass of the higher buckets.
-// One wave (wave 0) walks; the result goes to every thread.
+// Thread t takes buckets NB-1-8t .. NB-8-8t (descending); the crossing thread
+// walks its eight; the result goes to every thread.
 __device__ int walk_buckets(const Hist &h, unsigned long long target, unsigned long long *above, Lds &s) {
-    const int lane = threadIdx.x & (WAVE - 1);
-    if (threadIdx.x < WAVE) {
-        unsigned long long m[4], sum = 0;  // buckets 255 - 4 lane - x, descending
+    constexpr int BPT = NB / SB;
+    unsigned long long m[BPT], sum = 0;
 #pragma unroll
-        for (int x = 0; x < 4; x++) {
-            m[x] = h.mass[255 - 4 * lane - x];
-            sum += m[x];
-        }
-        unsigned long long incl = sum;
-#pragma unroll
-        for (int o = 1; o < WAVE; o <<= 1) {
-            const unsigned long long y = __shfl_up(incl, o, WAVE);
-            if (lane >= o) incl += y;
-        }
-        const unsigned long long base = *above + incl - sum;
-        const unsigned long long bal = __ballot(base + sum > target);
-        if (bal == 0) {
-            if (lane == 0) {
-                s.pick = -1;
-                s.s.above = *above + __shfl(incl, WAVE - 1, WAVE);
+    for (int x = 0; x < BPT; x++) {
+        m[x] = h.mass[NB - 1 - BPT * (int)threadIdx.x - x];
+        sum += m[x];
+    }
+    if (threadIdx.x == 0) s.pick = -1;
+    unsigned long long tot;
+    const unsigned long long base = *above + block_excl_scan(sum, s, &tot);  // (its barriers order s.pick)
+    if (base <= target && target < base + sum) {  // exactly one thread
+        unsigned long long run = base;
+        int sel = -1;
+        for (int x = 0; x < BPT; x++) {
+            if (run + m[x] > target) {
+                sel = NB - 1 - BPT * (int)threadIdx.x - x;
+                break;
             }
-        } else {
-            const int L = __ffsll((long long)bal) - 1;
-            if (lane == L) {
-                unsigned long long run = base;
-                int sel = -1;
-                for (int x = 0; x < 4; x++) {
-                    if (run + m[x] > target) {
-                        sel = 255 - 4 * lane - x;
-                        break;
-                    }
-                    run += m[x];
-                }
-                s.pick = sel;
-                s.s.above = run;
-            }
+            run += m[x];
         }
+        s.pick = sel;
+        s.s.above = run;
     }
     __syncthreads();
     const int sel = s.pick;
-    *above = s.s.above;
+    *above = sel >= 0 ? s.s.above : *above + tot;
     __syncthreads();
     return sel;
 }
@@ -293,16 +285,16 @@ struct Run {
 };
 
 __device__ void hist_clear(Hist &h) {
-    for (int i = threadIdx.x; i < 256; i += SB) {
+    for (int i = threadIdx.x; i < NB; i += SB) {
         h.cnt[i] = 0;
         h.lo[i] = 0xFFFFFFFFu;
         h.mass[i] = 0;
     }
 }
 
-// digit d histogram of the slice's candidates whose bits match prefix under
+// digit t histogram of the slice's candidates whose bits match prefix under
 // mask, added to the device histogram g
-__device__ void hist_digit(const float *p, int base, int n, float cutoff, int d, uint32_t prefix, uint32_t mask,
+__device__ void hist_digit(const float *p, int base, int n, float cutoff, int t, uint32_t prefix, uint32_t mask,
                            Hist *g, Lds &s) {
     hist_clear(s.h);
     float v[2][4];
@@ -316,11 +308,11 @@ __device__ void hist_digit(const float *p, int base, int n, float cutoff, int d,
             const int i = elem(base, k, x);
             const uint32_t key = __float_as_uint(v[k][x]);
             if (i < n && v[k][x] >= cutoff && (key & mask) == prefix)
-                run.add(s.h, (int)((key >> (8 * d)) & 255u), i, fix40(v[k][x]));
+                run.add(s.h, (int)((key >> dshift(t)) & dmask(t)), i, fix40(v[k][x]));
         }
     run.flush(s.h);
     __syncthreads();
-    for (int b = threadIdx.x; b < 256; b += SB)
+    for (int b = threadIdx.x; b < NB; b += SB)
         if (s.h.cnt[b]) {
             atomicAdd(&g->cnt[b], s.h.cnt[b]);
             atomicAdd(&g->mass[b], s.h.mass[b]);
@@ -375,13 +367,15 @@ __global__ __launch_bounds__(SB) void sample_penalty_kernel(SArgs a) {
     // enable_repeat_penalty's clamp (sampler.odin:42-44) applied here too, so a
     // C caller's penalty below 1 acts as 1 (off) rather than dividing by it
     const float T = ss->temperature, pen = ss->penalty < 1.0f ? 1.0f : ss->penalty;
-    if (blockIdx.x == 0)
-        for (int h = 0; h < NHIST; h++)
-            for (int i = tid; i < 256; i += SB) {
-                a.w->h[h].cnt[i] = 0;
-                a.w->h[h].lo[i] = 0xFFFFFFFFu;
-                a.w->h[h].mass[i] = 0;
-            }
+    {  // the digit histograms, cleared by all workgroups (bucket i of every histogram by one thread)
+        const int G = wg_count(a.n);
+        for (int i = blockIdx.x * SB + tid; i < NHIST * NB; i += G * SB) {
+            Hist &h = a.w->h[i / NB];
+            h.cnt[i % NB] = 0;
+            h.lo[i % NB] = 0xFFFFFFFFu;
+            h.mass[i % NB] = 0;
+        }
+    }
     for (int i = tid; i < SLICE / 32; i += SB) s.pen_bits[i] = 0;
     if (tid == 0) s.n_pen = 0;
     __syncthreads();
@@ -499,11 +493,12 @@ __global__ __launch_bounds__(SB) void sample_norm_kernel(SArgs a, int topp_mode)
 #pragma unroll
         for (int x = 0; x < 4; x++) {
             const int i = elem(base, k, x);
-            if (i < a.n && v[k][x] >= cutoff) run.add(s.h, (int)(__float_as_uint(v[k][x]) >> 24), i, fix40(v[k][x]));
+            if (i < a.n && v[k][x] >= cutoff)
+                run.add(s.h, (int)((__float_as_uint(v[k][x]) >> dshift(0)) & dmask(0)), i, fix40(v[k][x]));
         }
     run.flush(s.h);
     __syncthreads();
-    for (int b = threadIdx.x; b < 256; b += SB)
+    for (int b = threadIdx.x; b < NB; b += SB)
         if (s.h.cnt[b]) {
             atomicAdd(&a.w->h[0].cnt[b], s.h.cnt[b]);
             atomicAdd(&a.w->h[0].mass[b], s.h.mass[b]);
@@ -540,15 +535,15 @@ __global__ __launch_bounds__(SB) void sample_mult_kernel(SArgs a) {
 
 // Top-p digit rounds.  Stage k (0-based) reads a.w->sel[k] (stage 0: none)
 // and writes sel[k + 1]:
-//   stage 0: boundary target fix40(topp): walk digit 3 (h[0]), histogram digit 2 -> h[1]
-//   stages 1, 2: walk h[stage], histogram the next digit -> h[stage + 1]
-//   stage 3: walk h[3] -> the boundary value; c1 = the mass through it; coin
-//            target r = coin * c1: walk h[0] again, histogram digit 2 -> h[4]
-//   stages 4, 5: walk h[stage], histogram -> h[stage + 1]
-//   stage 6: walk h[6] -> the pick value; if its rank among equal
+//   stage 0: boundary target fix40(topp): walk digit 0 (h[0]), histogram digit 1 -> h[1]
+//   stage 1: walk h[1], histogram digit 2 -> h[2]
+//   stage 2: walk h[2] -> the boundary value; c1 = the mass through it; coin
+//            target r = coin * c1: walk h[0] again, histogram digit 1 -> h[3]
+//   stage 3: walk h[3], histogram digit 2 -> h[4]
+//   stage 4: walk h[4] -> the pick value; if its rank among equal
 //            probabilities is 0 (or it has no equal), the pick; otherwise
 //            each slice counts its equal elements
-//   stage 7: the slice holding that rank finds it
+//   stage 5: the slice holding that rank finds it
 __global__ __launch_bounds__(SB) void sample_topp_kernel(SArgs a, int stage) {
     __shared__ Lds s;
     const int base = blockIdx.x * SLICE, tid = threadIdx.x;
@@ -565,46 +560,46 @@ __global__ __launch_bounds__(SB) void sample_topp_kernel(SArgs a, int stage) {
         if (blockIdx.x == 0 && tid == 0) w->sel[stage + 1] = cur;
         return;
     }
-    auto walk_digit = [&](const Hist &gh, int d) -> int {
+    auto walk_digit = [&](const Hist &gh, int t) -> int {
         unsigned long long above = cur.above;
         const int sel = walk_buckets(gh, cur.target, &above, s);
         if (sel >= 0) {
             cur.above = above;
-            cur.prefix |= (uint32_t)sel << (8 * d);
-            cur.mask |= 255u << (8 * d);
+            cur.prefix |= (uint32_t)sel << dshift(t);
+            cur.mask |= dmask(t) << dshift(t);
             cur.tie_lo = gh.lo[sel];
             cur.tie_cnt = gh.cnt[sel];
         }
         return sel;
     };
-    if (stage == 0 || stage == 1 || stage == 2 || stage == 4 || stage == 5) {
-        const int hin = stage == 0 ? 0 : stage, d = stage >= 4 ? 6 - stage : 3 - stage;  // digit walked
-        const int sel = walk_digit(w->h[hin], d);
+    if (stage == 0 || stage == 1 || stage == 3) {
+        const int hin = stage == 0 ? 0 : stage, t = stage == 3 ? 1 : stage;  // histogram and digit walked
+        const int sel = cur.all ? -1 : walk_digit(w->h[hin], t);
         if (sel < 0) {
             // boundary: the candidates' whole mass is within topp, so all of
             // them are kept (the coin stage then takes c1 = that mass);
             // coin: unreachable (r < c1), pick 0 as the reference's fallback
-            if (stage < 3) cur.all = 1;
+            if (stage < 2) cur.all = 1;
             else {
                 cur.done = 1;
                 if (blockIdx.x == 0 && tid == 0) finalize(0, a.ss, a.state, a.tokens_out, a.pick_out);
             }
         } else {
-            hist_digit(a.p, base, a.n, cutoff, d - 1, cur.prefix, cur.mask, &w->h[hin + 1], s);
+            hist_digit(a.p, base, a.n, cutoff, t + 1, cur.prefix, cur.mask, &w->h[stage == 3 ? 4 : hin + 1], s);
         }
         if (blockIdx.x == 0 && tid == 0) w->sel[stage + 1] = cur;
         return;
     }
-    if (stage == 3) {
+    if (stage == 2) {
         if (!cur.all) {
-            walk_digit(w->h[3], 0);
+            walk_digit(w->h[2], 2);
             // equal probabilities in index order: the j-th crosses
             const uint64_t P = fix40(__uint_as_float(cur.prefix));
             const uint64_t j = P ? (cur.target - cur.above) / P : 0;
             cur.c1 = cur.above + (j + 1) * P;
         } else {
             unsigned long long t = 0;
-            for (int b = 0; b < 256; b++) t += w->h[0].mass[b];
+            for (int b = 0; b < NB; b++) t += w->h[0].mass[b];
             cur.c1 = t;
         }
         // r = coin * c1: (c1 * coin_k) >> 24 without overflow
@@ -612,18 +607,18 @@ __global__ __launch_bounds__(SB) void sample_topp_kernel(SArgs a, int stage) {
         Sel nxt{};
         nxt.target = (hi << 40) | (lo >> 24);
         cur = nxt;
-        const int sel = walk_digit(w->h[0], 3);
+        const int sel = walk_digit(w->h[0], 0);
         if (sel < 0) {  // unreachable: r < c1
             cur.done = 1;
             if (blockIdx.x == 0 && tid == 0) finalize(0, a.ss, a.state, a.tokens_out, a.pick_out);
         } else {
-            hist_digit(a.p, base, a.n, cutoff, 2, cur.prefix, cur.mask, &w->h[4], s);
+            hist_digit(a.p, base, a.n, cutoff, 1, cur.prefix, cur.mask, &w->h[3], s);
         }
         if (blockIdx.x == 0 && tid == 0) w->sel[stage + 1] = cur;
         return;
     }
-    if (stage == 6) {
-        const int sel = walk_digit(w->h[6], 0);
+    if (stage == 4) {
+        const int sel = walk_digit(w->h[4], 2);
         if (sel < 0) {  // unreachable
             cur.done = 1;
             if (blockIdx.x == 0 && tid == 0) finalize(0, a.ss, a.state, a.tokens_out, a.pick_out);
@@ -636,7 +631,7 @@ __global__ __launch_bounds__(SB) void sample_topp_kernel(SArgs a, int stage) {
             cur.done = 1;
             if (blockIdx.x == 0 && tid == 0) finalize((int)cur.tie_lo, a.ss, a.state, a.tokens_out, a.pick_out);
         } else {
-            cur.c1 = j;  // the rank, for stage 7
+            cur.c1 = j;  // the rank, for stage 5
             float v[2][4];
             load8(a.p, base, a.n, v);
             unsigned long long c = 0;
@@ -650,7 +645,7 @@ __global__ __launch_bounds__(SB) void sample_topp_kernel(SArgs a, int stage) {
         if (blockIdx.x == 0 && tid == 0) w->sel[stage + 1] = cur;
         return;
     }
-    // stage 7: rank j among the equal probabilities, in index order
+    // stage 5: rank j among the equal probabilities, in index order
     unsigned long long before = 0;
     for (int g = 0; g < (int)blockIdx.x; g++) before += w->pties[g];
     const unsigned long long j = cur.c1;
@@ -689,7 +684,7 @@ hipError_t launch_sample(const float *logits, float *p, int n, SampleState *ss, 
         hipLaunchKernelGGL(sample_mult_kernel, grid, dim3(SB), 0, st, a);
         return hipGetLastError();
     }
-    for (int stage = 0; stage < 8; stage++) hipLaunchKernelGGL(sample_topp_kernel, grid, dim3(SB), 0, st, a, stage);
+    for (int stage = 0; stage < 6; stage++) hipLaunchKernelGGL(sample_topp_kernel, grid, dim3(SB), 0, st, a, stage);
     return hipGetLastError();
 }
 
