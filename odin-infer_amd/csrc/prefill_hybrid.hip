@@ -502,17 +502,38 @@ __device__ __forceinline__ void dc_lower_block(int p, int &bi, int &bj) {
 // The chunk's q and k rows of k head kh (zeros past nb) as float4 pieces:
 // loaded into registers all at once, then stored to LDS rows of pitch HK + 4
 // (a loop that stores each piece as it arrives waits for every load in turn).
+// RAW: the conv output's q and k (rows of conv_dim), not yet normalised.
 constexpr int DC_QK4 = DC * 128 / 2 / DC_WG;
-template <int HK>
+template <int HK, bool RAW = false>
 __device__ __forceinline__ void dc_load_qk(const PfDnArgs &a, dc_f32x4 (&v)[DC_QK4], int tb, int nb, int kh) {
     static_assert(DC * HK / 2 == DC_QK4 * DC_WG, "staging shape");
-    const int KD = a.n_kh * HK;
+    const int KD = a.n_kh * HK, pitch = RAW ? 2 * KD + a.n_vh * a.hv : 2 * KD;
+    const float *src = RAW ? a.conv_out : a.qk;
 #pragma unroll
     for (int i = 0; i < DC_QK4; i++) {
         const int idx = threadIdx.x + i * DC_WG, t = idx / (HK / 2), e4 = idx % (HK / 2);
         const int side = e4 / (HK / 4), ee = 4 * (e4 % (HK / 4));
-        v[i] = t < nb ? *(const dc_f32x4 *)(a.qk + (size_t)(tb + t) * 2 * KD + side * KD + kh * HK + ee)
+        v[i] = t < nb ? *(const dc_f32x4 *)(src + (size_t)(tb + t) * pitch + side * KD + kh * HK + ee)
                       : dc_f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+}
+// pf_dn_prep_kernel's l2norm of the loaded raw rows, in registers: thread
+// piece i is token tb + idx / (HK / 2) of wave-half side (the 32 lanes of a
+// half hold one token's q or k row, four elements each); q also times
+// 1/sqrt(HK).  (The row sums run in another order than the prep kernel's.)
+template <int HK>
+__device__ __forceinline__ void dc_l2norm_qk(dc_f32x4 (&v)[DC_QK4]) {
+#pragma clang fp contract(off)
+    static_assert(HK / 4 == 32, "a q or k row is half a wave");
+    const bool isq = (threadIdx.x & (WAVE - 1)) < 32;
+#pragma unroll
+    for (int i = 0; i < DC_QK4; i++) {
+        float ss = v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3];
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) ss += __shfl_xor(ss, o, WAVE);
+        const float inv = 1.0f / fmaxf(sqrtf(ss), 1e-6f);
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[i][e] = isq ? v[i][e] * inv * (1.0f / sqrtf((float)HK)) : v[i][e] * inv;
     }
 }
 template <int HK>
@@ -903,14 +924,23 @@ __global__ __launch_bounds__(DC_WG) void pf_dc_single_kernel(PfDnArgs a) {
     {  // every load issued before any is stored
         constexpr int V4 = DC * DC_CB / 4 / DC_WG;
         static_assert(V4 == 1, "one v piece per thread");
+        // (this kernel also does pf_dn_prep_kernel's work for its heads: the
+        // conv output's q / k rows l2-normalised here, the gates from the b
+        // and a projections)
         dc_f32x4 qk4[DC_QK4];
-        dc_load_qk<HK>(a, qk4, 0, nb, kh);
+        dc_load_qk<HK, true>(a, qk4, 0, nb, kh);
         const int vt = threadIdx.x / (DC_CB / 4), vc = 4 * (threadIdx.x % (DC_CB / 4));
         const dc_f32x4 v4 = vt < nb ? *(const dc_f32x4 *)(a.conv_out + (size_t)vt * CD + 2 * KD + vh * HV + c0 + vc)
                                     : dc_f32x4{0.f, 0.f, 0.f, 0.f};
         const int t = threadIdx.x;
-        const float b = t < nb ? a.gates[(size_t)t * 3 * a.n_vh + vh] : 0.f;
-        const float g = t < nb ? a.gates[(size_t)t * 3 * a.n_vh + 2 * a.n_vh + vh] : 0.f;
+        float b = 0.f, g = 0.f;
+        if (t < nb) {
+            const size_t slice = (size_t)a.T * a.n_vh, i = (size_t)t * a.n_vh + vh;
+            const float bb = parts_at(a.b, a.bs, slice, i), av = parts_at(a.a, a.as, slice, i);
+            g = a.a_decay[vh] * softplus_ref(av + a.dt_bias[vh]);  // log of the decay
+            b = sigmoid_ref(bb);
+        }
+        dc_l2norm_qk<HK>(qk4);
 #pragma unroll
         for (int ct = 0; ct < 2; ct++)
 #pragma unroll
@@ -1108,8 +1138,9 @@ hipError_t launch_pf_deltanet(const PfDnArgs &a, hipStream_t st) {
         return hipErrorInvalidValue;
     const int CD = 2 * a.n_kh * a.hk + a.n_vh * a.hv;
     hipLaunchKernelGGL(pf_dn_conv_kernel<4>, dim3(nblk(CD, WG), nblk(a.T, DN_TT)), dim3(WG), 0, st, a);
-    hipLaunchKernelGGL(pf_dn_prep_kernel<128>, dim3((unsigned)a.T), dim3(WG), 0, st, a);
     const dim3 dgrid((unsigned)a.n_vh, 128 / 32);
+    // the one-launch chunk normalises q / k and forms the gates itself
+    if (!(a.chunk == 64 && a.T <= DC)) hipLaunchKernelGGL(pf_dn_prep_kernel<128>, dim3((unsigned)a.T), dim3(WG), 0, st, a);
     if (a.chunk == 64 && a.T <= DC) {
         hipLaunchKernelGGL((pf_dc_single_kernel<128, 128>), dim3((unsigned)a.n_vh, 128 / DC_CB), dim3(DC_WG), 0, st,
                            a);
