@@ -20,6 +20,7 @@ namespace oi {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
+template <int BS = WG>
 static __device__ __forceinline__ float block_sum(float v, float *red) {
     v = wave_sum(v);
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
@@ -28,7 +29,7 @@ static __device__ __forceinline__ float block_sum(float v, float *red) {
     __syncthreads();
     float s = 0.f;
 #pragma unroll
-    for (int w = 0; w < WG / WAVE; w++) s += red[w];
+    for (int w = 0; w < BS / WAVE; w++) s += red[w];
     return s;
 }
 
@@ -43,15 +44,17 @@ static __device__ __forceinline__ float block_sum(float v, float *red) {
 // myd set, the addend is instead a routed-expert FFN's output, the weighted
 // sum of the token's kp pair rows in slot order, sum_s mw[t kp + s] myd[t kp
 // + s] (the sum of pf_moe_combine_kernel, which this replaces ahead of a norm).
-// Grid: T; dim <= WG * 4 * NV.
+// Grid: T, BS threads (512 where dim allows one float4 per thread: twice the
+// loads in flight per token, 6.6 -> 5.6 us at config 5's 64-token chunk);
+// dim <= BS * 4 * NV.
 constexpr int PF_NPT = 64;
-template <int NV>
-__global__ __launch_bounds__(WG) void pf_addnorm16_kernel(float *x, const float *part, int split, const float *w,
+template <int NV, int BS = WG>
+__global__ __launch_bounds__(BS) void pf_addnorm16_kernel(float *x, const float *part, int split, const float *w,
                                                           float eps, int dim, int T, uint16_t *out, float *out32,
                                                           const float *mw, const float *myd, int kp) {
 #pragma clang fp contract(off)
     constexpr int PB = NV >= 16 ? 1 : 16 / NV;  // slices per round trip
-    __shared__ float red[WG / WAVE];
+    __shared__ float red[BS / WAVE];
     const size_t t = blockIdx.x;
     const int d4 = dim / 4;
     float4 *xt = (float4 *)(x + t * dim);
@@ -59,7 +62,7 @@ __global__ __launch_bounds__(WG) void pf_addnorm16_kernel(float *x, const float 
     float4 v[NV], wv[NV];
 #pragma unroll
     for (int r = 0; r < NV; r++) {  // every load of the row issued before any use
-        const int i = threadIdx.x + WG * r;
+        const int i = threadIdx.x + BS * r;
         if (i < d4) {
             v[r] = xt[i];
             wv[r] = w4[i];
@@ -75,7 +78,7 @@ __global__ __launch_bounds__(WG) void pf_addnorm16_kernel(float *x, const float 
                 if (z0 + k < split) {
 #pragma unroll
                     for (int r = 0; r < NV; r++) {
-                        const int i = threadIdx.x + WG * r;
+                        const int i = threadIdx.x + BS * r;
                         if (i < d4) pz[k][r] = p4[(z0 + k) * slice + i];
                     }
                 }
@@ -84,7 +87,7 @@ __global__ __launch_bounds__(WG) void pf_addnorm16_kernel(float *x, const float 
                 if (z0 + k < split) {
 #pragma unroll
                     for (int r = 0; r < NV; r++) {
-                        const int i = threadIdx.x + WG * r;
+                        const int i = threadIdx.x + BS * r;
                         if (i < d4) {
                             v[r].x += pz[k][r].x; v[r].y += pz[k][r].y; v[r].z += pz[k][r].z; v[r].w += pz[k][r].w;
                         }
@@ -106,7 +109,7 @@ __global__ __launch_bounds__(WG) void pf_addnorm16_kernel(float *x, const float 
                     wz[k] = mw[t * kp + s0 + k];
 #pragma unroll
                     for (int r = 0; r < NV; r++) {
-                        const int i = threadIdx.x + WG * r;
+                        const int i = threadIdx.x + BS * r;
                         if (i < d4) yz[k][r] = y4[(s0 + k) * d4 + i];
                     }
                 }
@@ -128,15 +131,15 @@ __global__ __launch_bounds__(WG) void pf_addnorm16_kernel(float *x, const float 
     float ss = 0.f;
 #pragma unroll
     for (int r = 0; r < NV; r++) {
-        const int i = threadIdx.x + WG * r;
+        const int i = threadIdx.x + BS * r;
         if (i < d4) ss += v[r].x * v[r].x + v[r].y * v[r].y + v[r].z * v[r].z + v[r].w * v[r].w;
     }
-    ss = block_sum(ss, red);
+    ss = block_sum<BS>(ss, red);
     const float s = 1.0f / sqrtf(ss / (float)dim + eps);
     uint2 *o4 = (uint2 *)(out + t * dim);
 #pragma unroll
     for (int r = 0; r < NV; r++) {
-        const int i = threadIdx.x + WG * r;
+        const int i = threadIdx.x + BS * r;
         if (i < d4) {
             if (part || myd) xt[i] = v[r];
             const float4 n{wv[r].x * (s * v[r].x), wv[r].y * (s * v[r].y), wv[r].z * (s * v[r].z),
@@ -560,7 +563,10 @@ hipError_t launch_pf_addnorm16(float *x, const float *part, int split, const flo
 #define PF_AN(NV)                                                                                              \
     hipLaunchKernelGGL(pf_addnorm16_kernel<NV>, dim3(T), dim3(WG), 0, st, x, part, split, w, eps, dim, T, out, out32, \
                        mw, myd, kp)
-    if (nv <= 1) PF_AN(1);
+    if (dim / 4 <= 2 * WG && dim / 4 > WG)
+        hipLaunchKernelGGL((pf_addnorm16_kernel<1, 2 * WG>), dim3(T), dim3(2 * WG), 0, st, x, part, split, w, eps, dim, T,
+                           out, out32, mw, myd, kp);
+    else if (nv <= 1) PF_AN(1);
     else if (nv <= 2) PF_AN(2);
     else if (nv <= 4) PF_AN(4);
     else if (nv <= 8) PF_AN(8);
