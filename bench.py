@@ -857,6 +857,57 @@ def remove_stale_models(min_age_s=120):
     return removed
 
 
+def layer_timeline(path):
+    """Per-layer timeline of one decode token from a rocprofv3 kernel trace: the
+    dispatches of the last whole token (embed_kernel to the next embed_kernel),
+    grouped into the 36 layers' six launches (QKV GEMV, attention splits,
+    split merge, wo GEMV, gate/up GEMV, down GEMV); for each launch its mean
+    duration and the mean gap from the previous dispatch's end to its start."""
+    import csv
+    rows = []
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            nm = r["Kernel_Name"]
+            nm = nm[:nm.rfind("(")] if nm.endswith(")") else nm  # without the parameter list
+            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), nm))
+    rows.sort()
+    starts = [i for i, r in enumerate(rows) if r[2].endswith("embed_kernel")]
+    # the last whole greedy token (the run ends with sampled tokens)
+    toks = [rows[a:b] for a, b in zip(starts, starts[1:])
+            if b - a > 1 + 36 * 6 and not any("sample" in r[2] for r in rows[a:b])]
+    if not toks:
+        sys.exit("no whole greedy token in the trace")
+    tok = toks[-1]
+    body = tok[1:]  # after the embedding
+    nl = 36
+    per = 6
+    if len(body) < nl * per:
+        sys.exit("unexpected dispatch count %d" % len(tok))
+    names = ["QKV GEMV (RMSNorm prologue)", "attention splits", "split merge", "wo GEMV (+ residual)",
+             "gate/up GEMV (RMSNorm prologue, SwiGLU)", "down GEMV (+ residual)"]
+    dur = [[] for _ in range(per)]
+    gap = [[] for _ in range(per)]
+    prev_end = tok[0][1]
+    for l in range(nl):
+        for k in range(per):
+            st, en, _ = body[l * per + k]
+            dur[k].append((en - st) / 1e3)
+            gap[k].append((st - prev_end) / 1e3)
+            prev_end = en
+    tail = body[nl * per:]
+    span = (tok[-1][1] - tok[0][0]) / 1e3
+    busy = sum((r[1] - r[0]) / 1e3 for r in tok)
+    print("token: %d dispatches, span %.1f us, kernel time %.1f us (%.1f%%)" % (len(tok), span, busy, 100 * busy / span))
+    print("%-42s %10s %10s %10s" % ("launch (mean over the 36 layers)", "gap us", "kernel us", "kernel"))
+    for k in range(per):
+        print("%-42s %10.2f %10.2f  %s" % (names[k], sum(gap[k]) / nl, sum(dur[k]) / nl, body[k][2][-60:]))
+    lay = sum(sum(d) for d in dur) / nl
+    lg = sum(sum(g) for g in gap) / nl
+    print("%-42s %10.2f %10.2f" % ("layer", lg, lay))
+    for st, en, nm in tail:
+        print("after the layers: %s %.2f us" % (nm[-60:], (en - st) / 1e3))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -880,7 +931,13 @@ def main():
     ap.add_argument("--c5-chunks", default="64,512", help="prompt chunk lengths of --only c5, comma-separated")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (3 times), to calibrate HBM counters")
+    ap.add_argument("--layer-timeline", default=None, metavar="TRACE_CSV",
+                    help="only summarise a rocprofv3 kernel trace of the decode (--only decode, OI_NO_GRAPH=1): "
+                         "per-layer kernel durations and gaps of its last whole token")
     args = ap.parse_args()
+    if args.layer_timeline:
+        layer_timeline(args.layer_timeline)
+        return
     remove_stale_models()
     if args.copy_calibration:
         import torch
