@@ -25,8 +25,10 @@
 // depend on the summation order (the reference's sequential f32 sums carry
 // ~1e-5 of rounding over 150k terms; picks can differ from it only when the
 // target lies within that rounding of a boundary).  The softmax sum is an f32
-// sum in a fixed order (per workgroup, then the workgroups in order), the
-// same in every workgroup that needs it.  The top-p order is never
+// sum in a fixed order (per workgroup of exp(x - the workgroup's maximum),
+// then the workgroups in order, each rescaled by exp(its maximum - the
+// maximum): one pass for the maximum and the sum), the same in every
+// workgroup that needs it.  The top-p order is never
 // materialised: the boundary element is found by radix selection over the
 // float bits of p (positive floats order as their bit patterns; the sign bit
 // is 0), three digits from the top (bits 30..20, 19..9, 8..0: 2048, 2048 and
@@ -35,7 +37,7 @@
 // workgroup walking the previous digit's histogram the same way (four 8-bit
 // digits took two launches more per draw: 63.5 us against ~50).
 //
-// Launches per draw: temperature 0: 2; multinomial: 4; top-p: 9.  The
+// Launches per draw: temperature 0: 2; multinomial: 3; top-p: 8.  The
 // sequence depends only on the mode (sample_mode), which the caller knows,
 // so a captured graph holds one mode's sequence.
 
@@ -284,19 +286,39 @@ struct Run {
     }
 };
 
-__device__ void hist_clear(Hist &h) {
+// (cnt_lo false: the masses only, the histogram of a digit whose counts and
+// lowest indices are not flushed)
+__device__ void hist_clear(Hist &h, bool cnt_lo) {
     for (int i = threadIdx.x; i < NB; i += SB) {
-        h.cnt[i] = 0;
-        h.lo[i] = 0xFFFFFFFFu;
+        if (cnt_lo) {
+            h.cnt[i] = 0;
+            h.lo[i] = 0xFFFFFFFFu;
+        }
         h.mass[i] = 0;
     }
+}
+
+// The workgroup's histogram added to the device histogram: the masses always
+// (a candidate's fix40 mass is > 0), the counts and lowest indices only for
+// the last digit, the only one whose are read (the pick's equal
+// probabilities); every atomic is one more on an address that all 75
+// workgroups update, so the first digits' histograms cost a third of it.
+__device__ void hist_flush(const Hist &h, Hist *g, bool cnt_lo) {
+    for (int b = threadIdx.x; b < NB; b += SB)
+        if (h.mass[b]) {
+            atomicAdd(&g->mass[b], h.mass[b]);
+            if (cnt_lo) {
+                atomicAdd(&g->cnt[b], h.cnt[b]);
+                atomicMin(&g->lo[b], h.lo[b]);
+            }
+        }
 }
 
 // digit t histogram of the slice's candidates whose bits match prefix under
 // mask, added to the device histogram g
 __device__ void hist_digit(const float *p, int base, int n, float cutoff, int t, uint32_t prefix, uint32_t mask,
                            Hist *g, Lds &s) {
-    hist_clear(s.h);
+    hist_clear(s.h, t == 2);
     float v[2][4];
     load8(p, base, n, v);
     __syncthreads();
@@ -312,12 +334,7 @@ __device__ void hist_digit(const float *p, int base, int n, float cutoff, int t,
         }
     run.flush(s.h);
     __syncthreads();
-    for (int b = threadIdx.x; b < NB; b += SB)
-        if (s.h.cnt[b]) {
-            atomicAdd(&g->cnt[b], s.h.cnt[b]);
-            atomicAdd(&g->mass[b], s.h.mass[b]);
-            atomicMin(&g->lo[b], s.h.lo[b]);
-        }
+    hist_flush(s.h, g, t == 2);
 }
 
 __device__ __forceinline__ float cutoff_of(const SampleState *ss, int n) {
@@ -414,50 +431,46 @@ __global__ __launch_bounds__(SB) void sample_penalty_kernel(SArgs a) {
         }
     store8(a.p, base, a.n, v);
     block_argmax(m, mi, s);
+    // the slice's sum of exp(x - its maximum), for the softmax's sum
+    float sum = 0.f;
+    if (!greedy && m != -INFINITY) {
+#pragma unroll
+        for (int k = 0; k < 2; k++)
+#pragma unroll
+            for (int x = 0; x < 4; x++)
+                if (elem(base, k, x) < a.n) sum += expf(v[k][x] - m);
+    }
+    sum = block_sum(sum, s);
     if (tid == 0) {
         a.w->pmax[blockIdx.x] = m;
         a.w->pidx[blockIdx.x] = mi;
+        a.w->psum[blockIdx.x] = sum;
     }
 }
 
 // 2. The maximum over the slices.  Temperature 0: workgroup 0 picks it.
-// Otherwise exp(x - max) into p and the slice's sum.
-__global__ __launch_bounds__(SB) void sample_exp_kernel(SArgs a, int greedy) {
+// Otherwise p = exp(x - max) / sum, the sum over the slices in order of each
+// slice's sum rescaled to the maximum (sum_g s_g exp(m_g - max), so the
+// maximum and the sum take one pass), then the slice's fixed-point mass
+// (multinomial) or its candidates' first-digit histogram (top-p).  Workgroup
+// 0 draws the coin (random_f32, sampler.odin:68-77).
+__global__ __launch_bounds__(SB) void sample_norm_kernel(SArgs a, int mode) {
 #pragma clang fp contract(off)
     __shared__ Lds s;
-    const int G = wg_count(a.n), base = blockIdx.x * SLICE;
-    float mx = a.w->pmax[0];
-    int mi = a.w->pidx[0];
-    for (int g = 1; g < G; g++) argmax_combine(mx, mi, a.w->pmax[g], a.w->pidx[g]);
-    if (greedy) {
+    const int G = wg_count(a.n), base = blockIdx.x * SLICE, tid = threadIdx.x;
+    // the slices' partials, one per thread (G <= 128 <= SB), requested
+    // together: a loop over them in one thread waited for each in turn
+    const float pm = tid < G ? a.w->pmax[tid] : -INFINITY, ps = tid < G ? a.w->psum[tid] : 0.f;
+    float mx = pm;
+    int mi = tid < G ? a.w->pidx[tid] : 0x7FFFFFFF;
+    block_argmax(mx, mi, s);
+    if (mode == SAMPLE_GREEDY) {
         if (blockIdx.x == 0 && threadIdx.x == 0)
             finalize(mi == 0x7FFFFFFF ? 0 : mi, a.ss, a.state, a.tokens_out, a.pick_out);
         return;
     }
-    float v[2][4], sum = 0.f;
-    load8(a.p, base, a.n, v);
-#pragma unroll
-    for (int k = 0; k < 2; k++)
-#pragma unroll
-        for (int x = 0; x < 4; x++)
-            if (elem(base, k, x) < a.n) {
-                v[k][x] = expf(v[k][x] - mx);
-                sum += v[k][x];
-            }
-    store8(a.p, base, a.n, v);
-    sum = block_sum(sum, s);
-    if (threadIdx.x == 0) a.w->psum[blockIdx.x] = sum;
-}
-
-// 3. p / sum (the sum over the slices in order), then the slice's fixed-point
-// mass (multinomial) or its candidates' first-digit histogram (top-p).
-// Workgroup 0 draws the coin (random_f32, sampler.odin:68-77).
-__global__ __launch_bounds__(SB) void sample_norm_kernel(SArgs a, int topp_mode) {
-#pragma clang fp contract(off)
-    __shared__ Lds s;
-    const int G = wg_count(a.n), base = blockIdx.x * SLICE;
-    float tot = 0.f;
-    for (int g = 0; g < G; g++) tot += a.w->psum[g];
+    const bool topp_mode = mode == SAMPLE_TOPP;
+    const float tot = block_sum(pm != -INFINITY ? ps * expf(pm - mx) : 0.f, s);
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         uint64_t x = a.ss->rng;
         x ^= x >> 12;
@@ -471,7 +484,7 @@ __global__ __launch_bounds__(SB) void sample_norm_kernel(SArgs a, int topp_mode)
 #pragma unroll
     for (int k = 0; k < 2; k++)
 #pragma unroll
-        for (int x = 0; x < 4; x++) v[k][x] = v[k][x] / tot;
+        for (int x = 0; x < 4; x++) v[k][x] = expf(v[k][x] - mx) / tot;
     store8(a.p, base, a.n, v);
     if (!topp_mode) {
         unsigned long long m = 0;
@@ -485,7 +498,7 @@ __global__ __launch_bounds__(SB) void sample_norm_kernel(SArgs a, int topp_mode)
         return;
     }
     const float cutoff = cutoff_of(a.ss, a.n);
-    hist_clear(s.h);
+    hist_clear(s.h, false);
     __syncthreads();
     Run run;
 #pragma unroll
@@ -498,24 +511,16 @@ __global__ __launch_bounds__(SB) void sample_norm_kernel(SArgs a, int topp_mode)
         }
     run.flush(s.h);
     __syncthreads();
-    for (int b = threadIdx.x; b < NB; b += SB)
-        if (s.h.cnt[b]) {
-            atomicAdd(&a.w->h[0].cnt[b], s.h.cnt[b]);
-            atomicAdd(&a.w->h[0].mass[b], s.h.mass[b]);
-            atomicMin(&a.w->h[0].lo[b], s.h.lo[b]);
-        }
+    hist_flush(s.h, &a.w->h[0], false);
 }
 
 // 4 (multinomial, sample_mult): the first index whose running mass exceeds
 // the coin; the last index when none does.
 __global__ __launch_bounds__(SB) void sample_mult_kernel(SArgs a) {
     __shared__ Lds s;
-    const int G = wg_count(a.n), base = blockIdx.x * SLICE;
-    unsigned long long before = 0, total = 0;
-    for (int g = 0; g < G; g++) {
-        if (g < (int)blockIdx.x) before += a.w->pmass[g];
-        total += a.w->pmass[g];
-    }
+    const int G = wg_count(a.n), base = blockIdx.x * SLICE, tid = threadIdx.x;
+    const unsigned long long pg = tid < G ? a.w->pmass[tid] : 0;  // one slice's mass per thread
+    const unsigned long long before = block_sum_u64(tid < (int)blockIdx.x ? pg : 0, s), total = block_sum_u64(pg, s);
     const unsigned long long target = (unsigned long long)a.w->coin_k << 16;  // coin * 2^40, exact
     if (total <= target) {
         if (blockIdx.x == 0 && threadIdx.x == 0) finalize(a.n - 1, a.ss, a.state, a.tokens_out, a.pick_out);
@@ -599,8 +604,8 @@ __global__ __launch_bounds__(SB) void sample_topp_kernel(SArgs a, int stage) {
             cur.c1 = cur.above + (j + 1) * P;
         } else {
             unsigned long long t = 0;
-            for (int b = 0; b < NB; b++) t += w->h[0].mass[b];
-            cur.c1 = t;
+            for (int b = tid; b < NB; b += SB) t += w->h[0].mass[b];
+            cur.c1 = block_sum_u64(t, s);
         }
         // r = coin * c1: (c1 * coin_k) >> 24 without overflow
         const unsigned long long ck = w->coin_k, lo = cur.c1 * ck, hi = __umul64hi(cur.c1, ck);
@@ -646,8 +651,8 @@ __global__ __launch_bounds__(SB) void sample_topp_kernel(SArgs a, int stage) {
         return;
     }
     // stage 5: rank j among the equal probabilities, in index order
-    unsigned long long before = 0;
-    for (int g = 0; g < (int)blockIdx.x; g++) before += w->pties[g];
+    const unsigned long long before =
+        block_sum_u64(tid < (int)blockIdx.x && tid < wg_count(a.n) ? w->pties[tid] : 0u, s);
     const unsigned long long j = cur.c1;
     if (!(before <= j && j < before + w->pties[blockIdx.x])) return;
     float v[2][4];
@@ -677,9 +682,8 @@ hipError_t launch_sample(const float *logits, float *p, int n, SampleState *ss, 
     const SArgs a{logits, p, n, ss, (SampleWork *)work, state, tokens_out, pick};
     const dim3 grid((unsigned)wg_count(n));
     hipLaunchKernelGGL(sample_penalty_kernel, grid, dim3(SB), 0, st, a);
-    hipLaunchKernelGGL(sample_exp_kernel, grid, dim3(SB), 0, st, a, (int)(mode == SAMPLE_GREEDY));
+    hipLaunchKernelGGL(sample_norm_kernel, grid, dim3(SB), 0, st, a, mode);
     if (mode == SAMPLE_GREEDY) return hipGetLastError();
-    hipLaunchKernelGGL(sample_norm_kernel, grid, dim3(SB), 0, st, a, (int)(mode == SAMPLE_TOPP));
     if (mode == SAMPLE_MULT) {
         hipLaunchKernelGGL(sample_mult_kernel, grid, dim3(SB), 0, st, a);
         return hipGetLastError();
