@@ -857,6 +857,41 @@ def remove_stale_models(min_age_s=120):
     return removed
 
 
+def prompt_breakdown(path, layers=48, calls=32):
+    """Kernel time of the first 64-token-chunk prompt in a rocprofv3 kernel trace
+    of --only c5: the first `calls` consecutive prefill calls (each starts with
+    embed_rows_kernel) whose routing runs on 64 tokens (pf_moe_topk_kernel over
+    64 workgroups, once per layer), summed by kernel and grid."""
+    import csv
+    import collections
+    rows = []
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            nm = r["Kernel_Name"]
+            nm = nm[:nm.rfind("(")] if nm.endswith(")") else nm
+            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), nm,
+                         int(r["Grid_Size_X"]) // max(1, int(r["Workgroup_Size_X"]))))
+    rows.sort()
+    starts = [i for i, r in enumerate(rows) if r[2].endswith("embed_rows_kernel")] + [len(rows)]
+    for k in range(len(starts) - calls):
+        seg = rows[starts[k]:starts[k + calls]]
+        topk = [r for r in seg if r[2].endswith("pf_moe_topk_kernel")]
+        if len(topk) == calls * layers and all(r[3] == 64 for r in topk):
+            break
+    else:
+        sys.exit("no %d-call prompt of 64-token chunks in the trace" % calls)
+    span = (seg[-1][1] - seg[0][0]) / 1e6
+    d = collections.defaultdict(list)
+    for st, en, nm, g in seg:
+        d[(nm, g)].append((en - st) / 1e3)
+    tot = sum(sum(v) for v in d.values())
+    print("first 64-token-chunk prompt: span %.1f ms, kernel time %.1f ms, %d dispatches" % (span, tot / 1e3, len(seg)))
+    for (nm, g), v in sorted(d.items(), key=lambda kv: -sum(kv[1])):
+        v.sort()
+        print("%-48s grid %5d n %5d median %6.1f us total %7.2f ms (%4.1f%%)" %
+              (nm[-48:], g, len(v), v[len(v) // 2], sum(v) / 1e3, 100 * sum(v) / tot))
+
+
 def layer_timeline(path):
     """Per-layer timeline of one decode token from a rocprofv3 kernel trace: the
     dispatches of the last whole token (embed_kernel to the next embed_kernel),
@@ -931,12 +966,18 @@ def main():
     ap.add_argument("--c5-chunks", default="64,512", help="prompt chunk lengths of --only c5, comma-separated")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (3 times), to calibrate HBM counters")
+    ap.add_argument("--prompt-breakdown", default=None, metavar="TRACE_CSV",
+                    help="only summarise a rocprofv3 kernel trace of --only c5: kernel time of the first "
+                         "64-token-chunk prompt, by kernel and grid")
     ap.add_argument("--layer-timeline", default=None, metavar="TRACE_CSV",
                     help="only summarise a rocprofv3 kernel trace of the decode (--only decode, OI_NO_GRAPH=1): "
                          "per-layer kernel durations and gaps of its last whole token")
     args = ap.parse_args()
     if args.layer_timeline:
         layer_timeline(args.layer_timeline)
+        return
+    if args.prompt_breakdown:
+        prompt_breakdown(args.prompt_breakdown)
         return
     remove_stale_models()
     if args.copy_calibration:
