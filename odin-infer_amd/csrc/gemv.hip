@@ -1307,14 +1307,15 @@ hipError_t launch_mt_dot4(const MtGemvArgs &a, int max_items, hipStream_t st) {
 // the loads alone to ~4 TB/s), while the operand takes 8 bytes of each of four
 // units.  The super-block headers of a tile (16 rows x NSB x 16 contiguous
 // bytes) are loaded whole, one tile ahead, NSB dwords per lane (HT = NSB, when
-// NSB divides 4 SBS, so that each step's headers sit in fixed registers of
-// known lanes), and each step takes its rows' headers from those lanes by
-// ds_bpermute; loaded per step instead (16 rows x 32 bytes, a quarter of 16
-// lines) they cost a fifth of the stream's time for a ninth of its bytes.
-// Otherwise (HT = 0) the headers pass through the staging rows.  The planes are combined across lanes at the
-// end of a tile into one result per lane (row n, pair G), held in registers
-// until the last tile (stores in the loop would share the memory counter with
-// the weight loads).
+// a tile takes more than one step and NSB divides 4 SBS, so that each step's
+// headers sit in fixed registers of known lanes: NSB = 4, 8), and each step
+// takes its rows' headers from those lanes by ds_bpermute; loaded per step
+// instead (16 rows x 32 bytes, a quarter of 16 lines) they cost a fifth of the
+// stream's time for a ninth of its bytes.  Otherwise (HT = 0) the headers pass
+// through the staging rows.  The planes are combined across lanes at the end
+// of a tile into one result per lane (row n, pair G), held in registers until
+// the last tile (stores in the loop would share the memory counter with the
+// weight loads).
 constexpr float QI_MAX = 268434432.f;  // 2^28 - 2^10: the rounded product stays below 2^28
 constexpr int QI_MAXT = 16;            // 16-row tiles per wave (rows of an item <= 16 * 16 * waves)
 typedef int i32x4 __attribute__((ext_vector_type(4)));
