@@ -237,7 +237,10 @@ constexpr int GW = 1024, GNW = GW / WAVE;
 // K is too long for that and both passes read x from memory after the
 // prefetch.  K/4 is a multiple of 8, so the 8-lane groups of quant4 are whole.
 // Prologue modes: NORM 0 takes x as it is, XN_RMS replaces it by rmsnorm(x) *
-// norm_w over the whole vector, XN_GATED finishes the gated RMSNorm of a
+// norm_w over the whole vector -- as norm_w * x, quantized without waiting
+// for the sum of squares: the inverse RMS is one factor of the whole row, so
+// xpre_finish returns it and the caller scales each row's dot product by it
+// (one workgroup barrier instead of two); XN_GATED finishes the gated RMSNorm of a
 // DeltaNet layer's output (qwen3_5/forward.odin:211-218): x holds o silu(z)
 // per head of GN_HV values and gss the head's four partial sums of o^2;
 // x = norm_w[j] (inv_h x), inv_h = 1 / sqrt(sum_h o^2 / GN_HV + eps).
@@ -274,15 +277,14 @@ static __device__ __forceinline__ void xpre_load(const GemvArgs &a, XPre<XR, NOR
 }
 
 template <int XR, int NORM>
-static __device__ __forceinline__ void xpre_finish(const GemvArgs &a, const XPre<XR, NORM> &p, u32x4 *xhi,
-                                                   u32x4 *xmid, u32x4 *xlo, float *xs, float *s32, float *s16,
-                                                   float *red) {
+static __device__ __forceinline__ float xpre_finish(const GemvArgs &a, const XPre<XR, NORM> &p, u32x4 *xhi,
+                                                    u32x4 *xmid, u32x4 *xlo, float *xs, float *s32, float *s16,
+                                                    float *red) {
     static_assert(NORM != XN_GATED || XR > 0, "the gated norm needs x in registers");
     const int K = a.K, tid = threadIdx.x;
     const float4 *gx = (const float4 *)a.x;
     const float4 *nw = (const float4 *)a.norm_w;
     uint32_t *hw = (uint32_t *)xhi, *mw = (uint32_t *)xmid, *lw = (uint32_t *)xlo;
-    float s = 1.f;
     if (NORM == XN_GATED) {
 #pragma unroll
         for (int i = 0; i < XR; i++) {
@@ -300,54 +302,51 @@ static __device__ __forceinline__ void xpre_finish(const GemvArgs &a, const XPre
             if (c < K / 4) quant4(g, c, hw, mw, lw, xs, s32, s16);
         }
         __syncthreads();
-        return;
-    }
-    if (xn_rms(NORM)) {
-        float ss = 0.f;
-        if (XR > 0) {
-#pragma unroll
-            for (int i = 0; i < XR; i++)
-                if (tid + i * GW < K / 4)
-                    ss += p.x[i].x * p.x[i].x + p.x[i].y * p.x[i].y + p.x[i].z * p.x[i].z + p.x[i].w * p.x[i].w;
-        } else {
-            for (int c = tid; c < K / 4; c += GW) {
-                const float4 v = gx[c];
-                ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-            }
-        }
-        ss = wave_sum(ss);
-        if ((tid & (WAVE - 1)) == 0) red[tid / WAVE] = ss;
-        __syncthreads();
-        float t[GNW / 2];
-#pragma unroll
-        for (int i = 0; i < GNW / 2; i++) t[i] = red[2 * i] + red[2 * i + 1];
-#pragma unroll
-        for (int w = GNW / 4; w >= 1; w >>= 1)
-#pragma unroll
-            for (int i = 0; i < w; i++) t[i] = t[2 * i] + t[2 * i + 1];
-        ss = t[0];
-        s = 1.0f / sqrtf(ss / (float)K + a.eps);
+        return 1.f;
     }
     auto one = [&](float4 v, float4 w, int c) {
         if (xn_rms(NORM)) {
 #pragma clang fp contract(off)
-            v.x = w.x * (s * v.x);
-            v.y = w.y * (s * v.y);
-            v.z = w.z * (s * v.z);
-            v.w = w.w * (s * v.w);
+            v.x = w.x * v.x;
+            v.y = w.y * v.y;
+            v.z = w.z * v.z;
+            v.w = w.w * v.w;
         }
         quant4(v, c, hw, mw, lw, xs, s32, s16);
     };
+    float ss = 0.f;
     if (XR > 0) {
 #pragma unroll
         for (int i = 0; i < XR; i++) {
             const int c = tid + i * GW;
-            if (c < K / 4) one(p.x[i], p.w[NORM ? i : 0], c);
+            if (c < K / 4) {
+                const float4 v = p.x[i];
+                if (xn_rms(NORM)) ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+                one(v, p.w[NORM ? i : 0], c);
+            }
         }
     } else {
-        for (int c = tid; c < K / 4; c += GW) one(gx[c], NORM ? nw[c] : gx[c], c);
+        for (int c = tid; c < K / 4; c += GW) {
+            const float4 v = gx[c];
+            if (xn_rms(NORM)) ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            one(v, NORM ? nw[c] : v, c);
+        }
+    }
+    if (xn_rms(NORM)) {
+        ss = wave_sum(ss);
+        if ((tid & (WAVE - 1)) == 0) red[tid / WAVE] = ss;
     }
     __syncthreads();
+    if (!xn_rms(NORM)) return 1.f;
+    // every thread sums the waves' partials in the same order
+    float t[GNW / 2];
+#pragma unroll
+    for (int i = 0; i < GNW / 2; i++) t[i] = red[2 * i] + red[2 * i + 1];
+#pragma unroll
+    for (int w = GNW / 4; w >= 1; w >>= 1)
+#pragma unroll
+        for (int i = 0; i < w; i++) t[i] = t[2 * i] + t[2 * i + 1];
+    return 1.0f / sqrtf(t[0] / (float)K + a.eps);
 }
 
 // LDS of gemv_q_kernel: the x planes and scales, then the workgroup's outputs
@@ -368,7 +367,8 @@ static size_t gemv_q_lds(int K, int out_rows) {
 // are clamped to the last row (computed, not stored).
 template <int T, int R, int NM, int XR, bool XU1, int NORM, int MOE = 0>
 static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int tb, int te, int wg,
-                                                const XPre<XR, NORM> &xp, int idv = 0, float wv = 0.f) {
+                                                const XPre<XR, NORM> &xp, int idv = 0, float wv = 0.f,
+                                                float xsc_r = 1.f) {
     using W = typename Types<T>::W;
     using X = typename Types<T>::X;
     extern __shared__ u32x4 smem[];
@@ -430,8 +430,10 @@ static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int 
     float *yo = s16 + K / 16;  // this workgroup's outputs
     const int wrow0 = tb * rpt, wrow1 = min(te * rpt, rows_m);
     if (tid == 0) tile_ctr = 0;  // read after the prologue's barriers
+    // xsc: the RMSNorm's inverse RMS, a factor of every row's dot product
+    float xsc = xsc_r;
     if (MOE == MOE_ROWS_R) __syncthreads();  // the kernel built the x planes before routing
-    else xpre_finish<XR, NORM>(a, xp, xhi, xmid, xlo, xs, s32, s16, red);
+    else xsc = xpre_finish<XR, NORM>(a, xp, xhi, xmid, xlo, xs, s32, s16, red);
     const XQ xq{xhi, xmid, xlo, xs, s32, s16};
     X xu;
     if (XU1) xload(xq, j, xu);
@@ -482,11 +484,11 @@ static __device__ __forceinline__ void gemv_run(const GemvArgs &a, int seg, int 
 #pragma unroll
                 for (int r = 0; r < R; r++) {
                     const int row = (tb + t) * rpt + rsub + r;
-                    float val = acc[0][r];
+                    float val = acc[0][r] * xsc;
                     if (NM == 2) {  // infer/forward.odin:128-132
 #pragma clang fp contract(off)
                         val *= 1.0f / (1.0f + expf(-val));
-                        val *= acc[NM - 1][r];
+                        val *= acc[NM - 1][r] * xsc;
                     }
                     yo[row - wrow0] = val;  // rows past the matrix land in the slack of yo
                     if (NM == 1 && a.mode == GEMV_ARGMAX && row < rows_m && better(val, row, bv, bi)) {
@@ -766,7 +768,8 @@ static __device__ __forceinline__ void router_load(const GemvArgs &a, int base, 
     }
 }
 template <int T>
-static __device__ __forceinline__ void router_logits(const GemvArgs &a, const XQ &xq, RouterPre<T> &p, float *rl) {
+static __device__ __forceinline__ void router_logits(const GemvArgs &a, const XQ &xq, RouterPre<T> &p, float *rl,
+                                                     float xsc) {
     using X = typename Types<T>::X;
     constexpr int RR = RouterPre<T>::RR;
     const int U = a.K >> 6, rpw = WAVE / U, n = a.moe_n;
@@ -778,7 +781,7 @@ static __device__ __forceinline__ void router_logits(const GemvArgs &a, const XQ
         if (base > 0) router_load<T>(a, base, p);
 #pragma unroll
         for (int st = 0; st < RR; st++) {
-            const float v = lane_group_sum(wdot(p.w[st], j, xu), U);
+            const float v = lane_group_sum(wdot(p.w[st], j, xu), U) * xsc;
             router_row<T>(a, base, st, r, j);
             if (j == 0 && r < n) rl[r] = v;
         }
@@ -828,14 +831,14 @@ __global__ __launch_bounds__(GW) void gemv_q_kernel(GemvArgs a) {
         const int K = a.K;
         u32x4 *xhi = smem, *xmid = smem + K / 16, *xlo = smem + 2 * (K / 16);
         float *xs = (float *)(smem + 3 * (K / 16)), *s32 = xs + K / 32, *s16 = s32 + K / 32;
-        xpre_finish<XR, NORM>(a, xp, xhi, xmid, xlo, xs, s32, s16, red_r);
+        const float xsc = xpre_finish<XR, NORM>(a, xp, xhi, xmid, xlo, xs, s32, s16, red_r);
         const XQ xq{xhi, xmid, xlo, xs, s32, s16};
-        router_logits<T>(a, xq, rp, rl);
+        router_logits<T>(a, xq, rp, rl, xsc);
         __syncthreads();
         int idv = 0;
         float wv = 0.f;
         moe_route(a, (int)threadIdx.x < a.moe_n ? rl[threadIdx.x] : 0.f, 0.f, idv, wv, wg);
-        gemv_run<T, R, NM, XR, XU1, NORM, MOE>(a, seg, tb, te, wg, xp, idv, wv);
+        gemv_run<T, R, NM, XR, XU1, NORM, MOE>(a, seg, tb, te, wg, xp, idv, wv, xsc);
     } else {
         XPre<XR, NORM> xp;
         xpre_load<XR, NORM>(a, xp);
