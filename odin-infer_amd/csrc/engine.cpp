@@ -1015,6 +1015,8 @@ int oi_engine_load(const char *path, const oi_opts *opts, oi_engine **out) {
     // the delta rule of a prefill chunk: in its chunked form over 64 tokens on
     // the matrix cores (default), token by token ("0"), or the lane-level
     // chunked form over 16 / 32 tokens
+    const char *pq = std::getenv("OI_PREFILL_XQ");
+    e->pf_xq_on = !(pq && pq[0] == '0');
     const char *pc = std::getenv("OI_PREFILL_DN_CHUNK");
     e->pf_dn_chunk = !pc                          ? 64
                      : std::strcmp(pc, "16") == 0 ? 16
@@ -1202,7 +1204,8 @@ int prefill_alloc(oi_engine *e) {
                                  moe ? T * KP * D * 4 : 0,
                                  moe ? T * KP * 4 : 0, moe ? T * KP * 4 : 0, moe ? NE * 4 : 0, moe ? NE * 4 : 0,
                                  moe ? NE * 4 : 0, 8 * tg, 8 * td, moe ? (size_t)8 : 0,
-                                 moe ? (T + 2 * ((T + MT_MFMA_FEW - 1) / MT_MFMA_FEW) * 16 + 4) * 4 : 0};
+                                 moe ? (T + 2 * ((T + MT_MFMA_FEW - 1) / MT_MFMA_FEW) * 16 + 4) * 4 : 0,
+                                 moe ? T * D * 4 : 0, moe ? T * (D / 32) * 4 : 0, moe ? T * 4 : 0};
     size_t total = 0;
     for (size_t b : sizes) total += al256(b);
     HIP_TRY(hipMalloc(&e->pf_mem, total));
@@ -1243,6 +1246,9 @@ int prefill_alloc(oi_engine *e) {
     e->pf_nitems = (int32_t *)take();
     e->pf_rt = (int32_t *)take();
     e->pf_rt_T = 0;
+    e->pf_xq = take();
+    e->pf_xq_sum = (float *)take();
+    e->pf_xq_scale = (float *)take();
     return OI_OK;
 }
 
@@ -1262,6 +1268,10 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T, bool combine = true) {
     // of 2048), so each workgroup stages its x once and the grid fills the GPU
     const int rps = D <= 2048 ? 8 : MT_PAIR_SLICE;
     const int slices = (T + rps - 1) / rps, pairs = T * KP;
+    // the normalized rows quantized once for the int8 kernels below (router,
+    // gate/up), instead of by each of their work items
+    const bool xq = e->pf_xq_on && (e->pf_experts == 0 || e->pf_experts == 6) && e->pf_xq && D % 256 == 0 && D <= 4096;
+    if (xq) HIP_TRY(launch_qi_rows(e->pf_xn, T, D, e->pf_xq, e->pf_xq_sum, e->pf_xq_scale, st));
     MtGemvArgs r{};
     r.m = L.router;
     r.K = D;
@@ -1286,6 +1296,9 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T, bool combine = true) {
         r.tiles = tiles_r;
         r.pair_slice = MT_MFMA_FEW;
         r.list = rl; r.items = ri; r.off = rh; r.cnt = rh + 1; r.nitems = rh + 2;
+        if (xq) {
+            r.xq = e->pf_xq; r.xq_sum = e->pf_xq_sum; r.xq_scale = e->pf_xq_scale;
+        }
         HIP_TRY(launch_mt_q4i8(r, nsr * tiles_r, st));
     } else {
         r.tile_rows = std::max(1, mt_gemv_tile_rows(D, E) / 8);  // one pass of the lane groups: more workgroups
@@ -1353,6 +1366,9 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T, bool combine = true) {
     g.list = e->pf_list; g.off = e->pf_off; g.cnt = e->pf_cnt;
     g.items = e->pf_items_gu; g.nitems = e->pf_nitems;
     g.pair_slice = ps;
+    if (xq && gu_i8) {
+        g.xq = e->pf_xq; g.xq_sum = e->pf_xq_sum; g.xq_scale = e->pf_xq_scale;
+    }
     HIP_TRY(gu_i8 ? launch_mt_q4i8(g, item_tiles * ma.tiles_gu, st)
             : gu_d4 ? launch_mt_dot4(g, item_tiles, st)
             : mm ? launch_mt_mfma(g, item_tiles * ma.tiles_gu, st, e->pf_experts == 2)

@@ -119,6 +119,11 @@ struct oi_engine {
     // the router's work items for mt_q4i8_kernel: list, items, then off / cnt / count (filled for pf_rt_T tokens)
     int32_t *pf_rt = nullptr;
     int pf_rt_T = 0;
+    // the chunk's normalized rows quantized once for the int8 router and
+    // gate/up items (launch_qi_rows): operand slots, group sums, scales
+    void *pf_xq = nullptr;
+    float *pf_xq_sum = nullptr, *pf_xq_scale = nullptr;
+    bool pf_xq_on = true;  // OI_PREFILL_XQ=0: every int8 item quantizes its x rows itself (tests)
     bool pf_fused = true;  // gate/up GEMM with the SwiGLU epilogue where it applies (OI_PREFILL_UNFUSED=1: off)
     int pf_experts = 0;  // routed experts of a prefill: 0 the default kernels, 1 the multi-token GEMV, 2 f32 MFMA
                          // only, 3 no few-pair items, 4 few-pair items on MFMA (OI_PREFILL_EXPERTS=gemv / f32 /

@@ -1325,7 +1325,12 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 // staging row stride in bytes: SBS x 4 units of 32 quant bytes (plane 0, then
 // plane 1), SBS x 16 header bytes (when HT = 0), 16 bytes against bank conflicts
 __host__ __device__ constexpr int qi_srow(int sbs, int ht) { return sbs * (ht ? 128 : 144) + 16; }
-template <int XI, int NWV, int SBS, int HT>
+// XQ: the x rows were quantized once per row by qi_rows_kernel (the same
+// planes, group sums and scale this prologue would compute), so the prologue
+// only copies each pair's 16-byte operand slots, sums and scale into LDS (one
+// barrier, no arithmetic) -- every item of a chunk otherwise requantized the
+// same token rows.
+template <int XI, int NWV, int SBS, int HT, bool XQ = false>
 __global__ __launch_bounds__(NWV * WAVE) void mt_q4i8_kernel(MtGemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) u32x4 md_smem[];
     constexpr int NP = MT_MFMA_FEW, QW = NWV * WAVE, NSTG = 2, SROW = qi_srow(SBS, HT), RPI = 16 / SBS;
@@ -1418,78 +1423,108 @@ __global__ __launch_bounds__(NWV * WAVE) void mt_q4i8_kernel(MtGemvArgs a) {
     // every pair's x (and x2) requested before any is used, and before the
     // first weights (the loads return in order: behind the weights, the x
     // rows of 8 waves took ~7 us to arrive, ~4 us ahead of them)
-    float4 xv[NP][XI], uv[NP][XI];
+    float4 xv[XQ ? 1 : NP][XI], uv[XQ ? 1 : NP][XI];
+    u32x4 qv[XQ ? 4 * XI : 1];  // XQ: this thread's operand slots (U * WAVE = 4 XI QW)
+    float qsum = 0.f, qscale = 0.f;
+    if constexpr (XQ) {
+        // the pairs' rows (uniform loads; absent pairs repeat the last), then
+        // slot idx = (unit u, lane l): plane (l >> 2) & 3 of pair l & 3, lane group l >> 4
+        int prow[NP];
 #pragma unroll
-    for (int pj = 0; pj < NP; pj++) {
-        const size_t xo = (size_t)(a.list[base + min(pj, n - 1)] / a.xdiv) * K;
+        for (int pj = 0; pj < NP; pj++) prow[pj] = a.list[base + min(pj, n - 1)] / a.xdiv;
+        const int lp = lane & 3, myrow = lp == 0 ? prow[0] : lp == 1 ? prow[1] : lp == 2 ? prow[2] : prow[3];
 #pragma unroll
-        for (int i = 0; i < XI; i++) {
-            const int c = min(tid + i * QW, K / 4 - 1);
-            xv[pj][i] = ((const float4 *)(a.x + xo))[c];
-            uv[pj][i] = a.x2 ? ((const float4 *)(a.x2 + xo))[c] : float4{0.f, 0.f, 0.f, 0.f};
+        for (int k = 0; k < 4 * XI; k++) {
+            const int idx = tid + k * QW, u = idx / WAVE;
+            qv[k] = ((const u32x4 *)a.xq)[((size_t)myrow * U + min(u, U - 1)) * 16 + (lane >> 4) * 4 + ((lane >> 2) & 3)];
+        }
+        const int G32 = K / 32, pj = min(tid / G32, NP - 1);  // NP * G32 <= QW for K <= 4096
+        const int srow = pj == 0 ? prow[0] : pj == 1 ? prow[1] : pj == 2 ? prow[2] : prow[3];
+        qsum = a.xq_sum[(size_t)srow * G32 + tid % G32];
+        qscale = a.xq_scale[lp == 0 ? prow[0] : lp == 1 ? prow[1] : lp == 2 ? prow[2] : prow[3]];
+    } else {
+#pragma unroll
+        for (int pj = 0; pj < NP; pj++) {
+            const size_t xo = (size_t)(a.list[base + min(pj, n - 1)] / a.xdiv) * K;
+#pragma unroll
+            for (int i = 0; i < XI; i++) {
+                const int c = min(tid + i * QW, K / 4 - 1);
+                xv[pj][i] = ((const float4 *)(a.x + xo))[c];
+                uv[pj][i] = a.x2 ? ((const float4 *)(a.x2 + xo))[c] : float4{0.f, 0.f, 0.f, 0.f};
+            }
         }
     }
     hload(0);
 #pragma unroll
     for (int i = 0; i < NSTG - 1; i++) issue(i, ring[i]);
-    float amax[NP];
+    if constexpr (XQ) {
+        // (operand rows of absent pairs hold the last pair's values; their results are not stored)
 #pragma unroll
-    for (int pj = 0; pj < NP; pj++) {
-        amax[pj] = 0.f;
+        for (int k = 0; k < 4 * XI; k++)
+            if (tid + k * QW < U * WAVE) xa[tid + k * QW] = qv[k];
+        if (tid < NP * (K / 32)) xsum[tid] = qsum;
+        if (tid < NP) xsc[tid] = qscale;
+        __syncthreads();
+    } else {
+        float amax[NP];
 #pragma unroll
-        for (int i = 0; i < XI; i++) {
-            float4 v = xv[pj][i];
-            if (a.x2) {  // SwiGLU (infer/forward.odin:128-132)
+        for (int pj = 0; pj < NP; pj++) {
+            amax[pj] = 0.f;
+#pragma unroll
+            for (int i = 0; i < XI; i++) {
+                float4 v = xv[pj][i];
+                if (a.x2) {  // SwiGLU (infer/forward.odin:128-132)
 #pragma clang fp contract(off)
-                const float4 u = uv[pj][i];
-                v.x *= 1.0f / (1.0f + expf(-v.x));
-                v.y *= 1.0f / (1.0f + expf(-v.y));
-                v.z *= 1.0f / (1.0f + expf(-v.z));
-                v.w *= 1.0f / (1.0f + expf(-v.w));
-                v.x *= u.x;
-                v.y *= u.y;
-                v.z *= u.z;
-                v.w *= u.w;
-                xv[pj][i] = v;
+                    const float4 u = uv[pj][i];
+                    v.x *= 1.0f / (1.0f + expf(-v.x));
+                    v.y *= 1.0f / (1.0f + expf(-v.y));
+                    v.z *= 1.0f / (1.0f + expf(-v.z));
+                    v.w *= 1.0f / (1.0f + expf(-v.w));
+                    v.x *= u.x;
+                    v.y *= u.y;
+                    v.z *= u.z;
+                    v.w *= u.w;
+                    xv[pj][i] = v;
+                }
+                if (tid + i * QW < K / 4)
+                    amax[pj] = fmaxf(amax[pj], fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
             }
-            if (tid + i * QW < K / 4)
-                amax[pj] = fmaxf(amax[pj], fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+            amax[pj] = wave_max_all(amax[pj]);
+            if (lane == 0) xsc[NP + wave * NP + pj] = amax[pj];
         }
-        amax[pj] = wave_max_all(amax[pj]);
-        if (lane == 0) xsc[NP + wave * NP + pj] = amax[pj];
-    }
-    __syncthreads();
+        __syncthreads();
 #pragma unroll
-    for (int pj = 0; pj < NP; pj++) {
-        float mx = 0.f;
+        for (int pj = 0; pj < NP; pj++) {
+            float mx = 0.f;
 #pragma unroll
-        for (int w = 0; w < NWV; w++) mx = fmaxf(mx, xsc[NP + w * NP + pj]);
-        const float inv = mx > 0.f ? QI_MAX / mx : 0.f;
+            for (int w = 0; w < NWV; w++) mx = fmaxf(mx, xsc[NP + w * NP + pj]);
+            const float inv = mx > 0.f ? QI_MAX / mx : 0.f;
 #pragma unroll
-        for (int i = 0; i < XI; i++) {
-            const int c = tid + i * QW;  // float4 c: elements 4c..4c+3 (K / 4 is a multiple of 64: whole waves)
-            if (c >= K / 4) break;
-            const float4 v = xv[pj][i];
-            const float sum = (v.x + v.y) + (v.z + v.w);
-            const float sum16 = dpp_sum4(sum);
-            const float sum32 = sum16 + dpp_mirror8(sum16);  // the 8 lanes of one 32-element group
-            if ((c & 7) == 0) xsum[pj * (K / 32) + (c >> 3)] = sum32;
-            const int q[4] = {(int)rintf(v.x * inv), (int)rintf(v.y * inv), (int)rintf(v.z * inv),
-                              (int)rintf(v.w * inv)};
-            // unit c / 16, group g = (c / 2) % 4 of its first (c % 16 < 8) or second half
-            uint32_t *cell = (uint32_t *)(xa + (c >> 4) * WAVE + ((c >> 1) & 3) * 16) + ((c >> 3) & 1) * 2 + (c & 1);
+            for (int i = 0; i < XI; i++) {
+                const int c = tid + i * QW;  // float4 c: elements 4c..4c+3 (K / 4 is a multiple of 64: whole waves)
+                if (c >= K / 4) break;
+                const float4 v = xv[pj][i];
+                const float sum = (v.x + v.y) + (v.z + v.w);
+                const float sum16 = dpp_sum4(sum);
+                const float sum32 = sum16 + dpp_mirror8(sum16);  // the 8 lanes of one 32-element group
+                if ((c & 7) == 0) xsum[pj * (K / 32) + (c >> 3)] = sum32;
+                const int q[4] = {(int)rintf(v.x * inv), (int)rintf(v.y * inv), (int)rintf(v.z * inv),
+                                  (int)rintf(v.w * inv)};
+                // unit c / 16, group g = (c / 2) % 4 of its first (c % 16 < 8) or second half
+                uint32_t *cell = (uint32_t *)(xa + (c >> 4) * WAVE + ((c >> 1) & 3) * 16) + ((c >> 3) & 1) * 2 + (c & 1);
 #pragma unroll
-            for (int pl = 0; pl < 4; pl++) {
-                const int sh = 21 - 7 * pl;
-                uint32_t b = 0;
+                for (int pl = 0; pl < 4; pl++) {
+                    const int sh = 21 - 7 * pl;
+                    uint32_t b = 0;
 #pragma unroll
-                for (int k = 0; k < 4; k++) b |= ((uint32_t)(q[k] >> sh) & (pl == 0 ? 0xFFu : 0x7Fu)) << (8 * k);
-                cell[(4 * pl + pj) * 4] = b;  // A row 4 plane + pair
+                    for (int k = 0; k < 4; k++) b |= ((uint32_t)(q[k] >> sh) & (pl == 0 ? 0xFFu : 0x7Fu)) << (8 * k);
+                    cell[(4 * pl + pj) * 4] = b;  // A row 4 plane + pair
+                }
             }
+            if (tid == 0) xsc[pj] = mx / QI_MAX;
         }
-        if (tid == 0) xsc[pj] = mx / QI_MAX;
+        __syncthreads();
     }
-    __syncthreads();
     float facc[4] = {0.f, 0.f, 0.f, 0.f}, fmin = 0.f;
     float res[QI_MAXT];  // tile results, the latest last
 #pragma unroll
@@ -1588,6 +1623,66 @@ __global__ __launch_bounds__(NWV * WAVE) void mt_q4i8_kernel(MtGemvArgs a) {
     }
 }
 
+// qi_rows_kernel: one x row per workgroup of 512 threads (grid = rows):
+// the int8 planes of mt_q4i8_kernel's A operand, stored slot by slot in its
+// order (row r, unit u, lane group G, plane pl: 16 bytes at ((r U + u) 16 +
+// 4 G + pl)), the 32-element group sums and the row's scale, computed as that
+// kernel's prologue computes them (the same maximum, rounding, and sum order
+// over the same lanes), so the results are the same bit for bit.
+template <int XI>
+__global__ __launch_bounds__(512) void qi_rows_kernel(const float *x, int32_t K, u32x4 *q, float *gsum, float *scale) {
+    constexpr int QW = 512;
+    __shared__ float wmx[QW / WAVE];
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid / WAVE, U = K >> 6;
+    const size_t r = blockIdx.x;
+    const float4 *xr = (const float4 *)(x + r * K);
+    float4 v[XI];
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < XI; i++) {
+        const int c = tid + i * QW;
+        v[i] = xr[min(c, K / 4 - 1)];
+        if (c < K / 4) amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+    }
+    amax = wave_max_all(amax);
+    if (lane == 0) wmx[wave] = amax;
+    __syncthreads();
+    float mx = 0.f;
+#pragma unroll
+    for (int w = 0; w < QW / WAVE; w++) mx = fmaxf(mx, wmx[w]);
+    const float inv = mx > 0.f ? QI_MAX / mx : 0.f;
+#pragma unroll
+    for (int i = 0; i < XI; i++) {
+        const int c = tid + i * QW;  // K / 4 is a multiple of 64: whole waves
+        if (c >= K / 4) break;
+        const float4 t = v[i];
+        const float sum = (t.x + t.y) + (t.z + t.w);
+        const float sum16 = dpp_sum4(sum);
+        const float sum32 = sum16 + dpp_mirror8(sum16);
+        if ((c & 7) == 0) gsum[r * (K / 32) + (c >> 3)] = sum32;
+        const int qi[4] = {(int)rintf(t.x * inv), (int)rintf(t.y * inv), (int)rintf(t.z * inv), (int)rintf(t.w * inv)};
+        const int u = c >> 4, i4 = c & 15;
+        uint32_t *dst = (uint32_t *)(q + (r * U + u) * 16 + ((i4 >> 1) & 3) * 4) + ((i4 >> 3) & 1) * 2 + (i4 & 1);
+#pragma unroll
+        for (int pl = 0; pl < 4; pl++) {
+            const int sh = 21 - 7 * pl;
+            uint32_t b = 0;
+#pragma unroll
+            for (int k = 0; k < 4; k++) b |= ((uint32_t)(qi[k] >> sh) & (pl == 0 ? 0xFFu : 0x7Fu)) << (8 * k);
+            dst[pl * 4] = b;
+        }
+    }
+    if (tid == 0) scale[r] = mx / QI_MAX;
+}
+
+hipError_t launch_qi_rows(const float *x, int32_t rows, int32_t K, void *q, float *gsum, float *scale,
+                          hipStream_t st) {
+    if (!x || !q || !gsum || !scale || rows <= 0 || K <= 0 || K % 256 || K > 4096) return hipErrorInvalidValue;
+    if (K <= 2048) hipLaunchKernelGGL(qi_rows_kernel<1>, dim3(rows), dim3(512), 0, st, x, K, (u32x4 *)q, gsum, scale);
+    else hipLaunchKernelGGL(qi_rows_kernel<2>, dim3(rows), dim3(512), 0, st, x, K, (u32x4 *)q, gsum, scale);
+    return hipGetLastError();
+}
+
 constexpr int QI_NW = 8;  // waves per workgroup: the x planes in LDS serve 8 waves (4 measured 2% slower)
 static int qi_sbs(int32_t K) { return (K / 256) % 2 == 0 ? 2 : 1; }
 // headers per tile when a tile takes more than one step and NSB divides 4 SBS
@@ -1618,6 +1713,22 @@ hipError_t launch_mt_q4i8(const MtGemvArgs &a, int max_items, hipStream_t st) {
     const size_t lds = mt_q4i8_lds(a.K, QI_NW);
     const dim3 grid((unsigned)(a.swiglu ? 2 * max_items : max_items)), block(QI_NW * WAVE);
     const bool x1 = a.K <= 4 * QI_NW * WAVE;  // K <= 2048: NSB <= 8
+    if (a.xq && !a.x2) {
+        if (!a.xq_sum || !a.xq_scale) return hipErrorInvalidValue;
+        switch (x1 ? qi_ht(a.K) : -1) {
+        case 8: hipLaunchKernelGGL((mt_q4i8_kernel<1, QI_NW, 2, 8, true>), grid, block, lds, st, b); break;
+        case 4: hipLaunchKernelGGL((mt_q4i8_kernel<1, QI_NW, 2, 4, true>), grid, block, lds, st, b); break;
+        case 0:
+            if (qi_sbs(a.K) == 2) hipLaunchKernelGGL((mt_q4i8_kernel<1, QI_NW, 2, 0, true>), grid, block, lds, st, b);
+            else hipLaunchKernelGGL((mt_q4i8_kernel<1, QI_NW, 1, 0, true>), grid, block, lds, st, b);
+            break;
+        default:
+            if (qi_sbs(a.K) == 2) hipLaunchKernelGGL((mt_q4i8_kernel<2, QI_NW, 2, 0, true>), grid, block, lds, st, b);
+            else hipLaunchKernelGGL((mt_q4i8_kernel<2, QI_NW, 1, 0, true>), grid, block, lds, st, b);
+            break;
+        }
+        return hipGetLastError();
+    }
     switch (x1 ? qi_ht(a.K) : -1) {
     case 8: hipLaunchKernelGGL((mt_q4i8_kernel<1, QI_NW, 2, 8>), grid, block, lds, st, b); break;
     case 4: hipLaunchKernelGGL((mt_q4i8_kernel<1, QI_NW, 2, 4>), grid, block, lds, st, b); break;

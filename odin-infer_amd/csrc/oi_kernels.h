@@ -301,6 +301,10 @@ struct MtGemvArgs {
     float *y2;
     const float *x2;
     int32_t mat_items;
+    // set (with x2 unset): the x rows already quantized by launch_qi_rows --
+    // planes in the int8 kernel's operand order, group sums, scales per row
+    const void *xq;
+    const float *xq_sum, *xq_scale;
 };
 // dense_n > 0: one "expert" (e = 0) holding pairs 0 .. dense_n-1, no lists (a
 // plain multi-token GEMV); item it = slice * tiles + row tile, max_items =
@@ -327,6 +331,10 @@ bool mt_dot4_supported(const DMat &m, int32_t K, int32_t rows);
 hipError_t launch_mt_dot4(const MtGemvArgs &a, int max_items, hipStream_t st);
 bool mt_q4i8_supported(const DMat &m, int32_t K, int32_t rows);
 hipError_t launch_mt_q4i8(const MtGemvArgs &a, int max_items, hipStream_t st);
+// x rows [rows][K] (K % 256 == 0, K <= 4096) quantized once for launch_mt_q4i8
+// (MtGemvArgs::xq): q [rows][K] 4-byte slots, gsum [rows][K / 32], scale [rows]
+hipError_t launch_qi_rows(const float *x, int32_t rows, int32_t K, void *q, float *gsum, float *scale,
+                          hipStream_t st);
 bool mt_mfma_supported(const DMat &m, int32_t K, int32_t rows);
 hipError_t launch_mt_mfma(const MtGemvArgs &a, int max_items, hipStream_t st, bool f32_only = false);
 struct PfMoeArgs {

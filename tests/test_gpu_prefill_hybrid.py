@@ -281,6 +281,37 @@ def test_prefill_expert_kernels_agree(tmp_path, monkeypatch, shape, n):
         assert err <= 1e-5, kind
 
 
+@pytest.mark.parametrize("shape,n,kind", [("c5", 64, "default"), ("c5", 200, "i8"), ("c4", 48, "default"),
+                                          ("c4", 200, "i8")])
+def test_prefill_int8_rows_quantized_once_bit_identical(tmp_path, monkeypatch, shape, n, kind):
+    """The int8 router and routed gate/up items take the chunk's normalized
+    rows quantized once per row (qi_rows_kernel: planes, group sums, scale)
+    instead of quantizing their pairs' rows in each item's prologue
+    (OI_PREFILL_XQ=0).  The two are the same arithmetic (the same maximum,
+    rounding and sum order), so the chunk's last logits are bit for bit the
+    same, items with fewer than four pairs included."""
+    from oi import synth
+    spec = (synth._hybrid(2048, 512, 1, 16, 2, 256, 4096, 4096, 64, 16, 32, 128, experts=512, used=10, eff=512,
+                          shared=512, interval=2, seed=59) if shape == "c5" else
+            synth._moe(2048, 1, 32, 4, 4096, 4096, 128, 8, 768, seed=61))
+    path = tmp_path / ("%s.gguf" % shape)
+    synth.write_gguf(path, spec)
+    toks = _tokens(23, n, 4096)
+    monkeypatch.setenv("OI_PREFILL_EXPERTS", kind)
+    out = {}
+    for xq in ("1", "0"):
+        monkeypatch.setenv("OI_PREFILL_XQ", xq)
+        e, ok = infer.engine_load(str(path), infer.Engine_Opts(max_ctx=256))
+        assert ok
+        try:
+            print("case %s n=%d experts %s OI_PREFILL_XQ=%s" % (shape, n, kind, xq), flush=True)
+            out[xq] = infer.engine_forward_batch(e, toks, 0).copy()
+        finally:
+            infer.engine_destroy(e)
+    assert np.all(np.isfinite(out["1"]))
+    assert np.array_equal(out["1"], out["0"]), scaled_err(out["1"], out["0"])
+
+
 @pytest.mark.parametrize("mode", ["massive", "group"])
 def test_prefill_int8_experts_outlier_activations(tmp_path, mode):
     """The routed experts of a 64-token chunk on the int8 matrix cores (the
