@@ -32,12 +32,15 @@
 
 namespace oi {
 
+// threads of an attn_kernel workgroup: one wave per query head of the group
+// (at least 4 waves), so no wave computes two heads in series
+static constexpr int attn_threads(int G) { return G > 4 ? G * WAVE : WG; }
+
 template <int HD>
 struct AttnShape {
     static constexpr int CH = 64;                     // positions per workgroup (one per lane)
     static constexpr int KPAD = HD + 8;               // LDS row stride of K, in halves
     static constexpr int CPR = HD / 8;                // 16-byte chunks per row
-    static constexpr int NLD = CH * CPR / WG;         // loads per thread per tensor
     static constexpr int DPW = HD / 4;                // score dimensions per wave
     static constexpr int DPL = HD / WAVE;             // o dimensions per lane
     static constexpr int PPL = CH / WAVE;             // score positions per lane
@@ -56,8 +59,9 @@ static __device__ __forceinline__ int a128_split_len(int n, int max_splits) {
 
 
 template <int HD, int G>
-__global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
+__global__ __launch_bounds__(attn_threads(G)) void attn_kernel(AttnArgs a) {
     using S = AttnShape<HD>;
+    constexpr int NT = attn_threads(G), NLD = S::CH * S::CPR / NT;  // threads; tile loads per thread per tensor
     __shared__ __attribute__((aligned(16))) uint16_t ks[S::CH * S::KPAD];
     __shared__ __attribute__((aligned(16))) uint16_t vs[S::CH * HD];
     __shared__ __attribute__((aligned(16))) float qr[G][HD];
@@ -77,18 +81,18 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
     const bool has_pos = pos < t1;
 
     // 1. small loads first (vector loads return in order), then the tiles
-    constexpr int QPT = (G * HD + WG - 1) / WG;
+    constexpr int QPT = (G * HD + NT - 1) / NT;
     float qreg[QPT];
 #pragma unroll
-    for (int i = 0; i < QPT; i++) qreg[i] = a.q[(size_t)kvh * G * HD + min(tid + i * WG, G * HD - 1)];
+    for (int i = 0; i < QPT; i++) qreg[i] = a.q[(size_t)kvh * G * HD + min(tid + i * NT, G * HD - 1)];
     const int hi = min(tid, HD - 1);
     const float kraw = a.k[(size_t)kvh * HD + hi], vraw = a.v[(size_t)kvh * HD + hi];
     const float2 csr = a.rope_cs[(size_t)pos * (HD / 2) + min(tid, HD / 2 - 1)];
     const float qnr = a.q_norm[hi], knr = a.k_norm[hi];
-    u32x4 kr[S::NLD], vr[S::NLD];
+    u32x4 kr[NLD], vr[NLD];
 #pragma unroll
-    for (int j = 0; j < S::NLD; j++) {
-        const int c = tid + j * WG, tl = min(c / S::CPR, n - 1), ch = c % S::CPR;
+    for (int j = 0; j < NLD; j++) {
+        const int c = tid + j * NT, tl = min(c / S::CPR, n - 1), ch = c % S::CPR;
         kr[j] = ldg_nt((const u32x4 *)(kc + (size_t)(t0 + tl) * HD) + ch);
         vr[j] = ldg_nt((const u32x4 *)(vc + (size_t)(t0 + tl) * HD) + ch);
     }
@@ -98,7 +102,7 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
     //    infer/forward.odin:57-85; cos/sin come from the host-built table
 #pragma unroll
     for (int i = 0; i < QPT; i++) {
-        const int idx = tid + i * WG;
+        const int idx = tid + i * NT;
         if (idx < G * HD) qr[idx / HD][idx % HD] = qreg[i];
     }
     if (tid < HD) {
@@ -110,7 +114,7 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
     if (tid < HD / 2) csl[tid] = csr;
     __syncthreads();
     const int nvec = G + (has_pos ? 1 : 0);
-    for (int g = wave; g < nvec; g += WG / WAVE) {
+    for (int g = wave; g < nvec; g += NT / WAVE) {
         const float *src = g < G ? qr[g] : kp;
         float ss = 0.f;
         for (int i = lane; i < HD; i += WAVE) ss += src[i] * src[i];
@@ -118,7 +122,7 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
         if (lane == 0) nrm[g] = 1.0f / sqrtf(ss / (float)HD + a.eps);
     }
     __syncthreads();
-    for (int idx = tid; idx < nvec * (HD / 2); idx += WG) {
+    for (int idx = tid; idx < nvec * (HD / 2); idx += NT) {
 #pragma clang fp contract(off)
         const int g = idx / (HD / 2), i = idx % (HD / 2);
         float *v = g < G ? qr[g] : kp;
@@ -133,8 +137,8 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
 
     // 3. stage the tiles in LDS (rows at or past n are zero; row pos-t0 is set below)
 #pragma unroll
-    for (int j = 0; j < S::NLD; j++) {
-        const int c = tid + j * WG, tl = c / S::CPR, ch = c % S::CPR;
+    for (int j = 0; j < NLD; j++) {
+        const int c = tid + j * NT, tl = c / S::CPR, ch = c % S::CPR;
         const bool ok = tl < n && t0 + tl != pos;
         const u32x4 z = {0u, 0u, 0u, 0u};
         *(u32x4 *)(ks + tl * S::KPAD + ch * 8) = ok ? kr[j] : z;
@@ -143,7 +147,7 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
     __syncthreads();
     if (has_pos) {
         const int tl = pos - t0;
-        for (int i = tid; i < HD; i += WG) {
+        for (int i = tid; i < HD; i += NT) {
             const uint16_t kb = f2h(kp[i]), vb = f2h(vp[i]);
             kc[(size_t)pos * HD + i] = kb;
             vc[(size_t)pos * HD + i] = vb;
@@ -160,7 +164,7 @@ __global__ __launch_bounds__(WG) void attn_kernel(AttnArgs a) {
     // (o, m, l).  Score = q.k / sqrt(hd) (infer/forward.odin:98 divides).
     const float div = sqrtf((float)HD);
     const int stride = HD + 2;
-    for (int g = wave; g < G; g += WG / WAVE) {
+    for (int g = wave; g < G; g += NT / WAVE) {
         float sc[S::PPL], m = -INFINITY;
 #pragma unroll
         for (int p = 0; p < S::PPL; p++) {
@@ -577,12 +581,12 @@ __global__ __launch_bounds__(A128_NT) void attn128_kernel(AttnArgs a) {
 
 template <int HD>
 static hipError_t launch_attn_hd(const AttnArgs &a, int G, hipStream_t st) {
-    dim3 grid(a.max_splits, a.n_kv_heads), block(WG);
+    dim3 grid(a.max_splits, a.n_kv_heads);
     switch (G) {
-    case 1: hipLaunchKernelGGL((attn_kernel<HD, 1>), grid, block, 0, st, a); break;
-    case 2: hipLaunchKernelGGL((attn_kernel<HD, 2>), grid, block, 0, st, a); break;
-    case 4: hipLaunchKernelGGL((attn_kernel<HD, 4>), grid, block, 0, st, a); break;
-    case 8: hipLaunchKernelGGL((attn_kernel<HD, 8>), grid, block, 0, st, a); break;
+    case 1: hipLaunchKernelGGL((attn_kernel<HD, 1>), grid, dim3(attn_threads(1)), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((attn_kernel<HD, 2>), grid, dim3(attn_threads(2)), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((attn_kernel<HD, 4>), grid, dim3(attn_threads(4)), 0, st, a); break;
+    case 8: hipLaunchKernelGGL((attn_kernel<HD, 8>), grid, dim3(attn_threads(8)), 0, st, a); break;
     default: return hipErrorInvalidValue;
     }
     hipError_t e = hipGetLastError();
