@@ -114,6 +114,7 @@ def c1_cpu_run(budget_s=60.0):
     """Qwen3-0.6B shape, Q8_0, f32 KV cache, max_ctx 4096,
     token 0 then 256 greedy steps on the CPU reference path (the oracle, host
     cores), and the same workload on the GPU (f16 KV) beside it."""
+    import numpy as np
     from oi import infer, synth
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import refcpu
@@ -146,6 +147,25 @@ def c1_cpu_run(budget_s=60.0):
         match = 0
         while match < n and gids[match] == ids[match]:
             match += 1
+        # the GPU's greedy path teacher-forced through the oracle with the
+        # GPU's cache precision (f16 KV): its pick against the oracle's argmax
+        # at each step, and where they differ the oracle's margin between the
+        # two (a near-tie that the cache precision alone can decide: at step
+        # 1 of this model the f32- and f16-KV oracles pick different ids)
+        K = min(64, len(gids))
+        r16 = refcpu.RefEngine(path, max_ctx=4096, num_threads=threads, kv_f16=True)
+        try:
+            agree, worst, prev = 0, 0.0, 0
+            for i in range(K):
+                lg = np.asarray(r16.forward(prev, i), np.float64)
+                pick = refcpu.argmax(lg)
+                if pick == int(gids[i]):
+                    agree += 1
+                else:
+                    worst = max(worst, float(lg[pick] - lg[int(gids[i])]) / float(np.abs(lg).max()))
+                prev = int(gids[i])
+        finally:
+            r16.close()
         wb = weight_bytes(spec)
         return {"workload": "Qwen3-0.6B shape Q8_0, token 0 + %d greedy steps, f32 KV (CPU) / f16 KV (GPU), "
                             "max_ctx 4096" % n,
@@ -154,7 +174,9 @@ def c1_cpu_run(budget_s=60.0):
                         "GBps": round(wb * n / el / 1e9, 2)},
                 "gpu": {"value": round(256 / gel, 1), "unit": "tok/s", "ms_per_token": round(1000 * gel / 256, 4),
                         "GBps": round(wb * 256 / gel / 1e9, 1)},
-                "greedy_matching_prefix": match, "compared_steps": n}
+                "greedy_matching_prefix": match, "compared_steps": n,
+                "gpu_path_vs_f16kv_oracle": {"steps": K, "argmax_equal": agree,
+                                             "max_rel_margin_where_different": worst}}
     finally:
         shutil.rmtree(d, ignore_errors=True)
 
@@ -1124,9 +1146,12 @@ def main():
             c5 = model_decode("qwen35-hybrid-moe", 0, 256, prompt=2048, cpu=not args.no_cpu)
         c1 = None if args.no_cpu else c1_cpu_run()
         if c1:
-            log("C1: CPU %.2f tok/s (%d threads), GPU %.1f tok/s, greedy prefix %d/%d" % (
-                c1["cpu"]["value"], c1["cpu"]["cores"], c1["gpu"]["value"], c1["greedy_matching_prefix"],
-                c1["compared_steps"]))
+            fk = c1["gpu_path_vs_f16kv_oracle"]
+            log("C1: CPU %.2f tok/s (%d threads), GPU %.1f tok/s, greedy prefix %d/%d against the f32-KV oracle; "
+                "GPU path through the f16-KV oracle: argmax equal at %d/%d steps (max relative margin where "
+                "different %.2g)" % (c1["cpu"]["value"], c1["cpu"]["cores"], c1["gpu"]["value"],
+                                     c1["greedy_matching_prefix"], c1["compared_steps"], fk["argmax_equal"],
+                                     fk["steps"], fk["max_rel_margin_where_different"]))
 
         cpu = None
         if not args.no_cpu:
