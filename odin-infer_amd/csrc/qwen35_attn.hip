@@ -12,8 +12,9 @@
 //   pos, of the new k, stored with v to the f16 cache), then positions
 //   [s CH, (s+1) CH) of the kv head for the group: one partial
 //   (m, l, o[head_dim]) per query head and split.
-// q35_combine_kernel (grid n_heads): merge of the splits, o / l, times
-//   sigmoid(gate).  Kernel boundaries order the cache store and the partials.
+// q35_combine_kernel (grid (n_heads, head_dim / 64)): merge of the splits,
+//   o / l, times sigmoid(gate).  Kernel boundaries order the cache store and
+//   the partials.
 
 #include <type_traits>
 
@@ -202,53 +203,61 @@ __global__ __launch_bounds__(WG) void q35_attn_kernel(Q35Args a) {
     }
 }
 
-// Merge of a head's splits: the split weights exp(m_s - M) are formed once
-// (in LDS), then every thread sums its dimensions over the splits with the
-// loads independent of each other.
+// Merge of a head's splits: one query head and 64 of its dimensions per
+// workgroup (grid (n_heads, HD / 64)), the 4 waves taking every 4th split,
+// the first Q35_PF splits' values requested together with the (m, l) pairs
+// (one memory round trip); the split weights exp(m_s - M) are formed once in
+// LDS by one wave.  out = (o / l) sigmoid(gate).
+constexpr int Q35_PF = 20;
 template <int HD>
 __global__ __launch_bounds__(WG) void q35_combine_kernel(Q35Args a) {
 #pragma clang fp contract(off)
-    __shared__ float wsp[Q35_MAXS];
-    __shared__ float red[WG / WAVE];
+    __shared__ float wm[Q35_MAXS], wl[Q35_MAXS];
+    __shared__ float ored[WG / WAVE][WAVE];
+    __shared__ float Ls;
     const int pos = a.state ? a.state[ST_POS] : a.pos;
     const int h = blockIdx.x, ns = (pos + Q35_CH) / Q35_CH, t = threadIdx.x;
-    const int lane = t & (WAVE - 1), wave = t / WAVE;
+    const int lane = t & (WAVE - 1), wave = t / WAVE, i = blockIdx.y * WAVE + lane;
     const float *pb = a.part + (size_t)h * a.max_splits * (HD + 2);
-    __shared__ float msp[Q35_MAXS], lsp[Q35_MAXS];
-    float mx = -INFINITY;
-    for (int s = t; s < ns; s += WG) {  // one memory round trip for every split's (m, l)
-        msp[s] = pb[(size_t)s * (HD + 2) + HD];
-        lsp[s] = pb[(size_t)s * (HD + 2) + HD + 1];
-        mx = fmaxf(mx, msp[s]);
+    float ov[Q35_PF];
+#pragma unroll
+    for (int k = 0; k < Q35_PF; k++) {
+        const int s = wave + (WG / WAVE) * k;
+        ov[k] = s < ns ? pb[(size_t)s * (HD + 2) + i] : 0.f;
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, WAVE));
-    if (lane == 0) red[wave] = mx;
-    __syncthreads();
-    float M = red[0];
-#pragma unroll
-    for (int w = 1; w < WG / WAVE; w++) M = fmaxf(M, red[w]);
-    __syncthreads();
-    float lp = 0.f;
+    const float gate = a.qproj[(size_t)h * 2 * HD + HD + i];
     for (int s = t; s < ns; s += WG) {
-        const float ms = msp[s];
-        const float w = ms == -INFINITY ? 0.f : expf(ms - M);
-        wsp[s] = w;
-        lp += lsp[s] * w;
+        wm[s] = pb[(size_t)s * (HD + 2) + HD];
+        wl[s] = pb[(size_t)s * (HD + 2) + HD + 1];
     }
-    lp = wave_sum(lp);
-    if (lane == 0) red[wave] = lp;
     __syncthreads();
-    float lt = 0.f;
-#pragma unroll
-    for (int w = 0; w < WG / WAVE; w++) lt += red[w];
-    for (int i = t; i < HD; i += WG) {
-        float acc = 0.f;
-#pragma unroll 8
-        for (int s = 0; s < ns; s++) acc += pb[(size_t)s * (HD + 2) + i] * wsp[s];
-        const float gate = a.qproj[(size_t)h * 2 * HD + HD + i];
-        a.out[(size_t)h * HD + i] = (acc / lt) * sigmoid_ref(gate);
+    if (wave == 0) {
+        float M = -INFINITY;
+        for (int s = lane; s < ns; s += WAVE) M = fmaxf(M, wm[s]);
+        M = wave_max_all(M);
+        float L = 0.f;
+        for (int s = lane; s < ns; s += WAVE) {
+            const float ms = wm[s];
+            const float w = ms == -INFINITY ? 0.f : expf(ms - M);
+            wm[s] = w;
+            L += wl[s] * w;
+        }
+        L = wave_sum(L);
+        if (lane == 0) Ls = L;
     }
+    __syncthreads();
+    float O = 0.f;
+#pragma unroll
+    for (int k = 0; k < Q35_PF; k++) {
+        const int s = wave + (WG / WAVE) * k;
+        if (s < ns) O += ov[k] * wm[s];
+    }
+    for (int s = wave + (WG / WAVE) * Q35_PF; s < ns; s += WG / WAVE) O += pb[(size_t)s * (HD + 2) + i] * wm[s];
+    ored[wave][lane] = O;
+    __syncthreads();
+    if (wave == 0)
+        a.out[(size_t)h * HD + i] = (((ored[0][lane] + ored[1][lane]) + (ored[2][lane] + ored[3][lane])) / Ls) *
+                                   sigmoid_ref(gate);
 }
 
 int q35_max_splits(int seq_len) { return (seq_len + Q35_CH - 1) / Q35_CH; }
@@ -260,7 +269,7 @@ hipError_t launch_q35_attn(const Q35Args &a, int head_dim, hipStream_t st) {
         a.n_heads / a.n_kv_heads > Q35_GMAX || ns > Q35_MAXS)
         return hipErrorInvalidValue;
     const int G = a.n_heads / a.n_kv_heads, gw = G % 4 == 0 ? 4 : G % 2 == 0 ? 2 : 1;
-    const dim3 g2((unsigned)(a.n_kv_heads * (G / gw)), (unsigned)ns), g3((unsigned)a.n_heads);
+    const dim3 g2((unsigned)(a.n_kv_heads * (G / gw)), (unsigned)ns), g3((unsigned)a.n_heads, (unsigned)(head_dim / WAVE));
     auto attn = [&](auto hd_tag) {
         constexpr int HD = decltype(hd_tag)::value;
         if (gw == 4) hipLaunchKernelGGL((q35_attn_kernel<HD, 4>), g2, dim3(WG), 0, st, a);
