@@ -542,7 +542,7 @@ def qwen35_attn_step(iters=100, seq_len=4096, cpu=True):
     out = {"shape": "16 q heads x 256 (+gate), 2 kv heads, rotary 64, position 4095 of a 4096 f16 cache",
            "avg_us": round(us, 3), "cache_copies": ncopy, "bytes": byts, "GBps": round(byts / us / 1e3, 1),
            "frac_hbm_peak": round(byts / us / 1e3 / PEAK_HBM_GBPS, 4),
-           "kernels": "q35_attn_kernel (q/k norm + RoPE fused; 2 kv heads x 2 head groups x 64 splits) + q35_combine_kernel"}
+           "kernels": "q35_lane_kernel (q/k norm + RoPE fused; 64 splits x 2 kv heads, one wave per query head) + q35_combine_kernel"}
     if cpu:
         rc = _oracle()
         kc16 = host["kc"].view(np.uint16).reshape(nkv, seq_len, hd)

@@ -16,6 +16,8 @@
 //   o / l, times sigmoid(gate).  Kernel boundaries order the cache store and
 //   the partials.
 
+#include <cstdlib>
+#include <cstring>
 #include <type_traits>
 
 #include "device_common.h"
@@ -203,6 +205,177 @@ __global__ __launch_bounds__(WG) void q35_attn_kernel(Q35Args a) {
     }
 }
 
+// q35_lane_kernel, grid (splits, n_kv_heads): one workgroup per (split of
+// Q35_CH positions, kv head) serves every query head of the kv head's group,
+// so each K / V row is read once, with one wave per query head (at least 4
+// waves) and no workgroup barrier after the staging:
+//   1. requests this token's q halves of the group's [q | gate] slices, k, v
+//      and the norm weights, then its K and V tiles (16 B per lane);
+//   2. RMSNorm and partial RoPE of the group's q heads (and, in the split that
+//      holds pos, of the new k, which goes with v to the f16 cache and to the
+//      LDS tile row pos - t0), as q35_attn_kernel;
+//   3. one wave per query head: scores with lane = position (the whole dot
+//      product of its K row, four chains) times 1/sqrt(head_dim), the split's
+//      max and exp-sum by wave reductions, p through the wave's LDS row, then
+//      o = sum_t p_t v_t with HD / 64 dimensions per lane, and the partial
+//      (o, m, l) that q35_combine_kernel merges.
+static constexpr int q35_lane_threads(int G) { return G > 4 ? G * WAVE : WG; }
+template <int HD, int G>
+__global__ __launch_bounds__(q35_lane_threads(G)) void q35_lane_kernel(Q35Args a) {
+    constexpr int NT = q35_lane_threads(G), CH = Q35_CH, KP = HD + 8, CPR = HD / 8, NLD = CH * CPR / NT;
+    constexpr int DPL = HD / WAVE, QPT = (G * HD + NT - 1) / NT;
+    static_assert(CH == WAVE && NLD * NT == CH * CPR, "one position per lane, whole tile loads");
+    __shared__ __attribute__((aligned(16))) uint16_t ks[CH * KP];
+    __shared__ __attribute__((aligned(16))) uint16_t vs[CH * HD];
+    __shared__ __attribute__((aligned(16))) float qs[G][HD];
+    __shared__ float kn[HD], vn[HD], qw[HD], kw[HD];
+    __shared__ __attribute__((aligned(16))) float sp[G][CH];
+    const int split = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
+    const int lane = tid & (WAVE - 1), wave = tid / WAVE;
+    const int pos = a.state ? a.state[ST_POS] : a.pos;  // the token loop keeps pos on the device
+    const int t0 = split * CH;
+    if (t0 > pos) return;  // a split past pos (graph launches size the grid for seq_len)
+    const int n = min(CH, pos + 1 - t0);
+    const bool has_pos = pos < t0 + CH;
+    uint16_t *kc = a.kc + (size_t)kvh * a.seq_len * HD, *vc = a.vc + (size_t)kvh * a.seq_len * HD;
+
+    // 1. the small loads first (vector loads return in order), then the tiles
+    float qreg[QPT];
+#pragma unroll
+    for (int i = 0; i < QPT; i++) {
+        const int idx = min(tid + i * NT, G * HD - 1);
+        qreg[i] = a.qproj[(size_t)(kvh * G + idx / HD) * 2 * HD + idx % HD];
+    }
+    const int hi = min(tid, HD - 1);
+    const float kraw = a.k[(size_t)kvh * HD + hi], vraw = a.v[(size_t)kvh * HD + hi];
+    const float qnr = a.q_norm[hi], knr = a.k_norm[hi];
+    u32x4 kr[NLD], vr[NLD];
+#pragma unroll
+    for (int j = 0; j < NLD; j++) {
+        const int c = tid + j * NT, tl = min(c / CPR, n - 1), ch = c % CPR;
+        kr[j] = ldg_nt((const u32x4 *)(kc + (size_t)(t0 + tl) * HD) + ch);
+        vr[j] = ldg_nt((const u32x4 *)(vc + (size_t)(t0 + tl) * HD) + ch);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. RMSNorm (ops.odin rmsnorm) and partial RoPE (qwen3_5/ops.odin:77-89)
+#pragma unroll
+    for (int i = 0; i < QPT; i++) {
+        const int idx = tid + i * NT;
+        if (idx < G * HD) qs[idx / HD][idx % HD] = qreg[i];
+    }
+    if (tid < HD) {
+        kn[tid] = kraw;
+        vn[tid] = vraw;
+        qw[tid] = qnr;
+        kw[tid] = knr;
+    }
+    __syncthreads();
+    for (int g = wave; g < G + (has_pos ? 1 : 0); g += NT / WAVE) {
+#pragma clang fp contract(off)
+        float *x = g < G ? qs[g] : kn;
+        const float *w = g < G ? qw : kw;
+        float ss = 0.f;
+        for (int i = lane; i < HD; i += WAVE) ss += x[i] * x[i];
+        ss = wave_sum(ss);
+        const float inv = 1.0f / sqrtf(ss / (float)HD + a.eps);
+        float xv[DPL];
+#pragma unroll
+        for (int e = 0; e < DPL; e++) xv[e] = w[lane + WAVE * e] * (inv * x[lane + WAVE * e]);
+#pragma unroll
+        for (int e = 0; e < DPL; e++) x[lane + WAVE * e] = xv[e];
+        const int half = a.rotary_dim / 2;
+        float yv[DPL];
+#pragma unroll
+        for (int e = 0; e < DPL; e++) {
+            const int i = lane + WAVE * e;
+            float v = xv[e];
+            if (i < a.rotary_dim) {
+                const int pr = i < half ? i : i - half;
+                const float ang = (float)pos * a.inv_freq[pr];
+                const float c = cosf(ang), sn = sinf(ang);
+                v = i < half ? x[i] * c - x[i + half] * sn : x[i - half] * sn + x[i] * c;
+            }
+            yv[e] = v;
+        }
+#pragma unroll
+        for (int e = 0; e < DPL; e++) x[lane + WAVE * e] = yv[e];
+    }
+
+    // 3. the tiles in LDS (rows at or past n are zero; row pos - t0 is set below)
+#pragma unroll
+    for (int j = 0; j < NLD; j++) {
+        const int c = tid + j * NT, tl = c / CPR, ch = c % CPR;
+        const bool ok = tl < n && t0 + tl != pos;
+        const u32x4 z = {0u, 0u, 0u, 0u};
+        *(u32x4 *)(ks + tl * KP + ch * 8) = ok ? kr[j] : z;
+        *(u32x4 *)(vs + tl * HD + ch * 8) = ok ? vr[j] : z;
+    }
+    __syncthreads();
+    if (has_pos) {
+        const int tl = pos - t0;
+        for (int i = tid; i < HD; i += NT) {
+            const uint16_t kb = f2h(kn[i]), vb = f2h(vn[i]);
+            kc[(size_t)pos * HD + i] = kb;
+            vc[(size_t)pos * HD + i] = vb;
+            ks[tl * KP + i] = kb;
+            vs[tl * HD + i] = vb;
+        }
+        __syncthreads();
+    }
+
+    // 4. one wave per query head
+    const float scale = 1.0f / sqrtf((float)HD);
+    for (int g = wave; g < G; g += NT / WAVE) {
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < HD / 8; c++) {
+            const u32x4 w = *(const u32x4 *)(ks + lane * KP + 8 * c);
+            const float4 q0 = *(const float4 *)&qs[g][8 * c];
+            const float4 q1 = *(const float4 *)&qs[g][8 * c + 4];
+            acc[c & 3] += q0.x * h2f(w.x & 0xFFFFu) + q0.y * h2f(w.x >> 16) + q0.z * h2f(w.y & 0xFFFFu) +
+                          q0.w * h2f(w.y >> 16) + q1.x * h2f(w.z & 0xFFFFu) + q1.y * h2f(w.z >> 16) +
+                          q1.z * h2f(w.w & 0xFFFFu) + q1.w * h2f(w.w >> 16);
+        }
+        const float s = lane < n ? ((acc[0] + acc[1]) + (acc[2] + acc[3])) * scale : -INFINITY;
+        const float m = wave_max_all(s);
+        const float e = lane < n ? expf(s - m) : 0.f;
+        sp[g][lane] = e;  // this wave's row only: DS operations of one wave complete in order
+        const float l = wave_sum(e);
+        __builtin_amdgcn_wave_barrier();
+        float o[4][DPL];
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int d = 0; d < DPL; d++) o[j][d] = 0.f;
+#pragma unroll 4
+        for (int t4 = 0; t4 < CH; t4 += 4) {
+            const float4 p4 = *(const float4 *)&sp[g][t4];  // rows past n hold p = 0 and zero V
+            const float pw[4] = {p4.x, p4.y, p4.z, p4.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint16_t *vrow = vs + (t4 + j) * HD + DPL * lane;
+                float vv[DPL];
+#pragma unroll
+                for (int d = 0; d < DPL; d += 2) {
+                    const uint32_t w2 = *(const uint32_t *)(vrow + d);
+                    vv[d] = h2f(w2 & 0xFFFFu);
+                    vv[d + 1] = h2f(w2 >> 16);
+                }
+#pragma unroll
+                for (int d = 0; d < DPL; d++) o[j][d] += pw[j] * vv[d];
+            }
+        }
+        float *pt = a.part + ((size_t)(kvh * G + g) * a.max_splits + split) * (HD + 2);
+#pragma unroll
+        for (int d = 0; d < DPL; d++) pt[DPL * lane + d] = (o[0][d] + o[1][d]) + (o[2][d] + o[3][d]);
+        if (lane == 0) {
+            pt[HD] = m;
+            pt[HD + 1] = l;
+        }
+    }
+}
+
 // Merge of a head's splits: one query head and 64 of its dimensions per
 // workgroup (grid (n_heads, HD / 64)), the 4 waves taking every 4th split,
 // the first Q35_PF splits' values requested together with the (m, l) pairs
@@ -270,8 +443,24 @@ hipError_t launch_q35_attn(const Q35Args &a, int head_dim, hipStream_t st) {
         return hipErrorInvalidValue;
     const int G = a.n_heads / a.n_kv_heads, gw = G % 4 == 0 ? 4 : G % 2 == 0 ? 2 : 1;
     const dim3 g2((unsigned)(a.n_kv_heads * (G / gw)), (unsigned)ns), g3((unsigned)a.n_heads, (unsigned)(head_dim / WAVE));
+    // the lane-per-position kernel (default; groups of 1, 2, 4 or 8 query
+    // heads), or the dimension-split kernel over groups of gw query heads
+    // (other groups, and OI_Q35_ATTN=groups)
+    const char *qa = std::getenv("OI_Q35_ATTN");
+    const bool lanes = !(qa && std::strcmp(qa, "groups") == 0) && (G == 1 || G == 2 || G == 4 || G == 8);
+    const dim3 gl((unsigned)ns, (unsigned)a.n_kv_heads);
     auto attn = [&](auto hd_tag) {
         constexpr int HD = decltype(hd_tag)::value;
+        if (lanes) {
+            switch (G) {
+            case 1: hipLaunchKernelGGL((q35_lane_kernel<HD, 1>), gl, dim3(q35_lane_threads(1)), 0, st, a); break;
+            case 2: hipLaunchKernelGGL((q35_lane_kernel<HD, 2>), gl, dim3(q35_lane_threads(2)), 0, st, a); break;
+            case 4: hipLaunchKernelGGL((q35_lane_kernel<HD, 4>), gl, dim3(q35_lane_threads(4)), 0, st, a); break;
+            default: hipLaunchKernelGGL((q35_lane_kernel<HD, 8>), gl, dim3(q35_lane_threads(8)), 0, st, a); break;
+            }
+            hipLaunchKernelGGL(q35_combine_kernel<HD>, g3, dim3(WG), 0, st, a);
+            return;
+        }
         if (gw == 4) hipLaunchKernelGGL((q35_attn_kernel<HD, 4>), g2, dim3(WG), 0, st, a);
         else if (gw == 2) hipLaunchKernelGGL((q35_attn_kernel<HD, 2>), g2, dim3(WG), 0, st, a);
         else hipLaunchKernelGGL((q35_attn_kernel<HD, 1>), g2, dim3(WG), 0, st, a);

@@ -25,13 +25,19 @@ def _case(rng, n_heads, n_kv, hd, seq_len, pos0, T):
             (1 + 0.1 * rng.standard_normal(hd)).astype(f), kc.view(np.uint16), vc.view(np.uint16))
 
 
+@pytest.mark.parametrize("kernel", ["lanes", "groups"])
 @pytest.mark.parametrize("n_heads,n_kv,hd,rd,seq_len,pos0,T", [
     (16, 2, 256, 64, 1024, 0, 40),     # measurement-plan shape from an empty cache
     (16, 2, 256, 64, 4096, 3000, 4),   # long context: 12 position splits
     (8, 2, 128, 128, 512, 100, 6),     # head_dim 128, full rotary
     (4, 4, 128, 0, 256, 7, 3),         # no rotary dimensions
+    (12, 2, 128, 64, 256, 70, 3),      # a group of 6 query heads (the dimension-split kernel either way)
 ])
-def test_qwen35_attn_vs_oracle(n_heads, n_kv, hd, rd, seq_len, pos0, T):
+def test_qwen35_attn_vs_oracle(monkeypatch, kernel, n_heads, n_kv, hd, rd, seq_len, pos0, T):
+    """Both kernels: lane per position with one wave per query head (the
+    default for groups of 1, 2, 4, 8 query heads) and the dimension-split
+    kernel over groups of query heads (OI_Q35_ATTN=groups)."""
+    monkeypatch.setenv("OI_Q35_ATTN", kernel)
     qproj, k, v, qn, kn, kc, vc = _case(np.random.default_rng(hd + pos0 + T), n_heads, n_kv, hd, seq_len, pos0, T)
     inv = refcpu.inv_freq(1e7, rd) if rd else np.zeros(1, np.float32)
     args = (n_heads, n_kv, hd, rd, seq_len, 1e-6, pos0, qproj, k, v, qn, kn, inv, kc, vc)
