@@ -196,4 +196,57 @@ static __device__ __forceinline__ unsigned long long wave_kth_key(const unsigned
     return T;
 }
 
+// Rows for the int8 expert and router kernels (mt_q4i8_kernel's A operand):
+// a row scaled by one factor, s = max|x| / QI_MAX, to integers below 2^28,
+// split into four 7-bit planes (the top one signed).
+constexpr float QI_MAX = 268434432.f;  // 2^28 - 2^10: the rounded product stays below 2^28
+// Row r held as NV float4 per thread of a BS-thread workgroup (float4 c =
+// thread + BS i, K / 4 a multiple of 64): its planes stored slot by slot in
+// the kernel's operand order (unit u, lane group G, plane pl: 16 bytes at
+// ((r U + u) 16 + 4 G + pl)), its 32-element group sums and its scale, with
+// that kernel's own prologue arithmetic (the same maximum, rounding, and sum
+// order over the same lanes).  red: BS / 64 floats of LDS, free on entry
+// after a barrier.
+template <int NV, int BS>
+static __device__ __forceinline__ void qi_quant_row(const float4 (&v)[NV], int K, size_t r, float *red, u32x4 *q,
+                                                    float *gsum, float *scale) {
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid / WAVE, U = K >> 6;
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int c = tid + i * BS;
+        if (c < K / 4) amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+    }
+    amax = wave_max_all(amax);
+    __syncthreads();  // the previous use of red is complete
+    if (lane == 0) red[wave] = amax;
+    __syncthreads();
+    float mx = 0.f;
+#pragma unroll
+    for (int w = 0; w < BS / WAVE; w++) mx = fmaxf(mx, red[w]);
+    const float inv = mx > 0.f ? QI_MAX / mx : 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int c = tid + i * BS;
+        if (c >= K / 4) break;  // whole waves
+        const float4 t = v[i];
+        const float sum = (t.x + t.y) + (t.z + t.w);
+        const float sum16 = dpp_sum4(sum);
+        const float sum32 = sum16 + dpp_mirror8(sum16);
+        if ((c & 7) == 0) gsum[r * (K / 32) + (c >> 3)] = sum32;
+        const int qi[4] = {(int)rintf(t.x * inv), (int)rintf(t.y * inv), (int)rintf(t.z * inv), (int)rintf(t.w * inv)};
+        const int u = c >> 4, i4 = c & 15;
+        uint32_t *dst = (uint32_t *)(q + (r * U + u) * 16 + ((i4 >> 1) & 3) * 4) + ((i4 >> 3) & 1) * 2 + (i4 & 1);
+#pragma unroll
+        for (int pl = 0; pl < 4; pl++) {
+            const int sh = 21 - 7 * pl;
+            uint32_t b = 0;
+#pragma unroll
+            for (int k = 0; k < 4; k++) b |= ((uint32_t)(qi[k] >> sh) & (pl == 0 ? 0xFFu : 0x7Fu)) << (8 * k);
+            dst[pl * 4] = b;
+        }
+    }
+    if (tid == 0) scale[r] = mx / QI_MAX;
+}
+
 }  // namespace oi

@@ -1260,6 +1260,13 @@ int prefill_alloc(oi_engine *e) {
 // into partial-product buffer 0.
 // combine = false: the pair rows and weights stay in pf_yd / pf_w for the next
 // residual add + norm, which sums them (launch_pf_addnorm16's myd)
+// The MoE FFN's normalized rows are also quantized for the int8 router and
+// gate/up items (by launch_pf_addnorm16, instead of by each item)
+static bool pf_xq_used(const oi_engine *e) {
+    const int64_t D = e->cfg.dim;
+    return e->pf_xq_on && (e->pf_experts == 0 || e->pf_experts == 6) && e->pf_xq && D % 256 == 0 && D <= 4096;
+}
+
 int prefill_moe(oi_engine *e, const LayerDev &L, int T, bool combine = true) {
     const hipStream_t st = e->stream;
     const int32_t D = (int32_t)e->cfg.dim, E = (int32_t)e->n_experts, EF = (int32_t)e->expert_ffn;
@@ -1268,10 +1275,9 @@ int prefill_moe(oi_engine *e, const LayerDev &L, int T, bool combine = true) {
     // of 2048), so each workgroup stages its x once and the grid fills the GPU
     const int rps = D <= 2048 ? 8 : MT_PAIR_SLICE;
     const int slices = (T + rps - 1) / rps, pairs = T * KP;
-    // the normalized rows quantized once for the int8 kernels below (router,
-    // gate/up), instead of by each of their work items
-    const bool xq = e->pf_xq_on && (e->pf_experts == 0 || e->pf_experts == 6) && e->pf_xq && D % 256 == 0 && D <= 4096;
-    if (xq) HIP_TRY(launch_qi_rows(e->pf_xn, T, D, e->pf_xq, e->pf_xq_sum, e->pf_xq_scale, st));
+    // the normalized rows, quantized once by the residual add + norm that
+    // wrote them, for the int8 kernels below (router, gate/up)
+    const bool xq = pf_xq_used(e);
     MtGemvArgs r{};
     r.m = L.router;
     r.K = D;
@@ -1483,8 +1489,10 @@ int prefill_chunk(oi_engine *e, const int32_t *tokens, int T, int pos, float *ro
             HIP_TRY(launch_pf_deltanet(da, st));
             HIP_TRY(launch_gemm_parts(L.ssm_out, e->pf_xb, T, P[0], PB[0], &s0, st));
         }
+        const bool xq = L.moe && pf_xq_used(e);
         HIP_TRY(launch_pf_addnorm16(e->pf_x, P[0], s0, L.ffn_norm, eps, D, T, e->pf_xb, st,
-                                    L.moe ? e->pf_xn : nullptr));
+                                    L.moe ? e->pf_xn : nullptr, nullptr, nullptr, 0, xq ? e->pf_xq : nullptr,
+                                    e->pf_xq_sum, e->pf_xq_scale));
         const bool last = l + 1 == e->layers.size();
         if (L.moe) {
             if (prefill_moe(e, L, T, last)) return -1;

@@ -1319,14 +1319,14 @@ hipError_t launch_mt_dot4(const MtGemvArgs &a, int max_items, hipStream_t st) {
 // of a tile into one result per lane (row n, pair G), held in registers until
 // the last tile (stores in the loop would share the memory counter with the
 // weight loads).
-constexpr float QI_MAX = 268434432.f;  // 2^28 - 2^10: the rounded product stays below 2^28
 constexpr int QI_MAXT = 16;            // 16-row tiles per wave (rows of an item <= 16 * 16 * waves)
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 // staging row stride in bytes: SBS x 4 units of 32 quant bytes (plane 0, then
 // plane 1), SBS x 16 header bytes (when HT = 0), 16 bytes against bank conflicts
 __host__ __device__ constexpr int qi_srow(int sbs, int ht) { return sbs * (ht ? 128 : 144) + 16; }
-// XQ: the x rows were quantized once per row by qi_rows_kernel (the same
-// planes, group sums and scale this prologue would compute), so the prologue
+// XQ: the x rows were quantized once per row (qi_quant_row, in the residual
+// add + norm that wrote them: the same planes, group sums and scale this
+// prologue would compute), so the prologue
 // only copies each pair's 16-byte operand slots, sums and scale into LDS (one
 // barrier, no arithmetic) -- every item of a chunk otherwise requantized the
 // same token rows.
@@ -1621,66 +1621,6 @@ __global__ __launch_bounds__(NWV * WAVE) void mt_q4i8_kernel(MtGemvArgs a) {
             if (i >= 0) yr[(size_t)i * NWV * 16] = res[k];
         }
     }
-}
-
-// qi_rows_kernel: one x row per workgroup of 512 threads (grid = rows):
-// the int8 planes of mt_q4i8_kernel's A operand, stored slot by slot in its
-// order (row r, unit u, lane group G, plane pl: 16 bytes at ((r U + u) 16 +
-// 4 G + pl)), the 32-element group sums and the row's scale, computed as that
-// kernel's prologue computes them (the same maximum, rounding, and sum order
-// over the same lanes), so the results are the same bit for bit.
-template <int XI>
-__global__ __launch_bounds__(512) void qi_rows_kernel(const float *x, int32_t K, u32x4 *q, float *gsum, float *scale) {
-    constexpr int QW = 512;
-    __shared__ float wmx[QW / WAVE];
-    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid / WAVE, U = K >> 6;
-    const size_t r = blockIdx.x;
-    const float4 *xr = (const float4 *)(x + r * K);
-    float4 v[XI];
-    float amax = 0.f;
-#pragma unroll
-    for (int i = 0; i < XI; i++) {
-        const int c = tid + i * QW;
-        v[i] = xr[min(c, K / 4 - 1)];
-        if (c < K / 4) amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
-    }
-    amax = wave_max_all(amax);
-    if (lane == 0) wmx[wave] = amax;
-    __syncthreads();
-    float mx = 0.f;
-#pragma unroll
-    for (int w = 0; w < QW / WAVE; w++) mx = fmaxf(mx, wmx[w]);
-    const float inv = mx > 0.f ? QI_MAX / mx : 0.f;
-#pragma unroll
-    for (int i = 0; i < XI; i++) {
-        const int c = tid + i * QW;  // K / 4 is a multiple of 64: whole waves
-        if (c >= K / 4) break;
-        const float4 t = v[i];
-        const float sum = (t.x + t.y) + (t.z + t.w);
-        const float sum16 = dpp_sum4(sum);
-        const float sum32 = sum16 + dpp_mirror8(sum16);
-        if ((c & 7) == 0) gsum[r * (K / 32) + (c >> 3)] = sum32;
-        const int qi[4] = {(int)rintf(t.x * inv), (int)rintf(t.y * inv), (int)rintf(t.z * inv), (int)rintf(t.w * inv)};
-        const int u = c >> 4, i4 = c & 15;
-        uint32_t *dst = (uint32_t *)(q + (r * U + u) * 16 + ((i4 >> 1) & 3) * 4) + ((i4 >> 3) & 1) * 2 + (i4 & 1);
-#pragma unroll
-        for (int pl = 0; pl < 4; pl++) {
-            const int sh = 21 - 7 * pl;
-            uint32_t b = 0;
-#pragma unroll
-            for (int k = 0; k < 4; k++) b |= ((uint32_t)(qi[k] >> sh) & (pl == 0 ? 0xFFu : 0x7Fu)) << (8 * k);
-            dst[pl * 4] = b;
-        }
-    }
-    if (tid == 0) scale[r] = mx / QI_MAX;
-}
-
-hipError_t launch_qi_rows(const float *x, int32_t rows, int32_t K, void *q, float *gsum, float *scale,
-                          hipStream_t st) {
-    if (!x || !q || !gsum || !scale || rows <= 0 || K <= 0 || K % 256 || K > 4096) return hipErrorInvalidValue;
-    if (K <= 2048) hipLaunchKernelGGL(qi_rows_kernel<1>, dim3(rows), dim3(512), 0, st, x, K, (u32x4 *)q, gsum, scale);
-    else hipLaunchKernelGGL(qi_rows_kernel<2>, dim3(rows), dim3(512), 0, st, x, K, (u32x4 *)q, gsum, scale);
-    return hipGetLastError();
 }
 
 constexpr int QI_NW = 8;  // waves per workgroup: the x planes in LDS serve 8 waves (4 measured 2% slower)

@@ -247,7 +247,8 @@ hipError_t launch_pf_add(float *x, const float *part, int split, int64_t total, 
 // myd (with part null): x += sum_s mw[t kp + s] myd[(t kp + s) dim ..], a routed FFN's pair rows
 hipError_t launch_pf_addnorm16(float *x, const float *part, int split, const float *w, float eps, int dim, int T,
                                uint16_t *out, hipStream_t st, float *out32 = nullptr, const float *mw = nullptr,
-                               const float *myd = nullptr, int kp = 0);
+                               const float *myd = nullptr, int kp = 0, void *xq = nullptr, float *xq_sum = nullptr,
+                               float *xq_scale = nullptr);
 hipError_t launch_pf_swiglu16(const float *g, int gs, const float *u, int us, int64_t total, uint16_t *out,
                               hipStream_t st);
 // prefill_hybrid.hip: batched prefill of the Qwen3.5 hybrid layers
@@ -301,8 +302,8 @@ struct MtGemvArgs {
     float *y2;
     const float *x2;
     int32_t mat_items;
-    // set (with x2 unset): the x rows already quantized by launch_qi_rows --
-    // planes in the int8 kernel's operand order, group sums, scales per row
+    // set (with x2 unset): the x rows already quantized (launch_pf_addnorm16's
+    // xq) -- planes in the int8 kernel's operand order, group sums, scales per row
     const void *xq;
     const float *xq_sum, *xq_scale;
 };
@@ -331,10 +332,6 @@ bool mt_dot4_supported(const DMat &m, int32_t K, int32_t rows);
 hipError_t launch_mt_dot4(const MtGemvArgs &a, int max_items, hipStream_t st);
 bool mt_q4i8_supported(const DMat &m, int32_t K, int32_t rows);
 hipError_t launch_mt_q4i8(const MtGemvArgs &a, int max_items, hipStream_t st);
-// x rows [rows][K] (K % 256 == 0, K <= 4096) quantized once for launch_mt_q4i8
-// (MtGemvArgs::xq): q [rows][K] 4-byte slots, gsum [rows][K / 32], scale [rows]
-hipError_t launch_qi_rows(const float *x, int32_t rows, int32_t K, void *q, float *gsum, float *scale,
-                          hipStream_t st);
 bool mt_mfma_supported(const DMat &m, int32_t K, int32_t rows);
 hipError_t launch_mt_mfma(const MtGemvArgs &a, int max_items, hipStream_t st, bool f32_only = false);
 struct PfMoeArgs {

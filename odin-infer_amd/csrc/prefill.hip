@@ -46,12 +46,16 @@ static __device__ __forceinline__ float block_sum(float v, float *red) {
 // + s] (the sum of pf_moe_combine_kernel, which this replaces ahead of a norm).
 // Grid: T, BS threads (512 where dim allows one float4 per thread: twice the
 // loads in flight per token, 6.6 -> 5.6 us at config 5's 64-token chunk);
-// dim <= BS * 4 * NV.
+// dim <= BS * 4 * NV.  With xq set (and out32), the f32 norm output is also
+// quantized for the int8 expert and router kernels: qi_quant_row's planes,
+// group sums and scale of the row (MtGemvArgs::xq), the same values as
+// launch_qi_rows computes from out32.
 constexpr int PF_NPT = 64;
 template <int NV, int BS = WG>
 __global__ __launch_bounds__(BS) void pf_addnorm16_kernel(float *x, const float *part, int split, const float *w,
                                                           float eps, int dim, int T, uint16_t *out, float *out32,
-                                                          const float *mw, const float *myd, int kp) {
+                                                          const float *mw, const float *myd, int kp, u32x4 *xq,
+                                                          float *xq_sum, float *xq_scale) {
 #pragma clang fp contract(off)
     constexpr int PB = NV >= 16 ? 1 : 16 / NV;  // slices per round trip
     __shared__ float red[BS / WAVE];
@@ -146,8 +150,10 @@ __global__ __launch_bounds__(BS) void pf_addnorm16_kernel(float *x, const float 
                            wv[r].w * (s * v[r].w)};
             o4[i] = uint2{(uint32_t)f2h(n.x) | ((uint32_t)f2h(n.y) << 16), (uint32_t)f2h(n.z) | ((uint32_t)f2h(n.w) << 16)};
             if (out32) ((float4 *)(out32 + t * dim))[i] = n;
+            v[r] = n;
         }
     }
+    if (xq) qi_quant_row<NV, BS>(v, dim, t, red, xq, xq_sum, xq_scale);
 }
 
 // Per token and head (grid (T, ceil(heads / 4)), one wave per head; q, k
@@ -557,15 +563,18 @@ hipError_t launch_pf_attn(const float *q, const uint16_t *kc, const uint16_t *vc
 }
 
 hipError_t launch_pf_addnorm16(float *x, const float *part, int split, const float *w, float eps, int dim, int T,
-                               uint16_t *out, hipStream_t st, float *out32, const float *mw, const float *myd, int kp) {
+                               uint16_t *out, hipStream_t st, float *out32, const float *mw, const float *myd, int kp,
+                               void *xq, float *xq_sum, float *xq_scale) {
     if (dim > WG * PF_NPT || (myd && (part || !mw || kp < 1))) return hipErrorInvalidValue;
+    if (xq && (!out32 || !xq_sum || !xq_scale || dim % 256 || dim > 4096)) return hipErrorInvalidValue;
+    u32x4 *q = (u32x4 *)xq;
     const int nv = (dim / 4 + WG - 1) / WG;
 #define PF_AN(NV)                                                                                              \
     hipLaunchKernelGGL(pf_addnorm16_kernel<NV>, dim3(T), dim3(WG), 0, st, x, part, split, w, eps, dim, T, out, out32, \
-                       mw, myd, kp)
+                       mw, myd, kp, q, xq_sum, xq_scale)
     if (dim / 4 <= 2 * WG && dim / 4 > WG)
         hipLaunchKernelGGL((pf_addnorm16_kernel<1, 2 * WG>), dim3(T), dim3(2 * WG), 0, st, x, part, split, w, eps, dim, T,
-                           out, out32, mw, myd, kp);
+                           out, out32, mw, myd, kp, q, xq_sum, xq_scale);
     else if (nv <= 1) PF_AN(1);
     else if (nv <= 2) PF_AN(2);
     else if (nv <= 4) PF_AN(4);
