@@ -31,6 +31,7 @@ def _case(rng, n_heads, n_kv, hd, seq_len, pos0, T):
     (16, 2, 256, 64, 4096, 3000, 4),   # long context: 12 position splits
     (8, 2, 128, 128, 512, 100, 6),     # head_dim 128, full rotary
     (4, 4, 128, 0, 256, 7, 3),         # no rotary dimensions
+    (4, 2, 256, 64, 512, 130, 5),      # a group of 2 query heads, head_dim 256
     (12, 2, 128, 64, 256, 70, 3),      # a group of 6 query heads (the dimension-split kernel either way)
 ])
 def test_qwen35_attn_vs_oracle(monkeypatch, kernel, n_heads, n_kv, hd, rd, seq_len, pos0, T):
