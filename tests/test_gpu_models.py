@@ -335,6 +335,41 @@ def test_split_deltanet_step_matches_fused(make_model, monkeypatch, name):
     assert worst <= 2e-4
 
 
+@pytest.mark.parametrize("overrides", [
+    {"n_heads": 16, "n_kv_heads": 2, "head_dim": 256},  # groups of 8 query heads (8-wave workgroups)
+    {"n_heads": 4, "n_kv_heads": 2, "head_dim": 256},   # groups of 2
+])
+def test_head_dim_256_decode_vs_oracle(make_model, overrides):
+    """Dense decode attention at head_dim 256 (attn_kernel<256, G>: 4 values
+    per lane in o, 32 16-byte chunks per K row): a two-layer model of the
+    small shape with the head layout overridden, KV pre-filled with N(0,1) to
+    300 positions (5 splits), logits of 4 steps within 1e-3 of the oracle
+    (f16 KV) and the same argmax."""
+    path = make_model("tiny-q4_k", **overrides)
+    L = 300
+    e, ok = infer.engine_load(path, infer.Engine_Opts(max_ctx=L + 16))
+    assert ok
+    r = refcpu.RefEngine(path, max_ctx=L + 16, num_threads=NTHREADS, kv_f16=True)
+    try:
+        cfg = infer.engine_config(e)
+        assert cfg.head_dim == 256
+        k, v = synth.kv_prefill(91, cfg.n_layers, cfg.n_kv_heads, L, cfg.head_dim)
+        infer.engine_kv_fill(e, 0, 0, k, v)
+        for l in range(cfg.n_layers):
+            r.kv_fill(l, 0, k[l], v[l])
+        toks = [int(t) for t in np.random.default_rng(9).integers(0, cfg.vocab_size, 4)]
+        for i, t in enumerate(toks):
+            got = infer.engine_forward(e, t, L + i).copy()
+            ref = r.forward(t, L + i)
+            err = scaled_err(got, ref)
+            print("head_dim 256, group %d, step %d: scaled error %.3g" % (cfg.n_heads // cfg.n_kv_heads, i, err))
+            assert err <= TOL
+            assert int(np.argmax(got)) == refcpu.argmax(ref)
+    finally:
+        infer.engine_destroy(e)
+        r.close()
+
+
 @pytest.mark.parametrize("name,overrides,L", [
     ("tiny-q4_k", {"n_heads": 2, "n_kv_heads": 2}, 700),  # 1 query head per KV head
     ("qwen3-0.6b-q8_0", {"n_layers": 2}, 1500),           # 2 (config 1's heads)
